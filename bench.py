@@ -1,0 +1,265 @@
+#!/usr/bin/env python3
+"""Talker decode-step benchmark on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload NAME] [--no-cpu-baseline]
+
+A "step" is one Talker decode step of the resident greedy loop (28 layers + final norm
++ codec head + greedy code0 + next-embedding gather), all inputs resident in HBM.
+Default workload = the north-star target: 1.7B-shape Talker, int8 per-row weights,
+batch 1, KV prefilled to 2048 positions by 2048 real decode steps, then K timed steps.
+Weights are seeded random-init N(0, 0.02) (no checkpoints offline), quantized on the
+device by the library's bit-exact int8 quantizer.
+
+Prints ONE JSON line (metric/unit from BASELINE.json).  The timed region is bracketed
+by hipDeviceSynchronize and measured with HIP events recorded on the library's stream.
+The roofline object is for the dominant kernel (norm+gate_up+SwiGLU matvec), timed
+the same way over repeated launches.  cpu_baseline times the reference engine's own
+qwen_talker_step (built from its sources into oracle/_ref) on the host cores.
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes as C
+import importlib.util
+import json
+import os
+import sys
+import tempfile
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+HBM_PEAK_GBS = 8000.0
+
+
+def _pkg():
+    pdir = os.path.join(ROOT, "qwen3-tts_amd")
+    spec = importlib.util.spec_from_file_location("qwen3_tts_amd", os.path.join(pdir, "__init__.py"),
+                                                  submodule_search_locations=[pdir])
+    mod = importlib.util.module_from_spec(spec)
+    sys.modules["qwen3_tts_amd"] = mod
+    spec.loader.exec_module(mod)
+    return mod
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+class HipEvents:
+    """hipEvent timing on an arbitrary stream (the library's, not torch's)."""
+
+    def __init__(self):
+        self.rt = C.CDLL("libamdhip64.so")
+        self.rt.hipEventCreate.argtypes = [C.POINTER(C.c_void_p)]
+        self.rt.hipEventRecord.argtypes = [C.c_void_p, C.c_void_p]
+        self.rt.hipEventSynchronize.argtypes = [C.c_void_p]
+        self.rt.hipEventElapsedTime.argtypes = [C.POINTER(C.c_float), C.c_void_p, C.c_void_p]
+        self.rt.hipDeviceSynchronize.argtypes = []
+
+    def event(self):
+        e = C.c_void_p()
+        assert self.rt.hipEventCreate(C.byref(e)) == 0
+        return e
+
+    def record(self, e, stream):
+        assert self.rt.hipEventRecord(e, stream) == 0
+
+    def elapsed_ms(self, a, b):
+        assert self.rt.hipEventSynchronize(b) == 0
+        ms = C.c_float()
+        assert self.rt.hipEventElapsedTime(C.byref(ms), a, b) == 0
+        return ms.value
+
+    def device_sync(self):
+        assert self.rt.hipDeviceSynchronize() == 0
+
+
+WORKLOADS = {
+    # name: (shape, precision, prefill L, default timed steps)
+    "talker-1.7B-int8-b1-L2048": ("1.7B", "int8", 2048, 64),
+    "talker-0.6B-int8-b1-L2048": ("0.6B", "int8", 2048, 64),
+    "talker-0.6B-bf16-b1-L256": ("0.6B", "bf16", 256, 256),
+    "talker-1.7B-int4-b1-L512": ("1.7B", "int4", 512, 64),
+    "talker-1.7B-int4-b1-L2048": ("1.7B", "int4", 2048, 64),
+    "talker-1.7B-int4-b1-L4096": ("1.7B", "int4", 4096, 64),
+}
+
+
+def weight_bytes(shape, prec):
+    """Algorithmic weight bytes per step: every layer matrix once (+ int8 row scales,
+    q4 f16 block scales), norms, final norm."""
+    s = shape
+    mats = [(s.q_dim + 2 * s.kv_dim, s.hidden), (s.hidden, s.q_dim), (2 * s.inter, s.hidden), (s.hidden, s.inter)]
+    per = 0
+    for r, c in mats:
+        if prec == "bf16":
+            per += r * c * 2
+        elif prec == "int8":
+            per += r * c + 4 * r
+        else:
+            per += r * c // 2 + 2 * r * (c // 32)
+    norms = (2 * s.hidden + 2 * s.head_dim) * 4
+    return s.layers * (per + norms) + s.hidden * 4
+
+
+def gate_up_bytes(shape, prec):
+    r, c = 2 * shape.inter, shape.hidden
+    w = {"bf16": r * c * 2, "int8": r * c + 4 * r, "int4": r * c // 2 + 2 * r * (c // 32)}[prec]
+    return w + c * 4 * 2 + r // 2 * 4      # + x and gain read, h written
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=None)
+    ap.add_argument("--warmup", type=int, default=8)
+    ap.add_argument("--workload", default="talker-1.7B-int8-b1-L2048", choices=sorted(WORKLOADS))
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-seconds", type=float, default=15.0)
+    ap.add_argument("--kernel-launches", type=int, default=200)
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build measures one GPU only: the decode path shards as independent "
+                                   "data-parallel streams with no exchange (see DESIGN.md); run --gpus 1"}))
+        sys.exit(2)
+
+    _pkg()
+    from qwen3_tts_amd import hip, synth
+    shape_name, prec, Lpre, dsteps = WORKLOADS[args.workload]
+    K = args.steps or dsteps
+    W = args.warmup
+    s = synth.SHAPES[shape_name]
+    kv_max = max(4096, Lpre + K + W + 8)
+    seed = 0x5EED0001
+
+    t0 = time.time()
+    only = lambda n: not n.startswith("talker.code_predictor.")  # noqa: E731
+    tens = synth.generate(s, seed, 0.0, threads=int(os.environ.get("OMP_NUM_THREADS", "16")), only=only)
+    log(f"[bench] generated {shape_name} weights in {time.time() - t0:.1f}s")
+    layers = hip.layers_from_tensors(tens, s)
+    cos, sin = synth.rope_tables(s.head_dim, s.rope_theta, kv_max)
+    fnorm = synth.bf16_to_f32(tens["talker.model.norm.weight"])
+    t0 = time.time()
+    g = hip.Talker(s, layers, fnorm, cos, sin, hip.BF16, kv_max, quantize_to=hip.PREC[prec])
+    log(f"[bench] device init + quantize ({prec}) {time.time() - t0:.1f}s")
+    head = np.ascontiguousarray(tens["talker.codec_head.weight"])
+    emb = np.ascontiguousarray(tens["talker.model.codec_embedding.weight"])
+    L = hip.lib()
+    ev = HipEvents()
+    stream = L.qwen_hip_talker_stream(g.h)
+
+    # prefill: Lpre real greedy decode steps on the device
+    e0 = synth.bf16_to_f32(emb[1234])
+    t0 = time.time()
+    if Lpre > 0:
+        toks, _ = g.greedy(head, emb, e0, 0, 0, Lpre)
+    else:
+        toks, _ = g.greedy(head, emb, e0, 0, 0, 1)
+        Lpre = 1
+    log(f"[bench] prefilled KV to {Lpre} positions with {Lpre} decode steps in {time.time() - t0:.2f}s")
+
+    # warmup, then exactly K timed steps
+    hip.check(L.qwen_hip_talker_greedy_async(g.h, W), "warmup")
+    hip.check(L.qwen_hip_talker_sync(g.h), "sync")
+    ev.device_sync()
+    a, b = ev.event(), ev.event()
+    ev.record(a, stream)
+    hip.check(L.qwen_hip_talker_greedy_async(g.h, K), "timed steps")
+    ev.record(b, stream)
+    ms_total = ev.elapsed_ms(a, b)
+    ev.device_sync()
+    ms = ms_total / K
+    L_mid = Lpre + W + K / 2.0
+    kv_bytes = 2 * s.layers * s.kv_dim * 2       # per position, K and V
+    step_bytes = weight_bytes(s, prec) + kv_bytes * (L_mid + 1) + s.codec_vocab * s.hidden * 2
+    step_gbs = step_bytes / (ms * 1e-3) / 1e9
+    log(f"[bench] {K} steps: {ms * 1e3:.1f} us/step, {step_gbs:.0f} GB/s algorithmic "
+        f"({100 * step_gbs / HBM_PEAK_GBS:.1f}% of 8 TB/s)")
+
+    # per-kernel averages (HIP events over repeated launches on the same stream)
+    kern = {}
+    names = ["qkv", "attn", "o_proj", "gate_up", "down", "final_norm"]
+    n = args.kernel_launches
+    for kid, nm in enumerate(names):
+        hip.check(L.qwen_hip_talker_launch_kernel(g.h, kid, 0, 10), "kernel warmup")
+        ev.record(a, stream)
+        hip.check(L.qwen_hip_talker_launch_kernel(g.h, kid, 0, n), "kernel launches")
+        ev.record(b, stream)
+        kern[nm] = ev.elapsed_ms(a, b) * 1e3 / n
+    log("[bench] per-kernel avg us: " + ", ".join(f"{k}={v:.2f}" for k, v in kern.items()))
+    gu_bytes = gate_up_bytes(s, prec)
+    achieved = gu_bytes / (kern["gate_up"] * 1e-6) / 1e9
+    roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                "kernel": f"k_mv<{prec}> norm+gate_up+SwiGLU, {2 * s.inter}x{s.hidden}",
+                "bytes_per_launch": gu_bytes, "avg_us": round(kern["gate_up"], 3)}
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        try:
+            cpu = cpu_baseline(s, prec, g, Lpre + W + K, tens, args.cpu_seconds)
+        except Exception as ex:  # the GPU number stands on its own; report why there is none
+            log(f"[bench] cpu baseline failed: {ex}")
+            cpu = {"value": None, "unit": "ms/step", "error": str(ex)[:200]}
+    g.free()
+
+    out = {
+        "metric": "Talker ms/decode-step (0.6B/1.7B, bf16/int8/int4) + achieved HBM GB/s",
+        "value": round(ms, 4), "unit": "ms/step", "n_gpus": 1, "steps": K, "warmup": W,
+        "ms_per_step": round(ms, 4), "higher_is_better": False, "scaling": "weak", "vs_baseline": None,
+        "dtype": prec if prec != "int4" else "q4_0", "data": "synthetic (seeded N(0,0.02) random-init weights)",
+        "config": {"workload": args.workload, "batch": 1, "kv_len_start": Lpre, "layers": s.layers,
+                   "hidden": s.hidden, "inter": s.inter},
+        "tokens_per_s": round(1000.0 / ms, 1),
+        "step_bytes": int(step_bytes), "step_hbm_gbs": round(step_gbs, 1),
+        "step_hbm_frac": round(step_gbs / HBM_PEAK_GBS, 4),
+        "kernels_us": {k: round(v, 3) for k, v in kern.items()},
+        "roofline": roofline, "cpu_baseline": cpu,
+    }
+    print(json.dumps(out), flush=True)
+
+
+def cpu_baseline(s, prec, g, kv_len, tens, seconds):
+    """The reference's own qwen_talker_step (oracle/_ref, reference flags) on a bounded
+    sample: same weights (written to safetensors and loaded + quantized by the
+    reference loader), KV = the device's first kv_len positions, timed steps until
+    about `seconds` of CPU work.  Threads = OMP_NUM_THREADS (the box's CPU share)."""
+    sys.path.insert(0, ROOT)
+    from oracle.oracle import RefModel
+    from qwen3_tts_amd import synth
+    flags = open("/proc/cpuinfo").read()
+    variant = "_avx512" if all(f in flags for f in (" avx512f", " avx512bw", " avx512vl")) else ""
+    threads = int(os.environ.get("OMP_NUM_THREADS", "16"))
+    t0 = time.time()
+    full = dict(tens)
+    full.update(synth.generate(s, 0x5EED0001, 0.0, threads=threads,
+                               only=lambda n: n.startswith("talker.code_predictor.")))
+    with tempfile.TemporaryDirectory(prefix="qwen_ref_", dir=os.environ.get("TMPDIR", "/tmp")) as d:
+        synth.write_model_dir(d, s, tensors=full)
+        del full
+        ref = RefModel(d, s, prec=prec, threads=threads, variant=variant)
+    log(f"[bench] cpu baseline: reference loaded + quantized in {time.time() - t0:.1f}s ({variant or '_avx2'})")
+    # reference KV <- device KV (the reference grows its cache by doubling on demand)
+    kk, vv = g.download_kv(kv_len)
+    rk, rv = ref.kv()
+    n0 = min(kv_len, rk.shape[1])
+    rk[:, :n0] = kk[:, :n0]
+    rv[:, :n0] = vv[:, :n0]
+    ref.kv_len = n0
+    emb = tens["talker.model.codec_embedding.weight"]
+    e = np.stack([synth.bf16_to_f32(emb[i * 7 + 1]) for i in range(64)])
+    out = np.empty(s.hidden, np.float32)
+    warm = ref.lib.ref_time_talker_steps(ref.h, e.ctypes.data, 2, out.ctypes.data) / 2
+    n = int(max(2, min(64, seconds / max(warm, 1e-3))))
+    dt = ref.lib.ref_time_talker_steps(ref.h, e.ctypes.data, n, out.ctypes.data)
+    ms = dt / n * 1e3
+    log(f"[bench] cpu baseline: {n} steps at L~{n0}: {ms:.1f} ms/step ({threads} threads)")
+    return {"value": round(ms, 3), "unit": "ms/step", "cores": threads, "kind": "reference",
+            "sample": f"{n} reference qwen_talker_step calls ({prec}, {variant.strip('_') or 'avx2'} build, "
+                      f"-O3 -ffast-math) at KV length {n0}..{n0 + n + 2}, same weights and KV as the GPU run"}
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,181 @@
+/*
+ * qwen_tts_hip.h — C ABI of the MI355X (gfx950) decode-step library, libqwen_tts_hip.so.
+ *
+ * Drop-in for the reference engine's GPU seams (paths relative to the reference root):
+ *   level 1  per-op backend vtable  (qwen_tts_backend.h:34-49, qwen_tts_cuda.h:23-35)
+ *            and the qwen_tts_kernels.h kernel signatures used as the parity surface;
+ *   level 2  resident fused steps   (qwen_tts_cuda.h:62-67, qwen_tts_cuda_talker.cu:313-947,
+ *            qwen_tts_metal.m:2246-2277 for the device-side CP frame).
+ * The reference's level-2 init functions take a qwen_tts_ctx_t*; this ABI takes plain
+ * pointers instead (qwen_hip_talker_desc_t), filled from the ctx by a ~40-line glue
+ * file on the reference side.  Weight pointers may be host or
+ * device memory; init copies them to the device and never aliases them.
+ *
+ * Error convention (mirrors the reference: init NULL -> caller stays on CPU):
+ *   init functions return NULL on any failure and print one line to stderr;
+ *   a state that hits a HIP error later is marked dead: its step functions return
+ *   nonzero, qwen_hip_last_error() describes the failure.
+ * Threading: one state = one HIP stream; a state must not be used from two threads
+ * at once.  All level-2 calls are synchronous unless named *_async.
+ */
+#ifndef QWEN_TTS_HIP_H
+#define QWEN_TTS_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum { QWEN_HIP_BF16 = 0, QWEN_HIP_INT8 = 1, QWEN_HIP_Q4_0 = 2 };
+
+/* One weight matrix [rows][cols] in the reference's host layout:
+ *   BF16  uint16 bf16 bits, row-major (qwen_tts.h:125-137);
+ *   INT8  int8 row-major + f32 scale[rows] (qwen_tts.h:143-155, quantizer k.c:2143);
+ *   Q4_0  q4_0_block_t[rows][cols/32] (18 B: u16 f16 scale, u8 qs[16]) (k.h:206-210). */
+typedef struct {
+    const void *w;
+    const float *scale;      /* INT8 only, else NULL */
+} qwen_hip_mat_t;
+
+/* One transformer layer: the fields of qwen_talker_layer_t / qwen_cp_layer_t the
+ * decode step reads (qwen_tts.h:125-229).  gate_up is the reference's row-interleaved
+ * fused matrix [2*inter][hidden] (qwen_tts_talker.c:378-388). */
+typedef struct {
+    qwen_hip_mat_t q, k, v, o, gate_up, down;
+    const float *input_norm, *post_attn_norm;   /* [hidden] */
+    const float *q_norm, *k_norm;               /* [head_dim] */
+} qwen_hip_layer_t;
+
+/* Everything qwen_cuda_talker_init reads from the ctx (qwen_tts_cuda_talker.cu:313-360). */
+typedef struct {
+    int hidden, inter, n_heads, n_kv_heads, head_dim, n_layers;
+    int kv_max;                 /* device KV capacity (positions) */
+    float eps;                  /* rms_norm_eps */
+    int prec;                   /* QWEN_HIP_* of the pointers in layers[] */
+    int quantize_to;            /* -1: keep; QWEN_HIP_INT8/Q4_0: quantize BF16 weights on device */
+    const qwen_hip_layer_t *layers;
+    const float *final_norm;    /* talker_norm [hidden]; CP: cp_norm */
+    const float *rope_cos, *rope_sin;  /* [rope_len][head_dim/2] (qwen_tts_talker.c:478-495) */
+    int rope_len;
+} qwen_hip_talker_desc_t;
+
+/* ---- level 2: resident Talker step (qwen_tts_cuda_talker.cu:313-438, 933-947) ---- */
+
+/* replaces qwen_cuda_talker_init(ctx)            (qwen_tts_cuda_talker.cu:313) */
+void *qwen_hip_talker_init(const qwen_hip_talker_desc_t *desc);
+/* replaces qwen_cuda_talker_step                 (qwen_tts_cuda_talker.cu:395):
+ * embed host f32[hidden] in, hidden_out host f32[hidden] (final-normed) out; appends
+ * KV at pos.  Returns 0 on success. */
+int   qwen_hip_talker_step(void *state, const float *embed, float *hidden_out, int pos);
+/* replaces qwen_cuda_talker_get_dec_x            (qwen_tts_cuda_talker.cu:419) */
+void  qwen_hip_talker_get_dec_x(void *state, float *out);
+/* replaces qwen_cuda_talker_upload_kv(state, ctx, prefill_len) (qwen_tts_cuda_talker.cu:424):
+ * kv_k/kv_v are the host bf16 caches [n_layers][host_kv_max][kv_dim] (qwen_tts.h:513-518). */
+int   qwen_hip_talker_upload_kv(void *state, const uint16_t *kv_k, const uint16_t *kv_v,
+                                int host_kv_max, int prefill_len);
+/* replaces qwen_cuda_talker_free                 (qwen_tts_cuda_talker.cu:933) */
+void  qwen_hip_talker_free(void *state);
+
+/* Reads back the device KV of positions [0, n) in the host layout (checks/tests). */
+int   qwen_hip_talker_download_kv(void *state, uint16_t *kv_k, uint16_t *kv_v, int host_kv_max, int n);
+
+/* Device-resident greedy decode (no counterpart in the reference's C engine; it fuses
+ * the per-frame glue of qwen_tts.c:1649-1694 + 919-924 with the step): runs n_steps
+ * Talker steps starting at pos with input embed (host f32[hidden]); after each step
+ * the codec head + greedy rule picks code0 and the next input is
+ * codec_embedding[code0].  tokens_out[n_steps], hidden_out (nullable) the last
+ * hidden.  frame0 is the frame index of the first step (EOS masked for frames < 2). */
+int   qwen_hip_talker_greedy(void *state, const uint16_t *codec_head, const uint16_t *codec_emb,
+                             int codec_vocab, const float *embed, int pos, int frame0,
+                             int n_steps, int *tokens_out, float *hidden_out);
+
+/* Timing entry for benchmarks: enqueue n_steps steps of the resident greedy loop on the
+ * state's stream without host synchronisation (inputs already resident on the device).
+ * Call qwen_hip_talker_greedy once first (it uploads the heads and seeds the loop). */
+int   qwen_hip_talker_greedy_async(void *state, int n_steps);
+int   qwen_hip_talker_sync(void *state);
+/* The state's stream (hipStream_t), for callers that time it with events. */
+void *qwen_hip_talker_stream(void *state);
+/* Same as qwen_hip_talker_step, but the device graph runs with graph capture disabled
+ * (one launch per kernel), for profiling and A/B checks. */
+int   qwen_hip_talker_step_nograph(void *state, const float *embed, float *hidden_out, int pos);
+
+/* Benchmark/profiling aid (no reference counterpart): enqueue n launches of one kernel
+ * of the step on the state's stream, no sync.  kernel: 0 norm+QKV, 1 attention at the
+ * current device position, 2 O projection, 3 norm+gate_up+SwiGLU, 4 down projection,
+ * 5 final norm.  Kernels 2 and 4 write scratch instead of the residual stream, so
+ * repeated launches leave the decode state unchanged (kernel 1 rewrites the KV slot at
+ * the current position with the same bits). */
+int   qwen_hip_talker_launch_kernel(void *state, int kernel, int layer, int n);
+
+/* ---- level 2: Code Predictor (qwen_tts_cuda_talker.cu:751-841; qwen_tts_metal.m:2246) ---- */
+
+typedef struct {
+    qwen_hip_talker_desc_t cp;      /* CP layers; final_norm = cp_norm; rope = cp tables */
+    int codebook;                   /* 2048 */
+    int lm_prec;                    /* precision of lm_head[] (QWEN_HIP_*) */
+    qwen_hip_mat_t lm_head[15];     /* [codebook][cp_hidden] */
+    const uint16_t *cp_codec_emb[15];  /* bf16 [codebook][emb_dim] */
+    const uint16_t *talker_codec_emb;  /* bf16 [codec_vocab][talker_hidden] */
+    int codec_vocab, talker_hidden, emb_dim;
+    int mtp_prec;                   /* small_to_mtp_projection precision (BF16/INT8) */
+    qwen_hip_mat_t mtp;             /* [cp_hidden][emb_dim] or w=NULL (identity) */
+    const float *mtp_bias;          /* f32 [cp_hidden] or NULL */
+} qwen_hip_cp_desc_t;
+
+/* replaces qwen_cuda_cp_init(ctx)                (qwen_tts_cuda_talker.cu:751) */
+void *qwen_hip_cp_init(const qwen_hip_cp_desc_t *desc);
+/* replaces qwen_cuda_cp_step(state, x, pos)      (qwen_tts_cuda_talker.cu:796):
+ * x host f32[cp_hidden] residual in/out (not normed); one 5-layer pass at pos. */
+int   qwen_hip_cp_step(void *state, float *x, int pos);
+/* twin of qwen_metal_cp_frame (qwen_tts_metal.m:2246-2277), the device-side version of
+ * qwen_cp_predict (qwen_tts_code_predictor.c:926-1045): 16 passes + 15 greedy lm-head
+ * picks + embedding gathers, one host sync.  out_codes[15]. */
+int   qwen_hip_cp_frame(void *state, const float *talker_hidden, int code0, int *out_codes);
+/* benchmark entry: n frames back to back on device inputs already uploaded by a
+ * previous qwen_hip_cp_frame call, no host sync. */
+int   qwen_hip_cp_frame_async(void *state, int n_frames);
+int   qwen_hip_cp_sync(void *state);
+void *qwen_hip_cp_stream(void *state);
+/* replaces qwen_cuda_cp_free                     (qwen_tts_cuda_talker.cu:917) */
+void  qwen_hip_cp_free(void *state);
+
+/* ---- level 1: per-op backend (qwen_tts_cuda.h:23-35, qwen_tts_backend.h:34-49) ---- */
+
+int   qwen_hip_available(void);
+void *qwen_hip_init(void);
+void  qwen_hip_free(void *ctx);
+/* y[rows] = W[rows,cols] @ x[cols] (W bf16; host pointers; W cached on device by
+ * host address like qwen_tts_cuda.c:96-112) */
+void  qwen_hip_matvec_bf16(void *ctx, float *y, const uint16_t *W, const float *x, int rows, int cols);
+/* Y[rows,B] = W[rows,cols] @ X[cols,B] (row-major f32, B<=64) */
+void  qwen_hip_matmat_bf16(void *ctx, float *Y, const uint16_t *W, const float *X, int rows, int cols, int B);
+
+/* qwen_tts_kernels.h signatures on the HIP kernels (host pointers in and out; every
+ * call uploads, computes, downloads).  Return 0 on success. */
+int qwen_hip_op_matvec_int8(float *y, const int8_t *W, const float *scale, const float *x, int rows, int cols);
+int qwen_hip_op_matvec_q4_0(float *y, const void *W, const float *x, int rows, int cols);
+int qwen_hip_op_matvec_bf16(float *y, const uint16_t *W, const float *x, int rows, int cols);
+int qwen_hip_op_causal_attention_bf16kv(float *out, const float *Q, const uint16_t *K, const uint16_t *V,
+                                        int seq_q, int seq_k, int n_heads, int n_kv_heads, int head_dim,
+                                        float scale, int q_offset);
+int qwen_hip_op_rms_norm(float *out, const float *x, const float *w, int seq, int dim, float eps);
+int qwen_hip_op_rms_norm_per_head(float *x, const float *w, int seq, int n_heads, int head_dim, float eps);
+int qwen_hip_op_swiglu(float *out, const float *gate_up, int n);
+int qwen_hip_op_argmax_matvec(int prec, const float *x, const void *W, const float *scale, int in_dim, int out_dim);
+/* qwen_quantize_bf16_to_int8 / _q4_0 (k.c:2143, k.c:2662) run on the device; output in
+ * the reference's host layout. */
+int qwen_hip_op_quantize_int8(const uint16_t *src, int rows, int cols, int8_t *dst, float *scale);
+int qwen_hip_op_quantize_q4_0(const uint16_t *src, int rows, int cols, void *dst_blocks);
+/* Dequantise rows of a resident Talker weight (layer, which: 0 q 1 k 2 v 3 o 4 gate_up
+ * 5 down) to f32, from the device copy: proves upload/repack is bit-exact. */
+int qwen_hip_talker_dequant(void *state, int layer, int which, int r0, int n, float *out);
+
+const char *qwen_hip_last_error(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* QWEN_TTS_HIP_H */

@@ -1,0 +1,264 @@
+// qt_attn.hip — single-query GQA attention over a bf16 KV cache (gfx950).
+//
+// Semantics of qwen_causal_attention_bf16kv (qwen_tts_kernels.c:3704-3846) for one
+// query row: for head h (kv head g = h / HPK) over keys j < L,
+//   s_j = (q . k_j) * scale,  o = sum_j softmax(s)_j v_j.
+// Split-K (flash-decoding): grid (G chunks, n_kv).  Workgroup (c, g) takes keys
+// [c*CH, c*CH+CH) with CH = roundup16(ceil(L/G)), so the grid is fixed while L grows
+// (graph-replay safe) and every workgroup reads K/V of ONE kv head once for all HPK
+// query heads that share it.  Per chunk it keeps (m, l, o[128]) per head; the last
+// workgroup of a kv head to finish (device-scope counter) merges the chunks:
+//   M = max m_c,  l = sum l_c e^(m_c-M),  o = sum o_c e^(m_c-M) / l.
+//
+// PREP (decode step) additionally does, from the raw QKV projection output:
+//   per-head RMSNorm of q and k with the shared [128] gains (qwen_tts_kernels.c:486-577),
+//   NeoX split-half RoPE from the uploaded cos/sin tables (qwen_tts_talker.c:203-251),
+//   and the KV append at `pos` with f32->bf16 TRUNCATION (qwen_tts_talker.c:612-615),
+//   done by the one workgroup whose chunk holds `pos` before it reads its keys.
+#include "qt_device.h"
+
+#define QT_HD 128
+#define QT_CH_MAX 256
+
+struct QtAttnArgs {
+    const float *q;          // PREP: raw [q | k | v]; else rotated q rows (this query row)
+    const float *qn, *kn;    // PREP: per-head gains
+    const float *rc, *rs;    // PREP: rope tables [rope_len][64]
+    float eps;
+    const int *d_pos;        // PREP: device position; L = pos + 1
+    int Lval;                // !PREP: number of keys
+    uint16_t *K, *V;         // layer cache base
+    long long pos_stride;    // elements between consecutive positions of one head
+    long long head_stride;   // elements between kv heads
+    int n_heads, n_kv;
+    float scale;
+    float *part;             // [n_kv][G][HPK][2 + 128]
+    unsigned *cnt;           // [n_kv]
+    float *out;              // [n_heads * 128]
+};
+
+template <int HPK, bool PREP>
+__global__ __launch_bounds__(QT_WG) void k_attn(QtAttnArgs a) {
+    const int g = blockIdx.y, c = blockIdx.x, G = gridDim.x;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int pos = PREP ? *a.d_pos : a.Lval - 1;
+    const int L = pos + 1;
+    int CH = (L + G - 1) / G;
+    CH = (CH + 15) & ~15;
+    const int nch = (L + CH - 1) / CH;
+    if (c >= nch) return;
+    const int j0 = c * CH;
+    const int n = min(CH, L - j0);
+
+    __shared__ float qs[HPK][QT_HD];
+    __shared__ float sc[HPK][QT_CH_MAX];
+    __shared__ float ored[QT_WAVES][HPK][QT_HD];
+    __shared__ float stat[HPK][2];
+    __shared__ int last_flag;
+
+    uint16_t *Kg = a.K + (long long)g * a.head_stride;
+    uint16_t *Vg = a.V + (long long)g * a.head_stride;
+
+    // ---- 1. query heads (and the new key/value) ----
+    if (PREP) {
+        const bool append = (pos >= j0 && pos < j0 + n);
+        const int ntask = HPK + (append ? 1 : 0);
+        for (int t = wave; t < ntask; t += QT_WAVES) {
+            const bool isk = (t == HPK);
+            const float *src = isk ? a.q + a.n_heads * QT_HD + g * QT_HD
+                                   : a.q + (g * HPK + t) * QT_HD;
+            const float *w = isk ? a.kn : a.qn;
+            float x0 = src[lane], x1 = src[lane + 64];
+            float ss = group_sum<64>(x0 * x0 + x1 * x1);
+            float inv = 1.0f / sqrtf(ss / (float)QT_HD + a.eps);
+            float n0 = (x0 * inv) * w[lane], n1 = (x1 * inv) * w[lane + 64];
+            float cs = a.rc[(size_t)pos * 64 + lane], sn = a.rs[(size_t)pos * 64 + lane];
+            float r0 = fmaf(n0, cs, -(n1 * sn));
+            float r1 = fmaf(n1, cs, n0 * sn);
+            if (!isk) {
+                qs[t][lane] = r0;
+                qs[t][lane + 64] = r1;
+            } else {
+                const float *vs = a.q + a.n_heads * QT_HD + a.n_kv * QT_HD + g * QT_HD;
+                uint16_t *kd = Kg + (long long)pos * a.pos_stride;
+                uint16_t *vd = Vg + (long long)pos * a.pos_stride;
+                kd[lane] = f2bf_trunc(r0);
+                kd[lane + 64] = f2bf_trunc(r1);
+                vd[lane] = f2bf_trunc(vs[lane]);
+                vd[lane + 64] = f2bf_trunc(vs[lane + 64]);
+            }
+        }
+    } else {
+        for (int i = tid; i < HPK * QT_HD; i += QT_WG)
+            qs[i / QT_HD][i % QT_HD] = a.q[(g * HPK + i / QT_HD) * QT_HD + i % QT_HD];
+    }
+    __syncthreads();
+
+    // ---- 2. scores: 16 lanes per key (8 dims each), 4 keys per wave per step ----
+    const int sub = lane & 15, pg = lane >> 4;
+    float qv[HPK][8];
+#pragma unroll
+    for (int h = 0; h < HPK; h++)
+#pragma unroll
+        for (int e = 0; e < 8; e++) qv[h][e] = qs[h][sub * 8 + e];
+
+    for (int base = wave * 4 + pg; base < n; base += 64) {
+        uint4 kw[4];
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            const int jj = base + 16 * u;
+            kw[u] = (jj < n) ? *reinterpret_cast<const uint4 *>(Kg + (long long)(j0 + jj) * a.pos_stride + sub * 8)
+                             : make_uint4(0, 0, 0, 0);
+        }
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            const uint32_t w4[4] = {kw[u].x, kw[u].y, kw[u].z, kw[u].w};
+            float kf[8];
+#pragma unroll
+            for (int m = 0; m < 4; m++) { kf[2 * m] = bf_lo(w4[m]); kf[2 * m + 1] = bf_hi(w4[m]); }
+            const int jj = base + 16 * u;
+#pragma unroll
+            for (int h = 0; h < HPK; h++) {
+                float s = 0.f;
+#pragma unroll
+                for (int e = 0; e < 8; e++) s = fmaf(qv[h][e], kf[e], s);
+                s = group_sum<16>(s);
+                if (sub == 0 && jj < n) sc[h][jj] = s * a.scale;
+            }
+        }
+    }
+    __syncthreads();
+
+    // ---- 3. chunk softmax statistics ----
+    for (int h = wave; h < HPK; h += QT_WAVES) {
+        float m = -INFINITY;
+        for (int j = lane; j < n; j += 64) m = fmaxf(m, sc[h][j]);
+        m = group_max<64>(m);
+        float l = 0.f;
+        for (int j = lane; j < n; j += 64) {
+            float p = expf(sc[h][j] - m);
+            sc[h][j] = p;
+            l += p;
+        }
+        l = group_sum<64>(l);
+        if (lane == 0) { stat[h][0] = m; stat[h][1] = l; }
+    }
+    __syncthreads();
+
+    // ---- 4. o = sum_j p_j v_j ----
+    float o[HPK][8];
+#pragma unroll
+    for (int h = 0; h < HPK; h++)
+#pragma unroll
+        for (int e = 0; e < 8; e++) o[h][e] = 0.f;
+    for (int base = wave * 4 + pg; base < n; base += 64) {
+        uint4 vw[4];
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            const int jj = base + 16 * u;
+            vw[u] = (jj < n) ? *reinterpret_cast<const uint4 *>(Vg + (long long)(j0 + jj) * a.pos_stride + sub * 8)
+                             : make_uint4(0, 0, 0, 0);
+        }
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            const int jj = base + 16 * u;
+            if (jj < n) {
+                const uint32_t w4[4] = {vw[u].x, vw[u].y, vw[u].z, vw[u].w};
+                float vf[8];
+#pragma unroll
+                for (int m = 0; m < 4; m++) { vf[2 * m] = bf_lo(w4[m]); vf[2 * m + 1] = bf_hi(w4[m]); }
+#pragma unroll
+                for (int h = 0; h < HPK; h++) {
+                    const float p = sc[h][jj];
+#pragma unroll
+                    for (int e = 0; e < 8; e++) o[h][e] = fmaf(p, vf[e], o[h][e]);
+                }
+            }
+        }
+    }
+#pragma unroll
+    for (int h = 0; h < HPK; h++)
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+            float v = o[h][e];
+            v += __shfl_xor(v, 16, 64);
+            v += __shfl_xor(v, 32, 64);
+            o[h][e] = v;
+        }
+    if (pg == 0) {
+#pragma unroll
+        for (int h = 0; h < HPK; h++)
+#pragma unroll
+            for (int e = 0; e < 8; e++) ored[wave][h][sub * 8 + e] = o[h][e];
+    }
+    __syncthreads();
+
+    // ---- 5. write (single chunk) or publish partial and merge in the last workgroup ----
+    if (nch == 1) {
+        for (int i = tid; i < HPK * QT_HD; i += QT_WG) {
+            const int h = i / QT_HD, d = i % QT_HD;
+            float v = ored[0][h][d] + ored[1][h][d] + ored[2][h][d] + ored[3][h][d];
+            a.out[(g * HPK + h) * QT_HD + d] = v * (1.0f / stat[h][1]);
+        }
+        return;
+    }
+    constexpr int PS = 2 + QT_HD;
+    float *mypart = a.part + ((size_t)(g * G + c) * HPK) * PS;
+    for (int i = tid; i < HPK * QT_HD; i += QT_WG) {
+        const int h = i / QT_HD, d = i % QT_HD;
+        mypart[h * PS + 2 + d] = ored[0][h][d] + ored[1][h][d] + ored[2][h][d] + ored[3][h][d];
+    }
+    if (tid < HPK) { mypart[tid * PS] = stat[tid][0]; mypart[tid * PS + 1] = stat[tid][1]; }
+    __threadfence();
+    __syncthreads();
+    if (tid == 0) last_flag = (atomicAdd(&a.cnt[g], 1u) == (unsigned)(nch - 1));
+    __syncthreads();
+    if (!last_flag) return;
+    __threadfence();
+    const float *gp = a.part + (size_t)g * G * HPK * PS;
+    for (int i = tid; i < HPK * QT_HD; i += QT_WG) {
+        const int h = i / QT_HD, d = i % QT_HD;
+        float M = -INFINITY;
+        for (int cc = 0; cc < nch; cc++) M = fmaxf(M, gp[(cc * HPK + h) * PS]);
+        float l = 0.f, v = 0.f;
+        for (int cc = 0; cc < nch; cc++) {
+            const float *pp = gp + (cc * HPK + h) * PS;
+            const float f = expf(pp[0] - M);
+            l = fmaf(pp[1], f, l);
+            v = fmaf(pp[2 + d], f, v);
+        }
+        a.out[(g * HPK + h) * QT_HD + d] = v * (1.0f / l);
+    }
+    if (tid == 0) a.cnt[g] = 0u;
+}
+
+extern "C" hipError_t qt_launch_attn(int prep, const float *q, const float *qn, const float *kn,
+                                     const float *rc, const float *rs, float eps, const int *d_pos,
+                                     int Lval, uint16_t *K, uint16_t *V, long long pos_stride,
+                                     long long head_stride, int n_heads, int n_kv, int head_dim,
+                                     float scale, float *part, unsigned *cnt, int G, float *out,
+                                     hipStream_t st) {
+    QtAttnArgs a;
+    a.q = q; a.qn = qn; a.kn = kn; a.rc = rc; a.rs = rs; a.eps = eps; a.d_pos = d_pos; a.Lval = Lval;
+    a.K = K; a.V = V; a.pos_stride = pos_stride; a.head_stride = head_stride;
+    a.n_heads = n_heads; a.n_kv = n_kv; a.scale = scale; a.part = part; a.cnt = cnt; a.out = out;
+    if (head_dim != QT_HD || n_kv <= 0 || n_heads % n_kv) return hipErrorInvalidValue;
+    if (G <= 0) return hipErrorInvalidValue;
+    const int hpk = n_heads / n_kv;
+    dim3 grid(G, n_kv);
+#define QT_ATT_CASE(H) \
+    if (prep) hipLaunchKernelGGL((k_attn<H, true>), grid, dim3(QT_WG), 0, st, a); \
+    else hipLaunchKernelGGL((k_attn<H, false>), grid, dim3(QT_WG), 0, st, a);
+    if (hpk == 1) { QT_ATT_CASE(1) }
+    else if (hpk == 2) { QT_ATT_CASE(2) }
+    else if (hpk == 4) { QT_ATT_CASE(4) }
+    else return hipErrorInvalidValue;
+#undef QT_ATT_CASE
+    return hipGetLastError();
+}
+
+// Number of split-K chunks the grid needs so that CH <= QT_CH_MAX for every L <= max_len.
+extern "C" int qt_attn_grid(int max_len) {
+    int g = (max_len + QT_CH_MAX - 1) / QT_CH_MAX;
+    return g < 32 ? 32 : g;
+}

@@ -1,0 +1,47 @@
+/* qt_launch.h — C declarations of the kernel launchers defined in the .hip files. */
+#ifndef QT_LAUNCH_H
+#define QT_LAUNCH_H
+#include <hip/hip_runtime_api.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum { QT_BF16 = 0, QT_INT8 = 1, QT_Q4 = 2 };
+enum { QT_EPI_STORE = 0, QT_EPI_RESID = 1, QT_EPI_SWIGLU = 2, QT_EPI_BIAS = 3 };
+
+hipError_t qt_launch_mv(int prec, int epi, int norm, const float *vin, const float *nw, float eps,
+                        const uint8_t *w, const float *scale, const uint16_t *s16, int rows, int cols,
+                        float *out, float *resid, const float *bias, hipStream_t st);
+hipError_t qt_launch_attn(int prep, const float *q, const float *qn, const float *kn, const float *rc,
+                          const float *rs, float eps, const int *d_pos, int Lval, uint16_t *K, uint16_t *V,
+                          long long pos_stride, long long head_stride, int n_heads, int n_kv, int head_dim,
+                          float scale, float *part, unsigned *cnt, int G, float *out, hipStream_t st);
+int qt_attn_grid(int max_len);
+hipError_t qt_launch_rmsnorm(const float *x, const float *w, float *out, int n, float eps, int *d_pos,
+                             hipStream_t st);
+hipError_t qt_launch_rmsnorm_rows(float *x, const float *w, int rows, int n, float eps, hipStream_t st);
+hipError_t qt_launch_swiglu(const float *gu, float *out, int n, hipStream_t st);
+hipError_t qt_launch_select(const float *logits, int n, int mode, int *d_frame, int advance, int *tok,
+                            int *hist, int hist_len, const uint16_t *emb, int emb_dim, float *out,
+                            hipStream_t st);
+hipError_t qt_launch_gather(const int *tok, int tok_max, const uint16_t *table, int dim, float *out,
+                            hipStream_t st);
+hipError_t qt_launch_copy_f32(const float *src, float *dst, int n, hipStream_t st);
+hipError_t qt_launch_quant_int8(const uint16_t *src, int rows, int cols, uint8_t *dst, float *scale,
+                                hipStream_t st);
+hipError_t qt_launch_flip_sign(uint8_t *p, size_t n, hipStream_t st);
+hipError_t qt_launch_repack_q4(const uint8_t *blocks, size_t nblocks, uint8_t *qs, uint16_t *s16,
+                               hipStream_t st);
+hipError_t qt_launch_quant_q4(const uint16_t *src, int rows, int cols, uint8_t *qs, uint16_t *s16,
+                              hipStream_t st);
+hipError_t qt_launch_dequant(int prec, const uint8_t *w, const float *scale, const uint16_t *s16, int cols,
+                             int r0, int n, float *out, hipStream_t st);
+hipError_t qt_launch_zero_u32(uint32_t *p, size_t n, hipStream_t st);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,331 @@
+// qt_matvec.hip — weight-streaming matvec kernels for the decode step (gfx950).
+//
+// One kernel family covers every projection of a Talker / Code-Predictor layer:
+//   y = W . f(v)   with  f = identity or RMSNorm(v)*g   (NORM)
+// and an epilogue (EPI):
+//   STORE   y[r] = acc                        (QKV, logits)
+//   RESID   x[r] += acc                       (O and down projections, residual add)
+//   SWIGLU  h[i] = silu(acc[2i]) * acc[2i+1]  (interleaved gate|up rows)
+//   BIAS    y[r] = acc + bias[r]              (CP small_to_mtp_projection)
+// Numerics follow the reference CPU path: f32 activations, f32 accumulation,
+// int8 row scale applied once per row (qwen_tts_kernels.c:2350-2351), q4 block value
+// (nib-8)*f16(scale) (qwen_tts_kernels.c:2810-2819), SwiGLU g/(1+expf(-g))*u
+// (qwen_tts_kernels.c:3857-3878), RMSNorm (x*inv)*w (qwen_tts_kernels.c:292-382).
+//
+// Work split: a workgroup stages the input vector (normalised if NORM) in LDS; each
+// lane copies the slice of it that its weight chunks multiply into registers once,
+// then a wave streams NR rows x CPL chunks per lane (NR*CPL independent 128-bit loads
+// in flight per lane) and reduces each row across its LPR lanes.  A wave owns
+// NR*(64/LPR) consecutive rows; a 256-thread workgroup owns 4x that.
+#include "qt_device.h"
+
+template <int PREC> struct QtPrec;
+template <> struct QtPrec<QT_BF16> { static constexpr int EPC = 8; };
+template <> struct QtPrec<QT_INT8> { static constexpr int EPC = 16; };
+template <> struct QtPrec<QT_Q4> { static constexpr int EPC = 32; };
+
+__device__ __forceinline__ size_t qt_row_bytes(int prec, int cols) {
+    return prec == QT_BF16 ? (size_t)cols * 2 : prec == QT_INT8 ? (size_t)cols : (size_t)cols / 2;
+}
+
+struct QtMvArgs {
+    const float *vin;    // input vector [cols]
+    const float *nw;     // RMSNorm gain [cols] (NORM)
+    float eps;
+    QtMat M;
+    float *out;          // STORE/SWIGLU/BIAS output
+    float *resid;        // RESID target
+    const float *bias;   // BIAS
+};
+
+// Stage vin (optionally RMS-normalised) into LDS; returns nothing, xs[] valid after.
+template <bool NORM>
+__device__ __forceinline__ void qt_stage(const QtMvArgs &a, float *xs, float *red) {
+    const int cols = a.M.cols;
+    float ss = 0.f;
+    for (int i = threadIdx.x * 4; i < cols; i += QT_WG * 4) {
+        float4 v = *reinterpret_cast<const float4 *>(a.vin + i);
+        *reinterpret_cast<float4 *>(xs + i) = v;
+        if (NORM) ss += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
+    }
+    if (NORM) {
+        float tot = block_sum(ss, red);
+        float inv = 1.0f / sqrtf(tot / (float)cols + a.eps);
+        __syncthreads();
+        for (int i = threadIdx.x; i < cols; i += QT_WG) xs[i] = (xs[i] * inv) * a.nw[i];
+    }
+    __syncthreads();
+}
+
+template <int EPI>
+__device__ __forceinline__ void qt_epilogue(const QtMvArgs &a, int row, float acc) {
+    if (EPI == QT_EPI_STORE) a.out[row] = acc;
+    else if (EPI == QT_EPI_RESID) a.resid[row] += acc;
+    else if (EPI == QT_EPI_BIAS) a.out[row] = acc + a.bias[row];
+}
+
+__device__ __forceinline__ float qt_silu_mul(float g, float u) {
+    return g / (1.0f + expf(-g)) * u;
+}
+
+template <int PREC, int LPR, int CPL, int NR, int EPI, bool NORM>
+__global__ __launch_bounds__(QT_WG) void k_mv(QtMvArgs a) {
+    constexpr int EPC = QtPrec<PREC>::EPC;
+    constexpr int RPW = NR * (64 / LPR);
+    extern __shared__ float xs[];
+    __shared__ float red[QT_WAVES];
+    qt_stage<NORM>(a, xs, red);
+
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int grp = lane / LPR, sub = lane % LPR;
+    const int row0 = (blockIdx.x * QT_WAVES + wave) * RPW + grp * NR;
+    const int rows = a.M.rows, cols = a.M.cols;
+    const size_t rb = qt_row_bytes(PREC, cols);
+
+    // activation slice for this lane's chunks (c = sub + LPR*j)
+    float xr[CPL][EPC];
+    float xsum[CPL];
+#pragma unroll
+    for (int j = 0; j < CPL; j++) {
+        const int c = sub + LPR * j;
+        const float *src = xs + c * EPC;
+        float s = 0.f;
+        if (PREC == QT_Q4) {
+            // word m of the chunk holds elements 8m..8m+7: low nibbles are the even ones
+#pragma unroll
+            for (int m = 0; m < 4; m++)
+#pragma unroll
+                for (int b = 0; b < 4; b++) {
+                    xr[j][m * 4 + b] = src[8 * m + 2 * b];
+                    xr[j][16 + m * 4 + b] = src[8 * m + 2 * b + 1];
+                }
+        } else {
+#pragma unroll
+            for (int e = 0; e < EPC; e++) xr[j][e] = src[e];
+        }
+        if (PREC != QT_BF16) {
+#pragma unroll
+            for (int e = 0; e < EPC; e++) s += xr[j][e];
+        }
+        xsum[j] = s;
+    }
+
+    uint4 wv[NR][CPL];
+    float sc[NR][CPL];
+#pragma unroll
+    for (int r = 0; r < NR; r++) {
+        const int row = row0 + r;
+#pragma unroll
+        for (int j = 0; j < CPL; j++) {
+            const int c = sub + LPR * j;
+            if (row < rows) {
+                wv[r][j] = ld_chunk(a.M.w + (size_t)row * rb + (size_t)c * 16);
+                if (PREC == QT_Q4) sc[r][j] = ref_f16_to_f32(a.M.s16[(size_t)row * (cols / 32) + c]);
+            } else {
+                wv[r][j] = make_uint4(0, 0, 0, 0);
+                sc[r][j] = 0.f;
+            }
+        }
+    }
+
+    float acc[NR];
+#pragma unroll
+    for (int r = 0; r < NR; r++) {
+        float s = 0.f;
+#pragma unroll
+        for (int j = 0; j < CPL; j++) {
+            const uint32_t w4[4] = {wv[r][j].x, wv[r][j].y, wv[r][j].z, wv[r][j].w};
+            if (PREC == QT_BF16) {
+#pragma unroll
+                for (int m = 0; m < 4; m++) {
+                    s = fmaf(bf_lo(w4[m]), xr[j][2 * m], s);
+                    s = fmaf(bf_hi(w4[m]), xr[j][2 * m + 1], s);
+                }
+            } else if (PREC == QT_INT8) {
+                float t = 0.f;
+#pragma unroll
+                for (int m = 0; m < 4; m++) {
+                    const uint32_t w = w4[m];
+                    t = fmaf((float)(w & 0xFFu), xr[j][4 * m + 0], t);
+                    t = fmaf((float)((w >> 8) & 0xFFu), xr[j][4 * m + 1], t);
+                    t = fmaf((float)((w >> 16) & 0xFFu), xr[j][4 * m + 2], t);
+                    t = fmaf((float)(w >> 24), xr[j][4 * m + 3], t);
+                }
+                s += t - 128.0f * xsum[j];
+            } else {
+                float t = 0.f;
+#pragma unroll
+                for (int m = 0; m < 4; m++) {
+                    const uint32_t lo = w4[m] & 0x0F0F0F0Fu, hi = (w4[m] >> 4) & 0x0F0F0F0Fu;
+                    t = fmaf((float)(lo & 0xFFu), xr[j][m * 4 + 0], t);
+                    t = fmaf((float)((lo >> 8) & 0xFFu), xr[j][m * 4 + 1], t);
+                    t = fmaf((float)((lo >> 16) & 0xFFu), xr[j][m * 4 + 2], t);
+                    t = fmaf((float)(lo >> 24), xr[j][m * 4 + 3], t);
+                    t = fmaf((float)(hi & 0xFFu), xr[j][16 + m * 4 + 0], t);
+                    t = fmaf((float)((hi >> 8) & 0xFFu), xr[j][16 + m * 4 + 1], t);
+                    t = fmaf((float)((hi >> 16) & 0xFFu), xr[j][16 + m * 4 + 2], t);
+                    t = fmaf((float)(hi >> 24), xr[j][16 + m * 4 + 3], t);
+                }
+                s = fmaf(sc[r][j], t - 8.0f * xsum[j], s);
+            }
+        }
+        acc[r] = group_sum<LPR>(s);
+    }
+
+    if (sub == 0) {
+        if (EPI == QT_EPI_SWIGLU) {
+#pragma unroll
+            for (int r = 0; r < NR; r += 2) {
+                const int row = row0 + r;
+                if (row + 1 < rows) {
+                    float g = acc[r], u = acc[r + 1];
+                    if (PREC == QT_INT8) { g *= a.M.scale[row]; u *= a.M.scale[row + 1]; }
+                    a.out[row >> 1] = qt_silu_mul(g, u);
+                }
+            }
+        } else {
+#pragma unroll
+            for (int r = 0; r < NR; r++) {
+                const int row = row0 + r;
+                if (row < rows) {
+                    float v = acc[r];
+                    if (PREC == QT_INT8) v *= a.M.scale[row];
+                    qt_epilogue<EPI>(a, row, v);
+                }
+            }
+        }
+    }
+}
+
+// Generic fallback for shapes the tuned instantiations do not cover (per-op API with
+// arbitrary rows/cols): one wave per row (pair of rows for SWIGLU), lane-strided
+// scalar reads, same numerics.
+template <int PREC, int EPI, bool NORM>
+__global__ __launch_bounds__(QT_WG) void k_mv_generic(QtMvArgs a) {
+    extern __shared__ float xs[];
+    __shared__ float red[QT_WAVES];
+    const int cols = a.M.cols, rows = a.M.rows;
+    // staging without the float4 assumption
+    float ss = 0.f;
+    for (int i = threadIdx.x; i < cols; i += QT_WG) {
+        float v = a.vin[i];
+        xs[i] = v;
+        if (NORM) ss += v * v;
+    }
+    if (NORM) {
+        float tot = block_sum(ss, red);
+        float inv = 1.0f / sqrtf(tot / (float)cols + a.eps);
+        __syncthreads();
+        for (int i = threadIdx.x; i < cols; i += QT_WG) xs[i] = (xs[i] * inv) * a.nw[i];
+    }
+    __syncthreads();
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int per = (EPI == QT_EPI_SWIGLU) ? 2 : 1;
+    const int row0 = (blockIdx.x * QT_WAVES + wave) * per;
+    float acc[2] = {0.f, 0.f};
+    for (int r = 0; r < per; r++) {
+        const int row = row0 + r;
+        if (row >= rows) break;
+        float s = 0.f;
+        for (int k = lane; k < cols; k += 64) {
+            float w;
+            if (PREC == QT_BF16) {
+                w = bf16f(reinterpret_cast<const uint16_t *>(a.M.w)[(size_t)row * cols + k]);
+            } else if (PREC == QT_INT8) {
+                w = (float)((int)a.M.w[(size_t)row * cols + k] - 128);
+            } else {
+                const uint8_t byte = a.M.w[(size_t)row * (cols / 2) + k / 2];
+                const int nib = (k & 1) ? (byte >> 4) : (byte & 0xF);
+                w = (float)(nib - 8) * ref_f16_to_f32(a.M.s16[(size_t)row * (cols / 32) + k / 32]);
+            }
+            s = fmaf(w, xs[k], s);
+        }
+        s = group_sum<64>(s);
+        if (PREC == QT_INT8) s *= a.M.scale[row];
+        acc[r] = s;
+    }
+    if (lane == 0) {
+        if (EPI == QT_EPI_SWIGLU) {
+            if (row0 + 1 < rows) a.out[row0 >> 1] = qt_silu_mul(acc[0], acc[1]);
+        } else if (row0 < rows) {
+            qt_epilogue<EPI>(a, row0, acc[0]);
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------------
+// host-side dispatch (C ABI, used by qwen_tts_hip.c)
+
+template <int PREC, int LPR, int CPL, int NR, int EPI, bool NORM>
+static hipError_t launch_tuned(const QtMvArgs &a, hipStream_t st) {
+    constexpr int RPW = NR * (64 / LPR);
+    const int per_wg = RPW * QT_WAVES;
+    const int grid = (a.M.rows + per_wg - 1) / per_wg;
+    hipLaunchKernelGGL((k_mv<PREC, LPR, CPL, NR, EPI, NORM>), dim3(grid), dim3(QT_WG),
+                       (size_t)a.M.cols * sizeof(float), st, a);
+    return hipGetLastError();
+}
+
+template <int PREC, int EPI, bool NORM>
+static hipError_t launch_generic(const QtMvArgs &a, hipStream_t st) {
+    const int per = (EPI == QT_EPI_SWIGLU) ? 2 : 1;
+    const int grid = (a.M.rows + per * QT_WAVES - 1) / (per * QT_WAVES);
+    hipLaunchKernelGGL((k_mv_generic<PREC, EPI, NORM>), dim3(grid), dim3(QT_WG),
+                       (size_t)a.M.cols * sizeof(float), st, a);
+    return hipGetLastError();
+}
+
+// (prec, cols) -> tuned instantiation; NR*CPL ~ 8-12 128-bit loads in flight per lane.
+template <int EPI, bool NORM>
+static hipError_t dispatch(int prec, const QtMvArgs &a, hipStream_t st) {
+    const int c = a.M.cols;
+    const bool aligned = ((uintptr_t)a.M.w % 16 == 0) && ((uintptr_t)a.vin % 16 == 0);
+    if (aligned) {
+        if (prec == QT_BF16) {
+            switch (c) {
+            case 1024: return launch_tuned<QT_BF16, 64, 2, 4, EPI, NORM>(a, st);
+            case 2048: return launch_tuned<QT_BF16, 64, 4, 2, EPI, NORM>(a, st);
+            case 3072: return launch_tuned<QT_BF16, 64, 6, 2, EPI, NORM>(a, st);
+            case 6144: return launch_tuned<QT_BF16, 64, 12, 2, EPI, NORM>(a, st);
+            }
+        } else if (prec == QT_INT8) {
+            switch (c) {
+            case 1024: return launch_tuned<QT_INT8, 64, 1, 8, EPI, NORM>(a, st);
+            case 2048: return launch_tuned<QT_INT8, 64, 2, 4, EPI, NORM>(a, st);
+            case 3072: return launch_tuned<QT_INT8, 64, 3, 4, EPI, NORM>(a, st);
+            case 6144: return launch_tuned<QT_INT8, 64, 6, 2, EPI, NORM>(a, st);
+            }
+        } else {
+            switch (c) {
+            case 1024: return launch_tuned<QT_Q4, 32, 1, 8, EPI, NORM>(a, st);
+            case 2048: return launch_tuned<QT_Q4, 64, 1, 8, EPI, NORM>(a, st);
+            case 3072: return launch_tuned<QT_Q4, 32, 3, 4, EPI, NORM>(a, st);
+            case 6144: return launch_tuned<QT_Q4, 64, 3, 4, EPI, NORM>(a, st);
+            }
+        }
+    }
+    if (prec == QT_BF16) return launch_generic<QT_BF16, EPI, NORM>(a, st);
+    if (prec == QT_INT8) return launch_generic<QT_INT8, EPI, NORM>(a, st);
+    return launch_generic<QT_Q4, EPI, NORM>(a, st);
+}
+
+extern "C" hipError_t qt_launch_mv(int prec, int epi, int norm, const float *vin, const float *nw,
+                                   float eps, const uint8_t *w, const float *scale,
+                                   const uint16_t *s16, int rows, int cols, float *out,
+                                   float *resid, const float *bias, hipStream_t st) {
+    QtMvArgs a;
+    a.vin = vin; a.nw = nw; a.eps = eps;
+    a.M.w = w; a.M.scale = scale; a.M.s16 = s16; a.M.rows = rows; a.M.cols = cols;
+    a.out = out; a.resid = resid; a.bias = bias;
+    if (rows <= 0 || cols <= 0) return hipErrorInvalidValue;
+    if (epi == QT_EPI_SWIGLU && (rows & 1)) return hipErrorInvalidValue;
+    if (prec == QT_Q4 && (cols % 32)) return hipErrorInvalidValue;
+    if ((size_t)cols * sizeof(float) > 64 * 1024) return hipErrorInvalidValue;
+    switch (epi) {
+    case QT_EPI_STORE: return norm ? dispatch<QT_EPI_STORE, true>(prec, a, st) : dispatch<QT_EPI_STORE, false>(prec, a, st);
+    case QT_EPI_RESID: return norm ? dispatch<QT_EPI_RESID, true>(prec, a, st) : dispatch<QT_EPI_RESID, false>(prec, a, st);
+    case QT_EPI_SWIGLU: return norm ? dispatch<QT_EPI_SWIGLU, true>(prec, a, st) : dispatch<QT_EPI_SWIGLU, false>(prec, a, st);
+    case QT_EPI_BIAS: return norm ? dispatch<QT_EPI_BIAS, true>(prec, a, st) : dispatch<QT_EPI_BIAS, false>(prec, a, st);
+    }
+    return hipErrorInvalidValue;
+}

@@ -1,0 +1,282 @@
+// qt_misc.hip — small kernels around the decode step: final RMSNorm, greedy
+// codec-head / lm-head selection, embedding gather, load-time weight preparation
+// (int8 quantizer, q4_0 repack, int8 re-encoding) and a dequantiser for bit checks.
+#include "qt_device.h"
+
+// out = RMSNorm(x)*w (qwen_tts_kernels.c:292-382); optionally advance *d_pos by one
+// (the resident decode loop's device-side position).  One workgroup.
+__global__ __launch_bounds__(QT_WG) void k_rmsnorm(const float *x, const float *w, float *out, int n,
+                                                   float eps, int *d_pos) {
+    __shared__ float red[QT_WAVES];
+    float ss = 0.f;
+    for (int i = threadIdx.x; i < n; i += QT_WG) ss += x[i] * x[i];
+    float tot = block_sum(ss, red);
+    float inv = 1.0f / sqrtf(tot / (float)n + eps);
+    for (int i = threadIdx.x; i < n; i += QT_WG) out[i] = (x[i] * inv) * w[i];
+    if (d_pos && threadIdx.x == 0) *d_pos += 1;
+}
+
+extern "C" hipError_t qt_launch_rmsnorm(const float *x, const float *w, float *out, int n, float eps,
+                                        int *d_pos, hipStream_t st) {
+    hipLaunchKernelGGL(k_rmsnorm, dim3(1), dim3(QT_WG), 0, st, x, w, out, n, eps, d_pos);
+    return hipGetLastError();
+}
+
+// Per-row RMSNorm of `rows` vectors of length n (per-head norm, k.c:486-577), in place.
+__global__ __launch_bounds__(64) void k_rmsnorm_rows(float *x, const float *w, int n, float eps) {
+    float *r = x + (size_t)blockIdx.x * n;
+    float ss = 0.f;
+    for (int i = threadIdx.x; i < n; i += 64) ss += r[i] * r[i];
+    ss = group_sum<64>(ss);
+    float inv = 1.0f / sqrtf(ss / (float)n + eps);
+    for (int i = threadIdx.x; i < n; i += 64) r[i] = (r[i] * inv) * w[i];
+}
+
+extern "C" hipError_t qt_launch_rmsnorm_rows(float *x, const float *w, int rows, int n, float eps,
+                                             hipStream_t st) {
+    hipLaunchKernelGGL(k_rmsnorm_rows, dim3(rows), dim3(64), 0, st, x, w, n, eps);
+    return hipGetLastError();
+}
+
+// SwiGLU over interleaved pairs, out[i] = g/(1+expf(-g))*u (k.c:3857-3878).
+__global__ void k_swiglu(const float *gu, float *out, int n) {
+    int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) { float g = gu[2 * i], u = gu[2 * i + 1]; out[i] = g / (1.0f + expf(-g)) * u; }
+}
+extern "C" hipError_t qt_launch_swiglu(const float *gu, float *out, int n, hipStream_t st) {
+    hipLaunchKernelGGL(k_swiglu, dim3((n + 255) / 256), dim3(256), 0, st, gu, out, n);
+    return hipGetLastError();
+}
+
+// Greedy pick over `n` logits, lowest index on ties.  mode 0: plain argmax with the
+// fused argmax-matvec start value -1e30 (qwen_tts_kernels.c:4652-4759, CP lm heads);
+// mode 1: the codec-head rule of qwen_tts.c:1652-1663 + qwen_tts_sampling.c:175-182
+// (clip to +-100, tokens >= 2048 except EOS 2150 masked, EOS masked while the frame
+// index *d_frame < 2).  Writes the token to tok[0] and, when hist != NULL, to
+// hist[*d_frame % hist_len]; advance != 0 increments *d_frame.  When emb != NULL it
+// also gathers the next input embedding out[i] = bf16(emb[tok*emb_dim + i])
+// (qwen_tts.c:919-924).  One workgroup.
+__global__ __launch_bounds__(QT_WG) void k_select(const float *logits, int n, int mode, int *d_frame, int advance,
+                                                  int *tok, int *hist, int hist_len, const uint16_t *emb,
+                                                  int emb_dim, float *out) {
+    __shared__ float bv_s[QT_WAVES];
+    __shared__ int bi_s[QT_WAVES];
+    __shared__ int t_s;
+    const int frame = d_frame ? *d_frame : 0;
+    float bv = (mode == 0) ? -1e30f : -INFINITY;
+    int bi = 0x7FFFFFFF;
+    for (int i = threadIdx.x; i < n; i += QT_WG) {
+        float v = logits[i];
+        if (mode == 1) {
+            v = fminf(fmaxf(v, -100.0f), 100.0f);
+            if (i >= 2048 && i != 2150) v = -1e30f;
+            if (i == 2150 && frame < 2) v = -1e30f;
+        }
+        if (v > bv || (v == bv && i < bi)) { bv = v; bi = i; }
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        float ov = __shfl_xor(bv, o, 64);
+        int oi = __shfl_xor(bi, o, 64);
+        if (ov > bv || (ov == bv && oi < bi)) { bv = ov; bi = oi; }
+    }
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    if (lane == 0) { bv_s[wave] = bv; bi_s[wave] = bi; }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        float b = bv_s[0]; int ix = bi_s[0];
+        for (int w = 1; w < QT_WAVES; w++)
+            if (bv_s[w] > b || (bv_s[w] == b && bi_s[w] < ix)) { b = bv_s[w]; ix = bi_s[w]; }
+        if (ix == 0x7FFFFFFF) ix = 0;   // nothing beat the start value: index 0
+        tok[0] = ix;
+        if (hist) hist[frame % hist_len] = ix;
+        t_s = ix;
+    }
+    __syncthreads();
+    if (emb) {
+        const int t = t_s;
+        for (int i = threadIdx.x; i < emb_dim; i += QT_WG) out[i] = bf16f(emb[(size_t)t * emb_dim + i]);
+    }
+    if (advance && d_frame && threadIdx.x == 0) *d_frame = frame + 1;
+}
+
+extern "C" hipError_t qt_launch_select(const float *logits, int n, int mode, int *d_frame, int advance, int *tok,
+                                       int *hist, int hist_len, const uint16_t *emb, int emb_dim, float *out,
+                                       hipStream_t st) {
+    hipLaunchKernelGGL(k_select, dim3(1), dim3(QT_WG), 0, st, logits, n, mode, d_frame, advance, tok, hist,
+                       hist_len, emb, emb_dim, out);
+    return hipGetLastError();
+}
+
+__global__ void k_copy_f32(const float *src, float *dst, int n) {
+    for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) dst[i] = src[i];
+}
+extern "C" hipError_t qt_launch_copy_f32(const float *src, float *dst, int n, hipStream_t st) {
+    hipLaunchKernelGGL(k_copy_f32, dim3(4), dim3(256), 0, st, src, dst, n);
+    return hipGetLastError();
+}
+
+// x[i] = bf16(table[tok*dim + i]), tok read on device (embedding gather).
+__global__ void k_gather(const int *tok, int tok_max, const uint16_t *table, int dim, float *out) {
+    const int t = *tok;
+    for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < dim; i += gridDim.x * blockDim.x)
+        out[i] = (t >= 0 && t < tok_max) ? bf16f(table[(size_t)t * dim + i]) : 0.0f;
+}
+extern "C" hipError_t qt_launch_gather(const int *tok, int tok_max, const uint16_t *table, int dim, float *out,
+                                       hipStream_t st) {
+    hipLaunchKernelGGL(k_gather, dim3(4), dim3(256), 0, st, tok, tok_max, table, dim, out);
+    return hipGetLastError();
+}
+
+// ---- load-time weight preparation ------------------------------------------------
+
+// Per-row absmax int8 quantizer, bit-exact with the reference binary
+// (qwen_tts_kernels.c:2143-2238 compiled with -O3 -ffast-math): scale = amax*(1/127)
+// (the constant division becomes a multiply by the f32 reciprocal), inv = 127/amax,
+// q = round-half-even(v*inv) on the 8-wide body, roundf on the cols%8 tail, saturated.
+// Output in the device encoding u = q ^ 0x80.  One workgroup per row.
+__global__ __launch_bounds__(QT_WG) void k_quant_int8(const uint16_t *src, int cols, uint8_t *dst, float *scale) {
+    __shared__ float red[QT_WAVES];
+    const uint16_t *row = src + (size_t)blockIdx.x * cols;
+    float amax = 0.f;
+    for (int k = threadIdx.x; k < cols; k += QT_WG) amax = fmaxf(amax, fabsf(bf16f(row[k])));
+    amax = group_max<64>(amax);
+    __syncthreads();
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = amax;
+    __syncthreads();
+    amax = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    const float s = amax * (1.0f / 127.0f);
+    const float inv = (s > 0.f) ? 127.0f / amax : 0.f;
+    if (threadIdx.x == 0) scale[blockIdx.x] = s;
+    const int body = cols - cols % 8;
+    for (int k = threadIdx.x; k < cols; k += QT_WG) {
+        const float p = bf16f(row[k]) * inv;
+        int v = (k < body) ? (int)__builtin_rintf(p) : (int)roundf(p);
+        v = v < -128 ? -128 : (v > 127 ? 127 : v);
+        dst[(size_t)blockIdx.x * cols + k] = (uint8_t)((v & 0xFF) ^ 0x80);
+    }
+}
+extern "C" hipError_t qt_launch_quant_int8(const uint16_t *src, int rows, int cols, uint8_t *dst, float *scale,
+                                           hipStream_t st) {
+    hipLaunchKernelGGL(k_quant_int8, dim3(rows), dim3(QT_WG), 0, st, src, cols, dst, scale);
+    return hipGetLastError();
+}
+
+// Reference int8 bytes q -> device encoding q ^ 0x80 (n bytes, in place).
+__global__ void k_flip_sign(uint8_t *p, size_t n) {
+    size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    size_t stride = (size_t)gridDim.x * blockDim.x;
+    for (; i < n; i += stride) p[i] ^= 0x80;
+}
+extern "C" hipError_t qt_launch_flip_sign(uint8_t *p, size_t n, hipStream_t st) {
+    hipLaunchKernelGGL(k_flip_sign, dim3(1024), dim3(256), 0, st, p, n);
+    return hipGetLastError();
+}
+
+// Reference q4_0 blocks {u16 scale; u8 qs[16]} (18 B, qwen_tts_kernels.h:206-210) ->
+// qs rows [rows][cols/2] + f16 scale bits [rows][cols/32].  Pure byte moves.
+__global__ void k_repack_q4(const uint8_t *blocks, size_t nblocks, uint8_t *qs, uint16_t *s16) {
+    size_t b = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    size_t stride = (size_t)gridDim.x * blockDim.x;
+    for (; b < nblocks; b += stride) {
+        const uint8_t *src = blocks + b * 18;
+        s16[b] = (uint16_t)(src[0] | (src[1] << 8));
+        uint8_t *d = qs + b * 16;
+#pragma unroll
+        for (int i = 0; i < 16; i++) d[i] = src[2 + i];
+    }
+}
+extern "C" hipError_t qt_launch_repack_q4(const uint8_t *blocks, size_t nblocks, uint8_t *qs, uint16_t *s16,
+                                          hipStream_t st) {
+    hipLaunchKernelGGL(k_repack_q4, dim3(1024), dim3(256), 0, st, blocks, nblocks, qs, s16);
+    return hipGetLastError();
+}
+
+// Weighted-LSQ q4_0 quantizer (qwen_tts_kernels.c:2662-2726) into the device layout
+// (qs rows + f16 scale bits).  One thread per 32-block; double accumulation in index
+// order.  The reference binary's vectorised double sums may round differently in the
+// last place, so block scales match it except on rare f16 rounding ties.
+__device__ uint16_t ref_f32_to_f16(float f) {
+    uint32_t u = __float_as_uint(f);
+    uint32_t sign = (u >> 16) & 0x8000u;
+    int e = (int)((u >> 23) & 0xFF) - 112;
+    uint32_t m = u & 0x7FFFFFu;
+    if (e >= 31) return (uint16_t)(sign | 0x7C00u);
+    if (e <= 0) {
+        if (e < -10) return (uint16_t)sign;
+        uint32_t full = m | 0x800000u, sh = (uint32_t)(14 - e);
+        uint32_t r = full >> sh;
+        if ((full >> (sh - 1)) & 1u) r++;
+        return (uint16_t)(sign | r);
+    }
+    uint32_t r = sign | ((uint32_t)e << 10) | (m >> 13);
+    if (m & 0x1000u) r++;
+    return (uint16_t)r;
+}
+
+__global__ void k_quant_q4(const uint16_t *src, int rows, int cols, uint8_t *qs, uint16_t *s16) {
+    const int nb = cols / 32;
+    size_t b = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (b >= (size_t)rows * nb) return;
+    const uint16_t *blk = src + b * 32;   // rows are contiguous: block b = row*nb + j
+    float v[32], amax = 0.f, vmax = 0.f;
+    for (int i = 0; i < 32; i++) {
+        v[i] = bf16f(blk[i]);
+        float a = fabsf(v[i]);
+        if (a > amax) { amax = a; vmax = v[i]; }
+    }
+    const float isc = (vmax != 0.f) ? -8.0f / vmax : 0.f;
+    int q[32];
+    double num = 0.0, den = 0.0;
+    for (int i = 0; i < 32; i++) {
+        int t = (int)roundf(v[i] * isc);
+        t = t < -8 ? -8 : (t > 7 ? 7 : t);
+        q[i] = t;
+        double w = (double)v[i] * (double)v[i];
+        num = __dadd_rn(num, __dmul_rn(__dmul_rn(w, (double)v[i]), (double)t));
+        den = __dadd_rn(den, __dmul_rn(__dmul_rn(w, (double)t), (double)t));
+    }
+    const float s = (den > 0.0) ? (float)(num / den) : 0.f;
+    s16[b] = ref_f32_to_f16(s);
+    uint8_t *d = qs + b * 16;
+    for (int i = 0; i < 16; i++) d[i] = (uint8_t)((q[2 * i] + 8) | ((q[2 * i + 1] + 8) << 4));
+}
+extern "C" hipError_t qt_launch_quant_q4(const uint16_t *src, int rows, int cols, uint8_t *qs, uint16_t *s16,
+                                         hipStream_t st) {
+    size_t nb = (size_t)rows * (cols / 32);
+    hipLaunchKernelGGL(k_quant_q4, dim3((unsigned)((nb + 255) / 256)), dim3(256), 0, st, src, rows, cols, qs, s16);
+    return hipGetLastError();
+}
+
+// Dequantise rows [r0, r0+n) of a device matrix to f32 (bit-exactness checks):
+// bf16 -> f32 shift; int8 -> (float)q * scale; q4 -> (nib-8) * f16(scale).
+__global__ void k_dequant(int prec, const uint8_t *w, const float *scale, const uint16_t *s16, int cols,
+                          int r0, int n, float *out) {
+    size_t total = (size_t)n * cols;
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += (size_t)gridDim.x * blockDim.x) {
+        const int r = r0 + (int)(i / cols), k = (int)(i % cols);
+        float v;
+        if (prec == QT_BF16) v = bf16f(reinterpret_cast<const uint16_t *>(w)[(size_t)r * cols + k]);
+        else if (prec == QT_INT8) v = (float)((int)w[(size_t)r * cols + k] - 128) * scale[r];
+        else {
+            const uint8_t byte = w[(size_t)r * (cols / 2) + k / 2];
+            const int nib = (k & 1) ? (byte >> 4) : (byte & 0xF);
+            v = (float)(nib - 8) * ref_f16_to_f32(s16[(size_t)r * (cols / 32) + k / 32]);
+        }
+        out[i] = v;
+    }
+}
+extern "C" hipError_t qt_launch_dequant(int prec, const uint8_t *w, const float *scale, const uint16_t *s16,
+                                        int cols, int r0, int n, float *out, hipStream_t st) {
+    hipLaunchKernelGGL(k_dequant, dim3(512), dim3(256), 0, st, prec, w, scale, s16, cols, r0, n, out);
+    return hipGetLastError();
+}
+
+// Fill a buffer with zeros (graph-capturable replacement for hipMemsetAsync).
+__global__ void k_zero_u32(uint32_t *p, size_t n) {
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x) p[i] = 0;
+}
+extern "C" hipError_t qt_launch_zero_u32(uint32_t *p, size_t n, hipStream_t st) {
+    hipLaunchKernelGGL(k_zero_u32, dim3(64), dim3(256), 0, st, p, n);
+    return hipGetLastError();
+}

@@ -1,0 +1,1053 @@
+/*
+ * qwen_tts_hip.c — host side of the MI355X decode-step library (C, HIP runtime API).
+ *
+ * What the reference's qwen_tts_cuda_talker.cu host code does (resident weights + KV,
+ * one graph per step, device-side position; qwen_tts_cuda_talker.cu:313-438), redone
+ * for gfx950:
+ *   - weights are uploaded once into the device encodings of qt_device.h (Q|K|V rows
+ *     concatenated into one matrix per layer so the QKV projection is one launch;
+ *     int8 re-encoded q^0x80; q4_0 split into qs rows + f16 scale bits);
+ *   - the KV cache stays bf16 on the device (the reference keeps f32 with truncated
+ *     mantissas, qwen_tts_cuda_talker.cu:203-208, 350-351), head-major
+ *     [layer][kv_head][kv_max][128], so upload is a strided memcpy of the host bits and
+ *     a chunk of keys of one head is contiguous;
+ *   - a layer is 5 launches: norm+QKV, attention (q/k norm + RoPE + KV append +
+ *     split-K + merge), O+residual, norm+gate_up+SwiGLU, down+residual; the step
+ *     (n_layers*5 + 1 launches) is captured once into a hipGraph and replayed with the
+ *     position read on the device.
+ * Every HIP call is checked; a failure marks the state dead and is reported through
+ * qwen_hip_last_error().
+ */
+#include "qwen_tts_hip.h"
+#include "qt_launch.h"
+
+#include <hip/hip_runtime_api.h>
+#include <math.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+
+static __thread char g_err[512];
+const char *qwen_hip_last_error(void) { return g_err; }
+
+#define SETERR(...) do { snprintf(g_err, sizeof g_err, __VA_ARGS__); fprintf(stderr, "[qwen_hip] %s\n", g_err); } while (0)
+#define HCK(call) do { hipError_t e_ = (call); if (e_ != hipSuccess) { \
+    SETERR("%s:%d %s -> %s", __FILE__, __LINE__, #call, hipGetErrorString(e_)); goto fail; } } while (0)
+#define REQ(cond, ...) do { if (!(cond)) { SETERR(__VA_ARGS__); goto fail; } } while (0)
+
+/* ---- device matrices --------------------------------------------------------------- */
+
+typedef struct {
+    int prec, rows, cols;
+    uint8_t *w;        /* chunk rows (bf16 bits | q^0x80 | q4 qs) */
+    float *scale;      /* int8 */
+    uint16_t *s16;     /* q4 f16 scale bits */
+} dmat_t;
+
+static size_t row_bytes(int prec, int cols) {
+    return prec == QWEN_HIP_BF16 ? (size_t)cols * 2 : prec == QWEN_HIP_INT8 ? (size_t)cols : (size_t)cols / 2;
+}
+
+static int dmat_alloc(dmat_t *m, int prec, int rows, int cols) {
+    memset(m, 0, sizeof *m);
+    m->prec = prec; m->rows = rows; m->cols = cols;
+    HCK(hipMalloc((void **)&m->w, row_bytes(prec, cols) * rows));
+    if (prec == QWEN_HIP_INT8) HCK(hipMalloc((void **)&m->scale, (size_t)rows * sizeof(float)));
+    if (prec == QWEN_HIP_Q4_0) HCK(hipMalloc((void **)&m->s16, (size_t)rows * (cols / 32) * sizeof(uint16_t)));
+    return 0;
+fail:
+    return -1;
+}
+
+static void dmat_free(dmat_t *m) {
+    if (m->w) (void)hipFree(m->w);
+    if (m->scale) (void)hipFree(m->scale);
+    if (m->s16) (void)hipFree(m->s16);
+    memset(m, 0, sizeof *m);
+}
+
+/* Copy a source matrix (reference host layout, precision src_prec, host or device
+ * memory) into rows [r0, r0+rows) of m, converting to m->prec on the device.
+ * tmp: device scratch of at least rows*cols*2 bytes. */
+static int dmat_put(dmat_t *m, int r0, const qwen_hip_mat_t *src, int src_prec, int rows, hipStream_t st, void *tmp) {
+    const int cols = m->cols;
+    REQ(src && src->w, "missing weight pointer");
+    if (src_prec == m->prec) {
+        if (m->prec == QWEN_HIP_BF16) {
+            HCK(hipMemcpyAsync(m->w + (size_t)r0 * cols * 2, src->w, (size_t)rows * cols * 2, hipMemcpyDefault, st));
+        } else if (m->prec == QWEN_HIP_INT8) {
+            REQ(src->scale, "int8 weight without scale");
+            HCK(hipMemcpyAsync(m->w + (size_t)r0 * cols, src->w, (size_t)rows * cols, hipMemcpyDefault, st));
+            HCK(qt_launch_flip_sign(m->w + (size_t)r0 * cols, (size_t)rows * cols, st));
+            HCK(hipMemcpyAsync(m->scale + r0, src->scale, (size_t)rows * sizeof(float), hipMemcpyDefault, st));
+        } else {
+            size_t nb = (size_t)rows * (cols / 32);
+            HCK(hipMemcpyAsync(tmp, src->w, nb * 18, hipMemcpyDefault, st));
+            HCK(qt_launch_repack_q4((const uint8_t *)tmp, nb, m->w + (size_t)r0 * (cols / 2),
+                                    m->s16 + (size_t)r0 * (cols / 32), st));
+        }
+    } else {
+        REQ(src_prec == QWEN_HIP_BF16, "can only quantize from bf16 (got prec %d -> %d)", src_prec, m->prec);
+        HCK(hipMemcpyAsync(tmp, src->w, (size_t)rows * cols * 2, hipMemcpyDefault, st));
+        if (m->prec == QWEN_HIP_INT8)
+            HCK(qt_launch_quant_int8((const uint16_t *)tmp, rows, cols, m->w + (size_t)r0 * cols, m->scale + r0, st));
+        else
+            HCK(qt_launch_quant_q4((const uint16_t *)tmp, rows, cols, m->w + (size_t)r0 * (cols / 2),
+                                   m->s16 + (size_t)r0 * (cols / 32), st));
+    }
+    HCK(hipStreamSynchronize(st));   /* tmp is reused by the next put */
+    return 0;
+fail:
+    return -1;
+}
+
+static hipError_t mv(const dmat_t *m, int epi, int norm, const float *vin, const float *nw, float eps,
+                     float *out, float *resid, const float *bias, hipStream_t st) {
+    return qt_launch_mv(m->prec, epi, norm, vin, nw, eps, m->w, m->scale, m->s16, m->rows, m->cols,
+                        out, resid, bias, st);
+}
+
+static float *up_f32(const float *src, size_t n, hipStream_t st) {
+    float *d = NULL;
+    if (!src) { SETERR("missing f32 tensor"); return NULL; }
+    if (hipMalloc((void **)&d, n * sizeof(float)) != hipSuccess) { SETERR("hipMalloc %zu f32 failed", n); return NULL; }
+    if (hipMemcpyAsync(d, src, n * sizeof(float), hipMemcpyDefault, st) != hipSuccess) {
+        (void)hipFree(d); SETERR("upload f32 failed"); return NULL;
+    }
+    return d;
+}
+
+/* ---- one stack of transformer layers on the device (Talker: 28, CP: 5) ------------ */
+
+typedef struct {
+    int H, F, nh, nkv, hd, L, kv_max, qd, kvd, prec, rope_len, attn_G;
+    float eps;
+    dmat_t *qkv, *o, *gu, *dn;
+    float **in_norm, **post_norm, **qn, **kn;
+    float *final_norm, *rope_cos, *rope_sin;
+    uint16_t *kc, *vc;         /* [L][nkv][kv_max][hd] */
+    float *qkvbuf, *attn, *hbuf;
+    float *part; unsigned *cnt;
+} stack_t;
+
+static void stack_free(stack_t *s) {
+    for (int l = 0; l < s->L; l++) {
+        if (s->qkv) dmat_free(&s->qkv[l]);
+        if (s->o) dmat_free(&s->o[l]);
+        if (s->gu) dmat_free(&s->gu[l]);
+        if (s->dn) dmat_free(&s->dn[l]);
+        if (s->in_norm && s->in_norm[l]) (void)hipFree(s->in_norm[l]);
+        if (s->post_norm && s->post_norm[l]) (void)hipFree(s->post_norm[l]);
+        if (s->qn && s->qn[l]) (void)hipFree(s->qn[l]);
+        if (s->kn && s->kn[l]) (void)hipFree(s->kn[l]);
+    }
+    free(s->qkv); free(s->o); free(s->gu); free(s->dn);
+    free(s->in_norm); free(s->post_norm); free(s->qn); free(s->kn);
+    void *bufs[] = {s->final_norm, s->rope_cos, s->rope_sin, s->kc, s->vc, s->qkvbuf, s->attn, s->hbuf, s->part, s->cnt};
+    for (size_t i = 0; i < sizeof bufs / sizeof bufs[0]; i++) if (bufs[i]) (void)hipFree(bufs[i]);
+    memset(s, 0, sizeof *s);
+}
+
+static int stack_init(stack_t *s, const qwen_hip_talker_desc_t *d, hipStream_t st) {
+    void *tmp = NULL;
+    memset(s, 0, sizeof *s);
+    REQ(d && d->layers, "null descriptor");
+    REQ(d->head_dim == 128, "head_dim %d unsupported (128 only)", d->head_dim);
+    REQ(d->n_kv_heads > 0 && d->n_heads % d->n_kv_heads == 0, "bad head counts %d/%d", d->n_heads, d->n_kv_heads);
+    REQ(d->kv_max > 0 && d->kv_max <= 65536, "kv_max %d out of range", d->kv_max);
+    REQ(d->rope_cos && d->rope_sin && d->rope_len > 0, "missing rope tables");
+    REQ(d->prec >= 0 && d->prec <= 2, "bad prec %d", d->prec);
+    s->H = d->hidden; s->F = d->inter; s->nh = d->n_heads; s->nkv = d->n_kv_heads; s->hd = d->head_dim;
+    s->L = d->n_layers; s->kv_max = d->kv_max; s->eps = d->eps;
+    s->qd = s->nh * s->hd; s->kvd = s->nkv * s->hd;
+    s->prec = (d->quantize_to >= 0) ? d->quantize_to : d->prec;
+    REQ(s->prec == d->prec || d->prec == QWEN_HIP_BF16, "quantize_to needs bf16 source weights");
+    if (s->prec == QWEN_HIP_Q4_0)
+        REQ(s->H % 32 == 0 && s->F % 32 == 0 && s->qd % 32 == 0, "q4_0 needs dims divisible by 32");
+    s->rope_len = d->rope_len < d->kv_max ? d->rope_len : d->kv_max;
+    /* split-K grid: short caches (the CP's <= 64 positions) use one chunk per kv head */
+    s->attn_G = s->kv_max <= 128 ? 1 : qt_attn_grid(s->kv_max);
+    const int L = s->L, H = s->H, F = s->F;
+    s->qkv = calloc(L, sizeof(dmat_t)); s->o = calloc(L, sizeof(dmat_t));
+    s->gu = calloc(L, sizeof(dmat_t)); s->dn = calloc(L, sizeof(dmat_t));
+    s->in_norm = calloc(L, sizeof(float *)); s->post_norm = calloc(L, sizeof(float *));
+    s->qn = calloc(L, sizeof(float *)); s->kn = calloc(L, sizeof(float *));
+    REQ(s->qkv && s->o && s->gu && s->dn && s->in_norm && s->post_norm && s->qn && s->kn, "host alloc failed");
+    size_t tmp_bytes = (size_t)2 * F * H * 2;
+    if ((size_t)(s->qd + 2 * s->kvd) * H * 2 > tmp_bytes) tmp_bytes = (size_t)(s->qd + 2 * s->kvd) * H * 2;
+    HCK(hipMalloc(&tmp, tmp_bytes));
+    for (int l = 0; l < L; l++) {
+        const qwen_hip_layer_t *ly = &d->layers[l];
+        REQ(dmat_alloc(&s->qkv[l], s->prec, s->qd + 2 * s->kvd, H) == 0, "alloc qkv");
+        REQ(dmat_put(&s->qkv[l], 0, &ly->q, d->prec, s->qd, st, tmp) == 0, "upload q (layer %d)", l);
+        REQ(dmat_put(&s->qkv[l], s->qd, &ly->k, d->prec, s->kvd, st, tmp) == 0, "upload k (layer %d)", l);
+        REQ(dmat_put(&s->qkv[l], s->qd + s->kvd, &ly->v, d->prec, s->kvd, st, tmp) == 0, "upload v (layer %d)", l);
+        REQ(dmat_alloc(&s->o[l], s->prec, H, s->qd) == 0, "alloc o");
+        REQ(dmat_put(&s->o[l], 0, &ly->o, d->prec, H, st, tmp) == 0, "upload o (layer %d)", l);
+        REQ(dmat_alloc(&s->gu[l], s->prec, 2 * F, H) == 0, "alloc gate_up");
+        REQ(dmat_put(&s->gu[l], 0, &ly->gate_up, d->prec, 2 * F, st, tmp) == 0, "upload gate_up (layer %d)", l);
+        REQ(dmat_alloc(&s->dn[l], s->prec, H, F) == 0, "alloc down");
+        REQ(dmat_put(&s->dn[l], 0, &ly->down, d->prec, H, st, tmp) == 0, "upload down (layer %d)", l);
+        REQ((s->in_norm[l] = up_f32(ly->input_norm, H, st)) != NULL, "input_norm %d", l);
+        REQ((s->post_norm[l] = up_f32(ly->post_attn_norm, H, st)) != NULL, "post_norm %d", l);
+        REQ((s->qn[l] = up_f32(ly->q_norm, s->hd, st)) != NULL, "q_norm %d", l);
+        REQ((s->kn[l] = up_f32(ly->k_norm, s->hd, st)) != NULL, "k_norm %d", l);
+    }
+    REQ((s->final_norm = up_f32(d->final_norm, H, st)) != NULL, "final_norm");
+    REQ((s->rope_cos = up_f32(d->rope_cos, (size_t)s->rope_len * (s->hd / 2), st)) != NULL, "rope_cos");
+    REQ((s->rope_sin = up_f32(d->rope_sin, (size_t)s->rope_len * (s->hd / 2), st)) != NULL, "rope_sin");
+    size_t kvn = (size_t)L * s->nkv * s->kv_max * s->hd;
+    HCK(hipMalloc((void **)&s->kc, kvn * 2));
+    HCK(hipMalloc((void **)&s->vc, kvn * 2));
+    HCK(hipMemsetAsync(s->kc, 0, kvn * 2, st));
+    HCK(hipMemsetAsync(s->vc, 0, kvn * 2, st));
+    HCK(hipMalloc((void **)&s->qkvbuf, (size_t)(s->qd + 2 * s->kvd) * sizeof(float)));
+    HCK(hipMalloc((void **)&s->attn, (size_t)s->qd * sizeof(float)));
+    HCK(hipMalloc((void **)&s->hbuf, (size_t)(F > H ? F : H) * sizeof(float)));
+    HCK(hipMalloc((void **)&s->part, (size_t)s->nkv * s->attn_G * (s->nh / s->nkv) * 130 * sizeof(float)));
+    HCK(hipMalloc((void **)&s->cnt, (size_t)s->nkv * sizeof(unsigned)));
+    HCK(hipMemsetAsync(s->cnt, 0, (size_t)s->nkv * sizeof(unsigned), st));
+    HCK(hipStreamSynchronize(st));
+    (void)hipFree(tmp);
+    return 0;
+fail:
+    if (tmp) (void)hipFree(tmp);
+    stack_free(s);
+    return -1;
+}
+
+/* The layers of one pass: x (device residual) in/out, position read from d_pos.
+ * Mirrors qwen_talker_step's layer loop (qwen_tts_talker.c:580-690) and
+ * cp_layer_body (qwen_tts_code_predictor.c:595-717). */
+static hipError_t stack_body(stack_t *s, float *x, const int *d_pos, hipStream_t st) {
+    hipError_t e;
+    const float scale = 1.0f / sqrtf((float)s->hd);
+    for (int l = 0; l < s->L; l++) {
+        const size_t lay = (size_t)l * s->nkv * s->kv_max * s->hd;
+        if ((e = mv(&s->qkv[l], QT_EPI_STORE, 1, x, s->in_norm[l], s->eps, s->qkvbuf, NULL, NULL, st))) return e;
+        if ((e = qt_launch_attn(1, s->qkvbuf, s->qn[l], s->kn[l], s->rope_cos, s->rope_sin, s->eps, d_pos, 0,
+                                s->kc + lay, s->vc + lay, s->hd, (long long)s->kv_max * s->hd, s->nh, s->nkv,
+                                s->hd, scale, s->part, s->cnt, s->attn_G, s->attn, st))) return e;
+        if ((e = mv(&s->o[l], QT_EPI_RESID, 0, s->attn, NULL, s->eps, NULL, x, NULL, st))) return e;
+        if ((e = mv(&s->gu[l], QT_EPI_SWIGLU, 1, x, s->post_norm[l], s->eps, s->hbuf, NULL, NULL, st))) return e;
+        if ((e = mv(&s->dn[l], QT_EPI_RESID, 0, s->hbuf, NULL, s->eps, NULL, x, NULL, st))) return e;
+    }
+    return hipSuccess;
+}
+
+/* ---- Talker state ------------------------------------------------------------------ */
+
+typedef struct {
+    stack_t s;
+    hipStream_t st;
+    float *io;              /* device [hidden_out H | x H] */
+    int *d_pos;             /* device: position of the next step */
+    int *d_frame, *d_tok, *d_hist;
+    float *h_in, *h_out;    /* pinned: embed in; [hidden | x] out */
+    int *h_pos;
+    hipGraphExec_t exec, gexec;
+    int graph_ready, ggraph_ready;
+    int dev_pos;            /* host mirror of *d_pos (-1 unknown) */
+    int dead;
+    /* greedy loop */
+    const uint16_t *head_host, *emb_host;
+    uint16_t *codec_head, *codec_emb;
+    int codec_vocab;
+    float *logits;
+    dmat_t head_m;
+    int hist_len;
+} talker_t;
+
+static void talker_destroy(talker_t *t) {
+    if (!t) return;
+    if (t->graph_ready) (void)hipGraphExecDestroy(t->exec);
+    if (t->ggraph_ready) (void)hipGraphExecDestroy(t->gexec);
+    stack_free(&t->s);
+    void *bufs[] = {t->io, t->d_pos, t->d_frame, t->d_tok, t->d_hist, t->codec_head, t->codec_emb, t->logits};
+    for (size_t i = 0; i < sizeof bufs / sizeof bufs[0]; i++) if (bufs[i]) (void)hipFree(bufs[i]);
+    if (t->h_in) (void)hipHostFree(t->h_in);
+    if (t->h_out) (void)hipHostFree(t->h_out);
+    if (t->h_pos) (void)hipHostFree(t->h_pos);
+    if (t->st) (void)hipStreamDestroy(t->st);
+    free(t);
+}
+
+void *qwen_hip_talker_init(const qwen_hip_talker_desc_t *desc) {
+    talker_t *t = calloc(1, sizeof *t);
+    if (!t) { SETERR("out of host memory"); return NULL; }
+    HCK(hipStreamCreateWithFlags(&t->st, hipStreamNonBlocking));
+    if (stack_init(&t->s, desc, t->st) != 0) goto fail;   /* g_err already set */
+    const int H = t->s.H;
+    t->hist_len = 4096;
+    HCK(hipMalloc((void **)&t->io, (size_t)2 * H * sizeof(float)));
+    HCK(hipMalloc((void **)&t->d_pos, sizeof(int)));
+    HCK(hipMalloc((void **)&t->d_frame, sizeof(int)));
+    HCK(hipMalloc((void **)&t->d_tok, sizeof(int)));
+    HCK(hipMalloc((void **)&t->d_hist, (size_t)t->hist_len * sizeof(int)));
+    HCK(hipHostMalloc((void **)&t->h_in, (size_t)H * sizeof(float), hipHostMallocDefault));
+    HCK(hipHostMalloc((void **)&t->h_out, (size_t)2 * H * sizeof(float), hipHostMallocDefault));
+    HCK(hipHostMalloc((void **)&t->h_pos, 4 * sizeof(int), hipHostMallocDefault));
+    HCK(hipMemsetAsync(t->io, 0, (size_t)2 * H * sizeof(float), t->st));
+    HCK(hipStreamSynchronize(t->st));
+    t->dev_pos = -1;
+    return t;
+fail:
+    talker_destroy(t);
+    return NULL;
+}
+
+void qwen_hip_talker_free(void *state) { talker_destroy((talker_t *)state); }
+void *qwen_hip_talker_stream(void *state) { return state ? (void *)((talker_t *)state)->st : NULL; }
+
+static hipError_t talker_body(talker_t *t) {
+    hipError_t e;
+    float *x = t->io + t->s.H;
+    if ((e = stack_body(&t->s, x, t->d_pos, t->st))) return e;
+    /* final norm into io[0:H); advances *d_pos for the next step */
+    return qt_launch_rmsnorm(x, t->s.final_norm, t->io, t->s.H, t->s.eps, t->d_pos, t->st);
+}
+
+static int capture(hipStream_t st, hipGraphExec_t *exec, hipError_t (*body)(void *), void *arg) {
+    hipGraph_t g = NULL;
+    hipError_t be;
+    HCK(hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal));
+    be = body(arg);
+    {
+        hipError_t ee = hipStreamEndCapture(st, &g);
+        if (be != hipSuccess || ee != hipSuccess) {
+            SETERR("graph capture failed: %s / %s", hipGetErrorString(be), hipGetErrorString(ee));
+            if (g) (void)hipGraphDestroy(g);
+            return -1;
+        }
+    }
+    HCK(hipGraphInstantiate(exec, g, NULL, NULL, 0));
+    (void)hipGraphDestroy(g);
+    return 0;
+fail:
+    if (g) (void)hipGraphDestroy(g);
+    return -1;
+}
+
+static hipError_t talker_body_cb(void *a) { return talker_body((talker_t *)a); }
+
+static int talker_set_pos(talker_t *t, int pos) {
+    if (t->dev_pos == pos) return 0;
+    t->h_pos[0] = pos;
+    HCK(hipMemcpyAsync(t->d_pos, t->h_pos, sizeof(int), hipMemcpyHostToDevice, t->st));
+    /* h_pos is reused: make sure the copy has consumed it before the host changes it */
+    HCK(hipStreamSynchronize(t->st));
+    t->dev_pos = pos;
+    return 0;
+fail:
+    return -1;
+}
+
+static int talker_step_impl(talker_t *t, const float *embed, float *hidden_out, int pos, int use_graph) {
+    if (!t || t->dead) { SETERR("talker state is dead or NULL"); return -1; }
+    const int H = t->s.H;
+    REQ(pos >= 0 && pos < t->s.kv_max && pos < t->s.rope_len, "pos %d out of range (kv_max %d, rope %d)",
+        pos, t->s.kv_max, t->s.rope_len);
+    if (talker_set_pos(t, pos) != 0) goto fail;
+    memcpy(t->h_in, embed, (size_t)H * sizeof(float));
+    HCK(hipMemcpyAsync(t->io + H, t->h_in, (size_t)H * sizeof(float), hipMemcpyHostToDevice, t->st));
+    if (use_graph) {
+        if (!t->graph_ready) {
+            if (capture(t->st, &t->exec, talker_body_cb, t) != 0) goto fail;
+            t->graph_ready = 1;
+        }
+        HCK(hipGraphLaunch(t->exec, t->st));
+    } else {
+        HCK(talker_body(t));
+    }
+    HCK(hipMemcpyAsync(t->h_out, t->io, (size_t)2 * H * sizeof(float), hipMemcpyDeviceToHost, t->st));
+    HCK(hipStreamSynchronize(t->st));
+    t->dev_pos = pos + 1;
+    if (hidden_out) memcpy(hidden_out, t->h_out, (size_t)H * sizeof(float));
+    return 0;
+fail:
+    if (t) { t->dead = 1; t->dev_pos = -1; }
+    return -1;
+}
+
+int qwen_hip_talker_step(void *state, const float *embed, float *hidden_out, int pos) {
+    return talker_step_impl((talker_t *)state, embed, hidden_out, pos, 1);
+}
+int qwen_hip_talker_step_nograph(void *state, const float *embed, float *hidden_out, int pos) {
+    return talker_step_impl((talker_t *)state, embed, hidden_out, pos, 0);
+}
+
+void qwen_hip_talker_get_dec_x(void *state, float *out) {
+    talker_t *t = (talker_t *)state;
+    if (t && out) memcpy(out, t->h_out + t->s.H, (size_t)t->s.H * sizeof(float));
+}
+
+int qwen_hip_talker_upload_kv(void *state, const uint16_t *kv_k, const uint16_t *kv_v, int host_kv_max,
+                              int prefill_len) {
+    talker_t *t = (talker_t *)state;
+    if (!t || t->dead) { SETERR("talker state is dead or NULL"); return -1; }
+    stack_t *s = &t->s;
+    if (prefill_len <= 0) return 0;
+    REQ(prefill_len <= s->kv_max && prefill_len <= host_kv_max, "prefill_len %d exceeds kv_max", prefill_len);
+    for (int l = 0; l < s->L; l++)
+        for (int g = 0; g < s->nkv; g++) {
+            size_t dst = (((size_t)l * s->nkv + g) * s->kv_max) * s->hd;
+            size_t src = (size_t)l * host_kv_max * s->kvd + (size_t)g * s->hd;
+            HCK(hipMemcpy2DAsync(s->kc + dst, s->hd * 2, kv_k + src, (size_t)s->kvd * 2, s->hd * 2, prefill_len,
+                                 hipMemcpyDefault, t->st));
+            HCK(hipMemcpy2DAsync(s->vc + dst, s->hd * 2, kv_v + src, (size_t)s->kvd * 2, s->hd * 2, prefill_len,
+                                 hipMemcpyDefault, t->st));
+        }
+    HCK(hipStreamSynchronize(t->st));
+    return 0;
+fail:
+    return -1;
+}
+
+int qwen_hip_talker_download_kv(void *state, uint16_t *kv_k, uint16_t *kv_v, int host_kv_max, int n) {
+    talker_t *t = (talker_t *)state;
+    if (!t) { SETERR("NULL state"); return -1; }
+    stack_t *s = &t->s;
+    REQ(n >= 0 && n <= s->kv_max && n <= host_kv_max, "n %d out of range", n);
+    if (n == 0) return 0;
+    for (int l = 0; l < s->L; l++)
+        for (int g = 0; g < s->nkv; g++) {
+            size_t src = (((size_t)l * s->nkv + g) * s->kv_max) * s->hd;
+            size_t dst = (size_t)l * host_kv_max * s->kvd + (size_t)g * s->hd;
+            HCK(hipMemcpy2DAsync(kv_k + dst, (size_t)s->kvd * 2, s->kc + src, s->hd * 2, s->hd * 2, n,
+                                 hipMemcpyDefault, t->st));
+            HCK(hipMemcpy2DAsync(kv_v + dst, (size_t)s->kvd * 2, s->vc + src, s->hd * 2, s->hd * 2, n,
+                                 hipMemcpyDefault, t->st));
+        }
+    HCK(hipStreamSynchronize(t->st));
+    return 0;
+fail:
+    return -1;
+}
+
+/* -- resident greedy loop: step -> codec head -> greedy code0 -> next embed ---------- */
+
+static hipError_t greedy_body(void *a) {
+    talker_t *t = (talker_t *)a;
+    hipError_t e;
+    const int H = t->s.H;
+    if ((e = talker_body(t))) return e;
+    if ((e = mv(&t->head_m, QT_EPI_STORE, 0, t->io, NULL, t->s.eps, t->logits, NULL, NULL, t->st))) return e;
+    return qt_launch_select(t->logits, t->codec_vocab, 1, t->d_frame, 1, t->d_tok, t->d_hist, t->hist_len,
+                            t->codec_emb, H, t->io + H, t->st);
+}
+
+int qwen_hip_talker_greedy(void *state, const uint16_t *codec_head, const uint16_t *codec_emb, int codec_vocab,
+                           const float *embed, int pos, int frame0, int n_steps, int *tokens_out,
+                           float *hidden_out) {
+    talker_t *t = (talker_t *)state;
+    if (!t || t->dead) { SETERR("talker state is dead or NULL"); return -1; }
+    const int H = t->s.H;
+    REQ(codec_head && codec_emb && codec_vocab > 0, "missing codec head/embedding");
+    REQ(n_steps >= 0 && n_steps <= t->hist_len, "n_steps %d out of range", n_steps);
+    REQ(pos >= 0 && pos + n_steps <= t->s.kv_max && pos + n_steps <= t->s.rope_len, "positions exceed kv_max");
+    if (t->head_host != codec_head || t->emb_host != codec_emb || t->codec_vocab != codec_vocab) {
+        if (t->ggraph_ready) { (void)hipGraphExecDestroy(t->gexec); t->ggraph_ready = 0; }
+        dmat_free(&t->head_m);
+        if (t->codec_emb) (void)hipFree(t->codec_emb);
+        if (t->logits) (void)hipFree(t->logits);
+        t->codec_emb = NULL; t->logits = NULL;
+        qwen_hip_mat_t hm = {codec_head, NULL};
+        REQ(dmat_alloc(&t->head_m, QWEN_HIP_BF16, codec_vocab, H) == 0, "alloc codec head");
+        REQ(dmat_put(&t->head_m, 0, &hm, QWEN_HIP_BF16, codec_vocab, t->st, NULL) == 0, "upload codec head");
+        HCK(hipMalloc((void **)&t->codec_emb, (size_t)codec_vocab * H * 2));
+        HCK(hipMemcpy(t->codec_emb, codec_emb, (size_t)codec_vocab * H * 2, hipMemcpyDefault));
+        HCK(hipMalloc((void **)&t->logits, (size_t)codec_vocab * sizeof(float)));
+        t->head_host = codec_head; t->emb_host = codec_emb; t->codec_vocab = codec_vocab;
+    }
+    if (talker_set_pos(t, pos) != 0) goto fail;
+    t->h_pos[1] = frame0;
+    HCK(hipMemcpyAsync(t->d_frame, t->h_pos + 1, sizeof(int), hipMemcpyHostToDevice, t->st));
+    memcpy(t->h_in, embed, (size_t)H * sizeof(float));
+    HCK(hipMemcpyAsync(t->io + H, t->h_in, (size_t)H * sizeof(float), hipMemcpyHostToDevice, t->st));
+    if (!t->ggraph_ready) {
+        if (capture(t->st, &t->gexec, greedy_body, t) != 0) goto fail;
+        t->ggraph_ready = 1;
+    }
+    for (int i = 0; i < n_steps; i++) HCK(hipGraphLaunch(t->gexec, t->st));
+    {
+        int *hist = (int *)malloc((size_t)t->hist_len * sizeof(int));
+        REQ(hist, "host alloc");
+        hipError_t e1 = hipMemcpyAsync(hist, t->d_hist, (size_t)t->hist_len * sizeof(int), hipMemcpyDeviceToHost, t->st);
+        hipError_t e2 = hipMemcpyAsync(t->h_out, t->io, (size_t)2 * H * sizeof(float), hipMemcpyDeviceToHost, t->st);
+        hipError_t e3 = hipStreamSynchronize(t->st);
+        if (e1 || e2 || e3) { free(hist); SETERR("greedy readback failed"); goto fail; }
+        for (int i = 0; i < n_steps; i++) tokens_out[i] = hist[(frame0 + i) % t->hist_len];
+        free(hist);
+    }
+    t->dev_pos = pos + n_steps;
+    if (hidden_out) memcpy(hidden_out, t->h_out, (size_t)H * sizeof(float));
+    return 0;
+fail:
+    if (t) { t->dead = 1; t->dev_pos = -1; }
+    return -1;
+}
+
+int qwen_hip_talker_greedy_async(void *state, int n_steps) {
+    talker_t *t = (talker_t *)state;
+    if (!t || t->dead || !t->ggraph_ready) { SETERR("greedy loop not initialised"); return -1; }
+    REQ(t->dev_pos >= 0 && t->dev_pos + n_steps <= t->s.kv_max && t->dev_pos + n_steps <= t->s.rope_len,
+        "positions exceed kv_max");
+    for (int i = 0; i < n_steps; i++) HCK(hipGraphLaunch(t->gexec, t->st));
+    t->dev_pos += n_steps;
+    return 0;
+fail:
+    if (t) t->dead = 1;
+    return -1;
+}
+
+int qwen_hip_talker_sync(void *state) {
+    talker_t *t = (talker_t *)state;
+    if (!t) return -1;
+    HCK(hipStreamSynchronize(t->st));
+    return 0;
+fail:
+    t->dead = 1;
+    return -1;
+}
+
+/* Enqueue n launches of one kernel of the step (benchmark/profiling aid, no sync):
+ * kernel 0 norm+QKV, 1 attention (at the current device position), 2 O+residual,
+ * 3 norm+gate_up+SwiGLU, 4 down+residual, 5 final norm (position not advanced). */
+int qwen_hip_talker_launch_kernel(void *state, int kernel, int layer, int n) {
+    talker_t *t = (talker_t *)state;
+    if (!t || t->dead) { SETERR("talker state is dead or NULL"); return -1; }
+    stack_t *s = &t->s;
+    REQ(layer >= 0 && layer < s->L && kernel >= 0 && kernel <= 5 && n >= 0, "bad kernel/layer");
+    REQ(t->dev_pos >= 0 && t->dev_pos < s->kv_max, "device position unknown: run a step first");
+    float *x = t->io + s->H;
+    const size_t lay = (size_t)layer * s->nkv * s->kv_max * s->hd;
+    for (int i = 0; i < n; i++) {
+        switch (kernel) {
+        case 0: HCK(mv(&s->qkv[layer], QT_EPI_STORE, 1, x, s->in_norm[layer], s->eps, s->qkvbuf, NULL, NULL, t->st)); break;
+        case 1: HCK(qt_launch_attn(1, s->qkvbuf, s->qn[layer], s->kn[layer], s->rope_cos, s->rope_sin, s->eps, t->d_pos, 0,
+                                   s->kc + lay, s->vc + lay, s->hd, (long long)s->kv_max * s->hd, s->nh, s->nkv,
+                                   s->hd, 1.0f / sqrtf((float)s->hd), s->part, s->cnt, s->attn_G, s->attn, t->st)); break;
+        case 2: HCK(mv(&s->o[layer], QT_EPI_STORE, 0, s->attn, NULL, s->eps, s->hbuf, NULL, NULL, t->st)); break;
+        case 3: HCK(mv(&s->gu[layer], QT_EPI_SWIGLU, 1, x, s->post_norm[layer], s->eps, s->hbuf, NULL, NULL, t->st)); break;
+        case 4: HCK(mv(&s->dn[layer], QT_EPI_STORE, 0, s->hbuf, NULL, s->eps, s->attn, NULL, NULL, t->st)); break;
+        case 5: HCK(qt_launch_rmsnorm(x, s->final_norm, t->io, s->H, s->eps, NULL, t->st)); break;
+        }
+    }
+    return 0;
+fail:
+    return -1;
+}
+
+int qwen_hip_talker_dequant(void *state, int layer, int which, int r0, int n, float *out) {
+    talker_t *t = (talker_t *)state;
+    float *d = NULL;
+    if (!t) { SETERR("NULL state"); return -1; }
+    stack_t *s = &t->s;
+    REQ(layer >= 0 && layer < s->L && which >= 0 && which <= 5, "bad layer/which");
+    const dmat_t *m = which <= 2 ? &s->qkv[layer] : which == 3 ? &s->o[layer] : which == 4 ? &s->gu[layer] : &s->dn[layer];
+    int off = which == 1 ? s->qd : which == 2 ? s->qd + s->kvd : 0;
+    int lim = which == 0 ? s->qd : which <= 2 ? s->kvd : m->rows;
+    REQ(r0 >= 0 && n >= 0 && r0 + n <= lim, "row range out of bounds");
+    HCK(hipMalloc((void **)&d, (size_t)n * m->cols * sizeof(float) + 4));
+    HCK(qt_launch_dequant(m->prec, m->w, m->scale, m->s16, m->cols, off + r0, n, d, t->st));
+    HCK(hipMemcpyAsync(out, d, (size_t)n * m->cols * sizeof(float), hipMemcpyDeviceToHost, t->st));
+    HCK(hipStreamSynchronize(t->st));
+    (void)hipFree(d);
+    return 0;
+fail:
+    if (d) (void)hipFree(d);
+    return -1;
+}
+
+/* ---- Code Predictor state ------------------------------------------------------------ */
+
+typedef struct {
+    stack_t s;
+    hipStream_t st;
+    int codebook, lm_prec, codec_vocab, talker_hidden, emb_dim;
+    dmat_t lm[15];
+    uint16_t *cp_emb[15];
+    uint16_t *talker_emb;
+    dmat_t mtp; int has_mtp; float *mtp_bias;
+    float *x, *x1, *ebuf, *logits, *th;   /* device */
+    int *d_posv;                          /* [64]: 0..63, per-pass positions */
+    int *d_codes;                         /* [16]: [0] = code0, [1..15] = out codes */
+    float *h_x; int *h_codes;             /* pinned */
+    hipGraphExec_t fexec, pexec;
+    int fready, pready;
+    int *d_steppos;
+    int dead;
+} cp_t;
+
+static void cp_destroy(cp_t *c) {
+    if (!c) return;
+    if (c->fready) (void)hipGraphExecDestroy(c->fexec);
+    if (c->pready) (void)hipGraphExecDestroy(c->pexec);
+    stack_free(&c->s);
+    for (int g = 0; g < 15; g++) { dmat_free(&c->lm[g]); if (c->cp_emb[g]) (void)hipFree(c->cp_emb[g]); }
+    dmat_free(&c->mtp);
+    void *bufs[] = {c->talker_emb, c->mtp_bias, c->x, c->x1, c->ebuf, c->logits, c->th, c->d_posv, c->d_codes, c->d_steppos};
+    for (size_t i = 0; i < sizeof bufs / sizeof bufs[0]; i++) if (bufs[i]) (void)hipFree(bufs[i]);
+    if (c->h_x) (void)hipHostFree(c->h_x);
+    if (c->h_codes) (void)hipHostFree(c->h_codes);
+    if (c->st) (void)hipStreamDestroy(c->st);
+    free(c);
+}
+
+void *qwen_hip_cp_init(const qwen_hip_cp_desc_t *d) {
+    cp_t *c = calloc(1, sizeof *c);
+    void *tmp = NULL;
+    if (!c) { SETERR("out of host memory"); return NULL; }
+    REQ(d, "null descriptor");
+    HCK(hipStreamCreateWithFlags(&c->st, hipStreamNonBlocking));
+    if (stack_init(&c->s, &d->cp, c->st) != 0) goto fail;   /* g_err already set */
+    c->codebook = d->codebook; c->codec_vocab = d->codec_vocab;
+    c->talker_hidden = d->talker_hidden; c->emb_dim = d->emb_dim;
+    c->lm_prec = (d->cp.quantize_to >= 0) ? d->cp.quantize_to : d->lm_prec;
+    const int H = c->s.H;
+    REQ(c->s.kv_max >= 16, "CP kv_max must hold 16 positions");
+    size_t tb = (size_t)c->codebook * (H > c->emb_dim ? H : c->emb_dim) * 2 + 64;
+    HCK(hipMalloc(&tmp, tb));
+    for (int g = 0; g < 15; g++) {
+        REQ(dmat_alloc(&c->lm[g], c->lm_prec, c->codebook, H) == 0, "alloc lm_head");
+        REQ(dmat_put(&c->lm[g], 0, &d->lm_head[g], d->lm_prec, c->codebook, c->st, tmp) == 0, "upload lm_head %d", g);
+        REQ(d->cp_codec_emb[g], "missing cp codec embedding %d", g);
+        HCK(hipMalloc((void **)&c->cp_emb[g], (size_t)c->codebook * c->emb_dim * 2));
+        HCK(hipMemcpy(c->cp_emb[g], d->cp_codec_emb[g], (size_t)c->codebook * c->emb_dim * 2, hipMemcpyDefault));
+    }
+    REQ(d->talker_codec_emb, "missing talker codec embedding");
+    HCK(hipMalloc((void **)&c->talker_emb, (size_t)c->codec_vocab * c->talker_hidden * 2));
+    HCK(hipMemcpy(c->talker_emb, d->talker_codec_emb, (size_t)c->codec_vocab * c->talker_hidden * 2, hipMemcpyDefault));
+    c->has_mtp = d->mtp.w != NULL;
+    if (c->has_mtp) {
+        int mp = d->mtp_prec;
+        REQ(dmat_alloc(&c->mtp, mp, H, c->emb_dim) == 0, "alloc mtp");
+        REQ(dmat_put(&c->mtp, 0, &d->mtp, mp, H, c->st, tmp) == 0, "upload mtp");
+        REQ(d->mtp_bias, "mtp projection without bias");
+        REQ((c->mtp_bias = up_f32(d->mtp_bias, H, c->st)) != NULL, "mtp bias");
+    } else {
+        REQ(c->emb_dim == H && c->talker_hidden == H, "no mtp projection but emb_dim != cp_hidden");
+    }
+    int E = c->emb_dim > c->talker_hidden ? c->emb_dim : c->talker_hidden;
+    HCK(hipMalloc((void **)&c->x, (size_t)H * sizeof(float)));
+    HCK(hipMalloc((void **)&c->x1, (size_t)H * sizeof(float)));
+    HCK(hipMalloc((void **)&c->ebuf, (size_t)E * sizeof(float)));
+    HCK(hipMalloc((void **)&c->th, (size_t)E * sizeof(float)));
+    HCK(hipMalloc((void **)&c->logits, (size_t)c->codebook * sizeof(float)));
+    HCK(hipMalloc((void **)&c->d_posv, 64 * sizeof(int)));
+    HCK(hipMalloc((void **)&c->d_codes, 16 * sizeof(int)));
+    HCK(hipMalloc((void **)&c->d_steppos, sizeof(int)));
+    HCK(hipHostMalloc((void **)&c->h_x, (size_t)(E > H ? E : H) * sizeof(float), hipHostMallocDefault));
+    HCK(hipHostMalloc((void **)&c->h_codes, 64 * sizeof(int), hipHostMallocDefault));
+    for (int i = 0; i < 64; i++) c->h_codes[i] = i;
+    HCK(hipMemcpy(c->d_posv, c->h_codes, 64 * sizeof(int), hipMemcpyHostToDevice));
+    (void)hipFree(tmp);
+    return c;
+fail:
+    if (tmp) (void)hipFree(tmp);
+    cp_destroy(c);
+    return NULL;
+}
+
+void qwen_hip_cp_free(void *state) { cp_destroy((cp_t *)state); }
+void *qwen_hip_cp_stream(void *state) { return state ? (void *)((cp_t *)state)->st : NULL; }
+
+/* dst = mtp(src) (qwen_tts_code_predictor.c:907-924) */
+static hipError_t cp_project(cp_t *c, const float *src, float *dst) {
+    if (c->has_mtp)
+        return mv(&c->mtp, QT_EPI_BIAS, 0, src, NULL, c->s.eps, dst, NULL, c->mtp_bias, c->st);
+    return qt_launch_copy_f32(src, dst, c->s.H, c->st);
+}
+
+static hipError_t cp_pass_body(void *a) {
+    cp_t *c = (cp_t *)a;
+    return stack_body(&c->s, c->x, c->d_steppos, c->st);
+}
+
+/* The whole frame (qwen_tts_code_predictor.c:926-1045) as one launch sequence:
+ * th = talker hidden (device), d_codes[0] = code0. */
+static hipError_t cp_frame_body(void *a) {
+    cp_t *c = (cp_t *)a;
+    hipError_t e;
+    const int H = c->s.H;
+    if ((e = cp_project(c, c->th, c->x))) return e;
+    if ((e = qt_launch_gather(c->d_codes, c->codec_vocab, c->talker_emb, c->talker_hidden, c->ebuf, c->st))) return e;
+    if ((e = cp_project(c, c->ebuf, c->x1))) return e;
+    if ((e = stack_body(&c->s, c->x, c->d_posv + 0, c->st))) return e;
+    if ((e = qt_launch_copy_f32(c->x1, c->x, H, c->st))) return e;
+    if ((e = stack_body(&c->s, c->x, c->d_posv + 1, c->st))) return e;
+    for (int g = 0; g < 15; g++) {
+        if (g > 0) {
+            if ((e = qt_launch_gather(c->d_codes + g, c->codebook, c->cp_emb[g - 1], c->emb_dim, c->ebuf, c->st))) return e;
+            if ((e = cp_project(c, c->ebuf, c->x))) return e;
+            if ((e = stack_body(&c->s, c->x, c->d_posv + g + 1, c->st))) return e;
+        }
+        if ((e = mv(&c->lm[g], QT_EPI_STORE, 1, c->x, c->s.final_norm, c->s.eps, c->logits, NULL, NULL, c->st))) return e;
+        if ((e = qt_launch_select(c->logits, c->codebook, 0, NULL, 0, c->d_codes + g + 1, NULL, 0, NULL, 0, NULL, c->st))) return e;
+    }
+    return hipSuccess;
+}
+
+int qwen_hip_cp_frame(void *state, const float *talker_hidden, int code0, int *out_codes) {
+    cp_t *c = (cp_t *)state;
+    if (!c || c->dead) { SETERR("CP state is dead or NULL"); return -1; }
+    memcpy(c->h_x, talker_hidden, (size_t)c->talker_hidden * sizeof(float));
+    c->h_codes[0] = code0;
+    HCK(hipMemcpyAsync(c->th, c->h_x, (size_t)c->talker_hidden * sizeof(float), hipMemcpyHostToDevice, c->st));
+    HCK(hipMemcpyAsync(c->d_codes, c->h_codes, sizeof(int), hipMemcpyHostToDevice, c->st));
+    if (!c->fready) {
+        if (capture(c->st, &c->fexec, cp_frame_body, c) != 0) goto fail;
+        c->fready = 1;
+    }
+    HCK(hipGraphLaunch(c->fexec, c->st));
+    HCK(hipMemcpyAsync(c->h_codes + 16, c->d_codes, 16 * sizeof(int), hipMemcpyDeviceToHost, c->st));
+    HCK(hipStreamSynchronize(c->st));
+    for (int g = 0; g < 15; g++) out_codes[g] = c->h_codes[16 + 1 + g];
+    for (int i = 0; i < 16; i++) c->h_codes[16 + i] = 0;
+    c->h_codes[0] = 0;
+    return 0;
+fail:
+    if (c) c->dead = 1;
+    return -1;
+}
+
+int qwen_hip_cp_frame_async(void *state, int n_frames) {
+    cp_t *c = (cp_t *)state;
+    if (!c || c->dead || !c->fready) { SETERR("CP frame graph not initialised"); return -1; }
+    for (int i = 0; i < n_frames; i++) HCK(hipGraphLaunch(c->fexec, c->st));
+    return 0;
+fail:
+    c->dead = 1;
+    return -1;
+}
+
+int qwen_hip_cp_sync(void *state) {
+    cp_t *c = (cp_t *)state;
+    if (!c) return -1;
+    HCK(hipStreamSynchronize(c->st));
+    return 0;
+fail:
+    c->dead = 1;
+    return -1;
+}
+
+int qwen_hip_cp_step(void *state, float *x, int pos) {
+    cp_t *c = (cp_t *)state;
+    if (!c || c->dead) { SETERR("CP state is dead or NULL"); return -1; }
+    REQ(pos >= 0 && pos < c->s.kv_max && pos < c->s.rope_len, "CP pos %d out of range", pos);
+    const int H = c->s.H;
+    memcpy(c->h_x, x, (size_t)H * sizeof(float));
+    c->h_codes[32] = pos;
+    HCK(hipMemcpyAsync(c->x, c->h_x, (size_t)H * sizeof(float), hipMemcpyHostToDevice, c->st));
+    HCK(hipMemcpyAsync(c->d_steppos, c->h_codes + 32, sizeof(int), hipMemcpyHostToDevice, c->st));
+    if (!c->pready) {
+        if (capture(c->st, &c->pexec, cp_pass_body, c) != 0) goto fail;
+        c->pready = 1;
+    }
+    HCK(hipGraphLaunch(c->pexec, c->st));
+    HCK(hipMemcpyAsync(c->h_x, c->x, (size_t)H * sizeof(float), hipMemcpyDeviceToHost, c->st));
+    HCK(hipStreamSynchronize(c->st));
+    memcpy(x, c->h_x, (size_t)H * sizeof(float));
+    return 0;
+fail:
+    if (c) c->dead = 1;
+    return -1;
+}
+
+/* ---- level 1: per-op backend + kernel-API parity surface ----------------------------- */
+
+typedef struct { const void *host; int rows, cols; dmat_t m; } wcache_t;
+typedef struct {
+    hipStream_t st;
+    wcache_t *cache; int ncache, capcache;
+} backend_t;
+
+int qwen_hip_available(void) {
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess) return 0;
+    return n > 0;
+}
+
+void *qwen_hip_init(void) {
+    backend_t *b = calloc(1, sizeof *b);
+    if (!b) return NULL;
+    if (!qwen_hip_available()) { SETERR("no HIP device"); free(b); return NULL; }
+    if (hipStreamCreateWithFlags(&b->st, hipStreamNonBlocking) != hipSuccess) { SETERR("stream create failed"); free(b); return NULL; }
+    return b;
+}
+
+void qwen_hip_free(void *ctx) {
+    backend_t *b = (backend_t *)ctx;
+    if (!b) return;
+    for (int i = 0; i < b->ncache; i++) dmat_free(&b->cache[i].m);
+    free(b->cache);
+    (void)hipStreamDestroy(b->st);
+    free(b);
+}
+
+static dmat_t *cached_bf16(backend_t *b, const uint16_t *W, int rows, int cols) {
+    for (int i = 0; i < b->ncache; i++)
+        if (b->cache[i].host == W && b->cache[i].rows == rows && b->cache[i].cols == cols) return &b->cache[i].m;
+    if (b->ncache == b->capcache) {
+        int nc = b->capcache ? 2 * b->capcache : 64;
+        wcache_t *n = realloc(b->cache, (size_t)nc * sizeof *n);
+        if (!n) return NULL;
+        b->cache = n; b->capcache = nc;
+    }
+    wcache_t *e = &b->cache[b->ncache];
+    qwen_hip_mat_t src = {W, NULL};
+    if (dmat_alloc(&e->m, QWEN_HIP_BF16, rows, cols) != 0) return NULL;
+    if (dmat_put(&e->m, 0, &src, QWEN_HIP_BF16, rows, b->st, NULL) != 0) { dmat_free(&e->m); return NULL; }
+    e->host = W; e->rows = rows; e->cols = cols;
+    b->ncache++;
+    return &e->m;
+}
+
+void qwen_hip_matvec_bf16(void *ctx, float *y, const uint16_t *W, const float *x, int rows, int cols) {
+    qwen_hip_matmat_bf16(ctx, y, W, x, rows, cols, 1);
+}
+
+void qwen_hip_matmat_bf16(void *ctx, float *Y, const uint16_t *W, const float *X, int rows, int cols, int B) {
+    backend_t *b = (backend_t *)ctx;
+    float *dx = NULL, *dy = NULL, *hx = NULL, *hy = NULL;
+    dmat_t *m;
+    REQ(b && B >= 1 && B <= 64, "bad backend call");
+    REQ((m = cached_bf16(b, W, rows, cols)) != NULL, "weight upload failed");
+    HCK(hipMalloc((void **)&dx, (size_t)cols * B * sizeof(float)));
+    HCK(hipMalloc((void **)&dy, (size_t)rows * B * sizeof(float)));
+    hx = malloc((size_t)cols * B * sizeof(float)); hy = malloc((size_t)rows * B * sizeof(float));
+    REQ(hx && hy, "host alloc");
+    /* X is [cols][B] row-major: gather column b into a contiguous vector */
+    for (int k = 0; k < cols; k++) for (int j = 0; j < B; j++) hx[(size_t)j * cols + k] = X[(size_t)k * B + j];
+    HCK(hipMemcpyAsync(dx, hx, (size_t)cols * B * sizeof(float), hipMemcpyHostToDevice, b->st));
+    for (int j = 0; j < B; j++)
+        HCK(mv(m, QT_EPI_STORE, 0, dx + (size_t)j * cols, NULL, 0.f, dy + (size_t)j * rows, NULL, NULL, b->st));
+    HCK(hipMemcpyAsync(hy, dy, (size_t)rows * B * sizeof(float), hipMemcpyDeviceToHost, b->st));
+    HCK(hipStreamSynchronize(b->st));
+    for (int r = 0; r < rows; r++) for (int j = 0; j < B; j++) Y[(size_t)r * B + j] = hy[(size_t)j * rows + r];
+fail:
+    if (dx) (void)hipFree(dx);
+    if (dy) (void)hipFree(dy);
+    free(hx); free(hy);
+}
+
+/* a private stream for the one-shot op entry points */
+static hipStream_t op_stream(void) {
+    static hipStream_t s = NULL;
+    if (!s && hipStreamCreateWithFlags(&s, hipStreamNonBlocking) != hipSuccess) s = NULL;
+    return s;
+}
+
+static int op_matvec(int prec, float *y, const void *W, const float *scale, const float *x, int rows, int cols) {
+    hipStream_t st = op_stream();
+    dmat_t m; memset(&m, 0, sizeof m);
+    float *dx = NULL, *dy = NULL; void *tmp = NULL;
+    qwen_hip_mat_t src = {W, scale};
+    REQ(st, "no stream");
+    REQ(rows > 0 && cols > 0, "bad shape");
+    REQ(dmat_alloc(&m, prec, rows, cols) == 0, "alloc");
+    if (prec == QWEN_HIP_Q4_0) HCK(hipMalloc(&tmp, (size_t)rows * (cols / 32) * 18 + 16));
+    REQ(dmat_put(&m, 0, &src, prec, rows, st, tmp) == 0, "upload");
+    HCK(hipMalloc((void **)&dx, (size_t)cols * sizeof(float)));
+    HCK(hipMalloc((void **)&dy, (size_t)rows * sizeof(float)));
+    HCK(hipMemcpyAsync(dx, x, (size_t)cols * sizeof(float), hipMemcpyHostToDevice, st));
+    HCK(mv(&m, QT_EPI_STORE, 0, dx, NULL, 0.f, dy, NULL, NULL, st));
+    HCK(hipMemcpyAsync(y, dy, (size_t)rows * sizeof(float), hipMemcpyDeviceToHost, st));
+    HCK(hipStreamSynchronize(st));
+    dmat_free(&m); (void)hipFree(dx); (void)hipFree(dy); if (tmp) (void)hipFree(tmp);
+    return 0;
+fail:
+    dmat_free(&m); if (dx) (void)hipFree(dx); if (dy) (void)hipFree(dy); if (tmp) (void)hipFree(tmp);
+    return -1;
+}
+
+int qwen_hip_op_matvec_bf16(float *y, const uint16_t *W, const float *x, int rows, int cols) {
+    return op_matvec(QWEN_HIP_BF16, y, W, NULL, x, rows, cols);
+}
+int qwen_hip_op_matvec_int8(float *y, const int8_t *W, const float *scale, const float *x, int rows, int cols) {
+    return op_matvec(QWEN_HIP_INT8, y, W, scale, x, rows, cols);
+}
+int qwen_hip_op_matvec_q4_0(float *y, const void *W, const float *x, int rows, int cols) {
+    if (cols % 32) { SETERR("q4_0 needs cols %% 32 == 0"); return -1; }
+    return op_matvec(QWEN_HIP_Q4_0, y, W, NULL, x, rows, cols);
+}
+
+int qwen_hip_op_argmax_matvec(int prec, const float *x, const void *W, const float *scale, int in_dim, int out_dim) {
+    hipStream_t st = op_stream();
+    dmat_t m; memset(&m, 0, sizeof m);
+    float *dx = NULL, *dy = NULL; int *dt = NULL; void *tmp = NULL; int tok = -1;
+    qwen_hip_mat_t src = {W, scale};
+    REQ(st, "no stream");
+    REQ(dmat_alloc(&m, prec, out_dim, in_dim) == 0, "alloc");
+    if (prec == QWEN_HIP_Q4_0) HCK(hipMalloc(&tmp, (size_t)out_dim * (in_dim / 32) * 18 + 16));
+    REQ(dmat_put(&m, 0, &src, prec, out_dim, st, tmp) == 0, "upload");
+    HCK(hipMalloc((void **)&dx, (size_t)in_dim * sizeof(float)));
+    HCK(hipMalloc((void **)&dy, (size_t)out_dim * sizeof(float)));
+    HCK(hipMalloc((void **)&dt, sizeof(int)));
+    HCK(hipMemcpyAsync(dx, x, (size_t)in_dim * sizeof(float), hipMemcpyHostToDevice, st));
+    HCK(mv(&m, QT_EPI_STORE, 0, dx, NULL, 0.f, dy, NULL, NULL, st));
+    HCK(qt_launch_select(dy, out_dim, 0, NULL, 0, dt, NULL, 0, NULL, 0, NULL, st));
+    HCK(hipMemcpyAsync(&tok, dt, sizeof(int), hipMemcpyDeviceToHost, st));
+    HCK(hipStreamSynchronize(st));
+fail:
+    dmat_free(&m); if (dx) (void)hipFree(dx); if (dy) (void)hipFree(dy); if (dt) (void)hipFree(dt);
+    if (tmp) (void)hipFree(tmp);
+    return tok;
+}
+
+int qwen_hip_op_causal_attention_bf16kv(float *out, const float *Q, const uint16_t *K, const uint16_t *V,
+                                        int seq_q, int seq_k, int n_heads, int n_kv_heads, int head_dim,
+                                        float scale, int q_offset) {
+    hipStream_t st = op_stream();
+    float *dq = NULL, *dout = NULL, *part = NULL; uint16_t *dk = NULL, *dv = NULL; unsigned *cnt = NULL;
+    REQ(st, "no stream");
+    REQ(head_dim == 128 && seq_q > 0 && seq_k > 0 && n_kv_heads > 0, "unsupported attention shape");
+    const int qh = n_heads * head_dim, kvd = n_kv_heads * head_dim;
+    const int G = qt_attn_grid(seq_k);
+    const int hpk = n_heads / n_kv_heads;
+    HCK(hipMalloc((void **)&dq, (size_t)seq_q * qh * sizeof(float)));
+    HCK(hipMalloc((void **)&dout, (size_t)seq_q * qh * sizeof(float)));
+    HCK(hipMalloc((void **)&dk, (size_t)seq_k * kvd * 2));
+    HCK(hipMalloc((void **)&dv, (size_t)seq_k * kvd * 2));
+    HCK(hipMalloc((void **)&part, (size_t)n_kv_heads * G * hpk * 130 * sizeof(float)));
+    HCK(hipMalloc((void **)&cnt, (size_t)n_kv_heads * sizeof(unsigned)));
+    HCK(hipMemsetAsync(cnt, 0, (size_t)n_kv_heads * sizeof(unsigned), st));
+    HCK(hipMemcpyAsync(dq, Q, (size_t)seq_q * qh * sizeof(float), hipMemcpyHostToDevice, st));
+    HCK(hipMemcpyAsync(dk, K, (size_t)seq_k * kvd * 2, hipMemcpyHostToDevice, st));
+    HCK(hipMemcpyAsync(dv, V, (size_t)seq_k * kvd * 2, hipMemcpyHostToDevice, st));
+    for (int i = 0; i < seq_q; i++) {
+        int k_end = q_offset + i + 1;
+        if (k_end > seq_k) k_end = seq_k;
+        if (k_end <= 0) {
+            HCK(hipMemsetAsync(dout + (size_t)i * qh, 0, (size_t)qh * sizeof(float), st));
+            continue;
+        }
+        HCK(qt_launch_attn(0, dq + (size_t)i * qh, NULL, NULL, NULL, NULL, 0.f, NULL, k_end, dk, dv, kvd, head_dim,
+                           n_heads, n_kv_heads, head_dim, scale, part, cnt, G, dout + (size_t)i * qh, st));
+    }
+    HCK(hipMemcpyAsync(out, dout, (size_t)seq_q * qh * sizeof(float), hipMemcpyDeviceToHost, st));
+    HCK(hipStreamSynchronize(st));
+    (void)hipFree(dq); (void)hipFree(dout); (void)hipFree(dk); (void)hipFree(dv); (void)hipFree(part); (void)hipFree(cnt);
+    return 0;
+fail:
+    if (dq) (void)hipFree(dq);
+    if (dout) (void)hipFree(dout);
+    if (dk) (void)hipFree(dk);
+    if (dv) (void)hipFree(dv);
+    if (part) (void)hipFree(part);
+    if (cnt) (void)hipFree(cnt);
+    return -1;
+}
+
+int qwen_hip_op_rms_norm(float *out, const float *x, const float *w, int seq, int dim, float eps) {
+    hipStream_t st = op_stream();
+    float *dx = NULL, *dw = NULL, *dout = NULL;
+    REQ(st && seq > 0 && dim > 0, "bad args");
+    HCK(hipMalloc((void **)&dx, (size_t)seq * dim * sizeof(float)));
+    HCK(hipMalloc((void **)&dout, (size_t)seq * dim * sizeof(float)));
+    HCK(hipMalloc((void **)&dw, (size_t)dim * sizeof(float)));
+    HCK(hipMemcpyAsync(dx, x, (size_t)seq * dim * sizeof(float), hipMemcpyHostToDevice, st));
+    HCK(hipMemcpyAsync(dw, w, (size_t)dim * sizeof(float), hipMemcpyHostToDevice, st));
+    for (int s = 0; s < seq; s++)
+        HCK(qt_launch_rmsnorm(dx + (size_t)s * dim, dw, dout + (size_t)s * dim, dim, eps, NULL, st));
+    HCK(hipMemcpyAsync(out, dout, (size_t)seq * dim * sizeof(float), hipMemcpyDeviceToHost, st));
+    HCK(hipStreamSynchronize(st));
+    (void)hipFree(dx); (void)hipFree(dout); (void)hipFree(dw);
+    return 0;
+fail:
+    if (dx) (void)hipFree(dx);
+    if (dout) (void)hipFree(dout);
+    if (dw) (void)hipFree(dw);
+    return -1;
+}
+
+int qwen_hip_op_rms_norm_per_head(float *x, const float *w, int seq, int n_heads, int head_dim, float eps) {
+    hipStream_t st = op_stream();
+    float *dx = NULL, *dw = NULL;
+    const size_t n = (size_t)seq * n_heads * head_dim;
+    REQ(st && seq > 0 && n_heads > 0 && head_dim > 0, "bad args");
+    HCK(hipMalloc((void **)&dx, n * sizeof(float)));
+    HCK(hipMalloc((void **)&dw, (size_t)head_dim * sizeof(float)));
+    HCK(hipMemcpyAsync(dx, x, n * sizeof(float), hipMemcpyHostToDevice, st));
+    HCK(hipMemcpyAsync(dw, w, (size_t)head_dim * sizeof(float), hipMemcpyHostToDevice, st));
+    HCK(qt_launch_rmsnorm_rows(dx, dw, seq * n_heads, head_dim, eps, st));
+    HCK(hipMemcpyAsync(x, dx, n * sizeof(float), hipMemcpyDeviceToHost, st));
+    HCK(hipStreamSynchronize(st));
+    (void)hipFree(dx); (void)hipFree(dw);
+    return 0;
+fail:
+    if (dx) (void)hipFree(dx);
+    if (dw) (void)hipFree(dw);
+    return -1;
+}
+
+int qwen_hip_op_swiglu(float *out, const float *gate_up, int n) {
+    hipStream_t st = op_stream();
+    float *dg = NULL, *dout = NULL;
+    REQ(st && n > 0, "bad args");
+    HCK(hipMalloc((void **)&dg, (size_t)2 * n * sizeof(float)));
+    HCK(hipMalloc((void **)&dout, (size_t)n * sizeof(float)));
+    HCK(hipMemcpyAsync(dg, gate_up, (size_t)2 * n * sizeof(float), hipMemcpyHostToDevice, st));
+    HCK(qt_launch_swiglu(dg, dout, n, st));
+    HCK(hipMemcpyAsync(out, dout, (size_t)n * sizeof(float), hipMemcpyDeviceToHost, st));
+    HCK(hipStreamSynchronize(st));
+    (void)hipFree(dg); (void)hipFree(dout);
+    return 0;
+fail:
+    if (dg) (void)hipFree(dg);
+    if (dout) (void)hipFree(dout);
+    return -1;
+}
+
+int qwen_hip_op_quantize_int8(const uint16_t *src, int rows, int cols, int8_t *dst, float *scale) {
+    hipStream_t st = op_stream();
+    uint16_t *ds = NULL; uint8_t *dq = NULL; float *dsc = NULL;
+    REQ(st && rows > 0 && cols > 0, "bad args");
+    HCK(hipMalloc((void **)&ds, (size_t)rows * cols * 2));
+    HCK(hipMalloc((void **)&dq, (size_t)rows * cols));
+    HCK(hipMalloc((void **)&dsc, (size_t)rows * sizeof(float)));
+    HCK(hipMemcpyAsync(ds, src, (size_t)rows * cols * 2, hipMemcpyHostToDevice, st));
+    HCK(qt_launch_quant_int8(ds, rows, cols, dq, dsc, st));
+    HCK(qt_launch_flip_sign(dq, (size_t)rows * cols, st));   /* back to the reference's q */
+    HCK(hipMemcpyAsync(dst, dq, (size_t)rows * cols, hipMemcpyDeviceToHost, st));
+    HCK(hipMemcpyAsync(scale, dsc, (size_t)rows * sizeof(float), hipMemcpyDeviceToHost, st));
+    HCK(hipStreamSynchronize(st));
+    (void)hipFree(ds); (void)hipFree(dq); (void)hipFree(dsc);
+    return 0;
+fail:
+    if (ds) (void)hipFree(ds);
+    if (dq) (void)hipFree(dq);
+    if (dsc) (void)hipFree(dsc);
+    return -1;
+}
+
+int qwen_hip_op_quantize_q4_0(const uint16_t *src, int rows, int cols, void *dst_blocks) {
+    hipStream_t st = op_stream();
+    uint16_t *ds = NULL, *s16 = NULL; uint8_t *qs = NULL, *hq = NULL; uint16_t *hs = NULL;
+    const size_t nb = (size_t)rows * (cols / 32);
+    REQ(st && rows > 0 && cols > 0 && cols % 32 == 0, "bad args");
+    HCK(hipMalloc((void **)&ds, (size_t)rows * cols * 2));
+    HCK(hipMalloc((void **)&qs, nb * 16));
+    HCK(hipMalloc((void **)&s16, nb * 2));
+    HCK(hipMemcpyAsync(ds, src, (size_t)rows * cols * 2, hipMemcpyHostToDevice, st));
+    HCK(qt_launch_quant_q4(ds, rows, cols, qs, s16, st));
+    hq = malloc(nb * 16); hs = malloc(nb * 2);
+    REQ(hq && hs, "host alloc");
+    HCK(hipMemcpyAsync(hq, qs, nb * 16, hipMemcpyDeviceToHost, st));
+    HCK(hipMemcpyAsync(hs, s16, nb * 2, hipMemcpyDeviceToHost, st));
+    HCK(hipStreamSynchronize(st));
+    for (size_t b = 0; b < nb; b++) {
+        uint8_t *o = (uint8_t *)dst_blocks + b * 18;
+        o[0] = (uint8_t)(hs[b] & 0xFF); o[1] = (uint8_t)(hs[b] >> 8);
+        memcpy(o + 2, hq + b * 16, 16);
+    }
+    free(hq); free(hs);
+    (void)hipFree(ds); (void)hipFree(qs); (void)hipFree(s16);
+    return 0;
+fail:
+    free(hq); free(hs);
+    if (ds) (void)hipFree(ds);
+    if (qs) (void)hipFree(qs);
+    if (s16) (void)hipFree(s16);
+    return -1;
+}

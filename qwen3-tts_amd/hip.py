@@ -1,0 +1,281 @@
+"""ctypes binding of libqwen_tts_hip.so (the C ABI declared in include/qwen_tts_hip.h).
+
+The library is loaded from this package directory; there is no fallback: if the
+shared object is missing or no GPU is present the calls fail loudly.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+
+import numpy as np
+
+PKG = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(PKG, "libqwen_tts_hip.so")
+
+BF16, INT8, Q4_0 = 0, 1, 2
+PREC = {"bf16": BF16, "int8": INT8, "int4": Q4_0, "q4_0": Q4_0}
+
+# every symbol the header declares (checked by the CPU test suite)
+EXPORTS = [
+    "qwen_hip_talker_init", "qwen_hip_talker_step", "qwen_hip_talker_get_dec_x",
+    "qwen_hip_talker_upload_kv", "qwen_hip_talker_free", "qwen_hip_talker_download_kv",
+    "qwen_hip_talker_greedy", "qwen_hip_talker_greedy_async", "qwen_hip_talker_sync",
+    "qwen_hip_talker_stream", "qwen_hip_talker_step_nograph", "qwen_hip_talker_launch_kernel", "qwen_hip_cp_init", "qwen_hip_cp_step",
+    "qwen_hip_cp_frame", "qwen_hip_cp_frame_async", "qwen_hip_cp_sync", "qwen_hip_cp_stream",
+    "qwen_hip_cp_free", "qwen_hip_available", "qwen_hip_init", "qwen_hip_free", "qwen_hip_matvec_bf16",
+    "qwen_hip_matmat_bf16", "qwen_hip_op_matvec_int8", "qwen_hip_op_matvec_q4_0",
+    "qwen_hip_op_matvec_bf16", "qwen_hip_op_causal_attention_bf16kv", "qwen_hip_op_rms_norm",
+    "qwen_hip_op_rms_norm_per_head", "qwen_hip_op_swiglu", "qwen_hip_op_argmax_matvec",
+    "qwen_hip_op_quantize_int8", "qwen_hip_op_quantize_q4_0", "qwen_hip_talker_dequant",
+    "qwen_hip_last_error",
+]
+
+
+class Mat(C.Structure):
+    _fields_ = [("w", C.c_void_p), ("scale", C.c_void_p)]
+
+
+class Layer(C.Structure):
+    _fields_ = [("q", Mat), ("k", Mat), ("v", Mat), ("o", Mat), ("gate_up", Mat), ("down", Mat),
+                ("input_norm", C.c_void_p), ("post_attn_norm", C.c_void_p),
+                ("q_norm", C.c_void_p), ("k_norm", C.c_void_p)]
+
+
+class TalkerDesc(C.Structure):
+    _fields_ = [("hidden", C.c_int), ("inter", C.c_int), ("n_heads", C.c_int), ("n_kv_heads", C.c_int),
+                ("head_dim", C.c_int), ("n_layers", C.c_int), ("kv_max", C.c_int), ("eps", C.c_float),
+                ("prec", C.c_int), ("quantize_to", C.c_int), ("layers", C.POINTER(Layer)),
+                ("final_norm", C.c_void_p), ("rope_cos", C.c_void_p), ("rope_sin", C.c_void_p),
+                ("rope_len", C.c_int)]
+
+
+class CpDesc(C.Structure):
+    _fields_ = [("cp", TalkerDesc), ("codebook", C.c_int), ("lm_prec", C.c_int), ("lm_head", Mat * 15),
+                ("cp_codec_emb", C.c_void_p * 15), ("talker_codec_emb", C.c_void_p),
+                ("codec_vocab", C.c_int), ("talker_hidden", C.c_int), ("emb_dim", C.c_int),
+                ("mtp_prec", C.c_int), ("mtp", Mat), ("mtp_bias", C.c_void_p)]
+
+
+def _p(a):
+    return None if a is None else a.ctypes.data_as(C.c_void_p)
+
+
+_lib = None
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(f"{LIB_PATH} not built: run __graft_entry__.build()")
+        L = C.CDLL(LIB_PATH)
+        vp, i, f = C.c_void_p, C.c_int, C.c_float
+        L.qwen_hip_talker_init.argtypes = [C.POINTER(TalkerDesc)]; L.qwen_hip_talker_init.restype = vp
+        L.qwen_hip_talker_step.argtypes = [vp, vp, vp, i]; L.qwen_hip_talker_step.restype = i
+        L.qwen_hip_talker_step_nograph.argtypes = [vp, vp, vp, i]; L.qwen_hip_talker_step_nograph.restype = i
+        L.qwen_hip_talker_get_dec_x.argtypes = [vp, vp]
+        L.qwen_hip_talker_upload_kv.argtypes = [vp, vp, vp, i, i]; L.qwen_hip_talker_upload_kv.restype = i
+        L.qwen_hip_talker_download_kv.argtypes = [vp, vp, vp, i, i]; L.qwen_hip_talker_download_kv.restype = i
+        L.qwen_hip_talker_free.argtypes = [vp]
+        L.qwen_hip_talker_greedy.argtypes = [vp, vp, vp, i, vp, i, i, i, vp, vp]
+        L.qwen_hip_talker_greedy.restype = i
+        L.qwen_hip_talker_greedy_async.argtypes = [vp, i]; L.qwen_hip_talker_greedy_async.restype = i
+        L.qwen_hip_talker_sync.argtypes = [vp]; L.qwen_hip_talker_sync.restype = i
+        L.qwen_hip_talker_stream.argtypes = [vp]; L.qwen_hip_talker_stream.restype = vp
+        L.qwen_hip_talker_launch_kernel.argtypes = [vp, i, i, i]; L.qwen_hip_talker_launch_kernel.restype = i
+        L.qwen_hip_talker_dequant.argtypes = [vp, i, i, i, i, vp]; L.qwen_hip_talker_dequant.restype = i
+        L.qwen_hip_cp_init.argtypes = [C.POINTER(CpDesc)]; L.qwen_hip_cp_init.restype = vp
+        L.qwen_hip_cp_step.argtypes = [vp, vp, i]; L.qwen_hip_cp_step.restype = i
+        L.qwen_hip_cp_frame.argtypes = [vp, vp, i, vp]; L.qwen_hip_cp_frame.restype = i
+        L.qwen_hip_cp_frame_async.argtypes = [vp, i]; L.qwen_hip_cp_frame_async.restype = i
+        L.qwen_hip_cp_sync.argtypes = [vp]; L.qwen_hip_cp_sync.restype = i
+        L.qwen_hip_cp_stream.argtypes = [vp]; L.qwen_hip_cp_stream.restype = vp
+        L.qwen_hip_cp_free.argtypes = [vp]
+        L.qwen_hip_available.restype = i
+        L.qwen_hip_init.restype = vp
+        L.qwen_hip_free.argtypes = [vp]
+        L.qwen_hip_matvec_bf16.argtypes = [vp, vp, vp, vp, i, i]
+        L.qwen_hip_matmat_bf16.argtypes = [vp, vp, vp, vp, i, i, i]
+        L.qwen_hip_op_matvec_int8.argtypes = [vp, vp, vp, vp, i, i]; L.qwen_hip_op_matvec_int8.restype = i
+        L.qwen_hip_op_matvec_q4_0.argtypes = [vp, vp, vp, i, i]; L.qwen_hip_op_matvec_q4_0.restype = i
+        L.qwen_hip_op_matvec_bf16.argtypes = [vp, vp, vp, i, i]; L.qwen_hip_op_matvec_bf16.restype = i
+        L.qwen_hip_op_causal_attention_bf16kv.argtypes = [vp, vp, vp, vp, i, i, i, i, i, f, i]
+        L.qwen_hip_op_causal_attention_bf16kv.restype = i
+        L.qwen_hip_op_rms_norm.argtypes = [vp, vp, vp, i, i, f]; L.qwen_hip_op_rms_norm.restype = i
+        L.qwen_hip_op_rms_norm_per_head.argtypes = [vp, vp, i, i, i, f]; L.qwen_hip_op_rms_norm_per_head.restype = i
+        L.qwen_hip_op_swiglu.argtypes = [vp, vp, i]; L.qwen_hip_op_swiglu.restype = i
+        L.qwen_hip_op_argmax_matvec.argtypes = [i, vp, vp, vp, i, i]; L.qwen_hip_op_argmax_matvec.restype = i
+        L.qwen_hip_op_quantize_int8.argtypes = [vp, i, i, vp, vp]; L.qwen_hip_op_quantize_int8.restype = i
+        L.qwen_hip_op_quantize_q4_0.argtypes = [vp, i, i, vp]; L.qwen_hip_op_quantize_q4_0.restype = i
+        L.qwen_hip_last_error.restype = C.c_char_p
+        _lib = L
+    return _lib
+
+
+def last_error():
+    return lib().qwen_hip_last_error().decode(errors="replace")
+
+
+def check(rc, what):
+    if rc != 0:
+        raise RuntimeError(f"{what} failed: {last_error()}")
+
+
+class Talker:
+    """Resident Talker (or any stack of layers) on the GPU.
+
+    ``layers`` is a list of dicts {q,k,v,o,gate_up,down: (w, scale|None),
+    input_norm, post_attn_norm, q_norm, k_norm}; arrays are numpy (host)."""
+
+    def __init__(self, shape, layers, final_norm, rope_cos, rope_sin, prec, kv_max,
+                 quantize_to=-1, cp=False):
+        s = shape
+        self.keep = []
+        nl = len(layers)
+        arr = (Layer * nl)()
+        for l, ly in enumerate(layers):
+            for nm in ["q", "k", "v", "o", "gate_up", "down"]:
+                w, sc = ly[nm]
+                self.keep += [w, sc]
+                getattr(arr[l], nm).w = w.ctypes.data
+                getattr(arr[l], nm).scale = None if sc is None else sc.ctypes.data
+            for nm in ["input_norm", "post_attn_norm", "q_norm", "k_norm"]:
+                a = np.ascontiguousarray(ly[nm], np.float32)
+                self.keep.append(a)
+                setattr(arr[l], nm, a.ctypes.data)
+        fn = np.ascontiguousarray(final_norm, np.float32)
+        rc_, rs_ = np.ascontiguousarray(rope_cos, np.float32), np.ascontiguousarray(rope_sin, np.float32)
+        self.keep += [fn, rc_, rs_, arr]
+        H, F = (s.cp_hidden, s.cp_inter) if cp else (s.hidden, s.inter)
+        nh, nkv, hd = (s.cp_heads, s.cp_kv_heads, s.cp_head_dim) if cp else (s.heads, s.kv_heads, s.head_dim)
+        self.H = H
+        self.desc = TalkerDesc(hidden=H, inter=F, n_heads=nh, n_kv_heads=nkv, head_dim=hd, n_layers=nl,
+                               kv_max=kv_max, eps=s.eps, prec=prec, quantize_to=quantize_to, layers=arr,
+                               final_norm=fn.ctypes.data, rope_cos=rc_.ctypes.data, rope_sin=rs_.ctypes.data,
+                               rope_len=rc_.shape[0])
+        self.kv_max = kv_max
+        self.kvd = nkv * hd
+        self.nl = nl
+        self.h = lib().qwen_hip_talker_init(C.byref(self.desc))
+        if not self.h:
+            raise RuntimeError("qwen_hip_talker_init failed: " + last_error())
+
+    def step(self, embed, pos, graph=True):
+        out = np.empty(self.H, np.float32)
+        e = np.ascontiguousarray(embed, np.float32)
+        fn = lib().qwen_hip_talker_step if graph else lib().qwen_hip_talker_step_nograph
+        check(fn(self.h, _p(e), _p(out), pos), "talker_step")
+        return out
+
+    def dec_x(self):
+        out = np.empty(self.H, np.float32)
+        lib().qwen_hip_talker_get_dec_x(self.h, _p(out))
+        return out
+
+    def upload_kv(self, kv_k, kv_v, n):
+        check(lib().qwen_hip_talker_upload_kv(self.h, _p(kv_k), _p(kv_v), kv_k.shape[1], n), "upload_kv")
+
+    def download_kv(self, n):
+        k = np.zeros((self.nl, self.kv_max, self.kvd), np.uint16)
+        v = np.zeros_like(k)
+        check(lib().qwen_hip_talker_download_kv(self.h, _p(k), _p(v), self.kv_max, n), "download_kv")
+        return k, v
+
+    def greedy(self, codec_head, codec_emb, embed, pos, frame0, n_steps):
+        toks = np.empty(n_steps, np.int32)
+        hid = np.empty(self.H, np.float32)
+        self._heads = (codec_head, codec_emb)
+        check(lib().qwen_hip_talker_greedy(self.h, _p(codec_head), _p(codec_emb), codec_head.shape[0],
+                                           _p(np.ascontiguousarray(embed, np.float32)), pos, frame0, n_steps,
+                                           _p(toks), _p(hid)), "talker_greedy")
+        return toks, hid
+
+    def dequant(self, layer, which, r0, n, cols):
+        out = np.empty((n, cols), np.float32)
+        check(lib().qwen_hip_talker_dequant(self.h, layer, which, r0, n, _p(out)), "dequant")
+        return out
+
+    def free(self):
+        if self.h:
+            lib().qwen_hip_talker_free(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
+class CodePredictor:
+    def __init__(self, desc: CpDesc, keep):
+        self.desc, self.keep = desc, keep
+        self.h = lib().qwen_hip_cp_init(C.byref(desc))
+        if not self.h:
+            raise RuntimeError("qwen_hip_cp_init failed: " + last_error())
+        self.H = desc.cp.hidden
+
+    def frame(self, talker_hidden, code0):
+        out = (C.c_int * 15)()
+        check(lib().qwen_hip_cp_frame(self.h, _p(np.ascontiguousarray(talker_hidden, np.float32)), code0, out),
+              "cp_frame")
+        return np.array(list(out), np.int32)
+
+    def step(self, x, pos):
+        x = np.array(x, np.float32, copy=True)
+        check(lib().qwen_hip_cp_step(self.h, _p(x), pos), "cp_step")
+        return x
+
+    def free(self):
+        if self.h:
+            lib().qwen_hip_cp_free(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
+def layers_from_ref(ref, prec_code, cp=False):
+    """Layer dicts over the reference-loaded (and reference-quantized) weights."""
+    s = ref.shape
+    nl = s.cp_layers if cp else s.layers
+    kind = {BF16: "bf16", INT8: "int8", Q4_0: "q4"}[prec_code]
+    out = []
+    for l in range(nl):
+        d = {}
+        for nm in ["q", "k", "v", "o", "gate_up", "down"]:
+            m = ref.layer_mat(l, nm, cp=cp)
+            d[nm] = (m[kind], m["scale"] if prec_code == INT8 else None)
+        d["input_norm"] = ref.layer_norm(l, "input", cp=cp)
+        d["post_attn_norm"] = ref.layer_norm(l, "post", cp=cp)
+        d["q_norm"] = ref.layer_norm(l, "q", cp=cp)
+        d["k_norm"] = ref.layer_norm(l, "k", cp=cp)
+        out.append(d)
+    return out
+
+
+def layers_from_tensors(t, shape, cp=False):
+    """Layer dicts (bf16) straight from synth tensors {name: uint16 array}; gate|up
+    interleaved the way the reference loader does (qwen_tts_talker.c:378-388)."""
+    from .synth import interleave_gate_up, bf16_to_f32
+    s = shape
+    nl = s.cp_layers if cp else s.layers
+    pre = "talker.code_predictor.model.layers." if cp else "talker.model.layers."
+    out = []
+    for l in range(nl):
+        p = f"{pre}{l}."
+        gu = interleave_gate_up(t[p + "mlp.gate_proj.weight"], t[p + "mlp.up_proj.weight"])
+        out.append({
+            "q": (t[p + "self_attn.q_proj.weight"], None), "k": (t[p + "self_attn.k_proj.weight"], None),
+            "v": (t[p + "self_attn.v_proj.weight"], None), "o": (t[p + "self_attn.o_proj.weight"], None),
+            "gate_up": (gu, None), "down": (t[p + "mlp.down_proj.weight"], None),
+            "input_norm": bf16_to_f32(t[p + "input_layernorm.weight"]),
+            "post_attn_norm": bf16_to_f32(t[p + "post_attention_layernorm.weight"]),
+            "q_norm": bf16_to_f32(t[p + "self_attn.q_norm.weight"]),
+            "k_norm": bf16_to_f32(t[p + "self_attn.k_norm.weight"]),
+        })
+    return out
