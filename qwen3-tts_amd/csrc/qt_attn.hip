@@ -14,11 +14,15 @@
 //   per-head RMSNorm of q and k with the shared [128] gains (qwen_tts_kernels.c:486-577),
 //   NeoX split-half RoPE from the uploaded cos/sin tables (qwen_tts_talker.c:203-251),
 //   and the KV append at `pos` with f32->bf16 TRUNCATION (qwen_tts_talker.c:612-615),
-//   done by the one workgroup whose chunk holds `pos` before it reads its keys.
+//   done by the one workgroup whose chunk holds `pos`.
+// Latency: every lane issues its K and V loads for the chunk's first 64 keys at kernel
+// entry, before the q/k preparation, so HBM latency overlaps the prologue; the key at
+// `pos` (just appended by this workgroup) is taken from LDS instead of the prefetch.
 #include "qt_device.h"
 
 #define QT_HD 128
 #define QT_CH_MAX 256
+#define QT_ATT_G 32
 
 struct QtAttnArgs {
     const float *q;          // PREP: raw [q | k | v]; else rotated q rows (this query row)
@@ -37,6 +41,11 @@ struct QtAttnArgs {
     float *out;              // [n_heads * 128]
 };
 
+// 8 dims (16 bytes) of key/value j for this lane, raw bf16 bits.
+__device__ __forceinline__ uint4 qt_ld_kv(const uint16_t *base, long long pos_stride, int j, int sub) {
+    return *reinterpret_cast<const uint4 *>(base + (long long)j * pos_stride + sub * 8);
+}
+
 template <int HPK, bool PREP>
 __global__ __launch_bounds__(QT_WG) void k_attn(QtAttnArgs a) {
     const int g = blockIdx.y, c = blockIdx.x, G = gridDim.x;
@@ -49,19 +58,37 @@ __global__ __launch_bounds__(QT_WG) void k_attn(QtAttnArgs a) {
     if (c >= nch) return;
     const int j0 = c * CH;
     const int n = min(CH, L - j0);
+    const bool append = PREP && (pos >= j0 && pos < j0 + n);
 
     __shared__ float qs[HPK][QT_HD];
     __shared__ float sc[HPK][QT_CH_MAX];
     __shared__ float ored[QT_WAVES][HPK][QT_HD];
     __shared__ float stat[HPK][2];
+    __shared__ __align__(16) uint16_t knew[QT_HD];
+    __shared__ __align__(16) uint16_t vnew[QT_HD];
+    __shared__ float mst[QT_ATT_G * HPK][2];
     __shared__ int last_flag;
 
-    uint16_t *Kg = a.K + (long long)g * a.head_stride;
-    uint16_t *Vg = a.V + (long long)g * a.head_stride;
+    const uint16_t *Kg = a.K + (long long)g * a.head_stride;
+    const uint16_t *Vg = a.V + (long long)g * a.head_stride;
+    const int sub = lane & 15, pg = lane >> 4;
+
+    // ---- 0. prefetch this lane's K/V chunks of the first 64 keys (independent of q) ----
+    uint4 kpre[4], vpre[4];
+#pragma unroll
+    for (int u = 0; u < 4; u++) {
+        const int jj = wave * 4 + pg + 16 * u;
+        if (jj < n) {
+            kpre[u] = qt_ld_kv(Kg, a.pos_stride, j0 + jj, sub);
+            vpre[u] = qt_ld_kv(Vg, a.pos_stride, j0 + jj, sub);
+        } else {
+            kpre[u] = make_uint4(0, 0, 0, 0);
+            vpre[u] = make_uint4(0, 0, 0, 0);
+        }
+    }
 
     // ---- 1. query heads (and the new key/value) ----
     if (PREP) {
-        const bool append = (pos >= j0 && pos < j0 + n);
         const int ntask = HPK + (append ? 1 : 0);
         for (int t = wave; t < ntask; t += QT_WAVES) {
             const bool isk = (t == HPK);
@@ -80,12 +107,14 @@ __global__ __launch_bounds__(QT_WG) void k_attn(QtAttnArgs a) {
                 qs[t][lane + 64] = r1;
             } else {
                 const float *vs = a.q + a.n_heads * QT_HD + a.n_kv * QT_HD + g * QT_HD;
-                uint16_t *kd = Kg + (long long)pos * a.pos_stride;
-                uint16_t *vd = Vg + (long long)pos * a.pos_stride;
-                kd[lane] = f2bf_trunc(r0);
-                kd[lane + 64] = f2bf_trunc(r1);
-                vd[lane] = f2bf_trunc(vs[lane]);
-                vd[lane + 64] = f2bf_trunc(vs[lane + 64]);
+                const uint16_t k0 = f2bf_trunc(r0), k1 = f2bf_trunc(r1);
+                const uint16_t v0 = f2bf_trunc(vs[lane]), v1 = f2bf_trunc(vs[lane + 64]);
+                uint16_t *kd = a.K + (long long)g * a.head_stride + (long long)pos * a.pos_stride;
+                uint16_t *vd = a.V + (long long)g * a.head_stride + (long long)pos * a.pos_stride;
+                kd[lane] = k0; kd[lane + 64] = k1;
+                vd[lane] = v0; vd[lane + 64] = v1;
+                knew[lane] = k0; knew[lane + 64] = k1;
+                vnew[lane] = v0; vnew[lane + 64] = v1;
             }
         }
     } else {
@@ -95,20 +124,20 @@ __global__ __launch_bounds__(QT_WG) void k_attn(QtAttnArgs a) {
     __syncthreads();
 
     // ---- 2. scores: 16 lanes per key (8 dims each), 4 keys per wave per step ----
-    const int sub = lane & 15, pg = lane >> 4;
     float qv[HPK][8];
 #pragma unroll
     for (int h = 0; h < HPK; h++)
 #pragma unroll
         for (int e = 0; e < 8; e++) qv[h][e] = qs[h][sub * 8 + e];
 
-    for (int base = wave * 4 + pg; base < n; base += 64) {
+    for (int blk = 0; blk < n; blk += 64) {
         uint4 kw[4];
 #pragma unroll
         for (int u = 0; u < 4; u++) {
-            const int jj = base + 16 * u;
-            kw[u] = (jj < n) ? *reinterpret_cast<const uint4 *>(Kg + (long long)(j0 + jj) * a.pos_stride + sub * 8)
-                             : make_uint4(0, 0, 0, 0);
+            const int jj = blk + wave * 4 + pg + 16 * u;
+            if (blk == 0) kw[u] = kpre[u];
+            else kw[u] = (jj < n) ? qt_ld_kv(Kg, a.pos_stride, j0 + jj, sub) : make_uint4(0, 0, 0, 0);
+            if (append && j0 + jj == pos) kw[u] = *reinterpret_cast<const uint4 *>(knew + sub * 8);
         }
 #pragma unroll
         for (int u = 0; u < 4; u++) {
@@ -116,7 +145,7 @@ __global__ __launch_bounds__(QT_WG) void k_attn(QtAttnArgs a) {
             float kf[8];
 #pragma unroll
             for (int m = 0; m < 4; m++) { kf[2 * m] = bf_lo(w4[m]); kf[2 * m + 1] = bf_hi(w4[m]); }
-            const int jj = base + 16 * u;
+            const int jj = blk + wave * 4 + pg + 16 * u;
 #pragma unroll
             for (int h = 0; h < HPK; h++) {
                 float s = 0.f;
@@ -151,17 +180,18 @@ __global__ __launch_bounds__(QT_WG) void k_attn(QtAttnArgs a) {
     for (int h = 0; h < HPK; h++)
 #pragma unroll
         for (int e = 0; e < 8; e++) o[h][e] = 0.f;
-    for (int base = wave * 4 + pg; base < n; base += 64) {
+    for (int blk = 0; blk < n; blk += 64) {
         uint4 vw[4];
 #pragma unroll
         for (int u = 0; u < 4; u++) {
-            const int jj = base + 16 * u;
-            vw[u] = (jj < n) ? *reinterpret_cast<const uint4 *>(Vg + (long long)(j0 + jj) * a.pos_stride + sub * 8)
-                             : make_uint4(0, 0, 0, 0);
+            const int jj = blk + wave * 4 + pg + 16 * u;
+            if (blk == 0) vw[u] = vpre[u];
+            else vw[u] = (jj < n) ? qt_ld_kv(Vg, a.pos_stride, j0 + jj, sub) : make_uint4(0, 0, 0, 0);
+            if (append && j0 + jj == pos) vw[u] = *reinterpret_cast<const uint4 *>(vnew + sub * 8);
         }
 #pragma unroll
         for (int u = 0; u < 4; u++) {
-            const int jj = base + 16 * u;
+            const int jj = blk + wave * 4 + pg + 16 * u;
             if (jj < n) {
                 const uint32_t w4[4] = {vw[u].x, vw[u].y, vw[u].z, vw[u].w};
                 float vf[8];
@@ -203,33 +233,50 @@ __global__ __launch_bounds__(QT_WG) void k_attn(QtAttnArgs a) {
         return;
     }
     constexpr int PS = 2 + QT_HD;
+    // Publish the partial with agent-scope (L2-bypassing) stores, wait for them to be
+    // acknowledged, then count arrivals with a relaxed device-scope atomic.  This avoids
+    // __threadfence(), whose L2 write-back + invalidate on every XCD costs ~17 us for a
+    // 256-workgroup grid on MI355X; the merging workgroup reads with agent-scope loads.
     float *mypart = a.part + ((size_t)(g * G + c) * HPK) * PS;
     for (int i = tid; i < HPK * QT_HD; i += QT_WG) {
         const int h = i / QT_HD, d = i % QT_HD;
-        mypart[h * PS + 2 + d] = ored[0][h][d] + ored[1][h][d] + ored[2][h][d] + ored[3][h][d];
+        st_agent(mypart + h * PS + 2 + d, ored[0][h][d] + ored[1][h][d] + ored[2][h][d] + ored[3][h][d]);
     }
-    if (tid < HPK) { mypart[tid * PS] = stat[tid][0]; mypart[tid * PS + 1] = stat[tid][1]; }
-    __threadfence();
+    if (tid < HPK) { st_agent(mypart + tid * PS, stat[tid][0]); st_agent(mypart + tid * PS + 1, stat[tid][1]); }
+    __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
-    if (tid == 0) last_flag = (atomicAdd(&a.cnt[g], 1u) == (unsigned)(nch - 1));
+    if (tid == 0)
+        last_flag = (__hip_atomic_fetch_add(&a.cnt[g], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+                     (unsigned)(nch - 1));
     __syncthreads();
     if (!last_flag) return;
-    __threadfence();
+    // Merge: chunk statistics into LDS with one parallel load round; then each thread
+    // owns one (head, dim) output and issues the loads of all chunk partials at once.
     const float *gp = a.part + (size_t)g * G * HPK * PS;
+    for (int i = tid; i < nch * HPK; i += QT_WG) {
+        mst[i][0] = ld_agent(gp + (size_t)i * PS);
+        mst[i][1] = ld_agent(gp + (size_t)i * PS + 1);
+    }
+    __syncthreads();
     for (int i = tid; i < HPK * QT_HD; i += QT_WG) {
         const int h = i / QT_HD, d = i % QT_HD;
+        float pv[QT_ATT_G];
+#pragma unroll
+        for (int cc = 0; cc < QT_ATT_G; cc++) pv[cc] = (cc < nch) ? ld_agent(gp + (size_t)(cc * HPK + h) * PS + 2 + d) : 0.f;
         float M = -INFINITY;
-        for (int cc = 0; cc < nch; cc++) M = fmaxf(M, gp[(cc * HPK + h) * PS]);
+        for (int cc = 0; cc < nch; cc++) M = fmaxf(M, mst[cc * HPK + h][0]);
         float l = 0.f, v = 0.f;
-        for (int cc = 0; cc < nch; cc++) {
-            const float *pp = gp + (cc * HPK + h) * PS;
-            const float f = expf(pp[0] - M);
-            l = fmaf(pp[1], f, l);
-            v = fmaf(pp[2 + d], f, v);
+#pragma unroll
+        for (int cc = 0; cc < QT_ATT_G; cc++) {
+            if (cc < nch) {
+                const float f = expf(mst[cc * HPK + h][0] - M);
+                l = fmaf(mst[cc * HPK + h][1], f, l);
+                v = fmaf(pv[cc], f, v);
+            }
         }
         a.out[(g * HPK + h) * QT_HD + d] = v * (1.0f / l);
     }
-    if (tid == 0) a.cnt[g] = 0u;
+    if (tid == 0) __hip_atomic_store(&a.cnt[g], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 extern "C" hipError_t qt_launch_attn(int prep, const float *q, const float *qn, const float *kn,
@@ -243,7 +290,8 @@ extern "C" hipError_t qt_launch_attn(int prep, const float *q, const float *qn, 
     a.K = K; a.V = V; a.pos_stride = pos_stride; a.head_stride = head_stride;
     a.n_heads = n_heads; a.n_kv = n_kv; a.scale = scale; a.part = part; a.cnt = cnt; a.out = out;
     if (head_dim != QT_HD || n_kv <= 0 || n_heads % n_kv) return hipErrorInvalidValue;
-    if (G <= 0) return hipErrorInvalidValue;
+    if (G <= 0 || G > QT_ATT_G) return hipErrorInvalidValue;
+    if (!prep && (Lval <= 0 || Lval > G * QT_CH_MAX)) return hipErrorInvalidValue;
     const int hpk = n_heads / n_kv;
     dim3 grid(G, n_kv);
 #define QT_ATT_CASE(H) \
@@ -257,8 +305,9 @@ extern "C" hipError_t qt_launch_attn(int prep, const float *q, const float *qn, 
     return hipGetLastError();
 }
 
-// Number of split-K chunks the grid needs so that CH <= QT_CH_MAX for every L <= max_len.
+// Split-K grid: QT_ATT_G chunks per kv head (256 workgroups for 8 kv heads); a chunk
+// holds at most QT_CH_MAX keys, so the grid serves caches up to 8192 positions.
+// Returns -1 when max_len does not fit.
 extern "C" int qt_attn_grid(int max_len) {
-    int g = (max_len + QT_CH_MAX - 1) / QT_CH_MAX;
-    return g < 32 ? 32 : g;
+    return max_len <= QT_ATT_G * QT_CH_MAX ? QT_ATT_G : -1;
 }

@@ -75,6 +75,17 @@ __device__ __forceinline__ float block_sum(float v, float *red) {
     return t;
 }
 
+// Agent-scope relaxed accesses: compiled to global_load/store with the sc1 bit, so they
+// go to the device coherence point instead of a (per-XCD, non-coherent) L2 line.  Used
+// for the few values one workgroup publishes to workgroups on other XCDs inside one
+// kernel; ordering is by s_waitcnt + a device-scope atomic, no L2 write-back/invalidate.
+__device__ __forceinline__ void st_agent(float *p, float v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float ld_agent(const float *p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 __device__ __forceinline__ uint4 ld_chunk(const uint8_t *p) {
     return *reinterpret_cast<const uint4 *>(p);
 }

@@ -14,7 +14,7 @@ enum { QT_EPI_STORE = 0, QT_EPI_RESID = 1, QT_EPI_SWIGLU = 2, QT_EPI_BIAS = 3 };
 
 hipError_t qt_launch_mv(int prec, int epi, int norm, const float *vin, const float *nw, float eps,
                         const uint8_t *w, const float *scale, const uint16_t *s16, int rows, int cols,
-                        float *out, float *resid, const float *bias, hipStream_t st);
+                        float *out, float *resid, const float *bias, float *nout, hipStream_t st);
 hipError_t qt_launch_attn(int prep, const float *q, const float *qn, const float *kn, const float *rc,
                           const float *rs, float eps, const int *d_pos, int Lval, uint16_t *K, uint16_t *V,
                           long long pos_stride, long long head_stride, int n_heads, int n_kv, int head_dim,
@@ -26,7 +26,7 @@ hipError_t qt_launch_rmsnorm_rows(float *x, const float *w, int rows, int n, flo
 hipError_t qt_launch_swiglu(const float *gu, float *out, int n, hipStream_t st);
 hipError_t qt_launch_select(const float *logits, int n, int mode, int *d_frame, int advance, int *tok,
                             int *hist, int hist_len, const uint16_t *emb, int emb_dim, float *out,
-                            hipStream_t st);
+                            int *d_pos, hipStream_t st);
 hipError_t qt_launch_gather(const int *tok, int tok_max, const uint16_t *table, int dim, float *out,
                             hipStream_t st);
 hipError_t qt_launch_copy_f32(const float *src, float *dst, int n, hipStream_t st);

@@ -12,11 +12,16 @@
 // (nib-8)*f16(scale) (qwen_tts_kernels.c:2810-2819), SwiGLU g/(1+expf(-g))*u
 // (qwen_tts_kernels.c:3857-3878), RMSNorm (x*inv)*w (qwen_tts_kernels.c:292-382).
 //
-// Work split: a workgroup stages the input vector (normalised if NORM) in LDS; each
-// lane copies the slice of it that its weight chunks multiply into registers once,
-// then a wave streams NR rows x CPL chunks per lane (NR*CPL independent 128-bit loads
-// in flight per lane) and reduces each row across its LPR lanes.  A wave owns
-// NR*(64/LPR) consecutive rows; a 256-thread workgroup owns 4x that.
+// Work split: a wave owns NR*(64/LPR) consecutive rows; each row is split over LPR
+// lanes, lane `sub` holding the 16-byte chunks c = sub + LPR*j (j < CPL) of it, so
+// NR*CPL independent 128-bit weight loads are in flight per lane and consecutive lanes
+// read consecutive 16-byte chunks (1 KiB per wave per load instruction).
+// Latency (about 1 us per cold miss on MI355X) is paid once: every load the wave needs
+// (weights, its slice of the input vector, norm gains, row scales, residual values) is
+// issued at entry, before any of them is consumed.  The input slice a lane needs is
+// exactly the columns of its chunks, read straight from global memory (coalesced; the
+// four waves of a workgroup share it through L1), and an LPR-lane group covers the whole
+// vector, so the RMSNorm statistic is a group reduction: no LDS staging, no barrier.
 #include "qt_device.h"
 
 template <int PREC> struct QtPrec;
@@ -36,26 +41,8 @@ struct QtMvArgs {
     float *out;          // STORE/SWIGLU/BIAS output
     float *resid;        // RESID target
     const float *bias;   // BIAS
+    float *nout;         // NORM: if set, workgroup 0 / wave 0 also writes RMSNorm(vin)*nw here
 };
-
-// Stage vin (optionally RMS-normalised) into LDS; returns nothing, xs[] valid after.
-template <bool NORM>
-__device__ __forceinline__ void qt_stage(const QtMvArgs &a, float *xs, float *red) {
-    const int cols = a.M.cols;
-    float ss = 0.f;
-    for (int i = threadIdx.x * 4; i < cols; i += QT_WG * 4) {
-        float4 v = *reinterpret_cast<const float4 *>(a.vin + i);
-        *reinterpret_cast<float4 *>(xs + i) = v;
-        if (NORM) ss += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
-    }
-    if (NORM) {
-        float tot = block_sum(ss, red);
-        float inv = 1.0f / sqrtf(tot / (float)cols + a.eps);
-        __syncthreads();
-        for (int i = threadIdx.x; i < cols; i += QT_WG) xs[i] = (xs[i] * inv) * a.nw[i];
-    }
-    __syncthreads();
-}
 
 template <int EPI>
 __device__ __forceinline__ void qt_epilogue(const QtMvArgs &a, int row, float acc) {
@@ -72,44 +59,15 @@ template <int PREC, int LPR, int CPL, int NR, int EPI, bool NORM>
 __global__ __launch_bounds__(QT_WG) void k_mv(QtMvArgs a) {
     constexpr int EPC = QtPrec<PREC>::EPC;
     constexpr int RPW = NR * (64 / LPR);
-    extern __shared__ float xs[];
-    __shared__ float red[QT_WAVES];
-    qt_stage<NORM>(a, xs, red);
+    constexpr int COLS = LPR * CPL * EPC;
 
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int grp = lane / LPR, sub = lane % LPR;
     const int row0 = (blockIdx.x * QT_WAVES + wave) * RPW + grp * NR;
-    const int rows = a.M.rows, cols = a.M.cols;
-    const size_t rb = qt_row_bytes(PREC, cols);
+    const int rows = a.M.rows;
+    constexpr size_t rb = PREC == QT_BF16 ? (size_t)COLS * 2 : PREC == QT_INT8 ? (size_t)COLS : (size_t)COLS / 2;
 
-    // activation slice for this lane's chunks (c = sub + LPR*j)
-    float xr[CPL][EPC];
-    float xsum[CPL];
-#pragma unroll
-    for (int j = 0; j < CPL; j++) {
-        const int c = sub + LPR * j;
-        const float *src = xs + c * EPC;
-        float s = 0.f;
-        if (PREC == QT_Q4) {
-            // word m of the chunk holds elements 8m..8m+7: low nibbles are the even ones
-#pragma unroll
-            for (int m = 0; m < 4; m++)
-#pragma unroll
-                for (int b = 0; b < 4; b++) {
-                    xr[j][m * 4 + b] = src[8 * m + 2 * b];
-                    xr[j][16 + m * 4 + b] = src[8 * m + 2 * b + 1];
-                }
-        } else {
-#pragma unroll
-            for (int e = 0; e < EPC; e++) xr[j][e] = src[e];
-        }
-        if (PREC != QT_BF16) {
-#pragma unroll
-            for (int e = 0; e < EPC; e++) s += xr[j][e];
-        }
-        xsum[j] = s;
-    }
-
+    // ---- every load up front ----
     uint4 wv[NR][CPL];
     float sc[NR][CPL];
 #pragma unroll
@@ -120,12 +78,93 @@ __global__ __launch_bounds__(QT_WG) void k_mv(QtMvArgs a) {
             const int c = sub + LPR * j;
             if (row < rows) {
                 wv[r][j] = ld_chunk(a.M.w + (size_t)row * rb + (size_t)c * 16);
-                if (PREC == QT_Q4) sc[r][j] = ref_f16_to_f32(a.M.s16[(size_t)row * (cols / 32) + c]);
+                if (PREC == QT_Q4) sc[r][j] = ref_f16_to_f32(a.M.s16[(size_t)row * (COLS / 32) + c]);
             } else {
                 wv[r][j] = make_uint4(0, 0, 0, 0);
                 sc[r][j] = 0.f;
             }
         }
+    }
+    float4 xv[CPL][EPC / 4];
+    float4 gv[CPL][EPC / 4];
+#pragma unroll
+    for (int j = 0; j < CPL; j++) {
+        const int c = sub + LPR * j;
+#pragma unroll
+        for (int q = 0; q < EPC / 4; q++) {
+            xv[j][q] = *reinterpret_cast<const float4 *>(a.vin + c * EPC + 4 * q);
+            if (NORM) gv[j][q] = *reinterpret_cast<const float4 *>(a.nw + c * EPC + 4 * q);
+        }
+    }
+    float rsc[NR], rres[NR];
+#pragma unroll
+    for (int r = 0; r < NR; r++) {
+        const int row = row0 + r;
+        const bool ok = sub == 0 && row < rows;
+        rsc[r] = (PREC == QT_INT8 && ok) ? a.M.scale[row] : 1.0f;
+        rres[r] = ((EPI == QT_EPI_RESID || EPI == QT_EPI_BIAS) && ok)
+                      ? (EPI == QT_EPI_RESID ? a.resid[row] : a.bias[row]) : 0.f;
+    }
+
+    // ---- input slice (RMS-normalised when NORM) in element order ----
+    float xe[CPL][EPC];
+#pragma unroll
+    for (int j = 0; j < CPL; j++)
+#pragma unroll
+        for (int q = 0; q < EPC / 4; q++) {
+            xe[j][4 * q + 0] = xv[j][q].x; xe[j][4 * q + 1] = xv[j][q].y;
+            xe[j][4 * q + 2] = xv[j][q].z; xe[j][4 * q + 3] = xv[j][q].w;
+        }
+    if (NORM) {
+        float ss = 0.f;
+#pragma unroll
+        for (int j = 0; j < CPL; j++)
+#pragma unroll
+            for (int e = 0; e < EPC; e++) ss = fmaf(xe[j][e], xe[j][e], ss);
+        ss = group_sum<LPR>(ss);
+        const float inv = 1.0f / sqrtf(ss / (float)COLS + a.eps);
+#pragma unroll
+        for (int j = 0; j < CPL; j++)
+#pragma unroll
+            for (int q = 0; q < EPC / 4; q++) {
+                xe[j][4 * q + 0] = (xe[j][4 * q + 0] * inv) * gv[j][q].x;
+                xe[j][4 * q + 1] = (xe[j][4 * q + 1] * inv) * gv[j][q].y;
+                xe[j][4 * q + 2] = (xe[j][4 * q + 2] * inv) * gv[j][q].z;
+                xe[j][4 * q + 3] = (xe[j][4 * q + 3] * inv) * gv[j][q].w;
+            }
+        if (a.nout && blockIdx.x == 0 && wave == 0 && grp == 0) {
+#pragma unroll
+            for (int j = 0; j < CPL; j++)
+#pragma unroll
+                for (int q = 0; q < EPC / 4; q++)
+                    *reinterpret_cast<float4 *>(a.nout + (sub + LPR * j) * EPC + 4 * q) =
+                        make_float4(xe[j][4 * q], xe[j][4 * q + 1], xe[j][4 * q + 2], xe[j][4 * q + 3]);
+        }
+    }
+    // operand order of the weight chunk: bf16/int8 natural; q4 word m holds elements
+    // 8m..8m+7 with the even ones in the low nibbles
+    float xr[CPL][EPC];
+    float xsum[CPL];
+#pragma unroll
+    for (int j = 0; j < CPL; j++) {
+        if (PREC == QT_Q4) {
+#pragma unroll
+            for (int m = 0; m < 4; m++)
+#pragma unroll
+                for (int b = 0; b < 4; b++) {
+                    xr[j][m * 4 + b] = xe[j][8 * m + 2 * b];
+                    xr[j][16 + m * 4 + b] = xe[j][8 * m + 2 * b + 1];
+                }
+        } else {
+#pragma unroll
+            for (int e = 0; e < EPC; e++) xr[j][e] = xe[j][e];
+        }
+        float s = 0.f;
+        if (PREC != QT_BF16) {
+#pragma unroll
+            for (int e = 0; e < EPC; e++) s += xr[j][e];
+        }
+        xsum[j] = s;
     }
 
     float acc[NR];
@@ -178,8 +217,7 @@ __global__ __launch_bounds__(QT_WG) void k_mv(QtMvArgs a) {
             for (int r = 0; r < NR; r += 2) {
                 const int row = row0 + r;
                 if (row + 1 < rows) {
-                    float g = acc[r], u = acc[r + 1];
-                    if (PREC == QT_INT8) { g *= a.M.scale[row]; u *= a.M.scale[row + 1]; }
+                    const float g = acc[r] * rsc[r], u = acc[r + 1] * rsc[r + 1];
                     a.out[row >> 1] = qt_silu_mul(g, u);
                 }
             }
@@ -188,9 +226,10 @@ __global__ __launch_bounds__(QT_WG) void k_mv(QtMvArgs a) {
             for (int r = 0; r < NR; r++) {
                 const int row = row0 + r;
                 if (row < rows) {
-                    float v = acc[r];
-                    if (PREC == QT_INT8) v *= a.M.scale[row];
-                    qt_epilogue<EPI>(a, row, v);
+                    const float v = acc[r] * rsc[r];
+                    if (EPI == QT_EPI_STORE) a.out[row] = v;
+                    else if (EPI == QT_EPI_RESID) a.resid[row] = rres[r] + v;
+                    else a.out[row] = v + rres[r];
                 }
             }
         }
@@ -216,7 +255,10 @@ __global__ __launch_bounds__(QT_WG) void k_mv_generic(QtMvArgs a) {
         float tot = block_sum(ss, red);
         float inv = 1.0f / sqrtf(tot / (float)cols + a.eps);
         __syncthreads();
-        for (int i = threadIdx.x; i < cols; i += QT_WG) xs[i] = (xs[i] * inv) * a.nw[i];
+        for (int i = threadIdx.x; i < cols; i += QT_WG) {
+            xs[i] = (xs[i] * inv) * a.nw[i];
+            if (a.nout && blockIdx.x == 0) a.nout[i] = xs[i];
+        }
     }
     __syncthreads();
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -261,8 +303,7 @@ static hipError_t launch_tuned(const QtMvArgs &a, hipStream_t st) {
     constexpr int RPW = NR * (64 / LPR);
     const int per_wg = RPW * QT_WAVES;
     const int grid = (a.M.rows + per_wg - 1) / per_wg;
-    hipLaunchKernelGGL((k_mv<PREC, LPR, CPL, NR, EPI, NORM>), dim3(grid), dim3(QT_WG),
-                       (size_t)a.M.cols * sizeof(float), st, a);
+    hipLaunchKernelGGL((k_mv<PREC, LPR, CPL, NR, EPI, NORM>), dim3(grid), dim3(QT_WG), 0, st, a);
     return hipGetLastError();
 }
 
@@ -275,7 +316,21 @@ static hipError_t launch_generic(const QtMvArgs &a, hipStream_t st) {
     return hipGetLastError();
 }
 
-// (prec, cols) -> tuned instantiation; NR*CPL ~ 8-12 128-bit loads in flight per lane.
+// Rows per lane-group: the largest of {4, 2, 1} (at most NRMAX) that still gives >= 2048
+// waves (two per SIMD on 256 CUs); SwiGLU needs gate/up row pairs, so NR >= 2 there.
+template <int PREC, int LPR, int CPL, int NRMAX, int EPI, bool NORM>
+static hipError_t launch_nr(const QtMvArgs &a, hipStream_t st) {
+    constexpr int G = 64 / LPR;
+    const int rows = a.M.rows;
+    if (NRMAX >= 4 && rows / (4 * G) >= 2048) return launch_tuned<PREC, LPR, CPL, 4, EPI, NORM>(a, st);
+    if (NRMAX >= 2 && (EPI == QT_EPI_SWIGLU || rows / (2 * G) >= 2048))
+        return launch_tuned<PREC, LPR, CPL, 2, EPI, NORM>(a, st);
+    if (EPI == QT_EPI_SWIGLU) return launch_tuned<PREC, LPR, CPL, 2, EPI, NORM>(a, st);
+    return launch_tuned<PREC, LPR, CPL, 1, EPI, NORM>(a, st);
+}
+
+// (prec, cols) -> tuned instantiation: one 16-byte chunk per lane per load, CPL chunks
+// per row per lane, NR*CPL independent 128-bit loads in flight per lane.
 template <int EPI, bool NORM>
 static hipError_t dispatch(int prec, const QtMvArgs &a, hipStream_t st) {
     const int c = a.M.cols;
@@ -283,24 +338,24 @@ static hipError_t dispatch(int prec, const QtMvArgs &a, hipStream_t st) {
     if (aligned) {
         if (prec == QT_BF16) {
             switch (c) {
-            case 1024: return launch_tuned<QT_BF16, 64, 2, 4, EPI, NORM>(a, st);
-            case 2048: return launch_tuned<QT_BF16, 64, 4, 2, EPI, NORM>(a, st);
-            case 3072: return launch_tuned<QT_BF16, 64, 6, 2, EPI, NORM>(a, st);
-            case 6144: return launch_tuned<QT_BF16, 64, 12, 2, EPI, NORM>(a, st);
+            case 1024: return launch_nr<QT_BF16, 64, 2, 4, EPI, NORM>(a, st);
+            case 2048: return launch_nr<QT_BF16, 64, 4, 2, EPI, NORM>(a, st);
+            case 3072: return launch_nr<QT_BF16, 64, 6, 2, EPI, NORM>(a, st);
+            case 6144: return launch_nr<QT_BF16, 64, 12, 2, EPI, NORM>(a, st);
             }
         } else if (prec == QT_INT8) {
             switch (c) {
-            case 1024: return launch_tuned<QT_INT8, 64, 1, 8, EPI, NORM>(a, st);
-            case 2048: return launch_tuned<QT_INT8, 64, 2, 4, EPI, NORM>(a, st);
-            case 3072: return launch_tuned<QT_INT8, 64, 3, 4, EPI, NORM>(a, st);
-            case 6144: return launch_tuned<QT_INT8, 64, 6, 2, EPI, NORM>(a, st);
+            case 1024: return launch_nr<QT_INT8, 64, 1, 4, EPI, NORM>(a, st);
+            case 2048: return launch_nr<QT_INT8, 64, 2, 4, EPI, NORM>(a, st);
+            case 3072: return launch_nr<QT_INT8, 64, 3, 4, EPI, NORM>(a, st);
+            case 6144: return launch_nr<QT_INT8, 64, 6, 2, EPI, NORM>(a, st);
             }
         } else {
             switch (c) {
-            case 1024: return launch_tuned<QT_Q4, 32, 1, 8, EPI, NORM>(a, st);
-            case 2048: return launch_tuned<QT_Q4, 64, 1, 8, EPI, NORM>(a, st);
-            case 3072: return launch_tuned<QT_Q4, 32, 3, 4, EPI, NORM>(a, st);
-            case 6144: return launch_tuned<QT_Q4, 64, 3, 4, EPI, NORM>(a, st);
+            case 1024: return launch_nr<QT_Q4, 32, 1, 4, EPI, NORM>(a, st);
+            case 2048: return launch_nr<QT_Q4, 64, 1, 4, EPI, NORM>(a, st);
+            case 3072: return launch_nr<QT_Q4, 32, 3, 4, EPI, NORM>(a, st);
+            case 6144: return launch_nr<QT_Q4, 64, 3, 4, EPI, NORM>(a, st);
             }
         }
     }
@@ -312,11 +367,11 @@ static hipError_t dispatch(int prec, const QtMvArgs &a, hipStream_t st) {
 extern "C" hipError_t qt_launch_mv(int prec, int epi, int norm, const float *vin, const float *nw,
                                    float eps, const uint8_t *w, const float *scale,
                                    const uint16_t *s16, int rows, int cols, float *out,
-                                   float *resid, const float *bias, hipStream_t st) {
+                                   float *resid, const float *bias, float *nout, hipStream_t st) {
     QtMvArgs a;
     a.vin = vin; a.nw = nw; a.eps = eps;
     a.M.w = w; a.M.scale = scale; a.M.s16 = s16; a.M.rows = rows; a.M.cols = cols;
-    a.out = out; a.resid = resid; a.bias = bias;
+    a.out = out; a.resid = resid; a.bias = bias; a.nout = nout;
     if (rows <= 0 || cols <= 0) return hipErrorInvalidValue;
     if (epi == QT_EPI_SWIGLU && (rows & 1)) return hipErrorInvalidValue;
     if (prec == QT_Q4 && (cols % 32)) return hipErrorInvalidValue;

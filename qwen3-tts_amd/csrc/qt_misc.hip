@@ -4,21 +4,47 @@
 #include "qt_device.h"
 
 // out = RMSNorm(x)*w (qwen_tts_kernels.c:292-382); optionally advance *d_pos by one
-// (the resident decode loop's device-side position).  One workgroup.
-__global__ __launch_bounds__(QT_WG) void k_rmsnorm(const float *x, const float *w, float *out, int n,
-                                                   float eps, int *d_pos) {
-    __shared__ float red[QT_WAVES];
+// (the resident decode loop's device-side position).  One 1024-thread workgroup; every
+// thread issues its (<= 4) loads before using any, so the kernel pays one memory latency.
+#define QT_BIG 1024
+__device__ __forceinline__ float big_block_sum(float v, float *red) {
+    v = group_sum<64>(v);
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    if (lane == 0) red[wave] = v;
+    __syncthreads();
+    float t = 0.f;
+#pragma unroll
+    for (int i = 0; i < QT_BIG / 64; i++) t += red[i];
+    return t;
+}
+
+__global__ __launch_bounds__(QT_BIG) void k_rmsnorm(const float *x, const float *w, float *out, int n,
+                                                    float eps, int *d_pos) {
+    __shared__ float red[QT_BIG / 64];
+    float xv[4], wv[4];
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        const int i = threadIdx.x + k * QT_BIG;
+        xv[k] = i < n ? x[i] : 0.f;
+        wv[k] = i < n ? w[i] : 0.f;
+    }
     float ss = 0.f;
-    for (int i = threadIdx.x; i < n; i += QT_WG) ss += x[i] * x[i];
-    float tot = block_sum(ss, red);
-    float inv = 1.0f / sqrtf(tot / (float)n + eps);
-    for (int i = threadIdx.x; i < n; i += QT_WG) out[i] = (x[i] * inv) * w[i];
+#pragma unroll
+    for (int k = 0; k < 4; k++) ss += xv[k] * xv[k];
+    const float tot = big_block_sum(ss, red);
+    const float inv = 1.0f / sqrtf(tot / (float)n + eps);
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        const int i = threadIdx.x + k * QT_BIG;
+        if (i < n) out[i] = (xv[k] * inv) * wv[k];
+    }
     if (d_pos && threadIdx.x == 0) *d_pos += 1;
 }
 
 extern "C" hipError_t qt_launch_rmsnorm(const float *x, const float *w, float *out, int n, float eps,
                                         int *d_pos, hipStream_t st) {
-    hipLaunchKernelGGL(k_rmsnorm, dim3(1), dim3(QT_WG), 0, st, x, w, out, n, eps, d_pos);
+    if (n <= 0 || n > 4 * QT_BIG) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_rmsnorm, dim3(1), dim3(QT_BIG), 0, st, x, w, out, n, eps, d_pos);
     return hipGetLastError();
 }
 
@@ -56,17 +82,26 @@ extern "C" hipError_t qt_launch_swiglu(const float *gu, float *out, int n, hipSt
 // hist[*d_frame % hist_len]; advance != 0 increments *d_frame.  When emb != NULL it
 // also gathers the next input embedding out[i] = bf16(emb[tok*emb_dim + i])
 // (qwen_tts.c:919-924).  One workgroup.
-__global__ __launch_bounds__(QT_WG) void k_select(const float *logits, int n, int mode, int *d_frame, int advance,
-                                                  int *tok, int *hist, int hist_len, const uint16_t *emb,
-                                                  int emb_dim, float *out) {
-    __shared__ float bv_s[QT_WAVES];
-    __shared__ int bi_s[QT_WAVES];
+__global__ __launch_bounds__(QT_BIG) void k_select(const float *logits, int n, int mode, int *d_frame, int advance,
+                                                   int *tok, int *hist, int hist_len, const uint16_t *emb,
+                                                   int emb_dim, float *out, int *d_pos) {
+    __shared__ float bv_s[QT_BIG / 64];
+    __shared__ int bi_s[QT_BIG / 64];
     __shared__ int t_s;
     const int frame = d_frame ? *d_frame : 0;
+    float lv[4];
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        const int i = threadIdx.x + k * QT_BIG;
+        lv[k] = i < n ? logits[i] : -INFINITY;
+    }
     float bv = (mode == 0) ? -1e30f : -INFINITY;
     int bi = 0x7FFFFFFF;
-    for (int i = threadIdx.x; i < n; i += QT_WG) {
-        float v = logits[i];
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        const int i = threadIdx.x + k * QT_BIG;
+        if (i >= n) continue;
+        float v = lv[k];
         if (mode == 1) {
             v = fminf(fmaxf(v, -100.0f), 100.0f);
             if (i >= 2048 && i != 2150) v = -1e30f;
@@ -85,26 +120,28 @@ __global__ __launch_bounds__(QT_WG) void k_select(const float *logits, int n, in
     __syncthreads();
     if (threadIdx.x == 0) {
         float b = bv_s[0]; int ix = bi_s[0];
-        for (int w = 1; w < QT_WAVES; w++)
+        for (int w = 1; w < QT_BIG / 64; w++)
             if (bv_s[w] > b || (bv_s[w] == b && bi_s[w] < ix)) { b = bv_s[w]; ix = bi_s[w]; }
         if (ix == 0x7FFFFFFF) ix = 0;   // nothing beat the start value: index 0
         tok[0] = ix;
         if (hist) hist[frame % hist_len] = ix;
         t_s = ix;
+        if (advance && d_frame) *d_frame = frame + 1;
+        if (d_pos) *d_pos += 1;
     }
     __syncthreads();
     if (emb) {
         const int t = t_s;
-        for (int i = threadIdx.x; i < emb_dim; i += QT_WG) out[i] = bf16f(emb[(size_t)t * emb_dim + i]);
+        for (int i = threadIdx.x; i < emb_dim; i += QT_BIG) out[i] = bf16f(emb[(size_t)t * emb_dim + i]);
     }
-    if (advance && d_frame && threadIdx.x == 0) *d_frame = frame + 1;
 }
 
 extern "C" hipError_t qt_launch_select(const float *logits, int n, int mode, int *d_frame, int advance, int *tok,
                                        int *hist, int hist_len, const uint16_t *emb, int emb_dim, float *out,
-                                       hipStream_t st) {
-    hipLaunchKernelGGL(k_select, dim3(1), dim3(QT_WG), 0, st, logits, n, mode, d_frame, advance, tok, hist,
-                       hist_len, emb, emb_dim, out);
+                                       int *d_pos, hipStream_t st) {
+    if (n <= 0 || n > 4 * QT_BIG) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_select, dim3(1), dim3(QT_BIG), 0, st, logits, n, mode, d_frame, advance, tok, hist,
+                       hist_len, emb, emb_dim, out, d_pos);
     return hipGetLastError();
 }
 

@@ -104,7 +104,7 @@ fail:
 static hipError_t mv(const dmat_t *m, int epi, int norm, const float *vin, const float *nw, float eps,
                      float *out, float *resid, const float *bias, hipStream_t st) {
     return qt_launch_mv(m->prec, epi, norm, vin, nw, eps, m->w, m->scale, m->s16, m->rows, m->cols,
-                        out, resid, bias, st);
+                        out, resid, bias, NULL, st);
 }
 
 static float *up_f32(const float *src, size_t n, hipStream_t st) {
@@ -154,7 +154,7 @@ static int stack_init(stack_t *s, const qwen_hip_talker_desc_t *d, hipStream_t s
     REQ(d && d->layers, "null descriptor");
     REQ(d->head_dim == 128, "head_dim %d unsupported (128 only)", d->head_dim);
     REQ(d->n_kv_heads > 0 && d->n_heads % d->n_kv_heads == 0, "bad head counts %d/%d", d->n_heads, d->n_kv_heads);
-    REQ(d->kv_max > 0 && d->kv_max <= 65536, "kv_max %d out of range", d->kv_max);
+    REQ(d->kv_max > 0 && qt_attn_grid(d->kv_max) > 0, "kv_max %d out of range (1..8192)", d->kv_max);
     REQ(d->rope_cos && d->rope_sin && d->rope_len > 0, "missing rope tables");
     REQ(d->prec >= 0 && d->prec <= 2, "bad prec %d", d->prec);
     s->H = d->hidden; s->F = d->inter; s->nh = d->n_heads; s->nkv = d->n_kv_heads; s->hd = d->head_dim;
@@ -246,7 +246,7 @@ typedef struct {
     float *h_in, *h_out;    /* pinned: embed in; [hidden | x] out */
     int *h_pos;
     hipGraphExec_t exec, gexec;
-    int graph_ready, ggraph_ready;
+    int graph_ready, ggraph_ready, greedy_ready;
     int dev_pos;            /* host mirror of *d_pos (-1 unknown) */
     int dead;
     /* greedy loop */
@@ -330,6 +330,14 @@ fail:
 
 static hipError_t talker_body_cb(void *a) { return talker_body((talker_t *)a); }
 
+/* QWEN_HIP_GRAPH=0 replays the same launch sequence directly on the stream instead of
+ * through a captured hipGraph (profilers that cannot trace graph replays; A/B checks). */
+static int graphs_enabled(void) {
+    static int on = -1;
+    if (on < 0) { const char *e = getenv("QWEN_HIP_GRAPH"); on = !(e && e[0] == '0'); }
+    return on;
+}
+
 static int talker_set_pos(talker_t *t, int pos) {
     if (t->dev_pos == pos) return 0;
     t->h_pos[0] = pos;
@@ -350,7 +358,7 @@ static int talker_step_impl(talker_t *t, const float *embed, float *hidden_out, 
     if (talker_set_pos(t, pos) != 0) goto fail;
     memcpy(t->h_in, embed, (size_t)H * sizeof(float));
     HCK(hipMemcpyAsync(t->io + H, t->h_in, (size_t)H * sizeof(float), hipMemcpyHostToDevice, t->st));
-    if (use_graph) {
+    if (use_graph && graphs_enabled()) {
         if (!t->graph_ready) {
             if (capture(t->st, &t->exec, talker_body_cb, t) != 0) goto fail;
             t->graph_ready = 1;
@@ -430,10 +438,15 @@ static hipError_t greedy_body(void *a) {
     talker_t *t = (talker_t *)a;
     hipError_t e;
     const int H = t->s.H;
-    if ((e = talker_body(t))) return e;
-    if ((e = mv(&t->head_m, QT_EPI_STORE, 0, t->io, NULL, t->s.eps, t->logits, NULL, NULL, t->st))) return e;
+    float *x = t->io + H;
+    if ((e = stack_body(&t->s, x, t->d_pos, t->st))) return e;
+    /* final norm fused into the codec head: the head matvec normalises x with
+     * talker_norm and also writes the normed hidden to io[0:H) */
+    if ((e = qt_launch_mv(t->head_m.prec, QT_EPI_STORE, 1, x, t->s.final_norm, t->s.eps, t->head_m.w, NULL, NULL,
+                          t->head_m.rows, t->head_m.cols, t->logits, NULL, NULL, t->io, t->st))) return e;
+    /* greedy code0, next embedding into x, frame and position advance */
     return qt_launch_select(t->logits, t->codec_vocab, 1, t->d_frame, 1, t->d_tok, t->d_hist, t->hist_len,
-                            t->codec_emb, H, t->io + H, t->st);
+                            t->codec_emb, H, x, t->d_pos, t->st);
 }
 
 int qwen_hip_talker_greedy(void *state, const uint16_t *codec_head, const uint16_t *codec_emb, int codec_vocab,
@@ -447,6 +460,7 @@ int qwen_hip_talker_greedy(void *state, const uint16_t *codec_head, const uint16
     REQ(pos >= 0 && pos + n_steps <= t->s.kv_max && pos + n_steps <= t->s.rope_len, "positions exceed kv_max");
     if (t->head_host != codec_head || t->emb_host != codec_emb || t->codec_vocab != codec_vocab) {
         if (t->ggraph_ready) { (void)hipGraphExecDestroy(t->gexec); t->ggraph_ready = 0; }
+        t->greedy_ready = 0;
         dmat_free(&t->head_m);
         if (t->codec_emb) (void)hipFree(t->codec_emb);
         if (t->logits) (void)hipFree(t->logits);
@@ -464,11 +478,12 @@ int qwen_hip_talker_greedy(void *state, const uint16_t *codec_head, const uint16
     HCK(hipMemcpyAsync(t->d_frame, t->h_pos + 1, sizeof(int), hipMemcpyHostToDevice, t->st));
     memcpy(t->h_in, embed, (size_t)H * sizeof(float));
     HCK(hipMemcpyAsync(t->io + H, t->h_in, (size_t)H * sizeof(float), hipMemcpyHostToDevice, t->st));
-    if (!t->ggraph_ready) {
+    if (graphs_enabled() && !t->ggraph_ready) {
         if (capture(t->st, &t->gexec, greedy_body, t) != 0) goto fail;
         t->ggraph_ready = 1;
     }
-    for (int i = 0; i < n_steps; i++) HCK(hipGraphLaunch(t->gexec, t->st));
+    t->greedy_ready = 1;
+    for (int i = 0; i < n_steps; i++) HCK(graphs_enabled() ? hipGraphLaunch(t->gexec, t->st) : greedy_body(t));
     {
         int *hist = (int *)malloc((size_t)t->hist_len * sizeof(int));
         REQ(hist, "host alloc");
@@ -489,10 +504,10 @@ fail:
 
 int qwen_hip_talker_greedy_async(void *state, int n_steps) {
     talker_t *t = (talker_t *)state;
-    if (!t || t->dead || !t->ggraph_ready) { SETERR("greedy loop not initialised"); return -1; }
+    if (!t || t->dead || !t->greedy_ready) { SETERR("greedy loop not initialised"); return -1; }
     REQ(t->dev_pos >= 0 && t->dev_pos + n_steps <= t->s.kv_max && t->dev_pos + n_steps <= t->s.rope_len,
         "positions exceed kv_max");
-    for (int i = 0; i < n_steps; i++) HCK(hipGraphLaunch(t->gexec, t->st));
+    for (int i = 0; i < n_steps; i++) HCK(graphs_enabled() ? hipGraphLaunch(t->gexec, t->st) : greedy_body(t));
     t->dev_pos += n_steps;
     return 0;
 fail:
@@ -574,7 +589,7 @@ typedef struct {
     int *d_codes;                         /* [16]: [0] = code0, [1..15] = out codes */
     float *h_x; int *h_codes;             /* pinned */
     hipGraphExec_t fexec, pexec;
-    int fready, pready;
+    int fready, pready, frame_ready;
     int *d_steppos;
     int dead;
 } cp_t;
@@ -683,7 +698,7 @@ static hipError_t cp_frame_body(void *a) {
             if ((e = stack_body(&c->s, c->x, c->d_posv + g + 1, c->st))) return e;
         }
         if ((e = mv(&c->lm[g], QT_EPI_STORE, 1, c->x, c->s.final_norm, c->s.eps, c->logits, NULL, NULL, c->st))) return e;
-        if ((e = qt_launch_select(c->logits, c->codebook, 0, NULL, 0, c->d_codes + g + 1, NULL, 0, NULL, 0, NULL, c->st))) return e;
+        if ((e = qt_launch_select(c->logits, c->codebook, 0, NULL, 0, c->d_codes + g + 1, NULL, 0, NULL, 0, NULL, NULL, c->st))) return e;
     }
     return hipSuccess;
 }
@@ -695,11 +710,12 @@ int qwen_hip_cp_frame(void *state, const float *talker_hidden, int code0, int *o
     c->h_codes[0] = code0;
     HCK(hipMemcpyAsync(c->th, c->h_x, (size_t)c->talker_hidden * sizeof(float), hipMemcpyHostToDevice, c->st));
     HCK(hipMemcpyAsync(c->d_codes, c->h_codes, sizeof(int), hipMemcpyHostToDevice, c->st));
-    if (!c->fready) {
+    if (graphs_enabled() && !c->fready) {
         if (capture(c->st, &c->fexec, cp_frame_body, c) != 0) goto fail;
         c->fready = 1;
     }
-    HCK(hipGraphLaunch(c->fexec, c->st));
+    c->frame_ready = 1;
+    HCK(graphs_enabled() ? hipGraphLaunch(c->fexec, c->st) : cp_frame_body(c));
     HCK(hipMemcpyAsync(c->h_codes + 16, c->d_codes, 16 * sizeof(int), hipMemcpyDeviceToHost, c->st));
     HCK(hipStreamSynchronize(c->st));
     for (int g = 0; g < 15; g++) out_codes[g] = c->h_codes[16 + 1 + g];
@@ -713,8 +729,8 @@ fail:
 
 int qwen_hip_cp_frame_async(void *state, int n_frames) {
     cp_t *c = (cp_t *)state;
-    if (!c || c->dead || !c->fready) { SETERR("CP frame graph not initialised"); return -1; }
-    for (int i = 0; i < n_frames; i++) HCK(hipGraphLaunch(c->fexec, c->st));
+    if (!c || c->dead || !c->frame_ready) { SETERR("CP frame not initialised"); return -1; }
+    for (int i = 0; i < n_frames; i++) HCK(graphs_enabled() ? hipGraphLaunch(c->fexec, c->st) : cp_frame_body(c));
     return 0;
 fail:
     c->dead = 1;
@@ -740,11 +756,11 @@ int qwen_hip_cp_step(void *state, float *x, int pos) {
     c->h_codes[32] = pos;
     HCK(hipMemcpyAsync(c->x, c->h_x, (size_t)H * sizeof(float), hipMemcpyHostToDevice, c->st));
     HCK(hipMemcpyAsync(c->d_steppos, c->h_codes + 32, sizeof(int), hipMemcpyHostToDevice, c->st));
-    if (!c->pready) {
+    if (graphs_enabled() && !c->pready) {
         if (capture(c->st, &c->pexec, cp_pass_body, c) != 0) goto fail;
         c->pready = 1;
     }
-    HCK(hipGraphLaunch(c->pexec, c->st));
+    HCK(graphs_enabled() ? hipGraphLaunch(c->pexec, c->st) : cp_pass_body(c));
     HCK(hipMemcpyAsync(c->h_x, c->x, (size_t)H * sizeof(float), hipMemcpyDeviceToHost, c->st));
     HCK(hipStreamSynchronize(c->st));
     memcpy(x, c->h_x, (size_t)H * sizeof(float));
@@ -886,7 +902,7 @@ int qwen_hip_op_argmax_matvec(int prec, const float *x, const void *W, const flo
     HCK(hipMalloc((void **)&dt, sizeof(int)));
     HCK(hipMemcpyAsync(dx, x, (size_t)in_dim * sizeof(float), hipMemcpyHostToDevice, st));
     HCK(mv(&m, QT_EPI_STORE, 0, dx, NULL, 0.f, dy, NULL, NULL, st));
-    HCK(qt_launch_select(dy, out_dim, 0, NULL, 0, dt, NULL, 0, NULL, 0, NULL, st));
+    HCK(qt_launch_select(dy, out_dim, 0, NULL, 0, dt, NULL, 0, NULL, 0, NULL, NULL, st));
     HCK(hipMemcpyAsync(&tok, dt, sizeof(int), hipMemcpyDeviceToHost, st));
     HCK(hipStreamSynchronize(st));
 fail:
@@ -905,6 +921,7 @@ int qwen_hip_op_causal_attention_bf16kv(float *out, const float *Q, const uint16
     const int qh = n_heads * head_dim, kvd = n_kv_heads * head_dim;
     const int G = qt_attn_grid(seq_k);
     const int hpk = n_heads / n_kv_heads;
+    REQ(G > 0, "seq_k %d exceeds the split-K grid (8192 keys)", seq_k);
     HCK(hipMalloc((void **)&dq, (size_t)seq_q * qh * sizeof(float)));
     HCK(hipMalloc((void **)&dout, (size_t)seq_q * qh * sizeof(float)));
     HCK(hipMalloc((void **)&dk, (size_t)seq_k * kvd * 2));
