@@ -21,12 +21,17 @@ LIB = os.path.join(PKG, "libqwen_tts_hip.so")
 ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
 ARCH = os.environ.get("QWEN_HIP_ARCH", "gfx950")
 
-HIP_SOURCES = ["qt_matvec.hip", "qt_attn.hip", "qt_misc.hip"]
+HIP_SOURCES = ["qt_matvec.hip", "qt_attn.hip", "qt_misc.hip", "qt_pstep.hip"]
 C_SOURCES = ["qwen_tts_hip.c"]
 
 HIPCC_FLAGS = ["-O3", "-fPIC", "-std=c++17", f"--offload-arch={ARCH}",
                "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+               "-ffp-contract=off",
                "-Wall", "-Wno-unused-function", "-I", CSRC, "-I", os.path.join(ROOT, "include")]
+# -ffp-contract=off: every fused multiply-add in the kernels is an explicit fmaf, so two
+# kernels that state the same arithmetic round identically (hipcc's default contracts
+# a*b+c wherever instruction selection finds it, e.g. an RMSNorm product into the int8
+# activation sum, and then the fused step and the per-kernel path disagree by an ulp).
 CC_FLAGS = ["-O2", "-fPIC", "-std=gnu11", "-Wall", "-Wextra", "-Wno-unused-parameter",
             "-D__HIP_PLATFORM_AMD__", "-I", os.path.join(ROCM, "include"), "-I", CSRC,
             "-I", os.path.join(ROOT, "include")]

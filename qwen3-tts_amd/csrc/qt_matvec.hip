@@ -190,7 +190,7 @@ __global__ __launch_bounds__(QT_WG) void k_mv(QtMvArgs a) {
                     t = fmaf((float)((w >> 16) & 0xFFu), xr[j][4 * m + 2], t);
                     t = fmaf((float)(w >> 24), xr[j][4 * m + 3], t);
                 }
-                s += t - 128.0f * xsum[j];
+                s += fmaf(-128.0f, xsum[j], t);
             } else {
                 float t = 0.f;
 #pragma unroll
@@ -205,7 +205,7 @@ __global__ __launch_bounds__(QT_WG) void k_mv(QtMvArgs a) {
                     t = fmaf((float)((hi >> 16) & 0xFFu), xr[j][16 + m * 4 + 2], t);
                     t = fmaf((float)(hi >> 24), xr[j][16 + m * 4 + 3], t);
                 }
-                s = fmaf(sc[r][j], t - 8.0f * xsum[j], s);
+                s = fmaf(sc[r][j], fmaf(-8.0f, xsum[j], t), s);
             }
         }
         acc[r] = group_sum<LPR>(s);
@@ -217,7 +217,7 @@ __global__ __launch_bounds__(QT_WG) void k_mv(QtMvArgs a) {
             for (int r = 0; r < NR; r += 2) {
                 const int row = row0 + r;
                 if (row + 1 < rows) {
-                    const float g = acc[r] * rsc[r], u = acc[r + 1] * rsc[r + 1];
+                    const float g = __fmul_rn(acc[r], rsc[r]), u = __fmul_rn(acc[r + 1], rsc[r + 1]);
                     a.out[row >> 1] = qt_silu_mul(g, u);
                 }
             }
@@ -226,10 +226,10 @@ __global__ __launch_bounds__(QT_WG) void k_mv(QtMvArgs a) {
             for (int r = 0; r < NR; r++) {
                 const int row = row0 + r;
                 if (row < rows) {
-                    const float v = acc[r] * rsc[r];
+                    const float v = __fmul_rn(acc[r], rsc[r]);
                     if (EPI == QT_EPI_STORE) a.out[row] = v;
-                    else if (EPI == QT_EPI_RESID) a.resid[row] = rres[r] + v;
-                    else a.out[row] = v + rres[r];
+                    else if (EPI == QT_EPI_RESID) a.resid[row] = __fadd_rn(rres[r], v);
+                    else a.out[row] = __fadd_rn(v, rres[r]);
                 }
             }
         }

@@ -256,20 +256,94 @@ typedef struct {
     float *logits;
     dmat_t head_m;
     int hist_len;
+    /* persistent single-kernel step (qt_pstep.hip) */
+    int ps_on;
+    void *ps_layers;        /* device layer table */
+    float *ps_ring, *ps_part, *ps_slots, *ps_xin;
+    unsigned *ps_cnt, *ps_bar;
+    int *ps_err;
+    int *h_err;             /* pinned */
+    size_t ps_P, ps_OXB;    /* ring block floats per layer, offset of xb */
 } talker_t;
+
+static int persistent_enabled(void) {
+    static int on = -1;
+    if (on < 0) { const char *e = getenv("QWEN_HIP_PERSISTENT"); on = !(e && e[0] == '0'); }
+    return on;
+}
 
 static void talker_destroy(talker_t *t) {
     if (!t) return;
     if (t->graph_ready) (void)hipGraphExecDestroy(t->exec);
     if (t->ggraph_ready) (void)hipGraphExecDestroy(t->gexec);
     stack_free(&t->s);
-    void *bufs[] = {t->io, t->d_pos, t->d_frame, t->d_tok, t->d_hist, t->codec_head, t->codec_emb, t->logits};
+    void *bufs[] = {t->io, t->d_pos, t->d_frame, t->d_tok, t->d_hist, t->codec_head, t->codec_emb, t->logits,
+                    t->ps_layers, t->ps_ring, t->ps_part, t->ps_slots, t->ps_xin, t->ps_cnt, t->ps_bar, t->ps_err};
     for (size_t i = 0; i < sizeof bufs / sizeof bufs[0]; i++) if (bufs[i]) (void)hipFree(bufs[i]);
     if (t->h_in) (void)hipHostFree(t->h_in);
     if (t->h_out) (void)hipHostFree(t->h_out);
     if (t->h_pos) (void)hipHostFree(t->h_pos);
+    if (t->h_err) (void)hipHostFree(t->h_err);
     if (t->st) (void)hipStreamDestroy(t->st);
     free(t);
+}
+
+/* Resources of the persistent step: activation ring, layer table, barrier blocks. */
+static int ps_setup(talker_t *t) {
+    stack_t *s = &t->s;
+    void *host_tab = NULL;
+    const size_t lb = qt_pstep_layer_bytes();
+    t->ps_P = (size_t)(s->qd + 2 * s->kvd) + s->qd + 2 * (size_t)s->H + s->F;
+    t->ps_OXB = (size_t)(s->qd + 2 * s->kvd) + s->qd + s->H + s->F;
+    HCK(hipMalloc((void **)&t->ps_ring, qt_pstep_ring_floats(s->H, s->F, s->L) * sizeof(float)));
+    HCK(hipMalloc((void **)&t->ps_part, (size_t)s->nkv * 32 * (s->nh / s->nkv) * 130 * sizeof(float)));
+    HCK(hipMalloc((void **)&t->ps_cnt, 64 * sizeof(unsigned)));
+    HCK(hipMalloc((void **)&t->ps_bar, qt_pstep_bar_words() * sizeof(unsigned)));
+    HCK(hipMalloc((void **)&t->ps_err, 64));
+    HCK(hipMalloc((void **)&t->ps_slots, 256 * 2 * sizeof(float)));
+    HCK(hipMalloc((void **)&t->ps_xin, (size_t)s->H * sizeof(float)));
+    HCK(hipHostMalloc((void **)&t->h_err, 64, hipHostMallocDefault));
+    HCK(hipMemsetAsync(t->ps_cnt, 0, 64 * sizeof(unsigned), t->st));
+    HCK(hipMemsetAsync(t->ps_bar, 0, qt_pstep_bar_words() * sizeof(unsigned), t->st));
+    HCK(hipMemsetAsync(t->ps_err, 0, 64, t->st));
+    HCK(hipMemsetAsync(t->ps_ring, 0, qt_pstep_ring_floats(s->H, s->F, s->L) * sizeof(float), t->st));
+    host_tab = calloc((size_t)s->L, lb);
+    REQ(host_tab, "host alloc");
+    for (int l = 0; l < s->L; l++) {
+        const uint8_t *w[4] = {s->qkv[l].w, s->o[l].w, s->gu[l].w, s->dn[l].w};
+        const float *sc[4] = {s->qkv[l].scale, s->o[l].scale, s->gu[l].scale, s->dn[l].scale};
+        const uint16_t *s16[4] = {s->qkv[l].s16, s->o[l].s16, s->gu[l].s16, s->dn[l].s16};
+        qt_pstep_fill_layer((char *)host_tab + (size_t)l * lb, w, sc, s16, s->in_norm[l], s->post_norm[l], s->qn[l], s->kn[l]);
+    }
+    HCK(hipMalloc(&t->ps_layers, (size_t)s->L * lb));
+    HCK(hipMemcpy(t->ps_layers, host_tab, (size_t)s->L * lb, hipMemcpyHostToDevice));
+    HCK(hipStreamSynchronize(t->st));
+    free(host_tab);
+    t->ps_on = 1;
+    return 0;
+fail:
+    free(host_tab);
+    return -1;
+}
+
+/* One launch of the persistent kernel: n_steps decode steps (with_head: greedy loop). */
+static hipError_t ps_launch(talker_t *t, int n_steps, int with_head) {
+    stack_t *s = &t->s;
+    return qt_launch_pstep(s->prec, s->H, t->ps_layers, s->L, s->final_norm, s->rope_cos, s->rope_sin, s->kc, s->vc,
+                           s->kv_max, s->eps, 1.0f / sqrtf((float)s->hd), t->ps_ring, t->ps_part, t->ps_cnt, t->io,
+                           t->ps_xin, t->d_pos, t->ps_bar, t->ps_err, n_steps, with_head,
+                           with_head ? t->head_m.w ? (const uint16_t *)t->head_m.w : NULL : NULL,
+                           with_head ? t->codec_emb : NULL, t->codec_vocab, t->ps_slots, t->d_frame, t->d_hist,
+                           t->hist_len, t->st);
+}
+
+/* After a synchronous persistent launch: the kernel's own error flag. */
+static int ps_check(talker_t *t) {
+    if (t->h_err[0] != 0) {
+        SETERR("persistent decode step: barrier wait timed out (device error flag set)");
+        return -1;
+    }
+    return 0;
 }
 
 void *qwen_hip_talker_init(const qwen_hip_talker_desc_t *desc) {
@@ -290,6 +364,9 @@ void *qwen_hip_talker_init(const qwen_hip_talker_desc_t *desc) {
     HCK(hipMemsetAsync(t->io, 0, (size_t)2 * H * sizeof(float), t->st));
     HCK(hipStreamSynchronize(t->st));
     t->dev_pos = -1;
+    if (persistent_enabled() && qt_pstep_supported(t->s.prec, H, t->s.F, t->s.nh, t->s.nkv, t->s.hd, t->s.kv_max)) {
+        if (ps_setup(t) != 0) goto fail;
+    }
     return t;
 fail:
     talker_destroy(t);
@@ -357,6 +434,20 @@ static int talker_step_impl(talker_t *t, const float *embed, float *hidden_out, 
         pos, t->s.kv_max, t->s.rope_len);
     if (talker_set_pos(t, pos) != 0) goto fail;
     memcpy(t->h_in, embed, (size_t)H * sizeof(float));
+    if (use_graph && t->ps_on) {
+        stack_t *s = &t->s;
+        HCK(hipMemcpyAsync(t->ps_xin, t->h_in, (size_t)H * sizeof(float), hipMemcpyHostToDevice, t->st));
+        HCK(ps_launch(t, 1, 0));
+        HCK(hipMemcpyAsync(t->h_out, t->io, (size_t)H * sizeof(float), hipMemcpyDeviceToHost, t->st));
+        HCK(hipMemcpyAsync(t->h_out + H, t->ps_ring + (size_t)(s->L - 1) * t->ps_P + t->ps_OXB,
+                           (size_t)H * sizeof(float), hipMemcpyDeviceToHost, t->st));
+        HCK(hipMemcpyAsync(t->h_err, t->ps_err, sizeof(int), hipMemcpyDeviceToHost, t->st));
+        HCK(hipStreamSynchronize(t->st));
+        if (ps_check(t) != 0) goto fail;
+        t->dev_pos = pos + 1;
+        if (hidden_out) memcpy(hidden_out, t->h_out, (size_t)H * sizeof(float));
+        return 0;
+    }
     HCK(hipMemcpyAsync(t->io + H, t->h_in, (size_t)H * sizeof(float), hipMemcpyHostToDevice, t->st));
     if (use_graph && graphs_enabled()) {
         if (!t->graph_ready) {
@@ -477,6 +568,11 @@ int qwen_hip_talker_greedy(void *state, const uint16_t *codec_head, const uint16
     t->h_pos[1] = frame0;
     HCK(hipMemcpyAsync(t->d_frame, t->h_pos + 1, sizeof(int), hipMemcpyHostToDevice, t->st));
     memcpy(t->h_in, embed, (size_t)H * sizeof(float));
+    if (t->ps_on && codec_vocab == 3072) {
+        HCK(hipMemcpyAsync(t->ps_xin, t->h_in, (size_t)H * sizeof(float), hipMemcpyHostToDevice, t->st));
+        t->greedy_ready = 2;
+        if (n_steps > 0) HCK(ps_launch(t, n_steps, 1));
+    } else {
     HCK(hipMemcpyAsync(t->io + H, t->h_in, (size_t)H * sizeof(float), hipMemcpyHostToDevice, t->st));
     if (graphs_enabled() && !t->ggraph_ready) {
         if (capture(t->st, &t->gexec, greedy_body, t) != 0) goto fail;
@@ -484,13 +580,16 @@ int qwen_hip_talker_greedy(void *state, const uint16_t *codec_head, const uint16
     }
     t->greedy_ready = 1;
     for (int i = 0; i < n_steps; i++) HCK(graphs_enabled() ? hipGraphLaunch(t->gexec, t->st) : greedy_body(t));
+    }
     {
         int *hist = (int *)malloc((size_t)t->hist_len * sizeof(int));
         REQ(hist, "host alloc");
         hipError_t e1 = hipMemcpyAsync(hist, t->d_hist, (size_t)t->hist_len * sizeof(int), hipMemcpyDeviceToHost, t->st);
         hipError_t e2 = hipMemcpyAsync(t->h_out, t->io, (size_t)2 * H * sizeof(float), hipMemcpyDeviceToHost, t->st);
+        hipError_t e4 = t->ps_on ? hipMemcpyAsync(t->h_err, t->ps_err, sizeof(int), hipMemcpyDeviceToHost, t->st) : hipSuccess;
         hipError_t e3 = hipStreamSynchronize(t->st);
-        if (e1 || e2 || e3) { free(hist); SETERR("greedy readback failed"); goto fail; }
+        if (e1 || e2 || e3 || e4) { free(hist); SETERR("greedy readback failed"); goto fail; }
+        if (t->greedy_ready == 2 && ps_check(t) != 0) { free(hist); goto fail; }
         for (int i = 0; i < n_steps; i++) tokens_out[i] = hist[(frame0 + i) % t->hist_len];
         free(hist);
     }
@@ -507,7 +606,11 @@ int qwen_hip_talker_greedy_async(void *state, int n_steps) {
     if (!t || t->dead || !t->greedy_ready) { SETERR("greedy loop not initialised"); return -1; }
     REQ(t->dev_pos >= 0 && t->dev_pos + n_steps <= t->s.kv_max && t->dev_pos + n_steps <= t->s.rope_len,
         "positions exceed kv_max");
-    for (int i = 0; i < n_steps; i++) HCK(graphs_enabled() ? hipGraphLaunch(t->gexec, t->st) : greedy_body(t));
+    if (t->greedy_ready == 2) {
+        if (n_steps > 0) HCK(ps_launch(t, n_steps, 1));
+    } else {
+        for (int i = 0; i < n_steps; i++) HCK(graphs_enabled() ? hipGraphLaunch(t->gexec, t->st) : greedy_body(t));
+    }
     t->dev_pos += n_steps;
     return 0;
 fail:
@@ -518,7 +621,9 @@ fail:
 int qwen_hip_talker_sync(void *state) {
     talker_t *t = (talker_t *)state;
     if (!t) return -1;
+    if (t->ps_on) HCK(hipMemcpyAsync(t->h_err, t->ps_err, sizeof(int), hipMemcpyDeviceToHost, t->st));
     HCK(hipStreamSynchronize(t->st));
+    if (t->ps_on && ps_check(t) != 0) goto fail;
     return 0;
 fail:
     t->dead = 1;
