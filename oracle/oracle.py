@@ -126,6 +126,22 @@ class Oracle:
                                      seq_q, seq_k, nh, nkv, hd, scale, q_off)
         return out
 
+    def talker_step(self, t, embed, pos):
+        """One oracle decode step on OTalker t: (hidden f32[H], dec_x f32[H])."""
+        h = np.empty(t.hidden, np.float32); dx = np.empty(t.hidden, np.float32)
+        rc = self.lib.qo_talker_step(C.byref(t), _p(np.ascontiguousarray(embed, np.float32)), pos, _p(h), _p(dx), None)
+        if rc != 0:
+            raise RuntimeError("qo_talker_step failed")
+        return h, dx
+
+    def cp_frame(self, f, talker_hidden, code0):
+        """16 CP passes + 15 argmax codes on OCpFrame f."""
+        out = np.empty(15, np.int32)
+        rc = self.lib.qo_cp_frame(C.byref(f), _p(np.ascontiguousarray(talker_hidden, np.float32)), code0, _p(out))
+        if rc != 0:
+            raise RuntimeError("qo_cp_frame failed")
+        return out
+
     def swiglu(self, gu):
         gu = np.array(gu, np.float32, copy=True)
         self.lib.qo_swiglu(_p(gu), gu.size // 2)
@@ -366,3 +382,95 @@ def oracle_talker(ref: RefModel, prec_code: int, kv_max: int, cp=False):
                 rope_cos=cos.ctypes.data, rope_sin=sin.ctypes.data, rope_len=cos.shape[0],
                 kv_k=kvk.ctypes.data, kv_v=kvv.ctypes.data)
     return t, {"keep": keep, "kv_k": kvk, "kv_v": kvv}
+
+
+_PREC_CODE = {"bf16": 0, "int8": 1, "int4": 2}
+
+
+def _quantized(orc: Oracle, w_bf16, prec):
+    """(weight bytes, scale) of one matrix in the reference's host encoding, made by the
+    oracle's own quantizers (qwen_tts_kernels.c:2143-2238, :2662-2726)."""
+    if prec == "bf16":
+        return np.ascontiguousarray(w_bf16), None
+    if prec == "int8":
+        return orc.quantize_int8(w_bf16)
+    return orc.quantize_q4_0(w_bf16), None
+
+
+def talker_from_tensors(orc: Oracle, tens, shape, prec, kv_max, rope_cos, rope_sin, cp=False):
+    """An OTalker over synthetic tensors {reference name: bf16 array}, quantized by the
+    oracle itself, with the given RoPE tables.  Mirrors the reference loader: gate|up
+    rows interleaved (qwen_tts_talker.c:378-388), norm gains bf16 -> f32.
+    Returns (struct, keepalive dict with the KV arrays)."""
+    s = shape
+    nl = s.cp_layers if cp else s.layers
+    pre = "talker.code_predictor.model.layers." if cp else "talker.model.layers."
+    layers = (OLayer * nl)()
+    keep = []
+    b2f = lambda a: (np.asarray(a, np.uint16).astype(np.uint32) << 16).view(np.float32)  # noqa: E731
+    for l in range(nl):
+        p = f"{pre}{l}."
+        gu = np.empty((2 * tens[p + "mlp.gate_proj.weight"].shape[0], tens[p + "mlp.gate_proj.weight"].shape[1]),
+                      np.uint16)
+        gu[0::2] = tens[p + "mlp.gate_proj.weight"]
+        gu[1::2] = tens[p + "mlp.up_proj.weight"]
+        mats = {"q": tens[p + "self_attn.q_proj.weight"], "k": tens[p + "self_attn.k_proj.weight"],
+                "v": tens[p + "self_attn.v_proj.weight"], "o": tens[p + "self_attn.o_proj.weight"],
+                "gate_up": gu, "down": tens[p + "mlp.down_proj.weight"]}
+        ly = layers[l]
+        for nm, w in mats.items():
+            wq, sc = _quantized(orc, w, prec)
+            keep += [wq, sc]
+            getattr(ly, nm).w = wq.ctypes.data
+            getattr(ly, nm).scale = sc.ctypes.data if sc is not None else None
+        for fld, key in [("input_norm", "input_layernorm.weight"), ("post_attn_norm", "post_attention_layernorm.weight"),
+                         ("q_norm", "self_attn.q_norm.weight"), ("k_norm", "self_attn.k_norm.weight")]:
+            a = np.ascontiguousarray(b2f(tens[p + key]))
+            keep.append(a)
+            setattr(ly, fld, a.ctypes.data)
+    if cp:
+        H, F, nh, nkv, hd = s.cp_hidden, s.cp_inter, s.cp_heads, s.cp_kv_heads, s.cp_head_dim
+        fn = np.ascontiguousarray(b2f(tens["talker.code_predictor.model.norm.weight"]))
+    else:
+        H, F, nh, nkv, hd = s.hidden, s.inter, s.heads, s.kv_heads, s.head_dim
+        fn = np.ascontiguousarray(b2f(tens["talker.model.norm.weight"]))
+    cos = np.ascontiguousarray(rope_cos, np.float32)
+    sin = np.ascontiguousarray(rope_sin, np.float32)
+    kvk = np.zeros((nl, kv_max, nkv * hd), np.uint16)
+    kvv = np.zeros((nl, kv_max, nkv * hd), np.uint16)
+    keep += [cos, sin, fn, kvk, kvv, layers]
+    t = OTalker(hidden=H, inter=F, n_heads=nh, n_kv_heads=nkv, head_dim=hd, n_layers=nl,
+                kv_max=kv_max, eps=s.eps, prec=_PREC_CODE[prec], layers=layers, final_norm=fn.ctypes.data,
+                rope_cos=cos.ctypes.data, rope_sin=sin.ctypes.data, rope_len=cos.shape[0],
+                kv_k=kvk.ctypes.data, kv_v=kvv.ctypes.data)
+    return t, {"keep": keep, "kv_k": kvk, "kv_v": kvv}
+
+
+def cp_frame_from_tensors(orc: Oracle, tens, shape, prec, cp_cos, cp_sin):
+    """An OCpFrame over synthetic tensors (CP layers, 15 lm heads in the CP precision,
+    bf16 codec embeddings; no small_to_mtp_projection when the Talker and CP hidden
+    sizes agree, qwen_tts_code_predictor.c:907-924).  Returns (struct, keepalive)."""
+    s = shape
+    cpt, keep = talker_from_tensors(orc, tens, s, prec, 64, cp_cos, cp_sin, cp=True)
+    keep = {"cp": cpt, "inner": keep, "arrs": []}
+    f = OCpFrame()
+    f.cp = C.pointer(cpt)
+    f.lm_prec = _PREC_CODE[prec]
+    for g in range(15):
+        wq, sc = _quantized(orc, tens[f"talker.code_predictor.lm_head.{g}.weight"], prec)
+        e = np.ascontiguousarray(tens[f"talker.code_predictor.model.codec_embedding.{g}.weight"])
+        keep["arrs"] += [wq, sc, e]
+        f.lm_head[g] = wq.ctypes.data
+        f.lm_scale[g] = sc.ctypes.data if sc is not None else None
+        f.cp_emb[g] = e.ctypes.data
+    te = np.ascontiguousarray(tens["talker.model.codec_embedding.weight"])
+    keep["arrs"].append(te)
+    f.talker_codec_emb = te.ctypes.data
+    f.talker_hidden = s.hidden
+    f.emb_dim = s.hidden
+    f.codebook = s.codebook
+    f.codec_vocab = s.codec_vocab
+    if "talker.code_predictor.small_to_mtp_projection.weight" in tens:
+        raise NotImplementedError("mtp projection: build the frame from RefModel instead")
+    f.mtp_w = None
+    return f, keep
