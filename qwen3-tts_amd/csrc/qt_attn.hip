@@ -66,7 +66,7 @@ __global__ __launch_bounds__(QT_WG) void k_attn(QtAttnArgs a) {
     __shared__ float stat[HPK][2];
     __shared__ __align__(16) uint16_t knew[QT_HD];
     __shared__ __align__(16) uint16_t vnew[QT_HD];
-    __shared__ float mst[QT_ATT_G * HPK][2];
+    __shared__ float mpart[QT_ATT_G * HPK * (2 + QT_HD)];   // chunk partials (merging workgroup)
     __shared__ int last_flag;
 
     const uint16_t *Kg = a.K + (long long)g * a.head_stride;
@@ -250,31 +250,20 @@ __global__ __launch_bounds__(QT_WG) void k_attn(QtAttnArgs a) {
                      (unsigned)(nch - 1));
     __syncthreads();
     if (!last_flag) return;
-    // Merge: chunk statistics into LDS with one parallel load round; then each thread
-    // owns one (head, dim) output and issues the loads of all chunk partials at once.
+    // Merge: all chunk partials into LDS with one parallel load round, then each half-wave
+    // merges one (head, dim) output over the chunks (softmax_merge32, lane = chunk).
     const float *gp = a.part + (size_t)g * G * HPK * PS;
-    for (int i = tid; i < nch * HPK; i += QT_WG) {
-        mst[i][0] = ld_agent(gp + (size_t)i * PS);
-        mst[i][1] = ld_agent(gp + (size_t)i * PS + 1);
-    }
+    for (int i = tid; i < nch * HPK * PS; i += QT_WG) mpart[i] = ld_agent(gp + i);
     __syncthreads();
-    for (int i = tid; i < HPK * QT_HD; i += QT_WG) {
-        const int h = i / QT_HD, d = i % QT_HD;
-        float pv[QT_ATT_G];
-#pragma unroll
-        for (int cc = 0; cc < QT_ATT_G; cc++) pv[cc] = (cc < nch) ? ld_agent(gp + (size_t)(cc * HPK + h) * PS + 2 + d) : 0.f;
-        float M = -INFINITY;
-        for (int cc = 0; cc < nch; cc++) M = fmaxf(M, mst[cc * HPK + h][0]);
-        float l = 0.f, v = 0.f;
-#pragma unroll
-        for (int cc = 0; cc < QT_ATT_G; cc++) {
-            if (cc < nch) {
-                const float f = expf(mst[cc * HPK + h][0] - M);
-                l = fmaf(mst[cc * HPK + h][1], f, l);
-                v = fmaf(pv[cc], f, v);
-            }
+    {
+        const int half = lane >> 5, cc = lane & 31;
+        const bool valid = cc < nch;
+        for (int i = wave * 2 + half; i < HPK * QT_HD; i += QT_WAVES * 2) {
+            const int h = i / QT_HD, d = i % QT_HD;
+            const float *pr = mpart + (size_t)(cc * HPK + h) * PS;
+            const float r = softmax_merge32(valid ? pr[0] : 0.f, valid ? pr[1] : 0.f, valid ? pr[2 + d] : 0.f, valid);
+            if (cc == 0) a.out[(g * HPK + h) * QT_HD + d] = r;
         }
-        a.out[(g * HPK + h) * QT_HD + d] = v * (1.0f / l);
     }
     if (tid == 0) __hip_atomic_store(&a.cnt[g], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }

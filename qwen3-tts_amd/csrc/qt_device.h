@@ -49,17 +49,57 @@ __device__ __forceinline__ float ref_f16_to_f32(uint32_t h) {
     return __uint_as_float(bits);
 }
 
+// Reductions over W-lane groups (W = 16, 32 or 64) with DPP lane moves (VALU, no LDS
+// round trip).  Inside a 16-lane row the steps are symmetric exchanges (quad xor 1,
+// quad xor 2, half-row mirror, row mirror), so every lane of a row ends with the same
+// bits; rows are then combined with row_bcast15/31 and the group's last lane is
+// broadcast, so every lane of a group returns the identical value.
+template <int CTRL, int ROW_MASK = 0xf>
+__device__ __forceinline__ float dpp_mov(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, ROW_MASK, 0xf, false));
+}
+template <int CTRL, int ROW_MASK = 0xf>
+__device__ __forceinline__ float dpp_mov_keep(float v) {   // lanes outside ROW_MASK keep v
+    return __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(v), __float_as_int(v), CTRL, ROW_MASK, 0xf, false));
+}
+constexpr int DPP_QXOR1 = 0xB1, DPP_QXOR2 = 0x4E, DPP_HALF_MIRROR = 0x141, DPP_MIRROR = 0x140,
+              DPP_BCAST15 = 0x142, DPP_BCAST31 = 0x143;
+
+__device__ __forceinline__ float lane_bcast(float v, int lane) {
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), lane));
+}
+
 template <int W>
 __device__ __forceinline__ float group_sum(float v) {
-#pragma unroll
-    for (int o = W / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
-    return v;
+    static_assert(W == 16 || W == 32 || W == 64, "group width");
+    v += dpp_mov<DPP_QXOR1>(v);
+    v += dpp_mov<DPP_QXOR2>(v);
+    v += dpp_mov<DPP_HALF_MIRROR>(v);
+    v += dpp_mov<DPP_MIRROR>(v);
+    if (W == 16) return v;
+    v += dpp_mov<DPP_BCAST15, 0xa>(v);           // rows 1, 3: + row 0, row 2
+    if (W == 32) {
+        const float lo = lane_bcast(v, 31), hi = lane_bcast(v, 63);
+        return (threadIdx.x & 32) ? hi : lo;
+    }
+    v += dpp_mov<DPP_BCAST31, 0xc>(v);           // rows 2, 3: + lane 31 (rows 0+1)
+    return lane_bcast(v, 63);
 }
 template <int W>
 __device__ __forceinline__ float group_max(float v) {
-#pragma unroll
-    for (int o = W / 2; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
-    return v;
+    static_assert(W == 16 || W == 32 || W == 64, "group width");
+    v = fmaxf(v, dpp_mov_keep<DPP_QXOR1>(v));
+    v = fmaxf(v, dpp_mov_keep<DPP_QXOR2>(v));
+    v = fmaxf(v, dpp_mov_keep<DPP_HALF_MIRROR>(v));
+    v = fmaxf(v, dpp_mov_keep<DPP_MIRROR>(v));
+    if (W == 16) return v;
+    v = fmaxf(v, dpp_mov_keep<DPP_BCAST15, 0xa>(v));
+    if (W == 32) {
+        const float lo = lane_bcast(v, 31), hi = lane_bcast(v, 63);
+        return (threadIdx.x & 32) ? hi : lo;
+    }
+    v = fmaxf(v, dpp_mov_keep<DPP_BCAST31, 0xc>(v));
+    return lane_bcast(v, 63);
 }
 
 // Block-wide sum over QT_WG threads; every thread gets the result.  `red` >= QT_WAVES floats.
@@ -73,6 +113,20 @@ __device__ __forceinline__ float block_sum(float v, float *red) {
 #pragma unroll
     for (int i = 0; i < QT_WAVES; i++) t += red[i];
     return t;
+}
+
+// Merge of split-K softmax partials, one key chunk per lane of a 32-lane half-wave:
+// lane cc holds the chunk's running max m, exp-sum l and unnormalised output o (valid
+// for cc < nch).  out = sum_cc o_cc f_cc / sum_cc l_cc f_cc with f_cc = exp(m_cc - M),
+// M = max_cc m_cc; both sums are half-wave reductions, so every merge of the same
+// partials (per-kernel attention or the fused step) rounds identically.  A single
+// chunk reduces exactly to o / l.
+__device__ __forceinline__ float softmax_merge32(float m, float l, float o, bool valid) {
+    const float M = group_max<32>(valid ? m : -INFINITY);
+    const float f = valid ? expf(m - M) : 0.f;
+    const float L = group_sum<32>(valid ? l * f : 0.f);
+    const float V = group_sum<32>(valid ? o * f : 0.f);
+    return V * (1.0f / L);
 }
 
 // Agent-scope relaxed accesses: compiled to global_load/store with the sc1 bit, so they

@@ -43,17 +43,15 @@ hipError_t qt_launch_zero_u32(uint32_t *p, size_t n, hipStream_t st);
 
 /* persistent decode step (qt_pstep.hip) */
 int qt_pstep_supported(int prec, int hidden, int inter, int n_heads, int n_kv, int head_dim, int kv_max);
-size_t qt_pstep_ring_floats(int hidden, int inter, int n_layers);
-size_t qt_pstep_bar_words(void);
+size_t qt_pstep_ring_words(int hidden, int inter, int n_layers);
 size_t qt_pstep_layer_bytes(void);
 void qt_pstep_fill_layer(void *dst, const uint8_t *const w[4], const float *const s[4], const uint16_t *const s16[4],
                          const float *in_norm, const float *post_norm, const float *qn, const float *kn);
 hipError_t qt_launch_pstep(int prec, int hidden, const void *layers_dev, int n_layers, const float *final_norm,
                            const float *rope_cos, const float *rope_sin, uint16_t *kc, uint16_t *vc, int kv_max,
-                           float eps, float scale, float *ring, float *part, unsigned *cnt, float *hid, float *xin,
-                           int *d_pos, unsigned *bar, int *err, int n_steps, int with_head, const uint16_t *head_w,
-                           const uint16_t *emb, int vocab, float *slots, int *d_frame, int *hist, int hist_len,
-                           hipStream_t st);
+                           float eps, float scale, unsigned long long *ring, float *hid, float *decx, float *xin,
+                           int *d_pos, unsigned *epoch, int *err, int n_steps, int with_head, const uint16_t *head_w,
+                           const uint16_t *emb, int vocab, int *d_frame, int *hist, int hist_len, hipStream_t st);
 
 #ifdef __cplusplus
 }

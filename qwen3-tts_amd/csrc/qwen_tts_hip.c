@@ -259,11 +259,11 @@ typedef struct {
     /* persistent single-kernel step (qt_pstep.hip) */
     int ps_on;
     void *ps_layers;        /* device layer table */
-    float *ps_ring, *ps_part, *ps_slots, *ps_xin;
-    unsigned *ps_cnt, *ps_bar;
+    unsigned long long *ps_ring;   /* tagged activation words */
+    float *ps_xin;          /* step-0 input of a launch */
+    unsigned *ps_epoch;     /* tag of the next step */
     int *ps_err;
     int *h_err;             /* pinned */
-    size_t ps_P, ps_OXB;    /* ring block floats per layer, offset of xb */
 } talker_t;
 
 static int persistent_enabled(void) {
@@ -278,7 +278,7 @@ static void talker_destroy(talker_t *t) {
     if (t->ggraph_ready) (void)hipGraphExecDestroy(t->gexec);
     stack_free(&t->s);
     void *bufs[] = {t->io, t->d_pos, t->d_frame, t->d_tok, t->d_hist, t->codec_head, t->codec_emb, t->logits,
-                    t->ps_layers, t->ps_ring, t->ps_part, t->ps_slots, t->ps_xin, t->ps_cnt, t->ps_bar, t->ps_err};
+                    t->ps_layers, t->ps_ring, t->ps_xin, t->ps_epoch, t->ps_err};
     for (size_t i = 0; i < sizeof bufs / sizeof bufs[0]; i++) if (bufs[i]) (void)hipFree(bufs[i]);
     if (t->h_in) (void)hipHostFree(t->h_in);
     if (t->h_out) (void)hipHostFree(t->h_out);
@@ -293,20 +293,16 @@ static int ps_setup(talker_t *t) {
     stack_t *s = &t->s;
     void *host_tab = NULL;
     const size_t lb = qt_pstep_layer_bytes();
-    t->ps_P = (size_t)(s->qd + 2 * s->kvd) + s->qd + 2 * (size_t)s->H + s->F;
-    t->ps_OXB = (size_t)(s->qd + 2 * s->kvd) + s->qd + s->H + s->F;
-    HCK(hipMalloc((void **)&t->ps_ring, qt_pstep_ring_floats(s->H, s->F, s->L) * sizeof(float)));
-    HCK(hipMalloc((void **)&t->ps_part, (size_t)s->nkv * 32 * (s->nh / s->nkv) * 130 * sizeof(float)));
-    HCK(hipMalloc((void **)&t->ps_cnt, 64 * sizeof(unsigned)));
-    HCK(hipMalloc((void **)&t->ps_bar, qt_pstep_bar_words() * sizeof(unsigned)));
+    const size_t words = qt_pstep_ring_words(s->H, s->F, s->L);
+    const unsigned one = 1;   /* ring words start with tag 0: the first step is tag 1 */
+    HCK(hipMalloc((void **)&t->ps_ring, words * sizeof(unsigned long long)));
+    HCK(hipMalloc((void **)&t->ps_epoch, 64));
     HCK(hipMalloc((void **)&t->ps_err, 64));
-    HCK(hipMalloc((void **)&t->ps_slots, 256 * 2 * sizeof(float)));
     HCK(hipMalloc((void **)&t->ps_xin, (size_t)s->H * sizeof(float)));
     HCK(hipHostMalloc((void **)&t->h_err, 64, hipHostMallocDefault));
-    HCK(hipMemsetAsync(t->ps_cnt, 0, 64 * sizeof(unsigned), t->st));
-    HCK(hipMemsetAsync(t->ps_bar, 0, qt_pstep_bar_words() * sizeof(unsigned), t->st));
+    HCK(hipMemsetAsync(t->ps_ring, 0, words * sizeof(unsigned long long), t->st));
     HCK(hipMemsetAsync(t->ps_err, 0, 64, t->st));
-    HCK(hipMemsetAsync(t->ps_ring, 0, qt_pstep_ring_floats(s->H, s->F, s->L) * sizeof(float), t->st));
+    HCK(hipMemcpyAsync(t->ps_epoch, &one, sizeof one, hipMemcpyHostToDevice, t->st));
     host_tab = calloc((size_t)s->L, lb);
     REQ(host_tab, "host alloc");
     for (int l = 0; l < s->L; l++) {
@@ -330,17 +326,16 @@ fail:
 static hipError_t ps_launch(talker_t *t, int n_steps, int with_head) {
     stack_t *s = &t->s;
     return qt_launch_pstep(s->prec, s->H, t->ps_layers, s->L, s->final_norm, s->rope_cos, s->rope_sin, s->kc, s->vc,
-                           s->kv_max, s->eps, 1.0f / sqrtf((float)s->hd), t->ps_ring, t->ps_part, t->ps_cnt, t->io,
-                           t->ps_xin, t->d_pos, t->ps_bar, t->ps_err, n_steps, with_head,
-                           with_head ? t->head_m.w ? (const uint16_t *)t->head_m.w : NULL : NULL,
-                           with_head ? t->codec_emb : NULL, t->codec_vocab, t->ps_slots, t->d_frame, t->d_hist,
-                           t->hist_len, t->st);
+                           s->kv_max, s->eps, 1.0f / sqrtf((float)s->hd), t->ps_ring, t->io, t->io + s->H, t->ps_xin,
+                           t->d_pos, t->ps_epoch, t->ps_err, n_steps, with_head,
+                           with_head ? (const uint16_t *)t->head_m.w : NULL, with_head ? t->codec_emb : NULL,
+                           t->codec_vocab, t->d_frame, t->d_hist, t->hist_len, t->st);
 }
 
 /* After a synchronous persistent launch: the kernel's own error flag. */
 static int ps_check(talker_t *t) {
     if (t->h_err[0] != 0) {
-        SETERR("persistent decode step: barrier wait timed out (device error flag set)");
+        SETERR("persistent decode step: a wait for another workgroup's data timed out (device error flag set)");
         return -1;
     }
     return 0;
@@ -435,12 +430,9 @@ static int talker_step_impl(talker_t *t, const float *embed, float *hidden_out, 
     if (talker_set_pos(t, pos) != 0) goto fail;
     memcpy(t->h_in, embed, (size_t)H * sizeof(float));
     if (use_graph && t->ps_on) {
-        stack_t *s = &t->s;
         HCK(hipMemcpyAsync(t->ps_xin, t->h_in, (size_t)H * sizeof(float), hipMemcpyHostToDevice, t->st));
         HCK(ps_launch(t, 1, 0));
-        HCK(hipMemcpyAsync(t->h_out, t->io, (size_t)H * sizeof(float), hipMemcpyDeviceToHost, t->st));
-        HCK(hipMemcpyAsync(t->h_out + H, t->ps_ring + (size_t)(s->L - 1) * t->ps_P + t->ps_OXB,
-                           (size_t)H * sizeof(float), hipMemcpyDeviceToHost, t->st));
+        HCK(hipMemcpyAsync(t->h_out, t->io, (size_t)2 * H * sizeof(float), hipMemcpyDeviceToHost, t->st));
         HCK(hipMemcpyAsync(t->h_err, t->ps_err, sizeof(int), hipMemcpyDeviceToHost, t->st));
         HCK(hipStreamSynchronize(t->st));
         if (ps_check(t) != 0) goto fail;
