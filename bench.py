@@ -6,14 +6,19 @@
 A "step" is one Talker decode step of the resident greedy loop (28 layers + final norm
 + codec head + greedy code0 + next-embedding gather), all inputs resident in HBM.
 Default workload = the north-star target: 1.7B-shape Talker, int8 per-row weights,
-batch 1, KV prefilled to 2048 positions by 2048 real decode steps, then K timed steps.
-Weights are seeded random-init N(0, 0.02) (no checkpoints offline), quantized on the
-device by the library's bit-exact int8 quantizer.
+batch 1, KV cache holding 2048 positions (seeded synthetic bf16 K/V uploaded through
+the library's upload_kv, as the reference does after its CPU prefill), then W warmup
+and K timed greedy steps, each run as ONE launch of the fused step kernel.  Weights
+are seeded random-init N(0, 0.02) (no checkpoints offline), quantized on the device
+by the library's bit-exact int8 quantizer.
 
 Prints ONE JSON line (metric/unit from BASELINE.json).  The timed region is bracketed
 by hipDeviceSynchronize and measured with HIP events recorded on the library's stream.
-The roofline object is for the dominant kernel (norm+gate_up+SwiGLU matvec), timed
-the same way over repeated launches.  cpu_baseline times the reference engine's own
+The roofline object is for the dominant (only) kernel of the timed region, the fused
+decode step: algorithmic bytes of the K steps of one launch / that launch's duration.
+With W == K the two launches rocprof sees have the same length, so its average kernel
+duration is comparable with the HIP-event figure.  kernels_us times the unfused
+per-kernel path (diagnostic).  cpu_baseline times the reference engine's own
 qwen_talker_step (built from its sources into oracle/_ref) on the host cores.
 """
 from __future__ import annotations
@@ -104,21 +109,18 @@ def weight_bytes(shape, prec):
     return s.layers * (per + norms) + s.hidden * 4
 
 
-def gate_up_bytes(shape, prec):
-    r, c = 2 * shape.inter, shape.hidden
-    w = {"bf16": r * c * 2, "int8": r * c + 4 * r, "int4": r * c // 2 + 2 * r * (c // 32)}[prec]
-    return w + c * 4 * 2 + r // 2 * 4      # + x and gain read, h written
-
-
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=None)
-    ap.add_argument("--warmup", type=int, default=8)
+    ap.add_argument("--warmup", type=int, default=None)
     ap.add_argument("--workload", default="talker-1.7B-int8-b1-L2048", choices=sorted(WORKLOADS))
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--kernel-launches", type=int, default=200)
+    ap.add_argument("--calib-copy-mb", type=int, default=0,
+                    help="before the timed region, one device-to-device copy of this many MiB (a kernel of "
+                         "known HBM traffic, to scale rocprofv3 FETCH_SIZE/WRITE_SIZE counters)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build measures one GPU only: the decode path shards as independent "
@@ -129,7 +131,7 @@ def main():
     from qwen3_tts_amd import hip, synth
     shape_name, prec, Lpre, dsteps = WORKLOADS[args.workload]
     K = args.steps or dsteps
-    W = args.warmup
+    W = K if args.warmup is None else args.warmup
     s = synth.SHAPES[shape_name]
     kv_max = max(4096, Lpre + K + W + 8)
     seed = 0x5EED0001
@@ -150,15 +152,29 @@ def main():
     ev = HipEvents()
     stream = L.qwen_hip_talker_stream(g.h)
 
-    # prefill: Lpre real greedy decode steps on the device
-    e0 = synth.bf16_to_f32(emb[1234])
+    # KV cache: Lpre positions of seeded synthetic bf16 K/V (values do not change timing)
+    rng = np.random.default_rng(0x5EED0002)
     t0 = time.time()
     if Lpre > 0:
-        toks, _ = g.greedy(head, emb, e0, 0, 0, Lpre)
-    else:
-        toks, _ = g.greedy(head, emb, e0, 0, 0, 1)
-        Lpre = 1
-    log(f"[bench] prefilled KV to {Lpre} positions with {Lpre} decode steps in {time.time() - t0:.2f}s")
+        kvk = synth.f32_to_bf16_rne(rng.normal(0, 1.0, (s.layers, Lpre, s.kv_dim)).astype(np.float32))
+        kvv = synth.f32_to_bf16_rne(rng.normal(0, 0.1, (s.layers, Lpre, s.kv_dim)).astype(np.float32))
+        hip.check(L.qwen_hip_talker_upload_kv(g.h, kvk.ctypes.data, kvv.ctypes.data, Lpre, Lpre), "upload_kv")
+        del kvk, kvv
+    log(f"[bench] KV cache filled to {Lpre} positions in {time.time() - t0:.2f}s")
+    e0 = synth.bf16_to_f32(emb[1234])
+    g.greedy(head, emb, e0, Lpre, 0, 0)     # set up the greedy loop at position Lpre (no steps)
+
+    if args.calib_copy_mb > 0:
+        nbytes = args.calib_copy_mb << 20
+        src, dst = C.c_void_p(), C.c_void_p()
+        ev.rt.hipMalloc.argtypes = [C.POINTER(C.c_void_p), C.c_size_t]
+        ev.rt.hipMemcpyAsync.argtypes = [C.c_void_p, C.c_void_p, C.c_size_t, C.c_int, C.c_void_p]
+        ev.rt.hipFree.argtypes = [C.c_void_p]
+        assert ev.rt.hipMalloc(C.byref(src), nbytes) == 0 and ev.rt.hipMalloc(C.byref(dst), nbytes) == 0
+        assert ev.rt.hipMemcpyAsync(dst, src, nbytes, 3, stream) == 0      # hipMemcpyDeviceToDevice
+        ev.device_sync()
+        ev.rt.hipFree(src); ev.rt.hipFree(dst)
+        log(f"[bench] calibration copy: {args.calib_copy_mb} MiB device to device")
 
     # warmup, then exactly K timed steps
     hip.check(L.qwen_hip_talker_greedy_async(g.h, W), "warmup")
@@ -182,19 +198,28 @@ def main():
     kern = {}
     names = ["qkv", "attn", "o_proj", "gate_up", "down", "final_norm"]
     n = args.kernel_launches
-    for kid, nm in enumerate(names):
+    for kid, nm in enumerate(names if n > 0 else []):
         hip.check(L.qwen_hip_talker_launch_kernel(g.h, kid, 0, 10), "kernel warmup")
         ev.record(a, stream)
         hip.check(L.qwen_hip_talker_launch_kernel(g.h, kid, 0, n), "kernel launches")
         ev.record(b, stream)
         kern[nm] = ev.elapsed_ms(a, b) * 1e3 / n
-    log("[bench] per-kernel avg us: " + ", ".join(f"{k}={v:.2f}" for k, v in kern.items()))
-    gu_bytes = gate_up_bytes(s, prec)
-    achieved = gu_bytes / (kern["gate_up"] * 1e-6) / 1e9
-    roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
-                "kernel": f"k_mv<{prec}> norm+gate_up+SwiGLU, {2 * s.inter}x{s.hidden}",
-                "bytes_per_launch": gu_bytes, "avg_us": round(kern["gate_up"], 3)}
+    if kern:
+        log("[bench] per-kernel avg us: " + ", ".join(f"{k}={v:.2f}" for k, v in kern.items()))
+    fused = bool(L.qwen_hip_talker_fused(g.h))
+    roofline = {"bound": "hbm", "achieved": round(step_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": round(step_gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                "kernel": (f"ps::k_pstep<{prec}> fused decode step" if fused else "unfused per-kernel path"),
+                "bytes_per_launch": int(step_bytes * K), "avg_us": round(ms_total * 1e3, 1),
+                "steps_per_launch": K}
+    # HBM bytes per launch from the committed rocprofv3 PMC passes for this workload
+    try:
+        t = json.load(open(os.path.join(ROOT, "profiles", "pstep_traffic.json")))
+        if fused and t["workload"] == args.workload and t["steps_per_launch"] == K:
+            roofline["traffic"] = t["traffic_bytes_per_launch"]
+            roofline["traffic_source"] = t["source"]
+    except (OSError, ValueError, KeyError):
+        pass
 
     cpu = None
     if not args.no_cpu_baseline:

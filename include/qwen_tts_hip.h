@@ -98,6 +98,10 @@ int   qwen_hip_talker_greedy_async(void *state, int n_steps);
 int   qwen_hip_talker_sync(void *state);
 /* The state's stream (hipStream_t), for callers that time it with events. */
 void *qwen_hip_talker_stream(void *state);
+/* Diagnostic query (no reference counterpart): 1 when steps run as the single fused
+ * persistent kernel, 0 when they run as the per-kernel sequence (shapes or devices the
+ * fused kernel does not cover), -1 for a NULL state. */
+int   qwen_hip_talker_fused(void *state);
 /* Same as qwen_hip_talker_step, but the device graph runs with graph capture disabled
  * (one launch per kernel), for profiling and A/B checks. */
 int   qwen_hip_talker_step_nograph(void *state, const float *embed, float *hidden_out, int pos);

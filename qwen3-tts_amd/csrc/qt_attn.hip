@@ -253,7 +253,17 @@ __global__ __launch_bounds__(QT_WG) void k_attn(QtAttnArgs a) {
     // Merge: all chunk partials into LDS with one parallel load round, then each half-wave
     // merges one (head, dim) output over the chunks (softmax_merge32, lane = chunk).
     const float *gp = a.part + (size_t)g * G * HPK * PS;
-    for (int i = tid; i < nch * HPK * PS; i += QT_WG) mpart[i] = ld_agent(gp + i);
+    {
+        // all loads issued before any is consumed (one round trip, not one per element)
+        constexpr int MK = (QT_ATT_G * HPK * PS + QT_WG - 1) / QT_WG;
+        const int np = nch * HPK * PS;
+        float t[MK];
+#pragma unroll
+        for (int k = 0; k < MK; k++) t[k] = (tid + k * QT_WG < np) ? ld_agent(gp + tid + k * QT_WG) : 0.f;
+#pragma unroll
+        for (int k = 0; k < MK; k++)
+            if (tid + k * QT_WG < np) mpart[tid + k * QT_WG] = t[k];
+    }
     __syncthreads();
     {
         const int half = lane >> 5, cc = lane & 31;

@@ -58,6 +58,15 @@ constexpr int MAXL = 64;         // layers whose table fits the LDS copy
 // LDS wait would stall on HBM.
 template <typename T>
 __device__ __forceinline__ T ldg(const T *p) { return *(const __attribute__((address_space(1))) T *)p; }
+// A pointer read from LDS lands in VGPRs; declaring it wave-uniform (readfirstlane)
+// lets loads use a scalar base plus a 32-bit lane offset instead of 64-bit per-lane
+// addresses that would otherwise be kept live in VGPRs.
+template <typename T>
+__device__ __forceinline__ T *uni(T *p) {
+    const unsigned long long v = (unsigned long long)p;
+    const unsigned lo = __builtin_amdgcn_readfirstlane((unsigned)v), hi = __builtin_amdgcn_readfirstlane((unsigned)(v >> 32));
+    return (T *)(((unsigned long long)hi << 32) | lo);
+}
 typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
 __device__ __forceinline__ uint4 ldg(const uint4 *p) {
     const u32x4_t v = *(const __attribute__((address_space(1))) u32x4_t *)p;
@@ -183,6 +192,8 @@ struct Tile {
 
     __device__ __forceinline__ void load(const uint8_t *W, const float *S, int row0w) {
         const int lane = threadIdx.x & 63;
+        W = uni(W);
+        if (PREC == QT_INT8) S = uni(S);
 #pragma unroll
         for (int r = 0; r < NR; r++)
 #pragma unroll
@@ -250,6 +261,7 @@ struct GainCh {
     float g[EPC];
     __device__ __forceinline__ void load(const float *src, int cols) {
         const int c = threadIdx.x;
+        src = uni(src);
         if (c * EPC < cols) {
 #pragma unroll
             for (int q = 0; q < EPC / 4; q++) {
@@ -431,7 +443,8 @@ __global__ __launch_bounds__(256, 1) void k_pstep(Args a) {
                     vpre[u] = make_uint4(0, 0, 0, 0);
                 }
             }
-            const float qn0 = ldg(ly.qn + lane), qn1 = ldg(ly.qn + lane + 64), kn0 = ldg(ly.kn + lane), kn1 = ldg(ly.kn + lane + 64);
+            const float *qnp = uni(ly.qn), *knp = uni(ly.kn);
+            const float qn0 = ldg(qnp + lane), qn1 = ldg(qnp + lane + 64), kn0 = ldg(knp + lane), kn1 = ldg(knp + lane + 64);
             const float rc = ldg(a.rope_cos + (size_t)pos * 64 + lane), rsn = ldg(a.rope_sin + (size_t)pos * 64 + lane);
             PS_MARK(ph, 1); ph++;
 

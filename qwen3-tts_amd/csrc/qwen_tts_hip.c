@@ -370,6 +370,7 @@ fail:
 
 void qwen_hip_talker_free(void *state) { talker_destroy((talker_t *)state); }
 void *qwen_hip_talker_stream(void *state) { return state ? (void *)((talker_t *)state)->st : NULL; }
+int qwen_hip_talker_fused(void *state) { return state ? ((talker_t *)state)->ps_on : -1; }
 
 static hipError_t talker_body(talker_t *t) {
     hipError_t e;
