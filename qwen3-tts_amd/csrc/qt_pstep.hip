@@ -119,18 +119,33 @@ __device__ __forceinline__ float val_of(unsigned long long w) { return __uint_as
 
 // Optional phase trace (build with -DQT_PSTEP_TRACE): s_memrealtime (100 MHz) of every
 // workgroup when its input for a phase has arrived (w=0) and when its output has been
-// issued (w=1), indexed by the phase's number in the launch; qt_pstep_trace_read
-// copies it out.
+// issued (w=1), indexed by the phase's number in the launch.  Marks are kept in LDS and
+// written out once at the end of the launch (a global store per mark would add its
+// acknowledgement to the next vmcnt wait); qt_pstep_trace_read copies them out.
 #ifdef QT_PSTEP_TRACE
-constexpr int TRACE_PH = 1024;
+constexpr int TRACE_PH = 640;
 __device__ unsigned long long ps_trace[TRACE_PH * 2 * NB];
+#define PS_TRACE_LDS __shared__ unsigned long long s_trace[TRACE_PH * 2];
 #define PS_MARK(k, w)                                                                          \
     do {                                                                                       \
         if (threadIdx.x == 0 && (unsigned)(k) < (unsigned)TRACE_PH)                            \
-            ps_trace[((size_t)(k) * 2 + (w)) * NB + blockIdx.x] = __builtin_amdgcn_s_memrealtime(); \
+            s_trace[(size_t)(k) * 2 + (w)] = __builtin_amdgcn_s_memrealtime();                 \
+    } while (0)
+#define PS_TRACE_FLUSH()                                                                       \
+    do {                                                                                       \
+        __syncthreads();                                                                       \
+        for (int i_ = threadIdx.x; i_ < TRACE_PH * 2; i_ += NT)                                \
+            ps_trace[(size_t)i_ * NB + blockIdx.x] = s_trace[i_];                              \
+    } while (0)
+#define PS_TRACE_CLEAR()                                                                       \
+    do {                                                                                       \
+        for (int i_ = threadIdx.x; i_ < TRACE_PH * 2; i_ += NT) s_trace[i_] = 0;               \
     } while (0)
 #else
+#define PS_TRACE_LDS
 #define PS_MARK(k, w) do { } while (0)
+#define PS_TRACE_FLUSH() do { } while (0)
+#define PS_TRACE_CLEAR() do { } while (0)
 #endif
 
 // ---- waiting for tagged data ------------------------------------------------------------
@@ -329,6 +344,16 @@ struct Ring {
 };
 
 // ---- the kernel ---------------------------------------------------------------------------
+// LDS of the attention phase (B) and the merge (M, which reuses sc for its inputs)
+template <int HPK>
+struct AttLds {
+    float qs[HPK][HD];                 // rotated queries
+    float sc[HPK][CHMAX];              // scores, then probabilities
+    float ored[NW][HPK][HD];           // per-wave P.V partial sums
+    float stat[HPK][2];                // chunk (max, sum) per head
+    __attribute__((aligned(16))) uint16_t knew[HD], vnew[HD];   // key/value at pos (bf16)
+};
+
 template <int PREC, int H, int F>
 __global__ __launch_bounds__(256, 1) void k_pstep(Args a) {
     constexpr int RPW_QKV = QKVR / (NB * NW);      // 4
@@ -338,11 +363,12 @@ __global__ __launch_bounds__(256, 1) void k_pstep(Args a) {
     constexpr int RPW_HEAD = 3;                    // 3072-row codec head
     using TQKV = Tile<PREC, H, RPW_QKV>;
     using TO = Tile<PREC, QD, RPW_O>;
-    using TGU = Tile<PREC, H, RPW_GU>;
+    constexpr int RGU = RPW_GU / 3;                // gate|up rows per piece (4 or 2)
+    using TGU = Tile<PREC, H, RGU>;
     using TDN = Tile<PREC, F, RPW_DN>;
     using THEAD = Tile<QT_BF16, H, RPW_HEAD>;
     using R = Ring<H, F>;
-    static_assert(RPW_GU % 2 == 0, "gate/up pairs stay in one wave");
+    static_assert(RPW_GU % 3 == 0 && RGU % 2 == 0, "gate/up pairs stay in one piece");
 
     __shared__ __align__(16) float s_x[H];       // layer input (kept for C's residual)
     __shared__ __align__(16) float s_xa[H];      // post-attention residual (kept for E)
@@ -350,14 +376,11 @@ __global__ __launch_bounds__(256, 1) void k_pstep(Args a) {
     __shared__ __align__(16) float s_xn[H];      // RMS-normalised input of A / D / head
     __shared__ __align__(16) float s_xs[(F > QD ? F : QD) / 16];   // int8 chunk sums
     __shared__ __align__(16) float s_qkv[HPK * HD + 2 * HD];
-    __shared__ float qs[HPK][HD];
-    __shared__ float sc[HPK][CHMAX];
-    __shared__ float ored[NW][HPK][HD];
-    __shared__ float stat[HPK][2];
-    __shared__ __align__(16) uint16_t knew[HD], vnew[HD];
+    __shared__ __align__(16) AttLds<HPK> att;                 // attention chunk (B), merge input (M)
     __shared__ float wbest_v[NW];
     __shared__ int wbest_i[NW];
     __shared__ Layer s_layers[MAXL];
+    PS_TRACE_LDS
 
     const int b = blockIdx.x, tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // uniform: row bases are scalar
@@ -381,6 +404,7 @@ __global__ __launch_bounds__(256, 1) void k_pstep(Args a) {
     const int rw_dn = b * (RPW_DN * NW) + wave * RPW_DN;
     const int rw_head = b * (RPW_HEAD * NW) + wave * RPW_HEAD;
 
+    PS_TRACE_CLEAR();
     // the layer table lives in LDS: reading it never waits behind weight loads
     for (int i = tid; i < L * (int)(sizeof(Layer) / 8); i += NT)
         reinterpret_cast<unsigned long long *>(s_layers)[i] = ldg(reinterpret_cast<const unsigned long long *>(a.layers) + i);
@@ -401,9 +425,34 @@ __global__ __launch_bounds__(256, 1) void k_pstep(Args a) {
         const int nch = (Lk + CH - 1) / CH;
         const int j0 = c * CH;
         const int n = (c < nch) ? min(CH, Lk - j0) : 0;
-        THEAD th;
-        GainCh<QT_BF16> gf;
 
+        // B's operands, loaded one phase ahead: K/V of this workgroup's chunk (first 64
+        // keys), the q/k norm gains and the RoPE row of pos
+        static_assert(HPK * HD == NT, "one attention output per thread");
+        uint4 kpre[4], vpre[4];
+        float qn0 = 0.f, qn1 = 0.f, kn0 = 0.f, kn1 = 0.f, rc = 0.f, rsn = 0.f;
+        const uint16_t *Kg = a.kc, *Vg = a.vc;
+        auto prefetch_kv = [&](int lk) {
+            Kg = a.kc + (((size_t)lk * NKV + g) * a.kv_max) * HD;
+            Vg = a.vc + (((size_t)lk * NKV + g) * a.kv_max) * HD;
+            {
+                const int ksub = lane & 15, kpg = lane >> 4;
+#pragma unroll
+                for (int u = 0; u < 4; u++) {
+                    const int jj = wave * 4 + kpg + 16 * u;
+                    if (jj < n && j0 + jj != pos) {
+                        kpre[u] = ldg(reinterpret_cast<const uint4 *>(Kg + (size_t)(j0 + jj) * HD + ksub * 8));
+                        vpre[u] = ldg(reinterpret_cast<const uint4 *>(Vg + (size_t)(j0 + jj) * HD + ksub * 8));
+                    } else {
+                        kpre[u] = make_uint4(0, 0, 0, 0);
+                        vpre[u] = make_uint4(0, 0, 0, 0);
+                    }
+                }
+            }
+            const float *qnp = uni(s_layers[lk].qn), *knp = uni(s_layers[lk].kn);
+            qn0 = ldg(qnp + lane); qn1 = ldg(qnp + lane + 64); kn0 = ldg(knp + lane); kn1 = ldg(knp + lane + 64);
+            rc = ldg(a.rope_cos + (size_t)pos * 64 + lane); rsn = ldg(a.rope_sin + (size_t)pos * 64 + lane);
+        };
         for (int l = 0; l < L; l++) {
             const Layer &ly = s_layers[l];
             unsigned long long *blk = ring.blk(par, l);
@@ -426,26 +475,14 @@ __global__ __launch_bounds__(256, 1) void k_pstep(Args a) {
                 for (int r = 0; r < RPW_QKV; r++)
                     if (lane == r) st_tag(blk + R::OQKV + rw_qkv + r, PREC == QT_INT8 ? __fmul_rn(acc[r], tq.rs[r]) : acc[r], tag);
             }
-            // next phase's operands (issued after this phase's output): K/V of this
-            // workgroup's chunk (first 64 keys), q/k norm gains, the RoPE row
-            const uint16_t *Kg = a.kc + (((size_t)l * NKV + g) * a.kv_max) * HD;
-            const uint16_t *Vg = a.vc + (((size_t)l * NKV + g) * a.kv_max) * HD;
-            const int ksub = lane & 15, kpg = lane >> 4;
-            uint4 kpre[4], vpre[4];
-#pragma unroll
-            for (int u = 0; u < 4; u++) {
-                const int jj = wave * 4 + kpg + 16 * u;
-                if (jj < n && j0 + jj != pos) {
-                    kpre[u] = ldg(reinterpret_cast<const uint4 *>(Kg + (size_t)(j0 + jj) * HD + ksub * 8));
-                    vpre[u] = ldg(reinterpret_cast<const uint4 *>(Vg + (size_t)(j0 + jj) * HD + ksub * 8));
-                } else {
-                    kpre[u] = make_uint4(0, 0, 0, 0);
-                    vpre[u] = make_uint4(0, 0, 0, 0);
-                }
-            }
-            const float *qnp = uni(ly.qn), *knp = uni(ly.kn);
-            const float qn0 = ldg(qnp + lane), qn1 = ldg(qnp + lane + 64), kn0 = ldg(knp + lane), kn1 = ldg(knp + lane + 64);
-            const float rc = ldg(a.rope_cos + (size_t)pos * 64 + lane), rsn = ldg(a.rope_sin + (size_t)pos * 64 + lane);
+            if (l == 0) prefetch_kv(0);
+            // next operands (issued after this phase's output): W_o, first gate|up piece, post-norm gains
+            TO to;
+            to.load(ly.w[1], ly.s[1], rw_o);
+            TGU tg0, tg1, tg2;
+            GainCh<PREC> gp;
+            tg0.load(ly.w[2], ly.s[2], rw_gu);
+            gp.load(ly.post_norm, H);
             PS_MARK(ph, 1); ph++;
 
             // ---------------- B: attention chunk -----------------
@@ -470,29 +507,21 @@ __global__ __launch_bounds__(256, 1) void k_pstep(Args a) {
                     const float n0 = (x0 * inv) * w0, n1 = (x1 * inv) * w1;
                     const float r0 = fmaf(n0, rc, -(n1 * rsn)), r1 = fmaf(n1, rc, n0 * rsn);
                     if (!isk) {
-                        qs[t][lane] = r0;
-                        qs[t][lane + 64] = r1;
+                        att.qs[t][lane] = r0;
+                        att.qs[t][lane + 64] = r1;
                     } else {
                         const float *vs = s_qkv + HPK * HD + HD;
-                        knew[lane] = f2bf_trunc(r0); knew[lane + 64] = f2bf_trunc(r1);
-                        vnew[lane] = f2bf_trunc(vs[lane]); vnew[lane + 64] = f2bf_trunc(vs[lane + 64]);
+                        att.knew[lane] = f2bf_trunc(r0); att.knew[lane + 64] = f2bf_trunc(r1);
+                        att.vnew[lane] = f2bf_trunc(vs[lane]); att.vnew[lane + 64] = f2bf_trunc(vs[lane + 64]);
                     }
                 }
                 __syncthreads();
-                if (append && wave == NW - 1) {
-                    // KV append: agent-scope 32-bit stores of adjacent bf16 pairs
-                    uint32_t *kd = reinterpret_cast<uint32_t *>(a.kc + (((size_t)l * NKV + g) * a.kv_max + pos) * HD);
-                    uint32_t *vd = reinterpret_cast<uint32_t *>(a.vc + (((size_t)l * NKV + g) * a.kv_max + pos) * HD);
-                    const uint32_t kk = (uint32_t)knew[2 * lane] | ((uint32_t)knew[2 * lane + 1] << 16);
-                    const uint32_t vv = (uint32_t)vnew[2 * lane] | ((uint32_t)vnew[2 * lane + 1] << 16);
-                    __hip_atomic_store(kd + lane, kk, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                    __hip_atomic_store(vd + lane, vv, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                }
+                const int ksub = lane & 15, kpg = lane >> 4;
                 float qv[HPK][8];
 #pragma unroll
                 for (int h = 0; h < HPK; h++)
 #pragma unroll
-                    for (int e = 0; e < 8; e++) qv[h][e] = qs[h][ksub * 8 + e];
+                    for (int e = 0; e < 8; e++) qv[h][e] = att.qs[h][ksub * 8 + e];
                 for (int blk0 = 0; blk0 < n; blk0 += 64) {
                     uint4 kw[4];
 #pragma unroll
@@ -501,7 +530,7 @@ __global__ __launch_bounds__(256, 1) void k_pstep(Args a) {
                         if (blk0 == 0) kw[u] = kpre[u];
                         else kw[u] = (jj < n && j0 + jj != pos) ? ldg(reinterpret_cast<const uint4 *>(Kg + (size_t)(j0 + jj) * HD + ksub * 8))
                                                                : make_uint4(0, 0, 0, 0);
-                        if (j0 + jj == pos && jj < n) kw[u] = *reinterpret_cast<const uint4 *>(knew + ksub * 8);
+                        if (j0 + jj == pos && jj < n) kw[u] = *reinterpret_cast<const uint4 *>(att.knew + ksub * 8);
                     }
 #pragma unroll
                     for (int u = 0; u < 4; u++) {
@@ -516,23 +545,23 @@ __global__ __launch_bounds__(256, 1) void k_pstep(Args a) {
 #pragma unroll
                             for (int e = 0; e < 8; e++) s = fmaf(qv[h][e], kf[e], s);
                             s = group_sum<16>(s);
-                            if (ksub == 0 && jj < n) sc[h][jj] = s * a.scale;
+                            if (ksub == 0 && jj < n) att.sc[h][jj] = s * a.scale;
                         }
                     }
                 }
                 __syncthreads();
                 for (int h = wave; h < HPK; h += NW) {
                     float m = -INFINITY;
-                    for (int j = lane; j < n; j += 64) m = fmaxf(m, sc[h][j]);
+                    for (int j = lane; j < n; j += 64) m = fmaxf(m, att.sc[h][j]);
                     m = group_max<64>(m);
                     float lsum = 0.f;
                     for (int j = lane; j < n; j += 64) {
-                        const float p = expf(sc[h][j] - m);
-                        sc[h][j] = p;
+                        const float p = expf(att.sc[h][j] - m);
+                        att.sc[h][j] = p;
                         lsum += p;
                     }
                     lsum = group_sum<64>(lsum);
-                    if (lane == 0) { stat[h][0] = m; stat[h][1] = lsum; }
+                    if (lane == 0) { att.stat[h][0] = m; att.stat[h][1] = lsum; }
                 }
                 __syncthreads();
                 float o[HPK][8];
@@ -548,7 +577,7 @@ __global__ __launch_bounds__(256, 1) void k_pstep(Args a) {
                         if (blk0 == 0) vw[u] = vpre[u];
                         else vw[u] = (jj < n && j0 + jj != pos) ? ldg(reinterpret_cast<const uint4 *>(Vg + (size_t)(j0 + jj) * HD + ksub * 8))
                                                                : make_uint4(0, 0, 0, 0);
-                        if (j0 + jj == pos && jj < n) vw[u] = *reinterpret_cast<const uint4 *>(vnew + ksub * 8);
+                        if (j0 + jj == pos && jj < n) vw[u] = *reinterpret_cast<const uint4 *>(att.vnew + ksub * 8);
                     }
 #pragma unroll
                     for (int u = 0; u < 4; u++) {
@@ -560,7 +589,7 @@ __global__ __launch_bounds__(256, 1) void k_pstep(Args a) {
                             for (int m = 0; m < 4; m++) { vf[2 * m] = bf_lo(w4[m]); vf[2 * m + 1] = bf_hi(w4[m]); }
 #pragma unroll
                             for (int h = 0; h < HPK; h++) {
-                                const float p = sc[h][jj];
+                                const float p = att.sc[h][jj];
 #pragma unroll
                                 for (int e = 0; e < 8; e++) o[h][e] = fmaf(p, vf[e], o[h][e]);
                             }
@@ -580,21 +609,30 @@ __global__ __launch_bounds__(256, 1) void k_pstep(Args a) {
 #pragma unroll
                     for (int h = 0; h < HPK; h++)
 #pragma unroll
-                        for (int e = 0; e < 8; e++) ored[wave][h][ksub * 8 + e] = o[h][e];
+                        for (int e = 0; e < 8; e++) att.ored[wave][h][ksub * 8 + e] = o[h][e];
                 }
                 __syncthreads();
                 unsigned long long *mypart = blk + R::OPART + (size_t)(g * G + c) * HPK * PS;
                 for (int i = tid; i < HPK * HD; i += NT) {
                     const int h = i / HD, d = i % HD;
-                    st_tag(mypart + h * PS + 2 + d, ored[0][h][d] + ored[1][h][d] + ored[2][h][d] + ored[3][h][d], tag);
+                    st_tag(mypart + h * PS + 2 + d, att.ored[0][h][d] + att.ored[1][h][d] + att.ored[2][h][d] + att.ored[3][h][d], tag);
                 }
                 if (tid < HPK) {
-                    st_tag(mypart + tid * PS, stat[tid][0], tag);
-                    st_tag(mypart + tid * PS + 1, stat[tid][1], tag);
+                    st_tag(mypart + tid * PS, att.stat[tid][0], tag);
+                    st_tag(mypart + tid * PS + 1, att.stat[tid][1], tag);
+                }
+                if (append && wave == NW - 1) {
+                    // KV append: agent-scope 32-bit stores of adjacent bf16 pairs (after the
+                    // attention, so no wait inside it covers their acknowledgement)
+                    uint32_t *kd = reinterpret_cast<uint32_t *>(a.kc + (((size_t)l * NKV + g) * a.kv_max + pos) * HD);
+                    uint32_t *vd = reinterpret_cast<uint32_t *>(a.vc + (((size_t)l * NKV + g) * a.kv_max + pos) * HD);
+                    const uint32_t kk = (uint32_t)att.knew[2 * lane] | ((uint32_t)att.knew[2 * lane + 1] << 16);
+                    const uint32_t vv = (uint32_t)att.vnew[2 * lane] | ((uint32_t)att.vnew[2 * lane + 1] << 16);
+                    __hip_atomic_store(kd + lane, kk, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    __hip_atomic_store(vd + lane, vv, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                 }
             }
-            TO to;
-            to.load(ly.w[1], ly.s[1], rw_o);
+            tg1.load(ly.w[2], ly.s[2], rw_gu + RGU);
             PS_MARK(ph, 1); ph++;
 
             // ---------------- M: merge 8 attention outputs -----------------
@@ -602,7 +640,7 @@ __global__ __launch_bounds__(256, 1) void k_pstep(Args a) {
                 const int hh = c >> 4, d0 = (c & 15) * 8;
                 const unsigned long long *gp = blk + R::OPART + (size_t)g * G * HPK * PS + hh * PS;
                 // element i: chunk i/10, field i%10 (0 max, 1 sum, 2.. dims d0..d0+7)
-                float *st = &sc[0][0];
+                float *st = &att.sc[0][0];
                 gather<2>(nch * 10, [&](int i) {
                     const int cc = i / 10, f = i % 10;
                     return gp + (size_t)cc * HPK * PS + (f < 2 ? f : 2 + d0 + (f - 2));
@@ -616,6 +654,7 @@ __global__ __launch_bounds__(256, 1) void k_pstep(Args a) {
                 if (cc == 0) st_tag(blk + R::OATT + (2 * g + hh) * HD + d0 + dd, r, tag);
                 __syncthreads();   // st (the scores' LDS) is reused by the next B
             }
+            tg2.load(ly.w[2], ly.s[2], rw_gu + 2 * RGU);
             PS_MARK(ph, 1); ph++;
 
             // ---------------- C: xa = x + W_o . attn -----------------
@@ -635,10 +674,8 @@ __global__ __launch_bounds__(256, 1) void k_pstep(Args a) {
                         st_tag(blk + R::OXA + rw_o + r, __fadd_rn(s_x[rw_o + r], v), tag);
                     }
             }
-            TGU tg;
-            GainCh<PREC> gp;
-            tg.load(ly.w[2], ly.s[2], rw_gu);
-            gp.load(ly.post_norm, H);
+            TDN td;
+            td.load(ly.w[3], ly.s[3], rw_dn);
             PS_MARK(ph, 1); ph++;
 
             // ---------------- D: h = SwiGLU(W_gu . RMSNorm(xa)) -----------------
@@ -649,19 +686,27 @@ __global__ __launch_bounds__(256, 1) void k_pstep(Args a) {
             PS_MARK(ph, 0);
             {
                 stage_norm<PREC, H>(s_xa, gp, a.eps, s_xn, s_xs);
-                float acc[RPW_GU];
-                tile_dot<PREC, H, RPW_GU>(tg, s_xn, s_xs, acc);
-                // rows 2i, 2i+1 are the gate and up rows of h[(rw_gu >> 1) + i]
+                float acc[3][RGU];
+                tile_dot<PREC, H, RGU>(tg0, s_xn, s_xs, acc[0]);
+                tile_dot<PREC, H, RGU>(tg1, s_xn, s_xs, acc[1]);
+                tile_dot<PREC, H, RGU>(tg2, s_xn, s_xs, acc[2]);
+                // rows 2i, 2i+1 of a piece are the gate and up rows of one h element
 #pragma unroll
-                for (int i = 0; i < RPW_GU / 2; i++)
-                    if (lane == i) {
-                        const float gt = PREC == QT_INT8 ? __fmul_rn(acc[2 * i], tg.rs[2 * i]) : acc[2 * i];
-                        const float up = PREC == QT_INT8 ? __fmul_rn(acc[2 * i + 1], tg.rs[2 * i + 1]) : acc[2 * i + 1];
-                        st_tag(blk + R::OH + (rw_gu >> 1) + i, gt / (1.0f + expf(-gt)) * up, tag);
-                    }
+                for (int pc = 0; pc < 3; pc++) {
+                    const TGU &t = pc == 0 ? tg0 : pc == 1 ? tg1 : tg2;
+#pragma unroll
+                    for (int i = 0; i < RGU / 2; i++)
+                        if (lane == pc * (RGU / 2) + i) {
+                            const float gt = PREC == QT_INT8 ? __fmul_rn(acc[pc][2 * i], t.rs[2 * i]) : acc[pc][2 * i];
+                            const float up = PREC == QT_INT8 ? __fmul_rn(acc[pc][2 * i + 1], t.rs[2 * i + 1]) : acc[pc][2 * i + 1];
+                            st_tag(blk + R::OH + ((rw_gu + pc * RGU) >> 1) + i, gt / (1.0f + expf(-gt)) * up, tag);
+                        }
+                }
             }
-            TDN td;
-            td.load(ly.w[3], ly.s[3], rw_dn);
+            if (l + 1 < L) {
+                tq.load(s_layers[l + 1].w[0], s_layers[l + 1].s[0], rw_qkv);
+                gq.load(s_layers[l + 1].in_norm, H);
+            }
             PS_MARK(ph, 1); ph++;
 
             // ---------------- E: x' = xa + W_dn . h -----------------
@@ -681,13 +726,7 @@ __global__ __launch_bounds__(256, 1) void k_pstep(Args a) {
                         st_tag(blk + R::OX + rw_dn + r, __fadd_rn(s_xa[rw_dn + r], v), tag);
                     }
             }
-            if (l + 1 < L) {
-                tq.load(s_layers[l + 1].w[0], s_layers[l + 1].s[0], rw_qkv);
-                gq.load(s_layers[l + 1].in_norm, H);
-            } else if (a.with_head) {
-                th.load(a.head_w, nullptr, rw_head);
-                gf.load(a.final_norm, H);
-            }
+            if (l + 1 < L) prefetch_kv(l + 1);
             PS_MARK(ph, 1); ph++;
         }
 
@@ -704,6 +743,12 @@ __global__ __launch_bounds__(256, 1) void k_pstep(Args a) {
             }
         } else {
             // ---------------- head: logits rows + masked local argmax -----------------
+            // (its tile is loaded here rather than during the last layer: a tile carried
+            // through the layer loop would hold its registers for the whole loop)
+            THEAD th;
+            GainCh<QT_BF16> gf;
+            th.load(a.head_w, nullptr, rw_head);
+            gf.load(a.final_norm, H);
             gather<H / NT>(H, [&](int i) { return xfin + i; }, s_x, tag, a.err);
             PS_MARK(ph, 0);
             stage_norm<QT_BF16, H>(s_x, gf, a.eps, s_xn, s_xs);
@@ -775,6 +820,7 @@ __global__ __launch_bounds__(256, 1) void k_pstep(Args a) {
             *a.epoch = tag0 + (unsigned)a.n_steps;
         }
     }
+    PS_TRACE_FLUSH();
 }
 }  // namespace ps
 
