@@ -52,6 +52,7 @@ constexpr int CHMAX = 256;       // keys per chunk at most (kv_max <= G * CHMAX)
 constexpr int PS = 2 + HD;       // partial record per head: max, sum, o[HD]
 constexpr unsigned POLL_LIMIT = 1u << 17;
 constexpr int MAXL = 64;         // layers whose table fits the LDS copy
+constexpr int KVB = 128;         // keys of a chunk staged in LDS at once (K and V: 64 KiB)
 
 // Loads through pointers read from memory are made explicitly global (address space
 // 1): a generic (flat) load would also count against the LDS counter, so every later
@@ -68,6 +69,12 @@ __device__ __forceinline__ T *uni(T *p) {
     return (T *)(((unsigned long long)hi << 32) | lo);
 }
 typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
+// 16 bytes per lane from global memory straight into LDS (global_load_lds_dwordx4):
+// lane i's bytes land at dst + 16*i, dst wave-uniform.  Counted by vmcnt like a load.
+__device__ __forceinline__ void lds_copy16(const void *src, void *dst) {
+    __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void *)src,
+                                     (__attribute__((address_space(3))) void *)dst, 16, 0, 0);
+}
 __device__ __forceinline__ uint4 ldg(const uint4 *p) {
     const u32x4_t v = *(const __attribute__((address_space(1))) u32x4_t *)p;
     return make_uint4(v.x, v.y, v.z, v.w);
@@ -118,28 +125,29 @@ __device__ __forceinline__ unsigned tag_of(unsigned long long w) { return (unsig
 __device__ __forceinline__ float val_of(unsigned long long w) { return __uint_as_float((unsigned)w); }
 
 // Optional phase trace (build with -DQT_PSTEP_TRACE): s_memrealtime (100 MHz) of every
-// workgroup when its input for a phase has arrived (w=0) and when its output has been
-// issued (w=1), indexed by the phase's number in the launch.  Marks are kept in LDS and
+// workgroup when its input for a phase has arrived (w=0), at two points inside the
+// phase (w=2, 3) and when its output and the next loads have been issued (w=1),
+// indexed by the phase's number in the launch.  Marks are kept in LDS and
 // written out once at the end of the launch (a global store per mark would add its
 // acknowledgement to the next vmcnt wait); qt_pstep_trace_read copies them out.
 #ifdef QT_PSTEP_TRACE
-constexpr int TRACE_PH = 640;
-__device__ unsigned long long ps_trace[TRACE_PH * 2 * NB];
-#define PS_TRACE_LDS __shared__ unsigned long long s_trace[TRACE_PH * 2];
+constexpr int TRACE_PH = 520;
+__device__ unsigned long long ps_trace[TRACE_PH * 4 * NB];
+#define PS_TRACE_LDS __shared__ unsigned long long s_trace[TRACE_PH * 4];
 #define PS_MARK(k, w)                                                                          \
     do {                                                                                       \
         if (threadIdx.x == 0 && (unsigned)(k) < (unsigned)TRACE_PH)                            \
-            s_trace[(size_t)(k) * 2 + (w)] = __builtin_amdgcn_s_memrealtime();                 \
+            s_trace[(size_t)(k) * 4 + (w)] = __builtin_amdgcn_s_memrealtime();                 \
     } while (0)
 #define PS_TRACE_FLUSH()                                                                       \
     do {                                                                                       \
         __syncthreads();                                                                       \
-        for (int i_ = threadIdx.x; i_ < TRACE_PH * 2; i_ += NT)                                \
+        for (int i_ = threadIdx.x; i_ < TRACE_PH * 4; i_ += NT)                                \
             ps_trace[(size_t)i_ * NB + blockIdx.x] = s_trace[i_];                              \
     } while (0)
 #define PS_TRACE_CLEAR()                                                                       \
     do {                                                                                       \
-        for (int i_ = threadIdx.x; i_ < TRACE_PH * 2; i_ += NT) s_trace[i_] = 0;               \
+        for (int i_ = threadIdx.x; i_ < TRACE_PH * 4; i_ += NT) s_trace[i_] = 0;               \
     } while (0)
 #else
 #define PS_TRACE_LDS
@@ -152,7 +160,10 @@ __device__ unsigned long long ps_trace[TRACE_PH * 2 * NB];
 // Each thread gathers elements i = tid + k*NT (k < K, i < n) whose words addr(i) must
 // carry `tag`; all reads are issued before any is checked, then only stale words are
 // re-read, one round trip per round.  Values land in dst[i] (LDS); ends with a
-// workgroup barrier.
+// workgroup barrier.  n <= 0 gathers nothing.
+// (Issuing the next phase's weight loads between the first reads and their check, so
+// the issue overlaps the first round trip, was measured 30 % slower per step than
+// issuing them before the gather.)
 template <int K, typename AddrF>
 __device__ __forceinline__ void gather(int n, AddrF addr, float *dst, unsigned tag, int *err) {
     const int tid = threadIdx.x;
@@ -380,6 +391,7 @@ __global__ __launch_bounds__(256, 1) void k_pstep(Args a) {
     __shared__ float wbest_v[NW];
     __shared__ int wbest_i[NW];
     __shared__ Layer s_layers[MAXL];
+    __shared__ __align__(16) uint16_t s_kv[2][KVB * HD];          // K, V rows of the attention chunk (B)
     PS_TRACE_LDS
 
     const int b = blockIdx.x, tid = threadIdx.x, lane = tid & 63;
@@ -426,29 +438,31 @@ __global__ __launch_bounds__(256, 1) void k_pstep(Args a) {
         const int j0 = c * CH;
         const int n = (c < nch) ? min(CH, Lk - j0) : 0;
 
-        // B's operands, loaded one phase ahead: K/V of this workgroup's chunk (first 64
-        // keys), the q/k norm gains and the RoPE row of pos
+        // B's operands, loaded one phase ahead: K/V rows of this workgroup's chunk (the
+        // first KVB keys) copied straight into LDS by global_load_lds_dwordx4 (no VGPRs
+        // held; one wave instruction moves 4 keys = 1 KiB), the q/k norm gains and the
+        // RoPE row of pos.  Row pos is never loaded (its stale bits must not enter any
+        // cache: it is written by this step's B and read from the next step on); lanes
+        // past the chunk end load nothing.
         static_assert(HPK * HD == NT, "one attention output per thread");
-        uint4 kpre[4], vpre[4];
         float qn0 = 0.f, qn1 = 0.f, kn0 = 0.f, kn1 = 0.f, rc = 0.f, rsn = 0.f;
-        const uint16_t *Kg = a.kc, *Vg = a.vc;
-        auto prefetch_kv = [&](int lk) {
-            Kg = a.kc + (((size_t)lk * NKV + g) * a.kv_max) * HD;
-            Vg = a.vc + (((size_t)lk * NKV + g) * a.kv_max) * HD;
-            {
-                const int ksub = lane & 15, kpg = lane >> 4;
-#pragma unroll
-                for (int u = 0; u < 4; u++) {
-                    const int jj = wave * 4 + kpg + 16 * u;
-                    if (jj < n && j0 + jj != pos) {
-                        kpre[u] = ldg(reinterpret_cast<const uint4 *>(Kg + (size_t)(j0 + jj) * HD + ksub * 8));
-                        vpre[u] = ldg(reinterpret_cast<const uint4 *>(Vg + (size_t)(j0 + jj) * HD + ksub * 8));
-                    } else {
-                        kpre[u] = make_uint4(0, 0, 0, 0);
-                        vpre[u] = make_uint4(0, 0, 0, 0);
-                    }
+        auto stage_kv = [&](int lk, int kb, bool doK, bool doV) {
+            const uint16_t *Kl = a.kc + (((size_t)lk * NKV + g) * a.kv_max) * HD;
+            const uint16_t *Vl = a.vc + (((size_t)lk * NKV + g) * a.kv_max) * HD;
+            const int nk = min(KVB, n - kb);
+            const int ninst = (nk + 3) >> 2;
+            const int jq = lane >> 4, js = lane & 15;
+            for (int i = wave; i < ninst; i += NW) {
+                const int jj = kb + i * 4 + jq;
+                if (jj < n && j0 + jj != pos) {
+                    const size_t off = (size_t)(j0 + jj) * HD + js * 8;
+                    if (doK) lds_copy16(Kl + off, &s_kv[0][i * 4 * HD]);
+                    if (doV) lds_copy16(Vl + off, &s_kv[1][i * 4 * HD]);
                 }
             }
+        };
+        auto prefetch_kv = [&](int lk) {
+            if (n > 0) stage_kv(lk, 0, true, true);
             const float *qnp = uni(s_layers[lk].qn), *knp = uni(s_layers[lk].kn);
             qn0 = ldg(qnp + lane); qn1 = ldg(qnp + lane + 64); kn0 = ldg(knp + lane); kn1 = ldg(knp + lane + 64);
             rc = ldg(a.rope_cos + (size_t)pos * 64 + lane); rsn = ldg(a.rope_sin + (size_t)pos * 64 + lane);
@@ -469,11 +483,13 @@ __global__ __launch_bounds__(256, 1) void k_pstep(Args a) {
             PS_MARK(ph, 0);
             {
                 stage_norm<PREC, H>(s_x, gq, a.eps, s_xn, s_xs);
+                PS_MARK(ph, 2);
                 float acc[RPW_QKV];
                 tile_dot<PREC, H, RPW_QKV>(tq, s_xn, s_xs, acc);
 #pragma unroll
                 for (int r = 0; r < RPW_QKV; r++)
                     if (lane == r) st_tag(blk + R::OQKV + rw_qkv + r, PREC == QT_INT8 ? __fmul_rn(acc[r], tq.rs[r]) : acc[r], tag);
+                PS_MARK(ph, 3);
             }
             if (l == 0) prefetch_kv(0);
             // next operands (issued after this phase's output): W_o, first gate|up piece, post-norm gains
@@ -486,9 +502,9 @@ __global__ __launch_bounds__(256, 1) void k_pstep(Args a) {
             PS_MARK(ph, 1); ph++;
 
             // ---------------- B: attention chunk -----------------
-            if (n > 0) {
+            {
                 const unsigned long long *src = blk + R::OQKV;
-                gather<2>(HPK * HD + 2 * HD, [&](int i) {
+                gather<2>(n > 0 ? HPK * HD + 2 * HD : 0, [&](int i) {
                     return src + (i < HPK * HD ? g * HPK * HD + i
                                   : i < HPK * HD + HD ? QD + g * HD + (i - HPK * HD) : QD + KVD + g * HD + (i - HPK * HD - HD));
                 }, s_qkv, tag, a.err);
@@ -516,40 +532,41 @@ __global__ __launch_bounds__(256, 1) void k_pstep(Args a) {
                     }
                 }
                 __syncthreads();
+                // scores: lane (ksub, kpg) takes dims ksub*8.. of keys u*16 + wave*4 + kpg of
+                // each LDS block of KVB keys (the same keys, in the same order, as k_attn)
                 const int ksub = lane & 15, kpg = lane >> 4;
                 float qv[HPK][8];
 #pragma unroll
                 for (int h = 0; h < HPK; h++)
 #pragma unroll
                     for (int e = 0; e < 8; e++) qv[h][e] = att.qs[h][ksub * 8 + e];
-                for (int blk0 = 0; blk0 < n; blk0 += 64) {
-                    uint4 kw[4];
-#pragma unroll
-                    for (int u = 0; u < 4; u++) {
-                        const int jj = blk0 + wave * 4 + kpg + 16 * u;
-                        if (blk0 == 0) kw[u] = kpre[u];
-                        else kw[u] = (jj < n && j0 + jj != pos) ? ldg(reinterpret_cast<const uint4 *>(Kg + (size_t)(j0 + jj) * HD + ksub * 8))
-                                                               : make_uint4(0, 0, 0, 0);
-                        if (j0 + jj == pos && jj < n) kw[u] = *reinterpret_cast<const uint4 *>(att.knew + ksub * 8);
+                for (int kb = 0; kb < n; kb += KVB) {
+                    if (kb > 0) {   // chunks longer than KVB keys (caches beyond G*KVB positions)
+                        __syncthreads();
+                        stage_kv(l, kb, true, false);
+                        __syncthreads();
                     }
-#pragma unroll
-                    for (int u = 0; u < 4; u++) {
-                        const uint32_t w4[4] = {kw[u].x, kw[u].y, kw[u].z, kw[u].w};
+                    const int nk = min(KVB, n - kb);
+                    for (int u = 0; u * 16 < nk; u++) {
+                        const int jl = u * 16 + wave * 4 + kpg, jj = kb + jl;
+                        const uint4 kw = (j0 + jj == pos) ? *reinterpret_cast<const uint4 *>(att.knew + ksub * 8)
+                                                          : *reinterpret_cast<const uint4 *>(&s_kv[0][jl * HD + ksub * 8]);
+                        const uint32_t w4[4] = {kw.x, kw.y, kw.z, kw.w};
                         float kf[8];
 #pragma unroll
                         for (int m = 0; m < 4; m++) { kf[2 * m] = bf_lo(w4[m]); kf[2 * m + 1] = bf_hi(w4[m]); }
-                        const int jj = blk0 + wave * 4 + kpg + 16 * u;
 #pragma unroll
                         for (int h = 0; h < HPK; h++) {
-                            float s = 0.f;
+                            float sv = 0.f;
 #pragma unroll
-                            for (int e = 0; e < 8; e++) s = fmaf(qv[h][e], kf[e], s);
-                            s = group_sum<16>(s);
-                            if (ksub == 0 && jj < n) att.sc[h][jj] = s * a.scale;
+                            for (int e = 0; e < 8; e++) sv = fmaf(qv[h][e], kf[e], sv);
+                            sv = group_sum<16>(sv);
+                            if (ksub == 0 && jl < nk) att.sc[h][jj] = sv * a.scale;
                         }
                     }
                 }
                 __syncthreads();
+                PS_MARK(ph, 2);
                 for (int h = wave; h < HPK; h += NW) {
                     float m = -INFINITY;
                     for (int j = lane; j < n; j += 64) m = fmaxf(m, att.sc[h][j]);
@@ -569,21 +586,19 @@ __global__ __launch_bounds__(256, 1) void k_pstep(Args a) {
                 for (int h = 0; h < HPK; h++)
 #pragma unroll
                     for (int e = 0; e < 8; e++) o[h][e] = 0.f;
-                for (int blk0 = 0; blk0 < n; blk0 += 64) {
-                    uint4 vw[4];
-#pragma unroll
-                    for (int u = 0; u < 4; u++) {
-                        const int jj = blk0 + wave * 4 + kpg + 16 * u;
-                        if (blk0 == 0) vw[u] = vpre[u];
-                        else vw[u] = (jj < n && j0 + jj != pos) ? ldg(reinterpret_cast<const uint4 *>(Vg + (size_t)(j0 + jj) * HD + ksub * 8))
-                                                               : make_uint4(0, 0, 0, 0);
-                        if (j0 + jj == pos && jj < n) vw[u] = *reinterpret_cast<const uint4 *>(att.vnew + ksub * 8);
+                for (int kb = 0; kb < n; kb += KVB) {
+                    if (kb > 0) {
+                        __syncthreads();
+                        stage_kv(l, kb, false, true);
+                        __syncthreads();
                     }
-#pragma unroll
-                    for (int u = 0; u < 4; u++) {
-                        const int jj = blk0 + wave * 4 + kpg + 16 * u;
-                        if (jj < n) {
-                            const uint32_t w4[4] = {vw[u].x, vw[u].y, vw[u].z, vw[u].w};
+                    const int nk = min(KVB, n - kb);
+                    for (int u = 0; u * 16 < nk; u++) {
+                        const int jl = u * 16 + wave * 4 + kpg, jj = kb + jl;
+                        if (jl < nk) {
+                            const uint4 vw = (j0 + jj == pos) ? *reinterpret_cast<const uint4 *>(att.vnew + ksub * 8)
+                                                              : *reinterpret_cast<const uint4 *>(&s_kv[1][jl * HD + ksub * 8]);
+                            const uint32_t w4[4] = {vw.x, vw.y, vw.z, vw.w};
                             float vf[8];
 #pragma unroll
                             for (int m = 0; m < 4; m++) { vf[2 * m] = bf_lo(w4[m]); vf[2 * m + 1] = bf_hi(w4[m]); }
@@ -612,6 +627,7 @@ __global__ __launch_bounds__(256, 1) void k_pstep(Args a) {
                         for (int e = 0; e < 8; e++) att.ored[wave][h][ksub * 8 + e] = o[h][e];
                 }
                 __syncthreads();
+                PS_MARK(ph, 3);
                 unsigned long long *mypart = blk + R::OPART + (size_t)(g * G + c) * HPK * PS;
                 for (int i = tid; i < HPK * HD; i += NT) {
                     const int h = i / HD, d = i % HD;
@@ -686,6 +702,7 @@ __global__ __launch_bounds__(256, 1) void k_pstep(Args a) {
             PS_MARK(ph, 0);
             {
                 stage_norm<PREC, H>(s_xa, gp, a.eps, s_xn, s_xs);
+                PS_MARK(ph, 2);
                 float acc[3][RGU];
                 tile_dot<PREC, H, RGU>(tg0, s_xn, s_xs, acc[0]);
                 tile_dot<PREC, H, RGU>(tg1, s_xn, s_xs, acc[1]);
@@ -703,6 +720,7 @@ __global__ __launch_bounds__(256, 1) void k_pstep(Args a) {
                         }
                 }
             }
+            PS_MARK(ph, 3);
             if (l + 1 < L) {
                 tq.load(s_layers[l + 1].w[0], s_layers[l + 1].s[0], rw_qkv);
                 gq.load(s_layers[l + 1].in_norm, H);
@@ -717,6 +735,7 @@ __global__ __launch_bounds__(256, 1) void k_pstep(Args a) {
             PS_MARK(ph, 0);
             {
                 stage_sums<PREC, F>(s_in, s_xs);
+                PS_MARK(ph, 2);
                 float acc[RPW_DN];
                 tile_dot<PREC, F, RPW_DN>(td, s_in, s_xs, acc);
 #pragma unroll
@@ -726,6 +745,7 @@ __global__ __launch_bounds__(256, 1) void k_pstep(Args a) {
                         st_tag(blk + R::OX + rw_dn + r, __fadd_rn(s_xa[rw_dn + r], v), tag);
                     }
             }
+            PS_MARK(ph, 3);
             if (l + 1 < L) prefetch_kv(l + 1);
             PS_MARK(ph, 1); ph++;
         }
