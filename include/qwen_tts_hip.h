@@ -114,6 +114,36 @@ int   qwen_hip_talker_step_nograph(void *state, const float *embed, float *hidde
  * the current position with the same bits). */
 int   qwen_hip_talker_launch_kernel(void *state, int kernel, int layer, int n);
 
+/* ---- level 2: batched Talker step (qwen_tts_cuda_talker.cu:595-648; CPU twin
+ * batch_talker_step_impl, qwen_tts_talker.c:1192-1270, qwen_tts_batch.h:87-98) ----
+ * B <= 64 streams share the single state's device weights (read once per step for all
+ * streams; int8 weights on the MFMA GEMM, bf16/q4_0 as B matvecs); each stream has its
+ * own bf16 KV cache (single state's kv_max) and its own position (ragged).  Free the
+ * batch before the single state. */
+
+/* replaces qwen_cuda_talker_batch_init(single, B)      (qwen_tts_cuda_talker.cu:595) */
+void *qwen_hip_talker_batch_init(void *single, int B);
+/* replaces qwen_cuda_talker_batch_step                  (qwen_tts_cuda_talker.cu:618):
+ * embeds host f32[B][hidden], pos_arr host int[B] (each stream's position: its KV row
+ * written, RoPE and causal length pos+1), hidden_out host f32[B][hidden] final-normed. */
+int   qwen_hip_talker_batch_step(void *state, const float *embeds, const int *pos_arr, float *hidden_out);
+/* replaces qwen_cuda_talker_batch_upload_slot           (qwen_tts_cuda_talker.cu:629):
+ * seeds slot b's device KV from the batch engine's host bf16 caches laid out
+ * ((b*n_layers + l)*src_kv_max + pos)*kv_dim (qwen_tts_batch.h:26-27). */
+int   qwen_hip_talker_batch_upload_slot(void *state, int b, const uint16_t *kv_k, const uint16_t *kv_v,
+                                        int src_kv_max, int prefill_len);
+/* replaces qwen_cuda_talker_batch_free                  (qwen_tts_cuda_talker.cu:643);
+ * the shared weights stay with the single state. */
+void  qwen_hip_talker_batch_free(void *state);
+/* Reads slot b's positions [0, n) back in the upload layout (checks/tests; no
+ * reference counterpart). */
+int   qwen_hip_talker_batch_download_slot(void *state, int b, uint16_t *kv_k, uint16_t *kv_v, int dst_kv_max, int n);
+/* Benchmark entries (no reference counterpart): replay n steps of the last batch_step's
+ * inputs on the device without host sync; the state's stream. */
+int   qwen_hip_talker_batch_step_async(void *state, int n_steps);
+int   qwen_hip_talker_batch_sync(void *state);
+void *qwen_hip_talker_batch_stream(void *state);
+
 /* ---- level 2: Code Predictor (qwen_tts_cuda_talker.cu:751-841; qwen_tts_metal.m:2246) ---- */
 
 typedef struct {
@@ -145,6 +175,12 @@ int   qwen_hip_cp_sync(void *state);
 void *qwen_hip_cp_stream(void *state);
 /* replaces qwen_cuda_cp_free                     (qwen_tts_cuda_talker.cu:917) */
 void  qwen_hip_cp_free(void *state);
+/* CP batch twins (qwen_tts_cuda_talker.cu:879-915): B streams over the single CP state's
+ * weights; x host f32[B][cp_hidden] residuals in/out (not normed), one pass per stream
+ * at pos_arr[b] on its own CP KV. */
+void *qwen_hip_cp_batch_init(void *single, int B);
+int   qwen_hip_cp_batch_step(void *state, float *x, const int *pos_arr);
+void  qwen_hip_cp_batch_free(void *state);
 
 /* ---- level 1: per-op backend (qwen_tts_cuda.h:23-35, qwen_tts_backend.h:34-49) ---- */
 
@@ -169,6 +205,9 @@ int qwen_hip_op_rms_norm(float *out, const float *x, const float *w, int seq, in
 int qwen_hip_op_rms_norm_per_head(float *x, const float *w, int seq, int n_heads, int head_dim, float eps);
 int qwen_hip_op_swiglu(float *out, const float *gate_up, int n);
 int qwen_hip_op_argmax_matvec(int prec, const float *x, const void *W, const float *scale, int in_dim, int out_dim);
+/* qwen_matmat_int8 (qwen_tts_kernels.h:121-122): Y[rows][B] = (W*scale) @ X[cols][B]
+ * (row-major f32, B <= 64, cols a multiple of 64) on the batched MFMA kernel. */
+int qwen_hip_op_matmat_int8(float *Y, const int8_t *W, const float *scale, const float *X, int rows, int cols, int B);
 /* qwen_quantize_bf16_to_int8 / _q4_0 (k.c:2143, k.c:2662) run on the device; output in
  * the reference's host layout. */
 int qwen_hip_op_quantize_int8(const uint16_t *src, int rows, int cols, int8_t *dst, float *scale);

@@ -39,6 +39,9 @@ struct QtAttnArgs {
     float *part;             // [n_kv][G][HPK][2 + 128]
     unsigned *cnt;           // [n_kv]
     float *out;              // [n_heads * 128]
+    // independent streams (grid z): element offsets of stream z's q, K/V cache, output,
+    // partials and counters; d_pos + z is its position (batched step)
+    long long q_bs, kv_bs, out_bs, part_bs;
 };
 
 // 8 dims (16 bytes) of key/value j for this lane, raw bf16 bits.
@@ -48,6 +51,11 @@ __device__ __forceinline__ uint4 qt_ld_kv(const uint16_t *base, long long pos_st
 
 template <int HPK, bool PREP>
 __global__ __launch_bounds__(QT_WG) void k_attn(QtAttnArgs a) {
+    if (blockIdx.z) {
+        const int z = blockIdx.z;
+        a.q += z * a.q_bs; a.K += z * a.kv_bs; a.V += z * a.kv_bs; a.out += z * a.out_bs;
+        a.part += z * a.part_bs; a.cnt += (size_t)z * a.n_kv; a.d_pos += z;
+    }
     const int g = blockIdx.y, c = blockIdx.x, G = gridDim.x;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int pos = PREP ? *a.d_pos : a.Lval - 1;
@@ -278,6 +286,23 @@ __global__ __launch_bounds__(QT_WG) void k_attn(QtAttnArgs a) {
     if (tid == 0) __hip_atomic_store(&a.cnt[g], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+static hipError_t attn_launch(const QtAttnArgs &a, int prep, int head_dim, int G, int nz, hipStream_t st) {
+    if (head_dim != QT_HD || a.n_kv <= 0 || a.n_heads % a.n_kv) return hipErrorInvalidValue;
+    if (G <= 0 || G > QT_ATT_G || nz <= 0 || nz > 65535) return hipErrorInvalidValue;
+    if (!prep && (a.Lval <= 0 || a.Lval > G * QT_CH_MAX)) return hipErrorInvalidValue;
+    const int hpk = a.n_heads / a.n_kv;
+    dim3 grid(G, a.n_kv, nz);
+#define QT_ATT_CASE(H) \
+    if (prep) hipLaunchKernelGGL((k_attn<H, true>), grid, dim3(QT_WG), 0, st, a); \
+    else hipLaunchKernelGGL((k_attn<H, false>), grid, dim3(QT_WG), 0, st, a);
+    if (hpk == 1) { QT_ATT_CASE(1) }
+    else if (hpk == 2) { QT_ATT_CASE(2) }
+    else if (hpk == 4) { QT_ATT_CASE(4) }
+    else return hipErrorInvalidValue;
+#undef QT_ATT_CASE
+    return hipGetLastError();
+}
+
 extern "C" hipError_t qt_launch_attn(int prep, const float *q, const float *qn, const float *kn,
                                      const float *rc, const float *rs, float eps, const int *d_pos,
                                      int Lval, uint16_t *K, uint16_t *V, long long pos_stride,
@@ -288,20 +313,26 @@ extern "C" hipError_t qt_launch_attn(int prep, const float *q, const float *qn, 
     a.q = q; a.qn = qn; a.kn = kn; a.rc = rc; a.rs = rs; a.eps = eps; a.d_pos = d_pos; a.Lval = Lval;
     a.K = K; a.V = V; a.pos_stride = pos_stride; a.head_stride = head_stride;
     a.n_heads = n_heads; a.n_kv = n_kv; a.scale = scale; a.part = part; a.cnt = cnt; a.out = out;
-    if (head_dim != QT_HD || n_kv <= 0 || n_heads % n_kv) return hipErrorInvalidValue;
-    if (G <= 0 || G > QT_ATT_G) return hipErrorInvalidValue;
-    if (!prep && (Lval <= 0 || Lval > G * QT_CH_MAX)) return hipErrorInvalidValue;
-    const int hpk = n_heads / n_kv;
-    dim3 grid(G, n_kv);
-#define QT_ATT_CASE(H) \
-    if (prep) hipLaunchKernelGGL((k_attn<H, true>), grid, dim3(QT_WG), 0, st, a); \
-    else hipLaunchKernelGGL((k_attn<H, false>), grid, dim3(QT_WG), 0, st, a);
-    if (hpk == 1) { QT_ATT_CASE(1) }
-    else if (hpk == 2) { QT_ATT_CASE(2) }
-    else if (hpk == 4) { QT_ATT_CASE(4) }
-    else return hipErrorInvalidValue;
-#undef QT_ATT_CASE
-    return hipGetLastError();
+    a.q_bs = a.kv_bs = a.out_bs = a.part_bs = 0;
+    return attn_launch(a, prep, head_dim, G, 1, st);
+}
+
+// B independent streams in one launch (the batched step): stream z uses q + z*q_bs,
+// K/V + z*kv_bs (its own cache), position d_pos[z], partials part + z*part_bs, counters
+// cnt + z*n_kv, output out + z*out_bs.  Ragged positions are fine: each stream's chunks
+// follow its own length.
+extern "C" hipError_t qt_launch_attn_b(const float *q, long long q_bs, const float *qn, const float *kn,
+                                       const float *rc, const float *rs, float eps, const int *d_pos,
+                                       uint16_t *K, uint16_t *V, long long kv_bs, long long pos_stride,
+                                       long long head_stride, int n_heads, int n_kv, int head_dim, float scale,
+                                       float *part, long long part_bs, unsigned *cnt, int G, float *out,
+                                       long long out_bs, int B, hipStream_t st) {
+    QtAttnArgs a;
+    a.q = q; a.qn = qn; a.kn = kn; a.rc = rc; a.rs = rs; a.eps = eps; a.d_pos = d_pos; a.Lval = 0;
+    a.K = K; a.V = V; a.pos_stride = pos_stride; a.head_stride = head_stride;
+    a.n_heads = n_heads; a.n_kv = n_kv; a.scale = scale; a.part = part; a.cnt = cnt; a.out = out;
+    a.q_bs = q_bs; a.kv_bs = kv_bs; a.out_bs = out_bs; a.part_bs = part_bs;
+    return attn_launch(a, 1, head_dim, G, B, st);
 }
 
 // Split-K grid: QT_ATT_G chunks per kv head (256 workgroups for 8 kv heads); a chunk

@@ -1,0 +1,205 @@
+// qt_batch.hip — weight-shared projections for B concurrent decode streams (gfx950).
+//
+// The batched step (qwen_tts_talker.c:1192-1270, batch_talker_step_impl; CUDA twin
+// qwen_tts_cuda_talker.cu:441-560) reads every weight matrix ONCE per step for all B
+// streams: Y[b][r] = W[r,:] . X[b][:].  With B = 32 that is a real dense contraction
+// (32 x rows x cols), so it runs on the matrix cores with the int8 weights as they are:
+//
+//   Activation pieces.  Each stream's f32 activation row x (length K) is split exactly
+//   into three int8 planes with one power-of-two scale s = 2^(e-6), 2^e <= max|x| < 2^(e+1):
+//       x/s = p1 + p2*2^-7 + p3*2^-14 + e3,   p1 in [-128,127], p2,p3 in [0,127],
+//       0 <= e3 < 2^-14,
+//   every step (scale, floor, subtract, *128) exact in f32, so |x - s*(p1+p2/128+p3/16384)|
+//   < s*2^-14 <= max|x| * 2^-20.
+//   Integer products.  v_mfma_i32_16x16x64_i8 accumulates q*p exactly in int32
+//   (|sum| <= 128*128*6144 < 2^31), so the three dot products C1, C2, C3 are exact and
+//   independent of summation order; y = s * (C1 + C2/128 + C3/16384) is formed in f64
+//   (exact) and rounded once, then multiplied by the row scale as the reference does
+//   (qwen_tts_kernels.c:2350-2351).  Against the reference's f32 accumulation the result
+//   differs by the f32 rounding of its own sum (~1e-7 relative), nothing systematic.
+//
+// Layouts.  Weights: the device int8 rows of qt_device.h (u = q ^ 0x80); one XOR per
+// dword restores the signed byte for the MFMA.  Pieces: [K/64][3*Bp][64] int8, column
+// col = piece*Bp + b (Bp = B rounded up to 16; padding columns are zero), so the MFMA B
+// operand of N-tile t at k-block kb is one contiguous KiB (16 columns x 64 bytes).
+// MFMA operand mapping (16x16x64, wave64): lane l supplies 16 bytes of A row (l % 16)
+// and of B column (l % 16) for the same k group (l / 16); lane l receives D rows
+// 4*(l/16)+i (i < 4) of column l % 16.  A and B use the same k mapping, so any k order
+// within a group gives the same exact integer dot product.
+//
+// Work split: one workgroup per 16 weight rows, one wave per 512 columns of K (K/512
+// waves: 4 for K = 2048, 12 for K = 6144), partial int32 tiles summed through LDS.
+#include "qt_device.h"
+
+typedef int qt_v4i __attribute__((ext_vector_type(4)));
+
+#define QT_BG_KW 512           // K columns per wave
+#define QT_BG_MAXW 16          // waves per workgroup at most (K <= 8192)
+
+// ---- activation pieces ---------------------------------------------------------------
+// One workgroup (256 threads) per padded stream b < Bp.  x row b at x + b*xstride;
+// norm_w != NULL: the pieces are of RMSNorm(x)*w (qwen_tts_kernels.c:292-382), else of x.
+// Padding streams (b >= B) write zero pieces.
+__global__ __launch_bounds__(256) void k_bpieces(const float *x, long long xstride, const float *norm_w, float eps,
+                                                 int K, int B, int Bp, int8_t *P, float *S) {
+    __shared__ float red[QT_WAVES];
+    __shared__ float s_max[QT_WAVES];
+    const int b = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int col1 = b, col2 = Bp + b, col3 = 2 * Bp + b;
+    const size_t cs = (size_t)3 * Bp * 64;      // bytes per k-block of all columns
+    if (b >= B) {
+        for (int k = tid; k < K; k += 256) {
+            const size_t o = (size_t)(k >> 6) * cs + (k & 63);
+            P[o + (size_t)col1 * 64] = 0; P[o + (size_t)col2 * 64] = 0; P[o + (size_t)col3 * 64] = 0;
+        }
+        if (tid == 0) S[b] = 0.f;
+        return;
+    }
+    const float *xb = x + (size_t)b * xstride;
+    float inv = 1.0f;
+    if (norm_w) {
+        float ss = 0.f;
+        for (int k = tid; k < K; k += 256) ss = fmaf(xb[k], xb[k], ss);
+        ss = group_sum<64>(ss);
+        if (lane == 0) red[wave] = ss;
+        __syncthreads();
+        ss = red[0] + red[1] + red[2] + red[3];
+        inv = 1.0f / sqrtf(ss / (float)K + eps);
+    }
+    float m = 0.f;
+    for (int k = tid; k < K; k += 256) {
+        const float v = norm_w ? (xb[k] * inv) * norm_w[k] : xb[k];
+        m = fmaxf(m, fabsf(v));
+    }
+    m = group_max<64>(m);
+    if (lane == 0) s_max[wave] = m;
+    __syncthreads();
+    m = fmaxf(fmaxf(s_max[0], s_max[1]), fmaxf(s_max[2], s_max[3]));
+    // s = 2^(e-6) with 2^e <= m < 2^(e+1); m == 0 (or not finite) -> all pieces zero
+    const bool ok = m > 0.f && m <= 3.0e38f;
+    const int e = ok ? ilogbf(m) : 0;
+    const float sc = ok ? ldexpf(1.0f, e - 6) : 0.f, isc = ok ? ldexpf(1.0f, 6 - e) : 0.f;
+    for (int k = tid; k < K; k += 256) {
+        const float v = norm_w ? (xb[k] * inv) * norm_w[k] : xb[k];
+        int q1 = 0, q2 = 0, q3 = 0;
+        if (ok) {
+            const float y = v * isc;             // |y| < 128, exact
+            const float f1 = floorf(y);
+            const float r1 = (y - f1) * 128.0f;  // [0, 128), exact
+            const float f2 = floorf(r1);
+            const float r2 = (r1 - f2) * 128.0f;
+            const float f3 = floorf(r2);
+            q1 = (int)f1; q2 = (int)f2; q3 = (int)f3;
+        }
+        const size_t o = (size_t)(k >> 6) * cs + (k & 63);
+        P[o + (size_t)col1 * 64] = (int8_t)q1;
+        P[o + (size_t)col2 * 64] = (int8_t)q2;
+        P[o + (size_t)col3 * 64] = (int8_t)q3;
+    }
+    if (tid == 0) S[b] = sc;
+}
+
+// ---- int8 weights x activation pieces --------------------------------------------------
+struct QtBgArgs {
+    const uint8_t *w;     // device int8 rows (u = q ^ 0x80), [rows][K]
+    const float *scale;   // [rows]
+    int rows, K;
+    const int8_t *P;      // pieces [K/64][3*Bp][64]
+    const float *S;       // [Bp]
+    int B;
+    float *out;           // STORE: out[b*ostride + r]; SWIGLU: out[b*ostride + r/2]; RESID: out[b*ostride + r] +=
+    long long ostride;
+};
+
+template <int NT, int EPI>
+__global__ __launch_bounds__(QT_BG_MAXW * 64) void k_bgemm_i8(QtBgArgs a) {
+    constexpr int BP = NT * 16 / 3;                // padded streams
+    __shared__ int red[NT][4][64];                 // summed int32 tiles
+    const int nw = blockDim.x >> 6;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int r0 = blockIdx.x * 16;
+    const int m = lane & 15, grp = lane >> 4;
+    const int row = min(r0 + m, a.rows - 1);       // rows past the end repeat the last (discarded)
+    const uint8_t *wr = a.w + (size_t)row * a.K;
+    const size_t cs = (size_t)3 * BP * 64;
+
+    qt_v4i acc[NT];
+#pragma unroll
+    for (int t = 0; t < NT; t++) acc[t] = qt_v4i{0, 0, 0, 0};
+    const int kw0 = wave * QT_BG_KW;
+    const int nkb = max(0, min(QT_BG_KW, a.K - kw0)) >> 6;
+    for (int kb = 0; kb < nkb; kb++) {
+        const int k = kw0 + kb * 64;
+        const uint4 wa = *reinterpret_cast<const uint4 *>(wr + k + grp * 16);
+        const qt_v4i A = qt_v4i{(int)(wa.x ^ 0x80808080u), (int)(wa.y ^ 0x80808080u), (int)(wa.z ^ 0x80808080u),
+                                (int)(wa.w ^ 0x80808080u)};
+        const int8_t *pb = a.P + (size_t)(k >> 6) * cs + (size_t)m * 64 + grp * 16;
+#pragma unroll
+        for (int t = 0; t < NT; t++) {
+            const uint4 pv = *reinterpret_cast<const uint4 *>(pb + (size_t)t * 16 * 64);
+            const qt_v4i Bv = qt_v4i{(int)pv.x, (int)pv.y, (int)pv.z, (int)pv.w};
+            acc[t] = __builtin_amdgcn_mfma_i32_16x16x64_i8(A, Bv, acc[t], 0, 0, 0);
+        }
+    }
+    // sum the waves' tiles (exact; wave 0 stores, the others add in wave order)
+    for (int w = 0; w < nw; w++) {
+        if (wave == w) {
+#pragma unroll
+            for (int t = 0; t < NT; t++)
+#pragma unroll
+                for (int i = 0; i < 4; i++) red[t][i][lane] = (w == 0 ? 0 : red[t][i][lane]) + acc[t][i];
+        }
+        __syncthreads();
+    }
+    // epilogue: thread j -> (local row j / BP, stream j % BP)
+    for (int j = tid; j < 16 * BP; j += blockDim.x) {
+        const int rl = j / BP, b = j % BP, r = r0 + rl;
+        if (b >= a.B || r >= a.rows) continue;
+        if (EPI == QT_EPI_SWIGLU && (rl & 1)) continue;
+        auto val = [&](int rr) -> float {   // rr: local row
+            const int t0 = b >> 4, ln = (rr >> 2) * 16 + (b & 15), i = rr & 3;
+            const double c = (double)red[t0][i][ln] + (double)red[t0 + BP / 16][i][ln] * (1.0 / 128.0) +
+                             (double)red[t0 + 2 * BP / 16][i][ln] * (1.0 / 16384.0);
+            const float dot = (float)(c * (double)a.S[b]);
+            return __fmul_rn(dot, a.scale[r0 + rr]);
+        };
+        float *ob = a.out + (size_t)b * a.ostride;
+        if (EPI == QT_EPI_STORE) ob[r] = val(rl);
+        else if (EPI == QT_EPI_RESID) ob[r] = __fadd_rn(ob[r], val(rl));
+        else if (EPI == QT_EPI_SWIGLU) {
+            const float g = val(rl), u = val(rl + 1);
+            ob[r >> 1] = g / (1.0f + expf(-g)) * u;
+        }
+    }
+}
+
+extern "C" hipError_t qt_launch_bpieces(const float *x, long long xstride, const float *norm_w, float eps, int K, int B,
+                                        int Bp, int8_t *P, float *S, hipStream_t st) {
+    if (K <= 0 || (K & 63) || B <= 0 || Bp < B || (Bp & 15) || Bp > 64) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_bpieces, dim3(Bp), dim3(256), 0, st, x, xstride, norm_w, eps, K, B, Bp, P, S);
+    return hipGetLastError();
+}
+
+// Bp: padded stream count of the pieces (16, 32, 48, 64).
+extern "C" hipError_t qt_launch_bgemm_i8(int epi, const uint8_t *w, const float *scale, int rows, int K,
+                                         const int8_t *P, const float *S, int B, int Bp, float *out,
+                                         long long ostride, hipStream_t st) {
+    if (rows <= 0 || K <= 0 || (K & 63) || K > QT_BG_KW * QT_BG_MAXW || B <= 0 || B > Bp) return hipErrorInvalidValue;
+    if (epi == QT_EPI_SWIGLU && (rows & 1)) return hipErrorInvalidValue;
+    QtBgArgs a;
+    a.w = w; a.scale = scale; a.rows = rows; a.K = K; a.P = P; a.S = S; a.B = B; a.out = out; a.ostride = ostride;
+    const int nw = (K + QT_BG_KW - 1) / QT_BG_KW;
+    dim3 grid((rows + 15) / 16), block(nw * 64);
+#define QT_BG_CASE(NT_)                                                                                   \
+    if (epi == QT_EPI_STORE) hipLaunchKernelGGL((k_bgemm_i8<NT_, QT_EPI_STORE>), grid, block, 0, st, a);   \
+    else if (epi == QT_EPI_RESID) hipLaunchKernelGGL((k_bgemm_i8<NT_, QT_EPI_RESID>), grid, block, 0, st, a); \
+    else if (epi == QT_EPI_SWIGLU) hipLaunchKernelGGL((k_bgemm_i8<NT_, QT_EPI_SWIGLU>), grid, block, 0, st, a); \
+    else return hipErrorInvalidValue;
+    if (Bp == 16) { QT_BG_CASE(3) }
+    else if (Bp == 32) { QT_BG_CASE(6) }
+    else if (Bp == 48) { QT_BG_CASE(9) }
+    else if (Bp == 64) { QT_BG_CASE(12) }
+    else return hipErrorInvalidValue;
+#undef QT_BG_CASE
+    return hipGetLastError();
+}

@@ -19,7 +19,17 @@ hipError_t qt_launch_attn(int prep, const float *q, const float *qn, const float
                           const float *rs, float eps, const int *d_pos, int Lval, uint16_t *K, uint16_t *V,
                           long long pos_stride, long long head_stride, int n_heads, int n_kv, int head_dim,
                           float scale, float *part, unsigned *cnt, int G, float *out, hipStream_t st);
+hipError_t qt_launch_attn_b(const float *q, long long q_bs, const float *qn, const float *kn, const float *rc,
+                            const float *rs, float eps, const int *d_pos, uint16_t *K, uint16_t *V, long long kv_bs,
+                            long long pos_stride, long long head_stride, int n_heads, int n_kv, int head_dim,
+                            float scale, float *part, long long part_bs, unsigned *cnt, int G, float *out,
+                            long long out_bs, int B, hipStream_t st);
 int qt_attn_grid(int max_len);
+/* batched projections (qt_batch.hip) */
+hipError_t qt_launch_bpieces(const float *x, long long xstride, const float *norm_w, float eps, int K, int B, int Bp,
+                             int8_t *P, float *S, hipStream_t st);
+hipError_t qt_launch_bgemm_i8(int epi, const uint8_t *w, const float *scale, int rows, int K, const int8_t *P,
+                              const float *S, int B, int Bp, float *out, long long ostride, hipStream_t st);
 hipError_t qt_launch_rmsnorm(const float *x, const float *w, float *out, int n, float eps, int *d_pos,
                              hipStream_t st);
 hipError_t qt_launch_rmsnorm_rows(float *x, const float *w, int rows, int n, float eps, hipStream_t st);

@@ -868,6 +868,242 @@ fail:
     return -1;
 }
 
+/* ---- batched steps: B streams over one state's resident weights -------------------- */
+/* Twin of qwen_cuda_talker_batch_* / qwen_cuda_cp_batch_* (qwen_tts_cuda_talker.cu:595-648,
+ * 879-915) and of the CPU batch_talker_step_impl (qwen_tts_talker.c:1192-1270): B
+ * sequences, each at its own position pos_arr[b] (ragged), each with its own bf16 KV
+ * cache; the weights are the single state's (never freed here), read ONCE per step for
+ * all streams.  Per layer (int8 weights):
+ *   pieces(RMSNorm(x)) -> MFMA QKV -> attention (q/k norm, RoPE, KV append, split-K over
+ *   each stream's own length, B streams in one grid) -> pieces(attn) -> MFMA O + residual
+ *   -> pieces(RMSNorm(x)) -> MFMA gate|up + SwiGLU -> pieces(h) -> MFMA down + residual,
+ * captured once into a hipGraph (positions live on the device).  bf16 / q4_0 weights
+ * have no batched kernel here: their projections run as B matvecs per matrix (weights
+ * re-read per stream, like the reference's QWEN_BATCH_NOMATMUL diagnostic). */
+
+#define QWEN_HIP_BATCH_MAX 64
+
+typedef struct {
+    const stack_t *s;          /* borrowed weights / norms / rope tables */
+    int B, Bp, kv_max, is_cp;
+    hipStream_t st;
+    uint16_t *kc, *vc;         /* [B][L][nkv][kv_max][hd] */
+    float *x, *qkv, *attn, *h, *hid;
+    int8_t *pc; float *ps;     /* activation pieces [Kmax/64][3*Bp][64], scales [Bp] */
+    float *part; unsigned *cnt;
+    int *d_pos;                /* [B] */
+    float *h_io; int *h_pos;   /* pinned */
+    hipGraphExec_t exec; int graph_ready;
+    int dead;
+} batch_t;
+
+static void batch_destroy(batch_t *bt) {
+    if (!bt) return;
+    if (bt->graph_ready) (void)hipGraphExecDestroy(bt->exec);
+    void *bufs[] = {bt->kc, bt->vc, bt->x, bt->qkv, bt->attn, bt->h, bt->hid, bt->pc, bt->ps, bt->part, bt->cnt, bt->d_pos};
+    for (size_t i = 0; i < sizeof bufs / sizeof bufs[0]; i++) if (bufs[i]) (void)hipFree(bufs[i]);
+    if (bt->h_io) (void)hipHostFree(bt->h_io);
+    if (bt->h_pos) (void)hipHostFree(bt->h_pos);
+    if (bt->st) (void)hipStreamDestroy(bt->st);
+    free(bt);
+}
+
+static batch_t *batch_create(const stack_t *s, int B, int is_cp) {
+    batch_t *bt = calloc(1, sizeof *bt);
+    if (!bt) { SETERR("out of host memory"); return NULL; }
+    REQ(B >= 1 && B <= QWEN_HIP_BATCH_MAX, "batch size %d out of range (1..%d)", B, QWEN_HIP_BATCH_MAX);
+    REQ(s->H % 64 == 0 && s->F % 64 == 0 && s->qd % 64 == 0, "batched step needs dims divisible by 64");
+    bt->s = s; bt->B = B; bt->Bp = (B + 15) & ~15; bt->kv_max = s->kv_max; bt->is_cp = is_cp;
+    HCK(hipStreamCreateWithFlags(&bt->st, hipStreamNonBlocking));
+    const size_t per = (size_t)s->L * s->nkv * s->kv_max * s->hd;
+    const int K = s->F > s->H ? (s->F > s->qd ? s->F : s->qd) : (s->H > s->qd ? s->H : s->qd);
+    HCK(hipMalloc((void **)&bt->kc, (size_t)B * per * 2));
+    HCK(hipMalloc((void **)&bt->vc, (size_t)B * per * 2));
+    HCK(hipMemsetAsync(bt->kc, 0, (size_t)B * per * 2, bt->st));
+    HCK(hipMemsetAsync(bt->vc, 0, (size_t)B * per * 2, bt->st));
+    HCK(hipMalloc((void **)&bt->x, (size_t)B * s->H * sizeof(float)));
+    HCK(hipMalloc((void **)&bt->hid, (size_t)B * s->H * sizeof(float)));
+    HCK(hipMalloc((void **)&bt->qkv, (size_t)B * (s->qd + 2 * s->kvd) * sizeof(float)));
+    HCK(hipMalloc((void **)&bt->attn, (size_t)B * s->qd * sizeof(float)));
+    HCK(hipMalloc((void **)&bt->h, (size_t)B * s->F * sizeof(float)));
+    HCK(hipMalloc((void **)&bt->pc, (size_t)K * 3 * bt->Bp));
+    HCK(hipMalloc((void **)&bt->ps, (size_t)bt->Bp * sizeof(float)));
+    HCK(hipMalloc((void **)&bt->part, (size_t)B * s->nkv * s->attn_G * (s->nh / s->nkv) * 130 * sizeof(float)));
+    HCK(hipMalloc((void **)&bt->cnt, (size_t)B * s->nkv * sizeof(unsigned)));
+    HCK(hipMemsetAsync(bt->cnt, 0, (size_t)B * s->nkv * sizeof(unsigned), bt->st));
+    HCK(hipMalloc((void **)&bt->d_pos, (size_t)B * sizeof(int)));
+    HCK(hipHostMalloc((void **)&bt->h_io, (size_t)B * s->H * sizeof(float), hipHostMallocDefault));
+    HCK(hipHostMalloc((void **)&bt->h_pos, (size_t)B * sizeof(int), hipHostMallocDefault));
+    HCK(hipStreamSynchronize(bt->st));
+    return bt;
+fail:
+    batch_destroy(bt);
+    return NULL;
+}
+
+/* dst[b] = W . src[b] (+ epilogue) for the B streams.  Pieces of src (optionally
+ * RMS-normalised with nw) are computed first on the int8 path. */
+static hipError_t batch_proj(batch_t *bt, const dmat_t *m, int epi, const float *nw, const float *src, long long sstride,
+                             float *dst, long long dstride) {
+    const stack_t *s = bt->s;
+    hipError_t e;
+    if (m->prec == QWEN_HIP_INT8) {
+        if ((e = qt_launch_bpieces(src, sstride, nw, s->eps, m->cols, bt->B, bt->Bp, bt->pc, bt->ps, bt->st))) return e;
+        return qt_launch_bgemm_i8(epi, m->w, m->scale, m->rows, m->cols, bt->pc, bt->ps, bt->B, bt->Bp, dst, dstride, bt->st);
+    }
+    for (int b = 0; b < bt->B; b++) {
+        float *d = dst + (size_t)b * dstride;
+        if ((e = qt_launch_mv(m->prec, epi, nw != NULL, src + (size_t)b * sstride, nw, s->eps, m->w, m->scale, m->s16,
+                              m->rows, m->cols, epi == QT_EPI_RESID ? NULL : d, epi == QT_EPI_RESID ? d : NULL, NULL,
+                              NULL, bt->st))) return e;
+    }
+    return hipSuccess;
+}
+
+static hipError_t batch_body(void *arg) {
+    batch_t *bt = (batch_t *)arg;
+    const stack_t *s = bt->s;
+    hipError_t e;
+    const float scale = 1.0f / sqrtf((float)s->hd);
+    const int H = s->H, F = s->F, QKV = s->qd + 2 * s->kvd;
+    const long long per = (long long)s->L * s->nkv * s->kv_max * s->hd;
+    for (int l = 0; l < s->L; l++) {
+        const size_t lay = (size_t)l * s->nkv * s->kv_max * s->hd;
+        if ((e = batch_proj(bt, &s->qkv[l], QT_EPI_STORE, s->in_norm[l], bt->x, H, bt->qkv, QKV))) return e;
+        if ((e = qt_launch_attn_b(bt->qkv, QKV, s->qn[l], s->kn[l], s->rope_cos, s->rope_sin, s->eps, bt->d_pos,
+                                  bt->kc + lay, bt->vc + lay, per, s->hd, (long long)s->kv_max * s->hd, s->nh, s->nkv,
+                                  s->hd, scale, bt->part, (long long)s->nkv * s->attn_G * (s->nh / s->nkv) * 130,
+                                  bt->cnt, s->attn_G, bt->attn, s->qd, bt->B, bt->st))) return e;
+        if ((e = batch_proj(bt, &s->o[l], QT_EPI_RESID, NULL, bt->attn, s->qd, bt->x, H))) return e;
+        if ((e = batch_proj(bt, &s->gu[l], QT_EPI_SWIGLU, s->post_norm[l], bt->x, H, bt->h, F))) return e;
+        if ((e = batch_proj(bt, &s->dn[l], QT_EPI_RESID, NULL, bt->h, F, bt->x, H))) return e;
+    }
+    if (bt->is_cp) return hipSuccess;
+    if ((e = hipMemcpyAsync(bt->hid, bt->x, (size_t)bt->B * H * sizeof(float), hipMemcpyDeviceToDevice, bt->st))) return e;
+    return qt_launch_rmsnorm_rows(bt->hid, s->final_norm, bt->B, H, s->eps, bt->st);
+}
+
+/* One batched step: x[b] <- in[b] (host), positions <- pos_arr, run, out[b] <- hid or x. */
+static int batch_step_impl(batch_t *bt, const float *in, const int *pos_arr, float *out) {
+    if (!bt || bt->dead) { SETERR("batch state is dead or NULL"); return -1; }
+    const stack_t *s = bt->s;
+    const int B = bt->B, H = s->H;
+    REQ(in && pos_arr, "null embeds / positions");
+    for (int b = 0; b < B; b++)
+        REQ(pos_arr[b] >= 0 && pos_arr[b] < bt->kv_max && pos_arr[b] < s->rope_len,
+            "stream %d: pos %d out of range (kv_max %d, rope %d)", b, pos_arr[b], bt->kv_max, s->rope_len);
+    memcpy(bt->h_io, in, (size_t)B * H * sizeof(float));
+    memcpy(bt->h_pos, pos_arr, (size_t)B * sizeof(int));
+    HCK(hipMemcpyAsync(bt->x, bt->h_io, (size_t)B * H * sizeof(float), hipMemcpyHostToDevice, bt->st));
+    HCK(hipMemcpyAsync(bt->d_pos, bt->h_pos, (size_t)B * sizeof(int), hipMemcpyHostToDevice, bt->st));
+    if (graphs_enabled()) {
+        if (!bt->graph_ready) {
+            if (capture(bt->st, &bt->exec, batch_body, bt) != 0) goto fail;
+            bt->graph_ready = 1;
+        }
+        HCK(hipGraphLaunch(bt->exec, bt->st));
+    } else {
+        HCK(batch_body(bt));
+    }
+    HCK(hipMemcpyAsync(bt->h_io, bt->is_cp ? bt->x : bt->hid, (size_t)B * H * sizeof(float), hipMemcpyDeviceToHost, bt->st));
+    HCK(hipStreamSynchronize(bt->st));
+    if (out) memcpy(out, bt->h_io, (size_t)B * H * sizeof(float));
+    return 0;
+fail:
+    if (bt) bt->dead = 1;
+    return -1;
+}
+
+void *qwen_hip_talker_batch_init(void *single, int B) {
+    talker_t *t = (talker_t *)single;
+    if (!t || t->dead) { SETERR("batch init: single state is dead or NULL"); return NULL; }
+    return batch_create(&t->s, B, 0);
+}
+int qwen_hip_talker_batch_step(void *state, const float *embeds, const int *pos_arr, float *hidden_out) {
+    return batch_step_impl((batch_t *)state, embeds, pos_arr, hidden_out);
+}
+int qwen_hip_talker_batch_upload_slot(void *state, int b, const uint16_t *kv_k, const uint16_t *kv_v, int src_kv_max,
+                                      int prefill_len) {
+    batch_t *bt = (batch_t *)state;
+    if (!bt || bt->dead) { SETERR("batch state is dead or NULL"); return -1; }
+    const stack_t *s = bt->s;
+    if (prefill_len <= 0) return 0;
+    REQ(b >= 0 && b < bt->B, "slot %d out of range", b);
+    REQ(kv_k && kv_v, "null KV");
+    REQ(prefill_len <= bt->kv_max && prefill_len <= src_kv_max, "prefill_len %d exceeds kv_max", prefill_len);
+    const size_t per = (size_t)s->L * s->nkv * s->kv_max * s->hd;
+    for (int l = 0; l < s->L; l++)
+        for (int g = 0; g < s->nkv; g++) {
+            const size_t dst = (size_t)b * per + (((size_t)l * s->nkv + g) * s->kv_max) * s->hd;
+            const size_t src = (((size_t)b * s->L + l) * src_kv_max) * s->kvd + (size_t)g * s->hd;
+            HCK(hipMemcpy2DAsync(bt->kc + dst, s->hd * 2, kv_k + src, (size_t)s->kvd * 2, s->hd * 2, prefill_len,
+                                 hipMemcpyDefault, bt->st));
+            HCK(hipMemcpy2DAsync(bt->vc + dst, s->hd * 2, kv_v + src, (size_t)s->kvd * 2, s->hd * 2, prefill_len,
+                                 hipMemcpyDefault, bt->st));
+        }
+    HCK(hipStreamSynchronize(bt->st));
+    return 0;
+fail:
+    return -1;
+}
+int qwen_hip_talker_batch_download_slot(void *state, int b, uint16_t *kv_k, uint16_t *kv_v, int dst_kv_max, int n) {
+    batch_t *bt = (batch_t *)state;
+    if (!bt) { SETERR("NULL batch state"); return -1; }
+    const stack_t *s = bt->s;
+    REQ(b >= 0 && b < bt->B, "slot %d out of range", b);
+    REQ(n >= 0 && n <= bt->kv_max && n <= dst_kv_max, "n %d out of range", n);
+    if (n == 0) return 0;
+    const size_t per = (size_t)s->L * s->nkv * s->kv_max * s->hd;
+    for (int l = 0; l < s->L; l++)
+        for (int g = 0; g < s->nkv; g++) {
+            const size_t src = (size_t)b * per + (((size_t)l * s->nkv + g) * s->kv_max) * s->hd;
+            const size_t dst = (((size_t)b * s->L + l) * dst_kv_max) * s->kvd + (size_t)g * s->hd;
+            HCK(hipMemcpy2DAsync(kv_k + dst, (size_t)s->kvd * 2, bt->kc + src, s->hd * 2, s->hd * 2, n,
+                                 hipMemcpyDefault, bt->st));
+            HCK(hipMemcpy2DAsync(kv_v + dst, (size_t)s->kvd * 2, bt->vc + src, s->hd * 2, s->hd * 2, n,
+                                 hipMemcpyDefault, bt->st));
+        }
+    HCK(hipStreamSynchronize(bt->st));
+    return 0;
+fail:
+    return -1;
+}
+/* Benchmark entry: n batched steps on the device state of the last batch_step call
+ * (same inputs, positions unchanged: every step rewrites the same KV rows), no sync. */
+int qwen_hip_talker_batch_step_async(void *state, int n_steps) {
+    batch_t *bt = (batch_t *)state;
+    if (!bt || bt->dead || !bt->graph_ready) { SETERR("batch state not initialised by a batch_step call"); return -1; }
+    for (int i = 0; i < n_steps; i++) HCK(hipGraphLaunch(bt->exec, bt->st));
+    return 0;
+fail:
+    bt->dead = 1;
+    return -1;
+}
+int qwen_hip_talker_batch_sync(void *state) {
+    batch_t *bt = (batch_t *)state;
+    if (!bt) return -1;
+    HCK(hipStreamSynchronize(bt->st));
+    return 0;
+fail:
+    bt->dead = 1;
+    return -1;
+}
+void *qwen_hip_talker_batch_stream(void *state) { return state ? (void *)((batch_t *)state)->st : NULL; }
+void qwen_hip_talker_batch_free(void *state) { batch_destroy((batch_t *)state); }
+
+
+/* CP batch twins (qwen_tts_cuda_talker.cu:879-915): x[B][cp_hidden] host residuals in
+ * place, one 5-layer pass per stream at pos_arr[b] (each stream's own CP KV). */
+void *qwen_hip_cp_batch_init(void *single, int B) {
+    cp_t *c = (cp_t *)single;
+    if (!c || c->dead) { SETERR("CP batch init: single state is dead or NULL"); return NULL; }
+    return batch_create(&c->s, B, 1);
+}
+int qwen_hip_cp_batch_step(void *state, float *x, const int *pos_arr) {
+    return batch_step_impl((batch_t *)state, x, pos_arr, x);
+}
+void qwen_hip_cp_batch_free(void *state) { batch_destroy((batch_t *)state); }
+
 /* ---- level 1: per-op backend + kernel-API parity surface ----------------------------- */
 
 typedef struct { const void *host; int rows, cols; dmat_t m; } wcache_t;
@@ -972,6 +1208,45 @@ static int op_matvec(int prec, float *y, const void *W, const float *scale, cons
     return 0;
 fail:
     dmat_free(&m); if (dx) (void)hipFree(dx); if (dy) (void)hipFree(dy); if (tmp) (void)hipFree(tmp);
+    return -1;
+}
+
+/* qwen_matmat_int8 (qwen_tts_kernels.h:121-122): Y[rows][B] = (W*scale) @ X[cols][B],
+ * row-major f32, B <= 64, on the batched MFMA kernel (cols multiple of 64). */
+int qwen_hip_op_matmat_int8(float *Y, const int8_t *W, const float *scale, const float *X, int rows, int cols, int B) {
+    hipStream_t st = op_stream();
+    dmat_t m; memset(&m, 0, sizeof m);
+    float *dx = NULL, *dy = NULL, *hx = NULL, *hy = NULL, *ps = NULL;
+    int8_t *pc = NULL;
+    qwen_hip_mat_t src = {W, scale};
+    const int Bp = (B + 15) & ~15;
+    REQ(st, "no stream");
+    REQ(rows > 0 && cols > 0 && cols % 64 == 0 && cols <= 8192, "bad shape %dx%d (cols: multiple of 64, <= 8192)", rows, cols);
+    REQ(B >= 1 && B <= 64, "B %d out of range (1..64)", B);
+    REQ(dmat_alloc(&m, QWEN_HIP_INT8, rows, cols) == 0, "alloc");
+    REQ(dmat_put(&m, 0, &src, QWEN_HIP_INT8, rows, st, NULL) == 0, "upload");
+    hx = malloc((size_t)B * cols * sizeof(float)); hy = malloc((size_t)B * rows * sizeof(float));
+    REQ(hx && hy, "host alloc");
+    for (int k = 0; k < cols; k++) for (int j = 0; j < B; j++) hx[(size_t)j * cols + k] = X[(size_t)k * B + j];
+    HCK(hipMalloc((void **)&dx, (size_t)B * cols * sizeof(float)));
+    HCK(hipMalloc((void **)&dy, (size_t)B * rows * sizeof(float)));
+    HCK(hipMalloc((void **)&pc, (size_t)cols * 3 * Bp));
+    HCK(hipMalloc((void **)&ps, (size_t)Bp * sizeof(float)));
+    HCK(hipMemcpyAsync(dx, hx, (size_t)B * cols * sizeof(float), hipMemcpyHostToDevice, st));
+    HCK(qt_launch_bpieces(dx, cols, NULL, 0.f, cols, B, Bp, pc, ps, st));
+    HCK(qt_launch_bgemm_i8(QT_EPI_STORE, m.w, m.scale, rows, cols, pc, ps, B, Bp, dy, rows, st));
+    HCK(hipMemcpyAsync(hy, dy, (size_t)B * rows * sizeof(float), hipMemcpyDeviceToHost, st));
+    HCK(hipStreamSynchronize(st));
+    for (int r = 0; r < rows; r++) for (int j = 0; j < B; j++) Y[(size_t)r * B + j] = hy[(size_t)j * rows + r];
+    dmat_free(&m); (void)hipFree(dx); (void)hipFree(dy); (void)hipFree(pc); (void)hipFree(ps); free(hx); free(hy);
+    return 0;
+fail:
+    dmat_free(&m);
+    if (dx) (void)hipFree(dx);
+    if (dy) (void)hipFree(dy);
+    if (pc) (void)hipFree(pc);
+    if (ps) (void)hipFree(ps);
+    free(hx); free(hy);
     return -1;
 }
 

@@ -28,7 +28,10 @@ EXPORTS = [
     "qwen_hip_op_matvec_bf16", "qwen_hip_op_causal_attention_bf16kv", "qwen_hip_op_rms_norm",
     "qwen_hip_op_rms_norm_per_head", "qwen_hip_op_swiglu", "qwen_hip_op_argmax_matvec",
     "qwen_hip_op_quantize_int8", "qwen_hip_op_quantize_q4_0", "qwen_hip_talker_dequant",
-    "qwen_hip_last_error",
+    "qwen_hip_last_error", "qwen_hip_talker_batch_init", "qwen_hip_talker_batch_step",
+    "qwen_hip_talker_batch_upload_slot", "qwen_hip_talker_batch_free", "qwen_hip_talker_batch_download_slot",
+    "qwen_hip_talker_batch_step_async", "qwen_hip_talker_batch_sync", "qwen_hip_talker_batch_stream",
+    "qwen_hip_cp_batch_init", "qwen_hip_cp_batch_step", "qwen_hip_cp_batch_free", "qwen_hip_op_matmat_int8",
 ]
 
 
@@ -110,6 +113,20 @@ def lib():
         L.qwen_hip_op_quantize_int8.argtypes = [vp, i, i, vp, vp]; L.qwen_hip_op_quantize_int8.restype = i
         L.qwen_hip_op_quantize_q4_0.argtypes = [vp, i, i, vp]; L.qwen_hip_op_quantize_q4_0.restype = i
         L.qwen_hip_last_error.restype = C.c_char_p
+        L.qwen_hip_talker_batch_init.argtypes = [vp, i]; L.qwen_hip_talker_batch_init.restype = vp
+        L.qwen_hip_talker_batch_step.argtypes = [vp, vp, vp, vp]; L.qwen_hip_talker_batch_step.restype = i
+        L.qwen_hip_talker_batch_upload_slot.argtypes = [vp, i, vp, vp, i, i]
+        L.qwen_hip_talker_batch_upload_slot.restype = i
+        L.qwen_hip_talker_batch_download_slot.argtypes = [vp, i, vp, vp, i, i]
+        L.qwen_hip_talker_batch_download_slot.restype = i
+        L.qwen_hip_talker_batch_free.argtypes = [vp]
+        L.qwen_hip_talker_batch_step_async.argtypes = [vp, i]; L.qwen_hip_talker_batch_step_async.restype = i
+        L.qwen_hip_talker_batch_sync.argtypes = [vp]; L.qwen_hip_talker_batch_sync.restype = i
+        L.qwen_hip_talker_batch_stream.argtypes = [vp]; L.qwen_hip_talker_batch_stream.restype = vp
+        L.qwen_hip_cp_batch_init.argtypes = [vp, i]; L.qwen_hip_cp_batch_init.restype = vp
+        L.qwen_hip_cp_batch_step.argtypes = [vp, vp, vp]; L.qwen_hip_cp_batch_step.restype = i
+        L.qwen_hip_cp_batch_free.argtypes = [vp]
+        L.qwen_hip_op_matmat_int8.argtypes = [vp, vp, vp, vp, i, i, i]; L.qwen_hip_op_matmat_int8.restype = i
         _lib = L
     return _lib
 
@@ -209,6 +226,44 @@ class Talker:
             pass
 
 
+class TalkerBatch:
+    """B streams over a Talker's resident weights (qwen_hip_talker_batch_*)."""
+
+    def __init__(self, talker, B):
+        self.t, self.B = talker, B
+        self.h = lib().qwen_hip_talker_batch_init(talker.h, B)
+        if not self.h:
+            raise RuntimeError("qwen_hip_talker_batch_init failed: " + last_error())
+
+    def step(self, embeds, pos):
+        e = np.ascontiguousarray(embeds, np.float32).reshape(self.B, self.t.H)
+        p = np.ascontiguousarray(pos, np.int32)
+        out = np.empty((self.B, self.t.H), np.float32)
+        check(lib().qwen_hip_talker_batch_step(self.h, _p(e), _p(p), _p(out)), "talker_batch_step")
+        return out
+
+    def upload_slot(self, b, kv_k, kv_v, n):
+        """kv_k/kv_v: [B][n_layers][src_kv_max][kv_dim] bf16 (the batch engine layout)."""
+        check(lib().qwen_hip_talker_batch_upload_slot(self.h, b, _p(kv_k), _p(kv_v), kv_k.shape[2], n), "upload_slot")
+
+    def download_slot(self, b, n):
+        k = np.zeros((self.B, self.t.nl, self.t.kv_max, self.t.kvd), np.uint16)
+        v = np.zeros_like(k)
+        check(lib().qwen_hip_talker_batch_download_slot(self.h, b, _p(k), _p(v), self.t.kv_max, n), "download_slot")
+        return k[b], v[b]
+
+    def free(self):
+        if self.h:
+            lib().qwen_hip_talker_batch_free(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
 class CodePredictor:
     def __init__(self, desc: CpDesc, keep):
         self.desc, self.keep = desc, keep
@@ -228,7 +283,24 @@ class CodePredictor:
         check(lib().qwen_hip_cp_step(self.h, _p(x), pos), "cp_step")
         return x
 
+    def batch_step(self, x, pos):
+        """One pass for B streams (own CP KVs) over this CP's weights; x [B][H]."""
+        x = np.array(x, np.float32, copy=True)
+        B = x.shape[0]
+        if getattr(self, "_bh", None) is None or self._bB != B:
+            if getattr(self, "_bh", None):
+                lib().qwen_hip_cp_batch_free(self._bh)
+            self._bh = lib().qwen_hip_cp_batch_init(self.h, B)
+            self._bB = B
+            if not self._bh:
+                raise RuntimeError("qwen_hip_cp_batch_init failed: " + last_error())
+        check(lib().qwen_hip_cp_batch_step(self._bh, _p(x), _p(np.ascontiguousarray(pos, np.int32))), "cp_batch_step")
+        return x
+
     def free(self):
+        if getattr(self, "_bh", None):
+            lib().qwen_hip_cp_batch_free(self._bh)
+            self._bh = None
         if self.h:
             lib().qwen_hip_cp_free(self.h)
             self.h = None
