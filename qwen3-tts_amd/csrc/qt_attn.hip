@@ -15,9 +15,11 @@
 //   NeoX split-half RoPE from the uploaded cos/sin tables (qwen_tts_talker.c:203-251),
 //   and the KV append at `pos` with f32->bf16 TRUNCATION (qwen_tts_talker.c:612-615),
 //   done by the one workgroup whose chunk holds `pos`.
-// Latency: every lane issues its K and V loads for the chunk's first 64 keys at kernel
-// entry, before the q/k preparation, so HBM latency overlaps the prologue; the key at
-// `pos` (just appended by this workgroup) is taken from LDS instead of the prefetch.
+// Latency: the chunk's K and V rows (up to 128 keys) are copied into LDS with
+// global_load_lds at kernel entry, before the q/k preparation, so one HBM round trip
+// overlaps the prologue; the key at `pos` (appended by this workgroup) is not read from
+// memory but taken from LDS (knew/vnew).  The merging workgroup reuses that LDS for the
+// chunk partials, so a workgroup needs ~72 KB and two fit on a CU.
 #include "qt_device.h"
 
 #define QT_HD 128
@@ -42,58 +44,78 @@ struct QtAttnArgs {
     // independent streams (grid z): element offsets of stream z's q, K/V cache, output,
     // partials and counters; d_pos + z is its position (batched step)
     long long q_bs, kv_bs, out_bs, part_bs;
+    int min_chunk;           // chunks hold at least this many keys (0: ceil(L/G) rounded to 16)
 };
 
-// 8 dims (16 bytes) of key/value j for this lane, raw bf16 bits.
-__device__ __forceinline__ uint4 qt_ld_kv(const uint16_t *base, long long pos_stride, int j, int sub) {
-    return *reinterpret_cast<const uint4 *>(base + (long long)j * pos_stride + sub * 8);
+#define QT_KVB 128   // keys of a chunk staged in LDS at once
+
+// 16 bytes per lane from global memory straight into LDS (global_load_lds_dwordx4):
+// lane i's bytes land at dst + 16*i, dst wave-uniform.  Counted by vmcnt like a load.
+__device__ __forceinline__ void qt_lds_copy16(const void *src, void *dst) {
+    __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void *)src,
+                                     (__attribute__((address_space(3))) void *)dst, 16, 0, 0);
 }
 
-template <int HPK, bool PREP>
+// BATCH (many streams, throughput): grid (n_kv, streams, G) so the workgroups of chunk 0
+// of every stream and head are dispatched first and idle chunks last (a kv head per XCD
+// under round-robin dispatch); the key loops are unrolled with masking; the merging
+// workgroup computes each output as one weighted sum over the chunks (one thread per
+// output) instead of a half-wave reduction per output.  !BATCH keeps the arithmetic
+// order of the fused step's attention phase, which it must match bit for bit.
+template <int HPK, bool PREP, bool BATCH>
 __global__ __launch_bounds__(QT_WG) void k_attn(QtAttnArgs a) {
-    if (blockIdx.z) {
-        const int z = blockIdx.z;
+    const int z = BATCH ? blockIdx.y : blockIdx.z;
+    if (z) {
         a.q += z * a.q_bs; a.K += z * a.kv_bs; a.V += z * a.kv_bs; a.out += z * a.out_bs;
         a.part += z * a.part_bs; a.cnt += (size_t)z * a.n_kv; a.d_pos += z;
     }
-    const int g = blockIdx.y, c = blockIdx.x, G = gridDim.x;
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int g = BATCH ? blockIdx.x : blockIdx.y, c = BATCH ? blockIdx.z : blockIdx.x;
+    const int G = BATCH ? gridDim.z : gridDim.x;
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int pos = PREP ? *a.d_pos : a.Lval - 1;
     const int L = pos + 1;
     int CH = (L + G - 1) / G;
     CH = (CH + 15) & ~15;
+    CH = max(CH, a.min_chunk);
     const int nch = (L + CH - 1) / CH;
     if (c >= nch) return;
     const int j0 = c * CH;
     const int n = min(CH, L - j0);
     const bool append = PREP && (pos >= j0 && pos < j0 + n);
 
+    constexpr int PS = 2 + QT_HD;
+    constexpr int KVBYTES = 2 * QT_KVB * QT_HD * 2, MBYTES = QT_ATT_G * HPK * PS * 4;
     __shared__ float qs[HPK][QT_HD];
     __shared__ float sc[HPK][QT_CH_MAX];
     __shared__ float ored[QT_WAVES][HPK][QT_HD];
     __shared__ float stat[HPK][2];
     __shared__ __align__(16) uint16_t knew[QT_HD];
     __shared__ __align__(16) uint16_t vnew[QT_HD];
-    __shared__ float mpart[QT_ATT_G * HPK * (2 + QT_HD)];   // chunk partials (merging workgroup)
+    // K rows, V rows of a key block; reused as the merge staging
+    __shared__ __align__(16) uint16_t s_kvbuf[(KVBYTES > MBYTES ? KVBYTES : MBYTES) / 2];
+    uint16_t(*s_kv)[QT_KVB * QT_HD] = reinterpret_cast<uint16_t(*)[QT_KVB * QT_HD]>(s_kvbuf);
     __shared__ int last_flag;
 
     const uint16_t *Kg = a.K + (long long)g * a.head_stride;
     const uint16_t *Vg = a.V + (long long)g * a.head_stride;
     const int sub = lane & 15, pg = lane >> 4;
 
-    // ---- 0. prefetch this lane's K/V chunks of the first 64 keys (independent of q) ----
-    uint4 kpre[4], vpre[4];
-#pragma unroll
-    for (int u = 0; u < 4; u++) {
-        const int jj = wave * 4 + pg + 16 * u;
-        if (jj < n) {
-            kpre[u] = qt_ld_kv(Kg, a.pos_stride, j0 + jj, sub);
-            vpre[u] = qt_ld_kv(Vg, a.pos_stride, j0 + jj, sub);
-        } else {
-            kpre[u] = make_uint4(0, 0, 0, 0);
-            vpre[u] = make_uint4(0, 0, 0, 0);
+    // K and/or V rows of keys [kb, kb + min(QT_KVB, n - kb)) of the chunk into s_kv; the
+    // appended key (PREP) is not read from memory, it comes from knew/vnew.
+    auto stage = [&](int kb, bool doK, bool doV) {
+        const int nk = min(QT_KVB, n - kb);
+        const int ninst = (nk + 3) >> 2;
+        for (int i = wave; i < ninst; i += QT_WAVES) {
+            const int jj = kb + i * 4 + pg;
+            if (jj < n && !(PREP && j0 + jj == pos)) {
+                const long long off = (long long)(j0 + jj) * a.pos_stride + sub * 8;
+                if (doK) qt_lds_copy16(Kg + off, &s_kv[0][i * 4 * QT_HD]);
+                if (doV) qt_lds_copy16(Vg + off, &s_kv[1][i * 4 * QT_HD]);
+            }
         }
-    }
+    };
+    // ---- 0. K/V of the first key block in flight before anything else ----
+    stage(0, true, true);
 
     // ---- 1. query heads (and the new key/value) ----
     if (PREP) {
@@ -129,38 +151,38 @@ __global__ __launch_bounds__(QT_WG) void k_attn(QtAttnArgs a) {
         for (int i = tid; i < HPK * QT_HD; i += QT_WG)
             qs[i / QT_HD][i % QT_HD] = a.q[(g * HPK + i / QT_HD) * QT_HD + i % QT_HD];
     }
-    __syncthreads();
+    __syncthreads();   // (also: every wave's LDS copies of the first block have landed)
 
-    // ---- 2. scores: 16 lanes per key (8 dims each), 4 keys per wave per step ----
+    // ---- 2. scores: 16 lanes per key (8 dims each), keys u*16 + wave*4 + pg of a block ----
     float qv[HPK][8];
 #pragma unroll
     for (int h = 0; h < HPK; h++)
 #pragma unroll
         for (int e = 0; e < 8; e++) qv[h][e] = qs[h][sub * 8 + e];
-
-    for (int blk = 0; blk < n; blk += 64) {
-        uint4 kw[4];
-#pragma unroll
-        for (int u = 0; u < 4; u++) {
-            const int jj = blk + wave * 4 + pg + 16 * u;
-            if (blk == 0) kw[u] = kpre[u];
-            else kw[u] = (jj < n) ? qt_ld_kv(Kg, a.pos_stride, j0 + jj, sub) : make_uint4(0, 0, 0, 0);
-            if (append && j0 + jj == pos) kw[u] = *reinterpret_cast<const uint4 *>(knew + sub * 8);
+    for (int kb = 0; kb < n; kb += QT_KVB) {
+        if (kb > 0) {   // chunks longer than one block (caches beyond G*QT_KVB keys)
+            __syncthreads();
+            stage(kb, true, false);
+            __syncthreads();
         }
+        const int nk = min(QT_KVB, n - kb);
 #pragma unroll
-        for (int u = 0; u < 4; u++) {
-            const uint32_t w4[4] = {kw[u].x, kw[u].y, kw[u].z, kw[u].w};
+        for (int u = 0; u < (BATCH ? QT_KVB / 16 : 1 << 20); u++) {
+            if (!BATCH && u * 16 >= nk) break;
+            const int jl = u * 16 + wave * 4 + pg, jj = kb + jl;
+            const uint4 kw = (PREP && j0 + jj == pos) ? *reinterpret_cast<const uint4 *>(knew + sub * 8)
+                                                      : *reinterpret_cast<const uint4 *>(&s_kv[0][jl * QT_HD + sub * 8]);
+            const uint32_t w4[4] = {kw.x, kw.y, kw.z, kw.w};
             float kf[8];
 #pragma unroll
             for (int m = 0; m < 4; m++) { kf[2 * m] = bf_lo(w4[m]); kf[2 * m + 1] = bf_hi(w4[m]); }
-            const int jj = blk + wave * 4 + pg + 16 * u;
 #pragma unroll
             for (int h = 0; h < HPK; h++) {
                 float s = 0.f;
 #pragma unroll
                 for (int e = 0; e < 8; e++) s = fmaf(qv[h][e], kf[e], s);
                 s = group_sum<16>(s);
-                if (sub == 0 && jj < n) sc[h][jj] = s * a.scale;
+                if (sub == 0 && jl < nk) sc[h][jj] = s * a.scale;
             }
         }
     }
@@ -182,34 +204,36 @@ __global__ __launch_bounds__(QT_WG) void k_attn(QtAttnArgs a) {
     }
     __syncthreads();
 
-    // ---- 4. o = sum_j p_j v_j ----
+    // ---- 4. o = sum_j p_j v_j (same keys per lane, same order, as the scores) ----
     float o[HPK][8];
 #pragma unroll
     for (int h = 0; h < HPK; h++)
 #pragma unroll
         for (int e = 0; e < 8; e++) o[h][e] = 0.f;
-    for (int blk = 0; blk < n; blk += 64) {
-        uint4 vw[4];
-#pragma unroll
-        for (int u = 0; u < 4; u++) {
-            const int jj = blk + wave * 4 + pg + 16 * u;
-            if (blk == 0) vw[u] = vpre[u];
-            else vw[u] = (jj < n) ? qt_ld_kv(Vg, a.pos_stride, j0 + jj, sub) : make_uint4(0, 0, 0, 0);
-            if (append && j0 + jj == pos) vw[u] = *reinterpret_cast<const uint4 *>(vnew + sub * 8);
+    for (int kb = 0; kb < n; kb += QT_KVB) {
+        if (kb > 0) {
+            __syncthreads();
+            stage(kb, false, true);
+            __syncthreads();
         }
+        const int nk = min(QT_KVB, n - kb);
 #pragma unroll
-        for (int u = 0; u < 4; u++) {
-            const int jj = blk + wave * 4 + pg + 16 * u;
-            if (jj < n) {
-                const uint32_t w4[4] = {vw[u].x, vw[u].y, vw[u].z, vw[u].w};
+        for (int u = 0; u < (BATCH ? QT_KVB / 16 : 1 << 20); u++) {
+            if (!BATCH && u * 16 >= nk) break;
+            const int jl = u * 16 + wave * 4 + pg, jj = kb + jl;
+            const bool ok = jl < nk;
+            if (BATCH || ok) {
+                const uint4 vw = (PREP && j0 + jj == pos) ? *reinterpret_cast<const uint4 *>(vnew + sub * 8)
+                                                          : *reinterpret_cast<const uint4 *>(&s_kv[1][jl * QT_HD + sub * 8]);
+                const uint32_t w4[4] = {vw.x, vw.y, vw.z, vw.w};
                 float vf[8];
 #pragma unroll
                 for (int m = 0; m < 4; m++) { vf[2 * m] = bf_lo(w4[m]); vf[2 * m + 1] = bf_hi(w4[m]); }
 #pragma unroll
                 for (int h = 0; h < HPK; h++) {
-                    const float p = sc[h][jj];
+                    const float p = ok ? sc[h][min(jj, QT_CH_MAX - 1)] : 0.f;
 #pragma unroll
-                    for (int e = 0; e < 8; e++) o[h][e] = fmaf(p, vf[e], o[h][e]);
+                    for (int e = 0; e < 8; e++) o[h][e] = ok ? fmaf(p, vf[e], o[h][e]) : o[h][e];
                 }
             }
         }
@@ -240,7 +264,6 @@ __global__ __launch_bounds__(QT_WG) void k_attn(QtAttnArgs a) {
         }
         return;
     }
-    constexpr int PS = 2 + QT_HD;
     // Publish the partial with agent-scope (L2-bypassing) stores, wait for them to be
     // acknowledged, then count arrivals with a relaxed device-scope atomic.  This avoids
     // __threadfence(), whose L2 write-back + invalidate on every XCD costs ~17 us for a
@@ -258,8 +281,10 @@ __global__ __launch_bounds__(QT_WG) void k_attn(QtAttnArgs a) {
                      (unsigned)(nch - 1));
     __syncthreads();
     if (!last_flag) return;
-    // Merge: all chunk partials into LDS with one parallel load round, then each half-wave
-    // merges one (head, dim) output over the chunks (softmax_merge32, lane = chunk).
+    // Merge: all chunk partials into LDS (the K/V buffer, free now) with one parallel
+    // load round, then each half-wave merges one (head, dim) output over the chunks
+    // (softmax_merge32, lane = chunk).
+    float *mpart = reinterpret_cast<float *>(s_kvbuf);
     const float *gp = a.part + (size_t)g * G * HPK * PS;
     {
         // all loads issued before any is consumed (one round trip, not one per element)
@@ -273,7 +298,23 @@ __global__ __launch_bounds__(QT_WG) void k_attn(QtAttnArgs a) {
             if (tid + k * QT_WG < np) mpart[tid + k * QT_WG] = t[k];
     }
     __syncthreads();
-    {
+    if (BATCH) {
+        // one output (head h, dim d) per thread: M = max_c m_c, f_c = e^(m_c - M),
+        // out = sum_c o_c[d] f_c / sum_c l_c f_c, chunks in order
+        for (int i = tid; i < HPK * QT_HD; i += QT_WG) {
+            const int h = i / QT_HD, d = i % QT_HD;
+            float M = -INFINITY;
+            for (int cc = 0; cc < nch; cc++) M = fmaxf(M, mpart[(cc * HPK + h) * PS]);
+            float Lsum = 0.f, V = 0.f;
+            for (int cc = 0; cc < nch; cc++) {
+                const float *pr = mpart + (size_t)(cc * HPK + h) * PS;
+                const float f = expf(pr[0] - M);
+                Lsum = fmaf(pr[1], f, Lsum);
+                V = fmaf(pr[2 + d], f, V);
+            }
+            a.out[(g * HPK + h) * QT_HD + d] = V * (1.0f / Lsum);
+        }
+    } else {
         const int half = lane >> 5, cc = lane & 31;
         const bool valid = cc < nch;
         for (int i = wave * 2 + half; i < HPK * QT_HD; i += QT_WAVES * 2) {
@@ -291,10 +332,12 @@ static hipError_t attn_launch(const QtAttnArgs &a, int prep, int head_dim, int G
     if (G <= 0 || G > QT_ATT_G || nz <= 0 || nz > 65535) return hipErrorInvalidValue;
     if (!prep && (a.Lval <= 0 || a.Lval > G * QT_CH_MAX)) return hipErrorInvalidValue;
     const int hpk = a.n_heads / a.n_kv;
-    dim3 grid(G, a.n_kv, nz);
+    const bool batch = a.min_chunk > 0;
+    const dim3 grid = batch ? dim3(a.n_kv, nz, G) : dim3(G, a.n_kv, nz);
 #define QT_ATT_CASE(H) \
-    if (prep) hipLaunchKernelGGL((k_attn<H, true>), grid, dim3(QT_WG), 0, st, a); \
-    else hipLaunchKernelGGL((k_attn<H, false>), grid, dim3(QT_WG), 0, st, a);
+    if (batch && prep) hipLaunchKernelGGL((k_attn<H, true, true>), grid, dim3(QT_WG), 0, st, a); \
+    else if (prep) hipLaunchKernelGGL((k_attn<H, true, false>), grid, dim3(QT_WG), 0, st, a); \
+    else hipLaunchKernelGGL((k_attn<H, false, false>), grid, dim3(QT_WG), 0, st, a);
     if (hpk == 1) { QT_ATT_CASE(1) }
     else if (hpk == 2) { QT_ATT_CASE(2) }
     else if (hpk == 4) { QT_ATT_CASE(4) }
@@ -314,13 +357,16 @@ extern "C" hipError_t qt_launch_attn(int prep, const float *q, const float *qn, 
     a.K = K; a.V = V; a.pos_stride = pos_stride; a.head_stride = head_stride;
     a.n_heads = n_heads; a.n_kv = n_kv; a.scale = scale; a.part = part; a.cnt = cnt; a.out = out;
     a.q_bs = a.kv_bs = a.out_bs = a.part_bs = 0;
+    a.min_chunk = 0;
     return attn_launch(a, prep, head_dim, G, 1, st);
 }
 
 // B independent streams in one launch (the batched step): stream z uses q + z*q_bs,
 // K/V + z*kv_bs (its own cache), position d_pos[z], partials part + z*part_bs, counters
 // cnt + z*n_kv, output out + z*out_bs.  Ragged positions are fine: each stream's chunks
-// follow its own length.
+// follow its own length.  Chunks hold at least QT_KVB keys (one LDS block), so a
+// workgroup moves 64 KiB of K/V per HBM round trip and short streams use few
+// workgroups; throughput, not single-stream latency, is what the batch needs.
 extern "C" hipError_t qt_launch_attn_b(const float *q, long long q_bs, const float *qn, const float *kn,
                                        const float *rc, const float *rs, float eps, const int *d_pos,
                                        uint16_t *K, uint16_t *V, long long kv_bs, long long pos_stride,
@@ -332,6 +378,7 @@ extern "C" hipError_t qt_launch_attn_b(const float *q, long long q_bs, const flo
     a.K = K; a.V = V; a.pos_stride = pos_stride; a.head_stride = head_stride;
     a.n_heads = n_heads; a.n_kv = n_kv; a.scale = scale; a.part = part; a.cnt = cnt; a.out = out;
     a.q_bs = q_bs; a.kv_bs = kv_bs; a.out_bs = out_bs; a.part_bs = part_bs;
+    a.min_chunk = QT_KVB;
     return attn_launch(a, 1, head_dim, G, B, st);
 }
 

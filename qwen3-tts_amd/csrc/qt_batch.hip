@@ -37,18 +37,43 @@ typedef int qt_v4i __attribute__((ext_vector_type(4)));
 #define QT_BG_MAXW 16          // waves per workgroup at most (K <= 8192)
 
 // ---- activation pieces ---------------------------------------------------------------
-// One workgroup (256 threads) per padded stream b < Bp.  x row b at x + b*xstride;
-// norm_w != NULL: the pieces are of RMSNorm(x)*w (qwen_tts_kernels.c:292-382), else of x.
-// Padding streams (b >= B) write zero pieces.
-__global__ __launch_bounds__(256) void k_bpieces(const float *x, long long xstride, const float *norm_w, float eps,
-                                                 int K, int B, int Bp, int8_t *P, float *S) {
-    __shared__ float red[QT_WAVES];
-    __shared__ float s_max[QT_WAVES];
-    const int b = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+// One 1024-thread workgroup per padded stream b < Bp; each thread holds <= 8 elements in
+// registers (one load round), two block reductions (sum of squares, max).  x row b at
+// x + b*xstride; norm_w != NULL: the pieces are of RMSNorm(x)*w
+// (qwen_tts_kernels.c:292-382), else of x.  Padding streams (b >= B) write zero pieces.
+#define QT_BP_T 1024
+#define QT_BP_E 8              // elements per thread: K <= 8192
+__device__ __forceinline__ float bp_block_sum(float v, float *red) {
+    v = group_sum<64>(v);
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    __syncthreads();
+    if (lane == 0) red[wave] = v;
+    __syncthreads();
+    float t = 0.f;
+#pragma unroll
+    for (int i = 0; i < QT_BP_T / 64; i++) t += red[i];
+    return t;
+}
+__device__ __forceinline__ float bp_block_max(float v, float *red) {
+    v = group_max<64>(v);
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    __syncthreads();
+    if (lane == 0) red[wave] = v;
+    __syncthreads();
+    float t = 0.f;
+#pragma unroll
+    for (int i = 0; i < QT_BP_T / 64; i++) t = fmaxf(t, red[i]);
+    return t;
+}
+
+__global__ __launch_bounds__(QT_BP_T) void k_bpieces(const float *x, long long xstride, const float *norm_w, float eps,
+                                                     int K, int B, int Bp, int8_t *P, float *S) {
+    __shared__ float red[QT_BP_T / 64];
+    const int b = blockIdx.x, tid = threadIdx.x;
     const int col1 = b, col2 = Bp + b, col3 = 2 * Bp + b;
     const size_t cs = (size_t)3 * Bp * 64;      // bytes per k-block of all columns
     if (b >= B) {
-        for (int k = tid; k < K; k += 256) {
+        for (int k = tid; k < K; k += QT_BP_T) {
             const size_t o = (size_t)(k >> 6) * cs + (k & 63);
             P[o + (size_t)col1 * 64] = 0; P[o + (size_t)col2 * 64] = 0; P[o + (size_t)col3 * 64] = 0;
         }
@@ -56,34 +81,37 @@ __global__ __launch_bounds__(256) void k_bpieces(const float *x, long long xstri
         return;
     }
     const float *xb = x + (size_t)b * xstride;
-    float inv = 1.0f;
+    float v[QT_BP_E], w[QT_BP_E];
+#pragma unroll
+    for (int e = 0; e < QT_BP_E; e++) {
+        const int k = tid + e * QT_BP_T;
+        v[e] = k < K ? xb[k] : 0.f;
+        w[e] = (norm_w && k < K) ? norm_w[k] : 1.f;
+    }
     if (norm_w) {
         float ss = 0.f;
-        for (int k = tid; k < K; k += 256) ss = fmaf(xb[k], xb[k], ss);
-        ss = group_sum<64>(ss);
-        if (lane == 0) red[wave] = ss;
-        __syncthreads();
-        ss = red[0] + red[1] + red[2] + red[3];
-        inv = 1.0f / sqrtf(ss / (float)K + eps);
+#pragma unroll
+        for (int e = 0; e < QT_BP_E; e++) ss = fmaf(v[e], v[e], ss);
+        ss = bp_block_sum(ss, red);
+        const float inv = 1.0f / sqrtf(ss / (float)K + eps);
+#pragma unroll
+        for (int e = 0; e < QT_BP_E; e++) v[e] = (v[e] * inv) * w[e];
     }
     float m = 0.f;
-    for (int k = tid; k < K; k += 256) {
-        const float v = norm_w ? (xb[k] * inv) * norm_w[k] : xb[k];
-        m = fmaxf(m, fabsf(v));
-    }
-    m = group_max<64>(m);
-    if (lane == 0) s_max[wave] = m;
-    __syncthreads();
-    m = fmaxf(fmaxf(s_max[0], s_max[1]), fmaxf(s_max[2], s_max[3]));
+#pragma unroll
+    for (int e = 0; e < QT_BP_E; e++) m = fmaxf(m, fabsf(v[e]));
+    m = bp_block_max(m, red);
     // s = 2^(e-6) with 2^e <= m < 2^(e+1); m == 0 (or not finite) -> all pieces zero
     const bool ok = m > 0.f && m <= 3.0e38f;
-    const int e = ok ? ilogbf(m) : 0;
-    const float sc = ok ? ldexpf(1.0f, e - 6) : 0.f, isc = ok ? ldexpf(1.0f, 6 - e) : 0.f;
-    for (int k = tid; k < K; k += 256) {
-        const float v = norm_w ? (xb[k] * inv) * norm_w[k] : xb[k];
+    const int ex = ok ? ilogbf(m) : 0;
+    const float sc = ok ? ldexpf(1.0f, ex - 6) : 0.f, isc = ok ? ldexpf(1.0f, 6 - ex) : 0.f;
+#pragma unroll
+    for (int e = 0; e < QT_BP_E; e++) {
+        const int k = tid + e * QT_BP_T;
+        if (k >= K) break;
         int q1 = 0, q2 = 0, q3 = 0;
         if (ok) {
-            const float y = v * isc;             // |y| < 128, exact
+            const float y = v[e] * isc;          // |y| < 128, exact
             const float f1 = floorf(y);
             const float r1 = (y - f1) * 128.0f;  // [0, 128), exact
             const float f2 = floorf(r1);
@@ -127,18 +155,25 @@ __global__ __launch_bounds__(QT_BG_MAXW * 64) void k_bgemm_i8(QtBgArgs a) {
 #pragma unroll
     for (int t = 0; t < NT; t++) acc[t] = qt_v4i{0, 0, 0, 0};
     const int kw0 = wave * QT_BG_KW;
-    const int nkb = max(0, min(QT_BG_KW, a.K - kw0)) >> 6;
-    for (int kb = 0; kb < nkb; kb++) {
-        const int k = kw0 + kb * 64;
-        const uint4 wa = *reinterpret_cast<const uint4 *>(wr + k + grp * 16);
-        const qt_v4i A = qt_v4i{(int)(wa.x ^ 0x80808080u), (int)(wa.y ^ 0x80808080u), (int)(wa.z ^ 0x80808080u),
-                                (int)(wa.w ^ 0x80808080u)};
-        const int8_t *pb = a.P + (size_t)(k >> 6) * cs + (size_t)m * 64 + grp * 16;
+    const int nkb = max(0, min(QT_BG_KW, a.K - kw0)) >> 6;   // wave-uniform
+    // the wave's weights (8 k-blocks of 16 rows x 64 bytes) all in flight at once
+    uint4 wa[QT_BG_KW / 64];
 #pragma unroll
-        for (int t = 0; t < NT; t++) {
-            const uint4 pv = *reinterpret_cast<const uint4 *>(pb + (size_t)t * 16 * 64);
-            const qt_v4i Bv = qt_v4i{(int)pv.x, (int)pv.y, (int)pv.z, (int)pv.w};
-            acc[t] = __builtin_amdgcn_mfma_i32_16x16x64_i8(A, Bv, acc[t], 0, 0, 0);
+    for (int kb = 0; kb < QT_BG_KW / 64; kb++)
+        wa[kb] = kb < nkb ? *reinterpret_cast<const uint4 *>(wr + kw0 + kb * 64 + grp * 16) : make_uint4(0, 0, 0, 0);
+#pragma unroll
+    for (int kb = 0; kb < QT_BG_KW / 64; kb++) {
+        if (kb < nkb) {
+            const int k = kw0 + kb * 64;
+            const qt_v4i A = qt_v4i{(int)(wa[kb].x ^ 0x80808080u), (int)(wa[kb].y ^ 0x80808080u),
+                                    (int)(wa[kb].z ^ 0x80808080u), (int)(wa[kb].w ^ 0x80808080u)};
+            const int8_t *pb = a.P + (size_t)(k >> 6) * cs + (size_t)m * 64 + grp * 16;
+#pragma unroll
+            for (int t = 0; t < NT; t++) {
+                const uint4 pv = *reinterpret_cast<const uint4 *>(pb + (size_t)t * 16 * 64);
+                const qt_v4i Bv = qt_v4i{(int)pv.x, (int)pv.y, (int)pv.z, (int)pv.w};
+                acc[t] = __builtin_amdgcn_mfma_i32_16x16x64_i8(A, Bv, acc[t], 0, 0, 0);
+            }
         }
     }
     // sum the waves' tiles (exact; wave 0 stores, the others add in wave order)
@@ -176,7 +211,8 @@ __global__ __launch_bounds__(QT_BG_MAXW * 64) void k_bgemm_i8(QtBgArgs a) {
 extern "C" hipError_t qt_launch_bpieces(const float *x, long long xstride, const float *norm_w, float eps, int K, int B,
                                         int Bp, int8_t *P, float *S, hipStream_t st) {
     if (K <= 0 || (K & 63) || B <= 0 || Bp < B || (Bp & 15) || Bp > 64) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(k_bpieces, dim3(Bp), dim3(256), 0, st, x, xstride, norm_w, eps, K, B, Bp, P, S);
+    if (K > QT_BP_T * QT_BP_E) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_bpieces, dim3(Bp), dim3(QT_BP_T), 0, st, x, xstride, norm_w, eps, K, B, Bp, P, S);
     return hipGetLastError();
 }
 
@@ -201,5 +237,17 @@ extern "C" hipError_t qt_launch_bgemm_i8(int epi, const uint8_t *w, const float 
     else if (Bp == 64) { QT_BG_CASE(12) }
     else return hipErrorInvalidValue;
 #undef QT_BG_CASE
+    return hipGetLastError();
+}
+
+// pos[b] += 1 for b < n: the batched step's device positions advance after each step,
+// so replays of a captured step walk every stream forward by one position.
+__global__ void k_advance_pos(int *pos, int n) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) pos[i] += 1;
+}
+extern "C" hipError_t qt_launch_advance_pos(int *pos, int n, hipStream_t st) {
+    if (n <= 0) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_advance_pos, dim3((n + 63) / 64), dim3(64), 0, st, pos, n);
     return hipGetLastError();
 }

@@ -894,6 +894,7 @@ typedef struct {
     int *d_pos;                /* [B] */
     float *h_io; int *h_pos;   /* pinned */
     hipGraphExec_t exec; int graph_ready;
+    int last_async;            /* steps replayed since the last batch_step */
     int dead;
 } batch_t;
 
@@ -978,6 +979,7 @@ static hipError_t batch_body(void *arg) {
         if ((e = batch_proj(bt, &s->gu[l], QT_EPI_SWIGLU, s->post_norm[l], bt->x, H, bt->h, F))) return e;
         if ((e = batch_proj(bt, &s->dn[l], QT_EPI_RESID, NULL, bt->h, F, bt->x, H))) return e;
     }
+    if ((e = qt_launch_advance_pos(bt->d_pos, bt->B, bt->st))) return e;
     if (bt->is_cp) return hipSuccess;
     if ((e = hipMemcpyAsync(bt->hid, bt->x, (size_t)bt->B * H * sizeof(float), hipMemcpyDeviceToDevice, bt->st))) return e;
     return qt_launch_rmsnorm_rows(bt->hid, s->final_norm, bt->B, H, s->eps, bt->st);
@@ -994,6 +996,7 @@ static int batch_step_impl(batch_t *bt, const float *in, const int *pos_arr, flo
             "stream %d: pos %d out of range (kv_max %d, rope %d)", b, pos_arr[b], bt->kv_max, s->rope_len);
     memcpy(bt->h_io, in, (size_t)B * H * sizeof(float));
     memcpy(bt->h_pos, pos_arr, (size_t)B * sizeof(int));
+    bt->last_async = 0;
     HCK(hipMemcpyAsync(bt->x, bt->h_io, (size_t)B * H * sizeof(float), hipMemcpyHostToDevice, bt->st));
     HCK(hipMemcpyAsync(bt->d_pos, bt->h_pos, (size_t)B * sizeof(int), hipMemcpyHostToDevice, bt->st));
     if (graphs_enabled()) {
@@ -1068,11 +1071,17 @@ int qwen_hip_talker_batch_download_slot(void *state, int b, uint16_t *kv_k, uint
 fail:
     return -1;
 }
-/* Benchmark entry: n batched steps on the device state of the last batch_step call
- * (same inputs, positions unchanged: every step rewrites the same KV rows), no sync. */
+/* Benchmark entry: n more batched steps replaying the last batch_step's inputs, every
+ * stream advancing one position per step on the device, no host sync.  The caller
+ * keeps max(pos) + n within kv_max. */
 int qwen_hip_talker_batch_step_async(void *state, int n_steps) {
     batch_t *bt = (batch_t *)state;
     if (!bt || bt->dead || !bt->graph_ready) { SETERR("batch state not initialised by a batch_step call"); return -1; }
+    int maxp = 0;
+    for (int b = 0; b < bt->B; b++) if (bt->h_pos[b] > maxp) maxp = bt->h_pos[b];
+    bt->last_async += n_steps;
+    REQ(maxp + bt->last_async < bt->kv_max && maxp + bt->last_async < bt->s->rope_len,
+        "replayed positions would pass kv_max %d", bt->kv_max);
     for (int i = 0; i < n_steps; i++) HCK(hipGraphLaunch(bt->exec, bt->st));
     return 0;
 fail:
