@@ -161,20 +161,27 @@ __global__ __launch_bounds__(QT_BG_MAXW * 64) void k_bgemm_i8(QtBgArgs a) {
 #pragma unroll
     for (int kb = 0; kb < QT_BG_KW / 64; kb++)
         wa[kb] = kb < nkb ? *reinterpret_cast<const uint4 *>(wr + kw0 + kb * 64 + grp * 16) : make_uint4(0, 0, 0, 0);
+    // B fragments: every load of a full 512-column slice is unconditional, so the
+    // compiler can issue them ahead of the MFMAs that consume them
+    auto block = [&](int kb) {
+        const int k = kw0 + kb * 64;
+        const qt_v4i A = qt_v4i{(int)(wa[kb].x ^ 0x80808080u), (int)(wa[kb].y ^ 0x80808080u),
+                                (int)(wa[kb].z ^ 0x80808080u), (int)(wa[kb].w ^ 0x80808080u)};
+        const int8_t *pb = a.P + (size_t)(k >> 6) * cs + (size_t)m * 64 + grp * 16;
 #pragma unroll
-    for (int kb = 0; kb < QT_BG_KW / 64; kb++) {
-        if (kb < nkb) {
-            const int k = kw0 + kb * 64;
-            const qt_v4i A = qt_v4i{(int)(wa[kb].x ^ 0x80808080u), (int)(wa[kb].y ^ 0x80808080u),
-                                    (int)(wa[kb].z ^ 0x80808080u), (int)(wa[kb].w ^ 0x80808080u)};
-            const int8_t *pb = a.P + (size_t)(k >> 6) * cs + (size_t)m * 64 + grp * 16;
-#pragma unroll
-            for (int t = 0; t < NT; t++) {
-                const uint4 pv = *reinterpret_cast<const uint4 *>(pb + (size_t)t * 16 * 64);
-                const qt_v4i Bv = qt_v4i{(int)pv.x, (int)pv.y, (int)pv.z, (int)pv.w};
-                acc[t] = __builtin_amdgcn_mfma_i32_16x16x64_i8(A, Bv, acc[t], 0, 0, 0);
-            }
+        for (int t = 0; t < NT; t++) {
+            const uint4 pv = *reinterpret_cast<const uint4 *>(pb + (size_t)t * 16 * 64);
+            const qt_v4i Bv = qt_v4i{(int)pv.x, (int)pv.y, (int)pv.z, (int)pv.w};
+            acc[t] = __builtin_amdgcn_mfma_i32_16x16x64_i8(A, Bv, acc[t], 0, 0, 0);
         }
+    };
+    if (nkb == QT_BG_KW / 64) {
+#pragma unroll
+        for (int kb = 0; kb < QT_BG_KW / 64; kb++) block(kb);
+    } else {
+#pragma unroll
+        for (int kb = 0; kb < QT_BG_KW / 64; kb++)
+            if (kb < nkb) block(kb);
     }
     // sum the waves' tiles (exact; wave 0 stores, the others add in wave order)
     for (int w = 0; w < nw; w++) {
