@@ -44,8 +44,7 @@
 
 namespace ps {
 constexpr int NB = 256;          // workgroups (one per CU)
-constexpr int NW = 4;            // waves per workgroup
-constexpr int NT = NW * 64;      // threads per workgroup
+constexpr int NWB = 4;           // waves that run the attention chunk (B) and the merge (M)
 constexpr int HD = 128, NH = 16, NKV = 8, HPK = 2, QD = NH * HD, KVD = NKV * HD, QKVR = QD + 2 * KVD;
 constexpr int G = NB / NKV;      // attention chunks per kv head (32)
 constexpr int CHMAX = 256;       // keys per chunk at most (kv_max <= G * CHMAX)
@@ -142,12 +141,12 @@ __device__ unsigned long long ps_trace[TRACE_PH * 4 * NB];
 #define PS_TRACE_FLUSH()                                                                       \
     do {                                                                                       \
         __syncthreads();                                                                       \
-        for (int i_ = threadIdx.x; i_ < TRACE_PH * 4; i_ += NT)                                \
+        for (int i_ = threadIdx.x; i_ < TRACE_PH * 4; i_ += (int)blockDim.x)                   \
             ps_trace[(size_t)i_ * NB + blockIdx.x] = s_trace[i_];                              \
     } while (0)
 #define PS_TRACE_CLEAR()                                                                       \
     do {                                                                                       \
-        for (int i_ = threadIdx.x; i_ < TRACE_PH * 4; i_ += NT) s_trace[i_] = 0;               \
+        for (int i_ = threadIdx.x; i_ < TRACE_PH * 4; i_ += (int)blockDim.x) s_trace[i_] = 0;  \
     } while (0)
 #else
 #define PS_TRACE_LDS
@@ -164,7 +163,7 @@ __device__ unsigned long long ps_trace[TRACE_PH * 4 * NB];
 // (Issuing the next phase's weight loads between the first reads and their check, so
 // the issue overlaps the first round trip, was measured 30 % slower per step than
 // issuing them before the gather.)
-template <int K, typename AddrF>
+template <int K, int NT, typename AddrF>
 __device__ __forceinline__ void gather(int n, AddrF addr, float *dst, unsigned tag, int *err) {
     const int tid = threadIdx.x;
     unsigned long long v[K];
@@ -279,31 +278,21 @@ __device__ __forceinline__ void tile_dot(const Tile<PREC, COLS, NR> &t, const fl
     for (int r = 0; r < NR; r++) acc[r] = group_sum<64>(s[r]);
 }
 
-// Norm gains of the EPC-element chunk this thread normalises (thread tid < COLS/EPC
-// owns chunk tid), loaded one phase ahead.
-template <int PREC>
-struct GainCh {
-    static constexpr int EPC = Epc<PREC>::v;
-    float g[EPC];
-    __device__ __forceinline__ void load(const float *src, int cols) {
-        const int c = threadIdx.x;
-        src = uni(src);
-        if (c * EPC < cols) {
-#pragma unroll
-            for (int q = 0; q < EPC / 4; q++) {
-                const float4 t = ldg(reinterpret_cast<const float4 *>(src + c * EPC + 4 * q));
-                g[4 * q] = t.x; g[4 * q + 1] = t.y; g[4 * q + 2] = t.z; g[4 * q + 3] = t.w;
-            }
-        }
-    }
-};
+// Norm gains [cols] copied into LDS by global_load_lds (no registers held between the
+// phase that issues the copy and the phase that uses it), one phase ahead.
+template <int NW>
+__device__ __forceinline__ void load_gains(const float *src, int cols, float *dst) {
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    src = uni(src);
+    for (int i = wave; i * 256 < cols; i += NW) lds_copy16(src + i * 256 + lane * 4, dst + i * 256);
+}
 
 // xn = RMSNorm(x) * g into LDS, plus the int8 chunk sums xs.  The mean square is
 // accumulated exactly as k_mv does (lane l over chunks l + 64 j in element order, then
 // a wave butterfly), by every wave redundantly, so no extra barrier is needed; then
 // thread c normalises chunk c.  Ends with a workgroup barrier.
 template <int PREC, int COLS>
-__device__ __forceinline__ void stage_norm(const float *x, const GainCh<PREC> &gc, float eps, float *xn, float *xs) {
+__device__ __forceinline__ void stage_norm(const float *x, const float *gain, float eps, float *xn, float *xs) {
     constexpr int EPC = Epc<PREC>::v, CPL = COLS / (EPC * 64);
     const int lane = threadIdx.x & 63, c = threadIdx.x;
     float ss = 0.f;
@@ -320,7 +309,7 @@ __device__ __forceinline__ void stage_norm(const float *x, const GainCh<PREC> &g
         float sum = 0.f;
 #pragma unroll
         for (int e = 0; e < EPC; e++) {
-            const float v = (x[c * EPC + e] * inv) * gc.g[e];
+            const float v = (x[c * EPC + e] * inv) * gain[c * EPC + e];
             xn[c * EPC + e] = v;
             sum += v;
         }
@@ -330,7 +319,7 @@ __device__ __forceinline__ void stage_norm(const float *x, const GainCh<PREC> &g
 }
 
 // int8 chunk sums of an activation that is not normalised (inputs of W_o and W_dn)
-template <int PREC, int COLS>
+template <int PREC, int COLS, int NT>
 __device__ __forceinline__ void stage_sums(const float *x, float *xs) {
     constexpr int EPC = Epc<PREC>::v;
     if (PREC != QT_INT8) return;
@@ -360,18 +349,22 @@ template <int HPK>
 struct AttLds {
     float qs[HPK][HD];                 // rotated queries
     float sc[HPK][CHMAX];              // scores, then probabilities
-    float ored[NW][HPK][HD];           // per-wave P.V partial sums
+    float ored[NWB][HPK][HD];          // per-wave P.V partial sums
     float stat[HPK][2];                // chunk (max, sum) per head
     __attribute__((aligned(16))) uint16_t knew[HD], vnew[HD];   // key/value at pos (bf16)
 };
 
-template <int PREC, int H, int F>
-__global__ __launch_bounds__(256, 1) void k_pstep(Args a) {
-    constexpr int RPW_QKV = QKVR / (NB * NW);      // 4
-    constexpr int RPW_O = H / (NB * NW);           // 1 or 2
-    constexpr int RPW_GU = 2 * F / (NB * NW);      // 6 or 12
-    constexpr int RPW_DN = H / (NB * NW);          // 1 or 2
-    constexpr int RPW_HEAD = 3;                    // 3072-row codec head
+template <int PREC, int H, int F, int NW>
+__global__ __launch_bounds__(NW * 64, 1) void k_pstep(Args a) {
+    constexpr int NT = NW * 64;                    // threads per workgroup
+    constexpr int RPW_QKV = QKVR / (NB * NW);      // 4 (NW 4) or 2 (NW 8)
+    constexpr int RPW_O = H / (NB * NW);           // rows per wave of W_o
+    constexpr int RPW_GU = 2 * F / (NB * NW);      // rows per wave of gate|up
+    constexpr int RPW_DN = H / (NB * NW);          // rows per wave of W_down
+    constexpr int HEADR = 12;                      // 3072-row codec head: rows per workgroup
+    constexpr int RPW_HEAD = (HEADR + NW - 1) / NW;   // 3 (NW 4) or 2 (NW 8; waves 6, 7 idle)
+    static_assert(RPW_QKV >= 1 && RPW_O >= 1 && RPW_DN >= 1 && RPW_QKV * NB * NW == QKVR && RPW_O * NB * NW == H &&
+                  RPW_GU * NB * NW == 2 * F && RPW_DN * NB * NW == H, "row split");
     using TQKV = Tile<PREC, H, RPW_QKV>;
     using TO = Tile<PREC, QD, RPW_O>;
     constexpr int RGU = RPW_GU / 3;                // gate|up rows per piece (4 or 2)
@@ -383,7 +376,6 @@ __global__ __launch_bounds__(256, 1) void k_pstep(Args a) {
 
     __shared__ __align__(16) float s_x[H];       // layer input (kept for C's residual)
     __shared__ __align__(16) float s_xa[H];      // post-attention residual (kept for E)
-    __shared__ __align__(16) float s_in[F > QD ? F : QD];   // attn (C) / h (E) / slots (head)
     __shared__ __align__(16) float s_xn[H];      // RMS-normalised input of A / D / head
     __shared__ __align__(16) float s_xs[(F > QD ? F : QD) / 16];   // int8 chunk sums
     __shared__ __align__(16) float s_qkv[HPK * HD + 2 * HD];
@@ -392,6 +384,11 @@ __global__ __launch_bounds__(256, 1) void k_pstep(Args a) {
     __shared__ int wbest_i[NW];
     __shared__ Layer s_layers[MAXL];
     __shared__ __align__(16) uint16_t s_kv[2][KVB * HD];          // K, V rows of the attention chunk (B)
+    // attn (C) / h (E) / head slots share the K/V buffer: B is done with it before C
+    // writes, and the next layer's K/V copy is issued after E's dot products
+    static_assert((F > QD ? F : QD) * 4 <= 2 * KVB * HD * 2, "s_in fits the K/V buffer");
+    float *const s_in = reinterpret_cast<float *>(&s_kv[0][0]);
+    __shared__ __align__(16) float s_gain[2][H];                  // norm gains: [0] input (A), [1] post (D) / final
     PS_TRACE_LDS
 
     const int b = blockIdx.x, tid = threadIdx.x, lane = tid & 63;
@@ -414,7 +411,8 @@ __global__ __launch_bounds__(256, 1) void k_pstep(Args a) {
     const int rw_o = b * (RPW_O * NW) + wave * RPW_O;
     const int rw_gu = b * (RPW_GU * NW) + wave * RPW_GU;
     const int rw_dn = b * (RPW_DN * NW) + wave * RPW_DN;
-    const int rw_head = b * (RPW_HEAD * NW) + wave * RPW_HEAD;
+    const bool head_on = wave * RPW_HEAD < HEADR;
+    const int rw_head = b * HEADR + (head_on ? wave * RPW_HEAD : 0);
 
     PS_TRACE_CLEAR();
     // the layer table lives in LDS: reading it never waits behind weight loads
@@ -423,9 +421,8 @@ __global__ __launch_bounds__(256, 1) void k_pstep(Args a) {
     __syncthreads();
 
     TQKV tq;
-    GainCh<PREC> gq;
     tq.load(s_layers[0].w[0], s_layers[0].s[0], rw_qkv);
-    gq.load(s_layers[0].in_norm, H);
+    load_gains<NW>(s_layers[0].in_norm, H, s_gain[0]);
 
     for (int step = 0; step < a.n_steps; step++) {
         const int par = step & 1;
@@ -444,7 +441,6 @@ __global__ __launch_bounds__(256, 1) void k_pstep(Args a) {
         // RoPE row of pos.  Row pos is never loaded (its stale bits must not enter any
         // cache: it is written by this step's B and read from the next step on); lanes
         // past the chunk end load nothing.
-        static_assert(HPK * HD == NT, "one attention output per thread");
         float qn0 = 0.f, qn1 = 0.f, kn0 = 0.f, kn1 = 0.f, rc = 0.f, rsn = 0.f;
         auto stage_kv = [&](int lk, int kb, bool doK, bool doV) {
             const uint16_t *Kl = a.kc + (((size_t)lk * NKV + g) * a.kv_max) * HD;
@@ -474,7 +470,7 @@ __global__ __launch_bounds__(256, 1) void k_pstep(Args a) {
             // ---------------- A: q|k|v rows -----------------
             if (l > 0) {
                 const unsigned long long *src = ring.blk(par, l - 1) + R::OX;
-                gather<H / NT>(H, [&](int i) { return src + i; }, s_x, tag, a.err);
+                gather<H / NT, NT>(H, [&](int i) { return src + i; }, s_x, tag, a.err);
             } else {
                 for (int i = tid; i < H; i += NT)
                     s_x[i] = tok < 0 ? ldg(a.xin + i) : bf16f(ldg(a.emb + (size_t)tok * H + i));
@@ -482,7 +478,7 @@ __global__ __launch_bounds__(256, 1) void k_pstep(Args a) {
             }
             PS_MARK(ph, 0);
             {
-                stage_norm<PREC, H>(s_x, gq, a.eps, s_xn, s_xs);
+                stage_norm<PREC, H>(s_x, s_gain[0], a.eps, s_xn, s_xs);
                 PS_MARK(ph, 2);
                 float acc[RPW_QKV];
                 tile_dot<PREC, H, RPW_QKV>(tq, s_xn, s_xs, acc);
@@ -496,15 +492,14 @@ __global__ __launch_bounds__(256, 1) void k_pstep(Args a) {
             TO to;
             to.load(ly.w[1], ly.s[1], rw_o);
             TGU tg0, tg1, tg2;
-            GainCh<PREC> gp;
             tg0.load(ly.w[2], ly.s[2], rw_gu);
-            gp.load(ly.post_norm, H);
+            load_gains<NW>(ly.post_norm, H, s_gain[1]);
             PS_MARK(ph, 1); ph++;
 
             // ---------------- B: attention chunk -----------------
             {
                 const unsigned long long *src = blk + R::OQKV;
-                gather<2>(n > 0 ? HPK * HD + 2 * HD : 0, [&](int i) {
+                gather<2, NT>(n > 0 ? HPK * HD + 2 * HD : 0, [&](int i) {
                     return src + (i < HPK * HD ? g * HPK * HD + i
                                   : i < HPK * HD + HD ? QD + g * HD + (i - HPK * HD) : QD + KVD + g * HD + (i - HPK * HD - HD));
                 }, s_qkv, tag, a.err);
@@ -547,7 +542,12 @@ __global__ __launch_bounds__(256, 1) void k_pstep(Args a) {
                         __syncthreads();
                     }
                     const int nk = min(KVB, n - kb);
-                    for (int u = 0; u * 16 < nk; u++) {
+                    // unrolled over the block with masking (rows past nk read stale LDS and
+                    // are discarded), so the LDS reads of all keys are issued together;
+                    // waves 0..NWB-1 only (the key-to-lane map of the per-kernel twin)
+                    if (wave < NWB)
+#pragma unroll
+                    for (int u = 0; u < KVB / 16; u++) {
                         const int jl = u * 16 + wave * 4 + kpg, jj = kb + jl;
                         const uint4 kw = (j0 + jj == pos) ? *reinterpret_cast<const uint4 *>(att.knew + ksub * 8)
                                                           : *reinterpret_cast<const uint4 *>(&s_kv[0][jl * HD + ksub * 8]);
@@ -593,21 +593,22 @@ __global__ __launch_bounds__(256, 1) void k_pstep(Args a) {
                         __syncthreads();
                     }
                     const int nk = min(KVB, n - kb);
-                    for (int u = 0; u * 16 < nk; u++) {
+                    if (wave < NWB)
+#pragma unroll
+                    for (int u = 0; u < KVB / 16; u++) {
                         const int jl = u * 16 + wave * 4 + kpg, jj = kb + jl;
-                        if (jl < nk) {
-                            const uint4 vw = (j0 + jj == pos) ? *reinterpret_cast<const uint4 *>(att.vnew + ksub * 8)
-                                                              : *reinterpret_cast<const uint4 *>(&s_kv[1][jl * HD + ksub * 8]);
-                            const uint32_t w4[4] = {vw.x, vw.y, vw.z, vw.w};
-                            float vf[8];
+                        const bool ok = jl < nk;
+                        const uint4 vw = (j0 + jj == pos) ? *reinterpret_cast<const uint4 *>(att.vnew + ksub * 8)
+                                                          : *reinterpret_cast<const uint4 *>(&s_kv[1][jl * HD + ksub * 8]);
+                        const uint32_t w4[4] = {vw.x, vw.y, vw.z, vw.w};
+                        float vf[8];
 #pragma unroll
-                            for (int m = 0; m < 4; m++) { vf[2 * m] = bf_lo(w4[m]); vf[2 * m + 1] = bf_hi(w4[m]); }
+                        for (int m = 0; m < 4; m++) { vf[2 * m] = bf_lo(w4[m]); vf[2 * m + 1] = bf_hi(w4[m]); }
 #pragma unroll
-                            for (int h = 0; h < HPK; h++) {
-                                const float p = att.sc[h][jj];
+                        for (int h = 0; h < HPK; h++) {
+                            const float p = att.sc[h][min(jj, CHMAX - 1)];
 #pragma unroll
-                                for (int e = 0; e < 8; e++) o[h][e] = fmaf(p, vf[e], o[h][e]);
-                            }
+                            for (int e = 0; e < 8; e++) o[h][e] = ok ? fmaf(p, vf[e], o[h][e]) : o[h][e];
                         }
                     }
                 }
@@ -620,7 +621,7 @@ __global__ __launch_bounds__(256, 1) void k_pstep(Args a) {
                         v += __shfl_xor(v, 32, 64);
                         o[h][e] = v;
                     }
-                if (kpg == 0) {
+                if (kpg == 0 && wave < NWB) {
 #pragma unroll
                     for (int h = 0; h < HPK; h++)
 #pragma unroll
@@ -657,17 +658,19 @@ __global__ __launch_bounds__(256, 1) void k_pstep(Args a) {
                 const unsigned long long *gp = blk + R::OPART + (size_t)g * G * HPK * PS + hh * PS;
                 // element i: chunk i/10, field i%10 (0 max, 1 sum, 2.. dims d0..d0+7)
                 float *st = &att.sc[0][0];
-                gather<2>(nch * 10, [&](int i) {
+                gather<2, NT>(nch * 10, [&](int i) {
                     const int cc = i / 10, f = i % 10;
                     return gp + (size_t)cc * HPK * PS + (f < 2 ? f : 2 + d0 + (f - 2));
                 }, st, tag, a.err);
                 PS_MARK(ph, 0);
-                // half-wave per output dim d0 + dd, lane = chunk
-                const int half = lane >> 5, cc = lane & 31, dd = 2 * wave + half;
-                const bool valid = cc < nch;
-                const float r = softmax_merge32(valid ? st[cc * 10] : 0.f, valid ? st[cc * 10 + 1] : 0.f,
-                                                valid ? st[cc * 10 + 2 + dd] : 0.f, valid);
-                if (cc == 0) st_tag(blk + R::OATT + (2 * g + hh) * HD + d0 + dd, r, tag);
+                // half-wave per output dim d0 + dd, lane = chunk (waves 0..NWB-1)
+                if (wave < NWB) {
+                    const int half = lane >> 5, cc = lane & 31, dd = 2 * wave + half;
+                    const bool valid = cc < nch;
+                    const float r = softmax_merge32(valid ? st[cc * 10] : 0.f, valid ? st[cc * 10 + 1] : 0.f,
+                                                    valid ? st[cc * 10 + 2 + dd] : 0.f, valid);
+                    if (cc == 0) st_tag(blk + R::OATT + (2 * g + hh) * HD + d0 + dd, r, tag);
+                }
                 __syncthreads();   // st (the scores' LDS) is reused by the next B
             }
             tg2.load(ly.w[2], ly.s[2], rw_gu + 2 * RGU);
@@ -676,11 +679,11 @@ __global__ __launch_bounds__(256, 1) void k_pstep(Args a) {
             // ---------------- C: xa = x + W_o . attn -----------------
             {
                 const unsigned long long *src = blk + R::OATT;
-                gather<QD / NT>(QD, [&](int i) { return src + i; }, s_in, tag, a.err);
+                gather<QD / NT, NT>(QD, [&](int i) { return src + i; }, s_in, tag, a.err);
             }
             PS_MARK(ph, 0);
             {
-                stage_sums<PREC, QD>(s_in, s_xs);
+                stage_sums<PREC, QD, NT>(s_in, s_xs);
                 float acc[RPW_O];
                 tile_dot<PREC, QD, RPW_O>(to, s_in, s_xs, acc);
 #pragma unroll
@@ -697,11 +700,11 @@ __global__ __launch_bounds__(256, 1) void k_pstep(Args a) {
             // ---------------- D: h = SwiGLU(W_gu . RMSNorm(xa)) -----------------
             {
                 const unsigned long long *src = blk + R::OXA;
-                gather<H / NT>(H, [&](int i) { return src + i; }, s_xa, tag, a.err);
+                gather<H / NT, NT>(H, [&](int i) { return src + i; }, s_xa, tag, a.err);
             }
             PS_MARK(ph, 0);
             {
-                stage_norm<PREC, H>(s_xa, gp, a.eps, s_xn, s_xs);
+                stage_norm<PREC, H>(s_xa, s_gain[1], a.eps, s_xn, s_xs);
                 PS_MARK(ph, 2);
                 float acc[3][RGU];
                 tile_dot<PREC, H, RGU>(tg0, s_xn, s_xs, acc[0]);
@@ -723,18 +726,18 @@ __global__ __launch_bounds__(256, 1) void k_pstep(Args a) {
             PS_MARK(ph, 3);
             if (l + 1 < L) {
                 tq.load(s_layers[l + 1].w[0], s_layers[l + 1].s[0], rw_qkv);
-                gq.load(s_layers[l + 1].in_norm, H);
+                load_gains<NW>(s_layers[l + 1].in_norm, H, s_gain[0]);
             }
             PS_MARK(ph, 1); ph++;
 
             // ---------------- E: x' = xa + W_dn . h -----------------
             {
                 const unsigned long long *src = blk + R::OH;
-                gather<F / NT>(F, [&](int i) { return src + i; }, s_in, tag, a.err);
+                gather<F / NT, NT>(F, [&](int i) { return src + i; }, s_in, tag, a.err);
             }
             PS_MARK(ph, 0);
             {
-                stage_sums<PREC, F>(s_in, s_xs);
+                stage_sums<PREC, F, NT>(s_in, s_xs);
                 PS_MARK(ph, 2);
                 float acc[RPW_DN];
                 tile_dot<PREC, F, RPW_DN>(td, s_in, s_xs, acc);
@@ -755,10 +758,9 @@ __global__ __launch_bounds__(256, 1) void k_pstep(Args a) {
         if (!a.with_head) {
             // final norm of the residual -> hid, residual -> decx (workgroup 0)
             if (b == 0) {
-                GainCh<QT_BF16> gf;
-                gf.load(a.final_norm, H);
-                gather<H / NT>(H, [&](int i) { return xfin + i; }, s_x, tag, a.err);
-                stage_norm<QT_BF16, H>(s_x, gf, a.eps, s_xn, s_xs);
+                load_gains<NW>(a.final_norm, H, s_gain[1]);
+                gather<H / NT, NT>(H, [&](int i) { return xfin + i; }, s_x, tag, a.err);
+                stage_norm<QT_BF16, H>(s_x, s_gain[1], a.eps, s_xn, s_xs);
                 for (int i = tid; i < H; i += NT) { a.hid[i] = s_xn[i]; a.decx[i] = s_x[i]; }
             }
         } else {
@@ -766,12 +768,11 @@ __global__ __launch_bounds__(256, 1) void k_pstep(Args a) {
             // (its tile is loaded here rather than during the last layer: a tile carried
             // through the layer loop would hold its registers for the whole loop)
             THEAD th;
-            GainCh<QT_BF16> gf;
             th.load(a.head_w, nullptr, rw_head);
-            gf.load(a.final_norm, H);
-            gather<H / NT>(H, [&](int i) { return xfin + i; }, s_x, tag, a.err);
+            load_gains<NW>(a.final_norm, H, s_gain[1]);
+            gather<H / NT, NT>(H, [&](int i) { return xfin + i; }, s_x, tag, a.err);
             PS_MARK(ph, 0);
-            stage_norm<QT_BF16, H>(s_x, gf, a.eps, s_xn, s_xs);
+            stage_norm<QT_BF16, H>(s_x, s_gain[1], a.eps, s_xn, s_xs);
             if (last_step && b == 0)
                 for (int i = tid; i < H; i += NT) { a.hid[i] = s_xn[i]; a.decx[i] = s_x[i]; }
             float acc[RPW_HEAD];
@@ -781,6 +782,7 @@ __global__ __launch_bounds__(256, 1) void k_pstep(Args a) {
                 float bv = -INFINITY; int bi = 0x7FFFFFFF;
 #pragma unroll
                 for (int r = 0; r < RPW_HEAD; r++) {
+                    if (!head_on || wave * RPW_HEAD + r >= HEADR) break;
                     const int i = rw_head + r;
                     float v = fminf(fmaxf(acc[r], -100.0f), 100.0f);
                     if (i >= 2048 && i != 2150) v = -1e30f;
@@ -800,11 +802,11 @@ __global__ __launch_bounds__(256, 1) void k_pstep(Args a) {
             }
             if (!last_step) {
                 tq.load(s_layers[0].w[0], s_layers[0].s[0], rw_qkv);
-                gq.load(s_layers[0].in_norm, H);
+                load_gains<NW>(s_layers[0].in_norm, H, s_gain[0]);
             }
             PS_MARK(ph, 1); ph++;
             // global argmax over the 256 local winners (every workgroup, redundantly)
-            gather<2>(2 * NB, [&](int i) { return slots + i; }, s_in, tag, a.err);
+            gather<2, NT>(2 * NB, [&](int i) { return slots + i; }, s_in, tag, a.err);
             {
                 float bv = -INFINITY; int bi = 0x7FFFFFFF;
                 for (int i = tid; i < NB; i += NT) {
@@ -850,10 +852,13 @@ extern "C" hipError_t qt_pstep_trace_read(unsigned long long *out) {
 }
 #endif
 
+// 8 waves per workgroup (two per SIMD, so one wave's latency is covered by the other's
+// work) where the row split allows it (hidden 2048); 4 for hidden 1024.
 template <int PREC, int H, int F>
 static hipError_t ps_launch(const ps::Args &a, hipStream_t st) {
+    constexpr int NW = 4;
     void *args[] = {(void *)&a};
-    return hipLaunchCooperativeKernel((const void *)ps::k_pstep<PREC, H, F>, dim3(ps::NB), dim3(ps::NT), args, 0, st);
+    return hipLaunchCooperativeKernel((const void *)ps::k_pstep<PREC, H, F, NW>, dim3(ps::NB), dim3(NW * 64), args, 0, st);
 }
 
 extern "C" int qt_pstep_supported(int prec, int hidden, int inter, int n_heads, int n_kv, int head_dim, int kv_max) {
@@ -901,7 +906,7 @@ extern "C" hipError_t qt_launch_pstep(int prec, int hidden, const void *layers_d
     a.d_frame = d_frame; a.hist = hist; a.hist_len = hist_len;
     if (n_steps <= 0 || n_layers <= 0 || n_layers > ps::MAXL || kv_max > ps::G * ps::CHMAX) return hipErrorInvalidValue;
     if (!with_head && n_steps != 1) return hipErrorInvalidValue;   // without the head the next input is unknown
-    if (with_head && (vocab != ps::NB * ps::NW * 3 || !head_w || !emb || !d_frame || !hist || hist_len <= 0))
+    if (with_head && (vocab != ps::NB * 12 || !head_w || !emb || !d_frame || !hist || hist_len <= 0))
         return hipErrorInvalidValue;
     if (prec == QT_INT8 && hidden == 2048) return ps_launch<QT_INT8, 2048, 6144>(a, st);
     if (prec == QT_INT8 && hidden == 1024) return ps_launch<QT_INT8, 1024, 3072>(a, st);
