@@ -90,6 +90,10 @@ WORKLOADS = {
     "talker-1.7B-int4-b1-L2048": ("1.7B", "int4", 2048, 64),
     "talker-1.7B-int4-b1-L4096": ("1.7B", "int4", 4096, 64),
 }
+# Code Predictor frames: (shape, precision, default timed frames)
+CP_WORKLOADS = {
+    "cp-0.6B-bf16-frame": ("0.6B", "bf16", 500),
+}
 # batched workloads: (shape, precision, streams, KV length range, default timed steps)
 BATCH_WORKLOADS = {
     "talker-1.7B-int8-b32-ragged": ("1.7B", "int8", 32, (128, 4096), 16),
@@ -118,7 +122,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=None)
     ap.add_argument("--warmup", type=int, default=None)
-    ap.add_argument("--workload", default="talker-1.7B-int8-b1-L2048", choices=sorted(WORKLOADS) + sorted(BATCH_WORKLOADS))
+    ap.add_argument("--workload", default="talker-1.7B-int8-b1-L2048", choices=sorted(WORKLOADS) + sorted(BATCH_WORKLOADS) + sorted(CP_WORKLOADS))
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--kernel-launches", type=int, default=200)
@@ -134,6 +138,8 @@ def main():
     _pkg()
     if args.workload in BATCH_WORKLOADS:
         return bench_batch(args)
+    if args.workload in CP_WORKLOADS:
+        return bench_cp(args)
     from qwen3_tts_amd import hip, synth
     shape_name, prec, Lpre, dsteps = WORKLOADS[args.workload]
     K = args.steps or dsteps
@@ -316,6 +322,104 @@ def bench_batch(args):
         "cpu_baseline": None,
     }
     print(json.dumps(out), flush=True)
+
+
+def bench_cp(args):
+    """Config 4: the Code Predictor's per-frame work (qwen_cp_predict,
+    qwen_tts_code_predictor.c:926-1045) on the device: 16 passes of the 5-layer CP over a
+    fresh KV (positions 0..15) + 15 lm-head argmaxes + embedding gathers, captured once as
+    a hipGraph; frames replayed back to back on device-resident inputs (talker hidden =
+    RMS-normed N(0,1), code0 seeded).  value = ms per frame.  Algorithmic bytes per frame:
+    16 x (5 layers of weights + norms) + 15 x one 2048 x 1024 lm head (bf16); the CP's
+    157 MB of layer weights fit in the 256 MB MALL, so HBM traffic is lower than that."""
+    from qwen3_tts_amd import hip, synth
+    shape_name, prec, dframes = CP_WORKLOADS[args.workload]
+    K = args.steps or dframes
+    W = 20 if args.warmup is None else args.warmup
+    s = synth.SHAPES[shape_name]
+    t0 = time.time()
+    only = lambda n: n.startswith("talker.code_predictor.") or n == "talker.model.codec_embedding.weight"  # noqa: E731
+    tens = synth.generate(s, 0x5EED0001, 0.0, threads=int(os.environ.get("OMP_NUM_THREADS", "16")), only=only)
+    cp = hip.cp_from_tensors(tens, s, hip.PREC[prec])
+    log(f"[bench] cp: init {time.time() - t0:.1f}s")
+    rng = np.random.default_rng(0x5EED0002)
+    th = rng.standard_normal(s.hidden).astype(np.float32)
+    th /= np.sqrt((th ** 2).mean())
+    codes = cp.frame(th, int(rng.integers(0, 2048)))     # captures the frame graph
+    L = hip.lib()
+    ev = HipEvents()
+    stream = L.qwen_hip_cp_stream(cp.h)
+    hip.check(L.qwen_hip_cp_frame_async(cp.h, W), "cp warmup")
+    hip.check(L.qwen_hip_cp_sync(cp.h), "sync")
+    ev.device_sync()
+    a, b = ev.event(), ev.event()
+    ev.record(a, stream)
+    hip.check(L.qwen_hip_cp_frame_async(cp.h, K), "cp timed")
+    ev.record(b, stream)
+    ms_total = ev.elapsed_ms(a, b)
+    ev.device_sync()
+    ms = ms_total / K
+    per_layer = 0
+    for r, c in [(s.cp_heads * s.cp_head_dim + 2 * s.cp_kv_heads * s.cp_head_dim, s.cp_hidden),
+                 (s.cp_hidden, s.cp_heads * s.cp_head_dim), (2 * s.cp_inter, s.cp_hidden), (s.cp_hidden, s.cp_inter)]:
+        per_layer += r * c * 2
+    per_layer += (2 * s.cp_hidden + 2 * s.cp_head_dim) * 4
+    frame_bytes = 16 * s.cp_layers * per_layer + 15 * s.codebook * s.cp_hidden * 2
+    gbs = frame_bytes / (ms * 1e-3) / 1e9
+    log(f"[bench] cp: {ms * 1e3:.1f} us/frame, {gbs:.0f} GB/s algorithmic, codes[0:4] {list(codes[:4])}")
+    cp.free()
+    cpu = None
+    if not args.no_cpu_baseline:
+        try:
+            cpu = cpu_baseline_cp(s, prec, tens, th, args.cpu_seconds)
+        except Exception as ex:
+            log(f"[bench] cpu baseline failed: {ex}")
+            cpu = {"value": None, "unit": "ms/frame", "error": str(ex)[:200]}
+    out = {
+        "metric": "Talker ms/decode-step (0.6B/1.7B, bf16/int8/int4) + achieved HBM GB/s",
+        "value": round(ms, 4), "unit": "ms/frame", "n_gpus": 1, "steps": K, "warmup": W,
+        "ms_per_step": round(ms, 4), "higher_is_better": False, "scaling": "weak", "vs_baseline": None,
+        "dtype": prec, "data": "synthetic (seeded N(0,0.02) random-init weights)",
+        "config": {"workload": args.workload, "cp_layers": s.cp_layers, "cp_hidden": s.cp_hidden,
+                   "passes_per_frame": 16, "lm_heads": 15},
+        "frames_per_s": round(1000.0 / ms, 1), "frame_bytes": int(frame_bytes), "frame_gbs": round(gbs, 1),
+        "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": "CP frame (per-kernel launches replayed from one hipGraph)",
+                     "bytes_per_launch": int(frame_bytes), "avg_us": round(ms * 1e3, 1), "steps_per_launch": 1},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(out), flush=True)
+
+
+def cpu_baseline_cp(s, prec, tens, th, seconds):
+    """The reference's own qwen_cp_predict (oracle/_ref) on the host cores, same weights."""
+    sys.path.insert(0, ROOT)
+    from oracle.oracle import RefModel
+    from qwen3_tts_amd import synth
+    flags = open("/proc/cpuinfo").read()
+    variant = "_avx512" if all(f in flags for f in (" avx512f", " avx512bw", " avx512vl")) else ""
+    threads = int(os.environ.get("OMP_NUM_THREADS", "16"))
+    full = dict(tens)
+    full.update(synth.generate(s, 0x5EED0001, 0.0, threads=threads,
+                               only=lambda n: not n.startswith("talker.code_predictor.")
+                               and n != "talker.model.codec_embedding.weight"))
+    with tempfile.TemporaryDirectory(prefix="qwen_ref_", dir=os.environ.get("TMPDIR", "/tmp")) as d:
+        synth.write_model_dir(d, s, tensors=full)
+        del full
+        ref = RefModel(d, s, prec=prec, threads=threads, variant=variant)
+    t0 = time.perf_counter()
+    ref.cp_predict(th, 7)
+    one = time.perf_counter() - t0
+    n = int(max(2, min(50, seconds / max(one, 1e-3))))
+    t0 = time.perf_counter()
+    for i in range(n):
+        ref.cp_predict(th, (7 + 31 * i) % 2048)
+    ms = (time.perf_counter() - t0) / n * 1e3
+    log(f"[bench] cpu baseline: {n} reference qwen_cp_predict frames: {ms:.1f} ms/frame ({threads} threads)")
+    return {"value": round(ms, 3), "unit": "ms/frame", "cores": threads, "kind": "reference",
+            "sample": f"{n} reference qwen_cp_predict calls ({prec}, {variant.strip('_') or 'avx2'} build, "
+                      f"-O3 -ffast-math), same weights"}
 
 
 def cpu_baseline(s, prec, g, kv_len, tens, seconds):

@@ -58,10 +58,10 @@ __device__ __forceinline__ void qt_lds_copy16(const void *src, void *dst) {
 
 // BATCH (many streams, throughput): grid (n_kv, streams, G) so the workgroups of chunk 0
 // of every stream and head are dispatched first and idle chunks last (a kv head per XCD
-// under round-robin dispatch); the key loops are unrolled with masking; the merging
-// workgroup computes each output as one weighted sum over the chunks (one thread per
-// output) instead of a half-wave reduction per output.  !BATCH keeps the arithmetic
-// order of the fused step's attention phase, which it must match bit for bit.
+// under round-robin dispatch); the merging workgroup computes each output as one
+// weighted sum over the chunks (one thread per output) instead of a half-wave reduction
+// per output.  !BATCH keeps the arithmetic order of the fused step's attention phase,
+// which it must match bit for bit.  Both unroll the key loops over a block with masking.
 template <int HPK, bool PREP, bool BATCH>
 __global__ __launch_bounds__(QT_WG) void k_attn(QtAttnArgs a) {
     const int z = BATCH ? blockIdx.y : blockIdx.z;
@@ -167,8 +167,7 @@ __global__ __launch_bounds__(QT_WG) void k_attn(QtAttnArgs a) {
         }
         const int nk = min(QT_KVB, n - kb);
 #pragma unroll
-        for (int u = 0; u < (BATCH ? QT_KVB / 16 : 1 << 20); u++) {
-            if (!BATCH && u * 16 >= nk) break;
+        for (int u = 0; u < QT_KVB / 16; u++) {
             const int jl = u * 16 + wave * 4 + pg, jj = kb + jl;
             const uint4 kw = (PREP && j0 + jj == pos) ? *reinterpret_cast<const uint4 *>(knew + sub * 8)
                                                       : *reinterpret_cast<const uint4 *>(&s_kv[0][jl * QT_HD + sub * 8]);
@@ -218,11 +217,10 @@ __global__ __launch_bounds__(QT_WG) void k_attn(QtAttnArgs a) {
         }
         const int nk = min(QT_KVB, n - kb);
 #pragma unroll
-        for (int u = 0; u < (BATCH ? QT_KVB / 16 : 1 << 20); u++) {
-            if (!BATCH && u * 16 >= nk) break;
+        for (int u = 0; u < QT_KVB / 16; u++) {
             const int jl = u * 16 + wave * 4 + pg, jj = kb + jl;
             const bool ok = jl < nk;
-            if (BATCH || ok) {
+            {
                 const uint4 vw = (PREP && j0 + jj == pos) ? *reinterpret_cast<const uint4 *>(vnew + sub * 8)
                                                           : *reinterpret_cast<const uint4 *>(&s_kv[1][jl * QT_HD + sub * 8]);
                 const uint32_t w4[4] = {vw.x, vw.y, vw.z, vw.w};

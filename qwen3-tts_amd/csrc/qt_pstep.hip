@@ -155,6 +155,27 @@ __device__ unsigned long long ps_trace[TRACE_PH * 4 * NB];
 #define PS_TRACE_CLEAR() do { } while (0)
 #endif
 
+// ---- activation layout in LDS -------------------------------------------------------------
+// A COLS-element activation consumed in EPC-element chunks (one chunk per lane and 16-byte
+// weight load: EPC = 16 int8 or 8 bf16 weights) is kept chunk-transposed: float4 q of
+// chunk c sits at float4 slot q*(COLS/EPC) + c.  Lanes walk consecutive chunks, so every
+// wave-wide float4 read (norm statistics, chunk sums, dot products) is one contiguous
+// KiB: no LDS bank conflicts (a row-major layout puts consecutive lanes 4*EPC bytes apart,
+// a 4*EPC/16-way conflict).  Values and arithmetic order are unchanged.
+template <int EPC, int COLS>
+__device__ __forceinline__ int xpos(int i) {
+    constexpr int NCH = COLS / EPC;
+    const int c = i / EPC, e = i % EPC;
+    return ((e >> 2) * NCH + c) * 4 + (e & 3);
+}
+template <int EPC, int COLS>
+__device__ __forceinline__ float4 xchunk4(const float *x, int c, int q) {
+    return *reinterpret_cast<const float4 *>(x + (q * (COLS / EPC) + c) * 4);
+}
+struct PosId { __device__ __forceinline__ int operator()(int i) const { return i; } };
+template <int EPC, int COLS>
+struct PosChunk { __device__ __forceinline__ int operator()(int i) const { return xpos<EPC, COLS>(i); } };
+
 // ---- waiting for tagged data ------------------------------------------------------------
 // Each thread gathers elements i = tid + k*NT (k < K, i < n) whose words addr(i) must
 // carry `tag`; all reads are issued before any is checked, then only stale words are
@@ -163,8 +184,8 @@ __device__ unsigned long long ps_trace[TRACE_PH * 4 * NB];
 // (Issuing the next phase's weight loads between the first reads and their check, so
 // the issue overlaps the first round trip, was measured 30 % slower per step than
 // issuing them before the gather.)
-template <int K, int NT, typename AddrF>
-__device__ __forceinline__ void gather(int n, AddrF addr, float *dst, unsigned tag, int *err) {
+template <int K, int NT, typename AddrF, typename PosF = PosId>
+__device__ __forceinline__ void gather(int n, AddrF addr, float *dst, unsigned tag, int *err, PosF pos = PosF()) {
     const int tid = threadIdx.x;
     unsigned long long v[K];
 #pragma unroll
@@ -191,7 +212,7 @@ __device__ __forceinline__ void gather(int n, AddrF addr, float *dst, unsigned t
 #pragma unroll
     for (int k = 0; k < K; k++) {
         const int i = tid + k * NT;
-        if (i < n) dst[i] = val_of(v[k]);
+        if (i < n) dst[pos(i)] = val_of(v[k]);
     }
     __syncthreads();
 }
@@ -247,7 +268,7 @@ __device__ __forceinline__ void tile_dot(const Tile<PREC, COLS, NR> &t, const fl
         float xv[EPC];
 #pragma unroll
         for (int q = 0; q < EPC / 4; q++) {
-            const float4 v = *reinterpret_cast<const float4 *>(x + ci * EPC + 4 * q);
+            const float4 v = xchunk4<EPC, COLS>(x, ci, q);
             xv[4 * q] = v.x; xv[4 * q + 1] = v.y; xv[4 * q + 2] = v.z; xv[4 * q + 3] = v.w;
         }
         const float xsj = PREC == QT_INT8 ? xs[ci] : 0.f;
@@ -278,13 +299,18 @@ __device__ __forceinline__ void tile_dot(const Tile<PREC, COLS, NR> &t, const fl
     for (int r = 0; r < NR; r++) acc[r] = group_sum<64>(s[r]);
 }
 
-// Norm gains [cols] copied into LDS by global_load_lds (no registers held between the
-// phase that issues the copy and the phase that uses it), one phase ahead.
-template <int NW>
-__device__ __forceinline__ void load_gains(const float *src, int cols, float *dst) {
+// Norm gains [COLS] copied into LDS by global_load_lds (no registers held between the
+// phase that issues the copy and the phase that uses it), one phase ahead, in the
+// chunk-transposed layout: LDS float4 slot k = q*NCH + c takes global float4 c*EPC/4 + q.
+template <int NW, int EPC, int COLS>
+__device__ __forceinline__ void load_gains(const float *src, float *dst) {
+    constexpr int NCH = COLS / EPC;
     const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     src = uni(src);
-    for (int i = wave; i * 256 < cols; i += NW) lds_copy16(src + i * 256 + lane * 4, dst + i * 256);
+    for (int i = wave; i * 256 < COLS; i += NW) {
+        const int k = i * 64 + lane, q = k / NCH, c = k % NCH;
+        lds_copy16(src + (c * (EPC / 4) + q) * 4, dst + i * 256);
+    }
 }
 
 // xn = RMSNorm(x) * g into LDS, plus the int8 chunk sums xs.  The mean square is
@@ -300,7 +326,7 @@ __device__ __forceinline__ void stage_norm(const float *x, const float *gain, fl
     for (int j = 0; j < CPL; j++)
 #pragma unroll
         for (int q = 0; q < EPC / 4; q++) {
-            const float4 v = *reinterpret_cast<const float4 *>(x + (lane + 64 * j) * EPC + 4 * q);
+            const float4 v = xchunk4<EPC, COLS>(x, lane + 64 * j, q);
             ss = fmaf(v.x, v.x, ss); ss = fmaf(v.y, v.y, ss); ss = fmaf(v.z, v.z, ss); ss = fmaf(v.w, v.w, ss);
         }
     ss = group_sum<64>(ss);
@@ -308,10 +334,11 @@ __device__ __forceinline__ void stage_norm(const float *x, const float *gain, fl
     if (c * EPC < COLS) {
         float sum = 0.f;
 #pragma unroll
-        for (int e = 0; e < EPC; e++) {
-            const float v = (x[c * EPC + e] * inv) * gain[c * EPC + e];
-            xn[c * EPC + e] = v;
-            sum += v;
+        for (int q = 0; q < EPC / 4; q++) {
+            const float4 xv = xchunk4<EPC, COLS>(x, c, q), gv = xchunk4<EPC, COLS>(gain, c, q);
+            const float4 v = make_float4((xv.x * inv) * gv.x, (xv.y * inv) * gv.y, (xv.z * inv) * gv.z, (xv.w * inv) * gv.w);
+            *reinterpret_cast<float4 *>(xn + (q * (COLS / EPC) + c) * 4) = v;
+            sum += v.x; sum += v.y; sum += v.z; sum += v.w;
         }
         if (PREC == QT_INT8) xs[c] = sum;
     }
@@ -326,7 +353,10 @@ __device__ __forceinline__ void stage_sums(const float *x, float *xs) {
     for (int c = threadIdx.x; c * EPC < COLS; c += NT) {
         float sum = 0.f;
 #pragma unroll
-        for (int e = 0; e < EPC; e++) sum += x[c * EPC + e];
+        for (int q = 0; q < EPC / 4; q++) {
+            const float4 v = xchunk4<EPC, COLS>(x, c, q);
+            sum += v.x; sum += v.y; sum += v.z; sum += v.w;
+        }
         xs[c] = sum;
     }
     __syncthreads();
@@ -373,6 +403,8 @@ __global__ __launch_bounds__(NW * 64, 1) void k_pstep(Args a) {
     using THEAD = Tile<QT_BF16, H, RPW_HEAD>;
     using R = Ring<H, F>;
     static_assert(RPW_GU % 3 == 0 && RGU % 2 == 0, "gate/up pairs stay in one piece");
+    constexpr int EP = Epc<PREC>::v, EH = Epc<QT_BF16>::v;   // chunk sizes: layers, codec head
+    using PH = PosChunk<EP, H>;
 
     __shared__ __align__(16) float s_x[H];       // layer input (kept for C's residual)
     __shared__ __align__(16) float s_xa[H];      // post-attention residual (kept for E)
@@ -422,7 +454,7 @@ __global__ __launch_bounds__(NW * 64, 1) void k_pstep(Args a) {
 
     TQKV tq;
     tq.load(s_layers[0].w[0], s_layers[0].s[0], rw_qkv);
-    load_gains<NW>(s_layers[0].in_norm, H, s_gain[0]);
+    load_gains<NW, EP, H>(s_layers[0].in_norm, s_gain[0]);
 
     for (int step = 0; step < a.n_steps; step++) {
         const int par = step & 1;
@@ -470,10 +502,10 @@ __global__ __launch_bounds__(NW * 64, 1) void k_pstep(Args a) {
             // ---------------- A: q|k|v rows -----------------
             if (l > 0) {
                 const unsigned long long *src = ring.blk(par, l - 1) + R::OX;
-                gather<H / NT, NT>(H, [&](int i) { return src + i; }, s_x, tag, a.err);
+                gather<H / NT, NT>(H, [&](int i) { return src + i; }, s_x, tag, a.err, PH());
             } else {
                 for (int i = tid; i < H; i += NT)
-                    s_x[i] = tok < 0 ? ldg(a.xin + i) : bf16f(ldg(a.emb + (size_t)tok * H + i));
+                    s_x[xpos<EP, H>(i)] = tok < 0 ? ldg(a.xin + i) : bf16f(ldg(a.emb + (size_t)tok * H + i));
                 __syncthreads();
             }
             PS_MARK(ph, 0);
@@ -493,7 +525,7 @@ __global__ __launch_bounds__(NW * 64, 1) void k_pstep(Args a) {
             to.load(ly.w[1], ly.s[1], rw_o);
             TGU tg0, tg1, tg2;
             tg0.load(ly.w[2], ly.s[2], rw_gu);
-            load_gains<NW>(ly.post_norm, H, s_gain[1]);
+            load_gains<NW, EP, H>(ly.post_norm, s_gain[1]);
             PS_MARK(ph, 1); ph++;
 
             // ---------------- B: attention chunk -----------------
@@ -679,7 +711,7 @@ __global__ __launch_bounds__(NW * 64, 1) void k_pstep(Args a) {
             // ---------------- C: xa = x + W_o . attn -----------------
             {
                 const unsigned long long *src = blk + R::OATT;
-                gather<QD / NT, NT>(QD, [&](int i) { return src + i; }, s_in, tag, a.err);
+                gather<QD / NT, NT>(QD, [&](int i) { return src + i; }, s_in, tag, a.err, PosChunk<EP, QD>());
             }
             PS_MARK(ph, 0);
             {
@@ -690,7 +722,7 @@ __global__ __launch_bounds__(NW * 64, 1) void k_pstep(Args a) {
                 for (int r = 0; r < RPW_O; r++)
                     if (lane == r) {
                         const float v = PREC == QT_INT8 ? __fmul_rn(acc[r], to.rs[r]) : acc[r];
-                        st_tag(blk + R::OXA + rw_o + r, __fadd_rn(s_x[rw_o + r], v), tag);
+                        st_tag(blk + R::OXA + rw_o + r, __fadd_rn(s_x[xpos<EP, H>(rw_o + r)], v), tag);
                     }
             }
             TDN td;
@@ -700,7 +732,7 @@ __global__ __launch_bounds__(NW * 64, 1) void k_pstep(Args a) {
             // ---------------- D: h = SwiGLU(W_gu . RMSNorm(xa)) -----------------
             {
                 const unsigned long long *src = blk + R::OXA;
-                gather<H / NT, NT>(H, [&](int i) { return src + i; }, s_xa, tag, a.err);
+                gather<H / NT, NT>(H, [&](int i) { return src + i; }, s_xa, tag, a.err, PH());
             }
             PS_MARK(ph, 0);
             {
@@ -726,14 +758,14 @@ __global__ __launch_bounds__(NW * 64, 1) void k_pstep(Args a) {
             PS_MARK(ph, 3);
             if (l + 1 < L) {
                 tq.load(s_layers[l + 1].w[0], s_layers[l + 1].s[0], rw_qkv);
-                load_gains<NW>(s_layers[l + 1].in_norm, H, s_gain[0]);
+                load_gains<NW, EP, H>(s_layers[l + 1].in_norm, s_gain[0]);
             }
             PS_MARK(ph, 1); ph++;
 
             // ---------------- E: x' = xa + W_dn . h -----------------
             {
                 const unsigned long long *src = blk + R::OH;
-                gather<F / NT, NT>(F, [&](int i) { return src + i; }, s_in, tag, a.err);
+                gather<F / NT, NT>(F, [&](int i) { return src + i; }, s_in, tag, a.err, PosChunk<EP, F>());
             }
             PS_MARK(ph, 0);
             {
@@ -745,7 +777,7 @@ __global__ __launch_bounds__(NW * 64, 1) void k_pstep(Args a) {
                 for (int r = 0; r < RPW_DN; r++)
                     if (lane == r) {
                         const float v = PREC == QT_INT8 ? __fmul_rn(acc[r], td.rs[r]) : acc[r];
-                        st_tag(blk + R::OX + rw_dn + r, __fadd_rn(s_xa[rw_dn + r], v), tag);
+                        st_tag(blk + R::OX + rw_dn + r, __fadd_rn(s_xa[xpos<EP, H>(rw_dn + r)], v), tag);
                     }
             }
             PS_MARK(ph, 3);
@@ -758,10 +790,10 @@ __global__ __launch_bounds__(NW * 64, 1) void k_pstep(Args a) {
         if (!a.with_head) {
             // final norm of the residual -> hid, residual -> decx (workgroup 0)
             if (b == 0) {
-                load_gains<NW>(a.final_norm, H, s_gain[1]);
-                gather<H / NT, NT>(H, [&](int i) { return xfin + i; }, s_x, tag, a.err);
+                load_gains<NW, EH, H>(a.final_norm, s_gain[1]);
+                gather<H / NT, NT>(H, [&](int i) { return xfin + i; }, s_x, tag, a.err, PosChunk<EH, H>());
                 stage_norm<QT_BF16, H>(s_x, s_gain[1], a.eps, s_xn, s_xs);
-                for (int i = tid; i < H; i += NT) { a.hid[i] = s_xn[i]; a.decx[i] = s_x[i]; }
+                for (int i = tid; i < H; i += NT) { a.hid[i] = s_xn[xpos<EH, H>(i)]; a.decx[i] = s_x[xpos<EH, H>(i)]; }
             }
         } else {
             // ---------------- head: logits rows + masked local argmax -----------------
@@ -769,12 +801,12 @@ __global__ __launch_bounds__(NW * 64, 1) void k_pstep(Args a) {
             // through the layer loop would hold its registers for the whole loop)
             THEAD th;
             th.load(a.head_w, nullptr, rw_head);
-            load_gains<NW>(a.final_norm, H, s_gain[1]);
-            gather<H / NT, NT>(H, [&](int i) { return xfin + i; }, s_x, tag, a.err);
+            load_gains<NW, EH, H>(a.final_norm, s_gain[1]);
+            gather<H / NT, NT>(H, [&](int i) { return xfin + i; }, s_x, tag, a.err, PosChunk<EH, H>());
             PS_MARK(ph, 0);
             stage_norm<QT_BF16, H>(s_x, s_gain[1], a.eps, s_xn, s_xs);
             if (last_step && b == 0)
-                for (int i = tid; i < H; i += NT) { a.hid[i] = s_xn[i]; a.decx[i] = s_x[i]; }
+                for (int i = tid; i < H; i += NT) { a.hid[i] = s_xn[xpos<EH, H>(i)]; a.decx[i] = s_x[xpos<EH, H>(i)]; }
             float acc[RPW_HEAD];
             tile_dot<QT_BF16, H, RPW_HEAD>(th, s_xn, s_xs, acc);
             const int frame = frame0 + step;
@@ -802,7 +834,7 @@ __global__ __launch_bounds__(NW * 64, 1) void k_pstep(Args a) {
             }
             if (!last_step) {
                 tq.load(s_layers[0].w[0], s_layers[0].s[0], rw_qkv);
-                load_gains<NW>(s_layers[0].in_norm, H, s_gain[0]);
+                load_gains<NW, EP, H>(s_layers[0].in_norm, s_gain[0]);
             }
             PS_MARK(ph, 1); ph++;
             // global argmax over the 256 local winners (every workgroup, redundantly)

@@ -312,6 +312,55 @@ class CodePredictor:
             pass
 
 
+def cp_from_tensors(t, shape, prec=BF16, cp_kv_max=64):
+    """A CodePredictor (bf16 weights, optionally quantized on the device to ``prec``) over
+    synth tensors {reference name: bf16 array}: CP layers, cp_norm, the 15 lm heads and
+    codec embeddings, the Talker codec embedding.  No small_to_mtp_projection (the
+    Talker and CP hidden sizes must agree, as in the 0.6B model)."""
+    from .synth import bf16_to_f32, rope_tables
+    s = shape
+    if s.hidden != s.cp_hidden:
+        raise ValueError("cp_from_tensors: hidden != cp_hidden needs the mtp projection")
+    keep = []
+    layers = layers_from_tensors(t, s, cp=True)
+    arr = (Layer * len(layers))()
+    for l, ly in enumerate(layers):
+        for nm in ["q", "k", "v", "o", "gate_up", "down"]:
+            w, _ = ly[nm]
+            keep.append(w)
+            getattr(arr[l], nm).w = w.ctypes.data
+            getattr(arr[l], nm).scale = None
+        for nm in ["input_norm", "post_attn_norm", "q_norm", "k_norm"]:
+            a = np.ascontiguousarray(ly[nm], np.float32)
+            keep.append(a)
+            setattr(arr[l], nm, a.ctypes.data)
+    cos, sin = rope_tables(s.cp_head_dim, s.rope_theta, cp_kv_max)
+    fn = np.ascontiguousarray(bf16_to_f32(t["talker.code_predictor.model.norm.weight"]))
+    keep += [arr, cos, sin, fn]
+    d = CpDesc()
+    d.cp = TalkerDesc(hidden=s.cp_hidden, inter=s.cp_inter, n_heads=s.cp_heads, n_kv_heads=s.cp_kv_heads,
+                      head_dim=s.cp_head_dim, n_layers=len(layers), kv_max=cp_kv_max, eps=s.eps, prec=BF16,
+                      quantize_to=-1 if prec == BF16 else prec, layers=arr, final_norm=fn.ctypes.data,
+                      rope_cos=cos.ctypes.data, rope_sin=sin.ctypes.data, rope_len=cp_kv_max)
+    d.codebook = s.codebook
+    d.lm_prec = BF16
+    for g in range(15):
+        lm = np.ascontiguousarray(t[f"talker.code_predictor.lm_head.{g}.weight"])
+        ce = np.ascontiguousarray(t[f"talker.code_predictor.model.codec_embedding.{g}.weight"])
+        keep += [lm, ce]
+        d.lm_head[g].w = lm.ctypes.data
+        d.lm_head[g].scale = None
+        d.cp_codec_emb[g] = ce.ctypes.data
+    te = np.ascontiguousarray(t["talker.model.codec_embedding.weight"])
+    keep.append(te)
+    d.talker_codec_emb = te.ctypes.data
+    d.codec_vocab = s.codec_vocab
+    d.talker_hidden = s.hidden
+    d.emb_dim = s.hidden
+    d.mtp.w = None
+    return CodePredictor(d, keep)
+
+
 def layers_from_ref(ref, prec_code, cp=False):
     """Layer dicts over the reference-loaded (and reference-quantized) weights."""
     s = ref.shape
