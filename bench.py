@@ -90,9 +90,11 @@ WORKLOADS = {
     "talker-1.7B-int4-b1-L2048": ("1.7B", "int4", 2048, 64),
     "talker-1.7B-int4-b1-L4096": ("1.7B", "int4", 4096, 64),
 }
-# Code Predictor frames: (shape, precision, default timed frames)
+# Code Predictor frames: (shape, precision, default timed frames, two-position prefill)
 CP_WORKLOADS = {
-    "cp-0.6B-bf16-frame": ("0.6B", "bf16", 500),
+    "cp-0.6B-bf16-frame": ("0.6B", "bf16", 500, False),
+    "cp-0.6B-int8-frame": ("0.6B", "int8", 500, False),
+    "cp-0.6B-int8-frame-prefill2": ("0.6B", "int8", 500, True),
 }
 # batched workloads: (shape, precision, streams, KV length range, default timed steps)
 BATCH_WORKLOADS = {
@@ -330,10 +332,12 @@ def bench_cp(args):
     fresh KV (positions 0..15) + 15 lm-head argmaxes + embedding gathers, captured once as
     a hipGraph; frames replayed back to back on device-resident inputs (talker hidden =
     RMS-normed N(0,1), code0 seeded).  value = ms per frame.  Algorithmic bytes per frame:
-    16 x (5 layers of weights + norms) + 15 x one 2048 x 1024 lm head (bf16); the CP's
-    157 MB of layer weights fit in the 256 MB MALL, so HBM traffic is lower than that."""
+    16 x (5 layers of weights + norms) + 15 x one 2048 x 1024 lm head (bf16, or int8 +
+    row scales); with the two-position prefill (cp_prefill2, cp.c:816-902) positions 0
+    and 1 share one weight sweep, so 15 sweeps.  The CP's 157 MB of bf16 layer weights fit
+    in the 256 MB MALL, so HBM traffic is lower than that."""
     from qwen3_tts_amd import hip, synth
-    shape_name, prec, dframes = CP_WORKLOADS[args.workload]
+    shape_name, prec, dframes, pf2 = CP_WORKLOADS[args.workload]
     K = args.steps or dframes
     W = 20 if args.warmup is None else args.warmup
     s = synth.SHAPES[shape_name]
@@ -341,6 +345,8 @@ def bench_cp(args):
     only = lambda n: n.startswith("talker.code_predictor.") or n == "talker.model.codec_embedding.weight"  # noqa: E731
     tens = synth.generate(s, 0x5EED0001, 0.0, threads=int(os.environ.get("OMP_NUM_THREADS", "16")), only=only)
     cp = hip.cp_from_tensors(tens, s, hip.PREC[prec])
+    if pf2:
+        cp.set_prefill2(1)
     log(f"[bench] cp: init {time.time() - t0:.1f}s")
     rng = np.random.default_rng(0x5EED0002)
     th = rng.standard_normal(s.hidden).astype(np.float32)
@@ -359,12 +365,14 @@ def bench_cp(args):
     ms_total = ev.elapsed_ms(a, b)
     ev.device_sync()
     ms = ms_total / K
+    wb = (lambda r, c: r * c * 2) if prec == "bf16" else (lambda r, c: r * c + 4 * r)   # int8: + row scales
     per_layer = 0
     for r, c in [(s.cp_heads * s.cp_head_dim + 2 * s.cp_kv_heads * s.cp_head_dim, s.cp_hidden),
                  (s.cp_hidden, s.cp_heads * s.cp_head_dim), (2 * s.cp_inter, s.cp_hidden), (s.cp_hidden, s.cp_inter)]:
-        per_layer += r * c * 2
+        per_layer += wb(r, c)
     per_layer += (2 * s.cp_hidden + 2 * s.cp_head_dim) * 4
-    frame_bytes = 16 * s.cp_layers * per_layer + 15 * s.codebook * s.cp_hidden * 2
+    sweeps = 15 if pf2 else 16          # the two-position prefill reads the layer weights once for positions 0, 1
+    frame_bytes = sweeps * s.cp_layers * per_layer + 15 * wb(s.codebook, s.cp_hidden)
     gbs = frame_bytes / (ms * 1e-3) / 1e9
     log(f"[bench] cp: {ms * 1e3:.1f} us/frame, {gbs:.0f} GB/s algorithmic, codes[0:4] {list(codes[:4])}")
     cp.free()
@@ -381,7 +389,7 @@ def bench_cp(args):
         "ms_per_step": round(ms, 4), "higher_is_better": False, "scaling": "weak", "vs_baseline": None,
         "dtype": prec, "data": "synthetic (seeded N(0,0.02) random-init weights)",
         "config": {"workload": args.workload, "cp_layers": s.cp_layers, "cp_hidden": s.cp_hidden,
-                   "passes_per_frame": 16, "lm_heads": 15},
+                   "passes_per_frame": 16, "weight_sweeps_per_frame": sweeps, "lm_heads": 15},
         "frames_per_s": round(1000.0 / ms, 1), "frame_bytes": int(frame_bytes), "frame_gbs": round(gbs, 1),
         "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,

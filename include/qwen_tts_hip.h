@@ -175,6 +175,14 @@ int   qwen_hip_cp_sync(void *state);
 void *qwen_hip_cp_stream(void *state);
 /* replaces qwen_cuda_cp_free                     (qwen_tts_cuda_talker.cu:917) */
 void  qwen_hip_cp_free(void *state);
+/* two-position prefill, twin of cp_prefill2 (qwen_tts_code_predictor.c:816-902) and of
+ * its switch cp_prefill2_mode / QWEN_CP_PREFILL2 (:783-807).  set_prefill2(state, 1)
+ * needs int8 weights in every CP layer (the reference: quantized CP only) and makes
+ * qwen_hip_cp_frame run positions 0 and 1 as one two-column pass (weights read once);
+ * 0 restores the sequential passes (the default).  qwen_hip_cp_prefill2 runs that pass
+ * alone: x0, x1 host f32[cp_hidden] residuals in/out at positions 0 and 1. */
+int   qwen_hip_cp_set_prefill2(void *state, int on);
+int   qwen_hip_cp_prefill2(void *state, float *x0, float *x1);
 /* CP batch twins (qwen_tts_cuda_talker.cu:879-915): B streams over the single CP state's
  * weights; x host f32[B][cp_hidden] residuals in/out (not normed), one pass per stream
  * at pos_arr[b] on its own CP KV. */

@@ -689,6 +689,10 @@ typedef struct {
     hipGraphExec_t fexec, pexec;
     int fready, pready, frame_ready;
     int *d_steppos;
+    /* two-position prefill (positions 0 and 1 as one two-column pass) */
+    int prefill2;                         /* 1: the frame starts with cp_prefill2_body */
+    float *x2, *qkv2, *attn2, *h2;        /* device [2][H], [2][QKV], [2][qd], [2][F] */
+    int8_t *pc2; float *ps2;              /* activation pieces of the two columns */
     int dead;
 } cp_t;
 
@@ -699,7 +703,8 @@ static void cp_destroy(cp_t *c) {
     stack_free(&c->s);
     for (int g = 0; g < 15; g++) { dmat_free(&c->lm[g]); if (c->cp_emb[g]) (void)hipFree(c->cp_emb[g]); }
     dmat_free(&c->mtp);
-    void *bufs[] = {c->talker_emb, c->mtp_bias, c->x, c->x1, c->ebuf, c->logits, c->th, c->d_posv, c->d_codes, c->d_steppos};
+    void *bufs[] = {c->talker_emb, c->mtp_bias, c->x, c->x1, c->ebuf, c->logits, c->th, c->d_posv, c->d_codes, c->d_steppos,
+                    c->x2, c->qkv2, c->attn2, c->h2, c->pc2, c->ps2};
     for (size_t i = 0; i < sizeof bufs / sizeof bufs[0]; i++) if (bufs[i]) (void)hipFree(bufs[i]);
     if (c->h_x) (void)hipHostFree(c->h_x);
     if (c->h_codes) (void)hipHostFree(c->h_codes);
@@ -777,18 +782,121 @@ static hipError_t cp_pass_body(void *a) {
     return stack_body(&c->s, c->x, c->d_steppos, c->st);
 }
 
+/* Positions 0 and 1 of a frame as one two-column pass: the device twin of cp_prefill2
+ * (qwen_tts_code_predictor.c:816-902).  x2 = [x0 | x1] (residuals, not normed).  Every
+ * projection reads its int8 weights once for both columns (pieces + MFMA, the batched
+ * projection of qt_batch.hip); per-head norm, RoPE, KV append and attention run per
+ * position in order, so position 1 attends to the key/value that position 0 appended.
+ * Mathematically the two sequential passes; the projections round differently (exact
+ * integer products of 3-plane activation pieces instead of f32 dot products), the same
+ * kind of difference the reference accepts for its B=2 matmat. */
+static hipError_t cp_prefill2_body(cp_t *c) {
+    stack_t *s = &c->s;
+    hipError_t e;
+    const int H = s->H, F = s->F, QKV = s->qd + 2 * s->kvd;
+    const float scale = 1.0f / sqrtf((float)s->hd);
+    for (int l = 0; l < s->L; l++) {
+        const size_t lay = (size_t)l * s->nkv * s->kv_max * s->hd;
+        if ((e = qt_launch_bpieces(c->x2, H, s->in_norm[l], s->eps, H, 2, 16, c->pc2, c->ps2, c->st))) return e;
+        if ((e = qt_launch_bgemm_i8(QT_EPI_STORE, s->qkv[l].w, s->qkv[l].scale, QKV, H, c->pc2, c->ps2, 2, 16, c->qkv2, QKV,
+                                    c->st))) return e;
+        for (int p = 0; p < 2; p++)
+            if ((e = qt_launch_attn(1, c->qkv2 + (size_t)p * QKV, s->qn[l], s->kn[l], s->rope_cos, s->rope_sin, s->eps,
+                                    c->d_posv + p, 0, s->kc + lay, s->vc + lay, s->hd, (long long)s->kv_max * s->hd, s->nh,
+                                    s->nkv, s->hd, scale, s->part, s->cnt, s->attn_G, c->attn2 + (size_t)p * s->qd,
+                                    c->st))) return e;
+        if ((e = qt_launch_bpieces(c->attn2, s->qd, NULL, s->eps, s->qd, 2, 16, c->pc2, c->ps2, c->st))) return e;
+        if ((e = qt_launch_bgemm_i8(QT_EPI_RESID, s->o[l].w, s->o[l].scale, H, s->qd, c->pc2, c->ps2, 2, 16, c->x2, H,
+                                    c->st))) return e;
+        if ((e = qt_launch_bpieces(c->x2, H, s->post_norm[l], s->eps, H, 2, 16, c->pc2, c->ps2, c->st))) return e;
+        if ((e = qt_launch_bgemm_i8(QT_EPI_SWIGLU, s->gu[l].w, s->gu[l].scale, 2 * F, H, c->pc2, c->ps2, 2, 16, c->h2, F,
+                                    c->st))) return e;
+        if ((e = qt_launch_bpieces(c->h2, F, NULL, s->eps, F, 2, 16, c->pc2, c->ps2, c->st))) return e;
+        if ((e = qt_launch_bgemm_i8(QT_EPI_RESID, s->dn[l].w, s->dn[l].scale, H, F, c->pc2, c->ps2, 2, 16, c->x2, H,
+                                    c->st))) return e;
+    }
+    return hipSuccess;
+}
+
+/* Mode switch of the two-position prefill (the reference's QWEN_CP_PREFILL2,
+ * qwen_tts_code_predictor.c:783-807): on needs int8 weights in every CP layer.  The
+ * frame graph is rebuilt on the next frame. */
+int qwen_hip_cp_set_prefill2(void *state, int on) {
+    cp_t *c = (cp_t *)state;
+    if (!c || c->dead) { SETERR("CP state is dead or NULL"); return -1; }
+    stack_t *s = &c->s;
+    if (on) {
+        for (int l = 0; l < s->L; l++)
+            REQ(s->qkv[l].prec == QWEN_HIP_INT8 && s->o[l].prec == QWEN_HIP_INT8 && s->gu[l].prec == QWEN_HIP_INT8 &&
+                s->dn[l].prec == QWEN_HIP_INT8, "CP prefill2 needs int8 weights in every layer");
+        REQ(s->H % 64 == 0 && s->F % 64 == 0 && s->qd % 64 == 0, "CP prefill2 needs dims divisible by 64");
+        if (!c->x2) {
+            const int K = s->F > s->H ? (s->F > s->qd ? s->F : s->qd) : (s->H > s->qd ? s->H : s->qd);
+            HCK(hipMalloc((void **)&c->x2, (size_t)2 * s->H * sizeof(float)));
+            HCK(hipMalloc((void **)&c->qkv2, (size_t)2 * (s->qd + 2 * s->kvd) * sizeof(float)));
+            HCK(hipMalloc((void **)&c->attn2, (size_t)2 * s->qd * sizeof(float)));
+            HCK(hipMalloc((void **)&c->h2, (size_t)2 * s->F * sizeof(float)));
+            HCK(hipMalloc((void **)&c->pc2, (size_t)K * 3 * 16));
+            HCK(hipMalloc((void **)&c->ps2, 16 * sizeof(float)));
+        }
+    }
+    if (c->prefill2 != (on != 0) && c->fready) {
+        (void)hipGraphExecDestroy(c->fexec);
+        c->fready = 0;
+        c->frame_ready = 0;
+    }
+    c->prefill2 = on != 0;
+    return 0;
+fail:
+    return -1;
+}
+
+/* x0, x1: host f32[cp_hidden] residuals in/out; positions 0 and 1 (their KV rows are
+ * written).  The device twin of cp_prefill2(ctx, mode, x0, x1). */
+int qwen_hip_cp_prefill2(void *state, float *x0, float *x1) {
+    cp_t *c = (cp_t *)state;
+    if (!c || c->dead) { SETERR("CP state is dead or NULL"); return -1; }
+    if (!x0 || !x1) { SETERR("null residuals"); return -1; }            /* argument errors leave the state usable */
+    if (!c->x2) { SETERR("CP prefill2 is not enabled (qwen_hip_cp_set_prefill2)"); return -1; }
+    const int H = c->s.H;
+    memcpy(c->h_x, x0, (size_t)H * sizeof(float));
+    HCK(hipMemcpyAsync(c->x2, c->h_x, (size_t)H * sizeof(float), hipMemcpyHostToDevice, c->st));
+    HCK(hipStreamSynchronize(c->st));
+    memcpy(c->h_x, x1, (size_t)H * sizeof(float));
+    HCK(hipMemcpyAsync(c->x2 + H, c->h_x, (size_t)H * sizeof(float), hipMemcpyHostToDevice, c->st));
+    HCK(cp_prefill2_body(c));
+    HCK(hipMemcpyAsync(c->h_x, c->x2, (size_t)H * sizeof(float), hipMemcpyDeviceToHost, c->st));
+    HCK(hipStreamSynchronize(c->st));
+    memcpy(x0, c->h_x, (size_t)H * sizeof(float));
+    HCK(hipMemcpyAsync(c->h_x, c->x2 + H, (size_t)H * sizeof(float), hipMemcpyDeviceToHost, c->st));
+    HCK(hipStreamSynchronize(c->st));
+    memcpy(x1, c->h_x, (size_t)H * sizeof(float));
+    return 0;
+fail:
+    if (c) c->dead = 1;
+    return -1;
+}
+
 /* The whole frame (qwen_tts_code_predictor.c:926-1045) as one launch sequence:
  * th = talker hidden (device), d_codes[0] = code0. */
 static hipError_t cp_frame_body(void *a) {
     cp_t *c = (cp_t *)a;
     hipError_t e;
     const int H = c->s.H;
-    if ((e = cp_project(c, c->th, c->x))) return e;
-    if ((e = qt_launch_gather(c->d_codes, c->codec_vocab, c->talker_emb, c->talker_hidden, c->ebuf, c->st))) return e;
-    if ((e = cp_project(c, c->ebuf, c->x1))) return e;
-    if ((e = stack_body(&c->s, c->x, c->d_posv + 0, c->st))) return e;
-    if ((e = qt_launch_copy_f32(c->x1, c->x, H, c->st))) return e;
-    if ((e = stack_body(&c->s, c->x, c->d_posv + 1, c->st))) return e;
+    if (c->prefill2) {
+        if ((e = cp_project(c, c->th, c->x2))) return e;
+        if ((e = qt_launch_gather(c->d_codes, c->codec_vocab, c->talker_emb, c->talker_hidden, c->ebuf, c->st))) return e;
+        if ((e = cp_project(c, c->ebuf, c->x2 + H))) return e;
+        if ((e = cp_prefill2_body(c))) return e;
+        if ((e = qt_launch_copy_f32(c->x2 + H, c->x, H, c->st))) return e;
+    } else {
+        if ((e = cp_project(c, c->th, c->x))) return e;
+        if ((e = qt_launch_gather(c->d_codes, c->codec_vocab, c->talker_emb, c->talker_hidden, c->ebuf, c->st))) return e;
+        if ((e = cp_project(c, c->ebuf, c->x1))) return e;
+        if ((e = stack_body(&c->s, c->x, c->d_posv + 0, c->st))) return e;
+        if ((e = qt_launch_copy_f32(c->x1, c->x, H, c->st))) return e;
+        if ((e = stack_body(&c->s, c->x, c->d_posv + 1, c->st))) return e;
+    }
     for (int g = 0; g < 15; g++) {
         if (g > 0) {
             if ((e = qt_launch_gather(c->d_codes + g, c->codebook, c->cp_emb[g - 1], c->emb_dim, c->ebuf, c->st))) return e;

@@ -32,6 +32,7 @@ EXPORTS = [
     "qwen_hip_talker_batch_upload_slot", "qwen_hip_talker_batch_free", "qwen_hip_talker_batch_download_slot",
     "qwen_hip_talker_batch_step_async", "qwen_hip_talker_batch_sync", "qwen_hip_talker_batch_stream",
     "qwen_hip_cp_batch_init", "qwen_hip_cp_batch_step", "qwen_hip_cp_batch_free", "qwen_hip_op_matmat_int8",
+    "qwen_hip_cp_set_prefill2", "qwen_hip_cp_prefill2",
 ]
 
 
@@ -126,6 +127,8 @@ def lib():
         L.qwen_hip_cp_batch_init.argtypes = [vp, i]; L.qwen_hip_cp_batch_init.restype = vp
         L.qwen_hip_cp_batch_step.argtypes = [vp, vp, vp]; L.qwen_hip_cp_batch_step.restype = i
         L.qwen_hip_cp_batch_free.argtypes = [vp]
+        L.qwen_hip_cp_set_prefill2.argtypes = [vp, i]; L.qwen_hip_cp_set_prefill2.restype = i
+        L.qwen_hip_cp_prefill2.argtypes = [vp, vp, vp]; L.qwen_hip_cp_prefill2.restype = i
         L.qwen_hip_op_matmat_int8.argtypes = [vp, vp, vp, vp, i, i, i]; L.qwen_hip_op_matmat_int8.restype = i
         _lib = L
     return _lib
@@ -282,6 +285,17 @@ class CodePredictor:
         x = np.array(x, np.float32, copy=True)
         check(lib().qwen_hip_cp_step(self.h, _p(x), pos), "cp_step")
         return x
+
+    def set_prefill2(self, on):
+        """Frames start with the two-position pass (int8 CP weights only)."""
+        check(lib().qwen_hip_cp_set_prefill2(self.h, int(on)), "cp_set_prefill2")
+
+    def prefill2(self, x0, x1):
+        """Positions 0 and 1 as one two-column pass; returns the two residuals."""
+        x0 = np.array(x0, np.float32, copy=True)
+        x1 = np.array(x1, np.float32, copy=True)
+        check(lib().qwen_hip_cp_prefill2(self.h, _p(x0), _p(x1)), "cp_prefill2")
+        return x0, x1
 
     def batch_step(self, x, pos):
         """One pass for B streams (own CP KVs) over this CP's weights; x [B][H]."""

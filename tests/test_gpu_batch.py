@@ -223,3 +223,67 @@ def test_cp_batch_step_vs_oracle(oracle, prec):
             assert oracle.lib.qo_cp_pass(C.byref(streams[b][0]), want.ctypes.data, p) == 0
             assert rel_l2(got[b], want) <= 1e-3, (p, b, rel_l2(got[b], want))
     cp.free()
+
+
+@need_ref
+def test_cp_prefill2_vs_oracle_and_reference(oracle):
+    """Two-position prefill (cp_prefill2, qwen_tts_code_predictor.c:816-902): the
+    two-column pass against two sequential oracle passes at positions 0 and 1 (the
+    reference's own definition: 'the same math', its matmat only reorders rounding),
+    then whole frames with the prefill on against the compiled reference's
+    qwen_cp_predict with QWEN_CP_PREFILL2=1 (its mode is probed once per thread, so the
+    reference runs in a fresh thread)."""
+    import os
+    import threading
+    from test_gpu_parity import _gpu_cp
+    from oracle.oracle import oracle_talker
+    print("[case] cp prefill2 int8", flush=True)
+    ref, shape = _ref("mini", "int8")
+    cp = _gpu_cp(ref, shape, hip.INT8)
+    with pytest.raises(RuntimeError):
+        cp.prefill2(np.zeros(shape.cp_hidden, np.float32), np.zeros(shape.cp_hidden, np.float32))   # not enabled
+    cp.set_prefill2(1)
+    rng = np.random.default_rng(21)
+    for trial in range(3):
+        x0 = rng.standard_normal(shape.cp_hidden).astype(np.float32)
+        x1 = rng.standard_normal(shape.cp_hidden).astype(np.float32)
+        g0, g1 = cp.prefill2(x0, x1)
+        t, _ = oracle_talker(ref, hip.INT8, 64, cp=True)
+        w0, w1 = np.array(x0, copy=True), np.array(x1, copy=True)
+        assert oracle.lib.qo_cp_pass(C.byref(t), w0.ctypes.data, 0) == 0
+        assert oracle.lib.qo_cp_pass(C.byref(t), w1.ctypes.data, 1) == 0
+        for g, w in [(g0, w0), (g1, w1)]:
+            assert np.abs(g - w).max() <= 2e-2 and rel_l2(g, w) <= 1e-3, (trial, rel_l2(g, w))
+    frames = []
+    for f in range(4):
+        th = rng.standard_normal(shape.hidden).astype(np.float32)
+        th /= np.sqrt((th ** 2).mean())
+        frames.append((th, int(rng.integers(0, 2048))))
+    got = [list(cp.frame(th, c0)) for th, c0 in frames]
+    want = []
+    old = os.environ.get("QWEN_CP_PREFILL2")
+    os.environ["QWEN_CP_PREFILL2"] = "1"
+    try:
+        th_ = threading.Thread(target=lambda: want.extend(list(ref.cp_predict(th, c0)) for th, c0 in frames))
+        th_.start()
+        th_.join()
+    finally:
+        if old is None:
+            del os.environ["QWEN_CP_PREFILL2"]
+        else:
+            os.environ["QWEN_CP_PREFILL2"] = old
+    assert len(want) == len(frames)
+    assert got == want, (got, want)
+    cp.set_prefill2(0)                                  # back to sequential passes
+    assert [list(cp.frame(th, c0)) for th, c0 in frames] == [list(ref.cp_predict(th, c0)) for th, c0 in frames]
+    cp.free()
+
+
+@need_ref
+def test_cp_prefill2_needs_int8():
+    from test_gpu_parity import _gpu_cp
+    ref, shape = _ref("mini", "bf16")
+    cp = _gpu_cp(ref, shape, hip.BF16)
+    with pytest.raises(RuntimeError):
+        cp.set_prefill2(1)
+    cp.free()
