@@ -18,8 +18,8 @@
 //   (qwen_tts_kernels.c:2350-2351).  Against the reference's f32 accumulation the result
 //   differs by the f32 rounding of its own sum (~1e-7 relative), nothing systematic.
 //
-// Layouts.  Weights: the device int8 rows of qt_device.h (u = q ^ 0x80); one XOR per
-// dword restores the signed byte for the MFMA.  Pieces: [K/64][3*Bp][64] int8, column
+// Layouts.  Weights: the device int8 rows of qt_device.h (signed bytes q), fed to the
+// MFMA as they are.  Pieces: [K/64][3*Bp][64] int8, column
 // col = piece*Bp + b (Bp = B rounded up to 16; padding columns are zero), so the MFMA B
 // operand of N-tile t at k-block kb is one contiguous KiB (16 columns x 64 bytes).
 // MFMA operand mapping (16x16x64, wave64): lane l supplies 16 bytes of A row (l % 16)
@@ -129,7 +129,7 @@ __global__ __launch_bounds__(QT_BP_T) void k_bpieces(const float *x, long long x
 
 // ---- int8 weights x activation pieces --------------------------------------------------
 struct QtBgArgs {
-    const uint8_t *w;     // device int8 rows (u = q ^ 0x80), [rows][K]
+    const uint8_t *w;     // device int8 rows (signed q), [rows][K]
     const float *scale;   // [rows]
     int rows, K;
     const int8_t *P;      // pieces [K/64][3*Bp][64]
@@ -165,8 +165,7 @@ __global__ __launch_bounds__(QT_BG_MAXW * 64) void k_bgemm_i8(QtBgArgs a) {
     // compiler can issue them ahead of the MFMAs that consume them
     auto block = [&](int kb) {
         const int k = kw0 + kb * 64;
-        const qt_v4i A = qt_v4i{(int)(wa[kb].x ^ 0x80808080u), (int)(wa[kb].y ^ 0x80808080u),
-                                (int)(wa[kb].z ^ 0x80808080u), (int)(wa[kb].w ^ 0x80808080u)};
+        const qt_v4i A = qt_v4i{(int)wa[kb].x, (int)wa[kb].y, (int)wa[kb].z, (int)wa[kb].w};
         const int8_t *pb = a.P + (size_t)(k >> 6) * cs + (size_t)m * 64 + grp * 16;
 #pragma unroll
         for (int t = 0; t < NT; t++) {

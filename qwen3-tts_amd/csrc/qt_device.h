@@ -2,9 +2,8 @@
 //
 // Weight storage on the device (set up once by qwen_tts_hip.c at init):
 //   bf16  rows of 2*cols bytes, the reference's row-major bits unchanged;
-//   int8  rows of cols bytes holding u = q ^ 0x80 (= q + 128), so one
-//         v_cvt_f32_ubyteN converts a byte; the -128 offset is folded into a
-//         per-lane sum of the activation slice.  Scale f32 per row.
+//   int8  rows of cols signed bytes q, the reference's quantizer output unchanged
+//         (the integer dot products take them as they are).  Scale f32 per row.
 //   q4_0  the reference's 18-byte blocks split into qs rows (cols/2 bytes) and a
 //         [rows][cols/32] array of f16 scale bits, so qs rows are 16-byte aligned
 //         and one 128-bit load covers exactly one block.
@@ -127,6 +126,92 @@ __device__ __forceinline__ float softmax_merge32(float m, float l, float o, bool
     const float L = group_sum<32>(valid ? l * f : 0.f);
     const float V = group_sum<32>(valid ? o * f : 0.f);
     return V * (1.0f / L);
+}
+
+template <int W>
+__device__ __forceinline__ int group_sum_i(int v) {        // exact: integer adds
+    static_assert(W == 16 || W == 32 || W == 64, "group width");
+    v += __builtin_amdgcn_update_dpp(0, v, DPP_QXOR1, 0xf, 0xf, false);
+    v += __builtin_amdgcn_update_dpp(0, v, DPP_QXOR2, 0xf, 0xf, false);
+    v += __builtin_amdgcn_update_dpp(0, v, DPP_HALF_MIRROR, 0xf, 0xf, false);
+    v += __builtin_amdgcn_update_dpp(0, v, DPP_MIRROR, 0xf, 0xf, false);
+    if (W == 16) return v;
+    v += __builtin_amdgcn_update_dpp(0, v, DPP_BCAST15, 0xa, 0xf, false);
+    if (W == 32) {
+        const int lo = __builtin_amdgcn_readlane(v, 31), hi = __builtin_amdgcn_readlane(v, 63);
+        return (threadIdx.x & 32) ? hi : lo;
+    }
+    v += __builtin_amdgcn_update_dpp(0, v, DPP_BCAST31, 0xc, 0xf, false);
+    return __builtin_amdgcn_readlane(v, 63);
+}
+
+// ---- exact int8 activation pieces (every int8 matvec) ----------------------------------
+// An f32 activation vector v is written as one 30-bit integer per element with one
+// power-of-two scale: s = 2^(e-29), 2^e <= m = max|v| < 2^(e+1), Y = rint(v/s), so
+// |Y| <= 2^30 and |v - s*Y| <= s/2 <= m*2^-30 (Y is exact wherever |v| >= m*2^-6, since
+// v/s is then already an integer).  Y is split into four balanced base-256 digits, the
+// bytes of t = Y + 0x80808080 each minus 128 (int8 p0..p3, Y = p0 + 2^8 p1 + 2^16 p2 +
+// 2^24 p3), giving four int8 planes.  Their products with the int8 weights q are summed
+// exactly in int32 (|sum| <= 128*128*K < 2^31 for K < 131072), so the four dot products
+// D0..D3 depend neither on summation order nor on the instruction forming them (MFMA in
+// the fused step, v_dot4 in the matvec kernel).  The dot is
+// s*(D0 + 2^8 D1 + 2^16 D2 + 2^24 D3), formed exactly in f64 and rounded once to f32; the
+// row scale is then applied once in f32 as the reference does
+// (qwen_tts_kernels.c:2350-2351).  m < 2^-90 or not finite: s = 0, every piece 0.
+struct QtPcScale { float s, isc; };
+__device__ __forceinline__ QtPcScale qt_pc_scale(float m) {
+    const bool ok = m >= 0x1p-90f && m <= 3.0e38f;
+    const int e = ok ? ilogbf(m) : 0;
+    return {ok ? ldexpf(1.0f, e - 29) : 0.f, ok ? ldexpf(1.0f, 29 - e) : 0.f};
+}
+// biased word t = Y + 0x80808080 of one value
+__device__ __forceinline__ uint32_t qt_pc_word(float v, float isc) {
+    return (uint32_t)(int)rintf(v * isc) + 0x80808080u;
+}
+// 4x4 byte transpose of four biased words into the four planes of those values (plane
+// q, byte e = digit q of value e, as a signed int8)
+__device__ __forceinline__ void qt_pc_t4(uint32_t t0, uint32_t t1, uint32_t t2, uint32_t t3, uint32_t (&pl)[4]) {
+    const uint32_t a = __builtin_amdgcn_perm(t1, t0, 0x05010400u), b = __builtin_amdgcn_perm(t3, t2, 0x05010400u);
+    const uint32_t c = __builtin_amdgcn_perm(t1, t0, 0x07030602u), d = __builtin_amdgcn_perm(t3, t2, 0x07030602u);
+    pl[0] = __builtin_amdgcn_perm(b, a, 0x05040100u) ^ 0x80808080u;
+    pl[1] = __builtin_amdgcn_perm(b, a, 0x07060302u) ^ 0x80808080u;
+    pl[2] = __builtin_amdgcn_perm(d, c, 0x05040100u) ^ 0x80808080u;
+    pl[3] = __builtin_amdgcn_perm(d, c, 0x07060302u) ^ 0x80808080u;
+}
+// the four planes of 8 consecutive values (plane q: 8 bytes)
+__device__ __forceinline__ void qt_pc8(const float (&v)[8], float isc, uint2 (&pl)[4]) {
+    uint32_t lo[4], hi[4];
+    qt_pc_t4(qt_pc_word(v[0], isc), qt_pc_word(v[1], isc), qt_pc_word(v[2], isc), qt_pc_word(v[3], isc), lo);
+    qt_pc_t4(qt_pc_word(v[4], isc), qt_pc_word(v[5], isc), qt_pc_word(v[6], isc), qt_pc_word(v[7], isc), hi);
+#pragma unroll
+    for (int q = 0; q < 4; q++) pl[q] = make_uint2(lo[q], hi[q]);
+}
+// the four planes of 16 consecutive values (plane q: 16 bytes)
+__device__ __forceinline__ void qt_pc16(const float (&v)[16], float isc, uint4 (&pl)[4]) {
+    uint32_t w[4][4];
+#pragma unroll
+    for (int g = 0; g < 4; g++) {
+        uint32_t t[4];
+        qt_pc_t4(qt_pc_word(v[4 * g], isc), qt_pc_word(v[4 * g + 1], isc), qt_pc_word(v[4 * g + 2], isc),
+                 qt_pc_word(v[4 * g + 3], isc), t);
+#pragma unroll
+        for (int q = 0; q < 4; q++) w[q][g] = t[q];
+    }
+#pragma unroll
+    for (int q = 0; q < 4; q++) pl[q] = make_uint4(w[q][0], w[q][1], w[q][2], w[q][3]);
+}
+// the dot product from the four exact plane sums
+__device__ __forceinline__ float qt_pc_dot(int d0, int d1, int d2, int d3, float s) {
+    const double c = (double)d0 + (double)d1 * 0x1p8 + (double)d2 * 0x1p16 + (double)d3 * 0x1p24;
+    return (float)(c * (double)s);
+}
+// q . p for 16 weight bytes q and 16 piece bytes of one plane
+__device__ __forceinline__ int qt_dot16(uint4 w, uint4 p, int acc) {
+    acc = __builtin_amdgcn_sdot4((int)w.x, (int)p.x, acc, false);
+    acc = __builtin_amdgcn_sdot4((int)w.y, (int)p.y, acc, false);
+    acc = __builtin_amdgcn_sdot4((int)w.z, (int)p.z, acc, false);
+    acc = __builtin_amdgcn_sdot4((int)w.w, (int)p.w, acc, false);
+    return acc;
 }
 
 // Agent-scope relaxed accesses: compiled to global_load/store with the sc1 bit, so they

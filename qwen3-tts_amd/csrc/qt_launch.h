@@ -43,7 +43,6 @@ hipError_t qt_launch_gather(const int *tok, int tok_max, const uint16_t *table, 
 hipError_t qt_launch_copy_f32(const float *src, float *dst, int n, hipStream_t st);
 hipError_t qt_launch_quant_int8(const uint16_t *src, int rows, int cols, uint8_t *dst, float *scale,
                                 hipStream_t st);
-hipError_t qt_launch_flip_sign(uint8_t *p, size_t n, hipStream_t st);
 hipError_t qt_launch_repack_q4(const uint8_t *blocks, size_t nblocks, uint8_t *qs, uint16_t *s16,
                                hipStream_t st);
 hipError_t qt_launch_quant_q4(const uint16_t *src, int rows, int cols, uint8_t *qs, uint16_t *s16,

@@ -7,8 +7,10 @@
 //   RESID   x[r] += acc                       (O and down projections, residual add)
 //   SWIGLU  h[i] = silu(acc[2i]) * acc[2i+1]  (interleaved gate|up rows)
 //   BIAS    y[r] = acc + bias[r]              (CP small_to_mtp_projection)
-// Numerics follow the reference CPU path: f32 activations, f32 accumulation,
-// int8 row scale applied once per row (qwen_tts_kernels.c:2350-2351), q4 block value
+// Numerics follow the reference CPU path: f32 activations, f32 accumulation (bf16,
+// q4_0); int8 weights meet the activation as exact int8 pieces (qt_device.h) summed in
+// int32, so the dot is the exact one to ~2^-27 relative; the int8 row scale is applied
+// once per row (qwen_tts_kernels.c:2350-2351), q4 block value
 // (nib-8)*f16(scale) (qwen_tts_kernels.c:2810-2819), SwiGLU g/(1+expf(-g))*u
 // (qwen_tts_kernels.c:3857-3878), RMSNorm (x*inv)*w (qwen_tts_kernels.c:292-382).
 //
@@ -115,14 +117,42 @@ __global__ __launch_bounds__(QT_WG) void k_mv(QtMvArgs a) {
             xe[j][4 * q + 0] = xv[j][q].x; xe[j][4 * q + 1] = xv[j][q].y;
             xe[j][4 * q + 2] = xv[j][q].z; xe[j][4 * q + 3] = xv[j][q].w;
         }
+    float pc_m = 0.f;       // int8: bound of max|input| for the pieces' scale
     if (NORM) {
         float ss = 0.f;
+        if (PREC == QT_INT8) {
+            // the fused step's order (its gather): virtual thread t = lane + 64 w (w < 4)
+            // accumulates x[t + 256 k]^2 over k, butterfly per w, the four sums in order;
+            // the scale bound is inv * max|x*g| * (1 + 2^-20) (qt_pstep.hip, pc_norm_scale)
+            static_assert(PREC != QT_INT8 || (LPR == 64 && COLS % 256 == 0), "int8 norm order");
+            float mg = 0.f;
 #pragma unroll
-        for (int j = 0; j < CPL; j++)
+            for (int w = 0; w < 4; w++) {
+                float p = 0.f;
 #pragma unroll
-            for (int e = 0; e < EPC; e++) ss = fmaf(xe[j][e], xe[j][e], ss);
-        ss = group_sum<LPR>(ss);
+                for (int k = 0; k < COLS / 256; k++) {
+                    const float v = a.vin[lane + 64 * w + 256 * k];
+                    p = fmaf(v, v, p);
+                }
+                ss = w == 0 ? group_sum<64>(p) : ss + group_sum<64>(p);
+            }
+#pragma unroll
+            for (int j = 0; j < CPL; j++)
+#pragma unroll
+                for (int q = 0; q < EPC / 4; q++) {
+                    mg = fmaxf(mg, fabsf(xv[j][q].x * gv[j][q].x)); mg = fmaxf(mg, fabsf(xv[j][q].y * gv[j][q].y));
+                    mg = fmaxf(mg, fabsf(xv[j][q].z * gv[j][q].z)); mg = fmaxf(mg, fabsf(xv[j][q].w * gv[j][q].w));
+                }
+            pc_m = group_max<LPR>(mg);
+        } else {
+#pragma unroll
+            for (int j = 0; j < CPL; j++)
+#pragma unroll
+                for (int e = 0; e < EPC; e++) ss = fmaf(xe[j][e], xe[j][e], ss);
+            ss = group_sum<LPR>(ss);
+        }
         const float inv = 1.0f / sqrtf(ss / (float)COLS + a.eps);
+        if (PREC == QT_INT8) pc_m = (inv * pc_m) * (1.0f + 0x1p-20f);
 #pragma unroll
         for (int j = 0; j < CPL; j++)
 #pragma unroll
@@ -141,12 +171,36 @@ __global__ __launch_bounds__(QT_WG) void k_mv(QtMvArgs a) {
                         make_float4(xe[j][4 * q], xe[j][4 * q + 1], xe[j][4 * q + 2], xe[j][4 * q + 3]);
         }
     }
-    // operand order of the weight chunk: bf16/int8 natural; q4 word m holds elements
+    // int8: the exact pieces of the (normalised) input; the maximum is a group reduction
+    // (the LPR lanes of a group hold the whole vector), so every group agrees on s
+    uint4 pl[PREC == QT_INT8 ? CPL : 1][4];
+    float pcs = 0.f;
+    if (PREC == QT_INT8) {
+        if (!NORM) {
+            float mx = 0.f;
+#pragma unroll
+            for (int j = 0; j < CPL; j++)
+#pragma unroll
+                for (int e = 0; e < EPC; e++) mx = fmaxf(mx, fabsf(xe[j][e]));
+            pc_m = group_max<LPR>(mx);
+        }
+        const QtPcScale ps = qt_pc_scale(pc_m);
+        pcs = ps.s;
+#pragma unroll
+        for (int j = 0; j < CPL; j++) {
+            float v16[16];
+#pragma unroll
+            for (int e = 0; e < 16; e++) v16[e] = xe[j][e];
+            qt_pc16(v16, ps.isc, pl[j]);
+        }
+    }
+    // operand order of the weight chunk: bf16 natural; q4 word m holds elements
     // 8m..8m+7 with the even ones in the low nibbles
     float xr[CPL][EPC];
     float xsum[CPL];
 #pragma unroll
     for (int j = 0; j < CPL; j++) {
+        if (PREC == QT_INT8) { xsum[j] = 0.f; continue; }
         if (PREC == QT_Q4) {
 #pragma unroll
             for (int m = 0; m < 4; m++)
@@ -170,6 +224,17 @@ __global__ __launch_bounds__(QT_WG) void k_mv(QtMvArgs a) {
     float acc[NR];
 #pragma unroll
     for (int r = 0; r < NR; r++) {
+        if (PREC == QT_INT8) {
+            int d[4] = {0, 0, 0, 0};
+#pragma unroll
+            for (int j = 0; j < CPL; j++)
+#pragma unroll
+                for (int q = 0; q < 4; q++) d[q] = qt_dot16(wv[r][j], pl[j][q], d[q]);
+#pragma unroll
+            for (int q = 0; q < 4; q++) d[q] = group_sum_i<LPR>(d[q]);
+            acc[r] = qt_pc_dot(d[0], d[1], d[2], d[3], pcs);
+            continue;
+        }
         float s = 0.f;
 #pragma unroll
         for (int j = 0; j < CPL; j++) {
@@ -180,17 +245,6 @@ __global__ __launch_bounds__(QT_WG) void k_mv(QtMvArgs a) {
                     s = fmaf(bf_lo(w4[m]), xr[j][2 * m], s);
                     s = fmaf(bf_hi(w4[m]), xr[j][2 * m + 1], s);
                 }
-            } else if (PREC == QT_INT8) {
-                float t = 0.f;
-#pragma unroll
-                for (int m = 0; m < 4; m++) {
-                    const uint32_t w = w4[m];
-                    t = fmaf((float)(w & 0xFFu), xr[j][4 * m + 0], t);
-                    t = fmaf((float)((w >> 8) & 0xFFu), xr[j][4 * m + 1], t);
-                    t = fmaf((float)((w >> 16) & 0xFFu), xr[j][4 * m + 2], t);
-                    t = fmaf((float)(w >> 24), xr[j][4 * m + 3], t);
-                }
-                s += fmaf(-128.0f, xsum[j], t);
             } else {
                 float t = 0.f;
 #pragma unroll
@@ -261,6 +315,18 @@ __global__ __launch_bounds__(QT_WG) void k_mv_generic(QtMvArgs a) {
         }
     }
     __syncthreads();
+    QtPcScale ps = {0.f, 0.f};
+    if (PREC == QT_INT8) {          // scale of the exact pieces: block maximum of |x|
+        float mx = 0.f;
+        for (int i = threadIdx.x; i < cols; i += QT_WG) mx = fmaxf(mx, fabsf(xs[i]));
+        mx = group_max<64>(mx);
+        if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = mx;
+        __syncthreads();
+        mx = 0.f;
+#pragma unroll
+        for (int i = 0; i < QT_WAVES; i++) mx = fmaxf(mx, red[i]);
+        ps = qt_pc_scale(mx);
+    }
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int per = (EPI == QT_EPI_SWIGLU) ? 2 : 1;
     const int row0 = (blockIdx.x * QT_WAVES + wave) * per;
@@ -268,13 +334,24 @@ __global__ __launch_bounds__(QT_WG) void k_mv_generic(QtMvArgs a) {
     for (int r = 0; r < per; r++) {
         const int row = row0 + r;
         if (row >= rows) break;
+        if (PREC == QT_INT8) {
+            int d[4] = {0, 0, 0, 0};
+            for (int k = lane; k < cols; k += 64) {
+                const int q = (int)(int8_t)a.M.w[(size_t)row * cols + k];
+                const uint32_t t = qt_pc_word(xs[k], ps.isc);
+#pragma unroll
+                for (int i = 0; i < 4; i++) d[i] += q * ((int)((t >> (8 * i)) & 0xFFu) - 128);
+            }
+#pragma unroll
+            for (int q = 0; q < 4; q++) d[q] = group_sum_i<64>(d[q]);
+            acc[r] = qt_pc_dot(d[0], d[1], d[2], d[3], ps.s) * a.M.scale[row];
+            continue;
+        }
         float s = 0.f;
         for (int k = lane; k < cols; k += 64) {
             float w;
             if (PREC == QT_BF16) {
                 w = bf16f(reinterpret_cast<const uint16_t *>(a.M.w)[(size_t)row * cols + k]);
-            } else if (PREC == QT_INT8) {
-                w = (float)((int)a.M.w[(size_t)row * cols + k] - 128);
             } else {
                 const uint8_t byte = a.M.w[(size_t)row * (cols / 2) + k / 2];
                 const int nib = (k & 1) ? (byte >> 4) : (byte & 0xF);
@@ -282,9 +359,7 @@ __global__ __launch_bounds__(QT_WG) void k_mv_generic(QtMvArgs a) {
             }
             s = fmaf(w, xs[k], s);
         }
-        s = group_sum<64>(s);
-        if (PREC == QT_INT8) s *= a.M.scale[row];
-        acc[r] = s;
+        acc[r] = group_sum<64>(s);
     }
     if (lane == 0) {
         if (EPI == QT_EPI_SWIGLU) {

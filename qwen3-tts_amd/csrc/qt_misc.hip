@@ -190,23 +190,12 @@ __global__ __launch_bounds__(QT_WG) void k_quant_int8(const uint16_t *src, int c
         const float p = bf16f(row[k]) * inv;
         int v = (k < body) ? (int)__builtin_rintf(p) : (int)roundf(p);
         v = v < -128 ? -128 : (v > 127 ? 127 : v);
-        dst[(size_t)blockIdx.x * cols + k] = (uint8_t)((v & 0xFF) ^ 0x80);
+        dst[(size_t)blockIdx.x * cols + k] = (uint8_t)(v & 0xFF);
     }
 }
 extern "C" hipError_t qt_launch_quant_int8(const uint16_t *src, int rows, int cols, uint8_t *dst, float *scale,
                                            hipStream_t st) {
     hipLaunchKernelGGL(k_quant_int8, dim3(rows), dim3(QT_WG), 0, st, src, cols, dst, scale);
-    return hipGetLastError();
-}
-
-// Reference int8 bytes q -> device encoding q ^ 0x80 (n bytes, in place).
-__global__ void k_flip_sign(uint8_t *p, size_t n) {
-    size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
-    size_t stride = (size_t)gridDim.x * blockDim.x;
-    for (; i < n; i += stride) p[i] ^= 0x80;
-}
-extern "C" hipError_t qt_launch_flip_sign(uint8_t *p, size_t n, hipStream_t st) {
-    hipLaunchKernelGGL(k_flip_sign, dim3(1024), dim3(256), 0, st, p, n);
     return hipGetLastError();
 }
 
@@ -294,7 +283,7 @@ __global__ void k_dequant(int prec, const uint8_t *w, const float *scale, const 
         const int r = r0 + (int)(i / cols), k = (int)(i % cols);
         float v;
         if (prec == QT_BF16) v = bf16f(reinterpret_cast<const uint16_t *>(w)[(size_t)r * cols + k]);
-        else if (prec == QT_INT8) v = (float)((int)w[(size_t)r * cols + k] - 128) * scale[r];
+        else if (prec == QT_INT8) v = (float)(int)(int8_t)w[(size_t)r * cols + k] * scale[r];
         else {
             const uint8_t byte = w[(size_t)r * (cols / 2) + k / 2];
             const int nib = (k & 1) ? (byte >> 4) : (byte & 0xF);

@@ -41,6 +41,7 @@
 // Every wait is bounded: on timeout the kernel sets an error flag, the others see it
 // and stop waiting, and the launch runs to its end.
 #include "qt_device.h"
+#include <type_traits>
 
 namespace ps {
 constexpr int NB = 256;          // workgroups (one per CU)
@@ -184,8 +185,34 @@ struct PosChunk { __device__ __forceinline__ int operator()(int i) const { retur
 // (Issuing the next phase's weight loads between the first reads and their check, so
 // the issue overlaps the first round trip, was measured 30 % slower per step than
 // issuing them before the gather.)
+// Statistics for the int8 pieces, per wave into wst[2*wave], wst[2*wave+1] (read after
+// the gather's barrier): gains == nullptr: max|x|; else the RMSNorm partial sum of
+// squares (thread t: x[t + NT k]^2 accumulated in k order, then the wave's butterfly)
+// and max|x*g| over the thread's elements.
+template <int K, int NT, typename PosF>
+__device__ __forceinline__ void pc_stats(const float (&x)[K], int n, const float *gains, PosF pos, float *wst) {
+    const int tid = threadIdx.x;
+    float ss = 0.f, m = 0.f;
+#pragma unroll
+    for (int k = 0; k < K; k++) {
+        const int i = tid + k * NT;
+        if (i < n) {
+            if (gains) {
+                ss = fmaf(x[k], x[k], ss);
+                m = fmaxf(m, fabsf(x[k] * gains[pos(i)]));
+            } else {
+                m = fmaxf(m, fabsf(x[k]));
+            }
+        }
+    }
+    if (gains) ss = group_sum<64>(ss);
+    m = group_max<64>(m);
+    if ((tid & 63) == 0) { wst[2 * (tid >> 6)] = ss; wst[2 * (tid >> 6) + 1] = m; }
+}
+
 template <int K, int NT, typename AddrF, typename PosF = PosId>
-__device__ __forceinline__ void gather(int n, AddrF addr, float *dst, unsigned tag, int *err, PosF pos = PosF()) {
+__device__ __forceinline__ void gather(int n, AddrF addr, float *dst, unsigned tag, int *err, PosF pos = PosF(),
+                                       float *wst = nullptr, const float *gains = nullptr) {
     const int tid = threadIdx.x;
     unsigned long long v[K];
 #pragma unroll
@@ -213,6 +240,12 @@ __device__ __forceinline__ void gather(int n, AddrF addr, float *dst, unsigned t
     for (int k = 0; k < K; k++) {
         const int i = tid + k * NT;
         if (i < n) dst[pos(i)] = val_of(v[k]);
+    }
+    if (wst) {      // int8 pieces: per-wave statistics
+        float x[K];
+#pragma unroll
+        for (int k = 0; k < K; k++) x[k] = val_of(v[k]);
+        pc_stats<K, NT>(x, n, gains, pos, wst);
     }
     __syncthreads();
 }
@@ -250,12 +283,13 @@ struct Tile {
     }
 };
 
-// acc[r] = dot(row r, x) for the tile's rows, x read from LDS chunk by chunk (so no
-// activation slice occupies registers), reduced over the wave (valid in every lane).
-// xs[c] = sum of the 16 elements of chunk c (int8 only: folds the u8 offset).  Same
-// arithmetic, in the same order, as k_mv in qt_matvec.hip.
+// acc[r] = dot(row r, x) for the tile's rows (bf16 weights; int8 projections use the
+// exact pieces below), x read from LDS chunk by chunk (so no activation slice occupies
+// registers), reduced over the wave (valid in every lane).  Same arithmetic, in the same
+// order, as k_mv in qt_matvec.hip.
 template <int PREC, int COLS, int NR>
-__device__ __forceinline__ void tile_dot(const Tile<PREC, COLS, NR> &t, const float *x, const float *xs, float (&acc)[NR]) {
+__device__ __forceinline__ void tile_dot(const Tile<PREC, COLS, NR> &t, const float *x, float (&acc)[NR]) {
+    static_assert(PREC == QT_BF16, "int8 projections take the exact activation pieces");
     using T = Tile<PREC, COLS, NR>;
     constexpr int EPC = T::EPC;
     const int lane = threadIdx.x & 63;
@@ -271,27 +305,13 @@ __device__ __forceinline__ void tile_dot(const Tile<PREC, COLS, NR> &t, const fl
             const float4 v = xchunk4<EPC, COLS>(x, ci, q);
             xv[4 * q] = v.x; xv[4 * q + 1] = v.y; xv[4 * q + 2] = v.z; xv[4 * q + 3] = v.w;
         }
-        const float xsj = PREC == QT_INT8 ? xs[ci] : 0.f;
 #pragma unroll
         for (int r = 0; r < NR; r++) {
             const uint32_t w4[4] = {t.w[r][j].x, t.w[r][j].y, t.w[r][j].z, t.w[r][j].w};
-            if (PREC == QT_BF16) {
 #pragma unroll
-                for (int m = 0; m < 4; m++) {
-                    s[r] = fmaf(bf_lo(w4[m]), xv[2 * m], s[r]);
-                    s[r] = fmaf(bf_hi(w4[m]), xv[2 * m + 1], s[r]);
-                }
-            } else {
-                float u = 0.f;
-#pragma unroll
-                for (int m = 0; m < 4; m++) {
-                    const uint32_t w = w4[m];
-                    u = fmaf((float)(w & 0xFFu), xv[4 * m + 0], u);
-                    u = fmaf((float)((w >> 8) & 0xFFu), xv[4 * m + 1], u);
-                    u = fmaf((float)((w >> 16) & 0xFFu), xv[4 * m + 2], u);
-                    u = fmaf((float)(w >> 24), xv[4 * m + 3], u);
-                }
-                s[r] += fmaf(-128.0f, xsj, u);
+            for (int m = 0; m < 4; m++) {
+                s[r] = fmaf(bf_lo(w4[m]), xv[2 * m], s[r]);
+                s[r] = fmaf(bf_hi(w4[m]), xv[2 * m + 1], s[r]);
             }
         }
     }
@@ -313,12 +333,12 @@ __device__ __forceinline__ void load_gains(const float *src, float *dst) {
     }
 }
 
-// xn = RMSNorm(x) * g into LDS, plus the int8 chunk sums xs.  The mean square is
-// accumulated exactly as k_mv does (lane l over chunks l + 64 j in element order, then
-// a wave butterfly), by every wave redundantly, so no extra barrier is needed; then
-// thread c normalises chunk c.  Ends with a workgroup barrier.
+// xn = RMSNorm(x) * g into LDS (bf16 layers, the codec head).  The mean square is
+// accumulated exactly as k_mv does (lane l over chunks l + 64 j in element order, then a
+// wave butterfly), by every wave redundantly, so no extra barrier is needed; then thread
+// c normalises chunk c.  Ends with a workgroup barrier.
 template <int PREC, int COLS>
-__device__ __forceinline__ void stage_norm(const float *x, const float *gain, float eps, float *xn, float *xs) {
+__device__ __forceinline__ void stage_norm(const float *x, const float *gain, float eps, float *xn) {
     constexpr int EPC = Epc<PREC>::v, CPL = COLS / (EPC * 64);
     const int lane = threadIdx.x & 63, c = threadIdx.x;
     float ss = 0.f;
@@ -332,34 +352,276 @@ __device__ __forceinline__ void stage_norm(const float *x, const float *gain, fl
     ss = group_sum<64>(ss);
     const float inv = 1.0f / sqrtf(ss / (float)COLS + eps);
     if (c * EPC < COLS) {
-        float sum = 0.f;
 #pragma unroll
         for (int q = 0; q < EPC / 4; q++) {
             const float4 xv = xchunk4<EPC, COLS>(x, c, q), gv = xchunk4<EPC, COLS>(gain, c, q);
             const float4 v = make_float4((xv.x * inv) * gv.x, (xv.y * inv) * gv.y, (xv.z * inv) * gv.z, (xv.w * inv) * gv.w);
             *reinterpret_cast<float4 *>(xn + (q * (COLS / EPC) + c) * 4) = v;
-            sum += v.x; sum += v.y; sum += v.z; sum += v.w;
         }
-        if (PREC == QT_INT8) xs[c] = sum;
     }
     __syncthreads();
 }
 
-// int8 chunk sums of an activation that is not normalised (inputs of W_o and W_dn)
-template <int PREC, int COLS, int NT>
-__device__ __forceinline__ void stage_sums(const float *x, float *xs) {
-    constexpr int EPC = Epc<PREC>::v;
-    if (PREC != QT_INT8) return;
-    for (int c = threadIdx.x; c * EPC < COLS; c += NT) {
-        float sum = 0.f;
+// ---- int8: exact activation pieces and integer dot products -------------------------------
+// Every int8 projection takes its input as the four exact int8 planes of qt_device.h
+// (qt_pc8, one power-of-two scale per vector), so the dot products are exact int32 sums
+// whatever forms them; the per-kernel matvec (qt_matvec.hip) computes the same integers
+// with v_dot4 and the same f64 combination, so the two paths agree to the bit.
+//
+// Pieces live in LDS, 16 bytes per (16-element chunk c, plane q).  Two layouts:
+//  plane-major  q*COLS + 16c: a wave reading plane q of chunks lane + 64j reads one
+//               contiguous KiB (the v_dot4 path, one chunk per lane);
+//  swizzled     the 64-byte group of chunk c inside its 256-byte block is XORed with the
+//               block index, so the 16 lanes of an MFMA B-operand read (4 parts x 4 planes,
+//               parts 4 chunks apart) hit 16 different 16-byte bank groups.
+template <bool SW, int COLS>
+__device__ __forceinline__ int pc_off(int c, int q) {
+    if (SW) return ((c >> 2) << 8) | ((((c & 3) ^ ((c >> 2) & 3))) << 6) | (q << 4);
+    return q * COLS + 16 * c;
+}
+
+// Pieces are made in units of 8 elements (half a 16-element chunk): unit u is half u % 2
+// of chunk u / 2, read as two float4 of the chunk-transposed activation and written as
+// 8 bytes of each plane.
+template <bool SW, int COLS>
+__device__ __forceinline__ void pc_put8(uint8_t *pc, int u, const float (&v)[8], float isc) {
+    uint2 pl[4];
+    qt_pc8(v, isc, pl);
 #pragma unroll
-        for (int q = 0; q < EPC / 4; q++) {
-            const float4 v = xchunk4<EPC, COLS>(x, c, q);
-            sum += v.x; sum += v.y; sum += v.z; sum += v.w;
+    for (int q = 0; q < 4; q++) *reinterpret_cast<uint2 *>(pc + pc_off<SW, COLS>(u >> 1, q) + 8 * (u & 1)) = pl[q];
+}
+
+// Pieces of RMSNorm(x)*g (A, D) from the gather's statistics (pc_stats): the mean square
+// is the waves' partial sums added in wave order, and the scale comes from
+// M = inv * max|x*g| * (1 + 2^-20), an upper bound of max|(x*inv)*g| (two f32 roundings
+// lie far inside the margin).  k_mv forms both the same way.  Thread u normalises unit u
+// and writes its planes.  Returns s; ends with a barrier.
+template <int NW>
+__device__ __forceinline__ void pc_norm_scale(const float *wst, int cols, float eps, float &inv, QtPcScale &ps) {
+    float ss = wst[0], m = wst[1];
+#pragma unroll
+    for (int w = 1; w < NW; w++) { ss += wst[2 * w]; m = fmaxf(m, wst[2 * w + 1]); }
+    inv = 1.0f / sqrtf(ss / (float)cols + eps);
+    ps = qt_pc_scale((inv * m) * (1.0f + 0x1p-20f));
+}
+template <bool SW, int COLS, int NT>
+__device__ __forceinline__ float stage_norm_pc(const float *x, const float *gain, float eps, uint8_t *pc, const float *wst) {
+    constexpr int EPC = 16, NU = COLS / 8;
+    float inv;
+    QtPcScale ps;
+    pc_norm_scale<NT / 64>(wst, COLS, eps, inv, ps);
+    for (int u = threadIdx.x; u < NU; u += NT) {
+        float v[8];
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+            const float4 xv = xchunk4<EPC, COLS>(x, u >> 1, 2 * (u & 1) + h);
+            const float4 g = xchunk4<EPC, COLS>(gain, u >> 1, 2 * (u & 1) + h);
+            v[4 * h] = (xv.x * inv) * g.x; v[4 * h + 1] = (xv.y * inv) * g.y;
+            v[4 * h + 2] = (xv.z * inv) * g.z; v[4 * h + 3] = (xv.w * inv) * g.w;
         }
-        xs[c] = sum;
+        pc_put8<SW, COLS>(pc, u, v, ps.isc);
     }
     __syncthreads();
+    return ps.s;
+}
+
+// Pieces of x (C, E): m = max|x| from the gather's statistics.  Returns s; ends with a
+// barrier.
+template <bool SW, int COLS, int NT>
+__device__ __forceinline__ float stage_pc(const float *x, const float *wst, uint8_t *pc) {
+    constexpr int EPC = 16, NU = COLS / 8;
+    float m = wst[1];
+#pragma unroll
+    for (int w = 1; w < NT / 64; w++) m = fmaxf(m, wst[2 * w + 1]);
+    const QtPcScale ps = qt_pc_scale(m);
+    for (int u = threadIdx.x; u < NU; u += NT) {
+        float v[8];
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+            const float4 xv = xchunk4<EPC, COLS>(x, u >> 1, 2 * (u & 1) + h);
+            v[4 * h] = xv.x; v[4 * h + 1] = xv.y; v[4 * h + 2] = xv.z; v[4 * h + 3] = xv.w;
+        }
+        pc_put8<SW, COLS>(pc, u, v, ps.isc);
+    }
+    __syncthreads();
+    return ps.s;
+}
+
+// v_dot4 path (rows per wave, lanes over chunks, plane-major pieces): acc[r] = the dot of
+// row r (valid in every lane), before the row scale.
+template <int COLS, int NR>
+__device__ __forceinline__ void tile_dot_pc(const Tile<QT_INT8, COLS, NR> &t, const uint8_t *pc, float s, float (&acc)[NR]) {
+    using T = Tile<QT_INT8, COLS, NR>;
+    const int lane = threadIdx.x & 63;
+    int d[NR][4];
+#pragma unroll
+    for (int r = 0; r < NR; r++)
+#pragma unroll
+        for (int q = 0; q < 4; q++) d[r][q] = 0;
+#pragma unroll
+    for (int j = 0; j < T::CPL; j++) {
+        const int c = lane + 64 * j;
+        uint4 p[4];
+#pragma unroll
+        for (int q = 0; q < 4; q++) p[q] = *reinterpret_cast<const uint4 *>(pc + pc_off<false, COLS>(c, q));
+#pragma unroll
+        for (int r = 0; r < NR; r++)
+#pragma unroll
+            for (int q = 0; q < 4; q++) d[r][q] = qt_dot16(t.w[r][j], p[q], d[r][q]);
+    }
+#pragma unroll
+    for (int r = 0; r < NR; r++) {
+#pragma unroll
+        for (int q = 0; q < 4; q++) d[r][q] = group_sum_i<64>(d[r][q]);
+        acc[r] = qt_pc_dot(d[r][0], d[r][1], d[r][2], d[r][3], s);
+    }
+}
+
+// MFMA path (hidden 2048).  v_mfma_i32_16x16x64_i8 (wave64): lane l supplies 16 bytes of
+// A row (l % 16) and of B column (l % 16) for k group kg = l / 16, and receives D rows
+// 4*(l/16)+i (i < 4) of column l % 16.
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ i32x4 mfma_i8(uint4 w, uint4 p, i32x4 acc) {
+    const i32x4 A = i32x4{(int)w.x, (int)w.y, (int)w.z, (int)w.w};
+    const i32x4 B = i32x4{(int)p.x, (int)p.y, (int)p.z, (int)p.w};
+    return __builtin_amdgcn_mfma_i32_16x16x64_i8(A, B, acc, 0, 0, 0);
+}
+
+// 4 rows per wave (the wave's rows row0w..row0w+3) over all COLS: MFMA row m = row m % 4
+// of part m / 4; step s covers columns s*256 + part*64 + 16*kg .. +15, so one load
+// instruction reads 256 contiguous bytes of each of the 4 rows.  B column n = plane n % 4
+// of part n / 4.  D[4p+j][4p+q] (lane 20p+q, register j) is the part-p, plane-q sum of
+// row j.
+// Row scales are loaded per lane for the lanes that finish the rows (a lane-dependent
+// pick among wave-uniform values would make the compiler index an array in scratch):
+// PAIR = false: rs[0] = scale of row lane % 4; PAIR = true (gate|up pieces): rs[0], rs[1] =
+// scales of rows 2i, 2i+1 with i = lane % 2.
+template <int COLS, bool PAIR>
+struct TileM4 {
+    static constexpr int S = COLS / 256;
+    static_assert(S * 256 == COLS, "tile shape");
+    uint4 w[S];
+    float rs[2];
+    __device__ __forceinline__ void load(const uint8_t *W, const float *Sc, int row0w) {
+        const int lane = threadIdx.x & 63, m = lane & 15, kg = lane >> 4;
+        W = uni(W);
+        const uint8_t *p = W + (size_t)(row0w + (m & 3)) * COLS + (m >> 2) * 64 + kg * 16;
+#pragma unroll
+        for (int s = 0; s < S; s++) w[s] = ldg(reinterpret_cast<const uint4 *>(p + s * 256));
+        if (PAIR) {
+            rs[0] = ldg(Sc + row0w + 2 * (lane & 1));
+            rs[1] = ldg(Sc + row0w + 2 * (lane & 1) + 1);
+        } else {
+            rs[0] = ldg(Sc + row0w + (lane & 3));
+            rs[1] = 0.f;
+        }
+    }
+};
+// The B fragment of step s is read one step ahead; a single tile alternates two
+// accumulator chains (summed exactly at the end), three tiles share each B fragment.
+template <int COLS>
+__device__ __forceinline__ uint4 mf_b4(const uint8_t *pc, int s) {
+    const int lane = threadIdx.x & 63, n = lane & 15, kg = lane >> 4;
+    return *reinterpret_cast<const uint4 *>(pc + pc_off<true, COLS>(16 * s + 4 * (n >> 2) + kg, n & 3));
+}
+template <int COLS, bool PAIR>
+__device__ __forceinline__ i32x4 mf_dot4(const TileM4<COLS, PAIR> &t, const uint8_t *pc) {
+    constexpr int S = TileM4<COLS, PAIR>::S;
+    i32x4 acc[2] = {i32x4{0, 0, 0, 0}, i32x4{0, 0, 0, 0}};
+    uint4 b = mf_b4<COLS>(pc, 0);
+#pragma unroll
+    for (int s = 0; s < S; s++) {
+        const uint4 bn = mf_b4<COLS>(pc, s + 1 < S ? s + 1 : s);
+        acc[s & 1] = mfma_i8(t.w[s], b, acc[s & 1]);
+        b = bn;
+    }
+    return acc[0] + acc[1];
+}
+template <int COLS, bool PAIR>
+__device__ __forceinline__ void mf_dot4x3(const TileM4<COLS, PAIR> &t0, const TileM4<COLS, PAIR> &t1,
+                                          const TileM4<COLS, PAIR> &t2, const uint8_t *pc, i32x4 (&acc)[3]) {
+    constexpr int S = TileM4<COLS, PAIR>::S;
+#pragma unroll
+    for (int i = 0; i < 3; i++) acc[i] = i32x4{0, 0, 0, 0};
+    uint4 b = mf_b4<COLS>(pc, 0);
+#pragma unroll
+    for (int s = 0; s < S; s++) {
+        const uint4 bn = mf_b4<COLS>(pc, s + 1 < S ? s + 1 : s);
+        acc[0] = mfma_i8(t0.w[s], b, acc[0]);
+        acc[1] = mfma_i8(t1.w[s], b, acc[1]);
+        acc[2] = mfma_i8(t2.w[s], b, acc[2]);
+        b = bn;
+    }
+}
+// Part sums of a TileM4 result through 64 ints of the wave's own LDS scratch: the 16
+// lanes that hold same-part entries store them (mf_store4); then any lane may sum row j's
+// four parts per plane (mf_rowsum).  One wave writes and reads its own scratch, in order.
+__device__ __forceinline__ void mf_store4(i32x4 acc, int *red) {
+    const int lane = threadIdx.x & 63, n = lane & 15, g = lane >> 4;
+    if ((n >> 2) == g) *reinterpret_cast<i32x4 *>(red + (g * 4 + (n & 3)) * 4) = acc;
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+}
+__device__ __forceinline__ void mf_rowsum(const int *red, int j, int (&d)[4]) {
+#pragma unroll
+    for (int q = 0; q < 4; q++)
+        d[q] = red[(0 * 4 + q) * 4 + j] + red[(1 * 4 + q) * 4 + j] + red[(2 * 4 + q) * 4 + j] + red[(3 * 4 + q) * 4 + j];
+}
+
+// 8 rows per workgroup (row0..row0+7) with the columns split over the 4 waves (wave w:
+// columns w*COLS/4 ..): MFMA row m = row m % 8 of part m / 8; step s covers slice
+// columns s*128 + part*64 + 16*kg.  B column n < 8 = plane n % 4 of part n / 4.  The
+// useful entries D[8p+r][4p+q] sit in lanes 16*(2p + r/4) + 4p + q, register r % 4.
+template <int COLS>
+struct TileK8 {
+    static constexpr int S = COLS / 512;
+    static_assert(S * 512 == COLS, "tile shape");
+    uint4 w[S];
+    float rs;                // lane t < 8: scale of row row0 + t
+    __device__ __forceinline__ void load(const uint8_t *W, const float *Sc, int row0, int wave) {
+        const int lane = threadIdx.x & 63, m = lane & 15, kg = lane >> 4;
+        W = uni(W);
+        const uint8_t *p = W + (size_t)(row0 + (m & 7)) * COLS + wave * (COLS / 4) + (m >> 3) * 64 + kg * 16;
+#pragma unroll
+        for (int s = 0; s < S; s++) w[s] = ldg(reinterpret_cast<const uint4 *>(p + s * 128));
+        rs = ldg(Sc + row0 + (lane & 7));
+    }
+};
+template <int COLS>
+__device__ __forceinline__ uint4 mf_b8(const uint8_t *pc, int wave, int s) {
+    const int lane = threadIdx.x & 63, n = lane & 15, kg = lane >> 4;
+    uint4 b = make_uint4(0, 0, 0, 0);
+    if (n < 8) b = *reinterpret_cast<const uint4 *>(pc + pc_off<true, COLS>(wave * (COLS / 64) + 8 * s + 4 * (n >> 2) + kg, n & 3));
+    return b;
+}
+template <int COLS>
+__device__ __forceinline__ i32x4 mf_dot8(const TileK8<COLS> &t, const uint8_t *pc, int wave) {
+    constexpr int S = TileK8<COLS>::S;
+    i32x4 acc[2] = {i32x4{0, 0, 0, 0}, i32x4{0, 0, 0, 0}};
+    uint4 b = mf_b8<COLS>(pc, wave, 0);
+#pragma unroll
+    for (int s = 0; s < S; s++) {
+        const uint4 bn = mf_b8<COLS>(pc, wave, s + 1 < S ? s + 1 : s);
+        acc[s & 1] = mfma_i8(t.w[s], b, acc[s & 1]);
+        b = bn;
+    }
+    return acc[0] + acc[1];
+}
+// Cross-wave sum of TileK8 results: each wave stores its 16 useful lanes into red[wave]
+// (64 ints), barrier, then thread t < 8 sums row t over waves and parts per plane.
+template <int NW>
+__device__ __forceinline__ void mf_rows8(i32x4 acc, int *red, int wave, int (&d)[4]) {
+    const int lane = threadIdx.x & 63, n = lane & 15, g = lane >> 4;
+    if (n < 8 && (n >> 2) == (g >> 1)) *reinterpret_cast<i32x4 *>(red + wave * 64 + (g * 4 + (n & 3)) * 4) = acc;
+    __syncthreads();
+    const int t = threadIdx.x & 7, rh = t >> 2, i = t & 3;
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+        int v = 0;
+#pragma unroll
+        for (int w = 0; w < NW; w++) v += red[w * 64 + (rh * 4 + q) * 4 + i] + red[w * 64 + ((2 + rh) * 4 + q) * 4 + i];
+        d[q] = v;
+    }
 }
 
 // ---- ring layout (tagged words) -----------------------------------------------------------
@@ -395,11 +657,17 @@ __global__ __launch_bounds__(NW * 64, 1) void k_pstep(Args a) {
     constexpr int RPW_HEAD = (HEADR + NW - 1) / NW;   // 3 (NW 4) or 2 (NW 8; waves 6, 7 idle)
     static_assert(RPW_QKV >= 1 && RPW_O >= 1 && RPW_DN >= 1 && RPW_QKV * NB * NW == QKVR && RPW_O * NB * NW == H &&
                   RPW_GU * NB * NW == 2 * F && RPW_DN * NB * NW == H, "row split");
-    using TQKV = Tile<PREC, H, RPW_QKV>;
-    using TO = Tile<PREC, QD, RPW_O>;
+    // int8: exact activation pieces (PI); at hidden 2048 the dots run on MFMA (MF), with
+    // 4 rows per wave for q|k|v and gate|up and 8 rows per workgroup split over the waves'
+    // column slices for O and down
+    constexpr bool PI = PREC == QT_INT8;
+    constexpr bool MF = PI && H == 2048 && NW == 4;
     constexpr int RGU = RPW_GU / 3;                // gate|up rows per piece (4 or 2)
-    using TGU = Tile<PREC, H, RGU>;
-    using TDN = Tile<PREC, F, RPW_DN>;
+    static_assert(!MF || (RPW_QKV == 4 && RGU == 4 && H / NB == 8), "MFMA tile shapes");
+    using TQKV = std::conditional_t<MF, TileM4<H, false>, Tile<PREC, H, RPW_QKV>>;
+    using TO = std::conditional_t<MF, TileK8<QD>, Tile<PREC, QD, RPW_O>>;
+    using TGU = std::conditional_t<MF, TileM4<H, true>, Tile<PREC, H, RGU>>;
+    using TDN = std::conditional_t<MF, TileK8<F>, Tile<PREC, F, RPW_DN>>;
     using THEAD = Tile<QT_BF16, H, RPW_HEAD>;
     using R = Ring<H, F>;
     static_assert(RPW_GU % 3 == 0 && RGU % 2 == 0, "gate/up pairs stay in one piece");
@@ -409,7 +677,6 @@ __global__ __launch_bounds__(NW * 64, 1) void k_pstep(Args a) {
     __shared__ __align__(16) float s_x[H];       // layer input (kept for C's residual)
     __shared__ __align__(16) float s_xa[H];      // post-attention residual (kept for E)
     __shared__ __align__(16) float s_xn[H];      // RMS-normalised input of A / D / head
-    __shared__ __align__(16) float s_xs[(F > QD ? F : QD) / 16];   // int8 chunk sums
     __shared__ __align__(16) float s_qkv[HPK * HD + 2 * HD];
     __shared__ __align__(16) AttLds<HPK> att;                 // attention chunk (B), merge input (M)
     __shared__ float wbest_v[NW];
@@ -421,6 +688,13 @@ __global__ __launch_bounds__(NW * 64, 1) void k_pstep(Args a) {
     static_assert((F > QD ? F : QD) * 4 <= 2 * KVB * HD * 2, "s_in fits the K/V buffer");
     float *const s_in = reinterpret_cast<float *>(&s_kv[0][0]);
     __shared__ __align__(16) float s_gain[2][H];                  // norm gains: [0] input (A), [1] post (D) / final
+    // int8 pieces: A's in the s_xn space (unused by int8 layers), C/D/E's in the second
+    // half of the K/V buffer (free from C until the next layer's K/V copy after E)
+    static_assert(4 * H <= H * 4 && 32768 + 4 * (F > QD ? F : QD) <= 2 * KVB * HD * 2, "pieces fit");
+    uint8_t *const pcA = reinterpret_cast<uint8_t *>(s_xn);
+    uint8_t *const pcB = reinterpret_cast<uint8_t *>(&s_kv[0][0]) + 32768;
+    __shared__ __align__(16) int s_red[PI ? NW * 3 * 64 : 1];     // MFMA part sums
+    __shared__ float s_wst[2 * NW];                               // per-wave statistics of a gather (pieces)
     PS_TRACE_LDS
 
     const int b = blockIdx.x, tid = threadIdx.x, lane = tid & 63;
@@ -455,6 +729,7 @@ __global__ __launch_bounds__(NW * 64, 1) void k_pstep(Args a) {
     TQKV tq;
     tq.load(s_layers[0].w[0], s_layers[0].s[0], rw_qkv);
     load_gains<NW, EP, H>(s_layers[0].in_norm, s_gain[0]);
+
 
     for (int step = 0; step < a.n_steps; step++) {
         const int par = step & 1;
@@ -502,18 +777,45 @@ __global__ __launch_bounds__(NW * 64, 1) void k_pstep(Args a) {
             // ---------------- A: q|k|v rows -----------------
             if (l > 0) {
                 const unsigned long long *src = ring.blk(par, l - 1) + R::OX;
-                gather<H / NT, NT>(H, [&](int i) { return src + i; }, s_x, tag, a.err, PH());
+                gather<H / NT, NT>(H, [&](int i) { return src + i; }, s_x, tag, a.err, PH(), PI ? s_wst : nullptr, s_gain[0]);
             } else {
-                for (int i = tid; i < H; i += NT)
-                    s_x[xpos<EP, H>(i)] = tok < 0 ? ldg(a.xin + i) : bf16f(ldg(a.emb + (size_t)tok * H + i));
+                float xv[H / NT];
+#pragma unroll
+                for (int k = 0; k < H / NT; k++) {
+                    const int i = tid + k * NT;
+                    xv[k] = tok < 0 ? ldg(a.xin + i) : bf16f(ldg(a.emb + (size_t)tok * H + i));
+                    s_x[xpos<EP, H>(i)] = xv[k];
+                }
+                if (PI) {
+                    __syncthreads();                 // the gains' LDS copy has landed for every wave
+                    pc_stats<H / NT, NT>(xv, H, s_gain[0], PH(), s_wst);
+                }
                 __syncthreads();
             }
             PS_MARK(ph, 0);
-            {
-                stage_norm<PREC, H>(s_x, s_gain[0], a.eps, s_xn, s_xs);
+            if constexpr (MF) {
+                const float sA = stage_norm_pc<true, H, NT>(s_x, s_gain[0], a.eps, pcA, s_wst);
+                PS_MARK(ph, 2);
+                int d[4];
+                mf_store4(mf_dot4(tq, pcA), s_red + wave * 192);
+                mf_rowsum(s_red + wave * 192, lane & 3, d);
+                if (lane < 4)
+                    st_tag(blk + R::OQKV + rw_qkv + lane, __fmul_rn(qt_pc_dot(d[0], d[1], d[2], d[3], sA), tq.rs[0]), tag);
+                PS_MARK(ph, 3);
+            } else if constexpr (PI) {
+                const float sA = stage_norm_pc<false, H, NT>(s_x, s_gain[0], a.eps, pcA, s_wst);
                 PS_MARK(ph, 2);
                 float acc[RPW_QKV];
-                tile_dot<PREC, H, RPW_QKV>(tq, s_xn, s_xs, acc);
+                tile_dot_pc<H, RPW_QKV>(tq, pcA, sA, acc);
+#pragma unroll
+                for (int r = 0; r < RPW_QKV; r++)
+                    if (lane == r) st_tag(blk + R::OQKV + rw_qkv + r, __fmul_rn(acc[r], tq.rs[r]), tag);
+                PS_MARK(ph, 3);
+            } else {
+                stage_norm<PREC, H>(s_x, s_gain[0], a.eps, s_xn);
+                PS_MARK(ph, 2);
+                float acc[RPW_QKV];
+                tile_dot<PREC, H, RPW_QKV>(tq, s_xn, acc);
 #pragma unroll
                 for (int r = 0; r < RPW_QKV; r++)
                     if (lane == r) st_tag(blk + R::OQKV + rw_qkv + r, PREC == QT_INT8 ? __fmul_rn(acc[r], tq.rs[r]) : acc[r], tag);
@@ -522,7 +824,8 @@ __global__ __launch_bounds__(NW * 64, 1) void k_pstep(Args a) {
             if (l == 0) prefetch_kv(0);
             // next operands (issued after this phase's output): W_o, first gate|up piece, post-norm gains
             TO to;
-            to.load(ly.w[1], ly.s[1], rw_o);
+            if constexpr (MF) to.load(ly.w[1], ly.s[1], b * (H / NB), wave);
+            else to.load(ly.w[1], ly.s[1], rw_o);
             TGU tg0, tg1, tg2;
             tg0.load(ly.w[2], ly.s[2], rw_gu);
             load_gains<NW, EP, H>(ly.post_norm, s_gain[1]);
@@ -711,13 +1014,31 @@ __global__ __launch_bounds__(NW * 64, 1) void k_pstep(Args a) {
             // ---------------- C: xa = x + W_o . attn -----------------
             {
                 const unsigned long long *src = blk + R::OATT;
-                gather<QD / NT, NT>(QD, [&](int i) { return src + i; }, s_in, tag, a.err, PosChunk<EP, QD>());
+                gather<QD / NT, NT>(QD, [&](int i) { return src + i; }, s_in, tag, a.err, PosChunk<EP, QD>(),
+                                    PI ? s_wst : nullptr);
             }
             PS_MARK(ph, 0);
-            {
-                stage_sums<PREC, QD, NT>(s_in, s_xs);
+            if constexpr (PI) {
+                const float sC = stage_pc<MF, QD, NT>(s_in, s_wst, pcB);
+                if constexpr (MF) {
+                    int d[4];
+                    mf_rows8<NW>(mf_dot8(to, pcB, wave), s_red, wave, d);
+                    if (tid < H / NB) {
+                        const int r = b * (H / NB) + tid;
+                        const float v = __fmul_rn(qt_pc_dot(d[0], d[1], d[2], d[3], sC), to.rs);
+                        st_tag(blk + R::OXA + r, __fadd_rn(s_x[xpos<EP, H>(r)], v), tag);
+                    }
+                } else {
+                    float acc[RPW_O];
+                    tile_dot_pc<QD, RPW_O>(to, pcB, sC, acc);
+#pragma unroll
+                    for (int r = 0; r < RPW_O; r++)
+                        if (lane == r)
+                            st_tag(blk + R::OXA + rw_o + r, __fadd_rn(s_x[xpos<EP, H>(rw_o + r)], __fmul_rn(acc[r], to.rs[r])), tag);
+                }
+            } else {
                 float acc[RPW_O];
-                tile_dot<PREC, QD, RPW_O>(to, s_in, s_xs, acc);
+                tile_dot<PREC, QD, RPW_O>(to, s_in, acc);
 #pragma unroll
                 for (int r = 0; r < RPW_O; r++)
                     if (lane == r) {
@@ -726,22 +1047,62 @@ __global__ __launch_bounds__(NW * 64, 1) void k_pstep(Args a) {
                     }
             }
             TDN td;
-            td.load(ly.w[3], ly.s[3], rw_dn);
+            if constexpr (MF) td.load(ly.w[3], ly.s[3], b * (H / NB), wave);
+            else td.load(ly.w[3], ly.s[3], rw_dn);
             PS_MARK(ph, 1); ph++;
 
             // ---------------- D: h = SwiGLU(W_gu . RMSNorm(xa)) -----------------
             {
                 const unsigned long long *src = blk + R::OXA;
-                gather<H / NT, NT>(H, [&](int i) { return src + i; }, s_xa, tag, a.err, PH());
+                gather<H / NT, NT>(H, [&](int i) { return src + i; }, s_xa, tag, a.err, PH(), PI ? s_wst : nullptr, s_gain[1]);
             }
             PS_MARK(ph, 0);
-            {
-                stage_norm<PREC, H>(s_xa, s_gain[1], a.eps, s_xn, s_xs);
+            if constexpr (MF) {
+                const float sD = stage_norm_pc<true, H, NT>(s_xa, s_gain[1], a.eps, pcB, s_wst);
+                PS_MARK(ph, 2);
+                int *red = s_red + wave * 192;
+                i32x4 acc3[3];
+                mf_dot4x3(tg0, tg1, tg2, pcB, acc3);
+                mf_store4(acc3[0], red);
+                mf_store4(acc3[1], red + 64);
+                mf_store4(acc3[2], red + 128);
+                // lane t < 6: h element (piece t/2, pair t%2) from rows 2i (gate), 2i+1 (up)
+                const int pc = lane >> 1, i = lane & 1;
+                int dg[4], du[4];
+                mf_rowsum(red + (pc < 3 ? pc : 0) * 64, 2 * i, dg);
+                mf_rowsum(red + (pc < 3 ? pc : 0) * 64, 2 * i + 1, du);
+                if (lane < 6) {
+                    const float sg = pc == 0 ? tg0.rs[0] : pc == 1 ? tg1.rs[0] : tg2.rs[0];
+                    const float su = pc == 0 ? tg0.rs[1] : pc == 1 ? tg1.rs[1] : tg2.rs[1];
+                    const float gt = __fmul_rn(qt_pc_dot(dg[0], dg[1], dg[2], dg[3], sD), sg);
+                    const float up = __fmul_rn(qt_pc_dot(du[0], du[1], du[2], du[3], sD), su);
+                    st_tag(blk + R::OH + ((rw_gu + pc * RGU) >> 1) + i, gt / (1.0f + expf(-gt)) * up, tag);
+                }
+            } else if constexpr (PI) {
+                const float sD = stage_norm_pc<false, H, NT>(s_xa, s_gain[1], a.eps, pcB, s_wst);
                 PS_MARK(ph, 2);
                 float acc[3][RGU];
-                tile_dot<PREC, H, RGU>(tg0, s_xn, s_xs, acc[0]);
-                tile_dot<PREC, H, RGU>(tg1, s_xn, s_xs, acc[1]);
-                tile_dot<PREC, H, RGU>(tg2, s_xn, s_xs, acc[2]);
+                tile_dot_pc<H, RGU>(tg0, pcB, sD, acc[0]);
+                tile_dot_pc<H, RGU>(tg1, pcB, sD, acc[1]);
+                tile_dot_pc<H, RGU>(tg2, pcB, sD, acc[2]);
+#pragma unroll
+                for (int pc = 0; pc < 3; pc++) {
+                    const TGU &t = pc == 0 ? tg0 : pc == 1 ? tg1 : tg2;
+#pragma unroll
+                    for (int i = 0; i < RGU / 2; i++)
+                        if (lane == pc * (RGU / 2) + i) {
+                            const float gt = __fmul_rn(acc[pc][2 * i], t.rs[2 * i]);
+                            const float up = __fmul_rn(acc[pc][2 * i + 1], t.rs[2 * i + 1]);
+                            st_tag(blk + R::OH + ((rw_gu + pc * RGU) >> 1) + i, gt / (1.0f + expf(-gt)) * up, tag);
+                        }
+                }
+            } else {
+                stage_norm<PREC, H>(s_xa, s_gain[1], a.eps, s_xn);
+                PS_MARK(ph, 2);
+                float acc[3][RGU];
+                tile_dot<PREC, H, RGU>(tg0, s_xn, acc[0]);
+                tile_dot<PREC, H, RGU>(tg1, s_xn, acc[1]);
+                tile_dot<PREC, H, RGU>(tg2, s_xn, acc[2]);
                 // rows 2i, 2i+1 of a piece are the gate and up rows of one h element
 #pragma unroll
                 for (int pc = 0; pc < 3; pc++) {
@@ -765,14 +1126,33 @@ __global__ __launch_bounds__(NW * 64, 1) void k_pstep(Args a) {
             // ---------------- E: x' = xa + W_dn . h -----------------
             {
                 const unsigned long long *src = blk + R::OH;
-                gather<F / NT, NT>(F, [&](int i) { return src + i; }, s_in, tag, a.err, PosChunk<EP, F>());
+                gather<F / NT, NT>(F, [&](int i) { return src + i; }, s_in, tag, a.err, PosChunk<EP, F>(),
+                                   PI ? s_wst : nullptr);
             }
             PS_MARK(ph, 0);
-            {
-                stage_sums<PREC, F, NT>(s_in, s_xs);
+            if constexpr (PI) {
+                const float sE = stage_pc<MF, F, NT>(s_in, s_wst, pcB);
+                PS_MARK(ph, 2);
+                if constexpr (MF) {
+                    int d[4];
+                    mf_rows8<NW>(mf_dot8(td, pcB, wave), s_red, wave, d);
+                    if (tid < H / NB) {
+                        const int r = b * (H / NB) + tid;
+                        const float v = __fmul_rn(qt_pc_dot(d[0], d[1], d[2], d[3], sE), td.rs);
+                        st_tag(blk + R::OX + r, __fadd_rn(s_xa[xpos<EP, H>(r)], v), tag);
+                    }
+                } else {
+                    float acc[RPW_DN];
+                    tile_dot_pc<F, RPW_DN>(td, pcB, sE, acc);
+#pragma unroll
+                    for (int r = 0; r < RPW_DN; r++)
+                        if (lane == r)
+                            st_tag(blk + R::OX + rw_dn + r, __fadd_rn(s_xa[xpos<EP, H>(rw_dn + r)], __fmul_rn(acc[r], td.rs[r])), tag);
+                }
+            } else {
                 PS_MARK(ph, 2);
                 float acc[RPW_DN];
-                tile_dot<PREC, F, RPW_DN>(td, s_in, s_xs, acc);
+                tile_dot<PREC, F, RPW_DN>(td, s_in, acc);
 #pragma unroll
                 for (int r = 0; r < RPW_DN; r++)
                     if (lane == r) {
@@ -781,6 +1161,9 @@ __global__ __launch_bounds__(NW * 64, 1) void k_pstep(Args a) {
                     }
             }
             PS_MARK(ph, 3);
+            // the next layer's K/V copy lands in the buffer this phase's input and pieces
+            // occupy: every wave must be done reading them
+            __syncthreads();
             if (l + 1 < L) prefetch_kv(l + 1);
             PS_MARK(ph, 1); ph++;
         }
@@ -792,7 +1175,7 @@ __global__ __launch_bounds__(NW * 64, 1) void k_pstep(Args a) {
             if (b == 0) {
                 load_gains<NW, EH, H>(a.final_norm, s_gain[1]);
                 gather<H / NT, NT>(H, [&](int i) { return xfin + i; }, s_x, tag, a.err, PosChunk<EH, H>());
-                stage_norm<QT_BF16, H>(s_x, s_gain[1], a.eps, s_xn, s_xs);
+                stage_norm<QT_BF16, H>(s_x, s_gain[1], a.eps, s_xn);
                 for (int i = tid; i < H; i += NT) { a.hid[i] = s_xn[xpos<EH, H>(i)]; a.decx[i] = s_x[xpos<EH, H>(i)]; }
             }
         } else {
@@ -804,11 +1187,11 @@ __global__ __launch_bounds__(NW * 64, 1) void k_pstep(Args a) {
             load_gains<NW, EH, H>(a.final_norm, s_gain[1]);
             gather<H / NT, NT>(H, [&](int i) { return xfin + i; }, s_x, tag, a.err, PosChunk<EH, H>());
             PS_MARK(ph, 0);
-            stage_norm<QT_BF16, H>(s_x, s_gain[1], a.eps, s_xn, s_xs);
+            stage_norm<QT_BF16, H>(s_x, s_gain[1], a.eps, s_xn);
             if (last_step && b == 0)
                 for (int i = tid; i < H; i += NT) { a.hid[i] = s_xn[xpos<EH, H>(i)]; a.decx[i] = s_x[xpos<EH, H>(i)]; }
             float acc[RPW_HEAD];
-            tile_dot<QT_BF16, H, RPW_HEAD>(th, s_xn, s_xs, acc);
+            tile_dot<QT_BF16, H, RPW_HEAD>(th, s_xn, acc);
             const int frame = frame0 + step;
             if (lane == 0) {
                 float bv = -INFINITY; int bi = 0x7FFFFFFF;
@@ -884,8 +1267,9 @@ extern "C" hipError_t qt_pstep_trace_read(unsigned long long *out) {
 }
 #endif
 
-// 8 waves per workgroup (two per SIMD, so one wave's latency is covered by the other's
-// work) where the row split allows it (hidden 2048); 4 for hidden 1024.
+// 4 waves per workgroup (one per SIMD).  The kernel also builds with 8 (two per SIMD, so
+// one wave's latency could hide behind the other's work), but at 256 registers per wave
+// its tiles spill and the step is slower.
 template <int PREC, int H, int F>
 static hipError_t ps_launch(const ps::Args &a, hipStream_t st) {
     constexpr int NW = 4;

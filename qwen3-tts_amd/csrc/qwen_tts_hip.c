@@ -6,7 +6,7 @@
  * for gfx950:
  *   - weights are uploaded once into the device encodings of qt_device.h (Q|K|V rows
  *     concatenated into one matrix per layer so the QKV projection is one launch;
- *     int8 re-encoded q^0x80; q4_0 split into qs rows + f16 scale bits);
+ *     int8 the reference's signed bytes; q4_0 split into qs rows + f16 scale bits);
  *   - the KV cache stays bf16 on the device (the reference keeps f32 with truncated
  *     mantissas, qwen_tts_cuda_talker.cu:203-208, 350-351), head-major
  *     [layer][kv_head][kv_max][128], so upload is a strided memcpy of the host bits and
@@ -39,7 +39,7 @@ const char *qwen_hip_last_error(void) { return g_err; }
 
 typedef struct {
     int prec, rows, cols;
-    uint8_t *w;        /* chunk rows (bf16 bits | q^0x80 | q4 qs) */
+    uint8_t *w;        /* chunk rows (bf16 bits | int8 q | q4 qs) */
     float *scale;      /* int8 */
     uint16_t *s16;     /* q4 f16 scale bits */
 } dmat_t;
@@ -78,7 +78,6 @@ static int dmat_put(dmat_t *m, int r0, const qwen_hip_mat_t *src, int src_prec, 
         } else if (m->prec == QWEN_HIP_INT8) {
             REQ(src->scale, "int8 weight without scale");
             HCK(hipMemcpyAsync(m->w + (size_t)r0 * cols, src->w, (size_t)rows * cols, hipMemcpyDefault, st));
-            HCK(qt_launch_flip_sign(m->w + (size_t)r0 * cols, (size_t)rows * cols, st));
             HCK(hipMemcpyAsync(m->scale + r0, src->scale, (size_t)rows * sizeof(float), hipMemcpyDefault, st));
         } else {
             size_t nb = (size_t)rows * (cols / 32);
@@ -1515,7 +1514,6 @@ int qwen_hip_op_quantize_int8(const uint16_t *src, int rows, int cols, int8_t *d
     HCK(hipMalloc((void **)&dsc, (size_t)rows * sizeof(float)));
     HCK(hipMemcpyAsync(ds, src, (size_t)rows * cols * 2, hipMemcpyHostToDevice, st));
     HCK(qt_launch_quant_int8(ds, rows, cols, dq, dsc, st));
-    HCK(qt_launch_flip_sign(dq, (size_t)rows * cols, st));   /* back to the reference's q */
     HCK(hipMemcpyAsync(dst, dq, (size_t)rows * cols, hipMemcpyDeviceToHost, st));
     HCK(hipMemcpyAsync(scale, dsc, (size_t)rows * sizeof(float), hipMemcpyDeviceToHost, st));
     HCK(hipStreamSynchronize(st));

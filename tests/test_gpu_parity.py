@@ -223,12 +223,15 @@ def test_upload_kv_roundtrip_and_resume():
 
 
 @need_ref
-@pytest.mark.parametrize("prec", ["bf16", "int8"])
-def test_fused_step_matches_kernel_sequence(prec):
+@pytest.mark.parametrize("name,prec", [("mini", "bf16"), ("mini", "int8"), ("mini17", "bf16"), ("mini17", "int8")])
+def test_fused_step_matches_kernel_sequence(name, prec):
     """The default step (one persistent kernel, or the captured graph where that is
-    unavailable) against the plain launch sequence: same per-row arithmetic, so the
-    residual stream is bit-identical; the final RMSNorm reduces in a different order."""
-    ref, shape, _ = _ref("mini", prec)
+    unavailable) against the plain launch sequence: same per-row arithmetic (int8: the
+    same exact integer piece sums, MFMA in the fused step at hidden 2048, v_dot4 in the
+    matvec kernel), so the residual stream is bit-identical; the final RMSNorm reduces in
+    a different order."""
+    print(f"[case] fused vs kernels {name} {prec}", flush=True)
+    ref, shape, _ = _ref(name, prec)
     pc = hip.PREC[prec]
     ga = _gpu_talker(ref, shape, pc)
     gb = _gpu_talker(ref, shape, pc)
