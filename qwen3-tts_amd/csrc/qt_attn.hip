@@ -114,6 +114,9 @@ __global__ __launch_bounds__(QT_WG) void k_attn(QtAttnArgs a) {
             }
         }
     };
+    // LDS written by global_load_lds is counted by vmcnt, and a workgroup barrier does
+    // not wait for it: every staging is followed by an explicit full wait before the
+    // barrier that publishes the block to the other waves.
     // ---- 0. K/V of the first key block in flight before anything else ----
     stage(0, true, true);
 
@@ -151,6 +154,7 @@ __global__ __launch_bounds__(QT_WG) void k_attn(QtAttnArgs a) {
         for (int i = tid; i < HPK * QT_HD; i += QT_WG)
             qs[i / QT_HD][i % QT_HD] = a.q[(g * HPK + i / QT_HD) * QT_HD + i % QT_HD];
     }
+    __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();   // (also: every wave's LDS copies of the first block have landed)
 
     // ---- 2. scores: 16 lanes per key (8 dims each), keys u*16 + wave*4 + pg of a block ----
@@ -163,6 +167,7 @@ __global__ __launch_bounds__(QT_WG) void k_attn(QtAttnArgs a) {
         if (kb > 0) {   // chunks longer than one block (caches beyond G*QT_KVB keys)
             __syncthreads();
             stage(kb, true, false);
+            __builtin_amdgcn_s_waitcnt(0);
             __syncthreads();
         }
         const int nk = min(QT_KVB, n - kb);
@@ -213,6 +218,7 @@ __global__ __launch_bounds__(QT_WG) void k_attn(QtAttnArgs a) {
         if (kb > 0) {
             __syncthreads();
             stage(kb, false, true);
+            __builtin_amdgcn_s_waitcnt(0);
             __syncthreads();
         }
         const int nk = min(QT_KVB, n - kb);

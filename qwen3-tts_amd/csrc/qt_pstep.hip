@@ -70,7 +70,10 @@ __device__ __forceinline__ T *uni(T *p) {
 }
 typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
 // 16 bytes per lane from global memory straight into LDS (global_load_lds_dwordx4):
-// lane i's bytes land at dst + 16*i, dst wave-uniform.  Counted by vmcnt like a load.
+// lane i's bytes land at dst + 16*i, dst wave-uniform.  Counted by vmcnt like a load,
+// and a workgroup barrier does not wait for it: other waves may read the bytes only after
+// a barrier that the copying wave reached behind a wait covering the copy (the next
+// gather's wait, whose loads queue behind it, or an explicit s_waitcnt).
 __device__ __forceinline__ void lds_copy16(const void *src, void *dst) {
     __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void *)src,
                                      (__attribute__((address_space(3))) void *)dst, 16, 0, 0);
@@ -874,6 +877,7 @@ __global__ __launch_bounds__(NW * 64, 1) void k_pstep(Args a) {
                     if (kb > 0) {   // chunks longer than KVB keys (caches beyond G*KVB positions)
                         __syncthreads();
                         stage_kv(l, kb, true, false);
+                        __builtin_amdgcn_s_waitcnt(0);     // the barrier does not wait for LDS copies
                         __syncthreads();
                     }
                     const int nk = min(KVB, n - kb);
@@ -925,6 +929,7 @@ __global__ __launch_bounds__(NW * 64, 1) void k_pstep(Args a) {
                     if (kb > 0) {
                         __syncthreads();
                         stage_kv(l, kb, false, true);
+                        __builtin_amdgcn_s_waitcnt(0);
                         __syncthreads();
                     }
                     const int nk = min(KVB, n - kb);

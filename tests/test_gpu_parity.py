@@ -61,7 +61,7 @@ def test_op_matvec(oracle, prec, rows, cols):
     assert err < 2e-5, err
 
 
-@pytest.mark.parametrize("seq_k", [1, 2, 17, 64, 300, 2048, 4096])
+@pytest.mark.parametrize("seq_k", [1, 2, 17, 64, 300, 2048, 4096, 4097, 5000, 8192])
 def test_op_attention(oracle, seq_k):
     print(f"[case] attention seq_k={seq_k}", flush=True)
     nh, nkv, hd = 16, 8, 128
@@ -245,6 +245,37 @@ def test_fused_step_matches_kernel_sequence(name, prec):
     ka, va = ga.download_kv(10)
     kb, vb = gb.download_kv(10)
     assert np.array_equal(ka, kb) and np.array_equal(va, vb)
+
+
+@need_ref
+def test_fused_step_long_context_matches_kernel_sequence():
+    """Caches beyond 4096 positions: every attention chunk holds more than one 128-key
+    LDS block (the second block is staged inside the phase).  Fused step == per-kernel
+    sequence bit for bit, and the per-kernel step against the oracle's attention-level
+    tolerance through the final hidden state."""
+    print("[case] fused vs kernels, KV 5000", flush=True)
+    ref, shape, _ = _ref("mini17", "int8")
+    pc = hip.INT8
+    kv_max, n0 = 6144, 5000
+    ga = _gpu_talker(ref, shape, pc, kv_max=kv_max)
+    gb = _gpu_talker(ref, shape, pc, kv_max=kv_max)
+    rng = np.random.default_rng(11)
+    L, kvd = shape.layers, shape.kv_dim
+    kk = synth.f32_to_bf16_rne(rng.standard_normal((L, n0, kvd)).astype(np.float32))
+    vv = synth.f32_to_bf16_rne((rng.standard_normal((L, n0, kvd)) * 0.5).astype(np.float32))
+    for g in (ga, gb):
+        g.upload_kv(kk, vv, n0)
+    emb = ref.codec_emb()
+    for i in range(3):
+        e = synth.bf16_to_f32(emb[100 + i])
+        a = ga.step(e, n0 + i, graph=True)
+        b = gb.step(e, n0 + i, graph=False)
+        assert np.array_equal(ga.dec_x(), gb.dec_x()), i
+        assert rel_l2(a, b) < 1e-6, i
+    ka, va = ga.download_kv(n0 + 3)
+    kb, vb = gb.download_kv(n0 + 3)
+    assert np.array_equal(ka, kb) and np.array_equal(va, vb)
+    assert np.array_equal(ka[:, :n0], kk) and np.array_equal(va[:, :n0], vv)
 
 
 @need_ref
