@@ -881,27 +881,37 @@ __global__ __launch_bounds__(NW * 64, 1) void k_pstep(Args a) {
                         __syncthreads();
                     }
                     const int nk = min(KVB, n - kb);
-                    // unrolled over the block with masking (rows past nk read stale LDS and
-                    // are discarded), so the LDS reads of all keys are issued together;
-                    // waves 0..NWB-1 only (the key-to-lane map of the per-kernel twin)
-                    if (wave < NWB)
+                    // unrolled over the keys of the block with masking (rows past nk read
+                    // stale LDS and are discarded), so the LDS reads of all keys are issued
+                    // together; the unrolled length is the block's 16-key groups rounded up
+                    // to an even count (uniform branch); waves 0..NWB-1 only (the key-to-lane
+                    // map of the per-kernel twin)
+                    auto scores = [&](auto nuc) {
+                        constexpr int NU = decltype(nuc)::value;
 #pragma unroll
-                    for (int u = 0; u < KVB / 16; u++) {
-                        const int jl = u * 16 + wave * 4 + kpg, jj = kb + jl;
-                        const uint4 kw = (j0 + jj == pos) ? *reinterpret_cast<const uint4 *>(att.knew + ksub * 8)
-                                                          : *reinterpret_cast<const uint4 *>(&s_kv[0][jl * HD + ksub * 8]);
-                        const uint32_t w4[4] = {kw.x, kw.y, kw.z, kw.w};
-                        float kf[8];
+                        for (int u = 0; u < NU; u++) {
+                            const int jl = u * 16 + wave * 4 + kpg, jj = kb + jl;
+                            const uint4 kw = (j0 + jj == pos) ? *reinterpret_cast<const uint4 *>(att.knew + ksub * 8)
+                                                              : *reinterpret_cast<const uint4 *>(&s_kv[0][jl * HD + ksub * 8]);
+                            const uint32_t w4[4] = {kw.x, kw.y, kw.z, kw.w};
+                            float kf[8];
 #pragma unroll
-                        for (int m = 0; m < 4; m++) { kf[2 * m] = bf_lo(w4[m]); kf[2 * m + 1] = bf_hi(w4[m]); }
+                            for (int m = 0; m < 4; m++) { kf[2 * m] = bf_lo(w4[m]); kf[2 * m + 1] = bf_hi(w4[m]); }
 #pragma unroll
-                        for (int h = 0; h < HPK; h++) {
-                            float sv = 0.f;
+                            for (int h = 0; h < HPK; h++) {
+                                float sv = 0.f;
 #pragma unroll
-                            for (int e = 0; e < 8; e++) sv = fmaf(qv[h][e], kf[e], sv);
-                            sv = group_sum<16>(sv);
-                            if (ksub == 0 && jl < nk) att.sc[h][jj] = sv * a.scale;
+                                for (int e = 0; e < 8; e++) sv = fmaf(qv[h][e], kf[e], sv);
+                                sv = group_sum<16>(sv);
+                                if (ksub == 0 && jl < nk) att.sc[h][jj] = sv * a.scale;
+                            }
                         }
+                    };
+                    if (wave < NWB) {
+                        if (nk <= 32) scores(std::integral_constant<int, 2>());
+                        else if (nk <= 64) scores(std::integral_constant<int, 4>());
+                        else if (nk <= 96) scores(std::integral_constant<int, 6>());
+                        else scores(std::integral_constant<int, 8>());
                     }
                 }
                 __syncthreads();
@@ -933,33 +943,45 @@ __global__ __launch_bounds__(NW * 64, 1) void k_pstep(Args a) {
                         __syncthreads();
                     }
                     const int nk = min(KVB, n - kb);
-                    if (wave < NWB)
+                    auto pv = [&](auto nuc) {
+                        constexpr int NU = decltype(nuc)::value;
 #pragma unroll
-                    for (int u = 0; u < KVB / 16; u++) {
-                        const int jl = u * 16 + wave * 4 + kpg, jj = kb + jl;
-                        const bool ok = jl < nk;
-                        const uint4 vw = (j0 + jj == pos) ? *reinterpret_cast<const uint4 *>(att.vnew + ksub * 8)
-                                                          : *reinterpret_cast<const uint4 *>(&s_kv[1][jl * HD + ksub * 8]);
-                        const uint32_t w4[4] = {vw.x, vw.y, vw.z, vw.w};
-                        float vf[8];
+                        for (int u = 0; u < NU; u++) {
+                            const int jl = u * 16 + wave * 4 + kpg, jj = kb + jl;
+                            const bool ok = jl < nk;
+                            const uint4 vw = (j0 + jj == pos) ? *reinterpret_cast<const uint4 *>(att.vnew + ksub * 8)
+                                                              : *reinterpret_cast<const uint4 *>(&s_kv[1][jl * HD + ksub * 8]);
+                            const uint32_t w4[4] = {vw.x, vw.y, vw.z, vw.w};
+                            float vf[8];
 #pragma unroll
-                        for (int m = 0; m < 4; m++) { vf[2 * m] = bf_lo(w4[m]); vf[2 * m + 1] = bf_hi(w4[m]); }
+                            for (int m = 0; m < 4; m++) { vf[2 * m] = bf_lo(w4[m]); vf[2 * m + 1] = bf_hi(w4[m]); }
 #pragma unroll
-                        for (int h = 0; h < HPK; h++) {
-                            const float p = att.sc[h][min(jj, CHMAX - 1)];
+                            for (int h = 0; h < HPK; h++) {
+                                const float p = att.sc[h][min(jj, CHMAX - 1)];
 #pragma unroll
-                            for (int e = 0; e < 8; e++) o[h][e] = ok ? fmaf(p, vf[e], o[h][e]) : o[h][e];
+                                for (int e = 0; e < 8; e++) o[h][e] = ok ? fmaf(p, vf[e], o[h][e]) : o[h][e];
+                            }
                         }
+                    };
+                    if (wave < NWB) {
+                        if (nk <= 32) pv(std::integral_constant<int, 2>());
+                        else if (nk <= 64) pv(std::integral_constant<int, 4>());
+                        else if (nk <= 96) pv(std::integral_constant<int, 6>());
+                        else pv(std::integral_constant<int, 8>());
                     }
                 }
+                // sum over the 4 key groups of a wave (lanes l, l^16, l^32, l^48) with the
+                // gfx950 row swaps: same additions, in the same order, as the per-kernel
+                // twin's shuffles
 #pragma unroll
                 for (int h = 0; h < HPK; h++)
 #pragma unroll
                     for (int e = 0; e < 8; e++) {
-                        float v = o[h][e];
-                        v += __shfl_xor(v, 16, 64);
-                        v += __shfl_xor(v, 32, 64);
-                        o[h][e] = v;
+                        const float v = o[h][e];
+                        const auto r16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+                        const float a16 = __uint_as_float(r16[0]) + __uint_as_float(r16[1]);
+                        const auto r32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(a16), __float_as_uint(a16), false, false);
+                        o[h][e] = __uint_as_float(r32[0]) + __uint_as_float(r32[1]);
                     }
                 if (kpg == 0 && wave < NWB) {
 #pragma unroll
