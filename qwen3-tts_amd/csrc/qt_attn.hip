@@ -20,7 +20,7 @@
 // overlaps the prologue; the key at `pos` (appended by this workgroup) is not read from
 // memory but taken from LDS (knew/vnew).  The merging workgroup reuses that LDS for the
 // chunk partials, so a workgroup needs ~72 KB and two fit on a CU.
-#include "qt_device.h"
+#include "qt_attn_mf.h"
 
 #define QT_HD 128
 #define QT_CH_MAX 256
@@ -85,12 +85,13 @@ __global__ __launch_bounds__(QT_WG) void k_attn(QtAttnArgs a) {
 
     constexpr int PS = 2 + QT_HD;
     constexpr int KVBYTES = 2 * QT_KVB * QT_HD * 2, MBYTES = QT_ATT_G * HPK * PS * 4;
-    __shared__ float qs[HPK][QT_HD];
-    __shared__ float sc[HPK][QT_CH_MAX];
-    __shared__ float ored[QT_WAVES][HPK][QT_HD];
+    __shared__ __align__(16) uint16_t qp[HPK * 3][QT_HD];       // query pieces (qt_attn_mf.h)
+    __shared__ float sc[HPK][QT_CH_MAX];                         // scores
+    __shared__ __align__(16) uint16_t pp[HPK * 3][QT_CH_MAX];   // probability pieces, 0 past the chunk
     __shared__ float stat[HPK][2];
     __shared__ __align__(16) uint16_t knew[QT_HD];
     __shared__ __align__(16) uint16_t vnew[QT_HD];
+    __shared__ __align__(16) uint16_t zeros[8];
     // K rows, V rows of a key block; reused as the merge staging
     __shared__ __align__(16) uint16_t s_kvbuf[(KVBYTES > MBYTES ? KVBYTES : MBYTES) / 2];
     uint16_t(*s_kv)[QT_KVB * QT_HD] = reinterpret_cast<uint16_t(*)[QT_KVB * QT_HD]>(s_kvbuf);
@@ -100,17 +101,18 @@ __global__ __launch_bounds__(QT_WG) void k_attn(QtAttnArgs a) {
     const uint16_t *Vg = a.V + (long long)g * a.head_stride;
     const int sub = lane & 15, pg = lane >> 4;
 
-    // K and/or V rows of keys [kb, kb + min(QT_KVB, n - kb)) of the chunk into s_kv; the
-    // appended key (PREP) is not read from memory, it comes from knew/vnew.
+    // K and/or V rows of keys [kb, kb + min(QT_KVB, n - kb)) of the chunk into s_kv, in
+    // the swizzled slot order of qt_attn_mf.h (lane (pg, sub) fills slot sub of block row
+    // 4i + pg); the appended key (PREP) is not read from memory, it comes from knew/vnew.
     auto stage = [&](int kb, bool doK, bool doV) {
         const int nk = min(QT_KVB, n - kb);
         const int ninst = (nk + 3) >> 2;
         for (int i = wave; i < ninst; i += QT_WAVES) {
-            const int jj = kb + i * 4 + pg;
+            const int jl = i * 4 + pg, jj = kb + jl;
             if (jj < n && !(PREP && j0 + jj == pos)) {
-                const long long off = (long long)(j0 + jj) * a.pos_stride + sub * 8;
-                if (doK) qt_lds_copy16(Kg + off, &s_kv[0][i * 4 * QT_HD]);
-                if (doV) qt_lds_copy16(Vg + off, &s_kv[1][i * 4 * QT_HD]);
+                const long long row = (long long)(j0 + jj) * a.pos_stride;
+                if (doK) qt_lds_copy16(Kg + row + qt_kslot(jl, sub) * 8, &s_kv[0][i * 4 * QT_HD]);
+                if (doV) qt_lds_copy16(Vg + row + qt_vslot(jl, sub) * 8, &s_kv[1][i * 4 * QT_HD]);
             }
         }
     };
@@ -136,8 +138,8 @@ __global__ __launch_bounds__(QT_WG) void k_attn(QtAttnArgs a) {
             float r0 = fmaf(n0, cs, -(n1 * sn));
             float r1 = fmaf(n1, cs, n0 * sn);
             if (!isk) {
-                qs[t][lane] = r0;
-                qs[t][lane + 64] = r1;
+                qt_put_pieces(&qp[3 * t][lane], QT_HD, r0);
+                qt_put_pieces(&qp[3 * t][lane + 64], QT_HD, r1);
             } else {
                 const float *vs = a.q + a.n_heads * QT_HD + a.n_kv * QT_HD + g * QT_HD;
                 const uint16_t k0 = f2bf_trunc(r0), k1 = f2bf_trunc(r1);
@@ -152,17 +154,13 @@ __global__ __launch_bounds__(QT_WG) void k_attn(QtAttnArgs a) {
         }
     } else {
         for (int i = tid; i < HPK * QT_HD; i += QT_WG)
-            qs[i / QT_HD][i % QT_HD] = a.q[(g * HPK + i / QT_HD) * QT_HD + i % QT_HD];
+            qt_put_pieces(&qp[3 * (i / QT_HD)][i % QT_HD], QT_HD, a.q[(g * HPK + i / QT_HD) * QT_HD + i % QT_HD]);
     }
+    if (tid < 8) zeros[tid] = 0;
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();   // (also: every wave's LDS copies of the first block have landed)
 
-    // ---- 2. scores: 16 lanes per key (8 dims each), keys u*16 + wave*4 + pg of a block ----
-    float qv[HPK][8];
-#pragma unroll
-    for (int h = 0; h < HPK; h++)
-#pragma unroll
-        for (int e = 0; e < 8; e++) qv[h][e] = qs[h][sub * 8 + e];
+    // ---- 2. scores on MFMA: 16-key tiles u = wave, wave + 4 of each block ----
     for (int kb = 0; kb < n; kb += QT_KVB) {
         if (kb > 0) {   // chunks longer than one block (caches beyond G*QT_KVB keys)
             __syncthreads();
@@ -171,23 +169,20 @@ __global__ __launch_bounds__(QT_WG) void k_attn(QtAttnArgs a) {
             __syncthreads();
         }
         const int nk = min(QT_KVB, n - kb);
-#pragma unroll
-        for (int u = 0; u < QT_KVB / 16; u++) {
-            const int jl = u * 16 + wave * 4 + pg, jj = kb + jl;
-            const uint4 kw = (PREP && j0 + jj == pos) ? *reinterpret_cast<const uint4 *>(knew + sub * 8)
-                                                      : *reinterpret_cast<const uint4 *>(&s_kv[0][jl * QT_HD + sub * 8]);
-            const uint32_t w4[4] = {kw.x, kw.y, kw.z, kw.w};
-            float kf[8];
-#pragma unroll
-            for (int m = 0; m < 4; m++) { kf[2 * m] = bf_lo(w4[m]); kf[2 * m + 1] = bf_hi(w4[m]); }
-#pragma unroll
-            for (int h = 0; h < HPK; h++) {
-                float s = 0.f;
-#pragma unroll
-                for (int e = 0; e < 8; e++) s = fmaf(qv[h][e], kf[e], s);
-                s = group_sum<16>(s);
-                if (sub == 0 && jl < nk) sc[h][jj] = s * a.scale;
+        const int nrow = PREP ? pos - j0 - kb : -1;   // block row of the appended key
+        if ((wave + QT_WAVES) * 16 < nk) {
+            const int r0[2] = {wave * 16, (wave + QT_WAVES) * 16};
+            float sv[2];
+            qt_att_qk<HPK, 2>(&qp[0][0], s_kv[0], knew, r0, nrow, lane, sv);
+            if (pg < HPK) {
+                sc[pg][kb + r0[0] + sub] = sv[0] * a.scale;
+                if (r0[1] + sub < nk) sc[pg][kb + r0[1] + sub] = sv[1] * a.scale;
             }
+        } else if (wave * 16 < nk) {
+            const int r0[1] = {wave * 16};
+            float sv[1];
+            qt_att_qk<HPK, 1>(&qp[0][0], s_kv[0], knew, r0, nrow, lane, sv);
+            if (pg < HPK && r0[0] + sub < nk) sc[pg][kb + r0[0] + sub] = sv[0] * a.scale;
         }
     }
     __syncthreads();
@@ -200,20 +195,19 @@ __global__ __launch_bounds__(QT_WG) void k_attn(QtAttnArgs a) {
         float l = 0.f;
         for (int j = lane; j < n; j += 64) {
             float p = expf(sc[h][j] - m);
-            sc[h][j] = p;
+            qt_put_pieces(&pp[3 * h][j], QT_CH_MAX, p);
             l += p;
         }
         l = group_sum<64>(l);
         if (lane == 0) { stat[h][0] = m; stat[h][1] = l; }
+        for (int j = n + lane; j < ((n + 31) & ~31); j += 64)   // P.V key tiles past the chunk
+            qt_put_pieces(&pp[3 * h][j], QT_CH_MAX, 0.f);
     }
     __syncthreads();
 
-    // ---- 4. o = sum_j p_j v_j (same keys per lane, same order, as the scores) ----
-    float o[HPK][8];
-#pragma unroll
-    for (int h = 0; h < HPK; h++)
-#pragma unroll
-        for (int e = 0; e < 8; e++) o[h][e] = 0.f;
+    // ---- 4. o = sum_j p_j v_j on MFMA: wave w owns dims [32w, 32w + 32) as two 16-dim
+    // tiles; lane (h, d) = (pg, sub) ends with head h's sums for dims 32w + d, 32w + 16 + d ----
+    qt_f32x4 acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
     for (int kb = 0; kb < n; kb += QT_KVB) {
         if (kb > 0) {
             __syncthreads();
@@ -222,49 +216,22 @@ __global__ __launch_bounds__(QT_WG) void k_attn(QtAttnArgs a) {
             __syncthreads();
         }
         const int nk = min(QT_KVB, n - kb);
-#pragma unroll
-        for (int u = 0; u < QT_KVB / 16; u++) {
-            const int jl = u * 16 + wave * 4 + pg, jj = kb + jl;
-            const bool ok = jl < nk;
-            {
-                const uint4 vw = (PREP && j0 + jj == pos) ? *reinterpret_cast<const uint4 *>(vnew + sub * 8)
-                                                          : *reinterpret_cast<const uint4 *>(&s_kv[1][jl * QT_HD + sub * 8]);
-                const uint32_t w4[4] = {vw.x, vw.y, vw.z, vw.w};
-                float vf[8];
-#pragma unroll
-                for (int m = 0; m < 4; m++) { vf[2 * m] = bf_lo(w4[m]); vf[2 * m + 1] = bf_hi(w4[m]); }
-#pragma unroll
-                for (int h = 0; h < HPK; h++) {
-                    const float p = ok ? sc[h][min(jj, QT_CH_MAX - 1)] : 0.f;
-#pragma unroll
-                    for (int e = 0; e < 8; e++) o[h][e] = ok ? fmaf(p, vf[e], o[h][e]) : o[h][e];
-                }
-            }
-        }
+        const int nrow = PREP ? pos - j0 - kb : -1;
+        const int nkt = (nk + 31) >> 5;
+        if (nkt == 1) qt_att_pv<HPK, 1>(&pp[0][0], QT_CH_MAX, kb, s_kv[1], vnew, zeros, 32 * wave, nrow, nk, lane, acc0, acc1);
+        else if (nkt == 2) qt_att_pv<HPK, 2>(&pp[0][0], QT_CH_MAX, kb, s_kv[1], vnew, zeros, 32 * wave, nrow, nk, lane, acc0, acc1);
+        else if (nkt == 3) qt_att_pv<HPK, 3>(&pp[0][0], QT_CH_MAX, kb, s_kv[1], vnew, zeros, 32 * wave, nrow, nk, lane, acc0, acc1);
+        else qt_att_pv<HPK, 4>(&pp[0][0], QT_CH_MAX, kb, s_kv[1], vnew, zeros, 32 * wave, nrow, nk, lane, acc0, acc1);
     }
-#pragma unroll
-    for (int h = 0; h < HPK; h++)
-#pragma unroll
-        for (int e = 0; e < 8; e++) {
-            float v = o[h][e];
-            v += __shfl_xor(v, 16, 64);
-            v += __shfl_xor(v, 32, 64);
-            o[h][e] = v;
-        }
-    if (pg == 0) {
-#pragma unroll
-        for (int h = 0; h < HPK; h++)
-#pragma unroll
-            for (int e = 0; e < 8; e++) ored[wave][h][sub * 8 + e] = o[h][e];
-    }
-    __syncthreads();
+    const float o0 = (acc0[0] + acc0[1]) + acc0[2], o1 = (acc1[0] + acc1[1]) + acc1[2];
+    const int od = 32 * wave + sub;
 
     // ---- 5. write (single chunk) or publish partial and merge in the last workgroup ----
     if (nch == 1) {
-        for (int i = tid; i < HPK * QT_HD; i += QT_WG) {
-            const int h = i / QT_HD, d = i % QT_HD;
-            float v = ored[0][h][d] + ored[1][h][d] + ored[2][h][d] + ored[3][h][d];
-            a.out[(g * HPK + h) * QT_HD + d] = v * (1.0f / stat[h][1]);
+        if (pg < HPK) {
+            const float r = 1.0f / stat[pg][1];
+            a.out[(g * HPK + pg) * QT_HD + od] = o0 * r;
+            a.out[(g * HPK + pg) * QT_HD + od + 16] = o1 * r;
         }
         return;
     }
@@ -273,9 +240,9 @@ __global__ __launch_bounds__(QT_WG) void k_attn(QtAttnArgs a) {
     // __threadfence(), whose L2 write-back + invalidate on every XCD costs ~17 us for a
     // 256-workgroup grid on MI355X; the merging workgroup reads with agent-scope loads.
     float *mypart = a.part + ((size_t)(g * G + c) * HPK) * PS;
-    for (int i = tid; i < HPK * QT_HD; i += QT_WG) {
-        const int h = i / QT_HD, d = i % QT_HD;
-        st_agent(mypart + h * PS + 2 + d, ored[0][h][d] + ored[1][h][d] + ored[2][h][d] + ored[3][h][d]);
+    if (pg < HPK) {
+        st_agent(mypart + pg * PS + 2 + od, o0);
+        st_agent(mypart + pg * PS + 2 + od + 16, o1);
     }
     if (tid < HPK) { st_agent(mypart + tid * PS, stat[tid][0]); st_agent(mypart + tid * PS + 1, stat[tid][1]); }
     __builtin_amdgcn_s_waitcnt(0);

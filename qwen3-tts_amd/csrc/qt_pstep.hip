@@ -40,7 +40,7 @@
 // from LDS in the step that writes it), so no cache holds a stale copy.
 // Every wait is bounded: on timeout the kernel sets an error flag, the others see it
 // and stop waiting, and the launch runs to its end.
-#include "qt_device.h"
+#include "qt_attn_mf.h"
 #include <type_traits>
 
 namespace ps {
@@ -642,11 +642,12 @@ struct Ring {
 // LDS of the attention phase (B) and the merge (M, which reuses sc for its inputs)
 template <int HPK>
 struct AttLds {
-    float qs[HPK][HD];                 // rotated queries
-    float sc[HPK][CHMAX];              // scores, then probabilities
-    float ored[NWB][HPK][HD];          // per-wave P.V partial sums
+    __attribute__((aligned(16))) uint16_t qp[HPK * 3][HD];       // rotated queries as bf16 pieces (qt_attn_mf.h)
+    float sc[HPK][CHMAX];                                         // scores
+    __attribute__((aligned(16))) uint16_t pp[HPK * 3][CHMAX];    // probability pieces, 0 past the chunk
     float stat[HPK][2];                // chunk (max, sum) per head
     __attribute__((aligned(16))) uint16_t knew[HD], vnew[HD];   // key/value at pos (bf16)
+    __attribute__((aligned(16))) uint16_t zeros[8];             // value rows past the chunk (P.V)
 };
 
 template <int PREC, int H, int F, int NW>
@@ -727,6 +728,7 @@ __global__ __launch_bounds__(NW * 64, 1) void k_pstep(Args a) {
     // the layer table lives in LDS: reading it never waits behind weight loads
     for (int i = tid; i < L * (int)(sizeof(Layer) / 8); i += NT)
         reinterpret_cast<unsigned long long *>(s_layers)[i] = ldg(reinterpret_cast<const unsigned long long *>(a.layers) + i);
+    if (tid < 8) att.zeros[tid] = 0;
     __syncthreads();
 
     TQKV tq;
@@ -759,11 +761,11 @@ __global__ __launch_bounds__(NW * 64, 1) void k_pstep(Args a) {
             const int ninst = (nk + 3) >> 2;
             const int jq = lane >> 4, js = lane & 15;
             for (int i = wave; i < ninst; i += NW) {
-                const int jj = kb + i * 4 + jq;
-                if (jj < n && j0 + jj != pos) {
-                    const size_t off = (size_t)(j0 + jj) * HD + js * 8;
-                    if (doK) lds_copy16(Kl + off, &s_kv[0][i * 4 * HD]);
-                    if (doV) lds_copy16(Vl + off, &s_kv[1][i * 4 * HD]);
+                const int jl = i * 4 + jq, jj = kb + jl;
+                if (jj < n && j0 + jj != pos) {   // slot js of block row jl: swizzled source chunk
+                    const size_t row = (size_t)(j0 + jj) * HD;
+                    if (doK) lds_copy16(Kl + row + qt_kslot(jl, js) * 8, &s_kv[0][i * 4 * HD]);
+                    if (doV) lds_copy16(Vl + row + qt_vslot(jl, js) * 8, &s_kv[1][i * 4 * HD]);
                 }
             }
         };
@@ -856,8 +858,8 @@ __global__ __launch_bounds__(NW * 64, 1) void k_pstep(Args a) {
                     const float n0 = (x0 * inv) * w0, n1 = (x1 * inv) * w1;
                     const float r0 = fmaf(n0, rc, -(n1 * rsn)), r1 = fmaf(n1, rc, n0 * rsn);
                     if (!isk) {
-                        att.qs[t][lane] = r0;
-                        att.qs[t][lane + 64] = r1;
+                        qt_put_pieces(&att.qp[3 * t][lane], HD, r0);
+                        qt_put_pieces(&att.qp[3 * t][lane + 64], HD, r1);
                     } else {
                         const float *vs = s_qkv + HPK * HD + HD;
                         att.knew[lane] = f2bf_trunc(r0); att.knew[lane + 64] = f2bf_trunc(r1);
@@ -865,14 +867,9 @@ __global__ __launch_bounds__(NW * 64, 1) void k_pstep(Args a) {
                     }
                 }
                 __syncthreads();
-                // scores: lane (ksub, kpg) takes dims ksub*8.. of keys u*16 + wave*4 + kpg of
-                // each LDS block of KVB keys (the same keys, in the same order, as k_attn)
-                const int ksub = lane & 15, kpg = lane >> 4;
-                float qv[HPK][8];
-#pragma unroll
-                for (int h = 0; h < HPK; h++)
-#pragma unroll
-                    for (int e = 0; e < 8; e++) qv[h][e] = att.qs[h][ksub * 8 + e];
+                // scores on MFMA (qt_attn_mf.h): 16-key tiles u = wave, wave + NWB of each
+                // LDS block of KVB keys, the same tiles and arithmetic as k_attn
+                const int hq = lane >> 4, dq = lane & 15;
                 for (int kb = 0; kb < n; kb += KVB) {
                     if (kb > 0) {   // chunks longer than KVB keys (caches beyond G*KVB positions)
                         __syncthreads();
@@ -881,37 +878,20 @@ __global__ __launch_bounds__(NW * 64, 1) void k_pstep(Args a) {
                         __syncthreads();
                     }
                     const int nk = min(KVB, n - kb);
-                    // unrolled over the keys of the block with masking (rows past nk read
-                    // stale LDS and are discarded), so the LDS reads of all keys are issued
-                    // together; the unrolled length is the block's 16-key groups rounded up
-                    // to an even count (uniform branch); waves 0..NWB-1 only (the key-to-lane
-                    // map of the per-kernel twin)
-                    auto scores = [&](auto nuc) {
-                        constexpr int NU = decltype(nuc)::value;
-#pragma unroll
-                        for (int u = 0; u < NU; u++) {
-                            const int jl = u * 16 + wave * 4 + kpg, jj = kb + jl;
-                            const uint4 kw = (j0 + jj == pos) ? *reinterpret_cast<const uint4 *>(att.knew + ksub * 8)
-                                                              : *reinterpret_cast<const uint4 *>(&s_kv[0][jl * HD + ksub * 8]);
-                            const uint32_t w4[4] = {kw.x, kw.y, kw.z, kw.w};
-                            float kf[8];
-#pragma unroll
-                            for (int m = 0; m < 4; m++) { kf[2 * m] = bf_lo(w4[m]); kf[2 * m + 1] = bf_hi(w4[m]); }
-#pragma unroll
-                            for (int h = 0; h < HPK; h++) {
-                                float sv = 0.f;
-#pragma unroll
-                                for (int e = 0; e < 8; e++) sv = fmaf(qv[h][e], kf[e], sv);
-                                sv = group_sum<16>(sv);
-                                if (ksub == 0 && jl < nk) att.sc[h][jj] = sv * a.scale;
-                            }
+                    const int nrow = pos - j0 - kb;        // block row of the appended key
+                    if (wave < NWB && (wave + NWB) * 16 < nk) {
+                        const int r0[2] = {wave * 16, (wave + NWB) * 16};
+                        float sv[2];
+                        qt_att_qk<HPK, 2>(&att.qp[0][0], s_kv[0], att.knew, r0, nrow, lane, sv);
+                        if (hq < HPK) {
+                            att.sc[hq][kb + r0[0] + dq] = sv[0] * a.scale;
+                            if (r0[1] + dq < nk) att.sc[hq][kb + r0[1] + dq] = sv[1] * a.scale;
                         }
-                    };
-                    if (wave < NWB) {
-                        if (nk <= 32) scores(std::integral_constant<int, 2>());
-                        else if (nk <= 64) scores(std::integral_constant<int, 4>());
-                        else if (nk <= 96) scores(std::integral_constant<int, 6>());
-                        else scores(std::integral_constant<int, 8>());
+                    } else if (wave < NWB && wave * 16 < nk) {
+                        const int r0[1] = {wave * 16};
+                        float sv[1];
+                        qt_att_qk<HPK, 1>(&att.qp[0][0], s_kv[0], att.knew, r0, nrow, lane, sv);
+                        if (hq < HPK && r0[0] + dq < nk) att.sc[hq][kb + r0[0] + dq] = sv[0] * a.scale;
                     }
                 }
                 __syncthreads();
@@ -923,18 +903,17 @@ __global__ __launch_bounds__(NW * 64, 1) void k_pstep(Args a) {
                     float lsum = 0.f;
                     for (int j = lane; j < n; j += 64) {
                         const float p = expf(att.sc[h][j] - m);
-                        att.sc[h][j] = p;
+                        qt_put_pieces(&att.pp[3 * h][j], CHMAX, p);
                         lsum += p;
                     }
                     lsum = group_sum<64>(lsum);
                     if (lane == 0) { att.stat[h][0] = m; att.stat[h][1] = lsum; }
+                    for (int j = n + lane; j < ((n + 31) & ~31); j += 64)   // P.V tiles past the chunk
+                        qt_put_pieces(&att.pp[3 * h][j], CHMAX, 0.f);
                 }
                 __syncthreads();
-                float o[HPK][8];
-#pragma unroll
-                for (int h = 0; h < HPK; h++)
-#pragma unroll
-                    for (int e = 0; e < 8; e++) o[h][e] = 0.f;
+                // P.V on MFMA: wave w < NWB owns dims [32w, 32w + 32) as two 16-dim tiles
+                qt_f32x4 acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
                 for (int kb = 0; kb < n; kb += KVB) {
                     if (kb > 0) {
                         __syncthreads();
@@ -943,58 +922,22 @@ __global__ __launch_bounds__(NW * 64, 1) void k_pstep(Args a) {
                         __syncthreads();
                     }
                     const int nk = min(KVB, n - kb);
-                    auto pv = [&](auto nuc) {
-                        constexpr int NU = decltype(nuc)::value;
-#pragma unroll
-                        for (int u = 0; u < NU; u++) {
-                            const int jl = u * 16 + wave * 4 + kpg, jj = kb + jl;
-                            const bool ok = jl < nk;
-                            const uint4 vw = (j0 + jj == pos) ? *reinterpret_cast<const uint4 *>(att.vnew + ksub * 8)
-                                                              : *reinterpret_cast<const uint4 *>(&s_kv[1][jl * HD + ksub * 8]);
-                            const uint32_t w4[4] = {vw.x, vw.y, vw.z, vw.w};
-                            float vf[8];
-#pragma unroll
-                            for (int m = 0; m < 4; m++) { vf[2 * m] = bf_lo(w4[m]); vf[2 * m + 1] = bf_hi(w4[m]); }
-#pragma unroll
-                            for (int h = 0; h < HPK; h++) {
-                                const float p = att.sc[h][min(jj, CHMAX - 1)];
-#pragma unroll
-                                for (int e = 0; e < 8; e++) o[h][e] = ok ? fmaf(p, vf[e], o[h][e]) : o[h][e];
-                            }
-                        }
-                    };
+                    const int nrow = pos - j0 - kb;
                     if (wave < NWB) {
-                        if (nk <= 32) pv(std::integral_constant<int, 2>());
-                        else if (nk <= 64) pv(std::integral_constant<int, 4>());
-                        else if (nk <= 96) pv(std::integral_constant<int, 6>());
-                        else pv(std::integral_constant<int, 8>());
+                        const uint16_t *pp = &att.pp[0][0], *vn = att.vnew, *zr = att.zeros;
+                        const int nkt = (nk + 31) >> 5, d0 = 32 * wave;
+                        if (nkt == 1) qt_att_pv<HPK, 1>(pp, CHMAX, kb, s_kv[1], vn, zr, d0, nrow, nk, lane, acc0, acc1);
+                        else if (nkt == 2) qt_att_pv<HPK, 2>(pp, CHMAX, kb, s_kv[1], vn, zr, d0, nrow, nk, lane, acc0, acc1);
+                        else if (nkt == 3) qt_att_pv<HPK, 3>(pp, CHMAX, kb, s_kv[1], vn, zr, d0, nrow, nk, lane, acc0, acc1);
+                        else qt_att_pv<HPK, 4>(pp, CHMAX, kb, s_kv[1], vn, zr, d0, nrow, nk, lane, acc0, acc1);
                     }
                 }
-                // sum over the 4 key groups of a wave (lanes l, l^16, l^32, l^48) with the
-                // gfx950 row swaps: same additions, in the same order, as the per-kernel
-                // twin's shuffles
-#pragma unroll
-                for (int h = 0; h < HPK; h++)
-#pragma unroll
-                    for (int e = 0; e < 8; e++) {
-                        const float v = o[h][e];
-                        const auto r16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-                        const float a16 = __uint_as_float(r16[0]) + __uint_as_float(r16[1]);
-                        const auto r32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(a16), __float_as_uint(a16), false, false);
-                        o[h][e] = __uint_as_float(r32[0]) + __uint_as_float(r32[1]);
-                    }
-                if (kpg == 0 && wave < NWB) {
-#pragma unroll
-                    for (int h = 0; h < HPK; h++)
-#pragma unroll
-                        for (int e = 0; e < 8; e++) att.ored[wave][h][ksub * 8 + e] = o[h][e];
-                }
-                __syncthreads();
                 PS_MARK(ph, 3);
                 unsigned long long *mypart = blk + R::OPART + (size_t)(g * G + c) * HPK * PS;
-                for (int i = tid; i < HPK * HD; i += NT) {
-                    const int h = i / HD, d = i % HD;
-                    st_tag(mypart + h * PS + 2 + d, att.ored[0][h][d] + att.ored[1][h][d] + att.ored[2][h][d] + att.ored[3][h][d], tag);
+                if (wave < NWB && hq < HPK) {
+                    const int od = 32 * wave + dq;
+                    st_tag(mypart + hq * PS + 2 + od, (acc0[0] + acc0[1]) + acc0[2], tag);
+                    st_tag(mypart + hq * PS + 2 + od + 16, (acc1[0] + acc1[1]) + acc1[2], tag);
                 }
                 if (tid < HPK) {
                     st_tag(mypart + tid * PS, att.stat[tid][0], tag);
