@@ -85,10 +85,10 @@ __global__ __launch_bounds__(QT_WG) void k_attn(QtAttnArgs a) {
 
     constexpr int PS = 2 + QT_HD;
     constexpr int KVBYTES = 2 * QT_KVB * QT_HD * 2, MBYTES = QT_ATT_G * HPK * PS * 4;
+    static_assert(QT_WAVES * 32 == QT_KVB, "each wave takes two 16-key tiles of a block");
     __shared__ __align__(16) uint16_t qp[HPK * 3][QT_HD];       // query pieces (qt_attn_mf.h)
-    __shared__ float sc[HPK][QT_CH_MAX];                         // scores
-    __shared__ __align__(16) uint16_t pp[HPK * 3][QT_CH_MAX];   // probability pieces, 0 past the chunk
-    __shared__ float stat[HPK][2];
+    __shared__ __align__(16) uint16_t pp[HPK * 3][QT_KVB];      // probability pieces of a block (k-tile w: wave w)
+    __shared__ float ml[QT_WAVES][HPK][2];                      // per-k-tile (max, exp-sum)
     __shared__ __align__(16) uint16_t knew[QT_HD];
     __shared__ __align__(16) uint16_t vnew[QT_HD];
     __shared__ __align__(16) uint16_t zeros[8];
@@ -160,78 +160,35 @@ __global__ __launch_bounds__(QT_WG) void k_attn(QtAttnArgs a) {
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();   // (also: every wave's LDS copies of the first block have landed)
 
-    // ---- 2. scores on MFMA: 16-key tiles u = wave, wave + 4 of each block ----
+    // ---- 2. per block (qt_attn_mf.h): wave w scores its k-tile (16-key tiles w, w + 4),
+    // barrier, then takes dims [32w, 32w + 32) of P.V over all k-tiles ----
+    QtAttRun run;
+    qt_att_run_init(run);
     for (int kb = 0; kb < n; kb += QT_KVB) {
         if (kb > 0) {   // chunks longer than one block (caches beyond G*QT_KVB keys)
             __syncthreads();
-            stage(kb, true, false);
+            stage(kb, true, true);
             __builtin_amdgcn_s_waitcnt(0);
             __syncthreads();
         }
         const int nk = min(QT_KVB, n - kb);
         const int nrow = PREP ? pos - j0 - kb : -1;   // block row of the appended key
-        if ((wave + QT_WAVES) * 16 < nk) {
-            const int r0[2] = {wave * 16, (wave + QT_WAVES) * 16};
-            float sv[2];
-            qt_att_qk<HPK, 2>(&qp[0][0], s_kv[0], knew, r0, nrow, lane, sv);
-            if (pg < HPK) {
-                sc[pg][kb + r0[0] + sub] = sv[0] * a.scale;
-                if (r0[1] + sub < nk) sc[pg][kb + r0[1] + sub] = sv[1] * a.scale;
-            }
-        } else if (wave * 16 < nk) {
-            const int r0[1] = {wave * 16};
-            float sv[1];
-            qt_att_qk<HPK, 1>(&qp[0][0], s_kv[0], knew, r0, nrow, lane, sv);
-            if (pg < HPK && r0[0] + sub < nk) sc[pg][kb + r0[0] + sub] = sv[0] * a.scale;
-        }
+        qt_att_tiles<HPK, QT_WAVES>(&qp[0][0], s_kv[0], knew, &pp[0][0], QT_KVB, &ml[0][0][0], wave, nk, nrow, a.scale,
+                                    lane);
+        __syncthreads();
+        float o[2], M, l;
+        qt_att_pv<HPK, QT_WAVES>(&pp[0][0], QT_KVB, &ml[0][0][0], s_kv[1], vnew, zeros, 32 * wave, nk, nrow, lane, o, M, l);
+        qt_att_run_add(run, o, M, l);
     }
-    __syncthreads();
-
-    // ---- 3. chunk softmax statistics ----
-    for (int h = wave; h < HPK; h += QT_WAVES) {
-        float m = -INFINITY;
-        for (int j = lane; j < n; j += 64) m = fmaxf(m, sc[h][j]);
-        m = group_max<64>(m);
-        float l = 0.f;
-        for (int j = lane; j < n; j += 64) {
-            float p = expf(sc[h][j] - m);
-            qt_put_pieces(&pp[3 * h][j], QT_CH_MAX, p);
-            l += p;
-        }
-        l = group_sum<64>(l);
-        if (lane == 0) { stat[h][0] = m; stat[h][1] = l; }
-        for (int j = n + lane; j < ((n + 31) & ~31); j += 64)   // P.V key tiles past the chunk
-            qt_put_pieces(&pp[3 * h][j], QT_CH_MAX, 0.f);
-    }
-    __syncthreads();
-
-    // ---- 4. o = sum_j p_j v_j on MFMA: wave w owns dims [32w, 32w + 32) as two 16-dim
-    // tiles; lane (h, d) = (pg, sub) ends with head h's sums for dims 32w + d, 32w + 16 + d ----
-    qt_f32x4 acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
-    for (int kb = 0; kb < n; kb += QT_KVB) {
-        if (kb > 0) {
-            __syncthreads();
-            stage(kb, false, true);
-            __builtin_amdgcn_s_waitcnt(0);
-            __syncthreads();
-        }
-        const int nk = min(QT_KVB, n - kb);
-        const int nrow = PREP ? pos - j0 - kb : -1;
-        const int nkt = (nk + 31) >> 5;
-        if (nkt == 1) qt_att_pv<HPK, 1>(&pp[0][0], QT_CH_MAX, kb, s_kv[1], vnew, zeros, 32 * wave, nrow, nk, lane, acc0, acc1);
-        else if (nkt == 2) qt_att_pv<HPK, 2>(&pp[0][0], QT_CH_MAX, kb, s_kv[1], vnew, zeros, 32 * wave, nrow, nk, lane, acc0, acc1);
-        else if (nkt == 3) qt_att_pv<HPK, 3>(&pp[0][0], QT_CH_MAX, kb, s_kv[1], vnew, zeros, 32 * wave, nrow, nk, lane, acc0, acc1);
-        else qt_att_pv<HPK, 4>(&pp[0][0], QT_CH_MAX, kb, s_kv[1], vnew, zeros, 32 * wave, nrow, nk, lane, acc0, acc1);
-    }
-    const float o0 = (acc0[0] + acc0[1]) + acc0[2], o1 = (acc1[0] + acc1[1]) + acc1[2];
+    // lane: head pg, dims 32*wave + sub and + 16
     const int od = 32 * wave + sub;
 
-    // ---- 5. write (single chunk) or publish partial and merge in the last workgroup ----
+    // ---- 3. write (single chunk) or publish partial and merge in the last workgroup ----
     if (nch == 1) {
         if (pg < HPK) {
-            const float r = 1.0f / stat[pg][1];
-            a.out[(g * HPK + pg) * QT_HD + od] = o0 * r;
-            a.out[(g * HPK + pg) * QT_HD + od + 16] = o1 * r;
+            const float r = 1.0f / run.l;
+            a.out[(g * HPK + pg) * QT_HD + od] = run.o[0] * r;
+            a.out[(g * HPK + pg) * QT_HD + od + 16] = run.o[1] * r;
         }
         return;
     }
@@ -241,10 +198,10 @@ __global__ __launch_bounds__(QT_WG) void k_attn(QtAttnArgs a) {
     // 256-workgroup grid on MI355X; the merging workgroup reads with agent-scope loads.
     float *mypart = a.part + ((size_t)(g * G + c) * HPK) * PS;
     if (pg < HPK) {
-        st_agent(mypart + pg * PS + 2 + od, o0);
-        st_agent(mypart + pg * PS + 2 + od + 16, o1);
+        st_agent(mypart + pg * PS + 2 + od, run.o[0]);
+        st_agent(mypart + pg * PS + 2 + od + 16, run.o[1]);
+        if (wave == 0 && sub == 0) { st_agent(mypart + pg * PS, run.m); st_agent(mypart + pg * PS + 1, run.l); }
     }
-    if (tid < HPK) { st_agent(mypart + tid * PS, stat[tid][0]); st_agent(mypart + tid * PS + 1, stat[tid][1]); }
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
     if (tid == 0)

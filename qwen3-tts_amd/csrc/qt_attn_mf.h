@@ -108,39 +108,99 @@ __device__ __forceinline__ void qt_att_qk(const uint16_t *qp, const uint16_t *kb
     }
 }
 
-// P.V over NKT 32-key tiles from block row 0 for the dims d0 .. d0+15 and d0+16 .. d0+31:
-// A = probability pieces pp[(3h + p) * stride + kp + key] (LDS, zero past the chunk),
-// B = value rows of the staged V block vb read with the transposing LDS load (lane j of
-// a 16-lane group points at row j/4, dims 4(j%4) .. +3 and receives dim j of the 4
-// rows); row nrow comes from vnew, rows >= nk (stale LDS) from 8 zero bytes.
-template <int HPK, int NKT>
-__device__ __forceinline__ void qt_att_pv(const uint16_t *pp, int stride, int kp, const uint16_t *vb,
-                                          const uint16_t *vnew, const uint16_t *zeros, int d0, int nrow, int nk,
-                                          int lane, qt_f32x4 &acc0, qt_f32x4 &acc1) {
-    const int j = lane & 15, kg = lane >> 4;
-    qt_u32x4 pa[NKT], vv[NKT][2];
+// ---- a staged block of NWV*32 keys in two steps, one workgroup barrier between ----
+// Step 1 (qt_att_tiles), wave w: scores of its 16-key tiles w and w + NWV (block rows
+// 16w .. +15 and 16(w+NWV) .. +15 = k-tile w), their max m_w per head, p = e^(s - m_w)
+// as pieces into column 32w + k of pp, and l_w = sum p; (m_w, l_w) into ml.
+// Step 2 (qt_att_pv), wave w: dims d0 .. d0+31 of every head over all NWV k-tiles, one
+// MFMA per (k-tile, 16 dims), then o = sum_t e^(m_t - M) o_t with M = max_t m_t, and
+// l = sum_t e^(m_t - M) l_t.  Lane l works on head l/16 throughout.
+__device__ __forceinline__ void qt_wave_lds_sync() {   // this wave's LDS stores before its loads
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+template <int HPK, int NWV>
+__device__ __forceinline__ void qt_att_tiles(const uint16_t *qp, const uint16_t *kblk, const uint16_t *knew,
+                                             uint16_t *pp, int pstride, float *ml, int w, int nk, int nrow,
+                                             float scale, int lane) {
+    const int r0[2] = {16 * w, 16 * (w + NWV)};
+    float sv[2];
+    qt_att_qk<HPK, 2>(qp, kblk, knew, r0, nrow, lane, sv);   // rows past nk: discarded
+    const int h = lane >> 4, key = lane & 15;
+    const bool va = r0[0] + key < nk, vb = r0[1] + key < nk;
+    const float sa = va ? sv[0] * scale : -INFINITY, sb = vb ? sv[1] * scale : -INFINITY;
+    const float m = group_max<16>(fmaxf(sa, sb));            // -inf: no keys in this k-tile
+    const float pa = va ? expf(sa - m) : 0.f, pb = vb ? expf(sb - m) : 0.f;
+    const float ls = group_sum<16>(pa + pb);
+    if (h < HPK) {
+        qt_put_pieces(pp + 3 * h * pstride + 32 * w + key, pstride, pa);
+        qt_put_pieces(pp + 3 * h * pstride + 32 * w + 16 + key, pstride, pb);
+        if (key == 0) { ml[(w * HPK + h) * 2] = m; ml[(w * HPK + h) * 2 + 1] = ls; }
+    }
+}
+
+template <int HPK, int NWV>
+__device__ __forceinline__ void qt_att_pv(const uint16_t *pp, int pstride, const float *ml, const uint16_t *vblk,
+                                          const uint16_t *vnew, const uint16_t *zeros, int d0, int nk, int nrow,
+                                          int lane, float (&o)[2], float &M, float &l) {
+    const int kg = lane >> 4, j = lane & 15, h = lane >> 4;
+    const int hc = h < HPK ? h : HPK - 1;
+    qt_u32x4 pa[NWV], vv[NWV][2];
+    float mw[NWV], lw[NWV];
 #pragma unroll
-    for (int t = 0; t < NKT; t++) {
-        pa[t] = qt_att_rowpiece<HPK>(pp, stride, kp + 32 * t, lane);
+    for (int t = 0; t < NWV; t++) {
+        pa[t] = qt_att_rowpiece<HPK>(pp, pstride, 32 * t, lane);
+        mw[t] = ml[(t * HPK + hc) * 2];
+        lw[t] = ml[(t * HPK + hc) * 2 + 1];
 #pragma unroll
         for (int dt = 0; dt < 2; dt++) {
             const int col = d0 + 16 * dt + 4 * (j & 3);
             const uint16_t *p[2];
 #pragma unroll
             for (int r2 = 0; r2 < 2; r2++) {
-                const int row = 32 * t + 8 * kg + 4 * r2 + (j >> 2);
-                p[r2] = row == nrow ? vnew + col : row >= nk ? zeros : vb + row * 128 + qt_vslot(row, col >> 3) * 8 + (col & 7);
+                const int kk = 8 * kg + 4 * r2 + (j >> 2);
+                const int row = kk < 16 ? 16 * t + kk : 16 * (t + NWV) + kk - 16;
+                p[r2] = row == nrow ? vnew + col
+                      : row >= nk   ? zeros
+                                    : vblk + row * 128 + qt_vslot(row, col >> 3) * 8 + (col & 7);
             }
             vv[t][dt] = qt_lds_tr8x2(p[0], p[1]);
         }
     }
-    static_assert(NKT >= 1 && NKT <= 4, "one to four key tiles");
-    constexpr int T1 = NKT > 1 ? 1 : 0, T2 = NKT > 2 ? 2 : 0, T3 = NKT > 3 ? 3 : 0;
-    asm volatile("" : "+v"(pa[0]), "+v"(vv[0][0]), "+v"(vv[0][1]), "+v"(pa[T1]), "+v"(vv[T1][0]), "+v"(vv[T1][1]),
-                 "+v"(pa[T2]), "+v"(vv[T2][0]), "+v"(vv[T2][1]), "+v"(pa[T3]), "+v"(vv[T3][0]), "+v"(vv[T3][1]));
+    static_assert(NWV == 4, "four k-tiles");
+    asm volatile("" : "+v"(pa[0]), "+v"(pa[1]), "+v"(pa[2]), "+v"(pa[3]), "+v"(vv[0][0]), "+v"(vv[0][1]),
+                 "+v"(vv[1][0]), "+v"(vv[1][1]), "+v"(vv[2][0]), "+v"(vv[2][1]), "+v"(vv[3][0]), "+v"(vv[3][1]));
+    qt_f32x4 acc[NWV][2];
 #pragma unroll
-    for (int t = 0; t < NKT; t++) {
-        acc0 = qt_mfma_bf16(pa[t], vv[t][0], acc0);
-        acc1 = qt_mfma_bf16(pa[t], vv[t][1], acc1);
+    for (int t = 0; t < NWV; t++)
+#pragma unroll
+        for (int dt = 0; dt < 2; dt++) acc[t][dt] = qt_mfma_bf16(pa[t], vv[t][dt], qt_f32x4{0.f, 0.f, 0.f, 0.f});
+    M = -INFINITY;
+#pragma unroll
+    for (int t = 0; t < NWV; t++) M = fmaxf(M, mw[t]);
+    o[0] = o[1] = 0.f;
+    l = 0.f;
+#pragma unroll
+    for (int t = 0; t < NWV; t++) {
+        const float f = mw[t] == -INFINITY ? 0.f : expf(mw[t] - M);
+        l = fmaf(lw[t], f, l);
+#pragma unroll
+        for (int dt = 0; dt < 2; dt++) o[dt] = fmaf((acc[t][dt][0] + acc[t][dt][1]) + acc[t][dt][2], f, o[dt]);
     }
+}
+
+// Running (max, sum, output) across the blocks of a chunk longer than one block.
+struct QtAttRun {
+    float m, l, o[2];
+};
+__device__ __forceinline__ void qt_att_run_init(QtAttRun &r) { r.m = -INFINITY; r.l = 0.f; r.o[0] = r.o[1] = 0.f; }
+__device__ __forceinline__ void qt_att_run_add(QtAttRun &r, const float (&o)[2], float M, float l) {
+    const float mn = fmaxf(r.m, M);
+    const float fr = r.m == -INFINITY ? 0.f : expf(r.m - mn), fb = expf(M - mn);
+    r.l = fmaf(r.l, fr, l * fb);
+    r.o[0] = fmaf(r.o[0], fr, o[0] * fb);
+    r.o[1] = fmaf(r.o[1], fr, o[1] * fb);
+    r.m = mn;
 }

@@ -53,6 +53,7 @@ constexpr int PS = 2 + HD;       // partial record per head: max, sum, o[HD]
 constexpr unsigned POLL_LIMIT = 1u << 17;
 constexpr int MAXL = 64;         // layers whose table fits the LDS copy
 constexpr int KVB = 128;         // keys of a chunk staged in LDS at once (K and V: 64 KiB)
+static_assert(NWB * 32 == KVB, "each attention wave takes two 16-key tiles of a block");
 
 // Loads through pointers read from memory are made explicitly global (address space
 // 1): a generic (flat) load would also count against the LDS counter, so every later
@@ -639,13 +640,13 @@ struct Ring {
 };
 
 // ---- the kernel ---------------------------------------------------------------------------
-// LDS of the attention phase (B) and the merge (M, which reuses sc for its inputs)
+// LDS of the attention phase (B) and the merge (M)
 template <int HPK>
 struct AttLds {
-    __attribute__((aligned(16))) uint16_t qp[HPK * 3][HD];       // rotated queries as bf16 pieces (qt_attn_mf.h)
-    float sc[HPK][CHMAX];                                         // scores
-    __attribute__((aligned(16))) uint16_t pp[HPK * 3][CHMAX];    // probability pieces, 0 past the chunk
-    float stat[HPK][2];                // chunk (max, sum) per head
+    __attribute__((aligned(16))) uint16_t qp[HPK * 3][HD];     // rotated queries as bf16 pieces (qt_attn_mf.h)
+    __attribute__((aligned(16))) uint16_t pp[HPK * 3][KVB];    // probability pieces of a block (k-tile w: wave w)
+    float ml[NWB][HPK][2];                                      // per-k-tile (max, exp-sum)
+    float mst[G * 10];                                          // merge (M) inputs
     __attribute__((aligned(16))) uint16_t knew[HD], vnew[HD];   // key/value at pos (bf16)
     __attribute__((aligned(16))) uint16_t zeros[8];             // value rows past the chunk (P.V)
 };
@@ -867,81 +868,42 @@ __global__ __launch_bounds__(NW * 64, 1) void k_pstep(Args a) {
                     }
                 }
                 __syncthreads();
-                // scores on MFMA (qt_attn_mf.h): 16-key tiles u = wave, wave + NWB of each
-                // LDS block of KVB keys, the same tiles and arithmetic as k_attn
-                const int hq = lane >> 4, dq = lane & 15;
+                // per LDS block (qt_attn_mf.h, the same arithmetic as k_attn): wave w scores
+                // its k-tile (16-key tiles w, w + NWB), barrier, then takes dims [32w, 32w + 32)
+                // of P.V over all k-tiles
+                QtAttRun run;
+                qt_att_run_init(run);
                 for (int kb = 0; kb < n; kb += KVB) {
                     if (kb > 0) {   // chunks longer than KVB keys (caches beyond G*KVB positions)
                         __syncthreads();
-                        stage_kv(l, kb, true, false);
+                        stage_kv(l, kb, true, true);
                         __builtin_amdgcn_s_waitcnt(0);     // the barrier does not wait for LDS copies
                         __syncthreads();
                     }
                     const int nk = min(KVB, n - kb);
                     const int nrow = pos - j0 - kb;        // block row of the appended key
-                    if (wave < NWB && (wave + NWB) * 16 < nk) {
-                        const int r0[2] = {wave * 16, (wave + NWB) * 16};
-                        float sv[2];
-                        qt_att_qk<HPK, 2>(&att.qp[0][0], s_kv[0], att.knew, r0, nrow, lane, sv);
-                        if (hq < HPK) {
-                            att.sc[hq][kb + r0[0] + dq] = sv[0] * a.scale;
-                            if (r0[1] + dq < nk) att.sc[hq][kb + r0[1] + dq] = sv[1] * a.scale;
-                        }
-                    } else if (wave < NWB && wave * 16 < nk) {
-                        const int r0[1] = {wave * 16};
-                        float sv[1];
-                        qt_att_qk<HPK, 1>(&att.qp[0][0], s_kv[0], att.knew, r0, nrow, lane, sv);
-                        if (hq < HPK && r0[0] + dq < nk) att.sc[hq][kb + r0[0] + dq] = sv[0] * a.scale;
-                    }
-                }
-                __syncthreads();
-                PS_MARK(ph, 2);
-                for (int h = wave; h < HPK; h += NW) {
-                    float m = -INFINITY;
-                    for (int j = lane; j < n; j += 64) m = fmaxf(m, att.sc[h][j]);
-                    m = group_max<64>(m);
-                    float lsum = 0.f;
-                    for (int j = lane; j < n; j += 64) {
-                        const float p = expf(att.sc[h][j] - m);
-                        qt_put_pieces(&att.pp[3 * h][j], CHMAX, p);
-                        lsum += p;
-                    }
-                    lsum = group_sum<64>(lsum);
-                    if (lane == 0) { att.stat[h][0] = m; att.stat[h][1] = lsum; }
-                    for (int j = n + lane; j < ((n + 31) & ~31); j += 64)   // P.V tiles past the chunk
-                        qt_put_pieces(&att.pp[3 * h][j], CHMAX, 0.f);
-                }
-                __syncthreads();
-                // P.V on MFMA: wave w < NWB owns dims [32w, 32w + 32) as two 16-dim tiles
-                qt_f32x4 acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
-                for (int kb = 0; kb < n; kb += KVB) {
-                    if (kb > 0) {
-                        __syncthreads();
-                        stage_kv(l, kb, false, true);
-                        __builtin_amdgcn_s_waitcnt(0);
-                        __syncthreads();
-                    }
-                    const int nk = min(KVB, n - kb);
-                    const int nrow = pos - j0 - kb;
+                    if (wave < NWB)
+                        qt_att_tiles<HPK, NWB>(&att.qp[0][0], s_kv[0], att.knew, &att.pp[0][0], KVB, &att.ml[0][0][0],
+                                               wave, nk, nrow, a.scale, lane);
+                    __syncthreads();
+                    PS_MARK(ph, 2);
                     if (wave < NWB) {
-                        const uint16_t *pp = &att.pp[0][0], *vn = att.vnew, *zr = att.zeros;
-                        const int nkt = (nk + 31) >> 5, d0 = 32 * wave;
-                        if (nkt == 1) qt_att_pv<HPK, 1>(pp, CHMAX, kb, s_kv[1], vn, zr, d0, nrow, nk, lane, acc0, acc1);
-                        else if (nkt == 2) qt_att_pv<HPK, 2>(pp, CHMAX, kb, s_kv[1], vn, zr, d0, nrow, nk, lane, acc0, acc1);
-                        else if (nkt == 3) qt_att_pv<HPK, 3>(pp, CHMAX, kb, s_kv[1], vn, zr, d0, nrow, nk, lane, acc0, acc1);
-                        else qt_att_pv<HPK, 4>(pp, CHMAX, kb, s_kv[1], vn, zr, d0, nrow, nk, lane, acc0, acc1);
+                        float o[2], M, lsum;
+                        qt_att_pv<HPK, NWB>(&att.pp[0][0], KVB, &att.ml[0][0][0], s_kv[1], att.vnew, att.zeros, 32 * wave,
+                                            nk, nrow, lane, o, M, lsum);
+                        qt_att_run_add(run, o, M, lsum);
                     }
                 }
                 PS_MARK(ph, 3);
                 unsigned long long *mypart = blk + R::OPART + (size_t)(g * G + c) * HPK * PS;
+                const int hq = lane >> 4, od = 32 * wave + (lane & 15);
                 if (wave < NWB && hq < HPK) {
-                    const int od = 32 * wave + dq;
-                    st_tag(mypart + hq * PS + 2 + od, (acc0[0] + acc0[1]) + acc0[2], tag);
-                    st_tag(mypart + hq * PS + 2 + od + 16, (acc1[0] + acc1[1]) + acc1[2], tag);
-                }
-                if (tid < HPK) {
-                    st_tag(mypart + tid * PS, att.stat[tid][0], tag);
-                    st_tag(mypart + tid * PS + 1, att.stat[tid][1], tag);
+                    st_tag(mypart + hq * PS + 2 + od, run.o[0], tag);
+                    st_tag(mypart + hq * PS + 2 + od + 16, run.o[1], tag);
+                    if (wave == 0 && (lane & 15) == 0) {
+                        st_tag(mypart + hq * PS, run.m, tag);
+                        st_tag(mypart + hq * PS + 1, run.l, tag);
+                    }
                 }
                 if (append && wave == NW - 1) {
                     // KV append: agent-scope 32-bit stores of adjacent bf16 pairs (after the
@@ -962,7 +924,7 @@ __global__ __launch_bounds__(NW * 64, 1) void k_pstep(Args a) {
                 const int hh = c >> 4, d0 = (c & 15) * 8;
                 const unsigned long long *gp = blk + R::OPART + (size_t)g * G * HPK * PS + hh * PS;
                 // element i: chunk i/10, field i%10 (0 max, 1 sum, 2.. dims d0..d0+7)
-                float *st = &att.sc[0][0];
+                float *st = att.mst;
                 gather<2, NT>(nch * 10, [&](int i) {
                     const int cc = i / 10, f = i % 10;
                     return gp + (size_t)cc * HPK * PS + (f < 2 ? f : 2 + d0 + (f - 2));
@@ -976,7 +938,6 @@ __global__ __launch_bounds__(NW * 64, 1) void k_pstep(Args a) {
                                                     valid ? st[cc * 10 + 2 + dd] : 0.f, valid);
                     if (cc == 0) st_tag(blk + R::OATT + (2 * g + hh) * HD + d0 + dd, r, tag);
                 }
-                __syncthreads();   // st (the scores' LDS) is reused by the next B
             }
             tg2.load(ly.w[2], ly.s[2], rw_gu + 2 * RGU);
             PS_MARK(ph, 1); ph++;
