@@ -86,12 +86,11 @@ __global__ __launch_bounds__(QT_WG) void k_attn(QtAttnArgs a) {
     constexpr int PS = 2 + QT_HD;
     constexpr int KVBYTES = 2 * QT_KVB * QT_HD * 2, MBYTES = QT_ATT_G * HPK * PS * 4;
     static_assert(QT_WAVES * 32 == QT_KVB, "each wave takes two 16-key tiles of a block");
-    __shared__ __align__(16) uint16_t qp[HPK * 3][QT_HD];       // query pieces (qt_attn_mf.h)
-    __shared__ __align__(16) uint16_t pp[HPK * 3][QT_KVB];      // probability pieces of a block (k-tile w: wave w)
+    __shared__ __align__(16) uint16_t qp[16][QT_HD];            // query pieces, row 4h+p (qt_attn_mf.h)
+    __shared__ __align__(16) uint16_t pp[16][QT_KVB];           // probability pieces of a block (k-tile w: wave w)
     __shared__ float ml[QT_WAVES][HPK][2];                      // per-k-tile (max, exp-sum)
     __shared__ __align__(16) uint16_t knew[QT_HD];
     __shared__ __align__(16) uint16_t vnew[QT_HD];
-    __shared__ __align__(16) uint16_t zeros[8];
     // K rows, V rows of a key block; reused as the merge staging
     __shared__ __align__(16) uint16_t s_kvbuf[(KVBYTES > MBYTES ? KVBYTES : MBYTES) / 2];
     uint16_t(*s_kv)[QT_KVB * QT_HD] = reinterpret_cast<uint16_t(*)[QT_KVB * QT_HD]>(s_kvbuf);
@@ -138,8 +137,8 @@ __global__ __launch_bounds__(QT_WG) void k_attn(QtAttnArgs a) {
             float r0 = fmaf(n0, cs, -(n1 * sn));
             float r1 = fmaf(n1, cs, n0 * sn);
             if (!isk) {
-                qt_put_pieces(&qp[3 * t][lane], QT_HD, r0);
-                qt_put_pieces(&qp[3 * t][lane + 64], QT_HD, r1);
+                qt_put_pieces(&qp[4 * t][lane], QT_HD, r0);
+                qt_put_pieces(&qp[4 * t][lane + 64], QT_HD, r1);
             } else {
                 const float *vs = a.q + a.n_heads * QT_HD + a.n_kv * QT_HD + g * QT_HD;
                 const uint16_t k0 = f2bf_trunc(r0), k1 = f2bf_trunc(r1);
@@ -150,34 +149,43 @@ __global__ __launch_bounds__(QT_WG) void k_attn(QtAttnArgs a) {
                 vd[lane] = v0; vd[lane + 64] = v1;
                 knew[lane] = k0; knew[lane + 64] = k1;
                 vnew[lane] = v0; vnew[lane + 64] = v1;
+                const int r = pos - j0;            // its row in the first staged block
+                if (r < QT_KVB) {
+                    s_kv[0][qt_kidx(r, lane)] = k0; s_kv[0][qt_kidx(r, lane + 64)] = k1;
+                    s_kv[1][qt_vidx(r, lane)] = v0; s_kv[1][qt_vidx(r, lane + 64)] = v1;
+                }
             }
         }
     } else {
         for (int i = tid; i < HPK * QT_HD; i += QT_WG)
-            qt_put_pieces(&qp[3 * (i / QT_HD)][i % QT_HD], QT_HD, a.q[(g * HPK + i / QT_HD) * QT_HD + i % QT_HD]);
+            qt_put_pieces(&qp[4 * (i / QT_HD)][i % QT_HD], QT_HD, a.q[(g * HPK + i / QT_HD) * QT_HD + i % QT_HD]);
     }
-    if (tid < 8) zeros[tid] = 0;
+    qt_att_zero_rows<HPK>(&qp[0][0], QT_HD, tid, QT_WG);
+    qt_att_zero_rows<HPK>(&pp[0][0], QT_KVB, tid, QT_WG);
+    qt_att_zero_vrows(s_kv[1], min(QT_KVB, n), QT_KVB, tid, QT_WG);
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();   // (also: every wave's LDS copies of the first block have landed)
 
     // ---- 2. per block (qt_attn_mf.h): wave w scores its k-tile (16-key tiles w, w + 4),
     // barrier, then takes dims [32w, 32w + 32) of P.V over all k-tiles ----
+    const float scale2 = a.scale * QT_LOG2E;
     QtAttRun run;
     qt_att_run_init(run);
     for (int kb = 0; kb < n; kb += QT_KVB) {
+        const int nk = min(QT_KVB, n - kb);
         if (kb > 0) {   // chunks longer than one block (caches beyond G*QT_KVB keys)
             __syncthreads();
             stage(kb, true, true);
             __builtin_amdgcn_s_waitcnt(0);
+            const int nrow = pos - j0 - kb;   // the appended key's row, if in this block
+            if (PREP && wave == 0 && nrow >= 0 && nrow < nk) qt_att_put_kv(s_kv[0], s_kv[1], nrow, knew, vnew, lane);
+            qt_att_zero_vrows(s_kv[1], nk, QT_KVB, tid, QT_WG);
             __syncthreads();
         }
-        const int nk = min(QT_KVB, n - kb);
-        const int nrow = PREP ? pos - j0 - kb : -1;   // block row of the appended key
-        qt_att_tiles<HPK, QT_WAVES>(&qp[0][0], s_kv[0], knew, &pp[0][0], QT_KVB, &ml[0][0][0], wave, nk, nrow, a.scale,
-                                    lane);
+        qt_att_tiles<HPK, QT_WAVES>(&qp[0][0], s_kv[0], &pp[0][0], QT_KVB, &ml[0][0][0], wave, nk, scale2, lane);
         __syncthreads();
         float o[2], M, l;
-        qt_att_pv<HPK, QT_WAVES>(&pp[0][0], QT_KVB, &ml[0][0][0], s_kv[1], vnew, zeros, 32 * wave, nk, nrow, lane, o, M, l);
+        qt_att_pv<HPK, QT_WAVES>(&pp[0][0], QT_KVB, &ml[0][0][0], s_kv[1], 32 * wave, lane, o, M, l);
         qt_att_run_add(run, o, M, l);
     }
     // lane: head pg, dims 32*wave + sub and + 16
@@ -236,7 +244,7 @@ __global__ __launch_bounds__(QT_WG) void k_attn(QtAttnArgs a) {
             float Lsum = 0.f, V = 0.f;
             for (int cc = 0; cc < nch; cc++) {
                 const float *pr = mpart + (size_t)(cc * HPK + h) * PS;
-                const float f = expf(pr[0] - M);
+                const float f = qt_exp2(pr[0] - M);
                 Lsum = fmaf(pr[1], f, Lsum);
                 V = fmaf(pr[2 + d], f, V);
             }

@@ -7,13 +7,15 @@
 // l's accumulator i.  An f32 value x is split into three bf16 pieces whose sum is x
 // exactly (x truncated to bf16, the truncated rest, the remaining <= 8 significant
 // bits); a bf16 x bf16 product is exact in f32, so the matrix core adds, in f32, exact
-// products of the f32 query (probabilities) with the bf16 keys (values).
-//   scores: A = query pieces (row 4h+p = piece p of head h; p == 3 and h >= HPK rows
-//           zero), B = 16 key rows (key = column): lane l ends with the three piece
-//           sums of head l/16, key l%16, and the score is (D0 + D1) + D2.
-//   P.V:    A = probability pieces (same rows) over 32 keys, B = those keys' value rows
-//           for 16 dims, read with the transposing LDS load: lane l ends with head
-//           l/16, dim l%16, again as (D0 + D1) + D2 after the last key tile.
+// products of the f32 query (probabilities) with the bf16 keys (values).  The pieces
+// live in LDS as 16 rows, row 4h+p = piece p of head h; rows with p == 3 and heads >=
+// HPK stay zero (qt_att_zero_rows), so every lane reads its A operand unconditionally.
+//   scores: A = query pieces, B = 16 key rows (key = column): lane l ends with the three
+//           piece sums of head l/16, key l%16, and the score is (D0 + D1) + D2.
+//   P.V:    A = probability pieces over 32 keys, B = those keys' value rows for 16 dims,
+//           read with the transposing LDS load: lane l ends with head l/16, dim l%16.
+// Softmax runs in base 2: scores are scaled by scale*log2(e), so e^(s - m) is
+// 2^(s' - m') (v_exp_f32), and chunk maxima are published in those units.
 //
 // LDS layout of a staged key block (row j = 128 bf16 = 16 chunks of 16 bytes):
 //   K: chunk c of row j at slot c ^ (j & 15)   — the 16 keys of a score tile read one
@@ -22,7 +24,10 @@
 //      a transposing read covers rows {b..b+3, b+8..b+11} x 32 bytes per half-wave,
 //      which land on 8 different 32-byte bank groups.
 // The global->LDS copies pick their source chunk so that lane L of a 1-KiB copy (block
-// row 4i + L/16, slot L%16) fetches the chunk that belongs in that slot.
+// row 4i + L/16, slot L%16) fetches the chunk that belongs in that slot.  The key
+// appended by this step is written into its row by the workgroup (qt_kidx/qt_vidx,
+// qt_att_put_kv), and value rows past the chunk are zeroed (qt_att_zero_vrows): their
+// probabilities are 0, and stale bits could be NaN.
 #pragma once
 #include "qt_device.h"
 
@@ -31,8 +36,11 @@ typedef float qt_f32x4 __attribute__((ext_vector_type(4)));
 typedef short qt_i16x4 __attribute__((ext_vector_type(4)));
 typedef unsigned qt_u32x4 __attribute__((ext_vector_type(4)));
 
+#define QT_LOG2E 1.4426950408889634f
+
 __device__ __forceinline__ int qt_kslot(int row, int c) { return c ^ (row & 15); }
 __device__ __forceinline__ int qt_vslot(int row, int c) { return c ^ (2 * ((row & 3) | ((row >> 1) & 4))); }
+__device__ __forceinline__ float qt_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
 __device__ __forceinline__ qt_f32x4 qt_mfma_bf16(qt_u32x4 a, qt_u32x4 b, qt_f32x4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(qt_bf16x8, a), __builtin_bit_cast(qt_bf16x8, b),
@@ -58,49 +66,53 @@ __device__ __forceinline__ void qt_put_pieces(uint16_t *dst, int stride, float x
     dst[2 * stride] = (uint16_t)(__float_as_uint(r2) >> 16);
 }
 
-// A operand (row 4h+p = piece p of head h, rows with p == 3 or h >= HPK zero) for the
-// 8 consecutive k at column k0 + 8(l/16) of piece rows pc[(3h + p) * stride] (LDS)
+// Zero the rows of a [16][cols] piece array that no head writes (p == 3, h >= HPK).
 template <int HPK>
-__device__ __forceinline__ qt_u32x4 qt_att_rowpiece(const uint16_t *pc, int stride, int k0, int lane) {
-    const int m = lane & 15, h = m >> 2, p = m & 3;
-    const bool on = h < HPK && p < 3;
-    const qt_u32x4 v = qt_lds16(pc + ((h < HPK ? h : HPK - 1) * 3 + (p < 3 ? p : 2)) * stride + k0 + 8 * (lane >> 4));
-    return on ? v : qt_u32x4{0u, 0u, 0u, 0u};
+__device__ __forceinline__ void qt_att_zero_rows(uint16_t *pc, int cols, int tid, int nt) {
+    for (int i = tid; i < 16 * cols / 8; i += nt) {
+        const int row = i / (cols / 8);
+        if ((row & 3) == 3 || (row >> 2) >= HPK) *reinterpret_cast<uint4 *>(pc + 8 * i) = make_uint4(0u, 0u, 0u, 0u);
+    }
 }
 
-// Unscaled scores of T 16-key tiles (block rows r0[t] .. r0[t]+15 of the staged K block
-// kb): lane l gets the score of head l/16 with key row r0[t] + l%16 in sc[t].  qp: query
-// pieces [HPK][3][128] (LDS).  Row nrow (the key appended by this step, not staged) is
-// read from knew.  Every LDS read is issued before the first MFMA.
-template <int HPK, int T>
-__device__ __forceinline__ void qt_att_qk(const uint16_t *qp, const uint16_t *kb, const uint16_t *knew,
-                                          const int (&r0)[T], int nrow, int lane, float (&sc)[T]) {
-    const int kg = lane >> 4;
-    qt_u32x4 qa[4], kv[T][4];
+// Zero the value rows [nk, rows) of a staged V block (any slot order).
+__device__ __forceinline__ void qt_att_zero_vrows(uint16_t *vblk, int nk, int rows, int tid, int nt) {
+    for (int i = nk * 16 + tid; i < rows * 16; i += nt) *reinterpret_cast<uint4 *>(vblk + 8 * i) = make_uint4(0u, 0u, 0u, 0u);
+}
+
+// Element d (0..127) of block row `row`, at its swizzled place.
+__device__ __forceinline__ int qt_kidx(int row, int d) { return row * 128 + qt_kslot(row, d >> 3) * 8 + (d & 7); }
+__device__ __forceinline__ int qt_vidx(int row, int d) { return row * 128 + qt_vslot(row, d >> 3) * 8 + (d & 7); }
+
+// Block row `row` of K and V from the bf16 rows knew / vnew (lanes 0..31 of one wave).
+__device__ __forceinline__ void qt_att_put_kv(uint16_t *kblk, uint16_t *vblk, int row, const uint16_t *knew,
+                                              const uint16_t *vnew, int lane) {
+    if (lane < 16)
+        *reinterpret_cast<uint4 *>(kblk + row * 128 + qt_kslot(row, lane) * 8) = *reinterpret_cast<const uint4 *>(knew + 8 * lane);
+    else if (lane < 32)
+        *reinterpret_cast<uint4 *>(vblk + row * 128 + qt_vslot(row, lane - 16) * 8) =
+            *reinterpret_cast<const uint4 *>(vnew + 8 * (lane - 16));
+}
+
+// Scores of two 16-key tiles (block rows r0[t] .. r0[t]+15 of the staged K block kb):
+// lane l gets the q.k sum of head l/16 with key row r0[t] + l%16 in sc[t].  qp: query
+// pieces [16][128] (LDS).  Every LDS read is issued before the first MFMA.
+__device__ __forceinline__ void qt_att_qk2(const uint16_t *qp, const uint16_t *kb, const int (&r0)[2], int lane,
+                                           float (&sc)[2]) {
+    const int kg = lane >> 4, key = lane & 15;
+    qt_u32x4 qa[4], kv[2][4];
 #pragma unroll
-    for (int s = 0; s < 4; s++) qa[s] = qt_att_rowpiece<HPK>(qp, 128, 32 * s, lane);
+    for (int s = 0; s < 4; s++) qa[s] = qt_lds16(qp + key * 128 + 32 * s + 8 * kg);
 #pragma unroll
-    for (int t = 0; t < T; t++) {
-        const int row = r0[t] + (lane & 15);
-        const bool nw = row == nrow;
+    for (int t = 0; t < 2; t++)
 #pragma unroll
-        for (int s = 0; s < 4; s++) {
-            const int c = 4 * s + kg;
-            kv[t][s] = qt_lds16(nw ? knew + c * 8 : kb + row * 128 + qt_kslot(row, c) * 8);
-        }
-    }
+        for (int s = 0; s < 4; s++) kv[t][s] = qt_lds16(kb + (r0[t] + key) * 128 + ((4 * s + kg) ^ key) * 8);
     // one empty asm that takes every operand: all reads are issued before it, and it
     // waits once for all of them
-    static_assert(T == 1 || T == 2, "one or two score tiles");
-    if constexpr (T == 1)
-        asm volatile("" : "+v"(qa[0]), "+v"(qa[1]), "+v"(qa[2]), "+v"(qa[3]), "+v"(kv[0][0]), "+v"(kv[0][1]),
-                     "+v"(kv[0][2]), "+v"(kv[0][3]));
-    else
-        asm volatile("" : "+v"(qa[0]), "+v"(qa[1]), "+v"(qa[2]), "+v"(qa[3]), "+v"(kv[0][0]), "+v"(kv[0][1]),
-                     "+v"(kv[0][2]), "+v"(kv[0][3]), "+v"(kv[T - 1][0]), "+v"(kv[T - 1][1]), "+v"(kv[T - 1][2]),
-                     "+v"(kv[T - 1][3]));
+    asm volatile("" : "+v"(qa[0]), "+v"(qa[1]), "+v"(qa[2]), "+v"(qa[3]), "+v"(kv[0][0]), "+v"(kv[0][1]),
+                 "+v"(kv[0][2]), "+v"(kv[0][3]), "+v"(kv[1][0]), "+v"(kv[1][1]), "+v"(kv[1][2]), "+v"(kv[1][3]));
 #pragma unroll
-    for (int t = 0; t < T; t++) {
+    for (int t = 0; t < 2; t++) {
         qt_f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int s = 0; s < 4; s++) acc = qt_mfma_bf16(qa[s], kv[t][s], acc);
@@ -109,67 +121,62 @@ __device__ __forceinline__ void qt_att_qk(const uint16_t *qp, const uint16_t *kb
 }
 
 // ---- a staged block of NWV*32 keys in two steps, one workgroup barrier between ----
-// Step 1 (qt_att_tiles), wave w: scores of its 16-key tiles w and w + NWV (block rows
-// 16w .. +15 and 16(w+NWV) .. +15 = k-tile w), their max m_w per head, p = e^(s - m_w)
-// as pieces into column 32w + k of pp, and l_w = sum p; (m_w, l_w) into ml.
+// Step 1 (qt_att_tiles), wave w: scores (base 2) of its 16-key tiles w and w + NWV
+// (block rows 16w .. +15 and 16(w+NWV) .. +15 = k-tile w), their max m_w per head,
+// p = 2^(s - m_w) as pieces into columns 32w .. 32w+31 of pp, l_w = sum p; (m_w, l_w)
+// into ml.
 // Step 2 (qt_att_pv), wave w: dims d0 .. d0+31 of every head over all NWV k-tiles, one
-// MFMA per (k-tile, 16 dims), then o = sum_t e^(m_t - M) o_t with M = max_t m_t, and
-// l = sum_t e^(m_t - M) l_t.  Lane l works on head l/16 throughout.
-__device__ __forceinline__ void qt_wave_lds_sync() {   // this wave's LDS stores before its loads
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-}
-
+// MFMA per (k-tile, 16 dims), then o = sum_t 2^(m_t - M) o_t with M = max_t m_t, and
+// l = sum_t 2^(m_t - M) l_t.  Lane l works on head l/16 throughout.
 template <int HPK, int NWV>
-__device__ __forceinline__ void qt_att_tiles(const uint16_t *qp, const uint16_t *kblk, const uint16_t *knew,
-                                             uint16_t *pp, int pstride, float *ml, int w, int nk, int nrow,
-                                             float scale, int lane) {
+__device__ __forceinline__ void qt_att_tiles(const uint16_t *qp, const uint16_t *kblk, uint16_t *pp, int pstride,
+                                             float *ml, int w, int nk, float scale2, int lane) {
     const int r0[2] = {16 * w, 16 * (w + NWV)};
     float sv[2];
-    qt_att_qk<HPK, 2>(qp, kblk, knew, r0, nrow, lane, sv);   // rows past nk: discarded
+    qt_att_qk2(qp, kblk, r0, lane, sv);                    // rows past nk: discarded
     const int h = lane >> 4, key = lane & 15;
-    const bool va = r0[0] + key < nk, vb = r0[1] + key < nk;
-    const float sa = va ? sv[0] * scale : -INFINITY, sb = vb ? sv[1] * scale : -INFINITY;
-    const float m = group_max<16>(fmaxf(sa, sb));            // -inf: no keys in this k-tile
-    const float pa = va ? expf(sa - m) : 0.f, pb = vb ? expf(sb - m) : 0.f;
+    const float sa = r0[0] + key < nk ? sv[0] * scale2 : -INFINITY;
+    const float sb = r0[1] + key < nk ? sv[1] * scale2 : -INFINITY;
+    const float m = group_max<16>(fmaxf(sa, sb));         // -inf: no keys in this k-tile
+    const float mr = m == -INFINITY ? 0.f : m;
+    const float pa = qt_exp2(sa - mr), pb = qt_exp2(sb - mr);   // 2^-inf == 0
     const float ls = group_sum<16>(pa + pb);
     if (h < HPK) {
-        qt_put_pieces(pp + 3 * h * pstride + 32 * w + key, pstride, pa);
-        qt_put_pieces(pp + 3 * h * pstride + 32 * w + 16 + key, pstride, pb);
+        qt_put_pieces(pp + 4 * h * pstride + 32 * w + key, pstride, pa);
+        qt_put_pieces(pp + 4 * h * pstride + 32 * w + 16 + key, pstride, pb);
         if (key == 0) { ml[(w * HPK + h) * 2] = m; ml[(w * HPK + h) * 2 + 1] = ls; }
     }
 }
 
 template <int HPK, int NWV>
 __device__ __forceinline__ void qt_att_pv(const uint16_t *pp, int pstride, const float *ml, const uint16_t *vblk,
-                                          const uint16_t *vnew, const uint16_t *zeros, int d0, int nk, int nrow,
-                                          int lane, float (&o)[2], float &M, float &l) {
+                                          int d0, int lane, float (&o)[2], float &M, float &l) {
+    static_assert(NWV == 4, "four k-tiles");
     const int kg = lane >> 4, j = lane & 15, h = lane >> 4;
     const int hc = h < HPK ? h : HPK - 1;
     qt_u32x4 pa[NWV], vv[NWV][2];
     float mw[NWV], lw[NWV];
+    // transposed value reads: lane (kg, j) points at k-tile rows 8kg + 4r2 + j/4 (tile
+    // a: block rows 16t + k, tile b: rows 16(t + NWV) + k - 16), dims col .. col+3; the
+    // 16t part leaves the swizzle (row bits 0, 1, 3) unchanged
+    int vb[2][2];
+#pragma unroll
+    for (int dt = 0; dt < 2; dt++)
+#pragma unroll
+        for (int r2 = 0; r2 < 2; r2++) {
+            const int kk = 8 * kg + 4 * r2 + (j >> 2);
+            const int row = kk < 16 ? kk : kk + 16 * NWV - 16;
+            vb[dt][r2] = qt_vidx(row, d0 + 16 * dt + 4 * (j & 3));
+        }
 #pragma unroll
     for (int t = 0; t < NWV; t++) {
-        pa[t] = qt_att_rowpiece<HPK>(pp, pstride, 32 * t, lane);
+        pa[t] = qt_lds16(pp + (lane & 15) * pstride + 32 * t + 8 * kg);
         mw[t] = ml[(t * HPK + hc) * 2];
         lw[t] = ml[(t * HPK + hc) * 2 + 1];
 #pragma unroll
-        for (int dt = 0; dt < 2; dt++) {
-            const int col = d0 + 16 * dt + 4 * (j & 3);
-            const uint16_t *p[2];
-#pragma unroll
-            for (int r2 = 0; r2 < 2; r2++) {
-                const int kk = 8 * kg + 4 * r2 + (j >> 2);
-                const int row = kk < 16 ? 16 * t + kk : 16 * (t + NWV) + kk - 16;
-                p[r2] = row == nrow ? vnew + col
-                      : row >= nk   ? zeros
-                                    : vblk + row * 128 + qt_vslot(row, col >> 3) * 8 + (col & 7);
-            }
-            vv[t][dt] = qt_lds_tr8x2(p[0], p[1]);
-        }
+        for (int dt = 0; dt < 2; dt++)
+            vv[t][dt] = qt_lds_tr8x2(vblk + vb[dt][0] + 16 * t * 128, vblk + vb[dt][1] + 16 * t * 128);
     }
-    static_assert(NWV == 4, "four k-tiles");
     asm volatile("" : "+v"(pa[0]), "+v"(pa[1]), "+v"(pa[2]), "+v"(pa[3]), "+v"(vv[0][0]), "+v"(vv[0][1]),
                  "+v"(vv[1][0]), "+v"(vv[1][1]), "+v"(vv[2][0]), "+v"(vv[2][1]), "+v"(vv[3][0]), "+v"(vv[3][1]));
     qt_f32x4 acc[NWV][2];
@@ -177,14 +184,12 @@ __device__ __forceinline__ void qt_att_pv(const uint16_t *pp, int pstride, const
     for (int t = 0; t < NWV; t++)
 #pragma unroll
         for (int dt = 0; dt < 2; dt++) acc[t][dt] = qt_mfma_bf16(pa[t], vv[t][dt], qt_f32x4{0.f, 0.f, 0.f, 0.f});
-    M = -INFINITY;
-#pragma unroll
-    for (int t = 0; t < NWV; t++) M = fmaxf(M, mw[t]);
+    M = fmaxf(fmaxf(mw[0], mw[1]), fmaxf(mw[2], mw[3]));   // finite: k-tile 0 holds key 0
     o[0] = o[1] = 0.f;
     l = 0.f;
 #pragma unroll
     for (int t = 0; t < NWV; t++) {
-        const float f = mw[t] == -INFINITY ? 0.f : expf(mw[t] - M);
+        const float f = qt_exp2(mw[t] - M);                 // 0 for a k-tile without keys
         l = fmaf(lw[t], f, l);
 #pragma unroll
         for (int dt = 0; dt < 2; dt++) o[dt] = fmaf((acc[t][dt][0] + acc[t][dt][1]) + acc[t][dt][2], f, o[dt]);
@@ -198,7 +203,7 @@ struct QtAttRun {
 __device__ __forceinline__ void qt_att_run_init(QtAttRun &r) { r.m = -INFINITY; r.l = 0.f; r.o[0] = r.o[1] = 0.f; }
 __device__ __forceinline__ void qt_att_run_add(QtAttRun &r, const float (&o)[2], float M, float l) {
     const float mn = fmaxf(r.m, M);
-    const float fr = r.m == -INFINITY ? 0.f : expf(r.m - mn), fb = expf(M - mn);
+    const float fr = qt_exp2(r.m - mn), fb = qt_exp2(M - mn);   // first block: fr = 0, fb = 1
     r.l = fmaf(r.l, fr, l * fb);
     r.o[0] = fmaf(r.o[0], fr, o[0] * fb);
     r.o[1] = fmaf(r.o[1], fr, o[1] * fb);

@@ -115,14 +115,14 @@ __device__ __forceinline__ float block_sum(float v, float *red) {
 }
 
 // Merge of split-K softmax partials, one key chunk per lane of a 32-lane half-wave:
-// lane cc holds the chunk's running max m, exp-sum l and unnormalised output o (valid
-// for cc < nch).  out = sum_cc o_cc f_cc / sum_cc l_cc f_cc with f_cc = exp(m_cc - M),
-// M = max_cc m_cc; both sums are half-wave reductions, so every merge of the same
+// lane cc holds the chunk's running max m (in base-2 units: scores scaled by log2(e)),
+// exp-sum l and unnormalised output o (valid for cc < nch).  out = sum_cc o_cc f_cc /
+// sum_cc l_cc f_cc with f_cc = 2^(m_cc - M), M = max_cc m_cc; both sums are half-wave reductions, so every merge of the same
 // partials (per-kernel attention or the fused step) rounds identically.  A single
 // chunk reduces exactly to o / l.
 __device__ __forceinline__ float softmax_merge32(float m, float l, float o, bool valid) {
     const float M = group_max<32>(valid ? m : -INFINITY);
-    const float f = valid ? expf(m - M) : 0.f;
+    const float f = valid ? __builtin_amdgcn_exp2f(m - M) : 0.f;
     const float L = group_sum<32>(valid ? l * f : 0.f);
     const float V = group_sum<32>(valid ? o * f : 0.f);
     return V * (1.0f / L);

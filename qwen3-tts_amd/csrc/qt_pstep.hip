@@ -643,12 +643,11 @@ struct Ring {
 // LDS of the attention phase (B) and the merge (M)
 template <int HPK>
 struct AttLds {
-    __attribute__((aligned(16))) uint16_t qp[HPK * 3][HD];     // rotated queries as bf16 pieces (qt_attn_mf.h)
-    __attribute__((aligned(16))) uint16_t pp[HPK * 3][KVB];    // probability pieces of a block (k-tile w: wave w)
+    __attribute__((aligned(16))) uint16_t qp[16][HD];          // rotated queries as bf16 pieces, row 4h+p (qt_attn_mf.h)
+    __attribute__((aligned(16))) uint16_t pp[16][KVB];         // probability pieces of a block (k-tile w: wave w)
     float ml[NWB][HPK][2];                                      // per-k-tile (max, exp-sum)
     float mst[G * 10];                                          // merge (M) inputs
     __attribute__((aligned(16))) uint16_t knew[HD], vnew[HD];   // key/value at pos (bf16)
-    __attribute__((aligned(16))) uint16_t zeros[8];             // value rows past the chunk (P.V)
 };
 
 template <int PREC, int H, int F, int NW>
@@ -729,7 +728,8 @@ __global__ __launch_bounds__(NW * 64, 1) void k_pstep(Args a) {
     // the layer table lives in LDS: reading it never waits behind weight loads
     for (int i = tid; i < L * (int)(sizeof(Layer) / 8); i += NT)
         reinterpret_cast<unsigned long long *>(s_layers)[i] = ldg(reinterpret_cast<const unsigned long long *>(a.layers) + i);
-    if (tid < 8) att.zeros[tid] = 0;
+    qt_att_zero_rows<HPK>(&att.qp[0][0], HD, tid, NT);
+    qt_att_zero_rows<HPK>(&att.pp[0][0], KVB, tid, NT);
     __syncthreads();
 
     TQKV tq;
@@ -859,38 +859,48 @@ __global__ __launch_bounds__(NW * 64, 1) void k_pstep(Args a) {
                     const float n0 = (x0 * inv) * w0, n1 = (x1 * inv) * w1;
                     const float r0 = fmaf(n0, rc, -(n1 * rsn)), r1 = fmaf(n1, rc, n0 * rsn);
                     if (!isk) {
-                        qt_put_pieces(&att.qp[3 * t][lane], HD, r0);
-                        qt_put_pieces(&att.qp[3 * t][lane + 64], HD, r1);
+                        qt_put_pieces(&att.qp[4 * t][lane], HD, r0);
+                        qt_put_pieces(&att.qp[4 * t][lane + 64], HD, r1);
                     } else {
                         const float *vs = s_qkv + HPK * HD + HD;
-                        att.knew[lane] = f2bf_trunc(r0); att.knew[lane + 64] = f2bf_trunc(r1);
-                        att.vnew[lane] = f2bf_trunc(vs[lane]); att.vnew[lane + 64] = f2bf_trunc(vs[lane + 64]);
+                        const uint16_t k0 = f2bf_trunc(r0), k1 = f2bf_trunc(r1);
+                        const uint16_t v0 = f2bf_trunc(vs[lane]), v1 = f2bf_trunc(vs[lane + 64]);
+                        att.knew[lane] = k0; att.knew[lane + 64] = k1;
+                        att.vnew[lane] = v0; att.vnew[lane + 64] = v1;
+                        const int r = pos - j0;            // its row in the first staged block
+                        if (r < KVB) {
+                            s_kv[0][qt_kidx(r, lane)] = k0; s_kv[0][qt_kidx(r, lane + 64)] = k1;
+                            s_kv[1][qt_vidx(r, lane)] = v0; s_kv[1][qt_vidx(r, lane + 64)] = v1;
+                        }
                     }
                 }
+                qt_att_zero_vrows(s_kv[1], min(KVB, n), KVB, tid, NT);
                 __syncthreads();
                 // per LDS block (qt_attn_mf.h, the same arithmetic as k_attn): wave w scores
                 // its k-tile (16-key tiles w, w + NWB), barrier, then takes dims [32w, 32w + 32)
                 // of P.V over all k-tiles
+                const float scale2 = a.scale * QT_LOG2E;
                 QtAttRun run;
                 qt_att_run_init(run);
                 for (int kb = 0; kb < n; kb += KVB) {
+                    const int nk = min(KVB, n - kb);
                     if (kb > 0) {   // chunks longer than KVB keys (caches beyond G*KVB positions)
                         __syncthreads();
                         stage_kv(l, kb, true, true);
                         __builtin_amdgcn_s_waitcnt(0);     // the barrier does not wait for LDS copies
+                        const int nrow = pos - j0 - kb;    // the appended key's row, if in this block
+                        if (wave == 0 && nrow >= 0 && nrow < nk) qt_att_put_kv(s_kv[0], s_kv[1], nrow, att.knew, att.vnew, lane);
+                        qt_att_zero_vrows(s_kv[1], nk, KVB, tid, NT);
                         __syncthreads();
                     }
-                    const int nk = min(KVB, n - kb);
-                    const int nrow = pos - j0 - kb;        // block row of the appended key
                     if (wave < NWB)
-                        qt_att_tiles<HPK, NWB>(&att.qp[0][0], s_kv[0], att.knew, &att.pp[0][0], KVB, &att.ml[0][0][0],
-                                               wave, nk, nrow, a.scale, lane);
+                        qt_att_tiles<HPK, NWB>(&att.qp[0][0], s_kv[0], &att.pp[0][0], KVB, &att.ml[0][0][0], wave, nk,
+                                               scale2, lane);
                     __syncthreads();
                     PS_MARK(ph, 2);
                     if (wave < NWB) {
                         float o[2], M, lsum;
-                        qt_att_pv<HPK, NWB>(&att.pp[0][0], KVB, &att.ml[0][0][0], s_kv[1], att.vnew, att.zeros, 32 * wave,
-                                            nk, nrow, lane, o, M, lsum);
+                        qt_att_pv<HPK, NWB>(&att.pp[0][0], KVB, &att.ml[0][0][0], s_kv[1], 32 * wave, lane, o, M, lsum);
                         qt_att_run_add(run, o, M, lsum);
                     }
                 }
