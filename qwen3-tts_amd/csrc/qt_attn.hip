@@ -162,12 +162,12 @@ __global__ __launch_bounds__(QT_WG) void k_attn(QtAttnArgs a) {
     }
     qt_att_zero_rows<HPK>(&qp[0][0], QT_HD, tid, QT_WG);
     qt_att_zero_rows<HPK>(&pp[0][0], QT_KVB, tid, QT_WG);
-    qt_att_zero_vrows(s_kv[1], min(QT_KVB, n), QT_KVB, tid, QT_WG);
+    qt_att_zero_vrows(s_kv[1], min(QT_KVB, n), (min(QT_KVB, n) + 31) & ~31, tid, QT_WG);
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();   // (also: every wave's LDS copies of the first block have landed)
 
-    // ---- 2. per block (qt_attn_mf.h): wave w scores its k-tile (16-key tiles w, w + 4),
-    // barrier, then takes dims [32w, 32w + 32) of P.V over all k-tiles ----
+    // ---- 2. per block (qt_attn_mf.h): wave w scores its k-tile (block rows 32w .. +31),
+    // barrier, then takes dims [32w, 32w + 32) of P.V over the k-tiles holding keys ----
     const float scale2 = a.scale * QT_LOG2E;
     QtAttRun run;
     qt_att_run_init(run);
@@ -179,13 +179,14 @@ __global__ __launch_bounds__(QT_WG) void k_attn(QtAttnArgs a) {
             __builtin_amdgcn_s_waitcnt(0);
             const int nrow = pos - j0 - kb;   // the appended key's row, if in this block
             if (PREP && wave == 0 && nrow >= 0 && nrow < nk) qt_att_put_kv(s_kv[0], s_kv[1], nrow, knew, vnew, lane);
-            qt_att_zero_vrows(s_kv[1], nk, QT_KVB, tid, QT_WG);
+            qt_att_zero_vrows(s_kv[1], nk, (nk + 31) & ~31, tid, QT_WG);
             __syncthreads();
         }
-        qt_att_tiles<HPK, QT_WAVES>(&qp[0][0], s_kv[0], &pp[0][0], QT_KVB, &ml[0][0][0], wave, nk, scale2, lane);
+        if (32 * wave < nk)
+            qt_att_tiles<HPK>(&qp[0][0], s_kv[0], &pp[0][0], QT_KVB, &ml[0][0][0], wave, nk, scale2, lane);
         __syncthreads();
         float o[2], M, l;
-        qt_att_pv<HPK, QT_WAVES>(&pp[0][0], QT_KVB, &ml[0][0][0], s_kv[1], 32 * wave, lane, o, M, l);
+        qt_att_pv_n<HPK>((nk + 31) >> 5, &pp[0][0], QT_KVB, &ml[0][0][0], s_kv[1], 32 * wave, lane, o, M, l);
         qt_att_run_add(run, o, M, l);
     }
     // lane: head pg, dims 32*wave + sub and + 16

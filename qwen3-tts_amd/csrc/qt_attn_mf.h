@@ -75,7 +75,8 @@ __device__ __forceinline__ void qt_att_zero_rows(uint16_t *pc, int cols, int tid
     }
 }
 
-// Zero the value rows [nk, rows) of a staged V block (any slot order).
+// Zero the value rows [nk, rows) of a staged V block (any slot order); rows =
+// 32 * ceil(nk / 32), the rows the P.V k-tiles read.
 __device__ __forceinline__ void qt_att_zero_vrows(uint16_t *vblk, int nk, int rows, int tid, int nt) {
     for (int i = nk * 16 + tid; i < rows * 16; i += nt) *reinterpret_cast<uint4 *>(vblk + 8 * i) = make_uint4(0u, 0u, 0u, 0u);
 }
@@ -120,80 +121,95 @@ __device__ __forceinline__ void qt_att_qk2(const uint16_t *qp, const uint16_t *k
     }
 }
 
-// ---- a staged block of NWV*32 keys in two steps, one workgroup barrier between ----
-// Step 1 (qt_att_tiles), wave w: scores (base 2) of its 16-key tiles w and w + NWV
-// (block rows 16w .. +15 and 16(w+NWV) .. +15 = k-tile w), their max m_w per head,
-// p = 2^(s - m_w) as pieces into columns 32w .. 32w+31 of pp, l_w = sum p; (m_w, l_w)
-// into ml.
-// Step 2 (qt_att_pv), wave w: dims d0 .. d0+31 of every head over all NWV k-tiles, one
-// MFMA per (k-tile, 16 dims), then o = sum_t 2^(m_t - M) o_t with M = max_t m_t, and
-// l = sum_t 2^(m_t - M) l_t.  Lane l works on head l/16 throughout.
-template <int HPK, int NWV>
+// ---- a staged block of up to 128 keys in two steps, one workgroup barrier between ----
+// k-tile t = block rows 32t .. 32t+31; only the nkt = ceil(nk/32) k-tiles holding keys
+// take part, and value rows [nk, 32*nkt) are zeroed before step 2.
+// Step 1 (qt_att_tiles), wave w < nkt: scores (base 2) of k-tile w as two 16-key score
+// tiles, their max m_w per head, p = 2^(s - m_w) as pieces into columns 32w .. 32w+31 of
+// pp, l_w = sum p; (m_w, l_w) into ml.
+// Step 2 (qt_att_pv), every wave: dims d0 .. d0+31 of every head over the NKT k-tiles,
+// one MFMA per (k-tile, 16 dims), then o = sum_t 2^(m_t - M) o_t with M = max_t m_t,
+// and l = sum_t 2^(m_t - M) l_t.  Lane l works on head l/16 throughout.
+template <int HPK>
 __device__ __forceinline__ void qt_att_tiles(const uint16_t *qp, const uint16_t *kblk, uint16_t *pp, int pstride,
                                              float *ml, int w, int nk, float scale2, int lane) {
-    const int r0[2] = {16 * w, 16 * (w + NWV)};
+    const int r0[2] = {32 * w, 32 * w + 16};
     float sv[2];
     qt_att_qk2(qp, kblk, r0, lane, sv);                    // rows past nk: discarded
     const int h = lane >> 4, key = lane & 15;
     const float sa = r0[0] + key < nk ? sv[0] * scale2 : -INFINITY;
     const float sb = r0[1] + key < nk ? sv[1] * scale2 : -INFINITY;
-    const float m = group_max<16>(fmaxf(sa, sb));         // -inf: no keys in this k-tile
-    const float mr = m == -INFINITY ? 0.f : m;
-    const float pa = qt_exp2(sa - mr), pb = qt_exp2(sb - mr);   // 2^-inf == 0
+    const float m = group_max<16>(fmaxf(sa, sb));         // finite: row 32w < nk
+    const float pa = qt_exp2(sa - m), pb = qt_exp2(sb - m);     // 2^-inf == 0
     const float ls = group_sum<16>(pa + pb);
     if (h < HPK) {
-        qt_put_pieces(pp + 4 * h * pstride + 32 * w + key, pstride, pa);
-        qt_put_pieces(pp + 4 * h * pstride + 32 * w + 16 + key, pstride, pb);
+        qt_put_pieces(pp + 4 * h * pstride + r0[0] + key, pstride, pa);
+        qt_put_pieces(pp + 4 * h * pstride + r0[1] + key, pstride, pb);
         if (key == 0) { ml[(w * HPK + h) * 2] = m; ml[(w * HPK + h) * 2 + 1] = ls; }
     }
 }
 
-template <int HPK, int NWV>
+template <int HPK, int NKT>
 __device__ __forceinline__ void qt_att_pv(const uint16_t *pp, int pstride, const float *ml, const uint16_t *vblk,
                                           int d0, int lane, float (&o)[2], float &M, float &l) {
-    static_assert(NWV == 4, "four k-tiles");
+    static_assert(NKT >= 1 && NKT <= 4, "one to four k-tiles");
     const int kg = lane >> 4, j = lane & 15, h = lane >> 4;
     const int hc = h < HPK ? h : HPK - 1;
-    qt_u32x4 pa[NWV], vv[NWV][2];
-    float mw[NWV], lw[NWV];
-    // transposed value reads: lane (kg, j) points at k-tile rows 8kg + 4r2 + j/4 (tile
-    // a: block rows 16t + k, tile b: rows 16(t + NWV) + k - 16), dims col .. col+3; the
-    // 16t part leaves the swizzle (row bits 0, 1, 3) unchanged
+    qt_u32x4 pa[4], vv[4][2];
+    float mw[NKT], lw[NKT];
+    // transposed value reads: lane (kg, j) points at k-tile rows 8kg + 4r2 + j/4, dims
+    // col .. col+3; the k-tile offset 32t leaves the swizzle (row bits 0, 1, 3) unchanged
     int vb[2][2];
 #pragma unroll
     for (int dt = 0; dt < 2; dt++)
 #pragma unroll
-        for (int r2 = 0; r2 < 2; r2++) {
-            const int kk = 8 * kg + 4 * r2 + (j >> 2);
-            const int row = kk < 16 ? kk : kk + 16 * NWV - 16;
-            vb[dt][r2] = qt_vidx(row, d0 + 16 * dt + 4 * (j & 3));
-        }
+        for (int r2 = 0; r2 < 2; r2++) vb[dt][r2] = qt_vidx(8 * kg + 4 * r2 + (j >> 2), d0 + 16 * dt + 4 * (j & 3));
 #pragma unroll
-    for (int t = 0; t < NWV; t++) {
+    for (int t = 0; t < NKT; t++) {
         pa[t] = qt_lds16(pp + (lane & 15) * pstride + 32 * t + 8 * kg);
         mw[t] = ml[(t * HPK + hc) * 2];
         lw[t] = ml[(t * HPK + hc) * 2 + 1];
 #pragma unroll
         for (int dt = 0; dt < 2; dt++)
-            vv[t][dt] = qt_lds_tr8x2(vblk + vb[dt][0] + 16 * t * 128, vblk + vb[dt][1] + 16 * t * 128);
+            vv[t][dt] = qt_lds_tr8x2(vblk + vb[dt][0] + 32 * t * 128, vblk + vb[dt][1] + 32 * t * 128);
     }
-    asm volatile("" : "+v"(pa[0]), "+v"(pa[1]), "+v"(pa[2]), "+v"(pa[3]), "+v"(vv[0][0]), "+v"(vv[0][1]),
-                 "+v"(vv[1][0]), "+v"(vv[1][1]), "+v"(vv[2][0]), "+v"(vv[2][1]), "+v"(vv[3][0]), "+v"(vv[3][1]));
-    qt_f32x4 acc[NWV][2];
+    // one empty asm over every operand: all reads issued before it, one wait
+    if constexpr (NKT == 1)
+        asm volatile("" : "+v"(pa[0]), "+v"(vv[0][0]), "+v"(vv[0][1]));
+    else if constexpr (NKT == 2)
+        asm volatile("" : "+v"(pa[0]), "+v"(vv[0][0]), "+v"(vv[0][1]), "+v"(pa[1]), "+v"(vv[1][0]), "+v"(vv[1][1]));
+    else if constexpr (NKT == 3)
+        asm volatile("" : "+v"(pa[0]), "+v"(vv[0][0]), "+v"(vv[0][1]), "+v"(pa[1]), "+v"(vv[1][0]), "+v"(vv[1][1]),
+                     "+v"(pa[2]), "+v"(vv[2][0]), "+v"(vv[2][1]));
+    else
+        asm volatile("" : "+v"(pa[0]), "+v"(vv[0][0]), "+v"(vv[0][1]), "+v"(pa[1]), "+v"(vv[1][0]), "+v"(vv[1][1]),
+                     "+v"(pa[2]), "+v"(vv[2][0]), "+v"(vv[2][1]), "+v"(pa[3]), "+v"(vv[3][0]), "+v"(vv[3][1]));
+    qt_f32x4 acc[NKT][2];
 #pragma unroll
-    for (int t = 0; t < NWV; t++)
+    for (int t = 0; t < NKT; t++)
 #pragma unroll
         for (int dt = 0; dt < 2; dt++) acc[t][dt] = qt_mfma_bf16(pa[t], vv[t][dt], qt_f32x4{0.f, 0.f, 0.f, 0.f});
-    M = fmaxf(fmaxf(mw[0], mw[1]), fmaxf(mw[2], mw[3]));   // finite: k-tile 0 holds key 0
+    M = mw[0];                                              // finite: k-tile 0 holds key 0
+#pragma unroll
+    for (int t = 1; t < NKT; t++) M = fmaxf(M, mw[t]);
     o[0] = o[1] = 0.f;
     l = 0.f;
 #pragma unroll
-    for (int t = 0; t < NWV; t++) {
-        const float f = qt_exp2(mw[t] - M);                 // 0 for a k-tile without keys
+    for (int t = 0; t < NKT; t++) {
+        const float f = qt_exp2(mw[t] - M);
         l = fmaf(lw[t], f, l);
 #pragma unroll
         for (int dt = 0; dt < 2; dt++) o[dt] = fmaf((acc[t][dt][0] + acc[t][dt][1]) + acc[t][dt][2], f, o[dt]);
     }
+}
+// step 2 for the block's k-tile count (uniform)
+template <int HPK>
+__device__ __forceinline__ void qt_att_pv_n(int nkt, const uint16_t *pp, int pstride, const float *ml,
+                                            const uint16_t *vblk, int d0, int lane, float (&o)[2], float &M, float &l) {
+    if (nkt <= 1) qt_att_pv<HPK, 1>(pp, pstride, ml, vblk, d0, lane, o, M, l);
+    else if (nkt == 2) qt_att_pv<HPK, 2>(pp, pstride, ml, vblk, d0, lane, o, M, l);
+    else if (nkt == 3) qt_att_pv<HPK, 3>(pp, pstride, ml, vblk, d0, lane, o, M, l);
+    else qt_att_pv<HPK, 4>(pp, pstride, ml, vblk, d0, lane, o, M, l);
 }
 
 // Running (max, sum, output) across the blocks of a chunk longer than one block.

@@ -874,11 +874,11 @@ __global__ __launch_bounds__(NW * 64, 1) void k_pstep(Args a) {
                         }
                     }
                 }
-                qt_att_zero_vrows(s_kv[1], min(KVB, n), KVB, tid, NT);
+                qt_att_zero_vrows(s_kv[1], min(KVB, n), (min(KVB, n) + 31) & ~31, tid, NT);
                 __syncthreads();
                 // per LDS block (qt_attn_mf.h, the same arithmetic as k_attn): wave w scores
-                // its k-tile (16-key tiles w, w + NWB), barrier, then takes dims [32w, 32w + 32)
-                // of P.V over all k-tiles
+                // its k-tile (block rows 32w .. +31), barrier, then takes dims [32w, 32w + 32)
+                // of P.V over the k-tiles holding keys
                 const float scale2 = a.scale * QT_LOG2E;
                 QtAttRun run;
                 qt_att_run_init(run);
@@ -890,17 +890,18 @@ __global__ __launch_bounds__(NW * 64, 1) void k_pstep(Args a) {
                         __builtin_amdgcn_s_waitcnt(0);     // the barrier does not wait for LDS copies
                         const int nrow = pos - j0 - kb;    // the appended key's row, if in this block
                         if (wave == 0 && nrow >= 0 && nrow < nk) qt_att_put_kv(s_kv[0], s_kv[1], nrow, att.knew, att.vnew, lane);
-                        qt_att_zero_vrows(s_kv[1], nk, KVB, tid, NT);
+                        qt_att_zero_vrows(s_kv[1], nk, (nk + 31) & ~31, tid, NT);
                         __syncthreads();
                     }
-                    if (wave < NWB)
-                        qt_att_tiles<HPK, NWB>(&att.qp[0][0], s_kv[0], &att.pp[0][0], KVB, &att.ml[0][0][0], wave, nk,
-                                               scale2, lane);
+                    if (wave < NWB && 32 * wave < nk)
+                        qt_att_tiles<HPK>(&att.qp[0][0], s_kv[0], &att.pp[0][0], KVB, &att.ml[0][0][0], wave, nk, scale2,
+                                          lane);
                     __syncthreads();
                     PS_MARK(ph, 2);
                     if (wave < NWB) {
                         float o[2], M, lsum;
-                        qt_att_pv<HPK, NWB>(&att.pp[0][0], KVB, &att.ml[0][0][0], s_kv[1], 32 * wave, lane, o, M, lsum);
+                        qt_att_pv_n<HPK>((nk + 31) >> 5, &att.pp[0][0], KVB, &att.ml[0][0][0], s_kv[1], 32 * wave, lane,
+                                         o, M, lsum);
                         qt_att_run_add(run, o, M, lsum);
                     }
                 }
