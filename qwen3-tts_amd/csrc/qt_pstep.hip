@@ -438,14 +438,24 @@ __device__ __forceinline__ float stage_pc(const float *x, const float *wst, uint
 #pragma unroll
     for (int w = 1; w < NT / 64; w++) m = fmaxf(m, wst[2 * w + 1]);
     const QtPcScale ps = qt_pc_scale(m);
-    for (int u = threadIdx.x; u < NU; u += NT) {
-        float v[8];
+    // unrolled over the thread's units: every LDS read is issued before the first convert
+    constexpr int NK = (NU + NT - 1) / NT;
+    float v[NK][8];
 #pragma unroll
-        for (int h = 0; h < 2; h++) {
-            const float4 xv = xchunk4<EPC, COLS>(x, u >> 1, 2 * (u & 1) + h);
-            v[4 * h] = xv.x; v[4 * h + 1] = xv.y; v[4 * h + 2] = xv.z; v[4 * h + 3] = xv.w;
+    for (int k = 0; k < NK; k++) {
+        const int u = threadIdx.x + k * NT;
+        if (NU % NT == 0 || u < NU) {
+#pragma unroll
+            for (int h = 0; h < 2; h++) {
+                const float4 xv = xchunk4<EPC, COLS>(x, u >> 1, 2 * (u & 1) + h);
+                v[k][4 * h] = xv.x; v[k][4 * h + 1] = xv.y; v[k][4 * h + 2] = xv.z; v[k][4 * h + 3] = xv.w;
+            }
         }
-        pc_put8<SW, COLS>(pc, u, v, ps.isc);
+    }
+#pragma unroll
+    for (int k = 0; k < NK; k++) {
+        const int u = threadIdx.x + k * NT;
+        if (NU % NT == 0 || u < NU) pc_put8<SW, COLS>(pc, u, v[k], ps.isc);
     }
     __syncthreads();
     return ps.s;
