@@ -78,6 +78,8 @@ class Oracle:
         L.qo_talker_step.argtypes = [C.POINTER(OTalker), vp, i, vp, vp, vp]
         L.qo_talker_step.restype = i
         L.qo_cp_pass.argtypes = [C.POINTER(OTalker), vp, i]; L.qo_cp_pass.restype = i
+        L.qo_talker_prefill.argtypes = [C.POINTER(OTalker), vp, i, vp]; L.qo_talker_prefill.restype = i
+        L.qo_attention_f32.argtypes = [vp, vp, vp, vp, i, i, i, i, i, f, i]
         L.qo_cp_frame.argtypes = [C.POINTER(OCpFrame), vp, i, vp]; L.qo_cp_frame.restype = i
 
     # -- scalar / array helpers
@@ -134,6 +136,22 @@ class Oracle:
             raise RuntimeError("qo_talker_step failed")
         return h, dx
 
+    def talker_prefill(self, t, embeds):
+        """Oracle prefill of embeds f32[seq][H] on OTalker t (bf16 weights): fills the
+        cache rows [0, seq) of t's KV arrays; returns dec_x f32[H]."""
+        e = np.ascontiguousarray(embeds, np.float32)
+        dx = np.empty(t.hidden, np.float32)
+        rc = self.lib.qo_talker_prefill(C.byref(t), _p(e), e.shape[0], _p(dx))
+        if rc != 0:
+            raise RuntimeError("qo_talker_prefill failed")
+        return dx
+
+    def attention_f32(self, Q, K, V, seq_q, seq_k, nh, nkv, hd, scale, q_off):
+        out = np.empty(seq_q * nh * hd, np.float32)
+        self.lib.qo_attention_f32(_p(out), _p(np.ascontiguousarray(Q, np.float32)), _p(np.ascontiguousarray(K, np.float32)),
+                                  _p(np.ascontiguousarray(V, np.float32)), seq_q, seq_k, nh, nkv, hd, scale, q_off)
+        return out
+
     def cp_frame(self, f, talker_hidden, code0):
         """16 CP passes + 15 argmax codes on OCpFrame f."""
         out = np.empty(15, np.int32)
@@ -175,6 +193,7 @@ class RefModel:
         L.ref_set_kv_len.argtypes = [vp, i]
         L.ref_set_threads.argtypes = [i]
         L.ref_talker_step.argtypes = [vp, vp, vp]; L.ref_talker_step.restype = i
+        L.ref_talker_prefill.argtypes = [vp, vp, i]; L.ref_talker_prefill.restype = i
         L.ref_talker_step_layers.argtypes = [vp, vp, vp, vp]; L.ref_talker_step_layers.restype = i
         L.ref_get_dec_x.argtypes = [vp, vp]
         L.ref_layer_ptr.argtypes = [vp, i, i, i, i]; L.ref_layer_ptr.restype = vp
@@ -221,6 +240,13 @@ class RefModel:
         rc = self.lib.ref_talker_step(self.h, _p(np.ascontiguousarray(embed, np.float32)), _p(out))
         assert rc == 0
         return out
+
+    def prefill(self, embeds):
+        """The reference prefill of embeds f32[seq][H]; kv_len becomes seq."""
+        e = np.ascontiguousarray(embeds, np.float32)
+        rc = self.lib.ref_talker_prefill(self.h, _p(e), e.shape[0])
+        assert rc == 0
+        return self.dec_x()
 
     def step_layers(self, embed):
         s = self.shape

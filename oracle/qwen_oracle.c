@@ -281,6 +281,46 @@ void qo_attention_bf16kv(float *out, const float *Q, const uint16_t *K, const ui
     }
 }
 
+/* The same online softmax over f32 K/V rows (qwen_causal_attention, k.c:3454-3560), used
+ * by the Talker prefill on the f32 q/k/v it has just computed (t.c:901-907). */
+void qo_attention_f32(float *out, const float *Q, const float *K, const float *V,
+                      int seq_q, int seq_k, int n_heads, int n_kv, int head_dim,
+                      float scale, int q_offset) {
+    int hpk = n_heads / n_kv, qh = n_heads * head_dim, kvh_dim = n_kv * head_dim;
+    for (int h = 0; h < n_heads; h++) {
+        int g = h / hpk;
+        for (int i = 0; i < seq_q; i++) {
+            const float *q = Q + (size_t)i * qh + (size_t)h * head_dim;
+            float *o = out + (size_t)i * qh + (size_t)h * head_dim;
+            int k_end = q_offset + i + 1;
+            if (k_end > seq_k) k_end = seq_k;
+            float mx = -1e30f, sum = 0.0f;
+            for (int d = 0; d < head_dim; d++) o[d] = 0.0f;
+            for (int j = 0; j < k_end; j++) {
+                const float *kr = K + (size_t)j * kvh_dim + (size_t)g * head_dim;
+                const float *vr = V + (size_t)j * kvh_dim + (size_t)g * head_dim;
+                float s = 0.0f;
+                for (int d = 0; d < head_dim; d++) s += q[d] * kr[d];
+                s *= scale;
+                if (s > mx) {
+                    float c = expf(mx - s);
+                    sum = sum * c + 1.0f;
+                    for (int d = 0; d < head_dim; d++) o[d] = o[d] * c + vr[d];
+                    mx = s;
+                } else {
+                    float w = expf(s - mx);
+                    sum += w;
+                    for (int d = 0; d < head_dim; d++) o[d] += vr[d] * w;
+                }
+            }
+            if (sum > 0.0f) {
+                float inv = 1.0f / sum;
+                for (int d = 0; d < head_dim; d++) o[d] *= inv;
+            }
+        }
+    }
+}
+
 /* Greedy argmax, lowest index on ties (strict >, qwen_tts_sampling.c:175-182). */
 int qo_argmax(const float *v, int n) {
     int best = 0; float bv = v[0];
@@ -373,6 +413,61 @@ int qo_talker_step(const qo_talker_t *t, const float *embed, int pos,
     if (dec_x_out) memcpy(dec_x_out, x, (size_t)H * 4);
     scratch_free(&s); free(x);
     return 0;
+}
+
+/* Talker prefill of seq positions (qwen_talker_prefill, t.c:730-1038), bf16 weights
+ * (the reference's prefill reads the bf16 layer weights whatever the decode precision,
+ * t.c:832-839, 845-847).  X[s] = embeds[s]; per layer, for every position s:
+ * xn = rmsnorm(X[s], input_norm); q|k|v = W . xn (f32 sums); per-head q/k norm; NeoX RoPE
+ * at position s (t.c:887-895); cache rows s = bf16 truncation of k, v (t.c:897-899);
+ * causal attention over the f32 q/k/v of positions <= s (t.c:901-907); X[s] += W_o . attn;
+ * xn = rmsnorm(X[s], post_norm); X[s] += W_down . SwiGLU(W_gu . xn) (t.c:909-1010).
+ * dec_x_out = X[seq-1] (t.c:1032-1033). */
+int qo_talker_prefill(const qo_talker_t *t, const float *embeds, int seq, float *dec_x_out) {
+    if (t->prec != QO_BF16 || seq < 1 || seq > t->kv_max || seq > t->rope_len) return -1;
+    int H = t->hidden, F = t->inter, nh = t->n_heads, nkv = t->n_kv_heads, hd = t->head_dim;
+    int qd = nh * hd, kvd = nkv * hd;
+    float *X = malloc((size_t)seq * H * 4), *xn = malloc((size_t)H * 4);
+    float *Q = malloc((size_t)seq * qd * 4), *K = malloc((size_t)seq * kvd * 4), *V = malloc((size_t)seq * kvd * 4);
+    float *A = malloc((size_t)seq * qd * 4), *proj = malloc((size_t)H * 4), *gu = malloc((size_t)2 * F * 4);
+    int rc = -1;
+    if (!X || !xn || !Q || !K || !V || !A || !proj || !gu) goto done;
+    memcpy(X, embeds, (size_t)seq * H * 4);
+    for (int l = 0; l < t->n_layers; l++) {
+        const qo_layer_t *ly = &t->layers[l];
+        for (int s = 0; s < seq; s++) {
+            float *q = Q + (size_t)s * qd, *k = K + (size_t)s * kvd, *v = V + (size_t)s * kvd;
+            qo_rms_norm(xn, X + (size_t)s * H, ly->input_norm, H, t->eps);
+            qo_matvec(QO_BF16, q, ly->q.w, NULL, xn, qd, H);
+            qo_matvec(QO_BF16, k, ly->k.w, NULL, xn, kvd, H);
+            qo_matvec(QO_BF16, v, ly->v.w, NULL, xn, kvd, H);
+            qo_rms_norm_per_head(q, ly->q_norm, nh, hd, t->eps);
+            qo_rms_norm_per_head(k, ly->k_norm, nkv, hd, t->eps);
+            qo_rope_neox(q, nh, hd, t->rope_cos, t->rope_sin, s);
+            qo_rope_neox(k, nkv, hd, t->rope_cos, t->rope_sin, s);
+            size_t row = ((size_t)l * t->kv_max + s) * kvd;
+            for (int i = 0; i < kvd; i++) {
+                t->kv_k[row + i] = qo_f32_to_bf16_trunc(k[i]);
+                t->kv_v[row + i] = qo_f32_to_bf16_trunc(v[i]);
+            }
+        }
+        qo_attention_f32(A, Q, K, V, seq, seq, nh, nkv, hd, 1.0f / sqrtf((float)hd), 0);
+        for (int s = 0; s < seq; s++) {
+            float *x = X + (size_t)s * H;
+            qo_matvec(QO_BF16, proj, ly->o.w, NULL, A + (size_t)s * qd, H, qd);
+            for (int i = 0; i < H; i++) x[i] += proj[i];
+            qo_rms_norm(xn, x, ly->post_attn_norm, H, t->eps);
+            qo_matvec(QO_BF16, gu, ly->gate_up.w, NULL, xn, 2 * F, H);
+            qo_swiglu(gu, F);
+            qo_matvec(QO_BF16, proj, ly->down.w, NULL, gu, H, F);
+            for (int i = 0; i < H; i++) x[i] += proj[i];
+        }
+    }
+    if (dec_x_out) memcpy(dec_x_out, X + (size_t)(seq - 1) * H, (size_t)H * 4);
+    rc = 0;
+done:
+    free(X); free(xn); free(Q); free(K); free(V); free(A); free(proj); free(gu);
+    return rc;
 }
 
 int qo_cp_pass(const qo_talker_t *cp, float *x, int pos) {

@@ -45,6 +45,9 @@ void qo_swiglu(float *gate_up, int n);
 void qo_attention_bf16kv(float *out, const float *Q, const uint16_t *K, const uint16_t *V,
                          int seq_q, int seq_k, int n_heads, int n_kv, int head_dim,
                          float scale, int q_offset);
+void qo_attention_f32(float *out, const float *Q, const float *K, const float *V,
+                      int seq_q, int seq_k, int n_heads, int n_kv, int head_dim,
+                      float scale, int q_offset);
 int  qo_argmax(const float *v, int n);
 int  qo_codec_greedy(const uint16_t *head, const float *hidden, int vocab, int hidden_dim,
                      int frame, float *logits_out);
@@ -71,6 +74,10 @@ typedef struct {
 int qo_talker_step(const qo_talker_t *t, const float *embed, int pos,
                    float *hidden_out, float *dec_x_out, float *residuals);
 
+/* Talker prefill of seq positions with bf16 weights (qwen_talker_prefill,
+ * qwen_tts_talker.c:730-1038): fills cache rows [0, seq) of every layer, dec_x_out
+ * (nullable) = the last position's residual. */
+int qo_talker_prefill(const qo_talker_t *t, const float *embeds, int seq, float *dec_x_out);
 /* One CP transformer pass over x (in/out residual) at pos (qwen_tts_code_predictor.c:737-761). */
 int qo_cp_pass(const qo_talker_t *cp, float *x, int pos);
 

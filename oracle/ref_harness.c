@@ -29,6 +29,7 @@ extern int qwen_talker_load(qwen_tts_ctx_t *ctx);
 extern int qwen_cp_load(qwen_tts_ctx_t *ctx);
 extern int qwen_talker_step(qwen_tts_ctx_t *ctx, float *embed, float *hidden_out);
 extern int qwen_cp_predict(qwen_tts_ctx_t *ctx, float *talker_hidden, int code0, int *out_codes);
+extern int qwen_talker_prefill(qwen_tts_ctx_t *ctx, float *input_embeds, int seq_len);
 
 typedef struct {
     qwen_tts_ctx_t *ctx;
@@ -116,6 +117,14 @@ int ref_talker_step_layers(void *hp, const float *embed, float *residuals /*[L][
     }
     ctx->kv_len = pos;
     return qwen_talker_step(ctx, (float *)embed, hidden_out);
+}
+
+/* The reference prefill (t.c:730-1038) over seq positions; embeds f32[seq][hidden] (the
+ * reference copies it into its residual buffer and does not write through it).  Sets
+ * kv_len = seq and dec_x = the last position's residual. */
+int ref_talker_prefill(void *hp, const float *embeds, int seq) {
+    ref_handle_t *h = (ref_handle_t *)hp;
+    return qwen_talker_prefill(h->ctx, (float *)embeds, seq);
 }
 
 void ref_get_dec_x(void *hp, float *out) {

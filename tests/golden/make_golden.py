@@ -1,6 +1,7 @@
 """Write the golden fixtures under tests/golden/ from the compiled reference.
 
     python tests/golden/make_golden.py        # needs oracle/_ref/libqwen_ref.so (make -C oracle ref)
+    python tests/golden/make_golden.py --only-prefill   # just golden_tiny_prefill.npz
 
 The reference commits no vectors for the decode path (its tests need real weights), so
 these fixtures are the reference's own outputs on seeded synthetic inputs, produced by
@@ -15,6 +16,10 @@ the reference C sources compiled by oracle/Makefile (ref_harness.c drives them):
   golden_tiny_<p>.npz the "tiny" synthetic model (seed 0x5EED0001): 8 Talker decode steps
                       (qwen_talker_step, t.c:537-699) and 3 Code-Predictor frames
                       (qwen_cp_predict, cp.c:926-1045) per precision p in bf16/int8/int4
+  golden_tiny_prefill.npz  the same model's Talker prefill (qwen_talker_prefill,
+                      t.c:730-1038) of 24 positions: the inputs, every layer's K/V rows and
+                      dec_x, with the reference loaded as bf16 and as int8 (its prefill reads
+                      the bf16 weights either way)
 
 Only data is written (inputs, expected outputs, a hash of the synthetic weights); the
 tests regenerate the weights from the seed with qwen3_tts_amd.synth and run the oracle.
@@ -169,8 +174,41 @@ def tiny_fixture(prec, d, shape, tens):
                 weights_sha256=np.array(tensor_hash(tens)))
 
 
+PREFILL_SEQ = 24
+
+
+def prefill_fixture(d, shape):
+    rng = np.random.default_rng(0x5EED0003)
+    out = {}
+    for prec in ("bf16", "int8"):
+        ref = RefModel(d, shape, prec=prec, threads=1)
+        if prec == "bf16":
+            emb = ref.codec_emb()
+            toks = rng.integers(0, 2048, PREFILL_SEQ // 2)
+            e = np.concatenate([synth.bf16_to_f32(emb[toks]),
+                                rng.normal(0, 0.5, (PREFILL_SEQ - toks.size, shape.hidden))]).astype(np.float32)
+            out["embeds"] = e
+        dx = ref.prefill(out["embeds"])
+        assert ref.kv_len == PREFILL_SEQ
+        kk, vv = ref.kv()
+        out[f"dec_x_{prec}"] = dx
+        out[f"kv_k_{prec}"] = np.array(kk[:, :PREFILL_SEQ])
+        out[f"kv_v_{prec}"] = np.array(vv[:, :PREFILL_SEQ])
+    cos, sin = ref.rope()
+    out["rope_cos"] = np.array(cos[:64]); out["rope_sin"] = np.array(sin[:64])
+    return out
+
+
 def main():
     L = RefModel.load_lib()
+    if "--only-prefill" in sys.argv:
+        shape = synth.SHAPES["tiny"]
+        tens = synth.generate(shape, SEED_W, 0.1, threads=8)
+        with tempfile.TemporaryDirectory() as td:
+            d = os.path.join(td, "tiny")
+            synth.write_model_dir(d, shape, SEED_W, 0.1, tensors=tens)
+            np.savez_compressed(os.path.join(HERE, "golden_tiny_prefill.npz"), **prefill_fixture(d, shape))
+        return
     np.savez_compressed(os.path.join(HERE, "golden_convert.npz"), **convert_fixture(L))
     np.savez_compressed(os.path.join(HERE, "golden_quant.npz"), **quant_fixture(L))
     np.savez_compressed(os.path.join(HERE, "golden_ops.npz"), **ops_fixture(L))
@@ -181,6 +219,7 @@ def main():
         synth.write_model_dir(d, shape, SEED_W, 0.1, tensors=tens)
         for prec in ("bf16", "int8", "int4"):
             np.savez_compressed(os.path.join(HERE, f"golden_tiny_{prec}.npz"), **tiny_fixture(prec, d, shape, tens))
+        np.savez_compressed(os.path.join(HERE, "golden_tiny_prefill.npz"), **prefill_fixture(d, shape))
     for f in sorted(os.listdir(HERE)):
         if f.endswith(".npz"):
             print(f, os.path.getsize(os.path.join(HERE, f)))

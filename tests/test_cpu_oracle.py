@@ -424,3 +424,80 @@ def test_gate_up_interleave_matches_reference_loader():
         p = f"talker.model.layers.{l}."
         gu = synth.interleave_gate_up(t[p + "mlp.gate_proj.weight"], t[p + "mlp.up_proj.weight"])
         assert np.array_equal(ref.layer_mat(l, "gate_up")["bf16"], gu)
+
+
+# ---------------------------------------------------------------------------------------
+# Talker prefill (qwen_talker_prefill, t.c:730-1038)
+# ---------------------------------------------------------------------------------------
+
+def _kv_close(a, b):
+    """bf16 K/V rows: truncation can flip one unit where the f32 values differ in the
+    last bits (different summation order); nothing else may differ."""
+    d = np.abs(bf16_to_f64(a) - bf16_to_f64(b))
+    return (a != b).mean() < 0.02 and d.max() < 0.05
+
+
+def test_prefill_golden(oracle):
+    from oracle.oracle import talker_from_tensors
+    from qwen3_tts_amd import synth
+    g = gold("golden_tiny_prefill.npz")
+    s = synth.SHAPES["tiny"]
+    ot, keep = talker_from_tensors(oracle, _tiny_tensors(), s, "bf16", 64, g["rope_cos"], g["rope_sin"])
+    dx = oracle.talker_prefill(ot, g["embeds"])
+    n = g["embeds"].shape[0]
+    assert rel_l2(dx, g["dec_x_bf16"]) <= 1e-4 and np.abs(dx - g["dec_x_bf16"]).max() <= 2e-3
+    assert _kv_close(keep["kv_k"][:, :n], g["kv_k_bf16"]) and _kv_close(keep["kv_v"][:, :n], g["kv_v_bf16"])
+    # the reference's prefill reads the bf16 weights whatever the decode precision
+    assert np.array_equal(g["dec_x_bf16"], g["dec_x_int8"]) and np.array_equal(g["kv_k_bf16"], g["kv_k_int8"])
+
+
+def test_prefill_layer0_kv_equals_decode_steps(oracle):
+    """Position s of a prefill and decode step s see the same layer-0 input and do the
+    same arithmetic up to the KV append, so layer 0's K/V rows agree bit for bit; deeper
+    layers differ only through the attention (f32 K/V in the prefill, bf16 cache in the
+    decode), which the dec_x tolerance bounds."""
+    from oracle.oracle import talker_from_tensors
+    from qwen3_tts_amd import synth
+    g = gold("golden_tiny_prefill.npz")
+    s = synth.SHAPES["tiny"]
+    t = _tiny_tensors()
+    e = g["embeds"][:12]
+    op, kp = talker_from_tensors(oracle, t, s, "bf16", 64, g["rope_cos"], g["rope_sin"])
+    od, kd = talker_from_tensors(oracle, t, s, "bf16", 64, g["rope_cos"], g["rope_sin"])
+    dx_p = oracle.talker_prefill(op, e)
+    for i in range(e.shape[0]):
+        _, dx_d = oracle.talker_step(od, e[i], i)
+    assert np.array_equal(kp["kv_k"][0, :12], kd["kv_k"][0, :12]) and np.array_equal(kp["kv_v"][0, :12], kd["kv_v"][0, :12])
+    assert rel_l2(dx_p, dx_d) <= 2e-2
+
+
+def test_attention_f32_matches_bf16_twin_on_bf16_values(oracle):
+    """On K/V that are exactly bf16, the f32-K/V attention equals the bf16-cache one."""
+    from qwen3_tts_amd import synth
+    rng = np.random.default_rng(3)
+    nh, nkv, hd, sq = 4, 2, 128, 9
+    q = rng.standard_normal(sq * nh * hd).astype(np.float32)
+    kb = synth.f32_to_bf16_rne(rng.standard_normal((sq, nkv * hd)).astype(np.float32))
+    vb = synth.f32_to_bf16_rne(rng.standard_normal((sq, nkv * hd)).astype(np.float32))
+    a = oracle.attention(q, kb, vb, sq, sq, nh, nkv, hd, 0.0883883, 0)
+    b = oracle.attention_f32(q, bf16_to_f64(kb).astype(np.float32), bf16_to_f64(vb).astype(np.float32),
+                             sq, sq, nh, nkv, hd, 0.0883883, 0)
+    assert np.array_equal(a, b)
+
+
+@need_ref
+def test_prefill_vs_reference_live(oracle):
+    """The oracle prefill against the compiled reference's, at another length and on
+    other inputs than the fixture."""
+    from conftest import model_dir
+    from oracle.oracle import RefModel, oracle_talker
+    d, shape, t = model_dir("tiny")
+    ref = RefModel(d, shape, prec="bf16", threads=4)
+    rng = np.random.default_rng(11)
+    e = rng.normal(0, 0.7, (37, shape.hidden)).astype(np.float32)
+    dx_r = ref.prefill(e)
+    kr, vr = ref.kv()
+    ot, keep = oracle_talker(ref, 0, 64)
+    dx_o = oracle.talker_prefill(ot, e)
+    assert rel_l2(dx_o, dx_r) <= 1e-4
+    assert _kv_close(keep["kv_k"][:, :37], np.array(kr[:, :37])) and _kv_close(keep["kv_v"][:, :37], np.array(vr[:, :37]))
