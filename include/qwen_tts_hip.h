@@ -78,6 +78,22 @@ int   qwen_hip_talker_upload_kv(void *state, const uint16_t *kv_k, const uint16_
 /* replaces qwen_cuda_talker_free                 (qwen_tts_cuda_talker.cu:933) */
 void  qwen_hip_talker_free(void *state);
 
+/* Talker prefill on the device: the twin of qwen_talker_prefill(ctx, input_embeds,
+ * seq_len) (qwen_tts_talker.c:730-1038), which the reference runs on the CPU before
+ * qwen_cuda_talker_upload_kv (qwen_tts.c:1454-1476); no GPU counterpart in the reference.
+ * input_embeds host f32[seq][hidden].  Writes KV rows [0, seq) of every layer of the
+ * state's device cache and dec_x (qwen_hip_talker_get_dec_x) = the last position's
+ * residual; the next step runs at pos = seq.  Projections use bf16 weights as the
+ * reference's prefill does (t.c:832-839): the state's own when it holds bf16, else
+ * bf16_layers (the descriptor's bf16 layer weights, copied to the device on the first
+ * call and kept; NULL is allowed after that or for a bf16 state).  Needs hidden, inter
+ * and the q|k|v row count divisible by 64.  Returns 0 on success; argument errors
+ * leave the state usable. */
+int   qwen_hip_talker_prefill(void *state, const qwen_hip_layer_t *bf16_layers, const float *input_embeds, int seq);
+/* Benchmark entry (no reference counterpart): enqueue n more prefills of the last
+ * prefill's inputs (seq <= the last call's seq) on the state's stream, no host sync. */
+int   qwen_hip_talker_prefill_async(void *state, int seq, int n);
+
 /* Reads back the device KV of positions [0, n) in the host layout (checks/tests). */
 int   qwen_hip_talker_download_kv(void *state, uint16_t *kv_k, uint16_t *kv_v, int host_kv_max, int n);
 
@@ -212,6 +228,11 @@ int qwen_hip_op_causal_attention_bf16kv(float *out, const float *Q, const uint16
 int qwen_hip_op_rms_norm(float *out, const float *x, const float *w, int seq, int dim, float eps);
 int qwen_hip_op_rms_norm_per_head(float *x, const float *w, int seq, int n_heads, int head_dim, float eps);
 int qwen_hip_op_swiglu(float *out, const float *gate_up, int n);
+/* The prefill projection alone (no reference counterpart as one call: the sgemm /
+ * qwen_matmat_bf16 of t.c:845-847, 913, 964, 990): Y[S][N] = X[S][K] . W[N][K]^T
+ * (epi 0), Y += that (epi 1), or SwiGLU of the interleaved gate|up rows into Y[S][N/2]
+ * (epi 2); W bf16, f32 host arrays, N and K multiples of 64. */
+int qwen_hip_op_prefill_gemm(float *Y, const uint16_t *W, const float *X, int S, int N, int K, int epi);
 int qwen_hip_op_argmax_matvec(int prec, const float *x, const void *W, const float *scale, int in_dim, int out_dim);
 /* qwen_matmat_int8 (qwen_tts_kernels.h:121-122): Y[rows][B] = (W*scale) @ X[cols][B]
  * (row-major f32, B <= 64, cols a multiple of 64) on the batched MFMA kernel. */

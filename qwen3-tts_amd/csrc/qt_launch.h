@@ -63,6 +63,19 @@ hipError_t qt_launch_pstep(int prec, int hidden, const void *layers_dev, int n_l
                            int *d_pos, unsigned *epoch, int *err, int n_steps, int with_head, const uint16_t *head_w,
                            const uint16_t *emb, int vocab, int *d_frame, int *hist, int hist_len, hipStream_t st);
 
+/* Talker prefill (qt_prefill.hip) */
+enum { QT_PF_STORE = 0, QT_PF_RESID = 1, QT_PF_SWIGLU = 2 };
+int qt_pf_spad(int S);
+hipError_t qt_launch_pf_pieces(const float *X, int ldx, int S, int K, const float *gain, float eps, uint16_t *P,
+                               hipStream_t st);
+hipError_t qt_launch_pf_gemm(int epi, const uint16_t *W, const uint16_t *P, int S, int N, int K, float *Y, int ldy,
+                             hipStream_t st);
+hipError_t qt_launch_pf_qkv_post(float *QKV, int ld, int S, int nh, int nkv, const float *qn, const float *kn,
+                                 const float *rc, const float *rs, float eps, uint16_t *kc, uint16_t *vc,
+                                 long long kv_max, hipStream_t st);
+hipError_t qt_launch_pf_attn(const float *QKV, int ld, int S, int nh, int nkv, float scale, float *A, int lda,
+                             hipStream_t st);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,0 +1,312 @@
+// qt_prefill.hip — Talker prefill (qwen_talker_prefill, qwen_tts_talker.c:730-1038) on gfx950.
+//
+// The reference runs the prompt's positions as dense projections Y[seq][out] =
+// Xn[seq][in] . W^T over the bf16 layer weights with f32 sums (sgemm or
+// qwen_matmat_bf16, t.c:845-847, 913, 964, 990), per-head q/k RMSNorm, NeoX RoPE at each
+// position, the bf16-truncated K/V store (t.c:897-899), causal attention over the f32
+// q/k/v (t.c:901-907), O + residual, RMSNorm + gate|up + SwiGLU, down + residual.
+//
+// Projections here run on the bf16 matrix cores.  The f32 activations are split
+// into three bf16 planes whose sum is each value exactly (x truncated to bf16, the
+// truncated rest, the remaining <= 8 significant bits; qt_attn_mf.h); W . x = sum over
+// the planes of W . x_p, and each bf16 x bf16 product is exact in f32, so the three
+// MFMAs per k-step accumulate, in f32, the exact products of the f32 activations with
+// the bf16 weights.  Both operands are read row-major exactly as stored: the MFMA A
+// operand is 16 weight rows x 8 consecutive k, the B operand 16 positions x 8
+// consecutive k of one plane, so neither needs a transpose.
+#include "qt_attn_mf.h"
+
+#define QT_PF_WG 256
+
+// ---- activation planes ---------------------------------------------------------------
+// Row s < S of X (ldx floats apart), optionally RMS-normalised with gain (the reference's
+// qwen_rms_norm: out = (x * inv) * w, inv = 1/sqrt(mean(x^2) + eps), k.c:292-382), as
+// three bf16 planes P[p][s][K] (plane stride Sp*K); rows S <= s < Sp are zero.
+__global__ __launch_bounds__(QT_PF_WG) void k_pf_pieces(const float *X, int ldx, int S, int Sp, int K,
+                                                         const float *gain, float eps, uint16_t *P) {
+    __shared__ float red[QT_WAVES];
+    const int s = blockIdx.x, tid = threadIdx.x;
+    const size_t plane = (size_t)Sp * K;
+    uint16_t *p0 = P + (size_t)s * K;
+    if (s >= S) {
+        for (int k = tid * 8; k < K; k += QT_PF_WG * 8)
+#pragma unroll
+            for (int p = 0; p < 3; p++) *reinterpret_cast<uint4 *>(p0 + p * plane + k) = make_uint4(0u, 0u, 0u, 0u);
+        return;
+    }
+    const float *x = X + (size_t)s * ldx;
+    float inv = 1.0f;
+    if (gain) {
+        float ss = 0.f;
+        for (int k = tid; k < K; k += QT_PF_WG) ss = fmaf(x[k], x[k], ss);
+        ss = block_sum(ss, red);
+        inv = 1.0f / sqrtf(ss / (float)K + eps);
+    }
+    for (int k = tid * 4; k < K; k += QT_PF_WG * 4) {
+        float4 v = *reinterpret_cast<const float4 *>(x + k);
+        if (gain) {
+            const float4 g = *reinterpret_cast<const float4 *>(gain + k);
+            v.x = (v.x * inv) * g.x; v.y = (v.y * inv) * g.y; v.z = (v.z * inv) * g.z; v.w = (v.w * inv) * g.w;
+        }
+        uint16_t pc[3][4];
+        const float e[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+        for (int i = 0; i < 4; i++) qt_put_pieces(&pc[0][i], 4, e[i]);
+#pragma unroll
+        for (int p = 0; p < 3; p++)
+            *reinterpret_cast<uint2 *>(p0 + p * plane + k) =
+                make_uint2((uint32_t)pc[p][0] | ((uint32_t)pc[p][1] << 16), (uint32_t)pc[p][2] | ((uint32_t)pc[p][3] << 16));
+    }
+}
+
+// ---- projection GEMM ------------------------------------------------------------------
+// Y = X . W^T: W bf16 [N][K] row-major, X as the planes P[3][Sp][K].  Workgroup tile:
+// 64*NR weight rows x 16*NSB positions; wave w takes rows [16*NR*w, 16*NR*(w+1)) of it
+// and every position.  Per 64-k chunk the planes' tile is staged in LDS (rows padded to
+// 144 B so the 16 lanes of a B-operand read hit 16 different bank groups) while the
+// next chunk's planes and weight fragments are already in flight; the weight fragments
+// go straight from HBM to registers (each wave reads its own rows once).
+//   PF_STORE   Y[s][n] = acc
+//   PF_RESID   Y[s][n] += acc                     (O, down: the residual stream)
+//   PF_SWIGLU  rows 2i, 2i+1 are gate_i, up_i (the reference's interleaved gate|up,
+//              t.c:378-388): Y[s][i] = g / (1 + e^-g) * u  (qwen_swiglu_inplace, k.c:3857)
+// (the same values as in qt_launch.h, which the .hip sources do not include)
+enum { QT_PF_STORE = 0, QT_PF_RESID = 1, QT_PF_SWIGLU = 2 };
+
+template <int EPI, int NR, int NSB>
+__global__ __launch_bounds__(QT_PF_WG) void k_pf_gemm(const uint16_t *__restrict__ W, const uint16_t *__restrict__ P,
+                                                       int S, int Sp, int K, float *Y, int ldy) {
+    constexpr int KC = 64, ST = 16 * NSB, ROWB = KC * 2 + 16;
+    constexpr int NSTG = 3 * ST * (KC / 8) / QT_PF_WG;   // 16-byte pieces of a chunk per thread
+    static_assert(NSTG * QT_PF_WG == 3 * ST * (KC / 8), "staging split");
+    __shared__ __align__(16) uint8_t sp[3 * ST * ROWB];
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, j = lane & 15, kg = lane >> 4;
+    const int n0 = blockIdx.x * (64 * NR) + wave * 16 * NR;
+    const int s0 = blockIdx.y * ST;
+    const size_t plane = (size_t)Sp * K;
+
+    // this thread's share of a chunk's planes: 16-byte piece i is row (p*ST + t) = idx/8,
+    // k-part idx%8 of the chunk, idx = tid + 256 i
+    const uint16_t *gsrc[NSTG];
+    int soff[NSTG];
+#pragma unroll
+    for (int i = 0; i < NSTG; i++) {
+        const int idx = tid + QT_PF_WG * i, row = idx >> 3, c = idx & 7;
+        gsrc[i] = P + (row / ST) * plane + (size_t)(s0 + row % ST) * K + 8 * c;
+        soff[i] = row * ROWB + c * 16;
+    }
+    const uint16_t *wrow[NR];
+#pragma unroll
+    for (int r = 0; r < NR; r++) wrow[r] = W + (size_t)(n0 + 16 * r + j) * K + 8 * kg;
+
+    qt_u32x4 stg[NSTG];
+    qt_u32x4 a[2][NR], an[2][NR];
+    qt_f32x4 acc[NR][NSB];
+#pragma unroll
+    for (int r = 0; r < NR; r++)
+#pragma unroll
+        for (int t = 0; t < NSB; t++) acc[r][t] = qt_f32x4{0.f, 0.f, 0.f, 0.f};
+
+#pragma unroll
+    for (int i = 0; i < NSTG; i++) stg[i] = *reinterpret_cast<const qt_u32x4 *>(gsrc[i]);
+#pragma unroll
+    for (int ks = 0; ks < 2; ks++)
+#pragma unroll
+        for (int r = 0; r < NR; r++) a[ks][r] = *reinterpret_cast<const qt_u32x4 *>(wrow[r] + 32 * ks);
+#pragma unroll
+    for (int i = 0; i < NSTG; i++) *reinterpret_cast<qt_u32x4 *>(sp + soff[i]) = stg[i];
+    __syncthreads();
+    for (int kc = 0; kc < K; kc += KC) {
+        const int kn = kc + KC < K ? kc + KC : kc;   // the last chunk reloads itself (unused)
+#pragma unroll
+        for (int i = 0; i < NSTG; i++) stg[i] = *reinterpret_cast<const qt_u32x4 *>(gsrc[i] + kn);
+#pragma unroll
+        for (int ks = 0; ks < 2; ks++)
+#pragma unroll
+            for (int r = 0; r < NR; r++) an[ks][r] = *reinterpret_cast<const qt_u32x4 *>(wrow[r] + kn + 32 * ks);
+#pragma unroll
+        for (int ks = 0; ks < 2; ks++) {
+            qt_u32x4 b[NSB][3];
+#pragma unroll
+            for (int t = 0; t < NSB; t++)
+#pragma unroll
+                for (int p = 0; p < 3; p++) b[t][p] = qt_lds16(sp + (p * ST + 16 * t + j) * ROWB + (32 * ks + 8 * kg) * 2);
+#pragma unroll
+            for (int r = 0; r < NR; r++)
+#pragma unroll
+                for (int t = 0; t < NSB; t++)
+#pragma unroll
+                    for (int p = 0; p < 3; p++) acc[r][t] = qt_mfma_bf16(a[ks][r], b[t][p], acc[r][t]);
+        }
+        __syncthreads();
+#pragma unroll
+        for (int i = 0; i < NSTG; i++) *reinterpret_cast<qt_u32x4 *>(sp + soff[i]) = stg[i];
+#pragma unroll
+        for (int ks = 0; ks < 2; ks++)
+#pragma unroll
+            for (int r = 0; r < NR; r++) a[ks][r] = an[ks][r];
+        __syncthreads();
+    }
+    // lane holds rows n0 + 16r + 4kg + i (i = 0..3) of position s0 + 16t + j
+#pragma unroll
+    for (int r = 0; r < NR; r++)
+#pragma unroll
+        for (int t = 0; t < NSB; t++) {
+            const int s = s0 + 16 * t + j, n = n0 + 16 * r + 4 * kg;
+            if (s >= S) continue;
+            const qt_f32x4 v = acc[r][t];
+            if constexpr (EPI == QT_PF_SWIGLU) {
+                const float g0 = v[0], u0 = v[1], g1 = v[2], u1 = v[3];
+                *reinterpret_cast<float2 *>(Y + (size_t)s * ldy + (n >> 1)) =
+                    make_float2(g0 / (1.0f + expf(-g0)) * u0, g1 / (1.0f + expf(-g1)) * u1);
+            } else {
+                float4 *y = reinterpret_cast<float4 *>(Y + (size_t)s * ldy + n);
+                if constexpr (EPI == QT_PF_RESID) {
+                    const float4 o = *y;
+                    *y = make_float4(o.x + v[0], o.y + v[1], o.z + v[2], o.w + v[3]);
+                } else {
+                    *y = make_float4(v[0], v[1], v[2], v[3]);
+                }
+            }
+        }
+}
+
+// ---- per-head q/k norm, RoPE, KV store ---------------------------------------------
+// Position s = blockIdx.x of QKV [S][ld] (q | k | v rows as the projection wrote them):
+// q and k heads RMS-normalised with their [128] gains (qwen_rms_norm_per_head,
+// k.c:486-577) and rotated at position s (apply_rope_neox_inplace, t.c:203-251:
+// x1' = x1 c - x2 s, x2' = x2 c + x1 s), in place; the cache rows s of kv head g get the
+// bf16 truncation of k and v (t.c:897-899).  One wave per head row, lane d holding
+// elements d and d + 64 (the RoPE pair).
+__global__ __launch_bounds__(QT_PF_WG) void k_pf_qkv_post(float *QKV, int ld, int nh, int nkv, const float *qn,
+                                                           const float *kn, const float *rc, const float *rs, float eps,
+                                                           uint16_t *kc, uint16_t *vc, long long kv_max) {
+    const int s = blockIdx.x, lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    float *row = QKV + (size_t)s * ld;
+    const float c = rc[(size_t)s * 64 + lane], sn = rs[(size_t)s * 64 + lane];
+    for (int hr = wave; hr < nh + 2 * nkv; hr += QT_WAVES) {
+        float *x = row + hr * 128;
+        const float x0 = x[lane], x1 = x[lane + 64];
+        if (hr < nh + nkv) {
+            const bool isk = hr >= nh;
+            const float *w = isk ? kn : qn;
+            const float ss = group_sum<64>(x0 * x0 + x1 * x1);
+            const float inv = 1.0f / sqrtf(ss / 128.0f + eps);
+            const float n0 = (x0 * inv) * w[lane], n1 = (x1 * inv) * w[lane + 64];
+            const float r0 = fmaf(n0, c, -(n1 * sn)), r1 = fmaf(n1, c, n0 * sn);
+            x[lane] = r0;
+            x[lane + 64] = r1;
+            if (isk) {
+                uint16_t *kd = kc + ((size_t)(hr - nh) * kv_max + s) * 128;
+                kd[lane] = f2bf_trunc(r0);
+                kd[lane + 64] = f2bf_trunc(r1);
+            }
+        } else {
+            uint16_t *vd = vc + ((size_t)(hr - nh - nkv) * kv_max + s) * 128;
+            vd[lane] = f2bf_trunc(x0);
+            vd[lane + 64] = f2bf_trunc(x1);
+        }
+    }
+}
+
+// ---- causal attention over the f32 q/k/v --------------------------------------------
+// qwen_causal_attention (k.c:3454-3560) as the prefill calls it (t.c:904-907): query i
+// of head h (kv head h / (nh/nkv)) over positions j <= i, one wave per query, lane d
+// holding dims d and d + 64; per key the online softmax of the reference (s > max:
+// c = e^(max - s), sum = sum c + 1, o = o c + v; else w = e^(s - max), sum += w,
+// o += v w), then o / sum.  Four keys' dot products are formed before their updates.
+__global__ __launch_bounds__(QT_PF_WG) void k_pf_attn(const float *QKV, int ld, int S, int nh, int nkv, float scale,
+                                                       float *A, int lda) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int i = blockIdx.x * QT_WAVES + wave, h = blockIdx.y, g = h / (nh / nkv);
+    if (i >= S) return;
+    const int qd = nh * 128, kvd = nkv * 128;
+    const float *qr = QKV + (size_t)i * ld + h * 128;
+    const float q0 = qr[lane], q1 = qr[lane + 64];
+    const float *kb = QKV + qd + g * 128, *vb = QKV + qd + kvd + g * 128;
+    float mx = -1e30f, sum = 0.f, o0 = 0.f, o1 = 0.f;
+    auto upd = [&](float sc, float v0, float v1) {
+        if (sc > mx) {
+            const float c = expf(mx - sc);
+            sum = sum * c + 1.0f;
+            o0 = o0 * c + v0; o1 = o1 * c + v1;
+            mx = sc;
+        } else {
+            const float w = expf(sc - mx);
+            sum += w;
+            o0 += v0 * w; o1 += v1 * w;
+        }
+    };
+    int jj = 0;
+    for (; jj + 3 <= i; jj += 4) {
+        float sc[4], v0[4], v1[4];
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            const float *kr = kb + (size_t)(jj + u) * ld, *vr = vb + (size_t)(jj + u) * ld;
+            sc[u] = q0 * kr[lane] + q1 * kr[lane + 64];
+            v0[u] = vr[lane]; v1[u] = vr[lane + 64];
+        }
+#pragma unroll
+        for (int u = 0; u < 4; u++) sc[u] = group_sum<64>(sc[u]) * scale;
+#pragma unroll
+        for (int u = 0; u < 4; u++) upd(sc[u], v0[u], v1[u]);
+    }
+    for (; jj <= i; jj++) {
+        const float *kr = kb + (size_t)jj * ld, *vr = vb + (size_t)jj * ld;
+        const float sc = group_sum<64>(q0 * kr[lane] + q1 * kr[lane + 64]) * scale;
+        upd(sc, vr[lane], vr[lane + 64]);
+    }
+    const float inv = 1.0f / sum;
+    A[(size_t)i * lda + h * 128 + lane] = o0 * inv;
+    A[(size_t)i * lda + h * 128 + lane + 64] = o1 * inv;
+}
+
+// ---- launchers -------------------------------------------------------------------------
+// Positions are padded to a multiple of QT_PF_SPAD for the planes (the GEMM's position
+// tile); weight rows must be a multiple of 64 and K a multiple of 64.
+#define QT_PF_SPAD 64
+
+extern "C" int qt_pf_spad(int S) { return (S + QT_PF_SPAD - 1) / QT_PF_SPAD * QT_PF_SPAD; }
+
+extern "C" hipError_t qt_launch_pf_pieces(const float *X, int ldx, int S, int K, const float *gain, float eps,
+                                          uint16_t *P, hipStream_t st) {
+    if (S <= 0 || K <= 0 || K % 8 || ldx % 4) return hipErrorInvalidValue;
+    const int Sp = qt_pf_spad(S);
+    hipLaunchKernelGGL(k_pf_pieces, dim3(Sp), dim3(QT_PF_WG), 0, st, X, ldx, S, Sp, K, gain, eps, P);
+    return hipGetLastError();
+}
+
+extern "C" hipError_t qt_launch_pf_gemm(int epi, const uint16_t *W, const uint16_t *P, int S, int N, int K, float *Y,
+                                        int ldy, hipStream_t st) {
+    if (S <= 0 || N <= 0 || K <= 0 || N % 64 || K % 64 || epi < 0 || epi > 2) return hipErrorInvalidValue;
+    if (epi != QT_PF_SWIGLU ? (ldy < N || ldy % 4) : (ldy < N / 2 || ldy % 2)) return hipErrorInvalidValue;
+    const int Sp = qt_pf_spad(S);
+    // 128-row tiles where they still give a few workgroups per CU's worth of work
+    const bool big = N % 128 == 0 && (long long)(N / 128) * (Sp / 64) >= 256;
+    const dim3 grid(big ? N / 128 : N / 64, Sp / 64);
+#define QT_PF_GEMM(E)                                                                                   \
+    if (big) hipLaunchKernelGGL((k_pf_gemm<E, 2, 4>), grid, dim3(QT_PF_WG), 0, st, W, P, S, Sp, K, Y, ldy); \
+    else hipLaunchKernelGGL((k_pf_gemm<E, 1, 4>), grid, dim3(QT_PF_WG), 0, st, W, P, S, Sp, K, Y, ldy);
+    if (epi == QT_PF_STORE) { QT_PF_GEMM(QT_PF_STORE) }
+    else if (epi == QT_PF_RESID) { QT_PF_GEMM(QT_PF_RESID) }
+    else { QT_PF_GEMM(QT_PF_SWIGLU) }
+#undef QT_PF_GEMM
+    return hipGetLastError();
+}
+
+extern "C" hipError_t qt_launch_pf_qkv_post(float *QKV, int ld, int S, int nh, int nkv, const float *qn,
+                                            const float *kn, const float *rc, const float *rs, float eps, uint16_t *kc,
+                                            uint16_t *vc, long long kv_max, hipStream_t st) {
+    if (S <= 0 || nh <= 0 || nkv <= 0 || nh % nkv || S > kv_max) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_pf_qkv_post, dim3(S), dim3(QT_PF_WG), 0, st, QKV, ld, nh, nkv, qn, kn, rc, rs, eps, kc, vc,
+                       kv_max);
+    return hipGetLastError();
+}
+
+extern "C" hipError_t qt_launch_pf_attn(const float *QKV, int ld, int S, int nh, int nkv, float scale, float *A,
+                                        int lda, hipStream_t st) {
+    if (S <= 0 || nh <= 0 || nkv <= 0 || nh % nkv) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_pf_attn, dim3((S + QT_WAVES - 1) / QT_WAVES, nh), dim3(QT_PF_WG), 0, st, QKV, ld, S, nh, nkv,
+                       scale, A, lda);
+    return hipGetLastError();
+}

@@ -263,6 +263,12 @@ typedef struct {
     unsigned *ps_epoch;     /* tag of the next step */
     int *ps_err;
     int *h_err;             /* pinned */
+    /* Talker prefill (qt_prefill.hip): bf16 projection weights (the step's own when they
+     * are bf16, else owned copies made on the first prefill) and position buffers */
+    dmat_t *pf_qkv, *pf_o, *pf_gu, *pf_dn;
+    int pf_cap;             /* positions the buffers below hold */
+    float *pf_x, *pf_qkvb, *pf_attn, *pf_h;
+    uint16_t *pf_p;         /* activation planes [3][spad][max(H, qd, F)] */
 } talker_t;
 
 static int persistent_enabled(void) {
@@ -275,9 +281,16 @@ static void talker_destroy(talker_t *t) {
     if (!t) return;
     if (t->graph_ready) (void)hipGraphExecDestroy(t->exec);
     if (t->ggraph_ready) (void)hipGraphExecDestroy(t->gexec);
+    if (t->pf_qkv) {
+        for (int l = 0; l < t->s.L; l++) {
+            dmat_free(&t->pf_qkv[l]); dmat_free(&t->pf_o[l]); dmat_free(&t->pf_gu[l]); dmat_free(&t->pf_dn[l]);
+        }
+        free(t->pf_qkv); free(t->pf_o); free(t->pf_gu); free(t->pf_dn);
+    }
     stack_free(&t->s);
     void *bufs[] = {t->io, t->d_pos, t->d_frame, t->d_tok, t->d_hist, t->codec_head, t->codec_emb, t->logits,
-                    t->ps_layers, t->ps_ring, t->ps_xin, t->ps_epoch, t->ps_err};
+                    t->ps_layers, t->ps_ring, t->ps_xin, t->ps_epoch, t->ps_err,
+                    t->pf_x, t->pf_qkvb, t->pf_attn, t->pf_h, t->pf_p};
     for (size_t i = 0; i < sizeof bufs / sizeof bufs[0]; i++) if (bufs[i]) (void)hipFree(bufs[i]);
     if (t->h_in) (void)hipHostFree(t->h_in);
     if (t->h_out) (void)hipHostFree(t->h_out);
@@ -512,6 +525,136 @@ int qwen_hip_talker_download_kv(void *state, uint16_t *kv_k, uint16_t *kv_v, int
     HCK(hipStreamSynchronize(t->st));
     return 0;
 fail:
+    return -1;
+}
+
+/* -- Talker prefill (qwen_talker_prefill, qwen_tts_talker.c:730-1038) ------------------ */
+
+/* bf16 copies of the projection weights for the prefill (the reference's prefill reads
+ * the bf16 layer weights whatever the decode precision, t.c:832-839). */
+static int pf_weights(talker_t *t, const qwen_hip_layer_t *ly) {
+    stack_t *s = &t->s;
+    const int L = s->L, H = s->H, F = s->F, qd = s->qd, kvd = s->kvd;
+    void *tmp = NULL;
+    size_t tb = (size_t)2 * F * H * 2;
+    if ((size_t)(qd + 2 * kvd) * H * 2 > tb) tb = (size_t)(qd + 2 * kvd) * H * 2;
+    t->pf_qkv = calloc(L, sizeof(dmat_t)); t->pf_o = calloc(L, sizeof(dmat_t));
+    t->pf_gu = calloc(L, sizeof(dmat_t)); t->pf_dn = calloc(L, sizeof(dmat_t));
+    REQ(t->pf_qkv && t->pf_o && t->pf_gu && t->pf_dn, "host alloc failed");
+    HCK(hipMalloc(&tmp, tb));
+    for (int l = 0; l < L; l++) {
+        REQ(dmat_alloc(&t->pf_qkv[l], QWEN_HIP_BF16, qd + 2 * kvd, H) == 0, "alloc prefill qkv");
+        REQ(dmat_put(&t->pf_qkv[l], 0, &ly[l].q, QWEN_HIP_BF16, qd, t->st, tmp) == 0, "upload q %d", l);
+        REQ(dmat_put(&t->pf_qkv[l], qd, &ly[l].k, QWEN_HIP_BF16, kvd, t->st, tmp) == 0, "upload k %d", l);
+        REQ(dmat_put(&t->pf_qkv[l], qd + kvd, &ly[l].v, QWEN_HIP_BF16, kvd, t->st, tmp) == 0, "upload v %d", l);
+        REQ(dmat_alloc(&t->pf_o[l], QWEN_HIP_BF16, H, qd) == 0, "alloc prefill o");
+        REQ(dmat_put(&t->pf_o[l], 0, &ly[l].o, QWEN_HIP_BF16, H, t->st, tmp) == 0, "upload o %d", l);
+        REQ(dmat_alloc(&t->pf_gu[l], QWEN_HIP_BF16, 2 * F, H) == 0, "alloc prefill gate_up");
+        REQ(dmat_put(&t->pf_gu[l], 0, &ly[l].gate_up, QWEN_HIP_BF16, 2 * F, t->st, tmp) == 0, "upload gate_up %d", l);
+        REQ(dmat_alloc(&t->pf_dn[l], QWEN_HIP_BF16, H, F) == 0, "alloc prefill down");
+        REQ(dmat_put(&t->pf_dn[l], 0, &ly[l].down, QWEN_HIP_BF16, H, t->st, tmp) == 0, "upload down %d", l);
+    }
+    (void)hipFree(tmp);
+    return 0;
+fail:
+    if (tmp) (void)hipFree(tmp);
+    return -1;
+}
+
+static void pf_free_bufs(talker_t *t) {
+    void *b[] = {t->pf_x, t->pf_qkvb, t->pf_attn, t->pf_h, t->pf_p};
+    for (size_t i = 0; i < sizeof b / sizeof b[0]; i++) if (b[i]) (void)hipFree(b[i]);
+    t->pf_x = t->pf_qkvb = t->pf_attn = t->pf_h = NULL; t->pf_p = NULL; t->pf_cap = 0;
+}
+
+int qwen_hip_talker_prefill(void *state, const qwen_hip_layer_t *bf16_layers, const float *embeds, int seq) {
+    talker_t *t = (talker_t *)state;
+    if (!t || t->dead) { SETERR("talker state is dead or NULL"); return -1; }
+    stack_t *s = &t->s;
+    const int L = s->L, H = s->H, F = s->F, qd = s->qd, qkvr = s->qd + 2 * s->kvd;
+    /* argument errors leave the state usable */
+    if (!embeds) { SETERR("null embeds"); return -1; }
+    if (seq < 1 || seq > s->kv_max || seq > s->rope_len) {
+        SETERR("seq %d out of range (1..%d)", seq, s->kv_max < s->rope_len ? s->kv_max : s->rope_len);
+        return -1;
+    }
+    if (H % 64 || F % 64 || qkvr % 64 || qd % 64) { SETERR("prefill needs hidden, inter, q|k|v rows, q dim divisible by 64"); return -1; }
+    const dmat_t *wq = s->qkv, *wo = s->o, *wgu = s->gu, *wdn = s->dn;
+    if (s->prec != QWEN_HIP_BF16) {
+        if (!t->pf_qkv) {
+            if (!bf16_layers) { SETERR("prefill of a non-bf16 state needs the bf16 layer weights"); return -1; }
+            if (pf_weights(t, bf16_layers) != 0) goto fail;
+        }
+        wq = t->pf_qkv; wo = t->pf_o; wgu = t->pf_gu; wdn = t->pf_dn;
+    }
+    if (seq > t->pf_cap) {
+        pf_free_bufs(t);
+        const int sp = qt_pf_spad(seq);
+        int km = H > qd ? H : qd;
+        if (F > km) km = F;
+        HCK(hipMalloc((void **)&t->pf_x, (size_t)seq * H * sizeof(float)));
+        HCK(hipMalloc((void **)&t->pf_qkvb, (size_t)seq * qkvr * sizeof(float)));
+        HCK(hipMalloc((void **)&t->pf_attn, (size_t)seq * qd * sizeof(float)));
+        HCK(hipMalloc((void **)&t->pf_h, (size_t)seq * F * sizeof(float)));
+        HCK(hipMalloc((void **)&t->pf_p, (size_t)3 * sp * km * sizeof(uint16_t)));
+        t->pf_cap = seq;
+    }
+    HCK(hipMemcpyAsync(t->pf_x, embeds, (size_t)seq * H * sizeof(float), hipMemcpyDefault, t->st));
+    const float scale = 1.0f / sqrtf((float)s->hd);
+    for (int l = 0; l < L; l++) {
+        const size_t lay = (size_t)l * s->nkv * s->kv_max * s->hd;
+        HCK(qt_launch_pf_pieces(t->pf_x, H, seq, H, s->in_norm[l], s->eps, t->pf_p, t->st));
+        HCK(qt_launch_pf_gemm(QT_PF_STORE, (const uint16_t *)wq[l].w, t->pf_p, seq, qkvr, H, t->pf_qkvb, qkvr, t->st));
+        HCK(qt_launch_pf_qkv_post(t->pf_qkvb, qkvr, seq, s->nh, s->nkv, s->qn[l], s->kn[l], s->rope_cos, s->rope_sin,
+                                  s->eps, s->kc + lay, s->vc + lay, s->kv_max, t->st));
+        HCK(qt_launch_pf_attn(t->pf_qkvb, qkvr, seq, s->nh, s->nkv, scale, t->pf_attn, qd, t->st));
+        HCK(qt_launch_pf_pieces(t->pf_attn, qd, seq, qd, NULL, 0.f, t->pf_p, t->st));
+        HCK(qt_launch_pf_gemm(QT_PF_RESID, (const uint16_t *)wo[l].w, t->pf_p, seq, H, qd, t->pf_x, H, t->st));
+        HCK(qt_launch_pf_pieces(t->pf_x, H, seq, H, s->post_norm[l], s->eps, t->pf_p, t->st));
+        HCK(qt_launch_pf_gemm(QT_PF_SWIGLU, (const uint16_t *)wgu[l].w, t->pf_p, seq, 2 * F, H, t->pf_h, F, t->st));
+        HCK(qt_launch_pf_pieces(t->pf_h, F, seq, F, NULL, 0.f, t->pf_p, t->st));
+        HCK(qt_launch_pf_gemm(QT_PF_RESID, (const uint16_t *)wdn[l].w, t->pf_p, seq, H, F, t->pf_x, H, t->st));
+    }
+    /* dec_x = the last position's residual (t.c:1032-1033), where get_dec_x reads it */
+    HCK(hipMemcpyAsync(t->io + H, t->pf_x + (size_t)(seq - 1) * H, (size_t)H * sizeof(float), hipMemcpyDeviceToDevice, t->st));
+    HCK(hipMemcpyAsync(t->h_out + H, t->io + H, (size_t)H * sizeof(float), hipMemcpyDeviceToHost, t->st));
+    HCK(hipStreamSynchronize(t->st));
+    return 0;
+fail:
+    t->dead = 1;
+    return -1;
+}
+
+/* Benchmark entry: enqueue n prefills of the last prefill's inputs (already on the
+ * device) without host synchronisation. */
+int qwen_hip_talker_prefill_async(void *state, int seq, int n) {
+    talker_t *t = (talker_t *)state;
+    if (!t || t->dead) { SETERR("talker state is dead or NULL"); return -1; }
+    stack_t *s = &t->s;
+    const int L = s->L, H = s->H, F = s->F, qd = s->qd, qkvr = s->qd + 2 * s->kvd;
+    if (seq < 1 || seq > t->pf_cap || n < 0) { SETERR("call qwen_hip_talker_prefill with at least seq positions first"); return -1; }
+    const dmat_t *wq = s->prec == QWEN_HIP_BF16 ? s->qkv : t->pf_qkv, *wo = s->prec == QWEN_HIP_BF16 ? s->o : t->pf_o;
+    const dmat_t *wgu = s->prec == QWEN_HIP_BF16 ? s->gu : t->pf_gu, *wdn = s->prec == QWEN_HIP_BF16 ? s->dn : t->pf_dn;
+    if (!wq) { SETERR("no prefill weights"); return -1; }
+    const float scale = 1.0f / sqrtf((float)s->hd);
+    for (int it = 0; it < n; it++)
+        for (int l = 0; l < L; l++) {
+            const size_t lay = (size_t)l * s->nkv * s->kv_max * s->hd;
+            HCK(qt_launch_pf_pieces(t->pf_x, H, seq, H, s->in_norm[l], s->eps, t->pf_p, t->st));
+            HCK(qt_launch_pf_gemm(QT_PF_STORE, (const uint16_t *)wq[l].w, t->pf_p, seq, qkvr, H, t->pf_qkvb, qkvr, t->st));
+            HCK(qt_launch_pf_qkv_post(t->pf_qkvb, qkvr, seq, s->nh, s->nkv, s->qn[l], s->kn[l], s->rope_cos, s->rope_sin,
+                                      s->eps, s->kc + lay, s->vc + lay, s->kv_max, t->st));
+            HCK(qt_launch_pf_attn(t->pf_qkvb, qkvr, seq, s->nh, s->nkv, scale, t->pf_attn, qd, t->st));
+            HCK(qt_launch_pf_pieces(t->pf_attn, qd, seq, qd, NULL, 0.f, t->pf_p, t->st));
+            HCK(qt_launch_pf_gemm(QT_PF_RESID, (const uint16_t *)wo[l].w, t->pf_p, seq, H, qd, t->pf_x, H, t->st));
+            HCK(qt_launch_pf_pieces(t->pf_x, H, seq, H, s->post_norm[l], s->eps, t->pf_p, t->st));
+            HCK(qt_launch_pf_gemm(QT_PF_SWIGLU, (const uint16_t *)wgu[l].w, t->pf_p, seq, 2 * F, H, t->pf_h, F, t->st));
+            HCK(qt_launch_pf_pieces(t->pf_h, F, seq, F, NULL, 0.f, t->pf_p, t->st));
+            HCK(qt_launch_pf_gemm(QT_PF_RESID, (const uint16_t *)wdn[l].w, t->pf_p, seq, H, F, t->pf_x, H, t->st));
+        }
+    return 0;
+fail:
+    t->dead = 1;
     return -1;
 }
 
@@ -1484,6 +1627,36 @@ int qwen_hip_op_rms_norm_per_head(float *x, const float *w, int seq, int n_heads
 fail:
     if (dx) (void)hipFree(dx);
     if (dw) (void)hipFree(dw);
+    return -1;
+}
+
+/* The prefill projection on its own: Y[S][N] = X[S][K] . W[N][K]^T (epi 0), Y += (epi 1),
+ * or SwiGLU of the interleaved rows into Y[S][N/2] (epi 2); host pointers, W bf16. */
+int qwen_hip_op_prefill_gemm(float *Y, const uint16_t *W, const float *X, int S, int N, int K, int epi) {
+    hipStream_t st = op_stream();
+    uint16_t *dw = NULL, *dp = NULL;
+    float *dx = NULL, *dy = NULL;
+    REQ(st, "no stream");
+    REQ(S >= 1 && N >= 64 && K >= 64 && N % 64 == 0 && K % 64 == 0 && epi >= 0 && epi <= 2, "bad shape/epi");
+    const int ny = epi == QT_PF_SWIGLU ? N / 2 : N;
+    HCK(hipMalloc((void **)&dw, (size_t)N * K * 2));
+    HCK(hipMalloc((void **)&dx, (size_t)S * K * sizeof(float)));
+    HCK(hipMalloc((void **)&dy, (size_t)S * ny * sizeof(float)));
+    HCK(hipMalloc((void **)&dp, (size_t)3 * qt_pf_spad(S) * K * 2));
+    HCK(hipMemcpyAsync(dw, W, (size_t)N * K * 2, hipMemcpyHostToDevice, st));
+    HCK(hipMemcpyAsync(dx, X, (size_t)S * K * sizeof(float), hipMemcpyHostToDevice, st));
+    if (epi == QT_PF_RESID) HCK(hipMemcpyAsync(dy, Y, (size_t)S * ny * sizeof(float), hipMemcpyHostToDevice, st));
+    HCK(qt_launch_pf_pieces(dx, K, S, K, NULL, 0.f, dp, st));
+    HCK(qt_launch_pf_gemm(epi, dw, dp, S, N, K, dy, ny, st));
+    HCK(hipMemcpyAsync(Y, dy, (size_t)S * ny * sizeof(float), hipMemcpyDeviceToHost, st));
+    HCK(hipStreamSynchronize(st));
+    (void)hipFree(dw); (void)hipFree(dx); (void)hipFree(dy); (void)hipFree(dp);
+    return 0;
+fail:
+    if (dw) (void)hipFree(dw);
+    if (dx) (void)hipFree(dx);
+    if (dy) (void)hipFree(dy);
+    if (dp) (void)hipFree(dp);
     return -1;
 }
 

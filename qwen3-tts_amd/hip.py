@@ -33,6 +33,7 @@ EXPORTS = [
     "qwen_hip_talker_batch_step_async", "qwen_hip_talker_batch_sync", "qwen_hip_talker_batch_stream",
     "qwen_hip_cp_batch_init", "qwen_hip_cp_batch_step", "qwen_hip_cp_batch_free", "qwen_hip_op_matmat_int8",
     "qwen_hip_cp_set_prefill2", "qwen_hip_cp_prefill2",
+    "qwen_hip_talker_prefill", "qwen_hip_talker_prefill_async", "qwen_hip_op_prefill_gemm",
 ]
 
 
@@ -80,6 +81,9 @@ def lib():
         L.qwen_hip_talker_step_nograph.argtypes = [vp, vp, vp, i]; L.qwen_hip_talker_step_nograph.restype = i
         L.qwen_hip_talker_get_dec_x.argtypes = [vp, vp]
         L.qwen_hip_talker_upload_kv.argtypes = [vp, vp, vp, i, i]; L.qwen_hip_talker_upload_kv.restype = i
+        L.qwen_hip_talker_prefill.argtypes = [vp, vp, vp, i]; L.qwen_hip_talker_prefill.restype = i
+        L.qwen_hip_talker_prefill_async.argtypes = [vp, i, i]; L.qwen_hip_talker_prefill_async.restype = i
+        L.qwen_hip_op_prefill_gemm.argtypes = [vp, vp, vp, i, i, i, i]; L.qwen_hip_op_prefill_gemm.restype = i
         L.qwen_hip_talker_download_kv.argtypes = [vp, vp, vp, i, i]; L.qwen_hip_talker_download_kv.restype = i
         L.qwen_hip_talker_free.argtypes = [vp]
         L.qwen_hip_talker_greedy.argtypes = [vp, vp, vp, i, vp, i, i, i, vp, vp]
@@ -196,6 +200,18 @@ class Talker:
 
     def upload_kv(self, kv_k, kv_v, n):
         check(lib().qwen_hip_talker_upload_kv(self.h, _p(kv_k), _p(kv_v), kv_k.shape[1], n), "upload_kv")
+
+    def prefill(self, embeds, bf16_layers=None):
+        """Device prefill of embeds f32[seq][H] (qwen_talker_prefill); fills KV rows
+        [0, seq) and dec_x.  A state built from bf16 descriptors (also when quantized on
+        the device) passes its own descriptor layers as the bf16 weights."""
+        e = np.ascontiguousarray(embeds, np.float32)
+        if bf16_layers is None and self.desc.prec == BF16:
+            bf16_layers = self.desc.layers
+        lp = None if bf16_layers is None else C.cast(bf16_layers, C.c_void_p)
+        check(lib().qwen_hip_talker_prefill(self.h, lp, _p(e), e.shape[0]), "talker_prefill")
+        self._pf_keep = e
+        return self.dec_x()
 
     def download_kv(self, n):
         k = np.zeros((self.nl, self.kv_max, self.kvd), np.uint16)
