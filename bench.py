@@ -96,6 +96,12 @@ CP_WORKLOADS = {
     "cp-0.6B-int8-frame": ("0.6B", "int8", 500, False),
     "cp-0.6B-int8-frame-prefill2": ("0.6B", "int8", 500, True),
 }
+# Talker prefill of S positions (qwen_talker_prefill): (shape, decode precision, S, default timed prefills)
+PREFILL_WORKLOADS = {
+    "talker-1.7B-prefill-S128": ("1.7B", "int8", 128, 20),
+    "talker-1.7B-prefill-S512": ("1.7B", "int8", 512, 8),
+}
+BF16_MFMA_PEAK_TFS = 2500.0
 # batched workloads: (shape, precision, streams, KV length range, default timed steps)
 BATCH_WORKLOADS = {
     "talker-1.7B-int8-b32-ragged": ("1.7B", "int8", 32, (128, 4096), 16),
@@ -124,7 +130,8 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=None)
     ap.add_argument("--warmup", type=int, default=None)
-    ap.add_argument("--workload", default="talker-1.7B-int8-b1-L2048", choices=sorted(WORKLOADS) + sorted(BATCH_WORKLOADS) + sorted(CP_WORKLOADS))
+    ap.add_argument("--workload", default="talker-1.7B-int8-b1-L2048", choices=sorted(WORKLOADS) + sorted(BATCH_WORKLOADS) + sorted(CP_WORKLOADS)
+                    + sorted(PREFILL_WORKLOADS))
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--kernel-launches", type=int, default=200)
@@ -142,6 +149,8 @@ def main():
         return bench_batch(args)
     if args.workload in CP_WORKLOADS:
         return bench_cp(args)
+    if args.workload in PREFILL_WORKLOADS:
+        return bench_prefill(args)
     from qwen3_tts_amd import hip, synth
     shape_name, prec, Lpre, dsteps = WORKLOADS[args.workload]
     K = args.steps or dsteps
@@ -324,6 +333,113 @@ def bench_batch(args):
         "cpu_baseline": None,
     }
     print(json.dumps(out), flush=True)
+
+
+def prefill_flops(s, S):
+    """Algorithmic flops of one prefill of S positions: the four projections per position
+    and layer (2 flops per weight), plus causal attention (q.k and P.V over the keys at or
+    before each position: 2 x 128 MACs per key per head, each 2 flops)."""
+    macs = (s.q_dim + 2 * s.kv_dim) * s.hidden + s.hidden * s.q_dim + 2 * s.inter * s.hidden + s.hidden * s.inter
+    attn = 2 * s.heads * s.head_dim * S * (S + 1)       # MACs: S(S+1)/2 keys x 128 x (q.k + P.V) per head
+    return s.layers * (2.0 * S * macs + 2.0 * attn)
+
+
+def bench_prefill(args):
+    """Talker prefill (qwen_talker_prefill, qwen_tts_talker.c:730-1038) of S positions on
+    the device, for the decode state of the headline workload (1.7B, int8 per-row weights
+    quantized on the device): the prefill projections run on the bf16 weights, as the
+    reference's do, as bf16 MFMA GEMMs over exact three-plane f32 activations.  Inputs:
+    S codec-embedding rows (seeded).  value = ms per prefill (W warmup, K timed, back to
+    back on the state's stream, inputs resident).  roofline: algorithmic flops (the
+    projections + causal attention; the three activation planes triple the matrix-core
+    work, which is not counted) per second against the dense bf16 MFMA peak."""
+    from qwen3_tts_amd import hip, synth
+    shape_name, prec, S, dk = PREFILL_WORKLOADS[args.workload]
+    K = args.steps or dk
+    W = 3 if args.warmup is None else args.warmup
+    s = synth.SHAPES[shape_name]
+    t0 = time.time()
+    only = lambda n: n.startswith("talker.model.")  # noqa: E731
+    tens = synth.generate(s, 0x5EED0001, 0.0, threads=int(os.environ.get("OMP_NUM_THREADS", "16")), only=only)
+    layers = hip.layers_from_tensors(tens, s)
+    cos, sin = synth.rope_tables(s.head_dim, s.rope_theta, S + 16)
+    fnorm = synth.bf16_to_f32(tens["talker.model.norm.weight"])
+    g = hip.Talker(s, layers, fnorm, cos, sin, hip.BF16, S + 16, quantize_to=hip.PREC[prec])
+    emb = tens["talker.model.codec_embedding.weight"]
+    rng = np.random.default_rng(0x5EED0004)
+    E = synth.bf16_to_f32(emb[rng.integers(0, 2048, S)]).astype(np.float32)
+    dx = g.prefill(E)                                   # uploads the bf16 copies, sizes the buffers
+    log(f"[bench] prefill: S={S}, init {time.time() - t0:.1f}s, dec_x[0:3] {dx[:3]}")
+    L = hip.lib()
+    ev = HipEvents()
+    stream = L.qwen_hip_talker_stream(g.h)
+    hip.check(L.qwen_hip_talker_prefill_async(g.h, S, W), "prefill warmup")
+    hip.check(L.qwen_hip_talker_sync(g.h), "sync")
+    ev.device_sync()
+    a, b = ev.event(), ev.event()
+    ev.record(a, stream)
+    hip.check(L.qwen_hip_talker_prefill_async(g.h, S, K), "prefill timed")
+    ev.record(b, stream)
+    ms_total = ev.elapsed_ms(a, b)
+    ev.device_sync()
+    ms = ms_total / K
+    fl = prefill_flops(s, S)
+    tfs = fl / (ms * 1e-3) / 1e12
+    log(f"[bench] prefill: {ms:.3f} ms per prefill of {S} positions, {S / ms * 1e3:.0f} positions/s, "
+        f"{tfs:.1f} TFLOP/s algorithmic ({100 * tfs / BF16_MFMA_PEAK_TFS:.1f}% of bf16 MFMA peak)")
+    cpu = None
+    if not args.no_cpu_baseline:
+        try:
+            cpu = cpu_baseline_prefill(s, tens, E, args.cpu_seconds)
+        except Exception as ex:
+            log(f"[bench] cpu baseline failed: {ex}")
+            cpu = {"value": None, "unit": "ms/prefill", "error": str(ex)[:200]}
+    g.free()
+    out = {
+        "metric": "Talker prefill ms (prompt of S positions) + achieved TFLOP/s",
+        "value": round(ms, 4), "unit": "ms/prefill", "n_gpus": 1, "steps": K, "warmup": W,
+        "ms_per_step": round(ms, 4), "higher_is_better": False, "scaling": "weak", "vs_baseline": None,
+        "dtype": "bf16", "data": "synthetic (seeded N(0,0.02) random-init weights, codec-embedding inputs)",
+        "config": {"workload": args.workload, "positions": S, "layers": s.layers, "hidden": s.hidden, "inter": s.inter,
+                   "decode_precision": prec},
+        "positions_per_s": round(S * 1000.0 / ms, 1), "flops_per_prefill": fl,
+        "roofline": {"bound": "mfma", "achieved": round(tfs, 2), "peak": BF16_MFMA_PEAK_TFS, "unit": "TFLOP/s",
+                     "frac": round(tfs / BF16_MFMA_PEAK_TFS, 4), "traffic": None,
+                     "kernel": "prefill (k_pf_gemm projections dominate; pieces, q/k norm + RoPE + KV store, attention)",
+                     "flops_per_launch": fl, "avg_us": round(ms * 1e3, 1), "steps_per_launch": 1},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(out), flush=True)
+
+
+def cpu_baseline_prefill(s, tens, E, seconds):
+    """The reference's own qwen_talker_prefill (oracle/_ref, its matmat_bf16 path: no BLAS
+    in this image) on the host cores, same weights and inputs."""
+    sys.path.insert(0, ROOT)
+    from oracle.oracle import RefModel
+    from qwen3_tts_amd import synth
+    flags = open("/proc/cpuinfo").read()
+    variant = "_avx512" if all(f in flags for f in (" avx512f", " avx512bw", " avx512vl")) else ""
+    threads = int(os.environ.get("OMP_NUM_THREADS", "16"))
+    full = dict(tens)
+    full.update(synth.generate(s, 0x5EED0001, 0.0, threads=threads,
+                               only=lambda n: not n.startswith("talker.model.")))
+    with tempfile.TemporaryDirectory(prefix="qwen_ref_", dir=os.environ.get("TMPDIR", "/tmp")) as d:
+        synth.write_model_dir(d, s, tensors=full)
+        del full
+        ref = RefModel(d, s, prec="bf16", threads=threads, variant=variant)
+    t0 = time.perf_counter()
+    ref.prefill(E)
+    one = time.perf_counter() - t0
+    n = int(max(1, min(5, seconds / max(one, 1e-3))))
+    t0 = time.perf_counter()
+    for _ in range(n):
+        ref.prefill(E)
+    ms = (time.perf_counter() - t0) / n * 1e3
+    log(f"[bench] cpu baseline: {n} reference qwen_talker_prefill calls, S={E.shape[0]}: {ms:.1f} ms ({threads} threads)")
+    return {"value": round(ms, 2), "unit": "ms/prefill", "cores": threads, "kind": "reference",
+            "sample": f"{n} reference qwen_talker_prefill calls of {E.shape[0]} positions (matmat_bf16 path, "
+                      f"{variant.strip('_') or 'avx2'} build, -O3 -ffast-math), same weights and inputs"}
 
 
 def bench_cp(args):
