@@ -69,7 +69,7 @@ int qt_pf_spad(int S);
 hipError_t qt_launch_pf_pieces(const float *X, int ldx, int S, int K, const float *gain, float eps, uint16_t *P,
                                hipStream_t st);
 hipError_t qt_launch_pf_gemm(int epi, const uint16_t *W, const uint16_t *P, int S, int N, int K, float *Y, int ldy,
-                             hipStream_t st);
+                             float *part, hipStream_t st);
 hipError_t qt_launch_pf_qkv_post(float *QKV, int ld, int S, int nh, int nkv, const float *qn, const float *kn,
                                  const float *rc, const float *rs, float eps, uint16_t *kc, uint16_t *vc,
                                  long long kv_max, hipStream_t st);

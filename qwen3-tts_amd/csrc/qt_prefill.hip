@@ -61,11 +61,9 @@ __global__ __launch_bounds__(QT_PF_WG) void k_pf_pieces(const float *X, int ldx,
 
 // ---- projection GEMM ------------------------------------------------------------------
 // Y = X . W^T: W bf16 [N][K] row-major, X as the planes P[3][Sp][K].  Workgroup tile:
-// 64*NR weight rows x 16*NSB positions; wave w takes rows [16*NR*w, 16*NR*(w+1)) of it
-// and every position.  Per 64-k chunk the planes' tile is staged in LDS (rows padded to
-// 144 B so the 16 lanes of a B-operand read hit 16 different bank groups) while the
-// next chunk's planes and weight fragments are already in flight; the weight fragments
-// go straight from HBM to registers (each wave reads its own rows once).
+// 64*NR weight rows x 64 positions; wave w takes rows [16*NR*w, 16*NR*(w+1)) of it and
+// every position; the weight fragments go straight from HBM to registers (each wave reads
+// its own rows once), the planes' tile is shared through LDS.
 //   PF_STORE   Y[s][n] = acc
 //   PF_RESID   Y[s][n] += acc                     (O, down: the residual stream)
 //   PF_SWIGLU  rows 2i, 2i+1 are gate_i, up_i (the reference's interleaved gate|up,
@@ -73,85 +71,111 @@ __global__ __launch_bounds__(QT_PF_WG) void k_pf_pieces(const float *X, int ldx,
 // (the same values as in qt_launch.h, which the .hip sources do not include)
 enum { QT_PF_STORE = 0, QT_PF_RESID = 1, QT_PF_SWIGLU = 2 };
 
-template <int EPI, int NR, int NSB>
-__global__ __launch_bounds__(QT_PF_WG) void k_pf_gemm(const uint16_t *__restrict__ W, const uint16_t *__restrict__ P,
-                                                       int S, int Sp, int K, float *Y, int ldy) {
-    constexpr int KC = 64, ST = 16 * NSB, ROWB = KC * 2 + 16;
-    constexpr int NSTG = 3 * ST * (KC / 8) / QT_PF_WG;   // 16-byte pieces of a chunk per thread
-    static_assert(NSTG * QT_PF_WG == 3 * ST * (KC / 8), "staging split");
-    __shared__ __align__(16) uint8_t sp[3 * ST * ROWB];
+// NST chunks of 64 k are in flight: each chunk's planes (3 x 64
+// positions x 128 B) go straight from HBM into LDS stage c % NST by global_load_lds (no
+// registers; lane L of a 1-KiB copy fills slot L%8 of row 8b + L/8 and fetches the chunk
+// that belongs there: chunk c of row r sits at slot c ^ ((r >> 1) & 7), so the 16 lanes of
+// a B-operand read (rows j, one chunk) hit 16 different bank groups), and its weight
+// fragments into registers, NST - 1 chunks ahead.  One barrier per chunk: after the wait
+// for chunk c, every wave is also done with chunk c - 1, whose stage takes chunk
+// c + NST - 1.  blockIdx.z selects one of gridDim.z equal K ranges (split K): with
+// PF_PART the workgroup stores its partial tile at Y + z * S * ldy (k_pf_reduce adds the
+// ranges in order).
+enum { QT_PF_PART = 3 };
+template <int N>
+__device__ __forceinline__ void qt_vmcnt() {   // wait until at most N vector-memory ops are outstanding
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+template <int EPI, int NR, int NST>
+__global__ __launch_bounds__(QT_PF_WG) void k_pf_gemm2(const uint16_t *__restrict__ W, const uint16_t *__restrict__ P,
+                                                        int S, int Sp, int K, float *Y, int ldy) {
+    constexpr int KC = 64, ST = 64, STB = 3 * ST * KC * 2;      // one stage: 24 KiB
+    constexpr int NB = STB / 1024 / QT_WAVES;                   // 1-KiB copies per wave per chunk (6)
+    constexpr int OPS = NB + 2 * NR;                            // vector-memory ops per wave per chunk
+    static_assert(NB * 1024 * QT_WAVES == STB, "copy split");
+    __shared__ __align__(16) uint8_t sp[NST * STB];             // NST stages
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, j = lane & 15, kg = lane >> 4;
     const int n0 = blockIdx.x * (64 * NR) + wave * 16 * NR;
     const int s0 = blockIdx.y * ST;
+    const int kr = K / gridDim.z, k0 = blockIdx.z * kr, nch = kr / KC;
     const size_t plane = (size_t)Sp * K;
+    if (EPI == QT_PF_PART) Y += (size_t)blockIdx.z * S * ldy;
 
-    // this thread's share of a chunk's planes: 16-byte piece i is row (p*ST + t) = idx/8,
-    // k-part idx%8 of the chunk, idx = tid + 256 i
-    const uint16_t *gsrc[NSTG];
-    int soff[NSTG];
+    // this lane's source of each 1-KiB copy (chunk offset added per chunk)
+    const uint16_t *src[NB];
 #pragma unroll
-    for (int i = 0; i < NSTG; i++) {
-        const int idx = tid + QT_PF_WG * i, row = idx >> 3, c = idx & 7;
-        gsrc[i] = P + (row / ST) * plane + (size_t)(s0 + row % ST) * K + 8 * c;
-        soff[i] = row * ROWB + c * 16;
+    for (int b = 0; b < NB; b++) {
+        const int row = 8 * (wave * NB + b) + (lane >> 3), c = (lane & 7) ^ ((row >> 1) & 7);
+        src[b] = P + (row / ST) * plane + (size_t)(s0 + row % ST) * K + k0 + 8 * c;
     }
     const uint16_t *wrow[NR];
 #pragma unroll
-    for (int r = 0; r < NR; r++) wrow[r] = W + (size_t)(n0 + 16 * r + j) * K + 8 * kg;
-
-    qt_u32x4 stg[NSTG];
-    qt_u32x4 a[2][NR], an[2][NR];
-    qt_f32x4 acc[NR][NSB];
+    for (int r = 0; r < NR; r++) wrow[r] = W + (size_t)(n0 + 16 * r + j) * K + k0 + 8 * kg;
+    qt_u32x4 a[NST][2][NR];
+    auto issue = [&](int c, int st) {   // chunk c into stage st (compile-time st)
+        uint8_t *dst = sp + st * STB + (wave * NB) * 1024;
+#pragma unroll
+        for (int b = 0; b < NB; b++)
+            __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void *)(src[b] + c * KC),
+                                             (__attribute__((address_space(3))) void *)(dst + b * 1024), 16, 0, 0);
+    };
+    qt_f32x4 acc[NR][4];
 #pragma unroll
     for (int r = 0; r < NR; r++)
 #pragma unroll
-        for (int t = 0; t < NSB; t++) acc[r][t] = qt_f32x4{0.f, 0.f, 0.f, 0.f};
+        for (int t = 0; t < 4; t++) acc[r][t] = qt_f32x4{0.f, 0.f, 0.f, 0.f};
 
 #pragma unroll
-    for (int i = 0; i < NSTG; i++) stg[i] = *reinterpret_cast<const qt_u32x4 *>(gsrc[i]);
+    for (int c = 0; c < NST - 1; c++)
+        if (c < nch) {
+            issue(c, c);
 #pragma unroll
-    for (int ks = 0; ks < 2; ks++)
+            for (int ks = 0; ks < 2; ks++)
 #pragma unroll
-        for (int r = 0; r < NR; r++) a[ks][r] = *reinterpret_cast<const qt_u32x4 *>(wrow[r] + 32 * ks);
-#pragma unroll
-    for (int i = 0; i < NSTG; i++) *reinterpret_cast<qt_u32x4 *>(sp + soff[i]) = stg[i];
-    __syncthreads();
-    for (int kc = 0; kc < K; kc += KC) {
-        const int kn = kc + KC < K ? kc + KC : kc;   // the last chunk reloads itself (unused)
-#pragma unroll
-        for (int i = 0; i < NSTG; i++) stg[i] = *reinterpret_cast<const qt_u32x4 *>(gsrc[i] + kn);
-#pragma unroll
-        for (int ks = 0; ks < 2; ks++)
-#pragma unroll
-            for (int r = 0; r < NR; r++) an[ks][r] = *reinterpret_cast<const qt_u32x4 *>(wrow[r] + kn + 32 * ks);
-#pragma unroll
-        for (int ks = 0; ks < 2; ks++) {
-            qt_u32x4 b[NSB][3];
-#pragma unroll
-            for (int t = 0; t < NSB; t++)
-#pragma unroll
-                for (int p = 0; p < 3; p++) b[t][p] = qt_lds16(sp + (p * ST + 16 * t + j) * ROWB + (32 * ks + 8 * kg) * 2);
-#pragma unroll
-            for (int r = 0; r < NR; r++)
-#pragma unroll
-                for (int t = 0; t < NSB; t++)
-#pragma unroll
-                    for (int p = 0; p < 3; p++) acc[r][t] = qt_mfma_bf16(a[ks][r], b[t][p], acc[r][t]);
+                for (int r = 0; r < NR; r++) a[c][ks][r] = *reinterpret_cast<const qt_u32x4 *>(wrow[r] + c * KC + 32 * ks);
         }
-        __syncthreads();
+    const int f = j >> 1;                               // row swizzle of this lane's B rows
+    for (int cb = 0; cb < nch; cb += NST) {
 #pragma unroll
-        for (int i = 0; i < NSTG; i++) *reinterpret_cast<qt_u32x4 *>(sp + soff[i]) = stg[i];
+        for (int u = 0; u < NST; u++) {
+            const int c = cb + u;
+            if (c >= nch) break;
+            if (c + NST - 2 < nch) qt_vmcnt<(NST - 2) * OPS>();
+            else qt_vmcnt<0>();
+            __syncthreads();
+            const int cn = c + NST - 1;                  // stage (u + NST - 1) % NST held chunk c - 1
+            if (cn < nch) {
+                issue(cn, (u + NST - 1) % NST);
 #pragma unroll
-        for (int ks = 0; ks < 2; ks++)
+                for (int ks = 0; ks < 2; ks++)
 #pragma unroll
-            for (int r = 0; r < NR; r++) a[ks][r] = an[ks][r];
-        __syncthreads();
+                    for (int r = 0; r < NR; r++)
+                        a[(u + NST - 1) % NST][ks][r] = *reinterpret_cast<const qt_u32x4 *>(wrow[r] + cn * KC + 32 * ks);
+            }
+            const uint8_t *stg = sp + u * STB;
+#pragma unroll
+            for (int ks = 0; ks < 2; ks++) {
+                qt_u32x4 b[4][3];
+#pragma unroll
+                for (int t = 0; t < 4; t++)
+#pragma unroll
+                    for (int p = 0; p < 3; p++)
+                        b[t][p] = qt_lds16(stg + (p * ST + 16 * t + j) * (KC * 2) + 16 * ((4 * ks + kg) ^ f));
+#pragma unroll
+                for (int r = 0; r < NR; r++)
+#pragma unroll
+                    for (int t = 0; t < 4; t++)
+#pragma unroll
+                        for (int p = 0; p < 3; p++) acc[r][t] = qt_mfma_bf16(a[u][ks][r], b[t][p], acc[r][t]);
+            }
+        }
     }
-    // lane holds rows n0 + 16r + 4kg + i (i = 0..3) of position s0 + 16t + j
 #pragma unroll
     for (int r = 0; r < NR; r++)
 #pragma unroll
-        for (int t = 0; t < NSB; t++) {
+        for (int t = 0; t < 4; t++) {
             const int s = s0 + 16 * t + j, n = n0 + 16 * r + 4 * kg;
             if (s >= S) continue;
             const qt_f32x4 v = acc[r][t];
@@ -169,6 +193,21 @@ __global__ __launch_bounds__(QT_PF_WG) void k_pf_gemm(const uint16_t *__restrict
                 }
             }
         }
+}
+
+// Y[s][n] += sum over the nz K ranges of part[z][s][n], ranges in order.
+__global__ __launch_bounds__(QT_PF_WG) void k_pf_reduce(const float *part, int nz, int S, int N, float *Y, int ldy) {
+    const int i = blockIdx.x * QT_PF_WG + threadIdx.x;
+    if (i >= S * N / 4) return;
+    const int s = i / (N / 4), n = 4 * (i % (N / 4));
+    float4 acc = *reinterpret_cast<const float4 *>(part + (size_t)s * N + n);
+    for (int z = 1; z < nz; z++) {
+        const float4 v = *reinterpret_cast<const float4 *>(part + ((size_t)z * S + s) * N + n);
+        acc.x += v.x; acc.y += v.y; acc.z += v.z; acc.w += v.w;
+    }
+    float4 *y = reinterpret_cast<float4 *>(Y + (size_t)s * ldy + n);
+    const float4 o = *y;
+    *y = make_float4(o.x + acc.x, o.y + acc.y, o.z + acc.z, o.w + acc.w);
 }
 
 // ---- per-head q/k norm, RoPE, KV store ---------------------------------------------
@@ -276,20 +315,38 @@ extern "C" hipError_t qt_launch_pf_pieces(const float *X, int ldx, int S, int K,
     return hipGetLastError();
 }
 
+// part: workspace of 4 * S * N floats for split K (nullable: no split).  The residual
+// projections (few weight rows) split K so the grid fills the CUs; the partial ranges
+// are added in order (deterministic).
 extern "C" hipError_t qt_launch_pf_gemm(int epi, const uint16_t *W, const uint16_t *P, int S, int N, int K, float *Y,
-                                        int ldy, hipStream_t st) {
+                                        int ldy, float *part, hipStream_t st) {
+    constexpr int NST = 4;
     if (S <= 0 || N <= 0 || K <= 0 || N % 64 || K % 64 || epi < 0 || epi > 2) return hipErrorInvalidValue;
     if (epi != QT_PF_SWIGLU ? (ldy < N || ldy % 4) : (ldy < N / 2 || ldy % 2)) return hipErrorInvalidValue;
     const int Sp = qt_pf_spad(S);
-    // 128-row tiles where they still give a few workgroups per CU's worth of work
+    // 128-row tiles where they still give a workgroup per CU
     const bool big = N % 128 == 0 && (long long)(N / 128) * (Sp / 64) >= 256;
-    const dim3 grid(big ? N / 128 : N / 64, Sp / 64);
-#define QT_PF_GEMM(E)                                                                                   \
-    if (big) hipLaunchKernelGGL((k_pf_gemm<E, 2, 4>), grid, dim3(QT_PF_WG), 0, st, W, P, S, Sp, K, Y, ldy); \
-    else hipLaunchKernelGGL((k_pf_gemm<E, 1, 4>), grid, dim3(QT_PF_WG), 0, st, W, P, S, Sp, K, Y, ldy);
-    if (epi == QT_PF_STORE) { QT_PF_GEMM(QT_PF_STORE) }
-    else if (epi == QT_PF_RESID) { QT_PF_GEMM(QT_PF_RESID) }
-    else { QT_PF_GEMM(QT_PF_SWIGLU) }
+    const int gx = big ? N / 128 : N / 64;
+    int sk = 1;
+    if (epi == QT_PF_RESID && part)
+        while (sk < 4 && (long long)gx * (Sp / 64) * sk < 256 && (K / 64) % (2 * sk) == 0) sk *= 2;
+    const dim3 grid(gx, Sp / 64, sk);
+#define QT_PF_GEMM(E, OUT, LD)                                                                                         \
+    if (big) hipLaunchKernelGGL((k_pf_gemm2<E, 2, NST>), grid, dim3(QT_PF_WG), 0, st, W, P, S, Sp, K, OUT, LD);      \
+    else hipLaunchKernelGGL((k_pf_gemm2<E, 1, NST>), grid, dim3(QT_PF_WG), 0, st, W, P, S, Sp, K, OUT, LD);
+    if (sk > 1) {
+        QT_PF_GEMM(QT_PF_PART, part, N)
+        const hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+        hipLaunchKernelGGL(k_pf_reduce, dim3((S * N / 4 + QT_PF_WG - 1) / QT_PF_WG), dim3(QT_PF_WG), 0, st, part, sk, S,
+                           N, Y, ldy);
+    } else if (epi == QT_PF_STORE) {
+        QT_PF_GEMM(QT_PF_STORE, Y, ldy)
+    } else if (epi == QT_PF_RESID) {
+        QT_PF_GEMM(QT_PF_RESID, Y, ldy)
+    } else {
+        QT_PF_GEMM(QT_PF_SWIGLU, Y, ldy)
+    }
 #undef QT_PF_GEMM
     return hipGetLastError();
 }

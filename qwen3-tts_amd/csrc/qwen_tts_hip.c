@@ -268,6 +268,7 @@ typedef struct {
     dmat_t *pf_qkv, *pf_o, *pf_gu, *pf_dn;
     int pf_cap;             /* positions the buffers below hold */
     float *pf_x, *pf_qkvb, *pf_attn, *pf_h;
+    float *pf_part;         /* split-K partial sums [4][cap][H] */
     uint16_t *pf_p;         /* activation planes [3][spad][max(H, qd, F)] */
 } talker_t;
 
@@ -290,7 +291,7 @@ static void talker_destroy(talker_t *t) {
     stack_free(&t->s);
     void *bufs[] = {t->io, t->d_pos, t->d_frame, t->d_tok, t->d_hist, t->codec_head, t->codec_emb, t->logits,
                     t->ps_layers, t->ps_ring, t->ps_xin, t->ps_epoch, t->ps_err,
-                    t->pf_x, t->pf_qkvb, t->pf_attn, t->pf_h, t->pf_p};
+                    t->pf_x, t->pf_qkvb, t->pf_attn, t->pf_h, t->pf_p, t->pf_part};
     for (size_t i = 0; i < sizeof bufs / sizeof bufs[0]; i++) if (bufs[i]) (void)hipFree(bufs[i]);
     if (t->h_in) (void)hipHostFree(t->h_in);
     if (t->h_out) (void)hipHostFree(t->h_out);
@@ -562,9 +563,9 @@ fail:
 }
 
 static void pf_free_bufs(talker_t *t) {
-    void *b[] = {t->pf_x, t->pf_qkvb, t->pf_attn, t->pf_h, t->pf_p};
+    void *b[] = {t->pf_x, t->pf_qkvb, t->pf_attn, t->pf_h, t->pf_p, t->pf_part};
     for (size_t i = 0; i < sizeof b / sizeof b[0]; i++) if (b[i]) (void)hipFree(b[i]);
-    t->pf_x = t->pf_qkvb = t->pf_attn = t->pf_h = NULL; t->pf_p = NULL; t->pf_cap = 0;
+    t->pf_x = t->pf_qkvb = t->pf_attn = t->pf_h = t->pf_part = NULL; t->pf_p = NULL; t->pf_cap = 0;
 }
 
 int qwen_hip_talker_prefill(void *state, const qwen_hip_layer_t *bf16_layers, const float *embeds, int seq) {
@@ -597,6 +598,7 @@ int qwen_hip_talker_prefill(void *state, const qwen_hip_layer_t *bf16_layers, co
         HCK(hipMalloc((void **)&t->pf_attn, (size_t)seq * qd * sizeof(float)));
         HCK(hipMalloc((void **)&t->pf_h, (size_t)seq * F * sizeof(float)));
         HCK(hipMalloc((void **)&t->pf_p, (size_t)3 * sp * km * sizeof(uint16_t)));
+        HCK(hipMalloc((void **)&t->pf_part, (size_t)4 * seq * H * sizeof(float)));
         t->pf_cap = seq;
     }
     HCK(hipMemcpyAsync(t->pf_x, embeds, (size_t)seq * H * sizeof(float), hipMemcpyDefault, t->st));
@@ -604,16 +606,16 @@ int qwen_hip_talker_prefill(void *state, const qwen_hip_layer_t *bf16_layers, co
     for (int l = 0; l < L; l++) {
         const size_t lay = (size_t)l * s->nkv * s->kv_max * s->hd;
         HCK(qt_launch_pf_pieces(t->pf_x, H, seq, H, s->in_norm[l], s->eps, t->pf_p, t->st));
-        HCK(qt_launch_pf_gemm(QT_PF_STORE, (const uint16_t *)wq[l].w, t->pf_p, seq, qkvr, H, t->pf_qkvb, qkvr, t->st));
+        HCK(qt_launch_pf_gemm(QT_PF_STORE, (const uint16_t *)wq[l].w, t->pf_p, seq, qkvr, H, t->pf_qkvb, qkvr, NULL, t->st));
         HCK(qt_launch_pf_qkv_post(t->pf_qkvb, qkvr, seq, s->nh, s->nkv, s->qn[l], s->kn[l], s->rope_cos, s->rope_sin,
                                   s->eps, s->kc + lay, s->vc + lay, s->kv_max, t->st));
         HCK(qt_launch_pf_attn(t->pf_qkvb, qkvr, seq, s->nh, s->nkv, scale, t->pf_attn, qd, t->st));
         HCK(qt_launch_pf_pieces(t->pf_attn, qd, seq, qd, NULL, 0.f, t->pf_p, t->st));
-        HCK(qt_launch_pf_gemm(QT_PF_RESID, (const uint16_t *)wo[l].w, t->pf_p, seq, H, qd, t->pf_x, H, t->st));
+        HCK(qt_launch_pf_gemm(QT_PF_RESID, (const uint16_t *)wo[l].w, t->pf_p, seq, H, qd, t->pf_x, H, t->pf_part, t->st));
         HCK(qt_launch_pf_pieces(t->pf_x, H, seq, H, s->post_norm[l], s->eps, t->pf_p, t->st));
-        HCK(qt_launch_pf_gemm(QT_PF_SWIGLU, (const uint16_t *)wgu[l].w, t->pf_p, seq, 2 * F, H, t->pf_h, F, t->st));
+        HCK(qt_launch_pf_gemm(QT_PF_SWIGLU, (const uint16_t *)wgu[l].w, t->pf_p, seq, 2 * F, H, t->pf_h, F, NULL, t->st));
         HCK(qt_launch_pf_pieces(t->pf_h, F, seq, F, NULL, 0.f, t->pf_p, t->st));
-        HCK(qt_launch_pf_gemm(QT_PF_RESID, (const uint16_t *)wdn[l].w, t->pf_p, seq, H, F, t->pf_x, H, t->st));
+        HCK(qt_launch_pf_gemm(QT_PF_RESID, (const uint16_t *)wdn[l].w, t->pf_p, seq, H, F, t->pf_x, H, t->pf_part, t->st));
     }
     /* dec_x = the last position's residual (t.c:1032-1033), where get_dec_x reads it */
     HCK(hipMemcpyAsync(t->io + H, t->pf_x + (size_t)(seq - 1) * H, (size_t)H * sizeof(float), hipMemcpyDeviceToDevice, t->st));
@@ -641,16 +643,16 @@ int qwen_hip_talker_prefill_async(void *state, int seq, int n) {
         for (int l = 0; l < L; l++) {
             const size_t lay = (size_t)l * s->nkv * s->kv_max * s->hd;
             HCK(qt_launch_pf_pieces(t->pf_x, H, seq, H, s->in_norm[l], s->eps, t->pf_p, t->st));
-            HCK(qt_launch_pf_gemm(QT_PF_STORE, (const uint16_t *)wq[l].w, t->pf_p, seq, qkvr, H, t->pf_qkvb, qkvr, t->st));
+            HCK(qt_launch_pf_gemm(QT_PF_STORE, (const uint16_t *)wq[l].w, t->pf_p, seq, qkvr, H, t->pf_qkvb, qkvr, NULL, t->st));
             HCK(qt_launch_pf_qkv_post(t->pf_qkvb, qkvr, seq, s->nh, s->nkv, s->qn[l], s->kn[l], s->rope_cos, s->rope_sin,
                                       s->eps, s->kc + lay, s->vc + lay, s->kv_max, t->st));
             HCK(qt_launch_pf_attn(t->pf_qkvb, qkvr, seq, s->nh, s->nkv, scale, t->pf_attn, qd, t->st));
             HCK(qt_launch_pf_pieces(t->pf_attn, qd, seq, qd, NULL, 0.f, t->pf_p, t->st));
-            HCK(qt_launch_pf_gemm(QT_PF_RESID, (const uint16_t *)wo[l].w, t->pf_p, seq, H, qd, t->pf_x, H, t->st));
+            HCK(qt_launch_pf_gemm(QT_PF_RESID, (const uint16_t *)wo[l].w, t->pf_p, seq, H, qd, t->pf_x, H, t->pf_part, t->st));
             HCK(qt_launch_pf_pieces(t->pf_x, H, seq, H, s->post_norm[l], s->eps, t->pf_p, t->st));
-            HCK(qt_launch_pf_gemm(QT_PF_SWIGLU, (const uint16_t *)wgu[l].w, t->pf_p, seq, 2 * F, H, t->pf_h, F, t->st));
+            HCK(qt_launch_pf_gemm(QT_PF_SWIGLU, (const uint16_t *)wgu[l].w, t->pf_p, seq, 2 * F, H, t->pf_h, F, NULL, t->st));
             HCK(qt_launch_pf_pieces(t->pf_h, F, seq, F, NULL, 0.f, t->pf_p, t->st));
-            HCK(qt_launch_pf_gemm(QT_PF_RESID, (const uint16_t *)wdn[l].w, t->pf_p, seq, H, F, t->pf_x, H, t->st));
+            HCK(qt_launch_pf_gemm(QT_PF_RESID, (const uint16_t *)wdn[l].w, t->pf_p, seq, H, F, t->pf_x, H, t->pf_part, t->st));
         }
     return 0;
 fail:
@@ -1635,7 +1637,7 @@ fail:
 int qwen_hip_op_prefill_gemm(float *Y, const uint16_t *W, const float *X, int S, int N, int K, int epi) {
     hipStream_t st = op_stream();
     uint16_t *dw = NULL, *dp = NULL;
-    float *dx = NULL, *dy = NULL;
+    float *dx = NULL, *dy = NULL, *dpart = NULL;
     REQ(st, "no stream");
     REQ(S >= 1 && N >= 64 && K >= 64 && N % 64 == 0 && K % 64 == 0 && epi >= 0 && epi <= 2, "bad shape/epi");
     const int ny = epi == QT_PF_SWIGLU ? N / 2 : N;
@@ -1643,16 +1645,18 @@ int qwen_hip_op_prefill_gemm(float *Y, const uint16_t *W, const float *X, int S,
     HCK(hipMalloc((void **)&dx, (size_t)S * K * sizeof(float)));
     HCK(hipMalloc((void **)&dy, (size_t)S * ny * sizeof(float)));
     HCK(hipMalloc((void **)&dp, (size_t)3 * qt_pf_spad(S) * K * 2));
+    HCK(hipMalloc((void **)&dpart, (size_t)4 * S * N * sizeof(float)));
     HCK(hipMemcpyAsync(dw, W, (size_t)N * K * 2, hipMemcpyHostToDevice, st));
     HCK(hipMemcpyAsync(dx, X, (size_t)S * K * sizeof(float), hipMemcpyHostToDevice, st));
     if (epi == QT_PF_RESID) HCK(hipMemcpyAsync(dy, Y, (size_t)S * ny * sizeof(float), hipMemcpyHostToDevice, st));
     HCK(qt_launch_pf_pieces(dx, K, S, K, NULL, 0.f, dp, st));
-    HCK(qt_launch_pf_gemm(epi, dw, dp, S, N, K, dy, ny, st));
+    HCK(qt_launch_pf_gemm(epi, dw, dp, S, N, K, dy, ny, dpart, st));
     HCK(hipMemcpyAsync(Y, dy, (size_t)S * ny * sizeof(float), hipMemcpyDeviceToHost, st));
     HCK(hipStreamSynchronize(st));
-    (void)hipFree(dw); (void)hipFree(dx); (void)hipFree(dy); (void)hipFree(dp);
+    (void)hipFree(dw); (void)hipFree(dx); (void)hipFree(dy); (void)hipFree(dp); (void)hipFree(dpart);
     return 0;
 fail:
+    if (dpart) (void)hipFree(dpart);
     if (dw) (void)hipFree(dw);
     if (dx) (void)hipFree(dx);
     if (dy) (void)hipFree(dy);
