@@ -233,6 +233,10 @@ int qwen_hip_op_swiglu(float *out, const float *gate_up, int n);
  * (epi 0), Y += that (epi 1), or SwiGLU of the interleaved gate|up rows into Y[S][N/2]
  * (epi 2); W bf16, f32 host arrays, N and K multiples of 64. */
 int qwen_hip_op_prefill_gemm(float *Y, const uint16_t *W, const float *X, int S, int N, int K, int epi);
+/* The prefill's causal attention alone (qwen_causal_attention, k.c:3454-3560, as
+ * t.c:904-907 calls it): out f32[S][nh*128] from QKV f32[S][(nh + 2 nkv)*128] holding the
+ * normed, rotated q | k | v rows of every position. */
+int qwen_hip_op_prefill_attention(float *out, const float *QKV, int S, int nh, int nkv, float scale);
 int qwen_hip_op_argmax_matvec(int prec, const float *x, const void *W, const float *scale, int in_dim, int out_dim);
 /* qwen_matmat_int8 (qwen_tts_kernels.h:121-122): Y[rows][B] = (W*scale) @ X[cols][B]
  * (row-major f32, B <= 64, cols a multiple of 64) on the batched MFMA kernel. */

@@ -248,56 +248,122 @@ __global__ __launch_bounds__(QT_PF_WG) void k_pf_qkv_post(float *QKV, int ld, in
     }
 }
 
-// ---- causal attention over the f32 q/k/v --------------------------------------------
-// qwen_causal_attention (k.c:3454-3560) as the prefill calls it (t.c:904-907): query i
-// of head h (kv head h / (nh/nkv)) over positions j <= i, one wave per query, lane d
-// holding dims d and d + 64; per key the online softmax of the reference (s > max:
-// c = e^(max - s), sum = sum c + 1, o = o c + v; else w = e^(s - max), sum += w,
-// o += v w), then o / sum.  Four keys' dot products are formed before their updates.
-__global__ __launch_bounds__(QT_PF_WG) void k_pf_attn(const float *QKV, int ld, int S, int nh, int nkv, float scale,
-                                                       float *A, int lda) {
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int i = blockIdx.x * QT_WAVES + wave, h = blockIdx.y, g = h / (nh / nkv);
-    if (i >= S) return;
+// ---- causal attention, tiled -------------------------------------------------------
+// The same attention for 64 queries of one head per workgroup, over 64-key blocks held in
+// LDS (flash-style: per block, row max -> rescale of the running sums -> P.V).  Thread t
+// takes queries r = t/16 + 16a (a = 0..3) and, for the scores, keys t%16 + 16b, for P.V
+// the dims 4(t%16) + 64h + e (h = 0..1, e = 0..3); the 16 threads of a query row are one
+// DPP row, so row max and row sum are 16-lane reductions.  K rows are padded to 132
+// floats so the 16 key rows a wave reads at one offset fall in 16 different bank groups.
+#define QT_PF_KP 132
+template <int QA>   // queries per thread: 16 * QA queries per workgroup
+__global__ __launch_bounds__(QT_PF_WG) void k_pf_fattn(const float *QKV, int ld, int S, int nh, int nkv, float scale,
+                                                        float *A, int lda) {
+    constexpr int QB = 16 * QA;
+    __shared__ __align__(16) float qs[QB][128];
+    __shared__ __align__(16) float ks[64][QT_PF_KP];
+    __shared__ __align__(16) float vs[64][128];
+    __shared__ __align__(16) float ps[QB][68];
+    const int tid = threadIdx.x, rq = tid >> 4, cg = tid & 15;
+    const int q0 = blockIdx.x * QB, h = blockIdx.y, g = h / (nh / nkv);
     const int qd = nh * 128, kvd = nkv * 128;
-    const float *qr = QKV + (size_t)i * ld + h * 128;
-    const float q0 = qr[lane], q1 = qr[lane + 64];
-    const float *kb = QKV + qd + g * 128, *vb = QKV + qd + kvd + g * 128;
-    float mx = -1e30f, sum = 0.f, o0 = 0.f, o1 = 0.f;
-    auto upd = [&](float sc, float v0, float v1) {
-        if (sc > mx) {
-            const float c = expf(mx - sc);
-            sum = sum * c + 1.0f;
-            o0 = o0 * c + v0; o1 = o1 * c + v1;
-            mx = sc;
-        } else {
-            const float w = expf(sc - mx);
-            sum += w;
-            o0 += v0 * w; o1 += v1 * w;
-        }
-    };
-    int jj = 0;
-    for (; jj + 3 <= i; jj += 4) {
-        float sc[4], v0[4], v1[4];
-#pragma unroll
-        for (int u = 0; u < 4; u++) {
-            const float *kr = kb + (size_t)(jj + u) * ld, *vr = vb + (size_t)(jj + u) * ld;
-            sc[u] = q0 * kr[lane] + q1 * kr[lane + 64];
-            v0[u] = vr[lane]; v1[u] = vr[lane + 64];
-        }
-#pragma unroll
-        for (int u = 0; u < 4; u++) sc[u] = group_sum<64>(sc[u]) * scale;
-#pragma unroll
-        for (int u = 0; u < 4; u++) upd(sc[u], v0[u], v1[u]);
+    // Q block (rows past S: zeros)
+    for (int i = tid; i < QB * 32; i += QT_PF_WG) {
+        const int r = i >> 5, c = (i & 31) * 4, q = q0 + r;
+        *reinterpret_cast<float4 *>(&qs[r][c]) =
+            q < S ? *reinterpret_cast<const float4 *>(QKV + (size_t)q * ld + h * 128 + c) : make_float4(0.f, 0.f, 0.f, 0.f);
     }
-    for (; jj <= i; jj++) {
-        const float *kr = kb + (size_t)jj * ld, *vr = vb + (size_t)jj * ld;
-        const float sc = group_sum<64>(q0 * kr[lane] + q1 * kr[lane + 64]) * scale;
-        upd(sc, vr[lane], vr[lane + 64]);
+    float m[QA], l[QA], o[QA][8];
+#pragma unroll
+    for (int a = 0; a < QA; a++) {
+        m[a] = -INFINITY; l[a] = 0.f;
+#pragma unroll
+        for (int e = 0; e < 8; e++) o[a][e] = 0.f;
     }
-    const float inv = 1.0f / sum;
-    A[(size_t)i * lda + h * 128 + lane] = o0 * inv;
-    A[(size_t)i * lda + h * 128 + lane + 64] = o1 * inv;
+    const int nkb = (q0 + QB - 1) / 64 + 1;              // key blocks up to the one holding the last query
+    for (int kb = 0; kb < nkb; kb++) {
+        const int j0 = kb * 64;
+        __syncthreads();                                // previous block's K/V/P reads done
+        for (int i = tid; i < 64 * 32; i += QT_PF_WG) {
+            const int r = i >> 5, c = (i & 31) * 4, j = j0 + r;
+            float4 kv = make_float4(0.f, 0.f, 0.f, 0.f), vv = kv;
+            if (j < S) {
+                kv = *reinterpret_cast<const float4 *>(QKV + (size_t)j * ld + qd + g * 128 + c);
+                vv = *reinterpret_cast<const float4 *>(QKV + (size_t)j * ld + qd + kvd + g * 128 + c);
+            }
+            *reinterpret_cast<float4 *>(&ks[r][c]) = kv;
+            *reinterpret_cast<float4 *>(&vs[r][c]) = vv;
+        }
+        __syncthreads();
+        // scores of queries rq + 16a with keys cg + 16b
+        float sc[QA][4];
+#pragma unroll
+        for (int a = 0; a < QA; a++)
+#pragma unroll
+            for (int b = 0; b < 4; b++) sc[a][b] = 0.f;
+        for (int d = 0; d < 128; d += 4) {
+            float4 qv[QA], kv[4];
+#pragma unroll
+            for (int a = 0; a < QA; a++) qv[a] = *reinterpret_cast<const float4 *>(&qs[rq + 16 * a][d]);
+#pragma unroll
+            for (int b = 0; b < 4; b++) kv[b] = *reinterpret_cast<const float4 *>(&ks[cg + 16 * b][d]);
+#pragma unroll
+            for (int a = 0; a < QA; a++)
+#pragma unroll
+                for (int b = 0; b < 4; b++)
+                    sc[a][b] = fmaf(qv[a].w, kv[b].w, fmaf(qv[a].z, kv[b].z, fmaf(qv[a].y, kv[b].y, fmaf(qv[a].x, kv[b].x, sc[a][b]))));
+        }
+        // causal mask (keys after the query, keys past S), block max, rescale, P
+#pragma unroll
+        for (int a = 0; a < QA; a++) {
+            const int q = q0 + rq + 16 * a;
+            float bm = -INFINITY;
+#pragma unroll
+            for (int b = 0; b < 4; b++) {
+                const int j = j0 + cg + 16 * b;
+                sc[a][b] = (j <= q && j < S) ? sc[a][b] * scale : -INFINITY;
+                bm = fmaxf(bm, sc[a][b]);
+            }
+            bm = group_max<16>(bm);
+            const float mn = fmaxf(m[a], bm);
+            const float mr = mn == -INFINITY ? 0.f : mn;   // a query row past S has no key at all
+            const float c = expf(m[a] - mr);
+            float rs = 0.f;
+#pragma unroll
+            for (int b = 0; b < 4; b++) {
+                const float pv = expf(sc[a][b] - mr);
+                ps[rq + 16 * a][cg + 16 * b] = pv;
+                rs += pv;
+            }
+            l[a] = l[a] * c + group_sum<16>(rs);
+            m[a] = mn;
+#pragma unroll
+            for (int e = 0; e < 8; e++) o[a][e] *= c;
+        }
+        __syncthreads();
+        // o[a][4h + e] += sum_j P[rq + 16a][j] * V[j][64h + 4cg + e]
+        for (int jj = 0; jj < 64; jj++) {
+            const float4 v0 = *reinterpret_cast<const float4 *>(&vs[jj][4 * cg]);
+            const float4 v1 = *reinterpret_cast<const float4 *>(&vs[jj][64 + 4 * cg]);
+#pragma unroll
+            for (int a = 0; a < QA; a++) {
+                const float pv = ps[rq + 16 * a][jj];
+                o[a][0] = fmaf(pv, v0.x, o[a][0]); o[a][1] = fmaf(pv, v0.y, o[a][1]);
+                o[a][2] = fmaf(pv, v0.z, o[a][2]); o[a][3] = fmaf(pv, v0.w, o[a][3]);
+                o[a][4] = fmaf(pv, v1.x, o[a][4]); o[a][5] = fmaf(pv, v1.y, o[a][5]);
+                o[a][6] = fmaf(pv, v1.z, o[a][6]); o[a][7] = fmaf(pv, v1.w, o[a][7]);
+            }
+        }
+    }
+#pragma unroll
+    for (int a = 0; a < QA; a++) {
+        const int q = q0 + rq + 16 * a;
+        if (q >= S) continue;
+        const float inv = 1.0f / l[a];
+        float *out = A + (size_t)q * lda + h * 128;
+        *reinterpret_cast<float4 *>(out + 4 * cg) = make_float4(o[a][0] * inv, o[a][1] * inv, o[a][2] * inv, o[a][3] * inv);
+        *reinterpret_cast<float4 *>(out + 64 + 4 * cg) = make_float4(o[a][4] * inv, o[a][5] * inv, o[a][6] * inv, o[a][7] * inv);
+    }
 }
 
 // ---- launchers -------------------------------------------------------------------------
@@ -324,15 +390,18 @@ extern "C" hipError_t qt_launch_pf_gemm(int epi, const uint16_t *W, const uint16
     if (S <= 0 || N <= 0 || K <= 0 || N % 64 || K % 64 || epi < 0 || epi > 2) return hipErrorInvalidValue;
     if (epi != QT_PF_SWIGLU ? (ldy < N || ldy % 4) : (ldy < N / 2 || ldy % 2)) return hipErrorInvalidValue;
     const int Sp = qt_pf_spad(S);
-    // 128-row tiles where they still give a workgroup per CU
-    const bool big = N % 128 == 0 && (long long)(N / 128) * (Sp / 64) >= 256;
-    const int gx = big ? N / 128 : N / 64;
+    // the tallest weight tile (256, 128 or 64 rows) that still gives a workgroup per CU:
+    // taller tiles reuse each LDS read of the planes over more rows
+    const int nr = (N % 256 == 0 && (long long)(N / 256) * (Sp / 64) >= 256) ? 4
+                 : (N % 128 == 0 && (long long)(N / 128) * (Sp / 64) >= 256) ? 2 : 1;
+    const int gx = N / (64 * nr);
     int sk = 1;
     if (epi == QT_PF_RESID && part)
         while (sk < 4 && (long long)gx * (Sp / 64) * sk < 256 && (K / 64) % (2 * sk) == 0) sk *= 2;
     const dim3 grid(gx, Sp / 64, sk);
 #define QT_PF_GEMM(E, OUT, LD)                                                                                         \
-    if (big) hipLaunchKernelGGL((k_pf_gemm2<E, 2, NST>), grid, dim3(QT_PF_WG), 0, st, W, P, S, Sp, K, OUT, LD);      \
+    if (nr == 4) hipLaunchKernelGGL((k_pf_gemm2<E, 4, 3>), grid, dim3(QT_PF_WG), 0, st, W, P, S, Sp, K, OUT, LD);    \
+    else if (nr == 2) hipLaunchKernelGGL((k_pf_gemm2<E, 2, NST>), grid, dim3(QT_PF_WG), 0, st, W, P, S, Sp, K, OUT, LD); \
     else hipLaunchKernelGGL((k_pf_gemm2<E, 1, NST>), grid, dim3(QT_PF_WG), 0, st, W, P, S, Sp, K, OUT, LD);
     if (sk > 1) {
         QT_PF_GEMM(QT_PF_PART, part, N)
@@ -363,7 +432,10 @@ extern "C" hipError_t qt_launch_pf_qkv_post(float *QKV, int ld, int S, int nh, i
 extern "C" hipError_t qt_launch_pf_attn(const float *QKV, int ld, int S, int nh, int nkv, float scale, float *A,
                                         int lda, hipStream_t st) {
     if (S <= 0 || nh <= 0 || nkv <= 0 || nh % nkv) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(k_pf_attn, dim3((S + QT_WAVES - 1) / QT_WAVES, nh), dim3(QT_PF_WG), 0, st, QKV, ld, S, nh, nkv,
-                       scale, A, lda);
+    // 32-query workgroups where 64-query ones would leave CUs idle
+    if ((long long)((S + 63) / 64) * nh >= 256)
+        hipLaunchKernelGGL(k_pf_fattn<4>, dim3((S + 63) / 64, nh), dim3(QT_PF_WG), 0, st, QKV, ld, S, nh, nkv, scale, A, lda);
+    else
+        hipLaunchKernelGGL(k_pf_fattn<2>, dim3((S + 31) / 32, nh), dim3(QT_PF_WG), 0, st, QKV, ld, S, nh, nkv, scale, A, lda);
     return hipGetLastError();
 }

@@ -1664,6 +1664,27 @@ fail:
     return -1;
 }
 
+/* The prefill's causal attention alone: out[S][nh*128] from QKV host f32[S][(nh+2nkv)*128]
+ * (q | k | v rows as the prefill holds them after norm and RoPE). */
+int qwen_hip_op_prefill_attention(float *out, const float *QKV, int S, int nh, int nkv, float scale) {
+    hipStream_t st = op_stream();
+    float *dq = NULL, *dout = NULL;
+    REQ(st && S >= 1 && nh > 0 && nkv > 0 && nh % nkv == 0, "bad args");
+    const int ld = (nh + 2 * nkv) * 128;
+    HCK(hipMalloc((void **)&dq, (size_t)S * ld * sizeof(float)));
+    HCK(hipMalloc((void **)&dout, (size_t)S * nh * 128 * sizeof(float)));
+    HCK(hipMemcpyAsync(dq, QKV, (size_t)S * ld * sizeof(float), hipMemcpyHostToDevice, st));
+    HCK(qt_launch_pf_attn(dq, ld, S, nh, nkv, scale, dout, nh * 128, st));
+    HCK(hipMemcpyAsync(out, dout, (size_t)S * nh * 128 * sizeof(float), hipMemcpyDeviceToHost, st));
+    HCK(hipStreamSynchronize(st));
+    (void)hipFree(dq); (void)hipFree(dout);
+    return 0;
+fail:
+    if (dq) (void)hipFree(dq);
+    if (dout) (void)hipFree(dout);
+    return -1;
+}
+
 int qwen_hip_op_swiglu(float *out, const float *gate_up, int n) {
     hipStream_t st = op_stream();
     float *dg = NULL, *dout = NULL;

@@ -34,6 +34,7 @@ EXPORTS = [
     "qwen_hip_cp_batch_init", "qwen_hip_cp_batch_step", "qwen_hip_cp_batch_free", "qwen_hip_op_matmat_int8",
     "qwen_hip_cp_set_prefill2", "qwen_hip_cp_prefill2",
     "qwen_hip_talker_prefill", "qwen_hip_talker_prefill_async", "qwen_hip_op_prefill_gemm",
+    "qwen_hip_op_prefill_attention",
 ]
 
 
@@ -84,6 +85,8 @@ def lib():
         L.qwen_hip_talker_prefill.argtypes = [vp, vp, vp, i]; L.qwen_hip_talker_prefill.restype = i
         L.qwen_hip_talker_prefill_async.argtypes = [vp, i, i]; L.qwen_hip_talker_prefill_async.restype = i
         L.qwen_hip_op_prefill_gemm.argtypes = [vp, vp, vp, i, i, i, i]; L.qwen_hip_op_prefill_gemm.restype = i
+        L.qwen_hip_op_prefill_attention.argtypes = [vp, vp, i, i, i, C.c_float]
+        L.qwen_hip_op_prefill_attention.restype = i
         L.qwen_hip_talker_download_kv.argtypes = [vp, vp, vp, i, i]; L.qwen_hip_talker_download_kv.restype = i
         L.qwen_hip_talker_free.argtypes = [vp]
         L.qwen_hip_talker_greedy.argtypes = [vp, vp, vp, i, vp, i, i, i, vp, vp]

@@ -28,7 +28,8 @@ def _gemm(W, X, epi, Y0=None):
 
 
 @pytest.mark.parametrize("S,N,K", [(1, 64, 64), (17, 128, 256), (24, 1024, 256), (64, 4096, 2048),
-                                   (100, 2048, 6144), (257, 192, 320), (200, 12288, 2048)])
+                                   (100, 2048, 6144), (257, 192, 320), (200, 12288, 2048),
+                                   (512, 8192, 256)])
 def test_op_prefill_gemm(S, N, K):
     print(f"[case] prefill gemm S={S} N={N} K={K}", flush=True)
     rng = np.random.default_rng(S * 131 + N + K)
@@ -58,6 +59,23 @@ def test_op_prefill_gemm_planes_are_exact():
     X = (rng.standard_normal((S, K)) * np.exp(rng.uniform(-20, 20, (S, K)))).astype(np.float32)
     Y = _gemm(W, X, 0)
     assert np.array_equal(Y, X[:, (7 * np.arange(N)) % K])
+
+
+@pytest.mark.parametrize("S,nh,nkv", [(1, 16, 8), (37, 16, 8), (100, 4, 2), (300, 16, 8), (1000, 16, 8)])
+def test_op_prefill_attention(oracle, S, nh, nkv):
+    """The tiled causal attention (32- and 64-query workgroups) against the oracle's f32
+    attention (qwen_causal_attention restated)."""
+    print(f"[case] prefill attention S={S} nh={nh} nkv={nkv}", flush=True)
+    rng = np.random.default_rng(S + nh)
+    ld = (nh + 2 * nkv) * 128
+    qkv = (rng.standard_normal((S, ld)) * 1.5).astype(np.float32)
+    out = np.empty((S, nh * 128), np.float32)
+    sc = np.float32(1.0 / np.sqrt(128.0))
+    hip.check(hip.lib().qwen_hip_op_prefill_attention(out.ctypes.data, qkv.ctypes.data, S, nh, nkv, sc), "pf_attn")
+    q = np.ascontiguousarray(qkv[:, :nh * 128]); k = np.ascontiguousarray(qkv[:, nh * 128:(nh + nkv) * 128])
+    v = np.ascontiguousarray(qkv[:, (nh + nkv) * 128:])
+    ref = oracle.attention_f32(q, k, v, S, S, nh, nkv, 128, float(sc), 0).reshape(S, nh * 128)
+    assert rel_l2(out, ref) < 2e-6 and np.abs(out - ref).max() < 1e-5
 
 
 def _tiny_talker(prec_code, quantize_to=-1, kv_max=64):
