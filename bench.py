@@ -90,6 +90,10 @@ WORKLOADS = {
     "talker-1.7B-int4-b1-L2048": ("1.7B", "int4", 2048, 64),
     "talker-1.7B-int4-b1-L4096": ("1.7B", "int4", 4096, 64),
 }
+# KV grown from 0 over the timed steps (config 2): (shape, precision, total steps, steps per launch)
+GROW_WORKLOADS = {
+    "talker-0.6B-int8-grow2048": ("0.6B", "int8", 2048, 256),
+}
 # Code Predictor frames: (shape, precision, default timed frames, two-position prefill)
 CP_WORKLOADS = {
     "cp-0.6B-bf16-frame": ("0.6B", "bf16", 500, False),
@@ -131,7 +135,7 @@ def main():
     ap.add_argument("--steps", type=int, default=None)
     ap.add_argument("--warmup", type=int, default=None)
     ap.add_argument("--workload", default="talker-1.7B-int8-b1-L2048", choices=sorted(WORKLOADS) + sorted(BATCH_WORKLOADS) + sorted(CP_WORKLOADS)
-                    + sorted(PREFILL_WORKLOADS))
+                    + sorted(PREFILL_WORKLOADS) + sorted(GROW_WORKLOADS))
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--kernel-launches", type=int, default=200)
@@ -151,6 +155,8 @@ def main():
         return bench_cp(args)
     if args.workload in PREFILL_WORKLOADS:
         return bench_prefill(args)
+    if args.workload in GROW_WORKLOADS:
+        return bench_grow(args)
     from qwen3_tts_amd import hip, synth
     shape_name, prec, Lpre, dsteps = WORKLOADS[args.workload]
     K = args.steps or dsteps
@@ -330,6 +336,71 @@ def bench_batch(args):
                      "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
                      "kernel": "batched step (MFMA int8 GEMMs + ragged split-K attention), whole step",
                      "bytes_per_launch": int(step_bytes), "avg_us": round(ms * 1e3, 1), "steps_per_launch": 1},
+        "cpu_baseline": None,
+    }
+    print(json.dumps(out), flush=True)
+
+
+def bench_grow(args):
+    """Config 2: the greedy decode with the KV cache grown from 0 to N positions over N
+    steps (no upload), as N / seg launches of seg steps each, every launch timed with HIP
+    events; reports ms/step per KV-length segment and the mean over all N steps (value).
+    A 16-step launch from position 0 runs first (untimed) and the loop is re-seeded at 0."""
+    from qwen3_tts_amd import hip, synth
+    shape_name, prec, N, seg = GROW_WORKLOADS[args.workload]
+    s = synth.SHAPES[shape_name]
+    kv_max = N + 64
+    only = lambda n: not n.startswith("talker.code_predictor.")  # noqa: E731
+    tens = synth.generate(s, 0x5EED0001, 0.0, threads=int(os.environ.get("OMP_NUM_THREADS", "16")), only=only)
+    layers = hip.layers_from_tensors(tens, s)
+    cos, sin = synth.rope_tables(s.head_dim, s.rope_theta, kv_max)
+    fnorm = synth.bf16_to_f32(tens["talker.model.norm.weight"])
+    g = hip.Talker(s, layers, fnorm, cos, sin, hip.BF16, kv_max, quantize_to=hip.PREC[prec])
+    head = np.ascontiguousarray(tens["talker.codec_head.weight"])
+    emb = np.ascontiguousarray(tens["talker.model.codec_embedding.weight"])
+    L = hip.lib()
+    ev = HipEvents()
+    stream = L.qwen_hip_talker_stream(g.h)
+    e0 = synth.bf16_to_f32(emb[1234])
+    g.greedy(head, emb, e0, 0, 0, 0)
+    hip.check(L.qwen_hip_talker_greedy_async(g.h, 16), "warmup")
+    hip.check(L.qwen_hip_talker_sync(g.h), "sync")
+    g.greedy(head, emb, e0, 0, 0, 0)                   # re-seed at position 0
+    ev.device_sync()
+    segs = []
+    kv_bytes = 2 * s.layers * s.kv_dim * 2
+    total_ms = 0.0
+    for i in range(N // seg):
+        a, b = ev.event(), ev.event()
+        ev.record(a, stream)
+        hip.check(L.qwen_hip_talker_greedy_async(g.h, seg), "grow steps")
+        ev.record(b, stream)
+        ms_total = ev.elapsed_ms(a, b)
+        ev.device_sync()
+        total_ms += ms_total
+        ms = ms_total / seg
+        lm = i * seg + seg / 2.0
+        gbs = (weight_bytes(s, prec) + kv_bytes * (lm + 1) + s.codec_vocab * s.hidden * 2) / (ms * 1e-3) / 1e9
+        segs.append({"kv_from": i * seg, "kv_to": (i + 1) * seg, "ms_per_step": round(ms, 4), "gbs": round(gbs, 1)})
+        log(f"[bench] grow: KV {i * seg:5d}..{(i + 1) * seg:5d}: {ms * 1e3:.1f} us/step, {gbs:.0f} GB/s")
+    fused = bool(L.qwen_hip_talker_fused(g.h))
+    g.free()
+    ms = total_ms / N
+    byts = sum(weight_bytes(s, prec) + kv_bytes * (j + 1) + s.codec_vocab * s.hidden * 2 for j in range(N)) / N
+    gbs = byts / (ms * 1e-3) / 1e9
+    out = {
+        "metric": "Talker ms/decode-step (0.6B/1.7B, bf16/int8/int4) + achieved HBM GB/s",
+        "value": round(ms, 4), "unit": "ms/step", "n_gpus": 1, "steps": N, "warmup": 16,
+        "ms_per_step": round(ms, 4), "higher_is_better": False, "scaling": "weak", "vs_baseline": None,
+        "dtype": prec, "data": "synthetic (seeded N(0,0.02) random-init weights; KV written by the steps themselves)",
+        "config": {"workload": args.workload, "batch": 1, "kv_len_start": 0, "kv_len_end": N, "layers": s.layers,
+                   "hidden": s.hidden, "inter": s.inter},
+        "segments": segs,
+        "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": (f"ps::k_pstep<{prec}> fused decode step" if fused else "unfused per-kernel path"),
+                     "bytes_per_launch": int(byts * seg), "avg_us": round(total_ms / (N // seg) * 1e3, 1),
+                     "steps_per_launch": seg},
         "cpu_baseline": None,
     }
     print(json.dumps(out), flush=True)
