@@ -258,42 +258,66 @@ __device__ __forceinline__ void gather(int n, AddrF addr, float *dst, unsigned t
 template <int PREC> struct Epc;
 template <> struct Epc<QT_BF16> { static constexpr int v = 8; };
 template <> struct Epc<QT_INT8> { static constexpr int v = 16; };
+template <> struct Epc<QT_Q4> { static constexpr int v = 32; };
 
 // NR consecutive rows per wave of a [rows][COLS] matrix; each row is split over the 64
 // lanes, lane l holding the 16-byte chunks c = l + 64*j (j < CPL).  Also carries the
-// int8 row scales; row0w is wave-uniform, so those are scalar loads (SGPRs, counted
-// apart from the vector loads in flight).
+// int8 row scales (row0w is wave-uniform, so those are scalar loads: SGPRs, counted
+// apart from the vector loads in flight) or, for q4_0, the f16 bits of each chunk's
+// block scale (one 32-weight block per chunk: [rows][COLS/32] halves, vector loads).
 template <int PREC, int COLS, int NR_>
 struct Tile {
     static constexpr int NR = NR_;
     static constexpr int EPC = Epc<PREC>::v;
     static constexpr int CPL = COLS / (EPC * 64);
-    static constexpr size_t RB = PREC == QT_BF16 ? (size_t)COLS * 2 : (size_t)COLS;
+    static constexpr size_t RB = PREC == QT_BF16 ? (size_t)COLS * 2 : PREC == QT_INT8 ? (size_t)COLS : (size_t)COLS / 2;
     static_assert(CPL >= 1 && CPL * EPC * 64 == COLS, "tile shape");
+    static constexpr int NQ = PREC == QT_Q4 ? NR : 1, CQ = PREC == QT_Q4 ? CPL : 1;
     uint4 w[NR][CPL];
     float rs[NR];
+    uint32_t bs[NQ][CQ];
 
-    __device__ __forceinline__ void load(const uint8_t *W, const float *S, int row0w) {
+    // S: int8 row scales (float) or q4 block-scale halves (uint16_t), per precision
+    __device__ __forceinline__ void load(const uint8_t *W, const void *S, int row0w) {
         const int lane = threadIdx.x & 63;
         W = uni(W);
-        if (PREC == QT_INT8) S = uni(S);
 #pragma unroll
         for (int r = 0; r < NR; r++)
 #pragma unroll
             for (int j = 0; j < CPL; j++)
                 w[r][j] = ldg(reinterpret_cast<const uint4 *>(W + (size_t)(row0w + r) * RB + (size_t)(lane + 64 * j) * 16));
+        if constexpr (PREC == QT_INT8) {
+            const float *Sf = uni(static_cast<const float *>(S));
 #pragma unroll
-        for (int r = 0; r < NR; r++) rs[r] = PREC == QT_INT8 ? ldg(S + row0w + r) : 1.0f;
+            for (int r = 0; r < NR; r++) rs[r] = ldg(Sf + row0w + r);
+        } else {
+#pragma unroll
+            for (int r = 0; r < NR; r++) rs[r] = 1.0f;
+        }
+        if constexpr (PREC == QT_Q4) {
+            const uint16_t *Sh = uni(static_cast<const uint16_t *>(S));
+#pragma unroll
+            for (int r = 0; r < NR; r++)
+#pragma unroll
+                for (int j = 0; j < CPL; j++) bs[r][j] = ldg(Sh + (size_t)(row0w + r) * (COLS / 32) + lane + 64 * j);
+        }
     }
 };
 
-// acc[r] = dot(row r, x) for the tile's rows (bf16 weights; int8 projections use the
-// exact pieces below), x read from LDS chunk by chunk (so no activation slice occupies
+// scale pointer of projection i in the form this precision's tiles take
+template <int PREC>
+__device__ __forceinline__ const void *lsc(const Layer &ly, int i) {
+    return PREC == QT_Q4 ? static_cast<const void *>(ly.s16[i]) : static_cast<const void *>(ly.s[i]);
+}
+
+// acc[r] = dot(row r, x) for the tile's rows (bf16 or q4_0 weights; int8 projections use
+// the exact pieces below), x read from LDS chunk by chunk (so no activation slice occupies
 // registers), reduced over the wave (valid in every lane).  Same arithmetic, in the same
-// order, as k_mv in qt_matvec.hip.
+// order, as k_mv in qt_matvec.hip: q4_0 chunk = one block, dot = d * (sum q*x - 8 sum x)
+// with the nibbles in storage order (word m: elements 8m..8m+7, even ones low).
 template <int PREC, int COLS, int NR>
 __device__ __forceinline__ void tile_dot(const Tile<PREC, COLS, NR> &t, const float *x, float (&acc)[NR]) {
-    static_assert(PREC == QT_BF16, "int8 projections take the exact activation pieces");
+    static_assert(PREC != QT_INT8, "int8 projections take the exact activation pieces");
     using T = Tile<PREC, COLS, NR>;
     constexpr int EPC = T::EPC;
     const int lane = threadIdx.x & 63;
@@ -309,13 +333,45 @@ __device__ __forceinline__ void tile_dot(const Tile<PREC, COLS, NR> &t, const fl
             const float4 v = xchunk4<EPC, COLS>(x, ci, q);
             xv[4 * q] = v.x; xv[4 * q + 1] = v.y; xv[4 * q + 2] = v.z; xv[4 * q + 3] = v.w;
         }
+        if constexpr (PREC == QT_Q4) {
+            float xr[32];
 #pragma unroll
-        for (int r = 0; r < NR; r++) {
-            const uint32_t w4[4] = {t.w[r][j].x, t.w[r][j].y, t.w[r][j].z, t.w[r][j].w};
+            for (int m = 0; m < 4; m++)
 #pragma unroll
-            for (int m = 0; m < 4; m++) {
-                s[r] = fmaf(bf_lo(w4[m]), xv[2 * m], s[r]);
-                s[r] = fmaf(bf_hi(w4[m]), xv[2 * m + 1], s[r]);
+                for (int b = 0; b < 4; b++) {
+                    xr[m * 4 + b] = xv[8 * m + 2 * b];
+                    xr[16 + m * 4 + b] = xv[8 * m + 2 * b + 1];
+                }
+            float xsum = 0.f;
+#pragma unroll
+            for (int e = 0; e < 32; e++) xsum += xr[e];
+#pragma unroll
+            for (int r = 0; r < NR; r++) {
+                const uint32_t w4[4] = {t.w[r][j].x, t.w[r][j].y, t.w[r][j].z, t.w[r][j].w};
+                float u = 0.f;
+#pragma unroll
+                for (int m = 0; m < 4; m++) {
+                    const uint32_t lo = w4[m] & 0x0F0F0F0Fu, hi = (w4[m] >> 4) & 0x0F0F0F0Fu;
+                    u = fmaf((float)(lo & 0xFFu), xr[m * 4 + 0], u);
+                    u = fmaf((float)((lo >> 8) & 0xFFu), xr[m * 4 + 1], u);
+                    u = fmaf((float)((lo >> 16) & 0xFFu), xr[m * 4 + 2], u);
+                    u = fmaf((float)(lo >> 24), xr[m * 4 + 3], u);
+                    u = fmaf((float)(hi & 0xFFu), xr[16 + m * 4 + 0], u);
+                    u = fmaf((float)((hi >> 8) & 0xFFu), xr[16 + m * 4 + 1], u);
+                    u = fmaf((float)((hi >> 16) & 0xFFu), xr[16 + m * 4 + 2], u);
+                    u = fmaf((float)(hi >> 24), xr[16 + m * 4 + 3], u);
+                }
+                s[r] = fmaf(ref_f16_to_f32(t.bs[r][j]), fmaf(-8.0f, xsum, u), s[r]);
+            }
+        } else {
+#pragma unroll
+            for (int r = 0; r < NR; r++) {
+                const uint32_t w4[4] = {t.w[r][j].x, t.w[r][j].y, t.w[r][j].z, t.w[r][j].w};
+#pragma unroll
+                for (int m = 0; m < 4; m++) {
+                    s[r] = fmaf(bf_lo(w4[m]), xv[2 * m], s[r]);
+                    s[r] = fmaf(bf_hi(w4[m]), xv[2 * m + 1], s[r]);
+                }
             }
         }
     }
@@ -516,7 +572,8 @@ struct TileM4 {
     static_assert(S * 256 == COLS, "tile shape");
     uint4 w[S];
     float rs[2];
-    __device__ __forceinline__ void load(const uint8_t *W, const float *Sc, int row0w) {
+    __device__ __forceinline__ void load(const uint8_t *W, const void *Sv, int row0w) {
+        const float *Sc = static_cast<const float *>(Sv);   // int8 row scales
         const int lane = threadIdx.x & 63, m = lane & 15, kg = lane >> 4;
         W = uni(W);
         const uint8_t *p = W + (size_t)(row0w + (m & 3)) * COLS + (m >> 2) * 64 + kg * 16;
@@ -592,7 +649,8 @@ struct TileK8 {
     static_assert(S * 512 == COLS, "tile shape");
     uint4 w[S];
     float rs;                // lane t < 8: scale of row row0 + t
-    __device__ __forceinline__ void load(const uint8_t *W, const float *Sc, int row0, int wave) {
+    __device__ __forceinline__ void load(const uint8_t *W, const void *Sv, int row0, int wave) {
+        const float *Sc = static_cast<const float *>(Sv);   // int8 row scales
         const int lane = threadIdx.x & 63, m = lane & 15, kg = lane >> 4;
         W = uni(W);
         const uint8_t *p = W + (size_t)(row0 + (m & 7)) * COLS + wave * (COLS / 4) + (m >> 3) * 64 + kg * 16;
@@ -743,7 +801,7 @@ __global__ __launch_bounds__(NW * 64, 1) void k_pstep(Args a) {
     __syncthreads();
 
     TQKV tq;
-    tq.load(s_layers[0].w[0], s_layers[0].s[0], rw_qkv);
+    tq.load(s_layers[0].w[0], lsc<PREC>(s_layers[0], 0), rw_qkv);
     load_gains<NW, EP, H>(s_layers[0].in_norm, s_gain[0]);
 
 
@@ -841,9 +899,9 @@ __global__ __launch_bounds__(NW * 64, 1) void k_pstep(Args a) {
             // next operands (issued after this phase's output): W_o, first gate|up piece, post-norm gains
             TO to;
             if constexpr (MF) to.load(ly.w[1], ly.s[1], b * (H / NB), wave);
-            else to.load(ly.w[1], ly.s[1], rw_o);
+            else to.load(ly.w[1], lsc<PREC>(ly, 1), rw_o);
             TGU tg0, tg1, tg2;
-            tg0.load(ly.w[2], ly.s[2], rw_gu);
+            tg0.load(ly.w[2], lsc<PREC>(ly, 2), rw_gu);
             load_gains<NW, EP, H>(ly.post_norm, s_gain[1]);
             PS_MARK(ph, 1); ph++;
 
@@ -937,7 +995,7 @@ __global__ __launch_bounds__(NW * 64, 1) void k_pstep(Args a) {
                     __hip_atomic_store(vd + lane, vv, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                 }
             }
-            tg1.load(ly.w[2], ly.s[2], rw_gu + RGU);
+            tg1.load(ly.w[2], lsc<PREC>(ly, 2), rw_gu + RGU);
             PS_MARK(ph, 1); ph++;
 
             // ---------------- M: merge 8 attention outputs -----------------
@@ -960,7 +1018,7 @@ __global__ __launch_bounds__(NW * 64, 1) void k_pstep(Args a) {
                     if (cc == 0) st_tag(blk + R::OATT + (2 * g + hh) * HD + d0 + dd, r, tag);
                 }
             }
-            tg2.load(ly.w[2], ly.s[2], rw_gu + 2 * RGU);
+            tg2.load(ly.w[2], lsc<PREC>(ly, 2), rw_gu + 2 * RGU);
             PS_MARK(ph, 1); ph++;
 
             // ---------------- C: xa = x + W_o . attn -----------------
@@ -1000,7 +1058,7 @@ __global__ __launch_bounds__(NW * 64, 1) void k_pstep(Args a) {
             }
             TDN td;
             if constexpr (MF) td.load(ly.w[3], ly.s[3], b * (H / NB), wave);
-            else td.load(ly.w[3], ly.s[3], rw_dn);
+            else td.load(ly.w[3], lsc<PREC>(ly, 3), rw_dn);
             PS_MARK(ph, 1); ph++;
 
             // ---------------- D: h = SwiGLU(W_gu . RMSNorm(xa)) -----------------
@@ -1070,7 +1128,7 @@ __global__ __launch_bounds__(NW * 64, 1) void k_pstep(Args a) {
             }
             PS_MARK(ph, 3);
             if (l + 1 < L) {
-                tq.load(s_layers[l + 1].w[0], s_layers[l + 1].s[0], rw_qkv);
+                tq.load(s_layers[l + 1].w[0], lsc<PREC>(s_layers[l + 1], 0), rw_qkv);
                 load_gains<NW, EP, H>(s_layers[l + 1].in_norm, s_gain[0]);
             }
             PS_MARK(ph, 1); ph++;
@@ -1168,7 +1226,7 @@ __global__ __launch_bounds__(NW * 64, 1) void k_pstep(Args a) {
                 st_tag(slots + 2 * b + 1, __int_as_float(bi), tag);
             }
             if (!last_step) {
-                tq.load(s_layers[0].w[0], s_layers[0].s[0], rw_qkv);
+                tq.load(s_layers[0].w[0], lsc<PREC>(s_layers[0], 0), rw_qkv);
                 load_gains<NW, EP, H>(s_layers[0].in_norm, s_gain[0]);
             }
             PS_MARK(ph, 1); ph++;
@@ -1232,8 +1290,9 @@ static hipError_t ps_launch(const ps::Args &a, hipStream_t st) {
 extern "C" int qt_pstep_supported(int prec, int hidden, int inter, int n_heads, int n_kv, int head_dim, int kv_max) {
     if (n_heads != ps::NH || n_kv != ps::NKV || head_dim != ps::HD) return 0;
     if (kv_max > ps::G * ps::CHMAX) return 0;
-    if (prec != QT_BF16 && prec != QT_INT8) return 0;
+    if (prec != QT_BF16 && prec != QT_INT8 && prec != QT_Q4) return 0;
     if (!((hidden == 1024 && inter == 3072) || (hidden == 2048 && inter == 6144))) return 0;
+    if (prec == QT_Q4 && hidden != 2048) return 0;   // a q4 chunk is 32 columns: 64 lanes need 2048
     int dev = 0, cus = 0, coop = 0;
     if (hipGetDevice(&dev) != hipSuccess) return 0;
     if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
@@ -1280,5 +1339,6 @@ extern "C" hipError_t qt_launch_pstep(int prec, int hidden, const void *layers_d
     if (prec == QT_INT8 && hidden == 1024) return ps_launch<QT_INT8, 1024, 3072>(a, st);
     if (prec == QT_BF16 && hidden == 2048) return ps_launch<QT_BF16, 2048, 6144>(a, st);
     if (prec == QT_BF16 && hidden == 1024) return ps_launch<QT_BF16, 1024, 3072>(a, st);
+    if (prec == QT_Q4 && hidden == 2048) return ps_launch<QT_Q4, 2048, 6144>(a, st);
     return hipErrorInvalidValue;
 }

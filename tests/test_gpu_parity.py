@@ -137,10 +137,12 @@ def test_quantize_q4_vs_reference():
 # ------------------------------------------------------------------------- Talker step
 
 @need_ref
-@pytest.mark.parametrize("prec", ["bf16", "int8", "int4"])
-def test_talker_steps_vs_reference(prec):
-    print(f"[case] talker mini {prec}", flush=True)
-    ref, shape, _ = _ref("mini", prec)
+@pytest.mark.parametrize("name,prec", [("mini", "bf16"), ("mini", "int8"), ("mini", "int4"), ("mini17", "int4")])
+def test_talker_steps_vs_reference(name, prec):
+    """mini17 int4 runs the fused step with q4_0 tiles (hidden 2048); mini int4 the
+    per-kernel path."""
+    print(f"[case] talker {name} {prec}", flush=True)
+    ref, shape, _ = _ref(name, prec)
     pc = hip.PREC[prec]
     g = _gpu_talker(ref, shape, pc)
     emb = ref.codec_emb()
@@ -223,7 +225,8 @@ def test_upload_kv_roundtrip_and_resume():
 
 
 @need_ref
-@pytest.mark.parametrize("name,prec", [("mini", "bf16"), ("mini", "int8"), ("mini17", "bf16"), ("mini17", "int8")])
+@pytest.mark.parametrize("name,prec", [("mini", "bf16"), ("mini", "int8"), ("mini17", "bf16"), ("mini17", "int8"),
+                                       ("mini17", "int4")])
 def test_fused_step_matches_kernel_sequence(name, prec):
     """The default step (one persistent kernel, or the captured graph where that is
     unavailable) against the plain launch sequence: same per-row arithmetic (int8: the
@@ -298,9 +301,10 @@ def test_dequant_bitexact(oracle, prec):
 
 
 @need_ref
-@pytest.mark.parametrize("prec", ["bf16", "int8"])
-def test_greedy_tokens_match_reference(prec):
-    ref, shape, _ = _ref("mini", prec)
+@pytest.mark.parametrize("name,prec", [("mini", "bf16"), ("mini", "int8"), ("mini17", "int4")])
+def test_greedy_tokens_match_reference(name, prec):
+    print(f"[case] greedy {name} {prec}", flush=True)
+    ref, shape, _ = _ref(name, prec)
     pc = hip.PREC[prec]
     g = _gpu_talker(ref, shape, pc)
     emb = ref.codec_emb()
