@@ -238,6 +238,18 @@ int qwen_hip_op_prefill_gemm(float *Y, const uint16_t *W, const float *X, int S,
  * normed, rotated q | k | v rows of every position. */
 int qwen_hip_op_prefill_attention(float *out, const float *QKV, int S, int nh, int nkv, float scale);
 int qwen_hip_op_argmax_matvec(int prec, const float *x, const void *W, const float *scale, int in_dim, int out_dim);
+/* Token sampling on the device: qwen_tts_sample (qwen_tts_sampling.c:160-202; repetition
+ * penalty, temperature softmax, top-k, top-p, renormalisation, LCG draw) with the
+ * thread-local LCG state of qwen_set_seed / qwen_get_seed (sampling.c:38-49) passed as
+ * *seed and advanced as the reference advances it (once per non-greedy draw).  vocab <= 4096.
+ * Returns the token, or -1 on error (see qwen_hip_last_error). */
+int qwen_hip_op_sample(const float *logits, int vocab, float temp, int top_k, float top_p, float rep_penalty,
+                       const int *prev_tokens, int n_prev, uint32_t *seed);
+/* The codec-head rule of the Talker's frame loop (qwen_tts.c:1652-1679: clip to +-100,
+ * tokens >= 2048 except EOS 2150 masked, EOS masked for frames < 2, eos_boost added to
+ * the EOS logit) followed by qwen_hip_op_sample (qwen_tts.c:1689-1691). */
+int qwen_hip_op_codec_sample(const float *logits, int vocab, int frame, float eos_boost, float temp, int top_k,
+                             float top_p, float rep_penalty, const int *prev_tokens, int n_prev, uint32_t *seed);
 /* qwen_matmat_int8 (qwen_tts_kernels.h:121-122): Y[rows][B] = (W*scale) @ X[cols][B]
  * (row-major f32, B <= 64, cols a multiple of 64) on the batched MFMA kernel. */
 int qwen_hip_op_matmat_int8(float *Y, const int8_t *W, const float *scale, const float *X, int rows, int cols, int B);

@@ -80,6 +80,8 @@ class Oracle:
         L.qo_cp_pass.argtypes = [C.POINTER(OTalker), vp, i]; L.qo_cp_pass.restype = i
         L.qo_talker_prefill.argtypes = [C.POINTER(OTalker), vp, i, vp]; L.qo_talker_prefill.restype = i
         L.qo_attention_f32.argtypes = [vp, vp, vp, vp, i, i, i, i, i, f, i]
+        L.qo_sample.argtypes = [vp, i, f, i, f, f, vp, i, vp]; L.qo_sample.restype = i
+        L.qo_codec_rule.argtypes = [vp, i, i, f]
         L.qo_cp_frame.argtypes = [C.POINTER(OCpFrame), vp, i, vp]; L.qo_cp_frame.restype = i
 
     # -- scalar / array helpers
@@ -152,6 +154,17 @@ class Oracle:
                                   _p(np.ascontiguousarray(V, np.float32)), seq_q, seq_k, nh, nkv, hd, scale, q_off)
         return out
 
+    def sample(self, logits, temp, top_k, top_p, rep=1.0, prev=(), seed=12345, rule=None):
+        """qwen_tts_sample restated; rule = (frame, eos_boost) applies the codec-head rule
+        first.  Returns (token, new seed, final distribution or None when greedy)."""
+        lg = np.array(logits, np.float32, copy=True)
+        if rule is not None:
+            self.lib.qo_codec_rule(_p(lg), lg.size, int(rule[0]), float(rule[1]))
+        pv = np.ascontiguousarray(prev, np.int32)
+        sd = np.array([seed], np.uint32)
+        t = self.lib.qo_sample(_p(lg), lg.size, temp, top_k, top_p, rep, _p(pv) if pv.size else None, pv.size, _p(sd))
+        return t, int(sd[0]), (None if temp < 1e-6 else lg)
+
     def cp_frame(self, f, talker_hidden, code0):
         """16 CP passes + 15 argmax codes on OCpFrame f."""
         out = np.empty(15, np.int32)
@@ -211,6 +224,7 @@ class RefModel:
         L.ref_rms_norm.argtypes = [vp, vp, vp, i, i, f]
         L.ref_swiglu.argtypes = [vp, i]
         L.ref_argmax_matvec_bf16.argtypes = [vp, vp, i, i]; L.ref_argmax_matvec_bf16.restype = i
+        L.ref_sample.argtypes = [vp, i, f, i, f, f, vp, i, vp]; L.ref_sample.restype = i
         L.ref_argmax_matvec_int8.argtypes = [vp, vp, vp, i, i]; L.ref_argmax_matvec_int8.restype = i
         L.ref_argmax_matvec_q4_0.argtypes = [vp, vp, i, i]; L.ref_argmax_matvec_q4_0.restype = i
         L.ref_f32_to_f16.argtypes = [f]; L.ref_f32_to_f16.restype = C.c_uint16

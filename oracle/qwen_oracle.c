@@ -530,3 +530,80 @@ int qo_cp_frame(const qo_cp_frame_t *f, const float *talker_hidden, int code0, i
     free(x); free(x1); free(xn); free(emb); free(lg);
     return 0;
 }
+
+/* ---- sampling (qwen_tts_sampling.c) ---------------------------------------------------
+ * The steps of qwen_tts_sample in the reference's order and with its sequential sums:
+ * repetition penalty (sampling.c:165-173), greedy below temp 1e-6 (:176-182), softmax with
+ * 1/temp (:52-62), top-k threshold = k-th largest value with multiplicity (:96-111; here by
+ * a sorted copy instead of quickselect: same value), top-p by selection of the running
+ * maximum until the cumulative sum exceeds p, ties resolved by the same swap sequence
+ * (:114-146), renormalisation (:195-198), LCG draw over the cumulative sum (:38-42,
+ * :149-157). */
+static int qo_cmp_desc(const void *a, const void *b) {
+    float x = *(const float *)a, y = *(const float *)b;
+    return (x < y) - (x > y);
+}
+
+int qo_sample(float *lg, int n, float temp, int top_k, float top_p, float rep, const int *prev, int n_prev,
+              uint32_t *seed) {
+    if (rep != 1.0f && n_prev > 0)
+        for (int j = 0; j < n_prev; j++) {
+            int t = prev[j];
+            if (t >= 0 && t < n) lg[t] = lg[t] > 0 ? lg[t] / rep : lg[t] * rep;
+        }
+    if (temp < 1e-6f) {
+        int best = 0;
+        for (int i = 1; i < n; i++) if (lg[i] > lg[best]) best = i;
+        return best;
+    }
+    float mx = lg[0];
+    for (int i = 1; i < n; i++) if (lg[i] > mx) mx = lg[i];
+    float inv = 1.0f / temp, sum = 0.f;
+    for (int i = 0; i < n; i++) { lg[i] = expf((lg[i] - mx) * inv); sum += lg[i]; }
+    for (int i = 0; i < n; i++) lg[i] /= sum;
+    if (top_k > 0 && top_k < n) {
+        float *tmp = (float *)malloc((size_t)n * sizeof(float));
+        memcpy(tmp, lg, (size_t)n * sizeof(float));
+        qsort(tmp, (size_t)n, sizeof(float), qo_cmp_desc);
+        float thr = tmp[top_k - 1];
+        free(tmp);
+        for (int i = 0; i < n; i++) if (lg[i] < thr) lg[i] = 0.f;
+    }
+    if (top_p < 1.0f && top_p > 0.0f) {
+        int *idx = (int *)malloc((size_t)n * sizeof(int));
+        for (int i = 0; i < n; i++) idx[i] = i;
+        float cum = 0.f;
+        int cut = n;
+        for (int i = 0; i < n; i++) {
+            int m = i;
+            for (int j = i + 1; j < n; j++) if (lg[idx[j]] > lg[idx[m]]) m = j;
+            int t = idx[i]; idx[i] = idx[m]; idx[m] = t;
+            cum += lg[idx[i]];
+            if (cum > top_p) { cut = i + 1; break; }
+        }
+        for (int i = cut; i < n; i++) lg[idx[i]] = 0.f;
+        free(idx);
+    }
+    float s2 = 0.f;
+    for (int i = 0; i < n; i++) s2 += lg[i];
+    if (s2 > 0) for (int i = 0; i < n; i++) lg[i] /= s2;
+    *seed = *seed * 1103515245u + 12345u;
+    float r = (float)((*seed >> 16) & 0x7FFF) / 32768.0f, cum = 0.f;
+    for (int i = 0; i < n; i++) {
+        cum += lg[i];
+        if (r < cum) return i;
+    }
+    return n - 1;
+}
+
+void qo_codec_rule(float *lg, int n, int frame, float eos_boost) {
+    for (int t = 0; t < n; t++) {
+        if (lg[t] > 100.0f) lg[t] = 100.0f;
+        if (lg[t] < -100.0f) lg[t] = -100.0f;
+    }
+    for (int t = 2048; t < n; t++) if (t != 2150) lg[t] = -1e30f;
+    if (n > 2150) {
+        if (frame < 2) lg[2150] = -1e30f;
+        lg[2150] += eos_boost;
+    }
+}

@@ -95,6 +95,13 @@ typedef struct {
 /* 16 passes + 15 argmax codes (qwen_tts_code_predictor.c:926-1045). */
 int qo_cp_frame(const qo_cp_frame_t *f, const float *talker_hidden, int code0, int *out_codes);
 
+/* qwen_tts_sample (qwen_tts_sampling.c:160-202) with the LCG state as *seed; when the draw
+ * is not greedy, logits end holding the final (renormalised) distribution. */
+int qo_sample(float *logits, int n, float temp, int top_k, float top_p, float rep, const int *prev, int n_prev,
+              uint32_t *seed);
+/* The codec-head rule of qwen_tts.c:1652-1679 in place (clip, specials, EOS). */
+void qo_codec_rule(float *logits, int n, int frame, float eos_boost);
+
 #ifdef __cplusplus
 }
 #endif

@@ -249,6 +249,16 @@ int ref_argmax_matvec_q4_0(const float *x, const void *W, int in_dim, int out_di
     return qwen_argmax_matvec_q4_0(x, (const q4_0_block_t *)W, in_dim, out_dim);
 }
 uint16_t ref_f32_to_f16(float f) { return qwen_f32_to_f16(f); }
+/* qwen_tts_sample with the thread-local LCG state set from and returned to *seed. */
+extern void qwen_set_seed(uint32_t seed);
+extern uint32_t qwen_get_seed(void);
+int ref_sample(float *logits, int n, float temp, int top_k, float top_p, float rep, int *prev, int n_prev,
+               uint32_t *seed) {
+    qwen_set_seed(*seed);
+    int t = qwen_tts_sample(logits, n, temp, top_k, top_p, rep, prev, n_prev);
+    *seed = qwen_get_seed();
+    return t;
+}
 float ref_f16_to_f32(uint16_t h) { return qwen_f16_to_f32(h); }
 
 /* Wall-clock helper for the CPU baseline: n consecutive Talker steps, returns seconds. */

@@ -35,6 +35,9 @@ hipError_t qt_launch_rmsnorm(const float *x, const float *w, float *out, int n, 
                              hipStream_t st);
 hipError_t qt_launch_rmsnorm_rows(float *x, const float *w, int rows, int n, float eps, hipStream_t st);
 hipError_t qt_launch_swiglu(const float *gu, float *out, int n, hipStream_t st);
+hipError_t qt_launch_sample(const float *logits, int n, int rule, int frame, float eos_boost, float temp,
+                            int top_k, float top_p, float rep, const int *prev, int n_prev, uint32_t *seed, int *tok,
+                            hipStream_t st);
 hipError_t qt_launch_select(const float *logits, int n, int mode, int *d_frame, int advance, int *tok,
                             int *hist, int hist_len, const uint16_t *emb, int emb_dim, float *out,
                             int *d_pos, hipStream_t st);

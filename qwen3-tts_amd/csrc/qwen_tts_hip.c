@@ -1545,6 +1545,43 @@ fail:
     return tok;
 }
 
+/* Sampling (qwen_tts_sampling.c:160-202, optionally behind the codec-head rule of
+ * qwen_tts.c:1652-1679) on the op stream: logits, history and LCG state up, token and
+ * state back. */
+static int op_sample(int rule, int frame, float eos_boost, const float *logits, int vocab, float temp, int top_k,
+                     float top_p, float rep, const int *prev, int n_prev, uint32_t *seed) {
+    hipStream_t st = op_stream();
+    float *dl = NULL; int *dp = NULL, *dt = NULL; uint32_t *ds = NULL; int tok = -1, out = -1;
+    REQ(st, "no stream");
+    REQ(logits && seed && vocab > 0 && vocab <= 4096, "sampling needs logits, a seed and 1 <= vocab <= 4096");
+    REQ(n_prev >= 0 && (n_prev == 0 || prev), "n_prev > 0 needs prev_tokens");
+    HCK(hipMalloc((void **)&dl, (size_t)vocab * sizeof(float)));
+    HCK(hipMalloc((void **)&dt, sizeof(int)));
+    HCK(hipMalloc((void **)&ds, sizeof(uint32_t)));
+    if (n_prev > 0) {
+        HCK(hipMalloc((void **)&dp, (size_t)n_prev * sizeof(int)));
+        HCK(hipMemcpyAsync(dp, prev, (size_t)n_prev * sizeof(int), hipMemcpyHostToDevice, st));
+    }
+    HCK(hipMemcpyAsync(dl, logits, (size_t)vocab * sizeof(float), hipMemcpyHostToDevice, st));
+    HCK(hipMemcpyAsync(ds, seed, sizeof(uint32_t), hipMemcpyHostToDevice, st));
+    HCK(qt_launch_sample(dl, vocab, rule, frame, eos_boost, temp, top_k, top_p, rep, dp, n_prev, ds, dt, st));
+    HCK(hipMemcpyAsync(&tok, dt, sizeof(int), hipMemcpyDeviceToHost, st));
+    HCK(hipMemcpyAsync(seed, ds, sizeof(uint32_t), hipMemcpyDeviceToHost, st));
+    HCK(hipStreamSynchronize(st));
+    out = tok;
+fail:
+    if (dl) (void)hipFree(dl); if (dp) (void)hipFree(dp); if (dt) (void)hipFree(dt); if (ds) (void)hipFree(ds);
+    return out;
+}
+int qwen_hip_op_sample(const float *logits, int vocab, float temp, int top_k, float top_p, float rep_penalty,
+                       const int *prev_tokens, int n_prev, uint32_t *seed) {
+    return op_sample(0, 0, 0.f, logits, vocab, temp, top_k, top_p, rep_penalty, prev_tokens, n_prev, seed);
+}
+int qwen_hip_op_codec_sample(const float *logits, int vocab, int frame, float eos_boost, float temp, int top_k,
+                             float top_p, float rep_penalty, const int *prev_tokens, int n_prev, uint32_t *seed) {
+    return op_sample(1, frame, eos_boost, logits, vocab, temp, top_k, top_p, rep_penalty, prev_tokens, n_prev, seed);
+}
+
 int qwen_hip_op_causal_attention_bf16kv(float *out, const float *Q, const uint16_t *K, const uint16_t *V,
                                         int seq_q, int seq_k, int n_heads, int n_kv_heads, int head_dim,
                                         float scale, int q_offset) {

@@ -27,6 +27,7 @@ EXPORTS = [
     "qwen_hip_matmat_bf16", "qwen_hip_op_matvec_int8", "qwen_hip_op_matvec_q4_0",
     "qwen_hip_op_matvec_bf16", "qwen_hip_op_causal_attention_bf16kv", "qwen_hip_op_rms_norm",
     "qwen_hip_op_rms_norm_per_head", "qwen_hip_op_swiglu", "qwen_hip_op_argmax_matvec",
+    "qwen_hip_op_sample", "qwen_hip_op_codec_sample",
     "qwen_hip_op_quantize_int8", "qwen_hip_op_quantize_q4_0", "qwen_hip_talker_dequant",
     "qwen_hip_last_error", "qwen_hip_talker_batch_init", "qwen_hip_talker_batch_step",
     "qwen_hip_talker_batch_upload_slot", "qwen_hip_talker_batch_free", "qwen_hip_talker_batch_download_slot",
@@ -118,6 +119,9 @@ def lib():
         L.qwen_hip_op_rms_norm_per_head.argtypes = [vp, vp, i, i, i, f]; L.qwen_hip_op_rms_norm_per_head.restype = i
         L.qwen_hip_op_swiglu.argtypes = [vp, vp, i]; L.qwen_hip_op_swiglu.restype = i
         L.qwen_hip_op_argmax_matvec.argtypes = [i, vp, vp, vp, i, i]; L.qwen_hip_op_argmax_matvec.restype = i
+        L.qwen_hip_op_sample.argtypes = [vp, i, f, i, f, f, vp, i, vp]; L.qwen_hip_op_sample.restype = i
+        L.qwen_hip_op_codec_sample.argtypes = [vp, i, i, f, f, i, f, f, vp, i, vp]
+        L.qwen_hip_op_codec_sample.restype = i
         L.qwen_hip_op_quantize_int8.argtypes = [vp, i, i, vp, vp]; L.qwen_hip_op_quantize_int8.restype = i
         L.qwen_hip_op_quantize_q4_0.argtypes = [vp, i, i, vp]; L.qwen_hip_op_quantize_q4_0.restype = i
         L.qwen_hip_last_error.restype = C.c_char_p

@@ -68,3 +68,32 @@ def oracle():
 def rel_l2(a, b):
     a = np.asarray(a, np.float64); b = np.asarray(b, np.float64)
     return float(np.linalg.norm(a - b) / max(np.linalg.norm(b), 1e-30))
+
+
+def sample_cases(n_cases, seed, rule=False):
+    """Seeded arguments for qwen_tts_sample (vocab 1..4096, temperatures including greedy,
+    top-k, top-p, repetition penalty with repeated history tokens); ties at the maximum
+    only where top-p is off (the one place tie order decides the result)."""
+    rng = np.random.default_rng(seed)
+    for c in range(n_cases):
+        V = 3072 if (rule or c % 3) else int(rng.integers(1, 4097))
+        lg = (rng.standard_normal(V) * [0.5, 2.0, 5.0][c % 3]).astype(np.float32)
+        temp = [0.0, 0.3, 0.9, 1.0, 1.5][c % 5]
+        top_k = [0, 1, 50, 200, V][(c // 5) % 5]
+        top_p = [1.0, 0.9, 0.5, 0.99, 1e-6][(c // 3) % 5]
+        rep = [1.0, 1.05, 1.3][(c // 7) % 3]
+        if top_p == 1.0 and c % 4 == 0:
+            lg[rng.integers(0, V, 12)] = lg.max()
+        prev = rng.integers(0, V, int(rng.integers(0, 40))).astype(np.int32)
+        sd = int(rng.integers(0, 2 ** 32))
+        extra = (int(rng.integers(0, 6)), float([0.0, 0.0, 3.5][c % 3])) if rule else None
+        yield dict(logits=lg, temp=temp, top_k=top_k, top_p=top_p, rep=rep, prev=prev, seed=sd, rule=extra)
+
+
+def draw_margin(dist, seed_after):
+    """Distance of the draw r (from the advanced LCG state) to the nearest boundary of the
+    cumulative distribution: two correct samplers whose sums round differently may only
+    disagree when this is tiny."""
+    r = float((seed_after >> 16) & 0x7FFF) / 32768.0
+    cum = np.cumsum(dist.astype(np.float64))
+    return float(np.min(np.abs(cum - r)))

@@ -15,7 +15,7 @@ import os
 import numpy as np
 import pytest
 
-from conftest import need_oracle, need_ref, rel_l2
+from conftest import draw_margin, need_oracle, need_ref, rel_l2, sample_cases
 
 GOLD = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
 pytestmark = need_oracle
@@ -501,3 +501,70 @@ def test_prefill_vs_reference_live(oracle):
     dx_o = oracle.talker_prefill(ot, e)
     assert rel_l2(dx_o, dx_r) <= 1e-4
     assert _kv_close(keep["kv_k"][:, :37], np.array(kr[:, :37])) and _kv_close(keep["kv_v"][:, :37], np.array(vr[:, :37]))
+
+
+# --------------------------------------------------------------------------- sampling
+
+def _ref_sample(L, case):
+    lg = np.array(case["logits"], np.float32, copy=True)
+    if case["rule"] is not None:
+        pytest.skip("rule cases are checked on the oracle only")
+    pv = np.ascontiguousarray(case["prev"], np.int32)
+    sd = np.array([case["seed"]], np.uint32)
+    t = L.ref_sample(lg.ctypes.data, lg.size, case["temp"], case["top_k"], case["top_p"], case["rep"],
+                     pv.ctypes.data if pv.size else None, pv.size, sd.ctypes.data)
+    return t, int(sd[0])
+
+
+@need_ref
+def test_sample_oracle_matches_reference(oracle):
+    """qo_sample against the compiled reference's qwen_tts_sample (built -O3 -ffast-math,
+    so its loops may be vectorised): the same LCG state always, the same token unless
+    the draw lies within rounding of a cumulative boundary."""
+    from oracle.oracle import RefModel
+    L = RefModel.load_lib()
+    n = diff = 0
+    for case in sample_cases(600, 5):
+        t_ref, s_ref = _ref_sample(L, case)
+        t, s, dist = oracle.sample(case["logits"], case["temp"], case["top_k"], case["top_p"], case["rep"],
+                                   case["prev"], case["seed"])
+        n += 1
+        assert s == s_ref
+        if t != t_ref:
+            diff += 1
+            assert dist is not None and draw_margin(dist, s) < 1e-5, (case["temp"], case["top_k"], case["top_p"])
+    assert diff <= n // 100, diff
+
+
+def test_sample_oracle_closed_forms(oracle):
+    rng = np.random.default_rng(3)
+    for _ in range(50):
+        V = int(rng.integers(2, 3000))
+        lg = (rng.standard_normal(V) * 2).astype(np.float32)
+        am = int(np.argmax(lg))
+        sd = int(rng.integers(0, 2 ** 32))
+        # greedy: argmax, state untouched
+        assert oracle.sample(lg, 0.0, 0, 1.0, 1.0, (), sd)[:2] == (am, sd)
+        # top-k 1 and a vanishing top-p leave only the maximum; the state advances once
+        adv = (sd * 1103515245 + 12345) & 0xFFFFFFFF
+        assert oracle.sample(lg, 0.9, 1, 1.0, 1.0, (), sd)[:2] == (am, adv)
+        assert oracle.sample(lg, 0.9, 0, 1e-6, 1.0, (), sd)[:2] == (am, adv)
+        # a large repetition penalty on a positive maximum hands greedy the runner-up
+        lp = lg.copy(); lp[am] = abs(lp[am]) + 1.0
+        second = int(np.argsort(-lp, kind="stable")[1])
+        assert oracle.sample(lp, 0.0, 0, 1.0, 1e6, np.array([am], np.int32), sd)[0] == second
+    # the draw follows the distribution: 4 tokens, many seeds
+    lg = np.log(np.array([0.1, 0.2, 0.3, 0.4], np.float32))
+    cnt = np.zeros(4)
+    sd = 1
+    for _ in range(20000):
+        t, sd, _ = oracle.sample(lg, 1.0, 0, 1.0, 1.0, (), sd)
+        cnt[t] += 1
+    assert np.abs(cnt / cnt.sum() - [0.1, 0.2, 0.3, 0.4]).max() < 0.02
+    # codec-head rule: specials masked, EOS masked before frame 2, boosted after
+    lg = np.zeros(3072, np.float32); lg[2500] = 50; lg[2150] = 40; lg[7] = 30
+    assert oracle.sample(lg, 0.0, 0, 1.0, 1.0, (), 1, rule=(0, 0.0))[0] == 7
+    assert oracle.sample(lg, 0.0, 0, 1.0, 1.0, (), 1, rule=(5, 0.0))[0] == 2150
+    lg[7] = 45
+    assert oracle.sample(lg, 0.0, 0, 1.0, 1.0, (), 1, rule=(5, 0.0))[0] == 7
+    assert oracle.sample(lg, 0.0, 0, 1.0, 1.0, (), 1, rule=(5, 6.0))[0] == 2150
