@@ -243,6 +243,17 @@ int qwen_hip_op_argmax_matvec(int prec, const float *x, const void *W, const flo
  * thread-local LCG state of qwen_set_seed / qwen_get_seed (sampling.c:38-49) passed as
  * *seed and advanced as the reference advances it (once per non-greedy draw).  vocab <= 4096.
  * Returns the token, or -1 on error (see qwen_hip_last_error). */
+/* The Talker's frame loop with sampling on the device (qwen_tts.c:1649-1721 for code0):
+ * n_steps x (Talker step at pos + i, final norm + codec head, codec-head rule for frame
+ * frame0 + i, qwen_tts_sample with the repetition penalty over prev_tokens and the tokens
+ * drawn so far, next input codec_emb[token]).  Same head/embedding arguments as
+ * qwen_hip_talker_greedy; *seed is the LCG state in and out; tokens_out[n_steps], the last
+ * step's normed hidden state in hidden_out (may be NULL).  Afterwards the greedy loop must
+ * be re-seeded with qwen_hip_talker_greedy before qwen_hip_talker_greedy_async. */
+int qwen_hip_talker_sample(void *state, const uint16_t *codec_head, const uint16_t *codec_emb, int codec_vocab,
+                           const float *embed, int pos, int frame0, int n_steps, float temp, int top_k, float top_p,
+                           float rep_penalty, const int *prev_tokens, int n_prev, uint32_t *seed, int *tokens_out,
+                           float *hidden_out);
 int qwen_hip_op_sample(const float *logits, int vocab, float temp, int top_k, float top_p, float rep_penalty,
                        const int *prev_tokens, int n_prev, uint32_t *seed);
 /* The codec-head rule of the Talker's frame loop (qwen_tts.c:1652-1679: clip to +-100,

@@ -677,15 +677,10 @@ static hipError_t greedy_body(void *a) {
                             t->codec_emb, H, x, t->d_pos, t->st);
 }
 
-int qwen_hip_talker_greedy(void *state, const uint16_t *codec_head, const uint16_t *codec_emb, int codec_vocab,
-                           const float *embed, int pos, int frame0, int n_steps, int *tokens_out,
-                           float *hidden_out) {
-    talker_t *t = (talker_t *)state;
-    if (!t || t->dead) { SETERR("talker state is dead or NULL"); return -1; }
+/* codec head (bf16) and embedding table on the device, re-uploaded when the caller's
+ * arrays change */
+static int head_setup(talker_t *t, const uint16_t *codec_head, const uint16_t *codec_emb, int codec_vocab) {
     const int H = t->s.H;
-    REQ(codec_head && codec_emb && codec_vocab > 0, "missing codec head/embedding");
-    REQ(n_steps >= 0 && n_steps <= t->hist_len, "n_steps %d out of range", n_steps);
-    REQ(pos >= 0 && pos + n_steps <= t->s.kv_max && pos + n_steps <= t->s.rope_len, "positions exceed kv_max");
     if (t->head_host != codec_head || t->emb_host != codec_emb || t->codec_vocab != codec_vocab) {
         if (t->ggraph_ready) { (void)hipGraphExecDestroy(t->gexec); t->ggraph_ready = 0; }
         t->greedy_ready = 0;
@@ -701,6 +696,21 @@ int qwen_hip_talker_greedy(void *state, const uint16_t *codec_head, const uint16
         HCK(hipMalloc((void **)&t->logits, (size_t)codec_vocab * sizeof(float)));
         t->head_host = codec_head; t->emb_host = codec_emb; t->codec_vocab = codec_vocab;
     }
+    return 0;
+fail:
+    return -1;
+}
+
+int qwen_hip_talker_greedy(void *state, const uint16_t *codec_head, const uint16_t *codec_emb, int codec_vocab,
+                           const float *embed, int pos, int frame0, int n_steps, int *tokens_out,
+                           float *hidden_out) {
+    talker_t *t = (talker_t *)state;
+    if (!t || t->dead) { SETERR("talker state is dead or NULL"); return -1; }
+    const int H = t->s.H;
+    REQ(codec_head && codec_emb && codec_vocab > 0, "missing codec head/embedding");
+    REQ(n_steps >= 0 && n_steps <= t->hist_len, "n_steps %d out of range", n_steps);
+    REQ(pos >= 0 && pos + n_steps <= t->s.kv_max && pos + n_steps <= t->s.rope_len, "positions exceed kv_max");
+    if (head_setup(t, codec_head, codec_emb, codec_vocab) != 0) goto fail;
     if (talker_set_pos(t, pos) != 0) goto fail;
     t->h_pos[1] = frame0;
     HCK(hipMemcpyAsync(t->d_frame, t->h_pos + 1, sizeof(int), hipMemcpyHostToDevice, t->st));
@@ -735,6 +745,66 @@ int qwen_hip_talker_greedy(void *state, const uint16_t *codec_head, const uint16
     return 0;
 fail:
     if (t) { t->dead = 1; t->dev_pos = -1; }
+    return -1;
+}
+
+/* Sampled frame loop on the device (qwen_tts.c:1649-1721, code0 only): per step the Talker
+ * step, the final norm fused into the codec head, the codec-head rule + qwen_tts_sample
+ * (k_sample) with the repetition penalty over the code0 history (prev_tokens, then every
+ * token drawn here, appended as qwen_tts.c:1721 appends them) and the next input =
+ * codec_emb[token].  Logits, history and LCG state stay on the device until the end. */
+int qwen_hip_talker_sample(void *state, const uint16_t *codec_head, const uint16_t *codec_emb, int codec_vocab,
+                           const float *embed, int pos, int frame0, int n_steps, float temp, int top_k, float top_p,
+                           float rep_penalty, const int *prev_tokens, int n_prev, uint32_t *seed, int *tokens_out,
+                           float *hidden_out) {
+    talker_t *t = (talker_t *)state;
+    int *dh = NULL, *posv = NULL; uint32_t *ds = NULL;
+    if (!t || t->dead) { SETERR("talker state is dead or NULL"); return -1; }
+    const int H = t->s.H;
+    if (!codec_head || !codec_emb || codec_vocab <= 0 || codec_vocab > 4096 || !seed || !tokens_out || n_steps < 0 ||
+        n_prev < 0 || (n_prev > 0 && !prev_tokens) || !embed) {
+        SETERR("talker_sample: bad arguments"); return -1;
+    }
+    if (pos < 0 || pos + n_steps > t->s.kv_max || pos + n_steps > t->s.rope_len) {
+        SETERR("talker_sample: positions exceed kv_max"); return -1;
+    }
+    if (head_setup(t, codec_head, codec_emb, codec_vocab) != 0) goto fail;
+    posv = (int *)malloc((size_t)(n_steps + 1) * sizeof(int));
+    REQ(posv, "host alloc");
+    for (int i = 0; i <= n_steps; i++) posv[i] = pos + i;   /* read by the async copies: kept until the sync */
+    HCK(hipMalloc((void **)&dh, (size_t)(n_prev + n_steps + 1) * sizeof(int)));
+    HCK(hipMalloc((void **)&ds, sizeof(uint32_t)));
+    if (n_prev > 0) HCK(hipMemcpyAsync(dh, prev_tokens, (size_t)n_prev * sizeof(int), hipMemcpyHostToDevice, t->st));
+    HCK(hipMemcpyAsync(ds, seed, sizeof(uint32_t), hipMemcpyHostToDevice, t->st));
+    memcpy(t->h_in, embed, (size_t)H * sizeof(float));
+    HCK(hipMemcpyAsync(t->io + H, t->h_in, (size_t)H * sizeof(float), hipMemcpyHostToDevice, t->st));
+    for (int i = 0; i < n_steps; i++) {
+        float *x = t->io + H;
+        int *tok = dh + n_prev + i;
+        HCK(hipMemcpyAsync(t->d_pos, posv + i, sizeof(int), hipMemcpyHostToDevice, t->st));
+        HCK(stack_body(&t->s, x, t->d_pos, t->st));
+        HCK(qt_launch_mv(t->head_m.prec, QT_EPI_STORE, 1, x, t->s.final_norm, t->s.eps, t->head_m.w, NULL, NULL,
+                         t->head_m.rows, t->head_m.cols, t->logits, NULL, NULL, t->io, t->st));
+        HCK(qt_launch_sample(t->logits, codec_vocab, 1, frame0 + i, 0.0f, temp, top_k, top_p, rep_penalty, dh,
+                             n_prev + i, ds, tok, t->st));
+        HCK(qt_launch_gather(tok, codec_vocab, t->codec_emb, H, x, t->st));
+    }
+    HCK(hipMemcpyAsync(t->d_pos, posv + n_steps, sizeof(int), hipMemcpyHostToDevice, t->st));
+    if (n_steps > 0)
+        HCK(hipMemcpyAsync(tokens_out, dh + n_prev, (size_t)n_steps * sizeof(int), hipMemcpyDeviceToHost, t->st));
+    HCK(hipMemcpyAsync(seed, ds, sizeof(uint32_t), hipMemcpyDeviceToHost, t->st));
+    HCK(hipMemcpyAsync(t->h_out, t->io, (size_t)2 * H * sizeof(float), hipMemcpyDeviceToHost, t->st));
+    HCK(hipStreamSynchronize(t->st));
+    if (hidden_out) memcpy(hidden_out, t->h_out, (size_t)H * sizeof(float));
+    t->dev_pos = pos + n_steps;
+    t->greedy_ready = 0;            /* the fused greedy loop's input is stale: re-seed it with talker_greedy */
+    free(posv); (void)hipFree(dh); (void)hipFree(ds);
+    return 0;
+fail:
+    free(posv);
+    if (dh) (void)hipFree(dh);
+    if (ds) (void)hipFree(ds);
+    t->dead = 1; t->dev_pos = -1;
     return -1;
 }
 

@@ -27,7 +27,7 @@ EXPORTS = [
     "qwen_hip_matmat_bf16", "qwen_hip_op_matvec_int8", "qwen_hip_op_matvec_q4_0",
     "qwen_hip_op_matvec_bf16", "qwen_hip_op_causal_attention_bf16kv", "qwen_hip_op_rms_norm",
     "qwen_hip_op_rms_norm_per_head", "qwen_hip_op_swiglu", "qwen_hip_op_argmax_matvec",
-    "qwen_hip_op_sample", "qwen_hip_op_codec_sample",
+    "qwen_hip_op_sample", "qwen_hip_op_codec_sample", "qwen_hip_talker_sample",
     "qwen_hip_op_quantize_int8", "qwen_hip_op_quantize_q4_0", "qwen_hip_talker_dequant",
     "qwen_hip_last_error", "qwen_hip_talker_batch_init", "qwen_hip_talker_batch_step",
     "qwen_hip_talker_batch_upload_slot", "qwen_hip_talker_batch_free", "qwen_hip_talker_batch_download_slot",
@@ -120,6 +120,8 @@ def lib():
         L.qwen_hip_op_swiglu.argtypes = [vp, vp, i]; L.qwen_hip_op_swiglu.restype = i
         L.qwen_hip_op_argmax_matvec.argtypes = [i, vp, vp, vp, i, i]; L.qwen_hip_op_argmax_matvec.restype = i
         L.qwen_hip_op_sample.argtypes = [vp, i, f, i, f, f, vp, i, vp]; L.qwen_hip_op_sample.restype = i
+        L.qwen_hip_talker_sample.argtypes = [vp, vp, vp, i, vp, i, i, i, f, i, f, f, vp, i, vp, vp, vp]
+        L.qwen_hip_talker_sample.restype = i
         L.qwen_hip_op_codec_sample.argtypes = [vp, i, i, f, f, i, f, f, vp, i, vp]
         L.qwen_hip_op_codec_sample.restype = i
         L.qwen_hip_op_quantize_int8.argtypes = [vp, i, i, vp, vp]; L.qwen_hip_op_quantize_int8.restype = i
@@ -234,6 +236,19 @@ class Talker:
                                            _p(np.ascontiguousarray(embed, np.float32)), pos, frame0, n_steps,
                                            _p(toks), _p(hid)), "talker_greedy")
         return toks, hid
+
+    def sample(self, codec_head, codec_emb, embed, pos, frame0, n_steps, temp, top_k, top_p, rep, prev=(), seed=12345):
+        """Device frame loop with sampling; returns (tokens, last normed hidden, new seed)."""
+        toks = np.empty(n_steps, np.int32)
+        hid = np.empty(self.H, np.float32)
+        pv = np.ascontiguousarray(prev, np.int32)
+        sd = np.array([seed], np.uint32)
+        self._heads = (codec_head, codec_emb)
+        check(lib().qwen_hip_talker_sample(self.h, _p(codec_head), _p(codec_emb), codec_head.shape[0],
+                                           _p(np.ascontiguousarray(embed, np.float32)), pos, frame0, n_steps, temp,
+                                           top_k, top_p, rep, _p(pv) if pv.size else None, pv.size, _p(sd),
+                                           _p(toks), _p(hid)), "talker_sample")
+        return toks, hid, int(sd[0])
 
     def dequant(self, layer, which, r0, n, cols):
         out = np.empty((n, cols), np.float32)

@@ -322,6 +322,51 @@ def test_greedy_tokens_match_reference(name, prec):
     assert list(toks) == toks_ref
 
 
+@need_ref
+@pytest.mark.parametrize("name,prec", [("mini", "int8"), ("mini17", "int4")])
+def test_sampled_loop_matches_reference(oracle, name, prec):
+    """qwen_hip_talker_sample (step -> codec head -> rule + qwen_tts_sample -> next embed, all
+    on the device) against the reference's step and codec head with the oracle sampler
+    (pinned to the reference's qwen_tts_sample) at the reference's default settings.  A
+    token may differ only where the draw lies within rounding of a cumulative boundary;
+    the trajectories part there, so the comparison stops.  At temperature 0 the loop gives
+    the greedy loop's tokens and leaves the LCG state alone."""
+    from conftest import draw_margin
+    print(f"[case] sampled loop {name} {prec}", flush=True)
+    ref, shape, _ = _ref(name, prec)
+    pc = hip.PREC[prec]
+    emb = ref.codec_emb()
+    head = np.ascontiguousarray(ref.codec_head())
+    embc = np.ascontiguousarray(emb)
+    e0 = synth.bf16_to_f32(emb[321])
+    prev0 = [5, 17, 5, 900]
+    n = 24
+    g = _gpu_talker(ref, shape, pc)
+    toks, _, seed_dev = g.sample(head, embc, e0, 0, 0, n, 0.9, 50, 1.0, 1.05, prev0, 777)
+    seed, prev, e, same = 777, list(prev0), e0, 0
+    for f in range(n):
+        h = ref.step(e)
+        _, lg = ref.codec_greedy(h, f)
+        t, seed, dist = oracle.sample(lg, 0.9, 50, 1.0, 1.05, prev, seed, rule=(f, 0.0))
+        if int(toks[f]) != t:
+            assert draw_margin(dist, seed) < 1e-4, (f, int(toks[f]), t)
+            break
+        same += 1
+        prev.append(t)
+        e = synth.bf16_to_f32(emb[t])
+    if same == n:
+        assert seed_dev == seed
+    print(f"[result] sampled loop {name} {prec}: {same}/{n} tokens identical")
+    g.free()
+    # temperature 0: the greedy loop's tokens, LCG state untouched
+    ga, gb = _gpu_talker(ref, shape, pc), _gpu_talker(ref, shape, pc)
+    t_s, h_s, sd = ga.sample(head, embc, e0, 0, 0, 16, 0.0, 0, 1.0, 1.0, (), 99)
+    t_g, h_g = gb.greedy(head, embc, e0, 0, 0, 16)
+    assert list(t_s) == list(t_g) and sd == 99
+    assert rel_l2(h_s, h_g) < 1e-5
+    ga.free(); gb.free()
+
+
 # ------------------------------------------------------------------------ Code Predictor
 
 def _gpu_cp(ref, shape, prec_code):
