@@ -118,6 +118,12 @@ void *qwen_hip_talker_stream(void *state);
  * persistent kernel, 0 when they run as the per-kernel sequence (shapes or devices the
  * fused kernel does not cover), -1 for a NULL state. */
 int   qwen_hip_talker_fused(void *state);
+/* Diagnostic (no reference counterpart; the device twin of the per-layer check the
+ * reference's own tests make by truncating num_layers, qwen_tts_talker.c:659-665): one step
+ * like qwen_hip_talker_step that also returns the residual after every layer,
+ * residuals host f32[n_layers][hidden].  The fused kernel's values are read back from its
+ * activation ring (tags checked); the per-kernel path copies x after each layer. */
+int   qwen_hip_talker_step_layers(void *state, const float *embed, float *residuals, float *hidden_out, int pos);
 /* Same as qwen_hip_talker_step, but the device graph runs with graph capture disabled
  * (one launch per kernel), for profiling and A/B checks. */
 int   qwen_hip_talker_step_nograph(void *state, const float *embed, float *hidden_out, int pos);
@@ -238,22 +244,39 @@ int qwen_hip_op_prefill_gemm(float *Y, const uint16_t *W, const float *X, int S,
  * normed, rotated q | k | v rows of every position. */
 int qwen_hip_op_prefill_attention(float *out, const float *QKV, int S, int nh, int nkv, float scale);
 int qwen_hip_op_argmax_matvec(int prec, const float *x, const void *W, const float *scale, int in_dim, int out_dim);
+/* Sampling settings of the Talker's frame loop: the fields of qwen_tts_ctx_t that the loop
+ * of qwen_tts.c:1649-1721 reads (defaults at qwen_tts.c:559: temperature 0.9, top_k 50,
+ * top_p 1.0, rep_penalty 1.05, greedy_warmup 0). */
+typedef struct {
+    float temperature;      /* ctx->temperature; < 1e-6 = greedy */
+    int top_k;              /* ctx->top_k (0 = off) */
+    float top_p;            /* ctx->top_p (1.0 = off) */
+    float rep_penalty;      /* ctx->rep_penalty (1.0 = off) */
+    int greedy_warmup;      /* ctx->greedy_warmup: frames below it draw greedily (temp 0, top_k 1) */
+    int text_len;           /* text_content_len: EOS boost 0.5 per frame past 2 x 3 x text_len, capped
+                             * at 10 (qwen_tts.c:1666-1675); 0 = no boost */
+} qwen_hip_sample_params_t;
+
+/* The Talker's frame loop with sampling on the device (qwen_tts.c:1649-1721 for code0):
+ * n_steps x (Talker step at pos + i, final norm + codec head, codec-head rule for frame
+ * frame0 + i incl. the EOS boost, qwen_tts_sample with the repetition penalty over
+ * prev_tokens and the tokens drawn so far, next input codec_emb[token]).  Same head and
+ * embedding arguments as qwen_hip_talker_greedy; *seed is the LCG state in and out
+ * (qwen_set_seed / qwen_get_seed, sampling.c:38-49); tokens_out[n_steps]; the last step's
+ * normed hidden state in hidden_out (may be NULL).  Like the reference's loop, generation
+ * ends at the first EOS (2150): that token is the last one returned, the LCG state and the
+ * history stop there, and the remaining steps' results are discarded.  Returns the number
+ * of tokens generated (<= n_steps, the last one EOS when EOS was drawn) or -1.
+ * n_prev + n_steps < 16384.  Allocates nothing per call.  Afterwards the greedy loop must
+ * be re-seeded with qwen_hip_talker_greedy before qwen_hip_talker_greedy_async. */
+int qwen_hip_talker_sample(void *state, const uint16_t *codec_head, const uint16_t *codec_emb, int codec_vocab,
+                           const float *embed, int pos, int frame0, int n_steps, const qwen_hip_sample_params_t *params,
+                           const int *prev_tokens, int n_prev, uint32_t *seed, int *tokens_out, float *hidden_out);
 /* Token sampling on the device: qwen_tts_sample (qwen_tts_sampling.c:160-202; repetition
  * penalty, temperature softmax, top-k, top-p, renormalisation, LCG draw) with the
  * thread-local LCG state of qwen_set_seed / qwen_get_seed (sampling.c:38-49) passed as
  * *seed and advanced as the reference advances it (once per non-greedy draw).  vocab <= 4096.
  * Returns the token, or -1 on error (see qwen_hip_last_error). */
-/* The Talker's frame loop with sampling on the device (qwen_tts.c:1649-1721 for code0):
- * n_steps x (Talker step at pos + i, final norm + codec head, codec-head rule for frame
- * frame0 + i, qwen_tts_sample with the repetition penalty over prev_tokens and the tokens
- * drawn so far, next input codec_emb[token]).  Same head/embedding arguments as
- * qwen_hip_talker_greedy; *seed is the LCG state in and out; tokens_out[n_steps], the last
- * step's normed hidden state in hidden_out (may be NULL).  Afterwards the greedy loop must
- * be re-seeded with qwen_hip_talker_greedy before qwen_hip_talker_greedy_async. */
-int qwen_hip_talker_sample(void *state, const uint16_t *codec_head, const uint16_t *codec_emb, int codec_vocab,
-                           const float *embed, int pos, int frame0, int n_steps, float temp, int top_k, float top_p,
-                           float rep_penalty, const int *prev_tokens, int n_prev, uint32_t *seed, int *tokens_out,
-                           float *hidden_out);
 int qwen_hip_op_sample(const float *logits, int vocab, float temp, int top_k, float top_p, float rep_penalty,
                        const int *prev_tokens, int n_prev, uint32_t *seed);
 /* The codec-head rule of the Talker's frame loop (qwen_tts.c:1652-1679: clip to +-100,

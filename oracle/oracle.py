@@ -204,6 +204,8 @@ class RefModel:
                   "ref_cp_rope_cos", "ref_cp_rope_sin", "ref_cp_dec_x"]:
             getattr(L, n).argtypes = [vp]; getattr(L, n).restype = vp
         L.ref_set_kv_len.argtypes = [vp, i]
+        L.ref_kv_reserve.argtypes = [vp, i]; L.ref_kv_reserve.restype = i
+        L.ref_ctx.argtypes = [vp]; L.ref_ctx.restype = vp
         L.ref_set_threads.argtypes = [i]
         L.ref_talker_step.argtypes = [vp, vp, vp]; L.ref_talker_step.restype = i
         L.ref_talker_prefill.argtypes = [vp, vp, i]; L.ref_talker_prefill.restype = i
@@ -218,11 +220,13 @@ class RefModel:
         L.ref_quantize_int8.argtypes = [vp, i, i, vp, vp]
         L.ref_quantize_q4_0.argtypes = [vp, i, i, vp]
         L.ref_matvec_bf16.argtypes = [vp, vp, vp, i, i]
+        L.ref_matmat_bf16.argtypes = [vp, vp, vp, i, i, i]
         L.ref_matvec_int8.argtypes = [vp, vp, vp, vp, i, i]
         L.ref_matvec_q4_0.argtypes = [vp, vp, vp, i, i]
         L.ref_attention_bf16kv.argtypes = [vp, vp, vp, vp, i, i, i, i, i, f, i]
         L.ref_rms_norm.argtypes = [vp, vp, vp, i, i, f]
         L.ref_swiglu.argtypes = [vp, i]
+        L.ref_rms_norm_per_head.argtypes = [vp, vp, i, i, i, f]
         L.ref_argmax_matvec_bf16.argtypes = [vp, vp, i, i]; L.ref_argmax_matvec_bf16.restype = i
         L.ref_sample.argtypes = [vp, i, f, i, f, f, vp, i, vp]; L.ref_sample.restype = i
         L.ref_argmax_matvec_int8.argtypes = [vp, vp, vp, i, i]; L.ref_argmax_matvec_int8.restype = i
@@ -282,6 +286,18 @@ class RefModel:
     @kv_len.setter
     def kv_len(self, n):
         self.lib.ref_set_kv_len(self.h, n)
+
+    def kv_reserve(self, n):
+        """Grow the reference KV cache to at least n positions (views from kv() go stale)."""
+        assert self.lib.ref_kv_reserve(self.h, n) == 0
+
+    def set_kv(self, k, v, n):
+        """Positions [0, n) of the reference cache <- k, v [layers][>= n][kv_dim]; kv_len = n."""
+        self.kv_reserve(n + 1)
+        rk, rv = self.kv()
+        rk[:, :n] = k[:, :n]
+        rv[:, :n] = v[:, :n]
+        self.kv_len = n
 
     def kv(self):
         s = self.shape

@@ -88,6 +88,9 @@ void *ref_open(const char *dir, const int *cfg, float eps, float theta,
     return h;
 }
 
+/* the reference context of a handle (for the glue under test) */
+void *ref_ctx(void *hp) { return ((ref_handle_t *)hp)->ctx; }
+
 void ref_set_threads(int n) { qwen_set_threads(n > 0 ? n : 1); }
 
 /* ---- Talker ------------------------------------------------------------ */
@@ -130,6 +133,29 @@ int ref_talker_prefill(void *hp, const float *embeds, int seq) {
 void ref_get_dec_x(void *hp, float *out) {
     ref_handle_t *h = (ref_handle_t *)hp;
     memcpy(out, h->ctx->dec_x, (size_t)h->ctx->config.hidden_size * sizeof(float));
+}
+/* Grow the reference's Talker KV cache to hold at least n positions before the caller
+ * writes rows into it (the reference grows by doubling when a step needs room,
+ * qwen_tts_talker.c:257-280; its buffers are released with free()).  Keeps rows
+ * [0, kv_len).  Returns 0, or -1 when out of memory. */
+int ref_kv_reserve(void *hp, int n) {
+    qwen_tts_ctx_t *ctx = ((ref_handle_t *)hp)->ctx;
+    if (n <= ctx->kv_max) return 0;
+    int nm = ctx->kv_max;
+    while (nm < n) nm *= 2;
+    const size_t kvd = (size_t)ctx->config.num_kv_heads * ctx->config.head_dim, L = (size_t)ctx->config.num_layers;
+    void *nk = NULL, *nv = NULL;
+    if (posix_memalign(&nk, 64, L * nm * kvd * sizeof(uint16_t)) || posix_memalign(&nv, 64, L * nm * kvd * sizeof(uint16_t))) {
+        free(nk); free(nv); return -1;
+    }
+    for (size_t l = 0; l < L; l++) {
+        memcpy((uint16_t *)nk + l * nm * kvd, ctx->kv_cache_k + l * ctx->kv_max * kvd, (size_t)ctx->kv_len * kvd * 2);
+        memcpy((uint16_t *)nv + l * nm * kvd, ctx->kv_cache_v + l * ctx->kv_max * kvd, (size_t)ctx->kv_len * kvd * 2);
+    }
+    free(ctx->kv_cache_k); free(ctx->kv_cache_v);
+    ctx->kv_cache_k = (uint16_t *)nk; ctx->kv_cache_v = (uint16_t *)nv;
+    ctx->kv_max = nm;
+    return 0;
 }
 int ref_kv_len(void *hp) { return ((ref_handle_t *)hp)->ctx->kv_len; }
 void ref_set_kv_len(void *hp, int n) { ((ref_handle_t *)hp)->ctx->kv_len = n; }
@@ -220,6 +246,9 @@ void ref_quantize_q4_0(const uint16_t *src, int rows, int cols, void *dst) {
 }
 void ref_matvec_bf16(float *y, const uint16_t *W, const float *x, int rows, int cols) {
     qwen_matvec_bf16(y, W, x, rows, cols);
+}
+void ref_matmat_bf16(float *Y, const uint16_t *W, const float *X, int rows, int cols, int B) {
+    qwen_matmat_bf16(Y, W, X, rows, cols, B);
 }
 void ref_matvec_int8(float *y, const int8_t *W, const float *s, const float *x, int rows, int cols) {
     qwen_matvec_int8(y, W, s, x, rows, cols);

@@ -9,8 +9,13 @@
 extern "C" {
 #endif
 
+/* sets the text qwen_hip_last_error() returns (and prints it) */
+void qt_seterr(const char *fmt, ...) __attribute__((format(printf, 1, 2)));
+
 enum { QT_BF16 = 0, QT_INT8 = 1, QT_Q4 = 2 };
 enum { QT_EPI_STORE = 0, QT_EPI_RESID = 1, QT_EPI_SWIGLU = 2, QT_EPI_BIAS = 3 };
+/* token history of the device sampled loop: previous tokens + tokens drawn in one call */
+enum { QT_SAMPLE_HIST_MAX = 16384 };
 
 hipError_t qt_launch_mv(int prec, int epi, int norm, const float *vin, const float *nw, float eps,
                         const uint8_t *w, const float *scale, const uint16_t *s16, int rows, int cols,
@@ -37,7 +42,7 @@ hipError_t qt_launch_rmsnorm_rows(float *x, const float *w, int rows, int n, flo
 hipError_t qt_launch_swiglu(const float *gu, float *out, int n, hipStream_t st);
 hipError_t qt_launch_sample(const float *logits, int n, int rule, int frame, float eos_boost, float temp,
                             int top_k, float top_p, float rep, const int *prev, int n_prev, uint32_t *seed, int *tok,
-                            hipStream_t st);
+                            int *done, hipStream_t st);
 hipError_t qt_launch_select(const float *logits, int n, int mode, int *d_frame, int advance, int *tok,
                             int *hist, int hist_len, const uint16_t *emb, int emb_dim, float *out,
                             int *d_pos, hipStream_t st);
@@ -53,11 +58,15 @@ hipError_t qt_launch_quant_q4(const uint16_t *src, int rows, int cols, uint8_t *
 hipError_t qt_launch_dequant(int prec, const uint8_t *w, const float *scale, const uint16_t *s16, int cols,
                              int r0, int n, float *out, hipStream_t st);
 hipError_t qt_launch_zero_u32(uint32_t *p, size_t n, hipStream_t st);
+/* KV rows [n][nkv*hd] (host order) <-> head-major [nkv][kv_max][hd] (device cache) */
+hipError_t qt_launch_kv_relayout(const uint16_t *src, uint16_t *dst, int n, int nkv, int hd, int kv_max, int to_heads,
+                                 hipStream_t st);
 
 /* persistent decode step (qt_pstep.hip) */
 int qt_pstep_supported(int prec, int hidden, int inter, int n_heads, int n_kv, int head_dim, int kv_max);
 size_t qt_pstep_ring_words(int hidden, int inter, int n_layers);
 size_t qt_pstep_layer_bytes(void);
+size_t qt_pstep_ring_x_offset(int hidden, int inter, int n_layers, int par, int l);
 void qt_pstep_fill_layer(void *dst, const uint8_t *const w[4], const float *const s[4], const uint16_t *const s16[4],
                          const float *in_norm, const float *post_norm, const float *qn, const float *kn);
 hipError_t qt_launch_pstep(int prec, int hidden, const void *layers_dev, int n_layers, const float *final_norm,

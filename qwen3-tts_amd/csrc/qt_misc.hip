@@ -306,3 +306,35 @@ extern "C" hipError_t qt_launch_zero_u32(uint32_t *p, size_t n, hipStream_t st) 
     hipLaunchKernelGGL(k_zero_u32, dim3(64), dim3(256), 0, st, p, n);
     return hipGetLastError();
 }
+
+// KV layout change between the reference's host cache rows (position-major:
+// [n][n_kv*head_dim] bf16, qwen_tts.h:513-518) and the device cache (head-major:
+// [n_kv][kv_max][head_dim], one contiguous row per head and position).  One thread per
+// 16-byte chunk (8 bf16): reads of a position's row are contiguous, and so are the
+// writes of one head's row.  to_heads = 1: rows -> heads (upload), 0: heads -> rows.
+__global__ void k_kv_relayout(const uint4 *src, uint4 *dst, int n, int nkv, int hd, long long kv_max, int to_heads) {
+    const int cpr = hd / 8;                              // 16-byte chunks per head row
+    const long long total = (long long)n * nkv * cpr;
+    for (long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x; i < total;
+         i += (long long)gridDim.x * blockDim.x) {
+        const int c = (int)(i % cpr);
+        const long long t = i / cpr;
+        const int g = (int)(t % nkv);
+        const long long p = t / nkv;
+        const long long row_idx = (p * nkv + g) * cpr + c;           // position-major
+        const long long head_idx = ((long long)g * kv_max + p) * cpr + c;   // head-major
+        if (to_heads) dst[head_idx] = src[row_idx];
+        else dst[row_idx] = src[head_idx];
+    }
+}
+extern "C" hipError_t qt_launch_kv_relayout(const uint16_t *src, uint16_t *dst, int n, int nkv, int hd, int kv_max,
+                                            int to_heads, hipStream_t st) {
+    if (n <= 0) return hipSuccess;
+    if (hd % 8 || nkv <= 0 || kv_max < n) return hipErrorInvalidValue;
+    const long long total = (long long)n * nkv * (hd / 8);
+    long long blocks = (total + 255) / 256;
+    if (blocks > 4096) blocks = 4096;
+    hipLaunchKernelGGL(k_kv_relayout, dim3((unsigned)blocks), dim3(256), 0, st, (const uint4 *)src, (uint4 *)dst, n, nkv,
+                       hd, (long long)kv_max, to_heads);
+    return hipGetLastError();
+}

@@ -1307,6 +1307,12 @@ extern "C" size_t qt_pstep_ring_words(int hidden, int inter, int n_layers) {
     return 2 * (size_t)n_layers * P + 2 * (size_t)ps::NB * 2;
 }
 extern "C" size_t qt_pstep_layer_bytes(void) { return sizeof(ps::Layer); }
+// word offset of layer l's output x (phase E) in the ring block of parity par
+extern "C" size_t qt_pstep_ring_x_offset(int hidden, int inter, int n_layers, int par, int l) {
+    const size_t OX = (size_t)ps::QKVR + (size_t)ps::NKV * ps::G * ps::HPK * ps::PS + ps::QD + (size_t)hidden + inter;
+    const size_t P = OX + hidden;
+    return ((size_t)par * n_layers + l) * P + OX;
+}
 
 // Layer table entry, filled on the host in this exact order.
 extern "C" void qt_pstep_fill_layer(void *dst, const uint8_t *const w[4], const float *const s[4], const uint16_t *const s16[4],

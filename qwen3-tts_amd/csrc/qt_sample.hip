@@ -38,7 +38,14 @@ struct QsArgs {
     int n_prev;
     uint32_t *seed;
     int *tok;
+    int *done;      // nullable: once a token equal to EOS is drawn under the rule, later
+                    // calls write EOS without drawing (the reference's loop ends there)
 };
+
+__device__ __forceinline__ void qs_put(const QsArgs &a, int t) {
+    a.tok[0] = t;
+    if (a.done && a.rule && t == 2150) a.done[0] = 1;
+}
 
 // total of v over the workgroup, in every thread (wave butterflies, then the 16 wave sums
 // in wave order)
@@ -90,6 +97,10 @@ __global__ __launch_bounds__(QS_T) void k_sample(QsArgs a) {
     __shared__ unsigned hist[16];
     __shared__ int s_min;
     const int tid = threadIdx.x, n = a.n;
+    if (a.done && a.done[0]) {           // uniform: every thread reads the same flag
+        if (tid == 0) a.tok[0] = 2150;
+        return;
+    }
 
     // logits (and the codec-head rule) into LDS
 #pragma unroll
@@ -130,7 +141,7 @@ __global__ __launch_bounds__(QS_T) void k_sample(QsArgs a) {
         float M = red[0];
         for (int w = 1; w < QS_T / 64; w++) M = fmaxf(M, red[w]);
         const int best = qs_min(bv == M ? bi : 0x7FFFFFFF, &s_min);
-        if (tid == 0) a.tok[0] = best == 0x7FFFFFFF ? 0 : best;
+        if (tid == 0) qs_put(a, best == 0x7FFFFFFF ? 0 : best);
         return;
     }
 
@@ -246,17 +257,18 @@ __global__ __launch_bounds__(QS_T) void k_sample(QsArgs a) {
         if (cand == 0x7FFFFFFF && 4 * tid + k < n && r < base + c[k]) cand = 4 * tid + k;
     const int first = qs_min(cand, &s_min);
     if (tid == 0) {
-        a.tok[0] = first == 0x7FFFFFFF ? n - 1 : first;
+        qs_put(a, first == 0x7FFFFFFF ? n - 1 : first);
         a.seed[0] = seed;
     }
 }
 
 extern "C" hipError_t qt_launch_sample(const float *logits, int n, int rule, int frame, float eos_boost, float temp,
                                        int top_k, float top_p, float rep, const int *prev, int n_prev,
-                                       uint32_t *seed, int *tok, hipStream_t st) {
-    if (n <= 0 || n > QS_NMAX || n_prev < 0 || (n_prev > 0 && !prev) || !seed || !tok || !logits)
+                                       uint32_t *seed, int *tok, int *done, hipStream_t st) {
+    if (n <= 0 || n > QS_NMAX || n_prev < 0 || (n_prev > 0 && !prev) || !seed || !tok || !logits ||
+        (done && (!rule || n <= 2150)))
         return hipErrorInvalidValue;
-    QsArgs a = {logits, n, rule, frame, eos_boost, temp, top_k, top_p, rep, prev, n_prev, seed, tok};
+    QsArgs a = {logits, n, rule, frame, eos_boost, temp, top_k, top_p, rep, prev, n_prev, seed, tok, done};
     hipLaunchKernelGGL(k_sample, dim3(1), dim3(QS_T), 0, st, a);
     return hipGetLastError();
 }

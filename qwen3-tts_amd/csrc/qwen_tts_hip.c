@@ -23,6 +23,7 @@
 
 #include <hip/hip_runtime_api.h>
 #include <math.h>
+#include <stdarg.h>
 #include <stdio.h>
 #include <stdlib.h>
 #include <string.h>
@@ -31,6 +32,15 @@ static __thread char g_err[512];
 const char *qwen_hip_last_error(void) { return g_err; }
 
 #define SETERR(...) do { snprintf(g_err, sizeof g_err, __VA_ARGS__); fprintf(stderr, "[qwen_hip] %s\n", g_err); } while (0)
+
+/* error text from the kernel files (same channel as SETERR) */
+void qt_seterr(const char *fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(g_err, sizeof g_err, fmt, ap);
+    va_end(ap);
+    fprintf(stderr, "[qwen_hip] %s\n", g_err);
+}
 #define HCK(call) do { hipError_t e_ = (call); if (e_ != hipSuccess) { \
     SETERR("%s:%d %s -> %s", __FILE__, __LINE__, #call, hipGetErrorString(e_)); goto fail; } } while (0)
 #define REQ(cond, ...) do { if (!(cond)) { SETERR(__VA_ARGS__); goto fail; } } while (0)
@@ -116,6 +126,24 @@ static float *up_f32(const float *src, size_t n, hipStream_t st) {
     return d;
 }
 
+/* One layer's K or V between the host cache rows (position-major [n][n_kv*hd], the
+ * reference's kv_cache_k/v layer slice, contiguous) and the device cache (head-major
+ * [n_kv][kv_max][hd]): one contiguous copy through a device staging buffer plus a
+ * relayout kernel, instead of one strided copy per head with 256-byte rows (which
+ * pageable memory serves at tens of MB/s).  stage holds n*n_kv*hd bf16. */
+static hipError_t kv_xfer(uint16_t *dev_heads, int kv_max, uint16_t *host_rows, int n, int nkv, int hd, int upload,
+                          uint16_t *stage, hipStream_t st) {
+    hipError_t e;
+    const size_t bytes = (size_t)n * nkv * hd * sizeof(uint16_t);
+    if (n <= 0) return hipSuccess;
+    if (upload) {
+        if ((e = hipMemcpyAsync(stage, host_rows, bytes, hipMemcpyDefault, st))) return e;
+        return qt_launch_kv_relayout(stage, dev_heads, n, nkv, hd, kv_max, 1, st);
+    }
+    if ((e = qt_launch_kv_relayout(dev_heads, stage, n, nkv, hd, kv_max, 0, st))) return e;
+    return hipMemcpyAsync(host_rows, stage, bytes, hipMemcpyDefault, st);
+}
+
 /* ---- one stack of transformer layers on the device (Talker: 28, CP: 5) ------------ */
 
 typedef struct {
@@ -127,6 +155,7 @@ typedef struct {
     uint16_t *kc, *vc;         /* [L][nkv][kv_max][hd] */
     float *qkvbuf, *attn, *hbuf;
     float *part; unsigned *cnt;
+    uint16_t *kv_stage;        /* [kv_max][n_kv*hd]: KV upload/download staging, made on first use */
 } stack_t;
 
 static void stack_free(stack_t *s) {
@@ -142,7 +171,8 @@ static void stack_free(stack_t *s) {
     }
     free(s->qkv); free(s->o); free(s->gu); free(s->dn);
     free(s->in_norm); free(s->post_norm); free(s->qn); free(s->kn);
-    void *bufs[] = {s->final_norm, s->rope_cos, s->rope_sin, s->kc, s->vc, s->qkvbuf, s->attn, s->hbuf, s->part, s->cnt};
+    void *bufs[] = {s->final_norm, s->rope_cos, s->rope_sin, s->kc, s->vc, s->qkvbuf, s->attn, s->hbuf, s->part, s->cnt,
+                    s->kv_stage};
     for (size_t i = 0; i < sizeof bufs / sizeof bufs[0]; i++) if (bufs[i]) (void)hipFree(bufs[i]);
     memset(s, 0, sizeof *s);
 }
@@ -218,7 +248,7 @@ fail:
 /* The layers of one pass: x (device residual) in/out, position read from d_pos.
  * Mirrors qwen_talker_step's layer loop (qwen_tts_talker.c:580-690) and
  * cp_layer_body (qwen_tts_code_predictor.c:595-717). */
-static hipError_t stack_body(stack_t *s, float *x, const int *d_pos, hipStream_t st) {
+static hipError_t stack_body_ex(stack_t *s, float *x, const int *d_pos, hipStream_t st, float *layer_out) {
     hipError_t e;
     const float scale = 1.0f / sqrtf((float)s->hd);
     for (int l = 0; l < s->L; l++) {
@@ -230,8 +260,13 @@ static hipError_t stack_body(stack_t *s, float *x, const int *d_pos, hipStream_t
         if ((e = mv(&s->o[l], QT_EPI_RESID, 0, s->attn, NULL, s->eps, NULL, x, NULL, st))) return e;
         if ((e = mv(&s->gu[l], QT_EPI_SWIGLU, 1, x, s->post_norm[l], s->eps, s->hbuf, NULL, NULL, st))) return e;
         if ((e = mv(&s->dn[l], QT_EPI_RESID, 0, s->hbuf, NULL, s->eps, NULL, x, NULL, st))) return e;
+        if (layer_out && (e = qt_launch_copy_f32(x, layer_out + (size_t)l * s->H, s->H, st))) return e;
     }
     return hipSuccess;
+}
+
+static hipError_t stack_body(stack_t *s, float *x, const int *d_pos, hipStream_t st) {
+    return stack_body_ex(s, x, d_pos, st, NULL);
 }
 
 /* ---- Talker state ------------------------------------------------------------------ */
@@ -255,6 +290,11 @@ typedef struct {
     float *logits;
     dmat_t head_m;
     int hist_len;
+    /* sampled loop: token history (prev tokens + drawn tokens), LCG state, EOS flag;
+     * allocated once at init (QT_SAMPLE_HIST_MAX entries) */
+    int *smp_hist;
+    uint32_t *smp_seed;
+    int *smp_done;
     /* persistent single-kernel step (qt_pstep.hip) */
     int ps_on;
     void *ps_layers;        /* device layer table */
@@ -290,6 +330,7 @@ static void talker_destroy(talker_t *t) {
     }
     stack_free(&t->s);
     void *bufs[] = {t->io, t->d_pos, t->d_frame, t->d_tok, t->d_hist, t->codec_head, t->codec_emb, t->logits,
+                    t->smp_hist, t->smp_seed, t->smp_done,
                     t->ps_layers, t->ps_ring, t->ps_xin, t->ps_epoch, t->ps_err,
                     t->pf_x, t->pf_qkvb, t->pf_attn, t->pf_h, t->pf_p, t->pf_part};
     for (size_t i = 0; i < sizeof bufs / sizeof bufs[0]; i++) if (bufs[i]) (void)hipFree(bufs[i]);
@@ -366,6 +407,9 @@ void *qwen_hip_talker_init(const qwen_hip_talker_desc_t *desc) {
     HCK(hipMalloc((void **)&t->d_frame, sizeof(int)));
     HCK(hipMalloc((void **)&t->d_tok, sizeof(int)));
     HCK(hipMalloc((void **)&t->d_hist, (size_t)t->hist_len * sizeof(int)));
+    HCK(hipMalloc((void **)&t->smp_hist, (size_t)QT_SAMPLE_HIST_MAX * sizeof(int)));
+    HCK(hipMalloc((void **)&t->smp_seed, 64));
+    HCK(hipMalloc((void **)&t->smp_done, 64));
     HCK(hipHostMalloc((void **)&t->h_in, (size_t)H * sizeof(float), hipHostMallocDefault));
     HCK(hipHostMalloc((void **)&t->h_out, (size_t)2 * H * sizeof(float), hipHostMallocDefault));
     HCK(hipHostMalloc((void **)&t->h_pos, 4 * sizeof(int), hipHostMallocDefault));
@@ -486,6 +530,68 @@ void qwen_hip_talker_get_dec_x(void *state, float *out) {
     if (t && out) memcpy(out, t->h_out + t->s.H, (size_t)t->s.H * sizeof(float));
 }
 
+/* One step that also returns the residual after every layer (residuals[L][H]): the
+ * device twin of the per-layer check the reference tests use (running the step with
+ * num_layers truncated, qwen_tts_talker.c:659-665).  On the fused path the values are the
+ * persistent kernel's own: its activation ring keeps every layer's output x (phase E,
+ * tagged with the step number) until the slot is reused two steps later, so they are read
+ * back after the launch and their tags are checked.  On the per-kernel path x is copied
+ * after each layer of an ungraphed step.  Allocates a temporary device buffer (a
+ * diagnostic, not a hot-path call). */
+int qwen_hip_talker_step_layers(void *state, const float *embed, float *residuals, float *hidden_out, int pos) {
+    talker_t *t = (talker_t *)state;
+    void *tmp = NULL;
+    unsigned long long *words = NULL;
+    if (!t || t->dead) { SETERR("talker state is dead or NULL"); return -1; }
+    if (!embed || !residuals) { SETERR("null argument"); return -1; }
+    stack_t *s = &t->s;
+    const int H = s->H, L = s->L;
+    if (pos < 0 || pos >= s->kv_max || pos >= s->rope_len) { SETERR("pos %d out of range", pos); return -1; }
+    if (talker_set_pos(t, pos) != 0) goto fail;
+    memcpy(t->h_in, embed, (size_t)H * sizeof(float));
+    if (t->ps_on) {
+        unsigned tag = 0;
+        HCK(hipMemcpyAsync(t->ps_xin, t->h_in, (size_t)H * sizeof(float), hipMemcpyHostToDevice, t->st));
+        HCK(ps_launch(t, 1, 0));
+        HCK(hipMemcpyAsync(t->h_out, t->io, (size_t)2 * H * sizeof(float), hipMemcpyDeviceToHost, t->st));
+        HCK(hipMemcpyAsync(t->h_err, t->ps_err, sizeof(int), hipMemcpyDeviceToHost, t->st));
+        HCK(hipMemcpyAsync(&tag, t->ps_epoch, sizeof tag, hipMemcpyDeviceToHost, t->st));
+        HCK(hipStreamSynchronize(t->st));
+        if (ps_check(t) != 0) goto fail;
+        t->dev_pos = pos + 1;
+        words = (unsigned long long *)malloc((size_t)H * sizeof *words);
+        REQ(words, "host alloc");
+        for (int l = 0; l < L; l++) {
+            const size_t off = qt_pstep_ring_x_offset(H, s->F, L, 0, l);   /* a 1-step launch runs at parity 0 */
+            HCK(hipMemcpy(words, t->ps_ring + off, (size_t)H * sizeof *words, hipMemcpyDeviceToHost));
+            for (int i = 0; i < H; i++) {
+                REQ((unsigned)(words[i] >> 32) == tag - 1u, "ring word of layer %d carries tag %u, expected %u", l,
+                    (unsigned)(words[i] >> 32), tag - 1u);
+                const unsigned bits = (unsigned)words[i];
+                memcpy(residuals + (size_t)l * H + i, &bits, sizeof bits);
+            }
+        }
+        free(words);
+    } else {
+        HCK(hipMalloc(&tmp, (size_t)L * H * sizeof(float)));
+        HCK(hipMemcpyAsync(t->io + H, t->h_in, (size_t)H * sizeof(float), hipMemcpyHostToDevice, t->st));
+        HCK(stack_body_ex(s, t->io + H, t->d_pos, t->st, (float *)tmp));
+        HCK(qt_launch_rmsnorm(t->io + H, s->final_norm, t->io, H, s->eps, t->d_pos, t->st));
+        HCK(hipMemcpyAsync(t->h_out, t->io, (size_t)2 * H * sizeof(float), hipMemcpyDeviceToHost, t->st));
+        HCK(hipMemcpyAsync(residuals, tmp, (size_t)L * H * sizeof(float), hipMemcpyDeviceToHost, t->st));
+        HCK(hipStreamSynchronize(t->st));
+        (void)hipFree(tmp);
+        t->dev_pos = pos + 1;
+    }
+    if (hidden_out) memcpy(hidden_out, t->h_out, (size_t)H * sizeof(float));
+    return 0;
+fail:
+    free(words);
+    if (tmp) (void)hipFree(tmp);
+    t->dead = 1; t->dev_pos = -1;
+    return -1;
+}
+
 int qwen_hip_talker_upload_kv(void *state, const uint16_t *kv_k, const uint16_t *kv_v, int host_kv_max,
                               int prefill_len) {
     talker_t *t = (talker_t *)state;
@@ -493,15 +599,13 @@ int qwen_hip_talker_upload_kv(void *state, const uint16_t *kv_k, const uint16_t 
     stack_t *s = &t->s;
     if (prefill_len <= 0) return 0;
     REQ(prefill_len <= s->kv_max && prefill_len <= host_kv_max, "prefill_len %d exceeds kv_max", prefill_len);
-    for (int l = 0; l < s->L; l++)
-        for (int g = 0; g < s->nkv; g++) {
-            size_t dst = (((size_t)l * s->nkv + g) * s->kv_max) * s->hd;
-            size_t src = (size_t)l * host_kv_max * s->kvd + (size_t)g * s->hd;
-            HCK(hipMemcpy2DAsync(s->kc + dst, s->hd * 2, kv_k + src, (size_t)s->kvd * 2, s->hd * 2, prefill_len,
-                                 hipMemcpyDefault, t->st));
-            HCK(hipMemcpy2DAsync(s->vc + dst, s->hd * 2, kv_v + src, (size_t)s->kvd * 2, s->hd * 2, prefill_len,
-                                 hipMemcpyDefault, t->st));
-        }
+    REQ(kv_k && kv_v, "null KV");
+    if (!s->kv_stage) HCK(hipMalloc((void **)&s->kv_stage, (size_t)s->kv_max * s->kvd * sizeof(uint16_t)));
+    for (int l = 0; l < s->L; l++) {
+        const size_t lay = (size_t)l * s->nkv * s->kv_max * s->hd, src = (size_t)l * host_kv_max * s->kvd;
+        HCK(kv_xfer(s->kc + lay, s->kv_max, (uint16_t *)kv_k + src, prefill_len, s->nkv, s->hd, 1, s->kv_stage, t->st));
+        HCK(kv_xfer(s->vc + lay, s->kv_max, (uint16_t *)kv_v + src, prefill_len, s->nkv, s->hd, 1, s->kv_stage, t->st));
+    }
     HCK(hipStreamSynchronize(t->st));
     return 0;
 fail:
@@ -514,15 +618,13 @@ int qwen_hip_talker_download_kv(void *state, uint16_t *kv_k, uint16_t *kv_v, int
     stack_t *s = &t->s;
     REQ(n >= 0 && n <= s->kv_max && n <= host_kv_max, "n %d out of range", n);
     if (n == 0) return 0;
-    for (int l = 0; l < s->L; l++)
-        for (int g = 0; g < s->nkv; g++) {
-            size_t src = (((size_t)l * s->nkv + g) * s->kv_max) * s->hd;
-            size_t dst = (size_t)l * host_kv_max * s->kvd + (size_t)g * s->hd;
-            HCK(hipMemcpy2DAsync(kv_k + dst, (size_t)s->kvd * 2, s->kc + src, s->hd * 2, s->hd * 2, n,
-                                 hipMemcpyDefault, t->st));
-            HCK(hipMemcpy2DAsync(kv_v + dst, (size_t)s->kvd * 2, s->vc + src, s->hd * 2, s->hd * 2, n,
-                                 hipMemcpyDefault, t->st));
-        }
+    REQ(kv_k && kv_v, "null KV");
+    if (!s->kv_stage) HCK(hipMalloc((void **)&s->kv_stage, (size_t)s->kv_max * s->kvd * sizeof(uint16_t)));
+    for (int l = 0; l < s->L; l++) {
+        const size_t lay = (size_t)l * s->nkv * s->kv_max * s->hd, dst = (size_t)l * host_kv_max * s->kvd;
+        HCK(kv_xfer(s->kc + lay, s->kv_max, kv_k + dst, n, s->nkv, s->hd, 0, s->kv_stage, t->st));
+        HCK(kv_xfer(s->vc + lay, s->kv_max, kv_v + dst, n, s->nkv, s->hd, 0, s->kv_stage, t->st));
+    }
     HCK(hipStreamSynchronize(t->st));
     return 0;
 fail:
@@ -709,6 +811,8 @@ int qwen_hip_talker_greedy(void *state, const uint16_t *codec_head, const uint16
     const int H = t->s.H;
     REQ(codec_head && codec_emb && codec_vocab > 0, "missing codec head/embedding");
     REQ(n_steps >= 0 && n_steps <= t->hist_len, "n_steps %d out of range", n_steps);
+    REQ(frame0 >= 0, "frame0 %d must be >= 0", frame0);
+    REQ(tokens_out || n_steps == 0, "null tokens_out");
     REQ(pos >= 0 && pos + n_steps <= t->s.kv_max && pos + n_steps <= t->s.rope_len, "positions exceed kv_max");
     if (head_setup(t, codec_head, codec_emb, codec_vocab) != 0) goto fail;
     if (talker_set_pos(t, pos) != 0) goto fail;
@@ -749,61 +853,74 @@ fail:
 }
 
 /* Sampled frame loop on the device (qwen_tts.c:1649-1721, code0 only): per step the Talker
- * step, the final norm fused into the codec head, the codec-head rule + qwen_tts_sample
- * (k_sample) with the repetition penalty over the code0 history (prev_tokens, then every
- * token drawn here, appended as qwen_tts.c:1721 appends them) and the next input =
- * codec_emb[token].  Logits, history and LCG state stay on the device until the end. */
+ * step, the final norm fused into the codec head, the codec-head rule (clip, special-token
+ * mask, EOS masked on frames 0-1, EOS boost after 2 x 3 x text_len frames) +
+ * qwen_tts_sample (k_sample) with the repetition penalty over the code0 history
+ * (prev_tokens, then every token drawn here, appended as qwen_tts.c:1721 appends them) and
+ * the next input = codec_emb[token].  Frames below greedy_warmup draw greedily
+ * (qwen_tts.c:1688-1692).  The reference leaves its loop at EOS (qwen_tts.c:1716-1719): here
+ * the first EOS sets a device flag, after which the sampler writes EOS without drawing
+ * (the LCG state and the history stop where the reference's do) and the remaining steps'
+ * results are discarded.  Logits, history and LCG state stay on the device until the end;
+ * nothing is allocated per call. */
 int qwen_hip_talker_sample(void *state, const uint16_t *codec_head, const uint16_t *codec_emb, int codec_vocab,
-                           const float *embed, int pos, int frame0, int n_steps, float temp, int top_k, float top_p,
-                           float rep_penalty, const int *prev_tokens, int n_prev, uint32_t *seed, int *tokens_out,
-                           float *hidden_out) {
+                           const float *embed, int pos, int frame0, int n_steps, const qwen_hip_sample_params_t *sp,
+                           const int *prev_tokens, int n_prev, uint32_t *seed, int *tokens_out, float *hidden_out) {
     talker_t *t = (talker_t *)state;
-    int *dh = NULL, *posv = NULL; uint32_t *ds = NULL;
     if (!t || t->dead) { SETERR("talker state is dead or NULL"); return -1; }
     const int H = t->s.H;
-    if (!codec_head || !codec_emb || codec_vocab <= 0 || codec_vocab > 4096 || !seed || !tokens_out || n_steps < 0 ||
-        n_prev < 0 || (n_prev > 0 && !prev_tokens) || !embed) {
+    if (!codec_head || !codec_emb || codec_vocab <= 2150 || codec_vocab > 4096 || !seed || !sp ||
+        (n_steps > 0 && !tokens_out) || n_steps < 0 || frame0 < 0 || n_prev < 0 || (n_prev > 0 && !prev_tokens) || !embed) {
         SETERR("talker_sample: bad arguments"); return -1;
+    }
+    if ((long long)n_prev + n_steps + 1 > QT_SAMPLE_HIST_MAX) {
+        SETERR("talker_sample: history of %d + %d tokens exceeds %d", n_prev, n_steps, QT_SAMPLE_HIST_MAX - 1); return -1;
     }
     if (pos < 0 || pos + n_steps > t->s.kv_max || pos + n_steps > t->s.rope_len) {
         SETERR("talker_sample: positions exceed kv_max"); return -1;
     }
     if (head_setup(t, codec_head, codec_emb, codec_vocab) != 0) goto fail;
-    posv = (int *)malloc((size_t)(n_steps + 1) * sizeof(int));
-    REQ(posv, "host alloc");
-    for (int i = 0; i <= n_steps; i++) posv[i] = pos + i;   /* read by the async copies: kept until the sync */
-    HCK(hipMalloc((void **)&dh, (size_t)(n_prev + n_steps + 1) * sizeof(int)));
-    HCK(hipMalloc((void **)&ds, sizeof(uint32_t)));
-    if (n_prev > 0) HCK(hipMemcpyAsync(dh, prev_tokens, (size_t)n_prev * sizeof(int), hipMemcpyHostToDevice, t->st));
-    HCK(hipMemcpyAsync(ds, seed, sizeof(uint32_t), hipMemcpyHostToDevice, t->st));
+    if (talker_set_pos(t, pos) != 0) goto fail;
+    if (n_prev > 0) HCK(hipMemcpyAsync(t->smp_hist, prev_tokens, (size_t)n_prev * sizeof(int), hipMemcpyHostToDevice, t->st));
+    t->h_pos[2] = (int)*seed;
+    t->h_pos[3] = 0;
+    HCK(hipMemcpyAsync(t->smp_seed, t->h_pos + 2, sizeof(uint32_t), hipMemcpyHostToDevice, t->st));
+    HCK(hipMemcpyAsync(t->smp_done, t->h_pos + 3, sizeof(int), hipMemcpyHostToDevice, t->st));
     memcpy(t->h_in, embed, (size_t)H * sizeof(float));
     HCK(hipMemcpyAsync(t->io + H, t->h_in, (size_t)H * sizeof(float), hipMemcpyHostToDevice, t->st));
+    const int expected = sp->text_len * 3, boost_start = expected * 2;
     for (int i = 0; i < n_steps; i++) {
         float *x = t->io + H;
-        int *tok = dh + n_prev + i;
-        HCK(hipMemcpyAsync(t->d_pos, posv + i, sizeof(int), hipMemcpyHostToDevice, t->st));
+        const int frame = frame0 + i;
+        float boost = 0.0f;
+        if (expected > 0 && frame > boost_start) {
+            boost = 0.5f * (float)(frame - boost_start);
+            if (boost > 10.0f) boost = 10.0f;
+        }
+        const int warm = sp->greedy_warmup > 0 && frame < sp->greedy_warmup;
         HCK(stack_body(&t->s, x, t->d_pos, t->st));
         HCK(qt_launch_mv(t->head_m.prec, QT_EPI_STORE, 1, x, t->s.final_norm, t->s.eps, t->head_m.w, NULL, NULL,
                          t->head_m.rows, t->head_m.cols, t->logits, NULL, NULL, t->io, t->st));
-        HCK(qt_launch_sample(t->logits, codec_vocab, 1, frame0 + i, 0.0f, temp, top_k, top_p, rep_penalty, dh,
-                             n_prev + i, ds, tok, t->st));
-        HCK(qt_launch_gather(tok, codec_vocab, t->codec_emb, H, x, t->st));
+        HCK(qt_launch_sample(t->logits, codec_vocab, 1, frame, boost, warm ? 0.0f : sp->temperature,
+                             warm ? 1 : sp->top_k, sp->top_p, sp->rep_penalty, t->smp_hist, n_prev + i, t->smp_seed,
+                             t->smp_hist + n_prev + i, t->smp_done, t->st));
+        HCK(qt_launch_gather(t->smp_hist + n_prev + i, codec_vocab, t->codec_emb, H, x, t->st));
+        HCK(qt_launch_advance_pos(t->d_pos, 1, t->st));
     }
-    HCK(hipMemcpyAsync(t->d_pos, posv + n_steps, sizeof(int), hipMemcpyHostToDevice, t->st));
     if (n_steps > 0)
-        HCK(hipMemcpyAsync(tokens_out, dh + n_prev, (size_t)n_steps * sizeof(int), hipMemcpyDeviceToHost, t->st));
-    HCK(hipMemcpyAsync(seed, ds, sizeof(uint32_t), hipMemcpyDeviceToHost, t->st));
+        HCK(hipMemcpyAsync(tokens_out, t->smp_hist + n_prev, (size_t)n_steps * sizeof(int), hipMemcpyDeviceToHost, t->st));
+    HCK(hipMemcpyAsync(t->h_pos + 2, t->smp_seed, sizeof(uint32_t), hipMemcpyDeviceToHost, t->st));
     HCK(hipMemcpyAsync(t->h_out, t->io, (size_t)2 * H * sizeof(float), hipMemcpyDeviceToHost, t->st));
     HCK(hipStreamSynchronize(t->st));
+    *seed = (uint32_t)t->h_pos[2];
     if (hidden_out) memcpy(hidden_out, t->h_out, (size_t)H * sizeof(float));
     t->dev_pos = pos + n_steps;
     t->greedy_ready = 0;            /* the fused greedy loop's input is stale: re-seed it with talker_greedy */
-    free(posv); (void)hipFree(dh); (void)hipFree(ds);
-    return 0;
+    int n_gen = n_steps;
+    for (int i = 0; i < n_steps; i++)
+        if (tokens_out[i] == 2150) { n_gen = i + 1; break; }
+    return n_gen;
 fail:
-    free(posv);
-    if (dh) (void)hipFree(dh);
-    if (ds) (void)hipFree(ds);
     t->dead = 1; t->dev_pos = -1;
     return -1;
 }
@@ -1217,13 +1334,15 @@ typedef struct {
     float *h_io; int *h_pos;   /* pinned */
     hipGraphExec_t exec; int graph_ready;
     int last_async;            /* steps replayed since the last batch_step */
+    uint16_t *kv_stage;        /* [kv_max][n_kv*hd]: slot upload/download staging, made on first use */
     int dead;
 } batch_t;
 
 static void batch_destroy(batch_t *bt) {
     if (!bt) return;
     if (bt->graph_ready) (void)hipGraphExecDestroy(bt->exec);
-    void *bufs[] = {bt->kc, bt->vc, bt->x, bt->qkv, bt->attn, bt->h, bt->hid, bt->pc, bt->ps, bt->part, bt->cnt, bt->d_pos};
+    void *bufs[] = {bt->kc, bt->vc, bt->x, bt->qkv, bt->attn, bt->h, bt->hid, bt->pc, bt->ps, bt->part, bt->cnt, bt->d_pos,
+                    bt->kv_stage};
     for (size_t i = 0; i < sizeof bufs / sizeof bufs[0]; i++) if (bufs[i]) (void)hipFree(bufs[i]);
     if (bt->h_io) (void)hipHostFree(bt->h_io);
     if (bt->h_pos) (void)hipHostFree(bt->h_pos);
@@ -1357,15 +1476,13 @@ int qwen_hip_talker_batch_upload_slot(void *state, int b, const uint16_t *kv_k, 
     REQ(kv_k && kv_v, "null KV");
     REQ(prefill_len <= bt->kv_max && prefill_len <= src_kv_max, "prefill_len %d exceeds kv_max", prefill_len);
     const size_t per = (size_t)s->L * s->nkv * s->kv_max * s->hd;
-    for (int l = 0; l < s->L; l++)
-        for (int g = 0; g < s->nkv; g++) {
-            const size_t dst = (size_t)b * per + (((size_t)l * s->nkv + g) * s->kv_max) * s->hd;
-            const size_t src = (((size_t)b * s->L + l) * src_kv_max) * s->kvd + (size_t)g * s->hd;
-            HCK(hipMemcpy2DAsync(bt->kc + dst, s->hd * 2, kv_k + src, (size_t)s->kvd * 2, s->hd * 2, prefill_len,
-                                 hipMemcpyDefault, bt->st));
-            HCK(hipMemcpy2DAsync(bt->vc + dst, s->hd * 2, kv_v + src, (size_t)s->kvd * 2, s->hd * 2, prefill_len,
-                                 hipMemcpyDefault, bt->st));
-        }
+    if (!bt->kv_stage) HCK(hipMalloc((void **)&bt->kv_stage, (size_t)bt->kv_max * s->kvd * sizeof(uint16_t)));
+    for (int l = 0; l < s->L; l++) {
+        const size_t dst = (size_t)b * per + (size_t)l * s->nkv * s->kv_max * s->hd;
+        const size_t src = (((size_t)b * s->L + l) * src_kv_max) * s->kvd;
+        HCK(kv_xfer(bt->kc + dst, s->kv_max, (uint16_t *)kv_k + src, prefill_len, s->nkv, s->hd, 1, bt->kv_stage, bt->st));
+        HCK(kv_xfer(bt->vc + dst, s->kv_max, (uint16_t *)kv_v + src, prefill_len, s->nkv, s->hd, 1, bt->kv_stage, bt->st));
+    }
     HCK(hipStreamSynchronize(bt->st));
     return 0;
 fail:
@@ -1379,15 +1496,14 @@ int qwen_hip_talker_batch_download_slot(void *state, int b, uint16_t *kv_k, uint
     REQ(n >= 0 && n <= bt->kv_max && n <= dst_kv_max, "n %d out of range", n);
     if (n == 0) return 0;
     const size_t per = (size_t)s->L * s->nkv * s->kv_max * s->hd;
-    for (int l = 0; l < s->L; l++)
-        for (int g = 0; g < s->nkv; g++) {
-            const size_t src = (size_t)b * per + (((size_t)l * s->nkv + g) * s->kv_max) * s->hd;
-            const size_t dst = (((size_t)b * s->L + l) * dst_kv_max) * s->kvd + (size_t)g * s->hd;
-            HCK(hipMemcpy2DAsync(kv_k + dst, (size_t)s->kvd * 2, bt->kc + src, s->hd * 2, s->hd * 2, n,
-                                 hipMemcpyDefault, bt->st));
-            HCK(hipMemcpy2DAsync(kv_v + dst, (size_t)s->kvd * 2, bt->vc + src, s->hd * 2, s->hd * 2, n,
-                                 hipMemcpyDefault, bt->st));
-        }
+    REQ(kv_k && kv_v, "null KV");
+    if (!bt->kv_stage) HCK(hipMalloc((void **)&bt->kv_stage, (size_t)bt->kv_max * s->kvd * sizeof(uint16_t)));
+    for (int l = 0; l < s->L; l++) {
+        const size_t src = (size_t)b * per + (size_t)l * s->nkv * s->kv_max * s->hd;
+        const size_t dst = (((size_t)b * s->L + l) * dst_kv_max) * s->kvd;
+        HCK(kv_xfer(bt->kc + src, s->kv_max, kv_k + dst, n, s->nkv, s->hd, 0, bt->kv_stage, bt->st));
+        HCK(kv_xfer(bt->vc + src, s->kv_max, kv_v + dst, n, s->nkv, s->hd, 0, bt->kv_stage, bt->st));
+    }
     HCK(hipStreamSynchronize(bt->st));
     return 0;
 fail:
@@ -1634,13 +1750,16 @@ static int op_sample(int rule, int frame, float eos_boost, const float *logits, 
     }
     HCK(hipMemcpyAsync(dl, logits, (size_t)vocab * sizeof(float), hipMemcpyHostToDevice, st));
     HCK(hipMemcpyAsync(ds, seed, sizeof(uint32_t), hipMemcpyHostToDevice, st));
-    HCK(qt_launch_sample(dl, vocab, rule, frame, eos_boost, temp, top_k, top_p, rep, dp, n_prev, ds, dt, st));
+    HCK(qt_launch_sample(dl, vocab, rule, frame, eos_boost, temp, top_k, top_p, rep, dp, n_prev, ds, dt, NULL, st));
     HCK(hipMemcpyAsync(&tok, dt, sizeof(int), hipMemcpyDeviceToHost, st));
     HCK(hipMemcpyAsync(seed, ds, sizeof(uint32_t), hipMemcpyDeviceToHost, st));
     HCK(hipStreamSynchronize(st));
     out = tok;
 fail:
-    if (dl) (void)hipFree(dl); if (dp) (void)hipFree(dp); if (dt) (void)hipFree(dt); if (ds) (void)hipFree(ds);
+    if (dl) (void)hipFree(dl);
+    if (dp) (void)hipFree(dp);
+    if (dt) (void)hipFree(dt);
+    if (ds) (void)hipFree(ds);
     return out;
 }
 int qwen_hip_op_sample(const float *logits, int vocab, float temp, int top_k, float top_p, float rep_penalty,

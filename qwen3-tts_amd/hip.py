@@ -35,7 +35,7 @@ EXPORTS = [
     "qwen_hip_cp_batch_init", "qwen_hip_cp_batch_step", "qwen_hip_cp_batch_free", "qwen_hip_op_matmat_int8",
     "qwen_hip_cp_set_prefill2", "qwen_hip_cp_prefill2",
     "qwen_hip_talker_prefill", "qwen_hip_talker_prefill_async", "qwen_hip_op_prefill_gemm",
-    "qwen_hip_op_prefill_attention",
+    "qwen_hip_op_prefill_attention", "qwen_hip_talker_step_layers",
 ]
 
 
@@ -64,6 +64,11 @@ class CpDesc(C.Structure):
                 ("mtp_prec", C.c_int), ("mtp", Mat), ("mtp_bias", C.c_void_p)]
 
 
+class SampleParams(C.Structure):
+    _fields_ = [("temperature", C.c_float), ("top_k", C.c_int), ("top_p", C.c_float), ("rep_penalty", C.c_float),
+                ("greedy_warmup", C.c_int), ("text_len", C.c_int)]
+
+
 def _p(a):
     return None if a is None else a.ctypes.data_as(C.c_void_p)
 
@@ -81,6 +86,7 @@ def lib():
         L.qwen_hip_talker_init.argtypes = [C.POINTER(TalkerDesc)]; L.qwen_hip_talker_init.restype = vp
         L.qwen_hip_talker_step.argtypes = [vp, vp, vp, i]; L.qwen_hip_talker_step.restype = i
         L.qwen_hip_talker_step_nograph.argtypes = [vp, vp, vp, i]; L.qwen_hip_talker_step_nograph.restype = i
+        L.qwen_hip_talker_step_layers.argtypes = [vp, vp, vp, vp, i]; L.qwen_hip_talker_step_layers.restype = i
         L.qwen_hip_talker_get_dec_x.argtypes = [vp, vp]
         L.qwen_hip_talker_upload_kv.argtypes = [vp, vp, vp, i, i]; L.qwen_hip_talker_upload_kv.restype = i
         L.qwen_hip_talker_prefill.argtypes = [vp, vp, vp, i]; L.qwen_hip_talker_prefill.restype = i
@@ -120,7 +126,7 @@ def lib():
         L.qwen_hip_op_swiglu.argtypes = [vp, vp, i]; L.qwen_hip_op_swiglu.restype = i
         L.qwen_hip_op_argmax_matvec.argtypes = [i, vp, vp, vp, i, i]; L.qwen_hip_op_argmax_matvec.restype = i
         L.qwen_hip_op_sample.argtypes = [vp, i, f, i, f, f, vp, i, vp]; L.qwen_hip_op_sample.restype = i
-        L.qwen_hip_talker_sample.argtypes = [vp, vp, vp, i, vp, i, i, i, f, i, f, f, vp, i, vp, vp, vp]
+        L.qwen_hip_talker_sample.argtypes = [vp, vp, vp, i, vp, i, i, i, C.POINTER(SampleParams), vp, i, vp, vp, vp]
         L.qwen_hip_talker_sample.restype = i
         L.qwen_hip_op_codec_sample.argtypes = [vp, i, i, f, f, i, f, f, vp, i, vp]
         L.qwen_hip_op_codec_sample.restype = i
@@ -202,6 +208,14 @@ class Talker:
         check(fn(self.h, _p(e), _p(out), pos), "talker_step")
         return out
 
+    def step_layers(self, embed, pos):
+        """One step; returns (residual after every layer [n_layers][H], final-normed hidden)."""
+        res = np.empty((self.nl, self.H), np.float32)
+        out = np.empty(self.H, np.float32)
+        e = np.ascontiguousarray(embed, np.float32)
+        check(lib().qwen_hip_talker_step_layers(self.h, _p(e), _p(res), _p(out), pos), "talker_step_layers")
+        return res, out
+
     def dec_x(self):
         out = np.empty(self.H, np.float32)
         lib().qwen_hip_talker_get_dec_x(self.h, _p(out))
@@ -237,18 +251,23 @@ class Talker:
                                            _p(toks), _p(hid)), "talker_greedy")
         return toks, hid
 
-    def sample(self, codec_head, codec_emb, embed, pos, frame0, n_steps, temp, top_k, top_p, rep, prev=(), seed=12345):
-        """Device frame loop with sampling; returns (tokens, last normed hidden, new seed)."""
-        toks = np.empty(n_steps, np.int32)
+    def sample(self, codec_head, codec_emb, embed, pos, frame0, n_steps, temp, top_k, top_p, rep, prev=(), seed=12345,
+               greedy_warmup=0, text_len=0):
+        """Device frame loop with sampling; returns (tokens generated (ends at the first EOS),
+        last normed hidden, new seed)."""
+        toks = np.full(n_steps, -1, np.int32)
         hid = np.empty(self.H, np.float32)
         pv = np.ascontiguousarray(prev, np.int32)
         sd = np.array([seed], np.uint32)
+        sp = SampleParams(temperature=temp, top_k=top_k, top_p=top_p, rep_penalty=rep, greedy_warmup=greedy_warmup,
+                          text_len=text_len)
         self._heads = (codec_head, codec_emb)
-        check(lib().qwen_hip_talker_sample(self.h, _p(codec_head), _p(codec_emb), codec_head.shape[0],
-                                           _p(np.ascontiguousarray(embed, np.float32)), pos, frame0, n_steps, temp,
-                                           top_k, top_p, rep, _p(pv) if pv.size else None, pv.size, _p(sd),
-                                           _p(toks), _p(hid)), "talker_sample")
-        return toks, hid, int(sd[0])
+        n = lib().qwen_hip_talker_sample(self.h, _p(codec_head), _p(codec_emb), codec_head.shape[0],
+                                         _p(np.ascontiguousarray(embed, np.float32)), pos, frame0, n_steps,
+                                         C.byref(sp), _p(pv) if pv.size else None, pv.size, _p(sd), _p(toks), _p(hid))
+        if n < 0:
+            raise RuntimeError(f"talker_sample failed: {last_error()}")
+        return toks[:n], hid, int(sd[0])
 
     def dequant(self, layer, which, r0, n, cols):
         out = np.empty((n, cols), np.float32)

@@ -68,7 +68,8 @@ def test_ctypes_structs_match_c_layout():
     """Compile a probe against the header and compare sizeof/offsetof with hip.py."""
     from qwen3_tts_amd import hip
     structs = {"qwen_hip_mat_t": hip.Mat, "qwen_hip_layer_t": hip.Layer,
-               "qwen_hip_talker_desc_t": hip.TalkerDesc, "qwen_hip_cp_desc_t": hip.CpDesc}
+               "qwen_hip_talker_desc_t": hip.TalkerDesc, "qwen_hip_cp_desc_t": hip.CpDesc,
+               "qwen_hip_sample_params_t": hip.SampleParams}
     lines = ['#include <stdio.h>', '#include <stddef.h>', '#include "qwen_tts_hip.h"', 'int main(void){']
     for cname, py in structs.items():
         lines.append(f'printf("{cname} size %zu\\n", sizeof({cname}));')
@@ -133,3 +134,26 @@ def test_bench_refuses_more_than_one_gpu():
                        text=True, timeout=120)
     assert r.returncode == 2
     assert "one GPU" in r.stdout
+
+
+REF_ROOT = "/root/reference"
+
+
+@pytest.mark.skipif(not os.path.isdir(REF_ROOT), reason="reference sources not present")
+def test_glue_compiles_against_reference_header():
+    """The reference-side glue (qwen3-tts_amd/glue) is real C against the reference's own
+    qwen_tts.h: it compiles warning-free with the reference's flags."""
+    glue = os.path.join(ROOT, "qwen3-tts_amd", "glue")
+    r = subprocess.run(["gcc", "-fsyntax-only", "-O3", "-mavx2", "-mfma", "-ffast-math", "-Wall", "-Wextra",
+                        "-Wno-unused-parameter", "-Werror", f"-I{REF_ROOT}", f"-I{REF_ROOT}/vendor",
+                        f"-I{REF_ROOT}/third_party/ingot/include", "-I", os.path.join(ROOT, "include"), "-I", glue,
+                        os.path.join(glue, "qwen_tts_hip_glue.c")], capture_output=True, text=True)
+    assert r.returncode == 0, r.stderr
+
+
+def test_glue_calls_only_declared_entry_points():
+    """Every library function the glue calls is declared in include/qwen_tts_hip.h."""
+    src = open(os.path.join(ROOT, "qwen3-tts_amd", "glue", "qwen_tts_hip_glue.c")).read()
+    src = re.sub(r"/\*.*?\*/", "", src, flags=re.S)
+    called = set(re.findall(r"\b(qwen_hip_(?!glue_)\w+)\s*\(", src))
+    assert called and called <= set(header_functions()), called - set(header_functions())
