@@ -287,6 +287,17 @@ int qwen_hip_op_codec_sample(const float *logits, int vocab, int frame, float eo
 /* qwen_matmat_int8 (qwen_tts_kernels.h:121-122): Y[rows][B] = (W*scale) @ X[cols][B]
  * (row-major f32, B <= 64, cols a multiple of 64) on the batched MFMA kernel. */
 int qwen_hip_op_matmat_int8(float *Y, const int8_t *W, const float *scale, const float *X, int rows, int cols, int B);
+/* No counterpart in the reference: qwen_hip_op_matmat_int8 for callers that cannot
+ * allocate device memory (code under HIP graph capture, serving loops that forbid
+ * hipMalloc).  All pointers are the caller's DEVICE buffers: Y[B][rows] and X[B][cols]
+ * stream-major f32 (row b is stream b), W int8 [rows][cols] + scale f32[rows] in the
+ * reference's encoding; launched on `stream` (a hipStream_t; NULL = the null stream),
+ * asynchronous.  The activation pieces live in a file-scope device array of
+ * 8192*3*64 + 256 bytes per GPU (held until the process ends), so cols <= 8192 (a multiple
+ * of 64) and 1 <= B <= 64; larger shapes return -1 with qwen_hip_last_error() set.
+ * Allocates nothing.  Calls that overlap on one GPU share that array and race. */
+int qwen_hip_op_matmat_int8_noalloc(float *Y, const int8_t *W, const float *scale, const float *X, int rows, int cols,
+                                    int B, void *stream);
 /* qwen_quantize_bf16_to_int8 / _q4_0 (k.c:2143, k.c:2662) run on the device; output in
  * the reference's host layout. */
 int qwen_hip_op_quantize_int8(const uint16_t *src, int rows, int cols, int8_t *dst, float *scale);
