@@ -106,6 +106,11 @@ PREFILL_WORKLOADS = {
     "talker-1.7B-prefill-S512": ("1.7B", "int8", 512, 8),
 }
 BF16_MFMA_PEAK_TFS = 2500.0
+# the device frame loop with the reference's default sampling (temperature 0.9, top-k 50,
+# repetition penalty 1.05): (shape, precision, prefill L, default timed steps)
+SAMPLED_WORKLOADS = {
+    "talker-1.7B-int8-b1-L2048-sampled": ("1.7B", "int8", 2048, 64),
+}
 # batched workloads: (shape, precision, streams, KV length range, default timed steps)
 BATCH_WORKLOADS = {
     "talker-1.7B-int8-b32-ragged": ("1.7B", "int8", 32, (128, 4096), 16),
@@ -135,7 +140,7 @@ def main():
     ap.add_argument("--steps", type=int, default=None)
     ap.add_argument("--warmup", type=int, default=None)
     ap.add_argument("--workload", default="talker-1.7B-int8-b1-L2048", choices=sorted(WORKLOADS) + sorted(BATCH_WORKLOADS) + sorted(CP_WORKLOADS)
-                    + sorted(PREFILL_WORKLOADS) + sorted(GROW_WORKLOADS))
+                    + sorted(PREFILL_WORKLOADS) + sorted(GROW_WORKLOADS) + sorted(SAMPLED_WORKLOADS))
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--kernel-launches", type=int, default=200)
@@ -157,6 +162,8 @@ def main():
         return bench_prefill(args)
     if args.workload in GROW_WORKLOADS:
         return bench_grow(args)
+    if args.workload in SAMPLED_WORKLOADS:
+        return bench_sampled(args)
     from qwen3_tts_amd import hip, synth
     shape_name, prec, Lpre, dsteps = WORKLOADS[args.workload]
     K = args.steps or dsteps
@@ -181,15 +188,22 @@ def main():
     ev = HipEvents()
     stream = L.qwen_hip_talker_stream(g.h)
 
-    # KV cache: Lpre positions of seeded synthetic bf16 K/V (values do not change timing)
+    # KV cache: Lpre positions of seeded synthetic bf16 K/V (values do not change timing),
+    # handed over with upload_kv from pageable host memory (the reference's hand-off after
+    # its CPU prefill); the upload alone is timed
     rng = np.random.default_rng(0x5EED0002)
-    t0 = time.time()
+    kv_upload = None
     if Lpre > 0:
         kvk = synth.f32_to_bf16_rne(rng.normal(0, 1.0, (s.layers, Lpre, s.kv_dim)).astype(np.float32))
         kvv = synth.f32_to_bf16_rne(rng.normal(0, 0.1, (s.layers, Lpre, s.kv_dim)).astype(np.float32))
+        t0 = time.perf_counter()
         hip.check(L.qwen_hip_talker_upload_kv(g.h, kvk.ctypes.data, kvv.ctypes.data, Lpre, Lpre), "upload_kv")
+        dt = time.perf_counter() - t0
+        kv_upload = {"positions": Lpre, "bytes": int(kvk.nbytes + kvv.nbytes), "ms": round(dt * 1e3, 2),
+                     "gbs": round((kvk.nbytes + kvv.nbytes) / dt / 1e9, 2), "source": "pageable host memory"}
+        log(f"[bench] upload_kv of {Lpre} positions ({(kvk.nbytes + kvv.nbytes) / 1e6:.0f} MB): {dt * 1e3:.1f} ms, "
+            f"{kv_upload['gbs']:.1f} GB/s")
         del kvk, kvv
-    log(f"[bench] KV cache filled to {Lpre} positions in {time.time() - t0:.2f}s")
     e0 = synth.bf16_to_f32(emb[1234])
     g.greedy(head, emb, e0, Lpre, 0, 0)     # set up the greedy loop at position Lpre (no steps)
 
@@ -205,9 +219,11 @@ def main():
         ev.rt.hipFree(src); ev.rt.hipFree(dst)
         log(f"[bench] calibration copy: {args.calib_copy_mb} MiB device to device")
 
-    # warmup, then exactly K timed steps
+    # warmup, then the loop re-seeded at position Lpre (the warmup's rows past Lpre are
+    # rewritten before they are read), then exactly K timed steps over KV Lpre .. Lpre+K
     hip.check(L.qwen_hip_talker_greedy_async(g.h, W), "warmup")
     hip.check(L.qwen_hip_talker_sync(g.h), "sync")
+    g.greedy(head, emb, e0, Lpre, 0, 0)
     ev.device_sync()
     a, b = ev.event(), ev.event()
     ev.record(a, stream)
@@ -216,7 +232,7 @@ def main():
     ms_total = ev.elapsed_ms(a, b)
     ev.device_sync()
     ms = ms_total / K
-    L_mid = Lpre + W + K / 2.0
+    L_mid = Lpre + K / 2.0
     kv_bytes = 2 * s.layers * s.kv_dim * 2       # per position, K and V
     step_bytes = weight_bytes(s, prec) + kv_bytes * (L_mid + 1) + s.codec_vocab * s.hidden * 2
     step_gbs = step_bytes / (ms * 1e-3) / 1e9
@@ -241,11 +257,14 @@ def main():
                 "kernel": (f"ps::k_pstep<{prec}> fused decode step" if fused else "unfused per-kernel path"),
                 "bytes_per_launch": int(step_bytes * K), "avg_us": round(ms_total * 1e3, 1),
                 "steps_per_launch": K}
-    # HBM bytes per launch from the committed rocprofv3 PMC passes for this workload
+    # HBM bytes per launch from the committed rocprofv3 PMC passes for this workload: the
+    # measured bytes per step at the profiled mean KV length, moved to this run's mean KV
+    # length by the K/V bytes of the difference, times K
     try:
         t = json.load(open(os.path.join(ROOT, "profiles", "pstep_traffic.json")))
-        if fused and t["workload"] == args.workload and t["steps_per_launch"] == K:
-            roofline["traffic"] = t["traffic_bytes_per_launch"]
+        if fused and t["workload"] == args.workload:
+            per_step = t["traffic_bytes_per_step"] + kv_bytes * (L_mid - t["kv_len_mid"])
+            roofline["traffic"] = int(per_step * K)
             roofline["traffic_source"] = t["source"]
     except (OSError, ValueError, KeyError):
         pass
@@ -253,7 +272,7 @@ def main():
     cpu = None
     if not args.no_cpu_baseline:
         try:
-            cpu = cpu_baseline(s, prec, g, Lpre + W + K, tens, args.cpu_seconds)
+            cpu = cpu_baseline(s, prec, g, Lpre, tens, args.cpu_seconds)
         except Exception as ex:  # the GPU number stands on its own; report why there is none
             log(f"[bench] cpu baseline failed: {ex}")
             cpu = {"value": None, "unit": "ms/step", "error": str(ex)[:200]}
@@ -264,12 +283,13 @@ def main():
         "value": round(ms, 4), "unit": "ms/step", "n_gpus": 1, "steps": K, "warmup": W,
         "ms_per_step": round(ms, 4), "higher_is_better": False, "scaling": "weak", "vs_baseline": None,
         "dtype": prec if prec != "int4" else "q4_0", "data": "synthetic (seeded N(0,0.02) random-init weights)",
-        "config": {"workload": args.workload, "batch": 1, "kv_len_start": Lpre, "layers": s.layers,
-                   "hidden": s.hidden, "inter": s.inter},
+        "config": {"workload": args.workload, "batch": 1, "kv_len_start": Lpre, "kv_len_end": Lpre + K,
+                   "layers": s.layers, "hidden": s.hidden, "inter": s.inter},
         "tokens_per_s": round(1000.0 / ms, 1),
         "step_bytes": int(step_bytes), "step_hbm_gbs": round(step_gbs, 1),
         "step_hbm_frac": round(step_gbs / HBM_PEAK_GBS, 4),
         "kernels_us": {k: round(v, 3) for k, v in kern.items()},
+        "kv_upload": kv_upload,
         "roofline": roofline, "cpu_baseline": cpu,
     }
     print(json.dumps(out), flush=True)
@@ -401,6 +421,63 @@ def bench_grow(args):
                      "kernel": (f"ps::k_pstep<{prec}> fused decode step" if fused else "unfused per-kernel path"),
                      "bytes_per_launch": int(byts * seg), "avg_us": round(total_ms / (N // seg) * 1e3, 1),
                      "steps_per_launch": seg},
+        "cpu_baseline": None,
+    }
+    print(json.dumps(out), flush=True)
+
+
+def bench_sampled(args):
+    """The Talker frame loop with the reference's default sampling on the device
+    (qwen_hip_talker_sample: step, codec head, codec-head rule, qwen_tts_sample with
+    temperature 0.9, top-k 50, top-p 1.0, repetition penalty 1.05 over the code0 history,
+    next embedding; qwen_tts.c:559, :1649-1721), 1.7B int8, KV from 2048.  It runs on the
+    per-kernel step path (the fused kernel's in-kernel head is greedy), so a step is ~140
+    launches.  value = ms per step of one K-step call, host wall clock around the call
+    (the call's own launches and its final synchronisation included)."""
+    from qwen3_tts_amd import hip, synth
+    shape_name, prec, Lpre, dsteps = SAMPLED_WORKLOADS[args.workload]
+    K = args.steps or dsteps
+    W = 16 if args.warmup is None else args.warmup
+    s = synth.SHAPES[shape_name]
+    kv_max = Lpre + K + W + 64
+    only = lambda n: not n.startswith("talker.code_predictor.")  # noqa: E731
+    tens = synth.generate(s, 0x5EED0001, 0.0, threads=int(os.environ.get("OMP_NUM_THREADS", "16")), only=only)
+    layers = hip.layers_from_tensors(tens, s)
+    cos, sin = synth.rope_tables(s.head_dim, s.rope_theta, kv_max)
+    fnorm = synth.bf16_to_f32(tens["talker.model.norm.weight"])
+    g = hip.Talker(s, layers, fnorm, cos, sin, hip.BF16, kv_max, quantize_to=hip.PREC[prec])
+    head = np.ascontiguousarray(tens["talker.codec_head.weight"])
+    emb = np.ascontiguousarray(tens["talker.model.codec_embedding.weight"])
+    rng = np.random.default_rng(0x5EED0002)
+    kvk = synth.f32_to_bf16_rne(rng.normal(0, 1.0, (s.layers, Lpre, s.kv_dim)).astype(np.float32))
+    kvv = synth.f32_to_bf16_rne(rng.normal(0, 0.1, (s.layers, Lpre, s.kv_dim)).astype(np.float32))
+    hip.check(hip.lib().qwen_hip_talker_upload_kv(g.h, kvk.ctypes.data, kvv.ctypes.data, Lpre, Lpre), "upload_kv")
+    del kvk, kvv
+    e0 = synth.bf16_to_f32(emb[1234])
+    g.sample(head, emb, e0, Lpre, 10, W, 0.9, 50, 1.0, 1.05, (), 1234)          # warmup (uploads the heads)
+    t0 = time.perf_counter()
+    toks, _, _ = g.sample(head, emb, e0, Lpre, 10, K, 0.9, 50, 1.0, 1.05, (), 4321)
+    dt = time.perf_counter() - t0
+    g.free()
+    n = len(toks)                                     # < K only if EOS came first
+    ms = dt * 1e3 / max(n, 1)
+    L_mid = Lpre + n / 2.0
+    kv_bytes = 2 * s.layers * s.kv_dim * 2
+    step_bytes = weight_bytes(s, prec) + kv_bytes * (L_mid + 1) + s.codec_vocab * s.hidden * 2
+    gbs = step_bytes / (ms * 1e-3) / 1e9
+    log(f"[bench] sampled loop: {n} steps, {ms * 1e3:.1f} us/step, {gbs:.0f} GB/s algorithmic")
+    out = {
+        "metric": "Talker ms/decode-step (0.6B/1.7B, bf16/int8/int4) + achieved HBM GB/s",
+        "value": round(ms, 4), "unit": "ms/step", "n_gpus": 1, "steps": n, "warmup": W,
+        "ms_per_step": round(ms, 4), "higher_is_better": False, "scaling": "weak", "vs_baseline": None,
+        "dtype": prec, "data": "synthetic (seeded N(0,0.02) random-init weights)",
+        "config": {"workload": args.workload, "batch": 1, "kv_len_start": Lpre, "layers": s.layers,
+                   "hidden": s.hidden, "inter": s.inter, "temperature": 0.9, "top_k": 50, "rep_penalty": 1.05},
+        "tokens_per_s": round(1000.0 / ms, 1),
+        "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": "sampled frame loop (per-kernel step + codec head + k_sample + gather), whole call",
+                     "bytes_per_launch": int(step_bytes * n), "avg_us": round(dt * 1e6, 1), "steps_per_launch": n},
         "cpu_baseline": None,
     }
     print(json.dumps(out), flush=True)
@@ -617,11 +694,24 @@ def cpu_baseline_cp(s, prec, tens, th, seconds):
                       f"-O3 -ffast-math), same weights"}
 
 
+def host_info():
+    """CPU model and logical CPU count of this host (/proc/cpuinfo)."""
+    model, n = "unknown", 0
+    for ln in open("/proc/cpuinfo"):
+        if ln.startswith("model name") and model == "unknown":
+            model = ln.split(":", 1)[1].strip()
+        if ln.startswith("processor"):
+            n += 1
+    return model, n
+
+
 def cpu_baseline(s, prec, g, kv_len, tens, seconds):
     """The reference's own qwen_talker_step (oracle/_ref, reference flags) on a bounded
     sample: same weights (written to safetensors and loaded + quantized by the
-    reference loader), KV = the device's first kv_len positions, timed steps until
-    about `seconds` of CPU work.  Threads = OMP_NUM_THREADS (the box's CPU share)."""
+    reference loader), KV = the device's first kv_len positions; consecutive steps timed
+    one by one (clock_gettime around each qwen_talker_step, as the reference times
+    itself), first with N threads (OMP_NUM_THREADS, the box's CPU share) for about
+    `seconds`, then with 1 thread for about half that.  value = the N-thread median."""
     sys.path.insert(0, ROOT)
     from oracle.oracle import RefModel
     from qwen3_tts_amd import synth
@@ -637,24 +727,32 @@ def cpu_baseline(s, prec, g, kv_len, tens, seconds):
         del full
         ref = RefModel(d, s, prec=prec, threads=threads, variant=variant)
     log(f"[bench] cpu baseline: reference loaded + quantized in {time.time() - t0:.1f}s ({variant or '_avx2'})")
-    # reference KV <- device KV (the reference grows its cache by doubling on demand)
     kk, vv = g.download_kv(kv_len)
-    rk, rv = ref.kv()
-    n0 = min(kv_len, rk.shape[1])
-    rk[:, :n0] = kk[:, :n0]
-    rv[:, :n0] = vv[:, :n0]
-    ref.kv_len = n0
+    ref.set_kv(kk, vv, kv_len)
     emb = tens["talker.model.codec_embedding.weight"]
     e = np.stack([synth.bf16_to_f32(emb[i * 7 + 1]) for i in range(64)])
     out = np.empty(s.hidden, np.float32)
-    warm = ref.lib.ref_time_talker_steps(ref.h, e.ctypes.data, 2, out.ctypes.data) / 2
-    n = int(max(2, min(64, seconds / max(warm, 1e-3))))
-    dt = ref.lib.ref_time_talker_steps(ref.h, e.ctypes.data, n, out.ctypes.data)
-    ms = dt / n * 1e3
-    log(f"[bench] cpu baseline: {n} steps at L~{n0}: {ms:.1f} ms/step ({threads} threads)")
-    return {"value": round(ms, 3), "unit": "ms/step", "cores": threads, "kind": "reference",
-            "sample": f"{n} reference qwen_talker_step calls ({prec}, {variant.strip('_') or 'avx2'} build, "
-                      f"-O3 -ffast-math) at KV length {n0}..{n0 + n + 2}, same weights and KV as the GPU run"}
+    runs = {}
+    for nt, budget in ((threads, seconds), (1, seconds / 2)):
+        ref.lib.ref_set_threads(nt)
+        ref.kv_len = kv_len
+        w = np.empty(1, np.float64)
+        ref.lib.ref_time_talker_steps_each(ref.h, e.ctypes.data, 1, out.ctypes.data, w.ctypes.data)
+        n = int(max(3, min(64, budget / max(w[0], 1e-3))))
+        ref.kv_len = kv_len
+        ts = np.empty(n, np.float64)
+        ref.lib.ref_time_talker_steps_each(ref.h, e.ctypes.data, n, out.ctypes.data, ts.ctypes.data)
+        runs[nt] = {"threads": nt, "steps": n, "median_ms": round(float(np.median(ts)) * 1e3, 3),
+                    "p90_ms": round(float(np.percentile(ts, 90)) * 1e3, 3), "mean_ms": round(float(ts.mean()) * 1e3, 3)}
+        log(f"[bench] cpu baseline: {n} steps at KV {kv_len}, {nt} threads: median {runs[nt]['median_ms']:.1f} ms, "
+            f"p90 {runs[nt]['p90_ms']:.1f} ms")
+    model, ncpu = host_info()
+    return {"value": runs[threads]["median_ms"], "unit": "ms/step", "cores": threads, "kind": "reference",
+            "sample": f"{runs[threads]['steps']} consecutive reference qwen_talker_step calls ({prec}, "
+                      f"{variant.strip('_') or 'avx2'} build, -O3 -ffast-math) from KV length {kv_len}, same weights "
+                      f"and KV as the GPU run; median of per-step clock_gettime times",
+            "runs": [runs[threads], runs[1]], "host_cpu": model, "host_logical_cpus": ncpu,
+            "compiler": ref.lib.ref_build_info().decode()}
 
 
 if __name__ == "__main__":

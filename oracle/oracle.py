@@ -234,6 +234,8 @@ class RefModel:
         L.ref_f32_to_f16.argtypes = [f]; L.ref_f32_to_f16.restype = C.c_uint16
         L.ref_f16_to_f32.argtypes = [C.c_uint16]; L.ref_f16_to_f32.restype = f
         L.ref_time_talker_steps.argtypes = [vp, vp, i, vp]; L.ref_time_talker_steps.restype = C.c_double
+        L.ref_time_talker_steps_each.argtypes = [vp, vp, i, vp, vp]
+        L.ref_build_info.restype = C.c_char_p
         return L
 
     def __init__(self, model_dir, shape, prec="bf16", threads=1, variant=""):

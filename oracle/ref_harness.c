@@ -302,6 +302,22 @@ double ref_time_talker_steps(void *hp, const float *embeds, int n, float *hidden
     return (double)(t1.tv_sec - t0.tv_sec) + 1e-9 * (double)(t1.tv_nsec - t0.tv_nsec);
 }
 
+/* Same, with each step's wall time in seconds in times[n] (median / p90 for the baseline). */
+void ref_time_talker_steps_each(void *hp, const float *embeds, int n, float *hidden_out, double *times) {
+    ref_handle_t *h = (ref_handle_t *)hp;
+    int H = h->ctx->config.hidden_size;
+    for (int i = 0; i < n; i++) {
+        struct timespec t0, t1;
+        clock_gettime(CLOCK_MONOTONIC, &t0);
+        qwen_talker_step(h->ctx, (float *)(embeds + (size_t)i * H), hidden_out);
+        clock_gettime(CLOCK_MONOTONIC, &t1);
+        times[i] = (double)(t1.tv_sec - t0.tv_sec) + 1e-9 * (double)(t1.tv_nsec - t0.tv_nsec);
+    }
+}
+
+/* compiler that built this harness and the reference objects (same make run) */
+const char *ref_build_info(void) { return "gcc " __VERSION__; }
+
 /* per-head RMSNorm passthrough (checker for the device KV append) */
 void ref_rms_norm_per_head(float *x, const float *w, int seq, int n_heads, int head_dim, float eps) {
     qwen_rms_norm_per_head(x, w, seq, n_heads, head_dim, eps);
