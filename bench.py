@@ -111,6 +111,12 @@ BF16_MFMA_PEAK_TFS = 2500.0
 SAMPLED_WORKLOADS = {
     "talker-1.7B-int8-b1-L2048-sampled": ("1.7B", "int8", 2048, 64),
 }
+# the whole frame loop on the device (qwen_hip_generate: code0 sampling, CP frame, next
+# input, Talker step) at the reference's defaults: (shape, precision, prefill L, frames)
+FRAME_WORKLOADS = {
+    "frame-0.6B-bf16-sampled": ("0.6B", "bf16", 256, 64),
+    "frame-1.7B-int8-sampled": ("1.7B", "int8", 2048, 64),
+}
 # batched workloads: (shape, precision, streams, KV length range, default timed steps)
 BATCH_WORKLOADS = {
     "talker-1.7B-int8-b32-ragged": ("1.7B", "int8", 32, (128, 4096), 16),
@@ -140,7 +146,8 @@ def main():
     ap.add_argument("--steps", type=int, default=None)
     ap.add_argument("--warmup", type=int, default=None)
     ap.add_argument("--workload", default="talker-1.7B-int8-b1-L2048", choices=sorted(WORKLOADS) + sorted(BATCH_WORKLOADS) + sorted(CP_WORKLOADS)
-                    + sorted(PREFILL_WORKLOADS) + sorted(GROW_WORKLOADS) + sorted(SAMPLED_WORKLOADS))
+                    + sorted(PREFILL_WORKLOADS) + sorted(GROW_WORKLOADS) + sorted(SAMPLED_WORKLOADS)
+                    + sorted(FRAME_WORKLOADS))
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--kernel-launches", type=int, default=200)
@@ -164,6 +171,8 @@ def main():
         return bench_grow(args)
     if args.workload in SAMPLED_WORKLOADS:
         return bench_sampled(args)
+    if args.workload in FRAME_WORKLOADS:
+        return bench_frames(args)
     from qwen3_tts_amd import hip, synth
     shape_name, prec, Lpre, dsteps = WORKLOADS[args.workload]
     K = args.steps or dsteps
@@ -478,6 +487,75 @@ def bench_sampled(args):
                      "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
                      "kernel": "sampled frame loop (per-kernel step + codec head + k_sample + gather), whole call",
                      "bytes_per_launch": int(step_bytes * n), "avg_us": round(dt * 1e6, 1), "steps_per_launch": n},
+        "cpu_baseline": None,
+    }
+    print(json.dumps(out), flush=True)
+
+
+def bench_frames(args):
+    """The whole frame loop of qwen_tts_generate on the device (qwen_hip_generate,
+    qwen_tts.c:1649-1778): per frame code0 from the codec head with the reference's default
+    sampling (temperature 0.9, top-k 50, repetition penalty 1.05), the Code Predictor frame
+    (16 passes of 5 layers + 15 lm-head picks, one captured graph), the next input
+    (codec + 15 CP embeddings + tts_pad) and one Talker step (fused kernel), with the KV
+    cache holding L positions first.  value = ms per frame of one K-frame call (host wall
+    clock around the call, its final synchronisation included); frames/s; the reference's
+    real-time bar is 12.5 frames/s of audio (80 ms per frame)."""
+    from qwen3_tts_amd import hip, synth
+    shape_name, prec, Lpre, dframes = FRAME_WORKLOADS[args.workload]
+    K = args.steps or dframes
+    W = 8 if args.warmup is None else args.warmup
+    s = synth.SHAPES[shape_name]
+    kv_max = Lpre + K + W + 64
+    tens = synth.generate(s, 0x5EED0001, 0.0, threads=int(os.environ.get("OMP_NUM_THREADS", "16")))
+    layers = hip.layers_from_tensors(tens, s)
+    cos, sin = synth.rope_tables(s.head_dim, s.rope_theta, kv_max)
+    fnorm = synth.bf16_to_f32(tens["talker.model.norm.weight"])
+    g = hip.Talker(s, layers, fnorm, cos, sin, hip.BF16, kv_max, quantize_to=hip.PREC[prec])
+    cp = hip.cp_from_tensors(tens, s, hip.PREC[prec])
+    head = np.ascontiguousarray(tens["talker.codec_head.weight"])
+    emb = np.ascontiguousarray(tens["talker.model.codec_embedding.weight"])
+    rng = np.random.default_rng(0x5EED0002)
+    kvk = synth.f32_to_bf16_rne(rng.normal(0, 1.0, (s.layers, Lpre, s.kv_dim)).astype(np.float32))
+    kvv = synth.f32_to_bf16_rne(rng.normal(0, 0.1, (s.layers, Lpre, s.kv_dim)).astype(np.float32))
+    hip.check(hip.lib().qwen_hip_talker_upload_kv(g.h, kvk.ctypes.data, kvv.ctypes.data, Lpre, Lpre), "upload_kv")
+    del kvk, kvv
+    h0 = rng.standard_normal(s.hidden).astype(np.float32)
+    h0 /= np.sqrt((h0 ** 2).mean())
+    pad = (rng.standard_normal(s.hidden) * 0.02).astype(np.float32)
+    hip.generate(g, cp, head, emb, pad, h0, Lpre, 0, W, 0.9, 50, 1.0, 1.05, (), 99)        # warmup, graph capture
+    t0 = time.perf_counter()
+    codes, eos, _, _ = hip.generate(g, cp, head, emb, pad, h0, Lpre, 0, K, 0.9, 50, 1.0, 1.05, (), 4321)
+    dt = time.perf_counter() - t0
+    fused = bool(hip.lib().qwen_hip_talker_fused(g.h))
+    cp.free()
+    g.free()
+    n = len(codes) + (1 if eos is not None else 0)    # frames whose work ran before EOS ended the utterance
+    ms = dt * 1e3 / K
+    log(f"[bench] frame loop: {K} frames ({len(codes)} generated{' + EOS' if eos is not None else ''}), "
+        f"{ms:.3f} ms/frame, {1000.0 / ms:.0f} frames/s")
+    wb = (lambda r, c: r * c * 2) if prec == "bf16" else (lambda r, c: r * c + 4 * r)
+    per_layer = 0
+    for r, c in [(s.cp_heads * s.cp_head_dim + 2 * s.cp_kv_heads * s.cp_head_dim, s.cp_hidden),
+                 (s.cp_hidden, s.cp_heads * s.cp_head_dim), (2 * s.cp_inter, s.cp_hidden), (s.cp_hidden, s.cp_inter)]:
+        per_layer += wb(r, c)
+    cp_bytes = 16 * s.cp_layers * per_layer + 15 * wb(s.codebook, s.cp_hidden)
+    kv_bytes = 2 * s.layers * s.kv_dim * 2
+    frame_bytes = weight_bytes(s, prec) + kv_bytes * (Lpre + K / 2.0 + 1) + s.codec_vocab * s.hidden * 2 + cp_bytes
+    gbs = frame_bytes / (ms * 1e-3) / 1e9
+    out = {
+        "metric": "Talker ms/decode-step (0.6B/1.7B, bf16/int8/int4) + achieved HBM GB/s",
+        "value": round(ms, 4), "unit": "ms/frame", "n_gpus": 1, "steps": K, "warmup": W,
+        "ms_per_step": round(ms, 4), "higher_is_better": False, "scaling": "weak", "vs_baseline": None,
+        "dtype": prec, "data": "synthetic (seeded N(0,0.02) random-init weights)",
+        "config": {"workload": args.workload, "kv_len_start": Lpre, "layers": s.layers, "cp_layers": s.cp_layers,
+                   "hidden": s.hidden, "temperature": 0.9, "top_k": 50, "rep_penalty": 1.05,
+                   "talker_step": "fused" if fused else "per-kernel"},
+        "frames_per_s": round(1000.0 / ms, 1), "frames_generated": len(codes), "eos": eos is not None,
+        "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": "frame loop (head + k_sample + CP frame graph + k_frame_embed + k_pstep), whole call",
+                     "bytes_per_launch": int(frame_bytes * K), "avg_us": round(dt * 1e6, 1), "steps_per_launch": K},
         "cpu_baseline": None,
     }
     print(json.dumps(out), flush=True)

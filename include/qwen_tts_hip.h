@@ -272,6 +272,22 @@ typedef struct {
 int qwen_hip_talker_sample(void *state, const uint16_t *codec_head, const uint16_t *codec_emb, int codec_vocab,
                            const float *embed, int pos, int frame0, int n_steps, const qwen_hip_sample_params_t *params,
                            const int *prev_tokens, int n_prev, uint32_t *seed, int *tokens_out, float *hidden_out);
+/* The whole frame loop of qwen_tts_generate (qwen_tts.c:1649-1778, non-streaming) on the
+ * device, no counterpart as one call in the reference: per frame, codec head over the last
+ * normed hidden state -> codec-head rule + qwen_tts_sample (params; the code0 history
+ * prev_tokens + the tokens drawn here; *seed the LCG state in and out) -> the CP frame of
+ * cp_state for that hidden state and code0 (qwen_cp_predict, cp.c:926-1045) -> next input
+ * codec_emb[code0] + sum_g cp_codec_emb[g][code_g] + tts_pad (host f32[hidden], the text
+ * side's pad embedding) -> one Talker step at pos + f.  hidden0: the normed hidden state
+ * the loop starts from (host f32[hidden]: the prefill's last position, or the previous
+ * call's hidden_out).  codes_out[n_frames][16] = code0 then the 15 CP codes.  As in the
+ * reference the frame whose code0 is EOS ends the utterance (codes_out[n][0] == 2150 marks
+ * it when n < n_frames).  Returns the number of frames generated, or -1.  One host sync per
+ * call; allocates nothing; the CP state must not be used elsewhere meanwhile. */
+int qwen_hip_generate(void *talker_state, void *cp_state, const uint16_t *codec_head, const uint16_t *codec_emb,
+                      int codec_vocab, const float *tts_pad, const float *hidden0, int pos, int frame0, int n_frames,
+                      const qwen_hip_sample_params_t *params, const int *prev_tokens, int n_prev, uint32_t *seed,
+                      int *codes_out, float *hidden_out);
 /* Token sampling on the device: qwen_tts_sample (qwen_tts_sampling.c:160-202; repetition
  * penalty, temperature softmax, top-k, top-p, renormalisation, LCG draw) with the
  * thread-local LCG state of qwen_set_seed / qwen_get_seed (sampling.c:38-49) passed as

@@ -338,3 +338,36 @@ extern "C" hipError_t qt_launch_kv_relayout(const uint16_t *src, uint16_t *dst, 
                        hd, (long long)kv_max, to_heads);
     return hipGetLastError();
 }
+
+// Next Talker input of the frame loop (qwen_tts.c:1768-1778): e = codec_emb[code0] (bf16 -> f32,
+// zeros for an out-of-range code, lookup_codec_embed qwen_tts.c:919-924), then += each CP
+// group's embedding row cp_emb[g][codes[g + 1]] in g order (skipped when out of range,
+// qwen_bf16_accum_f32 k.c:3900-3925), then += tts_pad; one f32 add at a time per element,
+// as the reference does, so the result is bit-identical.  codes[0] = code0, codes[1..15].
+struct QtFrameEmb { const uint16_t *g[15]; };
+__global__ void k_frame_embed(const int *codes, int vocab, int codebook, const uint16_t *codec_emb, QtFrameEmb cp,
+                              const float *pad, int H, float *out) {
+    const int c0 = codes[0];
+    int cg[15];
+#pragma unroll
+    for (int g = 0; g < 15; g++) cg[g] = codes[g + 1];
+    for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < H; i += gridDim.x * blockDim.x) {
+        float e = (c0 >= 0 && c0 < vocab) ? bf16f(codec_emb[(size_t)c0 * H + i]) : 0.0f;
+#pragma unroll
+        for (int g = 0; g < 15; g++)
+            if (cg[g] >= 0 && cg[g] < codebook) e = __fadd_rn(e, bf16f(cp.g[g][(size_t)cg[g] * H + i]));
+        out[i] = __fadd_rn(e, pad[i]);
+    }
+}
+extern "C" hipError_t qt_launch_frame_embed(const int *codes, int vocab, int codebook, const uint16_t *codec_emb,
+                                            const uint16_t *const cp_emb[15], const float *pad, int H, float *out,
+                                            hipStream_t st) {
+    QtFrameEmb cp;
+    for (int g = 0; g < 15; g++) {
+        if (!cp_emb[g]) return hipErrorInvalidValue;
+        cp.g[g] = cp_emb[g];
+    }
+    hipLaunchKernelGGL(k_frame_embed, dim3((H + 255) / 256), dim3(256), 0, st, codes, vocab, codebook, codec_emb, cp, pad,
+                       H, out);
+    return hipGetLastError();
+}

@@ -295,6 +295,9 @@ typedef struct {
     int *smp_hist;
     uint32_t *smp_seed;
     int *smp_done;
+    /* device frame loop: the 16 codes of every frame of a call, the text-side pad embedding */
+    int *gen_codes;         /* [QT_SAMPLE_HIST_MAX][16] */
+    float *gen_pad;         /* [H] */
     /* persistent single-kernel step (qt_pstep.hip) */
     int ps_on;
     void *ps_layers;        /* device layer table */
@@ -330,7 +333,7 @@ static void talker_destroy(talker_t *t) {
     }
     stack_free(&t->s);
     void *bufs[] = {t->io, t->d_pos, t->d_frame, t->d_tok, t->d_hist, t->codec_head, t->codec_emb, t->logits,
-                    t->smp_hist, t->smp_seed, t->smp_done,
+                    t->smp_hist, t->smp_seed, t->smp_done, t->gen_codes, t->gen_pad,
                     t->ps_layers, t->ps_ring, t->ps_xin, t->ps_epoch, t->ps_err,
                     t->pf_x, t->pf_qkvb, t->pf_attn, t->pf_h, t->pf_p, t->pf_part};
     for (size_t i = 0; i < sizeof bufs / sizeof bufs[0]; i++) if (bufs[i]) (void)hipFree(bufs[i]);
@@ -410,6 +413,8 @@ void *qwen_hip_talker_init(const qwen_hip_talker_desc_t *desc) {
     HCK(hipMalloc((void **)&t->smp_hist, (size_t)QT_SAMPLE_HIST_MAX * sizeof(int)));
     HCK(hipMalloc((void **)&t->smp_seed, 64));
     HCK(hipMalloc((void **)&t->smp_done, 64));
+    HCK(hipMalloc((void **)&t->gen_codes, (size_t)QT_SAMPLE_HIST_MAX * 16 * sizeof(int)));
+    HCK(hipMalloc((void **)&t->gen_pad, (size_t)H * sizeof(float)));
     HCK(hipHostMalloc((void **)&t->h_in, (size_t)H * sizeof(float), hipHostMallocDefault));
     HCK(hipHostMalloc((void **)&t->h_out, (size_t)2 * H * sizeof(float), hipHostMallocDefault));
     HCK(hipHostMalloc((void **)&t->h_pos, 4 * sizeof(int), hipHostMallocDefault));
@@ -1240,6 +1245,16 @@ static hipError_t cp_frame_body(void *a) {
     return hipSuccess;
 }
 
+/* cp_frame_body with every launch on stream st (the ungraphed frame inside another
+ * state's stream, for QWEN_HIP_GRAPH=0) */
+static hipError_t cp_frame_body_on(cp_t *c, hipStream_t st) {
+    hipStream_t own = c->st;
+    c->st = st;
+    hipError_t e = cp_frame_body(c);
+    c->st = own;
+    return e;
+}
+
 int qwen_hip_cp_frame(void *state, const float *talker_hidden, int code0, int *out_codes) {
     cp_t *c = (cp_t *)state;
     if (!c || c->dead) { SETERR("CP state is dead or NULL"); return -1; }
@@ -1304,6 +1319,115 @@ int qwen_hip_cp_step(void *state, float *x, int pos) {
     return 0;
 fail:
     if (c) c->dead = 1;
+    return -1;
+}
+
+/* ---- the whole frame loop on the device ------------------------------------------------- */
+
+/* The Talker + Code Predictor frame loop of qwen_tts_generate (qwen_tts.c:1649-1778, the
+ * non-streaming path) with no host round trip per frame.  Per frame f, on the Talker's
+ * stream: codec head over the last normed hidden state -> codec-head rule (EOS boost,
+ * greedy warmup) + qwen_tts_sample with the code0 history (k_sample) -> the CP frame
+ * (its captured graph: mtp projection, 16 passes, 15 greedy lm-head picks) for that
+ * hidden state and code0 -> next input codec_emb[code0] + sum_g cp_codec_emb[g][code_g] +
+ * tts_pad (k_frame_embed) -> one Talker step (the fused persistent kernel reading that
+ * input from device memory, or the per-kernel step).  hidden0 is the normed hidden state
+ * the loop starts from (the prefill's last position, or the previous call's last step);
+ * the first step runs at pos.  As in the reference, the frame whose code0 is EOS ends the
+ * utterance: it is not a frame, and from it on the sampler draws nothing (the LCG state
+ * and the history stop there); the remaining frames' work runs and is discarded.
+ * codes_out[n_frames][16] (code0, then the 15 CP codes); returns the number of frames
+ * generated (codes_out[n][0] == 2150 marks where EOS was drawn, when n < n_frames), or -1.
+ * The CP state must not be used on its own stream meanwhile.  Allocates nothing. */
+int qwen_hip_generate(void *talker_state, void *cp_state, const uint16_t *codec_head, const uint16_t *codec_emb,
+                      int codec_vocab, const float *tts_pad, const float *hidden0, int pos, int frame0, int n_frames,
+                      const qwen_hip_sample_params_t *sp, const int *prev_tokens, int n_prev, uint32_t *seed,
+                      int *codes_out, float *hidden_out) {
+    talker_t *t = (talker_t *)talker_state;
+    cp_t *c = (cp_t *)cp_state;
+    if (!t || t->dead || !c || c->dead) { SETERR("generate: talker or CP state is dead or NULL"); return -1; }
+    const int H = t->s.H;
+    if (!codec_head || !codec_emb || codec_vocab <= 2150 || codec_vocab > 4096 || !tts_pad || !hidden0 || !sp || !seed ||
+        (n_frames > 0 && !codes_out) || n_frames < 0 || frame0 < 0 || n_prev < 0 || (n_prev > 0 && !prev_tokens)) {
+        SETERR("generate: bad arguments"); return -1;
+    }
+    if (c->talker_hidden != H || c->codec_vocab != codec_vocab || c->emb_dim != H) {
+        SETERR("generate: CP state built for talker hidden %d / vocab %d / emb_dim %d, Talker has %d / %d",
+               c->talker_hidden, c->codec_vocab, c->emb_dim, H, codec_vocab);
+        return -1;
+    }
+    if ((long long)n_prev + n_frames + 1 > QT_SAMPLE_HIST_MAX) {
+        SETERR("generate: history of %d + %d tokens exceeds %d", n_prev, n_frames, QT_SAMPLE_HIST_MAX - 1); return -1;
+    }
+    if (pos < 0 || pos + n_frames > t->s.kv_max || pos + n_frames > t->s.rope_len) {
+        SETERR("generate: positions exceed kv_max"); return -1;
+    }
+    if (head_setup(t, codec_head, codec_emb, codec_vocab) != 0) goto fail;
+    if (graphs_enabled() && !c->fready) {
+        if (capture(c->st, &c->fexec, cp_frame_body, c) != 0) goto fail;
+        c->fready = 1;
+    }
+    HCK(hipStreamSynchronize(c->st));               /* nothing of the CP's own stream still runs */
+    c->frame_ready = 1;
+    if (talker_set_pos(t, pos) != 0) goto fail;
+    if (n_prev > 0) HCK(hipMemcpyAsync(t->smp_hist, prev_tokens, (size_t)n_prev * sizeof(int), hipMemcpyHostToDevice, t->st));
+    t->h_pos[2] = (int)*seed;
+    t->h_pos[3] = 0;
+    HCK(hipMemcpyAsync(t->smp_seed, t->h_pos + 2, sizeof(uint32_t), hipMemcpyHostToDevice, t->st));
+    HCK(hipMemcpyAsync(t->smp_done, t->h_pos + 3, sizeof(int), hipMemcpyHostToDevice, t->st));
+    HCK(hipMemcpyAsync(t->gen_pad, tts_pad, (size_t)H * sizeof(float), hipMemcpyHostToDevice, t->st));
+    memcpy(t->h_in, hidden0, (size_t)H * sizeof(float));
+    HCK(hipMemcpyAsync(t->io, t->h_in, (size_t)H * sizeof(float), hipMemcpyHostToDevice, t->st));
+    {
+        const uint16_t *cpe[15];
+        for (int g = 0; g < 15; g++) cpe[g] = c->cp_emb[g];
+        const int expected = sp->text_len * 3, boost_start = expected * 2;
+        for (int i = 0; i < n_frames; i++) {
+            const int frame = frame0 + i;
+            float boost = 0.0f;
+            if (expected > 0 && frame > boost_start) {
+                boost = 0.5f * (float)(frame - boost_start);
+                if (boost > 10.0f) boost = 10.0f;
+            }
+            const int warm = sp->greedy_warmup > 0 && frame < sp->greedy_warmup;
+            int *tok = t->smp_hist + n_prev + i;
+            /* code0 from the last normed hidden state (io[0:H]) */
+            HCK(qt_launch_mv(t->head_m.prec, QT_EPI_STORE, 0, t->io, NULL, t->s.eps, t->head_m.w, NULL, NULL,
+                             t->head_m.rows, t->head_m.cols, t->logits, NULL, NULL, NULL, t->st));
+            HCK(qt_launch_sample(t->logits, codec_vocab, 1, frame, boost, warm ? 0.0f : sp->temperature,
+                                 warm ? 1 : sp->top_k, sp->top_p, sp->rep_penalty, t->smp_hist, n_prev + i, t->smp_seed,
+                                 tok, t->smp_done, t->st));
+            /* the CP frame for (hidden, code0) */
+            HCK(qt_launch_copy_f32(t->io, c->th, H, t->st));
+            HCK(hipMemcpyAsync(c->d_codes, tok, sizeof(int), hipMemcpyDeviceToDevice, t->st));
+            HCK(graphs_enabled() ? hipGraphLaunch(c->fexec, t->st) : cp_frame_body_on(c, t->st));
+            HCK(hipMemcpyAsync(t->gen_codes + (size_t)16 * i, c->d_codes, 16 * sizeof(int), hipMemcpyDeviceToDevice, t->st));
+            /* next input, then the Talker step */
+            float *xin = t->ps_on ? t->ps_xin : t->io + H;
+            HCK(qt_launch_frame_embed(c->d_codes, codec_vocab, c->codebook, t->codec_emb, cpe, t->gen_pad, H, xin, t->st));
+            if (t->ps_on) HCK(ps_launch(t, 1, 0));
+            else HCK(talker_body(t));
+        }
+    }
+    if (n_frames > 0)
+        HCK(hipMemcpyAsync(codes_out, t->gen_codes, (size_t)n_frames * 16 * sizeof(int), hipMemcpyDeviceToHost, t->st));
+    HCK(hipMemcpyAsync(t->h_pos + 2, t->smp_seed, sizeof(uint32_t), hipMemcpyDeviceToHost, t->st));
+    HCK(hipMemcpyAsync(t->h_out, t->io, (size_t)2 * H * sizeof(float), hipMemcpyDeviceToHost, t->st));
+    if (t->ps_on) HCK(hipMemcpyAsync(t->h_err, t->ps_err, sizeof(int), hipMemcpyDeviceToHost, t->st));
+    HCK(hipStreamSynchronize(t->st));
+    if (t->ps_on && ps_check(t) != 0) goto fail;
+    *seed = (uint32_t)t->h_pos[2];
+    if (hidden_out) memcpy(hidden_out, t->h_out, (size_t)H * sizeof(float));
+    t->dev_pos = pos + n_frames;
+    t->greedy_ready = 0;
+    {
+        int n_gen = n_frames;
+        for (int i = 0; i < n_frames; i++)
+            if (codes_out[(size_t)16 * i] == 2150) { n_gen = i; break; }
+        return n_gen;
+    }
+fail:
+    t->dead = 1; t->dev_pos = -1;
     return -1;
 }
 

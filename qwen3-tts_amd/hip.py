@@ -36,6 +36,7 @@ EXPORTS = [
     "qwen_hip_cp_set_prefill2", "qwen_hip_cp_prefill2",
     "qwen_hip_talker_prefill", "qwen_hip_talker_prefill_async", "qwen_hip_op_prefill_gemm",
     "qwen_hip_op_prefill_attention", "qwen_hip_talker_step_layers", "qwen_hip_op_matmat_int8_noalloc",
+    "qwen_hip_generate",
 ]
 
 
@@ -128,6 +129,8 @@ def lib():
         L.qwen_hip_op_sample.argtypes = [vp, i, f, i, f, f, vp, i, vp]; L.qwen_hip_op_sample.restype = i
         L.qwen_hip_talker_sample.argtypes = [vp, vp, vp, i, vp, i, i, i, C.POINTER(SampleParams), vp, i, vp, vp, vp]
         L.qwen_hip_talker_sample.restype = i
+        L.qwen_hip_generate.argtypes = [vp, vp, vp, vp, i, vp, vp, i, i, i, C.POINTER(SampleParams), vp, i, vp, vp, vp]
+        L.qwen_hip_generate.restype = i
         L.qwen_hip_op_codec_sample.argtypes = [vp, i, i, f, f, i, f, f, vp, i, vp]
         L.qwen_hip_op_codec_sample.restype = i
         L.qwen_hip_op_quantize_int8.argtypes = [vp, i, i, vp, vp]; L.qwen_hip_op_quantize_int8.restype = i
@@ -288,6 +291,26 @@ class Talker:
             pass
 
 
+def generate(talker, cp, codec_head, codec_emb, tts_pad, hidden0, pos, frame0, n_frames, temp=0.0, top_k=0,
+             top_p=1.0, rep=1.0, prev=(), seed=12345, greedy_warmup=0, text_len=0):
+    """The device frame loop (qwen_hip_generate): returns (codes [n][16] of the frames
+    generated, the codes row of the EOS frame or None, last normed hidden, new seed)."""
+    codes = np.full((n_frames, 16), -1, np.int32)
+    hid = np.empty(talker.H, np.float32)
+    pv = np.ascontiguousarray(prev, np.int32)
+    sd = np.array([seed], np.uint32)
+    sp = SampleParams(temperature=temp, top_k=top_k, top_p=top_p, rep_penalty=rep, greedy_warmup=greedy_warmup,
+                      text_len=text_len)
+    talker._heads = (codec_head, codec_emb)
+    n = lib().qwen_hip_generate(talker.h, cp.h, _p(codec_head), _p(codec_emb), codec_head.shape[0],
+                                _p(np.ascontiguousarray(tts_pad, np.float32)),
+                                _p(np.ascontiguousarray(hidden0, np.float32)), pos, frame0, n_frames, C.byref(sp),
+                                _p(pv) if pv.size else None, pv.size, _p(sd), _p(codes), _p(hid))
+    if n < 0:
+        raise RuntimeError(f"generate failed: {last_error()}")
+    return codes[:n], (codes[n] if n < n_frames else None), hid, int(sd[0])
+
+
 class TalkerBatch:
     """B streams over a Talker's resident weights (qwen_hip_talker_batch_*)."""
 
@@ -388,12 +411,10 @@ class CodePredictor:
 def cp_from_tensors(t, shape, prec=BF16, cp_kv_max=64):
     """A CodePredictor (bf16 weights, optionally quantized on the device to ``prec``) over
     synth tensors {reference name: bf16 array}: CP layers, cp_norm, the 15 lm heads and
-    codec embeddings, the Talker codec embedding.  No small_to_mtp_projection (the
-    Talker and CP hidden sizes must agree, as in the 0.6B model)."""
+    codec embeddings, the Talker codec embedding, and (when the Talker and CP hidden sizes
+    differ, as in the 1.7B model) the small_to_mtp_projection in bf16 with its bias."""
     from .synth import bf16_to_f32, rope_tables
     s = shape
-    if s.hidden != s.cp_hidden:
-        raise ValueError("cp_from_tensors: hidden != cp_hidden needs the mtp projection")
     keep = []
     layers = layers_from_tensors(t, s, cp=True)
     arr = (Layer * len(layers))()
@@ -431,6 +452,14 @@ def cp_from_tensors(t, shape, prec=BF16, cp_kv_max=64):
     d.talker_hidden = s.hidden
     d.emb_dim = s.hidden
     d.mtp.w = None
+    if s.hidden != s.cp_hidden:
+        mw = np.ascontiguousarray(t["talker.code_predictor.small_to_mtp_projection.weight"])
+        mb = np.ascontiguousarray(bf16_to_f32(t["talker.code_predictor.small_to_mtp_projection.bias"]))
+        keep += [mw, mb]
+        d.mtp_prec = BF16
+        d.mtp.w = mw.ctypes.data
+        d.mtp.scale = None
+        d.mtp_bias = mb.ctypes.data
     return CodePredictor(d, keep)
 
 
