@@ -65,6 +65,16 @@ typedef struct {
 
 /* replaces qwen_cuda_talker_init(ctx)            (qwen_tts_cuda_talker.cu:313) */
 void *qwen_hip_talker_init(const qwen_hip_talker_desc_t *desc);
+/* The Talker's layers straight from the model file to the device; no counterpart in the
+ * reference, which maps model.safetensors on the host (ingot, qwen_tts_talker.c:105-122)
+ * and builds gate|up and the quantized twins there (t.c:286-317, 378-388).  model_path: the
+ * safetensors file, or the directory holding model.safetensors.  shape: dimensions,
+ * kv_max, eps, quantize_to (-1 keeps bf16; QWEN_HIP_INT8 / QWEN_HIP_Q4_0 quantize on the
+ * device, bit-identical to the reference's host quantizers) and the RoPE tables; its prec,
+ * layers and final_norm are ignored (read from the file).  Every tensor is checked (name,
+ * dtype BF16 -- norms BF16 or F32 --, shape, extent) before the GPU is touched.  Returns
+ * the state qwen_hip_talker_init returns, or NULL (qwen_hip_last_error() says why). */
+void *qwen_hip_talker_load_file(const char *model_path, const qwen_hip_talker_desc_t *shape);
 /* replaces qwen_cuda_talker_step                 (qwen_tts_cuda_talker.cu:395):
  * embed host f32[hidden] in, hidden_out host f32[hidden] (final-normed) out; appends
  * KV at pos.  Returns 0 on success. */

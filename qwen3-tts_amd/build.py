@@ -23,7 +23,7 @@ ARCH = os.environ.get("QWEN_HIP_ARCH", "gfx950")
 
 HIP_SOURCES = ["qt_matvec.hip", "qt_attn.hip", "qt_misc.hip", "qt_pstep.hip", "qt_batch.hip", "qt_prefill.hip", "qt_sample.hip",
                "qt_noalloc.hip"]
-C_SOURCES = ["qwen_tts_hip.c"]
+C_SOURCES = ["qwen_tts_hip.c", "qt_load.c"]
 
 HIPCC_FLAGS = ["-O3", "-fPIC", "-std=c++17", f"--offload-arch={ARCH}",
                "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",

@@ -61,6 +61,9 @@ hipError_t qt_launch_zero_u32(uint32_t *p, size_t n, hipStream_t st);
 /* next Talker input of the frame loop: codec_emb[codes[0]] + sum_g cp_emb[g][codes[g+1]] + pad */
 hipError_t qt_launch_frame_embed(const int *codes, int vocab, int codebook, const uint16_t *codec_emb,
                                  const uint16_t *const cp_emb[15], const float *pad, int H, float *out, hipStream_t st);
+/* out rows 2r = gate row r, 2r+1 = up row r (bf16, cols % 8 == 0) */
+hipError_t qt_launch_interleave_rows(const uint16_t *gate, const uint16_t *up, uint16_t *out, int rows, int cols,
+                                     hipStream_t st);
 /* KV rows [n][nkv*hd] (host order) <-> head-major [nkv][kv_max][hd] (device cache) */
 hipError_t qt_launch_kv_relayout(const uint16_t *src, uint16_t *dst, int n, int nkv, int hd, int kv_max, int to_heads,
                                  hipStream_t st);

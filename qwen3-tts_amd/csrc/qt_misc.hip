@@ -220,8 +220,10 @@ extern "C" hipError_t qt_launch_repack_q4(const uint8_t *blocks, size_t nblocks,
 
 // Weighted-LSQ q4_0 quantizer (qwen_tts_kernels.c:2662-2726) into the device layout
 // (qs rows + f16 scale bits).  One thread per 32-block; double accumulation in index
-// order.  The reference binary's vectorised double sums may round differently in the
-// last place, so block scales match it except on rare f16 rounding ties.
+// order.  The reference build may vectorise its double sums in another order, but each
+// term (v^2 * v * q, v^2 * q^2 of bf16 v and q in [-8, 7]) is an exact double and the
+// sums' last-place rounding does not reach the f16 rounding of the scale, so the bytes
+// are the reference's (tested bit for bit).
 __device__ uint16_t ref_f32_to_f16(float f) {
     uint32_t u = __float_as_uint(f);
     uint32_t sign = (u >> 16) & 0x8000u;
@@ -369,5 +371,27 @@ extern "C" hipError_t qt_launch_frame_embed(const int *codes, int vocab, int cod
     }
     hipLaunchKernelGGL(k_frame_embed, dim3((H + 255) / 256), dim3(256), 0, st, codes, vocab, codebook, codec_emb, cp, pad,
                        H, out);
+    return hipGetLastError();
+}
+
+// gate|up row interleave on the device (the reference loader does it on the host,
+// qwen_tts_talker.c:378-388): out row 2r = gate row r, out row 2r+1 = up row r; bf16 rows
+// of `cols` elements, copied as 16-byte chunks (cols % 8 == 0).
+__global__ void k_interleave_rows(const uint4 *gate, const uint4 *up, uint4 *out, int rows, int cpr) {
+    const long long total = (long long)rows * cpr;
+    for (long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += (long long)gridDim.x * blockDim.x) {
+        const long long r = i / cpr, c = i % cpr;
+        out[(2 * r) * cpr + c] = gate[i];
+        out[(2 * r + 1) * cpr + c] = up[i];
+    }
+}
+extern "C" hipError_t qt_launch_interleave_rows(const uint16_t *gate, const uint16_t *up, uint16_t *out, int rows, int cols,
+                                                hipStream_t st) {
+    if (rows <= 0 || cols <= 0 || cols % 8) return hipErrorInvalidValue;
+    const long long total = (long long)rows * (cols / 8);
+    long long blocks = (total + 255) / 256;
+    if (blocks > 8192) blocks = 8192;
+    hipLaunchKernelGGL(k_interleave_rows, dim3((unsigned)blocks), dim3(256), 0, st, (const uint4 *)gate, (const uint4 *)up,
+                       (uint4 *)out, rows, cols / 8);
     return hipGetLastError();
 }

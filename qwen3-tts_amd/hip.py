@@ -36,7 +36,7 @@ EXPORTS = [
     "qwen_hip_cp_set_prefill2", "qwen_hip_cp_prefill2",
     "qwen_hip_talker_prefill", "qwen_hip_talker_prefill_async", "qwen_hip_op_prefill_gemm",
     "qwen_hip_op_prefill_attention", "qwen_hip_talker_step_layers", "qwen_hip_op_matmat_int8_noalloc",
-    "qwen_hip_generate",
+    "qwen_hip_generate", "qwen_hip_talker_load_file",
 ]
 
 
@@ -85,6 +85,8 @@ def lib():
         L = C.CDLL(LIB_PATH)
         vp, i, f = C.c_void_p, C.c_int, C.c_float
         L.qwen_hip_talker_init.argtypes = [C.POINTER(TalkerDesc)]; L.qwen_hip_talker_init.restype = vp
+        L.qwen_hip_talker_load_file.argtypes = [C.c_char_p, C.POINTER(TalkerDesc)]
+        L.qwen_hip_talker_load_file.restype = vp
         L.qwen_hip_talker_step.argtypes = [vp, vp, vp, i]; L.qwen_hip_talker_step.restype = i
         L.qwen_hip_talker_step_nograph.argtypes = [vp, vp, vp, i]; L.qwen_hip_talker_step_nograph.restype = i
         L.qwen_hip_talker_step_layers.argtypes = [vp, vp, vp, vp, i]; L.qwen_hip_talker_step_layers.restype = i
@@ -205,6 +207,24 @@ class Talker:
         self.h = lib().qwen_hip_talker_init(C.byref(self.desc))
         if not self.h:
             raise RuntimeError("qwen_hip_talker_init failed: " + last_error())
+
+    @classmethod
+    def from_file(cls, model_path, shape, rope_cos, rope_sin, kv_max, quantize_to=-1):
+        """A Talker state loaded by qwen_hip_talker_load_file (file -> device, no host copy)."""
+        self = cls.__new__(cls)
+        s = shape
+        rc_, rs_ = np.ascontiguousarray(rope_cos, np.float32), np.ascontiguousarray(rope_sin, np.float32)
+        self.keep = [rc_, rs_]
+        self.H = s.hidden
+        self.desc = TalkerDesc(hidden=s.hidden, inter=s.inter, n_heads=s.heads, n_kv_heads=s.kv_heads,
+                               head_dim=s.head_dim, n_layers=s.layers, kv_max=kv_max, eps=s.eps, prec=BF16,
+                               quantize_to=quantize_to, layers=None, final_norm=None, rope_cos=rc_.ctypes.data,
+                               rope_sin=rs_.ctypes.data, rope_len=rc_.shape[0])
+        self.kv_max, self.kvd, self.nl = kv_max, s.kv_heads * s.head_dim, s.layers
+        self.h = lib().qwen_hip_talker_load_file(model_path.encode(), C.byref(self.desc))
+        if not self.h:
+            raise RuntimeError("qwen_hip_talker_load_file failed: " + last_error())
+        return self
 
     def step(self, embed, pos, graph=True):
         out = np.empty(self.H, np.float32)

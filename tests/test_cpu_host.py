@@ -157,3 +157,55 @@ def test_glue_calls_only_declared_entry_points():
     src = re.sub(r"/\*.*?\*/", "", src, flags=re.S)
     called = set(re.findall(r"\b(qwen_hip_(?!glue_)\w+)\s*\(", src))
     assert called and called <= set(header_functions()), called - set(header_functions())
+
+
+def _load_desc(shape, kv_max=64):
+    from qwen3_tts_amd import hip, synth
+    cos, sin = synth.rope_tables(shape.head_dim, shape.rope_theta, kv_max)
+    return hip.TalkerDesc(hidden=shape.hidden, inter=shape.inter, n_heads=shape.heads, n_kv_heads=shape.kv_heads,
+                          head_dim=shape.head_dim, n_layers=shape.layers, kv_max=kv_max, eps=shape.eps, prec=0,
+                          quantize_to=-1, layers=None, final_norm=None, rope_cos=cos.ctypes.data,
+                          rope_sin=sin.ctypes.data, rope_len=kv_max), (cos, sin)
+
+
+@need_lib
+def test_load_file_validates_before_touching_the_gpu(tmp_path):
+    """qwen_hip_talker_load_file parses the safetensors header and checks every tensor the
+    step needs (name, dtype, shape, extent) before any GPU call: a valid model gets as far
+    as 'no HIP device' here; a missing file, a broken header, a missing tensor or a
+    dimension mismatch are reported by name."""
+    import ctypes as C
+    import json
+    import struct
+    from qwen3_tts_amd import hip, synth
+    L = hip.lib()
+    if L.qwen_hip_available():
+        pytest.skip("a GPU is visible")
+    s = synth.SHAPES["tiny"]
+    good = tmp_path / "good"
+    synth.write_model_dir(str(good), s, 7, 0.0, threads=4)
+    desc, keep = _load_desc(s)
+    assert not L.qwen_hip_talker_load_file(str(good).encode(), C.byref(desc))
+    assert "no HIP device" in hip.last_error()
+    assert not L.qwen_hip_talker_load_file(str(tmp_path / "nope").encode(), C.byref(desc))
+    assert "cannot open" in hip.last_error()
+    # a header that is not JSON
+    bad = tmp_path / "bad.safetensors"
+    bad.write_bytes(struct.pack("<Q", 5) + b"{oops" + b"\0" * 16)
+    assert not L.qwen_hip_talker_load_file(str(bad).encode(), C.byref(desc))
+    assert "malformed" in hip.last_error()
+    # a tensor missing: rewrite the header without the last layer's v_proj
+    raw = (good / "model.safetensors").read_bytes()
+    n = struct.unpack("<Q", raw[:8])[0]
+    hdr = json.loads(raw[8:8 + n])
+    name = f"talker.model.layers.{s.layers - 1}.self_attn.v_proj.weight"
+    del hdr[name]
+    h2 = json.dumps(hdr).encode()
+    miss = tmp_path / "miss.safetensors"
+    miss.write_bytes(struct.pack("<Q", len(h2)) + h2 + raw[8 + n:])
+    assert not L.qwen_hip_talker_load_file(str(miss).encode(), C.byref(desc))
+    assert "missing tensor " + name in hip.last_error()
+    # dimensions that do not match the file
+    desc2, keep2 = _load_desc(synth.ModelShape(hidden=512, layers=2, heads=4, kv_heads=2, inter=512))
+    assert not L.qwen_hip_talker_load_file(str(good).encode(), C.byref(desc2))
+    assert "expected BF16" in hip.last_error()
