@@ -120,6 +120,8 @@ FRAME_WORKLOADS = {
 # batched workloads: (shape, precision, streams, KV length range, default timed steps)
 BATCH_WORKLOADS = {
     "talker-1.7B-int8-b32-ragged": ("1.7B", "int8", 32, (128, 4096), 16),
+    "talker-1.7B-int4-b32-ragged": ("1.7B", "int4", 32, (128, 4096), 16),
+    "talker-1.7B-bf16-b32-ragged": ("1.7B", "bf16", 32, (128, 4096), 16),
 }
 
 
@@ -305,9 +307,10 @@ def main():
 
 
 def bench_batch(args):
-    """Config 5: B concurrent 1.7B int8 streams on one GPU, each stream's KV length drawn
+    """Config 5: B concurrent 1.7B streams on one GPU, each stream's KV length drawn
     uniform in [lo, hi] from a seed (ragged), weights read once per step for all streams
-    (MFMA int8 GEMM), attention over every stream's own cache.  A step = one batched step
+    (int8 / q4_0: MFMA over exact int8 activation pieces; bf16: MFMA over exact bf16
+    planes), attention over every stream's own cache.  A step = one batched step
     of all B streams; value = ms per batched step (device-resident inputs, positions
     advancing on the device), tokens_per_s = B / step time.  The KV contents are zeros
     beyond what the steps write (attention reads every byte regardless of value)."""
@@ -363,7 +366,7 @@ def bench_batch(args):
         "tokens_per_s": round(B * 1000.0 / ms, 1), "step_bytes": int(step_bytes), "step_hbm_gbs": round(gbs, 1),
         "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
-                     "kernel": "batched step (MFMA int8 GEMMs + ragged split-K attention), whole step",
+                     "kernel": f"batched step (MFMA {prec} GEMMs + ragged split-K attention), whole step",
                      "bytes_per_launch": int(step_bytes), "avg_us": round(ms * 1e3, 1), "steps_per_launch": 1},
         "cpu_baseline": None,
     }

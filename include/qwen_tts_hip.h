@@ -230,7 +230,8 @@ void  qwen_hip_free(void *ctx);
 /* y[rows] = W[rows,cols] @ x[cols] (W bf16; host pointers; W cached on device by
  * host address like qwen_tts_cuda.c:96-112) */
 void  qwen_hip_matvec_bf16(void *ctx, float *y, const uint16_t *W, const float *x, int rows, int cols);
-/* Y[rows,B] = W[rows,cols] @ X[cols,B] (row-major f32, B<=64) */
+/* Y[rows,B] = W[rows,cols] @ X[cols,B] (row-major f32, B<=64); W read once for all B columns
+ * (exact bf16 planes of X on the bf16 MFMA) when rows and cols are multiples of 64 */
 void  qwen_hip_matmat_bf16(void *ctx, float *Y, const uint16_t *W, const float *X, int rows, int cols, int B);
 
 /* qwen_tts_kernels.h signatures on the HIP kernels (host pointers in and out; every
@@ -313,6 +314,12 @@ int qwen_hip_op_codec_sample(const float *logits, int vocab, int frame, float eo
 /* qwen_matmat_int8 (qwen_tts_kernels.h:121-122): Y[rows][B] = (W*scale) @ X[cols][B]
  * (row-major f32, B <= 64, cols a multiple of 64) on the batched MFMA kernel. */
 int qwen_hip_op_matmat_int8(float *Y, const int8_t *W, const float *scale, const float *X, int rows, int cols, int B);
+/* qwen_matmat_q4_0 (qwen_tts_kernels.h:226-227): Y[rows][B] = dequant(W) @ X[cols][B] with W
+ * in the reference's 18-byte q4_0 blocks (row-major f32 X/Y, B <= 64, cols a multiple of 64,
+ * <= 8192): the weights are read once for all B columns, each 32-block's dot product is an
+ * exact integer sum of the nibbles against exact int8 pieces of X, scaled by the block's f16
+ * scale in f32. */
+int qwen_hip_op_matmat_q4_0(float *Y, const void *W, const float *X, int rows, int cols, int B);
 /* No counterpart in the reference: qwen_hip_op_matmat_int8 for callers that cannot
  * allocate device memory (code under HIP graph capture, serving loops that forbid
  * hipMalloc).  All pointers are the caller's DEVICE buffers: Y[B][rows] and X[B][cols]

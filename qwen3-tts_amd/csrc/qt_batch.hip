@@ -214,6 +214,174 @@ __global__ __launch_bounds__(QT_BG_MAXW * 64) void k_bgemm_i8(QtBgArgs a) {
     }
 }
 
+// ---- q4_0 weights x activation pieces -------------------------------------------------
+// Y[b][r] = sum over 32-blocks j of d[r][j] * sum_{k in j} (nib[r][k] - 8) * x[b][k]
+// (qwen_matmat_q4_0, qwen_tts_kernels.c:1954; dequant (nib-8)*f16(scale), k.c:2810-2819),
+// weights read once for all streams.  (nib - 8) is an exact int8, so each block's three
+// piece sums C1, C2, C3 are exact int32 MFMA results; C = C1*2^14 + C2*2^7 + C3 is exact in
+// int32 (|C| < 2^30), and x = s * 2^-14 * (p1*2^14 + p2*2^7 + p3) gives the block's dot as
+// s * 2^-14 * C: one rounding to f32 per block, then d * 2^-14 (exact: a power-of-two
+// multiple of an f16) folded in by one fma into the f32 row sum.  The block scale must
+// stay outside the integer sum, so every MFMA covers one block: the 64-k operand of
+// v_mfma_i32_16x16x64_i8 spans two blocks (lane groups 0-1 and 2-3), and two MFMAs take
+// the same B fragment with the other block's A lanes zeroed.
+// Weight layout: the device q4 rows (qt_device.h) -- K/2 bytes per row, byte i holds
+// elements 2i (low nibble) and 2i+1 (high) -- and f16 scale bits s16[rows][K/32].
+struct QtBgQ4Args {
+    const uint8_t *w;       // [rows][K/2]
+    const uint16_t *s16;    // [rows][K/32]
+    int rows, K;
+    const int8_t *P;        // pieces [K/64][3*Bp][64]
+    const float *S;         // [Bp]
+    int B;
+    float *out;
+    long long ostride;
+};
+
+// 8 bytes of q4 (16 nibbles, elements e0..e15 in order) -> 16 int8 (e - 8), element order
+__device__ __forceinline__ qt_v4i q4_unpack16(uint2 w) {
+    const uint32_t l0 = ((w.x & 0x0F0F0F0Fu) + 0x78787878u) ^ 0x80808080u;   // bytes: e0 e2 e4 e6 (minus 8)
+    const uint32_t h0 = (((w.x >> 4) & 0x0F0F0F0Fu) + 0x78787878u) ^ 0x80808080u;   // e1 e3 e5 e7
+    const uint32_t l1 = ((w.y & 0x0F0F0F0Fu) + 0x78787878u) ^ 0x80808080u;
+    const uint32_t h1 = (((w.y >> 4) & 0x0F0F0F0Fu) + 0x78787878u) ^ 0x80808080u;
+    // v_perm_b32(hi, lo, sel): selector bytes 0-3 pick lo's bytes, 4-7 hi's
+    return qt_v4i{(int)__builtin_amdgcn_perm(h0, l0, 0x05010400u), (int)__builtin_amdgcn_perm(h0, l0, 0x07030602u),
+                  (int)__builtin_amdgcn_perm(h1, l1, 0x05010400u), (int)__builtin_amdgcn_perm(h1, l1, 0x07030602u)};
+}
+
+// KB k-blocks of 64 per wave, at most 8 waves (KB = 16 for K > 4096), so a lane may hold
+// 256 registers: two sets of B fragments, the block's MFMA results and the q4 weights.
+#define QT_BQ_MAXW 8
+template <int NT, int EPI, int KB>
+__global__ __launch_bounds__(QT_BQ_MAXW * 64) void k_bgemm_q4(QtBgQ4Args a) {
+    constexpr int BP = NT * 16 / 3, NS = BP / 16;   // padded streams, stream tiles
+    __shared__ float red[NS][4][64];
+    const int nw = blockDim.x >> 6;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int r0 = blockIdx.x * 16;
+    const int m = lane & 15, grp = lane >> 4;
+    const int row = min(r0 + m, a.rows - 1);       // rows past the end repeat the last (discarded)
+    const int nb32 = a.K >> 5;
+    const uint8_t *wr = a.w + (size_t)row * (a.K >> 1);
+    const size_t cs = (size_t)3 * BP * 64;
+    const int kw0 = wave * KB * 64;
+    const int nkb = max(0, min(KB * 64, a.K - kw0)) >> 6;   // wave-uniform
+
+    uint2 wq[KB];
+#pragma unroll
+    for (int kb = 0; kb < KB; kb++)
+        wq[kb] = kb < nkb ? *reinterpret_cast<const uint2 *>(wr + ((kw0 + kb * 64) >> 1) + grp * 8) : make_uint2(0u, 0u);
+    // block scales of the four output rows this lane receives (rows 4*grp + i), times 2^-14
+    const uint16_t *sr[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) sr[i] = a.s16 + (size_t)min(r0 + 4 * grp + i, a.rows - 1) * nb32 + (kw0 >> 5);
+
+    float acc[NS][4];
+#pragma unroll
+    for (int s = 0; s < NS; s++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) acc[s][i] = 0.f;
+    // one block's three piece sums -> C = C1*2^14 + C2*2^7 + C3 (exact), times d*2^-14 into acc
+    auto fold = [&](const qt_v4i (&c)[NT], int blk) {
+        float d[4];
+#pragma unroll
+        for (int i = 0; i < 4; i++) d[i] = ref_f16_to_f32(sr[i][blk]) * 0x1p-14f;
+#pragma unroll
+        for (int s = 0; s < NS; s++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int v = (c[s][i] << 14) + (c[NS + s][i] << 7) + c[2 * NS + s][i];
+                acc[s][i] = fmaf((float)v, d[i], acc[s][i]);
+            }
+    };
+    // B fragments one k-block ahead (two register sets); the scheduling barrier after each
+    // block keeps the compiler from hoisting every block's loads at once (register spills)
+    auto loadB = [&](qt_v4i (&Bv)[NT], int kb) {
+        const int8_t *pb = a.P + (size_t)((kw0 >> 6) + kb) * cs + (size_t)m * 64 + grp * 16;
+#pragma unroll
+        for (int t = 0; t < NT; t++) {
+            const uint4 pv = *reinterpret_cast<const uint4 *>(pb + (size_t)t * 16 * 64);
+            Bv[t] = qt_v4i{(int)pv.x, (int)pv.y, (int)pv.z, (int)pv.w};
+        }
+    };
+    auto block = [&](int kb, const qt_v4i (&Bv)[NT]) {
+        const qt_v4i A = q4_unpack16(wq[kb]);
+        const qt_v4i Z = qt_v4i{0, 0, 0, 0};
+        const qt_v4i A0 = grp < 2 ? A : Z, A1 = grp < 2 ? Z : A;
+        qt_v4i c[NT];
+#pragma unroll
+        for (int t = 0; t < NT; t++) c[t] = __builtin_amdgcn_mfma_i32_16x16x64_i8(A0, Bv[t], Z, 0, 0, 0);
+        fold(c, 2 * kb);
+#pragma unroll
+        for (int t = 0; t < NT; t++) c[t] = __builtin_amdgcn_mfma_i32_16x16x64_i8(A1, Bv[t], Z, 0, 0, 0);
+        fold(c, 2 * kb + 1);
+    };
+    qt_v4i Bb0[NT], Bb1[NT];
+    if (nkb > 0) loadB(Bb0, 0);
+#pragma unroll
+    for (int kb = 0; kb < KB; kb++) {
+        if (kb >= nkb) break;
+        if (kb + 1 < nkb) {
+            if (kb & 1) loadB(Bb0, kb + 1);
+            else loadB(Bb1, kb + 1);
+        }
+        if (kb & 1) block(kb, Bb1);
+        else block(kb, Bb0);
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    // the waves' partial row sums, added in wave order
+    for (int w = 0; w < nw; w++) {
+        if (wave == w) {
+#pragma unroll
+            for (int s = 0; s < NS; s++)
+#pragma unroll
+                for (int i = 0; i < 4; i++) red[s][i][lane] = (w == 0 ? 0.f : red[s][i][lane]) + acc[s][i];
+        }
+        __syncthreads();
+    }
+    for (int j = tid; j < 16 * BP; j += blockDim.x) {
+        const int rl = j / BP, b = j % BP, r = r0 + rl;
+        if (b >= a.B || r >= a.rows) continue;
+        if (EPI == QT_EPI_SWIGLU && (rl & 1)) continue;
+        auto val = [&](int rr) -> float { return red[b >> 4][rr & 3][(rr >> 2) * 16 + (b & 15)] * a.S[b]; };
+        float *ob = a.out + (size_t)b * a.ostride;
+        if (EPI == QT_EPI_STORE) ob[r] = val(rl);
+        else if (EPI == QT_EPI_RESID) ob[r] = __fadd_rn(ob[r], val(rl));
+        else if (EPI == QT_EPI_SWIGLU) {
+            const float g = val(rl), u = val(rl + 1);
+            ob[r >> 1] = g / (1.0f + expf(-g)) * u;
+        }
+    }
+}
+
+extern "C" hipError_t qt_launch_bgemm_q4(int epi, const uint8_t *w, const uint16_t *s16, int rows, int K,
+                                         const int8_t *P, const float *S, int B, int Bp, float *out, long long ostride,
+                                         hipStream_t st) {
+    if (rows <= 0 || K <= 0 || (K & 63) || K > 16 * 64 * QT_BQ_MAXW || B <= 0 || B > Bp) return hipErrorInvalidValue;
+    if (epi == QT_EPI_SWIGLU && (rows & 1)) return hipErrorInvalidValue;
+    QtBgQ4Args a;
+    a.w = w; a.s16 = s16; a.rows = rows; a.K = K; a.P = P; a.S = S; a.B = B; a.out = out; a.ostride = ostride;
+    const int kb = K > 8 * 64 * QT_BQ_MAXW ? 16 : 8;
+    const int nw = (K + kb * 64 - 1) / (kb * 64);
+    dim3 grid((rows + 15) / 16), block(nw * 64);
+#define QT_BQ_KB(NT_, E_)                                                                              \
+    if (kb == 8) hipLaunchKernelGGL((k_bgemm_q4<NT_, E_, 8>), grid, block, 0, st, a);                   \
+    else hipLaunchKernelGGL((k_bgemm_q4<NT_, E_, 16>), grid, block, 0, st, a);
+#define QT_BQ_CASE(NT_)                                                                                   \
+    if (epi == QT_EPI_STORE) { QT_BQ_KB(NT_, QT_EPI_STORE) }                                              \
+    else if (epi == QT_EPI_RESID) { QT_BQ_KB(NT_, QT_EPI_RESID) }                                         \
+    else if (epi == QT_EPI_SWIGLU) { QT_BQ_KB(NT_, QT_EPI_SWIGLU) }                                       \
+    else return hipErrorInvalidValue;
+    if (Bp == 16) { QT_BQ_CASE(3) }
+    else if (Bp == 32) { QT_BQ_CASE(6) }
+    else if (Bp == 48) { QT_BQ_CASE(9) }
+    else if (Bp == 64) { QT_BQ_CASE(12) }
+    else return hipErrorInvalidValue;
+#undef QT_BQ_CASE
+#undef QT_BQ_KB
+    return hipGetLastError();
+}
+
 extern "C" hipError_t qt_launch_bpieces(const float *x, long long xstride, const float *norm_w, float eps, int K, int B,
                                         int Bp, int8_t *P, float *S, hipStream_t st) {
     if (K <= 0 || (K & 63) || B <= 0 || Bp < B || (Bp & 15) || Bp > 64) return hipErrorInvalidValue;

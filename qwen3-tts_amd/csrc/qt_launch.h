@@ -35,6 +35,8 @@ hipError_t qt_launch_bpieces(const float *x, long long xstride, const float *nor
                              int8_t *P, float *S, hipStream_t st);
 hipError_t qt_launch_bgemm_i8(int epi, const uint8_t *w, const float *scale, int rows, int K, const int8_t *P,
                               const float *S, int B, int Bp, float *out, long long ostride, hipStream_t st);
+hipError_t qt_launch_bgemm_q4(int epi, const uint8_t *w, const uint16_t *s16, int rows, int K, const int8_t *P,
+                              const float *S, int B, int Bp, float *out, long long ostride, hipStream_t st);
 hipError_t qt_launch_advance_pos(int *pos, int n, hipStream_t st);
 hipError_t qt_launch_rmsnorm(const float *x, const float *w, float *out, int n, float eps, int *d_pos,
                              hipStream_t st);

@@ -1440,9 +1440,11 @@ fail:
  *   pieces(RMSNorm(x)) -> MFMA QKV -> attention (q/k norm, RoPE, KV append, split-K over
  *   each stream's own length, B streams in one grid) -> pieces(attn) -> MFMA O + residual
  *   -> pieces(RMSNorm(x)) -> MFMA gate|up + SwiGLU -> pieces(h) -> MFMA down + residual,
- * captured once into a hipGraph (positions live on the device).  bf16 / q4_0 weights
- * have no batched kernel here: their projections run as B matvecs per matrix (weights
- * re-read per stream, like the reference's QWEN_BATCH_NOMATMUL diagnostic). */
+ * captured once into a hipGraph (positions live on the device).  q4_0 weights take the
+ * same pieces into qt_launch_bgemm_q4 (per-32-block integer sums, block scale in f32);
+ * bf16 weights take the prefill's projection GEMM (three exact bf16 activation planes on
+ * the bf16 MFMA, split K for the residual projections).  Every weight is read once per
+ * step for all B streams in every precision. */
 
 #define QWEN_HIP_BATCH_MAX 64
 
@@ -1453,6 +1455,7 @@ typedef struct {
     uint16_t *kc, *vc;         /* [B][L][nkv][kv_max][hd] */
     float *x, *qkv, *attn, *h, *hid;
     int8_t *pc; float *ps;     /* activation pieces [Kmax/64][3*Bp][64], scales [Bp] */
+    uint16_t *pf_p; float *pf_part; /* bf16: activation planes [3][64][Kmax], split-K partials [4][B][H] */
     float *part; unsigned *cnt;
     int *d_pos;                /* [B] */
     float *h_io; int *h_pos;   /* pinned */
@@ -1466,7 +1469,7 @@ static void batch_destroy(batch_t *bt) {
     if (!bt) return;
     if (bt->graph_ready) (void)hipGraphExecDestroy(bt->exec);
     void *bufs[] = {bt->kc, bt->vc, bt->x, bt->qkv, bt->attn, bt->h, bt->hid, bt->pc, bt->ps, bt->part, bt->cnt, bt->d_pos,
-                    bt->kv_stage};
+                    bt->kv_stage, bt->pf_p, bt->pf_part};
     for (size_t i = 0; i < sizeof bufs / sizeof bufs[0]; i++) if (bufs[i]) (void)hipFree(bufs[i]);
     if (bt->h_io) (void)hipHostFree(bt->h_io);
     if (bt->h_pos) (void)hipHostFree(bt->h_pos);
@@ -1494,6 +1497,10 @@ static batch_t *batch_create(const stack_t *s, int B, int is_cp) {
     HCK(hipMalloc((void **)&bt->h, (size_t)B * s->F * sizeof(float)));
     HCK(hipMalloc((void **)&bt->pc, (size_t)K * 3 * bt->Bp));
     HCK(hipMalloc((void **)&bt->ps, (size_t)bt->Bp * sizeof(float)));
+    if (s->prec == QWEN_HIP_BF16) {
+        HCK(hipMalloc((void **)&bt->pf_p, (size_t)3 * qt_pf_spad(B) * K * sizeof(uint16_t)));
+        HCK(hipMalloc((void **)&bt->pf_part, (size_t)4 * B * s->H * sizeof(float)));
+    }
     HCK(hipMalloc((void **)&bt->part, (size_t)B * s->nkv * s->attn_G * (s->nh / s->nkv) * 130 * sizeof(float)));
     HCK(hipMalloc((void **)&bt->cnt, (size_t)B * s->nkv * sizeof(unsigned)));
     HCK(hipMemsetAsync(bt->cnt, 0, (size_t)B * s->nkv * sizeof(unsigned), bt->st));
@@ -1513,17 +1520,15 @@ static hipError_t batch_proj(batch_t *bt, const dmat_t *m, int epi, const float 
                              float *dst, long long dstride) {
     const stack_t *s = bt->s;
     hipError_t e;
-    if (m->prec == QWEN_HIP_INT8) {
-        if ((e = qt_launch_bpieces(src, sstride, nw, s->eps, m->cols, bt->B, bt->Bp, bt->pc, bt->ps, bt->st))) return e;
+    if (m->prec == QWEN_HIP_BF16) {
+        if ((e = qt_launch_pf_pieces(src, (int)sstride, bt->B, m->cols, nw, s->eps, bt->pf_p, bt->st))) return e;
+        return qt_launch_pf_gemm(epi, (const uint16_t *)m->w, bt->pf_p, bt->B, m->rows, m->cols, dst, (int)dstride,
+                                 bt->pf_part, bt->st);
+    }
+    if ((e = qt_launch_bpieces(src, sstride, nw, s->eps, m->cols, bt->B, bt->Bp, bt->pc, bt->ps, bt->st))) return e;
+    if (m->prec == QWEN_HIP_INT8)
         return qt_launch_bgemm_i8(epi, m->w, m->scale, m->rows, m->cols, bt->pc, bt->ps, bt->B, bt->Bp, dst, dstride, bt->st);
-    }
-    for (int b = 0; b < bt->B; b++) {
-        float *d = dst + (size_t)b * dstride;
-        if ((e = qt_launch_mv(m->prec, epi, nw != NULL, src + (size_t)b * sstride, nw, s->eps, m->w, m->scale, m->s16,
-                              m->rows, m->cols, epi == QT_EPI_RESID ? NULL : d, epi == QT_EPI_RESID ? d : NULL, NULL,
-                              NULL, bt->st))) return e;
-    }
-    return hipSuccess;
+    return qt_launch_bgemm_q4(epi, m->w, m->s16, m->rows, m->cols, bt->pc, bt->ps, bt->B, bt->Bp, dst, dstride, bt->st);
 }
 
 static hipError_t batch_body(void *arg) {
@@ -1731,6 +1736,7 @@ void qwen_hip_matvec_bf16(void *ctx, float *y, const uint16_t *W, const float *x
 void qwen_hip_matmat_bf16(void *ctx, float *Y, const uint16_t *W, const float *X, int rows, int cols, int B) {
     backend_t *b = (backend_t *)ctx;
     float *dx = NULL, *dy = NULL, *hx = NULL, *hy = NULL;
+    uint16_t *dp = NULL;
     dmat_t *m;
     REQ(b && B >= 1 && B <= 64, "bad backend call");
     REQ((m = cached_bf16(b, W, rows, cols)) != NULL, "weight upload failed");
@@ -1741,14 +1747,22 @@ void qwen_hip_matmat_bf16(void *ctx, float *Y, const uint16_t *W, const float *X
     /* X is [cols][B] row-major: gather column b into a contiguous vector */
     for (int k = 0; k < cols; k++) for (int j = 0; j < B; j++) hx[(size_t)j * cols + k] = X[(size_t)k * B + j];
     HCK(hipMemcpyAsync(dx, hx, (size_t)cols * B * sizeof(float), hipMemcpyHostToDevice, b->st));
-    for (int j = 0; j < B; j++)
-        HCK(mv(m, QT_EPI_STORE, 0, dx + (size_t)j * cols, NULL, 0.f, dy + (size_t)j * rows, NULL, NULL, b->st));
+    if (rows % 64 == 0 && cols % 64 == 0) {
+        /* weights read once for all B columns: exact bf16 planes of X on the bf16 MFMA */
+        HCK(hipMalloc((void **)&dp, (size_t)3 * qt_pf_spad(B) * cols * sizeof(uint16_t)));
+        HCK(qt_launch_pf_pieces(dx, cols, B, cols, NULL, 0.f, dp, b->st));
+        HCK(qt_launch_pf_gemm(QT_PF_STORE, (const uint16_t *)m->w, dp, B, rows, cols, dy, rows, NULL, b->st));
+    } else {
+        for (int j = 0; j < B; j++)
+            HCK(mv(m, QT_EPI_STORE, 0, dx + (size_t)j * cols, NULL, 0.f, dy + (size_t)j * rows, NULL, NULL, b->st));
+    }
     HCK(hipMemcpyAsync(hy, dy, (size_t)rows * B * sizeof(float), hipMemcpyDeviceToHost, b->st));
     HCK(hipStreamSynchronize(b->st));
     for (int r = 0; r < rows; r++) for (int j = 0; j < B; j++) Y[(size_t)r * B + j] = hy[(size_t)j * rows + r];
 fail:
     if (dx) (void)hipFree(dx);
     if (dy) (void)hipFree(dy);
+    if (dp) (void)hipFree(dp);
     free(hx); free(hy);
 }
 
@@ -1782,20 +1796,22 @@ fail:
     return -1;
 }
 
-/* qwen_matmat_int8 (qwen_tts_kernels.h:121-122): Y[rows][B] = (W*scale) @ X[cols][B],
- * row-major f32, B <= 64, on the batched MFMA kernel (cols multiple of 64). */
-int qwen_hip_op_matmat_int8(float *Y, const int8_t *W, const float *scale, const float *X, int rows, int cols, int B) {
+/* Y[rows][B] = W @ X[cols][B] (row-major f32, B <= 64, cols a multiple of 64) on the
+ * batched MFMA kernels: exact int8 activation pieces against int8 (qt_launch_bgemm_i8) or
+ * q4_0 (qt_launch_bgemm_q4) weights, each weight read once for all B columns. */
+static int op_matmat(int prec, float *Y, const void *W, const float *scale, const float *X, int rows, int cols, int B) {
     hipStream_t st = op_stream();
     dmat_t m; memset(&m, 0, sizeof m);
     float *dx = NULL, *dy = NULL, *hx = NULL, *hy = NULL, *ps = NULL;
-    int8_t *pc = NULL;
+    int8_t *pc = NULL; void *tmp = NULL;
     qwen_hip_mat_t src = {W, scale};
     const int Bp = (B + 15) & ~15;
     REQ(st, "no stream");
     REQ(rows > 0 && cols > 0 && cols % 64 == 0 && cols <= 8192, "bad shape %dx%d (cols: multiple of 64, <= 8192)", rows, cols);
     REQ(B >= 1 && B <= 64, "B %d out of range (1..64)", B);
-    REQ(dmat_alloc(&m, QWEN_HIP_INT8, rows, cols) == 0, "alloc");
-    REQ(dmat_put(&m, 0, &src, QWEN_HIP_INT8, rows, st, NULL) == 0, "upload");
+    REQ(dmat_alloc(&m, prec, rows, cols) == 0, "alloc");
+    if (prec == QWEN_HIP_Q4_0) HCK(hipMalloc(&tmp, (size_t)rows * (cols / 32) * 18 + 16));
+    REQ(dmat_put(&m, 0, &src, prec, rows, st, tmp) == 0, "upload");
     hx = malloc((size_t)B * cols * sizeof(float)); hy = malloc((size_t)B * rows * sizeof(float));
     REQ(hx && hy, "host alloc");
     for (int k = 0; k < cols; k++) for (int j = 0; j < B; j++) hx[(size_t)j * cols + k] = X[(size_t)k * B + j];
@@ -1805,11 +1821,16 @@ int qwen_hip_op_matmat_int8(float *Y, const int8_t *W, const float *scale, const
     HCK(hipMalloc((void **)&ps, (size_t)Bp * sizeof(float)));
     HCK(hipMemcpyAsync(dx, hx, (size_t)B * cols * sizeof(float), hipMemcpyHostToDevice, st));
     HCK(qt_launch_bpieces(dx, cols, NULL, 0.f, cols, B, Bp, pc, ps, st));
-    HCK(qt_launch_bgemm_i8(QT_EPI_STORE, m.w, m.scale, rows, cols, pc, ps, B, Bp, dy, rows, st));
+    if (prec == QWEN_HIP_INT8)
+        HCK(qt_launch_bgemm_i8(QT_EPI_STORE, m.w, m.scale, rows, cols, pc, ps, B, Bp, dy, rows, st));
+    else
+        HCK(qt_launch_bgemm_q4(QT_EPI_STORE, m.w, m.s16, rows, cols, pc, ps, B, Bp, dy, rows, st));
     HCK(hipMemcpyAsync(hy, dy, (size_t)B * rows * sizeof(float), hipMemcpyDeviceToHost, st));
     HCK(hipStreamSynchronize(st));
     for (int r = 0; r < rows; r++) for (int j = 0; j < B; j++) Y[(size_t)r * B + j] = hy[(size_t)j * rows + r];
-    dmat_free(&m); (void)hipFree(dx); (void)hipFree(dy); (void)hipFree(pc); (void)hipFree(ps); free(hx); free(hy);
+    dmat_free(&m); (void)hipFree(dx); (void)hipFree(dy); (void)hipFree(pc); (void)hipFree(ps);
+    if (tmp) (void)hipFree(tmp);
+    free(hx); free(hy);
     return 0;
 fail:
     dmat_free(&m);
@@ -1817,8 +1838,18 @@ fail:
     if (dy) (void)hipFree(dy);
     if (pc) (void)hipFree(pc);
     if (ps) (void)hipFree(ps);
+    if (tmp) (void)hipFree(tmp);
     free(hx); free(hy);
     return -1;
+}
+
+/* qwen_matmat_int8 (qwen_tts_kernels.h:121-122): Y[rows][B] = (W*scale) @ X[cols][B]. */
+int qwen_hip_op_matmat_int8(float *Y, const int8_t *W, const float *scale, const float *X, int rows, int cols, int B) {
+    return op_matmat(QWEN_HIP_INT8, Y, W, scale, X, rows, cols, B);
+}
+/* qwen_matmat_q4_0 (qwen_tts_kernels.h:226-227): Y[rows][B] = dequant(W) @ X[cols][B]. */
+int qwen_hip_op_matmat_q4_0(float *Y, const void *W, const float *X, int rows, int cols, int B) {
+    return op_matmat(QWEN_HIP_Q4_0, Y, W, NULL, X, rows, cols, B);
 }
 
 int qwen_hip_op_matvec_bf16(float *y, const uint16_t *W, const float *x, int rows, int cols) {

@@ -32,7 +32,7 @@ EXPORTS = [
     "qwen_hip_last_error", "qwen_hip_talker_batch_init", "qwen_hip_talker_batch_step",
     "qwen_hip_talker_batch_upload_slot", "qwen_hip_talker_batch_free", "qwen_hip_talker_batch_download_slot",
     "qwen_hip_talker_batch_step_async", "qwen_hip_talker_batch_sync", "qwen_hip_talker_batch_stream",
-    "qwen_hip_cp_batch_init", "qwen_hip_cp_batch_step", "qwen_hip_cp_batch_free", "qwen_hip_op_matmat_int8",
+    "qwen_hip_cp_batch_init", "qwen_hip_cp_batch_step", "qwen_hip_cp_batch_free", "qwen_hip_op_matmat_int8", "qwen_hip_op_matmat_q4_0",
     "qwen_hip_cp_set_prefill2", "qwen_hip_cp_prefill2",
     "qwen_hip_talker_prefill", "qwen_hip_talker_prefill_async", "qwen_hip_op_prefill_gemm",
     "qwen_hip_op_prefill_attention", "qwen_hip_talker_step_layers", "qwen_hip_op_matmat_int8_noalloc",
@@ -154,6 +154,7 @@ def lib():
         L.qwen_hip_cp_set_prefill2.argtypes = [vp, i]; L.qwen_hip_cp_set_prefill2.restype = i
         L.qwen_hip_cp_prefill2.argtypes = [vp, vp, vp]; L.qwen_hip_cp_prefill2.restype = i
         L.qwen_hip_op_matmat_int8.argtypes = [vp, vp, vp, vp, i, i, i]; L.qwen_hip_op_matmat_int8.restype = i
+        L.qwen_hip_op_matmat_q4_0.argtypes = [vp, vp, vp, i, i, i]; L.qwen_hip_op_matmat_q4_0.restype = i
         L.qwen_hip_op_matmat_int8_noalloc.argtypes = [vp, vp, vp, vp, i, i, i, vp]
         L.qwen_hip_op_matmat_int8_noalloc.restype = i
         _lib = L

@@ -87,6 +87,62 @@ def test_op_matmat_matches_matvec_per_column(oracle):
         assert rel_l2(Y[:, j], y) < 5e-6
 
 
+def _matmat_q4(blocks, rows, cols, X):
+    B = X.shape[1]
+    Y = np.empty((rows, B), np.float32)
+    Xc = np.ascontiguousarray(X, np.float32)
+    hip.check(hip.lib().qwen_hip_op_matmat_q4_0(Y.ctypes.data, blocks.ctypes.data, Xc.ctypes.data, rows, cols, B),
+              "matmat_q4_0")
+    return Y
+
+
+@pytest.mark.parametrize("rows,cols,B", [(16, 64, 1), (64, 2048, 32), (4096, 1024, 16), (2048, 6144, 32),
+                                         (257, 320, 5), (100, 2048, 33), (48, 8192, 64), (12288, 2048, 8)])
+def test_op_matmat_q4_0(oracle, rows, cols, B):
+    """Y = dequant(W_q4) @ X (weights read once for all B columns) against the f64 product
+    of the dequantised weights (oracle dequant_q4_0, k.c:2810-2819): each block's dot
+    product is an exact integer sum rounded once, so only f32 roundings remain."""
+    print(f"[case] matmat q4_0 {rows}x{cols} B={B}", flush=True)
+    rng = np.random.default_rng(rows * 7 + cols + B)
+    w = synth.f32_to_bf16_rne((rng.standard_normal((rows, cols)) * 0.02).astype(np.float32))
+    blocks = oracle.quantize_q4_0(w)
+    X = rng.standard_normal((cols, B)).astype(np.float32)
+    X[:, 0] *= 1e-3
+    if B > 2:
+        X[:, 2] = 0.0
+    Y = _matmat_q4(blocks, rows, cols, X)
+    Wf = oracle.dequant_q4_0(blocks, rows, cols).astype(np.float64)
+    Y64 = Wf @ X.astype(np.float64)
+    for j in range(B):
+        den = np.abs(Y64[:, j]).max()
+        if den == 0:
+            assert np.all(Y[:, j] == 0)
+            continue
+        err = np.abs(Y[:, j] - Y64[:, j]).max() / den
+        assert err < 1e-5, (j, err)
+
+
+def test_op_matmat_q4_0_exact_inputs(oracle):
+    """Power-of-two block scales (the second block of each row scaled by zero) and
+    activations that the int8 planes hold exactly: every block's integer dot product, its
+    conversion and its scaling are exact, so Y equals the f64 product."""
+    rows, cols, B = 32, 64, 16
+    rng = np.random.default_rng(5)
+    nib = rng.integers(0, 16, (rows, cols))
+    blocks = np.zeros((rows, cols // 32, 18), np.uint8)
+    for r in range(rows):
+        for j in range(cols // 32):
+            e = int(rng.integers(-6, 3))
+            h = np.float16(2.0 ** e) if j == 0 else np.float16(0.0)
+            blocks[r, j, :2] = np.frombuffer(h.tobytes(), np.uint8)
+            q = nib[r, 32 * j:32 * j + 32]
+            blocks[r, j, 2:] = (q[0::2] | (q[1::2] << 4)).astype(np.uint8)
+    X = (rng.integers(-(1 << 14), 1 << 14, (cols, B)) * 2.0 ** -10).astype(np.float32)
+    Y = _matmat_q4(blocks, rows, cols, X)
+    Wf = oracle.dequant_q4_0(blocks.reshape(-1), rows, cols).astype(np.float64)
+    assert np.array_equal(Y, (Wf @ X.astype(np.float64)).astype(np.float32))
+
+
 # ------------------------------------------------------------------ batched Talker step
 
 def _ref(name, prec):
@@ -101,7 +157,7 @@ def _streams(ref, prec_code, B, kv_max):
 
 
 @need_ref
-@pytest.mark.parametrize("prec,B", [("int8", 5), ("int8", 32), ("bf16", 3), ("int4", 2)])
+@pytest.mark.parametrize("prec,B", [("int8", 5), ("int8", 32), ("bf16", 3), ("bf16", 32), ("int4", 2), ("int4", 17), ("int4", 32)])
 def test_batch_step_ragged_vs_oracle(oracle, prec, B):
     """B streams prefilled to different lengths (upload_slot), then stepped together,
     each at its own position; every stream against its own oracle decode."""
