@@ -27,8 +27,9 @@
 // 4*(l/16)+i (i < 4) of column l % 16.  A and B use the same k mapping, so any k order
 // within a group gives the same exact integer dot product.
 //
-// Work split: one workgroup per 16 weight rows, one wave per 512 columns of K (K/512
-// waves: 4 for K = 2048, 12 for K = 6144), partial int32 tiles summed through LDS.
+// Work split (k_bgemm_i8, any K that is a multiple of 64): one workgroup per 16 weight
+// rows, one wave per 512 columns of K, partial int32 tiles summed through LDS.  The
+// batched step uses k_bgemm2_i8 (below) where K is a multiple of 1024.
 #include "qt_device.h"
 
 typedef int qt_v4i __attribute__((ext_vector_type(4)));
@@ -212,6 +213,190 @@ __global__ __launch_bounds__(QT_BG_MAXW * 64) void k_bgemm_i8(QtBgArgs a) {
             ob[r >> 1] = g / (1.0f + expf(-g)) * u;
         }
     }
+}
+
+// ---- int8 weights x activation pieces, tall tiles and split K --------------------------
+// The batched step's projections have 2048-12288 rows; at 16 rows per workgroup the
+// 2048-row ones fill half the CUs, and each B fragment (1 KiB of pieces from L2) serves
+// one 16-row MFMA tile, so the pieces traffic is ~6x the weight bytes.  Here a
+// workgroup (4 waves, one per SIMD, so a lane may hold 512 registers) owns RT row tiles
+// (16*RT rows) and one of S equal K ranges; wave w takes KB k-blocks of 64 of that range,
+// holds all its weight fragments in registers from the start (RT*KB*16 bytes per lane in
+// flight), streams its B fragments one k-block ahead, and feeds each B fragment to the
+// RT row tiles.  The waves' int32 tiles are summed in LDS (exact).  With S > 1 each
+// workgroup publishes its exact int32 tile (agent-scope stores), counts itself in with a
+// device-scope atomic, and the last of the S workgroups of a row group adds the others'
+// tiles (integer sums: the order cannot change the result) and runs the epilogue, then
+// re-arms the counter for the next call.  (Issuing every B fragment at entry as well,
+// with 8 waves of 256 columns, measured slower: 3.85 against 3.76 ms per batched step.)
+#define QT_B2_W 4
+struct QtBg2Args {
+    const uint8_t *w; const float *scale;
+    int rows, K;
+    const int8_t *P; const float *S;
+    int B;
+    float *out; long long ostride;
+    int *part;          // S > 1: [gridDim.x][S][RT*NT*256] int32
+    unsigned *cnt;      // S > 1: [gridDim.x], zero between calls
+};
+
+template <int NT, int EPI, int RT, int KB>
+__global__ __launch_bounds__(QT_B2_W * 64) void k_bgemm2_i8(QtBg2Args a) {
+    constexpr int BP = NT * 16 / 3;
+    constexpr int TILE = RT * NT * 256;               // ints of one workgroup tile
+    __shared__ int red[RT][NT][4][64];
+    __shared__ unsigned last_flag;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int m = lane & 15, grp = lane >> 4;
+    const int x = blockIdx.x, z = blockIdx.y, S = gridDim.y;
+    const int r0 = x * 16 * RT;
+    const int kw0 = z * (a.K / S) + wave * KB * 64;
+    const size_t cs = (size_t)3 * BP * 64;
+
+    uint4 wa[RT][KB];
+#pragma unroll
+    for (int rt = 0; rt < RT; rt++) {
+        const uint8_t *wr = a.w + (size_t)min(r0 + 16 * rt + m, a.rows - 1) * a.K + kw0 + grp * 16;
+#pragma unroll
+        for (int kb = 0; kb < KB; kb++) wa[rt][kb] = *reinterpret_cast<const uint4 *>(wr + kb * 64);
+    }
+    qt_v4i acc[RT][NT];
+#pragma unroll
+    for (int rt = 0; rt < RT; rt++)
+#pragma unroll
+        for (int t = 0; t < NT; t++) acc[rt][t] = qt_v4i{0, 0, 0, 0};
+    const int8_t *pbase = a.P + (size_t)(kw0 >> 6) * cs + (size_t)m * 64 + grp * 16;
+    auto loadB = [&](qt_v4i (&Bv)[NT], int kb) {
+#pragma unroll
+        for (int t = 0; t < NT; t++) {
+            const uint4 pv = *reinterpret_cast<const uint4 *>(pbase + (size_t)kb * cs + (size_t)t * 16 * 64);
+            Bv[t] = qt_v4i{(int)pv.x, (int)pv.y, (int)pv.z, (int)pv.w};
+        }
+    };
+    qt_v4i Bb0[NT], Bb1[NT];
+    loadB(Bb0, 0);
+#pragma unroll
+    for (int kb = 0; kb < KB; kb++) {
+        if (kb + 1 < KB) {
+            if (kb & 1) loadB(Bb0, kb + 1);
+            else loadB(Bb1, kb + 1);
+        }
+#pragma unroll
+        for (int rt = 0; rt < RT; rt++) {
+            const qt_v4i A = qt_v4i{(int)wa[rt][kb].x, (int)wa[rt][kb].y, (int)wa[rt][kb].z, (int)wa[rt][kb].w};
+#pragma unroll
+            for (int t = 0; t < NT; t++)
+                acc[rt][t] = __builtin_amdgcn_mfma_i32_16x16x64_i8(A, (kb & 1) ? Bb1[t] : Bb0[t], acc[rt][t], 0, 0, 0);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    for (int w = 0; w < QT_B2_W; w++) {
+        if (wave == w) {
+#pragma unroll
+            for (int rt = 0; rt < RT; rt++)
+#pragma unroll
+                for (int t = 0; t < NT; t++)
+#pragma unroll
+                    for (int i = 0; i < 4; i++)
+                        red[rt][t][i][lane] = (w == 0 ? 0 : red[rt][t][i][lane]) + acc[rt][t][i];
+        }
+        __syncthreads();
+    }
+    int *flat = &red[0][0][0][0];
+    if (S > 1) {
+        int *mine = a.part + ((size_t)x * S + z) * TILE;
+        for (int i = tid; i < TILE; i += QT_B2_W * 64)
+            __hip_atomic_store(mine + i, flat[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __builtin_amdgcn_s_waitcnt(0);
+        __syncthreads();
+        if (tid == 0)
+            last_flag = __hip_atomic_fetch_add(&a.cnt[x], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+                        (unsigned)(S - 1);
+        __syncthreads();
+        if (!last_flag) return;
+        for (int zz = 0; zz < S; zz++) {
+            if (zz == z) continue;
+            const int *other = a.part + ((size_t)x * S + zz) * TILE;
+            for (int i = tid; i < TILE; i += QT_B2_W * 64)
+                flat[i] += __hip_atomic_load(other + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        __syncthreads();
+        if (tid == 0) __hip_atomic_store(&a.cnt[x], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    // epilogue: thread j -> stream b = j / (16 RT), local row rl = j % (16 RT), so
+    // consecutive threads write consecutive rows of one stream
+    constexpr int NR = 16 * RT;
+    for (int j = tid; j < NR * BP; j += QT_B2_W * 64) {
+        const int b = j / NR, rl = j % NR, r = r0 + rl;
+        if (b >= a.B || r >= a.rows) continue;
+        if (EPI == QT_EPI_SWIGLU && (rl & 1)) continue;
+        auto val = [&](int rr) -> float {   // rr: local row
+            const int rt = rr >> 4, lr = rr & 15;
+            const int t0 = b >> 4, ln = (lr >> 2) * 16 + (b & 15), i = lr & 3;
+            const double c = (double)red[rt][t0][i][ln] + (double)red[rt][t0 + BP / 16][i][ln] * (1.0 / 128.0) +
+                             (double)red[rt][t0 + 2 * BP / 16][i][ln] * (1.0 / 16384.0);
+            const float dot = (float)(c * (double)a.S[b]);
+            return __fmul_rn(dot, a.scale[r0 + rr]);
+        };
+        float *ob = a.out + (size_t)b * a.ostride;
+        if (EPI == QT_EPI_STORE) ob[r] = val(rl);
+        else if (EPI == QT_EPI_RESID) ob[r] = __fadd_rn(ob[r], val(rl));
+        else if (EPI == QT_EPI_SWIGLU) {
+            const float g = val(rl), u = val(rl + 1);
+            ob[r >> 1] = g / (1.0f + expf(-g)) * u;
+        }
+    }
+}
+
+// The tiling qt_launch_bgemm2_i8 uses for a (rows, K) projection: KB k-blocks per wave,
+// S K ranges, RT row tiles per workgroup.  Returns 0 if the shape has none (K not a
+// multiple of 1024), else fills the workspace it needs (ints of partial tiles and
+// counters; 0 when S == 1).
+extern "C" int qt_bgemm2_plan(int rows, int K, int Bp, int *kb, int *S, int *rt, size_t *part_ints, int *n_cnt) {
+    int KB, SS;
+    if (K % 2048 == 0) { KB = 8; SS = K / 2048; }
+    else if (K % 1024 == 0) { KB = 4; SS = K / 1024; }
+    else return 0;
+    const int tiles = (rows + 15) / 16;
+    if (KB == 8 && tiles * SS < 256) { KB = 4; SS *= 2; }
+    int RT = tiles * SS / 256;
+    RT = RT < 1 ? 1 : RT > 3 ? 3 : RT;
+    const int gx = (tiles + RT - 1) / RT;
+    *kb = KB; *S = SS; *rt = RT;
+    *part_ints = SS > 1 ? (size_t)gx * SS * RT * (3 * Bp / 16) * 256 : 0;
+    *n_cnt = SS > 1 ? gx : 0;
+    return 1;
+}
+
+// part / cnt: workspace from qt_bgemm2_plan (cnt zeroed once at allocation; the kernel
+// re-arms it).  Returns hipErrorInvalidValue for shapes without a plan.
+extern "C" hipError_t qt_launch_bgemm2_i8(int epi, const uint8_t *w, const float *scale, int rows, int K,
+                                          const int8_t *P, const float *S, int B, int Bp, float *out, long long ostride,
+                                          int *part, unsigned *cnt, hipStream_t st) {
+    int KB, SS, RT, ncnt; size_t pints;
+    if (rows <= 0 || B <= 0 || B > Bp || !qt_bgemm2_plan(rows, K, Bp, &KB, &SS, &RT, &pints, &ncnt)) return hipErrorInvalidValue;
+    if (epi == QT_EPI_SWIGLU && (rows & 1)) return hipErrorInvalidValue;
+    if (SS > 1 && (!part || !cnt)) return hipErrorInvalidValue;
+    QtBg2Args a;
+    a.w = w; a.scale = scale; a.rows = rows; a.K = K; a.P = P; a.S = S; a.B = B; a.out = out; a.ostride = ostride;
+    a.part = part; a.cnt = cnt;
+    const dim3 grid(((rows + 15) / 16 + RT - 1) / RT, SS), block(QT_B2_W * 64);
+#define QT_B2_GO(NT_, E_, RT_, KB_) hipLaunchKernelGGL((k_bgemm2_i8<NT_, E_, RT_, KB_>), grid, block, 0, st, a)
+#define QT_B2_KB(NT_, E_, RT_) if (KB == 8) QT_B2_GO(NT_, E_, RT_, 8); else QT_B2_GO(NT_, E_, RT_, 4);
+#define QT_B2_RT(NT_, E_) if (RT == 1) { QT_B2_KB(NT_, E_, 1) } else if (RT == 2) { QT_B2_KB(NT_, E_, 2) } else { QT_B2_KB(NT_, E_, 3) }
+#define QT_B2_EPI(NT_) if (epi == QT_EPI_STORE) { QT_B2_RT(NT_, QT_EPI_STORE) } \
+    else if (epi == QT_EPI_RESID) { QT_B2_RT(NT_, QT_EPI_RESID) } \
+    else if (epi == QT_EPI_SWIGLU) { QT_B2_RT(NT_, QT_EPI_SWIGLU) } else return hipErrorInvalidValue;
+    if (Bp == 16) { QT_B2_EPI(3) }
+    else if (Bp == 32) { QT_B2_EPI(6) }
+    else if (Bp == 48) { QT_B2_EPI(9) }
+    else if (Bp == 64) { QT_B2_EPI(12) }
+    else return hipErrorInvalidValue;
+#undef QT_B2_EPI
+#undef QT_B2_RT
+#undef QT_B2_KB
+#undef QT_B2_GO
+    return hipGetLastError();
 }
 
 // ---- q4_0 weights x activation pieces -------------------------------------------------

@@ -35,6 +35,10 @@ hipError_t qt_launch_bpieces(const float *x, long long xstride, const float *nor
                              int8_t *P, float *S, hipStream_t st);
 hipError_t qt_launch_bgemm_i8(int epi, const uint8_t *w, const float *scale, int rows, int K, const int8_t *P,
                               const float *S, int B, int Bp, float *out, long long ostride, hipStream_t st);
+int qt_bgemm2_plan(int rows, int K, int Bp, int *kb, int *S, int *rt, size_t *part_ints, int *n_cnt);
+hipError_t qt_launch_bgemm2_i8(int epi, const uint8_t *w, const float *scale, int rows, int K, const int8_t *P,
+                               const float *S, int B, int Bp, float *out, long long ostride, int *part, unsigned *cnt,
+                               hipStream_t st);
 hipError_t qt_launch_bgemm_q4(int epi, const uint8_t *w, const uint16_t *s16, int rows, int K, const int8_t *P,
                               const float *S, int B, int Bp, float *out, long long ostride, hipStream_t st);
 hipError_t qt_launch_advance_pos(int *pos, int n, hipStream_t st);

@@ -1456,6 +1456,7 @@ typedef struct {
     float *x, *qkv, *attn, *h, *hid;
     int8_t *pc; float *ps;     /* activation pieces [Kmax/64][3*Bp][64], scales [Bp] */
     uint16_t *pf_p; float *pf_part; /* bf16: activation planes [3][64][Kmax], split-K partials [4][B][H] */
+    int *g2_part; unsigned *g2_cnt; /* int8: split-K tiles and counters of qt_launch_bgemm2_i8 */
     float *part; unsigned *cnt;
     int *d_pos;                /* [B] */
     float *h_io; int *h_pos;   /* pinned */
@@ -1469,7 +1470,7 @@ static void batch_destroy(batch_t *bt) {
     if (!bt) return;
     if (bt->graph_ready) (void)hipGraphExecDestroy(bt->exec);
     void *bufs[] = {bt->kc, bt->vc, bt->x, bt->qkv, bt->attn, bt->h, bt->hid, bt->pc, bt->ps, bt->part, bt->cnt, bt->d_pos,
-                    bt->kv_stage, bt->pf_p, bt->pf_part};
+                    bt->kv_stage, bt->pf_p, bt->pf_part, bt->g2_part, bt->g2_cnt};
     for (size_t i = 0; i < sizeof bufs / sizeof bufs[0]; i++) if (bufs[i]) (void)hipFree(bufs[i]);
     if (bt->h_io) (void)hipHostFree(bt->h_io);
     if (bt->h_pos) (void)hipHostFree(bt->h_pos);
@@ -1501,6 +1502,23 @@ static batch_t *batch_create(const stack_t *s, int B, int is_cp) {
         HCK(hipMalloc((void **)&bt->pf_p, (size_t)3 * qt_pf_spad(B) * K * sizeof(uint16_t)));
         HCK(hipMalloc((void **)&bt->pf_part, (size_t)4 * B * s->H * sizeof(float)));
     }
+    if (s->prec == QWEN_HIP_INT8) {
+        /* workspace of the largest split-K plan over the layer's four projections */
+        const int shp[4][2] = {{s->qd + 2 * s->kvd, s->H}, {s->H, s->qd}, {2 * s->F, s->H}, {s->H, s->F}};
+        size_t pmax = 0; int cmax = 0;
+        for (int i = 0; i < 4; i++) {
+            int kb_, S_, rt_, nc; size_t pi;
+            if (qt_bgemm2_plan(shp[i][0], shp[i][1], bt->Bp, &kb_, &S_, &rt_, &pi, &nc)) {
+                if (pi > pmax) pmax = pi;
+                if (nc > cmax) cmax = nc;
+            }
+        }
+        if (pmax) {
+            HCK(hipMalloc((void **)&bt->g2_part, pmax * sizeof(int)));
+            HCK(hipMalloc((void **)&bt->g2_cnt, (size_t)cmax * sizeof(unsigned)));
+            HCK(hipMemsetAsync(bt->g2_cnt, 0, (size_t)cmax * sizeof(unsigned), bt->st));
+        }
+    }
     HCK(hipMalloc((void **)&bt->part, (size_t)B * s->nkv * s->attn_G * (s->nh / s->nkv) * 130 * sizeof(float)));
     HCK(hipMalloc((void **)&bt->cnt, (size_t)B * s->nkv * sizeof(unsigned)));
     HCK(hipMemsetAsync(bt->cnt, 0, (size_t)B * s->nkv * sizeof(unsigned), bt->st));
@@ -1526,8 +1544,13 @@ static hipError_t batch_proj(batch_t *bt, const dmat_t *m, int epi, const float 
                                  bt->pf_part, bt->st);
     }
     if ((e = qt_launch_bpieces(src, sstride, nw, s->eps, m->cols, bt->B, bt->Bp, bt->pc, bt->ps, bt->st))) return e;
-    if (m->prec == QWEN_HIP_INT8)
+    if (m->prec == QWEN_HIP_INT8) {
+        int kb_, S_, rt_, nc; size_t pi;
+        if (qt_bgemm2_plan(m->rows, m->cols, bt->Bp, &kb_, &S_, &rt_, &pi, &nc) && (S_ == 1 || bt->g2_part))
+            return qt_launch_bgemm2_i8(epi, m->w, m->scale, m->rows, m->cols, bt->pc, bt->ps, bt->B, bt->Bp, dst, dstride,
+                                       bt->g2_part, bt->g2_cnt, bt->st);
         return qt_launch_bgemm_i8(epi, m->w, m->scale, m->rows, m->cols, bt->pc, bt->ps, bt->B, bt->Bp, dst, dstride, bt->st);
+    }
     return qt_launch_bgemm_q4(epi, m->w, m->s16, m->rows, m->cols, bt->pc, bt->ps, bt->B, bt->Bp, dst, dstride, bt->st);
 }
 
@@ -1804,6 +1827,7 @@ static int op_matmat(int prec, float *Y, const void *W, const float *scale, cons
     dmat_t m; memset(&m, 0, sizeof m);
     float *dx = NULL, *dy = NULL, *hx = NULL, *hy = NULL, *ps = NULL;
     int8_t *pc = NULL; void *tmp = NULL;
+    int *g2p = NULL; unsigned *g2c = NULL;
     qwen_hip_mat_t src = {W, scale};
     const int Bp = (B + 15) & ~15;
     REQ(st, "no stream");
@@ -1821,15 +1845,27 @@ static int op_matmat(int prec, float *Y, const void *W, const float *scale, cons
     HCK(hipMalloc((void **)&ps, (size_t)Bp * sizeof(float)));
     HCK(hipMemcpyAsync(dx, hx, (size_t)B * cols * sizeof(float), hipMemcpyHostToDevice, st));
     HCK(qt_launch_bpieces(dx, cols, NULL, 0.f, cols, B, Bp, pc, ps, st));
-    if (prec == QWEN_HIP_INT8)
-        HCK(qt_launch_bgemm_i8(QT_EPI_STORE, m.w, m.scale, rows, cols, pc, ps, B, Bp, dy, rows, st));
-    else
+    if (prec == QWEN_HIP_INT8) {
+        int kb_, S_, rt_, nc; size_t pi;
+        if (qt_bgemm2_plan(rows, cols, Bp, &kb_, &S_, &rt_, &pi, &nc)) {
+            if (pi) {
+                HCK(hipMalloc((void **)&g2p, pi * sizeof(int)));
+                HCK(hipMalloc((void **)&g2c, (size_t)nc * sizeof(unsigned)));
+                HCK(hipMemsetAsync(g2c, 0, (size_t)nc * sizeof(unsigned), st));
+            }
+            HCK(qt_launch_bgemm2_i8(QT_EPI_STORE, m.w, m.scale, rows, cols, pc, ps, B, Bp, dy, rows, g2p, g2c, st));
+        } else {
+            HCK(qt_launch_bgemm_i8(QT_EPI_STORE, m.w, m.scale, rows, cols, pc, ps, B, Bp, dy, rows, st));
+        }
+    } else
         HCK(qt_launch_bgemm_q4(QT_EPI_STORE, m.w, m.s16, rows, cols, pc, ps, B, Bp, dy, rows, st));
     HCK(hipMemcpyAsync(hy, dy, (size_t)B * rows * sizeof(float), hipMemcpyDeviceToHost, st));
     HCK(hipStreamSynchronize(st));
     for (int r = 0; r < rows; r++) for (int j = 0; j < B; j++) Y[(size_t)r * B + j] = hy[(size_t)j * rows + r];
     dmat_free(&m); (void)hipFree(dx); (void)hipFree(dy); (void)hipFree(pc); (void)hipFree(ps);
     if (tmp) (void)hipFree(tmp);
+    if (g2p) (void)hipFree(g2p);
+    if (g2c) (void)hipFree(g2c);
     free(hx); free(hy);
     return 0;
 fail:
@@ -1839,6 +1875,8 @@ fail:
     if (pc) (void)hipFree(pc);
     if (ps) (void)hipFree(ps);
     if (tmp) (void)hipFree(tmp);
+    if (g2p) (void)hipFree(g2p);
+    if (g2c) (void)hipFree(g2c);
     free(hx); free(hy);
     return -1;
 }
