@@ -339,6 +339,34 @@ int qwen_hip_op_quantize_q4_0(const uint16_t *src, int rows, int cols, void *dst
  * 5 down) to f32, from the device copy: proves upload/repack is bit-exact. */
 int qwen_hip_talker_dequant(void *state, int layer, int which, int r0, int n, float *out);
 
+/* ---- speech decoder: codes -> 24 kHz audio (qwen_tts_speech_decoder.c) ---- */
+/* Tensor lookup by the reference's names (the role of get_f32 over ctx->speech_safetensors,
+ * sd.c:77-80): a host pointer to n_elems contiguous f32 values, or NULL if the tensor is
+ * missing or has another size.  The pointer need only stay valid until the next call. */
+typedef const float *(*qwen_hip_sd_get_fn)(void *user, const char *name, long long n_elems);
+/* replaces qwen_speech_decoder_load (sd.c:372-578): uploads the decoder's weights (the
+ * codebooks dequantised from their EMA sums on the device) and returns a state, or NULL
+ * (qwen_hip_last_error() names the missing tensor). */
+void *qwen_hip_sd_init(qwen_hip_sd_get_fn get, void *user);
+/* The same from the speech tokenizer's safetensors file (F32 tensors; a directory is taken
+ * to hold speech_decoder.safetensors), read straight from the file. */
+void *qwen_hip_sd_load_file(const char *path);
+/* replaces qwen_speech_decoder_decode (sd.c:579-1290, the one-shot decode): codes
+ * [n_frames][16] (code0, then the 15 CP codes; values outside [0, 2048) contribute
+ * nothing) -> audio_out[1920 n_frames] in [-1, 1].  1 <= n_frames <= 8000.  Returns the
+ * sample count (1920 n_frames), or -1 (audio_out too small: max_samples). */
+int qwen_hip_sd_decode(void *state, const int *codes, int n_frames, float *audio_out, int max_samples);
+/* No counterpart in the reference: the same on device buffers (d_codes int[n][16],
+ * d_audio f32[1920 n]), enqueued on qwen_hip_sd_stream(state) without a host sync, for
+ * callers whose codes are already on the device (qwen_hip_generate's output). */
+int qwen_hip_sd_decode_device(void *state, const int *d_codes, int n_frames, float *d_audio);
+/* No counterpart in the reference as one call: the VQ lookup and the pre-transformer alone
+ * (sd.c:599-1044, what the reference's streaming decode caches per frame): latent_out
+ * [n_frames][1024], time-major. */
+int qwen_hip_sd_latent(void *state, const int *codes, int n_frames, float *latent_out);
+void *qwen_hip_sd_stream(void *state);
+void qwen_hip_sd_free(void *state);
+
 const char *qwen_hip_last_error(void);
 
 #ifdef __cplusplus

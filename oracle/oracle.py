@@ -532,3 +532,33 @@ def cp_frame_from_tensors(orc: Oracle, tens, shape, prec, cp_cos, cp_sin):
         raise NotImplementedError("mtp projection: build the frame from RefModel instead")
     f.mtp_w = None
     return f, keep
+
+
+class RefSpeechDecoder:
+    """The reference's own speech decoder (qwen_speech_decoder_load + the one-shot
+    qwen_speech_decoder_decode, qwen_tts_speech_decoder.c:372-1290) from oracle/_ref, over
+    an F32 safetensors file of the decoder's tensors."""
+
+    def __init__(self, path, threads=8, variant=""):
+        L = C.CDLL(RefModel.lib_path(variant))
+        vp, i = C.c_void_p, C.c_int
+        L.ref_sd_open.argtypes = [C.c_char_p, i]; L.ref_sd_open.restype = vp
+        L.ref_sd_decode.argtypes = [vp, vp, i, vp, i]; L.ref_sd_decode.restype = i
+        L.ref_time_sd_decode.argtypes = [vp, vp, i]; L.ref_time_sd_decode.restype = C.c_double
+        self.L = L
+        self.h = L.ref_sd_open(str(path).encode(), threads)
+        if not self.h:
+            raise RuntimeError("reference speech decoder load failed")
+
+    def decode(self, codes):
+        codes = np.ascontiguousarray(codes, np.int32)
+        n = codes.shape[0]
+        out = np.empty(n * 1920, np.float32)
+        ns = self.L.ref_sd_decode(self.h, codes.ctypes.data, n, out.ctypes.data, out.size)
+        if ns < 0:
+            raise RuntimeError("reference decode failed")
+        return out[:ns]
+
+    def time_decode(self, codes):
+        codes = np.ascontiguousarray(codes, np.int32)
+        return self.L.ref_time_sd_decode(self.h, codes.ctypes.data, codes.shape[0])

@@ -322,3 +322,62 @@ const char *ref_build_info(void) { return "gcc " __VERSION__; }
 void ref_rms_norm_per_head(float *x, const float *w, int seq, int n_heads, int head_dim, float eps) {
     qwen_rms_norm_per_head(x, w, seq, n_heads, head_dim, eps);
 }
+
+/* ---- speech decoder (qwen_tts_speech_decoder.c) --------------------------------------
+ * The reference's own loader and one-shot decode over an F32 safetensors file holding the
+ * decoder's tensors (qwen_speech_decoder_load reads them by name, sd.c:372-578).  The
+ * config fields the decoder reads are set to the 12 Hz codec's values (qwen_tts.c:207-223). */
+extern int qwen_speech_decoder_load(qwen_tts_ctx_t *ctx);
+extern int qwen_speech_decoder_decode(qwen_tts_ctx_t *ctx, const int *codes, int n_frames, float **audio_out,
+                                      int *n_samples);
+
+void *ref_sd_open(const char *path, int threads) {
+    qwen_tts_ctx_t *ctx = calloc(1, sizeof *ctx);
+    if (!ctx) return NULL;
+    qwen_tts_config_t *c = &ctx->config;
+    c->codebook_size = 2048;
+    c->dec_num_layers = 8;
+    c->dec_head_dim = 64;
+    c->dec_rope_theta = 10000.0f;
+    c->dec_rms_norm_eps = 1e-5f;
+    ctx->silent = 1;
+    qwen_set_threads(threads > 0 ? threads : 1);
+    char err[512];
+    ingot_st *st = NULL;
+    if (ingot_st_open(&st, path, err, sizeof err) != 0) {
+        fprintf(stderr, "ref_sd_open: %s\n", err);
+        free(ctx);
+        return NULL;
+    }
+    ctx->speech_safetensors = st;
+    if (qwen_speech_decoder_load(ctx) != 0) {
+        fprintf(stderr, "ref_sd_open: load failed\n");
+        free(ctx);
+        return NULL;
+    }
+    return ctx;
+}
+
+/* audio of n_frames x 16 codes into out[cap]; returns the sample count, or -1 */
+int ref_sd_decode(void *h, const int *codes, int n_frames, float *out, int cap) {
+    float *audio = NULL;
+    int n = 0;
+    if (qwen_speech_decoder_decode((qwen_tts_ctx_t *)h, codes, n_frames, &audio, &n) != 0 || !audio) return -1;
+    if (n > cap) n = cap;
+    memcpy(out, audio, (size_t)n * sizeof(float));
+    free(audio);
+    return n;
+}
+
+/* wall time of one decode in seconds (the CPU baseline of the device decoder) */
+double ref_time_sd_decode(void *h, const int *codes, int n_frames) {
+    struct timespec t0, t1;
+    float *audio = NULL;
+    int n = 0;
+    clock_gettime(CLOCK_MONOTONIC, &t0);
+    const int rc = qwen_speech_decoder_decode((qwen_tts_ctx_t *)h, codes, n_frames, &audio, &n);
+    clock_gettime(CLOCK_MONOTONIC, &t1);
+    free(audio);
+    if (rc != 0) return -1.0;
+    return (double)(t1.tv_sec - t0.tv_sec) + 1e-9 * (double)(t1.tv_nsec - t0.tv_nsec);
+}

@@ -21,9 +21,9 @@ LIB = os.path.join(PKG, "libqwen_tts_hip.so")
 ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
 ARCH = os.environ.get("QWEN_HIP_ARCH", "gfx950")
 
-HIP_SOURCES = ["qt_matvec.hip", "qt_attn.hip", "qt_misc.hip", "qt_pstep.hip", "qt_batch.hip", "qt_prefill.hip", "qt_sample.hip",
+HIP_SOURCES = ["qt_matvec.hip", "qt_attn.hip", "qt_misc.hip", "qt_pstep.hip", "qt_batch.hip", "qt_prefill.hip", "qt_sample.hip", "qt_sd.hip",
                "qt_noalloc.hip"]
-C_SOURCES = ["qwen_tts_hip.c", "qt_load.c"]
+C_SOURCES = ["qwen_tts_hip.c", "qt_load.c", "qt_sd_host.c"]
 
 HIPCC_FLAGS = ["-O3", "-fPIC", "-std=c++17", f"--offload-arch={ARCH}",
                "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",

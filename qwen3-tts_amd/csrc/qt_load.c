@@ -405,3 +405,53 @@ fail:
     st_close(&f);
     return state;
 }
+
+/* ---- speech decoder from its safetensors file ------------------------------------------- */
+typedef struct {
+    st_file_t f;
+    float *buf;
+    size_t cap;
+} sd_src_t;
+
+/* qwen_hip_sd_get_fn over the file: the F32 tensor `name` of n floats, read into a buffer
+ * that the next call reuses */
+static const float *sd_file_get(void *user, const char *name, long long n) {
+    sd_src_t *S = (sd_src_t *)user;
+    const st_tensor_t *t = st_find(&S->f, name);
+    if (!t) { qt_seterr("load: missing tensor %s", name); return NULL; }
+    if (t->dtype != ST_F32 || t->off1 - t->off0 != (unsigned long long)n * 4) {
+        qt_seterr("load: tensor %s is dtype %d with %llu bytes, expected F32 with %lld floats", name, t->dtype,
+                  t->off1 - t->off0, n);
+        return NULL;
+    }
+    if ((size_t)n > S->cap) {
+        free(S->buf);
+        S->buf = (float *)malloc((size_t)n * sizeof(float));
+        S->cap = S->buf ? (size_t)n : 0;
+        if (!S->buf) { qt_seterr("load: out of host memory"); return NULL; }
+    }
+    size_t got = 0, bytes = (size_t)n * 4;
+    while (got < bytes) {
+        ssize_t r = pread(S->f.fd, (char *)S->buf + got, bytes - got, (off_t)(S->f.data_start + t->off0 + got));
+        if (r <= 0) { qt_seterr("load: read of %s failed", name); return NULL; }
+        got += (size_t)r;
+    }
+    return S->buf;
+}
+
+void *qwen_hip_sd_load_file(const char *path) {
+    char buf[4096];
+    struct stat sb;
+    if (!path) { qt_seterr("load: null path"); return NULL; }
+    if (stat(path, &sb) == 0 && S_ISDIR(sb.st_mode)) {
+        snprintf(buf, sizeof buf, "%s/speech_decoder.safetensors", path);
+        path = buf;
+    }
+    sd_src_t S;
+    memset(&S, 0, sizeof S);
+    if (st_open(&S.f, path)) return NULL;
+    void *state = qwen_hip_sd_init(sd_file_get, &S);
+    st_close(&S.f);
+    free(S.buf);
+    return state;
+}

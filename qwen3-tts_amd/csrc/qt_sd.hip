@@ -1,0 +1,372 @@
+// qt_sd.hip — the speech decoder (codes -> 24 kHz audio) on gfx950.
+//
+// The reference's one-shot decode (qwen_speech_decoder_decode, qwen_tts_speech_decoder.c:
+// 579-1290) is a VQ lookup, an 8-layer windowed-attention transformer over the frames and
+// a convolutional upsampler (ConvNeXt x2, then four blocks of transposed conv + dilated
+// residual units) to 1920 samples per frame.  All of it is f32.  Here every activation is
+// kept time-major ([T][C], channels contiguous), and every projection, convolution and
+// transposed convolution is one implicit GEMM on the f32 matrix cores:
+//
+//   Y[t*os + z][n] = epi( sum over taps p, channels k of X[t + off_p][k] * W[z][p][k][n] )
+//
+// (rows of X outside [0, Tx) read as zero: the causal left padding).  A causal conv of
+// kernel K and dilation d has taps off_p = (p - K + 1) d; a transposed conv of stride s
+// and kernel 2s is s phases z (output rows t*s + z), each with taps at offsets 0 and -1
+// (kernel columns z and z + s); a linear layer is one tap.  The epilogue adds a bias,
+// applies GELU, scales per column (layer scale, ConvNeXt gamma) and adds a residual.
+// Products accumulate in f32 in MFMA order (the reference sums in loop order): the
+// results agree to f32 rounding, not bitwise.
+#include "qt_device.h"
+
+typedef float qt_sd_f4 __attribute__((ext_vector_type(4)));
+
+#define SD_WG 256
+#define SD_TM 64                 // output rows (time) per workgroup
+#define SD_TN 64                 // output columns (channels) per workgroup
+#define SD_KC 16                 // K chunk staged per step
+#define SD_AS (SD_KC + 1)        // A tile row stride (floats): 17 spreads 16 rows over banks
+#define SD_BS 80                 // B tile row stride: rows k, k+1 land on opposite bank halves
+#define SD_MAXTAP 8
+
+enum { SD_EPI_BIAS = 1, SD_EPI_GELU = 2, SD_EPI_CSCALE = 4, SD_EPI_RESID = 8 };
+
+struct SdGemmArgs {
+    const float *X; int ldx, Tx;          // input rows [Tx][ldx]
+    const float *W;                       // [phases][ntap][K][N]
+    int K, N, ntap;
+    int off[SD_MAXTAP];
+    int T;                                // output rows per phase (t < T)
+    float *Y; int ldy, os;                // output row t*os + phase
+    const float *bias, *cscale;
+    const float *R;                       // residual, same indexing as Y (may alias Y)
+    int epi;
+};
+
+__device__ __forceinline__ float sd_gelu(float x) {
+    return 0.5f * x * (1.0f + erff(x * 0.7071067811865476f));
+}
+
+// 64 x 64 output tile, four waves of 32 x 32 (2 x 2 MFMA tiles of 16 x 16); K in chunks of
+// 16 staged through LDS, the next chunk's global loads in registers while the MFMAs run.
+// v_mfma_f32_16x16x4_f32: lane l supplies A[l % 16][l / 16] and B[l / 16][l % 16] and
+// receives D[4 (l / 16) + r][l % 16], r < 4.
+__global__ __launch_bounds__(SD_WG) void k_sd_gemm(SdGemmArgs a) {
+    __shared__ float As[2][SD_TM * SD_AS];
+    __shared__ float Bs[2][SD_KC * SD_BS];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int t0 = blockIdx.x * SD_TM, n0 = blockIdx.y * SD_TN, z = blockIdx.z;
+    const float *W = a.W + (size_t)z * a.ntap * a.K * a.N;
+    const int kpt = a.K / SD_KC, nch = a.ntap * kpt;
+    // staging roles: A: row tid/4, 4 columns at (tid%4)*4; B: row tid/16, 4 columns at (tid%16)*4
+    const int ar = tid >> 2, ac = (tid & 3) * 4, br = tid >> 4, bc = (tid & 15) * 4;
+    const bool a_row_ok = t0 + ar < a.T, b_col_ok = n0 + bc < a.N;
+    auto fetch = [&](int c, float4 &av, float4 &bv) {
+        const int p = c / kpt, k0 = (c - p * kpt) * SD_KC;
+        const int xr = t0 + ar + a.off[p];
+        av = (a_row_ok && xr >= 0 && xr < a.Tx) ? *reinterpret_cast<const float4 *>(a.X + (size_t)xr * a.ldx + k0 + ac)
+                                                : make_float4(0.f, 0.f, 0.f, 0.f);
+        bv = b_col_ok ? *reinterpret_cast<const float4 *>(W + ((size_t)p * a.K + k0 + br) * a.N + n0 + bc)
+                      : make_float4(0.f, 0.f, 0.f, 0.f);
+    };
+    auto stage = [&](int buf, const float4 &av, const float4 &bv) {
+        float *as = As[buf] + ar * SD_AS + ac;
+        as[0] = av.x; as[1] = av.y; as[2] = av.z; as[3] = av.w;
+        *reinterpret_cast<float4 *>(Bs[buf] + br * SD_BS + bc) = bv;
+    };
+    const int wm = (wave >> 1) * 32, wn = (wave & 1) * 32;
+    const int li = lane & 15, lk = lane >> 4;
+    qt_sd_f4 acc[2][2];
+#pragma unroll
+    for (int i = 0; i < 2; i++)
+#pragma unroll
+        for (int j = 0; j < 2; j++) acc[i][j] = qt_sd_f4{0.f, 0.f, 0.f, 0.f};
+    float4 av, bv;
+    fetch(0, av, bv);
+    stage(0, av, bv);
+    __syncthreads();
+    for (int c = 0; c < nch; c++) {
+        const int buf = c & 1;
+        if (c + 1 < nch) fetch(c + 1, av, bv);
+        const float *as = As[buf], *bs = Bs[buf];
+#pragma unroll
+        for (int kk = 0; kk < SD_KC; kk += 4) {
+            float fa[2], fb[2];
+#pragma unroll
+            for (int i = 0; i < 2; i++) fa[i] = as[(wm + 16 * i + li) * SD_AS + kk + lk];
+#pragma unroll
+            for (int j = 0; j < 2; j++) fb[j] = bs[(kk + lk) * SD_BS + wn + 16 * j + li];
+#pragma unroll
+            for (int i = 0; i < 2; i++)
+#pragma unroll
+                for (int j = 0; j < 2; j++) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(fa[i], fb[j], acc[i][j], 0, 0, 0);
+        }
+        if (c + 1 < nch) stage(buf ^ 1, av, bv);
+        __syncthreads();
+    }
+#pragma unroll
+    for (int i = 0; i < 2; i++)
+#pragma unroll
+        for (int j = 0; j < 2; j++) {
+            const int n = n0 + wn + 16 * j + li;
+            if (n >= a.N) continue;
+            const float bn = (a.epi & SD_EPI_BIAS) ? a.bias[n] : 0.f;
+            const float sn = (a.epi & SD_EPI_CSCALE) ? a.cscale[n] : 1.f;
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const int t = t0 + wm + 16 * i + 4 * lk + r;
+                if (t >= a.T) continue;
+                const size_t o = (size_t)(t * a.os + z) * a.ldy + n;
+                float v = acc[i][j][r];
+                if (a.epi & SD_EPI_BIAS) v += bn;
+                if (a.epi & SD_EPI_GELU) v = sd_gelu(v);
+                if (a.epi & SD_EPI_CSCALE) v *= sn;
+                if (a.epi & SD_EPI_RESID) v = a.R[o] + v;
+                a.Y[o] = v;
+            }
+        }
+}
+
+// ---- elementwise / small kernels ---------------------------------------------------------
+
+// codebook = embedding_sum / max(cluster_usage, 1e-5) (sd.c:383-405), [rows][dim]
+__global__ void k_sd_cb_dequant(const float *es, const float *cu, float *cb, int rows, int dim) {
+    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < (size_t)rows * dim) cb[i] = es[i] / fmaxf(cu[i / dim], 1e-5f);
+}
+
+// exp of the snake log-parameters: a = e^alpha, ib = e^-beta (k.c:4475-4476)
+__global__ void k_sd_snake_params(const float *la, const float *lb, float *a, float *ib, int n) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) { a[i] = expf(la[i]); ib[i] = expf(-lb[i]); }
+}
+
+// per frame: E[f][0:256] = codebook 0 row, E[f][256:512] = sum of codebooks 1..15 rows in
+// order (sd.c:604-625); codes outside [0, 2048) add nothing
+__global__ void k_sd_vq(const int *codes, const float *cb, float *E, int cbsize) {
+    const int f = blockIdx.x, d = threadIdx.x;        // 256 threads = codebook dim
+    const int *c = codes + f * 16;
+    const int c0 = c[0];
+    E[(size_t)f * 512 + d] = (c0 >= 0 && c0 < cbsize) ? cb[(size_t)c0 * 256 + d] : 0.f;
+    float s = 0.f;
+    for (int k = 1; k < 16; k++) {
+        const int ck = c[k];
+        if (ck >= 0 && ck < cbsize) s += cb[((size_t)k * cbsize + ck) * 256 + d];
+    }
+    E[(size_t)f * 512 + 256 + d] = s;
+}
+
+// RMSNorm of rows (qwen_rms_norm, k.c:292-382): out = x * (1/sqrt(mean(x^2) + eps)) * w
+__global__ __launch_bounds__(SD_WG) void k_sd_rmsnorm(const float *x, const float *w, float *out, int C, float eps) {
+    __shared__ float red[QT_WAVES];
+    const float *xr = x + (size_t)blockIdx.x * C;
+    float ss = 0.f;
+    for (int i = threadIdx.x; i < C; i += SD_WG) ss = fmaf(xr[i], xr[i], ss);
+    ss = block_sum(ss, red);
+    const float inv = 1.0f / sqrtf(ss / (float)C + eps);
+    for (int i = threadIdx.x; i < C; i += SD_WG) out[(size_t)blockIdx.x * C + i] = (xr[i] * inv) * w[i];
+}
+
+// NeoX split-half RoPE of q and k (columns [0, 1024) and [1024, 2048) of a [T][3072] row),
+// 16 heads of 64, tables [pos][32] (sd.c:790-860)
+__global__ void k_sd_rope(float *qkv, const float *cs, const float *sn, int T) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;      // (t, which, head, pair)
+    if (i >= T * 2 * 16 * 32) return;
+    const int pr = i & 31, h = (i >> 5) & 15, which = (i >> 9) & 1, t = i >> 10;
+    float *v = qkv + (size_t)t * 3072 + which * 1024 + h * 64;
+    const float c = cs[t * 32 + pr], s = sn[t * 32 + pr];
+    const float x1 = v[pr], x2 = v[pr + 32];
+    v[pr] = x1 * c - x2 * s;
+    v[pr + 32] = x2 * c + x1 * s;
+}
+
+// windowed causal attention (qwen_causal_attention_windowed, k.c:3579-3700; seq_q == seq_k,
+// q_offset 0): query t of head h over keys [max(0, t + 1 - window), t].  One wave per
+// (t, h): lanes take keys for the scores (dot over 64 dims), then lanes take dims for
+// the weighted sum of values.
+__global__ __launch_bounds__(SD_WG) void k_sd_attn(const float *qkv, float *out, int T, int window, float scale) {
+    __shared__ float sq[QT_WAVES][64];
+    __shared__ float sp[QT_WAVES][128];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int item = blockIdx.x * QT_WAVES + wave;
+    if (item >= T * 16) return;
+    const int t = item >> 4, h = item & 15;
+    const int j0 = max(0, t + 1 - window), nk = t + 1 - j0;   // nk <= window <= 128
+    sq[wave][lane] = qkv[(size_t)t * 3072 + h * 64 + lane];
+    __builtin_amdgcn_s_waitcnt(0);
+    __builtin_amdgcn_wave_barrier();
+    float sc[2];
+    float mx = -INFINITY;
+#pragma unroll
+    for (int r = 0; r < 2; r++) {
+        const int j = r * 64 + lane;
+        float s = -INFINITY;
+        if (j < nk) {
+            const float *kr = qkv + (size_t)(j0 + j) * 3072 + 1024 + h * 64;
+            float d = 0.f;
+            for (int e = 0; e < 64; e += 4) {
+                const float4 kv = *reinterpret_cast<const float4 *>(kr + e);
+                d = fmaf(sq[wave][e], kv.x, d); d = fmaf(sq[wave][e + 1], kv.y, d);
+                d = fmaf(sq[wave][e + 2], kv.z, d); d = fmaf(sq[wave][e + 3], kv.w, d);
+            }
+            s = d * scale;
+        }
+        sc[r] = s;
+        mx = fmaxf(mx, s);
+    }
+    mx = group_max<64>(mx);
+    float l = 0.f;
+#pragma unroll
+    for (int r = 0; r < 2; r++) {
+        const int j = r * 64 + lane;
+        const float p = j < nk ? expf(sc[r] - mx) : 0.f;
+        sp[wave][j] = p;
+        l += p;
+    }
+    l = group_sum<64>(l);
+    __builtin_amdgcn_s_waitcnt(0);
+    __builtin_amdgcn_wave_barrier();
+    float o = 0.f;
+    for (int j = 0; j < nk; j++) o = fmaf(sp[wave][j], qkv[(size_t)(j0 + j) * 3072 + 2048 + h * 64 + lane], o);
+    out[(size_t)t * 1024 + h * 64 + lane] = o * (1.0f / l);
+}
+
+// m[t][i] = g / (1 + e^-g) * u for the [T][2C] gate|up rows (sd.c:946-950)
+__global__ void k_sd_swiglu(const float *gu, float *m, int T, int C) {
+    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= (size_t)T * C) return;
+    const size_t t = i / C, c = i % C;
+    const float g = gu[t * 2 * C + c], u = gu[t * 2 * C + C + c];
+    m[i] = g / (1.0f + expf(-g)) * u;
+}
+
+// ConvNeXt: depthwise causal conv (k = 7, pad 6) + LayerNorm over the channels of each
+// time step (mean and E[x^2] - mean^2, eps 1e-5), sd.c:1086-1116.  One workgroup per t.
+__global__ __launch_bounds__(SD_WG) void k_sd_dwln(const float *x, const float *dw, const float *db, const float *lw,
+                                                   const float *lb, float *out, int T, int C) {
+    __shared__ float red[QT_WAVES];
+    const int t = blockIdx.x;
+    float v[4];
+    float s = 0.f, s2 = 0.f;
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+        const int c = threadIdx.x + q * SD_WG;
+        float d = 0.f;
+        if (c < C) {
+            d = db[c];
+            for (int j = 0; j < 7; j++) {
+                const int ti = t - 6 + j;
+                if (ti >= 0) d = fmaf(dw[c * 7 + j], x[(size_t)ti * C + c], d);
+            }
+        }
+        v[q] = d;
+        s += d;
+        s2 = fmaf(d, d, s2);
+    }
+    s = block_sum(s, red);
+    __syncthreads();
+    s2 = block_sum(s2, red);
+    const float mean = s / (float)C;
+    const float var = s2 / (float)C - mean * mean;
+    const float inv = 1.0f / sqrtf(var + 1e-5f);
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+        const int c = threadIdx.x + q * SD_WG;
+        if (c < C) out[(size_t)t * C + c] = (v[q] - mean) * inv * lw[c] + lb[c];
+    }
+}
+
+// snake (k.c:4472-4600): y = x + ib[c] * sin(a[c] x)^2, per channel c of [T][C]
+__global__ void k_sd_snake(const float *x, float *y, const float *a, const float *ib, size_t n, int C) {
+    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    const int c = (int)(i % C);
+    const float xv = x[i];
+    const float s = sinf(a[c] * xv);
+    y[i] = fmaf(ib[c], s * s, xv);
+}
+
+// final conv to one channel (k = 7, pad 6) + clamp to [-1, 1] (sd.c:1259-1279); x [T][C]
+// already through the final snake
+__global__ void k_sd_final(const float *x, const float *w, const float *b, float *audio, int T, int C) {
+    const int t = blockIdx.x * blockDim.x + threadIdx.x;
+    if (t >= T) return;
+    float s = b[0];
+    for (int j = 0; j < 7; j++) {
+        const int ti = t - 6 + j;
+        if (ti < 0) continue;
+        const float *xr = x + (size_t)ti * C;
+        for (int c = 0; c < C; c++) s = fmaf(w[c * 7 + j], xr[c], s);
+    }
+    audio[t] = fminf(fmaxf(s, -1.0f), 1.0f);
+}
+
+// ---- launchers ----------------------------------------------------------------------------
+
+extern "C" hipError_t qt_launch_sd_gemm(const float *X, int ldx, int Tx, const float *W, int K, int N, int ntap,
+                                        const int *off, int phases, int T, float *Y, int ldy, const float *bias,
+                                        const float *cscale, const float *R, int epi, hipStream_t st) {
+    if (!X || !W || !Y || K <= 0 || K % SD_KC || N <= 0 || N % 4 || ntap < 1 || ntap > SD_MAXTAP || phases < 1 ||
+        T <= 0 || Tx <= 0 || ldx % 4 || ldx < K || ldy < N)
+        return hipErrorInvalidValue;
+    if (((epi & 1) && !bias) || ((epi & 4) && !cscale) || ((epi & 8) && !R)) return hipErrorInvalidValue;
+    SdGemmArgs a;
+    a.X = X; a.ldx = ldx; a.Tx = Tx; a.W = W; a.K = K; a.N = N; a.ntap = ntap;
+    for (int i = 0; i < SD_MAXTAP; i++) a.off[i] = i < ntap ? off[i] : 0;
+    a.T = T; a.Y = Y; a.ldy = ldy; a.os = phases; a.bias = bias; a.cscale = cscale; a.R = R; a.epi = epi;
+    dim3 grid((T + SD_TM - 1) / SD_TM, (N + SD_TN - 1) / SD_TN, phases);
+    hipLaunchKernelGGL(k_sd_gemm, grid, dim3(SD_WG), 0, st, a);
+    return hipGetLastError();
+}
+
+extern "C" hipError_t qt_launch_sd_cb_dequant(const float *es, const float *cu, float *cb, int rows, int dim,
+                                              hipStream_t st) {
+    const size_t n = (size_t)rows * dim;
+    hipLaunchKernelGGL(k_sd_cb_dequant, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, es, cu, cb, rows, dim);
+    return hipGetLastError();
+}
+extern "C" hipError_t qt_launch_sd_snake_params(const float *la, const float *lb, float *a, float *ib, int n,
+                                                hipStream_t st) {
+    hipLaunchKernelGGL(k_sd_snake_params, dim3((n + 255) / 256), dim3(256), 0, st, la, lb, a, ib, n);
+    return hipGetLastError();
+}
+extern "C" hipError_t qt_launch_sd_vq(const int *codes, const float *cb, float *E, int n, int cbsize, hipStream_t st) {
+    hipLaunchKernelGGL(k_sd_vq, dim3(n), dim3(256), 0, st, codes, cb, E, cbsize);
+    return hipGetLastError();
+}
+extern "C" hipError_t qt_launch_sd_rmsnorm(const float *x, const float *w, float *out, int T, int C, float eps,
+                                           hipStream_t st) {
+    hipLaunchKernelGGL(k_sd_rmsnorm, dim3(T), dim3(SD_WG), 0, st, x, w, out, C, eps);
+    return hipGetLastError();
+}
+extern "C" hipError_t qt_launch_sd_rope(float *qkv, const float *cs, const float *sn, int T, hipStream_t st) {
+    const int n = T * 1024;
+    hipLaunchKernelGGL(k_sd_rope, dim3((n + 255) / 256), dim3(256), 0, st, qkv, cs, sn, T);
+    return hipGetLastError();
+}
+extern "C" hipError_t qt_launch_sd_attn(const float *qkv, float *out, int T, int window, float scale, hipStream_t st) {
+    if (window <= 0 || window > 128) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_sd_attn, dim3((T * 16 + QT_WAVES - 1) / QT_WAVES), dim3(SD_WG), 0, st, qkv, out, T, window, scale);
+    return hipGetLastError();
+}
+extern "C" hipError_t qt_launch_sd_swiglu(const float *gu, float *m, int T, int C, hipStream_t st) {
+    const size_t n = (size_t)T * C;
+    hipLaunchKernelGGL(k_sd_swiglu, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, gu, m, T, C);
+    return hipGetLastError();
+}
+extern "C" hipError_t qt_launch_sd_dwln(const float *x, const float *dw, const float *db, const float *lw, const float *lb,
+                                        float *out, int T, int C, hipStream_t st) {
+    if (C > 4 * SD_WG) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_sd_dwln, dim3(T), dim3(SD_WG), 0, st, x, dw, db, lw, lb, out, T, C);
+    return hipGetLastError();
+}
+extern "C" hipError_t qt_launch_sd_snake(const float *x, float *y, const float *a, const float *ib, int T, int C,
+                                         hipStream_t st) {
+    const size_t n = (size_t)T * C;
+    hipLaunchKernelGGL(k_sd_snake, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, x, y, a, ib, n, C);
+    return hipGetLastError();
+}
+extern "C" hipError_t qt_launch_sd_final(const float *x, const float *w, const float *b, float *audio, int T, int C,
+                                         hipStream_t st) {
+    hipLaunchKernelGGL(k_sd_final, dim3((T + 255) / 256), dim3(256), 0, st, x, w, b, audio, T, C);
+    return hipGetLastError();
+}

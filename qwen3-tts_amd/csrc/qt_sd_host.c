@@ -1,0 +1,464 @@
+/* qt_sd_host.c — host side of the device speech decoder (qt_sd.hip): weights by the reference's
+ * tensor names (qwen_speech_decoder_load, qwen_tts_speech_decoder.c:372-578) rearranged
+ * into the implicit-GEMM layouts, and the one-shot decode sequence of
+ * qwen_speech_decoder_decode (sd.c:579-1290) as kernel launches on one stream.
+ *
+ * Layouts on the device (all f32): activations [T][C]; a conv or linear layer is
+ * W[phase][tap][K = in][N = out] with per-tap input row offsets:
+ *   linear   [out][in]              -> one tap, offset 0 (W transposed);
+ *   conv1d   [out][in][k], dil d    -> k taps, offsets (p - k + 1) d;
+ *   convT    [in][out][2s], stride s-> s phases (output rows t*s + z), taps: column z at
+ *            offset 0 and column z + s at offset -1 (when z + s < kernel).
+ */
+#include "qwen_tts_hip.h"
+#include "qt_launch.h"
+
+#include <hip/hip_runtime_api.h>
+#include <math.h>
+#include <stdarg.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+
+#define SD_CB 256
+#define SD_CBSIZE 2048
+#define SD_ROPE_POS 8000
+#define SD_SPF 1920               /* samples per frame */
+
+enum { SD_BIAS = 1, SD_GELU = 2, SD_CSCALE = 4, SD_RESID = 8 };
+
+typedef struct {
+    float *w, *b;
+    int K, N, ntap, phases;
+    int off[8];
+} sd_conv_t;
+
+typedef struct { float *a, *ib; } sd_snake_t;
+
+typedef struct {
+    float *n1, *n2, *ls1, *ls2;
+    sd_conv_t qkv, o, gu, dn;
+} sd_layer_t;
+
+typedef struct {
+    hipStream_t st;
+    float *cb;                    /* [16][2048][256] dequantised codebooks */
+    sd_conv_t vq, pre, inp, outp, init;
+    sd_layer_t L[8];
+    float *fnorm;
+    struct { sd_conv_t up, pw1, pw2; float *dw, *db, *lw, *lb, *gamma; } cn[2];
+    struct { sd_snake_t s; sd_conv_t up; struct { sd_snake_t s1, s2; sd_conv_t c1, c2; } r[3]; } blk[4];
+    sd_snake_t fs;
+    float *fw, *fb;
+    float *rope_c, *rope_s;       /* [8000][32] */
+    /* workspace, grown to the largest call */
+    int cap;
+    float *E, *V, *P, *H, *XN, *QKV, *A, *GU, *M, *LAT, *big[3];
+    int *dcodes; float *daudio;
+    void **allocs; int n_allocs, cap_allocs;
+} sd_t;
+
+static const int UP_RATE[4] = {8, 5, 4, 3}, UP_CH[4] = {768, 384, 192, 96}, DIL[3] = {1, 3, 9};
+
+/* ---- allocation bookkeeping ------------------------------------------------------------ */
+static void *sd_dalloc(sd_t *s, size_t bytes) {
+    void *p = NULL;
+    if (s->n_allocs == s->cap_allocs) {
+        int nc = s->cap_allocs ? 2 * s->cap_allocs : 256;
+        void **na = (void **)realloc(s->allocs, (size_t)nc * sizeof *na);
+        if (!na) return NULL;
+        s->allocs = na; s->cap_allocs = nc;
+    }
+    if (hipMalloc(&p, bytes ? bytes : 4) != hipSuccess) return NULL;
+    s->allocs[s->n_allocs++] = p;
+    return p;
+}
+
+void qwen_hip_sd_free(void *state) {
+    sd_t *s = (sd_t *)state;
+    if (!s) return;
+    if (s->st) (void)hipStreamSynchronize(s->st);
+    for (int i = 0; i < s->n_allocs; i++) (void)hipFree(s->allocs[i]);
+    free(s->allocs);
+    float *ws[] = {s->E, s->V, s->P, s->H, s->XN, s->QKV, s->A, s->GU, s->M, s->LAT, s->big[0], s->big[1], s->big[2],
+                   s->daudio};
+    for (size_t i = 0; i < sizeof ws / sizeof ws[0]; i++) if (ws[i]) (void)hipFree(ws[i]);
+    if (s->dcodes) (void)hipFree(s->dcodes);
+    if (s->st) (void)hipStreamDestroy(s->st);
+    free(s);
+}
+
+/* ---- weights ------------------------------------------------------------------------------ */
+typedef struct {
+    qwen_hip_sd_get_fn get;
+    void *user;
+    sd_t *s;
+    float *tmp; size_t tmp_n;
+    int bad;
+} sd_ld_t;
+
+static const float *sd_get(sd_ld_t *L, const char *name, long long n) {
+    if (L->bad) return NULL;
+    const float *p = L->get(L->user, name, n);
+    if (!p) {
+        if (!qwen_hip_last_error()[0] || !strstr(qwen_hip_last_error(), name))
+            qt_seterr("sd_init: missing tensor %s (%lld floats)", name, n);
+        L->bad = 1;
+    }
+    return p;
+}
+
+static float *sd_tmp(sd_ld_t *L, size_t n) {
+    if (n > L->tmp_n) {
+        free(L->tmp);
+        L->tmp = (float *)malloc(n * sizeof(float));
+        L->tmp_n = L->tmp ? n : 0;
+        if (!L->tmp) { qt_seterr("sd_init: out of host memory"); L->bad = 1; }
+    }
+    return L->tmp;
+}
+
+/* host f32 -> new device buffer (synchronous: the host source may be reused) */
+static float *sd_put(sd_ld_t *L, const float *src, size_t n) {
+    if (L->bad || !src) return NULL;
+    float *d = (float *)sd_dalloc(L->s, n * sizeof(float));
+    if (!d || hipMemcpy(d, src, n * sizeof(float), hipMemcpyHostToDevice) != hipSuccess) {
+        qt_seterr("sd_init: device allocation or upload failed");
+        L->bad = 1;
+        return NULL;
+    }
+    return d;
+}
+
+static float *sd_vec(sd_ld_t *L, const char *name, long long n) { return sd_put(L, sd_get(L, name, n), (size_t)n); }
+
+static sd_snake_t sd_snake(sd_ld_t *L, const char *pa, const char *pb, int n) {
+    sd_snake_t r = {NULL, NULL};
+    float *la = sd_vec(L, pa, n), *lb = sd_vec(L, pb, n);
+    if (L->bad) return r;
+    r.a = (float *)sd_dalloc(L->s, (size_t)n * sizeof(float));
+    r.ib = (float *)sd_dalloc(L->s, (size_t)n * sizeof(float));
+    if (!r.a || !r.ib || qt_launch_sd_snake_params(la, lb, r.a, r.ib, n, L->s->st) != hipSuccess) L->bad = 1;
+    return r;
+}
+
+/* linear [out][in] (+ bias) -> one tap [in][out] */
+static sd_conv_t sd_linear(sd_ld_t *L, const char *wn, const char *bn, int out, int in) {
+    sd_conv_t c; memset(&c, 0, sizeof c);
+    c.K = in; c.N = out; c.ntap = 1; c.phases = 1;
+    const float *w = sd_get(L, wn, (long long)out * in);
+    float *t = sd_tmp(L, (size_t)out * in);
+    if (L->bad) return c;
+    for (int o = 0; o < out; o++) for (int i = 0; i < in; i++) t[(size_t)i * out + o] = w[(size_t)o * in + i];
+    c.w = sd_put(L, t, (size_t)out * in);
+    if (bn) c.b = sd_vec(L, bn, out);
+    return c;
+}
+
+/* causal conv [out][in][k], dilation d -> k taps [p][in][out] at offsets (p - k + 1) d */
+static sd_conv_t sd_conv(sd_ld_t *L, const char *wn, const char *bn, int out, int in, int k, int d) {
+    sd_conv_t c; memset(&c, 0, sizeof c);
+    c.K = in; c.N = out; c.ntap = k; c.phases = 1;
+    for (int p = 0; p < k; p++) c.off[p] = (p - k + 1) * d;
+    const float *w = sd_get(L, wn, (long long)out * in * k);
+    float *t = sd_tmp(L, (size_t)out * in * k);
+    if (L->bad) return c;
+    for (int o = 0; o < out; o++)
+        for (int i = 0; i < in; i++)
+            for (int p = 0; p < k; p++) t[((size_t)p * in + i) * out + o] = w[((size_t)o * in + i) * k + p];
+    c.w = sd_put(L, t, (size_t)out * in * k);
+    if (bn) c.b = sd_vec(L, bn, out);
+    return c;
+}
+
+/* causal transposed conv [in][out][k], stride s (k <= 2s) -> s phases of taps at offsets
+ * 0 (column z) and -1 (column z + s, when it exists) */
+static sd_conv_t sd_convt(sd_ld_t *L, const char *wn, const char *bn, int in, int out, int k, int s) {
+    sd_conv_t c; memset(&c, 0, sizeof c);
+    c.K = in; c.N = out; c.phases = s; c.ntap = k > s ? 2 : 1;
+    c.off[0] = 0; c.off[1] = -1;
+    const float *w = sd_get(L, wn, (long long)in * out * k);
+    const size_t per = (size_t)in * out;
+    float *t = sd_tmp(L, (size_t)s * c.ntap * per);
+    if (L->bad) return c;
+    for (int z = 0; z < s; z++)
+        for (int p = 0; p < c.ntap; p++) {
+            const int col = z + p * s;
+            float *dst = t + ((size_t)z * c.ntap + p) * per;
+            for (int i = 0; i < in; i++)
+                for (int o = 0; o < out; o++) dst[(size_t)i * out + o] = w[((size_t)i * out + o) * k + col];
+        }
+    c.w = sd_put(L, t, (size_t)s * c.ntap * per);
+    if (bn) c.b = sd_vec(L, bn, out);
+    return c;
+}
+
+void *qwen_hip_sd_init(qwen_hip_sd_get_fn get, void *user) {
+    int ndev = 0;
+    if (!get) { qt_seterr("sd_init: no tensor getter"); return NULL; }
+    if (hipGetDeviceCount(&ndev) != hipSuccess || ndev < 1) { qt_seterr("sd_init: no HIP device"); return NULL; }
+    sd_t *s = (sd_t *)calloc(1, sizeof *s);
+    if (!s) { qt_seterr("sd_init: out of host memory"); return NULL; }
+    sd_ld_t L = {get, user, s, NULL, 0, 0};
+    char nm[160], nb[160];
+    if (hipStreamCreateWithFlags(&s->st, hipStreamNonBlocking) != hipSuccess) { qt_seterr("sd_init: stream"); goto fail; }
+    /* codebooks: EMA sums over usage, on the device */
+    s->cb = (float *)sd_dalloc(s, (size_t)16 * SD_CBSIZE * SD_CB * sizeof(float));
+    if (!s->cb) { qt_seterr("sd_init: device allocation failed"); goto fail; }
+    for (int k = 0; k < 16 && !L.bad; k++) {
+        const char *pfx = k == 0 ? "decoder.quantizer.rvq_first.vq.layers.0._codebook" : NULL;
+        char pb[128];
+        if (!pfx) { snprintf(pb, sizeof pb, "decoder.quantizer.rvq_rest.vq.layers.%d._codebook", k - 1); pfx = pb; }
+        snprintf(nm, sizeof nm, "%s.embedding_sum", pfx);
+        snprintf(nb, sizeof nb, "%s.cluster_usage", pfx);
+        float *es = sd_vec(&L, nm, (long long)SD_CBSIZE * SD_CB), *cu = sd_vec(&L, nb, SD_CBSIZE);
+        if (L.bad) break;
+        if (qt_launch_sd_cb_dequant(es, cu, s->cb + (size_t)k * SD_CBSIZE * SD_CB, SD_CBSIZE, SD_CB, s->st) != hipSuccess ||
+            hipStreamSynchronize(s->st) != hipSuccess) { qt_seterr("sd_init: codebook dequantisation failed"); goto fail; }
+    }
+    /* VQ projections as one K = 512 product of [codebook 0 | sum of 1..15] rows */
+    {
+        s->vq.K = 2 * SD_CB; s->vq.N = 512; s->vq.ntap = 1; s->vq.phases = 1;
+        const float *w1 = sd_get(&L, "decoder.quantizer.rvq_first.output_proj.weight", 512LL * SD_CB);
+        float *t = sd_tmp(&L, (size_t)2 * SD_CB * 512);
+        if (!L.bad) for (int o = 0; o < 512; o++) for (int i = 0; i < SD_CB; i++) t[(size_t)i * 512 + o] = w1[(size_t)o * SD_CB + i];
+        const float *w2 = sd_get(&L, "decoder.quantizer.rvq_rest.output_proj.weight", 512LL * SD_CB);
+        if (!L.bad) for (int o = 0; o < 512; o++) for (int i = 0; i < SD_CB; i++) t[(size_t)(SD_CB + i) * 512 + o] = w2[(size_t)o * SD_CB + i];
+        s->vq.w = sd_put(&L, t, (size_t)2 * SD_CB * 512);
+    }
+    s->pre = sd_conv(&L, "decoder.pre_conv.conv.weight", "decoder.pre_conv.conv.bias", 1024, 512, 3, 1);
+    s->inp = sd_linear(&L, "decoder.pre_transformer.input_proj.weight", "decoder.pre_transformer.input_proj.bias", 512, 1024);
+    for (int l = 0; l < 8 && !L.bad; l++) {
+        sd_layer_t *y = &s->L[l];
+#define LN(sfx) (snprintf(nm, sizeof nm, "decoder.pre_transformer.layers.%d.%s", l, sfx), nm)
+        y->n1 = sd_vec(&L, LN("input_layernorm.weight"), 512);
+        y->n2 = sd_vec(&L, LN("post_attention_layernorm.weight"), 512);
+        y->ls1 = sd_vec(&L, LN("self_attn_layer_scale.scale"), 512);
+        y->ls2 = sd_vec(&L, LN("mlp_layer_scale.scale"), 512);
+        /* q | k | v as one [512][3072] tap, gate | up as one [512][2048] tap */
+        {
+            y->qkv.K = 512; y->qkv.N = 3072; y->qkv.ntap = 1; y->qkv.phases = 1;
+            float *t = sd_tmp(&L, (size_t)512 * 3072);
+            const char *nmq[3] = {"self_attn.q_proj.weight", "self_attn.k_proj.weight", "self_attn.v_proj.weight"};
+            for (int q = 0; q < 3 && !L.bad; q++) {
+                const float *w = sd_get(&L, LN(nmq[q]), 1024LL * 512);
+                if (L.bad) break;
+                for (int o = 0; o < 1024; o++) for (int i = 0; i < 512; i++) t[(size_t)i * 3072 + q * 1024 + o] = w[(size_t)o * 512 + i];
+            }
+            y->qkv.w = sd_put(&L, t, (size_t)512 * 3072);
+        }
+        y->o = sd_linear(&L, LN("self_attn.o_proj.weight"), NULL, 512, 1024);
+        {
+            y->gu.K = 512; y->gu.N = 2048; y->gu.ntap = 1; y->gu.phases = 1;
+            float *t = sd_tmp(&L, (size_t)512 * 2048);
+            const char *nmg[2] = {"mlp.gate_proj.weight", "mlp.up_proj.weight"};
+            for (int q = 0; q < 2 && !L.bad; q++) {
+                const float *w = sd_get(&L, LN(nmg[q]), 1024LL * 512);
+                if (L.bad) break;
+                for (int o = 0; o < 1024; o++) for (int i = 0; i < 512; i++) t[(size_t)i * 2048 + q * 1024 + o] = w[(size_t)o * 512 + i];
+            }
+            y->gu.w = sd_put(&L, t, (size_t)512 * 2048);
+        }
+        y->dn = sd_linear(&L, LN("mlp.down_proj.weight"), NULL, 512, 1024);
+#undef LN
+    }
+    s->fnorm = sd_vec(&L, "decoder.pre_transformer.norm.weight", 512);
+    s->outp = sd_linear(&L, "decoder.pre_transformer.output_proj.weight", "decoder.pre_transformer.output_proj.bias", 1024, 512);
+    for (int b = 0; b < 2 && !L.bad; b++) {
+#define CN(sfx) (snprintf(nm, sizeof nm, "decoder.upsample.%d.%s", b, sfx), nm)
+#define CB(sfx) (snprintf(nb, sizeof nb, "decoder.upsample.%d.%s", b, sfx), nb)
+        s->cn[b].up = sd_convt(&L, CN("0.conv.weight"), CB("0.conv.bias"), 1024, 1024, 2, 2);
+        s->cn[b].dw = sd_vec(&L, CN("1.dwconv.conv.weight"), 1024 * 7);
+        s->cn[b].db = sd_vec(&L, CN("1.dwconv.conv.bias"), 1024);
+        s->cn[b].lw = sd_vec(&L, CN("1.norm.weight"), 1024);
+        s->cn[b].lb = sd_vec(&L, CN("1.norm.bias"), 1024);
+        s->cn[b].gamma = sd_vec(&L, CN("1.gamma"), 1024);
+        s->cn[b].pw1 = sd_linear(&L, CN("1.pwconv1.weight"), CB("1.pwconv1.bias"), 4096, 1024);
+        s->cn[b].pw2 = sd_linear(&L, CN("1.pwconv2.weight"), CB("1.pwconv2.bias"), 1024, 4096);
+#undef CN
+#undef CB
+    }
+    s->init = sd_conv(&L, "decoder.decoder.0.conv.weight", "decoder.decoder.0.conv.bias", 1536, 1024, 7, 1);
+    {
+        int cin = 1536;
+        for (int b = 0; b < 4 && !L.bad; b++) {
+            const int r = UP_RATE[b], c = UP_CH[b];
+#define BN(sfx) (snprintf(nm, sizeof nm, "decoder.decoder.%d.block.%s", b + 1, sfx), nm)
+#define BB(sfx) (snprintf(nb, sizeof nb, "decoder.decoder.%d.block.%s", b + 1, sfx), nb)
+            s->blk[b].s = sd_snake(&L, BN("0.alpha"), BB("0.beta"), cin);
+            s->blk[b].up = sd_convt(&L, BN("1.conv.weight"), BB("1.conv.bias"), cin, c, 2 * r, r);
+            for (int u = 0; u < 3 && !L.bad; u++) {
+                char sa[64], sb[64];
+                snprintf(sa, sizeof sa, "%d.act1.alpha", u + 2); snprintf(sb, sizeof sb, "%d.act1.beta", u + 2);
+                s->blk[b].r[u].s1 = sd_snake(&L, BN(sa), BB(sb), c);
+                snprintf(sa, sizeof sa, "%d.act2.alpha", u + 2); snprintf(sb, sizeof sb, "%d.act2.beta", u + 2);
+                s->blk[b].r[u].s2 = sd_snake(&L, BN(sa), BB(sb), c);
+                snprintf(sa, sizeof sa, "%d.conv1.conv.weight", u + 2); snprintf(sb, sizeof sb, "%d.conv1.conv.bias", u + 2);
+                s->blk[b].r[u].c1 = sd_conv(&L, BN(sa), BB(sb), c, c, 7, DIL[u]);
+                snprintf(sa, sizeof sa, "%d.conv2.conv.weight", u + 2); snprintf(sb, sizeof sb, "%d.conv2.conv.bias", u + 2);
+                s->blk[b].r[u].c2 = sd_conv(&L, BN(sa), BB(sb), c, c, 1, 1);
+            }
+#undef BN
+#undef BB
+            cin = c;
+        }
+    }
+    s->fs = sd_snake(&L, "decoder.decoder.5.alpha", "decoder.decoder.5.beta", 96);
+    s->fw = sd_vec(&L, "decoder.decoder.6.conv.weight", 96 * 7);
+    s->fb = sd_vec(&L, "decoder.decoder.6.conv.bias", 1);
+    if (L.bad) goto fail;
+    /* RoPE tables of the pre-transformer: angle = pos / theta^(2i/64) (sd.c:455-463) */
+    {
+        float *c = sd_tmp(&L, (size_t)2 * SD_ROPE_POS * 32);
+        if (L.bad) goto fail;
+        for (int p = 0; p < SD_ROPE_POS; p++)
+            for (int i = 0; i < 32; i++) {
+                const float ang = (float)p / powf(10000.0f, (float)(2 * i) / 64.0f);
+                c[p * 32 + i] = cosf(ang);
+                c[SD_ROPE_POS * 32 + p * 32 + i] = sinf(ang);
+            }
+        s->rope_c = sd_put(&L, c, (size_t)SD_ROPE_POS * 32);
+        s->rope_s = sd_put(&L, c + SD_ROPE_POS * 32, (size_t)SD_ROPE_POS * 32);
+    }
+    if (L.bad || hipStreamSynchronize(s->st) != hipSuccess) goto fail;
+    free(L.tmp);
+    return s;
+fail:
+    free(L.tmp);
+    if (!qwen_hip_last_error()[0]) qt_seterr("sd_init failed");
+    qwen_hip_sd_free(s);
+    return NULL;
+}
+
+/* ---- decode --------------------------------------------------------------------------------- */
+static size_t sd_big_floats(int n) {
+    /* the largest [T][C] of the conv stages: block 4 at T = 1920 n, C = 96 (ConvNeXt pw1
+     * [4n][4096] and the others are smaller) */
+    return (size_t)SD_SPF * n * 96 + 64;
+}
+
+static int sd_reserve(sd_t *s, int n) {
+    if (n <= s->cap) return 0;
+    float **ws[] = {&s->E, &s->V, &s->P, &s->H, &s->XN, &s->QKV, &s->A, &s->GU, &s->M, &s->LAT, &s->big[0], &s->big[1],
+                    &s->big[2], &s->daudio};
+    const size_t sz[] = {512, 512, 1024, 512, 512, 3072, 1024, 2048, 1024, 1024, 0, 0, 0, SD_SPF};
+    (void)hipStreamSynchronize(s->st);
+    for (size_t i = 0; i < sizeof ws / sizeof ws[0]; i++) {
+        if (*ws[i]) (void)hipFree(*ws[i]);
+        *ws[i] = NULL;
+        const size_t f = sz[i] ? sz[i] * (size_t)n : sd_big_floats(n);
+        if (hipMalloc((void **)ws[i], f * sizeof(float)) != hipSuccess) { s->cap = 0; qt_seterr("sd_decode: out of device memory for %d frames", n); return -1; }
+    }
+    if (s->dcodes) (void)hipFree(s->dcodes);
+    s->dcodes = NULL;
+    if (hipMalloc((void **)&s->dcodes, (size_t)n * 16 * sizeof(int)) != hipSuccess) { s->cap = 0; qt_seterr("sd_decode: out of device memory"); return -1; }
+    s->cap = n;
+    return 0;
+}
+
+static hipError_t sd_run(const sd_t *s, const sd_conv_t *c, const float *X, int Tx, int T, float *Y, int epi,
+                         const float *cscale, const float *R) {
+    return qt_launch_sd_gemm(X, c->K, Tx, c->w, c->K, c->N, c->ntap, c->off, c->phases, T, Y, c->N,
+                             c->b, cscale, R, epi | (c->b ? SD_BIAS : 0), s->st);
+}
+
+#define SCK(call) do { hipError_t e_ = (call); if (e_ != hipSuccess) { \
+    qt_seterr("sd_decode: %s -> %s", #call, hipGetErrorString(e_)); return -1; } } while (0)
+
+/* VQ + pre-transformer: codes -> s->LAT [n][1024] (sd.c:599-1044) */
+static int sd_enqueue_latent(sd_t *s, const int *d_codes, int n) {
+    const hipStream_t st = s->st;
+    SCK(qt_launch_sd_vq(d_codes, s->cb, s->E, n, SD_CBSIZE, st));
+    SCK(sd_run(s, &s->vq, s->E, n, n, s->V, 0, NULL, NULL));
+    SCK(sd_run(s, &s->pre, s->V, n, n, s->P, 0, NULL, NULL));
+    SCK(sd_run(s, &s->inp, s->P, n, n, s->H, 0, NULL, NULL));
+    for (int l = 0; l < 8; l++) {
+        const sd_layer_t *y = &s->L[l];
+        SCK(qt_launch_sd_rmsnorm(s->H, y->n1, s->XN, n, 512, 1e-5f, st));
+        SCK(sd_run(s, &y->qkv, s->XN, n, n, s->QKV, 0, NULL, NULL));
+        SCK(qt_launch_sd_rope(s->QKV, s->rope_c, s->rope_s, n, st));
+        SCK(qt_launch_sd_attn(s->QKV, s->A, n, 72, 0.125f, st));
+        SCK(sd_run(s, &y->o, s->A, n, n, s->H, SD_CSCALE | SD_RESID, y->ls1, s->H));
+        SCK(qt_launch_sd_rmsnorm(s->H, y->n2, s->XN, n, 512, 1e-5f, st));
+        SCK(sd_run(s, &y->gu, s->XN, n, n, s->GU, 0, NULL, NULL));
+        SCK(qt_launch_sd_swiglu(s->GU, s->M, n, 1024, st));
+        SCK(sd_run(s, &y->dn, s->M, n, n, s->H, SD_CSCALE | SD_RESID, y->ls2, s->H));
+    }
+    SCK(qt_launch_sd_rmsnorm(s->H, s->fnorm, s->XN, n, 512, 1e-5f, st));
+    SCK(sd_run(s, &s->outp, s->XN, n, n, s->LAT, 0, NULL, NULL));
+    return 0;
+}
+
+/* the decode on device buffers, enqueued on the state's stream */
+static int sd_enqueue(sd_t *s, const int *d_codes, int n, float *d_audio) {
+    const hipStream_t st = s->st;
+    if (sd_enqueue_latent(s, d_codes, n)) return -1;
+    /* ConvNeXt upsamplers: sig [T][1024] -> [2T][1024] each */
+    float *sig = s->LAT, *b0 = s->big[0], *b1 = s->big[1], *b2 = s->big[2];
+    int T = n;
+    for (int b = 0; b < 2; b++) {
+        float *up = b == 0 ? b0 : b2, *dl = b == 0 ? b1 : b0, *pw = b == 0 ? b2 : b1;
+        SCK(sd_run(s, &s->cn[b].up, sig, T, T, up, 0, NULL, NULL));
+        T *= 2;
+        SCK(qt_launch_sd_dwln(up, s->cn[b].dw, s->cn[b].db, s->cn[b].lw, s->cn[b].lb, dl, T, 1024, st));
+        SCK(sd_run(s, &s->cn[b].pw1, dl, T, T, pw, SD_GELU, NULL, NULL));
+        SCK(sd_run(s, &s->cn[b].pw2, pw, T, T, up, SD_CSCALE | SD_RESID, s->cn[b].gamma, up));
+        sig = up;
+    }
+    /* sig == b2 here; initial conv 1024 -> 1536 */
+    SCK(sd_run(s, &s->init, sig, T, T, b0, 0, NULL, NULL));
+    float *cur = b0, *f1 = b1, *f2 = b2;
+    int C = 1536;
+    for (int b = 0; b < 4; b++) {
+        const int r = UP_RATE[b], c = UP_CH[b];
+        SCK(qt_launch_sd_snake(cur, cur, s->blk[b].s.a, s->blk[b].s.ib, T, C, st));
+        SCK(sd_run(s, &s->blk[b].up, cur, T, T, f1, 0, NULL, NULL));
+        T *= r; C = c;
+        { float *t_ = cur; cur = f1; f1 = t_; }          /* cur: the upsampled signal */
+        for (int u = 0; u < 3; u++) {
+            SCK(qt_launch_sd_snake(cur, f1, s->blk[b].r[u].s1.a, s->blk[b].r[u].s1.ib, T, C, st));
+            SCK(sd_run(s, &s->blk[b].r[u].c1, f1, T, T, f2, 0, NULL, NULL));
+            SCK(qt_launch_sd_snake(f2, f2, s->blk[b].r[u].s2.a, s->blk[b].r[u].s2.ib, T, C, st));
+            SCK(sd_run(s, &s->blk[b].r[u].c2, f2, T, T, cur, SD_RESID, NULL, cur));
+        }
+    }
+    SCK(qt_launch_sd_snake(cur, cur, s->fs.a, s->fs.ib, T, C, st));
+    SCK(qt_launch_sd_final(cur, s->fw, s->fb, d_audio, T, C, st));
+    return 0;
+}
+
+int qwen_hip_sd_decode_device(void *state, const int *d_codes, int n_frames, float *d_audio) {
+    sd_t *s = (sd_t *)state;
+    if (!s || !d_codes || !d_audio) { qt_seterr("sd_decode_device: null argument"); return -1; }
+    if (n_frames < 1 || n_frames > SD_ROPE_POS) { qt_seterr("sd_decode_device: %d frames (1..%d)", n_frames, SD_ROPE_POS); return -1; }
+    if (sd_reserve(s, n_frames)) return -1;
+    return sd_enqueue(s, d_codes, n_frames, d_audio);
+}
+
+int qwen_hip_sd_decode(void *state, const int *codes, int n_frames, float *audio_out, int max_samples) {
+    sd_t *s = (sd_t *)state;
+    if (!s || !codes || !audio_out) { qt_seterr("sd_decode: null argument"); return -1; }
+    if (n_frames < 1 || n_frames > SD_ROPE_POS) { qt_seterr("sd_decode: %d frames (1..%d)", n_frames, SD_ROPE_POS); return -1; }
+    const long long ns = (long long)n_frames * SD_SPF;
+    if (max_samples < ns) { qt_seterr("sd_decode: %d frames need %lld samples, buffer holds %d", n_frames, ns, max_samples); return -1; }
+    if (sd_reserve(s, n_frames)) return -1;
+    SCK(hipMemcpyAsync(s->dcodes, codes, (size_t)n_frames * 16 * sizeof(int), hipMemcpyHostToDevice, s->st));
+    if (sd_enqueue(s, s->dcodes, n_frames, s->daudio)) return -1;
+    SCK(hipMemcpyAsync(audio_out, s->daudio, (size_t)ns * sizeof(float), hipMemcpyDeviceToHost, s->st));
+    SCK(hipStreamSynchronize(s->st));
+    return (int)ns;
+}
+
+int qwen_hip_sd_latent(void *state, const int *codes, int n_frames, float *latent_out) {
+    sd_t *s = (sd_t *)state;
+    if (!s || !codes || !latent_out) { qt_seterr("sd_latent: null argument"); return -1; }
+    if (n_frames < 1 || n_frames > SD_ROPE_POS) { qt_seterr("sd_latent: %d frames (1..%d)", n_frames, SD_ROPE_POS); return -1; }
+    if (sd_reserve(s, n_frames)) return -1;
+    SCK(hipMemcpyAsync(s->dcodes, codes, (size_t)n_frames * 16 * sizeof(int), hipMemcpyHostToDevice, s->st));
+    if (sd_enqueue_latent(s, s->dcodes, n_frames)) return -1;
+    SCK(hipMemcpyAsync(latent_out, s->LAT, (size_t)n_frames * 1024 * sizeof(float), hipMemcpyDeviceToHost, s->st));
+    SCK(hipStreamSynchronize(s->st));
+    return 0;
+}
+
+void *qwen_hip_sd_stream(void *state) { return state ? (void *)((sd_t *)state)->st : NULL; }

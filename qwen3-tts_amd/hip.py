@@ -37,7 +37,12 @@ EXPORTS = [
     "qwen_hip_talker_prefill", "qwen_hip_talker_prefill_async", "qwen_hip_op_prefill_gemm",
     "qwen_hip_op_prefill_attention", "qwen_hip_talker_step_layers", "qwen_hip_op_matmat_int8_noalloc",
     "qwen_hip_generate", "qwen_hip_talker_load_file",
+    "qwen_hip_sd_init", "qwen_hip_sd_load_file", "qwen_hip_sd_decode", "qwen_hip_sd_decode_device",
+    "qwen_hip_sd_latent", "qwen_hip_sd_stream", "qwen_hip_sd_free",
 ]
+
+SD_GET_FN = C.CFUNCTYPE(C.c_void_p, C.c_void_p, C.c_char_p, C.c_longlong)
+SD_SAMPLES_PER_FRAME = 1920
 
 
 class Mat(C.Structure):
@@ -157,6 +162,13 @@ def lib():
         L.qwen_hip_op_matmat_q4_0.argtypes = [vp, vp, vp, i, i, i]; L.qwen_hip_op_matmat_q4_0.restype = i
         L.qwen_hip_op_matmat_int8_noalloc.argtypes = [vp, vp, vp, vp, i, i, i, vp]
         L.qwen_hip_op_matmat_int8_noalloc.restype = i
+        L.qwen_hip_sd_init.argtypes = [SD_GET_FN, vp]; L.qwen_hip_sd_init.restype = vp
+        L.qwen_hip_sd_load_file.argtypes = [C.c_char_p]; L.qwen_hip_sd_load_file.restype = vp
+        L.qwen_hip_sd_decode.argtypes = [vp, vp, i, vp, i]; L.qwen_hip_sd_decode.restype = i
+        L.qwen_hip_sd_decode_device.argtypes = [vp, vp, i, vp]; L.qwen_hip_sd_decode_device.restype = i
+        L.qwen_hip_sd_latent.argtypes = [vp, vp, i, vp]; L.qwen_hip_sd_latent.restype = i
+        L.qwen_hip_sd_stream.argtypes = [vp]; L.qwen_hip_sd_stream.restype = vp
+        L.qwen_hip_sd_free.argtypes = [vp]
         _lib = L
     return _lib
 
@@ -330,6 +342,54 @@ def generate(talker, cp, codec_head, codec_emb, tts_pad, hidden0, pos, frame0, n
     if n < 0:
         raise RuntimeError(f"generate failed: {last_error()}")
     return codes[:n], (codes[n] if n < n_frames else None), hid, int(sd[0])
+
+
+class SpeechDecoder:
+    """The device speech decoder (qwen_hip_sd_*): codes [n][16] -> audio [1920 n]."""
+
+    def __init__(self, h):
+        if not h:
+            raise RuntimeError(f"speech decoder init failed: {last_error()}")
+        self.h = h
+
+    @classmethod
+    def from_file(cls, path):
+        return cls(lib().qwen_hip_sd_load_file(str(path).encode()))
+
+    @classmethod
+    def from_tensors(cls, tensors):
+        """Through qwen_hip_sd_init with a getter over a {name: f32 array} dict."""
+        keep = {}
+
+        def get(_user, name, n):
+            a = tensors.get(name.decode())
+            if a is None or a.size != n:
+                return None
+            keep["cur"] = np.ascontiguousarray(a, np.float32)
+            return keep["cur"].ctypes.data
+
+        cb = SD_GET_FN(get)
+        return cls(lib().qwen_hip_sd_init(cb, None))
+
+    def decode(self, codes):
+        codes = np.ascontiguousarray(codes, np.int32)
+        n = codes.shape[0]
+        out = np.empty(n * SD_SAMPLES_PER_FRAME, np.float32)
+        ns = lib().qwen_hip_sd_decode(self.h, codes.ctypes.data, n, out.ctypes.data, out.size)
+        if ns < 0:
+            raise RuntimeError(f"sd_decode failed: {last_error()}")
+        return out[:ns]
+
+    def latent(self, codes):
+        codes = np.ascontiguousarray(codes, np.int32)
+        out = np.empty((codes.shape[0], 1024), np.float32)
+        check(lib().qwen_hip_sd_latent(self.h, codes.ctypes.data, codes.shape[0], out.ctypes.data), "sd_latent")
+        return out
+
+    def free(self):
+        if self.h:
+            lib().qwen_hip_sd_free(self.h)
+            self.h = None
 
 
 class TalkerBatch:

@@ -57,6 +57,29 @@ def model_dir(name, seed=0x5EED0001, gain_jitter=0.1):
     return _MODEL_CACHE[key]
 
 
+_SD_CACHE = {}
+
+
+def sd_model(seed=0x5EED0D0C):
+    """Write (once per session) the synthetic speech-decoder file; returns (path, tensors)."""
+    from qwen3_tts_amd import synth_sd
+    if seed not in _SD_CACHE:
+        base = os.environ.get("QWEN_TEST_MODELS", "/tmp/qwen3tts_test_models")
+        t = synth_sd.generate_sd(seed)
+        _SD_CACHE[seed] = (synth_sd.write_sd(os.path.join(base, f"sd_{seed:x}"), seed, tensors=t), t)
+    return _SD_CACHE[seed]
+
+
+def sd_codes(n, seed):
+    """Seeded codes [n][16] in [0, 2048), with one code out of range (-1 or 2048) in every
+    third frame (the reference skips those lookups, sd.c:607-623)."""
+    rng = np.random.default_rng(seed)
+    c = rng.integers(0, 2048, (n, 16)).astype(np.int32)
+    for f in range(0, n, 3):
+        c[f, int(rng.integers(0, 16))] = -1 if f % 2 else 2048
+    return c
+
+
 @pytest.fixture(scope="session")
 def oracle():
     from oracle.oracle import Oracle

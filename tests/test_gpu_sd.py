@@ -1,0 +1,87 @@
+"""The device speech decoder (qwen_hip_sd_*, qt_sd.hip) against the reference's own compiled
+one-shot decode (qwen_speech_decoder_decode, qwen_tts_speech_decoder.c:579-1290) and the
+float64 oracle (oracle/sd_oracle.py, itself pinned to the compiled reference in
+tests/test_cpu_sd.py).  Both sides compute in f32 with different summation orders (the
+reference in naive loop order, the device in MFMA order), so the bar is the north star's
+float tolerance: max-abs 2e-2 and rel-L2 1e-3 on the audio and on the latent."""
+import numpy as np
+import pytest
+
+from conftest import need_ref, rel_l2, sd_codes, sd_model
+
+pytestmark = pytest.mark.gpu
+
+from qwen3_tts_amd import hip  # noqa: E402
+
+_DEC = {}
+
+
+def _dec():
+    if "d" not in _DEC:
+        path, _ = sd_model()
+        _DEC["d"] = hip.SpeechDecoder.from_file(path)
+    return _DEC["d"]
+
+
+@need_ref
+@pytest.mark.parametrize("n", [1, 3, 6])
+def test_sd_decode_matches_reference(n):
+    """Codes (with out-of-range entries) -> 1920 n samples, against the compiled reference."""
+    from oracle.oracle import RefSpeechDecoder
+    print(f"[case] sd decode n={n}", flush=True)
+    path, _ = sd_model()
+    codes = sd_codes(n, 100 + n)
+    want = RefSpeechDecoder(path, threads=8).decode(codes)
+    got = _dec().decode(codes)
+    assert got.shape == want.shape == (1920 * n,)
+    err, r = float(np.abs(got - want).max()), rel_l2(got, want)
+    print(f"[result] sd decode n={n}: max-abs {err:.2e}, rel-L2 {r:.2e}, audio rms {float(np.sqrt((want ** 2).mean())):.3f}")
+    assert err <= 2e-2 and r <= 1e-3, (err, r)
+
+
+def test_sd_latent_long_matches_oracle():
+    """100 frames, so the pre-transformer's 72-frame attention window is exercised: the
+    device latent (VQ + pre-conv + 8 layers + final norm + output projection) against the
+    oracle's."""
+    from oracle import sd_oracle
+    _, t = sd_model()
+    codes = sd_codes(100, 7)
+    got = _dec().latent(codes)
+    v = sd_oracle.vq(t, codes)
+    x = sd_oracle.conv1d(v.T, np.asarray(t["decoder.pre_conv.conv.weight"], np.float64),
+                         np.asarray(t["decoder.pre_conv.conv.bias"], np.float64))
+    h = x.T @ np.asarray(t["decoder.pre_transformer.input_proj.weight"], np.float64).T + \
+        np.asarray(t["decoder.pre_transformer.input_proj.bias"], np.float64)
+    want = sd_oracle.pre_transformer(t, h)
+    err, r = float(np.abs(got - want).max()), rel_l2(got, want)
+    print(f"[result] sd latent n=100: max-abs {err:.2e}, rel-L2 {r:.2e}")
+    assert err <= 2e-2 and r <= 1e-3, (err, r)
+
+
+def test_sd_getter_init_matches_load_file():
+    """qwen_hip_sd_init through a tensor getter builds the same state as the file loader:
+    identical audio, bit for bit."""
+    _, t = sd_model()
+    codes = sd_codes(2, 5)
+    a = _dec().decode(codes)
+    d2 = hip.SpeechDecoder.from_tensors(t)
+    b = d2.decode(codes)
+    d2.free()
+    assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+
+
+def test_sd_rejects_bad_arguments():
+    _, t = sd_model()
+    L = hip.lib()
+    d = _dec()
+    codes = sd_codes(2, 1)
+    out = np.empty(1920 * 2, np.float32)
+    assert L.qwen_hip_sd_decode(d.h, codes.ctypes.data, 0, out.ctypes.data, out.size) == -1
+    assert L.qwen_hip_sd_decode(d.h, codes.ctypes.data, 2, out.ctypes.data, out.size - 1) == -1
+    assert "samples" in hip.last_error()
+    missing = dict(t)
+    del missing["decoder.pre_transformer.layers.3.mlp.up_proj.weight"]
+    with pytest.raises(RuntimeError, match="layers.3.mlp.up_proj"):
+        hip.SpeechDecoder.from_tensors(missing)
+    assert not L.qwen_hip_sd_load_file(b"/nonexistent/speech_decoder.safetensors")
+    assert np.array_equal(d.decode(codes), d.decode(codes))        # the state stays usable
