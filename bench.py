@@ -117,6 +117,11 @@ FRAME_WORKLOADS = {
     "frame-0.6B-bf16-sampled": ("0.6B", "bf16", 256, 64),
     "frame-1.7B-int8-sampled": ("1.7B", "int8", 2048, 64),
 }
+# the speech decoder (codes -> 24 kHz audio, one-shot): (frames per decode, default timed decodes)
+SD_WORKLOADS = {
+    "sd-decode-125frames": (125, 10),
+}
+F32_MFMA_PEAK_TFS = 157.3
 # batched workloads: (shape, precision, streams, KV length range, default timed steps)
 BATCH_WORKLOADS = {
     "talker-1.7B-int8-b32-ragged": ("1.7B", "int8", 32, (128, 4096), 16),
@@ -149,7 +154,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=None)
     ap.add_argument("--workload", default="talker-1.7B-int8-b1-L2048", choices=sorted(WORKLOADS) + sorted(BATCH_WORKLOADS) + sorted(CP_WORKLOADS)
                     + sorted(PREFILL_WORKLOADS) + sorted(GROW_WORKLOADS) + sorted(SAMPLED_WORKLOADS)
-                    + sorted(FRAME_WORKLOADS))
+                    + sorted(FRAME_WORKLOADS) + sorted(SD_WORKLOADS))
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--kernel-launches", type=int, default=200)
@@ -175,6 +180,8 @@ def main():
         return bench_sampled(args)
     if args.workload in FRAME_WORKLOADS:
         return bench_frames(args)
+    if args.workload in SD_WORKLOADS:
+        return bench_sd(args)
     from qwen3_tts_amd import hip, synth
     shape_name, prec, Lpre, dsteps = WORKLOADS[args.workload]
     K = args.steps or dsteps
@@ -773,6 +780,103 @@ def cpu_baseline_cp(s, prec, tens, th, seconds):
     return {"value": round(ms, 3), "unit": "ms/frame", "cores": threads, "kind": "reference",
             "sample": f"{n} reference qwen_cp_predict calls ({prec}, {variant.strip('_') or 'avx2'} build, "
                       f"-O3 -ffast-math), same weights"}
+
+
+def sd_flops(n):
+    """Algorithmic multiply-add work (2 flops each) of one decode of n frames: every
+    projection, conv and transposed conv as output rows x output channels x (taps x input
+    channels), plus the windowed attention; elementwise work is not counted."""
+    f = 2 * n * 512 * 512 + 2 * n * 1024 * 3 * 512 + 2 * n * 512 * 1024            # vq, pre-conv, input proj
+    att = sum(2 * 2 * 16 * 64 * min(72, t + 1) for t in range(n))
+    f += 8 * (2 * n * 3072 * 512 + 2 * n * 512 * 1024 + 2 * n * 2048 * 512 + 2 * n * 512 * 1024) + 8 * att
+    f += 2 * n * 1024 * 512                                                         # output proj
+    T = n
+    for _ in range(2):                                                              # ConvNeXt upsamplers
+        T *= 2
+        f += 2 * T * 1024 * 1024 + 2 * (2 * T * 4096 * 1024)
+    f += 2 * T * 1536 * 7 * 1024                                                    # initial conv
+    cin = 1536
+    for r, c in zip((8, 5, 4, 3), (768, 384, 192, 96)):
+        Tin, T = T, T * r
+        f += 2 * T * c * 2 * cin + 3 * (2 * T * c * 7 * c + 2 * T * c * c)
+        cin = c
+    return f + 2 * T * 96 * 7
+
+
+def bench_sd(args):
+    """The speech decoder: one decode of n frames (codes -> 1920 n samples of 24 kHz audio,
+    the reference's one-shot qwen_speech_decoder_decode) on device-resident codes
+    (qwen_hip_sd_decode_device), synthetic F32 weights of the real architecture.
+    value = ms per decode; roofline = algorithmic MFMA flops over the f32 matrix peak."""
+    from qwen3_tts_amd import hip, synth_sd
+    n, dk = SD_WORKLOADS[args.workload]
+    K = args.steps or dk
+    W = 2 if args.warmup is None else args.warmup
+    t0 = time.time()
+    tens = synth_sd.generate_sd()
+    path = synth_sd.write_sd(os.path.join(os.environ.get("TMPDIR", "/tmp"), "qwen3tts_bench_sd"), tensors=tens)
+    dec = hip.SpeechDecoder.from_file(path)
+    log(f"[bench] sd: weights + device init {time.time() - t0:.1f}s")
+    rng = np.random.default_rng(0x5EED0D0E)
+    codes = rng.integers(0, 2048, (n, 16)).astype(np.int32)
+    ev = HipEvents()
+    rt = ev.rt
+    rt.hipMalloc.argtypes = [C.POINTER(C.c_void_p), C.c_size_t]
+    rt.hipMemcpy.argtypes = [C.c_void_p, C.c_void_p, C.c_size_t, C.c_int]
+    dc, da = C.c_void_p(), C.c_void_p()
+    assert rt.hipMalloc(C.byref(dc), codes.nbytes) == 0 and rt.hipMalloc(C.byref(da), n * 1920 * 4) == 0
+    assert rt.hipMemcpy(dc, codes.ctypes.data, codes.nbytes, 1) == 0
+    L = hip.lib()
+    stream = L.qwen_hip_sd_stream(dec.h)
+    for _ in range(W):
+        hip.check(L.qwen_hip_sd_decode_device(dec.h, dc, n, da), "sd warmup")
+    ev.device_sync()
+    a, b = ev.event(), ev.event()
+    ev.record(a, stream)
+    for _ in range(K):
+        hip.check(L.qwen_hip_sd_decode_device(dec.h, dc, n, da), "sd timed")
+    ev.record(b, stream)
+    ms = ev.elapsed_ms(a, b) / K
+    ev.device_sync()
+    fl = sd_flops(n)
+    tfs = fl / (ms * 1e-3) / 1e12
+    audio_s = n * 1920 / 24000.0
+    log(f"[bench] sd: {n} frames ({audio_s:.1f} s of audio) in {ms:.3f} ms, {tfs:.1f} TFLOP/s, "
+        f"{audio_s / (ms * 1e-3):.0f}x real time")
+    cpu = None
+    if not args.no_cpu_baseline:
+        try:
+            sys.path.insert(0, ROOT)
+            from oracle.oracle import RefSpeechDecoder
+            threads = int(os.environ.get("OMP_NUM_THREADS", "16"))
+            ref = RefSpeechDecoder(path, threads=threads)
+            ns = 2
+            secs = ref.time_decode(codes[:ns])
+            model, ncpu = host_info()
+            cpu = {"value": round(secs * 1e3 / ns * n, 1), "unit": "ms/decode", "cores": threads, "kind": "reference",
+                   "sample": f"one reference qwen_speech_decoder_decode of the first {ns} frames of the same codes "
+                             f"({secs:.2f} s; oracle/_ref build: reference flags, no BLAS, so its convs run as the "
+                             f"naive single-thread loops and only the snake uses the {threads}-thread pool), "
+                             f"scaled linearly to {n} frames",
+                   "host_cpu": model, "host_logical_cpus": ncpu}
+            log(f"[bench] sd cpu baseline: {secs:.2f} s for {ns} frames")
+        except Exception as ex:  # noqa: BLE001
+            cpu = {"value": None, "unit": "ms/decode", "error": str(ex)[:200]}
+    dec.free()
+    out = {
+        "metric": "speech decoder ms/decode (codes -> 24 kHz audio) + achieved MFMA TFLOP/s",
+        "value": round(ms, 3), "unit": "ms/decode", "n_gpus": 1, "steps": K, "warmup": W, "ms_per_step": round(ms, 3),
+        "higher_is_better": False, "scaling": "weak", "vs_baseline": None, "dtype": "f32",
+        "data": "synthetic (seeded random-init F32 decoder weights of the 12 Hz codec architecture; random codes)",
+        "config": {"workload": args.workload, "frames": n, "samples": n * 1920, "audio_seconds": audio_s},
+        "realtime_factor": round(audio_s / (ms * 1e-3), 1),
+        "roofline": {"bound": "mfma", "achieved": round(tfs, 2), "peak": F32_MFMA_PEAK_TFS, "unit": "TFLOP/s",
+                     "frac": round(tfs / F32_MFMA_PEAK_TFS, 4), "traffic": None,
+                     "kernel": "one decode (all kernels; k_sd_gemm carries the flops)", "flops_per_launch": int(fl),
+                     "avg_us": round(ms * 1e3, 1), "steps_per_launch": 1},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(out), flush=True)
 
 
 def host_info():

@@ -13,7 +13,9 @@
 // kernel K and dilation d has taps off_p = (p - K + 1) d; a transposed conv of stride s
 // and kernel 2s is s phases z (output rows t*s + z), each with taps at offsets 0 and -1
 // (kernel columns z and z + s); a linear layer is one tap.  The epilogue adds a bias,
-// applies GELU, scales per column (layer scale, ConvNeXt gamma) and adds a residual.
+// applies GELU, scales per column (layer scale, ConvNeXt gamma), adds a residual and
+// applies the snake activation that the next layer needs on its input (so no separate
+// pass over the activation: the upsampler's snakes all live in the producing GEMM).
 // Products accumulate in f32 in MFMA order (the reference sums in loop order): the
 // results agree to f32 rounding, not bitwise.
 #include "qt_device.h"
@@ -21,14 +23,11 @@
 typedef float qt_sd_f4 __attribute__((ext_vector_type(4)));
 
 #define SD_WG 256
-#define SD_TM 64                 // output rows (time) per workgroup
-#define SD_TN 64                 // output columns (channels) per workgroup
 #define SD_KC 16                 // K chunk staged per step
 #define SD_AS (SD_KC + 1)        // A tile row stride (floats): 17 spreads 16 rows over banks
-#define SD_BS 80                 // B tile row stride: rows k, k+1 land on opposite bank halves
 #define SD_MAXTAP 8
 
-enum { SD_EPI_BIAS = 1, SD_EPI_GELU = 2, SD_EPI_CSCALE = 4, SD_EPI_RESID = 8 };
+enum { SD_EPI_BIAS = 1, SD_EPI_GELU = 2, SD_EPI_CSCALE = 4, SD_EPI_RESID = 8, SD_EPI_SNAKE = 16, SD_EPI_SNAKE2 = 32 };
 
 struct SdGemmArgs {
     const float *X; int ldx, Tx;          // input rows [Tx][ldx]
@@ -39,6 +38,8 @@ struct SdGemmArgs {
     float *Y; int ldy, os;                // output row t*os + phase
     const float *bias, *cscale;
     const float *R;                       // residual, same indexing as Y (may alias Y)
+    const float *sa, *sib;                // SNAKE: Y = snake(v) with per-column a, 1/b
+    float *Y2;                            // SNAKE2: Y = v and Y2 = snake(v) (same indexing)
     int epi;
 };
 
@@ -46,71 +47,99 @@ __device__ __forceinline__ float sd_gelu(float x) {
     return 0.5f * x * (1.0f + erff(x * 0.7071067811865476f));
 }
 
-// 64 x 64 output tile, four waves of 32 x 32 (2 x 2 MFMA tiles of 16 x 16); K in chunks of
-// 16 staged through LDS, the next chunk's global loads in registers while the MFMAs run.
+// snake (k.c:4472-4600): x + (1/b) sin(a x)^2 with a = e^alpha, 1/b = e^-beta per channel
+__device__ __forceinline__ float sd_snake(float x, float a, float ib) {
+    const float s = sinf(a * x);
+    return fmaf(ib, s * s, x);
+}
+
+// TM x TN output tile (64 x 64 or 128 x 128), four waves of (TM/2) x (TN/2), each a grid
+// of 16 x 16 MFMA tiles; K in chunks of 16 staged through LDS, the next chunk's global
+// loads held in registers while the MFMAs run.  The 128 x 128 tile reads each A and B
+// value from LDS once per four MFMAs (twice as many as the 64 x 64 tile's two).
 // v_mfma_f32_16x16x4_f32: lane l supplies A[l % 16][l / 16] and B[l / 16][l % 16] and
 // receives D[4 (l / 16) + r][l % 16], r < 4.
+template <int TM, int TN>
 __global__ __launch_bounds__(SD_WG) void k_sd_gemm(SdGemmArgs a) {
-    __shared__ float As[2][SD_TM * SD_AS];
-    __shared__ float Bs[2][SD_KC * SD_BS];
+    constexpr int AQ = TM / 64, BQ = TN / 64;          // float4 loads per thread per chunk
+    constexpr int BS = TN + 16;                        // B row stride: rows k, k+1 on opposite bank halves
+    constexpr int MI = TM / 32, NJ = TN / 32;          // MFMA tiles per wave
+    __shared__ float As[2][TM * SD_AS];
+    __shared__ float Bs[2][SD_KC * BS];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int t0 = blockIdx.x * SD_TM, n0 = blockIdx.y * SD_TN, z = blockIdx.z;
+    const int t0 = blockIdx.x * TM, n0 = blockIdx.y * TN, z = blockIdx.z;
     const float *W = a.W + (size_t)z * a.ntap * a.K * a.N;
     const int kpt = a.K / SD_KC, nch = a.ntap * kpt;
-    // staging roles: A: row tid/4, 4 columns at (tid%4)*4; B: row tid/16, 4 columns at (tid%16)*4
-    const int ar = tid >> 2, ac = (tid & 3) * 4, br = tid >> 4, bc = (tid & 15) * 4;
-    const bool a_row_ok = t0 + ar < a.T, b_col_ok = n0 + bc < a.N;
-    auto fetch = [&](int c, float4 &av, float4 &bv) {
+    float4 av[AQ], bv[BQ];
+    auto fetch = [&](int c) {
         const int p = c / kpt, k0 = (c - p * kpt) * SD_KC;
-        const int xr = t0 + ar + a.off[p];
-        av = (a_row_ok && xr >= 0 && xr < a.Tx) ? *reinterpret_cast<const float4 *>(a.X + (size_t)xr * a.ldx + k0 + ac)
-                                                : make_float4(0.f, 0.f, 0.f, 0.f);
-        bv = b_col_ok ? *reinterpret_cast<const float4 *>(W + ((size_t)p * a.K + k0 + br) * a.N + n0 + bc)
-                      : make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+        for (int q = 0; q < AQ; q++) {
+            const int f = tid + q * SD_WG, ar = f >> 2, ac = (f & 3) * 4;
+            const int xr = t0 + ar + a.off[p];
+            av[q] = (t0 + ar < a.T && xr >= 0 && xr < a.Tx)
+                        ? *reinterpret_cast<const float4 *>(a.X + (size_t)xr * a.ldx + k0 + ac)
+                        : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+#pragma unroll
+        for (int q = 0; q < BQ; q++) {
+            const int f = tid + q * SD_WG, br = f / (TN / 4), bc = (f % (TN / 4)) * 4;
+            bv[q] = n0 + bc < a.N ? *reinterpret_cast<const float4 *>(W + ((size_t)p * a.K + k0 + br) * a.N + n0 + bc)
+                                  : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
     };
-    auto stage = [&](int buf, const float4 &av, const float4 &bv) {
-        float *as = As[buf] + ar * SD_AS + ac;
-        as[0] = av.x; as[1] = av.y; as[2] = av.z; as[3] = av.w;
-        *reinterpret_cast<float4 *>(Bs[buf] + br * SD_BS + bc) = bv;
+    auto stage = [&](int buf) {
+#pragma unroll
+        for (int q = 0; q < AQ; q++) {
+            const int f = tid + q * SD_WG, ar = f >> 2, ac = (f & 3) * 4;
+            float *as = As[buf] + ar * SD_AS + ac;
+            as[0] = av[q].x; as[1] = av[q].y; as[2] = av[q].z; as[3] = av[q].w;
+        }
+#pragma unroll
+        for (int q = 0; q < BQ; q++) {
+            const int f = tid + q * SD_WG, br = f / (TN / 4), bc = (f % (TN / 4)) * 4;
+            *reinterpret_cast<float4 *>(Bs[buf] + br * BS + bc) = bv[q];
+        }
     };
-    const int wm = (wave >> 1) * 32, wn = (wave & 1) * 32;
+    const int wm = (wave >> 1) * (TM / 2), wn = (wave & 1) * (TN / 2);
     const int li = lane & 15, lk = lane >> 4;
-    qt_sd_f4 acc[2][2];
+    qt_sd_f4 acc[MI][NJ];
 #pragma unroll
-    for (int i = 0; i < 2; i++)
+    for (int i = 0; i < MI; i++)
 #pragma unroll
-        for (int j = 0; j < 2; j++) acc[i][j] = qt_sd_f4{0.f, 0.f, 0.f, 0.f};
-    float4 av, bv;
-    fetch(0, av, bv);
-    stage(0, av, bv);
+        for (int j = 0; j < NJ; j++) acc[i][j] = qt_sd_f4{0.f, 0.f, 0.f, 0.f};
+    fetch(0);
+    stage(0);
     __syncthreads();
     for (int c = 0; c < nch; c++) {
         const int buf = c & 1;
-        if (c + 1 < nch) fetch(c + 1, av, bv);
+        if (c + 1 < nch) fetch(c + 1);
         const float *as = As[buf], *bs = Bs[buf];
 #pragma unroll
         for (int kk = 0; kk < SD_KC; kk += 4) {
-            float fa[2], fb[2];
+            float fa[MI], fb[NJ];
 #pragma unroll
-            for (int i = 0; i < 2; i++) fa[i] = as[(wm + 16 * i + li) * SD_AS + kk + lk];
+            for (int i = 0; i < MI; i++) fa[i] = as[(wm + 16 * i + li) * SD_AS + kk + lk];
 #pragma unroll
-            for (int j = 0; j < 2; j++) fb[j] = bs[(kk + lk) * SD_BS + wn + 16 * j + li];
+            for (int j = 0; j < NJ; j++) fb[j] = bs[(kk + lk) * BS + wn + 16 * j + li];
 #pragma unroll
-            for (int i = 0; i < 2; i++)
+            for (int i = 0; i < MI; i++)
 #pragma unroll
-                for (int j = 0; j < 2; j++) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(fa[i], fb[j], acc[i][j], 0, 0, 0);
+                for (int j = 0; j < NJ; j++) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(fa[i], fb[j], acc[i][j], 0, 0, 0);
         }
-        if (c + 1 < nch) stage(buf ^ 1, av, bv);
+        if (c + 1 < nch) stage(buf ^ 1);
         __syncthreads();
     }
 #pragma unroll
-    for (int i = 0; i < 2; i++)
+    for (int i = 0; i < MI; i++)
 #pragma unroll
-        for (int j = 0; j < 2; j++) {
+        for (int j = 0; j < NJ; j++) {
             const int n = n0 + wn + 16 * j + li;
             if (n >= a.N) continue;
             const float bn = (a.epi & SD_EPI_BIAS) ? a.bias[n] : 0.f;
             const float sn = (a.epi & SD_EPI_CSCALE) ? a.cscale[n] : 1.f;
+            const float pa = (a.epi & (SD_EPI_SNAKE | SD_EPI_SNAKE2)) ? a.sa[n] : 0.f;
+            const float pb = (a.epi & (SD_EPI_SNAKE | SD_EPI_SNAKE2)) ? a.sib[n] : 0.f;
 #pragma unroll
             for (int r = 0; r < 4; r++) {
                 const int t = t0 + wm + 16 * i + 4 * lk + r;
@@ -121,7 +150,12 @@ __global__ __launch_bounds__(SD_WG) void k_sd_gemm(SdGemmArgs a) {
                 if (a.epi & SD_EPI_GELU) v = sd_gelu(v);
                 if (a.epi & SD_EPI_CSCALE) v *= sn;
                 if (a.epi & SD_EPI_RESID) v = a.R[o] + v;
-                a.Y[o] = v;
+                if (a.epi & SD_EPI_SNAKE2) {
+                    a.Y[o] = v;
+                    a.Y2[o] = sd_snake(v, pa, pb);
+                } else {
+                    a.Y[o] = (a.epi & SD_EPI_SNAKE) ? sd_snake(v, pa, pb) : v;
+                }
             }
         }
 }
@@ -275,46 +309,62 @@ __global__ __launch_bounds__(SD_WG) void k_sd_dwln(const float *x, const float *
     }
 }
 
-// snake (k.c:4472-4600): y = x + ib[c] * sin(a[c] x)^2, per channel c of [T][C]
-__global__ void k_sd_snake(const float *x, float *y, const float *a, const float *ib, size_t n, int C) {
-    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= n) return;
-    const int c = (int)(i % C);
-    const float xv = x[i];
-    const float s = sinf(a[c] * xv);
-    y[i] = fmaf(ib[c], s * s, xv);
-}
-
 // final conv to one channel (k = 7, pad 6) + clamp to [-1, 1] (sd.c:1259-1279); x [T][C]
-// already through the final snake
-__global__ void k_sd_final(const float *x, const float *w, const float *b, float *audio, int T, int C) {
-    const int t = blockIdx.x * blockDim.x + threadIdx.x;
-    if (t >= T) return;
-    float s = b[0];
-    for (int j = 0; j < 7; j++) {
-        const int ti = t - 6 + j;
-        if (ti < 0) continue;
-        const float *xr = x + (size_t)ti * C;
-        for (int c = 0; c < C; c++) s = fmaf(w[c * 7 + j], xr[c], s);
+// already through the final snake.  A workgroup takes 64 samples: the 70 input rows they
+// need go to LDS (row stride C + 1, so the 64 lanes of a read, one row each, hit distinct
+// banks); wave w sums channels [w C/4, (w+1) C/4) for its lane's sample, and the four
+// partial sums are added in wave order.
+#define SD_FIN_T 64
+__global__ __launch_bounds__(SD_WG) void k_sd_final(const float *x, const float *w, const float *b, float *audio, int T,
+                                                    int C) {
+    extern __shared__ float xs[];                        // [70][C + 1]
+    __shared__ float part[QT_WAVES][SD_FIN_T];
+    const int t0 = blockIdx.x * SD_FIN_T, ld = C + 1;
+    for (int i = threadIdx.x; i < (SD_FIN_T + 6) * C; i += SD_WG) {
+        const int r = i / C, c = i % C, ti = t0 - 6 + r;
+        xs[r * ld + c] = (ti >= 0 && ti < T) ? x[(size_t)ti * C + c] : 0.f;
     }
-    audio[t] = fminf(fmaxf(s, -1.0f), 1.0f);
+    __syncthreads();
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int cw = C / QT_WAVES, c0 = wave * cw;
+    float s = 0.f;
+    for (int c = c0; c < c0 + cw; c++)
+#pragma unroll
+        for (int j = 0; j < 7; j++) s = fmaf(w[c * 7 + j], xs[(lane + j) * ld + c], s);
+    part[wave][lane] = s;
+    __syncthreads();
+    if (wave == 0 && t0 + lane < T) {
+        const float v = b[0] + part[0][lane] + part[1][lane] + part[2][lane] + part[3][lane];
+        audio[t0 + lane] = fminf(fmaxf(v, -1.0f), 1.0f);
+    }
 }
 
 // ---- launchers ----------------------------------------------------------------------------
 
+// tile: 0 = by size (128 x 128 where that still gives two workgroups per CU), 64 or 128 = forced
 extern "C" hipError_t qt_launch_sd_gemm(const float *X, int ldx, int Tx, const float *W, int K, int N, int ntap,
                                         const int *off, int phases, int T, float *Y, int ldy, const float *bias,
-                                        const float *cscale, const float *R, int epi, hipStream_t st) {
+                                        const float *cscale, const float *R, const float *sa, const float *sib,
+                                        float *Y2, int epi, int tile, hipStream_t st) {
     if (!X || !W || !Y || K <= 0 || K % SD_KC || N <= 0 || N % 4 || ntap < 1 || ntap > SD_MAXTAP || phases < 1 ||
         T <= 0 || Tx <= 0 || ldx % 4 || ldx < K || ldy < N)
         return hipErrorInvalidValue;
     if (((epi & 1) && !bias) || ((epi & 4) && !cscale) || ((epi & 8) && !R)) return hipErrorInvalidValue;
+    if ((epi & (SD_EPI_SNAKE | SD_EPI_SNAKE2)) && (!sa || !sib)) return hipErrorInvalidValue;
+    if ((epi & SD_EPI_SNAKE2) && (!Y2 || (epi & SD_EPI_SNAKE))) return hipErrorInvalidValue;
     SdGemmArgs a;
     a.X = X; a.ldx = ldx; a.Tx = Tx; a.W = W; a.K = K; a.N = N; a.ntap = ntap;
     for (int i = 0; i < SD_MAXTAP; i++) a.off[i] = i < ntap ? off[i] : 0;
     a.T = T; a.Y = Y; a.ldy = ldy; a.os = phases; a.bias = bias; a.cscale = cscale; a.R = R; a.epi = epi;
-    dim3 grid((T + SD_TM - 1) / SD_TM, (N + SD_TN - 1) / SD_TN, phases);
-    hipLaunchKernelGGL(k_sd_gemm, grid, dim3(SD_WG), 0, st, a);
+    a.sa = sa; a.sib = sib; a.Y2 = Y2;
+    const long long big = (long long)((T + 127) / 128) * ((N + 127) / 128) * phases;
+    if (tile == 128 || (tile == 0 && N >= 128 && big >= 512)) {
+        dim3 grid((T + 127) / 128, (N + 127) / 128, phases);
+        hipLaunchKernelGGL((k_sd_gemm<128, 128>), grid, dim3(SD_WG), 0, st, a);
+    } else {
+        dim3 grid((T + 63) / 64, (N + 63) / 64, phases);
+        hipLaunchKernelGGL((k_sd_gemm<64, 64>), grid, dim3(SD_WG), 0, st, a);
+    }
     return hipGetLastError();
 }
 
@@ -359,14 +409,10 @@ extern "C" hipError_t qt_launch_sd_dwln(const float *x, const float *dw, const f
     hipLaunchKernelGGL(k_sd_dwln, dim3(T), dim3(SD_WG), 0, st, x, dw, db, lw, lb, out, T, C);
     return hipGetLastError();
 }
-extern "C" hipError_t qt_launch_sd_snake(const float *x, float *y, const float *a, const float *ib, int T, int C,
-                                         hipStream_t st) {
-    const size_t n = (size_t)T * C;
-    hipLaunchKernelGGL(k_sd_snake, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, x, y, a, ib, n, C);
-    return hipGetLastError();
-}
 extern "C" hipError_t qt_launch_sd_final(const float *x, const float *w, const float *b, float *audio, int T, int C,
                                          hipStream_t st) {
-    hipLaunchKernelGGL(k_sd_final, dim3((T + 255) / 256), dim3(256), 0, st, x, w, b, audio, T, C);
+    if (C % QT_WAVES || C > 256) return hipErrorInvalidValue;
+    const size_t lds = (size_t)(SD_FIN_T + 6) * (C + 1) * sizeof(float);
+    hipLaunchKernelGGL(k_sd_final, dim3((T + SD_FIN_T - 1) / SD_FIN_T), dim3(SD_WG), lds, st, x, w, b, audio, T, C);
     return hipGetLastError();
 }

@@ -25,7 +25,7 @@
 #define SD_ROPE_POS 8000
 #define SD_SPF 1920               /* samples per frame */
 
-enum { SD_BIAS = 1, SD_GELU = 2, SD_CSCALE = 4, SD_RESID = 8 };
+enum { SD_BIAS = 1, SD_GELU = 2, SD_CSCALE = 4, SD_RESID = 8, SD_SNAKE = 16, SD_SNAKE2 = 32 };
 
 typedef struct {
     float *w, *b;
@@ -172,7 +172,7 @@ static sd_conv_t sd_conv(sd_ld_t *L, const char *wn, const char *bn, int out, in
 }
 
 /* causal transposed conv [in][out][k], stride s (k <= 2s) -> s phases of taps at offsets
- * 0 (column z) and -1 (column z + s, when it exists) */
+ * 0 (column z) and -1 (column z + s; zero where z + s >= k) */
 static sd_conv_t sd_convt(sd_ld_t *L, const char *wn, const char *bn, int in, int out, int k, int s) {
     sd_conv_t c; memset(&c, 0, sizeof c);
     c.K = in; c.N = out; c.phases = s; c.ntap = k > s ? 2 : 1;
@@ -186,7 +186,7 @@ static sd_conv_t sd_convt(sd_ld_t *L, const char *wn, const char *bn, int in, in
             const int col = z + p * s;
             float *dst = t + ((size_t)z * c.ntap + p) * per;
             for (int i = 0; i < in; i++)
-                for (int o = 0; o < out; o++) dst[(size_t)i * out + o] = w[((size_t)i * out + o) * k + col];
+                for (int o = 0; o < out; o++) dst[(size_t)i * out + o] = col < k ? w[((size_t)i * out + o) * k + col] : 0.f;
         }
     c.w = sd_put(L, t, (size_t)s * c.ntap * per);
     if (bn) c.b = sd_vec(L, bn, out);
@@ -359,7 +359,14 @@ static int sd_reserve(sd_t *s, int n) {
 static hipError_t sd_run(const sd_t *s, const sd_conv_t *c, const float *X, int Tx, int T, float *Y, int epi,
                          const float *cscale, const float *R) {
     return qt_launch_sd_gemm(X, c->K, Tx, c->w, c->K, c->N, c->ntap, c->off, c->phases, T, Y, c->N,
-                             c->b, cscale, R, epi | (c->b ? SD_BIAS : 0), s->st);
+                             c->b, cscale, R, NULL, NULL, NULL, epi | (c->b ? SD_BIAS : 0), 0, s->st);
+}
+
+/* the same with a snake on the output: in place (Y2 == NULL) or into Y2 beside Y */
+static hipError_t sd_run_snake(const sd_t *s, const sd_conv_t *c, const float *X, int Tx, int T, float *Y, int epi,
+                               const float *R, const sd_snake_t *sn, float *Y2) {
+    return qt_launch_sd_gemm(X, c->K, Tx, c->w, c->K, c->N, c->ntap, c->off, c->phases, T, Y, c->N, c->b, NULL, R,
+                             sn->a, sn->ib, Y2, epi | (c->b ? SD_BIAS : 0) | (Y2 ? SD_SNAKE2 : SD_SNAKE), 0, s->st);
 }
 
 #define SCK(call) do { hipError_t e_ = (call); if (e_ != hipSuccess) { \
@@ -405,25 +412,28 @@ static int sd_enqueue(sd_t *s, const int *d_codes, int n, float *d_audio) {
         SCK(sd_run(s, &s->cn[b].pw2, pw, T, T, up, SD_CSCALE | SD_RESID, s->cn[b].gamma, up));
         sig = up;
     }
-    /* sig == b2 here; initial conv 1024 -> 1536 */
-    SCK(sd_run(s, &s->init, sig, T, T, b0, 0, NULL, NULL));
+    /* sig == b2 here; initial conv 1024 -> 1536, its output through block 1's input snake.
+     * Every snake of the upsampler is applied by the GEMM that produces its input:
+     * transposed conv -> signal + snake1(signal) of unit 1; conv1 -> snake2 in place;
+     * conv2 (+ residual) -> signal + snake1 of the next unit, or, after unit 3, the signal
+     * through the next block's input snake (or the final snake) in place. */
+    SCK(sd_run_snake(s, &s->init, sig, T, T, b0, 0, NULL, &s->blk[0].s, NULL));
     float *cur = b0, *f1 = b1, *f2 = b2;
-    int C = 1536;
     for (int b = 0; b < 4; b++) {
-        const int r = UP_RATE[b], c = UP_CH[b];
-        SCK(qt_launch_sd_snake(cur, cur, s->blk[b].s.a, s->blk[b].s.ib, T, C, st));
-        SCK(sd_run(s, &s->blk[b].up, cur, T, T, f1, 0, NULL, NULL));
-        T *= r; C = c;
-        { float *t_ = cur; cur = f1; f1 = t_; }          /* cur: the upsampled signal */
+        const int r = UP_RATE[b];
+        SCK(sd_run_snake(s, &s->blk[b].up, cur, T, T, f1, 0, NULL, &s->blk[b].r[0].s1, f2));
+        T *= r;
+        { float *t_ = cur; cur = f1; f1 = f2; f2 = t_; }  /* cur: signal, f1: snake1(signal) */
         for (int u = 0; u < 3; u++) {
-            SCK(qt_launch_sd_snake(cur, f1, s->blk[b].r[u].s1.a, s->blk[b].r[u].s1.ib, T, C, st));
-            SCK(sd_run(s, &s->blk[b].r[u].c1, f1, T, T, f2, 0, NULL, NULL));
-            SCK(qt_launch_sd_snake(f2, f2, s->blk[b].r[u].s2.a, s->blk[b].r[u].s2.ib, T, C, st));
-            SCK(sd_run(s, &s->blk[b].r[u].c2, f2, T, T, cur, SD_RESID, NULL, cur));
+            SCK(sd_run_snake(s, &s->blk[b].r[u].c1, f1, T, T, f2, 0, NULL, &s->blk[b].r[u].s2, NULL));
+            if (u < 2)
+                SCK(sd_run_snake(s, &s->blk[b].r[u].c2, f2, T, T, cur, SD_RESID, cur, &s->blk[b].r[u + 1].s1, f1));
+            else
+                SCK(sd_run_snake(s, &s->blk[b].r[u].c2, f2, T, T, cur, SD_RESID, cur, b < 3 ? &s->blk[b + 1].s : &s->fs,
+                                 NULL));
         }
     }
-    SCK(qt_launch_sd_snake(cur, cur, s->fs.a, s->fs.ib, T, C, st));
-    SCK(qt_launch_sd_final(cur, s->fw, s->fb, d_audio, T, C, st));
+    SCK(qt_launch_sd_final(cur, s->fw, s->fb, d_audio, T, 96, st));
     return 0;
 }
 
@@ -462,3 +472,61 @@ int qwen_hip_sd_latent(void *state, const int *codes, int n_frames, float *laten
 }
 
 void *qwen_hip_sd_stream(void *state) { return state ? (void *)((sd_t *)state)->st : NULL; }
+
+/* ---- single-layer entry points (parity tests of the implicit GEMM) ------------------------ */
+typedef struct { const float *w; long long n; } sd_one_t;
+static const float *sd_one_get(void *user, const char *name, long long n) {
+    const sd_one_t *o = (const sd_one_t *)user;
+    (void)name;
+    return n == o->n ? o->w : NULL;
+}
+
+/* one layer through the decoder's GEMM: conv (kernel k, dilation d) when stride == 0, else a
+ * transposed conv of that stride; X [Tin][Cin] time-major host array, Y [Tout][Cout] */
+static int sd_op(float *Y, const float *X, const float *W, const float *bias, int Tin, int Cin, int Cout, int k, int d,
+                 int stride, int tile) {
+    sd_t tmp;
+    memset(&tmp, 0, sizeof tmp);
+    float *dx = NULL, *dy = NULL;
+    int rc = -1;
+    if (!Y || !X || !W || Tin < 1 || Cin < 16 || Cin % 16 || Cout < 4 || Cout % 4 || k < 1 ||
+        (stride ? (k > 2 * stride || stride > 64) : k > 8) || (tile && tile != 64 && tile != 128)) {
+        qt_seterr("op_sd_conv: bad shape (Cin multiple of 16, Cout of 4; conv kernel 1..8, transposed kernel <= 2 stride)");
+        return -1;
+    }
+    sd_one_t one = {W, (long long)Cout * Cin * k};
+    sd_ld_t L = {sd_one_get, &one, &tmp, NULL, 0, 0};
+    if (hipStreamCreateWithFlags(&tmp.st, hipStreamNonBlocking) != hipSuccess) { qt_seterr("op_sd_conv: stream"); return -1; }
+    sd_conv_t c = stride ? sd_convt(&L, "w", NULL, Cin, Cout, k, stride) : sd_conv(&L, "w", NULL, Cout, Cin, k, d);
+    if (!L.bad && bias) c.b = sd_put(&L, bias, (size_t)Cout);
+    free(L.tmp);
+    const int Tout = stride ? Tin * stride : Tin;
+    if (L.bad) goto done;
+    if (hipMalloc((void **)&dx, (size_t)Tin * Cin * sizeof(float)) != hipSuccess ||
+        hipMalloc((void **)&dy, (size_t)Tout * Cout * sizeof(float)) != hipSuccess) { qt_seterr("op_sd_conv: alloc"); goto done; }
+    if (hipMemcpy(dx, X, (size_t)Tin * Cin * sizeof(float), hipMemcpyHostToDevice) != hipSuccess) goto done;
+    if (qt_launch_sd_gemm(dx, Cin, Tin, c.w, Cin, Cout, c.ntap, c.off, c.phases, Tin, dy, Cout, c.b, NULL, NULL, NULL,
+                          NULL, NULL, c.b ? SD_BIAS : 0, tile, tmp.st) != hipSuccess ||
+        hipMemcpyAsync(Y, dy, (size_t)Tout * Cout * sizeof(float), hipMemcpyDeviceToHost, tmp.st) != hipSuccess ||
+        hipStreamSynchronize(tmp.st) != hipSuccess) { qt_seterr("op_sd_conv: launch failed"); goto done; }
+    rc = 0;
+done:
+    if (dx) (void)hipFree(dx);
+    if (dy) (void)hipFree(dy);
+    for (int i = 0; i < tmp.n_allocs; i++) (void)hipFree(tmp.allocs[i]);
+    free(tmp.allocs);
+    (void)hipStreamDestroy(tmp.st);
+    return rc;
+}
+
+int qwen_hip_op_sd_conv(float *Y, const float *X, const float *W, const float *bias, int T, int Cin, int Cout,
+                        int kernel, int dilation, int tile) {
+    if (dilation < 1) { qt_seterr("op_sd_conv: dilation %d", dilation); return -1; }
+    return sd_op(Y, X, W, bias, T, Cin, Cout, kernel, dilation, 0, tile);
+}
+
+int qwen_hip_op_sd_conv_transpose(float *Y, const float *X, const float *W, const float *bias, int Tin, int Cin,
+                                  int Cout, int kernel, int stride, int tile) {
+    if (stride < 1) { qt_seterr("op_sd_conv_transpose: stride %d", stride); return -1; }
+    return sd_op(Y, X, W, bias, Tin, Cin, Cout, kernel, 1, stride, tile);
+}

@@ -38,7 +38,8 @@ EXPORTS = [
     "qwen_hip_op_prefill_attention", "qwen_hip_talker_step_layers", "qwen_hip_op_matmat_int8_noalloc",
     "qwen_hip_generate", "qwen_hip_talker_load_file",
     "qwen_hip_sd_init", "qwen_hip_sd_load_file", "qwen_hip_sd_decode", "qwen_hip_sd_decode_device",
-    "qwen_hip_sd_latent", "qwen_hip_sd_stream", "qwen_hip_sd_free",
+    "qwen_hip_sd_latent", "qwen_hip_sd_stream", "qwen_hip_sd_free", "qwen_hip_op_sd_conv",
+    "qwen_hip_op_sd_conv_transpose",
 ]
 
 SD_GET_FN = C.CFUNCTYPE(C.c_void_p, C.c_void_p, C.c_char_p, C.c_longlong)
@@ -169,6 +170,9 @@ def lib():
         L.qwen_hip_sd_latent.argtypes = [vp, vp, i, vp]; L.qwen_hip_sd_latent.restype = i
         L.qwen_hip_sd_stream.argtypes = [vp]; L.qwen_hip_sd_stream.restype = vp
         L.qwen_hip_sd_free.argtypes = [vp]
+        L.qwen_hip_op_sd_conv.argtypes = [vp, vp, vp, vp, i, i, i, i, i, i]; L.qwen_hip_op_sd_conv.restype = i
+        L.qwen_hip_op_sd_conv_transpose.argtypes = [vp, vp, vp, vp, i, i, i, i, i, i]
+        L.qwen_hip_op_sd_conv_transpose.restype = i
         _lib = L
     return _lib
 

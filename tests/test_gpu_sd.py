@@ -85,3 +85,50 @@ def test_sd_rejects_bad_arguments():
         hip.SpeechDecoder.from_tensors(missing)
     assert not L.qwen_hip_sd_load_file(b"/nonexistent/speech_decoder.safetensors")
     assert np.array_equal(d.decode(codes), d.decode(codes))        # the state stays usable
+
+
+def _conv_ref(x, w, b, d):
+    from oracle import sd_oracle
+    return sd_oracle.conv1d(x.T.astype(np.float64), w.astype(np.float64), None if b is None else b.astype(np.float64), d).T
+
+
+def _convt_ref(x, w, b, s):
+    from oracle import sd_oracle
+    return sd_oracle.conv_transpose1d(x.T.astype(np.float64), w.astype(np.float64),
+                                      None if b is None else b.astype(np.float64), s).T
+
+
+@pytest.mark.parametrize("tile", [0, 64, 128])
+@pytest.mark.parametrize("T,cin,cout,k,d", [(3000, 96, 96, 7, 9), (1000, 256, 384, 7, 3), (257, 1024, 1536, 7, 1),
+                                            (64, 512, 1024, 3, 1), (130, 16, 4, 1, 1)])
+def test_op_sd_conv_vs_f64(T, cin, cout, k, d, tile):
+    """One causal conv through the decoder's implicit GEMM (both tiles) against the float64
+    conv of the oracle (sd.c:98-119): f32 accumulation over K = kernel x Cin only."""
+    rng = np.random.default_rng(T + cin + k + tile)
+    x = rng.standard_normal((T, cin)).astype(np.float32)
+    w = (rng.standard_normal((cout, cin, k)) / np.sqrt(cin * k)).astype(np.float32)
+    b = (rng.standard_normal(cout) * 0.1).astype(np.float32) if cout % 8 == 0 else None
+    y = np.empty((T, cout), np.float32)
+    hip.check(hip.lib().qwen_hip_op_sd_conv(y.ctypes.data, x.ctypes.data, w.ctypes.data,
+                                            None if b is None else b.ctypes.data, T, cin, cout, k, d, tile), "op_sd_conv")
+    want = _conv_ref(x, w, b, d)
+    err = float(np.abs(y - want).max() / np.abs(want).max())
+    assert err < 2e-6 * max(1.0, np.sqrt(cin * k) / 8), err
+
+
+@pytest.mark.parametrize("tile", [0, 64, 128])
+@pytest.mark.parametrize("T,cin,cout,k,s", [(500, 192, 96, 6, 3), (300, 384, 192, 8, 4), (64, 1024, 1024, 2, 2),
+                                            (100, 64, 32, 3, 2), (40, 1536, 768, 16, 8)])
+def test_op_sd_conv_transpose_vs_f64(T, cin, cout, k, s, tile):
+    """One causal transposed conv (phases of the output, taps at offsets 0 and -1) against
+    the oracle's (sd.c:122-160), including a kernel shorter than 2 x stride."""
+    rng = np.random.default_rng(T + cin + k + s + tile)
+    x = rng.standard_normal((T, cin)).astype(np.float32)
+    w = (rng.standard_normal((cin, cout, k)) / np.sqrt(2 * cin)).astype(np.float32)
+    b = (rng.standard_normal(cout) * 0.1).astype(np.float32)
+    y = np.empty((T * s, cout), np.float32)
+    hip.check(hip.lib().qwen_hip_op_sd_conv_transpose(y.ctypes.data, x.ctypes.data, w.ctypes.data, b.ctypes.data, T,
+                                                      cin, cout, k, s, tile), "op_sd_conv_transpose")
+    want = _convt_ref(x, w, b, s)
+    err = float(np.abs(y - want).max() / np.abs(want).max())
+    assert err < 2e-6 * max(1.0, np.sqrt(2 * cin) / 8), err
