@@ -7,7 +7,10 @@
  */
 #include "qwen_tts_hip_glue.h"
 
+#include "ingot/safetensors.h"
+
 #include <stdio.h>
+#include <stdlib.h>
 #include <string.h>
 
 /* one matrix at precision prec; NULL w when that precision's pointer is absent */
@@ -154,4 +157,30 @@ int qwen_hip_glue_codec_sample(qwen_tts_ctx_t *ctx, int frame, int text_content_
     if (ctx->greedy_warmup > 0 && frame < ctx->greedy_warmup) { temp = 0.0f; top_k = 1; }
     return qwen_hip_op_codec_sample(ctx->logits, ctx->config.codec_vocab_size, frame, boost, temp, top_k, ctx->top_p,
                                     ctx->rep_penalty, ctx->prev_tokens, ctx->n_prev_tokens, lcg);
+}
+
+/* ---- speech decoder ----------------------------------------------------------------------- */
+/* the getter of qwen_hip_sd_init over the reference's mmap: the tensor's own F32 bytes, as
+ * get_f32 hands them to the CPU decoder (sd.c:77-80), checked for size and dtype */
+static const float *glue_sd_get(void *user, const char *name, long long n_elems) {
+    ingot_st *st = (ingot_st *)user;
+    const ingot_st_tensor *t = ingot_st_find(st, name);
+    if (!t || t->dtype != INGOT_DT_F32 || (long long)t->nelem != n_elems) return NULL;
+    return (const float *)ingot_st_data(st, t);
+}
+
+void *qwen_hip_glue_sd_init(qwen_tts_ctx_t *ctx) {
+    if (!ctx->speech_safetensors) return NULL;
+    return qwen_hip_sd_init(glue_sd_get, ctx->speech_safetensors);
+}
+
+int qwen_hip_glue_sd_decode(void *state, const int *codes, int n_frames, float **audio_out, int *n_samples) {
+    const int ns = n_frames * 1920;
+    float *a = (float *)malloc((size_t)ns * sizeof(float));
+    if (!a) return -1;
+    const int got = qwen_hip_sd_decode(state, codes, n_frames, a, ns);
+    if (got < 0) { free(a); return -1; }
+    *audio_out = a;
+    *n_samples = got;
+    return 0;
 }

@@ -40,4 +40,13 @@ int qwen_hip_glue_cp_step(void *state, qwen_tts_ctx_t *ctx, float *x, int pos);
  * Returns the token, or -1 (then the caller samples on the CPU). */
 int qwen_hip_glue_codec_sample(qwen_tts_ctx_t *ctx, int frame, int text_content_len, uint32_t *lcg);
 
+/* qwen_speech_decoder_load(ctx) (qwen_tts_speech_decoder.c:372): the decoder's F32 tensors
+ * from ctx->speech_safetensors by name, as get_f32 finds them (sd.c:77-80), onto the
+ * device.  NULL: stay on the CPU decoder. */
+void *qwen_hip_glue_sd_init(qwen_tts_ctx_t *ctx);
+/* qwen_speech_decoder_decode's contract (sd.c:579): codes [n_frames][16] -> *audio_out
+ * (malloc'd, the caller frees it as it frees the CPU decoder's) of *n_samples samples.
+ * 0 on success. */
+int qwen_hip_glue_sd_decode(void *state, const int *codes, int n_frames, float **audio_out, int *n_samples);
+
 #endif

@@ -132,3 +132,37 @@ def test_op_sd_conv_transpose_vs_f64(T, cin, cout, k, s, tile):
     want = _convt_ref(x, w, b, s)
     err = float(np.abs(y - want).max() / np.abs(want).max())
     assert err < 2e-6 * max(1.0, np.sqrt(2 * cin) / 8), err
+
+
+@need_ref
+def test_sd_glue_over_reference_ctx():
+    """The reference-side glue (qwen_hip_glue_sd_init over ctx->speech_safetensors, the
+    tensors the reference's get_f32 hands its own decoder; qwen_hip_glue_sd_decode with
+    qwen_speech_decoder_decode's contract) against the reference's decode of the same ctx
+    contents."""
+    import ctypes as C
+    import os
+    from conftest import ROOT
+    from oracle.oracle import RefSpeechDecoder
+    gp = os.path.join(ROOT, "oracle", "_ref", "libqwen_glue.so")
+    if not os.path.exists(gp):
+        pytest.skip("oracle/_ref/libqwen_glue.so not built")
+    G = C.CDLL(gp)
+    vp, i = C.c_void_p, C.c_int
+    G.qwen_hip_glue_sd_init.argtypes = [vp]; G.qwen_hip_glue_sd_init.restype = vp
+    G.qwen_hip_glue_sd_decode.argtypes = [vp, vp, i, C.POINTER(C.POINTER(C.c_float)), C.POINTER(C.c_int)]
+    G.qwen_hip_glue_sd_decode.restype = i
+    path, _ = sd_model()
+    ref = RefSpeechDecoder(path, threads=8)          # its ctx carries speech_safetensors
+    st = G.qwen_hip_glue_sd_init(ref.h)
+    assert st, hip.last_error()
+    codes = sd_codes(2, 77)
+    ap, ns = C.POINTER(C.c_float)(), C.c_int()
+    assert G.qwen_hip_glue_sd_decode(st, codes.ctypes.data, 2, C.byref(ap), C.byref(ns)) == 0
+    got = np.ctypeslib.as_array(ap, shape=(ns.value,)).copy()
+    C.CDLL("libc.so.6").free(ap)
+    hip.lib().qwen_hip_sd_free(st)
+    want = ref.decode(codes)
+    assert got.shape == want.shape
+    assert np.array_equal(got, _dec().decode(codes))                 # same weights -> same bits
+    assert np.abs(got - want).max() <= 2e-2 and rel_l2(got, want) <= 1e-3
