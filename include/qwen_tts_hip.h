@@ -366,6 +366,17 @@ int qwen_hip_sd_decode_device(void *state, const int *d_codes, int n_frames, flo
 int qwen_hip_sd_latent(void *state, const int *codes, int n_frames, float *latent_out);
 void *qwen_hip_sd_stream(void *state);
 void qwen_hip_sd_free(void *state);
+/* Streaming decode (qwen_speech_decoder_decode_streaming_st, sd.c:1881-2389, its exact path):
+ * a stream state over a decoder state (weights shared; several streams may share one
+ * decoder, calls on them are serialised on its stream).  Each call decodes new_frames more
+ * frames of the utterance and returns exactly their 1920 new_frames samples, equal to that
+ * slice of the one-shot decode of all frames so far (qwen_hip_sd_decode); at most 8000 frames
+ * per utterance.  reset starts a new utterance (qwen_sd_stream_init). */
+void *qwen_hip_sd_stream_new(void *sd_state);
+int qwen_hip_sd_stream_decode(void *stream_state, const int *new_codes, int new_frames, float *audio_out,
+                              int max_samples);
+int qwen_hip_sd_stream_reset(void *stream_state);
+void qwen_hip_sd_stream_free(void *stream_state);
 /* The decoder's layers one at a time, on time-major host arrays (X [T][Cin], Y [T][Cout]):
  * causal_conv1d (sd.c:98-119; W [Cout][Cin][kernel], left pad (kernel-1) dilation) and
  * causal_conv_transpose1d (sd.c:122-160; W [Cin][Cout][kernel], kernel <= 2 stride, Y

@@ -545,6 +545,9 @@ class RefSpeechDecoder:
         L.ref_sd_open.argtypes = [C.c_char_p, i]; L.ref_sd_open.restype = vp
         L.ref_sd_decode.argtypes = [vp, vp, i, vp, i]; L.ref_sd_decode.restype = i
         L.ref_time_sd_decode.argtypes = [vp, vp, i]; L.ref_time_sd_decode.restype = C.c_double
+        L.ref_sd_stream_new.argtypes = []; L.ref_sd_stream_new.restype = vp
+        L.ref_sd_stream_decode.argtypes = [vp, vp, vp, i, vp, i]; L.ref_sd_stream_decode.restype = i
+        L.ref_sd_stream_free.argtypes = [vp]
         self.L = L
         self.h = L.ref_sd_open(str(path).encode(), threads)
         if not self.h:
@@ -558,6 +561,23 @@ class RefSpeechDecoder:
         if ns < 0:
             raise RuntimeError("reference decode failed")
         return out[:ns]
+
+    def stream_decode(self, chunks):
+        """The reference's exact streaming decode over successive chunks of codes (one
+        fresh stream state); returns the concatenated audio."""
+        st = self.L.ref_sd_stream_new()
+        out = []
+        try:
+            for codes in chunks:
+                codes = np.ascontiguousarray(codes, np.int32)
+                buf = np.empty(codes.shape[0] * 1920, np.float32)
+                ns = self.L.ref_sd_stream_decode(self.h, st, codes.ctypes.data, codes.shape[0], buf.ctypes.data, buf.size)
+                if ns < 0:
+                    raise RuntimeError("reference streaming decode failed")
+                out.append(buf[:ns])
+        finally:
+            self.L.ref_sd_stream_free(st)
+        return np.concatenate(out)
 
     def time_decode(self, codes):
         codes = np.ascontiguousarray(codes, np.int32)

@@ -381,3 +381,33 @@ double ref_time_sd_decode(void *h, const int *codes, int n_frames) {
     if (rc != 0) return -1.0;
     return (double)(t1.tv_sec - t0.tv_sec) + 1e-9 * (double)(t1.tv_nsec - t0.tv_nsec);
 }
+
+/* the reference's exact streaming decode (qwen_speech_decoder_decode_streaming_st,
+ * sd.c:1881-2389) with a state of its own */
+extern void qwen_sd_stream_init(qwen_sd_stream_state_t *st);
+extern void qwen_sd_stream_free(qwen_sd_stream_state_t *st);
+extern int qwen_speech_decoder_decode_streaming_st(qwen_tts_ctx_t *ctx, qwen_sd_stream_state_t *st, const int *new_codes,
+                                                   int new_frames, float **audio_out, int *n_samples);
+
+void *ref_sd_stream_new(void) {
+    qwen_sd_stream_state_t *st = calloc(1, sizeof *st);
+    if (st) qwen_sd_stream_init(st);
+    return st;
+}
+
+int ref_sd_stream_decode(void *h, void *st, const int *codes, int n_frames, float *out, int cap) {
+    float *audio = NULL;
+    int n = 0;
+    if (qwen_speech_decoder_decode_streaming_st((qwen_tts_ctx_t *)h, (qwen_sd_stream_state_t *)st, codes, n_frames, &audio,
+                                                &n) != 0 || !audio) return -1;
+    if (n > cap) n = cap;
+    memcpy(out, audio, (size_t)n * sizeof(float));
+    free(audio);
+    return n;
+}
+
+void ref_sd_stream_free(void *st) {
+    if (!st) return;
+    qwen_sd_stream_free((qwen_sd_stream_state_t *)st);
+    free(st);
+}

@@ -101,7 +101,7 @@ hipError_t qt_launch_pf_attn(const float *QKV, int ld, int S, int nh, int nkv, f
                              hipStream_t st);
 
 /* speech decoder (qt_sd.hip) */
-hipError_t qt_launch_sd_gemm(const float *X, int ldx, int Tx, const float *W, int K, int N, int ntap, const int *off,
+hipError_t qt_launch_sd_gemm(const float *X, int ldx, int Tx, int xlo, const float *W, int K, int N, int ntap, const int *off,
                              int phases, int T, float *Y, int ldy, const float *bias, const float *cscale,
                              const float *R, const float *sa, const float *sib, float *Y2, int epi, int tile,
                              hipStream_t st);
@@ -109,13 +109,15 @@ hipError_t qt_launch_sd_cb_dequant(const float *es, const float *cu, float *cb, 
 hipError_t qt_launch_sd_snake_params(const float *la, const float *lb, float *a, float *ib, int n, hipStream_t st);
 hipError_t qt_launch_sd_vq(const int *codes, const float *cb, float *E, int n, int cbsize, hipStream_t st);
 hipError_t qt_launch_sd_rmsnorm(const float *x, const float *w, float *out, int T, int C, float eps, hipStream_t st);
-hipError_t qt_launch_sd_rope(float *qkv, const float *cs, const float *sn, int T, hipStream_t st);
-hipError_t qt_launch_sd_attn(const float *qkv, float *out, int T, int window, float scale, hipStream_t st);
+hipError_t qt_launch_sd_rope(float *qkv, const float *cs, const float *sn, int T, int row0, int pos0, hipStream_t st);
+hipError_t qt_launch_sd_attn(const float *qkv, float *out, int T, int q0, int kmin, int window, float scale,
+                             hipStream_t st);
 hipError_t qt_launch_sd_swiglu(const float *gu, float *m, int T, int C, hipStream_t st);
 hipError_t qt_launch_sd_dwln(const float *x, const float *dw, const float *db, const float *lw, const float *lb,
-                             float *out, int T, int C, hipStream_t st);
-hipError_t qt_launch_sd_final(const float *x, const float *w, const float *b, float *audio, int T, int C,
+                             float *out, int T, int C, int xlo, hipStream_t st);
+hipError_t qt_launch_sd_final(const float *x, const float *w, const float *b, float *audio, int T, int C, int xlo,
                               hipStream_t st);
+hipError_t qt_launch_sd_shift(float *buf, int H, int T, int C, hipStream_t st);
 #ifdef __cplusplus
 }
 #endif

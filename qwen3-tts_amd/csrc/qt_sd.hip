@@ -9,7 +9,8 @@
 //
 //   Y[t*os + z][n] = epi( sum over taps p, channels k of X[t + off_p][k] * W[z][p][k][n] )
 //
-// (rows of X outside [0, Tx) read as zero: the causal left padding).  A causal conv of
+// (rows of X outside [xlo, Tx) read as zero: the causal left padding; the streaming decode
+// keeps the previous chunk's last rows at negative indices, xlo < 0).  A causal conv of
 // kernel K and dilation d has taps off_p = (p - K + 1) d; a transposed conv of stride s
 // and kernel 2s is s phases z (output rows t*s + z), each with taps at offsets 0 and -1
 // (kernel columns z and z + s); a linear layer is one tap.  The epilogue adds a bias,
@@ -30,7 +31,7 @@ typedef float qt_sd_f4 __attribute__((ext_vector_type(4)));
 enum { SD_EPI_BIAS = 1, SD_EPI_GELU = 2, SD_EPI_CSCALE = 4, SD_EPI_RESID = 8, SD_EPI_SNAKE = 16, SD_EPI_SNAKE2 = 32 };
 
 struct SdGemmArgs {
-    const float *X; int ldx, Tx;          // input rows [Tx][ldx]
+    const float *X; int ldx, Tx, xlo;     // input rows [xlo, Tx) of a [.][ldx] buffer (xlo <= 0: history rows)
     const float *W;                       // [phases][ntap][K][N]
     int K, N, ntap;
     int off[SD_MAXTAP];
@@ -77,7 +78,7 @@ __global__ __launch_bounds__(SD_WG) void k_sd_gemm(SdGemmArgs a) {
         for (int q = 0; q < AQ; q++) {
             const int f = tid + q * SD_WG, ar = f >> 2, ac = (f & 3) * 4;
             const int xr = t0 + ar + a.off[p];
-            av[q] = (t0 + ar < a.T && xr >= 0 && xr < a.Tx)
+            av[q] = (t0 + ar < a.T && xr >= a.xlo && xr < a.Tx)
                         ? *reinterpret_cast<const float4 *>(a.X + (size_t)xr * a.ldx + k0 + ac)
                         : make_float4(0.f, 0.f, 0.f, 0.f);
         }
@@ -200,32 +201,36 @@ __global__ __launch_bounds__(SD_WG) void k_sd_rmsnorm(const float *x, const floa
     for (int i = threadIdx.x; i < C; i += SD_WG) out[(size_t)blockIdx.x * C + i] = (xr[i] * inv) * w[i];
 }
 
-// NeoX split-half RoPE of q and k (columns [0, 1024) and [1024, 2048) of a [T][3072] row),
-// 16 heads of 64, tables [pos][32] (sd.c:790-860)
-__global__ void k_sd_rope(float *qkv, const float *cs, const float *sn, int T) {
+// NeoX split-half RoPE of q and k (columns [0, 1024) and [1024, 2048) of a [.][3072] row),
+// 16 heads of 64, tables [pos][32] (sd.c:790-860): rows row0 .. row0 + T - 1 at positions
+// pos0 .. pos0 + T - 1
+__global__ void k_sd_rope(float *qkv, const float *cs, const float *sn, int T, int row0, int pos0) {
     const int i = blockIdx.x * blockDim.x + threadIdx.x;      // (t, which, head, pair)
     if (i >= T * 2 * 16 * 32) return;
     const int pr = i & 31, h = (i >> 5) & 15, which = (i >> 9) & 1, t = i >> 10;
-    float *v = qkv + (size_t)t * 3072 + which * 1024 + h * 64;
-    const float c = cs[t * 32 + pr], s = sn[t * 32 + pr];
+    float *v = qkv + (size_t)(row0 + t) * 3072 + which * 1024 + h * 64;
+    const int p = pos0 + t;
+    const float c = cs[p * 32 + pr], s = sn[p * 32 + pr];
     const float x1 = v[pr], x2 = v[pr + 32];
     v[pr] = x1 * c - x2 * s;
     v[pr + 32] = x2 * c + x1 * s;
 }
 
 // windowed causal attention (qwen_causal_attention_windowed, k.c:3579-3700; seq_q == seq_k,
-// q_offset 0): query t of head h over keys [max(0, t + 1 - window), t].  One wave per
-// (t, h): lanes take keys for the scores (dot over 64 dims), then lanes take dims for
-// the weighted sum of values.
-__global__ __launch_bounds__(SD_WG) void k_sd_attn(const float *qkv, float *out, int T, int window, float scale) {
+// q_offset 0): the query at buffer row q0 + t of head h over keys [max(kmin, q0 + t + 1 -
+// window), q0 + t] (kmin: the first row holding a key; the streaming decode keeps the
+// previous chunks' last window - 1 keys in rows [kmin, q0)).  One wave per (t, h): lanes take
+// keys for the scores (dot over 64 dims), then lanes take dims for the weighted sum of values.
+__global__ __launch_bounds__(SD_WG) void k_sd_attn(const float *qkv, float *out, int T, int q0, int kmin, int window,
+                                                   float scale) {
     __shared__ float sq[QT_WAVES][64];
     __shared__ float sp[QT_WAVES][128];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int item = blockIdx.x * QT_WAVES + wave;
     if (item >= T * 16) return;
-    const int t = item >> 4, h = item & 15;
-    const int j0 = max(0, t + 1 - window), nk = t + 1 - j0;   // nk <= window <= 128
-    sq[wave][lane] = qkv[(size_t)t * 3072 + h * 64 + lane];
+    const int t = item >> 4, h = item & 15, qr = q0 + t;
+    const int j0 = max(kmin, qr + 1 - window), nk = qr + 1 - j0;   // nk <= window <= 128
+    sq[wave][lane] = qkv[(size_t)qr * 3072 + h * 64 + lane];
     __builtin_amdgcn_s_waitcnt(0);
     __builtin_amdgcn_wave_barrier();
     float sc[2];
@@ -274,9 +279,10 @@ __global__ void k_sd_swiglu(const float *gu, float *m, int T, int C) {
 }
 
 // ConvNeXt: depthwise causal conv (k = 7, pad 6) + LayerNorm over the channels of each
-// time step (mean and E[x^2] - mean^2, eps 1e-5), sd.c:1086-1116.  One workgroup per t.
+// time step (mean and E[x^2] - mean^2, eps 1e-5), sd.c:1086-1116.  One workgroup per t;
+// input rows before xlo (<= 0) read as zero.
 __global__ __launch_bounds__(SD_WG) void k_sd_dwln(const float *x, const float *dw, const float *db, const float *lw,
-                                                   const float *lb, float *out, int T, int C) {
+                                                   const float *lb, float *out, int T, int C, int xlo) {
     __shared__ float red[QT_WAVES];
     const int t = blockIdx.x;
     float v[4];
@@ -289,7 +295,7 @@ __global__ __launch_bounds__(SD_WG) void k_sd_dwln(const float *x, const float *
             d = db[c];
             for (int j = 0; j < 7; j++) {
                 const int ti = t - 6 + j;
-                if (ti >= 0) d = fmaf(dw[c * 7 + j], x[(size_t)ti * C + c], d);
+                if (ti >= xlo) d = fmaf(dw[c * 7 + j], x[(size_t)ti * C + c], d);
             }
         }
         v[q] = d;
@@ -310,19 +316,20 @@ __global__ __launch_bounds__(SD_WG) void k_sd_dwln(const float *x, const float *
 }
 
 // final conv to one channel (k = 7, pad 6) + clamp to [-1, 1] (sd.c:1259-1279); x [T][C]
-// already through the final snake.  A workgroup takes 64 samples: the 70 input rows they
+// already through the final snake (rows before xlo <= 0 read as zero).  A workgroup takes
+// 64 samples: the 70 input rows they
 // need go to LDS (row stride C + 1, so the 64 lanes of a read, one row each, hit distinct
 // banks); wave w sums channels [w C/4, (w+1) C/4) for its lane's sample, and the four
 // partial sums are added in wave order.
 #define SD_FIN_T 64
 __global__ __launch_bounds__(SD_WG) void k_sd_final(const float *x, const float *w, const float *b, float *audio, int T,
-                                                    int C) {
+                                                    int C, int xlo) {
     extern __shared__ float xs[];                        // [70][C + 1]
     __shared__ float part[QT_WAVES][SD_FIN_T];
     const int t0 = blockIdx.x * SD_FIN_T, ld = C + 1;
     for (int i = threadIdx.x; i < (SD_FIN_T + 6) * C; i += SD_WG) {
         const int r = i / C, c = i % C, ti = t0 - 6 + r;
-        xs[r * ld + c] = (ti >= 0 && ti < T) ? x[(size_t)ti * C + c] : 0.f;
+        xs[r * ld + c] = (ti >= xlo && ti < T) ? x[(size_t)ti * C + c] : 0.f;
     }
     __syncthreads();
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -339,21 +346,29 @@ __global__ __launch_bounds__(SD_WG) void k_sd_final(const float *x, const float 
     }
 }
 
+// streaming history: the last H rows of a buffer's [H + T] rows become its first H rows
+// (one thread per column walks the rows forward, so overlapping ranges copy correctly)
+__global__ void k_sd_shift(float *buf, int H, int T, int C) {
+    const int c = blockIdx.x * blockDim.x + threadIdx.x;
+    if (c >= C) return;
+    for (int r = 0; r < H; r++) buf[(size_t)r * C + c] = buf[(size_t)(T + r) * C + c];
+}
+
 // ---- launchers ----------------------------------------------------------------------------
 
 // tile: 0 = by size (128 x 128 where that still gives two workgroups per CU), 64 or 128 = forced
-extern "C" hipError_t qt_launch_sd_gemm(const float *X, int ldx, int Tx, const float *W, int K, int N, int ntap,
+extern "C" hipError_t qt_launch_sd_gemm(const float *X, int ldx, int Tx, int xlo, const float *W, int K, int N, int ntap,
                                         const int *off, int phases, int T, float *Y, int ldy, const float *bias,
                                         const float *cscale, const float *R, const float *sa, const float *sib,
                                         float *Y2, int epi, int tile, hipStream_t st) {
     if (!X || !W || !Y || K <= 0 || K % SD_KC || N <= 0 || N % 4 || ntap < 1 || ntap > SD_MAXTAP || phases < 1 ||
-        T <= 0 || Tx <= 0 || ldx % 4 || ldx < K || ldy < N)
+        T <= 0 || Tx <= 0 || xlo > 0 || ldx % 4 || ldx < K || ldy < N)
         return hipErrorInvalidValue;
     if (((epi & 1) && !bias) || ((epi & 4) && !cscale) || ((epi & 8) && !R)) return hipErrorInvalidValue;
     if ((epi & (SD_EPI_SNAKE | SD_EPI_SNAKE2)) && (!sa || !sib)) return hipErrorInvalidValue;
     if ((epi & SD_EPI_SNAKE2) && (!Y2 || (epi & SD_EPI_SNAKE))) return hipErrorInvalidValue;
     SdGemmArgs a;
-    a.X = X; a.ldx = ldx; a.Tx = Tx; a.W = W; a.K = K; a.N = N; a.ntap = ntap;
+    a.X = X; a.ldx = ldx; a.Tx = Tx; a.xlo = xlo; a.W = W; a.K = K; a.N = N; a.ntap = ntap;
     for (int i = 0; i < SD_MAXTAP; i++) a.off[i] = i < ntap ? off[i] : 0;
     a.T = T; a.Y = Y; a.ldy = ldy; a.os = phases; a.bias = bias; a.cscale = cscale; a.R = R; a.epi = epi;
     a.sa = sa; a.sib = sib; a.Y2 = Y2;
@@ -388,14 +403,17 @@ extern "C" hipError_t qt_launch_sd_rmsnorm(const float *x, const float *w, float
     hipLaunchKernelGGL(k_sd_rmsnorm, dim3(T), dim3(SD_WG), 0, st, x, w, out, C, eps);
     return hipGetLastError();
 }
-extern "C" hipError_t qt_launch_sd_rope(float *qkv, const float *cs, const float *sn, int T, hipStream_t st) {
+extern "C" hipError_t qt_launch_sd_rope(float *qkv, const float *cs, const float *sn, int T, int row0, int pos0,
+                                        hipStream_t st) {
     const int n = T * 1024;
-    hipLaunchKernelGGL(k_sd_rope, dim3((n + 255) / 256), dim3(256), 0, st, qkv, cs, sn, T);
+    hipLaunchKernelGGL(k_sd_rope, dim3((n + 255) / 256), dim3(256), 0, st, qkv, cs, sn, T, row0, pos0);
     return hipGetLastError();
 }
-extern "C" hipError_t qt_launch_sd_attn(const float *qkv, float *out, int T, int window, float scale, hipStream_t st) {
-    if (window <= 0 || window > 128) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(k_sd_attn, dim3((T * 16 + QT_WAVES - 1) / QT_WAVES), dim3(SD_WG), 0, st, qkv, out, T, window, scale);
+extern "C" hipError_t qt_launch_sd_attn(const float *qkv, float *out, int T, int q0, int kmin, int window, float scale,
+                                        hipStream_t st) {
+    if (window <= 0 || window > 128 || kmin < 0 || kmin > q0) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_sd_attn, dim3((T * 16 + QT_WAVES - 1) / QT_WAVES), dim3(SD_WG), 0, st, qkv, out, T, q0, kmin,
+                       window, scale);
     return hipGetLastError();
 }
 extern "C" hipError_t qt_launch_sd_swiglu(const float *gu, float *m, int T, int C, hipStream_t st) {
@@ -404,15 +422,21 @@ extern "C" hipError_t qt_launch_sd_swiglu(const float *gu, float *m, int T, int 
     return hipGetLastError();
 }
 extern "C" hipError_t qt_launch_sd_dwln(const float *x, const float *dw, const float *db, const float *lw, const float *lb,
-                                        float *out, int T, int C, hipStream_t st) {
-    if (C > 4 * SD_WG) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(k_sd_dwln, dim3(T), dim3(SD_WG), 0, st, x, dw, db, lw, lb, out, T, C);
+                                        float *out, int T, int C, int xlo, hipStream_t st) {
+    if (C > 4 * SD_WG || xlo > 0) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_sd_dwln, dim3(T), dim3(SD_WG), 0, st, x, dw, db, lw, lb, out, T, C, xlo);
     return hipGetLastError();
 }
 extern "C" hipError_t qt_launch_sd_final(const float *x, const float *w, const float *b, float *audio, int T, int C,
-                                         hipStream_t st) {
-    if (C % QT_WAVES || C > 256) return hipErrorInvalidValue;
+                                         int xlo, hipStream_t st) {
+    if (C % QT_WAVES || C > 256 || xlo > 0) return hipErrorInvalidValue;
     const size_t lds = (size_t)(SD_FIN_T + 6) * (C + 1) * sizeof(float);
-    hipLaunchKernelGGL(k_sd_final, dim3((T + SD_FIN_T - 1) / SD_FIN_T), dim3(SD_WG), lds, st, x, w, b, audio, T, C);
+    hipLaunchKernelGGL(k_sd_final, dim3((T + SD_FIN_T - 1) / SD_FIN_T), dim3(SD_WG), lds, st, x, w, b, audio, T, C, xlo);
+    return hipGetLastError();
+}
+
+extern "C" hipError_t qt_launch_sd_shift(float *buf, int H, int T, int C, hipStream_t st) {
+    if (H <= 0) return hipSuccess;
+    hipLaunchKernelGGL(k_sd_shift, dim3((C + 255) / 256), dim3(256), 0, st, buf, H, T, C);
     return hipGetLastError();
 }

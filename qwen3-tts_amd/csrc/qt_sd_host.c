@@ -358,14 +358,14 @@ static int sd_reserve(sd_t *s, int n) {
 
 static hipError_t sd_run(const sd_t *s, const sd_conv_t *c, const float *X, int Tx, int T, float *Y, int epi,
                          const float *cscale, const float *R) {
-    return qt_launch_sd_gemm(X, c->K, Tx, c->w, c->K, c->N, c->ntap, c->off, c->phases, T, Y, c->N,
+    return qt_launch_sd_gemm(X, c->K, Tx, 0, c->w, c->K, c->N, c->ntap, c->off, c->phases, T, Y, c->N,
                              c->b, cscale, R, NULL, NULL, NULL, epi | (c->b ? SD_BIAS : 0), 0, s->st);
 }
 
 /* the same with a snake on the output: in place (Y2 == NULL) or into Y2 beside Y */
 static hipError_t sd_run_snake(const sd_t *s, const sd_conv_t *c, const float *X, int Tx, int T, float *Y, int epi,
                                const float *R, const sd_snake_t *sn, float *Y2) {
-    return qt_launch_sd_gemm(X, c->K, Tx, c->w, c->K, c->N, c->ntap, c->off, c->phases, T, Y, c->N, c->b, NULL, R,
+    return qt_launch_sd_gemm(X, c->K, Tx, 0, c->w, c->K, c->N, c->ntap, c->off, c->phases, T, Y, c->N, c->b, NULL, R,
                              sn->a, sn->ib, Y2, epi | (c->b ? SD_BIAS : 0) | (Y2 ? SD_SNAKE2 : SD_SNAKE), 0, s->st);
 }
 
@@ -383,8 +383,8 @@ static int sd_enqueue_latent(sd_t *s, const int *d_codes, int n) {
         const sd_layer_t *y = &s->L[l];
         SCK(qt_launch_sd_rmsnorm(s->H, y->n1, s->XN, n, 512, 1e-5f, st));
         SCK(sd_run(s, &y->qkv, s->XN, n, n, s->QKV, 0, NULL, NULL));
-        SCK(qt_launch_sd_rope(s->QKV, s->rope_c, s->rope_s, n, st));
-        SCK(qt_launch_sd_attn(s->QKV, s->A, n, 72, 0.125f, st));
+        SCK(qt_launch_sd_rope(s->QKV, s->rope_c, s->rope_s, n, 0, 0, st));
+        SCK(qt_launch_sd_attn(s->QKV, s->A, n, 0, 0, 72, 0.125f, st));
         SCK(sd_run(s, &y->o, s->A, n, n, s->H, SD_CSCALE | SD_RESID, y->ls1, s->H));
         SCK(qt_launch_sd_rmsnorm(s->H, y->n2, s->XN, n, 512, 1e-5f, st));
         SCK(sd_run(s, &y->gu, s->XN, n, n, s->GU, 0, NULL, NULL));
@@ -407,7 +407,7 @@ static int sd_enqueue(sd_t *s, const int *d_codes, int n, float *d_audio) {
         float *up = b == 0 ? b0 : b2, *dl = b == 0 ? b1 : b0, *pw = b == 0 ? b2 : b1;
         SCK(sd_run(s, &s->cn[b].up, sig, T, T, up, 0, NULL, NULL));
         T *= 2;
-        SCK(qt_launch_sd_dwln(up, s->cn[b].dw, s->cn[b].db, s->cn[b].lw, s->cn[b].lb, dl, T, 1024, st));
+        SCK(qt_launch_sd_dwln(up, s->cn[b].dw, s->cn[b].db, s->cn[b].lw, s->cn[b].lb, dl, T, 1024, 0, st));
         SCK(sd_run(s, &s->cn[b].pw1, dl, T, T, pw, SD_GELU, NULL, NULL));
         SCK(sd_run(s, &s->cn[b].pw2, pw, T, T, up, SD_CSCALE | SD_RESID, s->cn[b].gamma, up));
         sig = up;
@@ -433,7 +433,7 @@ static int sd_enqueue(sd_t *s, const int *d_codes, int n, float *d_audio) {
                                  NULL));
         }
     }
-    SCK(qt_launch_sd_final(cur, s->fw, s->fb, d_audio, T, 96, st));
+    SCK(qt_launch_sd_final(cur, s->fw, s->fb, d_audio, T, 96, 0, st));
     return 0;
 }
 
@@ -505,7 +505,7 @@ static int sd_op(float *Y, const float *X, const float *W, const float *bias, in
     if (hipMalloc((void **)&dx, (size_t)Tin * Cin * sizeof(float)) != hipSuccess ||
         hipMalloc((void **)&dy, (size_t)Tout * Cout * sizeof(float)) != hipSuccess) { qt_seterr("op_sd_conv: alloc"); goto done; }
     if (hipMemcpy(dx, X, (size_t)Tin * Cin * sizeof(float), hipMemcpyHostToDevice) != hipSuccess) goto done;
-    if (qt_launch_sd_gemm(dx, Cin, Tin, c.w, Cin, Cout, c.ntap, c.off, c.phases, Tin, dy, Cout, c.b, NULL, NULL, NULL,
+    if (qt_launch_sd_gemm(dx, Cin, Tin, 0, c.w, Cin, Cout, c.ntap, c.off, c.phases, Tin, dy, Cout, c.b, NULL, NULL, NULL,
                           NULL, NULL, c.b ? SD_BIAS : 0, tile, tmp.st) != hipSuccess ||
         hipMemcpyAsync(Y, dy, (size_t)Tout * Cout * sizeof(float), hipMemcpyDeviceToHost, tmp.st) != hipSuccess ||
         hipStreamSynchronize(tmp.st) != hipSuccess) { qt_seterr("op_sd_conv: launch failed"); goto done; }
@@ -529,4 +529,215 @@ int qwen_hip_op_sd_conv_transpose(float *Y, const float *X, const float *W, cons
                                   int Cout, int kernel, int stride, int tile) {
     if (stride < 1) { qt_seterr("op_sd_conv_transpose: stride %d", stride); return -1; }
     return sd_op(Y, X, W, bias, Tin, Cin, Cout, kernel, 1, stride, tile);
+}
+
+/* ---- streaming decode (qwen_speech_decoder_decode_streaming_st, sd.c:1881-2389) ------------
+ * The reference's exact streaming path: each call takes new frames and returns exactly
+ * their 1920 samples each, equal to that slice of a one-shot decode.  Here every stage whose
+ * kernel looks back in time keeps the previous chunk's last rows in front of its input
+ * buffer (history rows at negative indices, zero before the first chunk, which is the
+ * causal padding): pre-conv 2 rows, the pre-transformer's roped q|k|v 71 rows per layer
+ * (window 72, positions continue across chunks), the ConvNeXt depthwise convs 6, the initial
+ * conv 6, each block's transposed conv 1 (its input: the previous block's signal, or the
+ * initial conv's output), each residual unit's dilated conv 6 d, the final conv 6.  The GEMM
+ * reads those rows through its negative tap offsets, so a chunk computes only its own rows,
+ * in the same arithmetic order as the one-shot decode (chunking does not change a bit). */
+#define SDS_CAP 32            /* frames per internal chunk (longer calls are split) */
+#define SDS_KH 71             /* key history of the 72-frame attention window */
+
+typedef struct { float *p; int H, C; } sds_buf_t;   /* [H history + rows][C] */
+
+typedef struct {
+    sd_t *sd;
+    int frames;               /* frames decoded so far */
+    sds_buf_t V, Q[8], U[2], I, C0, S[4], F1[4][3];
+    float *E, *P, *Hh, *XN, *A, *GU, *M, *LAT, *CN0, *D, *PW, *F2;
+    int *dcodes; float *daudio;
+    void **allocs; int n_allocs;
+} sds_t;
+
+static float *sds_alloc(sds_t *q, size_t floats) {
+    void *p = NULL;
+    if (hipMalloc(&p, floats * sizeof(float)) != hipSuccess) return NULL;
+    void **na = (void **)realloc(q->allocs, (size_t)(q->n_allocs + 1) * sizeof *na);
+    if (!na) { (void)hipFree(p); return NULL; }
+    q->allocs = na;
+    q->allocs[q->n_allocs++] = p;
+    return (float *)p;
+}
+
+static int sds_buf(sds_t *q, sds_buf_t *b, int H, int rows, int C) {
+    b->H = H; b->C = C;
+    b->p = sds_alloc(q, (size_t)(H + rows) * C);
+    return b->p ? 0 : -1;
+}
+
+static float *sds_new_rows(const sds_buf_t *b) { return b->p + (size_t)b->H * b->C; }
+
+void qwen_hip_sd_stream_free(void *state) {
+    sds_t *q = (sds_t *)state;
+    if (!q) return;
+    if (q->sd && q->sd->st) (void)hipStreamSynchronize(q->sd->st);
+    for (int i = 0; i < q->n_allocs; i++) (void)hipFree(q->allocs[i]);
+    free(q->allocs);
+    if (q->dcodes) (void)hipFree(q->dcodes);
+    free(q);
+}
+
+/* every history back to zero: the next call starts a new utterance (qwen_sd_stream_init) */
+int qwen_hip_sd_stream_reset(void *state) {
+    sds_t *q = (sds_t *)state;
+    if (!q) { qt_seterr("sd_stream_reset: null state"); return -1; }
+    sds_buf_t *bs[] = {&q->V, &q->U[0], &q->U[1], &q->I, &q->C0, &q->S[0], &q->S[1], &q->S[2], &q->S[3]};
+    for (size_t i = 0; i < sizeof bs / sizeof bs[0]; i++)
+        if (hipMemsetAsync(bs[i]->p, 0, (size_t)bs[i]->H * bs[i]->C * sizeof(float), q->sd->st) != hipSuccess) goto fail;
+    for (int l = 0; l < 8; l++)
+        if (hipMemsetAsync(q->Q[l].p, 0, (size_t)q->Q[l].H * q->Q[l].C * sizeof(float), q->sd->st) != hipSuccess) goto fail;
+    for (int b = 0; b < 4; b++)
+        for (int u = 0; u < 3; u++)
+            if (hipMemsetAsync(q->F1[b][u].p, 0, (size_t)q->F1[b][u].H * q->F1[b][u].C * sizeof(float), q->sd->st) != hipSuccess)
+                goto fail;
+    if (hipStreamSynchronize(q->sd->st) != hipSuccess) goto fail;
+    q->frames = 0;
+    return 0;
+fail:
+    qt_seterr("sd_stream_reset: device memset failed");
+    return -1;
+}
+
+void *qwen_hip_sd_stream_new(void *sd_state) {
+    sd_t *s = (sd_t *)sd_state;
+    if (!s) { qt_seterr("sd_stream_new: null decoder state"); return NULL; }
+    sds_t *q = (sds_t *)calloc(1, sizeof *q);
+    if (!q) { qt_seterr("sd_stream_new: out of host memory"); return NULL; }
+    q->sd = s;
+    const int n = SDS_CAP;
+    int bad = 0;
+    bad |= sds_buf(q, &q->V, 2, n, 512);
+    for (int l = 0; l < 8; l++) bad |= sds_buf(q, &q->Q[l], SDS_KH, n, 3072);
+    bad |= sds_buf(q, &q->U[0], 6, 2 * n, 1024);
+    bad |= sds_buf(q, &q->U[1], 6, 4 * n, 1024);
+    bad |= sds_buf(q, &q->I, 6, 4 * n, 1024);
+    bad |= sds_buf(q, &q->C0, 1, 4 * n, 1536);
+    int T = 4 * n;
+    for (int b = 0; b < 4; b++) {
+        T *= UP_RATE[b];
+        bad |= sds_buf(q, &q->S[b], b < 3 ? 1 : 6, T, UP_CH[b]);
+        for (int u = 0; u < 3; u++) bad |= sds_buf(q, &q->F1[b][u], 6 * DIL[u], T, UP_CH[b]);
+    }
+    const size_t sz[] = {(size_t)n * 512, (size_t)n * 1024, (size_t)n * 512, (size_t)n * 512, (size_t)n * 1024, (size_t)n * 2048,
+                         (size_t)n * 1024, (size_t)n * 1024, (size_t)2 * n * 1024, (size_t)4 * n * 1024,
+                         (size_t)4 * n * 4096, (size_t)T * 96};
+    float **ws[] = {&q->E, &q->P, &q->Hh, &q->XN, &q->A, &q->GU, &q->M, &q->LAT, &q->CN0, &q->D, &q->PW, &q->F2};
+    for (size_t i = 0; i < sizeof ws / sizeof ws[0]; i++) if (!(*ws[i] = sds_alloc(q, sz[i]))) bad = 1;
+    if (!(q->daudio = sds_alloc(q, (size_t)n * SD_SPF))) bad = 1;
+    if (hipMalloc((void **)&q->dcodes, (size_t)n * 16 * sizeof(int)) != hipSuccess) bad = 1;
+    if (bad) { qt_seterr("sd_stream_new: out of device memory"); qwen_hip_sd_stream_free(q); return NULL; }
+    if (qwen_hip_sd_stream_reset(q)) { qwen_hip_sd_stream_free(q); return NULL; }
+    return q;
+}
+
+static hipError_t sds_gemm(const sd_t *s, const sd_conv_t *c, const float *X, int xlo, int T, float *Y, int epi,
+                           const float *cscale, const float *R, const sd_snake_t *sn, float *Y2) {
+    int e = epi | (c->b ? SD_BIAS : 0);
+    if (sn) e |= Y2 ? SD_SNAKE2 : SD_SNAKE;
+    return qt_launch_sd_gemm(X, c->K, T, xlo, c->w, c->K, c->N, c->ntap, c->off, c->phases, T, Y, c->N, c->b, cscale, R,
+                             sn ? sn->a : NULL, sn ? sn->ib : NULL, Y2, e, 0, s->st);
+}
+
+/* one chunk of n <= SDS_CAP frames: codes already in q->dcodes, audio into q->daudio */
+static int sds_chunk(sds_t *q, int n) {
+    sd_t *s = q->sd;
+    const hipStream_t st = s->st;
+    const int fb = q->frames;
+    SCK(qt_launch_sd_vq(q->dcodes, s->cb, q->E, n, SD_CBSIZE, st));
+    SCK(sds_gemm(s, &s->vq, q->E, 0, n, sds_new_rows(&q->V), 0, NULL, NULL, NULL, NULL));
+    SCK(sds_gemm(s, &s->pre, sds_new_rows(&q->V), -q->V.H, n, q->P, 0, NULL, NULL, NULL, NULL));
+    SCK(sds_gemm(s, &s->inp, q->P, 0, n, q->Hh, 0, NULL, NULL, NULL, NULL));
+    const int kh = fb < SDS_KH ? fb : SDS_KH;
+    for (int l = 0; l < 8; l++) {
+        const sd_layer_t *y = &s->L[l];
+        SCK(qt_launch_sd_rmsnorm(q->Hh, y->n1, q->XN, n, 512, 1e-5f, st));
+        SCK(sds_gemm(s, &y->qkv, q->XN, 0, n, sds_new_rows(&q->Q[l]), 0, NULL, NULL, NULL, NULL));
+        SCK(qt_launch_sd_rope(q->Q[l].p, s->rope_c, s->rope_s, n, SDS_KH, fb, st));
+        SCK(qt_launch_sd_attn(q->Q[l].p, q->A, n, SDS_KH, SDS_KH - kh, 72, 0.125f, st));
+        SCK(sds_gemm(s, &y->o, q->A, 0, n, q->Hh, SD_CSCALE | SD_RESID, y->ls1, q->Hh, NULL, NULL));
+        SCK(qt_launch_sd_rmsnorm(q->Hh, y->n2, q->XN, n, 512, 1e-5f, st));
+        SCK(sds_gemm(s, &y->gu, q->XN, 0, n, q->GU, 0, NULL, NULL, NULL, NULL));
+        SCK(qt_launch_sd_swiglu(q->GU, q->M, n, 1024, st));
+        SCK(sds_gemm(s, &y->dn, q->M, 0, n, q->Hh, SD_CSCALE | SD_RESID, y->ls2, q->Hh, NULL, NULL));
+    }
+    SCK(qt_launch_sd_rmsnorm(q->Hh, s->fnorm, q->XN, n, 512, 1e-5f, st));
+    SCK(sds_gemm(s, &s->outp, q->XN, 0, n, q->LAT, 0, NULL, NULL, NULL, NULL));
+    /* ConvNeXt upsamplers (the transposed convs look back 0 rows, the depthwise convs 6) */
+    int T = n;
+    const float *cin = q->LAT;
+    for (int b = 0; b < 2; b++) {
+        float *up = sds_new_rows(&q->U[b]);
+        float *out = b == 0 ? q->CN0 : sds_new_rows(&q->I);
+        SCK(sds_gemm(s, &s->cn[b].up, cin, 0, T, up, 0, NULL, NULL, NULL, NULL));
+        T *= 2;
+        SCK(qt_launch_sd_dwln(up, s->cn[b].dw, s->cn[b].db, s->cn[b].lw, s->cn[b].lb, q->D, T, 1024, -q->U[b].H, st));
+        SCK(sds_gemm(s, &s->cn[b].pw1, q->D, 0, T, q->PW, SD_GELU, NULL, NULL, NULL, NULL));
+        SCK(sds_gemm(s, &s->cn[b].pw2, q->PW, 0, T, out, SD_CSCALE | SD_RESID, s->cn[b].gamma, up, NULL, NULL));
+        cin = out;
+    }
+    /* initial conv (6 rows back), output through block 1's input snake */
+    SCK(sds_gemm(s, &s->init, sds_new_rows(&q->I), -q->I.H, T, sds_new_rows(&q->C0), 0, NULL, NULL, &s->blk[0].s, NULL));
+    const sds_buf_t *in = &q->C0;
+    for (int b = 0; b < 4; b++) {
+        const int r = UP_RATE[b];
+        float *sig = sds_new_rows(&q->S[b]);
+        SCK(sds_gemm(s, &s->blk[b].up, sds_new_rows(in), -in->H, T, sig, 0, NULL, NULL, &s->blk[b].r[0].s1,
+                     sds_new_rows(&q->F1[b][0])));
+        T *= r;
+        for (int u = 0; u < 3; u++) {
+            SCK(sds_gemm(s, &s->blk[b].r[u].c1, sds_new_rows(&q->F1[b][u]), -q->F1[b][u].H, T, q->F2, 0, NULL, NULL,
+                         &s->blk[b].r[u].s2, NULL));
+            if (u < 2)
+                SCK(sds_gemm(s, &s->blk[b].r[u].c2, q->F2, 0, T, sig, SD_RESID, NULL, sig, &s->blk[b].r[u + 1].s1,
+                             sds_new_rows(&q->F1[b][u + 1])));
+            else
+                SCK(sds_gemm(s, &s->blk[b].r[u].c2, q->F2, 0, T, sig, SD_RESID, NULL, sig, b < 3 ? &s->blk[b + 1].s : &s->fs,
+                             NULL));
+        }
+        in = &q->S[b];
+    }
+    SCK(qt_launch_sd_final(sds_new_rows(&q->S[3]), s->fw, s->fb, q->daudio, T, 96, -q->S[3].H, st));
+    /* histories for the next chunk: each buffer's last H rows (of H + its rows this chunk) */
+    SCK(qt_launch_sd_shift(q->V.p, q->V.H, n, 512, st));
+    for (int l = 0; l < 8; l++) SCK(qt_launch_sd_shift(q->Q[l].p, SDS_KH, n, 3072, st));
+    SCK(qt_launch_sd_shift(q->U[0].p, q->U[0].H, 2 * n, 1024, st));
+    SCK(qt_launch_sd_shift(q->U[1].p, q->U[1].H, 4 * n, 1024, st));
+    SCK(qt_launch_sd_shift(q->I.p, q->I.H, 4 * n, 1024, st));
+    SCK(qt_launch_sd_shift(q->C0.p, q->C0.H, 4 * n, 1536, st));
+    T = 4 * n;
+    for (int b = 0; b < 4; b++) {
+        T *= UP_RATE[b];
+        SCK(qt_launch_sd_shift(q->S[b].p, q->S[b].H, T, UP_CH[b], st));
+        for (int u = 0; u < 3; u++) SCK(qt_launch_sd_shift(q->F1[b][u].p, q->F1[b][u].H, T, UP_CH[b], st));
+    }
+    q->frames += n;
+    return 0;
+}
+
+int qwen_hip_sd_stream_decode(void *state, const int *new_codes, int new_frames, float *audio_out, int max_samples) {
+    sds_t *q = (sds_t *)state;
+    if (!q || !new_codes || !audio_out) { qt_seterr("sd_stream_decode: null argument"); return -1; }
+    if (new_frames < 1 || q->frames + new_frames > SD_ROPE_POS) {
+        qt_seterr("sd_stream_decode: %d new frames after %d (at most %d in a stream)", new_frames, q->frames, SD_ROPE_POS);
+        return -1;
+    }
+    const long long ns = (long long)new_frames * SD_SPF;
+    if (max_samples < ns) { qt_seterr("sd_stream_decode: %d frames need %lld samples, buffer holds %d", new_frames, ns, max_samples); return -1; }
+    for (int off = 0; off < new_frames; off += SDS_CAP) {
+        const int n = new_frames - off < SDS_CAP ? new_frames - off : SDS_CAP;
+        SCK(hipMemcpyAsync(q->dcodes, new_codes + (size_t)off * 16, (size_t)n * 16 * sizeof(int), hipMemcpyHostToDevice,
+                           q->sd->st));
+        if (sds_chunk(q, n)) return -1;
+        SCK(hipMemcpyAsync(audio_out + (size_t)off * SD_SPF, q->daudio, (size_t)n * SD_SPF * sizeof(float),
+                           hipMemcpyDeviceToHost, q->sd->st));
+    }
+    SCK(hipStreamSynchronize(q->sd->st));
+    return (int)ns;
 }

@@ -39,7 +39,8 @@ EXPORTS = [
     "qwen_hip_generate", "qwen_hip_talker_load_file",
     "qwen_hip_sd_init", "qwen_hip_sd_load_file", "qwen_hip_sd_decode", "qwen_hip_sd_decode_device",
     "qwen_hip_sd_latent", "qwen_hip_sd_stream", "qwen_hip_sd_free", "qwen_hip_op_sd_conv",
-    "qwen_hip_op_sd_conv_transpose",
+    "qwen_hip_op_sd_conv_transpose", "qwen_hip_sd_stream_new", "qwen_hip_sd_stream_decode",
+    "qwen_hip_sd_stream_reset", "qwen_hip_sd_stream_free",
 ]
 
 SD_GET_FN = C.CFUNCTYPE(C.c_void_p, C.c_void_p, C.c_char_p, C.c_longlong)
@@ -173,6 +174,10 @@ def lib():
         L.qwen_hip_op_sd_conv.argtypes = [vp, vp, vp, vp, i, i, i, i, i, i]; L.qwen_hip_op_sd_conv.restype = i
         L.qwen_hip_op_sd_conv_transpose.argtypes = [vp, vp, vp, vp, i, i, i, i, i, i]
         L.qwen_hip_op_sd_conv_transpose.restype = i
+        L.qwen_hip_sd_stream_new.argtypes = [vp]; L.qwen_hip_sd_stream_new.restype = vp
+        L.qwen_hip_sd_stream_decode.argtypes = [vp, vp, i, vp, i]; L.qwen_hip_sd_stream_decode.restype = i
+        L.qwen_hip_sd_stream_reset.argtypes = [vp]; L.qwen_hip_sd_stream_reset.restype = i
+        L.qwen_hip_sd_stream_free.argtypes = [vp]
         _lib = L
     return _lib
 
@@ -393,6 +398,32 @@ class SpeechDecoder:
     def free(self):
         if self.h:
             lib().qwen_hip_sd_free(self.h)
+            self.h = None
+
+
+class SpeechDecoderStream:
+    """Streaming decode over a SpeechDecoder (qwen_hip_sd_stream_*): each call returns the
+    new frames' 1920 samples each."""
+
+    def __init__(self, dec):
+        self.h = lib().qwen_hip_sd_stream_new(dec.h)
+        if not self.h:
+            raise RuntimeError(f"sd stream init failed: {last_error()}")
+
+    def decode(self, codes):
+        codes = np.ascontiguousarray(codes, np.int32)
+        out = np.empty(codes.shape[0] * SD_SAMPLES_PER_FRAME, np.float32)
+        ns = lib().qwen_hip_sd_stream_decode(self.h, codes.ctypes.data, codes.shape[0], out.ctypes.data, out.size)
+        if ns < 0:
+            raise RuntimeError(f"sd_stream_decode failed: {last_error()}")
+        return out[:ns]
+
+    def reset(self):
+        check(lib().qwen_hip_sd_stream_reset(self.h), "sd_stream_reset")
+
+    def free(self):
+        if self.h:
+            lib().qwen_hip_sd_stream_free(self.h)
             self.h = None
 
 

@@ -166,3 +166,59 @@ def test_sd_glue_over_reference_ctx():
     assert got.shape == want.shape
     assert np.array_equal(got, _dec().decode(codes))                 # same weights -> same bits
     assert np.abs(got - want).max() <= 2e-2 and rel_l2(got, want) <= 1e-3
+
+
+@pytest.mark.parametrize("chunks", [[1, 2, 5, 3], [40, 1, 59], [7]])
+def test_sd_stream_equals_one_shot_bitwise(chunks):
+    """The streaming decode (qwen_hip_sd_stream_*, the reference's exact streaming contract,
+    sd.c:2313-2339) returns each chunk's own samples, and the concatenation equals the
+    one-shot decode of all frames bit for bit: chunking changes which rows a kernel computes,
+    never the order of any sum.  [40, 1, 59] crosses the 72-frame attention window and the
+    32-frame internal chunk."""
+    n = sum(chunks)
+    print(f"[case] sd stream chunks {chunks}", flush=True)
+    codes = sd_codes(n, 900 + n)
+    d = _dec()
+    whole = d.decode(codes)
+    st = hip.SpeechDecoderStream(d)
+    parts, off = [], 0
+    for c in chunks:
+        a = st.decode(codes[off:off + c])
+        assert a.shape == (1920 * c,)
+        parts.append(a)
+        off += c
+    got = np.concatenate(parts)
+    st.reset()
+    again = np.concatenate([st.decode(codes[:chunks[0]])] + ([st.decode(codes[chunks[0]:])] if len(chunks) > 1 else []))
+    st.free()
+    assert np.array_equal(got.view(np.uint32), whole.view(np.uint32))
+    assert np.array_equal(again.view(np.uint32), whole.view(np.uint32))
+
+
+@need_ref
+def test_sd_stream_matches_reference_streaming():
+    """Against the reference's own streaming decode over the same chunks (its exact path,
+    per-conv tails and a KV cache)."""
+    from oracle.oracle import RefSpeechDecoder
+    path, _ = sd_model()
+    codes = sd_codes(6, 31)
+    chunks = [codes[:2], codes[2:3], codes[3:]]
+    want = RefSpeechDecoder(path, threads=8).stream_decode(chunks)
+    st = hip.SpeechDecoderStream(_dec())
+    got = np.concatenate([st.decode(c) for c in chunks])
+    st.free()
+    err, r = float(np.abs(got - want).max()), rel_l2(got, want)
+    print(f"[result] sd stream vs reference stream: max-abs {err:.2e}, rel-L2 {r:.2e}")
+    assert err <= 2e-2 and r <= 1e-3, (err, r)
+
+
+def test_sd_stream_rejects_bad_arguments():
+    L = hip.lib()
+    st = hip.SpeechDecoderStream(_dec())
+    codes = sd_codes(2, 2)
+    out = np.empty(1920 * 2, np.float32)
+    assert L.qwen_hip_sd_stream_decode(st.h, codes.ctypes.data, 0, out.ctypes.data, out.size) == -1
+    assert L.qwen_hip_sd_stream_decode(st.h, codes.ctypes.data, 2, out.ctypes.data, out.size - 1) == -1
+    assert not L.qwen_hip_sd_stream_new(None)
+    assert st.decode(codes).shape == (3840,)                     # the state stays usable
+    st.free()
