@@ -216,40 +216,57 @@ __global__ __launch_bounds__(QT_BG_MAXW * 64) void k_bgemm_i8(QtBgArgs a) {
 }
 
 // ---- int8 weights x activation pieces, tall tiles and split K --------------------------
-// The batched step's projections have 2048-12288 rows; at 16 rows per workgroup the
-// 2048-row ones fill half the CUs, and each B fragment (1 KiB of pieces from L2) serves
-// one 16-row MFMA tile, so the pieces traffic is ~6x the weight bytes.  Here a
-// workgroup (4 waves, one per SIMD, so a lane may hold 512 registers) owns RT row tiles
-// (16*RT rows) and one of S equal K ranges; wave w takes KB k-blocks of 64 of that range,
-// holds all its weight fragments in registers from the start (RT*KB*16 bytes per lane in
-// flight), streams its B fragments one k-block ahead, and feeds each B fragment to the
-// RT row tiles.  The waves' int32 tiles are summed in LDS (exact).  With S > 1 each
-// workgroup publishes its exact int32 tile (agent-scope stores), counts itself in with a
-// device-scope atomic, and the last of the S workgroups of a row group adds the others'
-// tiles (integer sums: the order cannot change the result) and runs the epilogue, then
-// re-arms the counter for the next call.  (Issuing every B fragment at entry as well,
-// with 8 waves of 256 columns, measured slower: 3.85 against 3.76 ms per batched step.)
-#define QT_B2_W 4
+// The batched step's projections have 2048-12288 rows and K = 1024..6144.  A workgroup
+// of QT_B2_W waves owns RT row tiles (16*RT rows) and one of S equal K ranges; wave w
+// takes KB consecutive k-blocks of 64 of that range.  Every weight fragment and every B
+// fragment of the wave is issued at entry (all of a workgroup's HBM and L2 traffic in
+// flight at once: one memory latency, not one per k-block), together with the
+// epilogue's operands (row scales, stream scales, the residual rows), so the only
+// dependent round trip left is the split-K hand-off.  Each B fragment feeds the RT row
+// tiles.  After the MFMAs each wave parks its int32 tiles in LDS; one barrier; then
+// each thread sums, over the waves, the three plane sums of the outputs it writes and
+// folds them into one exact integer T = C1*2^14 + C2*2^7 + C3 (|T| < 2^42), so that
+// s * (C1 + C2/128 + C3/16384) = s * T * 2^-14 is formed exactly in f64 and rounded
+// once, as in k_bgemm_i8.  With S > 1 each workgroup publishes its T values (agent-scope
+// stores), counts itself in with a device-scope atomic, and the last of the S
+// workgroups of a row group adds the others' T (integers: the order cannot change the
+// result; all of its loads are issued before any is added) and writes the outputs, then
+// re-arms the counter for the next call.  Outputs of one workgroup are numbered
+// unit u = b * NRU + q (stream b, row q; SwiGLU: row pair q), so consecutive threads
+// write consecutive rows of one stream.
+#define QT_B2_W 8
 struct QtBg2Args {
     const uint8_t *w; const float *scale;
     int rows, K;
     const int8_t *P; const float *S;
     int B;
     float *out; long long ostride;
-    int *part;          // S > 1: [gridDim.x][S][RT*NT*256] int32
+    long long *part;    // S > 1: [gridDim.x][S][units][1 or 2] exact sums
     unsigned *cnt;      // S > 1: [gridDim.x], zero between calls
 };
 
+// registers of a (NT, RT, KB) wave: B fragments, weight fragments, accumulators
+__host__ __device__ constexpr int qt_b2_regs(int nt, int rt, int kb) { return 4 * (kb * nt + rt * kb + rt * nt); }
+// LDS row of 64 ints (one accumulator register of a 16x16 tile) padded to 68, so the
+// sums that read the same register of 16 consecutive rows hit 16 different banks
+#define QT_B2_ROW 68
+__host__ __device__ constexpr bool qt_b2_ok(int nt, int rt, int kb) {
+    return qt_b2_regs(nt, rt, kb) <= 220 && QT_B2_W * rt * nt * 4 * QT_B2_ROW * 4 <= 159 * 1024;
+}
+
 template <int NT, int EPI, int RT, int KB>
 __global__ __launch_bounds__(QT_B2_W * 64) void k_bgemm2_i8(QtBg2Args a) {
-    constexpr int BP = NT * 16 / 3;
-    constexpr int TILE = RT * NT * 256;               // ints of one workgroup tile
-    __shared__ int red[RT][NT][4][64];
+    constexpr int BP = NT * 16 / 3, NTH = QT_B2_W * 64, NR = 16 * RT;
+    constexpr int TILE = RT * NT * 4 * QT_B2_ROW;     // ints of one wave's tiles (padded rows)
+    constexpr bool SW = EPI == QT_EPI_SWIGLU;
+    constexpr int NRU = SW ? NR / 2 : NR;             // output rows (SwiGLU: row pairs)
+    constexpr int NU = NRU * BP, PU = (NU + NTH - 1) / NTH, H = SW ? 2 : 1;
+    __shared__ int wred[QT_B2_W][TILE];
     __shared__ unsigned last_flag;
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int m = lane & 15, grp = lane >> 4;
     const int x = blockIdx.x, z = blockIdx.y, S = gridDim.y;
-    const int r0 = x * 16 * RT;
+    const int r0 = x * NR;
     const int kw0 = z * (a.K / S) + wave * KB * 64;
     const size_t cs = (size_t)3 * BP * 64;
 
@@ -260,53 +277,74 @@ __global__ __launch_bounds__(QT_B2_W * 64) void k_bgemm2_i8(QtBg2Args a) {
 #pragma unroll
         for (int kb = 0; kb < KB; kb++) wa[rt][kb] = *reinterpret_cast<const uint4 *>(wr + kb * 64);
     }
+    const int8_t *pbase = a.P + (size_t)(kw0 >> 6) * cs + (size_t)m * 64 + grp * 16;
+    uint4 bv[KB][NT];
+#pragma unroll
+    for (int kb = 0; kb < KB; kb++)
+#pragma unroll
+        for (int t = 0; t < NT; t++) bv[kb][t] = *reinterpret_cast<const uint4 *>(pbase + (size_t)kb * cs + (size_t)t * 16 * 64);
+    // epilogue operands of this thread's units
+    float e_sc[PU][H], e_S[PU], e_res[PU];
+#pragma unroll
+    for (int u = 0; u < PU; u++) {
+        const int j = tid + u * NTH, b = j / NRU, r = r0 + (SW ? 2 : 1) * (j % NRU);
+        const bool ok = j < NU && b < a.B && r < a.rows;
+#pragma unroll
+        for (int h = 0; h < H; h++) e_sc[u][h] = ok ? a.scale[r + h] : 0.f;
+        e_S[u] = ok ? a.S[b] : 0.f;
+        e_res[u] = (ok && EPI == QT_EPI_RESID) ? a.out[(size_t)b * a.ostride + r] : 0.f;
+    }
     qt_v4i acc[RT][NT];
 #pragma unroll
     for (int rt = 0; rt < RT; rt++)
 #pragma unroll
         for (int t = 0; t < NT; t++) acc[rt][t] = qt_v4i{0, 0, 0, 0};
-    const int8_t *pbase = a.P + (size_t)(kw0 >> 6) * cs + (size_t)m * 64 + grp * 16;
-    auto loadB = [&](qt_v4i (&Bv)[NT], int kb) {
 #pragma unroll
-        for (int t = 0; t < NT; t++) {
-            const uint4 pv = *reinterpret_cast<const uint4 *>(pbase + (size_t)kb * cs + (size_t)t * 16 * 64);
-            Bv[t] = qt_v4i{(int)pv.x, (int)pv.y, (int)pv.z, (int)pv.w};
-        }
-    };
-    qt_v4i Bb0[NT], Bb1[NT];
-    loadB(Bb0, 0);
-#pragma unroll
-    for (int kb = 0; kb < KB; kb++) {
-        if (kb + 1 < KB) {
-            if (kb & 1) loadB(Bb0, kb + 1);
-            else loadB(Bb1, kb + 1);
-        }
+    for (int kb = 0; kb < KB; kb++)
 #pragma unroll
         for (int rt = 0; rt < RT; rt++) {
             const qt_v4i A = qt_v4i{(int)wa[rt][kb].x, (int)wa[rt][kb].y, (int)wa[rt][kb].z, (int)wa[rt][kb].w};
 #pragma unroll
             for (int t = 0; t < NT; t++)
-                acc[rt][t] = __builtin_amdgcn_mfma_i32_16x16x64_i8(A, (kb & 1) ? Bb1[t] : Bb0[t], acc[rt][t], 0, 0, 0);
+                acc[rt][t] = __builtin_amdgcn_mfma_i32_16x16x64_i8(
+                    A, qt_v4i{(int)bv[kb][t].x, (int)bv[kb][t].y, (int)bv[kb][t].z, (int)bv[kb][t].w}, acc[rt][t], 0, 0, 0);
         }
-        __builtin_amdgcn_sched_barrier(0);
-    }
-    for (int w = 0; w < QT_B2_W; w++) {
-        if (wave == w) {
 #pragma unroll
-            for (int rt = 0; rt < RT; rt++)
+    for (int rt = 0; rt < RT; rt++)
 #pragma unroll
-                for (int t = 0; t < NT; t++)
+        for (int t = 0; t < NT; t++)
 #pragma unroll
-                    for (int i = 0; i < 4; i++)
-                        red[rt][t][i][lane] = (w == 0 ? 0 : red[rt][t][i][lane]) + acc[rt][t][i];
+            for (int i = 0; i < 4; i++) wred[wave][((rt * NT + t) * 4 + i) * QT_B2_ROW + lane] = acc[rt][t][i];
+    __syncthreads();
+    // exact sums of this thread's outputs: D row 4(l/16)+i, column l%16 of tile (rt, t)
+    long long T[PU][H];
+#pragma unroll
+    for (int u = 0; u < PU; u++) {
+        const int j = tid + u * NTH, b = j / NRU, q = j % NRU;
+#pragma unroll
+        for (int h = 0; h < H; h++) {
+            long long v = 0;
+            if (j < NU) {
+                const int rr = (SW ? 2 : 1) * q + h, rt = rr >> 4, lr = rr & 15;
+                const int e = ((rt * NT + (b >> 4)) * 4 + (lr & 3)) * QT_B2_ROW + (lr >> 2) * 16 + (b & 15);
+                int c[3] = {0, 0, 0};
+#pragma unroll
+                for (int w = 0; w < QT_B2_W; w++)
+#pragma unroll
+                    for (int p = 0; p < 3; p++) c[p] += wred[w][e + p * (BP / 16) * 4 * QT_B2_ROW];
+                v = (long long)c[0] * 16384 + (long long)c[1] * 128 + (long long)c[2];
+            }
+            T[u][h] = v;
         }
-        __syncthreads();
     }
-    int *flat = &red[0][0][0][0];
     if (S > 1) {
-        int *mine = a.part + ((size_t)x * S + z) * TILE;
-        for (int i = tid; i < TILE; i += QT_B2_W * 64)
-            __hip_atomic_store(mine + i, flat[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        long long *mine = a.part + ((size_t)x * S + z) * NU * H;
+#pragma unroll
+        for (int u = 0; u < PU; u++)
+#pragma unroll
+            for (int h = 0; h < H; h++)
+                if (tid + u * NTH < NU)
+                    __hip_atomic_store(mine + (size_t)(tid + u * NTH) * H + h, T[u][h], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         __builtin_amdgcn_s_waitcnt(0);
         __syncthreads();
         if (tid == 0)
@@ -316,56 +354,92 @@ __global__ __launch_bounds__(QT_B2_W * 64) void k_bgemm2_i8(QtBg2Args a) {
         if (!last_flag) return;
         for (int zz = 0; zz < S; zz++) {
             if (zz == z) continue;
-            const int *other = a.part + ((size_t)x * S + zz) * TILE;
-            for (int i = tid; i < TILE; i += QT_B2_W * 64)
-                flat[i] += __hip_atomic_load(other + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            const long long *other = a.part + ((size_t)x * S + zz) * NU * H;
+            long long t[PU][H];
+#pragma unroll
+            for (int u = 0; u < PU; u++)
+#pragma unroll
+                for (int h = 0; h < H; h++)
+                    t[u][h] = (tid + u * NTH < NU)
+                                  ? __hip_atomic_load(other + (size_t)(tid + u * NTH) * H + h, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+                                  : 0;
+#pragma unroll
+            for (int u = 0; u < PU; u++)
+#pragma unroll
+                for (int h = 0; h < H; h++) T[u][h] += t[u][h];
         }
-        __syncthreads();
         if (tid == 0) __hip_atomic_store(&a.cnt[x], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
-    // epilogue: thread j -> stream b = j / (16 RT), local row rl = j % (16 RT), so
-    // consecutive threads write consecutive rows of one stream
-    constexpr int NR = 16 * RT;
-    for (int j = tid; j < NR * BP; j += QT_B2_W * 64) {
-        const int b = j / NR, rl = j % NR, r = r0 + rl;
-        if (b >= a.B || r >= a.rows) continue;
-        if (EPI == QT_EPI_SWIGLU && (rl & 1)) continue;
-        auto val = [&](int rr) -> float {   // rr: local row
-            const int rt = rr >> 4, lr = rr & 15;
-            const int t0 = b >> 4, ln = (lr >> 2) * 16 + (b & 15), i = lr & 3;
-            const double c = (double)red[rt][t0][i][ln] + (double)red[rt][t0 + BP / 16][i][ln] * (1.0 / 128.0) +
-                             (double)red[rt][t0 + 2 * BP / 16][i][ln] * (1.0 / 16384.0);
-            const float dot = (float)(c * (double)a.S[b]);
-            return __fmul_rn(dot, a.scale[r0 + rr]);
-        };
-        float *ob = a.out + (size_t)b * a.ostride;
-        if (EPI == QT_EPI_STORE) ob[r] = val(rl);
-        else if (EPI == QT_EPI_RESID) ob[r] = __fadd_rn(ob[r], val(rl));
-        else if (EPI == QT_EPI_SWIGLU) {
-            const float g = val(rl), u = val(rl + 1);
-            ob[r >> 1] = g / (1.0f + expf(-g)) * u;
+#pragma unroll
+    for (int u = 0; u < PU; u++) {
+        const int j = tid + u * NTH, b = j / NRU, r = r0 + (SW ? 2 : 1) * (j % NRU);
+        if (j >= NU || b >= a.B || r >= a.rows) continue;
+        float y[H];
+#pragma unroll
+        for (int h = 0; h < H; h++) {
+            const float dot = (float)((double)T[u][h] * 0x1p-14 * (double)e_S[u]);
+            y[h] = __fmul_rn(dot, e_sc[u][h]);
         }
+        float *ob = a.out + (size_t)b * a.ostride;
+        if (EPI == QT_EPI_STORE) ob[r] = y[0];
+        else if (EPI == QT_EPI_RESID) ob[r] = __fadd_rn(e_res[u], y[0]);
+        else ob[r >> 1] = y[0] / (1.0f + expf(-y[0])) * y[H - 1];
     }
 }
 
 // The tiling qt_launch_bgemm2_i8 uses for a (rows, K) projection: KB k-blocks per wave,
-// S K ranges, RT row tiles per workgroup.  Returns 0 if the shape has none (K not a
-// multiple of 1024), else fills the workspace it needs (ints of partial tiles and
-// counters; 0 when S == 1).
+// S K ranges, RT row tiles per workgroup.  KB is the largest of {6, 4, 2} dividing
+// K/512 whose fragments fit the register budget; K ranges are split further (KB 4 -> 2,
+// 6 -> 2) while fewer than 128 workgroups would run; RT grows to 3 while more than 256
+// row-tile jobs remain per full grid and the registers and LDS allow.  Returns 0 if the
+// shape has none (K not a multiple of 1024, or no NT for Bp), else fills the workspace
+// it needs (ints of the split-K sums and counters; 0 when S == 1).
 extern "C" int qt_bgemm2_plan(int rows, int K, int Bp, int *kb, int *S, int *rt, size_t *part_ints, int *n_cnt) {
-    int KB, SS;
-    if (K % 2048 == 0) { KB = 8; SS = K / 2048; }
-    else if (K % 1024 == 0) { KB = 4; SS = K / 1024; }
-    else return 0;
+    if (rows <= 0 || K <= 0 || K % 1024 || (Bp != 16 && Bp != 32 && Bp != 48 && Bp != 64)) return 0;
+    const int NT = 3 * Bp / 16, nblk = K / 512;
+    int KB = 0;
+    const int cand[3] = {6, 4, 2};
+    for (int i = 0; i < 3 && !KB; i++)
+        if (nblk % cand[i] == 0 && qt_b2_ok(NT, 1, cand[i])) KB = cand[i];
+    if (!KB) return 0;
+    int SS = nblk / KB;
     const int tiles = (rows + 15) / 16;
-    if (KB == 8 && tiles * SS < 256) { KB = 4; SS *= 2; }
+    if (tiles * SS < 128 && KB > 2) { SS *= KB / 2; KB = 2; }
     int RT = tiles * SS / 256;
     RT = RT < 1 ? 1 : RT > 3 ? 3 : RT;
+    while (RT > 1 && !qt_b2_ok(NT, RT, KB)) RT--;
     const int gx = (tiles + RT - 1) / RT;
     *kb = KB; *S = SS; *rt = RT;
-    *part_ints = SS > 1 ? (size_t)gx * SS * RT * (3 * Bp / 16) * 256 : 0;
+    *part_ints = SS > 1 ? (size_t)gx * SS * 16 * RT * Bp * 2 : 0;
     *n_cnt = SS > 1 ? gx : 0;
     return 1;
+}
+
+template <int NT, int E, int RT, int KB>
+static void qt_b2_go(const QtBg2Args &a, dim3 grid, hipStream_t st, hipError_t &err) {
+    if constexpr (qt_b2_ok(NT, RT, KB))
+        hipLaunchKernelGGL((k_bgemm2_i8<NT, E, RT, KB>), grid, dim3(QT_B2_W * 64), 0, st, a);
+    else
+        err = hipErrorInvalidValue;
+}
+template <int NT, int E, int RT>
+static void qt_b2_kb(int KB, const QtBg2Args &a, dim3 grid, hipStream_t st, hipError_t &err) {
+    if (KB == 6) qt_b2_go<NT, E, RT, 6>(a, grid, st, err);
+    else if (KB == 4) qt_b2_go<NT, E, RT, 4>(a, grid, st, err);
+    else qt_b2_go<NT, E, RT, 2>(a, grid, st, err);
+}
+template <int NT, int E>
+static void qt_b2_rt(int RT, int KB, const QtBg2Args &a, dim3 grid, hipStream_t st, hipError_t &err) {
+    if (RT == 1) qt_b2_kb<NT, E, 1>(KB, a, grid, st, err);
+    else if (RT == 2) qt_b2_kb<NT, E, 2>(KB, a, grid, st, err);
+    else qt_b2_kb<NT, E, 3>(KB, a, grid, st, err);
+}
+template <int NT>
+static void qt_b2_epi(int epi, int RT, int KB, const QtBg2Args &a, dim3 grid, hipStream_t st, hipError_t &err) {
+    if (epi == QT_EPI_STORE) qt_b2_rt<NT, QT_EPI_STORE>(RT, KB, a, grid, st, err);
+    else if (epi == QT_EPI_RESID) qt_b2_rt<NT, QT_EPI_RESID>(RT, KB, a, grid, st, err);
+    else if (epi == QT_EPI_SWIGLU) qt_b2_rt<NT, QT_EPI_SWIGLU>(RT, KB, a, grid, st, err);
+    else err = hipErrorInvalidValue;
 }
 
 // part / cnt: workspace from qt_bgemm2_plan (cnt zeroed once at allocation; the kernel
@@ -379,23 +453,14 @@ extern "C" hipError_t qt_launch_bgemm2_i8(int epi, const uint8_t *w, const float
     if (SS > 1 && (!part || !cnt)) return hipErrorInvalidValue;
     QtBg2Args a;
     a.w = w; a.scale = scale; a.rows = rows; a.K = K; a.P = P; a.S = S; a.B = B; a.out = out; a.ostride = ostride;
-    a.part = part; a.cnt = cnt;
-    const dim3 grid(((rows + 15) / 16 + RT - 1) / RT, SS), block(QT_B2_W * 64);
-#define QT_B2_GO(NT_, E_, RT_, KB_) hipLaunchKernelGGL((k_bgemm2_i8<NT_, E_, RT_, KB_>), grid, block, 0, st, a)
-#define QT_B2_KB(NT_, E_, RT_) if (KB == 8) QT_B2_GO(NT_, E_, RT_, 8); else QT_B2_GO(NT_, E_, RT_, 4);
-#define QT_B2_RT(NT_, E_) if (RT == 1) { QT_B2_KB(NT_, E_, 1) } else if (RT == 2) { QT_B2_KB(NT_, E_, 2) } else { QT_B2_KB(NT_, E_, 3) }
-#define QT_B2_EPI(NT_) if (epi == QT_EPI_STORE) { QT_B2_RT(NT_, QT_EPI_STORE) } \
-    else if (epi == QT_EPI_RESID) { QT_B2_RT(NT_, QT_EPI_RESID) } \
-    else if (epi == QT_EPI_SWIGLU) { QT_B2_RT(NT_, QT_EPI_SWIGLU) } else return hipErrorInvalidValue;
-    if (Bp == 16) { QT_B2_EPI(3) }
-    else if (Bp == 32) { QT_B2_EPI(6) }
-    else if (Bp == 48) { QT_B2_EPI(9) }
-    else if (Bp == 64) { QT_B2_EPI(12) }
-    else return hipErrorInvalidValue;
-#undef QT_B2_EPI
-#undef QT_B2_RT
-#undef QT_B2_KB
-#undef QT_B2_GO
+    a.part = reinterpret_cast<long long *>(part); a.cnt = cnt;
+    const dim3 grid(((rows + 15) / 16 + RT - 1) / RT, SS);
+    hipError_t err = hipSuccess;
+    if (Bp == 16) qt_b2_epi<3>(epi, RT, KB, a, grid, st, err);
+    else if (Bp == 32) qt_b2_epi<6>(epi, RT, KB, a, grid, st, err);
+    else if (Bp == 48) qt_b2_epi<9>(epi, RT, KB, a, grid, st, err);
+    else qt_b2_epi<12>(epi, RT, KB, a, grid, st, err);
+    if (err != hipSuccess) return err;
     return hipGetLastError();
 }
 
