@@ -48,7 +48,7 @@ struct QtAttnArgs {
 };
 
 #define QT_KVB 128   // keys of a chunk staged in LDS at once
-#define QT_B_MIN_CHUNK 512   // batched step: minimum keys per chunk
+#define QT_B_MIN_CHUNK 384   // batched step: minimum keys per chunk
 
 // 16 bytes per lane from global memory straight into LDS (global_load_lds_dwordx4):
 // lane i's bytes land at dst + 16*i, dst wave-uniform.  Counted by vmcnt like a load.
@@ -85,27 +85,30 @@ __global__ __launch_bounds__(QT_WG) void k_attn(QtAttnArgs a) {
     const bool append = PREP && (pos >= j0 && pos < j0 + n);
 
     constexpr int PS = 2 + QT_HD;
-    constexpr int KVBYTES = 2 * QT_KVB * QT_HD * 2, MBYTES = QT_ATT_G * HPK * PS * 4;
-    static_assert(QT_WAVES * 32 == QT_KVB, "each wave takes two 16-key tiles of a block");
+    // keys staged per block: BATCH halves the block (half the LDS, so four workgroups
+    // share a CU and hide each other's block chains); !BATCH keeps the fused step's block
+    constexpr int KVB = BATCH ? QT_KVB / 2 : QT_KVB;
+    constexpr int KVBYTES = 2 * KVB * QT_HD * 2, MBYTES = QT_ATT_G * HPK * PS * 4;
+    static_assert(KVB % 32 == 0 && KVB <= QT_WAVES * 32, "each wave scores at most one 32-key tile of a block");
     __shared__ __align__(16) uint16_t qp[16][QT_HD];            // query pieces, row 4h+p (qt_attn_mf.h)
-    __shared__ __align__(16) uint16_t pp[16][QT_KVB];           // probability pieces of a block (k-tile w: wave w)
+    __shared__ __align__(16) uint16_t pp[16][KVB];           // probability pieces of a block (k-tile w: wave w)
     __shared__ float ml[QT_WAVES][HPK][2];                      // per-k-tile (max, exp-sum)
     __shared__ __align__(16) uint16_t knew[QT_HD];
     __shared__ __align__(16) uint16_t vnew[QT_HD];
     // K rows, V rows of a key block; reused as the merge staging
     __shared__ __align__(16) uint16_t s_kvbuf[(KVBYTES > MBYTES ? KVBYTES : MBYTES) / 2];
-    uint16_t(*s_kv)[QT_KVB * QT_HD] = reinterpret_cast<uint16_t(*)[QT_KVB * QT_HD]>(s_kvbuf);
+    uint16_t(*s_kv)[KVB * QT_HD] = reinterpret_cast<uint16_t(*)[KVB * QT_HD]>(s_kvbuf);
     __shared__ int last_flag;
 
     const uint16_t *Kg = a.K + (long long)g * a.head_stride;
     const uint16_t *Vg = a.V + (long long)g * a.head_stride;
     const int sub = lane & 15, pg = lane >> 4;
 
-    // K and/or V rows of keys [kb, kb + min(QT_KVB, n - kb)) of the chunk into s_kv, in
+    // K and/or V rows of keys [kb, kb + min(KVB, n - kb)) of the chunk into s_kv, in
     // the swizzled slot order of qt_attn_mf.h (lane (pg, sub) fills slot sub of block row
     // 4i + pg); the appended key (PREP) is not read from memory, it comes from knew/vnew.
     auto stage = [&](int kb, bool doK, bool doV) {
-        const int nk = min(QT_KVB, n - kb);
+        const int nk = min(KVB, n - kb);
         const int ninst = (nk + 3) >> 2;
         for (int i = wave; i < ninst; i += QT_WAVES) {
             const int jl = i * 4 + pg, jj = kb + jl;
@@ -151,7 +154,7 @@ __global__ __launch_bounds__(QT_WG) void k_attn(QtAttnArgs a) {
                 knew[lane] = k0; knew[lane + 64] = k1;
                 vnew[lane] = v0; vnew[lane + 64] = v1;
                 const int r = pos - j0;            // its row in the first staged block
-                if (r < QT_KVB) {
+                if (r < KVB) {
                     s_kv[0][qt_kidx(r, lane)] = k0; s_kv[0][qt_kidx(r, lane + 64)] = k1;
                     s_kv[1][qt_vidx(r, lane)] = v0; s_kv[1][qt_vidx(r, lane + 64)] = v1;
                 }
@@ -162,8 +165,8 @@ __global__ __launch_bounds__(QT_WG) void k_attn(QtAttnArgs a) {
             qt_put_pieces(&qp[4 * (i / QT_HD)][i % QT_HD], QT_HD, a.q[(g * HPK + i / QT_HD) * QT_HD + i % QT_HD]);
     }
     qt_att_zero_rows<HPK>(&qp[0][0], QT_HD, tid, QT_WG);
-    qt_att_zero_rows<HPK>(&pp[0][0], QT_KVB, tid, QT_WG);
-    qt_att_zero_vrows(s_kv[1], min(QT_KVB, n), (min(QT_KVB, n) + 31) & ~31, tid, QT_WG);
+    qt_att_zero_rows<HPK>(&pp[0][0], KVB, tid, QT_WG);
+    qt_att_zero_vrows(s_kv[1], min(KVB, n), (min(KVB, n) + 31) & ~31, tid, QT_WG);
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();   // (also: every wave's LDS copies of the first block have landed)
 
@@ -172,9 +175,9 @@ __global__ __launch_bounds__(QT_WG) void k_attn(QtAttnArgs a) {
     const float scale2 = a.scale * QT_LOG2E;
     QtAttRun run;
     qt_att_run_init(run);
-    for (int kb = 0; kb < n; kb += QT_KVB) {
-        const int nk = min(QT_KVB, n - kb);
-        if (kb > 0) {   // chunks longer than one block (caches beyond G*QT_KVB keys)
+    for (int kb = 0; kb < n; kb += KVB) {
+        const int nk = min(KVB, n - kb);
+        if (kb > 0) {   // chunks longer than one block (caches beyond G*KVB keys)
             __syncthreads();
             stage(kb, true, true);
             __builtin_amdgcn_s_waitcnt(0);
@@ -184,10 +187,10 @@ __global__ __launch_bounds__(QT_WG) void k_attn(QtAttnArgs a) {
             __syncthreads();
         }
         if (32 * wave < nk)
-            qt_att_tiles<HPK>(&qp[0][0], s_kv[0], &pp[0][0], QT_KVB, &ml[0][0][0], wave, nk, scale2, lane);
+            qt_att_tiles<HPK>(&qp[0][0], s_kv[0], &pp[0][0], KVB, &ml[0][0][0], wave, nk, scale2, lane);
         __syncthreads();
         float o[2], M, l;
-        qt_att_pv_n<HPK>((nk + 31) >> 5, &pp[0][0], QT_KVB, &ml[0][0][0], s_kv[1], 32 * wave, lane, o, M, l);
+        qt_att_pv_n<HPK>((nk + 31) >> 5, &pp[0][0], KVB, &ml[0][0][0], s_kv[1], 32 * wave, lane, o, M, l);
         qt_att_run_add(run, o, M, l);
     }
     // lane: head pg, dims 32*wave + sub and + 16
@@ -302,11 +305,14 @@ extern "C" hipError_t qt_launch_attn(int prep, const float *q, const float *qn, 
 // B independent streams in one launch (the batched step): stream z uses q + z*q_bs,
 // K/V + z*kv_bs (its own cache), position d_pos[z], partials part + z*part_bs, counters
 // cnt + z*n_kv, output out + z*out_bs.  Ragged positions are fine: each stream's chunks
-// follow its own length.  Chunks hold at least QT_B_MIN_CHUNK keys (four LDS blocks):
-// short streams use few workgroups, fewer partials are merged, and the two workgroups
-// a CU holds overlap each other's block loads; throughput, not single-stream latency,
-// is what the batch needs (32 ragged streams of 128..4096 keys on MI355X: minimum
-// 128 keys 3.76 ms/step, 256 3.49, 512 3.43, 1024 3.58).
+// follow its own length.  Chunks hold at least QT_B_MIN_CHUNK keys (six 64-key LDS
+// blocks): short streams use few workgroups, fewer partials are merged, and the four
+// workgroups a CU holds overlap each other's block loads and block computations;
+// throughput, not single-stream latency, is what the batch needs.  Measured on the whole
+// batched step (32 ragged streams of 128..4096 keys, 1.7B int8, MI355X): 128-key blocks
+// with a minimum of 128 / 256 / 512 / 1024 keys 3.76 / 3.49 / 3.43 / 3.58 ms/step; 64-key
+// blocks with 256 / 320 / 384 / 448 / 512 / 768 / 1024: 3.16 / 3.13 / 3.13 / 3.22 / 3.24 /
+// 3.20 / 3.28 ms/step (the count of workgroups against the four slots per CU decides).
 extern "C" hipError_t qt_launch_attn_b(const float *q, long long q_bs, const float *qn, const float *kn,
                                        const float *rc, const float *rs, float eps, const int *d_pos,
                                        uint16_t *K, uint16_t *V, long long kv_bs, long long pos_stride,

@@ -9,8 +9,9 @@
 //   into three int8 planes with one power-of-two scale s = 2^(e-6), 2^e <= max|x| < 2^(e+1):
 //       x/s = p1 + p2*2^-7 + p3*2^-14 + e3,   p1 in [-128,127], p2,p3 in [0,127],
 //       0 <= e3 < 2^-14,
-//   every step (scale, floor, subtract, *128) exact in f32, so |x - s*(p1+p2/128+p3/16384)|
-//   < s*2^-14 <= max|x| * 2^-20.
+//   every step (scale, floor, subtract, *128) exact in f32 except y - floor(y) for y in
+//   (-1/2, 0), which can round by 2^-25 (and, within 2^-25 of 0, up to 1: planes 2 and 3 are
+//   held to 127), so |x - s*(p1+p2/128+p3/16384)| < s*(2^-14 + 2^-25) <= max|x| * 2^-19.9.
 //   Integer products.  v_mfma_i32_16x16x64_i8 accumulates q*p exactly in int32
 //   (|sum| <= 128*128*6144 < 2^31), so the three dot products C1, C2, C3 are exact and
 //   independent of summation order; y = s * (C1 + C2/128 + C3/16384) is formed in f64
@@ -114,10 +115,14 @@ __global__ __launch_bounds__(QT_BP_T) void k_bpieces(const float *x, long long x
         if (ok) {
             const float y = v[e] * isc;          // |y| < 128, exact
             const float f1 = floorf(y);
-            const float r1 = (y - f1) * 128.0f;  // [0, 128), exact
-            const float f2 = floorf(r1);
+            // y - f1 is exact for |y| >= 1 and for y >= 0; for y in (-1/2, 0) it can round,
+            // and for -2^-25 < y < 0 it rounds up to 1.0, which would make plane 2 128 (an
+            // int8 -128): planes 2 and 3 are held to 127, so p1 + 127/128 + 127/16384 =
+            // p1 + 1 - 2^-14 stands for such a y, still within 2^-14 of it
+            const float r1 = (y - f1) * 128.0f;  // [0, 128]
+            const float f2 = fminf(floorf(r1), 127.0f);
             const float r2 = (r1 - f2) * 128.0f;
-            const float f3 = floorf(r2);
+            const float f3 = fminf(floorf(r2), 127.0f);
             q1 = (int)f1; q2 = (int)f2; q3 = (int)f3;
         }
         const size_t o = (size_t)(k >> 6) * cs + (k & 63);

@@ -69,6 +69,27 @@ def test_op_matmat_int8_exact_inputs(oracle):
     assert np.array_equal(Y, exact.astype(np.float32))
 
 
+def test_op_matmat_int8_tiny_negative_activations(oracle):
+    """Activations just below zero next to O(1) ones (SwiGLU outputs of very negative
+    gates): y = x/s in (-2^-25, 0) makes y - floor(y) round up to 1.0 in f32, which once
+    turned piece plane 2 into 128 (an int8 -128, an error of 2s on that element).  Every
+    stream, and each of the four tall-tile / split-K plans (K = 1024, 2048, 3072, 6144),
+    against the f64 product."""
+    rng = np.random.default_rng(0x71C)
+    for rows, cols, B in [(64, 1024, 32), (256, 2048, 32), (128, 3072, 16), (2048, 6144, 32)]:
+        print(f"[case] matmat int8 tiny negatives {rows}x{cols} B={B}", flush=True)
+        w = synth.f32_to_bf16_rne((rng.standard_normal((rows, cols)) * 0.02).astype(np.float32))
+        q, s = oracle.quantize_int8(w)
+        X = rng.standard_normal((cols, B)).astype(np.float32)
+        tiny = rng.random((cols, B)) < 0.25
+        X[tiny] = -(rng.random(int(tiny.sum())) * 1e-9 + 1e-12).astype(np.float32)
+        Y = _matmat(q, s, X)
+        Y64 = (q.astype(np.float64) * s.astype(np.float64)[:, None]) @ X.astype(np.float64)
+        for j in range(B):
+            err = np.abs(Y[:, j] - Y64[:, j]).max() / np.abs(Y64[:, j]).max()
+            assert err < 1e-5, (rows, cols, j, err)
+
+
 def test_op_matmat_matches_matvec_per_column(oracle):
     """Each column of the batched product is the single-stream matvec of that column
     (qwen_tts_kernels.h:117-122: 'with B==1 it equals matvec'), to the f32 rounding of
