@@ -510,7 +510,8 @@ __device__ __forceinline__ qt_v4i q4_unpack16(uint2 w) {
 template <int NT, int EPI, int KB>
 __global__ __launch_bounds__(QT_BQ_MAXW * 64) void k_bgemm_q4(QtBgQ4Args a) {
     constexpr int BP = NT * 16 / 3, NS = BP / 16;   // padded streams, stream tiles
-    __shared__ float red[NS][4][64];
+    __shared__ float wred[QT_BQ_MAXW][NS][4][64];   // each wave's partial row sums
+    __shared__ float sres[16 * BP], sS[BP];         // residual rows [row][stream], stream scales
     const int nw = blockDim.x >> 6;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int r0 = blockIdx.x * 16;
@@ -531,6 +532,13 @@ __global__ __launch_bounds__(QT_BQ_MAXW * 64) void k_bgemm_q4(QtBgQ4Args a) {
 #pragma unroll
     for (int i = 0; i < 4; i++) sr[i] = a.s16 + (size_t)min(r0 + 4 * grp + i, a.rows - 1) * nb32 + (kw0 >> 5);
 
+    // the epilogue's operands (stream scales, residual rows) into LDS right behind the
+    // weight loads, instead of one dependent load per output at the end
+    for (int i = tid; i < 16 * BP; i += (int)blockDim.x) {
+        const int rl = i / BP, b = i % BP, r = r0 + rl;
+        sres[i] = (EPI == QT_EPI_RESID && b < a.B && r < a.rows) ? a.out[(size_t)b * a.ostride + r] : 0.f;
+    }
+    for (int i = tid; i < BP; i += (int)blockDim.x) sS[i] = i < a.B ? a.S[i] : 0.f;
     float acc[NS][4];
 #pragma unroll
     for (int s = 0; s < NS; s++)
@@ -575,35 +583,37 @@ __global__ __launch_bounds__(QT_BQ_MAXW * 64) void k_bgemm_q4(QtBgQ4Args a) {
     if (nkb > 0) loadB(Bb0, 0);
 #pragma unroll
     for (int kb = 0; kb < KB; kb++) {
-        if (kb >= nkb) break;
-        if (kb + 1 < nkb) {
-            if (kb & 1) loadB(Bb0, kb + 1);
-            else loadB(Bb1, kb + 1);
+        if (kb < nkb) {       // wave-uniform; a guard, not a break, so the loop unrolls fully
+            if (kb + 1 < nkb) {
+                if (kb & 1) loadB(Bb0, kb + 1);
+                else loadB(Bb1, kb + 1);
+            }
+            if (kb & 1) block(kb, Bb1);
+            else block(kb, Bb0);
         }
-        if (kb & 1) block(kb, Bb1);
-        else block(kb, Bb0);
         __builtin_amdgcn_sched_barrier(0);
     }
-    // the waves' partial row sums, added in wave order
-    for (int w = 0; w < nw; w++) {
-        if (wave == w) {
+    // the waves' partial row sums: each wave parks its own, one barrier, then every output
+    // is summed over the waves in wave order from 0.0f (the order fixes the f32 result)
 #pragma unroll
-            for (int s = 0; s < NS; s++)
+    for (int s = 0; s < NS; s++)
 #pragma unroll
-                for (int i = 0; i < 4; i++) red[s][i][lane] = (w == 0 ? 0.f : red[s][i][lane]) + acc[s][i];
-        }
-        __syncthreads();
-    }
-    for (int j = tid; j < 16 * BP; j += blockDim.x) {
+        for (int i = 0; i < 4; i++) wred[wave][s][i][lane] = acc[s][i];
+    __syncthreads();
+    auto val = [&](int rr, int b) -> float {
+        float t = 0.f;
+        for (int w = 0; w < nw; w++) t += wred[w][b >> 4][rr & 3][(rr >> 2) * 16 + (b & 15)];
+        return t * sS[b];
+    };
+    for (int j = tid; j < 16 * BP; j += (int)blockDim.x) {
         const int rl = j / BP, b = j % BP, r = r0 + rl;
         if (b >= a.B || r >= a.rows) continue;
         if (EPI == QT_EPI_SWIGLU && (rl & 1)) continue;
-        auto val = [&](int rr) -> float { return red[b >> 4][rr & 3][(rr >> 2) * 16 + (b & 15)] * a.S[b]; };
         float *ob = a.out + (size_t)b * a.ostride;
-        if (EPI == QT_EPI_STORE) ob[r] = val(rl);
-        else if (EPI == QT_EPI_RESID) ob[r] = __fadd_rn(ob[r], val(rl));
+        if (EPI == QT_EPI_STORE) ob[r] = val(rl, b);
+        else if (EPI == QT_EPI_RESID) ob[r] = __fadd_rn(sres[j], val(rl, b));
         else if (EPI == QT_EPI_SWIGLU) {
-            const float g = val(rl), u = val(rl + 1);
+            const float g = val(rl, b), u = val(rl + 1, b);
             ob[r >> 1] = g / (1.0f + expf(-g)) * u;
         }
     }
