@@ -121,6 +121,10 @@ FRAME_WORKLOADS = {
 SD_WORKLOADS = {
     "sd-decode-125frames": (125, 10),
 }
+# the speech decoder's exact streaming decode: (frames per stream, frames per chunk, timed streams)
+SD_STREAM_WORKLOADS = {
+    "sd-stream-125frames-chunk10": (125, 10, 5),
+}
 F32_MFMA_PEAK_TFS = 157.3
 # batched workloads: (shape, precision, streams, KV length range, default timed steps)
 BATCH_WORKLOADS = {
@@ -154,7 +158,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=None)
     ap.add_argument("--workload", default="talker-1.7B-int8-b1-L2048", choices=sorted(WORKLOADS) + sorted(BATCH_WORKLOADS) + sorted(CP_WORKLOADS)
                     + sorted(PREFILL_WORKLOADS) + sorted(GROW_WORKLOADS) + sorted(SAMPLED_WORKLOADS)
-                    + sorted(FRAME_WORKLOADS) + sorted(SD_WORKLOADS))
+                    + sorted(FRAME_WORKLOADS) + sorted(SD_WORKLOADS) + sorted(SD_STREAM_WORKLOADS))
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--kernel-launches", type=int, default=200)
@@ -182,6 +186,8 @@ def main():
         return bench_frames(args)
     if args.workload in SD_WORKLOADS:
         return bench_sd(args)
+    if args.workload in SD_STREAM_WORKLOADS:
+        return bench_sd_stream(args)
     from qwen3_tts_amd import hip, synth
     shape_name, prec, Lpre, dsteps = WORKLOADS[args.workload]
     K = args.steps or dsteps
@@ -874,6 +880,83 @@ def bench_sd(args):
                      "frac": round(tfs / F32_MFMA_PEAK_TFS, 4), "traffic": None,
                      "kernel": "one decode (all kernels; k_sd_gemm carries the flops)", "flops_per_launch": int(fl),
                      "avg_us": round(ms * 1e3, 1), "steps_per_launch": 1},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(out), flush=True)
+
+
+def bench_sd_stream(args):
+    """The speech decoder's exact streaming decode (qwen_hip_sd_stream_decode, the twin of
+    qwen_speech_decoder_decode_streaming_st): a stream of n frames fed in chunks of c frames,
+    each call taking host codes and returning the chunk's 1920 c samples on the host (so
+    every chunk time includes its two small PCIe copies and a device sync).  value = ms for
+    the whole stream; also the first chunk's latency (time to first audio) and the mean
+    chunk latency.  Timed on the host clock around each call."""
+    from qwen3_tts_amd import hip, synth_sd
+    n, c, dk = SD_STREAM_WORKLOADS[args.workload]
+    K = args.steps or dk
+    W = 1 if args.warmup is None else args.warmup
+    t0 = time.time()
+    tens = synth_sd.generate_sd()
+    path = synth_sd.write_sd(os.path.join(os.environ.get("TMPDIR", "/tmp"), "qwen3tts_bench_sd"), tensors=tens)
+    dec = hip.SpeechDecoder.from_file(path)
+    log(f"[bench] sd-stream: weights + device init {time.time() - t0:.1f}s")
+    rng = np.random.default_rng(0x5EED0D0E)
+    codes = rng.integers(0, 2048, (n, 16)).astype(np.int32)
+    chunks = [codes[i:i + c] for i in range(0, n, c)]
+    st = hip.SpeechDecoderStream(dec)
+    firsts, totals, per_chunk = [], [], []
+    for it in range(W + K):
+        st.reset()
+        tt = []
+        for ch in chunks:
+            a = time.perf_counter()
+            st.decode(ch)
+            tt.append(time.perf_counter() - a)
+        if it >= W:
+            firsts.append(tt[0] * 1e3)
+            totals.append(sum(tt) * 1e3)
+            per_chunk.extend(x * 1e3 for x in tt)
+    st.free()
+    ms = float(np.median(totals))
+    audio_s = n * 1920 / 24000.0
+    fl = sd_flops(n)
+    tfs = fl / (ms * 1e-3) / 1e12
+    log(f"[bench] sd-stream: {n} frames in chunks of {c}: {ms:.2f} ms per stream (median of {K}), first chunk "
+        f"{np.median(firsts):.2f} ms, chunk mean {np.mean(per_chunk):.2f} ms")
+    cpu = None
+    if not args.no_cpu_baseline:
+        try:
+            sys.path.insert(0, ROOT)
+            from oracle.oracle import RefSpeechDecoder
+            threads = int(os.environ.get("OMP_NUM_THREADS", "16"))
+            ref = RefSpeechDecoder(path, threads=threads)
+            a = time.perf_counter()
+            ref.stream_decode(chunks[:1])
+            secs = time.perf_counter() - a
+            model, ncpu = host_info()
+            cpu = {"value": round(secs * 1e3, 1), "unit": "ms/first chunk", "cores": threads, "kind": "reference",
+                   "sample": f"the reference's streaming decode of the first {c}-frame chunk of the same codes "
+                             f"(oracle/_ref, reference flags, no BLAS): its time to first audio",
+                   "host_cpu": model, "host_logical_cpus": ncpu}
+            log(f"[bench] sd-stream cpu baseline: first chunk {secs:.2f} s")
+        except Exception as ex:  # noqa: BLE001
+            cpu = {"value": None, "unit": "ms/first chunk", "error": str(ex)[:200]}
+    dec.free()
+    out = {
+        "metric": "speech decoder streaming ms/stream (codes -> 24 kHz audio chunk by chunk) + time to first audio",
+        "value": round(ms, 3), "unit": "ms/stream", "n_gpus": 1, "steps": K, "warmup": W, "ms_per_step": round(ms, 3),
+        "higher_is_better": False, "scaling": "weak", "vs_baseline": None, "dtype": "f32",
+        "data": "synthetic (seeded random-init F32 decoder weights of the 12 Hz codec architecture; random codes)",
+        "config": {"workload": args.workload, "frames": n, "chunk_frames": c, "chunks": len(chunks),
+                   "audio_seconds": audio_s},
+        "first_chunk_ms": round(float(np.median(firsts)), 3), "chunk_ms_mean": round(float(np.mean(per_chunk)), 3),
+        "chunk_ms_p90": round(float(np.percentile(per_chunk, 90)), 3),
+        "realtime_factor": round(audio_s / (ms * 1e-3), 1),
+        "roofline": {"bound": "mfma", "achieved": round(tfs, 2), "peak": F32_MFMA_PEAK_TFS, "unit": "TFLOP/s",
+                     "frac": round(tfs / F32_MFMA_PEAK_TFS, 4), "traffic": None,
+                     "kernel": "one stream (one-shot decode flops over the stream's host-clock time)",
+                     "flops_per_launch": int(fl), "avg_us": round(ms * 1e3, 1), "steps_per_launch": 1},
         "cpu_baseline": cpu,
     }
     print(json.dumps(out), flush=True)
