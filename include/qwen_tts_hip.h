@@ -380,8 +380,8 @@ void qwen_hip_sd_stream_free(void *stream_state);
 /* The decoder's layers one at a time, on time-major host arrays (X [T][Cin], Y [T][Cout]):
  * causal_conv1d (sd.c:98-119; W [Cout][Cin][kernel], left pad (kernel-1) dilation) and
  * causal_conv_transpose1d (sd.c:122-160; W [Cin][Cout][kernel], kernel <= 2 stride, Y
- * [Tin stride][Cout]); the conv's kernel is at most 8.  bias may be NULL.  tile: 0 = as the decoder picks it, 64 or 128 =
- * force the implicit GEMM's tile.  Cin a multiple of 16, Cout of 4. */
+ * [Tin stride][Cout]); the conv's kernel is at most 8.  bias may be NULL.  tile: 0 = as the decoder picks it, 16, 32,
+ * 64 or 128 = force the implicit GEMM's row tile (every tile gives the same bits).  Cin a multiple of 16, Cout of 4. */
 int qwen_hip_op_sd_conv(float *Y, const float *X, const float *W, const float *bias, int T, int Cin, int Cout,
                         int kernel, int dilation, int tile);
 int qwen_hip_op_sd_conv_transpose(float *Y, const float *X, const float *W, const float *bias, int Tin, int Cin,

@@ -54,82 +54,120 @@ __device__ __forceinline__ float sd_snake(float x, float a, float ib) {
     return fmaf(ib, s * s, x);
 }
 
-// TM x TN output tile (64 x 64 or 128 x 128), four waves of (TM/2) x (TN/2), each a grid
-// of 16 x 16 MFMA tiles; K in chunks of 16 staged through LDS, the next chunk's global
-// loads held in registers while the MFMAs run.  The 128 x 128 tile reads each A and B
-// value from LDS once per four MFMAs (twice as many as the 64 x 64 tile's two).
+// TM x TN output tile (16, 32 or 64 x 64, or 128 x 128), four waves of a 2 x 2 grid (a
+// 1 x 4 grid for TM = 16), each a grid of 16 x 16 MFMA tiles; K in chunks of 16 staged through LDS (two buffers).  The global
+// loads of the next P chunks sit in a ring of P register slots: a chunk's loads are
+// issued P - 1 chunks before it is staged, which hides HBM latency when only a few
+// workgroups share a CU (a streaming chunk of a few frames gives the long-K convolutions
+// a few dozen tiles).  The fetch index is clamped to the last chunk rather than guarded,
+// so the loads are straight-line code and the compiler counts them exactly.  Every
+// output element still sums its products in chunk order, whatever TM, TN and P are.
+// The 128 x 128 tile reads each A and B value from LDS once per four MFMAs (twice as
+// many as the 64 x 64 tile's two).
 // v_mfma_f32_16x16x4_f32: lane l supplies A[l % 16][l / 16] and B[l / 16][l % 16] and
 // receives D[4 (l / 16) + r][l % 16], r < 4.
-template <int TM, int TN>
+template <int TM, int TN, int P>
 __global__ __launch_bounds__(SD_WG) void k_sd_gemm(SdGemmArgs a) {
-    constexpr int AQ = TM / 64, BQ = TN / 64;          // float4 loads per thread per chunk
+    static_assert(P >= 2 && P % 2 == 0, "chunk c sits in LDS buffer c & 1 == slot & 1");
+    // A chunk is TM x 16 floats = TM * 4 float4s: a 16-row tile loads it with one wave and
+    // the other three load a copy of the same rows (same addresses, nothing staged)
+    constexpr int AQ = TM >= 64 ? TM / 64 : 1, BQ = TN / 64;   // float4 loads per thread per chunk
+    constexpr int WMW = TM >= 32 ? 2 : 1, WNW = 4 / WMW;     // wave grid: WMW along M, WNW along N
     constexpr int BS = TN + 16;                        // B row stride: rows k, k+1 on opposite bank halves
-    constexpr int MI = TM / 32, NJ = TN / 32;          // MFMA tiles per wave
+    constexpr int MI = TM / (16 * WMW), NJ = TN / (16 * WNW);   // 16 x 16 MFMA tiles per wave
+    static_assert(MI >= 1 && NJ >= 1 && TN % 64 == 0, "tile shape");
     __shared__ float As[2][TM * SD_AS];
     __shared__ float Bs[2][SD_KC * BS];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int t0 = blockIdx.x * TM, n0 = blockIdx.y * TN, z = blockIdx.z;
     const float *W = a.W + (size_t)z * a.ntap * a.K * a.N;
     const int kpt = a.K / SD_KC, nch = a.ntap * kpt;
-    float4 av[AQ], bv[BQ];
-    auto fetch = [&](int c) {
+    // ring slots hold the loads as issued (clamped rows and columns); which of them are
+    // real (am: bit q of the slot's A loads, bok: B columns inside N) is applied when a
+    // slot is staged, so the loads have no use before then and nothing branches around them
+    float4 av[P][AQ], bv[P][BQ];
+    unsigned amk[P];
+    unsigned bok = 0;
+#pragma unroll
+    for (int q = 0; q < BQ; q++) bok |= (n0 + ((tid + q * SD_WG) % (TN / 4)) * 4 < a.N) ? 1u << q : 0u;
+    auto fetch = [&](int c, float4 (&ra)[AQ], float4 (&rb)[BQ], unsigned &am) {
         const int p = c / kpt, k0 = (c - p * kpt) * SD_KC;
 #pragma unroll
         for (int q = 0; q < AQ; q++) {
-            const int f = tid + q * SD_WG, ar = f >> 2, ac = (f & 3) * 4;
+            const int f = tid + q * SD_WG, ar = (f >> 2) % TM, ac = (f & 3) * 4;
             const int xr = t0 + ar + a.off[p];
-            av[q] = (t0 + ar < a.T && xr >= a.xlo && xr < a.Tx)
-                        ? *reinterpret_cast<const float4 *>(a.X + (size_t)xr * a.ldx + k0 + ac)
-                        : make_float4(0.f, 0.f, 0.f, 0.f);
+            const bool ok = t0 + ar < a.T && xr >= a.xlo && xr < a.Tx;
+            const int xc = min(max(xr, a.xlo), a.Tx - 1);   // in bounds; the value is dropped when !ok
+            ra[q] = *reinterpret_cast<const float4 *>(a.X + (ptrdiff_t)xc * a.ldx + k0 + ac);
+            am = ok ? am | (1u << q) : am & ~(1u << q);
         }
 #pragma unroll
         for (int q = 0; q < BQ; q++) {
             const int f = tid + q * SD_WG, br = f / (TN / 4), bc = (f % (TN / 4)) * 4;
-            bv[q] = n0 + bc < a.N ? *reinterpret_cast<const float4 *>(W + ((size_t)p * a.K + k0 + br) * a.N + n0 + bc)
-                                  : make_float4(0.f, 0.f, 0.f, 0.f);
+            const int nc = min(n0 + bc, a.N - 4);
+            rb[q] = *reinterpret_cast<const float4 *>(W + ((size_t)p * a.K + k0 + br) * a.N + nc);
         }
     };
-    auto stage = [&](int buf) {
+    auto stage = [&](int buf, const float4 (&ra)[AQ], const float4 (&rb)[BQ], unsigned am) {
+        // masks on the bits, value by value (a select of whole float4s becomes a select of
+        // their addresses, which moves the ring to scratch)
 #pragma unroll
         for (int q = 0; q < AQ; q++) {
             const int f = tid + q * SD_WG, ar = f >> 2, ac = (f & 3) * 4;
+            if (TM * 4 < SD_WG && f >= TM * 4) continue;    // the copies (whole waves)
+            const unsigned m = 0u - ((am >> q) & 1u);
             float *as = As[buf] + ar * SD_AS + ac;
-            as[0] = av[q].x; as[1] = av[q].y; as[2] = av[q].z; as[3] = av[q].w;
+            as[0] = __uint_as_float(__float_as_uint(ra[q].x) & m);
+            as[1] = __uint_as_float(__float_as_uint(ra[q].y) & m);
+            as[2] = __uint_as_float(__float_as_uint(ra[q].z) & m);
+            as[3] = __uint_as_float(__float_as_uint(ra[q].w) & m);
         }
 #pragma unroll
         for (int q = 0; q < BQ; q++) {
             const int f = tid + q * SD_WG, br = f / (TN / 4), bc = (f % (TN / 4)) * 4;
-            *reinterpret_cast<float4 *>(Bs[buf] + br * BS + bc) = bv[q];
+            const unsigned m = 0u - ((bok >> q) & 1u);
+            *reinterpret_cast<float4 *>(Bs[buf] + br * BS + bc) =
+                make_float4(__uint_as_float(__float_as_uint(rb[q].x) & m), __uint_as_float(__float_as_uint(rb[q].y) & m),
+                            __uint_as_float(__float_as_uint(rb[q].z) & m), __uint_as_float(__float_as_uint(rb[q].w) & m));
         }
     };
-    const int wm = (wave >> 1) * (TM / 2), wn = (wave & 1) * (TN / 2);
+    const int wm = (wave / WNW) * (TM / WMW), wn = (wave % WNW) * (TN / WNW);
     const int li = lane & 15, lk = lane >> 4;
     qt_sd_f4 acc[MI][NJ];
 #pragma unroll
     for (int i = 0; i < MI; i++)
 #pragma unroll
         for (int j = 0; j < NJ; j++) acc[i][j] = qt_sd_f4{0.f, 0.f, 0.f, 0.f};
-    fetch(0);
-    stage(0);
+#pragma unroll
+    for (int s = 0; s < P; s++) fetch(min(s, nch - 1), av[s], bv[s], amk[s]);
+    stage(0, av[0], bv[0], amk[0]);
     __syncthreads();
-    for (int c = 0; c < nch; c++) {
-        const int buf = c & 1;
-        if (c + 1 < nch) fetch(c + 1);
-        const float *as = As[buf], *bs = Bs[buf];
+    for (int c0 = 0; c0 < nch; c0 += P) {
 #pragma unroll
-        for (int kk = 0; kk < SD_KC; kk += 4) {
-            float fa[MI], fb[NJ];
+        for (int s = 0; s < P; s++) {
+            const int c = c0 + s;
+            // slot s held chunk c, staged one step ago: refill it with chunk c + P (loads
+            // issued on every path, so the waits before each stage count them exactly)
+            fetch(min(c + P, nch - 1), av[s], bv[s], amk[s]);
+            if (c < nch) {
+                const float *as = As[s & 1], *bs = Bs[s & 1];
 #pragma unroll
-            for (int i = 0; i < MI; i++) fa[i] = as[(wm + 16 * i + li) * SD_AS + kk + lk];
+                for (int kk = 0; kk < SD_KC; kk += 4) {
+                    float fa[MI], fb[NJ];
 #pragma unroll
-            for (int j = 0; j < NJ; j++) fb[j] = bs[(kk + lk) * BS + wn + 16 * j + li];
+                    for (int i = 0; i < MI; i++) fa[i] = as[(wm + 16 * i + li) * SD_AS + kk + lk];
 #pragma unroll
-            for (int i = 0; i < MI; i++)
+                    for (int j = 0; j < NJ; j++) fb[j] = bs[(kk + lk) * BS + wn + 16 * j + li];
 #pragma unroll
-                for (int j = 0; j < NJ; j++) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(fa[i], fb[j], acc[i][j], 0, 0, 0);
+                    for (int i = 0; i < MI; i++)
+#pragma unroll
+                        for (int j = 0; j < NJ; j++)
+                            acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(fa[i], fb[j], acc[i][j], 0, 0, 0);
+                }
+                if (c + 1 < nch) stage((s & 1) ^ 1, av[(s + 1) % P], bv[(s + 1) % P], amk[(s + 1) % P]);
+                __syncthreads();
+            }
         }
-        if (c + 1 < nch) stage(buf ^ 1);
-        __syncthreads();
     }
 #pragma unroll
     for (int i = 0; i < MI; i++)
@@ -346,17 +384,37 @@ __global__ __launch_bounds__(SD_WG) void k_sd_final(const float *x, const float 
     }
 }
 
-// streaming history: the last H rows of a buffer's [H + T] rows become its first H rows
-// (one thread per column walks the rows forward, so overlapping ranges copy correctly)
-__global__ void k_sd_shift(float *buf, int H, int T, int C) {
-    const int c = blockIdx.x * blockDim.x + threadIdx.x;
-    if (c >= C) return;
-    for (int r = 0; r < H; r++) buf[(size_t)r * C + c] = buf[(size_t)(T + r) * C + c];
+// streaming history: the last H rows of a buffer's [H + T] rows become its first H rows.
+// Source and destination overlap when T < H (a chunk of fewer new rows than the history),
+// so a workgroup owns 64 columns whole: its four waves read all H rows of them into
+// registers (loads of every row in flight at once), wait for the data, meet at one
+// barrier, and only then store.  No other workgroup touches those columns.
+#define SD_SHIFT_MAXH 96
+__global__ __launch_bounds__(SD_WG) void k_sd_shift(float *buf, int H, int T, int C) {
+    constexpr int NR = SD_SHIFT_MAXH / 4;
+    const int c = blockIdx.x * 64 + (threadIdx.x & 63), r0 = threadIdx.x >> 6;
+    float v[NR];
+#pragma unroll
+    for (int i = 0; i < NR; i++) {
+        const int r = r0 + 4 * i;
+        v[i] = (c < C && r < H) ? buf[(size_t)(T + r) * C + c] : 0.f;
+    }
+#pragma unroll
+    for (int i = 0; i < NR; i++) asm volatile("" : "+v"(v[i]));   // every load has returned
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < NR; i++) {
+        const int r = r0 + 4 * i;
+        if (c < C && r < H) buf[(size_t)r * C + c] = v[i];
+    }
 }
 
 // ---- launchers ----------------------------------------------------------------------------
 
-// tile: 0 = by size (128 x 128 where that still gives two workgroups per CU), 64 or 128 = forced
+// tile: 0 = by size (128 x 128 where that still gives two workgroups per CU, else the
+// largest of 64, 32, 16 rows x 64 columns that fills the CUs), 16, 32, 64 or 128 = forced.
+// Every tile sums each output's products in the same order, so the choice never changes
+// a result bit.
 extern "C" hipError_t qt_launch_sd_gemm(const float *X, int ldx, int Tx, int xlo, const float *W, int K, int N, int ntap,
                                         const int *off, int phases, int T, float *Y, int ldy, const float *bias,
                                         const float *cscale, const float *R, const float *sa, const float *sib,
@@ -372,13 +430,31 @@ extern "C" hipError_t qt_launch_sd_gemm(const float *X, int ldx, int Tx, int xlo
     for (int i = 0; i < SD_MAXTAP; i++) a.off[i] = i < ntap ? off[i] : 0;
     a.T = T; a.Y = Y; a.ldy = ldy; a.os = phases; a.bias = bias; a.cscale = cscale; a.R = R; a.epi = epi;
     a.sa = sa; a.sib = sib; a.Y2 = Y2;
+    const long long nt = (long long)((N + 63) / 64) * phases;
     const long long big = (long long)((T + 127) / 128) * ((N + 127) / 128) * phases;
-    if (tile == 128 || (tile == 0 && N >= 128 && big >= 512)) {
+    if (tile == 0) {
+        // the largest row tile whose grid still gives every CU a workgroup: a streaming
+        // chunk of a few frames leaves T at 10..320 rows, where 64-row tiles would be
+        // mostly padding on a few dozen CUs
+        if (N >= 128 && big >= 512) tile = 128;
+        else if ((T + 63) / 64 * nt >= 256) tile = 64;
+        else if ((T + 31) / 32 * nt >= 256) tile = 32;
+        else tile = 16;
+    }
+    if (tile == 128) {
         dim3 grid((T + 127) / 128, (N + 127) / 128, phases);
-        hipLaunchKernelGGL((k_sd_gemm<128, 128>), grid, dim3(SD_WG), 0, st, a);
-    } else {
+        hipLaunchKernelGGL((k_sd_gemm<128, 128, 4>), grid, dim3(SD_WG), 0, st, a);
+    } else if (tile == 64) {
         dim3 grid((T + 63) / 64, (N + 63) / 64, phases);
-        hipLaunchKernelGGL((k_sd_gemm<64, 64>), grid, dim3(SD_WG), 0, st, a);
+        hipLaunchKernelGGL((k_sd_gemm<64, 64, 8>), grid, dim3(SD_WG), 0, st, a);
+    } else if (tile == 32) {
+        dim3 grid((T + 31) / 32, (N + 63) / 64, phases);
+        hipLaunchKernelGGL((k_sd_gemm<32, 64, 8>), grid, dim3(SD_WG), 0, st, a);
+    } else if (tile == 16) {
+        dim3 grid((T + 15) / 16, (N + 63) / 64, phases);
+        hipLaunchKernelGGL((k_sd_gemm<16, 64, 8>), grid, dim3(SD_WG), 0, st, a);
+    } else {
+        return hipErrorInvalidValue;
     }
     return hipGetLastError();
 }
@@ -437,6 +513,7 @@ extern "C" hipError_t qt_launch_sd_final(const float *x, const float *w, const f
 
 extern "C" hipError_t qt_launch_sd_shift(float *buf, int H, int T, int C, hipStream_t st) {
     if (H <= 0) return hipSuccess;
-    hipLaunchKernelGGL(k_sd_shift, dim3((C + 255) / 256), dim3(256), 0, st, buf, H, T, C);
+    if (H > SD_SHIFT_MAXH || T <= 0 || C <= 0) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_sd_shift, dim3((C + 63) / 64), dim3(SD_WG), 0, st, buf, H, T, C);
     return hipGetLastError();
 }

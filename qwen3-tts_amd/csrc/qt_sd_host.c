@@ -490,7 +490,7 @@ static int sd_op(float *Y, const float *X, const float *W, const float *bias, in
     float *dx = NULL, *dy = NULL;
     int rc = -1;
     if (!Y || !X || !W || Tin < 1 || Cin < 16 || Cin % 16 || Cout < 4 || Cout % 4 || k < 1 ||
-        (stride ? (k > 2 * stride || stride > 64) : k > 8) || (tile && tile != 64 && tile != 128)) {
+        (stride ? (k > 2 * stride || stride > 64) : k > 8) || (tile && tile != 16 && tile != 32 && tile != 64 && tile != 128)) {
         qt_seterr("op_sd_conv: bad shape (Cin multiple of 16, Cout of 4; conv kernel 1..8, transposed kernel <= 2 stride)");
         return -1;
     }

@@ -98,7 +98,7 @@ def _convt_ref(x, w, b, s):
                                       None if b is None else b.astype(np.float64), s).T
 
 
-@pytest.mark.parametrize("tile", [0, 64, 128])
+@pytest.mark.parametrize("tile", [0, 16, 32, 64, 128])
 @pytest.mark.parametrize("T,cin,cout,k,d", [(3000, 96, 96, 7, 9), (1000, 256, 384, 7, 3), (257, 1024, 1536, 7, 1),
                                             (64, 512, 1024, 3, 1), (130, 16, 4, 1, 1)])
 def test_op_sd_conv_vs_f64(T, cin, cout, k, d, tile):
@@ -116,7 +116,7 @@ def test_op_sd_conv_vs_f64(T, cin, cout, k, d, tile):
     assert err < 2e-6 * max(1.0, np.sqrt(cin * k) / 8), err
 
 
-@pytest.mark.parametrize("tile", [0, 64, 128])
+@pytest.mark.parametrize("tile", [0, 16, 32, 64, 128])
 @pytest.mark.parametrize("T,cin,cout,k,s", [(500, 192, 96, 6, 3), (300, 384, 192, 8, 4), (64, 1024, 1024, 2, 2),
                                             (100, 64, 32, 3, 2), (40, 1536, 768, 16, 8)])
 def test_op_sd_conv_transpose_vs_f64(T, cin, cout, k, s, tile):
@@ -132,6 +132,33 @@ def test_op_sd_conv_transpose_vs_f64(T, cin, cout, k, s, tile):
     want = _convt_ref(x, w, b, s)
     err = float(np.abs(y - want).max() / np.abs(want).max())
     assert err < 2e-6 * max(1.0, np.sqrt(2 * cin) / 8), err
+
+
+@pytest.mark.parametrize("T,cin,cout,k,d,s", [(10, 512, 3072, 1, 1, 0), (40, 1024, 1536, 7, 1, 0), (45, 768, 768, 7, 9, 0),
+                                              (40, 1536, 768, 16, 8, 8), (333, 96, 96, 7, 3, 0)])
+def test_op_sd_tiles_same_bits(T, cin, cout, k, d, s):
+    """Every row tile of the implicit GEMM (16, 32, 64, 128 rows) sums each output's
+    products in the same chunk order, so they agree bit for bit; the streaming decoder
+    picks small tiles for a few frames and the one-shot decode large ones, and the
+    stream == one-shot identity rests on this."""
+    rng = np.random.default_rng(T * 7 + cin + k)
+    x = rng.standard_normal((T, cin)).astype(np.float32)
+    outs = []
+    for tile in (16, 32, 64, 128):
+        if s:
+            w = (rng.standard_normal((cin, cout, k)) / np.sqrt(2 * cin)).astype(np.float32) if not outs else w
+            y = np.empty((T * s, cout), np.float32)
+            hip.check(hip.lib().qwen_hip_op_sd_conv_transpose(y.ctypes.data, x.ctypes.data, w.ctypes.data, None, T,
+                                                              cin, cout, k, s, tile), "op_sd_conv_transpose")
+        else:
+            w = (rng.standard_normal((cout, cin, k)) / np.sqrt(cin * k)).astype(np.float32) if not outs else w
+            y = np.empty((T, cout), np.float32)
+            hip.check(hip.lib().qwen_hip_op_sd_conv(y.ctypes.data, x.ctypes.data, w.ctypes.data, None, T, cin, cout,
+                                                    k, d, tile), "op_sd_conv")
+        outs.append(y)
+    assert np.abs(outs[0]).max() > 0
+    for y in outs[1:]:
+        assert np.array_equal(y.view(np.uint32), outs[0].view(np.uint32))
 
 
 @need_ref
