@@ -24,8 +24,7 @@
 typedef float qt_sd_f4 __attribute__((ext_vector_type(4)));
 
 #define SD_WG 256
-#define SD_KC 16                 // K chunk staged per step
-#define SD_AS (SD_KC + 1)        // A tile row stride (floats): 17 spreads 16 rows over banks
+#define SD_KC 16                 // K chunk staged per step (the 16- and 32-row tiles stage 64 where K allows)
 #define SD_MAXTAP 8
 
 enum { SD_EPI_BIAS = 1, SD_EPI_GELU = 2, SD_EPI_CSCALE = 4, SD_EPI_RESID = 8, SD_EPI_SNAKE = 16, SD_EPI_SNAKE2 = 32 };
@@ -55,33 +54,39 @@ __device__ __forceinline__ float sd_snake(float x, float a, float ib) {
 }
 
 // TM x TN output tile (16, 32 or 64 x 64, or 128 x 128), four waves of a 2 x 2 grid (a
-// 1 x 4 grid for TM = 16), each a grid of 16 x 16 MFMA tiles; K in chunks of 16 staged through LDS (two buffers).  The global
+// 1 x 4 grid for TM = 16), each a grid of 16 x 16 MFMA tiles; K in chunks of KC (16, or
+// 64 for the small tiles where K allows) staged through LDS (two buffers).  The global
 // loads of the next P chunks sit in a ring of P register slots: a chunk's loads are
 // issued P - 1 chunks before it is staged, which hides HBM latency when only a few
 // workgroups share a CU (a streaming chunk of a few frames gives the long-K convolutions
 // a few dozen tiles).  The fetch index is clamped to the last chunk rather than guarded,
 // so the loads are straight-line code and the compiler counts them exactly.  Every
-// output element still sums its products in chunk order, whatever TM, TN and P are.
+// output element sums its products four k at a time in ascending k, one MFMA after
+// another, whatever TM, TN, P and KC are, so every tile gives the same bits.
 // The 128 x 128 tile reads each A and B value from LDS once per four MFMAs (twice as
 // many as the 64 x 64 tile's two).
 // v_mfma_f32_16x16x4_f32: lane l supplies A[l % 16][l / 16] and B[l / 16][l % 16] and
 // receives D[4 (l / 16) + r][l % 16], r < 4.
-template <int TM, int TN, int P>
+template <int TM, int TN, int P, int KC>
 __global__ __launch_bounds__(SD_WG) void k_sd_gemm(SdGemmArgs a) {
     static_assert(P >= 2 && P % 2 == 0, "chunk c sits in LDS buffer c & 1 == slot & 1");
-    // A chunk is TM x 16 floats = TM * 4 float4s: a 16-row tile loads it with one wave and
-    // the other three load a copy of the same rows (same addresses, nothing staged)
-    constexpr int AQ = TM >= 64 ? TM / 64 : 1, BQ = TN / 64;   // float4 loads per thread per chunk
+    static_assert(KC == 16 || KC == 64, "K chunk");
+    // A chunk is TM x KC floats = TM * KC / 4 float4s; where that is fewer than the 256
+    // threads (16 or 32 rows at KC = 16) the spare waves load a copy of the same rows
+    // (same addresses, nothing staged)
+    constexpr int AF4 = TM * KC / 4, AQ = AF4 >= SD_WG ? AF4 / SD_WG : 1;   // A float4 loads per thread
+    constexpr int BQ = KC * TN / (4 * SD_WG);                               // B float4 loads per thread
+    constexpr int AS = KC + (KC == 16 ? 1 : 17);   // A row stride = 17 mod 32 floats: 16 rows spread over banks
     constexpr int WMW = TM >= 32 ? 2 : 1, WNW = 4 / WMW;     // wave grid: WMW along M, WNW along N
     constexpr int BS = TN + 16;                        // B row stride: rows k, k+1 on opposite bank halves
     constexpr int MI = TM / (16 * WMW), NJ = TN / (16 * WNW);   // 16 x 16 MFMA tiles per wave
-    static_assert(MI >= 1 && NJ >= 1 && TN % 64 == 0, "tile shape");
-    __shared__ float As[2][TM * SD_AS];
-    __shared__ float Bs[2][SD_KC * BS];
+    static_assert(MI >= 1 && NJ >= 1 && TN % 64 == 0 && BQ >= 1, "tile shape");
+    __shared__ float As[2][TM * AS];
+    __shared__ float Bs[2][KC * BS];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int t0 = blockIdx.x * TM, n0 = blockIdx.y * TN, z = blockIdx.z;
     const float *W = a.W + (size_t)z * a.ntap * a.K * a.N;
-    const int kpt = a.K / SD_KC, nch = a.ntap * kpt;
+    const int kpt = a.K / KC, nch = a.ntap * kpt;
     // ring slots hold the loads as issued (clamped rows and columns); which of them are
     // real (am: bit q of the slot's A loads, bok: B columns inside N) is applied when a
     // slot is staged, so the loads have no use before then and nothing branches around them
@@ -91,10 +96,10 @@ __global__ __launch_bounds__(SD_WG) void k_sd_gemm(SdGemmArgs a) {
 #pragma unroll
     for (int q = 0; q < BQ; q++) bok |= (n0 + ((tid + q * SD_WG) % (TN / 4)) * 4 < a.N) ? 1u << q : 0u;
     auto fetch = [&](int c, float4 (&ra)[AQ], float4 (&rb)[BQ], unsigned &am) {
-        const int p = c / kpt, k0 = (c - p * kpt) * SD_KC;
+        const int p = c / kpt, k0 = (c - p * kpt) * KC;
 #pragma unroll
         for (int q = 0; q < AQ; q++) {
-            const int f = tid + q * SD_WG, ar = (f >> 2) % TM, ac = (f & 3) * 4;
+            const int f = tid + q * SD_WG, ar = (f / (KC / 4)) % TM, ac = (f % (KC / 4)) * 4;
             const int xr = t0 + ar + a.off[p];
             const bool ok = t0 + ar < a.T && xr >= a.xlo && xr < a.Tx;
             const int xc = min(max(xr, a.xlo), a.Tx - 1);   // in bounds; the value is dropped when !ok
@@ -113,10 +118,10 @@ __global__ __launch_bounds__(SD_WG) void k_sd_gemm(SdGemmArgs a) {
         // their addresses, which moves the ring to scratch)
 #pragma unroll
         for (int q = 0; q < AQ; q++) {
-            const int f = tid + q * SD_WG, ar = f >> 2, ac = (f & 3) * 4;
-            if (TM * 4 < SD_WG && f >= TM * 4) continue;    // the copies (whole waves)
+            const int f = tid + q * SD_WG, ar = f / (KC / 4), ac = (f % (KC / 4)) * 4;
+            if (AF4 < SD_WG && f >= AF4) continue;    // the copies (whole waves)
             const unsigned m = 0u - ((am >> q) & 1u);
-            float *as = As[buf] + ar * SD_AS + ac;
+            float *as = As[buf] + ar * AS + ac;
             as[0] = __uint_as_float(__float_as_uint(ra[q].x) & m);
             as[1] = __uint_as_float(__float_as_uint(ra[q].y) & m);
             as[2] = __uint_as_float(__float_as_uint(ra[q].z) & m);
@@ -152,10 +157,10 @@ __global__ __launch_bounds__(SD_WG) void k_sd_gemm(SdGemmArgs a) {
             if (c < nch) {
                 const float *as = As[s & 1], *bs = Bs[s & 1];
 #pragma unroll
-                for (int kk = 0; kk < SD_KC; kk += 4) {
+                for (int kk = 0; kk < KC; kk += 4) {
                     float fa[MI], fb[NJ];
 #pragma unroll
-                    for (int i = 0; i < MI; i++) fa[i] = as[(wm + 16 * i + li) * SD_AS + kk + lk];
+                    for (int i = 0; i < MI; i++) fa[i] = as[(wm + 16 * i + li) * AS + kk + lk];
 #pragma unroll
                     for (int j = 0; j < NJ; j++) fb[j] = bs[(kk + lk) * BS + wn + 16 * j + li];
 #pragma unroll
@@ -443,16 +448,22 @@ extern "C" hipError_t qt_launch_sd_gemm(const float *X, int ldx, int Tx, int xlo
     }
     if (tile == 128) {
         dim3 grid((T + 127) / 128, (N + 127) / 128, phases);
-        hipLaunchKernelGGL((k_sd_gemm<128, 128, 4>), grid, dim3(SD_WG), 0, st, a);
+        hipLaunchKernelGGL((k_sd_gemm<128, 128, 4, 16>), grid, dim3(SD_WG), 0, st, a);
     } else if (tile == 64) {
         dim3 grid((T + 63) / 64, (N + 63) / 64, phases);
-        hipLaunchKernelGGL((k_sd_gemm<64, 64, 8>), grid, dim3(SD_WG), 0, st, a);
-    } else if (tile == 32) {
-        dim3 grid((T + 31) / 32, (N + 63) / 64, phases);
-        hipLaunchKernelGGL((k_sd_gemm<32, 64, 8>), grid, dim3(SD_WG), 0, st, a);
-    } else if (tile == 16) {
-        dim3 grid((T + 15) / 16, (N + 63) / 64, phases);
-        hipLaunchKernelGGL((k_sd_gemm<16, 64, 8>), grid, dim3(SD_WG), 0, st, a);
+        hipLaunchKernelGGL((k_sd_gemm<64, 64, 8, 16>), grid, dim3(SD_WG), 0, st, a);
+    } else if (tile == 32 || tile == 16) {
+        // the small tiles stage 64-wide K chunks where K allows: a quarter of the barriers
+        // and LDS round trips per MFMA (the per-element order is the same)
+        dim3 grid((T + tile - 1) / tile, (N + 63) / 64, phases);
+        const bool k64 = K % 64 == 0;
+        if (tile == 32) {
+            if (k64) hipLaunchKernelGGL((k_sd_gemm<32, 64, 4, 64>), grid, dim3(SD_WG), 0, st, a);
+            else hipLaunchKernelGGL((k_sd_gemm<32, 64, 8, 16>), grid, dim3(SD_WG), 0, st, a);
+        } else {
+            if (k64) hipLaunchKernelGGL((k_sd_gemm<16, 64, 4, 64>), grid, dim3(SD_WG), 0, st, a);
+            else hipLaunchKernelGGL((k_sd_gemm<16, 64, 8, 16>), grid, dim3(SD_WG), 0, st, a);
+        }
     } else {
         return hipErrorInvalidValue;
     }
