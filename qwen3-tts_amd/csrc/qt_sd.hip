@@ -448,10 +448,10 @@ extern "C" hipError_t qt_launch_sd_gemm(const float *X, int ldx, int Tx, int xlo
     }
     if (tile == 128) {
         dim3 grid((T + 127) / 128, (N + 127) / 128, phases);
-        hipLaunchKernelGGL((k_sd_gemm<128, 128, 4, 16>), grid, dim3(SD_WG), 0, st, a);
+        hipLaunchKernelGGL((k_sd_gemm<128, 128, 2, 16>), grid, dim3(SD_WG), 0, st, a);
     } else if (tile == 64) {
         dim3 grid((T + 63) / 64, (N + 63) / 64, phases);
-        hipLaunchKernelGGL((k_sd_gemm<64, 64, 8, 16>), grid, dim3(SD_WG), 0, st, a);
+        hipLaunchKernelGGL((k_sd_gemm<64, 64, 2, 16>), grid, dim3(SD_WG), 0, st, a);
     } else if (tile == 32 || tile == 16) {
         // the small tiles stage 64-wide K chunks where K allows: a quarter of the barriers
         // and LDS round trips per MFMA (the per-element order is the same)

@@ -1460,7 +1460,7 @@ typedef struct {
     float *part; unsigned *cnt;
     int *d_pos;                /* [B] */
     float *h_io; int *h_pos;   /* pinned */
-    hipGraphExec_t exec; int graph_ready;
+    hipGraphExec_t exec; int graph_ready, stepped;   /* stepped: a batch_step has run (inputs set) */
     int last_async;            /* steps replayed since the last batch_step */
     uint16_t *kv_stage;        /* [kv_max][n_kv*hd]: slot upload/download staging, made on first use */
     int dead;
@@ -1601,6 +1601,7 @@ static int batch_step_impl(batch_t *bt, const float *in, const int *pos_arr, flo
     } else {
         HCK(batch_body(bt));
     }
+    bt->stepped = 1;
     HCK(hipMemcpyAsync(bt->h_io, bt->is_cp ? bt->x : bt->hid, (size_t)B * H * sizeof(float), hipMemcpyDeviceToHost, bt->st));
     HCK(hipStreamSynchronize(bt->st));
     if (out) memcpy(out, bt->h_io, (size_t)B * H * sizeof(float));
@@ -1666,13 +1667,13 @@ fail:
  * keeps max(pos) + n within kv_max. */
 int qwen_hip_talker_batch_step_async(void *state, int n_steps) {
     batch_t *bt = (batch_t *)state;
-    if (!bt || bt->dead || !bt->graph_ready) { SETERR("batch state not initialised by a batch_step call"); return -1; }
+    if (!bt || bt->dead || !bt->stepped) { SETERR("batch state not initialised by a batch_step call"); return -1; }
     int maxp = 0;
     for (int b = 0; b < bt->B; b++) if (bt->h_pos[b] > maxp) maxp = bt->h_pos[b];
     bt->last_async += n_steps;
     REQ(maxp + bt->last_async < bt->kv_max && maxp + bt->last_async < bt->s->rope_len,
         "replayed positions would pass kv_max %d", bt->kv_max);
-    for (int i = 0; i < n_steps; i++) HCK(hipGraphLaunch(bt->exec, bt->st));
+    for (int i = 0; i < n_steps; i++) HCK(bt->graph_ready ? hipGraphLaunch(bt->exec, bt->st) : batch_body(bt));
     return 0;
 fail:
     bt->dead = 1;
