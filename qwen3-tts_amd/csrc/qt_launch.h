@@ -92,8 +92,9 @@ enum { QT_PF_STORE = 0, QT_PF_RESID = 1, QT_PF_SWIGLU = 2 };
 int qt_pf_spad(int S);
 hipError_t qt_launch_pf_pieces(const float *X, int ldx, int S, int K, const float *gain, float eps, uint16_t *P,
                                hipStream_t st);
+/* part: split-K partials (part_cap floats; NULL: never split) */
 hipError_t qt_launch_pf_gemm(int epi, const uint16_t *W, const uint16_t *P, int S, int N, int K, float *Y, int ldy,
-                             float *part, hipStream_t st);
+                             float *part, long long part_cap, hipStream_t st);
 hipError_t qt_launch_pf_qkv_post(float *QKV, int ld, int S, int nh, int nkv, const float *qn, const float *kn,
                                  const float *rc, const float *rs, float eps, uint16_t *kc, uint16_t *vc,
                                  long long kv_max, hipStream_t st);

@@ -195,19 +195,37 @@ __global__ __launch_bounds__(QT_PF_WG) void k_pf_gemm2(const uint16_t *__restric
         }
 }
 
-// Y[s][n] += sum over the nz K ranges of part[z][s][n], ranges in order.
+// acc = sum over the nz K ranges of part[z][s][n..n+3], ranges in order (each range's
+// loads issued before the adds), then the projection's epilogue: Y = acc (STORE),
+// Y += acc (RESID), or the SwiGLU of the interleaved gate|up pairs into Y[s][n/2..n/2+1].
+template <int EPI>
 __global__ __launch_bounds__(QT_PF_WG) void k_pf_reduce(const float *part, int nz, int S, int N, float *Y, int ldy) {
     const int i = blockIdx.x * QT_PF_WG + threadIdx.x;
     if (i >= S * N / 4) return;
     const int s = i / (N / 4), n = 4 * (i % (N / 4));
     float4 acc = *reinterpret_cast<const float4 *>(part + (size_t)s * N + n);
-    for (int z = 1; z < nz; z++) {
-        const float4 v = *reinterpret_cast<const float4 *>(part + ((size_t)z * S + s) * N + n);
-        acc.x += v.x; acc.y += v.y; acc.z += v.z; acc.w += v.w;
+    constexpr int ZB = 8;
+    for (int z0 = 1; z0 < nz; z0 += ZB) {
+        float4 v[ZB];
+#pragma unroll
+        for (int k = 0; k < ZB; k++)
+            if (z0 + k < nz) v[k] = *reinterpret_cast<const float4 *>(part + ((size_t)(z0 + k) * S + s) * N + n);
+#pragma unroll
+        for (int k = 0; k < ZB; k++)
+            if (z0 + k < nz) { acc.x += v[k].x; acc.y += v[k].y; acc.z += v[k].z; acc.w += v[k].w; }
     }
-    float4 *y = reinterpret_cast<float4 *>(Y + (size_t)s * ldy + n);
-    const float4 o = *y;
-    *y = make_float4(o.x + acc.x, o.y + acc.y, o.z + acc.z, o.w + acc.w);
+    if constexpr (EPI == QT_PF_SWIGLU) {
+        *reinterpret_cast<float2 *>(Y + (size_t)s * ldy + (n >> 1)) =
+            make_float2(acc.x / (1.0f + expf(-acc.x)) * acc.y, acc.z / (1.0f + expf(-acc.z)) * acc.w);
+    } else {
+        float4 *y = reinterpret_cast<float4 *>(Y + (size_t)s * ldy + n);
+        if constexpr (EPI == QT_PF_RESID) {
+            const float4 o = *y;
+            *y = make_float4(o.x + acc.x, o.y + acc.y, o.z + acc.z, o.w + acc.w);
+        } else {
+            *y = acc;
+        }
+    }
 }
 
 // ---- per-head q/k norm, RoPE, KV store ---------------------------------------------
@@ -384,20 +402,36 @@ extern "C" hipError_t qt_launch_pf_pieces(const float *X, int ldx, int S, int K,
 // part: workspace of 4 * S * N floats for split K (nullable: no split).  The residual
 // projections (few weight rows) split K so the grid fills the CUs; the partial ranges
 // are added in order (deterministic).
+// Tile and K split of a projection: the tallest weight tile (256, 128 or 64 rows; a
+// taller tile reuses each LDS read of the planes over more rows and runs more MFMAs per
+// barrier) that reaches 256 workgroups, with its K split where needed into 2^k equal
+// ranges of at least four 64-k chunks whose partials fit in part_cap floats (added in
+// order by k_pf_reduce); else the largest grid.  Measured on the 1.7B prefill (128 / 512
+// positions): 4.16 / 9.46 ms, against 4.53 / 10.72 preferring an unsplit shorter tile,
+// 4.50 / 10.22 splitting to 512 workgroups, 4.27 / 9.46 with two-chunk ranges.
+static void qt_pf_plan(int S, int Sp, int N, int K, long long part_cap, int &nr, int &sk) {
+    const long long sy = Sp / 64;
+    long long best = -1;
+    nr = 1; sk = 1;
+    for (int r = 4; r >= 1; r >>= 1) {
+        if (N % (64 * r)) continue;
+        const long long g = (long long)(N / (64 * r)) * sy;
+        int k = 1;
+        while (g * k < 256 && (K / 64) % (2 * k) == 0 && K / 64 / (2 * k) >= 4 && 2LL * k * S * N <= part_cap) k *= 2;
+        if (g * k >= 256) { nr = r; sk = k; return; }
+        if (g * k > best) { best = g * k; nr = r; sk = k; }
+    }
+}
+
 extern "C" hipError_t qt_launch_pf_gemm(int epi, const uint16_t *W, const uint16_t *P, int S, int N, int K, float *Y,
-                                        int ldy, float *part, hipStream_t st) {
+                                        int ldy, float *part, long long part_cap, hipStream_t st) {
     constexpr int NST = 4;
     if (S <= 0 || N <= 0 || K <= 0 || N % 64 || K % 64 || epi < 0 || epi > 2) return hipErrorInvalidValue;
     if (epi != QT_PF_SWIGLU ? (ldy < N || ldy % 4) : (ldy < N / 2 || ldy % 2)) return hipErrorInvalidValue;
     const int Sp = qt_pf_spad(S);
-    // the tallest weight tile (256, 128 or 64 rows) that still gives a workgroup per CU:
-    // taller tiles reuse each LDS read of the planes over more rows
-    const int nr = (N % 256 == 0 && (long long)(N / 256) * (Sp / 64) >= 256) ? 4
-                 : (N % 128 == 0 && (long long)(N / 128) * (Sp / 64) >= 256) ? 2 : 1;
+    int nr, sk;
+    qt_pf_plan(S, Sp, N, K, part ? part_cap : 0, nr, sk);
     const int gx = N / (64 * nr);
-    int sk = 1;
-    if (epi == QT_PF_RESID && part)
-        while (sk < 4 && (long long)gx * (Sp / 64) * sk < 256 && (K / 64) % (2 * sk) == 0) sk *= 2;
     const dim3 grid(gx, Sp / 64, sk);
 #define QT_PF_GEMM(E, OUT, LD)                                                                                         \
     if (nr == 4) hipLaunchKernelGGL((k_pf_gemm2<E, 4, 3>), grid, dim3(QT_PF_WG), 0, st, W, P, S, Sp, K, OUT, LD);    \
@@ -407,8 +441,10 @@ extern "C" hipError_t qt_launch_pf_gemm(int epi, const uint16_t *W, const uint16
         QT_PF_GEMM(QT_PF_PART, part, N)
         const hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;
-        hipLaunchKernelGGL(k_pf_reduce, dim3((S * N / 4 + QT_PF_WG - 1) / QT_PF_WG), dim3(QT_PF_WG), 0, st, part, sk, S,
-                           N, Y, ldy);
+        const dim3 rg((S * N / 4 + QT_PF_WG - 1) / QT_PF_WG);
+        if (epi == QT_PF_STORE) hipLaunchKernelGGL(k_pf_reduce<QT_PF_STORE>, rg, dim3(QT_PF_WG), 0, st, part, sk, S, N, Y, ldy);
+        else if (epi == QT_PF_RESID) hipLaunchKernelGGL(k_pf_reduce<QT_PF_RESID>, rg, dim3(QT_PF_WG), 0, st, part, sk, S, N, Y, ldy);
+        else hipLaunchKernelGGL(k_pf_reduce<QT_PF_SWIGLU>, rg, dim3(QT_PF_WG), 0, st, part, sk, S, N, Y, ldy);
     } else if (epi == QT_PF_STORE) {
         QT_PF_GEMM(QT_PF_STORE, Y, ldy)
     } else if (epi == QT_PF_RESID) {

@@ -44,6 +44,10 @@ void qt_seterr(const char *fmt, ...) {
 #define HCK(call) do { hipError_t e_ = (call); if (e_ != hipSuccess) { \
     SETERR("%s:%d %s -> %s", __FILE__, __LINE__, #call, hipGetErrorString(e_)); goto fail; } } while (0)
 #define REQ(cond, ...) do { if (!(cond)) { SETERR(__VA_ARGS__); goto fail; } } while (0)
+/* split-K partials of the bf16 projection GEMMs (prefill, bf16 batch): 32 MiB; the
+ * launcher splits K only while its grid is short of the CUs, which bounds the partials
+ * well inside this, and never beyond it */
+#define PF_PART_FLOATS ((long long)8 << 20)
 
 /* ---- device matrices --------------------------------------------------------------- */
 
@@ -311,7 +315,7 @@ typedef struct {
     dmat_t *pf_qkv, *pf_o, *pf_gu, *pf_dn;
     int pf_cap;             /* positions the buffers below hold */
     float *pf_x, *pf_qkvb, *pf_attn, *pf_h;
-    float *pf_part;         /* split-K partial sums [4][cap][H] */
+    float *pf_part;         /* split-K partial sums, PF_PART_FLOATS */
     uint16_t *pf_p;         /* activation planes [3][spad][max(H, qd, F)] */
 } talker_t;
 
@@ -705,7 +709,7 @@ int qwen_hip_talker_prefill(void *state, const qwen_hip_layer_t *bf16_layers, co
         HCK(hipMalloc((void **)&t->pf_attn, (size_t)seq * qd * sizeof(float)));
         HCK(hipMalloc((void **)&t->pf_h, (size_t)seq * F * sizeof(float)));
         HCK(hipMalloc((void **)&t->pf_p, (size_t)3 * sp * km * sizeof(uint16_t)));
-        HCK(hipMalloc((void **)&t->pf_part, (size_t)4 * seq * H * sizeof(float)));
+        HCK(hipMalloc((void **)&t->pf_part, (size_t)PF_PART_FLOATS * sizeof(float)));
         t->pf_cap = seq;
     }
     HCK(hipMemcpyAsync(t->pf_x, embeds, (size_t)seq * H * sizeof(float), hipMemcpyDefault, t->st));
@@ -713,16 +717,16 @@ int qwen_hip_talker_prefill(void *state, const qwen_hip_layer_t *bf16_layers, co
     for (int l = 0; l < L; l++) {
         const size_t lay = (size_t)l * s->nkv * s->kv_max * s->hd;
         HCK(qt_launch_pf_pieces(t->pf_x, H, seq, H, s->in_norm[l], s->eps, t->pf_p, t->st));
-        HCK(qt_launch_pf_gemm(QT_PF_STORE, (const uint16_t *)wq[l].w, t->pf_p, seq, qkvr, H, t->pf_qkvb, qkvr, NULL, t->st));
+        HCK(qt_launch_pf_gemm(QT_PF_STORE, (const uint16_t *)wq[l].w, t->pf_p, seq, qkvr, H, t->pf_qkvb, qkvr, t->pf_part, PF_PART_FLOATS, t->st));
         HCK(qt_launch_pf_qkv_post(t->pf_qkvb, qkvr, seq, s->nh, s->nkv, s->qn[l], s->kn[l], s->rope_cos, s->rope_sin,
                                   s->eps, s->kc + lay, s->vc + lay, s->kv_max, t->st));
         HCK(qt_launch_pf_attn(t->pf_qkvb, qkvr, seq, s->nh, s->nkv, scale, t->pf_attn, qd, t->st));
         HCK(qt_launch_pf_pieces(t->pf_attn, qd, seq, qd, NULL, 0.f, t->pf_p, t->st));
-        HCK(qt_launch_pf_gemm(QT_PF_RESID, (const uint16_t *)wo[l].w, t->pf_p, seq, H, qd, t->pf_x, H, t->pf_part, t->st));
+        HCK(qt_launch_pf_gemm(QT_PF_RESID, (const uint16_t *)wo[l].w, t->pf_p, seq, H, qd, t->pf_x, H, t->pf_part, PF_PART_FLOATS, t->st));
         HCK(qt_launch_pf_pieces(t->pf_x, H, seq, H, s->post_norm[l], s->eps, t->pf_p, t->st));
-        HCK(qt_launch_pf_gemm(QT_PF_SWIGLU, (const uint16_t *)wgu[l].w, t->pf_p, seq, 2 * F, H, t->pf_h, F, NULL, t->st));
+        HCK(qt_launch_pf_gemm(QT_PF_SWIGLU, (const uint16_t *)wgu[l].w, t->pf_p, seq, 2 * F, H, t->pf_h, F, t->pf_part, PF_PART_FLOATS, t->st));
         HCK(qt_launch_pf_pieces(t->pf_h, F, seq, F, NULL, 0.f, t->pf_p, t->st));
-        HCK(qt_launch_pf_gemm(QT_PF_RESID, (const uint16_t *)wdn[l].w, t->pf_p, seq, H, F, t->pf_x, H, t->pf_part, t->st));
+        HCK(qt_launch_pf_gemm(QT_PF_RESID, (const uint16_t *)wdn[l].w, t->pf_p, seq, H, F, t->pf_x, H, t->pf_part, PF_PART_FLOATS, t->st));
     }
     /* dec_x = the last position's residual (t.c:1032-1033), where get_dec_x reads it */
     HCK(hipMemcpyAsync(t->io + H, t->pf_x + (size_t)(seq - 1) * H, (size_t)H * sizeof(float), hipMemcpyDeviceToDevice, t->st));
@@ -750,16 +754,16 @@ int qwen_hip_talker_prefill_async(void *state, int seq, int n) {
         for (int l = 0; l < L; l++) {
             const size_t lay = (size_t)l * s->nkv * s->kv_max * s->hd;
             HCK(qt_launch_pf_pieces(t->pf_x, H, seq, H, s->in_norm[l], s->eps, t->pf_p, t->st));
-            HCK(qt_launch_pf_gemm(QT_PF_STORE, (const uint16_t *)wq[l].w, t->pf_p, seq, qkvr, H, t->pf_qkvb, qkvr, NULL, t->st));
+            HCK(qt_launch_pf_gemm(QT_PF_STORE, (const uint16_t *)wq[l].w, t->pf_p, seq, qkvr, H, t->pf_qkvb, qkvr, t->pf_part, PF_PART_FLOATS, t->st));
             HCK(qt_launch_pf_qkv_post(t->pf_qkvb, qkvr, seq, s->nh, s->nkv, s->qn[l], s->kn[l], s->rope_cos, s->rope_sin,
                                       s->eps, s->kc + lay, s->vc + lay, s->kv_max, t->st));
             HCK(qt_launch_pf_attn(t->pf_qkvb, qkvr, seq, s->nh, s->nkv, scale, t->pf_attn, qd, t->st));
             HCK(qt_launch_pf_pieces(t->pf_attn, qd, seq, qd, NULL, 0.f, t->pf_p, t->st));
-            HCK(qt_launch_pf_gemm(QT_PF_RESID, (const uint16_t *)wo[l].w, t->pf_p, seq, H, qd, t->pf_x, H, t->pf_part, t->st));
+            HCK(qt_launch_pf_gemm(QT_PF_RESID, (const uint16_t *)wo[l].w, t->pf_p, seq, H, qd, t->pf_x, H, t->pf_part, PF_PART_FLOATS, t->st));
             HCK(qt_launch_pf_pieces(t->pf_x, H, seq, H, s->post_norm[l], s->eps, t->pf_p, t->st));
-            HCK(qt_launch_pf_gemm(QT_PF_SWIGLU, (const uint16_t *)wgu[l].w, t->pf_p, seq, 2 * F, H, t->pf_h, F, NULL, t->st));
+            HCK(qt_launch_pf_gemm(QT_PF_SWIGLU, (const uint16_t *)wgu[l].w, t->pf_p, seq, 2 * F, H, t->pf_h, F, t->pf_part, PF_PART_FLOATS, t->st));
             HCK(qt_launch_pf_pieces(t->pf_h, F, seq, F, NULL, 0.f, t->pf_p, t->st));
-            HCK(qt_launch_pf_gemm(QT_PF_RESID, (const uint16_t *)wdn[l].w, t->pf_p, seq, H, F, t->pf_x, H, t->pf_part, t->st));
+            HCK(qt_launch_pf_gemm(QT_PF_RESID, (const uint16_t *)wdn[l].w, t->pf_p, seq, H, F, t->pf_x, H, t->pf_part, PF_PART_FLOATS, t->st));
         }
     return 0;
 fail:
@@ -1455,7 +1459,7 @@ typedef struct {
     uint16_t *kc, *vc;         /* [B][L][nkv][kv_max][hd] */
     float *x, *qkv, *attn, *h, *hid;
     int8_t *pc; float *ps;     /* activation pieces [Kmax/64][3*Bp][64], scales [Bp] */
-    uint16_t *pf_p; float *pf_part; /* bf16: activation planes [3][64][Kmax], split-K partials [4][B][H] */
+    uint16_t *pf_p; float *pf_part; /* bf16: activation planes [3][64][Kmax], split-K partials (PF_PART_FLOATS) */
     int *g2_part; unsigned *g2_cnt; /* int8: split-K tiles and counters of qt_launch_bgemm2_i8 */
     float *part; unsigned *cnt;
     int *d_pos;                /* [B] */
@@ -1500,7 +1504,7 @@ static batch_t *batch_create(const stack_t *s, int B, int is_cp) {
     HCK(hipMalloc((void **)&bt->ps, (size_t)bt->Bp * sizeof(float)));
     if (s->prec == QWEN_HIP_BF16) {
         HCK(hipMalloc((void **)&bt->pf_p, (size_t)3 * qt_pf_spad(B) * K * sizeof(uint16_t)));
-        HCK(hipMalloc((void **)&bt->pf_part, (size_t)4 * B * s->H * sizeof(float)));
+        HCK(hipMalloc((void **)&bt->pf_part, (size_t)PF_PART_FLOATS * sizeof(float)));
     }
     if (s->prec == QWEN_HIP_INT8) {
         /* workspace of the largest split-K plan over the layer's four projections */
@@ -1541,7 +1545,7 @@ static hipError_t batch_proj(batch_t *bt, const dmat_t *m, int epi, const float 
     if (m->prec == QWEN_HIP_BF16) {
         if ((e = qt_launch_pf_pieces(src, (int)sstride, bt->B, m->cols, nw, s->eps, bt->pf_p, bt->st))) return e;
         return qt_launch_pf_gemm(epi, (const uint16_t *)m->w, bt->pf_p, bt->B, m->rows, m->cols, dst, (int)dstride,
-                                 bt->pf_part, bt->st);
+                                 bt->pf_part, PF_PART_FLOATS, bt->st);
     }
     if ((e = qt_launch_bpieces(src, sstride, nw, s->eps, m->cols, bt->B, bt->Bp, bt->pc, bt->ps, bt->st))) return e;
     if (m->prec == QWEN_HIP_INT8) {
@@ -1775,7 +1779,7 @@ void qwen_hip_matmat_bf16(void *ctx, float *Y, const uint16_t *W, const float *X
         /* weights read once for all B columns: exact bf16 planes of X on the bf16 MFMA */
         HCK(hipMalloc((void **)&dp, (size_t)3 * qt_pf_spad(B) * cols * sizeof(uint16_t)));
         HCK(qt_launch_pf_pieces(dx, cols, B, cols, NULL, 0.f, dp, b->st));
-        HCK(qt_launch_pf_gemm(QT_PF_STORE, (const uint16_t *)m->w, dp, B, rows, cols, dy, rows, NULL, b->st));
+        HCK(qt_launch_pf_gemm(QT_PF_STORE, (const uint16_t *)m->w, dp, B, rows, cols, dy, rows, NULL, 0, b->st));
     } else {
         for (int j = 0; j < B; j++)
             HCK(mv(m, QT_EPI_STORE, 0, dx + (size_t)j * cols, NULL, 0.f, dy + (size_t)j * rows, NULL, NULL, b->st));
@@ -2070,7 +2074,7 @@ int qwen_hip_op_prefill_gemm(float *Y, const uint16_t *W, const float *X, int S,
     HCK(hipMemcpyAsync(dx, X, (size_t)S * K * sizeof(float), hipMemcpyHostToDevice, st));
     if (epi == QT_PF_RESID) HCK(hipMemcpyAsync(dy, Y, (size_t)S * ny * sizeof(float), hipMemcpyHostToDevice, st));
     HCK(qt_launch_pf_pieces(dx, K, S, K, NULL, 0.f, dp, st));
-    HCK(qt_launch_pf_gemm(epi, dw, dp, S, N, K, dy, ny, dpart, st));
+    HCK(qt_launch_pf_gemm(epi, dw, dp, S, N, K, dy, ny, dpart, 4LL * S * N, st));
     HCK(hipMemcpyAsync(Y, dy, (size_t)S * ny * sizeof(float), hipMemcpyDeviceToHost, st));
     HCK(hipStreamSynchronize(st));
     (void)hipFree(dw); (void)hipFree(dx); (void)hipFree(dy); (void)hipFree(dp); (void)hipFree(dpart);
