@@ -88,8 +88,11 @@ __device__ __forceinline__ void qt_vmcnt() {   // wait until at most N vector-me
     __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
 }
 
+// Two waves per SIMD (amdgpu_waves_per_eu(2)): the 256-row tile with two stages fits in
+// 202 registers per lane, so two workgroups share a CU and hide each other's chunk waits
+// (the three-stage 256-row tile held 304 registers, one wave per SIMD).
 template <int EPI, int NR, int NST>
-__global__ __launch_bounds__(QT_PF_WG) void k_pf_gemm2(const uint16_t *__restrict__ W, const uint16_t *__restrict__ P,
+__global__ __launch_bounds__(QT_PF_WG) __attribute__((amdgpu_waves_per_eu(2))) void k_pf_gemm2(const uint16_t *__restrict__ W, const uint16_t *__restrict__ P,
                                                         int S, int Sp, int K, float *Y, int ldy) {
     constexpr int KC = 64, ST = 64, STB = 3 * ST * KC * 2;      // one stage: 24 KiB
     constexpr int NB = STB / 1024 / QT_WAVES;                   // 1-KiB copies per wave per chunk (6)
@@ -407,8 +410,10 @@ extern "C" hipError_t qt_launch_pf_pieces(const float *X, int ldx, int S, int K,
 // barrier) that reaches 256 workgroups, with its K split where needed into 2^k equal
 // ranges of at least four 64-k chunks whose partials fit in part_cap floats (added in
 // order by k_pf_reduce); else the largest grid.  Measured on the 1.7B prefill (128 / 512
-// positions): 4.16 / 9.46 ms, against 4.53 / 10.72 preferring an unsplit shorter tile,
-// 4.50 / 10.22 splitting to 512 workgroups, 4.27 / 9.46 with two-chunk ranges.
+// positions, three-stage 256-row tile): 4.16 / 9.46 ms, against 4.53 / 10.72 preferring an
+// unsplit shorter tile, 4.50 / 10.22 splitting to 512 workgroups, 4.27 / 9.46 with
+// two-chunk ranges; with the two-stage tile at two waves per SIMD 3.94 / 8.73, and
+// splitting to 512 workgroups there 4.50 / 9.56.
 static void qt_pf_plan(int S, int Sp, int N, int K, long long part_cap, int &nr, int &sk) {
     const long long sy = Sp / 64;
     long long best = -1;
@@ -434,7 +439,7 @@ extern "C" hipError_t qt_launch_pf_gemm(int epi, const uint16_t *W, const uint16
     const int gx = N / (64 * nr);
     const dim3 grid(gx, Sp / 64, sk);
 #define QT_PF_GEMM(E, OUT, LD)                                                                                         \
-    if (nr == 4) hipLaunchKernelGGL((k_pf_gemm2<E, 4, 3>), grid, dim3(QT_PF_WG), 0, st, W, P, S, Sp, K, OUT, LD);    \
+    if (nr == 4) hipLaunchKernelGGL((k_pf_gemm2<E, 4, 2>), grid, dim3(QT_PF_WG), 0, st, W, P, S, Sp, K, OUT, LD);    \
     else if (nr == 2) hipLaunchKernelGGL((k_pf_gemm2<E, 2, NST>), grid, dim3(QT_PF_WG), 0, st, W, P, S, Sp, K, OUT, LD); \
     else hipLaunchKernelGGL((k_pf_gemm2<E, 1, NST>), grid, dim3(QT_PF_WG), 0, st, W, P, S, Sp, K, OUT, LD);
     if (sk > 1) {
