@@ -473,10 +473,12 @@ extern "C" hipError_t qt_launch_pf_qkv_post(float *QKV, int ld, int S, int nh, i
 extern "C" hipError_t qt_launch_pf_attn(const float *QKV, int ld, int S, int nh, int nkv, float scale, float *A,
                                         int lda, hipStream_t st) {
     if (S <= 0 || nh <= 0 || nkv <= 0 || nh % nkv) return hipErrorInvalidValue;
-    // 32-query workgroups where 64-query ones would leave CUs idle
+    // 32- or 16-query workgroups where 64-query ones would leave CUs idle
     if ((long long)((S + 63) / 64) * nh >= 256)
         hipLaunchKernelGGL(k_pf_fattn<4>, dim3((S + 63) / 64, nh), dim3(QT_PF_WG), 0, st, QKV, ld, S, nh, nkv, scale, A, lda);
-    else
+    else if ((long long)((S + 31) / 32) * nh >= 256)
         hipLaunchKernelGGL(k_pf_fattn<2>, dim3((S + 31) / 32, nh), dim3(QT_PF_WG), 0, st, QKV, ld, S, nh, nkv, scale, A, lda);
+    else
+        hipLaunchKernelGGL(k_pf_fattn<1>, dim3((S + 15) / 16, nh), dim3(QT_PF_WG), 0, st, QKV, ld, S, nh, nkv, scale, A, lda);
     return hipGetLastError();
 }
