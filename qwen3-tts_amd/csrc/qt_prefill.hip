@@ -88,11 +88,12 @@ __device__ __forceinline__ void qt_vmcnt() {   // wait until at most N vector-me
     __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
 }
 
-// Two waves per SIMD (amdgpu_waves_per_eu(2)): the 256-row tile with two stages fits in
-// 202 registers per lane, so two workgroups share a CU and hide each other's chunk waits
-// (the three-stage 256-row tile held 304 registers, one wave per SIMD).
+// Two waves per SIMD for the two-stage tile (amdgpu_waves_per_eu(2)): the 256-row tile
+// with two stages fits in 202 registers per lane, so two workgroups share a CU and hide
+// each other's chunk waits (the three-stage 256-row tile held 304 registers, one wave per
+// SIMD); the four-stage tiles' 96 KB of LDS allow one workgroup per CU anyway.
 template <int EPI, int NR, int NST>
-__global__ __launch_bounds__(QT_PF_WG) __attribute__((amdgpu_waves_per_eu(2))) void k_pf_gemm2(const uint16_t *__restrict__ W, const uint16_t *__restrict__ P,
+__global__ __launch_bounds__(QT_PF_WG) __attribute__((amdgpu_waves_per_eu(NST == 2 ? 2 : 1))) void k_pf_gemm2(const uint16_t *__restrict__ W, const uint16_t *__restrict__ P,
                                                         int S, int Sp, int K, float *Y, int ldy) {
     constexpr int KC = 64, ST = 64, STB = 3 * ST * KC * 2;      // one stage: 24 KiB
     constexpr int NB = STB / 1024 / QT_WAVES;                   // 1-KiB copies per wave per chunk (6)
@@ -470,10 +471,137 @@ extern "C" hipError_t qt_launch_pf_qkv_post(float *QKV, int ld, int S, int nh, i
     return hipGetLastError();
 }
 
+// ---- causal attention on the f32 matrix cores -----------------------------------------
+// 64 queries of one head per workgroup, 16 per wave, over 64-key blocks staged in LDS (K
+// rows [key][dim]; V transposed, [dim][key]).  v_mfma_f32_16x16x4_f32 (lane l supplies
+// A[l%16][l/16] and B[l/16][l%16], receives D[4(l/16)+r][l%16]) computes the scores
+// transposed, S^T = K . Q^T, with k-step s of lane group g taking dim 32g + s: each lane
+// keeps its query's 32 dims (32g .. 32g+31) in registers and reads a key's four dims of
+// four steps as one float4.  Lane l then holds the scores of query l%16 with keys
+// 16t + 4g + r (tile t, register r) -- exactly the A operand of P.V when k-step s of tile
+// t takes key 16t + 4g + s, so the probabilities never leave the registers; the B
+// operand (4 keys of one dim) is one float4 of the transposed V.  Softmax per block as
+// in k_pf_fattn (scale, causal mask, block max, e^(s - m), running sums), the per-query
+// statistics exchanged across the four lane groups with shuffles; the P.V result rows
+// (queries 4g + r) take their rescale factors from the lanes that own those queries.
+#define QT_PF_VTP 68   // V^T row pitch (64 keys + 4: the float4 reads of a wave spread over banks)
+__global__ __launch_bounds__(QT_PF_WG) void k_pf_fattn_mf(const float *QKV, int ld, int S, int nh, int nkv, float scale,
+                                                           float *A, int lda) {
+    __shared__ __align__(16) float ks[64][QT_PF_KP];
+    __shared__ __align__(16) float vt[128][QT_PF_VTP];
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, li = lane & 15, g = lane >> 4;
+    const int h = blockIdx.y, kvh = h / (nh / nkv);
+    const int q0 = blockIdx.x * 64, qw = q0 + 16 * wave, q = qw + li;
+    const int qd = nh * 128, kvd = nkv * 128;
+    float qf[32];
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        const float4 v = q < S ? *reinterpret_cast<const float4 *>(QKV + (size_t)q * ld + h * 128 + 32 * g + 4 * i)
+                               : make_float4(0.f, 0.f, 0.f, 0.f);
+        qf[4 * i] = v.x; qf[4 * i + 1] = v.y; qf[4 * i + 2] = v.z; qf[4 * i + 3] = v.w;
+    }
+    float m = -INFINITY, l = 0.f;           // statistics of query q (the same in the four lane groups)
+    qt_f32x4 o[8];                          // O[query 4g + r][dim 16 dt + li]
+#pragma unroll
+    for (int dt = 0; dt < 8; dt++) o[dt] = qt_f32x4{0.f, 0.f, 0.f, 0.f};
+    const int nkb = (min(q0 + 64, S) - 1) / 64 + 1;
+    for (int kb = 0; kb < nkb; kb++) {
+        const int j0 = kb * 64;
+        __syncthreads();                                // previous block's K / V reads done
+        for (int i = tid; i < 64 * 32; i += QT_PF_WG) {
+            const int r = i >> 5, c = (i & 31) * 4, j = j0 + r;
+            float4 kv = make_float4(0.f, 0.f, 0.f, 0.f), vv = kv;
+            if (j < S) {
+                kv = *reinterpret_cast<const float4 *>(QKV + (size_t)j * ld + qd + kvh * 128 + c);
+                vv = *reinterpret_cast<const float4 *>(QKV + (size_t)j * ld + qd + kvd + kvh * 128 + c);
+            }
+            *reinterpret_cast<float4 *>(&ks[r][c]) = kv;
+            vt[c][r] = vv.x; vt[c + 1][r] = vv.y; vt[c + 2][r] = vv.z; vt[c + 3][r] = vv.w;
+        }
+        __syncthreads();
+        if (j0 > qw + 15) continue;                     // every query of this wave precedes the block (wave-uniform)
+        qt_f32x4 st[4];
+#pragma unroll
+        for (int t = 0; t < 4; t++) st[t] = qt_f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int s4 = 0; s4 < 8; s4++)
+#pragma unroll
+            for (int t = 0; t < 4; t++) {
+                const float4 kv = *reinterpret_cast<const float4 *>(&ks[16 * t + li][32 * g + 4 * s4]);
+                st[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(kv.x, qf[4 * s4], st[t], 0, 0, 0);
+                st[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(kv.y, qf[4 * s4 + 1], st[t], 0, 0, 0);
+                st[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(kv.z, qf[4 * s4 + 2], st[t], 0, 0, 0);
+                st[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(kv.w, qf[4 * s4 + 3], st[t], 0, 0, 0);
+            }
+        float bm = -INFINITY;
+#pragma unroll
+        for (int t = 0; t < 4; t++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const int j = j0 + 16 * t + 4 * g + r;
+                const float sv = (j <= q && j < S) ? st[t][r] * scale : -INFINITY;
+                st[t][r] = sv;
+                bm = fmaxf(bm, sv);
+            }
+        bm = fmaxf(bm, __shfl_xor(bm, 16));
+        bm = fmaxf(bm, __shfl_xor(bm, 32));
+        const float mn = fmaxf(m, bm);
+        const float mr = mn == -INFINITY ? 0.f : mn;     // a query row past S has no key at all
+        const float alpha = expf(m - mr);
+        float rs = 0.f;
+#pragma unroll
+        for (int t = 0; t < 4; t++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const float pv = expf(st[t][r] - mr);
+                st[t][r] = pv;
+                rs += pv;
+            }
+        rs += __shfl_xor(rs, 16);
+        rs += __shfl_xor(rs, 32);
+        l = l * alpha + rs;
+        m = mn;
+        float ar[4];
+#pragma unroll
+        for (int r = 0; r < 4; r++) ar[r] = __shfl(alpha, 4 * g + r);
+#pragma unroll
+        for (int dt = 0; dt < 8; dt++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) o[dt][r] *= ar[r];
+#pragma unroll
+        for (int t = 0; t < 4; t++)
+#pragma unroll
+            for (int dt = 0; dt < 8; dt++) {
+                const float4 vv = *reinterpret_cast<const float4 *>(&vt[16 * dt + li][16 * t + 4 * g]);
+                o[dt] = __builtin_amdgcn_mfma_f32_16x16x4f32(st[t][0], vv.x, o[dt], 0, 0, 0);
+                o[dt] = __builtin_amdgcn_mfma_f32_16x16x4f32(st[t][1], vv.y, o[dt], 0, 0, 0);
+                o[dt] = __builtin_amdgcn_mfma_f32_16x16x4f32(st[t][2], vv.z, o[dt], 0, 0, 0);
+                o[dt] = __builtin_amdgcn_mfma_f32_16x16x4f32(st[t][3], vv.w, o[dt], 0, 0, 0);
+            }
+    }
+    float lr[4];
+#pragma unroll
+    for (int r = 0; r < 4; r++) lr[r] = 1.0f / __shfl(l, 4 * g + r);
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+        const int qq = qw + 4 * g + r;
+        if (qq >= S) continue;
+#pragma unroll
+        for (int dt = 0; dt < 8; dt++) A[(size_t)qq * lda + h * 128 + 16 * dt + li] = o[dt][r] * lr[r];
+    }
+}
+
 extern "C" hipError_t qt_launch_pf_attn(const float *QKV, int ld, int S, int nh, int nkv, float scale, float *A,
                                         int lda, hipStream_t st) {
     if (S <= 0 || nh <= 0 || nkv <= 0 || nh % nkv) return hipErrorInvalidValue;
-    // 32- or 16-query workgroups where 64-query ones would leave CUs idle
+    // the matrix-core kernel where it has at least 64 workgroups (1.7B prefill, 512
+    // positions: 8.37 ms against 8.72 with the VALU kernel; at 128 positions, 32
+    // workgroups, 3.84 against 3.77), else the VALU kernel with 64-, 32- or 16-query
+    // workgroups, the largest that still fills the CUs
+    if ((long long)((S + 63) / 64) * nh >= 64) {
+        hipLaunchKernelGGL(k_pf_fattn_mf, dim3((S + 63) / 64, nh), dim3(QT_PF_WG), 0, st, QKV, ld, S, nh, nkv, scale, A, lda);
+        return hipGetLastError();
+    }
     if ((long long)((S + 63) / 64) * nh >= 256)
         hipLaunchKernelGGL(k_pf_fattn<4>, dim3((S + 63) / 64, nh), dim3(QT_PF_WG), 0, st, QKV, ld, S, nh, nkv, scale, A, lda);
     else if ((long long)((S + 31) / 32) * nh >= 256)

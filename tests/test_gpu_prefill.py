@@ -63,8 +63,9 @@ def test_op_prefill_gemm_planes_are_exact():
 
 @pytest.mark.parametrize("S,nh,nkv", [(1, 16, 8), (37, 16, 8), (100, 4, 2), (300, 16, 8), (1000, 16, 8)])
 def test_op_prefill_attention(oracle, S, nh, nkv):
-    """The tiled causal attention (32- and 64-query workgroups) against the oracle's f32
-    attention (qwen_causal_attention restated)."""
+    """The tiled causal attention against the oracle's f32 attention (qwen_causal_attention
+    restated): the VALU kernel's 16-query workgroups (S = 1, 37, 100) and the matrix-core
+    kernel (S = 300, 1000)."""
     print(f"[case] prefill attention S={S} nh={nh} nkv={nkv}", flush=True)
     rng = np.random.default_rng(S + nh)
     ld = (nh + 2 * nkv) * 128
