@@ -485,8 +485,8 @@ extern "C" hipError_t qt_launch_pf_qkv_post(float *QKV, int ld, int S, int nh, i
 // statistics exchanged across the four lane groups with shuffles; the P.V result rows
 // (queries 4g + r) take their rescale factors from the lanes that own those queries.
 #define QT_PF_VTP 68   // V^T row pitch (64 keys + 4: the float4 reads of a wave spread over banks)
-__global__ __launch_bounds__(QT_PF_WG) void k_pf_fattn_mf(const float *QKV, int ld, int S, int nh, int nkv, float scale,
-                                                           float *A, int lda) {
+__global__ __launch_bounds__(QT_PF_WG) __attribute__((amdgpu_waves_per_eu(2))) void k_pf_fattn_mf(
+    const float *QKV, int ld, int S, int nh, int nkv, float scale, float *A, int lda) {
     __shared__ __align__(16) float ks[64][QT_PF_KP];
     __shared__ __align__(16) float vt[128][QT_PF_VTP];
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, li = lane & 15, g = lane >> 4;
@@ -505,20 +505,33 @@ __global__ __launch_bounds__(QT_PF_WG) void k_pf_fattn_mf(const float *QKV, int 
 #pragma unroll
     for (int dt = 0; dt < 8; dt++) o[dt] = qt_f32x4{0.f, 0.f, 0.f, 0.f};
     const int nkb = (min(q0 + 64, S) - 1) / 64 + 1;
+    // the next block's K and V rows wait in registers while the current block computes
+    // (thread t: rows t/32 + 8i, float4 column t%32, i < 8)
+    constexpr int NP = 64 * 32 / QT_PF_WG;
+    float4 pk[NP], pv[NP];
+    auto fetch = [&](int j0) {
+#pragma unroll
+        for (int i = 0; i < NP; i++) {
+            const int r = (tid >> 5) + 8 * i, c = (tid & 31) * 4, j = j0 + r;
+            pk[i] = pv[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+            if (j < S) {
+                pk[i] = *reinterpret_cast<const float4 *>(QKV + (size_t)j * ld + qd + kvh * 128 + c);
+                pv[i] = *reinterpret_cast<const float4 *>(QKV + (size_t)j * ld + qd + kvd + kvh * 128 + c);
+            }
+        }
+    };
+    fetch(0);
     for (int kb = 0; kb < nkb; kb++) {
         const int j0 = kb * 64;
         __syncthreads();                                // previous block's K / V reads done
-        for (int i = tid; i < 64 * 32; i += QT_PF_WG) {
-            const int r = i >> 5, c = (i & 31) * 4, j = j0 + r;
-            float4 kv = make_float4(0.f, 0.f, 0.f, 0.f), vv = kv;
-            if (j < S) {
-                kv = *reinterpret_cast<const float4 *>(QKV + (size_t)j * ld + qd + kvh * 128 + c);
-                vv = *reinterpret_cast<const float4 *>(QKV + (size_t)j * ld + qd + kvd + kvh * 128 + c);
-            }
-            *reinterpret_cast<float4 *>(&ks[r][c]) = kv;
-            vt[c][r] = vv.x; vt[c + 1][r] = vv.y; vt[c + 2][r] = vv.z; vt[c + 3][r] = vv.w;
+#pragma unroll
+        for (int i = 0; i < NP; i++) {
+            const int r = (tid >> 5) + 8 * i, c = (tid & 31) * 4;
+            *reinterpret_cast<float4 *>(&ks[r][c]) = pk[i];
+            vt[c][r] = pv[i].x; vt[c + 1][r] = pv[i].y; vt[c + 2][r] = pv[i].z; vt[c + 3][r] = pv[i].w;
         }
         __syncthreads();
+        if (kb + 1 < nkb) fetch(j0 + 64);
         if (j0 > qw + 15) continue;                     // every query of this wave precedes the block (wave-uniform)
         qt_f32x4 st[4];
 #pragma unroll
