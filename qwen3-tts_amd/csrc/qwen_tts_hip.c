@@ -315,6 +315,7 @@ typedef struct {
     dmat_t *pf_qkv, *pf_o, *pf_gu, *pf_dn;
     int pf_cap;             /* positions the buffers below hold */
     float *pf_x, *pf_qkvb, *pf_attn, *pf_h;
+    float *pf_e;            /* the last prefill's embeddings (pf_x becomes the residual stream) */
     float *pf_part;         /* split-K partial sums, PF_PART_FLOATS */
     uint16_t *pf_p;         /* activation planes [3][spad][max(H, qd, F)] */
 } talker_t;
@@ -339,7 +340,7 @@ static void talker_destroy(talker_t *t) {
     void *bufs[] = {t->io, t->d_pos, t->d_frame, t->d_tok, t->d_hist, t->codec_head, t->codec_emb, t->logits,
                     t->smp_hist, t->smp_seed, t->smp_done, t->gen_codes, t->gen_pad,
                     t->ps_layers, t->ps_ring, t->ps_xin, t->ps_epoch, t->ps_err,
-                    t->pf_x, t->pf_qkvb, t->pf_attn, t->pf_h, t->pf_p, t->pf_part};
+                    t->pf_x, t->pf_qkvb, t->pf_attn, t->pf_h, t->pf_p, t->pf_part, t->pf_e};
     for (size_t i = 0; i < sizeof bufs / sizeof bufs[0]; i++) if (bufs[i]) (void)hipFree(bufs[i]);
     if (t->h_in) (void)hipHostFree(t->h_in);
     if (t->h_out) (void)hipHostFree(t->h_out);
@@ -674,9 +675,9 @@ fail:
 }
 
 static void pf_free_bufs(talker_t *t) {
-    void *b[] = {t->pf_x, t->pf_qkvb, t->pf_attn, t->pf_h, t->pf_p, t->pf_part};
+    void *b[] = {t->pf_x, t->pf_qkvb, t->pf_attn, t->pf_h, t->pf_p, t->pf_part, t->pf_e};
     for (size_t i = 0; i < sizeof b / sizeof b[0]; i++) if (b[i]) (void)hipFree(b[i]);
-    t->pf_x = t->pf_qkvb = t->pf_attn = t->pf_h = t->pf_part = NULL; t->pf_p = NULL; t->pf_cap = 0;
+    t->pf_x = t->pf_qkvb = t->pf_attn = t->pf_h = t->pf_part = t->pf_e = NULL; t->pf_p = NULL; t->pf_cap = 0;
 }
 
 int qwen_hip_talker_prefill(void *state, const qwen_hip_layer_t *bf16_layers, const float *embeds, int seq) {
@@ -710,9 +711,11 @@ int qwen_hip_talker_prefill(void *state, const qwen_hip_layer_t *bf16_layers, co
         HCK(hipMalloc((void **)&t->pf_h, (size_t)seq * F * sizeof(float)));
         HCK(hipMalloc((void **)&t->pf_p, (size_t)3 * sp * km * sizeof(uint16_t)));
         HCK(hipMalloc((void **)&t->pf_part, (size_t)PF_PART_FLOATS * sizeof(float)));
+        HCK(hipMalloc((void **)&t->pf_e, (size_t)seq * H * sizeof(float)));
         t->pf_cap = seq;
     }
-    HCK(hipMemcpyAsync(t->pf_x, embeds, (size_t)seq * H * sizeof(float), hipMemcpyDefault, t->st));
+    HCK(hipMemcpyAsync(t->pf_e, embeds, (size_t)seq * H * sizeof(float), hipMemcpyDefault, t->st));
+    HCK(hipMemcpyAsync(t->pf_x, t->pf_e, (size_t)seq * H * sizeof(float), hipMemcpyDeviceToDevice, t->st));
     const float scale = 1.0f / sqrtf((float)s->hd);
     for (int l = 0; l < L; l++) {
         const size_t lay = (size_t)l * s->nkv * s->kv_max * s->hd;
@@ -738,8 +741,9 @@ fail:
     return -1;
 }
 
-/* Benchmark entry: enqueue n prefills of the last prefill's inputs (already on the
- * device) without host synchronisation. */
+/* Benchmark entry: enqueue n prefills of the last prefill's embeddings (kept on the
+ * device) without host synchronisation; each one rewrites the cache rows and dec_x
+ * exactly as that prefill did. */
 int qwen_hip_talker_prefill_async(void *state, int seq, int n) {
     talker_t *t = (talker_t *)state;
     if (!t || t->dead) { SETERR("talker state is dead or NULL"); return -1; }
@@ -750,7 +754,9 @@ int qwen_hip_talker_prefill_async(void *state, int seq, int n) {
     const dmat_t *wgu = s->prec == QWEN_HIP_BF16 ? s->gu : t->pf_gu, *wdn = s->prec == QWEN_HIP_BF16 ? s->dn : t->pf_dn;
     if (!wq) { SETERR("no prefill weights"); return -1; }
     const float scale = 1.0f / sqrtf((float)s->hd);
-    for (int it = 0; it < n; it++)
+    if (!t->pf_e) { SETERR("no prefill inputs"); return -1; }
+    for (int it = 0; it < n; it++) {
+        HCK(hipMemcpyAsync(t->pf_x, t->pf_e, (size_t)seq * H * sizeof(float), hipMemcpyDeviceToDevice, t->st));
         for (int l = 0; l < L; l++) {
             const size_t lay = (size_t)l * s->nkv * s->kv_max * s->hd;
             HCK(qt_launch_pf_pieces(t->pf_x, H, seq, H, s->in_norm[l], s->eps, t->pf_p, t->st));
@@ -765,6 +771,9 @@ int qwen_hip_talker_prefill_async(void *state, int seq, int n) {
             HCK(qt_launch_pf_pieces(t->pf_h, F, seq, F, NULL, 0.f, t->pf_p, t->st));
             HCK(qt_launch_pf_gemm(QT_PF_RESID, (const uint16_t *)wdn[l].w, t->pf_p, seq, H, F, t->pf_x, H, t->pf_part, PF_PART_FLOATS, t->st));
         }
+        HCK(hipMemcpyAsync(t->io + H, t->pf_x + (size_t)(seq - 1) * H, (size_t)H * sizeof(float), hipMemcpyDeviceToDevice,
+                           t->st));
+    }
     return 0;
 fail:
     t->dead = 1;

@@ -114,6 +114,26 @@ def test_prefill_matches_reference_golden(quant):
     tk.free()
 
 
+def test_prefill_async_replays_reproduce_the_prefill():
+    """The benchmark entry qwen_hip_talker_prefill_async replays the last prefill from its
+    kept embeddings: after the cache rows are overwritten with zeros, two replays write
+    back exactly the first prefill's K/V rows and dec_x."""
+    print("[case] prefill async replay", flush=True)
+    tk, g, _ = _tiny_talker(hip.BF16, -1)
+    dx = tk.prefill(g["embeds"])
+    n = g["embeds"].shape[0]
+    k, v = tk.download_kv(n)
+    tk.upload_kv(np.zeros_like(k[:, :n]), np.zeros_like(v[:, :n]), n)
+    z, _ = tk.download_kv(n)
+    assert not z[:, :n].any()
+    hip.check(hip.lib().qwen_hip_talker_prefill_async(tk.h, n, 2), "prefill_async")
+    hip.check(hip.lib().qwen_hip_talker_sync(tk.h), "sync")
+    k2, v2 = tk.download_kv(n)
+    assert np.array_equal(k2[:, :n], k[:, :n]) and np.array_equal(v2[:, :n], v[:, :n])
+    assert np.array_equal(tk.dec_x(), dx)
+    tk.free()
+
+
 @pytest.mark.parametrize("name,seq", [("mini", 100), ("mini17", 40)])
 def test_prefill_matches_oracle_layer_shapes(oracle, name, seq):
     """The 0.6B / 1.7B layer shapes (2 layers) against the oracle prefill, then one decode
