@@ -48,7 +48,7 @@ struct QtAttnArgs {
 };
 
 #define QT_KVB 128   // keys of a chunk staged in LDS at once
-#define QT_B_MIN_CHUNK 384   // batched step: minimum keys per chunk
+#define QT_B_MIN_CHUNK 1536  // batched step: minimum keys per chunk
 
 // 16 bytes per lane from global memory straight into LDS (global_load_lds_dwordx4):
 // lane i's bytes land at dst + 16*i, dst wave-uniform.  Counted by vmcnt like a load.
@@ -61,8 +61,11 @@ __device__ __forceinline__ void qt_lds_copy16(const void *src, void *dst) {
 // of every stream and head are dispatched first and idle chunks last (a kv head per XCD
 // under round-robin dispatch); the merging workgroup computes each output as one
 // weighted sum over the chunks (one thread per output) instead of a half-wave reduction
-// per output.  !BATCH keeps the arithmetic order of the fused step's attention phase,
-// which it must match bit for bit.  Both unroll the key loops over a block with masking.
+// per output.  In a BATCH workgroup each wave streams its own 32-key tiles of the chunk
+// (tiles w, w + 4, ...: its own block rows, its own copies, its own running softmax) with
+// no workgroup barrier in the key loop, and the four wave states are merged at the end;
+// !BATCH keeps the arithmetic order of the fused step's attention phase, which it must
+// match bit for bit (waves share each 128-key block: scores, barrier, P.V per 32 dims).
 template <int HPK, bool PREP, bool BATCH>
 __global__ __launch_bounds__(QT_WG) void k_attn(QtAttnArgs a) {
     const int z = BATCH ? blockIdx.y : blockIdx.z;
@@ -85,9 +88,8 @@ __global__ __launch_bounds__(QT_WG) void k_attn(QtAttnArgs a) {
     const bool append = PREP && (pos >= j0 && pos < j0 + n);
 
     constexpr int PS = 2 + QT_HD;
-    // keys staged per block: BATCH halves the block (half the LDS, so four workgroups
-    // share a CU and hide each other's block chains); !BATCH keeps the fused step's block
-    constexpr int KVB = BATCH ? QT_KVB / 2 : QT_KVB;
+    // keys staged per block (BATCH: wave w's 32-key tiles in block rows 32w .. 32w+31)
+    constexpr int KVB = QT_KVB;
     constexpr int KVBYTES = 2 * KVB * QT_HD * 2, MBYTES = QT_ATT_G * HPK * PS * 4;
     static_assert(KVB % 32 == 0 && KVB <= QT_WAVES * 32, "each wave scores at most one 32-key tile of a block");
     __shared__ __align__(16) uint16_t qp[16][QT_HD];            // query pieces, row 4h+p (qt_attn_mf.h)
@@ -119,11 +121,30 @@ __global__ __launch_bounds__(QT_WG) void k_attn(QtAttnArgs a) {
             }
         }
     };
+    // BATCH: 32-key tile tix of the chunk (keys 32 tix .. +31) into this wave's block rows
+    // 32w .. 32w+31 (same swizzle: it depends on the row's low bits only), eight 1-KiB
+    // copies each for K and V; the appended key is not read (it comes from knew / vnew)
+    auto stage_w = [&](int tix) {
+        const int kb = 32 * tix;
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            const int jl = i * 4 + pg, jj = kb + jl;
+            if (jj < n && !(PREP && j0 + jj == pos)) {
+                const long long row = (long long)(j0 + jj) * a.pos_stride;
+                qt_lds_copy16(Kg + row + qt_kslot(jl, sub) * 8, &s_kv[0][(32 * wave + i * 4) * QT_HD]);
+                qt_lds_copy16(Vg + row + qt_vslot(jl, sub) * 8, &s_kv[1][(32 * wave + i * 4) * QT_HD]);
+            }
+        }
+    };
     // LDS written by global_load_lds is counted by vmcnt, and a workgroup barrier does
     // not wait for it: every staging is followed by an explicit full wait before the
     // barrier that publishes the block to the other waves.
-    // ---- 0. K/V of the first key block in flight before anything else ----
-    stage(0, true, true);
+    // ---- 0. K/V of the first key block (BATCH: each wave's first tile) in flight first ----
+    if (BATCH) {
+        if (32 * wave < n) stage_w(wave);
+    } else {
+        stage(0, true, true);
+    }
 
     // ---- 1. query heads (and the new key/value) ----
     if (PREP) {
@@ -154,7 +175,7 @@ __global__ __launch_bounds__(QT_WG) void k_attn(QtAttnArgs a) {
                 knew[lane] = k0; knew[lane + 64] = k1;
                 vnew[lane] = v0; vnew[lane + 64] = v1;
                 const int r = pos - j0;            // its row in the first staged block
-                if (r < KVB) {
+                if (!BATCH && r < KVB) {
                     s_kv[0][qt_kidx(r, lane)] = k0; s_kv[0][qt_kidx(r, lane + 64)] = k1;
                     s_kv[1][qt_vidx(r, lane)] = v0; s_kv[1][qt_vidx(r, lane + 64)] = v1;
                 }
@@ -166,15 +187,67 @@ __global__ __launch_bounds__(QT_WG) void k_attn(QtAttnArgs a) {
     }
     qt_att_zero_rows<HPK>(&qp[0][0], QT_HD, tid, QT_WG);
     qt_att_zero_rows<HPK>(&pp[0][0], KVB, tid, QT_WG);
-    qt_att_zero_vrows(s_kv[1], min(KVB, n), (min(KVB, n) + 31) & ~31, tid, QT_WG);
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();   // (also: every wave's LDS copies of the first block have landed)
+    if (!BATCH) qt_att_zero_vrows(s_kv[1], min(KVB, n), (min(KVB, n) + 31) & ~31, tid, QT_WG);
+    if (!BATCH) __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();   // (also, !BATCH: every wave's LDS copies of the first block have landed)
 
     // ---- 2. per block (qt_attn_mf.h): wave w scores its k-tile (block rows 32w .. +31),
     // barrier, then takes dims [32w, 32w + 32) of P.V over the k-tiles holding keys ----
     const float scale2 = a.scale * QT_LOG2E;
     QtAttRun run;
     qt_att_run_init(run);
+    if constexpr (BATCH) {
+        // ---- 2b. each wave streams its own 32-key tiles (tix = w, w + 4, ...) with no
+        // workgroup barrier: wait for its copies, put the appended key and zero the value
+        // rows past the chunk, score (qt_att_tiles on k-tile w), P.V over all 128 dims of
+        // that k-tile (four 32-dim slices), fold into the wave's running (m, l, o) ----
+        float wm = -INFINITY, wl = 0.f, wo[4][2];
+#pragma unroll
+        for (int sl = 0; sl < 4; sl++) wo[sl][0] = wo[sl][1] = 0.f;
+        const int ntile = (n + 31) >> 5;
+        for (int tix = wave; tix < ntile; tix += QT_WAVES) {
+            const int kb = 32 * tix, nk = min(32, n - kb);
+            __builtin_amdgcn_s_waitcnt(0);            // this wave's copies have landed
+            const int nrow = pos - j0 - kb;
+            if (PREP && nrow >= 0 && nrow < nk) qt_att_put_kv(s_kv[0], s_kv[1], 32 * wave + nrow, knew, vnew, lane);
+            if (nk < 32) qt_att_zero_vrows(s_kv[1] + 32 * wave * QT_HD, nk, 32, lane, 64);
+            qt_att_tiles<HPK>(&qp[0][0], s_kv[0], &pp[0][0], KVB, &ml[0][0][0], wave, 32 * wave + nk, scale2, lane);
+            float to[4][2], tM = 0.f, tl = 0.f;
+#pragma unroll
+            for (int sl = 0; sl < 4; sl++)
+                qt_att_pv<HPK, 1>(&pp[0][0] + 32 * wave, KVB, &ml[wave][0][0], s_kv[1] + 32 * wave * QT_HD, 32 * sl, lane,
+                                  to[sl], tM, tl);
+            // every LDS read of this tile has returned before the next tile's copies land
+            __builtin_amdgcn_s_waitcnt(0);
+            if (tix + QT_WAVES < ntile) stage_w(tix + QT_WAVES);
+            const float mn = fmaxf(wm, tM);
+            const float fr = qt_exp2(wm - mn), fb = qt_exp2(tM - mn);   // first tile: fr = 0, fb = 1
+            wl = fmaf(wl, fr, tl * fb);
+#pragma unroll
+            for (int sl = 0; sl < 4; sl++) {
+                wo[sl][0] = fmaf(wo[sl][0], fr, to[sl][0] * fb);
+                wo[sl][1] = fmaf(wo[sl][1], fr, to[sl][1] * fb);
+            }
+            wm = mn;
+        }
+        // ---- merge the four waves' states, waves in order, into the per-lane form of
+        // the epilogue (head pg, dims 32 wave + sub and + 16) ----
+        __syncthreads();                              // every wave is done with s_kv
+        float *ws = reinterpret_cast<float *>(s_kvbuf);  // [wave][lane][10]: m, l, o[4][2]
+        {
+            float *me = ws + (wave * 64 + lane) * 10;
+            me[0] = wm; me[1] = wl;
+#pragma unroll
+            for (int sl = 0; sl < 4; sl++) { me[2 + 2 * sl] = wo[sl][0]; me[3 + 2 * sl] = wo[sl][1]; }
+        }
+        __syncthreads();
+#pragma unroll
+        for (int w2 = 0; w2 < QT_WAVES; w2++) {
+            const float *src = ws + (w2 * 64 + lane) * 10;   // same lane: same head pg, same sub
+            const float o2[2] = {src[2 + 2 * wave], src[3 + 2 * wave]};
+            if (src[0] != -INFINITY) qt_att_run_add(run, o2, src[0], src[1]);
+        }
+    } else
     for (int kb = 0; kb < n; kb += KVB) {
         const int nk = min(KVB, n - kb);
         if (kb > 0) {   // chunks longer than one block (caches beyond G*KVB keys)
@@ -305,14 +378,15 @@ extern "C" hipError_t qt_launch_attn(int prep, const float *q, const float *qn, 
 // B independent streams in one launch (the batched step): stream z uses q + z*q_bs,
 // K/V + z*kv_bs (its own cache), position d_pos[z], partials part + z*part_bs, counters
 // cnt + z*n_kv, output out + z*out_bs.  Ragged positions are fine: each stream's chunks
-// follow its own length.  Chunks hold at least QT_B_MIN_CHUNK keys (six 64-key LDS
-// blocks): short streams use few workgroups, fewer partials are merged, and the four
-// workgroups a CU holds overlap each other's block loads and block computations;
-// throughput, not single-stream latency, is what the batch needs.  Measured on the whole
-// batched step (32 ragged streams of 128..4096 keys, 1.7B int8, MI355X): 128-key blocks
-// with a minimum of 128 / 256 / 512 / 1024 keys 3.76 / 3.49 / 3.43 / 3.58 ms/step; 64-key
-// blocks with 256 / 320 / 384 / 448 / 512 / 768 / 1024: 3.16 / 3.13 / 3.13 / 3.22 / 3.24 /
-// 3.20 / 3.28 ms/step (the count of workgroups against the four slots per CU decides).
+// follow its own length.  Chunks hold at least QT_B_MIN_CHUNK keys: short streams use few
+// workgroups, fewer partials are merged, and each wave streams a dozen tiles; throughput,
+// not single-stream latency, is what the batch needs.  Measured on the whole batched step
+// (32 ragged streams of 128..4096 keys, 1.7B int8, MI355X), wave-streamed tiles with a
+// minimum of 256 / 384 / 768 / 1536 / 2048 / 3072 / 4096 keys: 3.30 / 3.20 / 3.17 / 3.08 /
+// 3.20 / 3.41 / 3.59 ms/step.  Shared 128-key blocks (scores, barrier, P.V) had given 3.76 /
+// 3.49 / 3.43 / 3.58 at 128 / 256 / 512 / 1024, and shared 64-key blocks (four workgroups
+// per CU) 3.16 / 3.13 / 3.13 / 3.22 / 3.24 / 3.20 / 3.28 at 256 / 320 / 384 / 448 / 512 /
+// 768 / 1024.
 extern "C" hipError_t qt_launch_attn_b(const float *q, long long q_bs, const float *qn, const float *kn,
                                        const float *rc, const float *rs, float eps, const int *d_pos,
                                        uint16_t *K, uint16_t *V, long long kv_bs, long long pos_stride,
