@@ -406,26 +406,39 @@ extern "C" hipError_t qt_launch_pf_pieces(const float *X, int ldx, int S, int K,
 // part: workspace of 4 * S * N floats for split K (nullable: no split).  The residual
 // projections (few weight rows) split K so the grid fills the CUs; the partial ranges
 // are added in order (deterministic).
-// Tile and K split of a projection: the tallest weight tile (256, 128 or 64 rows; a
-// taller tile reuses each LDS read of the planes over more rows and runs more MFMAs per
-// barrier) that reaches 256 workgroups, with its K split where needed into 2^k equal
-// ranges of at least four 64-k chunks whose partials fit in part_cap floats (added in
-// order by k_pf_reduce); else the largest grid.  Measured on the 1.7B prefill (128 / 512
-// positions, three-stage 256-row tile): 4.16 / 9.46 ms, against 4.53 / 10.72 preferring an
-// unsplit shorter tile, 4.50 / 10.22 splitting to 512 workgroups, 4.27 / 9.46 with
-// two-chunk ranges; with the two-stage tile at two waves per SIMD 3.94 / 8.73, and
-// splitting to 512 workgroups there 4.50 / 9.56.
+// Tile and K split of a projection: a weight tile of 256, 192, 128 or 64 rows (a taller
+// tile reuses each LDS read of the planes over more rows and runs more MFMAs per barrier)
+// with its K split where needed into 2^k equal ranges of at least four 64-k chunks whose
+// partials fit in part_cap floats (added in order by k_pf_reduce), so that the grid
+// reaches 256 workgroups; among such plans the one with the least work on the busiest CU,
+// else the largest grid.  Measured on the 1.7B prefill (128 / 512 positions): with the
+// three-stage 256-row tile 4.16 / 9.46 ms against 4.53 / 10.72 preferring an unsplit
+// shorter tile, 4.50 / 10.22 splitting to 512 workgroups, 4.27 / 9.46 with two-chunk
+// ranges; with the two-stage tiles at two waves per SIMD 3.94 / 8.73 (splitting to 512
+// workgroups 4.50 / 9.56); choosing by the busiest CU's work (192-row tiles for gate|up:
+// 512 workgroups, two on every CU, where 256-row tiles gave 384) 3.64 / 7.79.
 static void qt_pf_plan(int S, int Sp, int N, int K, long long part_cap, int &nr, int &sk) {
+    // per-CU load of a plan: workgroups per CU (ceil over 256) x rows per workgroup / K ranges;
+    // among the plans that reach 256 workgroups the lightest, the taller tile on a tie
     const long long sy = Sp / 64;
     long long best = -1;
+    double bcost = 1e30;
+    bool reach = false;
     nr = 1; sk = 1;
-    for (int r = 4; r >= 1; r >>= 1) {
+    const int rs[4] = {4, 3, 2, 1};
+    for (int ri = 0; ri < 4; ri++) {
+        const int r = rs[ri];
         if (N % (64 * r)) continue;
         const long long g = (long long)(N / (64 * r)) * sy;
         int k = 1;
         while (g * k < 256 && (K / 64) % (2 * k) == 0 && K / 64 / (2 * k) >= 4 && 2LL * k * S * N <= part_cap) k *= 2;
-        if (g * k >= 256) { nr = r; sk = k; return; }
-        if (g * k > best) { best = g * k; nr = r; sk = k; }
+        if (g * k >= 256) {
+            const double cost = (double)((g * k + 255) / 256) * r / k;
+            if (!reach || cost < bcost) { nr = r; sk = k; bcost = cost; }
+            reach = true;
+        } else if (!reach && g * k > best) {
+            best = g * k; nr = r; sk = k;
+        }
     }
 }
 
@@ -441,6 +454,7 @@ extern "C" hipError_t qt_launch_pf_gemm(int epi, const uint16_t *W, const uint16
     const dim3 grid(gx, Sp / 64, sk);
 #define QT_PF_GEMM(E, OUT, LD)                                                                                         \
     if (nr == 4) hipLaunchKernelGGL((k_pf_gemm2<E, 4, 2>), grid, dim3(QT_PF_WG), 0, st, W, P, S, Sp, K, OUT, LD);    \
+    else if (nr == 3) hipLaunchKernelGGL((k_pf_gemm2<E, 3, 2>), grid, dim3(QT_PF_WG), 0, st, W, P, S, Sp, K, OUT, LD); \
     else if (nr == 2) hipLaunchKernelGGL((k_pf_gemm2<E, 2, NST>), grid, dim3(QT_PF_WG), 0, st, W, P, S, Sp, K, OUT, LD); \
     else hipLaunchKernelGGL((k_pf_gemm2<E, 1, NST>), grid, dim3(QT_PF_WG), 0, st, W, P, S, Sp, K, OUT, LD);
     if (sk > 1) {
