@@ -505,13 +505,20 @@ __device__ __forceinline__ qt_v4i q4_unpack16(uint2 w) {
 }
 
 // KB k-blocks of 64 per wave, at most 8 waves (KB = 16 for K > 4096), so a lane may hold
-// 256 registers: two sets of B fragments, the block's MFMA results and the q4 weights.
+// 256 registers: a ring of RING blocks' B fragments, the block's MFMA results and the q4
+// weights.  Every load a block needs is issued well before it: the weights of all KB
+// blocks and the first RING blocks' B fragments at entry (a consumed ring slot is refilled
+// with the block RING ahead; indices clamped to the last block instead of guarded, so the
+// loads are straight-line code and the compiler counts them), and the workgroup's block
+// scales go to LDS at entry, so no block waits on a dependent global load.
 #define QT_BQ_MAXW 8
 template <int NT, int EPI, int KB>
 __global__ __launch_bounds__(QT_BQ_MAXW * 64) void k_bgemm_q4(QtBgQ4Args a) {
     constexpr int BP = NT * 16 / 3, NS = BP / 16;   // padded streams, stream tiles
+    constexpr int RING = KB < 30 / NT ? KB : (30 / NT > 2 ? 30 / NT : 2);
     __shared__ float wred[QT_BQ_MAXW][NS][4][64];   // each wave's partial row sums
     __shared__ float sres[16 * BP], sS[BP];         // residual rows [row][stream], stream scales
+    __shared__ float ssc[16][QT_BQ_MAXW * KB * 2];  // block scales x 2^-14 of the 16 rows
     const int nw = blockDim.x >> 6;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int r0 = blockIdx.x * 16;
@@ -523,14 +530,28 @@ __global__ __launch_bounds__(QT_BQ_MAXW * 64) void k_bgemm_q4(QtBgQ4Args a) {
     const int kw0 = wave * KB * 64;
     const int nkb = max(0, min(KB * 64, a.K - kw0)) >> 6;   // wave-uniform
 
+    const int kl = max(nkb - 1, 0);                          // last block of this wave (clamp)
     uint2 wq[KB];
 #pragma unroll
     for (int kb = 0; kb < KB; kb++)
-        wq[kb] = kb < nkb ? *reinterpret_cast<const uint2 *>(wr + ((kw0 + kb * 64) >> 1) + grp * 8) : make_uint2(0u, 0u);
-    // block scales of the four output rows this lane receives (rows 4*grp + i), times 2^-14
-    const uint16_t *sr[4];
+        wq[kb] = *reinterpret_cast<const uint2 *>(wr + ((kw0 + min(kb, kl) * 64) >> 1) + grp * 8);
+    // B fragments of block kb, ring slot kb % RING
+    auto loadB = [&](qt_v4i (&Bv)[NT], int kb) {
+        const int8_t *pb = a.P + (size_t)((kw0 >> 6) + kb) * cs + (size_t)m * 64 + grp * 16;
 #pragma unroll
-    for (int i = 0; i < 4; i++) sr[i] = a.s16 + (size_t)min(r0 + 4 * grp + i, a.rows - 1) * nb32 + (kw0 >> 5);
+        for (int t = 0; t < NT; t++) {
+            const uint4 pv = *reinterpret_cast<const uint4 *>(pb + (size_t)t * 16 * 64);
+            Bv[t] = qt_v4i{(int)pv.x, (int)pv.y, (int)pv.z, (int)pv.w};
+        }
+    };
+    qt_v4i Br[RING][NT];
+#pragma unroll
+    for (int r = 0; r < RING; r++) loadB(Br[r], min(r, kl));
+    // block scales of the workgroup's 16 rows, times 2^-14, into LDS
+    for (int i = tid; i < 16 * nb32; i += (int)blockDim.x) {
+        const int rl = i / nb32, b = i % nb32;
+        ssc[rl][b] = ref_f16_to_f32(a.s16[(size_t)min(r0 + rl, a.rows - 1) * nb32 + b]) * 0x1p-14f;
+    }
 
     // the epilogue's operands (stream scales, residual rows) into LDS right behind the
     // weight loads, instead of one dependent load per output at the end
@@ -539,6 +560,7 @@ __global__ __launch_bounds__(QT_BQ_MAXW * 64) void k_bgemm_q4(QtBgQ4Args a) {
         sres[i] = (EPI == QT_EPI_RESID && b < a.B && r < a.rows) ? a.out[(size_t)b * a.ostride + r] : 0.f;
     }
     for (int i = tid; i < BP; i += (int)blockDim.x) sS[i] = i < a.B ? a.S[i] : 0.f;
+    __syncthreads();                                // block scales in LDS
     float acc[NS][4];
 #pragma unroll
     for (int s = 0; s < NS; s++)
@@ -548,7 +570,7 @@ __global__ __launch_bounds__(QT_BQ_MAXW * 64) void k_bgemm_q4(QtBgQ4Args a) {
     auto fold = [&](const qt_v4i (&c)[NT], int blk) {
         float d[4];
 #pragma unroll
-        for (int i = 0; i < 4; i++) d[i] = ref_f16_to_f32(sr[i][blk]) * 0x1p-14f;
+        for (int i = 0; i < 4; i++) d[i] = ssc[4 * grp + i][(kw0 >> 5) + blk];
 #pragma unroll
         for (int s = 0; s < NS; s++)
 #pragma unroll
@@ -556,16 +578,6 @@ __global__ __launch_bounds__(QT_BQ_MAXW * 64) void k_bgemm_q4(QtBgQ4Args a) {
                 const int v = (c[s][i] << 14) + (c[NS + s][i] << 7) + c[2 * NS + s][i];
                 acc[s][i] = fmaf((float)v, d[i], acc[s][i]);
             }
-    };
-    // B fragments one k-block ahead (two register sets); the scheduling barrier after each
-    // block keeps the compiler from hoisting every block's loads at once (register spills)
-    auto loadB = [&](qt_v4i (&Bv)[NT], int kb) {
-        const int8_t *pb = a.P + (size_t)((kw0 >> 6) + kb) * cs + (size_t)m * 64 + grp * 16;
-#pragma unroll
-        for (int t = 0; t < NT; t++) {
-            const uint4 pv = *reinterpret_cast<const uint4 *>(pb + (size_t)t * 16 * 64);
-            Bv[t] = qt_v4i{(int)pv.x, (int)pv.y, (int)pv.z, (int)pv.w};
-        }
     };
     auto block = [&](int kb, const qt_v4i (&Bv)[NT]) {
         const qt_v4i A = q4_unpack16(wq[kb]);
@@ -579,18 +591,10 @@ __global__ __launch_bounds__(QT_BQ_MAXW * 64) void k_bgemm_q4(QtBgQ4Args a) {
         for (int t = 0; t < NT; t++) c[t] = __builtin_amdgcn_mfma_i32_16x16x64_i8(A1, Bv[t], Z, 0, 0, 0);
         fold(c, 2 * kb + 1);
     };
-    qt_v4i Bb0[NT], Bb1[NT];
-    if (nkb > 0) loadB(Bb0, 0);
 #pragma unroll
     for (int kb = 0; kb < KB; kb++) {
-        if (kb < nkb) {       // wave-uniform; a guard, not a break, so the loop unrolls fully
-            if (kb + 1 < nkb) {
-                if (kb & 1) loadB(Bb0, kb + 1);
-                else loadB(Bb1, kb + 1);
-            }
-            if (kb & 1) block(kb, Bb1);
-            else block(kb, Bb0);
-        }
+        if (kb < nkb) block(kb, Br[kb % RING]);   // wave-uniform; a guard, not a break, so the loop unrolls fully
+        if (kb + RING < KB) loadB(Br[kb % RING], min(kb + RING, kl));
         __builtin_amdgcn_sched_barrier(0);
     }
     // the waves' partial row sums: each wave parks its own, one barrier, then every output
