@@ -100,6 +100,11 @@ CP_WORKLOADS = {
     "cp-0.6B-int8-frame": ("0.6B", "int8", 500, False),
     "cp-0.6B-int8-frame-prefill2": ("0.6B", "int8", 500, True),
 }
+# the Code Predictor's batched pass (qwen_hip_cp_batch_step): (shape, precision, streams)
+CP_BATCH_WORKLOADS = {
+    "cp-0.6B-int8-b32": ("0.6B", "int8", 32),
+    "cp-0.6B-bf16-b32": ("0.6B", "bf16", 32),
+}
 # Talker prefill of S positions (qwen_talker_prefill): (shape, decode precision, S, default timed prefills)
 PREFILL_WORKLOADS = {
     "talker-1.7B-prefill-S128": ("1.7B", "int8", 128, 20),
@@ -158,7 +163,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=None)
     ap.add_argument("--workload", default="talker-1.7B-int8-b1-L2048", choices=sorted(WORKLOADS) + sorted(BATCH_WORKLOADS) + sorted(CP_WORKLOADS)
                     + sorted(PREFILL_WORKLOADS) + sorted(GROW_WORKLOADS) + sorted(SAMPLED_WORKLOADS)
-                    + sorted(FRAME_WORKLOADS) + sorted(SD_WORKLOADS) + sorted(SD_STREAM_WORKLOADS))
+                    + sorted(FRAME_WORKLOADS) + sorted(SD_WORKLOADS) + sorted(SD_STREAM_WORKLOADS)
+                    + sorted(CP_BATCH_WORKLOADS))
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--kernel-launches", type=int, default=200)
@@ -176,6 +182,8 @@ def main():
         return bench_batch(args)
     if args.workload in CP_WORKLOADS:
         return bench_cp(args)
+    if args.workload in CP_BATCH_WORKLOADS:
+        return bench_cp_batch(args)
     if args.workload in PREFILL_WORKLOADS:
         return bench_prefill(args)
     if args.workload in GROW_WORKLOADS:
@@ -754,6 +762,74 @@ def bench_cp(args):
                      "kernel": "CP frame (per-kernel launches replayed from one hipGraph)",
                      "bytes_per_launch": int(frame_bytes), "avg_us": round(ms * 1e3, 1), "steps_per_launch": 1},
         "cpu_baseline": cpu,
+    }
+    print(json.dumps(out), flush=True)
+
+
+def bench_cp_batch(args):
+    """The Code Predictor's batched pass (qwen_hip_cp_batch_step, the CP twin of the
+    batched ragged step, qwen_tts_batch.h): B streams, each one pass of the 5-layer CP at
+    its own position (drawn in 0..15, advancing one per step), the layer weights read once
+    for all streams, replayed from the batch's hipGraph on device-resident inputs.
+    value = ms per batched pass.  Algorithmic bytes per pass: the layers' weights and norms
+    once + every stream's K/V rows at its length (bf16) + the appended rows."""
+    from qwen3_tts_amd import hip, synth
+    shape_name, prec, B = CP_BATCH_WORKLOADS[args.workload]
+    K = args.steps or 40
+    W = 4 if args.warmup is None else args.warmup
+    s = synth.SHAPES[shape_name]
+    cp_kv = 64
+    if W + K > cp_kv - 20:
+        raise SystemExit(f"cp batch: warmup + steps must stay within the CP cache ({cp_kv - 20})")
+    t0 = time.time()
+    tens = synth.generate(s, 0x5EED0001, 0.0, threads=int(os.environ.get("OMP_NUM_THREADS", "16")),
+                          only=lambda n: n.startswith("talker.code_predictor.") or n == "talker.model.codec_embedding.weight")
+    cp = hip.cp_from_tensors(tens, s, hip.PREC[prec], cp_kv_max=cp_kv)
+    log(f"[bench] cp batch: init {time.time() - t0:.1f}s")
+    rng = np.random.default_rng(0x5EED0003)
+    pos = rng.integers(0, 16, B).astype(np.int32)
+    x = rng.standard_normal((B, s.cp_hidden)).astype(np.float32)
+    cp.batch_step(x, pos)                                 # captures the batch graph
+    L = hip.lib()
+    bt = cp._bh
+    stream = L.qwen_hip_talker_batch_stream(bt)
+    ev = HipEvents()
+    hip.check(L.qwen_hip_talker_batch_step_async(bt, W), "cp batch warmup")
+    hip.check(L.qwen_hip_talker_batch_sync(bt), "sync")
+    ev.device_sync()
+    a, b = ev.event(), ev.event()
+    ev.record(a, stream)
+    hip.check(L.qwen_hip_talker_batch_step_async(bt, K), "cp batch timed")
+    ev.record(b, stream)
+    ms_total = ev.elapsed_ms(a, b)
+    ev.device_sync()
+    ms = ms_total / K
+    wb = (lambda r, c: r * c * 2) if prec == "bf16" else (lambda r, c: r * c + 4 * r)   # int8: + row scales
+    per_layer = 0
+    for r, c in [(s.cp_heads * s.cp_head_dim + 2 * s.cp_kv_heads * s.cp_head_dim, s.cp_hidden),
+                 (s.cp_hidden, s.cp_heads * s.cp_head_dim), (2 * s.cp_inter, s.cp_hidden), (s.cp_hidden, s.cp_inter)]:
+        per_layer += wb(r, c)
+    per_layer += (2 * s.cp_hidden + 2 * s.cp_head_dim) * 4
+    kv_row = 2 * s.cp_kv_heads * s.cp_head_dim * 2            # K and V rows of one position, bf16
+    # position of stream b at timed step i (the graph's first run took pos, then W warmups)
+    kv_pos = sum(int(p) + 1 + W + i + 1 for p in pos for i in range(K)) / K
+    step_bytes = s.cp_layers * (per_layer + kv_pos * kv_row + B * kv_row)
+    gbs = step_bytes / (ms * 1e-3) / 1e9
+    log(f"[bench] cp batch: {ms * 1e3:.1f} us per pass of {B} streams, {gbs:.0f} GB/s algorithmic")
+    cp.free()
+    out = {
+        "metric": "Talker ms/decode-step (0.6B/1.7B, bf16/int8/int4) + achieved HBM GB/s",
+        "value": round(ms, 4), "unit": "ms/batched CP pass", "n_gpus": 1, "steps": K, "warmup": W,
+        "ms_per_step": round(ms, 4), "higher_is_better": False, "scaling": "weak", "vs_baseline": None,
+        "dtype": prec, "data": "synthetic (seeded N(0,0.02) random-init weights, N(0,1) inputs)",
+        "config": {"workload": args.workload, "streams": B, "cp_layers": s.cp_layers, "cp_hidden": s.cp_hidden,
+                   "start_positions": [int(p) for p in pos]},
+        "stream_passes_per_s": round(B * 1000.0 / ms, 1),
+        "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": "batched CP pass (pieces + MFMA projections + batched attention, one hipGraph)",
+                     "bytes_per_launch": int(step_bytes), "avg_us": round(ms * 1e3, 1), "steps_per_launch": 1},
+        "cpu_baseline": None,
     }
     print(json.dumps(out), flush=True)
 
