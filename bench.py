@@ -174,7 +174,7 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build measures one GPU only: the decode path shards as independent "
-                                   "data-parallel streams with no exchange (see DESIGN.md); run --gpus 1"}))
+                                   "data-parallel streams with no exchange between GPUs; run --gpus 1"}))
         sys.exit(2)
 
     _pkg()

@@ -7,8 +7,8 @@
  *   level 2  resident fused steps   (qwen_tts_cuda.h:62-67, qwen_tts_cuda_talker.cu:313-947,
  *            qwen_tts_metal.m:2246-2277 for the device-side CP frame).
  * The reference's level-2 init functions take a qwen_tts_ctx_t*; this ABI takes plain
- * pointers instead (qwen_hip_talker_desc_t), filled from the ctx by a ~40-line glue
- * file on the reference side.  Weight pointers may be host or
+ * pointers instead (qwen_hip_talker_desc_t), filled from the ctx by a short glue file
+ * on the reference side (qwen3-tts_amd/glue/qwen_tts_hip_glue.c).  Weight pointers may be host or
  * device memory; init copies them to the device and never aliases them.
  *
  * Error convention (mirrors the reference: init NULL -> caller stays on CPU):

@@ -1,8 +1,8 @@
 /*
  * qwen_tts_hip_glue.c — reference-side glue between qwen_tts_ctx_t (the reference's
  * qwen_tts.h) and libqwen_tts_hip.so (include/qwen_tts_hip.h).  A maintainer adds this
- * file to the reference's HIP build and calls these functions at the
- * places where the reference delegates to its CUDA backend.  Everything here is a field
+ * file to the reference's build, links libqwen_tts_hip.so, and calls these functions at
+ * the places where the reference delegates to its CUDA backend.  Everything here is a field
  * copy plus the bookkeeping those call sites do (kv_len, dec_x); no arithmetic.
  */
 #include "qwen_tts_hip_glue.h"
