@@ -145,6 +145,42 @@ __device__ __forceinline__ int group_sum_i(int v) {        // exact: integer add
     return __builtin_amdgcn_readlane(v, 63);
 }
 
+// One reduce-scatter step over the first N values: the lane and its DPP partner differ
+// in one lane bit (`hi`); each keeps the half of the N values that bit selects and adds
+// the partner's copy of that half, so the first N/2 entries then hold pair sums.
+template <int CTRL, int N, int V>
+__device__ __forceinline__ void qt_scatter_step(int (&v)[V], bool hi) {
+#pragma unroll
+    for (int k = 0; k < N / 2; k++) {
+        const int send = hi ? v[k] : v[k + N / 2], keep = hi ? v[k + N / 2] : v[k];
+        v[k] = keep + __builtin_amdgcn_update_dpp(0, send, CTRL, 0xf, 0xf, false);
+    }
+}
+// Exact wave-wide sums of V = 4, 8 or 16 integers per lane, returned uniform.  Inside
+// each 16-lane row a reduce-scatter over the partners lane^15 (row mirror), lane^7
+// (half-row mirror), lane^2 and lane^1 leaves value i's row sum in the lanes whose bits
+// 3..0 spell i (in the top log2 V of them); the four rows are then added with the
+// row-pair and half-wave swaps, and value i is read from lane i*16/V.  About 3V lane
+// moves and selects instead of the 6V of V separate reductions; integer adds, so the
+// result does not depend on the order.
+template <int V>
+__device__ __forceinline__ void wave_sum_i_scatter(int (&v)[V], int (&out)[V]) {
+    static_assert(V == 4 || V == 8 || V == 16, "values");
+    const int lane = threadIdx.x & 63;
+    qt_scatter_step<DPP_MIRROR, V>(v, lane & 8);
+    qt_scatter_step<DPP_HALF_MIRROR, V / 2>(v, lane & 4);
+    if constexpr (V >= 8) qt_scatter_step<DPP_QXOR2, V / 4>(v, lane & 2);
+    else v[0] += __builtin_amdgcn_update_dpp(0, v[0], DPP_QXOR2, 0xf, 0xf, false);
+    if constexpr (V >= 16) qt_scatter_step<DPP_QXOR1, V / 8>(v, lane & 1);
+    else v[0] += __builtin_amdgcn_update_dpp(0, v[0], DPP_QXOR1, 0xf, 0xf, false);
+    const auto p = __builtin_amdgcn_permlane16_swap(v[0], v[0], false, false);   // rows 0+1, 2+3
+    const int t = (int)p[0] + (int)p[1];
+    const auto q = __builtin_amdgcn_permlane32_swap(t, t, false, false);         // halves
+    const int u = (int)q[0] + (int)q[1];
+#pragma unroll
+    for (int i = 0; i < V; i++) out[i] = __builtin_amdgcn_readlane(u, i * (16 / V));
+}
+
 // ---- exact int8 activation pieces (every int8 matvec) ----------------------------------
 // An f32 activation vector v is written as one 30-bit integer per element with one
 // power-of-two scale: s = 2^(e-29), 2^e <= m = max|v| < 2^(e+1), Y = rint(v/s), so

@@ -222,19 +222,29 @@ __global__ __launch_bounds__(QT_WG) void k_mv(QtMvArgs a) {
     }
 
     float acc[NR];
+    if (PREC == QT_INT8) {
+        // the 4*NR plane sums (row r, plane q at 4r+q), exact in int32
+        int d[4 * NR], D[4 * NR];
 #pragma unroll
-    for (int r = 0; r < NR; r++) {
-        if (PREC == QT_INT8) {
-            int d[4] = {0, 0, 0, 0};
+        for (int i = 0; i < 4 * NR; i++) d[i] = 0;
+#pragma unroll
+        for (int r = 0; r < NR; r++)
 #pragma unroll
             for (int j = 0; j < CPL; j++)
 #pragma unroll
-                for (int q = 0; q < 4; q++) d[q] = qt_dot16(wv[r][j], pl[j][q], d[q]);
+                for (int q = 0; q < 4; q++) d[4 * r + q] = qt_dot16(wv[r][j], pl[j][q], d[4 * r + q]);
+        if constexpr (LPR == 64) {
+            wave_sum_i_scatter<4 * NR>(d, D);
+        } else {
 #pragma unroll
-            for (int q = 0; q < 4; q++) d[q] = group_sum_i<LPR>(d[q]);
-            acc[r] = qt_pc_dot(d[0], d[1], d[2], d[3], pcs);
-            continue;
+            for (int i = 0; i < 4 * NR; i++) D[i] = group_sum_i<LPR>(d[i]);
         }
+#pragma unroll
+        for (int r = 0; r < NR; r++) acc[r] = qt_pc_dot(D[4 * r], D[4 * r + 1], D[4 * r + 2], D[4 * r + 3], pcs);
+    }
+#pragma unroll
+    for (int r = 0; r < NR; r++) {
+        if (PREC == QT_INT8) continue;
         float s = 0.f;
 #pragma unroll
         for (int j = 0; j < CPL; j++) {
@@ -392,13 +402,16 @@ static hipError_t launch_generic(const QtMvArgs &a, hipStream_t st) {
 }
 
 // Rows per lane-group: the largest of {4, 2, 1} (at most NRMAX) that still gives >= 2048
-// waves (two per SIMD on 256 CUs); SwiGLU needs gate/up row pairs, so NR >= 2 there.
+// waves (two per SIMD on 256 CUs), >= 1024 for int8, whose per-wave input work (norm, max,
+// the four activation planes) is shared by more rows that way; SwiGLU needs gate/up row
+// pairs, so NR >= 2 there.
 template <int PREC, int LPR, int CPL, int NRMAX, int EPI, bool NORM>
 static hipError_t launch_nr(const QtMvArgs &a, hipStream_t st) {
     constexpr int G = 64 / LPR;
+    constexpr int MW = PREC == QT_INT8 ? 1024 : 2048;
     const int rows = a.M.rows;
-    if (NRMAX >= 4 && rows / (4 * G) >= 2048) return launch_tuned<PREC, LPR, CPL, 4, EPI, NORM>(a, st);
-    if (NRMAX >= 2 && (EPI == QT_EPI_SWIGLU || rows / (2 * G) >= 2048))
+    if (NRMAX >= 4 && rows / (4 * G) >= MW) return launch_tuned<PREC, LPR, CPL, 4, EPI, NORM>(a, st);
+    if (NRMAX >= 2 && (EPI == QT_EPI_SWIGLU || rows / (2 * G) >= MW))
         return launch_tuned<PREC, LPR, CPL, 2, EPI, NORM>(a, st);
     if (EPI == QT_EPI_SWIGLU) return launch_tuned<PREC, LPR, CPL, 2, EPI, NORM>(a, st);
     return launch_tuned<PREC, LPR, CPL, 1, EPI, NORM>(a, st);
