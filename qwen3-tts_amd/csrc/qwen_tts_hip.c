@@ -1031,7 +1031,7 @@ typedef struct {
     uint16_t *cp_emb[15];
     uint16_t *talker_emb;
     dmat_t mtp; int has_mtp; float *mtp_bias;
-    float *x, *x1, *ebuf, *logits, *th;   /* device */
+    float *x, *ebuf, *logits, *th;   /* device */
     int *d_posv;                          /* [64]: 0..63, per-pass positions */
     int *d_codes;                         /* [16]: [0] = code0, [1..15] = out codes */
     float *h_x; int *h_codes;             /* pinned */
@@ -1052,7 +1052,7 @@ static void cp_destroy(cp_t *c) {
     stack_free(&c->s);
     for (int g = 0; g < 15; g++) { dmat_free(&c->lm[g]); if (c->cp_emb[g]) (void)hipFree(c->cp_emb[g]); }
     dmat_free(&c->mtp);
-    void *bufs[] = {c->talker_emb, c->mtp_bias, c->x, c->x1, c->ebuf, c->logits, c->th, c->d_posv, c->d_codes, c->d_steppos,
+    void *bufs[] = {c->talker_emb, c->mtp_bias, c->x, c->ebuf, c->logits, c->th, c->d_posv, c->d_codes, c->d_steppos,
                     c->x2, c->qkv2, c->attn2, c->h2, c->pc2, c->ps2};
     for (size_t i = 0; i < sizeof bufs / sizeof bufs[0]; i++) if (bufs[i]) (void)hipFree(bufs[i]);
     if (c->h_x) (void)hipHostFree(c->h_x);
@@ -1097,7 +1097,6 @@ void *qwen_hip_cp_init(const qwen_hip_cp_desc_t *d) {
     }
     int E = c->emb_dim > c->talker_hidden ? c->emb_dim : c->talker_hidden;
     HCK(hipMalloc((void **)&c->x, (size_t)H * sizeof(float)));
-    HCK(hipMalloc((void **)&c->x1, (size_t)H * sizeof(float)));
     HCK(hipMalloc((void **)&c->ebuf, (size_t)E * sizeof(float)));
     HCK(hipMalloc((void **)&c->th, (size_t)E * sizeof(float)));
     HCK(hipMalloc((void **)&c->logits, (size_t)c->codebook * sizeof(float)));
@@ -1232,28 +1231,37 @@ static hipError_t cp_frame_body(void *a) {
     cp_t *c = (cp_t *)a;
     hipError_t e;
     const int H = c->s.H;
+    /* Without the mtp projection an embedding row is the next pass's input itself, so the
+     * gathers write straight into the residual buffers (no copy kernel). */
+    const int mtp = c->has_mtp;
     if (c->prefill2) {
         if ((e = cp_project(c, c->th, c->x2))) return e;
-        if ((e = qt_launch_gather(c->d_codes, c->codec_vocab, c->talker_emb, c->talker_hidden, c->ebuf, c->st))) return e;
-        if ((e = cp_project(c, c->ebuf, c->x2 + H))) return e;
+        if ((e = qt_launch_gather(c->d_codes, c->codec_vocab, c->talker_emb, c->talker_hidden,
+                                  mtp ? c->ebuf : c->x2 + H, c->st))) return e;
+        if (mtp && (e = cp_project(c, c->ebuf, c->x2 + H))) return e;
         if ((e = cp_prefill2_body(c))) return e;
         if ((e = qt_launch_copy_f32(c->x2 + H, c->x, H, c->st))) return e;
     } else {
+        /* pass 0 on the projected Talker hidden state; code0's embedding, the input of
+         * pass 1, is looked up once pass 0 has consumed x */
         if ((e = cp_project(c, c->th, c->x))) return e;
-        if ((e = qt_launch_gather(c->d_codes, c->codec_vocab, c->talker_emb, c->talker_hidden, c->ebuf, c->st))) return e;
-        if ((e = cp_project(c, c->ebuf, c->x1))) return e;
         if ((e = stack_body(&c->s, c->x, c->d_posv + 0, c->st))) return e;
-        if ((e = qt_launch_copy_f32(c->x1, c->x, H, c->st))) return e;
+        if ((e = qt_launch_gather(c->d_codes, c->codec_vocab, c->talker_emb, c->talker_hidden,
+                                  mtp ? c->ebuf : c->x, c->st))) return e;
+        if (mtp && (e = cp_project(c, c->ebuf, c->x))) return e;
         if ((e = stack_body(&c->s, c->x, c->d_posv + 1, c->st))) return e;
     }
     for (int g = 0; g < 15; g++) {
         if (g > 0) {
-            if ((e = qt_launch_gather(c->d_codes + g, c->codebook, c->cp_emb[g - 1], c->emb_dim, c->ebuf, c->st))) return e;
-            if ((e = cp_project(c, c->ebuf, c->x))) return e;
+            if (mtp && (e = cp_project(c, c->ebuf, c->x))) return e;
             if ((e = stack_body(&c->s, c->x, c->d_posv + g + 1, c->st))) return e;
         }
         if ((e = mv(&c->lm[g], QT_EPI_STORE, 1, c->x, c->s.final_norm, c->s.eps, c->logits, NULL, NULL, c->st))) return e;
-        if ((e = qt_launch_select(c->logits, c->codebook, 0, NULL, 0, c->d_codes + g + 1, NULL, 0, NULL, 0, NULL, NULL, c->st))) return e;
+        /* the argmax also gathers code g+1's row of the next embedding table (the input
+         * of pass g+2), the lookup of qwen_tts_code_predictor.c:1008-1017 */
+        if ((e = qt_launch_select(c->logits, c->codebook, 0, NULL, 0, c->d_codes + g + 1, NULL, 0,
+                                  g < 14 ? c->cp_emb[g] : NULL, c->emb_dim, mtp ? c->ebuf : c->x, NULL, c->st)))
+            return e;
     }
     return hipSuccess;
 }
