@@ -49,13 +49,33 @@ extern "C" hipError_t qt_launch_rmsnorm(const float *x, const float *w, float *o
 }
 
 // Per-row RMSNorm of `rows` vectors of length n (per-head norm, k.c:486-577), in place.
+// Lane t accumulates r[t], r[t + 64], ... in index order; the loads go out eight at a time
+// (one memory round trip per 512 elements, not per 64), the sums in the same order.
 __global__ __launch_bounds__(64) void k_rmsnorm_rows(float *x, const float *w, int n, float eps) {
     float *r = x + (size_t)blockIdx.x * n;
     float ss = 0.f;
-    for (int i = threadIdx.x; i < n; i += 64) ss += r[i] * r[i];
+    for (int i0 = threadIdx.x; i0 < n; i0 += 64 * 8) {
+        float v[8];
+#pragma unroll
+        for (int k = 0; k < 8; k++) v[k] = i0 + 64 * k < n ? r[i0 + 64 * k] : 0.f;
+#pragma unroll
+        for (int k = 0; k < 8; k++)
+            if (i0 + 64 * k < n) ss += v[k] * v[k];
+    }
     ss = group_sum<64>(ss);
     float inv = 1.0f / sqrtf(ss / (float)n + eps);
-    for (int i = threadIdx.x; i < n; i += 64) r[i] = (r[i] * inv) * w[i];
+    for (int i0 = threadIdx.x; i0 < n; i0 += 64 * 8) {
+        float v[8], g[8];
+#pragma unroll
+        for (int k = 0; k < 8; k++) {
+            const bool ok = i0 + 64 * k < n;
+            v[k] = ok ? r[i0 + 64 * k] : 0.f;
+            g[k] = ok ? w[i0 + 64 * k] : 0.f;
+        }
+#pragma unroll
+        for (int k = 0; k < 8; k++)
+            if (i0 + 64 * k < n) r[i0 + 64 * k] = (v[k] * inv) * g[k];
+    }
 }
 
 extern "C" hipError_t qt_launch_rmsnorm_rows(float *x, const float *w, int rows, int n, float eps,
