@@ -45,6 +45,8 @@ hipError_t qt_launch_advance_pos(int *pos, int n, hipStream_t st);
 hipError_t qt_launch_rmsnorm(const float *x, const float *w, float *out, int n, float eps, int *d_pos,
                              hipStream_t st);
 hipError_t qt_launch_rmsnorm_rows(float *x, const float *w, int rows, int n, float eps, hipStream_t st);
+hipError_t qt_launch_rmsnorm_rows_to(const float *x, float *out, const float *w, int rows, int n, float eps,
+                                    int *pos, hipStream_t st);
 hipError_t qt_launch_swiglu(const float *gu, float *out, int n, hipStream_t st);
 hipError_t qt_launch_sample(const float *logits, int n, int rule, int frame, float eos_boost, float temp,
                             int top_k, float top_p, float rep, const int *prev, int n_prev, uint32_t *seed, int *tok,

@@ -49,10 +49,15 @@ extern "C" hipError_t qt_launch_rmsnorm(const float *x, const float *w, float *o
 }
 
 // Per-row RMSNorm of `rows` vectors of length n (per-head norm, k.c:486-577), in place.
-// Lane t accumulates r[t], r[t + 64], ... in index order; the loads go out eight at a time
+// Per-row RMSNorm of `rows` vectors of length n (per-head norm, k.c:486-577): out row b =
+// RMSNorm(x row b) * w (in place when out == x); pos != NULL: workgroup b also advances
+// pos[b] (the batched step's position advance, folded into its final norm).
+// Lane t accumulates x[t], x[t + 64], ... in index order; the loads go out eight at a time
 // (one memory round trip per 512 elements, not per 64), the sums in the same order.
-__global__ __launch_bounds__(64) void k_rmsnorm_rows(float *x, const float *w, int n, float eps) {
-    float *r = x + (size_t)blockIdx.x * n;
+__global__ __launch_bounds__(64) void k_rmsnorm_rows(const float *x, float *out, const float *w, int n, float eps,
+                                                     int *pos) {
+    const float *r = x + (size_t)blockIdx.x * n;
+    float *o = out + (size_t)blockIdx.x * n;
     float ss = 0.f;
     for (int i0 = threadIdx.x; i0 < n; i0 += 64 * 8) {
         float v[8];
@@ -74,13 +79,19 @@ __global__ __launch_bounds__(64) void k_rmsnorm_rows(float *x, const float *w, i
         }
 #pragma unroll
         for (int k = 0; k < 8; k++)
-            if (i0 + 64 * k < n) r[i0 + 64 * k] = (v[k] * inv) * g[k];
+            if (i0 + 64 * k < n) o[i0 + 64 * k] = (v[k] * inv) * g[k];
     }
+    if (pos && threadIdx.x == 0) pos[blockIdx.x] += 1;
 }
 
 extern "C" hipError_t qt_launch_rmsnorm_rows(float *x, const float *w, int rows, int n, float eps,
                                              hipStream_t st) {
-    hipLaunchKernelGGL(k_rmsnorm_rows, dim3(rows), dim3(64), 0, st, x, w, n, eps);
+    hipLaunchKernelGGL(k_rmsnorm_rows, dim3(rows), dim3(64), 0, st, x, x, w, n, eps, (int *)NULL);
+    return hipGetLastError();
+}
+extern "C" hipError_t qt_launch_rmsnorm_rows_to(const float *x, float *out, const float *w, int rows, int n,
+                                                float eps, int *pos, hipStream_t st) {
+    hipLaunchKernelGGL(k_rmsnorm_rows, dim3(rows), dim3(64), 0, st, x, out, w, n, eps, pos);
     return hipGetLastError();
 }
 

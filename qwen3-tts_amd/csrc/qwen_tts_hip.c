@@ -1593,10 +1593,9 @@ static hipError_t batch_body(void *arg) {
         if ((e = batch_proj(bt, &s->gu[l], QT_EPI_SWIGLU, s->post_norm[l], bt->x, H, bt->h, F))) return e;
         if ((e = batch_proj(bt, &s->dn[l], QT_EPI_RESID, NULL, bt->h, F, bt->x, H))) return e;
     }
-    if ((e = qt_launch_advance_pos(bt->d_pos, bt->B, bt->st))) return e;
-    if (bt->is_cp) return hipSuccess;
-    if ((e = hipMemcpyAsync(bt->hid, bt->x, (size_t)bt->B * H * sizeof(float), hipMemcpyDeviceToDevice, bt->st))) return e;
-    return qt_launch_rmsnorm_rows(bt->hid, s->final_norm, bt->B, H, s->eps, bt->st);
+    if (bt->is_cp) return qt_launch_advance_pos(bt->d_pos, bt->B, bt->st);
+    /* hid = final_norm(x) per stream, positions advanced by the same launch */
+    return qt_launch_rmsnorm_rows_to(bt->x, bt->hid, s->final_norm, bt->B, H, s->eps, bt->d_pos, bt->st);
 }
 
 /* One batched step: x[b] <- in[b] (host), positions <- pos_arr, run, out[b] <- hid or x. */
