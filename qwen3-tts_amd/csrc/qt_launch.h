@@ -97,11 +97,18 @@ hipError_t qt_launch_pf_pieces(const float *X, int ldx, int S, int K, const floa
 /* part: split-K partials (part_cap floats; NULL: never split) */
 hipError_t qt_launch_pf_gemm(int epi, const uint16_t *W, const uint16_t *P, int S, int N, int K, float *Y, int ldy,
                              float *part, long long part_cap, hipStream_t st);
+/* SwiGLU projection whose h goes out as the next projection's three input planes (S*N <= part_cap) */
+hipError_t qt_launch_pf_gemm_swiglu_planes(const uint16_t *W, const uint16_t *P, int S, int N, int K, uint16_t *Pout,
+                                           float *part, long long part_cap, hipStream_t st);
 hipError_t qt_launch_pf_qkv_post(float *QKV, int ld, int S, int nh, int nkv, const float *qn, const float *kn,
                                  const float *rc, const float *rs, float eps, uint16_t *kc, uint16_t *vc,
                                  long long kv_max, hipStream_t st);
 hipError_t qt_launch_pf_attn(const float *QKV, int ld, int S, int nh, int nkv, float scale, float *A, int lda,
                              hipStream_t st);
+/* as qt_launch_pf_attn; where the VALU kernel runs, the output goes out as the O projection's
+ * input planes P instead and *planes = 1 */
+hipError_t qt_launch_pf_attn_planes(const float *QKV, int ld, int S, int nh, int nkv, float scale, float *A, int lda,
+                                    uint16_t *P, int *planes, hipStream_t st);
 
 /* speech decoder (qt_sd.hip) */
 hipError_t qt_launch_sd_gemm(const float *X, int ldx, int Tx, int xlo, const float *W, int K, int N, int ntap, const int *off,

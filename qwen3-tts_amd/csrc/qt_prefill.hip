@@ -202,11 +202,7 @@ __global__ __launch_bounds__(QT_PF_WG) __attribute__((amdgpu_waves_per_eu(NST ==
 // acc = sum over the nz K ranges of part[z][s][n..n+3], ranges in order (each range's
 // loads issued before the adds), then the projection's epilogue: Y = acc (STORE),
 // Y += acc (RESID), or the SwiGLU of the interleaved gate|up pairs into Y[s][n/2..n/2+1].
-template <int EPI>
-__global__ __launch_bounds__(QT_PF_WG) void k_pf_reduce(const float *part, int nz, int S, int N, float *Y, int ldy) {
-    const int i = blockIdx.x * QT_PF_WG + threadIdx.x;
-    if (i >= S * N / 4) return;
-    const int s = i / (N / 4), n = 4 * (i % (N / 4));
+__device__ __forceinline__ float4 pf_sum_ranges(const float *part, int nz, int S, int N, int s, int n) {
     float4 acc = *reinterpret_cast<const float4 *>(part + (size_t)s * N + n);
     constexpr int ZB = 8;
     for (int z0 = 1; z0 < nz; z0 += ZB) {
@@ -218,6 +214,15 @@ __global__ __launch_bounds__(QT_PF_WG) void k_pf_reduce(const float *part, int n
         for (int k = 0; k < ZB; k++)
             if (z0 + k < nz) { acc.x += v[k].x; acc.y += v[k].y; acc.z += v[k].z; acc.w += v[k].w; }
     }
+    return acc;
+}
+
+template <int EPI>
+__global__ __launch_bounds__(QT_PF_WG) void k_pf_reduce(const float *part, int nz, int S, int N, float *Y, int ldy) {
+    const int i = blockIdx.x * QT_PF_WG + threadIdx.x;
+    if (i >= S * N / 4) return;
+    const int s = i / (N / 4), n = 4 * (i % (N / 4));
+    const float4 acc = pf_sum_ranges(part, nz, S, N, s, n);
     if constexpr (EPI == QT_PF_SWIGLU) {
         *reinterpret_cast<float2 *>(Y + (size_t)s * ldy + (n >> 1)) =
             make_float2(acc.x / (1.0f + expf(-acc.x)) * acc.y, acc.z / (1.0f + expf(-acc.z)) * acc.w);
@@ -230,6 +235,34 @@ __global__ __launch_bounds__(QT_PF_WG) void k_pf_reduce(const float *part, int n
             *y = acc;
         }
     }
+}
+
+// The SwiGLU epilogue of the summed K ranges written straight as the three planes of h,
+// the down projection's input (F = N/2 columns, P[p][s][F], plane stride Sp*F; rows
+// S <= s < Sp zero): the same h values and the same pieces as k_pf_reduce<SWIGLU> followed
+// by k_pf_pieces, one launch fewer.
+__global__ __launch_bounds__(QT_PF_WG) void k_pf_reduce_swiglu_planes(const float *part, int nz, int S, int Sp, int N,
+                                                                      uint16_t *P) {
+    const int i = blockIdx.x * QT_PF_WG + threadIdx.x;
+    if (i >= Sp * N / 4) return;
+    const int s = i / (N / 4), n = 4 * (i % (N / 4));
+    const int F = N / 2;
+    const size_t plane = (size_t)Sp * F;
+    uint16_t *dst = P + (size_t)s * F + (n >> 1);
+    if (s >= S) {
+#pragma unroll
+        for (int p = 0; p < 3; p++) *reinterpret_cast<uint32_t *>(dst + p * plane) = 0u;
+        return;
+    }
+    const float4 acc = pf_sum_ranges(part, nz, S, N, s, n);
+    // rounded products (__fmul_rn: no contraction into the piece split), as stored by k_pf_reduce
+    const float h0 = __fmul_rn(acc.x / (1.0f + expf(-acc.x)), acc.y), h1 = __fmul_rn(acc.z / (1.0f + expf(-acc.z)), acc.w);
+    uint16_t pc[3][2];
+    qt_put_pieces(&pc[0][0], 2, h0);
+    qt_put_pieces(&pc[0][1], 2, h1);
+#pragma unroll
+    for (int p = 0; p < 3; p++)
+        *reinterpret_cast<uint32_t *>(dst + p * plane) = (uint32_t)pc[p][0] | ((uint32_t)pc[p][1] << 16);
 }
 
 // ---- per-head q/k norm, RoPE, KV store ---------------------------------------------
@@ -278,9 +311,12 @@ __global__ __launch_bounds__(QT_PF_WG) void k_pf_qkv_post(float *QKV, int ld, in
 // DPP row, so row max and row sum are 16-lane reductions.  K rows are padded to 132
 // floats so the 16 key rows a wave reads at one offset fall in 16 different bank groups.
 #define QT_PF_KP 132
+// P != NULL: the output goes out as the three planes of the O projection's input
+// (P[p][s][nh*128], plane stride Sp*nh*128; the same pieces k_pf_pieces makes of the f32
+// output), and the workgroup of the last query tile zeroes rows S <= s < Sp of its head.
 template <int QA>   // queries per thread: 16 * QA queries per workgroup
 __global__ __launch_bounds__(QT_PF_WG) void k_pf_fattn(const float *QKV, int ld, int S, int nh, int nkv, float scale,
-                                                        float *A, int lda) {
+                                                        float *A, int lda, uint16_t *P, int Sp) {
     constexpr int QB = 16 * QA;
     __shared__ __align__(16) float qs[QB][128];
     __shared__ __align__(16) float ks[64][QT_PF_KP];
@@ -377,6 +413,34 @@ __global__ __launch_bounds__(QT_PF_WG) void k_pf_fattn(const float *QKV, int ld,
             }
         }
     }
+    if (P) {
+        const int K = nh * 128;
+        const size_t plane = (size_t)Sp * K;
+#pragma unroll
+        for (int a = 0; a < QA; a++) {
+            const int q = q0 + rq + 16 * a;
+            if (q >= S) continue;
+            const float inv = 1.0f / l[a];
+#pragma unroll
+            for (int hh = 0; hh < 2; hh++) {
+                uint16_t pc[3][4];
+#pragma unroll
+                for (int e = 0; e < 4; e++) qt_put_pieces(&pc[0][e], 4, __fmul_rn(o[a][4 * hh + e], inv));
+                uint16_t *dst = P + (size_t)q * K + h * 128 + 64 * hh + 4 * cg;
+#pragma unroll
+                for (int p = 0; p < 3; p++)
+                    *reinterpret_cast<uint2 *>(dst + p * plane) =
+                        make_uint2((uint32_t)pc[p][0] | ((uint32_t)pc[p][1] << 16), (uint32_t)pc[p][2] | ((uint32_t)pc[p][3] << 16));
+            }
+        }
+        if (blockIdx.x == gridDim.x - 1)
+            for (int i = threadIdx.x; i < (Sp - S) * 32; i += QT_PF_WG) {
+                uint16_t *dst = P + (size_t)(S + i / 32) * K + h * 128 + 4 * (i % 32);
+#pragma unroll
+                for (int p = 0; p < 3; p++) *reinterpret_cast<uint2 *>(dst + p * plane) = make_uint2(0u, 0u);
+            }
+        return;
+    }
 #pragma unroll
     for (int a = 0; a < QA; a++) {
         const int q = q0 + rq + 16 * a;
@@ -442,11 +506,15 @@ static void qt_pf_plan(int S, int Sp, int N, int K, long long part_cap, int &nr,
     }
 }
 
-extern "C" hipError_t qt_launch_pf_gemm(int epi, const uint16_t *W, const uint16_t *P, int S, int N, int K, float *Y,
-                                        int ldy, float *part, long long part_cap, hipStream_t st) {
+// Pout != NULL (SwiGLU only): h goes out as the three planes of the next projection's
+// input (k_pf_reduce_swiglu_planes) instead of f32 rows; needs part with S*N <= part_cap.
+static hipError_t pf_gemm(int epi, const uint16_t *W, const uint16_t *P, int S, int N, int K, float *Y, int ldy,
+                          float *part, long long part_cap, uint16_t *Pout, hipStream_t st) {
     constexpr int NST = 4;
     if (S <= 0 || N <= 0 || K <= 0 || N % 64 || K % 64 || epi < 0 || epi > 2) return hipErrorInvalidValue;
-    if (epi != QT_PF_SWIGLU ? (ldy < N || ldy % 4) : (ldy < N / 2 || ldy % 2)) return hipErrorInvalidValue;
+    if (Pout ? (epi != QT_PF_SWIGLU || !part || (long long)S * N > part_cap)
+             : (epi != QT_PF_SWIGLU ? (ldy < N || ldy % 4) : (ldy < N / 2 || ldy % 2)))
+        return hipErrorInvalidValue;
     const int Sp = qt_pf_spad(S);
     int nr, sk;
     qt_pf_plan(S, Sp, N, K, part ? part_cap : 0, nr, sk);
@@ -457,7 +525,13 @@ extern "C" hipError_t qt_launch_pf_gemm(int epi, const uint16_t *W, const uint16
     else if (nr == 3) hipLaunchKernelGGL((k_pf_gemm2<E, 3, 2>), grid, dim3(QT_PF_WG), 0, st, W, P, S, Sp, K, OUT, LD); \
     else if (nr == 2) hipLaunchKernelGGL((k_pf_gemm2<E, 2, NST>), grid, dim3(QT_PF_WG), 0, st, W, P, S, Sp, K, OUT, LD); \
     else hipLaunchKernelGGL((k_pf_gemm2<E, 1, NST>), grid, dim3(QT_PF_WG), 0, st, W, P, S, Sp, K, OUT, LD);
-    if (sk > 1) {
+    if (Pout) {
+        QT_PF_GEMM(QT_PF_PART, part, N)
+        const hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+        hipLaunchKernelGGL(k_pf_reduce_swiglu_planes, dim3((Sp * N / 4 + QT_PF_WG - 1) / QT_PF_WG), dim3(QT_PF_WG), 0, st,
+                           part, sk, S, Sp, N, Pout);
+    } else if (sk > 1) {
         QT_PF_GEMM(QT_PF_PART, part, N)
         const hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;
@@ -474,6 +548,15 @@ extern "C" hipError_t qt_launch_pf_gemm(int epi, const uint16_t *W, const uint16
     }
 #undef QT_PF_GEMM
     return hipGetLastError();
+}
+
+extern "C" hipError_t qt_launch_pf_gemm(int epi, const uint16_t *W, const uint16_t *P, int S, int N, int K, float *Y,
+                                        int ldy, float *part, long long part_cap, hipStream_t st) {
+    return pf_gemm(epi, W, P, S, N, K, Y, ldy, part, part_cap, NULL, st);
+}
+extern "C" hipError_t qt_launch_pf_gemm_swiglu_planes(const uint16_t *W, const uint16_t *P, int S, int N, int K,
+                                                      uint16_t *Pout, float *part, long long part_cap, hipStream_t st) {
+    return pf_gemm(QT_PF_SWIGLU, W, P, S, N, K, NULL, 0, part, part_cap, Pout, st);
 }
 
 extern "C" hipError_t qt_launch_pf_qkv_post(float *QKV, int ld, int S, int nh, int nkv, const float *qn,
@@ -618,9 +701,13 @@ __global__ __launch_bounds__(QT_PF_WG) __attribute__((amdgpu_waves_per_eu(2))) v
     }
 }
 
-extern "C" hipError_t qt_launch_pf_attn(const float *QKV, int ld, int S, int nh, int nkv, float scale, float *A,
-                                        int lda, hipStream_t st) {
+// P != NULL and the VALU kernel chosen: the output is written as the O projection's
+// input planes (rows padded to qt_pf_spad(S)) and *planes = 1; otherwise A gets the f32
+// rows and *planes = 0.
+static hipError_t pf_attn(const float *QKV, int ld, int S, int nh, int nkv, float scale, float *A, int lda,
+                          uint16_t *P, int *planes, hipStream_t st) {
     if (S <= 0 || nh <= 0 || nkv <= 0 || nh % nkv) return hipErrorInvalidValue;
+    if (planes) *planes = 0;
     // the matrix-core kernel where it has at least 64 workgroups (1.7B prefill, 512
     // positions: 8.37 ms against 8.72 with the VALU kernel; at 128 positions, 32
     // workgroups, 3.84 against 3.77), else the VALU kernel with 64-, 32- or 16-query
@@ -629,11 +716,23 @@ extern "C" hipError_t qt_launch_pf_attn(const float *QKV, int ld, int S, int nh,
         hipLaunchKernelGGL(k_pf_fattn_mf, dim3((S + 63) / 64, nh), dim3(QT_PF_WG), 0, st, QKV, ld, S, nh, nkv, scale, A, lda);
         return hipGetLastError();
     }
+    const int Sp = qt_pf_spad(S);
+    if (P && planes) *planes = 1;
+    else P = NULL;
     if ((long long)((S + 63) / 64) * nh >= 256)
-        hipLaunchKernelGGL(k_pf_fattn<4>, dim3((S + 63) / 64, nh), dim3(QT_PF_WG), 0, st, QKV, ld, S, nh, nkv, scale, A, lda);
+        hipLaunchKernelGGL(k_pf_fattn<4>, dim3((S + 63) / 64, nh), dim3(QT_PF_WG), 0, st, QKV, ld, S, nh, nkv, scale, A, lda, P, Sp);
     else if ((long long)((S + 31) / 32) * nh >= 256)
-        hipLaunchKernelGGL(k_pf_fattn<2>, dim3((S + 31) / 32, nh), dim3(QT_PF_WG), 0, st, QKV, ld, S, nh, nkv, scale, A, lda);
+        hipLaunchKernelGGL(k_pf_fattn<2>, dim3((S + 31) / 32, nh), dim3(QT_PF_WG), 0, st, QKV, ld, S, nh, nkv, scale, A, lda, P, Sp);
     else
-        hipLaunchKernelGGL(k_pf_fattn<1>, dim3((S + 15) / 16, nh), dim3(QT_PF_WG), 0, st, QKV, ld, S, nh, nkv, scale, A, lda);
+        hipLaunchKernelGGL(k_pf_fattn<1>, dim3((S + 15) / 16, nh), dim3(QT_PF_WG), 0, st, QKV, ld, S, nh, nkv, scale, A, lda, P, Sp);
     return hipGetLastError();
+}
+
+extern "C" hipError_t qt_launch_pf_attn(const float *QKV, int ld, int S, int nh, int nkv, float scale, float *A,
+                                        int lda, hipStream_t st) {
+    return pf_attn(QKV, ld, S, nh, nkv, scale, A, lda, NULL, NULL, st);
+}
+extern "C" hipError_t qt_launch_pf_attn_planes(const float *QKV, int ld, int S, int nh, int nkv, float scale, float *A,
+                                               int lda, uint16_t *P, int *planes, hipStream_t st) {
+    return pf_attn(QKV, ld, S, nh, nkv, scale, A, lda, P, planes, st);
 }

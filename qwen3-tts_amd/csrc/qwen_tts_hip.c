@@ -643,6 +643,44 @@ fail:
 
 /* -- Talker prefill (qwen_talker_prefill, qwen_tts_talker.c:730-1038) ------------------ */
 
+/* The prefill's layer loop (qwen_tts_talker.c:780-1030) over pf_x (seq residual rows):
+ * planes of the normed input -> q|k|v GEMM -> per-head norm, RoPE, KV store -> causal
+ * attention (written as planes by the VALU kernel) -> O GEMM + residual -> planes of the normed residual -> gate|up GEMM
+ * + SwiGLU (written as the down projection's planes when the split-K workspace holds all
+ * seq x 2F partials) -> down GEMM + residual. */
+static hipError_t pf_layers(talker_t *t, const dmat_t *wq, const dmat_t *wo, const dmat_t *wgu, const dmat_t *wdn,
+                            int seq) {
+    stack_t *s = &t->s;
+    const int L = s->L, H = s->H, F = s->F, qd = s->qd, qkvr = s->qd + 2 * s->kvd;
+    const float scale = 1.0f / sqrtf((float)s->hd);
+    const int h_planes = (long long)seq * 2 * F <= PF_PART_FLOATS;
+    hipError_t e;
+#define PFE(x) do { if ((e = (x)) != hipSuccess) return e; } while (0)
+    for (int l = 0; l < L; l++) {
+        const size_t lay = (size_t)l * s->nkv * s->kv_max * s->hd;
+        PFE(qt_launch_pf_pieces(t->pf_x, H, seq, H, s->in_norm[l], s->eps, t->pf_p, t->st));
+        PFE(qt_launch_pf_gemm(QT_PF_STORE, (const uint16_t *)wq[l].w, t->pf_p, seq, qkvr, H, t->pf_qkvb, qkvr, t->pf_part, PF_PART_FLOATS, t->st));
+        PFE(qt_launch_pf_qkv_post(t->pf_qkvb, qkvr, seq, s->nh, s->nkv, s->qn[l], s->kn[l], s->rope_cos, s->rope_sin,
+                                  s->eps, s->kc + lay, s->vc + lay, s->kv_max, t->st));
+        int att_planes = 0;
+        PFE(qt_launch_pf_attn_planes(t->pf_qkvb, qkvr, seq, s->nh, s->nkv, scale, t->pf_attn, qd, t->pf_p, &att_planes,
+                                     t->st));
+        if (!att_planes) PFE(qt_launch_pf_pieces(t->pf_attn, qd, seq, qd, NULL, 0.f, t->pf_p, t->st));
+        PFE(qt_launch_pf_gemm(QT_PF_RESID, (const uint16_t *)wo[l].w, t->pf_p, seq, H, qd, t->pf_x, H, t->pf_part, PF_PART_FLOATS, t->st));
+        PFE(qt_launch_pf_pieces(t->pf_x, H, seq, H, s->post_norm[l], s->eps, t->pf_p, t->st));
+        if (h_planes) {
+            PFE(qt_launch_pf_gemm_swiglu_planes((const uint16_t *)wgu[l].w, t->pf_p, seq, 2 * F, H, t->pf_p, t->pf_part,
+                                                PF_PART_FLOATS, t->st));
+        } else {
+            PFE(qt_launch_pf_gemm(QT_PF_SWIGLU, (const uint16_t *)wgu[l].w, t->pf_p, seq, 2 * F, H, t->pf_h, F, t->pf_part, PF_PART_FLOATS, t->st));
+            PFE(qt_launch_pf_pieces(t->pf_h, F, seq, F, NULL, 0.f, t->pf_p, t->st));
+        }
+        PFE(qt_launch_pf_gemm(QT_PF_RESID, (const uint16_t *)wdn[l].w, t->pf_p, seq, H, F, t->pf_x, H, t->pf_part, PF_PART_FLOATS, t->st));
+    }
+#undef PFE
+    return hipSuccess;
+}
+
 /* bf16 copies of the projection weights for the prefill (the reference's prefill reads
  * the bf16 layer weights whatever the decode precision, t.c:832-839). */
 static int pf_weights(talker_t *t, const qwen_hip_layer_t *ly) {
@@ -684,7 +722,7 @@ int qwen_hip_talker_prefill(void *state, const qwen_hip_layer_t *bf16_layers, co
     talker_t *t = (talker_t *)state;
     if (!t || t->dead) { SETERR("talker state is dead or NULL"); return -1; }
     stack_t *s = &t->s;
-    const int L = s->L, H = s->H, F = s->F, qd = s->qd, qkvr = s->qd + 2 * s->kvd;
+    const int H = s->H, F = s->F, qd = s->qd, qkvr = s->qd + 2 * s->kvd;
     /* argument errors leave the state usable */
     if (!embeds) { SETERR("null embeds"); return -1; }
     if (seq < 1 || seq > s->kv_max || seq > s->rope_len) {
@@ -716,21 +754,7 @@ int qwen_hip_talker_prefill(void *state, const qwen_hip_layer_t *bf16_layers, co
     }
     HCK(hipMemcpyAsync(t->pf_e, embeds, (size_t)seq * H * sizeof(float), hipMemcpyDefault, t->st));
     HCK(hipMemcpyAsync(t->pf_x, t->pf_e, (size_t)seq * H * sizeof(float), hipMemcpyDeviceToDevice, t->st));
-    const float scale = 1.0f / sqrtf((float)s->hd);
-    for (int l = 0; l < L; l++) {
-        const size_t lay = (size_t)l * s->nkv * s->kv_max * s->hd;
-        HCK(qt_launch_pf_pieces(t->pf_x, H, seq, H, s->in_norm[l], s->eps, t->pf_p, t->st));
-        HCK(qt_launch_pf_gemm(QT_PF_STORE, (const uint16_t *)wq[l].w, t->pf_p, seq, qkvr, H, t->pf_qkvb, qkvr, t->pf_part, PF_PART_FLOATS, t->st));
-        HCK(qt_launch_pf_qkv_post(t->pf_qkvb, qkvr, seq, s->nh, s->nkv, s->qn[l], s->kn[l], s->rope_cos, s->rope_sin,
-                                  s->eps, s->kc + lay, s->vc + lay, s->kv_max, t->st));
-        HCK(qt_launch_pf_attn(t->pf_qkvb, qkvr, seq, s->nh, s->nkv, scale, t->pf_attn, qd, t->st));
-        HCK(qt_launch_pf_pieces(t->pf_attn, qd, seq, qd, NULL, 0.f, t->pf_p, t->st));
-        HCK(qt_launch_pf_gemm(QT_PF_RESID, (const uint16_t *)wo[l].w, t->pf_p, seq, H, qd, t->pf_x, H, t->pf_part, PF_PART_FLOATS, t->st));
-        HCK(qt_launch_pf_pieces(t->pf_x, H, seq, H, s->post_norm[l], s->eps, t->pf_p, t->st));
-        HCK(qt_launch_pf_gemm(QT_PF_SWIGLU, (const uint16_t *)wgu[l].w, t->pf_p, seq, 2 * F, H, t->pf_h, F, t->pf_part, PF_PART_FLOATS, t->st));
-        HCK(qt_launch_pf_pieces(t->pf_h, F, seq, F, NULL, 0.f, t->pf_p, t->st));
-        HCK(qt_launch_pf_gemm(QT_PF_RESID, (const uint16_t *)wdn[l].w, t->pf_p, seq, H, F, t->pf_x, H, t->pf_part, PF_PART_FLOATS, t->st));
-    }
+    HCK(pf_layers(t, wq, wo, wgu, wdn, seq));
     /* dec_x = the last position's residual (t.c:1032-1033), where get_dec_x reads it */
     HCK(hipMemcpyAsync(t->io + H, t->pf_x + (size_t)(seq - 1) * H, (size_t)H * sizeof(float), hipMemcpyDeviceToDevice, t->st));
     HCK(hipMemcpyAsync(t->h_out + H, t->io + H, (size_t)H * sizeof(float), hipMemcpyDeviceToHost, t->st));
@@ -748,29 +772,15 @@ int qwen_hip_talker_prefill_async(void *state, int seq, int n) {
     talker_t *t = (talker_t *)state;
     if (!t || t->dead) { SETERR("talker state is dead or NULL"); return -1; }
     stack_t *s = &t->s;
-    const int L = s->L, H = s->H, F = s->F, qd = s->qd, qkvr = s->qd + 2 * s->kvd;
+    const int H = s->H;
     if (seq < 1 || seq > t->pf_cap || n < 0) { SETERR("call qwen_hip_talker_prefill with at least seq positions first"); return -1; }
     const dmat_t *wq = s->prec == QWEN_HIP_BF16 ? s->qkv : t->pf_qkv, *wo = s->prec == QWEN_HIP_BF16 ? s->o : t->pf_o;
     const dmat_t *wgu = s->prec == QWEN_HIP_BF16 ? s->gu : t->pf_gu, *wdn = s->prec == QWEN_HIP_BF16 ? s->dn : t->pf_dn;
     if (!wq) { SETERR("no prefill weights"); return -1; }
-    const float scale = 1.0f / sqrtf((float)s->hd);
     if (!t->pf_e) { SETERR("no prefill inputs"); return -1; }
     for (int it = 0; it < n; it++) {
         HCK(hipMemcpyAsync(t->pf_x, t->pf_e, (size_t)seq * H * sizeof(float), hipMemcpyDeviceToDevice, t->st));
-        for (int l = 0; l < L; l++) {
-            const size_t lay = (size_t)l * s->nkv * s->kv_max * s->hd;
-            HCK(qt_launch_pf_pieces(t->pf_x, H, seq, H, s->in_norm[l], s->eps, t->pf_p, t->st));
-            HCK(qt_launch_pf_gemm(QT_PF_STORE, (const uint16_t *)wq[l].w, t->pf_p, seq, qkvr, H, t->pf_qkvb, qkvr, t->pf_part, PF_PART_FLOATS, t->st));
-            HCK(qt_launch_pf_qkv_post(t->pf_qkvb, qkvr, seq, s->nh, s->nkv, s->qn[l], s->kn[l], s->rope_cos, s->rope_sin,
-                                      s->eps, s->kc + lay, s->vc + lay, s->kv_max, t->st));
-            HCK(qt_launch_pf_attn(t->pf_qkvb, qkvr, seq, s->nh, s->nkv, scale, t->pf_attn, qd, t->st));
-            HCK(qt_launch_pf_pieces(t->pf_attn, qd, seq, qd, NULL, 0.f, t->pf_p, t->st));
-            HCK(qt_launch_pf_gemm(QT_PF_RESID, (const uint16_t *)wo[l].w, t->pf_p, seq, H, qd, t->pf_x, H, t->pf_part, PF_PART_FLOATS, t->st));
-            HCK(qt_launch_pf_pieces(t->pf_x, H, seq, H, s->post_norm[l], s->eps, t->pf_p, t->st));
-            HCK(qt_launch_pf_gemm(QT_PF_SWIGLU, (const uint16_t *)wgu[l].w, t->pf_p, seq, 2 * F, H, t->pf_h, F, t->pf_part, PF_PART_FLOATS, t->st));
-            HCK(qt_launch_pf_pieces(t->pf_h, F, seq, F, NULL, 0.f, t->pf_p, t->st));
-            HCK(qt_launch_pf_gemm(QT_PF_RESID, (const uint16_t *)wdn[l].w, t->pf_p, seq, H, F, t->pf_x, H, t->pf_part, PF_PART_FLOATS, t->st));
-        }
+        HCK(pf_layers(t, wq, wo, wgu, wdn, seq));
         HCK(hipMemcpyAsync(t->io + H, t->pf_x + (size_t)(seq - 1) * H, (size_t)H * sizeof(float), hipMemcpyDeviceToDevice,
                            t->st));
     }
