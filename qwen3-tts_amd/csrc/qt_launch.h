@@ -105,8 +105,8 @@ hipError_t qt_launch_pf_qkv_post(float *QKV, int ld, int S, int nh, int nkv, con
                                  long long kv_max, hipStream_t st);
 hipError_t qt_launch_pf_attn(const float *QKV, int ld, int S, int nh, int nkv, float scale, float *A, int lda,
                              hipStream_t st);
-/* as qt_launch_pf_attn; where the VALU kernel runs, the output goes out as the O projection's
- * input planes P instead and *planes = 1 */
+/* as qt_launch_pf_attn, the output going out as the O projection's input planes P instead
+ * (*planes = 1) */
 hipError_t qt_launch_pf_attn_planes(const float *QKV, int ld, int S, int nh, int nkv, float scale, float *A, int lda,
                                     uint16_t *P, int *planes, hipStream_t st);
 

@@ -582,8 +582,9 @@ extern "C" hipError_t qt_launch_pf_qkv_post(float *QKV, int ld, int S, int nh, i
 // statistics exchanged across the four lane groups with shuffles; the P.V result rows
 // (queries 4g + r) take their rescale factors from the lanes that own those queries.
 #define QT_PF_VTP 68   // V^T row pitch (64 keys + 4: the float4 reads of a wave spread over banks)
+// P != NULL: output as the O projection's input planes, as k_pf_fattn does.
 __global__ __launch_bounds__(QT_PF_WG) __attribute__((amdgpu_waves_per_eu(2))) void k_pf_fattn_mf(
-    const float *QKV, int ld, int S, int nh, int nkv, float scale, float *A, int lda) {
+    const float *QKV, int ld, int S, int nh, int nkv, float scale, float *A, int lda, uint16_t *P, int Sp) {
     __shared__ __align__(16) float ks[64][QT_PF_KP];
     __shared__ __align__(16) float vt[128][QT_PF_VTP];
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, li = lane & 15, g = lane >> 4;
@@ -692,6 +693,24 @@ __global__ __launch_bounds__(QT_PF_WG) __attribute__((amdgpu_waves_per_eu(2))) v
     float lr[4];
 #pragma unroll
     for (int r = 0; r < 4; r++) lr[r] = 1.0f / __shfl(l, 4 * g + r);
+    if (P) {
+        const size_t plane = (size_t)Sp * qd;
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            const int qq = qw + 4 * g + r;
+            if (qq >= S) continue;
+#pragma unroll
+            for (int dt = 0; dt < 8; dt++)
+                qt_put_pieces(P + (size_t)qq * qd + h * 128 + 16 * dt + li, (int)plane, __fmul_rn(o[dt][r], lr[r]));
+        }
+        if (blockIdx.x == gridDim.x - 1)
+            for (int i = tid; i < (Sp - S) * 32; i += QT_PF_WG) {
+                uint16_t *dst = P + (size_t)(S + i / 32) * qd + h * 128 + 4 * (i % 32);
+#pragma unroll
+                for (int p = 0; p < 3; p++) *reinterpret_cast<uint2 *>(dst + p * plane) = make_uint2(0u, 0u);
+            }
+        return;
+    }
 #pragma unroll
     for (int r = 0; r < 4; r++) {
         const int qq = qw + 4 * g + r;
@@ -701,9 +720,8 @@ __global__ __launch_bounds__(QT_PF_WG) __attribute__((amdgpu_waves_per_eu(2))) v
     }
 }
 
-// P != NULL and the VALU kernel chosen: the output is written as the O projection's
-// input planes (rows padded to qt_pf_spad(S)) and *planes = 1; otherwise A gets the f32
-// rows and *planes = 0.
+// P != NULL (with planes): the output is written as the O projection's input planes
+// (rows padded to qt_pf_spad(S)) and *planes = 1; otherwise A gets the f32 rows.
 static hipError_t pf_attn(const float *QKV, int ld, int S, int nh, int nkv, float scale, float *A, int lda,
                           uint16_t *P, int *planes, hipStream_t st) {
     if (S <= 0 || nh <= 0 || nkv <= 0 || nh % nkv) return hipErrorInvalidValue;
@@ -712,13 +730,14 @@ static hipError_t pf_attn(const float *QKV, int ld, int S, int nh, int nkv, floa
     // positions: 8.37 ms against 8.72 with the VALU kernel; at 128 positions, 32
     // workgroups, 3.84 against 3.77), else the VALU kernel with 64-, 32- or 16-query
     // workgroups, the largest that still fills the CUs
-    if ((long long)((S + 63) / 64) * nh >= 64) {
-        hipLaunchKernelGGL(k_pf_fattn_mf, dim3((S + 63) / 64, nh), dim3(QT_PF_WG), 0, st, QKV, ld, S, nh, nkv, scale, A, lda);
-        return hipGetLastError();
-    }
     const int Sp = qt_pf_spad(S);
     if (P && planes) *planes = 1;
     else P = NULL;
+    if ((long long)((S + 63) / 64) * nh >= 64) {
+        hipLaunchKernelGGL(k_pf_fattn_mf, dim3((S + 63) / 64, nh), dim3(QT_PF_WG), 0, st, QKV, ld, S, nh, nkv, scale, A, lda,
+                           P, Sp);
+        return hipGetLastError();
+    }
     if ((long long)((S + 63) / 64) * nh >= 256)
         hipLaunchKernelGGL(k_pf_fattn<4>, dim3((S + 63) / 64, nh), dim3(QT_PF_WG), 0, st, QKV, ld, S, nh, nkv, scale, A, lda, P, Sp);
     else if ((long long)((S + 31) / 32) * nh >= 256)

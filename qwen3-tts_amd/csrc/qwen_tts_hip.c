@@ -645,7 +645,7 @@ fail:
 
 /* The prefill's layer loop (qwen_tts_talker.c:780-1030) over pf_x (seq residual rows):
  * planes of the normed input -> q|k|v GEMM -> per-head norm, RoPE, KV store -> causal
- * attention (written as planes by the VALU kernel) -> O GEMM + residual -> planes of the normed residual -> gate|up GEMM
+ * attention, written as the O projection's planes -> O GEMM + residual -> planes of the normed residual -> gate|up GEMM
  * + SwiGLU (written as the down projection's planes when the split-K workspace holds all
  * seq x 2F partials) -> down GEMM + residual. */
 static hipError_t pf_layers(talker_t *t, const dmat_t *wq, const dmat_t *wo, const dmat_t *wgu, const dmat_t *wdn,

@@ -134,10 +134,11 @@ def test_prefill_async_replays_reproduce_the_prefill():
     tk.free()
 
 
-@pytest.mark.parametrize("name,seq", [("mini", 100), ("mini17", 40)])
+@pytest.mark.parametrize("name,seq", [("mini", 100), ("mini17", 40), ("mini", 240)])
 def test_prefill_matches_oracle_layer_shapes(oracle, name, seq):
     """The 0.6B / 1.7B layer shapes (2 layers) against the oracle prefill, then one decode
-    step from each side's KV."""
+    step from each side's KV.  100 and 40 positions run the VALU attention, 240 the
+    matrix-core one (64 workgroups), with 16 padding rows in the O projection's planes."""
     from oracle.oracle import talker_from_tensors
     print(f"[case] prefill oracle {name} seq={seq}", flush=True)
     d, shape, t = model_dir(name)
