@@ -1600,6 +1600,15 @@ static hipError_t batch_body(void *arg) {
                                   s->hd, scale, bt->part, (long long)s->nkv * s->attn_G * (s->nh / s->nkv) * 130,
                                   bt->cnt, s->attn_G, bt->attn, s->qd, bt->B, bt->st))) return e;
         if ((e = batch_proj(bt, &s->o[l], QT_EPI_RESID, NULL, bt->attn, s->qd, bt->x, H))) return e;
+        if (s->gu[l].prec == QWEN_HIP_BF16 && s->dn[l].prec == QWEN_HIP_BF16 && (long long)bt->B * 2 * F <= PF_PART_FLOATS) {
+            /* bf16: the gate|up reduce writes h straight as the down projection's planes */
+            if ((e = qt_launch_pf_pieces(bt->x, H, bt->B, H, s->post_norm[l], s->eps, bt->pf_p, bt->st))) return e;
+            if ((e = qt_launch_pf_gemm_swiglu_planes((const uint16_t *)s->gu[l].w, bt->pf_p, bt->B, 2 * F, H, bt->pf_p,
+                                                     bt->pf_part, PF_PART_FLOATS, bt->st))) return e;
+            if ((e = qt_launch_pf_gemm(QT_PF_RESID, (const uint16_t *)s->dn[l].w, bt->pf_p, bt->B, H, F, bt->x, H,
+                                       bt->pf_part, PF_PART_FLOATS, bt->st))) return e;
+            continue;
+        }
         if ((e = batch_proj(bt, &s->gu[l], QT_EPI_SWIGLU, s->post_norm[l], bt->x, H, bt->h, F))) return e;
         if ((e = batch_proj(bt, &s->dn[l], QT_EPI_RESID, NULL, bt->h, F, bt->x, H))) return e;
     }
