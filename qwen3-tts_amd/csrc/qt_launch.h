@@ -100,6 +100,11 @@ hipError_t qt_launch_pf_gemm(int epi, const uint16_t *W, const uint16_t *P, int 
 /* SwiGLU projection whose h goes out as the next projection's three input planes (S*N <= part_cap) */
 hipError_t qt_launch_pf_gemm_swiglu_planes(const uint16_t *W, const uint16_t *P, int S, int N, int K, uint16_t *Pout,
                                            float *part, long long part_cap, hipStream_t st);
+/* residual projection (Y += W . x) whose updated rows, RMS-normalised with gain, go out as the next
+ * projection's input planes Pout (S*N <= part_cap) */
+hipError_t qt_launch_pf_gemm_resid_planes(const uint16_t *W, const uint16_t *P, int S, int N, int K, float *Y, int ldy,
+                                          const float *gain, float eps, uint16_t *Pout, float *part, long long part_cap,
+                                          hipStream_t st);
 hipError_t qt_launch_pf_qkv_post(float *QKV, int ld, int S, int nh, int nkv, const float *qn, const float *kn,
                                  const float *rc, const float *rs, float eps, uint16_t *kc, uint16_t *vc,
                                  long long kv_max, hipStream_t st);

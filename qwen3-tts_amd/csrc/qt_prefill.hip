@@ -265,6 +265,53 @@ __global__ __launch_bounds__(QT_PF_WG) void k_pf_reduce_swiglu_planes(const floa
         *reinterpret_cast<uint32_t *>(dst + p * plane) = (uint32_t)pc[p][0] | ((uint32_t)pc[p][1] << 16);
 }
 
+// The residual epilogue of the summed K ranges for one position row per workgroup (Y[s] +=
+// acc, as k_pf_reduce<RESID>), then that row RMS-normalised with `gain` and written as the
+// next projection's three input planes (P[p][s][N], plane stride Sp*N; rows S <= s < Sp
+// zero): the row is kept in LDS and the norm and pieces are k_pf_pieces' arithmetic in its
+// order (thread t sums x[t + 256 j]^2, block_sum, (x * inv) * g), one launch fewer.
+__global__ __launch_bounds__(QT_PF_WG) void k_pf_reduce_resid_planes(const float *part, int nz, int S, int Sp, int N,
+                                                                     float *Y, int ldy, const float *gain, float eps,
+                                                                     uint16_t *P) {
+    extern __shared__ __align__(16) float xr[];
+    __shared__ float red[QT_WAVES];
+    const int s = blockIdx.x, tid = threadIdx.x;
+    const size_t plane = (size_t)Sp * N;
+    uint16_t *p0 = P + (size_t)s * N;
+    if (s >= S) {
+        for (int k = tid * 8; k < N; k += QT_PF_WG * 8)
+#pragma unroll
+            for (int p = 0; p < 3; p++) *reinterpret_cast<uint4 *>(p0 + p * plane + k) = make_uint4(0u, 0u, 0u, 0u);
+        return;
+    }
+    for (int n = 4 * tid; n < N; n += 4 * QT_PF_WG) {
+        const float4 acc = pf_sum_ranges(part, nz, S, N, s, n);
+        float4 *y = reinterpret_cast<float4 *>(Y + (size_t)s * ldy + n);
+        const float4 o = *y;
+        const float4 r = make_float4(o.x + acc.x, o.y + acc.y, o.z + acc.z, o.w + acc.w);
+        *y = r;
+        *reinterpret_cast<float4 *>(xr + n) = r;
+    }
+    __syncthreads();
+    float ss = 0.f;
+    for (int k = tid; k < N; k += QT_PF_WG) ss = fmaf(xr[k], xr[k], ss);
+    ss = block_sum(ss, red);
+    const float inv = 1.0f / sqrtf(ss / (float)N + eps);
+    for (int k = tid * 4; k < N; k += QT_PF_WG * 4) {
+        float4 v = *reinterpret_cast<const float4 *>(xr + k);
+        const float4 g = *reinterpret_cast<const float4 *>(gain + k);
+        v.x = (v.x * inv) * g.x; v.y = (v.y * inv) * g.y; v.z = (v.z * inv) * g.z; v.w = (v.w * inv) * g.w;
+        uint16_t pc[3][4];
+        const float e[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+        for (int i = 0; i < 4; i++) qt_put_pieces(&pc[0][i], 4, e[i]);
+#pragma unroll
+        for (int p = 0; p < 3; p++)
+            *reinterpret_cast<uint2 *>(p0 + p * plane + k) =
+                make_uint2((uint32_t)pc[p][0] | ((uint32_t)pc[p][1] << 16), (uint32_t)pc[p][2] | ((uint32_t)pc[p][3] << 16));
+    }
+}
+
 // ---- per-head q/k norm, RoPE, KV store ---------------------------------------------
 // Position s = blockIdx.x of QKV [S][ld] (q | k | v rows as the projection wrote them):
 // q and k heads RMS-normalised with their [128] gains (qwen_rms_norm_per_head,
@@ -508,11 +555,16 @@ static void qt_pf_plan(int S, int Sp, int N, int K, long long part_cap, int &nr,
 
 // Pout != NULL (SwiGLU only): h goes out as the three planes of the next projection's
 // input (k_pf_reduce_swiglu_planes) instead of f32 rows; needs part with S*N <= part_cap.
+// Pout with RESID: Y += the product as usual, then RMSNorm(Y row) * gain goes out as the
+// next projection's input planes (k_pf_reduce_resid_planes); needs part, S*N <= part_cap.
 static hipError_t pf_gemm(int epi, const uint16_t *W, const uint16_t *P, int S, int N, int K, float *Y, int ldy,
-                          float *part, long long part_cap, uint16_t *Pout, hipStream_t st) {
+                          float *part, long long part_cap, uint16_t *Pout, const float *gain, float eps,
+                          hipStream_t st) {
     constexpr int NST = 4;
     if (S <= 0 || N <= 0 || K <= 0 || N % 64 || K % 64 || epi < 0 || epi > 2) return hipErrorInvalidValue;
-    if (Pout ? (epi != QT_PF_SWIGLU || !part || (long long)S * N > part_cap)
+    if (Pout ? ((epi != QT_PF_SWIGLU && !(epi == QT_PF_RESID && gain && Y && ldy >= N && ldy % 4 == 0 &&
+                                          (size_t)N * 4 <= 64 * 1024)) ||
+                !part || (long long)S * N > part_cap)
              : (epi != QT_PF_SWIGLU ? (ldy < N || ldy % 4) : (ldy < N / 2 || ldy % 2)))
         return hipErrorInvalidValue;
     const int Sp = qt_pf_spad(S);
@@ -529,8 +581,12 @@ static hipError_t pf_gemm(int epi, const uint16_t *W, const uint16_t *P, int S, 
         QT_PF_GEMM(QT_PF_PART, part, N)
         const hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;
-        hipLaunchKernelGGL(k_pf_reduce_swiglu_planes, dim3((Sp * N / 4 + QT_PF_WG - 1) / QT_PF_WG), dim3(QT_PF_WG), 0, st,
-                           part, sk, S, Sp, N, Pout);
+        if (epi == QT_PF_SWIGLU)
+            hipLaunchKernelGGL(k_pf_reduce_swiglu_planes, dim3((Sp * N / 4 + QT_PF_WG - 1) / QT_PF_WG), dim3(QT_PF_WG), 0,
+                               st, part, sk, S, Sp, N, Pout);
+        else
+            hipLaunchKernelGGL(k_pf_reduce_resid_planes, dim3(Sp), dim3(QT_PF_WG), (size_t)N * sizeof(float), st, part, sk,
+                               S, Sp, N, Y, ldy, gain, eps, Pout);
     } else if (sk > 1) {
         QT_PF_GEMM(QT_PF_PART, part, N)
         const hipError_t e = hipGetLastError();
@@ -552,11 +608,16 @@ static hipError_t pf_gemm(int epi, const uint16_t *W, const uint16_t *P, int S, 
 
 extern "C" hipError_t qt_launch_pf_gemm(int epi, const uint16_t *W, const uint16_t *P, int S, int N, int K, float *Y,
                                         int ldy, float *part, long long part_cap, hipStream_t st) {
-    return pf_gemm(epi, W, P, S, N, K, Y, ldy, part, part_cap, NULL, st);
+    return pf_gemm(epi, W, P, S, N, K, Y, ldy, part, part_cap, NULL, NULL, 0.f, st);
 }
 extern "C" hipError_t qt_launch_pf_gemm_swiglu_planes(const uint16_t *W, const uint16_t *P, int S, int N, int K,
                                                       uint16_t *Pout, float *part, long long part_cap, hipStream_t st) {
-    return pf_gemm(QT_PF_SWIGLU, W, P, S, N, K, NULL, 0, part, part_cap, Pout, st);
+    return pf_gemm(QT_PF_SWIGLU, W, P, S, N, K, NULL, 0, part, part_cap, Pout, NULL, 0.f, st);
+}
+extern "C" hipError_t qt_launch_pf_gemm_resid_planes(const uint16_t *W, const uint16_t *P, int S, int N, int K, float *Y,
+                                                     int ldy, const float *gain, float eps, uint16_t *Pout, float *part,
+                                                     long long part_cap, hipStream_t st) {
+    return pf_gemm(QT_PF_RESID, W, P, S, N, K, Y, ldy, part, part_cap, Pout, gain, eps, st);
 }
 
 extern "C" hipError_t qt_launch_pf_qkv_post(float *QKV, int ld, int S, int nh, int nkv, const float *qn,

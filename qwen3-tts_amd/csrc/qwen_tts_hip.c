@@ -645,20 +645,25 @@ fail:
 
 /* The prefill's layer loop (qwen_tts_talker.c:780-1030) over pf_x (seq residual rows):
  * planes of the normed input -> q|k|v GEMM -> per-head norm, RoPE, KV store -> causal
- * attention, written as the O projection's planes -> O GEMM + residual -> planes of the normed residual -> gate|up GEMM
- * + SwiGLU (written as the down projection's planes when the split-K workspace holds all
- * seq x 2F partials) -> down GEMM + residual. */
+ * attention, written as the O projection's planes -> O GEMM + residual, whose reduce also
+ * writes the planes of the post-attention-normed residual -> gate|up GEMM + SwiGLU, written
+ * as the down projection's planes -> down GEMM + residual, whose reduce writes the next
+ * layer's input planes.  The fused reduces need the split-K workspace to hold all the
+ * partials (seq x 2F for SwiGLU, seq x H for the residuals); beyond that the f32 rows and
+ * a separate plane kernel. */
 static hipError_t pf_layers(talker_t *t, const dmat_t *wq, const dmat_t *wo, const dmat_t *wgu, const dmat_t *wdn,
                             int seq) {
     stack_t *s = &t->s;
     const int L = s->L, H = s->H, F = s->F, qd = s->qd, qkvr = s->qd + 2 * s->kvd;
     const float scale = 1.0f / sqrtf((float)s->hd);
     const int h_planes = (long long)seq * 2 * F <= PF_PART_FLOATS;
+    const int x_planes = (long long)seq * H <= PF_PART_FLOATS;
     hipError_t e;
 #define PFE(x) do { if ((e = (x)) != hipSuccess) return e; } while (0)
     for (int l = 0; l < L; l++) {
         const size_t lay = (size_t)l * s->nkv * s->kv_max * s->hd;
-        PFE(qt_launch_pf_pieces(t->pf_x, H, seq, H, s->in_norm[l], s->eps, t->pf_p, t->st));
+        /* layer 0's input planes; later layers get them from the previous down projection */
+        if (l == 0 || !x_planes) PFE(qt_launch_pf_pieces(t->pf_x, H, seq, H, s->in_norm[l], s->eps, t->pf_p, t->st));
         PFE(qt_launch_pf_gemm(QT_PF_STORE, (const uint16_t *)wq[l].w, t->pf_p, seq, qkvr, H, t->pf_qkvb, qkvr, t->pf_part, PF_PART_FLOATS, t->st));
         PFE(qt_launch_pf_qkv_post(t->pf_qkvb, qkvr, seq, s->nh, s->nkv, s->qn[l], s->kn[l], s->rope_cos, s->rope_sin,
                                   s->eps, s->kc + lay, s->vc + lay, s->kv_max, t->st));
@@ -666,8 +671,13 @@ static hipError_t pf_layers(talker_t *t, const dmat_t *wq, const dmat_t *wo, con
         PFE(qt_launch_pf_attn_planes(t->pf_qkvb, qkvr, seq, s->nh, s->nkv, scale, t->pf_attn, qd, t->pf_p, &att_planes,
                                      t->st));
         if (!att_planes) PFE(qt_launch_pf_pieces(t->pf_attn, qd, seq, qd, NULL, 0.f, t->pf_p, t->st));
-        PFE(qt_launch_pf_gemm(QT_PF_RESID, (const uint16_t *)wo[l].w, t->pf_p, seq, H, qd, t->pf_x, H, t->pf_part, PF_PART_FLOATS, t->st));
-        PFE(qt_launch_pf_pieces(t->pf_x, H, seq, H, s->post_norm[l], s->eps, t->pf_p, t->st));
+        if (x_planes) {
+            PFE(qt_launch_pf_gemm_resid_planes((const uint16_t *)wo[l].w, t->pf_p, seq, H, qd, t->pf_x, H, s->post_norm[l],
+                                               s->eps, t->pf_p, t->pf_part, PF_PART_FLOATS, t->st));
+        } else {
+            PFE(qt_launch_pf_gemm(QT_PF_RESID, (const uint16_t *)wo[l].w, t->pf_p, seq, H, qd, t->pf_x, H, t->pf_part, PF_PART_FLOATS, t->st));
+            PFE(qt_launch_pf_pieces(t->pf_x, H, seq, H, s->post_norm[l], s->eps, t->pf_p, t->st));
+        }
         if (h_planes) {
             PFE(qt_launch_pf_gemm_swiglu_planes((const uint16_t *)wgu[l].w, t->pf_p, seq, 2 * F, H, t->pf_p, t->pf_part,
                                                 PF_PART_FLOATS, t->st));
@@ -675,7 +685,11 @@ static hipError_t pf_layers(talker_t *t, const dmat_t *wq, const dmat_t *wo, con
             PFE(qt_launch_pf_gemm(QT_PF_SWIGLU, (const uint16_t *)wgu[l].w, t->pf_p, seq, 2 * F, H, t->pf_h, F, t->pf_part, PF_PART_FLOATS, t->st));
             PFE(qt_launch_pf_pieces(t->pf_h, F, seq, F, NULL, 0.f, t->pf_p, t->st));
         }
-        PFE(qt_launch_pf_gemm(QT_PF_RESID, (const uint16_t *)wdn[l].w, t->pf_p, seq, H, F, t->pf_x, H, t->pf_part, PF_PART_FLOATS, t->st));
+        if (x_planes && l + 1 < L)
+            PFE(qt_launch_pf_gemm_resid_planes((const uint16_t *)wdn[l].w, t->pf_p, seq, H, F, t->pf_x, H, s->in_norm[l + 1],
+                                               s->eps, t->pf_p, t->pf_part, PF_PART_FLOATS, t->st));
+        else
+            PFE(qt_launch_pf_gemm(QT_PF_RESID, (const uint16_t *)wdn[l].w, t->pf_p, seq, H, F, t->pf_x, H, t->pf_part, PF_PART_FLOATS, t->st));
     }
 #undef PFE
     return hipSuccess;
