@@ -1606,23 +1606,38 @@ static hipError_t batch_body(void *arg) {
     const float scale = 1.0f / sqrtf((float)s->hd);
     const int H = s->H, F = s->F, QKV = s->qd + 2 * s->kvd;
     const long long per = (long long)s->L * s->nkv * s->kv_max * s->hd;
+    /* bf16 weights: each reduce writes the next projection's input planes (the SwiGLU
+     * output, the normed residual), so only layer 0's input and the attention output get a
+     * plane kernel of their own */
+    const int fused = s->prec == QWEN_HIP_BF16 && (long long)bt->B * 2 * F <= PF_PART_FLOATS;
     for (int l = 0; l < s->L; l++) {
         const size_t lay = (size_t)l * s->nkv * s->kv_max * s->hd;
-        if ((e = batch_proj(bt, &s->qkv[l], QT_EPI_STORE, s->in_norm[l], bt->x, H, bt->qkv, QKV))) return e;
+        if (fused) {
+            if (l == 0 && (e = qt_launch_pf_pieces(bt->x, H, bt->B, H, s->in_norm[0], s->eps, bt->pf_p, bt->st))) return e;
+            if ((e = qt_launch_pf_gemm(QT_PF_STORE, (const uint16_t *)s->qkv[l].w, bt->pf_p, bt->B, QKV, H, bt->qkv, QKV,
+                                       bt->pf_part, PF_PART_FLOATS, bt->st))) return e;
+        } else if ((e = batch_proj(bt, &s->qkv[l], QT_EPI_STORE, s->in_norm[l], bt->x, H, bt->qkv, QKV))) return e;
         if ((e = qt_launch_attn_b(bt->qkv, QKV, s->qn[l], s->kn[l], s->rope_cos, s->rope_sin, s->eps, bt->d_pos,
                                   bt->kc + lay, bt->vc + lay, per, s->hd, (long long)s->kv_max * s->hd, s->nh, s->nkv,
                                   s->hd, scale, bt->part, (long long)s->nkv * s->attn_G * (s->nh / s->nkv) * 130,
                                   bt->cnt, s->attn_G, bt->attn, s->qd, bt->B, bt->st))) return e;
-        if ((e = batch_proj(bt, &s->o[l], QT_EPI_RESID, NULL, bt->attn, s->qd, bt->x, H))) return e;
-        if (s->gu[l].prec == QWEN_HIP_BF16 && s->dn[l].prec == QWEN_HIP_BF16 && (long long)bt->B * 2 * F <= PF_PART_FLOATS) {
-            /* bf16: the gate|up reduce writes h straight as the down projection's planes */
-            if ((e = qt_launch_pf_pieces(bt->x, H, bt->B, H, s->post_norm[l], s->eps, bt->pf_p, bt->st))) return e;
+        if (fused) {
+            if ((e = qt_launch_pf_pieces(bt->attn, s->qd, bt->B, s->qd, NULL, 0.f, bt->pf_p, bt->st))) return e;
+            if ((e = qt_launch_pf_gemm_resid_planes((const uint16_t *)s->o[l].w, bt->pf_p, bt->B, H, s->qd, bt->x, H,
+                                                    s->post_norm[l], s->eps, bt->pf_p, bt->pf_part, PF_PART_FLOATS,
+                                                    bt->st))) return e;
             if ((e = qt_launch_pf_gemm_swiglu_planes((const uint16_t *)s->gu[l].w, bt->pf_p, bt->B, 2 * F, H, bt->pf_p,
                                                      bt->pf_part, PF_PART_FLOATS, bt->st))) return e;
-            if ((e = qt_launch_pf_gemm(QT_PF_RESID, (const uint16_t *)s->dn[l].w, bt->pf_p, bt->B, H, F, bt->x, H,
-                                       bt->pf_part, PF_PART_FLOATS, bt->st))) return e;
+            if (l + 1 < s->L)
+                e = qt_launch_pf_gemm_resid_planes((const uint16_t *)s->dn[l].w, bt->pf_p, bt->B, H, F, bt->x, H,
+                                                   s->in_norm[l + 1], s->eps, bt->pf_p, bt->pf_part, PF_PART_FLOATS, bt->st);
+            else
+                e = qt_launch_pf_gemm(QT_PF_RESID, (const uint16_t *)s->dn[l].w, bt->pf_p, bt->B, H, F, bt->x, H,
+                                      bt->pf_part, PF_PART_FLOATS, bt->st);
+            if (e) return e;
             continue;
         }
+        if ((e = batch_proj(bt, &s->o[l], QT_EPI_RESID, NULL, bt->attn, s->qd, bt->x, H))) return e;
         if ((e = batch_proj(bt, &s->gu[l], QT_EPI_SWIGLU, s->post_norm[l], bt->x, H, bt->h, F))) return e;
         if ((e = batch_proj(bt, &s->dn[l], QT_EPI_RESID, NULL, bt->h, F, bt->x, H))) return e;
     }
