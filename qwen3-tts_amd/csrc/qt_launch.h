@@ -102,6 +102,12 @@ hipError_t qt_launch_pf_gemm_swiglu_planes(const uint16_t *W, const uint16_t *P,
                                            float *part, long long part_cap, hipStream_t st);
 /* residual projection (Y += W . x) whose updated rows, RMS-normalised with gain, go out as the next
  * projection's input planes Pout (S*N <= part_cap) */
+/* q|k|v projection whose rows are finished as qt_launch_pf_qkv_post does (per-head norm, RoPE,
+ * KV store) by the split-K reduce itself (S*N <= part_cap) */
+hipError_t qt_launch_pf_gemm_qkv_post(const uint16_t *W, const uint16_t *P, int S, int N, int K, float *QKV, int ld, int nh,
+                                      int nkv, const float *qn, const float *kn, const float *rc, const float *rs, float eps,
+                                      uint16_t *kc, uint16_t *vc, long long kv_max, float *part, long long part_cap,
+                                      hipStream_t st);
 hipError_t qt_launch_pf_gemm_resid_planes(const uint16_t *W, const uint16_t *P, int S, int N, int K, float *Y, int ldy,
                                           const float *gain, float eps, uint16_t *Pout, float *part, long long part_cap,
                                           hipStream_t st);

@@ -350,6 +350,52 @@ __global__ __launch_bounds__(QT_PF_WG) void k_pf_qkv_post(float *QKV, int ld, in
     }
 }
 
+// The q|k|v projection's summed K ranges for one position row per workgroup, kept in LDS,
+// then k_pf_qkv_post's work on that row (per-head q/k norm, RoPE, KV store) with the same
+// arithmetic; the row (q, k rotated, v as summed) is written once.  One launch fewer.
+struct PfQkvPost {
+    int nh, nkv;
+    const float *qn, *kn, *rc, *rs;
+    float eps;
+    uint16_t *kc, *vc;
+    long long kv_max;
+};
+__global__ __launch_bounds__(QT_PF_WG) void k_pf_reduce_qkv_post(const float *part, int nz, int S, int N, float *QKV,
+                                                                 int ld, PfQkvPost a) {
+    extern __shared__ __align__(16) float xr[];
+    const int s = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    for (int n = 4 * tid; n < N; n += 4 * QT_PF_WG)
+        *reinterpret_cast<float4 *>(xr + n) = pf_sum_ranges(part, nz, S, N, s, n);
+    __syncthreads();
+    float *row = QKV + (size_t)s * ld;
+    const float c = a.rc[(size_t)s * 64 + lane], sn = a.rs[(size_t)s * 64 + lane];
+    for (int hr = wave; hr < a.nh + 2 * a.nkv; hr += QT_WAVES) {
+        float *x = row + hr * 128;
+        const float x0 = xr[hr * 128 + lane], x1 = xr[hr * 128 + lane + 64];
+        if (hr < a.nh + a.nkv) {
+            const bool isk = hr >= a.nh;
+            const float *w = isk ? a.kn : a.qn;
+            const float ss = group_sum<64>(x0 * x0 + x1 * x1);
+            const float inv = 1.0f / sqrtf(ss / 128.0f + a.eps);
+            const float n0 = (x0 * inv) * w[lane], n1 = (x1 * inv) * w[lane + 64];
+            const float r0 = fmaf(n0, c, -(n1 * sn)), r1 = fmaf(n1, c, n0 * sn);
+            x[lane] = r0;
+            x[lane + 64] = r1;
+            if (isk) {
+                uint16_t *kd = a.kc + ((size_t)(hr - a.nh) * a.kv_max + s) * 128;
+                kd[lane] = f2bf_trunc(r0);
+                kd[lane + 64] = f2bf_trunc(r1);
+            }
+        } else {
+            x[lane] = x0;
+            x[lane + 64] = x1;
+            uint16_t *vd = a.vc + ((size_t)(hr - a.nh - a.nkv) * a.kv_max + s) * 128;
+            vd[lane] = f2bf_trunc(x0);
+            vd[lane + 64] = f2bf_trunc(x1);
+        }
+    }
+}
+
 // ---- causal attention, tiled -------------------------------------------------------
 // The same attention for 64 queries of one head per workgroup, over 64-key blocks held in
 // LDS (flash-style: per block, row max -> rescale of the running sums -> P.V).  Thread t
@@ -557,10 +603,14 @@ static void qt_pf_plan(int S, int Sp, int N, int K, long long part_cap, int &nr,
 // input (k_pf_reduce_swiglu_planes) instead of f32 rows; needs part with S*N <= part_cap.
 // Pout with RESID: Y += the product as usual, then RMSNorm(Y row) * gain goes out as the
 // next projection's input planes (k_pf_reduce_resid_planes); needs part, S*N <= part_cap.
+// qp != NULL (STORE into the q|k|v rows Y): k_pf_reduce_qkv_post finishes the rows.
 static hipError_t pf_gemm(int epi, const uint16_t *W, const uint16_t *P, int S, int N, int K, float *Y, int ldy,
                           float *part, long long part_cap, uint16_t *Pout, const float *gain, float eps,
-                          hipStream_t st) {
+                          hipStream_t st, const PfQkvPost *qp = nullptr) {
     constexpr int NST = 4;
+    if (qp && (epi != QT_PF_STORE || Pout || !part || (long long)S * N > part_cap || N != (qp->nh + 2 * qp->nkv) * 128 ||
+               (size_t)N * 4 > 64 * 1024 || S > qp->kv_max))
+        return hipErrorInvalidValue;
     if (S <= 0 || N <= 0 || K <= 0 || N % 64 || K % 64 || epi < 0 || epi > 2) return hipErrorInvalidValue;
     if (Pout ? ((epi != QT_PF_SWIGLU && !(epi == QT_PF_RESID && gain && Y && ldy >= N && ldy % 4 == 0 &&
                                           (size_t)N * 4 <= 64 * 1024)) ||
@@ -577,7 +627,13 @@ static hipError_t pf_gemm(int epi, const uint16_t *W, const uint16_t *P, int S, 
     else if (nr == 3) hipLaunchKernelGGL((k_pf_gemm2<E, 3, 2>), grid, dim3(QT_PF_WG), 0, st, W, P, S, Sp, K, OUT, LD); \
     else if (nr == 2) hipLaunchKernelGGL((k_pf_gemm2<E, 2, NST>), grid, dim3(QT_PF_WG), 0, st, W, P, S, Sp, K, OUT, LD); \
     else hipLaunchKernelGGL((k_pf_gemm2<E, 1, NST>), grid, dim3(QT_PF_WG), 0, st, W, P, S, Sp, K, OUT, LD);
-    if (Pout) {
+    if (qp) {
+        QT_PF_GEMM(QT_PF_PART, part, N)
+        const hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+        hipLaunchKernelGGL(k_pf_reduce_qkv_post, dim3(S), dim3(QT_PF_WG), (size_t)N * sizeof(float), st, part, sk, S, N, Y,
+                           ldy, *qp);
+    } else if (Pout) {
         QT_PF_GEMM(QT_PF_PART, part, N)
         const hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;
@@ -613,6 +669,14 @@ extern "C" hipError_t qt_launch_pf_gemm(int epi, const uint16_t *W, const uint16
 extern "C" hipError_t qt_launch_pf_gemm_swiglu_planes(const uint16_t *W, const uint16_t *P, int S, int N, int K,
                                                       uint16_t *Pout, float *part, long long part_cap, hipStream_t st) {
     return pf_gemm(QT_PF_SWIGLU, W, P, S, N, K, NULL, 0, part, part_cap, Pout, NULL, 0.f, st);
+}
+extern "C" hipError_t qt_launch_pf_gemm_qkv_post(const uint16_t *W, const uint16_t *P, int S, int N, int K, float *QKV,
+                                                  int ld, int nh, int nkv, const float *qn, const float *kn,
+                                                  const float *rc, const float *rs, float eps, uint16_t *kc, uint16_t *vc,
+                                                  long long kv_max, float *part, long long part_cap, hipStream_t st) {
+    if (nh <= 0 || nkv <= 0 || nh % nkv) return hipErrorInvalidValue;
+    const PfQkvPost qp = {nh, nkv, qn, kn, rc, rs, eps, kc, vc, kv_max};
+    return pf_gemm(QT_PF_STORE, W, P, S, N, K, QKV, ld, part, part_cap, NULL, NULL, 0.f, st, &qp);
 }
 extern "C" hipError_t qt_launch_pf_gemm_resid_planes(const uint16_t *W, const uint16_t *P, int S, int N, int K, float *Y,
                                                      int ldy, const float *gain, float eps, uint16_t *Pout, float *part,

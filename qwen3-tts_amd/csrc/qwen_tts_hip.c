@@ -644,7 +644,8 @@ fail:
 /* -- Talker prefill (qwen_talker_prefill, qwen_tts_talker.c:730-1038) ------------------ */
 
 /* The prefill's layer loop (qwen_tts_talker.c:780-1030) over pf_x (seq residual rows):
- * planes of the normed input -> q|k|v GEMM -> per-head norm, RoPE, KV store -> causal
+ * planes of the normed input -> q|k|v GEMM, whose reduce does the per-head norm, RoPE and
+ * KV store -> causal
  * attention, written as the O projection's planes -> O GEMM + residual, whose reduce also
  * writes the planes of the post-attention-normed residual -> gate|up GEMM + SwiGLU, written
  * as the down projection's planes -> down GEMM + residual, whose reduce writes the next
@@ -664,9 +665,15 @@ static hipError_t pf_layers(talker_t *t, const dmat_t *wq, const dmat_t *wo, con
         const size_t lay = (size_t)l * s->nkv * s->kv_max * s->hd;
         /* layer 0's input planes; later layers get them from the previous down projection */
         if (l == 0 || !x_planes) PFE(qt_launch_pf_pieces(t->pf_x, H, seq, H, s->in_norm[l], s->eps, t->pf_p, t->st));
-        PFE(qt_launch_pf_gemm(QT_PF_STORE, (const uint16_t *)wq[l].w, t->pf_p, seq, qkvr, H, t->pf_qkvb, qkvr, t->pf_part, PF_PART_FLOATS, t->st));
-        PFE(qt_launch_pf_qkv_post(t->pf_qkvb, qkvr, seq, s->nh, s->nkv, s->qn[l], s->kn[l], s->rope_cos, s->rope_sin,
-                                  s->eps, s->kc + lay, s->vc + lay, s->kv_max, t->st));
+        if ((long long)seq * qkvr <= PF_PART_FLOATS) {
+            PFE(qt_launch_pf_gemm_qkv_post((const uint16_t *)wq[l].w, t->pf_p, seq, qkvr, H, t->pf_qkvb, qkvr, s->nh, s->nkv,
+                                           s->qn[l], s->kn[l], s->rope_cos, s->rope_sin, s->eps, s->kc + lay,
+                                           s->vc + lay, s->kv_max, t->pf_part, PF_PART_FLOATS, t->st));
+        } else {
+            PFE(qt_launch_pf_gemm(QT_PF_STORE, (const uint16_t *)wq[l].w, t->pf_p, seq, qkvr, H, t->pf_qkvb, qkvr, t->pf_part, PF_PART_FLOATS, t->st));
+            PFE(qt_launch_pf_qkv_post(t->pf_qkvb, qkvr, seq, s->nh, s->nkv, s->qn[l], s->kn[l], s->rope_cos, s->rope_sin,
+                                      s->eps, s->kc + lay, s->vc + lay, s->kv_max, t->st));
+        }
         int att_planes = 0;
         PFE(qt_launch_pf_attn_planes(t->pf_qkvb, qkvr, seq, s->nh, s->nkv, scale, t->pf_attn, qd, t->pf_p, &att_planes,
                                      t->st));
