@@ -935,8 +935,11 @@ int qwen_hip_talker_sample(void *state, const uint16_t *codec_head, const uint16
     t->h_pos[3] = 0;
     HCK(hipMemcpyAsync(t->smp_seed, t->h_pos + 2, sizeof(uint32_t), hipMemcpyHostToDevice, t->st));
     HCK(hipMemcpyAsync(t->smp_done, t->h_pos + 3, sizeof(int), hipMemcpyHostToDevice, t->st));
+    /* the step's input: the fused kernel reads it from ps_xin, the per-kernel step works on
+     * the residual io[H:2H] in place */
+    float *xin = t->ps_on ? t->ps_xin : t->io + H;
     memcpy(t->h_in, embed, (size_t)H * sizeof(float));
-    HCK(hipMemcpyAsync(t->io + H, t->h_in, (size_t)H * sizeof(float), hipMemcpyHostToDevice, t->st));
+    HCK(hipMemcpyAsync(xin, t->h_in, (size_t)H * sizeof(float), hipMemcpyHostToDevice, t->st));
     const int expected = sp->text_len * 3, boost_start = expected * 2;
     for (int i = 0; i < n_steps; i++) {
         float *x = t->io + H;
@@ -947,20 +950,25 @@ int qwen_hip_talker_sample(void *state, const uint16_t *codec_head, const uint16
             if (boost > 10.0f) boost = 10.0f;
         }
         const int warm = sp->greedy_warmup > 0 && frame < sp->greedy_warmup;
-        HCK(stack_body(&t->s, x, t->d_pos, t->st));
+        /* one decode step: the fused kernel (one launch; it leaves the residual in io[H:2H],
+         * bit-identical to the per-kernel layers, and advances the position) or the layers */
+        if (t->ps_on) HCK(ps_launch(t, 1, 0));
+        else HCK(stack_body(&t->s, x, t->d_pos, t->st));
         HCK(qt_launch_mv(t->head_m.prec, QT_EPI_STORE, 1, x, t->s.final_norm, t->s.eps, t->head_m.w, NULL, NULL,
                          t->head_m.rows, t->head_m.cols, t->logits, NULL, NULL, t->io, t->st));
         HCK(qt_launch_sample(t->logits, codec_vocab, 1, frame, boost, warm ? 0.0f : sp->temperature,
                              warm ? 1 : sp->top_k, sp->top_p, sp->rep_penalty, t->smp_hist, n_prev + i, t->smp_seed,
                              t->smp_hist + n_prev + i, t->smp_done, t->st));
-        HCK(qt_launch_gather(t->smp_hist + n_prev + i, codec_vocab, t->codec_emb, H, x, t->st));
-        HCK(qt_launch_advance_pos(t->d_pos, 1, t->st));
+        HCK(qt_launch_gather(t->smp_hist + n_prev + i, codec_vocab, t->codec_emb, H, xin, t->st));
+        if (!t->ps_on) HCK(qt_launch_advance_pos(t->d_pos, 1, t->st));
     }
     if (n_steps > 0)
         HCK(hipMemcpyAsync(tokens_out, t->smp_hist + n_prev, (size_t)n_steps * sizeof(int), hipMemcpyDeviceToHost, t->st));
     HCK(hipMemcpyAsync(t->h_pos + 2, t->smp_seed, sizeof(uint32_t), hipMemcpyDeviceToHost, t->st));
     HCK(hipMemcpyAsync(t->h_out, t->io, (size_t)2 * H * sizeof(float), hipMemcpyDeviceToHost, t->st));
+    if (t->ps_on) HCK(hipMemcpyAsync(t->h_err, t->ps_err, sizeof(int), hipMemcpyDeviceToHost, t->st));
     HCK(hipStreamSynchronize(t->st));
+    if (t->ps_on && ps_check(t) != 0) goto fail;
     *seed = (uint32_t)t->h_pos[2];
     if (hidden_out) memcpy(hidden_out, t->h_out, (size_t)H * sizeof(float));
     t->dev_pos = pos + n_steps;
