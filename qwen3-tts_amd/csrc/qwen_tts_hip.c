@@ -152,6 +152,7 @@ static hipError_t kv_xfer(uint16_t *dev_heads, int kv_max, uint16_t *host_rows, 
 
 typedef struct {
     int H, F, nh, nkv, hd, L, kv_max, qd, kvd, prec, rope_len, attn_G;
+    int step_G;                /* key chunks per kv head of the single-stream step's attention */
     float eps;
     dmat_t *qkv, *o, *gu, *dn;
     float **in_norm, **post_norm, **qn, **kn;
@@ -200,6 +201,7 @@ static int stack_init(stack_t *s, const qwen_hip_talker_desc_t *d, hipStream_t s
     s->rope_len = d->rope_len < d->kv_max ? d->rope_len : d->kv_max;
     /* split-K grid: short caches (the CP's <= 64 positions) use one chunk per kv head */
     s->attn_G = s->kv_max <= 128 ? 1 : qt_attn_grid(s->kv_max);
+    s->step_G = s->attn_G;
     const int L = s->L, H = s->H, F = s->F;
     s->qkv = calloc(L, sizeof(dmat_t)); s->o = calloc(L, sizeof(dmat_t));
     s->gu = calloc(L, sizeof(dmat_t)); s->dn = calloc(L, sizeof(dmat_t));
@@ -260,7 +262,7 @@ static hipError_t stack_body_ex(stack_t *s, float *x, const int *d_pos, hipStrea
         if ((e = mv(&s->qkv[l], QT_EPI_STORE, 1, x, s->in_norm[l], s->eps, s->qkvbuf, NULL, NULL, st))) return e;
         if ((e = qt_launch_attn(1, s->qkvbuf, s->qn[l], s->kn[l], s->rope_cos, s->rope_sin, s->eps, d_pos, 0,
                                 s->kc + lay, s->vc + lay, s->hd, (long long)s->kv_max * s->hd, s->nh, s->nkv,
-                                s->hd, scale, s->part, s->cnt, s->attn_G, s->attn, st))) return e;
+                                s->hd, scale, s->part, s->cnt, s->step_G, s->attn, st))) return e;
         if ((e = mv(&s->o[l], QT_EPI_RESID, 0, s->attn, NULL, s->eps, NULL, x, NULL, st))) return e;
         if ((e = mv(&s->gu[l], QT_EPI_SWIGLU, 1, x, s->post_norm[l], s->eps, s->hbuf, NULL, NULL, st))) return e;
         if ((e = mv(&s->dn[l], QT_EPI_RESID, 0, s->hbuf, NULL, s->eps, NULL, x, NULL, st))) return e;
@@ -306,6 +308,9 @@ typedef struct {
     int ps_on;
     void *ps_layers;        /* device layer table */
     unsigned long long *ps_ring;   /* tagged activation words */
+    int rs_on;              /* the role-specialised kernel (qt_rstep.hip) runs the fused step */
+    unsigned *rs_reg;       /* its hand-off words, [2][L][layer block], sentinel when empty */
+    unsigned long long *rs_slots;  /* its tagged winner words */
     float *ps_xin;          /* step-0 input of a launch */
     unsigned *ps_epoch;     /* tag of the next step */
     int *ps_err;
@@ -319,6 +324,14 @@ typedef struct {
     float *pf_part;         /* split-K partial sums, PF_PART_FLOATS */
     uint16_t *pf_p;         /* activation planes [3][spad][max(H, qd, F)] */
 } talker_t;
+
+/* QWEN_HIP_RSTEP=0 keeps the single-role persistent kernel (qt_pstep.hip) for shapes the
+ * role-specialised one (qt_rstep.hip) also covers. */
+static int rstep_enabled(void) {
+    static int on = -1;
+    if (on < 0) { const char *e = getenv("QWEN_HIP_RSTEP"); on = !(e && e[0] == '0'); }
+    return on;
+}
 
 static int persistent_enabled(void) {
     static int on = -1;
@@ -339,7 +352,7 @@ static void talker_destroy(talker_t *t) {
     stack_free(&t->s);
     void *bufs[] = {t->io, t->d_pos, t->d_frame, t->d_tok, t->d_hist, t->codec_head, t->codec_emb, t->logits,
                     t->smp_hist, t->smp_seed, t->smp_done, t->gen_codes, t->gen_pad,
-                    t->ps_layers, t->ps_ring, t->ps_xin, t->ps_epoch, t->ps_err,
+                    t->ps_layers, t->ps_ring, t->ps_xin, t->ps_epoch, t->ps_err, t->rs_reg, t->rs_slots,
                     t->pf_x, t->pf_qkvb, t->pf_attn, t->pf_h, t->pf_p, t->pf_part, t->pf_e};
     for (size_t i = 0; i < sizeof bufs / sizeof bufs[0]; i++) if (bufs[i]) (void)hipFree(bufs[i]);
     if (t->h_in) (void)hipHostFree(t->h_in);
@@ -357,12 +370,23 @@ static int ps_setup(talker_t *t) {
     const size_t lb = qt_pstep_layer_bytes();
     const size_t words = qt_pstep_ring_words(s->H, s->F, s->L);
     const unsigned one = 1;   /* ring words start with tag 0: the first step is tag 1 */
-    HCK(hipMalloc((void **)&t->ps_ring, words * sizeof(unsigned long long)));
+    if (rstep_enabled() && qt_rstep_supported(s->prec, s->H, s->F, s->nh, s->nkv, s->hd, s->kv_max, s->L)) {
+        /* hand-off words start empty (0xFF bytes: the sentinel), winner words with tag 0;
+         * the per-kernel step splits attention into the same key chunks */
+        const size_t rw = qt_rstep_region_words(s->L), sw = qt_rstep_slot_words();
+        HCK(hipMalloc((void **)&t->rs_reg, rw * sizeof(unsigned)));
+        HCK(hipMalloc((void **)&t->rs_slots, sw * sizeof(unsigned long long)));
+        HCK(hipMemsetAsync(t->rs_reg, 0xFF, rw * sizeof(unsigned), t->st));
+        HCK(hipMemsetAsync(t->rs_slots, 0, sw * sizeof(unsigned long long), t->st));
+        s->step_G = qt_rstep_chunks();
+        t->rs_on = 1;
+    }
+    HCK(hipMalloc((void **)&t->ps_ring, (t->rs_on ? 1 : words) * sizeof(unsigned long long)));
     HCK(hipMalloc((void **)&t->ps_epoch, 64));
     HCK(hipMalloc((void **)&t->ps_err, 64));
     HCK(hipMalloc((void **)&t->ps_xin, (size_t)s->H * sizeof(float)));
     HCK(hipHostMalloc((void **)&t->h_err, 64, hipHostMallocDefault));
-    HCK(hipMemsetAsync(t->ps_ring, 0, words * sizeof(unsigned long long), t->st));
+    HCK(hipMemsetAsync(t->ps_ring, 0, (t->rs_on ? 1 : words) * sizeof(unsigned long long), t->st));
     HCK(hipMemsetAsync(t->ps_err, 0, 64, t->st));
     HCK(hipMemcpyAsync(t->ps_epoch, &one, sizeof one, hipMemcpyHostToDevice, t->st));
     host_tab = calloc((size_t)s->L, lb);
@@ -384,15 +408,24 @@ fail:
     return -1;
 }
 
-/* One launch of the persistent kernel: n_steps decode steps (with_head: greedy loop). */
-static hipError_t ps_launch(talker_t *t, int n_steps, int with_head) {
+/* One launch of the persistent kernel: n_steps decode steps (with_head: greedy loop).
+ * layer_out (role-specialised kernel only, may be NULL): every layer's output x of the
+ * launch's last step, [L][H]. */
+static hipError_t ps_launch_ex(talker_t *t, int n_steps, int with_head, float *layer_out) {
     stack_t *s = &t->s;
+    if (t->rs_on)
+        return qt_launch_rstep(t->ps_layers, s->L, s->final_norm, s->rope_cos, s->rope_sin, s->kc, s->vc, s->kv_max, s->eps,
+                               1.0f / sqrtf((float)s->hd), t->rs_reg, t->rs_slots, t->io, t->io + s->H, t->ps_xin, t->d_pos,
+                               t->ps_epoch, t->ps_err, n_steps, with_head,
+                               with_head ? (const uint16_t *)t->head_m.w : NULL, with_head ? t->codec_emb : NULL,
+                               t->codec_vocab, t->d_frame, t->d_hist, t->hist_len, layer_out, t->st);
     return qt_launch_pstep(s->prec, s->H, t->ps_layers, s->L, s->final_norm, s->rope_cos, s->rope_sin, s->kc, s->vc,
                            s->kv_max, s->eps, 1.0f / sqrtf((float)s->hd), t->ps_ring, t->io, t->io + s->H, t->ps_xin,
                            t->d_pos, t->ps_epoch, t->ps_err, n_steps, with_head,
                            with_head ? (const uint16_t *)t->head_m.w : NULL, with_head ? t->codec_emb : NULL,
                            t->codec_vocab, t->d_frame, t->d_hist, t->hist_len, t->st);
 }
+static hipError_t ps_launch(talker_t *t, int n_steps, int with_head) { return ps_launch_ex(t, n_steps, with_head, NULL); }
 
 /* After a synchronous persistent launch: the kernel's own error flag. */
 static int ps_check(talker_t *t) {
@@ -559,7 +592,19 @@ int qwen_hip_talker_step_layers(void *state, const float *embed, float *residual
     if (pos < 0 || pos >= s->kv_max || pos >= s->rope_len) { SETERR("pos %d out of range", pos); return -1; }
     if (talker_set_pos(t, pos) != 0) goto fail;
     memcpy(t->h_in, embed, (size_t)H * sizeof(float));
-    if (t->ps_on) {
+    if (t->ps_on && t->rs_on) {
+        HCK(hipMalloc(&tmp, (size_t)L * H * sizeof(float)));
+        HCK(hipMemcpyAsync(t->ps_xin, t->h_in, (size_t)H * sizeof(float), hipMemcpyHostToDevice, t->st));
+        HCK(ps_launch_ex(t, 1, 0, (float *)tmp));
+        HCK(hipMemcpyAsync(t->h_out, t->io, (size_t)2 * H * sizeof(float), hipMemcpyDeviceToHost, t->st));
+        HCK(hipMemcpyAsync(t->h_err, t->ps_err, sizeof(int), hipMemcpyDeviceToHost, t->st));
+        HCK(hipMemcpyAsync(residuals, tmp, (size_t)L * H * sizeof(float), hipMemcpyDeviceToHost, t->st));
+        HCK(hipStreamSynchronize(t->st));
+        (void)hipFree(tmp);
+        tmp = NULL;
+        if (ps_check(t) != 0) goto fail;
+        t->dev_pos = pos + 1;
+    } else if (t->ps_on) {
         unsigned tag = 0;
         HCK(hipMemcpyAsync(t->ps_xin, t->h_in, (size_t)H * sizeof(float), hipMemcpyHostToDevice, t->st));
         HCK(ps_launch(t, 1, 0));
@@ -1027,7 +1072,7 @@ int qwen_hip_talker_launch_kernel(void *state, int kernel, int layer, int n) {
         case 0: HCK(mv(&s->qkv[layer], QT_EPI_STORE, 1, x, s->in_norm[layer], s->eps, s->qkvbuf, NULL, NULL, t->st)); break;
         case 1: HCK(qt_launch_attn(1, s->qkvbuf, s->qn[layer], s->kn[layer], s->rope_cos, s->rope_sin, s->eps, t->d_pos, 0,
                                    s->kc + lay, s->vc + lay, s->hd, (long long)s->kv_max * s->hd, s->nh, s->nkv,
-                                   s->hd, 1.0f / sqrtf((float)s->hd), s->part, s->cnt, s->attn_G, s->attn, t->st)); break;
+                                   s->hd, 1.0f / sqrtf((float)s->hd), s->part, s->cnt, s->step_G, s->attn, t->st)); break;
         case 2: HCK(mv(&s->o[layer], QT_EPI_STORE, 0, s->attn, NULL, s->eps, s->hbuf, NULL, NULL, t->st)); break;
         case 3: HCK(mv(&s->gu[layer], QT_EPI_SWIGLU, 1, x, s->post_norm[layer], s->eps, s->hbuf, NULL, NULL, t->st)); break;
         case 4: HCK(mv(&s->dn[layer], QT_EPI_STORE, 0, s->hbuf, NULL, s->eps, s->attn, NULL, NULL, t->st)); break;
