@@ -67,6 +67,23 @@ constexpr int CLR16 = LW / (4 * NHEAD);          // 16-byte groups of a layer bl
 static_assert(CLR16 * 4 * NHEAD == LW && CLR16 <= NT, "clear shares");
 constexpr int SC1 = 16;                          // buffer cache policy: agent scope (sc1)
 
+// Optional phase trace (build with -DQT_RSTEP_TRACE): s_memrealtime (100 MHz) of each
+// workgroup at marks k of (step, layer) — 0 its input wait starts, 1 the input has
+// arrived, 2 its output is published, 3 its next tile has landed; attention adds 4 (merge
+// input arrived) and 5 (merge output published); layer index L is the head (0 wait starts,
+// 1 x arrived, 2 winner published, 4 winners arrived).  Steps past TR_STEPS are not kept.
+#ifdef QT_RSTEP_TRACE
+constexpr int TR_STEPS = 8, TR_L = 33;
+__device__ unsigned long long rs_trace[NB][TR_STEPS * TR_L][8];
+#define RS_MARK(st, l, k)                                                                             \
+    do {                                                                                              \
+        if (threadIdx.x == 0 && (st) < TR_STEPS)                                                      \
+            rs_trace[blockIdx.x][(st) * TR_L + (l)][k] = __builtin_amdgcn_s_memrealtime();            \
+    } while (0)
+#else
+#define RS_MARK(st, l, k) do { } while (0)
+#endif
+
 struct RArgs {
     const Layer *layers;
     int n_layers;
@@ -108,9 +125,27 @@ __device__ __forceinline__ void land() { asm volatile("s_waitcnt vmcnt(0)" ::: "
 
 // Waits until the 16-byte groups i = tid + NT*k < n16 (byte offset off(i) in r) hold no
 // sentinel; stale groups are re-read after a short pause.  Bounded.
-template <int K, typename OffF>
+// A consumer usually waits most of a layer for its input, and re-reading all of it every
+// round trip would load the fabric with ~36 MB of polls per layer.  So each wave first
+// polls a sparse sample (groups PST*j, j = lane*4 + wave: every producer's range holds
+// some) until any sampled group is fresh — the producers then finish within a fraction of
+// a microsecond — and only then reads the whole input.
+template <int K, int PST, typename OffF>
 __device__ __forceinline__ void wait16(__amdgpu_buffer_rsrc_t r, int n16, OffF off, uint4 (&v)[K], int *err) {
-    const int tid = threadIdx.x;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    if (PST > 0) {
+        const int j = lane * 4 + wave, np = (n16 + PST - 1) / PST;
+        const bool act = j < np;
+        for (unsigned it = 0;; it++) {
+            const bool fresh = act && !stale16(ld16a(r, off(act ? j * PST : 0)));
+            if (__builtin_amdgcn_ballot_w64(fresh) != 0) break;
+            if ((it & 31) == 31) {
+                if (ld_i(err)) break;
+                if (it > POLL_LIMIT) { st_i(err, 1); break; }
+            }
+            __builtin_amdgcn_s_sleep(2);
+        }
+    }
 #pragma unroll
     for (int k = 0; k < K; k++) v[k] = (tid + NT * k < n16) ? ld16a(r, off(tid + NT * k)) : make_uint4(0, 0, 0, 0);
     for (unsigned it = 0;; it++) {
@@ -130,9 +165,23 @@ __device__ __forceinline__ void wait16(__amdgpu_buffer_rsrc_t r, int n16, OffF o
 }
 // Same for K single words per thread, element i = tid + NT*k at byte offset off(i): the
 // element-to-thread map of the RMSNorm statistics (pc_stats), so the sums keep their order.
-template <int K, typename OffF>
-__device__ __forceinline__ void wait4(__amdgpu_buffer_rsrc_t r, OffF off, unsigned (&v)[K], int *err) {
-    const int tid = threadIdx.x;
+// The sparse first poll samples words PST*j.
+template <int K, int PST, typename OffF>
+__device__ __forceinline__ void wait4(__amdgpu_buffer_rsrc_t r, int n, OffF off, unsigned (&v)[K], int *err) {
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    if (PST > 0) {
+        const int j = lane * 4 + wave, np = (n + PST - 1) / PST;
+        const bool act = j < np;
+        for (unsigned it = 0;; it++) {
+            const bool fresh = act && ld4a(r, off(act ? j * PST : 0)) != SENT;
+            if (__builtin_amdgcn_ballot_w64(fresh) != 0) break;
+            if ((it & 31) == 31) {
+                if (ld_i(err)) break;
+                if (it > POLL_LIMIT) { st_i(err, 1); break; }
+            }
+            __builtin_amdgcn_s_sleep(2);
+        }
+    }
 #pragma unroll
     for (int k = 0; k < K; k++) v[k] = ld4a(r, off(tid + NT * k));
     for (unsigned it = 0;; it++) {
@@ -297,7 +346,9 @@ __device__ __forceinline__ int head_phase(const Ctx &c, HeadLds &s, const THead 
     {
         uint4 v[2];
         const unsigned base = (c.blk(par, c.L - 1) + R_X) * 4u;
-        wait16<2>(c.rr, H / 4, [&](int i) { return base + (unsigned)i * 16u; }, v, a.err);
+        RS_MARK(step, c.L, 0);
+        wait16<2, 8>(c.rr, H / 4, [&](int i) { return base + (unsigned)i * 16u; }, v, a.err);
+        RS_MARK(step, c.L, 1);
 #pragma unroll
         for (int k = 0; k < 2; k++) put4<8, H>(s.x, 4 * (tid + NT * k), v[k]);
     }
@@ -328,15 +379,19 @@ __device__ __forceinline__ int head_phase(const Ctx &c, HeadLds &s, const THead 
             if (s.wbv[w] > bv || (s.wbv[w] == bv && s.wbi[w] < bi)) { bv = s.wbv[w]; bi = s.wbi[w]; }
     }
     // every store of this workgroup (the clears of the previous step's region among them)
-    // is performed before the winner is visible
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+    // is performed before the winner is visible: they are agent-scope (write-through)
+    // stores, so their acknowledgements are the release (a release fence would also write
+    // back the XCD's whole L2, several microseconds)
+    land();
     __syncthreads();
     unsigned long long *slots = a.slots + (size_t)par * NHEAD * 2;
     if (tid == 0) {
         st_tag(slots + 2 * c.hc, bv, tag);
         st_tag(slots + 2 * c.hc + 1, __int_as_float(bi), tag);
     }
+    RS_MARK(step, c.L, 2);
     gather<2, NT>(2 * NHEAD, [&](int i) { return slots + i; }, s.win, tag, a.err);
+    RS_MARK(step, c.L, 4);
     float gv = -INFINITY;
     int gi = 0x7FFFFFFF;
     for (int i = tid; i < NHEAD; i += NT) {
@@ -393,7 +448,9 @@ __device__ __forceinline__ void role_q(const Ctx &c, LdsP &s, int grp, int qi) {
             } else {
                 unsigned v[8];
                 const unsigned base = (c.blk(par, l - 1) + R_X) * 4u;
-                wait4<8>(c.rr, [&](int i) { return base + (unsigned)i * 4u; }, v, a.err);
+                RS_MARK(step, l, 0);
+                wait4<8, 32>(c.rr, H, [&](int i) { return base + (unsigned)i * 4u; }, v, a.err);
+                RS_MARK(step, l, 1);
 #pragma unroll
                 for (int k = 0; k < 8; k++) xv[k] = __uint_as_float(v[k]);
             }
@@ -403,8 +460,10 @@ __device__ __forceinline__ void role_q(const Ctx &c, LdsP &s, int grp, int qi) {
             pc_stats<8, NT>(xv, H, s.gain, PosChunk<16, H>(), s.wst);
             __syncthreads();
             const float sA = stage_norm_pc<true, H, NT>(s.x, s.gain, a.eps, s.pc, s.wst);
+            RS_MARK(step, l, 6);
             i32x4 acc[8];
             rdot<H, 8>(t, s.pc, 8, acc);
+            RS_MARK(step, l, 7);
             int *red = s.red[wave];
 #pragma unroll
             for (int q = 0; q < 8; q++) mf_store4(acc[q], red + q * 64);
@@ -413,11 +472,13 @@ __device__ __forceinline__ void role_q(const Ctx &c, LdsP &s, int grp, int qi) {
                 mf_rowsum(red + (lane >> 2) * 64, lane & 3, d);
                 put(c.wp(par, l, R_QKV + rw + lane), __fmul_rn(qt_pc_dot(d[0], d[1], d[2], d[3], sA), rs));
             }
+            RS_MARK(step, l, 2);
             if (step > 0) clear_share(c, par ^ 1, l);
             __syncthreads();   // the tile registers and the gains buffer are free
             if (l + 1 < c.L) load(l + 1);
             else if (!last) load(0);
             land();
+            RS_MARK(step, l, 3);
         }
         // the codec-head tile is loaded here, not inside the layer loop, so that its
         // registers are live only for the head
@@ -464,9 +525,11 @@ __device__ __forceinline__ void role_o(const Ctx &c, LdsP &s, int oi) {
                 const unsigned ba = (c.blk(par, l) + R_ATT) * 4u;
                 const unsigned bx = l > 0 ? (c.blk(par, l - 1) + R_X + row0) * 4u : 0u;
                 const int n16 = QD / 4 + (l > 0 ? OROWS / 4 : 0);
-                wait16<3>(c.rr, n16, [&](int i) {
+                RS_MARK(step, l, 0);
+                wait16<3, 8>(c.rr, n16, [&](int i) {
                     return i < QD / 4 ? ba + (unsigned)(2 * (i % NT) + i / NT) * 16u : bx + (unsigned)(i - QD / 4) * 16u;
                 }, v, a.err);
+                RS_MARK(step, l, 1);
             }
             float m = 0.f;
 #pragma unroll
@@ -488,8 +551,10 @@ __device__ __forceinline__ void role_o(const Ctx &c, LdsP &s, int oi) {
                 pc_put8<true, QD>(s.pc, tid, v8, ps.isc);
             }
             __syncthreads();
+            RS_MARK(step, l, 6);
             i32x4 acc[8];
             rdot<QD, 8>(t, s.pc, 8, acc);
+            RS_MARK(step, l, 7);
             int *red = s.red[wave];
 #pragma unroll
             for (int q = 0; q < 8; q++) mf_store4(acc[q], red + q * 64);
@@ -499,9 +564,11 @@ __device__ __forceinline__ void role_o(const Ctx &c, LdsP &s, int oi) {
                 const float vv = __fmul_rn(qt_pc_dot(d[0], d[1], d[2], d[3], ps.s), rs);
                 put(c.wp(par, l, R_XA + rw + lane), __fadd_rn(s.resid[wave * 32 + lane], vv));
             }
+            RS_MARK(step, l, 2);
             if (step > 0) clear_share(c, par ^ 1, l);
             __syncthreads();
             if (l + 1 < c.L) { load(l + 1); land(); }
+            RS_MARK(step, l, 3);
         }
         if (a.with_head) th.load(a.head_w, nullptr, c.hc * HEADR + wave * (HEADR / 4));
         land();
@@ -536,7 +603,9 @@ __device__ __forceinline__ void role_gu(const Ctx &c, LdsP &s, int gi) {
             {
                 unsigned v[8];
                 const unsigned base = (c.blk(par, l) + R_XA) * 4u;
-                wait4<8>(c.rr, [&](int i) { return base + (unsigned)i * 4u; }, v, a.err);
+                RS_MARK(step, l, 0);
+                wait4<8, 32>(c.rr, H, [&](int i) { return base + (unsigned)i * 4u; }, v, a.err);
+                RS_MARK(step, l, 1);
 #pragma unroll
                 for (int k = 0; k < 8; k++) { xv[k] = __uint_as_float(v[k]); s.x[xpos<16, H>(tid + NT * k)] = xv[k]; }
             }
@@ -544,8 +613,10 @@ __device__ __forceinline__ void role_gu(const Ctx &c, LdsP &s, int gi) {
             pc_stats<8, NT>(xv, H, s.gain, PosChunk<16, H>(), s.wst);
             __syncthreads();
             const float sD = stage_norm_pc<true, H, NT>(s.x, s.gain, a.eps, s.pc, s.wst);
+            RS_MARK(step, l, 6);
             i32x4 acc[8];
             rdot<H, 8>(t, s.pc, 8, acc);
+            RS_MARK(step, l, 7);
             int *red = s.red[wave];
 #pragma unroll
             for (int q = 0; q < 8; q++) mf_store4(acc[q], red + q * 64);
@@ -558,9 +629,11 @@ __device__ __forceinline__ void role_gu(const Ctx &c, LdsP &s, int gi) {
                 const float up = __fmul_rn(qt_pc_dot(du[0], du[1], du[2], du[3], sD), rsu);
                 put(c.wp(par, l, R_H + rw / 2 + lane), gt / (1.0f + expf(-gt)) * up);
             }
+            RS_MARK(step, l, 2);
             if (step > 0) clear_share(c, par ^ 1, l);
             __syncthreads();
             if (l + 1 < c.L) { load(l + 1); land(); }
+            RS_MARK(step, l, 3);
         }
         if (a.with_head) th.load(a.head_w, nullptr, c.hc * HEADR + wave * (HEADR / 4));
         land();
@@ -613,11 +686,13 @@ __device__ __forceinline__ void role_dn(const Ctx &c, LdsD &s, int di) {
             {
                 const unsigned bh = (c.blk(par, l) + R_H) * 4u, bx = (c.blk(par, l) + R_XA + row0) * 4u;
                 const int n16 = F / 4 + nrows / 4;
-                wait16<7>(c.rr, n16, [&](int i) {
+                RS_MARK(step, l, 0);
+                wait16<7, 16>(c.rr, n16, [&](int i) {
                     if (i >= F / 4) return bx + (unsigned)(i - F / 4) * 16u;
                     const int j = i / NT;                       // slot: unit tid + NT*(j/2), half j%2
                     return bh + (unsigned)(2 * (i % NT + NT * (j >> 1)) + (j & 1)) * 16u;
                 }, v, a.err);
+                RS_MARK(step, l, 1);
             }
             float m = 0.f;
 #pragma unroll
@@ -639,6 +714,7 @@ __device__ __forceinline__ void role_dn(const Ctx &c, LdsD &s, int di) {
                 pc_put8<true, F>(s.pc, tid + NT * k, v8, ps.isc);
             }
             __syncthreads();
+            RS_MARK(step, l, 6);
             // quads 0, 1 from registers, quad 2 from LDS; two accumulator chains each
             i32x4 acc[3][2];
 #pragma unroll
@@ -657,6 +733,7 @@ __device__ __forceinline__ void role_dn(const Ctx &c, LdsD &s, int di) {
                     w2 = w2n;
                 }
             }
+            RS_MARK(step, l, 7);
             int *red = s.red[wave];
 #pragma unroll
             for (int q = 0; q < 3; q++)
@@ -669,9 +746,11 @@ __device__ __forceinline__ void role_dn(const Ctx &c, LdsD &s, int di) {
                 put(c.wp(par, l, R_X + rw + lane), xo);
                 if (a.layer_out && last) a.layer_out[(size_t)l * H + rw + lane] = xo;
             }
+            RS_MARK(step, l, 2);
             if (step > 0) clear_share(c, par ^ 1, l);
             __syncthreads();
             if (l + 1 < c.L) { load(l + 1); land(); }
+            RS_MARK(step, l, 3);
         }
         if (a.with_head) th.load(a.head_w, nullptr, c.hc * HEADR + wave * (HEADR / 4));
         land();
@@ -739,11 +818,13 @@ __device__ __forceinline__ void role_att(const Ctx &c, LdsA &s, int g, int ch) {
                 {
                     uint4 v[1];
                     const unsigned bq = c.blk(par, l) * 4u;
-                    wait16<1>(c.rr, (HPK * HD + 2 * HD) / 4, [&](int i) {
+                    RS_MARK(step, l, 0);
+                    wait16<1, 0>(c.rr, (HPK * HD + 2 * HD) / 4, [&](int i) {
                         const int w = i < 64 ? R_QKV + HPK * HD * g + 4 * i
                                     : i < 96 ? R_QKV + QD + HD * g + 4 * (i - 64) : R_QKV + QD + KVD + HD * g + 4 * (i - 96);
                         return bq + (unsigned)w * 4u;
                     }, v, a.err);
+                    RS_MARK(step, l, 1);
                     if (tid < (HPK * HD + 2 * HD) / 4)
                         *reinterpret_cast<float4 *>(s.qkv + 4 * tid) = make_float4(
                             __uint_as_float(v[0].x), __uint_as_float(v[0].y), __uint_as_float(v[0].z), __uint_as_float(v[0].w));
@@ -792,6 +873,7 @@ __device__ __forceinline__ void role_att(const Ctx &c, LdsA &s, int g, int ch) {
                                         kf[b][tt * 4 + s2] = *reinterpret_cast<const uint4 *>(s.knew + 32 * s2 + 8 * kg);
                     }
                 }
+                RS_MARK(step, l, 6);
                 QtAttRun run;
                 qt_att_run_init(run);
 #pragma unroll
@@ -835,6 +917,7 @@ __device__ __forceinline__ void role_att(const Ctx &c, LdsA &s, int g, int ch) {
                     qt_att_pv_n<HPK>((nk + 31) >> 5, pp, KVB, ml, s.v[b], 32 * wave, lane, o, M, lsum);
                     qt_att_run_add(run, o, M, lsum);
                 }
+                RS_MARK(step, l, 7);
                 // partial of this chunk: o (head lane/16, dims 32 wave + lane%16 and +16), m, l
                 const int hq = lane >> 4;
                 if (hq < HPK) {
@@ -846,6 +929,7 @@ __device__ __forceinline__ void role_att(const Ctx &c, LdsA &s, int g, int ch) {
                         put(c.wp(par, l, R_PML + ((g * HPK + hq) * ACH + ch) * 2 + 1), run.l);
                     }
                 }
+                RS_MARK(step, l, 2);
                 if (append && wave == 3) {
                     // KV append: agent-scope 32-bit stores of adjacent bf16 pairs
                     uint32_t *kd = reinterpret_cast<uint32_t *>(a.kc + (((size_t)l * NKV + g) * a.kv_max + pos) * HD);
@@ -863,7 +947,7 @@ __device__ __forceinline__ void role_att(const Ctx &c, LdsA &s, int g, int ch) {
                 {
                     uint4 v[1];
                     const unsigned bo = (c.blk(par, l) + R_PO + ((g * HPK + hh) * 4 + dblk) * ACH * 32) * 4u;
-                    wait16<1>(c.rr, 8 * nch, [&](int i) { return bo + (unsigned)i * 16u; }, v, a.err);
+                    wait16<1, 0>(c.rr, 8 * nch, [&](int i) { return bo + (unsigned)i * 16u; }, v, a.err);
                     unsigned long long mlw = 0;
                     if (tid >= 64 && tid < 64 + nch) {
                         const unsigned long long *p = reinterpret_cast<const unsigned long long *>(
@@ -885,6 +969,7 @@ __device__ __forceinline__ void role_att(const Ctx &c, LdsA &s, int g, int ch) {
                             __uint_as_float(v[0].x), __uint_as_float(v[0].y), __uint_as_float(v[0].z), __uint_as_float(v[0].w));
                 }
                 __syncthreads();
+                RS_MARK(step, l, 4);
                 // output d = tid / 8 over the chunks cc = tid % 8: softmax_merge32 over 32
                 // lanes with lanes >= nch idle adds exact zeros after the 8-lane tree, so the
                 // 8-lane tree plus one +0 gives the same bits
@@ -902,11 +987,13 @@ __device__ __forceinline__ void role_att(const Ctx &c, LdsA &s, int g, int ch) {
                 Ls += dpp_mov<DPP_HALF_MIRROR>(Ls); Vs += dpp_mov<DPP_HALF_MIRROR>(Vs);
                 Ls = Ls + 0.0f; Vs = Vs + 0.0f;
                 if (cc == 0) put(c.wp(par, l, R_ATT + (2 * g + hh) * HD + 32 * dblk + d), Vs * (1.0f / Ls));
+                RS_MARK(step, l, 5);
             }
             __syncthreads();   // the chunk's LDS (values, staging) is free for the next copy
             if (l + 1 < c.L) prefetch(l + 1, ge);
             else if (!last) prefetch(0, Geo(pos + 1));
             land();
+            RS_MARK(step, l, 3);
         }
     }
 }
@@ -933,6 +1020,12 @@ __global__ __launch_bounds__(NT, 1) void k_rstep(RArgs a) {
 }
 }  // namespace rs
 }  // namespace ps
+
+#ifdef QT_RSTEP_TRACE
+extern "C" hipError_t qt_rstep_trace_read(unsigned long long *out) {
+    return hipMemcpyFromSymbol(out, HIP_SYMBOL(ps::rs::rs_trace), sizeof(ps::rs::rs_trace), 0, hipMemcpyDeviceToHost);
+}
+#endif
 
 extern "C" int qt_rstep_supported(int prec, int hidden, int inter, int n_heads, int n_kv, int head_dim, int kv_max,
                                   int n_layers) {
