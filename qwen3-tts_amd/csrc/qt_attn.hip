@@ -45,6 +45,8 @@ struct QtAttnArgs {
     // partials and counters; d_pos + z is its position (batched step)
     long long q_bs, kv_bs, out_bs, part_bs;
     int min_chunk;           // chunks hold at least this many keys (0: ceil(L/G) rounded to 16)
+    int onepass;             // !BATCH, chunks <= 512 keys: one softmax over the chunk (qt_att_fold)
+                             // instead of a running state across its 128-key blocks
 };
 
 #define QT_KVB 128   // keys of a chunk staged in LDS at once
@@ -247,6 +249,42 @@ __global__ __launch_bounds__(QT_WG) void k_attn(QtAttnArgs a) {
             const float o2[2] = {src[2 + 2 * wave], src[3 + 2 * wave]};
             if (src[0] != -INFINITY) qt_att_run_add(run, o2, src[0], src[1]);
         }
+    } else if (a.onepass) {
+        // ---- 2c. one pass: the blocks are staged and scored in turn, each k-tile's P.V is
+        // kept apart (qt_att_pv1) and all are folded once with the chunk maximum, the
+        // arithmetic of the fused role-specialised step (qt_rstep.hip) ----
+        constexpr int NT1 = 16;                   // k-tiles of 32 keys (chunks <= 512 keys)
+        float ot[NT1][2], mt[NT1], lt[NT1];
+        const int hc = pg < HPK ? pg : HPK - 1;
+#pragma unroll
+        for (int b = 0; b < NT1 / 4; b++) {
+            const int kb = KVB * b;
+            if (kb >= n) break;
+            const int nk = min(KVB, n - kb);
+            if (kb > 0) {
+                __syncthreads();
+                stage(kb, true, true);
+                __builtin_amdgcn_s_waitcnt(0);
+                const int nrow = pos - j0 - kb;
+                if (PREP && wave == 0 && nrow >= 0 && nrow < nk) qt_att_put_kv(s_kv[0], s_kv[1], nrow, knew, vnew, lane);
+                qt_att_zero_vrows(s_kv[1], nk, (nk + 31) & ~31, tid, QT_WG);
+                __syncthreads();
+            }
+            if (32 * wave < nk)
+                qt_att_tiles<HPK>(&qp[0][0], s_kv[0], &pp[0][0], KVB, &ml[0][0][0], wave, nk, scale2, lane);
+            __syncthreads();
+            {
+                float o4[4][2];
+                qt_att_pv4(&pp[0][0], KVB, 0, s_kv[1], 32 * wave, lane, o4);
+#pragma unroll
+                for (int t = 0; t < 4; t++) {
+                    ot[4 * b + t][0] = o4[t][0]; ot[4 * b + t][1] = o4[t][1];
+                    mt[4 * b + t] = ml[t][hc][0];
+                    lt[4 * b + t] = ml[t][hc][1];
+                }
+            }
+        }
+        qt_att_fold<NT1>((n + 31) >> 5, ot, mt, lt, run.o, run.m, run.l);
     } else
     for (int kb = 0; kb < n; kb += KVB) {
         const int nk = min(KVB, n - kb);
@@ -345,6 +383,7 @@ static hipError_t attn_launch(const QtAttnArgs &a, int prep, int head_dim, int G
     if (head_dim != QT_HD || a.n_kv <= 0 || a.n_heads % a.n_kv) return hipErrorInvalidValue;
     if (G <= 0 || G > QT_ATT_G || nz <= 0 || nz > 65535) return hipErrorInvalidValue;
     if (!prep && (a.Lval <= 0 || a.Lval > G * QT_CH_MAX)) return hipErrorInvalidValue;
+    if (a.onepass && a.min_chunk > 0) return hipErrorInvalidValue;
     const int hpk = a.n_heads / a.n_kv;
     const bool batch = a.min_chunk > 0;
     const dim3 grid = batch ? dim3(a.n_kv, nz, G) : dim3(G, a.n_kv, nz);
@@ -372,6 +411,25 @@ extern "C" hipError_t qt_launch_attn(int prep, const float *q, const float *qn, 
     a.n_heads = n_heads; a.n_kv = n_kv; a.scale = scale; a.part = part; a.cnt = cnt; a.out = out;
     a.q_bs = a.kv_bs = a.out_bs = a.part_bs = 0;
     a.min_chunk = 0;
+    a.onepass = 0;
+    return attn_launch(a, prep, head_dim, G, 1, st);
+}
+
+// The same with each chunk as one softmax over its keys (chunks of at most 512 keys:
+// G * 512 >= the cache length): the arithmetic of the role-specialised fused step.
+extern "C" hipError_t qt_launch_attn_onepass(int prep, const float *q, const float *qn, const float *kn,
+                                             const float *rc, const float *rs, float eps, const int *d_pos,
+                                             int Lval, uint16_t *K, uint16_t *V, long long pos_stride,
+                                             long long head_stride, int n_heads, int n_kv, int head_dim,
+                                             float scale, float *part, unsigned *cnt, int G, float *out,
+                                             hipStream_t st) {
+    QtAttnArgs a;
+    a.q = q; a.qn = qn; a.kn = kn; a.rc = rc; a.rs = rs; a.eps = eps; a.d_pos = d_pos; a.Lval = Lval;
+    a.K = K; a.V = V; a.pos_stride = pos_stride; a.head_stride = head_stride;
+    a.n_heads = n_heads; a.n_kv = n_kv; a.scale = scale; a.part = part; a.cnt = cnt; a.out = out;
+    a.q_bs = a.kv_bs = a.out_bs = a.part_bs = 0;
+    a.min_chunk = 0;
+    a.onepass = 1;
     return attn_launch(a, prep, head_dim, G, 1, st);
 }
 
@@ -399,6 +457,7 @@ extern "C" hipError_t qt_launch_attn_b(const float *q, long long q_bs, const flo
     a.n_heads = n_heads; a.n_kv = n_kv; a.scale = scale; a.part = part; a.cnt = cnt; a.out = out;
     a.q_bs = q_bs; a.kv_bs = kv_bs; a.out_bs = out_bs; a.part_bs = part_bs;
     a.min_chunk = QT_B_MIN_CHUNK;
+    a.onepass = 0;
     return attn_launch(a, 1, head_dim, G, B, st);
 }
 

@@ -24,6 +24,10 @@ hipError_t qt_launch_attn(int prep, const float *q, const float *qn, const float
                           const float *rs, float eps, const int *d_pos, int Lval, uint16_t *K, uint16_t *V,
                           long long pos_stride, long long head_stride, int n_heads, int n_kv, int head_dim,
                           float scale, float *part, unsigned *cnt, int G, float *out, hipStream_t st);
+hipError_t qt_launch_attn_onepass(int prep, const float *q, const float *qn, const float *kn, const float *rc,
+                          const float *rs, float eps, const int *d_pos, int Lval, uint16_t *K, uint16_t *V,
+                          long long pos_stride, long long head_stride, int n_heads, int n_kv, int head_dim,
+                          float scale, float *part, unsigned *cnt, int G, float *out, hipStream_t st);
 hipError_t qt_launch_attn_b(const float *q, long long q_bs, const float *qn, const float *kn, const float *rc,
                             const float *rs, float eps, const int *d_pos, uint16_t *K, uint16_t *V, long long kv_bs,
                             long long pos_stride, long long head_stride, int n_heads, int n_kv, int head_dim,

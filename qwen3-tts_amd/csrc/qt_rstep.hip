@@ -74,7 +74,7 @@ constexpr int SC1 = 16;                          // buffer cache policy: agent s
 // 1 x arrived, 2 winner published, 4 winners arrived).  Steps past TR_STEPS are not kept.
 #ifdef QT_RSTEP_TRACE
 constexpr int TR_STEPS = 8, TR_L = 33;
-__device__ unsigned long long rs_trace[NB][TR_STEPS * TR_L][8];
+__device__ unsigned long long rs_trace[NB][TR_STEPS * TR_L][12];
 #define RS_MARK(st, l, k)                                                                             \
     do {                                                                                              \
         if (threadIdx.x == 0 && (st) < TR_STEPS)                                                      \
@@ -207,60 +207,95 @@ __device__ __forceinline__ void put4(float *x, int e0, const uint4 &v) {
         make_float4(__uint_as_float(v.x), __uint_as_float(v.y), __uint_as_float(v.z), __uint_as_float(v.w));
 }
 
-// ---- MFMA row tiles (4 rows per MFMA: row m % 4 of column part m / 4, TileM4 layout) ----
-// NQ quads of 4 consecutive rows per wave over COLS columns: w[q][s] covers rows
-// row0 + 4q .. +3, columns s*256 + part*64 + 16*kg.
-template <int COLS, int NQD>
-struct RTile {
-    static constexpr int S = COLS / 256;
-    uint4 w[NQD][S];
-    // buffer loads: one 32-bit lane offset shared by every load, the row and step parts in
-    // scalar registers (64-bit per-lane addresses would hold two VGPRs per load in flight)
-    __device__ __forceinline__ void load(const uint8_t *W, int row0, int nq) {
+// ---- MFMA row tiles: 16 weight rows x 64 columns per v_mfma_i32_16x16x64_i8 -----------
+// A = 16 rows (lane l: row l % 16, columns 16*(l/16) .. +15 of the 64-column step), B =
+// the four activation planes of those 64 columns as columns 0..3 (columns 4..15 zero),
+// so D[r][n] accumulates the plane-n dot product of row r over the steps: lane l ends
+// with rows 4*(l/16) + i (register i) of plane l % 16, and the four planes of a row are
+// the four lanes of one quad (DPP quad broadcasts, no LDS round trip).  Exact int32 sums,
+// so the values equal every other way of forming the dot products.
+//
+// Pieces live in plane-major LDS rows of COLS + 16 bytes (the pad puts the four planes of
+// one column range on different banks).
+template <int COLS> constexpr int pcs() { return COLS + 16; }
+template <int COLS>
+__device__ __forceinline__ void pcw_put8(uint8_t *pc, int u, const float (&v)[8], float isc) {
+    uint2 pl[4];
+    qt_pc8(v, isc, pl);
+#pragma unroll
+    for (int q = 0; q < 4; q++) *reinterpret_cast<uint2 *>(pc + q * pcs<COLS>() + 8 * u) = pl[q];
+}
+// B fragment of columns col0 .. col0 + 63
+template <int COLS>
+__device__ __forceinline__ uint4 pcw_b(const uint8_t *pc, int col0) {
+    const int lane = threadIdx.x & 63, n = lane & 15, kg = lane >> 4;
+    const uint4 b = *reinterpret_cast<const uint4 *>(pc + (n & 3) * pcs<COLS>() + col0 + 16 * kg);
+    return n < 4 ? b : make_uint4(0, 0, 0, 0);
+}
+// NT16 tiles of 16 rows (row0 + 16t ..) over S 64-column steps from column c0.  Buffer
+// loads: one 32-bit lane offset shared by every load, the row and step parts in scalar
+// registers (64-bit per-lane addresses would hold two VGPRs per load in flight).  Rows at
+// or past row_end are not loaded (their A stays zero).
+template <int COLS, int NT16, int S>
+struct RTile16 {
+    uint4 w[NT16][S];
+    __device__ __forceinline__ void load(const uint8_t *W, int row0, int c0, int row_end) {
         const int lane = threadIdx.x & 63, m = lane & 15, kg = lane >> 4;
         const __amdgpu_buffer_rsrc_t r = brsrc(uni(W));
-        const unsigned voff = (unsigned)((m & 3) * COLS + (m >> 2) * 64 + kg * 16);
+        const unsigned voff = (unsigned)(m * COLS + 16 * kg);
 #pragma unroll
-        for (int q = 0; q < NQD; q++)
-            if (q < nq) {
+        for (int t = 0; t < NT16; t++) {
+            const bool ok = row0 + 16 * t + m < row_end;
 #pragma unroll
-                for (int s = 0; s < S; s++) {
-                    const u32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(
-                        r, voff, __builtin_amdgcn_readfirstlane((row0 + 4 * q) * COLS + s * 256), 0);
-                    w[q][s] = make_uint4(v.x, v.y, v.z, v.w);
-                }
+            for (int s = 0; s < S; s++) {
+                const u32x4_t v = ok ? __builtin_amdgcn_raw_buffer_load_b128(
+                                           r, voff, __builtin_amdgcn_readfirstlane((row0 + 16 * t) * COLS + c0 + 64 * s), 0)
+                                     : u32x4_t{0, 0, 0, 0};
+                w[t][s] = make_uint4(v.x, v.y, v.z, v.w);
             }
+        }
     }
 };
-// acc[q] = the TileM4 result of quad q against the pieces (B fragment of step s read one
-// step ahead, shared by the quads); quads >= nq are skipped.  Two accumulator chains per
-// quad when there are few quads, so no MFMA waits for the previous one of its chain.
-template <int COLS, int NQD>
-__device__ __forceinline__ void rdot(const RTile<COLS, NQD> &t, const uint8_t *pc, int nq, i32x4 (&acc)[NQD]) {
-    constexpr int S = COLS / 256;
-    constexpr int CH = NQD >= 4 ? 1 : 2;
-    i32x4 a[NQD][CH];
+// acc[t] = tile t against the pieces of columns c0 .. c0 + 64*S; CH accumulator chains per
+// tile so that no MFMA waits for the previous one of its chain
+template <int COLS, int NT16, int S, int CH>
+__device__ __forceinline__ void rdot16(const RTile16<COLS, NT16, S> &t, const uint8_t *pc, int c0, i32x4 (&acc)[NT16]) {
+    i32x4 a[NT16][CH];
 #pragma unroll
-    for (int q = 0; q < NQD; q++)
+    for (int q = 0; q < NT16; q++)
 #pragma unroll
         for (int c = 0; c < CH; c++) a[q][c] = i32x4{0, 0, 0, 0};
-    uint4 b = mf_b4<COLS>(pc, 0);
+    uint4 b = pcw_b<COLS>(pc, c0);
 #pragma unroll
     for (int s = 0; s < S; s++) {
-        const uint4 bn = mf_b4<COLS>(pc, s + 1 < S ? s + 1 : s);
+        const uint4 bn = pcw_b<COLS>(pc, c0 + 64 * (s + 1 < S ? s + 1 : s));
 #pragma unroll
-        for (int q = 0; q < NQD; q++)
-            if (q < nq) a[q][s % CH] = mfma_i8(t.w[q][s], b, a[q][s % CH]);
+        for (int q = 0; q < NT16; q++) a[q][s % CH] = mfma_i8(t.w[q][s], b, a[q][s % CH]);
         b = bn;
     }
 #pragma unroll
-    for (int q = 0; q < NQD; q++) {
+    for (int q = 0; q < NT16; q++) {
         acc[q] = a[q][0];
 #pragma unroll
         for (int c = 1; c < CH; c++) acc[q] += a[q][c];
     }
 }
-
+// plane q of each quad's lane 0 value, broadcast from lane q of the quad
+template <int Q>
+__device__ __forceinline__ int quad_bcast(int v) {
+    return __builtin_amdgcn_update_dpp(0, v, Q | (Q << 2) | (Q << 4) | (Q << 6), 0xf, 0xf, false);
+}
+// The four exact plane sums of row 4*(lane/16) + i of a tile, valid in lanes with lane % 16
+// == 0.
+__device__ __forceinline__ void tile_rows(const i32x4 &acc, int (&d)[4][4]) {
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        d[i][0] = acc[i];
+        d[i][1] = quad_bcast<1>(acc[i]);
+        d[i][2] = quad_bcast<2>(acc[i]);
+        d[i][3] = quad_bcast<3>(acc[i]);
+    }
+}
 // ---- LDS --------------------------------------------------------------------------------
 struct HeadLds {
     float x[H];                  // x of the last layer, chunk-transposed (EPC 8)
@@ -271,18 +306,17 @@ struct HeadLds {
     float win[2 * NHEAD];
 };
 struct LdsP {                    // Q, O, GU (2048-column projections)
-    float x[H];                  // gathered input, chunk-transposed (EPC 16)
-    float gain[H];
-    uint8_t pc[4 * H];
-    int red[4][8 * 64];
+    float xs[H];                 // the input in element order (RMSNorm: statistics order -> unit order)
+    uint8_t pc[4 * pcs<H>()];
+    int red[8 * 16][4][4];       // partial plane sums [row][wave][plane] (K split over the waves)
     float resid[OROWS];
     float wst[8];
     HeadLds hd;
 };
 struct LdsD {                    // DN
-    uint8_t pc[4 * F];
-    uint4 tw[4][F / 256][64];    // row-quad 2 of each wave's rows (when it has one): [wave][step][lane]
-    int red[4][3 * 64];
+    uint8_t pc[4 * pcs<F>()];
+    uint4 tw[4][F / 4 / 64][64]; // tile 2 (rows 32..47): [wave][step][lane]
+    int red[4][3][16][4];        // partial plane sums [wave][tile][row][plane]
     float resid[48];
     float wst[8];
     HeadLds hd;
@@ -290,8 +324,8 @@ struct LdsD {                    // DN
 struct LdsA {                    // ATT + MRG
     uint16_t v[ABLK][KVB * HD];  // value rows of the chunk (qt_attn_mf.h swizzle), per 128-key block
     uint16_t qp[16][HD];
-    uint16_t pp[2][16][KVB];     // probability pieces, by block parity
-    float ml[2][4][HPK][2];
+    uint16_t pp[16][ABLK * KVB]; // probability pieces of the chunk's keys, row 4h+p
+    float ml[4 * ABLK][HPK][2];  // per-k-tile (max, exp-sum)
     float qkv[HPK * HD + 2 * HD];
     uint16_t knew[HD], vnew[HD];
     float mo[ACH][32];           // merge inputs
@@ -419,18 +453,99 @@ __device__ __forceinline__ int head_phase(const Ctx &c, HeadLds &s, const THead 
     return a.with_head ? gi : -1;
 }
 
+// 16-byte / 8-byte agent-scope stores of hand-off words
+__device__ __forceinline__ void put4w(const Ctx &c, unsigned word, float a0, float a1, float a2, float a3) {
+    const u32x4_t v = {__float_as_uint(a0), __float_as_uint(a1), __float_as_uint(a2), __float_as_uint(a3)};
+    __builtin_amdgcn_raw_buffer_store_b128(v, c.rr, word * 4u, 0, SC1);
+}
+__device__ __forceinline__ void put2w(const Ctx &c, unsigned word, float a0, float a1) {
+    typedef unsigned u32x2_t __attribute__((ext_vector_type(2)));
+    const u32x2_t v = {__float_as_uint(a0), __float_as_uint(a1)};
+    __builtin_amdgcn_raw_buffer_store_b64(v, c.rr, word * 4u, 0, SC1);
+}
+
+// K split over the waves: each wave's partial plane sums of its tiles' rows into
+// red[row][wave][plane] (the lanes of plane columns 0..3), then a barrier; ksplit_row adds
+// the four waves' integers for one row.
+template <int NT16>
+__device__ __forceinline__ void ksplit_store(const i32x4 (&acc)[NT16], int (*red)[4][4]) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, n = lane & 15, kg = lane >> 4;
+    if (n < 4) {
+#pragma unroll
+        for (int t = 0; t < NT16; t++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) red[16 * t + 4 * kg + i][wave][n] = acc[t][i];
+    }
+    __syncthreads();
+}
+__device__ __forceinline__ void ksplit_row(const int (*red)[4][4], int r, int (&d)[4]) {
+    const int4 a = *reinterpret_cast<const int4 *>(red[r][0]), b = *reinterpret_cast<const int4 *>(red[r][1]);
+    const int4 e = *reinterpret_cast<const int4 *>(red[r][2]), f = *reinterpret_cast<const int4 *>(red[r][3]);
+    d[0] = a.x + b.x + e.x + f.x; d[1] = a.y + b.y + e.y + f.y;
+    d[2] = a.z + b.z + e.z + f.z; d[3] = a.w + b.w + e.w + f.w;
+}
+
+// Pieces of RMSNorm(x)*g: x arrives in the statistics' order (thread t: elements t + NT*k),
+// the statistics are summed in that order (thread in k order, wave butterfly, waves in
+// order: pc_stats), x goes through LDS to unit order (thread u: elements 8u .. 8u+7) and
+// the pieces are made there from the same values with the same operations as
+// stage_norm_pc.  gc: gains of the thread's statistics elements, gu: of its unit.  Returns
+// the pieces' scale; ends with a barrier.
+__device__ __forceinline__ float norm_pieces(const float (&xv)[8], const float (&gc)[8], const float (&gu)[8], float *xs,
+                                             float *wst, uint8_t *pc, float eps) {
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    float ss = 0.f, m = 0.f;
+#pragma unroll
+    for (int k = 0; k < 8; k++) {
+        ss = fmaf(xv[k], xv[k], ss);
+        m = fmaxf(m, fabsf(xv[k] * gc[k]));
+    }
+    ss = group_sum<64>(ss);
+    m = group_max<64>(m);
+    if (lane == 0) { wst[2 * wave] = ss; wst[2 * wave + 1] = m; }
+#pragma unroll
+    for (int k = 0; k < 8; k++) xs[tid + NT * k] = xv[k];
+    __syncthreads();
+    float inv;
+    QtPcScale ps;
+    pc_norm_scale<4>(wst, H, eps, inv, ps);
+    const float4 p0 = *reinterpret_cast<const float4 *>(xs + 8 * tid), p1 = *reinterpret_cast<const float4 *>(xs + 8 * tid + 4);
+    const float v[8] = {(p0.x * inv) * gu[0], (p0.y * inv) * gu[1], (p0.z * inv) * gu[2], (p0.w * inv) * gu[3],
+                        (p1.x * inv) * gu[4], (p1.y * inv) * gu[5], (p1.z * inv) * gu[6], (p1.w * inv) * gu[7]};
+    pcw_put8<H>(pc, tid, v, ps.isc);
+    __syncthreads();
+    return ps.s;
+}
+// the RMSNorm gains a thread needs: statistics elements tid + NT*k, unit elements 8 tid ..
+__device__ __forceinline__ void load_norm_gains(const float *g, float (&gc)[8], float (&gu)[8]) {
+    const int tid = threadIdx.x;
+    g = uni(g);
+#pragma unroll
+    for (int k = 0; k < 8; k++) gc[k] = ldg(g + tid + NT * k);
+    const float4 a = ldg(reinterpret_cast<const float4 *>(g + 8 * tid)), b = ldg(reinterpret_cast<const float4 *>(g + 8 * tid + 4));
+    gu[0] = a.x; gu[1] = a.y; gu[2] = a.z; gu[3] = a.w; gu[4] = b.x; gu[5] = b.y; gu[6] = b.z; gu[7] = b.w;
+}
+__device__ __forceinline__ float4 f4(const uint4 &v) {
+    return make_float4(__uint_as_float(v.x), __uint_as_float(v.y), __uint_as_float(v.z), __uint_as_float(v.w));
+}
+__device__ __forceinline__ float amax4(const uint4 &v) {
+    return fmaxf(fmaxf(fabsf(__uint_as_float(v.x)), fabsf(__uint_as_float(v.y))),
+                 fmaxf(fabsf(__uint_as_float(v.z)), fabsf(__uint_as_float(v.w))));
+}
+
 // ---- Q: q|k|v rows ------------------------------------------------------------------------
 __device__ __forceinline__ void role_q(const Ctx &c, LdsP &s, int grp, int qi) {
     const RArgs &a = c.a;
-    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    // 128 rows; wave w takes columns 512w .. +511 of all of them
     const int row0 = qi < 2 ? (2 * grp + qi) * HD : qi == 2 ? QD + grp * HD : QD + KVD + grp * HD;
-    const int rw = row0 + wave * 32;
-    RTile<H, 8> t;
+    RTile16<H, 8, H / 4 / 64> t;
     float rs = 0.f;
+    float gc[8], gu[8];
     auto load = [&](int l) {
-        t.load(c.ly[l].w[0], rw, 8);
-        if (lane < 32) rs = ldg(uni(c.ly[l].s[0]) + rw + lane);
-        load_gains<4, 16, H>(c.ly[l].in_norm, s.gain);
+        t.load(c.ly[l].w[0], row0, wave * (H / 4), row0 + QROWS);
+        if (tid < QROWS) rs = ldg(uni(c.ly[l].s[0]) + row0 + tid);
+        load_norm_gains(c.ly[l].in_norm, gc, gu);
     };
     THead th;
     load_gains<4, 8, H>(a.final_norm, s.hd.gain);
@@ -454,27 +569,20 @@ __device__ __forceinline__ void role_q(const Ctx &c, LdsP &s, int grp, int qi) {
 #pragma unroll
                 for (int k = 0; k < 8; k++) xv[k] = __uint_as_float(v[k]);
             }
-#pragma unroll
-            for (int k = 0; k < 8; k++) s.x[xpos<16, H>(tid + NT * k)] = xv[k];
-            __syncthreads();   // the gains' LDS copy has landed for every wave (land() before)
-            pc_stats<8, NT>(xv, H, s.gain, PosChunk<16, H>(), s.wst);
-            __syncthreads();
-            const float sA = stage_norm_pc<true, H, NT>(s.x, s.gain, a.eps, s.pc, s.wst);
+            const float sA = norm_pieces(xv, gc, gu, s.xs, s.wst, s.pc, a.eps);
             RS_MARK(step, l, 6);
             i32x4 acc[8];
-            rdot<H, 8>(t, s.pc, 8, acc);
+            rdot16<H, 8, H / 4 / 64, 1>(t, s.pc, wave * (H / 4), acc);
             RS_MARK(step, l, 7);
-            int *red = s.red[wave];
-#pragma unroll
-            for (int q = 0; q < 8; q++) mf_store4(acc[q], red + q * 64);
-            if (lane < 32) {
+            ksplit_store<8>(acc, s.red);
+            if (tid < QROWS) {
                 int d[4];
-                mf_rowsum(red + (lane >> 2) * 64, lane & 3, d);
-                put(c.wp(par, l, R_QKV + rw + lane), __fmul_rn(qt_pc_dot(d[0], d[1], d[2], d[3], sA), rs));
+                ksplit_row(s.red, tid, d);
+                put(c.wp(par, l, R_QKV + row0 + tid), __fmul_rn(qt_pc_dot(d[0], d[1], d[2], d[3], sA), rs));
             }
             RS_MARK(step, l, 2);
             if (step > 0) clear_share(c, par ^ 1, l);
-            __syncthreads();   // the tile registers and the gains buffer are free
+            __syncthreads();   // the LDS of this layer is free
             if (l + 1 < c.L) load(l + 1);
             else if (!last) load(0);
             land();
@@ -503,12 +611,12 @@ __device__ __forceinline__ void role_q(const Ctx &c, LdsP &s, int grp, int qi) {
 __device__ __forceinline__ void role_o(const Ctx &c, LdsP &s, int oi) {
     const RArgs &a = c.a;
     const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int row0 = oi * OROWS, rw = row0 + wave * 32;
-    RTile<QD, 8> t;
+    const int row0 = oi * OROWS;
+    RTile16<QD, 8, QD / 4 / 64> t;
     float rs = 0.f;
     auto load = [&](int l) {
-        t.load(c.ly[l].w[1], rw, 8);
-        if (lane < 32) rs = ldg(uni(c.ly[l].s[1]) + rw + lane);
+        t.load(c.ly[l].w[1], row0, wave * (QD / 4), row0 + OROWS);
+        if (tid < OROWS) rs = ldg(uni(c.ly[l].s[1]) + row0 + tid);
     };
     THead th;
     load_gains<4, 8, H>(a.final_norm, s.hd.gain);
@@ -531,38 +639,29 @@ __device__ __forceinline__ void role_o(const Ctx &c, LdsP &s, int oi) {
                 }, v, a.err);
                 RS_MARK(step, l, 1);
             }
-            float m = 0.f;
-#pragma unroll
-            for (int k = 0; k < 2; k++)
-                m = fmaxf(m, fmaxf(fmaxf(fabsf(__uint_as_float(v[k].x)), fabsf(__uint_as_float(v[k].y))),
-                                   fmaxf(fabsf(__uint_as_float(v[k].z)), fabsf(__uint_as_float(v[k].w)))));
-            if (l > 0 && tid < OROWS / 4)
-                *reinterpret_cast<float4 *>(s.resid + 4 * tid) = make_float4(
-                    __uint_as_float(v[2].x), __uint_as_float(v[2].y), __uint_as_float(v[2].z), __uint_as_float(v[2].w));
+            float m = fmaxf(amax4(v[0]), amax4(v[1]));
+            if (l > 0 && tid < OROWS / 4) *reinterpret_cast<float4 *>(s.resid + 4 * tid) = f4(v[2]);
             if (l == 0 && tid < OROWS) s.resid[tid] = x0_elem(a, tok, row0 + tid);
             m = group_max<64>(m);
             if (lane == 0) s.wst[wave] = m;
             __syncthreads();
             const QtPcScale ps = qt_pc_scale(fmaxf(fmaxf(s.wst[0], s.wst[1]), fmaxf(s.wst[2], s.wst[3])));
             {
-                const float v8[8] = {__uint_as_float(v[0].x), __uint_as_float(v[0].y), __uint_as_float(v[0].z),
-                                     __uint_as_float(v[0].w), __uint_as_float(v[1].x), __uint_as_float(v[1].y),
-                                     __uint_as_float(v[1].z), __uint_as_float(v[1].w)};
-                pc_put8<true, QD>(s.pc, tid, v8, ps.isc);
+                const float4 p0 = f4(v[0]), p1 = f4(v[1]);
+                const float v8[8] = {p0.x, p0.y, p0.z, p0.w, p1.x, p1.y, p1.z, p1.w};
+                pcw_put8<QD>(s.pc, tid, v8, ps.isc);
             }
             __syncthreads();
             RS_MARK(step, l, 6);
             i32x4 acc[8];
-            rdot<QD, 8>(t, s.pc, 8, acc);
+            rdot16<QD, 8, QD / 4 / 64, 1>(t, s.pc, wave * (QD / 4), acc);
             RS_MARK(step, l, 7);
-            int *red = s.red[wave];
-#pragma unroll
-            for (int q = 0; q < 8; q++) mf_store4(acc[q], red + q * 64);
-            if (lane < 32) {
+            ksplit_store<8>(acc, s.red);
+            if (tid < OROWS) {
                 int d[4];
-                mf_rowsum(red + (lane >> 2) * 64, lane & 3, d);
-                const float vv = __fmul_rn(qt_pc_dot(d[0], d[1], d[2], d[3], ps.s), rs);
-                put(c.wp(par, l, R_XA + rw + lane), __fadd_rn(s.resid[wave * 32 + lane], vv));
+                ksplit_row(s.red, tid, d);
+                put(c.wp(par, l, R_XA + row0 + tid),
+                    __fadd_rn(s.resid[tid], __fmul_rn(qt_pc_dot(d[0], d[1], d[2], d[3], ps.s), rs)));
             }
             RS_MARK(step, l, 2);
             if (step > 0) clear_share(c, par ^ 1, l);
@@ -580,16 +679,22 @@ __device__ __forceinline__ void role_o(const Ctx &c, LdsP &s, int oi) {
 }
 
 // ---- GU: h = SwiGLU(W_gu . RMSNorm(xa)) ---------------------------------------------------
+// Rows 2i, 2i+1 of the interleaved matrix are the gate and up rows of h element i.
 __device__ __forceinline__ void role_gu(const Ctx &c, LdsP &s, int gi) {
     const RArgs &a = c.a;
-    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int rw = gi * GROWS + wave * 32;
-    RTile<H, 8> t;
+    const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int row0 = gi * GROWS;
+    RTile16<H, 8, H / 4 / 64> t;
     float rsg = 0.f, rsu = 0.f;
+    float gc[8], gu[8];
     auto load = [&](int l) {
-        t.load(c.ly[l].w[2], rw, 8);
-        if (lane < 16) { const float *S = uni(c.ly[l].s[2]); rsg = ldg(S + rw + 2 * lane); rsu = ldg(S + rw + 2 * lane + 1); }
-        load_gains<4, 16, H>(c.ly[l].post_norm, s.gain);
+        t.load(c.ly[l].w[2], row0, wave * (H / 4), row0 + GROWS);
+        if (tid < GROWS / 2) {
+            const float *S = uni(c.ly[l].s[2]);
+            rsg = ldg(S + row0 + 2 * tid);
+            rsu = ldg(S + row0 + 2 * tid + 1);
+        }
+        load_norm_gains(c.ly[l].post_norm, gc, gu);
     };
     THead th;
     load_gains<4, 8, H>(a.final_norm, s.hd.gain);
@@ -607,27 +712,21 @@ __device__ __forceinline__ void role_gu(const Ctx &c, LdsP &s, int gi) {
                 wait4<8, 32>(c.rr, H, [&](int i) { return base + (unsigned)i * 4u; }, v, a.err);
                 RS_MARK(step, l, 1);
 #pragma unroll
-                for (int k = 0; k < 8; k++) { xv[k] = __uint_as_float(v[k]); s.x[xpos<16, H>(tid + NT * k)] = xv[k]; }
+                for (int k = 0; k < 8; k++) xv[k] = __uint_as_float(v[k]);
             }
-            __syncthreads();
-            pc_stats<8, NT>(xv, H, s.gain, PosChunk<16, H>(), s.wst);
-            __syncthreads();
-            const float sD = stage_norm_pc<true, H, NT>(s.x, s.gain, a.eps, s.pc, s.wst);
+            const float sD = norm_pieces(xv, gc, gu, s.xs, s.wst, s.pc, a.eps);
             RS_MARK(step, l, 6);
             i32x4 acc[8];
-            rdot<H, 8>(t, s.pc, 8, acc);
+            rdot16<H, 8, H / 4 / 64, 1>(t, s.pc, wave * (H / 4), acc);
             RS_MARK(step, l, 7);
-            int *red = s.red[wave];
-#pragma unroll
-            for (int q = 0; q < 8; q++) mf_store4(acc[q], red + q * 64);
-            if (lane < 16) {
-                // h element p of the wave: gate row 2p, up row 2p + 1 (quad p/2, rows 2(p%2), +1)
+            ksplit_store<8>(acc, s.red);
+            if (tid < GROWS / 2) {
                 int dg[4], du[4];
-                mf_rowsum(red + (lane >> 1) * 64, 2 * (lane & 1), dg);
-                mf_rowsum(red + (lane >> 1) * 64, 2 * (lane & 1) + 1, du);
+                ksplit_row(s.red, 2 * tid, dg);
+                ksplit_row(s.red, 2 * tid + 1, du);
                 const float gt = __fmul_rn(qt_pc_dot(dg[0], dg[1], dg[2], dg[3], sD), rsg);
                 const float up = __fmul_rn(qt_pc_dot(du[0], du[1], du[2], du[3], sD), rsu);
-                put(c.wp(par, l, R_H + rw / 2 + lane), gt / (1.0f + expf(-gt)) * up);
+                put(c.wp(par, l, R_H + row0 / 2 + tid), gt / (1.0f + expf(-gt)) * up);
             }
             RS_MARK(step, l, 2);
             if (step > 0) clear_share(c, par ^ 1, l);
@@ -645,34 +744,33 @@ __device__ __forceinline__ void role_gu(const Ctx &c, LdsP &s, int gi) {
 }
 
 // ---- DN: x' = xa + W_dn . h ---------------------------------------------------------------
-// Row quads 0 and 1 of a wave's rows in registers, quad 2 (when the wave has one) in LDS,
-// copied there straight from memory.  Thread t holds h values 8u .. 8u+7 for u = t + 256k
-// and makes their pieces from registers (the values, scale and order of stage_pc).
+// The workgroup's 48 or 40 rows are three 16-row tiles (the third partly empty for 40);
+// wave w takes columns 1536w .. +1535 of all three (tiles 0, 1 in registers, tile 2 in
+// LDS, copied there straight from memory) and the four waves' exact partial sums are
+// added through LDS.  Thread t holds h values 8u .. 8u+7 for u = t + 256k and makes their
+// pieces from registers (the values, scale and order of stage_pc).
 __device__ __forceinline__ void role_dn(const Ctx &c, LdsD &s, int di) {
     const RArgs &a = c.a;
     const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int m16 = lane & 15, kg = lane >> 4;
-    // 16 workgroups of 48 rows (12 per wave), 32 of 40 (12, 12, 8, 8)
-    const bool big = di < 16;
+    const bool big = di < 16;                  // 16 workgroups of 48 rows, 32 of 40
     const int row0 = big ? 48 * di : 768 + 40 * (di - 16);
     const int nrows = big ? 48 : 40;
-    const int woff = wave < 3 ? 12 * wave : (big ? 36 : 32);
-    const int nq = (big || wave < 2) ? 3 : 2;
-    const int rw = row0 + woff;
-    constexpr int S = F / 256;
-    RTile<F, 2> t;
+    constexpr int KW = F / 4, S = KW / 64;     // columns and 64-column steps per wave
+    const int c0 = wave * KW;
+    RTile16<F, 2, S> t;
     float rs = 0.f;
     auto load = [&](int l) {
-        t.load(c.ly[l].w[3], rw, 2);
-        if (nq > 2) {
+        t.load(c.ly[l].w[3], row0, c0, row0 + nrows);
+        if (row0 + 32 + m16 < row0 + nrows) {
             const __amdgpu_buffer_rsrc_t r = brsrc(uni(c.ly[l].w[3]));
-            const unsigned voff = (unsigned)((m16 & 3) * F + (m16 >> 2) * 64 + kg * 16);
+            const unsigned voff = (unsigned)(m16 * F + 16 * kg);
 #pragma unroll
             for (int st = 0; st < S; st++)
                 __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void *)&s.tw[wave][st][0], 16,
-                                                         voff, __builtin_amdgcn_readfirstlane((rw + 8) * F + st * 256), 0, 0);
+                                                         voff, __builtin_amdgcn_readfirstlane((row0 + 32) * F + c0 + 64 * st), 0, 0);
         }
-        if (lane < 4 * nq) rs = ldg(uni(c.ly[l].s[3]) + rw + lane);
+        if (tid < nrows) rs = ldg(uni(c.ly[l].s[3]) + row0 + tid);
     };
     THead th;
     load_gains<4, 8, H>(a.final_norm, s.hd.gain);
@@ -696,55 +794,59 @@ __device__ __forceinline__ void role_dn(const Ctx &c, LdsD &s, int di) {
             }
             float m = 0.f;
 #pragma unroll
-            for (int k = 0; k < 6; k++)
-                m = fmaxf(m, fmaxf(fmaxf(fabsf(__uint_as_float(v[k].x)), fabsf(__uint_as_float(v[k].y))),
-                                   fmaxf(fabsf(__uint_as_float(v[k].z)), fabsf(__uint_as_float(v[k].w)))));
-            if (tid < nrows / 4)
-                *reinterpret_cast<float4 *>(s.resid + 4 * tid) = make_float4(
-                    __uint_as_float(v[6].x), __uint_as_float(v[6].y), __uint_as_float(v[6].z), __uint_as_float(v[6].w));
+            for (int k = 0; k < 6; k++) m = fmaxf(m, amax4(v[k]));
+            if (tid < nrows / 4) *reinterpret_cast<float4 *>(s.resid + 4 * tid) = f4(v[6]);
             m = group_max<64>(m);
             if (lane == 0) s.wst[wave] = m;
             __syncthreads();
             const QtPcScale ps = qt_pc_scale(fmaxf(fmaxf(s.wst[0], s.wst[1]), fmaxf(s.wst[2], s.wst[3])));
 #pragma unroll
             for (int k = 0; k < 3; k++) {
-                const float v8[8] = {__uint_as_float(v[2 * k].x), __uint_as_float(v[2 * k].y), __uint_as_float(v[2 * k].z),
-                                     __uint_as_float(v[2 * k].w), __uint_as_float(v[2 * k + 1].x), __uint_as_float(v[2 * k + 1].y),
-                                     __uint_as_float(v[2 * k + 1].z), __uint_as_float(v[2 * k + 1].w)};
-                pc_put8<true, F>(s.pc, tid + NT * k, v8, ps.isc);
+                const float4 p0 = f4(v[2 * k]), p1 = f4(v[2 * k + 1]);
+                const float v8[8] = {p0.x, p0.y, p0.z, p0.w, p1.x, p1.y, p1.z, p1.w};
+                pcw_put8<F>(s.pc, tid + NT * k, v8, ps.isc);
             }
             __syncthreads();
             RS_MARK(step, l, 6);
-            // quads 0, 1 from registers, quad 2 from LDS; two accumulator chains each
-            i32x4 acc[3][2];
-#pragma unroll
-            for (int q = 0; q < 3; q++) acc[q][0] = acc[q][1] = i32x4{0, 0, 0, 0};
+            i32x4 acc[3];
             {
-                uint4 b = mf_b4<F>(s.pc, 0);
-                uint4 w2 = nq > 2 ? s.tw[wave][0][lane] : make_uint4(0, 0, 0, 0);
+                i32x4 ac[3][2];
+#pragma unroll
+                for (int q = 0; q < 3; q++) ac[q][0] = ac[q][1] = i32x4{0, 0, 0, 0};
+                uint4 b = pcw_b<F>(s.pc, c0);
+                uint4 w2 = s.tw[wave][0][lane];
 #pragma unroll
                 for (int st = 0; st < S; st++) {
-                    const uint4 bn = mf_b4<F>(s.pc, st + 1 < S ? st + 1 : st);
-                    const uint4 w2n = nq > 2 ? s.tw[wave][st + 1 < S ? st + 1 : st][lane] : make_uint4(0, 0, 0, 0);
-                    acc[0][st & 1] = mfma_i8(t.w[0][st], b, acc[0][st & 1]);
-                    acc[1][st & 1] = mfma_i8(t.w[1][st], b, acc[1][st & 1]);
-                    if (nq > 2) acc[2][st & 1] = mfma_i8(w2, b, acc[2][st & 1]);
+                    const int sn = st + 1 < S ? st + 1 : st;
+                    const uint4 bn = pcw_b<F>(s.pc, c0 + 64 * sn);
+                    const uint4 w2n = s.tw[wave][sn][lane];
+                    ac[0][st & 1] = mfma_i8(t.w[0][st], b, ac[0][st & 1]);
+                    ac[1][st & 1] = mfma_i8(t.w[1][st], b, ac[1][st & 1]);
+                    ac[2][st & 1] = mfma_i8(w2, b, ac[2][st & 1]);
                     b = bn;
                     w2 = w2n;
                 }
+#pragma unroll
+                for (int q = 0; q < 3; q++) acc[q] = ac[q][0] + ac[q][1];
             }
             RS_MARK(step, l, 7);
-            int *red = s.red[wave];
+            // partial plane sums of this wave: red[wave][tile][row][plane]
+            if (m16 < 4) {
 #pragma unroll
-            for (int q = 0; q < 3; q++)
-                if (q < nq) mf_store4(acc[q][0] + acc[q][1], red + q * 64);
-            if (lane < 4 * nq) {
+                for (int q = 0; q < 3; q++)
+#pragma unroll
+                    for (int i = 0; i < 4; i++) s.red[wave][q][4 * kg + i][m16] = acc[q][i];
+            }
+            __syncthreads();
+            if (tid < nrows) {
+                const int q = tid >> 4, rr = tid & 15;
                 int d[4];
-                mf_rowsum(red + (lane >> 2) * 64, lane & 3, d);
+#pragma unroll
+                for (int n = 0; n < 4; n++) d[n] = s.red[0][q][rr][n] + s.red[1][q][rr][n] + s.red[2][q][rr][n] + s.red[3][q][rr][n];
                 const float vv = __fmul_rn(qt_pc_dot(d[0], d[1], d[2], d[3], ps.s), rs);
-                const float xo = __fadd_rn(s.resid[woff + lane], vv);
-                put(c.wp(par, l, R_X + rw + lane), xo);
-                if (a.layer_out && last) a.layer_out[(size_t)l * H + rw + lane] = xo;
+                const float xo = __fadd_rn(s.resid[tid], vv);
+                put(c.wp(par, l, R_X + row0 + tid), xo);
+                if (a.layer_out && last) a.layer_out[(size_t)l * H + row0 + tid] = xo;
             }
             RS_MARK(step, l, 2);
             if (step > 0) clear_share(c, par ^ 1, l);
@@ -759,6 +861,86 @@ __device__ __forceinline__ void role_dn(const Ctx &c, LdsD &s, int di) {
         load(0);
         land();
     }
+}
+
+// ---- attention chunk (one pass) -----------------------------------------------------------
+// NBK 128-key blocks: K rows in kf (wave w holds k-tile w of each block), V rows in LDS.
+// Scores and the per-k-tile softmax are qt_att_tiles' (the key rows from registers); the
+// P.V of each k-tile is qt_att_pv1's, folded by qt_att_fold.  k-tiles past the chunk's
+// keys are computed and not folded.
+template <int NBK>
+__device__ __forceinline__ void att_chunk(LdsA &s, const uint4 (&kf)[ABLK][8], int n, float scale2, QtAttRun &run, int st_, int l_) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, kg = lane >> 4, key = lane & 15, hh = lane >> 4;
+    qt_u32x4 qa[4];
+#pragma unroll
+    for (int s2 = 0; s2 < 4; s2++) qa[s2] = qt_lds16(&s.qp[key][32 * s2 + 8 * kg]);
+    float sv[NBK][2];
+#pragma unroll
+    for (int b = 0; b < NBK; b++)
+#pragma unroll
+        for (int t2 = 0; t2 < 2; t2++) {
+            qt_f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int s2 = 0; s2 < 4; s2++) {
+                const uint4 kk = kf[b][t2 * 4 + s2];
+                acc = qt_mfma_bf16(qa[s2], qt_u32x4{kk.x, kk.y, kk.z, kk.w}, acc);
+            }
+            sv[b][t2] = (acc[0] + acc[1]) + acc[2];
+        }
+    RS_MARK(st_, l_, 8);
+#pragma unroll
+    for (int b = 0; b < NBK; b++) {
+        const int nk = min(KVB, n - KVB * b);
+        const int r00 = 32 * wave, r01 = 32 * wave + 16;
+        const float sa = r00 + key < nk ? sv[b][0] * scale2 : -INFINITY;
+        const float sb = r01 + key < nk ? sv[b][1] * scale2 : -INFINITY;
+        const float m = group_max<16>(fmaxf(sa, sb));
+        const float pa = qt_exp2(sa - m), pb = qt_exp2(sb - m);
+        const float ls = group_sum<16>(pa + pb);
+        if (hh < HPK) {
+            uint16_t *pp = &s.pp[0][0] + KVB * b;
+            qt_put_pieces(pp + 4 * hh * (ABLK * KVB) + r00 + key, ABLK * KVB, pa);
+            qt_put_pieces(pp + 4 * hh * (ABLK * KVB) + r01 + key, ABLK * KVB, pb);
+            if (key == 0) { s.ml[4 * b + wave][hh][0] = m; s.ml[4 * b + wave][hh][1] = ls; }
+        }
+    }
+    RS_MARK(st_, l_, 9);
+    __syncthreads();
+    RS_MARK(st_, l_, 10);
+    const int hc = hh < HPK ? hh : HPK - 1, j = lane & 15, d0 = 32 * wave;
+    float mt[NBK * 4], lt[NBK * 4], ot[NBK * 4][2];
+    // P.V in groups of (up to) two blocks: every LDS read of a group is issued before its
+    // MFMAs
+    constexpr int GB = NBK < 2 ? NBK : 2;
+#pragma unroll
+    for (int g0 = 0; g0 < NBK; g0 += GB) {
+        qt_u32x4 pa[GB * 4], vv[GB * 4][2];
+#pragma unroll
+        for (int u = 0; u < GB * 4; u++) {
+            const int t = 4 * g0 + u;
+            if (t >= NBK * 4) break;
+            const uint16_t *vt = &s.v[t >> 2][32 * (t & 3) * HD];
+            pa[u] = qt_lds16(&s.pp[0][0] + (lane & 15) * (ABLK * KVB) + 32 * t + 8 * kg);
+#pragma unroll
+            for (int dt = 0; dt < 2; dt++)
+                vv[u][dt] = qt_lds_tr8x2(vt + qt_vidx(8 * kg + j / 4, d0 + 16 * dt + 4 * (j & 3)),
+                                         vt + qt_vidx(8 * kg + 4 + j / 4, d0 + 16 * dt + 4 * (j & 3)));
+            mt[t] = s.ml[t][hc][0];
+            lt[t] = s.ml[t][hc][1];
+        }
+#pragma unroll
+        for (int u = 0; u < GB * 4; u++) {
+            const int t = 4 * g0 + u;
+            if (t >= NBK * 4) break;
+#pragma unroll
+            for (int dt = 0; dt < 2; dt++) {
+                const qt_f32x4 acc = qt_mfma_bf16(pa[u], vv[u][dt], qt_f32x4{0.f, 0.f, 0.f, 0.f});
+                ot[t][dt] = (acc[0] + acc[1]) + acc[2];
+            }
+        }
+    }
+    RS_MARK(st_, l_, 11);
+    qt_att_fold<NBK * 4>((n + 31) >> 5, ot, mt, lt, run.o, run.m, run.l);
 }
 
 // ---- ATT + MRG -----------------------------------------------------------------------------
@@ -799,8 +981,7 @@ __device__ __forceinline__ void role_att(const Ctx &c, LdsA &s, int g, int ch) {
         rc = ldg(a.rope_cos + (size_t)ge.pos * 64 + lane); rsn = ldg(a.rope_sin + (size_t)ge.pos * 64 + lane);
     };
     qt_att_zero_rows<HPK>(&s.qp[0][0], HD, tid, NT);
-    qt_att_zero_rows<HPK>(&s.pp[0][0][0], KVB, tid, NT);
-    qt_att_zero_rows<HPK>(&s.pp[1][0][0], KVB, tid, NT);
+    qt_att_zero_rows<HPK>(&s.pp[0][0], ABLK * KVB, tid, NT);
     prefetch(0, Geo(c.pos0));
     land();
     const float scale2 = a.scale * QT_LOG2E;
@@ -874,49 +1055,14 @@ __device__ __forceinline__ void role_att(const Ctx &c, LdsA &s, int g, int ch) {
                     }
                 }
                 RS_MARK(step, l, 6);
+                // one pass over the chunk (qt_att_fold), specialised on its block count so
+                // that it is straight-line code: every wave scores its k-tile of every block,
+                // one barrier, then P.V of its 32 dims over all k-tiles
                 QtAttRun run;
-                qt_att_run_init(run);
-#pragma unroll
-                for (int b = 0; b < ABLK; b++) {
-                    if (b >= nblk) break;
-                    const int nk = min(KVB, n - KVB * b);
-                    uint16_t *pp = &s.pp[b & 1][0][0];
-                    float *ml = &s.ml[b & 1][0][0][0];
-                    if (32 * wave < nk) {
-                        // scores of k-tile `wave` (two 16-key score tiles) against the query
-                        // pieces: qt_att_tiles with the key rows from registers
-                        qt_u32x4 qa[4];
-#pragma unroll
-                        for (int s2 = 0; s2 < 4; s2++) qa[s2] = qt_lds16(&s.qp[key][32 * s2 + 8 * kg]);
-                        float sv[2];
-#pragma unroll
-                        for (int t2 = 0; t2 < 2; t2++) {
-                            qt_f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-                            for (int s2 = 0; s2 < 4; s2++) {
-                                const uint4 kk = kf[b][t2 * 4 + s2];
-                                acc = qt_mfma_bf16(qa[s2], qt_u32x4{kk.x, kk.y, kk.z, kk.w}, acc);
-                            }
-                            sv[t2] = (acc[0] + acc[1]) + acc[2];
-                        }
-                        const int hh = lane >> 4;
-                        const int r00 = 32 * wave, r01 = 32 * wave + 16;
-                        const float sa = r00 + key < nk ? sv[0] * scale2 : -INFINITY;
-                        const float sb = r01 + key < nk ? sv[1] * scale2 : -INFINITY;
-                        const float m = group_max<16>(fmaxf(sa, sb));
-                        const float pa = qt_exp2(sa - m), pb = qt_exp2(sb - m);
-                        const float ls = group_sum<16>(pa + pb);
-                        if (hh < HPK) {
-                            qt_put_pieces(pp + 4 * hh * KVB + r00 + key, KVB, pa);
-                            qt_put_pieces(pp + 4 * hh * KVB + r01 + key, KVB, pb);
-                            if (key == 0) { ml[(wave * HPK + hh) * 2] = m; ml[(wave * HPK + hh) * 2 + 1] = ls; }
-                        }
-                    }
-                    __syncthreads();
-                    float o[2], M, lsum;
-                    qt_att_pv_n<HPK>((nk + 31) >> 5, pp, KVB, ml, s.v[b], 32 * wave, lane, o, M, lsum);
-                    qt_att_run_add(run, o, M, lsum);
-                }
+                if (nblk == 1) att_chunk<1>(s, kf, n, scale2, run, step, l);
+                else if (nblk == 2) att_chunk<2>(s, kf, n, scale2, run, step, l);
+                else if (nblk == 3) att_chunk<3>(s, kf, n, scale2, run, step, l);
+                else att_chunk<4>(s, kf, n, scale2, run, step, l);
                 RS_MARK(step, l, 7);
                 // partial of this chunk: o (head lane/16, dims 32 wave + lane%16 and +16), m, l
                 const int hq = lane >> 4;
@@ -990,8 +1136,11 @@ __device__ __forceinline__ void role_att(const Ctx &c, LdsA &s, int g, int ch) {
                 RS_MARK(step, l, 5);
             }
             __syncthreads();   // the chunk's LDS (values, staging) is free for the next copy
+            // (returning here, not falling out of the loops, shows the compiler that the key
+            // registers are always reloaded before the next use)
+            if (last && l + 1 == c.L) return;
             if (l + 1 < c.L) prefetch(l + 1, ge);
-            else if (!last) prefetch(0, Geo(pos + 1));
+            else prefetch(0, Geo(pos + 1));
             land();
             RS_MARK(step, l, 3);
         }

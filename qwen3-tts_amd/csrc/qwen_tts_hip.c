@@ -153,6 +153,7 @@ static hipError_t kv_xfer(uint16_t *dev_heads, int kv_max, uint16_t *host_rows, 
 typedef struct {
     int H, F, nh, nkv, hd, L, kv_max, qd, kvd, prec, rope_len, attn_G;
     int step_G;                /* key chunks per kv head of the single-stream step's attention */
+    int step_onepass;          /* ...and each chunk as one softmax (qt_launch_attn_onepass) */
     float eps;
     dmat_t *qkv, *o, *gu, *dn;
     float **in_norm, **post_norm, **qn, **kn;
@@ -260,7 +261,8 @@ static hipError_t stack_body_ex(stack_t *s, float *x, const int *d_pos, hipStrea
     for (int l = 0; l < s->L; l++) {
         const size_t lay = (size_t)l * s->nkv * s->kv_max * s->hd;
         if ((e = mv(&s->qkv[l], QT_EPI_STORE, 1, x, s->in_norm[l], s->eps, s->qkvbuf, NULL, NULL, st))) return e;
-        if ((e = qt_launch_attn(1, s->qkvbuf, s->qn[l], s->kn[l], s->rope_cos, s->rope_sin, s->eps, d_pos, 0,
+        if ((e = (s->step_onepass ? qt_launch_attn_onepass : qt_launch_attn)(
+                     1, s->qkvbuf, s->qn[l], s->kn[l], s->rope_cos, s->rope_sin, s->eps, d_pos, 0,
                                 s->kc + lay, s->vc + lay, s->hd, (long long)s->kv_max * s->hd, s->nh, s->nkv,
                                 s->hd, scale, s->part, s->cnt, s->step_G, s->attn, st))) return e;
         if ((e = mv(&s->o[l], QT_EPI_RESID, 0, s->attn, NULL, s->eps, NULL, x, NULL, st))) return e;
@@ -379,6 +381,7 @@ static int ps_setup(talker_t *t) {
         HCK(hipMemsetAsync(t->rs_reg, 0xFF, rw * sizeof(unsigned), t->st));
         HCK(hipMemsetAsync(t->rs_slots, 0, sw * sizeof(unsigned long long), t->st));
         s->step_G = qt_rstep_chunks();
+        s->step_onepass = 1;
         t->rs_on = 1;
     }
     HCK(hipMalloc((void **)&t->ps_ring, (t->rs_on ? 1 : words) * sizeof(unsigned long long)));
@@ -1070,7 +1073,8 @@ int qwen_hip_talker_launch_kernel(void *state, int kernel, int layer, int n) {
     for (int i = 0; i < n; i++) {
         switch (kernel) {
         case 0: HCK(mv(&s->qkv[layer], QT_EPI_STORE, 1, x, s->in_norm[layer], s->eps, s->qkvbuf, NULL, NULL, t->st)); break;
-        case 1: HCK(qt_launch_attn(1, s->qkvbuf, s->qn[layer], s->kn[layer], s->rope_cos, s->rope_sin, s->eps, t->d_pos, 0,
+        case 1: HCK((s->step_onepass ? qt_launch_attn_onepass : qt_launch_attn)(
+                        1, s->qkvbuf, s->qn[layer], s->kn[layer], s->rope_cos, s->rope_sin, s->eps, t->d_pos, 0,
                                    s->kc + lay, s->vc + lay, s->hd, (long long)s->kv_max * s->hd, s->nh, s->nkv,
                                    s->hd, 1.0f / sqrtf((float)s->hd), s->part, s->cnt, s->step_G, s->attn, t->st)); break;
         case 2: HCK(mv(&s->o[layer], QT_EPI_STORE, 0, s->attn, NULL, s->eps, s->hbuf, NULL, NULL, t->st)); break;
