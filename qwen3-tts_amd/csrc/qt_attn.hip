@@ -45,8 +45,8 @@ struct QtAttnArgs {
     // partials and counters; d_pos + z is its position (batched step)
     long long q_bs, kv_bs, out_bs, part_bs;
     int min_chunk;           // chunks hold at least this many keys (0: ceil(L/G) rounded to 16)
-    int onepass;             // !BATCH, chunks <= 512 keys: one softmax over the chunk (qt_att_fold)
-                             // instead of a running state across its 128-key blocks
+    int onepass;             // !BATCH, chunks <= 512 keys: one softmax over the chunk under its
+                             // maximum (qt_attn_mf.h) instead of a running state across blocks
 };
 
 #define QT_KVB 128   // keys of a chunk staged in LDS at once
@@ -68,8 +68,9 @@ __device__ __forceinline__ void qt_lds_copy16(const void *src, void *dst) {
 // no workgroup barrier in the key loop, and the four wave states are merged at the end;
 // !BATCH keeps the arithmetic order of the fused step's attention phase, which it must
 // match bit for bit (waves share each 128-key block: scores, barrier, P.V per 32 dims).
-template <int HPK, bool PREP, bool BATCH>
+template <int HPK, bool PREP, bool BATCH, bool ONEPASS>
 __global__ __launch_bounds__(QT_WG) void k_attn(QtAttnArgs a) {
+    static_assert(!(BATCH && ONEPASS), "one-pass chunks are single-stream");
     const int z = BATCH ? blockIdx.y : blockIdx.z;
     if (z) {
         a.q += z * a.q_bs; a.K += z * a.kv_bs; a.V += z * a.kv_bs; a.out += z * a.out_bs;
@@ -95,7 +96,9 @@ __global__ __launch_bounds__(QT_WG) void k_attn(QtAttnArgs a) {
     constexpr int KVBYTES = 2 * KVB * QT_HD * 2, MBYTES = QT_ATT_G * HPK * PS * 4;
     static_assert(KVB % 32 == 0 && KVB <= QT_WAVES * 32, "each wave scores at most one 32-key tile of a block");
     __shared__ __align__(16) uint16_t qp[16][QT_HD];            // query pieces, row 4h+p (qt_attn_mf.h)
-    __shared__ __align__(16) uint16_t pp[16][KVB];           // probability pieces of a block (k-tile w: wave w)
+    // probability pieces of a block (k-tile w: wave w); ONEPASS: of the whole chunk
+    constexpr int PPC = ONEPASS ? 4 * KVB : KVB;
+    __shared__ __align__(16) uint16_t pp[16][PPC];
     __shared__ float ml[QT_WAVES][HPK][2];                      // per-k-tile (max, exp-sum)
     __shared__ __align__(16) uint16_t knew[QT_HD];
     __shared__ __align__(16) uint16_t vnew[QT_HD];
@@ -188,7 +191,7 @@ __global__ __launch_bounds__(QT_WG) void k_attn(QtAttnArgs a) {
             qt_put_pieces(&qp[4 * (i / QT_HD)][i % QT_HD], QT_HD, a.q[(g * HPK + i / QT_HD) * QT_HD + i % QT_HD]);
     }
     qt_att_zero_rows<HPK>(&qp[0][0], QT_HD, tid, QT_WG);
-    qt_att_zero_rows<HPK>(&pp[0][0], KVB, tid, QT_WG);
+    qt_att_zero_rows<HPK>(&pp[0][0], PPC, tid, QT_WG);
     if (!BATCH) qt_att_zero_vrows(s_kv[1], min(KVB, n), (min(KVB, n) + 31) & ~31, tid, QT_WG);
     if (!BATCH) __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();   // (also, !BATCH: every wave's LDS copies of the first block have landed)
@@ -249,42 +252,77 @@ __global__ __launch_bounds__(QT_WG) void k_attn(QtAttnArgs a) {
             const float o2[2] = {src[2 + 2 * wave], src[3 + 2 * wave]};
             if (src[0] != -INFINITY) qt_att_run_add(run, o2, src[0], src[1]);
         }
-    } else if (a.onepass) {
-        // ---- 2c. one pass: the blocks are staged and scored in turn, each k-tile's P.V is
-        // kept apart (qt_att_pv1) and all are folded once with the chunk maximum, the
-        // arithmetic of the fused role-specialised step (qt_rstep.hip) ----
-        constexpr int NT1 = 16;                   // k-tiles of 32 keys (chunks <= 512 keys)
-        float ot[NT1][2], mt[NT1], lt[NT1];
+    } else if constexpr (ONEPASS) {
+        // ---- 2c. one pass under the chunk maximum (qt_attn_mf.h), the arithmetic of the
+        // fused role-specialised step (qt_rstep.hip): the K blocks staged in turn and
+        // scored into registers, the chunk maximum, the probabilities, then the V blocks in
+        // turn for P.V (block 0's values were staged with its keys) ----
+        constexpr int NB1 = 4;                    // 128-key blocks (chunks <= 512 keys)
+        const int nblk = (n + KVB - 1) / KVB;
         const int hc = pg < HPK ? pg : HPK - 1;
+        float sv[NB1][2];
+        float wm = -INFINITY;
 #pragma unroll
-        for (int b = 0; b < NT1 / 4; b++) {
-            const int kb = KVB * b;
-            if (kb >= n) break;
-            const int nk = min(KVB, n - kb);
-            if (kb > 0) {
-                __syncthreads();
-                stage(kb, true, true);
+        for (int b = 0; b < NB1; b++) {
+            sv[b][0] = sv[b][1] = -INFINITY;
+            if (b >= nblk) continue;
+            const int kb = KVB * b, nk = min(KVB, n - kb);
+            if (b > 0) {
+                __syncthreads();                  // every wave is done with the previous keys
+                stage(kb, true, false);
                 __builtin_amdgcn_s_waitcnt(0);
                 const int nrow = pos - j0 - kb;
-                if (PREP && wave == 0 && nrow >= 0 && nrow < nk) qt_att_put_kv(s_kv[0], s_kv[1], nrow, knew, vnew, lane);
+                if (PREP && wave == 0 && nrow >= 0 && nrow < nk && lane < 16)
+                    *reinterpret_cast<uint4 *>(&s_kv[0][nrow * QT_HD + qt_kslot(nrow, lane) * 8]) =
+                        *reinterpret_cast<const uint4 *>(knew + 8 * lane);
+                __syncthreads();
+            }
+            if (kb + 32 * wave < n) {
+                const int rr[2] = {32 * wave, 32 * wave + 16};
+                float sc[2];
+                qt_att_qk2(&qp[0][0], s_kv[0], rr, lane, sc);
+                sv[b][0] = rr[0] + sub < nk ? sc[0] * scale2 : -INFINITY;
+                sv[b][1] = rr[1] + sub < nk ? sc[1] * scale2 : -INFINITY;
+                wm = fmaxf(wm, group_max<16>(fmaxf(sv[b][0], sv[b][1])));
+            }
+        }
+        if (pg < HPK && sub == 0) ml[wave][pg][0] = wm;
+        __syncthreads();
+        const float M = fmaxf(fmaxf(ml[0][hc][0], ml[1][hc][0]), fmaxf(ml[2][hc][0], ml[3][hc][0]));
+        float lw = 0.f;
+#pragma unroll
+        for (int b = 0; b < NB1; b++)
+            if (b < nblk && KVB * b + 32 * wave < n)
+                lw += qt_cm_probs<HPK>(sv[b][0], sv[b][1], M, &pp[0][0], PPC, KVB * b + 32 * wave, lane);
+        if (pg < HPK && sub == 0) ml[wave][pg][1] = lw;
+        __syncthreads();
+        const int nt = (n + 31) >> 5;
+        qt_f32x4 acc[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
+        for (int b = 0; b < nblk; b++) {
+            const int kb = KVB * b, nk = min(KVB, n - kb);
+            if (b > 0) {
+                __syncthreads();                  // every wave is done with the previous values
+                stage(kb, false, true);
+                __builtin_amdgcn_s_waitcnt(0);
+                const int nrow = pos - j0 - kb;
+                if (PREP && wave == 0 && nrow >= 0 && nrow < nk && lane < 16)
+                    *reinterpret_cast<uint4 *>(&s_kv[1][nrow * QT_HD + qt_vslot(nrow, lane) * 8]) =
+                        *reinterpret_cast<const uint4 *>(vnew + 8 * lane);
                 qt_att_zero_vrows(s_kv[1], nk, (nk + 31) & ~31, tid, QT_WG);
                 __syncthreads();
             }
-            if (32 * wave < nk)
-                qt_att_tiles<HPK>(&qp[0][0], s_kv[0], &pp[0][0], KVB, &ml[0][0][0], wave, nk, scale2, lane);
-            __syncthreads();
-            {
-                float o4[4][2];
-                qt_att_pv4(&pp[0][0], KVB, 0, s_kv[1], 32 * wave, lane, o4);
 #pragma unroll
-                for (int t = 0; t < 4; t++) {
-                    ot[4 * b + t][0] = o4[t][0]; ot[4 * b + t][1] = o4[t][1];
-                    mt[4 * b + t] = ml[t][hc][0];
-                    lt[4 * b + t] = ml[t][hc][1];
-                }
+            for (int t = 0; t < 4; t++) {
+                if (4 * b + t >= nt) break;
+                qt_u32x4 pa, vv[2];
+                qt_cm_operands(&pp[0][0], PPC, kb + 32 * t, s_kv[1] + 32 * t * QT_HD, 32 * wave, lane, pa, vv);
+                qt_cm_mfma(pa, vv, acc);
             }
         }
-        qt_att_fold<NT1>((n + 31) >> 5, ot, mt, lt, run.o, run.m, run.l);
+#pragma unroll
+        for (int dt = 0; dt < 2; dt++) run.o[dt] = (acc[dt][0] + acc[dt][1]) + acc[dt][2];
+        run.m = M;
+        run.l = ((ml[0][hc][1] + ml[1][hc][1]) + ml[2][hc][1]) + ml[3][hc][1];
     } else
     for (int kb = 0; kb < n; kb += KVB) {
         const int nk = min(KVB, n - kb);
@@ -388,9 +426,11 @@ static hipError_t attn_launch(const QtAttnArgs &a, int prep, int head_dim, int G
     const bool batch = a.min_chunk > 0;
     const dim3 grid = batch ? dim3(a.n_kv, nz, G) : dim3(G, a.n_kv, nz);
 #define QT_ATT_CASE(H) \
-    if (batch && prep) hipLaunchKernelGGL((k_attn<H, true, true>), grid, dim3(QT_WG), 0, st, a); \
-    else if (prep) hipLaunchKernelGGL((k_attn<H, true, false>), grid, dim3(QT_WG), 0, st, a); \
-    else hipLaunchKernelGGL((k_attn<H, false, false>), grid, dim3(QT_WG), 0, st, a);
+    if (batch && prep) hipLaunchKernelGGL((k_attn<H, true, true, false>), grid, dim3(QT_WG), 0, st, a); \
+    else if (a.onepass && prep) hipLaunchKernelGGL((k_attn<H, true, false, true>), grid, dim3(QT_WG), 0, st, a); \
+    else if (a.onepass) hipLaunchKernelGGL((k_attn<H, false, false, true>), grid, dim3(QT_WG), 0, st, a); \
+    else if (prep) hipLaunchKernelGGL((k_attn<H, true, false, false>), grid, dim3(QT_WG), 0, st, a); \
+    else hipLaunchKernelGGL((k_attn<H, false, false, false>), grid, dim3(QT_WG), 0, st, a);
     if (hpk == 1) { QT_ATT_CASE(1) }
     else if (hpk == 2) { QT_ATT_CASE(2) }
     else if (hpk == 4) { QT_ATT_CASE(4) }

@@ -226,68 +226,44 @@ __device__ __forceinline__ void qt_att_run_add(QtAttRun &r, const float (&o)[2],
     r.m = mn;
 }
 
-// ---- one-pass chunks: every k-tile's P.V kept apart, folded once with the chunk maximum ----
-// The per-k-tile quantities (scores, p = 2^(s - m_t) as pieces, m_t, l_t) are those of
-// qt_att_tiles; qt_att_pv1 gives one k-tile's P.V (the three piece sums added as in
-// qt_att_pv), and qt_att_fold combines k-tiles 0..n-1 in order exactly as qt_att_pv does
-// within one block: M = max m_t, l = sum l_t 2^(m_t - M), o = sum o_t 2^(m_t - M).  A chunk
-// of up to 512 keys is thus one softmax over all its keys, with no per-block running
-// state; for one block it equals qt_att_pv.
-__device__ __forceinline__ void qt_att_pv1(const uint16_t *pp, int pstride, int pcol, const uint16_t *vtile, int d0, int lane,
-                                           float (&o)[2]) {
+// ---- one-pass chunks under the chunk maximum ------------------------------------------
+// A chunk of up to 512 keys (k-tiles t = 0 .. ceil(n/32) - 1 of 32 keys; k-tile t =
+// 4b + w belongs to wave w, block b) is one softmax with no running state:
+//   1. every wave scores its k-tiles (two 16-key score tiles each, s' = s * scale * log2 e,
+//      keys >= n at -inf) and takes its maximum per head, m_w;
+//   2. M = max_w m_w (one workgroup barrier; a maximum is exact in any order);
+//   3. p = 2^(s' - M) as pieces into the chunk's probability columns, l_w = sum over the
+//      wave's k-tiles in block order of group_sum<16>(p_a + p_b);
+//   4. (barrier) P.V: dims d0 .. d0 + 31 of every head, one accumulator per 16 dims,
+//      chained over the k-tiles in order t = 0, 1, ..; o = (D0 + D1) + D2 (the pieces);
+//      l = ((l_0 + l_1) + l_2) + l_3.
+// Every float operation and its order is fixed by this list, so the per-kernel attention
+// and the fused step, which stage keys differently, give the same bits.
+//
+// Step 3 for one k-tile of this wave: the pieces of p into rows 4h+p, columns col ..
+// col + 31 of pp (row stride pstride), and the k-tile's sum of p per head.
+template <int HPK>
+__device__ __forceinline__ float qt_cm_probs(float sa, float sb, float M, uint16_t *pp, int pstride, int col, int lane) {
+    const int h = lane >> 4, key = lane & 15;
+    const float pa = qt_exp2(sa - M), pb = qt_exp2(sb - M);     // 2^-inf == 0
+    if (h < HPK) {
+        qt_put_pieces(pp + 4 * h * pstride + col + key, pstride, pa);
+        qt_put_pieces(pp + 4 * h * pstride + col + 16 + key, pstride, pb);
+    }
+    return group_sum<16>(pa + pb);
+}
+// Step 4's operands for one k-tile: probability pieces of columns col .. col + 31 and the
+// transposed value rows of the k-tile starting at vtile, dims d0 .. d0 + 31.
+__device__ __forceinline__ void qt_cm_operands(const uint16_t *pp, int pstride, int col, const uint16_t *vtile, int d0,
+                                               int lane, qt_u32x4 &pa, qt_u32x4 (&vv)[2]) {
     const int kg = lane >> 4, j = lane & 15;
-    const qt_u32x4 pa = qt_lds16(pp + (lane & 15) * pstride + pcol + 8 * kg);
-    qt_u32x4 vv[2];
+    pa = qt_lds16(pp + (lane & 15) * pstride + col + 8 * kg);
 #pragma unroll
     for (int dt = 0; dt < 2; dt++)
         vv[dt] = qt_lds_tr8x2(vtile + qt_vidx(8 * kg + j / 4, d0 + 16 * dt + 4 * (j & 3)),
                               vtile + qt_vidx(8 * kg + 4 + j / 4, d0 + 16 * dt + 4 * (j & 3)));
-#pragma unroll
-    for (int dt = 0; dt < 2; dt++) {
-        const qt_f32x4 acc = qt_mfma_bf16(pa, vv[dt], qt_f32x4{0.f, 0.f, 0.f, 0.f});
-        o[dt] = (acc[0] + acc[1]) + acc[2];
-    }
 }
-template <int NMAX>
-__device__ __forceinline__ void qt_att_fold(int n, const float (&ot)[NMAX][2], const float (&mt)[NMAX], const float (&lt)[NMAX],
-                                            float (&o)[2], float &M, float &l) {
-    M = mt[0];                                              // finite: k-tile 0 holds key 0
-#pragma unroll
-    for (int t = 1; t < NMAX; t++)
-        if (t < n) M = fmaxf(M, mt[t]);
-    o[0] = o[1] = 0.f;
-    l = 0.f;
-#pragma unroll
-    for (int t = 0; t < NMAX; t++)
-        if (t < n) {
-            const float f = qt_exp2(mt[t] - M);
-            l = fmaf(lt[t], f, l);
-            o[0] = fmaf(ot[t][0], f, o[0]);
-            o[1] = fmaf(ot[t][1], f, o[1]);
-        }
-}
-// qt_att_pv1 for the four k-tiles of one 128-key block at once (columns pcol + 32t of pp,
-// value rows 32t .. of vblk): every LDS read is issued before the first MFMA.  k-tiles
-// past the chunk's keys give values the caller does not fold.
-__device__ __forceinline__ void qt_att_pv4(const uint16_t *pp, int pstride, int pcol, const uint16_t *vblk, int d0, int lane,
-                                           float (&ot)[4][2]) {
-    const int kg = lane >> 4, j = lane & 15;
-    qt_u32x4 pa[4], vv[4][2];
-#pragma unroll
-    for (int t = 0; t < 4; t++) {
-        pa[t] = qt_lds16(pp + (lane & 15) * pstride + pcol + 32 * t + 8 * kg);
-#pragma unroll
-        for (int dt = 0; dt < 2; dt++)
-            vv[t][dt] = qt_lds_tr8x2(vblk + 32 * t * 128 + qt_vidx(8 * kg + j / 4, d0 + 16 * dt + 4 * (j & 3)),
-                                     vblk + 32 * t * 128 + qt_vidx(8 * kg + 4 + j / 4, d0 + 16 * dt + 4 * (j & 3)));
-    }
-    asm volatile("" : "+v"(pa[0]), "+v"(vv[0][0]), "+v"(vv[0][1]), "+v"(pa[1]), "+v"(vv[1][0]), "+v"(vv[1][1]),
-                 "+v"(pa[2]), "+v"(vv[2][0]), "+v"(vv[2][1]), "+v"(pa[3]), "+v"(vv[3][0]), "+v"(vv[3][1]));
-#pragma unroll
-    for (int t = 0; t < 4; t++)
-#pragma unroll
-        for (int dt = 0; dt < 2; dt++) {
-            const qt_f32x4 acc = qt_mfma_bf16(pa[t], vv[t][dt], qt_f32x4{0.f, 0.f, 0.f, 0.f});
-            ot[t][dt] = (acc[0] + acc[1]) + acc[2];
-        }
+__device__ __forceinline__ void qt_cm_mfma(const qt_u32x4 &pa, const qt_u32x4 (&vv)[2], qt_f32x4 (&acc)[2]) {
+    acc[0] = qt_mfma_bf16(pa, vv[0], acc[0]);
+    acc[1] = qt_mfma_bf16(pa, vv[1], acc[1]);
 }

@@ -71,14 +71,17 @@ constexpr int SC1 = 16;                          // buffer cache policy: agent s
 // workgroup at marks k of (step, layer) — 0 its input wait starts, 1 the input has
 // arrived, 2 its output is published, 3 its next tile has landed; attention adds 4 (merge
 // input arrived) and 5 (merge output published); layer index L is the head (0 wait starts,
-// 1 x arrived, 2 winner published, 4 winners arrived).  Steps past TR_STEPS are not kept.
+// 1 x arrived, 2 winner published, 4 winners arrived).  Marks 1 and 2 also keep the shader
+// clock counter (s_memtime) in slots 13 and 14.  Steps past TR_STEPS are not kept.
 #ifdef QT_RSTEP_TRACE
 constexpr int TR_STEPS = 8, TR_L = 33;
-__device__ unsigned long long rs_trace[NB][TR_STEPS * TR_L][12];
+__device__ unsigned long long rs_trace[NB][TR_STEPS * TR_L][16];
 #define RS_MARK(st, l, k)                                                                             \
     do {                                                                                              \
-        if (threadIdx.x == 0 && (st) < TR_STEPS)                                                      \
+        if (threadIdx.x == 0 && (st) < TR_STEPS) {                                                    \
             rs_trace[blockIdx.x][(st) * TR_L + (l)][k] = __builtin_amdgcn_s_memrealtime();            \
+            if ((k) == 1 || (k) == 2) rs_trace[blockIdx.x][(st) * TR_L + (l)][12 + (k)] = __builtin_amdgcn_s_memtime(); \
+        }                                                                                             \
     } while (0)
 #else
 #define RS_MARK(st, l, k) do { } while (0)
@@ -325,7 +328,7 @@ struct LdsA {                    // ATT + MRG
     uint16_t v[ABLK][KVB * HD];  // value rows of the chunk (qt_attn_mf.h swizzle), per 128-key block
     uint16_t qp[16][HD];
     uint16_t pp[16][ABLK * KVB]; // probability pieces of the chunk's keys, row 4h+p
-    float ml[4 * ABLK][HPK][2];  // per-k-tile (max, exp-sum)
+    float ml[4][HPK][2];         // per-wave (max, exp-sum)
     float qkv[HPK * HD + 2 * HD];
     uint16_t knew[HD], vnew[HD];
     float mo[ACH][32];           // merge inputs
@@ -863,84 +866,79 @@ __device__ __forceinline__ void role_dn(const Ctx &c, LdsD &s, int di) {
     }
 }
 
-// ---- attention chunk (one pass) -----------------------------------------------------------
+// ---- attention chunk (one pass under the chunk maximum, qt_attn_mf.h) --------------------
 // NBK 128-key blocks: K rows in kf (wave w holds k-tile w of each block), V rows in LDS.
-// Scores and the per-k-tile softmax are qt_att_tiles' (the key rows from registers); the
-// P.V of each k-tile is qt_att_pv1's, folded by qt_att_fold.  k-tiles past the chunk's
-// keys are computed and not folded.
+// k-tiles holding no key are neither scored nor multiplied.
 template <int NBK>
 __device__ __forceinline__ void att_chunk(LdsA &s, const uint4 (&kf)[ABLK][8], int n, float scale2, QtAttRun &run, int st_, int l_) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, kg = lane >> 4, key = lane & 15, hh = lane >> 4;
+    const int hc = hh < HPK ? hh : HPK - 1;
     qt_u32x4 qa[4];
 #pragma unroll
     for (int s2 = 0; s2 < 4; s2++) qa[s2] = qt_lds16(&s.qp[key][32 * s2 + 8 * kg]);
+    // 1. scores and the wave's maximum
     float sv[NBK][2];
-#pragma unroll
-    for (int b = 0; b < NBK; b++)
-#pragma unroll
-        for (int t2 = 0; t2 < 2; t2++) {
-            qt_f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-            for (int s2 = 0; s2 < 4; s2++) {
-                const uint4 kk = kf[b][t2 * 4 + s2];
-                acc = qt_mfma_bf16(qa[s2], qt_u32x4{kk.x, kk.y, kk.z, kk.w}, acc);
-            }
-            sv[b][t2] = (acc[0] + acc[1]) + acc[2];
-        }
-    RS_MARK(st_, l_, 8);
+    float wm = -INFINITY;
 #pragma unroll
     for (int b = 0; b < NBK; b++) {
-        const int nk = min(KVB, n - KVB * b);
-        const int r00 = 32 * wave, r01 = 32 * wave + 16;
-        const float sa = r00 + key < nk ? sv[b][0] * scale2 : -INFINITY;
-        const float sb = r01 + key < nk ? sv[b][1] * scale2 : -INFINITY;
-        const float m = group_max<16>(fmaxf(sa, sb));
-        const float pa = qt_exp2(sa - m), pb = qt_exp2(sb - m);
-        const float ls = group_sum<16>(pa + pb);
-        if (hh < HPK) {
-            uint16_t *pp = &s.pp[0][0] + KVB * b;
-            qt_put_pieces(pp + 4 * hh * (ABLK * KVB) + r00 + key, ABLK * KVB, pa);
-            qt_put_pieces(pp + 4 * hh * (ABLK * KVB) + r01 + key, ABLK * KVB, pb);
-            if (key == 0) { s.ml[4 * b + wave][hh][0] = m; s.ml[4 * b + wave][hh][1] = ls; }
+        const int r0 = KVB * b + 32 * wave;
+        sv[b][0] = sv[b][1] = -INFINITY;
+        if (r0 < n) {
+#pragma unroll
+            for (int t2 = 0; t2 < 2; t2++) {
+                qt_f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int s2 = 0; s2 < 4; s2++) {
+                    const uint4 kk = kf[b][t2 * 4 + s2];
+                    acc = qt_mfma_bf16(qa[s2], qt_u32x4{kk.x, kk.y, kk.z, kk.w}, acc);
+                }
+                const float sc = (acc[0] + acc[1]) + acc[2];
+                sv[b][t2] = r0 + 16 * t2 + key < n ? sc * scale2 : -INFINITY;
+            }
+            wm = fmaxf(wm, group_max<16>(fmaxf(sv[b][0], sv[b][1])));
         }
     }
+    RS_MARK(st_, l_, 8);
+    if (hh < HPK && key == 0) s.ml[wave][hh][0] = wm;
+    __syncthreads();
+    // 2., 3. chunk maximum, probabilities, the wave's sums
+    const float M = fmaxf(fmaxf(s.ml[0][hc][0], s.ml[1][hc][0]), fmaxf(s.ml[2][hc][0], s.ml[3][hc][0]));
+    float lw = 0.f;
+#pragma unroll
+    for (int b = 0; b < NBK; b++) {
+        const int r0 = KVB * b + 32 * wave;
+        if (r0 < n) lw += qt_cm_probs<HPK>(sv[b][0], sv[b][1], M, &s.pp[0][0], ABLK * KVB, r0, lane);
+    }
+    if (hh < HPK && key == 0) s.ml[wave][hh][1] = lw;
     RS_MARK(st_, l_, 9);
     __syncthreads();
     RS_MARK(st_, l_, 10);
-    const int hc = hh < HPK ? hh : HPK - 1, j = lane & 15, d0 = 32 * wave;
-    float mt[NBK * 4], lt[NBK * 4], ot[NBK * 4][2];
-    // P.V in groups of (up to) two blocks: every LDS read of a group is issued before its
-    // MFMAs
-    constexpr int GB = NBK < 2 ? NBK : 2;
+    // 4. P.V over the k-tiles holding keys, operands of up to eight k-tiles read before
+    // their MFMAs
+    const int nt = (n + 31) >> 5, d0 = 32 * wave;
+    qt_f32x4 acc[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
+    constexpr int NTL = NBK * 4, GT = NTL < 8 ? NTL : 8;
 #pragma unroll
-    for (int g0 = 0; g0 < NBK; g0 += GB) {
-        qt_u32x4 pa[GB * 4], vv[GB * 4][2];
+    for (int g0 = 0; g0 < NTL; g0 += GT) {
+        qt_u32x4 pa[GT], vv[GT][2];
 #pragma unroll
-        for (int u = 0; u < GB * 4; u++) {
-            const int t = 4 * g0 + u;
-            if (t >= NBK * 4) break;
-            const uint16_t *vt = &s.v[t >> 2][32 * (t & 3) * HD];
-            pa[u] = qt_lds16(&s.pp[0][0] + (lane & 15) * (ABLK * KVB) + 32 * t + 8 * kg);
-#pragma unroll
-            for (int dt = 0; dt < 2; dt++)
-                vv[u][dt] = qt_lds_tr8x2(vt + qt_vidx(8 * kg + j / 4, d0 + 16 * dt + 4 * (j & 3)),
-                                         vt + qt_vidx(8 * kg + 4 + j / 4, d0 + 16 * dt + 4 * (j & 3)));
-            mt[t] = s.ml[t][hc][0];
-            lt[t] = s.ml[t][hc][1];
+        for (int u = 0; u < GT; u++) {
+            const int t = g0 + u;
+            if (t >= nt) break;
+            qt_cm_operands(&s.pp[0][0], ABLK * KVB, 32 * t, &s.v[t >> 2][32 * (t & 3) * HD], d0, lane, pa[u], vv[u]);
         }
 #pragma unroll
-        for (int u = 0; u < GB * 4; u++) {
-            const int t = 4 * g0 + u;
-            if (t >= NBK * 4) break;
-#pragma unroll
-            for (int dt = 0; dt < 2; dt++) {
-                const qt_f32x4 acc = qt_mfma_bf16(pa[u], vv[u][dt], qt_f32x4{0.f, 0.f, 0.f, 0.f});
-                ot[t][dt] = (acc[0] + acc[1]) + acc[2];
-            }
+        for (int u = 0; u < GT; u++) {
+            const int t = g0 + u;
+            if (t >= nt) break;
+            qt_cm_mfma(pa[u], vv[u], acc);
         }
     }
     RS_MARK(st_, l_, 11);
-    qt_att_fold<NBK * 4>((n + 31) >> 5, ot, mt, lt, run.o, run.m, run.l);
+#pragma unroll
+    for (int dt = 0; dt < 2; dt++) run.o[dt] = (acc[dt][0] + acc[dt][1]) + acc[dt][2];
+    run.m = M;
+    run.l = ((s.ml[0][hc][1] + s.ml[1][hc][1]) + s.ml[2][hc][1]) + s.ml[3][hc][1];
 }
 
 // ---- ATT + MRG -----------------------------------------------------------------------------
@@ -1055,9 +1053,10 @@ __device__ __forceinline__ void role_att(const Ctx &c, LdsA &s, int g, int ch) {
                     }
                 }
                 RS_MARK(step, l, 6);
-                // one pass over the chunk (qt_att_fold), specialised on its block count so
+                // one pass over the chunk (qt_attn_mf.h), specialised on its block count so
                 // that it is straight-line code: every wave scores its k-tile of every block,
-                // one barrier, then P.V of its 32 dims over all k-tiles
+                // two barriers (chunk maximum, probabilities), then P.V of its 32 dims over
+                // the k-tiles
                 QtAttRun run;
                 if (nblk == 1) att_chunk<1>(s, kf, n, scale2, run, step, l);
                 else if (nblk == 2) att_chunk<2>(s, kf, n, scale2, run, step, l);
