@@ -72,12 +72,15 @@ constexpr int SC1 = 16;                          // buffer cache policy: agent s
 // arrived, 2 its output is published, 3 its next tile has landed; attention adds 4 (merge
 // input arrived) and 5 (merge output published); layer index L is the head (0 wait starts,
 // 1 x arrived, 2 winner published, 4 winners arrived).  Marks 1 and 2 also keep the shader
-// clock counter (s_memtime) in slots 13 and 14.  Steps past TR_STEPS are not kept.
+// clock counter (s_memtime) in slots 13 and 14, and mark 1 of wave w is also kept in slot
+// 16 + w.  Steps past TR_STEPS are not kept.
 #ifdef QT_RSTEP_TRACE
 constexpr int TR_STEPS = 8, TR_L = 33;
-__device__ unsigned long long rs_trace[NB][TR_STEPS * TR_L][16];
+__device__ unsigned long long rs_trace[NB][TR_STEPS * TR_L][24];
 #define RS_MARK(st, l, k)                                                                             \
     do {                                                                                              \
+        if ((st) < TR_STEPS && (k) == 1 && (threadIdx.x & 63) == 0)                                   \
+            rs_trace[blockIdx.x][(st) * TR_L + (l)][16 + (threadIdx.x >> 6)] = __builtin_amdgcn_s_memrealtime(); \
         if (threadIdx.x == 0 && (st) < TR_STEPS) {                                                    \
             rs_trace[blockIdx.x][(st) * TR_L + (l)][k] = __builtin_amdgcn_s_memrealtime();            \
             if ((k) == 1 || (k) == 2) rs_trace[blockIdx.x][(st) * TR_L + (l)][12 + (k)] = __builtin_amdgcn_s_memtime(); \
@@ -125,6 +128,9 @@ __device__ __forceinline__ void put(unsigned *p, float v) {
 }
 __device__ __forceinline__ bool stale16(const uint4 &v) { return v.x == SENT || v.y == SENT || v.z == SENT || v.w == SENT; }
 __device__ __forceinline__ void land() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+// A wave's LDS accesses complete in program order, so LDS data a wave wrote for itself
+// needs no barrier before it reads it back: only the compiler must keep the order.
+__device__ __forceinline__ void wave_lds_order() { asm volatile("" ::: "memory"); }
 
 // Waits until the 16-byte groups i = tid + NT*k < n16 (byte offset off(i) in r) hold no
 // sentinel; stale groups are re-read after a short pause.  Bounded.
@@ -516,7 +522,7 @@ __device__ __forceinline__ float norm_pieces(const float (&xv)[8], const float (
     const float v[8] = {(p0.x * inv) * gu[0], (p0.y * inv) * gu[1], (p0.z * inv) * gu[2], (p0.w * inv) * gu[3],
                         (p1.x * inv) * gu[4], (p1.y * inv) * gu[5], (p1.z * inv) * gu[6], (p1.w * inv) * gu[7]};
     pcw_put8<H>(pc, tid, v, ps.isc);
-    __syncthreads();
+    wave_lds_order();   // unit tid: wave w makes the pieces of columns 512w .. +511, its own K slice
     return ps.s;
 }
 // the RMSNorm gains a thread needs: statistics elements tid + NT*k, unit elements 8 tid ..
@@ -654,7 +660,7 @@ __device__ __forceinline__ void role_o(const Ctx &c, LdsP &s, int oi) {
                 const float v8[8] = {p0.x, p0.y, p0.z, p0.w, p1.x, p1.y, p1.z, p1.w};
                 pcw_put8<QD>(s.pc, tid, v8, ps.isc);
             }
-            __syncthreads();
+            wave_lds_order();   // unit tid: wave w makes the pieces of columns 512w .. +511, its own K slice
             RS_MARK(step, l, 6);
             i32x4 acc[8];
             rdot16<QD, 8, QD / 4 / 64, 1>(t, s.pc, wave * (QD / 4), acc);
@@ -783,15 +789,17 @@ __device__ __forceinline__ void role_dn(const Ctx &c, LdsD &s, int di) {
         const int par = step & 1;
         const bool last = step + 1 == a.n_steps;
         for (int l = 0; l < c.L; l++) {
+            // thread (wave w, lane) takes h units 192w + lane + 64k (8 values each), all in
+            // the wave's own K slice, and the residual rows of xa
             uint4 v[7];
             {
                 const unsigned bh = (c.blk(par, l) + R_H) * 4u, bx = (c.blk(par, l) + R_XA + row0) * 4u;
-                const int n16 = F / 4 + nrows / 4;
+                const int n16 = 6 * NT + nrows / 4;
                 RS_MARK(step, l, 0);
                 wait16<7, 16>(c.rr, n16, [&](int i) {
-                    if (i >= F / 4) return bx + (unsigned)(i - F / 4) * 16u;
-                    const int j = i / NT;                       // slot: unit tid + NT*(j/2), half j%2
-                    return bh + (unsigned)(2 * (i % NT + NT * (j >> 1)) + (j & 1)) * 16u;
+                    const int k = i / NT, t = i % NT;
+                    if (k < 6) return bh + (unsigned)(2 * (192 * (t >> 6) + (t & 63) + 64 * (k >> 1)) + (k & 1)) * 16u;
+                    return bx + (unsigned)t * 16u;
                 }, v, a.err);
                 RS_MARK(step, l, 1);
             }
@@ -807,9 +815,9 @@ __device__ __forceinline__ void role_dn(const Ctx &c, LdsD &s, int di) {
             for (int k = 0; k < 3; k++) {
                 const float4 p0 = f4(v[2 * k]), p1 = f4(v[2 * k + 1]);
                 const float v8[8] = {p0.x, p0.y, p0.z, p0.w, p1.x, p1.y, p1.z, p1.w};
-                pcw_put8<F>(s.pc, tid + NT * k, v8, ps.isc);
+                pcw_put8<F>(s.pc, 192 * wave + lane + 64 * k, v8, ps.isc);
             }
-            __syncthreads();
+            wave_lds_order();   // the wave's own K slice
             RS_MARK(step, l, 6);
             i32x4 acc[3];
             {
