@@ -25,9 +25,11 @@ from __future__ import annotations
 
 import argparse
 import ctypes as C
+import hashlib
 import importlib.util
 import json
 import os
+import subprocess
 import sys
 import tempfile
 import time
@@ -79,6 +81,68 @@ class HipEvents:
 
     def device_sync(self):
         assert self.rt.hipDeviceSynchronize() == 0
+
+
+DEFAULT_WORKLOAD = "talker-1.7B-int8-b1-L2048"
+# fused kernel kinds (qwen_hip_talker_fused_kernel): label, the sources that define it
+FUSED_KERNELS = {
+    2: ("ps::rs::k_rstep role-specialised fused decode step ({prec})",
+        ("qt_rstep.hip", "qt_step_common.h", "qt_attn_mf.h", "qt_device.h")),
+    1: ("ps::k_pstep<{prec}> fused decode step", ("qt_pstep.hip", "qt_step_common.h", "qt_attn_mf.h", "qt_device.h")),
+}
+
+
+def kernel_source_sha256(kind):
+    h = hashlib.sha256()
+    for f in FUSED_KERNELS[kind][1]:
+        with open(os.path.join(ROOT, "qwen3-tts_amd", "csrc", f), "rb") as fh:
+            h.update(fh.read())
+    return h.hexdigest()
+
+
+def refuse_if_device_error(L, g, workload):
+    """The fused kernels' waits are bounded: one that gives up sets the device error flag
+    and the remaining steps end early, so a launch with the flag set must not be timed."""
+    if L.qwen_hip_talker_sync(g.h) != 0:
+        msg = L.qwen_hip_last_error().decode(errors="replace")
+        print(json.dumps({"error": f"{workload}: the timed launch failed: {msg}", "value": None}), flush=True)
+        sys.exit(1)
+
+
+# BASELINE configs 1-5 as short runs of their workloads (each in a child process, before the
+# headline's own measurement): (key, workload, extra arguments)
+CONFIG_RUNS = [
+    ("1_0.6B_bf16_L256", "talker-0.6B-bf16-b1-L256", ["--steps", "256", "--warmup", "16"]),
+    ("2_0.6B_int8_grow0-2048", "talker-0.6B-int8-grow2048", []),
+    ("3_1.7B_q4_0_L512", "talker-1.7B-int4-b1-L512", ["--steps", "32", "--warmup", "8"]),
+    ("3_1.7B_q4_0_L2048", "talker-1.7B-int4-b1-L2048", ["--steps", "32", "--warmup", "8"]),
+    ("3_1.7B_q4_0_L4096", "talker-1.7B-int4-b1-L4096", ["--steps", "32", "--warmup", "8"]),
+    ("4_cp_0.6B_bf16_frame", "cp-0.6B-bf16-frame", ["--steps", "100", "--warmup", "10"]),
+    ("5_1.7B_int8_b32_ragged", "talker-1.7B-int8-b32-ragged", ["--steps", "16", "--warmup", "4"]),
+]
+
+
+def run_configs():
+    res = {}
+    for key, wl, extra in CONFIG_RUNS:
+        cmd = [sys.executable, os.path.abspath(__file__), "--workload", wl, "--no-cpu-baseline", "--no-configs",
+               "--kernel-launches", "0", *extra]
+        t0 = time.time()
+        try:
+            p = subprocess.run(cmd, capture_output=True, text=True, timeout=240)
+            lines = [x for x in p.stdout.splitlines() if x.startswith("{")]
+            if not lines:
+                raise RuntimeError(f"exit {p.returncode}: " + " | ".join(p.stderr.strip().splitlines()[-3:]))
+            r = json.loads(lines[-1])
+            res[key] = {"workload": wl, "value": r.get("value"), "unit": r.get("unit"),
+                        "roofline_frac": (r.get("roofline") or {}).get("frac"), "steps": r.get("steps"),
+                        "wall_s": round(time.time() - t0, 1)}
+            if "error" in r:
+                res[key]["error"] = r["error"]
+        except Exception as ex:  # one config's failure is reported, not fatal to the line
+            res[key] = {"workload": wl, "value": None, "error": str(ex)[:200], "wall_s": round(time.time() - t0, 1)}
+        log(f"[bench] config {key}: {res[key]}")
+    return res
 
 
 WORKLOADS = {
@@ -161,11 +225,13 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=None)
     ap.add_argument("--warmup", type=int, default=None)
-    ap.add_argument("--workload", default="talker-1.7B-int8-b1-L2048", choices=sorted(WORKLOADS) + sorted(BATCH_WORKLOADS) + sorted(CP_WORKLOADS)
+    ap.add_argument("--workload", default=DEFAULT_WORKLOAD, choices=sorted(WORKLOADS) + sorted(BATCH_WORKLOADS) + sorted(CP_WORKLOADS)
                     + sorted(PREFILL_WORKLOADS) + sorted(GROW_WORKLOADS) + sorted(SAMPLED_WORKLOADS)
                     + sorted(FRAME_WORKLOADS) + sorted(SD_WORKLOADS) + sorted(SD_STREAM_WORKLOADS)
                     + sorted(CP_BATCH_WORKLOADS))
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-configs", action="store_true",
+                    help="skip the short runs of BASELINE configs 1-5 that the default workload's line carries")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--kernel-launches", type=int, default=200)
     ap.add_argument("--calib-copy-mb", type=int, default=0,
@@ -177,6 +243,10 @@ def main():
                                    "data-parallel streams with no exchange between GPUs; run --gpus 1"}))
         sys.exit(2)
 
+    # the config runs go first, each in a child process, while this process has not touched
+    # the GPU: a cooperative launch holds the device's global wave-sync resource until its
+    # process ends, so a child could not launch its own persistent kernel after ours
+    configs = run_configs() if (not args.no_configs and args.workload == DEFAULT_WORKLOAD) else None
     _pkg()
     if args.workload in BATCH_WORKLOADS:
         return bench_batch(args)
@@ -263,6 +333,7 @@ def main():
     ev.record(b, stream)
     ms_total = ev.elapsed_ms(a, b)
     ev.device_sync()
+    refuse_if_device_error(L, g, args.workload)
     ms = ms_total / K
     L_mid = Lpre + K / 2.0
     kv_bytes = 2 * s.layers * s.kv_dim * 2       # per position, K and V
@@ -283,21 +354,25 @@ def main():
         kern[nm] = ev.elapsed_ms(a, b) * 1e3 / n
     if kern:
         log("[bench] per-kernel avg us: " + ", ".join(f"{k}={v:.2f}" for k, v in kern.items()))
-    fused = bool(L.qwen_hip_talker_fused(g.h))
+    kind = L.qwen_hip_talker_fused_kernel(g.h)
     roofline = {"bound": "hbm", "achieved": round(step_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": round(step_gbs / HBM_PEAK_GBS, 4), "traffic": None,
-                "kernel": (f"ps::k_pstep<{prec}> fused decode step" if fused else "unfused per-kernel path"),
+                "kernel": FUSED_KERNELS.get(kind, ("unfused per-kernel path",))[0].format(prec=prec),
                 "bytes_per_launch": int(step_bytes * K), "avg_us": round(ms_total * 1e3, 1),
                 "steps_per_launch": K}
     # HBM bytes per launch from the committed rocprofv3 PMC passes for this workload: the
     # measured bytes per step at the profiled mean KV length, moved to this run's mean KV
-    # length by the K/V bytes of the difference, times K
+    # length by the K/V bytes of the difference, times K.  Only while the kernel's sources
+    # are the ones profiled (their sha256 is recorded with the counters): otherwise null.
     try:
         t = json.load(open(os.path.join(ROOT, "profiles", "pstep_traffic.json")))
-        if fused and t["workload"] == args.workload:
-            per_step = t["traffic_bytes_per_step"] + kv_bytes * (L_mid - t["kv_len_mid"])
-            roofline["traffic"] = int(per_step * K)
-            roofline["traffic_source"] = t["source"]
+        if kind in FUSED_KERNELS and t["workload"] == args.workload and t["kernel"] == FUSED_KERNELS[kind][0].format(prec=prec):
+            if t["source_sha256"] == kernel_source_sha256(kind):
+                per_step = t["traffic_bytes_per_step"] + kv_bytes * (L_mid - t["kv_len_mid"])
+                roofline["traffic"] = int(per_step * K)
+                roofline["traffic_source"] = t["source"]
+            else:
+                roofline["traffic_stale"] = "the kernel's sources changed since the committed counter passes"
     except (OSError, ValueError, KeyError):
         pass
 
@@ -324,6 +399,8 @@ def main():
         "kv_upload": kv_upload,
         "roofline": roofline, "cpu_baseline": cpu,
     }
+    if configs is not None:
+        out["configs"] = configs
     print(json.dumps(out), flush=True)
 
 
@@ -430,6 +507,7 @@ def bench_grow(args):
         ev.record(b, stream)
         ms_total = ev.elapsed_ms(a, b)
         ev.device_sync()
+        refuse_if_device_error(L, g, args.workload)
         total_ms += ms_total
         ms = ms_total / seg
         lm = i * seg + seg / 2.0
@@ -632,6 +710,7 @@ def bench_prefill(args):
     ev.record(b, stream)
     ms_total = ev.elapsed_ms(a, b)
     ev.device_sync()
+    refuse_if_device_error(L, g, args.workload)
     ms = ms_total / K
     fl = prefill_flops(s, S)
     tfs = fl / (ms * 1e-3) / 1e12
@@ -730,6 +809,7 @@ def bench_cp(args):
     ev.record(b, stream)
     ms_total = ev.elapsed_ms(a, b)
     ev.device_sync()
+    hip.check(L.qwen_hip_cp_sync(cp.h), "cp timed frames")
     ms = ms_total / K
     wb = (lambda r, c: r * c * 2) if prec == "bf16" else (lambda r, c: r * c + 4 * r)   # int8: + row scales
     per_layer = 0

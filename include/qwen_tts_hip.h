@@ -128,6 +128,10 @@ void *qwen_hip_talker_stream(void *state);
  * persistent kernel, 0 when they run as the per-kernel sequence (shapes or devices the
  * fused kernel does not cover), -1 for a NULL state. */
 int   qwen_hip_talker_fused(void *state);
+/* Diagnostic query (no reference counterpart): which fused kernel runs the steps —
+ * 2 the role-specialised persistent kernel (qt_rstep.hip), 1 the single-role persistent
+ * kernel (qt_pstep.hip), 0 the per-kernel sequence, -1 for a NULL state. */
+int   qwen_hip_talker_fused_kernel(void *state);
 /* Diagnostic (no reference counterpart; the device twin of the per-layer check the
  * reference's own tests make by truncating num_layers, qwen_tts_talker.c:659-665): one step
  * like qwen_hip_talker_step that also returns the residual after every layer,

@@ -474,6 +474,11 @@ fail:
 void qwen_hip_talker_free(void *state) { talker_destroy((talker_t *)state); }
 void *qwen_hip_talker_stream(void *state) { return state ? (void *)((talker_t *)state)->st : NULL; }
 int qwen_hip_talker_fused(void *state) { return state ? ((talker_t *)state)->ps_on : -1; }
+int qwen_hip_talker_fused_kernel(void *state) {
+    if (!state) return -1;
+    const talker_t *t = (const talker_t *)state;
+    return t->ps_on ? (t->rs_on ? 2 : 1) : 0;
+}
 
 static hipError_t talker_body(talker_t *t) {
     hipError_t e;
