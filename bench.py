@@ -365,7 +365,7 @@ def main():
     # length by the K/V bytes of the difference, times K.  Only while the kernel's sources
     # are the ones profiled (their sha256 is recorded with the counters): otherwise null.
     try:
-        t = json.load(open(os.path.join(ROOT, "profiles", "pstep_traffic.json")))
+        t = json.load(open(os.path.join(ROOT, "profiles", "fused_step_traffic.json")))
         if kind in FUSED_KERNELS and t["workload"] == args.workload and t["kernel"] == FUSED_KERNELS[kind][0].format(prec=prec):
             if t["source_sha256"] == kernel_source_sha256(kind):
                 per_step = t["traffic_bytes_per_step"] + kv_bytes * (L_mid - t["kv_len_mid"])
