@@ -153,7 +153,9 @@ int   qwen_hip_talker_launch_kernel(void *state, int kernel, int layer, int n);
 /* ---- level 2: batched Talker step (qwen_tts_cuda_talker.cu:595-648; CPU twin
  * batch_talker_step_impl, qwen_tts_talker.c:1192-1270, qwen_tts_batch.h:87-98) ----
  * B <= 64 streams share the single state's device weights (read once per step for all
- * streams; int8 weights on the MFMA GEMM, bf16/q4_0 as B matvecs); each stream has its
+ * streams: every precision runs each projection as one GEMM over the B streams on the
+ * matrix cores -- int8 and q4_0 on the integer MFMA with exact int8 activation pieces,
+ * bf16 on the bf16 MFMA with exact bf16 activation planes); each stream has its
  * own bf16 KV cache (single state's kv_max) and its own position (ragged).  Free the
  * batch before the single state. */
 
@@ -332,7 +334,9 @@ int qwen_hip_op_matmat_q4_0(float *Y, const void *W, const float *X, int rows, i
  * asynchronous.  The activation pieces live in a file-scope device array of
  * 8192*3*64 + 256 bytes per GPU (held until the process ends), so cols <= 8192 (a multiple
  * of 64) and 1 <= B <= 64; larger shapes return -1 with qwen_hip_last_error() set.
- * Allocates nothing.  Calls that overlap on one GPU share that array and race. */
+ * The array used is the one of the device `stream` belongs to (the current device for the
+ * null stream).  Allocates nothing.  Calls that overlap on one GPU share that array and
+ * race: callers must serialise them on one stream per GPU. */
 int qwen_hip_op_matmat_int8_noalloc(float *Y, const int8_t *W, const float *scale, const float *X, int rows, int cols,
                                     int B, void *stream);
 /* qwen_quantize_bf16_to_int8 / _q4_0 (k.c:2143, k.c:2662) run on the device; output in
@@ -370,8 +374,10 @@ int qwen_hip_sd_decode_device(void *state, const int *d_codes, int n_frames, flo
 int qwen_hip_sd_latent(void *state, const int *codes, int n_frames, float *latent_out);
 void *qwen_hip_sd_stream(void *state);
 void qwen_hip_sd_free(void *state);
-/* Streaming decode (qwen_speech_decoder_decode_streaming_st, sd.c:1881-2389, its exact path):
- * a stream state over a decoder state (weights shared; several streams may share one
+/* Streaming decode (qwen_speech_decoder_decode_streaming_st, sd.c:1881-2389: the same
+ * contract -- new frames in, exactly their samples out -- with the one-shot decode's
+ * arithmetic, so its ConvNeXt LayerNorm is E[x^2] - mean^2 where the reference's streaming
+ * path uses a two-pass one, sd.c:1343-1352): a stream state over a decoder state (weights shared; several streams may share one
  * decoder, calls on them are serialised on its stream).  Each call decodes new_frames more
  * frames of the utterance and returns exactly their 1920 new_frames samples, equal to that
  * slice of the one-shot decode of all frames so far (qwen_hip_sd_decode); at most 8000 frames

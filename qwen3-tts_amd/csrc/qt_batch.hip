@@ -352,6 +352,14 @@ __global__ __launch_bounds__(QT_B2_W * 64) void k_bgemm2_i8(QtBg2Args a) {
                     __hip_atomic_store(mine + (size_t)(tid + u * NTH) * H + h, T[u][h], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         __builtin_amdgcn_s_waitcnt(0);
         __syncthreads();
+        // Ordering without release/acquire fences: the partials are agent-scope atomic
+        // stores (sc1: written through to the device coherence point, never left dirty in
+        // an XCD's L2), the count is incremented only after s_waitcnt has seen every one of
+        // them acknowledged, and the last workgroup reads the others' partials with
+        // agent-scope atomic loads (sc1: not served from a stale L1/L2 line) issued after
+        // its own increment returned the final count.  An agent-scope acq_rel increment
+        // plus acquire fence would add an L2 write-back and invalidate per workgroup:
+        // measured 3.07 -> 3.35 ms per batched step (32 ragged streams, 1.7B int8).
         if (tid == 0)
             last_flag = __hip_atomic_fetch_add(&a.cnt[x], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
                         (unsigned)(S - 1);

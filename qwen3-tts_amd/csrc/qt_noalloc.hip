@@ -5,11 +5,12 @@
 // per-stream scales, qt_batch.hip) is a file-scope device array, so no call allocates.
 //
 // The array's name is only a host-side stand-in: its device address is taken once per
-// device with hipGetSymbolAddress (the device current at the first call) and kept in a
-// per-device table; kernels are given that address, never the name.  Every call on a
-// GPU shares that GPU's array, so calls that overlap on one GPU (two streams, two
-// threads) race; the pieces kernel writes every byte the GEMM reads (padding streams
-// included), so nothing needs clearing between calls.
+// device with hipGetSymbolAddress (with that device current) and kept in a per-device
+// table; kernels are given that address, never the name.  The device is the one the
+// `stream` argument belongs to (the current device for the null stream).  Every call on a
+// GPU shares that GPU's array, so calls that overlap on one GPU (two streams, two threads)
+// race: callers serialise them on one stream per GPU.  The pieces kernel writes every
+// byte the GEMM reads (padding streams included), so nothing needs clearing between calls.
 #include <hip/hip_runtime.h>
 #include <pthread.h>
 
@@ -27,19 +28,32 @@ static __device__ __align__(256) unsigned char scratch[QT_NA_BYTES];
 static pthread_mutex_t g_na_lock = PTHREAD_MUTEX_INITIALIZER;
 static void *g_na_ptr[QT_NA_MAX_DEV];
 
-// the current device's copy of the array (looked up once per device), NULL on error
-static void *na_scratch(void) {
+// the stream's device's copy of the array (looked up once per device), NULL on error
+static void *na_scratch(hipStream_t st) {
     int dev = -1;
-    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= QT_NA_MAX_DEV) {
-        qt_seterr("matmat_int8_noalloc: no current HIP device (or device index >= 64)");
+    if (st ? hipStreamGetDevice(st, &dev) != hipSuccess : hipGetDevice(&dev) != hipSuccess) {
+        qt_seterr("matmat_int8_noalloc: cannot tell the stream's device");
+        return NULL;
+    }
+    if (dev < 0 || dev >= QT_NA_MAX_DEV) {
+        qt_seterr("matmat_int8_noalloc: device index %d out of range (0..%d)", dev, QT_NA_MAX_DEV - 1);
         return NULL;
     }
     pthread_mutex_lock(&g_na_lock);
     void *p = g_na_ptr[dev];
     if (!p) {
-        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        // the symbol's address is per device: look it up with the stream's device current
+        int cur = -1;
+        hipError_t e = hipGetDevice(&cur);
+        if (e == hipSuccess && cur != dev) e = hipSetDevice(dev);
+        if (e == hipSuccess) e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (cur >= 0 && cur != dev) {
+            const hipError_t e2 = hipSetDevice(cur);
+            if (e == hipSuccess) e = e2;
+        }
         if (e != hipSuccess || !p) {
-            qt_seterr("matmat_int8_noalloc: hipGetSymbolAddress of the scratch array failed: %s", hipGetErrorString(e));
+            qt_seterr("matmat_int8_noalloc: hipGetSymbolAddress of the scratch array on device %d failed: %s", dev,
+                      hipGetErrorString(e));
             p = NULL;
         } else {
             g_na_ptr[dev] = p;
@@ -64,12 +78,12 @@ extern "C" int qwen_hip_op_matmat_int8_noalloc(float *Y, const int8_t *W, const 
         qt_seterr("matmat_int8_noalloc: B %d out of range (1..%d)", B, QT_NA_MAX_B);
         return -1;
     }
-    unsigned char *base = (unsigned char *)na_scratch();
+    hipStream_t st = (hipStream_t)stream;
+    unsigned char *base = (unsigned char *)na_scratch(st);
     if (!base) return -1;
     const int Bp = (B + 15) & ~15;
     int8_t *P = (int8_t *)base;
     float *S = (float *)(base + QT_NA_PIECE_BYTES);
-    hipStream_t st = (hipStream_t)stream;
     hipError_t e = qt_launch_bpieces(X, cols, NULL, 0.f, cols, B, Bp, P, S, st);
     if (e == hipSuccess)
         e = qt_launch_bgemm_i8(QT_EPI_STORE, (const uint8_t *)W, scale, rows, cols, P, S, B, Bp, Y, rows, st);

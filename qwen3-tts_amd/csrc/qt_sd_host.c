@@ -532,8 +532,10 @@ int qwen_hip_op_sd_conv_transpose(float *Y, const float *X, const float *W, cons
 }
 
 /* ---- streaming decode (qwen_speech_decoder_decode_streaming_st, sd.c:1881-2389) ------------
- * The reference's exact streaming path: each call takes new frames and returns exactly
- * their 1920 samples each, equal to that slice of a one-shot decode.  Here every stage whose
+ * The reference's streaming contract: each call takes new frames and returns exactly
+ * their 1920 samples each, equal to that slice of a one-shot decode (so the ConvNeXt
+ * LayerNorm is the one-shot decode's E[x^2] - mean^2; the reference's streaming path
+ * computes a two-pass one, qwen_tts_speech_decoder.c:1343-1352).  Here every stage whose
  * kernel looks back in time keeps the previous chunk's last rows in front of its input
  * buffer (history rows at negative indices, zero before the first chunk, which is the
  * causal padding): pre-conv 2 rows, the pre-transformer's roped q|k|v 71 rows per layer

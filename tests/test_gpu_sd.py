@@ -197,7 +197,7 @@ def test_sd_glue_over_reference_ctx():
 
 @pytest.mark.parametrize("chunks", [[1, 2, 5, 3], [40, 1, 59], [7]])
 def test_sd_stream_equals_one_shot_bitwise(chunks):
-    """The streaming decode (qwen_hip_sd_stream_*, the reference's exact streaming contract,
+    """The streaming decode (qwen_hip_sd_stream_*, the reference's streaming contract,
     sd.c:2313-2339) returns each chunk's own samples, and the concatenation equals the
     one-shot decode of all frames bit for bit: chunking changes which rows a kernel computes,
     never the order of any sum.  [40, 1, 59] crosses the 72-frame attention window and the
@@ -223,13 +223,27 @@ def test_sd_stream_equals_one_shot_bitwise(chunks):
 
 
 @need_ref
-def test_sd_stream_matches_reference_streaming():
-    """Against the reference's own streaming decode over the same chunks (its exact path,
-    per-conv tails and a KV cache)."""
+@pytest.mark.parametrize("sizes", [[2, 1, 3]])
+def test_sd_stream_matches_reference_streaming(sizes):
+    """Against the reference's own streaming decode over the same chunks (per-conv tails and
+    a KV cache).  The bars are the north-star ones, not bit equality: the reference's
+    streaming path normalises the ConvNeXt blocks with a two-pass LayerNorm
+    (qwen_tts_speech_decoder.c:1343-1352) where the device, like the reference's one-shot
+    path, uses E[x^2] - mean^2.  Longer chunkings (past the 72-frame attention window and
+    the 32-frame internal chunk) are out of reach of the reference build here (no BLAS in
+    the image: its convolutions run as naive loops, a 40-frame streaming chunk took more
+    than 180 s); they are pinned by stream == one-shot to the bit over [40, 1, 59]
+    (test_sd_stream_equals_one_shot_bitwise) and the one-shot decode against the oracle and
+    the reference."""
     from oracle.oracle import RefSpeechDecoder
+    print(f"[case] sd stream vs reference stream, chunks {sizes}", flush=True)
     path, _ = sd_model()
-    codes = sd_codes(6, 31)
-    chunks = [codes[:2], codes[2:3], codes[3:]]
+    n = sum(sizes)
+    codes = sd_codes(n, 31 if n == 6 else 977)
+    chunks, off = [], 0
+    for c in sizes:
+        chunks.append(codes[off:off + c])
+        off += c
     want = RefSpeechDecoder(path, threads=8).stream_decode(chunks)
     st = hip.SpeechDecoderStream(_dec())
     got = np.concatenate([st.decode(c) for c in chunks])
