@@ -184,3 +184,32 @@ int qwen_hip_glue_sd_decode(void *state, const int *codes, int n_frames, float *
     *n_samples = got;
     return 0;
 }
+
+/* ---- the backend vtable's HIP kind (qwen_tts_backend.h:34-49) ---------------------------- */
+static void hip_backend_matvec_bf16(qwen_backend_t *b, float *y, const uint16_t *W, const float *x, int rows, int cols) {
+    qwen_hip_matvec_bf16(b->impl, y, W, x, rows, cols);
+}
+static void hip_backend_matmat_bf16(qwen_backend_t *b, float *Y, const uint16_t *W, const float *X, int rows, int cols,
+                                    int B) {
+    qwen_hip_matmat_bf16(b->impl, Y, W, X, rows, cols, B);
+}
+static void hip_backend_free(qwen_backend_t *b) {
+    if (!b) return;
+    qwen_hip_free(b->impl);
+    free(b);
+}
+
+qwen_backend_t *qwen_hip_glue_backend_new(void) {
+    if (!qwen_hip_available()) return NULL;
+    void *impl = qwen_hip_init();
+    if (!impl) return NULL;
+    qwen_backend_t *b = calloc(1, sizeof *b);
+    if (!b) { qwen_hip_free(impl); return NULL; }
+    b->kind = QWEN_BACKEND_HIP;
+    b->name = "hip";
+    b->impl = impl;
+    b->matvec_bf16 = hip_backend_matvec_bf16;
+    b->matmat_bf16 = hip_backend_matmat_bf16;
+    b->free = hip_backend_free;
+    return b;
+}

@@ -11,7 +11,21 @@
 #include <stdint.h>
 
 #include "qwen_tts.h"
+#include "qwen_tts_backend.h"
 #include "qwen_tts_hip.h"
+
+/* The HIP kind of the reference's backend vtable (qwen_tts_backend.h:28-32 lists CPU 0,
+ * METAL 1, CUDA 2): the value a maintainer adds to qwen_backend_kind_t. */
+#define QWEN_BACKEND_HIP ((qwen_backend_kind_t)3)
+
+/* What qwen_backend_init(QWEN_BACKEND_HIP) returns (qwen_tts_backend.c:106-150, the CUDA
+ * branch's shape): a qwen_backend_t of kind QWEN_BACKEND_HIP, name "hip", whose
+ * matvec_bf16 / matmat_bf16 are qwen_hip_matvec_bf16 / qwen_hip_matmat_bf16 on a
+ * qwen_hip_init() context and whose free releases both.  NULL when no HIP device is
+ * present or the context cannot be made: the caller then keeps the CPU backend, as
+ * qwen_backend_init does.  qwen_backend_install_global(b) routes qwen_matvec_bf16 (and the
+ * fused bf16 QKV matvec) and qwen_matmat_bf16 through it unchanged. */
+qwen_backend_t *qwen_hip_glue_backend_new(void);
 
 /* qwen_cuda_talker_init(ctx) (qwen_tts_cuda_talker.cu:313): the Talker layers at the
  * precision their pointers carry (q4 > int8 > bf16, qwen_tts_talker.c:587-600); a device

@@ -266,3 +266,70 @@ def _check(a, b, tag):
     r = rel_l2(a, b)
     assert r <= 1e-3, (tag, r)
     return r
+
+
+def test_backend_vtable_hip_kind_through_reference_dispatch():
+    """The HIP kind of the reference's backend vtable (qwen_tts_backend.h:34-49), as the
+    glue builds it (qwen_hip_glue_backend_new), installed with the reference's own
+    qwen_backend_install_global (qwen_tts_backend.c:157-174) and driven through the
+    reference's dispatch: qwen_matvec_bf16, the fused bf16 QKV matvec and qwen_matmat_bf16
+    (qwen_tts_kernels.c:1091-1092, 2094-2101, 1327-1328) reach the device, equal the
+    vtable's own calls to the bit, and agree with the reference's CPU path (run before the
+    install and after the uninstall) within float-order tolerance."""
+    import ctypes as C
+    print("[case] backend vtable (HIP kind) via qwen_backend_install_global", flush=True)
+    G = _glue()
+    vp, i = C.c_void_p, C.c_int
+
+    class Backend(C.Structure):
+        _fields_ = [("kind", C.c_int), ("name", C.c_char_p), ("impl", vp),
+                    ("matvec_bf16", vp), ("matmat_bf16", vp), ("free", vp)]
+
+    G.qwen_hip_glue_backend_new.restype = C.POINTER(Backend)
+    G.qwen_backend_install_global.argtypes = [C.POINTER(Backend)]
+    G.qwen_matvec_bf16.argtypes = [vp, vp, vp, i, i]
+    G.qwen_matmat_bf16.argtypes = [vp, vp, vp, i, i, i]
+    G.qwen_matvec_bf16_qkv.argtypes = [vp, vp, vp, vp, vp, vp, vp, i, i, i]
+    MV = C.CFUNCTYPE(None, C.POINTER(Backend), vp, vp, vp, i, i)
+    MM = C.CFUNCTYPE(None, C.POINTER(Backend), vp, vp, vp, i, i, i)
+    FR = C.CFUNCTYPE(None, C.POINTER(Backend))
+    b = G.qwen_hip_glue_backend_new()
+    assert b, "no HIP backend"
+    assert b.contents.kind == 3 and b.contents.name == b"hip"
+    rng = np.random.default_rng(11)
+    rows, cols, B = 1000, 2048, 7
+    W = synth.f32_to_bf16_rne((rng.standard_normal((rows, cols)) * 0.02).astype(np.float32))
+    x = rng.standard_normal(cols).astype(np.float32)
+    X = rng.standard_normal((cols, B)).astype(np.float32)
+    qd, kvd = 512, 256
+    Wq = synth.f32_to_bf16_rne((rng.standard_normal((qd, cols)) * 0.02).astype(np.float32))
+    Wk = synth.f32_to_bf16_rne((rng.standard_normal((kvd, cols)) * 0.02).astype(np.float32))
+    Wv = synth.f32_to_bf16_rne((rng.standard_normal((kvd, cols)) * 0.02).astype(np.float32))
+
+    def through_dispatch():
+        y, Y = np.empty(rows, np.float32), np.empty((rows, B), np.float32)
+        q, k, v = np.empty(qd, np.float32), np.empty(kvd, np.float32), np.empty(kvd, np.float32)
+        G.qwen_matvec_bf16(y.ctypes.data, W.ctypes.data, x.ctypes.data, rows, cols)
+        G.qwen_matmat_bf16(Y.ctypes.data, W.ctypes.data, X.ctypes.data, rows, cols, B)
+        G.qwen_matvec_bf16_qkv(q.ctypes.data, k.ctypes.data, v.ctypes.data, Wq.ctypes.data, Wk.ctypes.data,
+                               Wv.ctypes.data, x.ctypes.data, cols, qd, kvd)
+        return y, Y, q, k, v
+
+    cpu = through_dispatch()                          # no hook: the reference's CPU kernels
+    try:
+        y_vt, Y_vt = np.empty(rows, np.float32), np.empty((rows, B), np.float32)
+        MV(b.contents.matvec_bf16)(b, y_vt.ctypes.data, W.ctypes.data, x.ctypes.data, rows, cols)
+        MM(b.contents.matmat_bf16)(b, Y_vt.ctypes.data, W.ctypes.data, X.ctypes.data, rows, cols, B)
+        G.qwen_backend_install_global(b)
+        dev = through_dispatch()
+    finally:
+        G.qwen_backend_install_global(None)
+    again = through_dispatch()                        # uninstalled: the CPU path again
+    FR(b.contents.free)(b)
+    assert np.array_equal(dev[0], y_vt) and np.array_equal(dev[1], Y_vt)
+    for a, c in zip(again, cpu):
+        assert np.array_equal(a, c)
+    for got, want in zip(dev, cpu):
+        err = rel_l2(got, want)
+        print(f"[result] vtable dispatch vs reference CPU: rel-L2 {err:.2e}")
+        assert err <= 1e-5
