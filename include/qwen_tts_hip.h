@@ -128,6 +128,17 @@ void *qwen_hip_talker_stream(void *state);
  * persistent kernel, 0 when they run as the per-kernel sequence (shapes or devices the
  * fused kernel does not cover), -1 for a NULL state. */
 int   qwen_hip_talker_fused(void *state);
+/* replaces kv_cache_grow(ctx, required) (qwen_tts_talker.c:257-280): the device KV cache's
+ * capacity doubles until it holds `required` positions (at most 8192, and within the rope
+ * table given at init); the rows are copied on the device and the decode keeps its fused
+ * kernel.  0 when the capacity already suffices or after growing, -1 with
+ * qwen_hip_last_error() set otherwise.  The step, prefill, upload and loop entry points
+ * grow the cache themselves when their positions need it (as qwen_talker_step does before
+ * its step, qwen_tts_talker.c:574, and qwen_talker_prefill, :773), so a caller only needs
+ * this to grow ahead of time. */
+int   qwen_hip_talker_grow_kv(void *state, int required);
+/* the device KV cache's current capacity in positions (-1 for a NULL state) */
+int   qwen_hip_talker_kv_max(void *state);
 /* Diagnostic query (no reference counterpart): which fused kernel runs the steps —
  * 2 the role-specialised persistent kernel (qt_rstep.hip), 1 the single-role persistent
  * kernel (qt_pstep.hip), 0 the per-kernel sequence, -1 for a NULL state. */

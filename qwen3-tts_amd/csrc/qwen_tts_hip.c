@@ -183,6 +183,8 @@ static void stack_free(stack_t *s) {
     memset(s, 0, sizeof *s);
 }
 
+#define KV_LIMIT 8192   /* the largest cache the attention grid covers (qt_attn_grid) */
+
 static int stack_init(stack_t *s, const qwen_hip_talker_desc_t *d, hipStream_t st) {
     void *tmp = NULL;
     memset(s, 0, sizeof *s);
@@ -199,7 +201,8 @@ static int stack_init(stack_t *s, const qwen_hip_talker_desc_t *d, hipStream_t s
     REQ(s->prec == d->prec || d->prec == QWEN_HIP_BF16, "quantize_to needs bf16 source weights");
     if (s->prec == QWEN_HIP_Q4_0)
         REQ(s->H % 32 == 0 && s->F % 32 == 0 && s->qd % 32 == 0, "q4_0 needs dims divisible by 32");
-    s->rope_len = d->rope_len < d->kv_max ? d->rope_len : d->kv_max;
+    /* the whole rope table (up to the largest cache), so that the KV cache can grow */
+    s->rope_len = d->rope_len < KV_LIMIT ? d->rope_len : KV_LIMIT;
     /* split-K grid: short caches (the CP's <= 64 positions) use one chunk per kv head */
     s->attn_G = s->kv_max <= 128 ? 1 : qt_attn_grid(s->kv_max);
     s->step_G = s->attn_G;
@@ -439,6 +442,82 @@ static int ps_check(talker_t *t) {
     return 0;
 }
 
+/* ---- KV capacity growth (kv_cache_grow, qwen_tts_talker.c:257-280) -------------------------
+ * The capacity doubles until it holds `required` positions (at most KV_LIMIT); the cache is
+ * copied into the larger one on the device (one strided copy each for K and V: the rows of
+ * one (layer, kv head) are contiguous), the attention split follows the new capacity, the
+ * captured graphs are dropped (they hold the old cache), and the fused step keeps running:
+ * past the role-specialised kernel's capacity the single-role persistent kernel takes over,
+ * with the same device position, step tag and next input. */
+static int ps_reselect(talker_t *t) {
+    stack_t *s = &t->s;
+    if (rstep_enabled() && qt_rstep_supported(s->prec, s->H, s->F, s->nh, s->nkv, s->hd, s->kv_max, s->L)) {
+        s->step_G = qt_rstep_chunks();
+        s->step_onepass = 1;
+        return 0;
+    }
+    /* both fused kernels cover the same shapes, and the single-role one every capacity */
+    REQ(persistent_enabled() && qt_pstep_supported(s->prec, s->H, s->F, s->nh, s->nkv, s->hd, s->kv_max),
+        "no fused kernel for a cache of %d positions", s->kv_max);
+    if (t->rs_on) {
+        /* tags carry over: ring words start at tag 0, older than any step's */
+        const size_t words = qt_pstep_ring_words(s->H, s->F, s->L);
+        (void)hipFree(t->rs_reg); (void)hipFree(t->rs_slots); (void)hipFree(t->ps_ring);
+        t->rs_reg = NULL; t->rs_slots = NULL; t->ps_ring = NULL; t->rs_on = 0;
+        HCK(hipMalloc((void **)&t->ps_ring, words * sizeof(unsigned long long)));
+        HCK(hipMemsetAsync(t->ps_ring, 0, words * sizeof(unsigned long long), t->st));
+        HCK(hipStreamSynchronize(t->st));
+    }
+    return 0;
+fail:
+    return -1;
+}
+
+static int talker_grow_kv(talker_t *t, int required) {
+    stack_t *s = &t->s;
+    uint16_t *nk = NULL, *nv = NULL;
+    float *npart = NULL;
+    if (required <= s->kv_max) return 0;
+    REQ(required <= KV_LIMIT, "a KV cache of %d positions exceeds %d", required, KV_LIMIT);
+    REQ(required <= s->rope_len, "position %d is past the rope table (%d positions)", required - 1, s->rope_len);
+    int nm = s->kv_max;
+    while (nm < required) nm *= 2;
+    if (nm > KV_LIMIT) nm = KV_LIMIT;
+    HCK(hipStreamSynchronize(t->st));
+    const size_t rows = (size_t)s->L * s->nkv, opitch = (size_t)s->kv_max * s->hd * 2, npitch = (size_t)nm * s->hd * 2;
+    HCK(hipMalloc((void **)&nk, rows * npitch));
+    HCK(hipMalloc((void **)&nv, rows * npitch));
+    HCK(hipMemsetAsync(nk, 0, rows * npitch, t->st));
+    HCK(hipMemsetAsync(nv, 0, rows * npitch, t->st));
+    HCK(hipMemcpy2DAsync(nk, npitch, s->kc, opitch, opitch, rows, hipMemcpyDeviceToDevice, t->st));
+    HCK(hipMemcpy2DAsync(nv, npitch, s->vc, opitch, opitch, rows, hipMemcpyDeviceToDevice, t->st));
+    const int G = nm <= 128 ? 1 : qt_attn_grid(nm);
+    if (G != s->attn_G)
+        HCK(hipMalloc((void **)&npart, (size_t)s->nkv * G * (s->nh / s->nkv) * 130 * sizeof(float)));
+    HCK(hipStreamSynchronize(t->st));
+    (void)hipFree(s->kc); (void)hipFree(s->vc);
+    s->kc = nk; s->vc = nv; nk = nv = NULL;
+    if (npart) { (void)hipFree(s->part); s->part = npart; npart = NULL; }
+    s->kv_max = nm; s->attn_G = G; s->step_G = G; s->step_onepass = 0;
+    if (s->kv_stage) { (void)hipFree(s->kv_stage); s->kv_stage = NULL; }
+    if (t->graph_ready) { (void)hipGraphExecDestroy(t->exec); t->graph_ready = 0; }
+    if (t->ggraph_ready) { (void)hipGraphExecDestroy(t->gexec); t->ggraph_ready = 0; }
+    if (t->ps_on && ps_reselect(t) != 0) { t->dead = 1; return -1; }
+    return 0;
+fail:
+    if (nk) (void)hipFree(nk);
+    if (nv) (void)hipFree(nv);
+    if (npart) (void)hipFree(npart);
+    return -1;
+}
+
+int qwen_hip_talker_grow_kv(void *state, int required) {
+    talker_t *t = (talker_t *)state;
+    if (!t || t->dead) { SETERR("talker state is dead or NULL"); return -1; }
+    return talker_grow_kv(t, required);
+}
+int qwen_hip_talker_kv_max(void *state) { return state ? ((talker_t *)state)->s.kv_max : -1; }
+
 void *qwen_hip_talker_init(const qwen_hip_talker_desc_t *desc) {
     talker_t *t = calloc(1, sizeof *t);
     if (!t) { SETERR("out of host memory"); return NULL; }
@@ -534,6 +613,7 @@ fail:
 static int talker_step_impl(talker_t *t, const float *embed, float *hidden_out, int pos, int use_graph) {
     if (!t || t->dead) { SETERR("talker state is dead or NULL"); return -1; }
     const int H = t->s.H;
+    if (pos >= 0 && talker_grow_kv(t, pos + 1) != 0) return -1;   /* qwen_talker_step grows first (t.c:574) */
     REQ(pos >= 0 && pos < t->s.kv_max && pos < t->s.rope_len, "pos %d out of range (kv_max %d, rope %d)",
         pos, t->s.kv_max, t->s.rope_len);
     if (talker_set_pos(t, pos) != 0) goto fail;
@@ -597,6 +677,7 @@ int qwen_hip_talker_step_layers(void *state, const float *embed, float *residual
     if (!embed || !residuals) { SETERR("null argument"); return -1; }
     stack_t *s = &t->s;
     const int H = s->H, L = s->L;
+    if (pos >= 0 && talker_grow_kv(t, pos + 1) != 0) return -1;
     if (pos < 0 || pos >= s->kv_max || pos >= s->rope_len) { SETERR("pos %d out of range", pos); return -1; }
     if (talker_set_pos(t, pos) != 0) goto fail;
     memcpy(t->h_in, embed, (size_t)H * sizeof(float));
@@ -661,6 +742,7 @@ int qwen_hip_talker_upload_kv(void *state, const uint16_t *kv_k, const uint16_t 
     if (!t || t->dead) { SETERR("talker state is dead or NULL"); return -1; }
     stack_t *s = &t->s;
     if (prefill_len <= 0) return 0;
+    if (prefill_len <= host_kv_max && talker_grow_kv(t, prefill_len) != 0) return -1;
     REQ(prefill_len <= s->kv_max && prefill_len <= host_kv_max, "prefill_len %d exceeds kv_max", prefill_len);
     REQ(kv_k && kv_v, "null KV");
     if (!s->kv_stage) HCK(hipMalloc((void **)&s->kv_stage, (size_t)s->kv_max * s->kvd * sizeof(uint16_t)));
@@ -799,6 +881,7 @@ int qwen_hip_talker_prefill(void *state, const qwen_hip_layer_t *bf16_layers, co
     const int H = s->H, F = s->F, qd = s->qd, qkvr = s->qd + 2 * s->kvd;
     /* argument errors leave the state usable */
     if (!embeds) { SETERR("null embeds"); return -1; }
+    if (seq >= 1 && seq <= s->rope_len && talker_grow_kv(t, seq) != 0) return -1;   /* t.c:773 */
     if (seq < 1 || seq > s->kv_max || seq > s->rope_len) {
         SETERR("seq %d out of range (1..%d)", seq, s->kv_max < s->rope_len ? s->kv_max : s->rope_len);
         return -1;
@@ -915,6 +998,7 @@ int qwen_hip_talker_greedy(void *state, const uint16_t *codec_head, const uint16
     REQ(n_steps >= 0 && n_steps <= t->hist_len, "n_steps %d out of range", n_steps);
     REQ(frame0 >= 0, "frame0 %d must be >= 0", frame0);
     REQ(tokens_out || n_steps == 0, "null tokens_out");
+    if (pos >= 0 && talker_grow_kv(t, pos + n_steps) != 0) return -1;
     REQ(pos >= 0 && pos + n_steps <= t->s.kv_max && pos + n_steps <= t->s.rope_len, "positions exceed kv_max");
     if (head_setup(t, codec_head, codec_emb, codec_vocab) != 0) goto fail;
     if (talker_set_pos(t, pos) != 0) goto fail;
@@ -978,6 +1062,7 @@ int qwen_hip_talker_sample(void *state, const uint16_t *codec_head, const uint16
     if ((long long)n_prev + n_steps + 1 > QT_SAMPLE_HIST_MAX) {
         SETERR("talker_sample: history of %d + %d tokens exceeds %d", n_prev, n_steps, QT_SAMPLE_HIST_MAX - 1); return -1;
     }
+    if (pos >= 0 && talker_grow_kv(t, pos + n_steps) != 0) return -1;
     if (pos < 0 || pos + n_steps > t->s.kv_max || pos + n_steps > t->s.rope_len) {
         SETERR("talker_sample: positions exceed kv_max"); return -1;
     }
@@ -1038,11 +1123,16 @@ fail:
 int qwen_hip_talker_greedy_async(void *state, int n_steps) {
     talker_t *t = (talker_t *)state;
     if (!t || t->dead || !t->greedy_ready) { SETERR("greedy loop not initialised"); return -1; }
+    if (t->dev_pos >= 0 && talker_grow_kv(t, t->dev_pos + n_steps) != 0) return -1;
     REQ(t->dev_pos >= 0 && t->dev_pos + n_steps <= t->s.kv_max && t->dev_pos + n_steps <= t->s.rope_len,
         "positions exceed kv_max");
     if (t->greedy_ready == 2) {
         if (n_steps > 0) HCK(ps_launch(t, n_steps, 1));
     } else {
+        if (graphs_enabled() && !t->ggraph_ready) {       /* dropped when the cache grew */
+            if (capture(t->st, &t->gexec, greedy_body, t) != 0) goto fail;
+            t->ggraph_ready = 1;
+        }
         for (int i = 0; i < n_steps; i++) HCK(graphs_enabled() ? hipGraphLaunch(t->gexec, t->st) : greedy_body(t));
     }
     t->dev_pos += n_steps;
@@ -1473,6 +1563,7 @@ int qwen_hip_generate(void *talker_state, void *cp_state, const uint16_t *codec_
     if ((long long)n_prev + n_frames + 1 > QT_SAMPLE_HIST_MAX) {
         SETERR("generate: history of %d + %d tokens exceeds %d", n_prev, n_frames, QT_SAMPLE_HIST_MAX - 1); return -1;
     }
+    if (pos >= 0 && talker_grow_kv(t, pos + n_frames) != 0) return -1;
     if (pos < 0 || pos + n_frames > t->s.kv_max || pos + n_frames > t->s.rope_len) {
         SETERR("generate: positions exceed kv_max"); return -1;
     }
@@ -1564,7 +1655,7 @@ fail:
 
 typedef struct {
     const stack_t *s;          /* borrowed weights / norms / rope tables */
-    int B, Bp, kv_max, is_cp;
+    int B, Bp, kv_max, is_cp, attn_G;
     hipStream_t st;
     uint16_t *kc, *vc;         /* [B][L][nkv][kv_max][hd] */
     float *x, *qkv, *attn, *h, *hid;
@@ -1633,7 +1724,8 @@ static batch_t *batch_create(const stack_t *s, int B, int is_cp) {
             HCK(hipMemsetAsync(bt->g2_cnt, 0, (size_t)cmax * sizeof(unsigned), bt->st));
         }
     }
-    HCK(hipMalloc((void **)&bt->part, (size_t)B * s->nkv * s->attn_G * (s->nh / s->nkv) * 130 * sizeof(float)));
+    bt->attn_G = s->attn_G;      /* its own: the single state's may change when its cache grows */
+    HCK(hipMalloc((void **)&bt->part, (size_t)B * s->nkv * bt->attn_G * (s->nh / s->nkv) * 130 * sizeof(float)));
     HCK(hipMalloc((void **)&bt->cnt, (size_t)B * s->nkv * sizeof(unsigned)));
     HCK(hipMemsetAsync(bt->cnt, 0, (size_t)B * s->nkv * sizeof(unsigned), bt->st));
     HCK(hipMalloc((void **)&bt->d_pos, (size_t)B * sizeof(int)));
@@ -1688,8 +1780,8 @@ static hipError_t batch_body(void *arg) {
         } else if ((e = batch_proj(bt, &s->qkv[l], QT_EPI_STORE, s->in_norm[l], bt->x, H, bt->qkv, QKV))) return e;
         if ((e = qt_launch_attn_b(bt->qkv, QKV, s->qn[l], s->kn[l], s->rope_cos, s->rope_sin, s->eps, bt->d_pos,
                                   bt->kc + lay, bt->vc + lay, per, s->hd, (long long)s->kv_max * s->hd, s->nh, s->nkv,
-                                  s->hd, scale, bt->part, (long long)s->nkv * s->attn_G * (s->nh / s->nkv) * 130,
-                                  bt->cnt, s->attn_G, bt->attn, s->qd, bt->B, bt->st))) return e;
+                                  s->hd, scale, bt->part, (long long)s->nkv * bt->attn_G * (s->nh / s->nkv) * 130,
+                                  bt->cnt, bt->attn_G, bt->attn, s->qd, bt->B, bt->st))) return e;
         if (fused) {
             if ((e = qt_launch_pf_pieces(bt->attn, s->qd, bt->B, s->qd, NULL, 0.f, bt->pf_p, bt->st))) return e;
             if ((e = qt_launch_pf_gemm_resid_planes((const uint16_t *)s->o[l].w, bt->pf_p, bt->B, H, s->qd, bt->x, H,

@@ -21,7 +21,7 @@ EXPORTS = [
     "qwen_hip_talker_init", "qwen_hip_talker_step", "qwen_hip_talker_get_dec_x",
     "qwen_hip_talker_upload_kv", "qwen_hip_talker_free", "qwen_hip_talker_download_kv",
     "qwen_hip_talker_greedy", "qwen_hip_talker_greedy_async", "qwen_hip_talker_sync",
-    "qwen_hip_talker_stream", "qwen_hip_talker_fused", "qwen_hip_talker_fused_kernel", "qwen_hip_talker_step_nograph", "qwen_hip_talker_launch_kernel", "qwen_hip_cp_init", "qwen_hip_cp_step",
+    "qwen_hip_talker_stream", "qwen_hip_talker_fused", "qwen_hip_talker_fused_kernel", "qwen_hip_talker_grow_kv", "qwen_hip_talker_kv_max", "qwen_hip_talker_step_nograph", "qwen_hip_talker_launch_kernel", "qwen_hip_cp_init", "qwen_hip_cp_step",
     "qwen_hip_cp_frame", "qwen_hip_cp_frame_async", "qwen_hip_cp_sync", "qwen_hip_cp_stream",
     "qwen_hip_cp_free", "qwen_hip_available", "qwen_hip_init", "qwen_hip_free", "qwen_hip_matvec_bf16",
     "qwen_hip_matmat_bf16", "qwen_hip_op_matvec_int8", "qwen_hip_op_matvec_q4_0",
@@ -113,6 +113,8 @@ def lib():
         L.qwen_hip_talker_stream.argtypes = [vp]; L.qwen_hip_talker_stream.restype = vp
         L.qwen_hip_talker_fused.argtypes = [vp]; L.qwen_hip_talker_fused.restype = i
         L.qwen_hip_talker_fused_kernel.argtypes = [vp]; L.qwen_hip_talker_fused_kernel.restype = i
+        L.qwen_hip_talker_grow_kv.argtypes = [vp, i]; L.qwen_hip_talker_grow_kv.restype = i
+        L.qwen_hip_talker_kv_max.argtypes = [vp]; L.qwen_hip_talker_kv_max.restype = i
         L.qwen_hip_talker_launch_kernel.argtypes = [vp, i, i, i]; L.qwen_hip_talker_launch_kernel.restype = i
         L.qwen_hip_talker_dequant.argtypes = [vp, i, i, i, i, vp]; L.qwen_hip_talker_dequant.restype = i
         L.qwen_hip_cp_init.argtypes = [C.POINTER(CpDesc)]; L.qwen_hip_cp_init.restype = vp
