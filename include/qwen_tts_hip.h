@@ -224,6 +224,10 @@ int   qwen_hip_cp_sync(void *state);
 void *qwen_hip_cp_stream(void *state);
 /* replaces qwen_cuda_cp_free                     (qwen_tts_cuda_talker.cu:917) */
 void  qwen_hip_cp_free(void *state);
+/* Diagnostic (no reference counterpart; what the reference keeps in ctx->cp_kv_k/cp_kv_v
+ * after qwen_cp_predict, qwen_tts_code_predictor.c:926-1045): positions [0, n) of the CP's
+ * device KV cache into host bf16 [cp_layers][host_kv_max][kv_heads*head_dim]. */
+int   qwen_hip_cp_download_kv(void *state, uint16_t *kv_k, uint16_t *kv_v, int host_kv_max, int n);
 /* two-position prefill, twin of cp_prefill2 (qwen_tts_code_predictor.c:816-902) and of
  * its switch cp_prefill2_mode / QWEN_CP_PREFILL2 (:783-807).  set_prefill2(state, 1)
  * needs int8 weights in every CP layer (the reference: quantized CP only) and makes

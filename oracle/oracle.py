@@ -392,6 +392,10 @@ class RefModel:
         return (self._view(self.lib.ref_cp_kv_k(self.h), np.uint16, n).reshape(s.cp_layers, kvm, kvd),
                 self._view(self.lib.ref_cp_kv_v(self.h), np.uint16, n).reshape(s.cp_layers, kvm, kvd))
 
+    def cp_dec_x(self):
+        """The CP residual after the last pass of the last qwen_cp_predict (ctx->cp_dec_x)."""
+        return self._view(self.lib.ref_cp_dec_x(self.h), np.float32, self.shape.cp_hidden).copy()
+
     def cp_predict(self, talker_hidden, code0):
         out = (C.c_int * 15)()
         rc = self.lib.ref_cp_predict(self.h, _p(np.ascontiguousarray(talker_hidden, np.float32)), code0, out)

@@ -757,23 +757,27 @@ fail:
     return -1;
 }
 
-int qwen_hip_talker_download_kv(void *state, uint16_t *kv_k, uint16_t *kv_v, int host_kv_max, int n) {
-    talker_t *t = (talker_t *)state;
-    if (!t) { SETERR("NULL state"); return -1; }
-    stack_t *s = &t->s;
+/* positions [0, n) of a stack's cache into the host layout [L][host_kv_max][n_kv * hd] */
+static int stack_download_kv(stack_t *s, hipStream_t st, uint16_t *kv_k, uint16_t *kv_v, int host_kv_max, int n) {
     REQ(n >= 0 && n <= s->kv_max && n <= host_kv_max, "n %d out of range", n);
     if (n == 0) return 0;
     REQ(kv_k && kv_v, "null KV");
     if (!s->kv_stage) HCK(hipMalloc((void **)&s->kv_stage, (size_t)s->kv_max * s->kvd * sizeof(uint16_t)));
     for (int l = 0; l < s->L; l++) {
         const size_t lay = (size_t)l * s->nkv * s->kv_max * s->hd, dst = (size_t)l * host_kv_max * s->kvd;
-        HCK(kv_xfer(s->kc + lay, s->kv_max, kv_k + dst, n, s->nkv, s->hd, 0, s->kv_stage, t->st));
-        HCK(kv_xfer(s->vc + lay, s->kv_max, kv_v + dst, n, s->nkv, s->hd, 0, s->kv_stage, t->st));
+        HCK(kv_xfer(s->kc + lay, s->kv_max, kv_k + dst, n, s->nkv, s->hd, 0, s->kv_stage, st));
+        HCK(kv_xfer(s->vc + lay, s->kv_max, kv_v + dst, n, s->nkv, s->hd, 0, s->kv_stage, st));
     }
-    HCK(hipStreamSynchronize(t->st));
+    HCK(hipStreamSynchronize(st));
     return 0;
 fail:
     return -1;
+}
+
+int qwen_hip_talker_download_kv(void *state, uint16_t *kv_k, uint16_t *kv_v, int host_kv_max, int n) {
+    talker_t *t = (talker_t *)state;
+    if (!t) { SETERR("NULL state"); return -1; }
+    return stack_download_kv(&t->s, t->st, kv_k, kv_v, host_kv_max, n);
 }
 
 /* -- Talker prefill (qwen_talker_prefill, qwen_tts_talker.c:730-1038) ------------------ */
@@ -1296,6 +1300,14 @@ fail:
     if (tmp) (void)hipFree(tmp);
     cp_destroy(c);
     return NULL;
+}
+
+/* the CP cache after a frame or passes: positions [0, n) as the reference keeps
+ * ctx->cp_kv_k / cp_kv_v ([layer][cp_kv_max][kv_dim]) */
+int qwen_hip_cp_download_kv(void *state, uint16_t *kv_k, uint16_t *kv_v, int host_kv_max, int n) {
+    cp_t *c = (cp_t *)state;
+    if (!c) { SETERR("NULL state"); return -1; }
+    return stack_download_kv(&c->s, c->st, kv_k, kv_v, host_kv_max, n);
 }
 
 void qwen_hip_cp_free(void *state) { cp_destroy((cp_t *)state); }

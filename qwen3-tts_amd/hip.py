@@ -21,7 +21,7 @@ EXPORTS = [
     "qwen_hip_talker_init", "qwen_hip_talker_step", "qwen_hip_talker_get_dec_x",
     "qwen_hip_talker_upload_kv", "qwen_hip_talker_free", "qwen_hip_talker_download_kv",
     "qwen_hip_talker_greedy", "qwen_hip_talker_greedy_async", "qwen_hip_talker_sync",
-    "qwen_hip_talker_stream", "qwen_hip_talker_fused", "qwen_hip_talker_fused_kernel", "qwen_hip_talker_grow_kv", "qwen_hip_talker_kv_max", "qwen_hip_talker_step_nograph", "qwen_hip_talker_launch_kernel", "qwen_hip_cp_init", "qwen_hip_cp_step",
+    "qwen_hip_talker_stream", "qwen_hip_talker_fused", "qwen_hip_talker_fused_kernel", "qwen_hip_talker_grow_kv", "qwen_hip_talker_kv_max", "qwen_hip_talker_step_nograph", "qwen_hip_talker_launch_kernel", "qwen_hip_cp_init", "qwen_hip_cp_step", "qwen_hip_cp_download_kv",
     "qwen_hip_cp_frame", "qwen_hip_cp_frame_async", "qwen_hip_cp_sync", "qwen_hip_cp_stream",
     "qwen_hip_cp_free", "qwen_hip_available", "qwen_hip_init", "qwen_hip_free", "qwen_hip_matvec_bf16",
     "qwen_hip_matmat_bf16", "qwen_hip_op_matvec_int8", "qwen_hip_op_matvec_q4_0",
@@ -119,6 +119,7 @@ def lib():
         L.qwen_hip_talker_dequant.argtypes = [vp, i, i, i, i, vp]; L.qwen_hip_talker_dequant.restype = i
         L.qwen_hip_cp_init.argtypes = [C.POINTER(CpDesc)]; L.qwen_hip_cp_init.restype = vp
         L.qwen_hip_cp_step.argtypes = [vp, vp, i]; L.qwen_hip_cp_step.restype = i
+        L.qwen_hip_cp_download_kv.argtypes = [vp, vp, vp, i, i]; L.qwen_hip_cp_download_kv.restype = i
         L.qwen_hip_cp_frame.argtypes = [vp, vp, i, vp]; L.qwen_hip_cp_frame.restype = i
         L.qwen_hip_cp_frame_async.argtypes = [vp, i]; L.qwen_hip_cp_frame_async.restype = i
         L.qwen_hip_cp_sync.argtypes = [vp]; L.qwen_hip_cp_sync.restype = i
@@ -486,6 +487,14 @@ class CodePredictor:
         x = np.array(x, np.float32, copy=True)
         check(lib().qwen_hip_cp_step(self.h, _p(x), pos), "cp_step")
         return x
+
+    def download_kv(self, n):
+        """Positions [0, n) of the CP cache as host bf16 [cp_layers][n][kv_dim]."""
+        L, kvd = self.desc.cp.n_layers, self.desc.cp.n_kv_heads * self.desc.cp.head_dim
+        k = np.zeros((L, n, kvd), np.uint16)
+        v = np.zeros_like(k)
+        check(lib().qwen_hip_cp_download_kv(self.h, _p(k), _p(v), n, n), "cp_download_kv")
+        return k, v
 
     def set_prefill2(self, on):
         """Frames start with the two-position pass (int8 CP weights only)."""

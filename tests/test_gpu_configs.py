@@ -257,6 +257,41 @@ def test_config3_1p7b_q4_kv(L0, n_greedy):
 
 # --------------------------------------------------------------- config 4 (CP, 5 layers)
 
+def _bf16_units(a, b):
+    """Distance between bf16 bit patterns in representable values (adjacent values: 1)."""
+    def line(x):
+        x = x.astype(np.int32)
+        return np.where(x & 0x8000, -(x & 0x7FFF), x)
+    return np.abs(line(a) - line(b))
+
+
+def _kv_check(dk, rk, where):
+    """A CP cache against the reference's, [layer][position][kv_dim] bf16: the row of
+    layer 0, position 0 (made from identical inputs: only the matvec's summation order
+    differs) within one bf16 unit elementwise; every (layer, position) row within rel-L2
+    2^-8 (one bf16 unit, relative) and max-abs 2^-7 times its largest magnitude (two units
+    there: K rows after the per-head norm and RoPE reach magnitudes where one unit is
+    3e-2, past the 2e-2 absolute bar of the f32 hidden states).  The stored values are truncated to
+    bf16, so wherever two f32 paths straddle a truncation boundary an element differs by a
+    whole unit (2^-8 relative); those paths sum in different orders, drift apart over the
+    passes and layers, and near zero an element then differs by many units.  Returns
+    (worst row rel-L2, fraction of elements more than one unit apart)."""
+    u = _bf16_units(dk, rk)
+    assert u[0, 0].max() <= 1, (where, _kv_where(u, dk, rk))
+    a, b = synth.bf16_to_f32(dk).astype(np.float64), synth.bf16_to_f32(rk).astype(np.float64)
+    rows = np.sqrt(((a - b) ** 2).sum(-1) / np.maximum((b ** 2).sum(-1), 1e-30))
+    big = np.abs(a - b).max(-1) / np.maximum(np.abs(b).max(-1), 1e-30)
+    assert rows.max() <= 2.0 ** -8 and big.max() <= 2.0 ** -7, (where, float(rows.max()), float(big.max()))
+    return float(rows.max()), float((u > 1).mean())
+
+
+def _kv_where(u, dev, ref):
+    """Where two caches differ most: (layer, position, element, device value, reference value)."""
+    l, p, e = np.unravel_index(int(np.argmax(u)), u.shape)
+    f = lambda v: float(synth.bf16_to_f32(np.array([v], np.uint16))[0])  # noqa: E731
+    return int(l), int(p), int(e), f(dev[l, p, e]), f(ref[l, p, e]), int((u > 1).sum())
+
+
 def _gpu_cp(ref, prec_code):
     from test_gpu_parity import _gpu_cp as mk
     return mk(ref, ref.shape, prec_code)
@@ -272,13 +307,22 @@ def test_config4_cp_frames(name, prec):
     assert s.cp_layers == 5
     cp = _gpu_cp(ref, hip.PREC[prec])
     rng = np.random.default_rng(0x5EED0005)
+    worst_kv, worst_fr = 0.0, 0.0
     for f in range(16):
         th = rng.standard_normal(s.hidden).astype(np.float32)
         th /= np.sqrt((th ** 2).mean())
         code0 = int(rng.integers(0, 2048))
         want = ref.cp_predict(th, code0)
+        rk, rv = (x[:, :16].copy() for x in ref.cp_kv())
         got = cp.frame(th, code0)
         assert list(got) == list(want), (f, list(got), list(want))
+        # every pass's K/V rows at every layer, within one bf16 unit of the reference's
+        dk, dv = cp.download_kv(16)
+        for (rr, fr) in (_kv_check(dk, rk, ("K", f)), _kv_check(dv, rv, ("V", f))):
+            worst_kv, worst_fr = max(worst_kv, rr), max(worst_fr, fr)
+    print(f"[result] config 4 {name} {prec}: 16 frames identical; CP K/V (5 layers x 16 positions) vs the "
+          f"reference: worst row rel-L2 {worst_kv:.1e}, at most {100 * worst_fr:.2f} % of elements more than one "
+          f"bf16 unit apart", flush=True)
     cp.free()
 
 
@@ -286,14 +330,15 @@ def test_config4_cp_step_hook():
     """The per-pass hook (qwen_hip_cp_step, the drop-in at qwen_tts_code_predictor.c:742-747)
     driving the reference's frame loop from the host: each of the 16 passes on the device,
     the cp_norm + lm-head argmax and the embedding lookups with the reference's own
-    kernels; the 15 codes must be those of qwen_cp_predict, and every pass's residual
-    within max-abs 2e-2 and rel-L2 3e-3 of the oracle's pass (the oracle's CP pass is
-    pinned to the reference by the frame tests).  The rel-L2 bar is looser than the
-    Talker's 1e-3 because a CP pass attends over at most 16 keys: where two f32 paths
-    straddle a bf16 truncation boundary of a K/V element (the reference and the f32
-    oracle disagree on 4-12 % of the CP's K elements over a frame, and their final
-    residuals by up to 6e-4 rel-L2, measured on these weights), few keys average the
-    one-unit difference away, so it shows in the pass output (1.4e-3 observed at pass 1)."""
+    kernels.  Against the compiled reference after its qwen_cp_predict of the same frame:
+    the 15 codes identical; every pass's K/V rows at every layer (ctx->cp_kv_k / cp_kv_v, 5
+    layers x 16 positions: each is a projection of that pass's normed residual at that
+    layer) as _kv_check holds them; the last pass's residual (ctx->cp_dec_x) within max-abs
+    2e-2 and rel-L2 1e-3.  The reference keeps its per-pass residuals internal
+    (cp_transformer_step is static), so every pass's residual is also held against the
+    oracle's pass, at rel-L2 3e-3: a CP pass attends over at most 16 keys, and where two f32
+    paths straddle a bf16 truncation boundary of a K/V element (one unit, as above) few keys
+    average the difference away (1.4e-3 observed at pass 1)."""
     print("[case] config 4: qwen_hip_cp_step hook, 0.6B bf16", flush=True)
     from oracle.oracle import Oracle, RefModel, oracle_talker
     ref, s = _ref("0.6B", "bf16")
@@ -304,12 +349,14 @@ def test_config4_cp_step_hook():
     emb = ref.codec_emb()
     cnorm = ref.cp_norm()
     rng = np.random.default_rng(0x5EED0006)
-    worst = 0.0
+    worst, worst_dx, worst_kv, worst_fr = 0.0, 0.0, 0.0, 0.0
     for f in range(3):
         th = rng.standard_normal(s.hidden).astype(np.float32)
         th /= np.sqrt((th ** 2).mean())
         code0 = int(rng.integers(0, 2048))
         want = ref.cp_predict(th, code0)
+        rk, rv = (a[:, :16].copy() for a in ref.cp_kv())
+        rdx = ref.cp_dec_x()
         codes = []
         x = th.copy()                                   # no mtp projection at 0.6B
         xo = th.copy()
@@ -330,7 +377,17 @@ def test_config4_cp_step_hook():
                 lm = ref.cp_lm_head(p - 1)["bf16"]
                 codes.append(int(R.ref_argmax_matvec_bf16(xn.ctypes.data, lm.ctypes.data, s.cp_hidden, s.codebook)))
         assert codes == list(want), (f, codes, list(want))
-    print(f"[result] cp_step hook: codes identical for 3 frames, worst pass rel-L2 vs oracle {worst:.2e}", flush=True)
+        r = rel_l2(x, rdx)
+        worst_dx = max(worst_dx, r)
+        print(f"[result] frame {f}: last residual vs the reference's cp_dec_x rel-L2 {r:.2e}, "
+              f"max-abs {np.abs(x - rdx).max():.1e}", flush=True)
+        assert r <= 1e-3 and np.abs(x - rdx).max() <= 2e-2, (f, r)
+        dk, dv = cp.download_kv(16)
+        for (rr, fr) in (_kv_check(dk, rk, ("K", f)), _kv_check(dv, rv, ("V", f))):
+            worst_kv, worst_fr = max(worst_kv, rr), max(worst_fr, fr)
+    print(f"[result] cp_step hook: codes identical for 3 frames; K/V of every pass and layer vs the reference: worst "
+          f"row rel-L2 {worst_kv:.1e} ({100 * worst_fr:.2f} % of elements more than one bf16 unit apart); last "
+          f"residual vs the reference's cp_dec_x rel-L2 {worst_dx:.2e}; worst pass vs oracle {worst:.2e}", flush=True)
     cp.free()
 
 
