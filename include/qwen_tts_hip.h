@@ -176,6 +176,11 @@ void *qwen_hip_talker_batch_init(void *single, int B);
  * embeds host f32[B][hidden], pos_arr host int[B] (each stream's position: its KV row
  * written, RoPE and causal length pos+1), hidden_out host f32[B][hidden] final-normed. */
 int   qwen_hip_talker_batch_step(void *state, const float *embeds, const int *pos_arr, float *hidden_out);
+/* Diagnostic (no reference counterpart; the batched twin of qwen_hip_talker_step_layers):
+ * one batched step run without graph capture that also returns every stream's residual after
+ * every layer, residuals host f32[n_layers][B][hidden].  Allocates a temporary device buffer. */
+int   qwen_hip_talker_batch_step_layers(void *state, const float *embeds, const int *pos_arr, float *residuals,
+                                        float *hidden_out);
 /* replaces qwen_cuda_talker_batch_upload_slot           (qwen_tts_cuda_talker.cu:629):
  * seeds slot b's device KV from the batch engine's host bf16 caches laid out
  * ((b*n_layers + l)*src_kv_max + pos)*kv_dim (qwen_tts_batch.h:26-27). */

@@ -1668,6 +1668,7 @@ fail:
 typedef struct {
     const stack_t *s;          /* borrowed weights / norms / rope tables */
     int B, Bp, kv_max, is_cp, attn_G;
+    float *layer_out;          /* diagnostic (ungraphed steps only): every layer's x, [L][B][H] */
     hipStream_t st;
     uint16_t *kc, *vc;         /* [B][L][nkv][kv_max][hd] */
     float *x, *qkv, *attn, *h, *hid;
@@ -1702,7 +1703,7 @@ static batch_t *batch_create(const stack_t *s, int B, int is_cp) {
     REQ(s->H % 64 == 0 && s->F % 64 == 0 && s->qd % 64 == 0, "batched step needs dims divisible by 64");
     bt->s = s; bt->B = B; bt->Bp = (B + 15) & ~15; bt->kv_max = s->kv_max; bt->is_cp = is_cp;
     HCK(hipStreamCreateWithFlags(&bt->st, hipStreamNonBlocking));
-    const size_t per = (size_t)s->L * s->nkv * s->kv_max * s->hd;
+    const size_t per = (size_t)s->L * s->nkv * bt->kv_max * s->hd;
     const int K = s->F > s->H ? (s->F > s->qd ? s->F : s->qd) : (s->H > s->qd ? s->H : s->qd);
     HCK(hipMalloc((void **)&bt->kc, (size_t)B * per * 2));
     HCK(hipMalloc((void **)&bt->vc, (size_t)B * per * 2));
@@ -1778,20 +1779,20 @@ static hipError_t batch_body(void *arg) {
     hipError_t e;
     const float scale = 1.0f / sqrtf((float)s->hd);
     const int H = s->H, F = s->F, QKV = s->qd + 2 * s->kvd;
-    const long long per = (long long)s->L * s->nkv * s->kv_max * s->hd;
+    const long long per = (long long)s->L * s->nkv * bt->kv_max * s->hd;
     /* bf16 weights: each reduce writes the next projection's input planes (the SwiGLU
      * output, the normed residual), so only layer 0's input and the attention output get a
      * plane kernel of their own */
     const int fused = s->prec == QWEN_HIP_BF16 && (long long)bt->B * 2 * F <= PF_PART_FLOATS;
     for (int l = 0; l < s->L; l++) {
-        const size_t lay = (size_t)l * s->nkv * s->kv_max * s->hd;
+        const size_t lay = (size_t)l * s->nkv * bt->kv_max * s->hd;
         if (fused) {
             if (l == 0 && (e = qt_launch_pf_pieces(bt->x, H, bt->B, H, s->in_norm[0], s->eps, bt->pf_p, bt->st))) return e;
             if ((e = qt_launch_pf_gemm(QT_PF_STORE, (const uint16_t *)s->qkv[l].w, bt->pf_p, bt->B, QKV, H, bt->qkv, QKV,
                                        bt->pf_part, PF_PART_FLOATS, bt->st))) return e;
         } else if ((e = batch_proj(bt, &s->qkv[l], QT_EPI_STORE, s->in_norm[l], bt->x, H, bt->qkv, QKV))) return e;
         if ((e = qt_launch_attn_b(bt->qkv, QKV, s->qn[l], s->kn[l], s->rope_cos, s->rope_sin, s->eps, bt->d_pos,
-                                  bt->kc + lay, bt->vc + lay, per, s->hd, (long long)s->kv_max * s->hd, s->nh, s->nkv,
+                                  bt->kc + lay, bt->vc + lay, per, s->hd, (long long)bt->kv_max * s->hd, s->nh, s->nkv,
                                   s->hd, scale, bt->part, (long long)s->nkv * bt->attn_G * (s->nh / s->nkv) * 130,
                                   bt->cnt, bt->attn_G, bt->attn, s->qd, bt->B, bt->st))) return e;
         if (fused) {
@@ -1808,11 +1809,14 @@ static hipError_t batch_body(void *arg) {
                 e = qt_launch_pf_gemm(QT_PF_RESID, (const uint16_t *)s->dn[l].w, bt->pf_p, bt->B, H, F, bt->x, H,
                                       bt->pf_part, PF_PART_FLOATS, bt->st);
             if (e) return e;
-            continue;
+        } else {
+            if ((e = batch_proj(bt, &s->o[l], QT_EPI_RESID, NULL, bt->attn, s->qd, bt->x, H))) return e;
+            if ((e = batch_proj(bt, &s->gu[l], QT_EPI_SWIGLU, s->post_norm[l], bt->x, H, bt->h, F))) return e;
+            if ((e = batch_proj(bt, &s->dn[l], QT_EPI_RESID, NULL, bt->h, F, bt->x, H))) return e;
         }
-        if ((e = batch_proj(bt, &s->o[l], QT_EPI_RESID, NULL, bt->attn, s->qd, bt->x, H))) return e;
-        if ((e = batch_proj(bt, &s->gu[l], QT_EPI_SWIGLU, s->post_norm[l], bt->x, H, bt->h, F))) return e;
-        if ((e = batch_proj(bt, &s->dn[l], QT_EPI_RESID, NULL, bt->h, F, bt->x, H))) return e;
+        if (bt->layer_out &&
+            (e = hipMemcpyAsync(bt->layer_out + (size_t)l * bt->B * H, bt->x, (size_t)bt->B * H * sizeof(float),
+                                hipMemcpyDeviceToDevice, bt->st))) return e;
     }
     if (bt->is_cp) return qt_launch_advance_pos(bt->d_pos, bt->B, bt->st);
     /* hid = final_norm(x) per stream, positions advanced by the same launch */
@@ -1820,7 +1824,7 @@ static hipError_t batch_body(void *arg) {
 }
 
 /* One batched step: x[b] <- in[b] (host), positions <- pos_arr, run, out[b] <- hid or x. */
-static int batch_step_impl(batch_t *bt, const float *in, const int *pos_arr, float *out) {
+static int batch_step_run(batch_t *bt, const float *in, const int *pos_arr, float *out, int use_graph) {
     if (!bt || bt->dead) { SETERR("batch state is dead or NULL"); return -1; }
     const stack_t *s = bt->s;
     const int B = bt->B, H = s->H;
@@ -1833,7 +1837,7 @@ static int batch_step_impl(batch_t *bt, const float *in, const int *pos_arr, flo
     bt->last_async = 0;
     HCK(hipMemcpyAsync(bt->x, bt->h_io, (size_t)B * H * sizeof(float), hipMemcpyHostToDevice, bt->st));
     HCK(hipMemcpyAsync(bt->d_pos, bt->h_pos, (size_t)B * sizeof(int), hipMemcpyHostToDevice, bt->st));
-    if (graphs_enabled()) {
+    if (use_graph && graphs_enabled()) {
         if (!bt->graph_ready) {
             if (capture(bt->st, &bt->exec, batch_body, bt) != 0) goto fail;
             bt->graph_ready = 1;
@@ -1849,6 +1853,34 @@ static int batch_step_impl(batch_t *bt, const float *in, const int *pos_arr, flo
     return 0;
 fail:
     if (bt) bt->dead = 1;
+    return -1;
+}
+
+static int batch_step_impl(batch_t *bt, const float *in, const int *pos_arr, float *out) {
+    return batch_step_run(bt, in, pos_arr, out, 1);
+}
+
+/* Diagnostic: one ungraphed batched step that also returns the residual x of every stream
+ * after every layer (residuals host [L][B][H]).  Allocates a temporary device buffer. */
+int qwen_hip_talker_batch_step_layers(void *state, const float *embeds, const int *pos_arr, float *residuals,
+                                      float *hidden_out) {
+    batch_t *bt = (batch_t *)state;
+    float *tmp = NULL;
+    if (!bt || bt->dead) { SETERR("batch state is dead or NULL"); return -1; }
+    if (!residuals) { SETERR("null residuals"); return -1; }
+    const size_t n = (size_t)bt->s->L * bt->B * bt->s->H;
+    HCK(hipMalloc((void **)&tmp, n * sizeof(float)));
+    bt->layer_out = tmp;
+    const int rc = batch_step_run(bt, embeds, pos_arr, hidden_out, 0);
+    bt->layer_out = NULL;
+    if (rc == 0) {
+        HCK(hipMemcpy(residuals, tmp, n * sizeof(float), hipMemcpyDeviceToHost));
+    }
+    (void)hipFree(tmp);
+    return rc;
+fail:
+    bt->layer_out = NULL;
+    if (tmp) (void)hipFree(tmp);
     return -1;
 }
 
@@ -1869,13 +1901,13 @@ int qwen_hip_talker_batch_upload_slot(void *state, int b, const uint16_t *kv_k, 
     REQ(b >= 0 && b < bt->B, "slot %d out of range", b);
     REQ(kv_k && kv_v, "null KV");
     REQ(prefill_len <= bt->kv_max && prefill_len <= src_kv_max, "prefill_len %d exceeds kv_max", prefill_len);
-    const size_t per = (size_t)s->L * s->nkv * s->kv_max * s->hd;
+    const size_t per = (size_t)s->L * s->nkv * bt->kv_max * s->hd;
     if (!bt->kv_stage) HCK(hipMalloc((void **)&bt->kv_stage, (size_t)bt->kv_max * s->kvd * sizeof(uint16_t)));
     for (int l = 0; l < s->L; l++) {
-        const size_t dst = (size_t)b * per + (size_t)l * s->nkv * s->kv_max * s->hd;
+        const size_t dst = (size_t)b * per + (size_t)l * s->nkv * bt->kv_max * s->hd;
         const size_t src = (((size_t)b * s->L + l) * src_kv_max) * s->kvd;
-        HCK(kv_xfer(bt->kc + dst, s->kv_max, (uint16_t *)kv_k + src, prefill_len, s->nkv, s->hd, 1, bt->kv_stage, bt->st));
-        HCK(kv_xfer(bt->vc + dst, s->kv_max, (uint16_t *)kv_v + src, prefill_len, s->nkv, s->hd, 1, bt->kv_stage, bt->st));
+        HCK(kv_xfer(bt->kc + dst, bt->kv_max, (uint16_t *)kv_k + src, prefill_len, s->nkv, s->hd, 1, bt->kv_stage, bt->st));
+        HCK(kv_xfer(bt->vc + dst, bt->kv_max, (uint16_t *)kv_v + src, prefill_len, s->nkv, s->hd, 1, bt->kv_stage, bt->st));
     }
     HCK(hipStreamSynchronize(bt->st));
     return 0;
@@ -1889,14 +1921,14 @@ int qwen_hip_talker_batch_download_slot(void *state, int b, uint16_t *kv_k, uint
     REQ(b >= 0 && b < bt->B, "slot %d out of range", b);
     REQ(n >= 0 && n <= bt->kv_max && n <= dst_kv_max, "n %d out of range", n);
     if (n == 0) return 0;
-    const size_t per = (size_t)s->L * s->nkv * s->kv_max * s->hd;
+    const size_t per = (size_t)s->L * s->nkv * bt->kv_max * s->hd;
     REQ(kv_k && kv_v, "null KV");
     if (!bt->kv_stage) HCK(hipMalloc((void **)&bt->kv_stage, (size_t)bt->kv_max * s->kvd * sizeof(uint16_t)));
     for (int l = 0; l < s->L; l++) {
-        const size_t src = (size_t)b * per + (size_t)l * s->nkv * s->kv_max * s->hd;
+        const size_t src = (size_t)b * per + (size_t)l * s->nkv * bt->kv_max * s->hd;
         const size_t dst = (((size_t)b * s->L + l) * dst_kv_max) * s->kvd;
-        HCK(kv_xfer(bt->kc + src, s->kv_max, kv_k + dst, n, s->nkv, s->hd, 0, bt->kv_stage, bt->st));
-        HCK(kv_xfer(bt->vc + src, s->kv_max, kv_v + dst, n, s->nkv, s->hd, 0, bt->kv_stage, bt->st));
+        HCK(kv_xfer(bt->kc + src, bt->kv_max, kv_k + dst, n, s->nkv, s->hd, 0, bt->kv_stage, bt->st));
+        HCK(kv_xfer(bt->vc + src, bt->kv_max, kv_v + dst, n, s->nkv, s->hd, 0, bt->kv_stage, bt->st));
     }
     HCK(hipStreamSynchronize(bt->st));
     return 0;

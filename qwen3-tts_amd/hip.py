@@ -29,7 +29,7 @@ EXPORTS = [
     "qwen_hip_op_rms_norm_per_head", "qwen_hip_op_swiglu", "qwen_hip_op_argmax_matvec",
     "qwen_hip_op_sample", "qwen_hip_op_codec_sample", "qwen_hip_talker_sample",
     "qwen_hip_op_quantize_int8", "qwen_hip_op_quantize_q4_0", "qwen_hip_talker_dequant",
-    "qwen_hip_last_error", "qwen_hip_talker_batch_init", "qwen_hip_talker_batch_step",
+    "qwen_hip_last_error", "qwen_hip_talker_batch_init", "qwen_hip_talker_batch_step", "qwen_hip_talker_batch_step_layers",
     "qwen_hip_talker_batch_upload_slot", "qwen_hip_talker_batch_free", "qwen_hip_talker_batch_download_slot",
     "qwen_hip_talker_batch_step_async", "qwen_hip_talker_batch_sync", "qwen_hip_talker_batch_stream",
     "qwen_hip_cp_batch_init", "qwen_hip_cp_batch_step", "qwen_hip_cp_batch_free", "qwen_hip_op_matmat_int8", "qwen_hip_op_matmat_q4_0",
@@ -151,6 +151,7 @@ def lib():
         L.qwen_hip_last_error.restype = C.c_char_p
         L.qwen_hip_talker_batch_init.argtypes = [vp, i]; L.qwen_hip_talker_batch_init.restype = vp
         L.qwen_hip_talker_batch_step.argtypes = [vp, vp, vp, vp]; L.qwen_hip_talker_batch_step.restype = i
+        L.qwen_hip_talker_batch_step_layers.argtypes = [vp, vp, vp, vp, vp]; L.qwen_hip_talker_batch_step_layers.restype = i
         L.qwen_hip_talker_batch_upload_slot.argtypes = [vp, i, vp, vp, i, i]
         L.qwen_hip_talker_batch_upload_slot.restype = i
         L.qwen_hip_talker_batch_download_slot.argtypes = [vp, i, vp, vp, i, i]
@@ -446,6 +447,15 @@ class TalkerBatch:
         out = np.empty((self.B, self.t.H), np.float32)
         check(lib().qwen_hip_talker_batch_step(self.h, _p(e), _p(p), _p(out)), "talker_batch_step")
         return out
+
+    def step_layers(self, embeds, pos):
+        """One ungraphed batched step; returns (residuals [n_layers][B][H], hidden [B][H])."""
+        e = np.ascontiguousarray(embeds, np.float32).reshape(self.B, self.t.H)
+        p = np.ascontiguousarray(pos, np.int32)
+        res = np.empty((self.t.nl, self.B, self.t.H), np.float32)
+        out = np.empty((self.B, self.t.H), np.float32)
+        check(lib().qwen_hip_talker_batch_step_layers(self.h, _p(e), _p(p), _p(res), _p(out)), "talker_batch_step_layers")
+        return res, out
 
     def upload_slot(self, b, kv_k, kv_v, n):
         """kv_k/kv_v: [B][n_layers][src_kv_max][kv_dim] bf16 (the batch engine layout)."""
