@@ -206,7 +206,7 @@ def test_generate_rejects_bad_arguments():
     with pytest.raises(RuntimeError):
         hip.generate(g, cp, head, embc, pad, h0, P, -1, 4)                 # frame0 < 0
     with pytest.raises(RuntimeError):
-        hip.generate(g, cp, head, embc, pad, h0, 120, 0, 40)               # past kv_max
+        hip.generate(g, cp, head, embc, pad, h0, 8190, 0, 40)              # past the largest cache (8192)
     codes, _, _, _ = hip.generate(g, cp, head, embc, pad, h0, P, 0, 2)     # the states stay usable
     assert len(codes) == 2
     cp.free()

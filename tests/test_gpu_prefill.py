@@ -166,7 +166,7 @@ def test_prefill_argument_errors_leave_state_usable():
     tk, g, _ = _tiny_talker(hip.BF16, -1, kv_max=64)
     L = hip.lib()
     e = np.zeros((65, tk.H), np.float32)
-    assert L.qwen_hip_talker_prefill(tk.h, None, e.ctypes.data, 65) != 0      # beyond kv_max
+    assert L.qwen_hip_talker_prefill(tk.h, None, e.ctypes.data, 65) != 0      # beyond the rope table (64)
     assert L.qwen_hip_talker_prefill(tk.h, None, None, 4) != 0               # no inputs
     dx = tk.prefill(g["embeds"])
     assert rel_l2(dx, g["dec_x_bf16"]) <= 1e-5
