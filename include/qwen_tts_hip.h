@@ -197,6 +197,11 @@ int   qwen_hip_talker_batch_download_slot(void *state, int b, uint16_t *kv_k, ui
 int   qwen_hip_talker_batch_step_async(void *state, int n_steps);
 int   qwen_hip_talker_batch_sync(void *state);
 void *qwen_hip_talker_batch_stream(void *state);
+/* Test/measurement switch (no reference counterpart): int8 projections make their
+ * activation pieces inside the projection launch (on = 1, the default wherever every
+ * projection shape allows it) or in a launch of their own (0); both give the same bytes.
+ * Applies to Talker and CP batch states.  Returns the mode in effect, -1 on error. */
+int   qwen_hip_batch_fold_pieces(void *state, int on);
 
 /* ---- level 2: Code Predictor (qwen_tts_cuda_talker.cu:751-841; qwen_tts_metal.m:2246) ---- */
 

@@ -50,6 +50,25 @@ struct QtAttnArgs {
 };
 
 #define QT_KVB 128   // keys of a chunk staged in LDS at once
+
+// The same copy issued from inline assembly: the compiler does not see it write LDS, so
+// it inserts no vmcnt(0) before later LDS reads (it cannot tell the K copies from the V
+// copies across the key loop); the caller waits for it with qt_wait_vm.  M0 holds the
+// LDS address (wave-uniform), one wait state after it is written.
+__device__ __forceinline__ void qt_lds_copy16_u(const void *src, void *dst) {
+    const unsigned lds = (unsigned)(uintptr_t)(__attribute__((address_space(3))) void *)dst;
+    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(lds) : "memory", "m0");
+}
+
+// s_waitcnt on one counter only, as assembly with a memory clobber so that no LDS access
+// moves across it
+template <int N>
+__device__ __forceinline__ void qt_wait_vm() {
+    static_assert(N == 0 || N == 8, "vmcnt");
+    if (N == 8) asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
+    else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+}
+__device__ __forceinline__ void qt_wait_lgkm0() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
 #define QT_B_MIN_CHUNK 1536  // batched step: minimum keys per chunk
 
 // 16 bytes per lane from global memory straight into LDS (global_load_lds_dwordx4):
@@ -102,16 +121,19 @@ __global__ __launch_bounds__(QT_WG) void k_attn(QtAttnArgs a) {
     __shared__ float ml[QT_WAVES][HPK][2];                      // per-k-tile (max, exp-sum)
     __shared__ __align__(16) uint16_t knew[QT_HD];
     __shared__ __align__(16) uint16_t vnew[QT_HD];
-    // K rows, V rows of a key block; reused as the merge staging
-    __shared__ __align__(16) uint16_t s_kvbuf[(KVBYTES > MBYTES ? KVBYTES : MBYTES) / 2];
-    uint16_t(*s_kv)[KVB * QT_HD] = reinterpret_cast<uint16_t(*)[KVB * QT_HD]>(s_kvbuf);
+    // K rows and V rows of a key block, two LDS objects so that the compiler's wait for the
+    // copies into one (global_load_lds, counted by vmcnt) leaves copies into the other in
+    // flight; the V object is also the merge staging
+    __shared__ __align__(16) uint16_t s_k[KVB * QT_HD];
+    __shared__ __align__(16) uint16_t s_vbuf[(KVBYTES / 2 > MBYTES ? KVBYTES / 2 : MBYTES) / 2];
+    uint16_t *const s_v = s_vbuf;
     __shared__ int last_flag;
 
     const uint16_t *Kg = a.K + (long long)g * a.head_stride;
     const uint16_t *Vg = a.V + (long long)g * a.head_stride;
     const int sub = lane & 15, pg = lane >> 4;
 
-    // K and/or V rows of keys [kb, kb + min(KVB, n - kb)) of the chunk into s_kv, in
+    // K and/or V rows of keys [kb, kb + min(KVB, n - kb)) of the chunk into s_k / s_v, in
     // the swizzled slot order of qt_attn_mf.h (lane (pg, sub) fills slot sub of block row
     // 4i + pg); the appended key (PREP) is not read from memory, it comes from knew/vnew.
     auto stage = [&](int kb, bool doK, bool doV) {
@@ -121,24 +143,25 @@ __global__ __launch_bounds__(QT_WG) void k_attn(QtAttnArgs a) {
             const int jl = i * 4 + pg, jj = kb + jl;
             if (jj < n && !(PREP && j0 + jj == pos)) {
                 const long long row = (long long)(j0 + jj) * a.pos_stride;
-                if (doK) qt_lds_copy16(Kg + row + qt_kslot(jl, sub) * 8, &s_kv[0][i * 4 * QT_HD]);
-                if (doV) qt_lds_copy16(Vg + row + qt_vslot(jl, sub) * 8, &s_kv[1][i * 4 * QT_HD]);
+                if (doK) qt_lds_copy16(Kg + row + qt_kslot(jl, sub) * 8, &s_k[i * 4 * QT_HD]);
+                if (doV) qt_lds_copy16(Vg + row + qt_vslot(jl, sub) * 8, &s_v[i * 4 * QT_HD]);
             }
         }
     };
-    // BATCH: 32-key tile tix of the chunk (keys 32 tix .. +31) into this wave's block rows
-    // 32w .. 32w+31 (same swizzle: it depends on the row's low bits only), eight 1-KiB
-    // copies each for K and V; the appended key is not read (it comes from knew / vnew)
-    auto stage_w = [&](int tix) {
+    // BATCH: the K (doK) or V rows of 32-key tile tix of the chunk (keys 32 tix .. +31) into
+    // this wave's block rows 32w .. 32w+31 (same swizzle: it depends on the row's low bits
+    // only), eight 1-KiB copies.  Every lane issues all eight, so the wave's vmcnt counts
+    // eight per staging: rows past the chunk copy its last row (their scores are masked and
+    // their value rows zeroed), and the appended key's row is copied too and then
+    // overwritten from knew / vnew once the copy has landed.
+    auto stage_w = [&](int tix, bool doK) {
         const int kb = 32 * tix;
 #pragma unroll
         for (int i = 0; i < 8; i++) {
-            const int jl = i * 4 + pg, jj = kb + jl;
-            if (jj < n && !(PREP && j0 + jj == pos)) {
-                const long long row = (long long)(j0 + jj) * a.pos_stride;
-                qt_lds_copy16(Kg + row + qt_kslot(jl, sub) * 8, &s_kv[0][(32 * wave + i * 4) * QT_HD]);
-                qt_lds_copy16(Vg + row + qt_vslot(jl, sub) * 8, &s_kv[1][(32 * wave + i * 4) * QT_HD]);
-            }
+            const int jl = i * 4 + pg;
+            const long long row = (long long)(j0 + min(kb + jl, n - 1)) * a.pos_stride;
+            if (doK) qt_lds_copy16_u(Kg + row + qt_kslot(jl, sub) * 8, &s_k[(32 * wave + i * 4) * QT_HD]);
+            else qt_lds_copy16_u(Vg + row + qt_vslot(jl, sub) * 8, &s_v[(32 * wave + i * 4) * QT_HD]);
         }
     };
     // LDS written by global_load_lds is counted by vmcnt, and a workgroup barrier does
@@ -146,7 +169,7 @@ __global__ __launch_bounds__(QT_WG) void k_attn(QtAttnArgs a) {
     // barrier that publishes the block to the other waves.
     // ---- 0. K/V of the first key block (BATCH: each wave's first tile) in flight first ----
     if (BATCH) {
-        if (32 * wave < n) stage_w(wave);
+        if (32 * wave < n) { stage_w(wave, true); stage_w(wave, false); }
     } else {
         stage(0, true, true);
     }
@@ -181,8 +204,8 @@ __global__ __launch_bounds__(QT_WG) void k_attn(QtAttnArgs a) {
                 vnew[lane] = v0; vnew[lane + 64] = v1;
                 const int r = pos - j0;            // its row in the first staged block
                 if (!BATCH && r < KVB) {
-                    s_kv[0][qt_kidx(r, lane)] = k0; s_kv[0][qt_kidx(r, lane + 64)] = k1;
-                    s_kv[1][qt_vidx(r, lane)] = v0; s_kv[1][qt_vidx(r, lane + 64)] = v1;
+                    s_k[qt_kidx(r, lane)] = k0; s_k[qt_kidx(r, lane + 64)] = k1;
+                    s_v[qt_vidx(r, lane)] = v0; s_v[qt_vidx(r, lane + 64)] = v1;
                 }
             }
         }
@@ -192,7 +215,7 @@ __global__ __launch_bounds__(QT_WG) void k_attn(QtAttnArgs a) {
     }
     qt_att_zero_rows<HPK>(&qp[0][0], QT_HD, tid, QT_WG);
     qt_att_zero_rows<HPK>(&pp[0][0], PPC, tid, QT_WG);
-    if (!BATCH) qt_att_zero_vrows(s_kv[1], min(KVB, n), (min(KVB, n) + 31) & ~31, tid, QT_WG);
+    if (!BATCH) qt_att_zero_vrows(s_v, min(KVB, n), (min(KVB, n) + 31) & ~31, tid, QT_WG);
     if (!BATCH) __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();   // (also, !BATCH: every wave's LDS copies of the first block have landed)
 
@@ -203,28 +226,39 @@ __global__ __launch_bounds__(QT_WG) void k_attn(QtAttnArgs a) {
     qt_att_run_init(run);
     if constexpr (BATCH) {
         // ---- 2b. each wave streams its own 32-key tiles (tix = w, w + 4, ...) with no
-        // workgroup barrier: wait for its copies, put the appended key and zero the value
-        // rows past the chunk, score (qt_att_tiles on k-tile w), P.V over all 128 dims of
-        // that k-tile (four 32-dim slices), fold into the wave's running (m, l, o) ----
+        // workgroup barrier: wait for the tile's keys, put the appended key, score
+        // (qt_att_tiles on k-tile w), then the next tile's keys go in flight while this
+        // tile's values are waited for (the appended value put, the value rows past the
+        // chunk zeroed) and P.V runs over all 128 dims of the k-tile (four 32-dim slices);
+        // then the next tile's values go in flight and the tile folds into the wave's
+        // running (m, l, o).  vmcnt counts eight per staging (stage_w), in issue order. ----
         float wm = -INFINITY, wl = 0.f, wo[4][2];
 #pragma unroll
         for (int sl = 0; sl < 4; sl++) wo[sl][0] = wo[sl][1] = 0.f;
         const int ntile = (n + 31) >> 5;
+        __builtin_amdgcn_s_waitcnt(0);                // the first tile (and phase 1's stores)
         for (int tix = wave; tix < ntile; tix += QT_WAVES) {
-            const int kb = 32 * tix, nk = min(32, n - kb);
-            __builtin_amdgcn_s_waitcnt(0);            // this wave's copies have landed
-            const int nrow = pos - j0 - kb;
-            if (PREP && nrow >= 0 && nrow < nk) qt_att_put_kv(s_kv[0], s_kv[1], 32 * wave + nrow, knew, vnew, lane);
-            if (nk < 32) qt_att_zero_vrows(s_kv[1] + 32 * wave * QT_HD, nk, 32, lane, 64);
-            qt_att_tiles<HPK>(&qp[0][0], s_kv[0], &pp[0][0], KVB, &ml[0][0][0], wave, 32 * wave + nk, scale2, lane);
+            const int kb = 32 * tix, nk = min(32, n - kb), row = 32 * wave + (pos - j0 - kb);
+            const bool more = tix + QT_WAVES < ntile, put = PREP && pos - j0 - kb >= 0 && pos - j0 - kb < nk;
+            qt_wait_vm<8>();                          // keys of tile tix (its values may be in flight)
+            if (put && lane < 16)
+                *reinterpret_cast<uint4 *>(s_k + row * QT_HD + qt_kslot(row, lane) * 8) =
+                    *reinterpret_cast<const uint4 *>(knew + 8 * lane);
+            qt_att_tiles<HPK>(&qp[0][0], s_k, &pp[0][0], KVB, &ml[0][0][0], wave, 32 * wave + nk, scale2, lane);
+            qt_wait_lgkm0();                          // every LDS read of the keys has returned
+            if (more) { stage_w(tix + QT_WAVES, true); qt_wait_vm<8>(); }
+            else qt_wait_vm<0>();                     // values of tile tix
+            if (put && lane < 16)
+                *reinterpret_cast<uint4 *>(s_v + row * QT_HD + qt_vslot(row, lane) * 8) =
+                    *reinterpret_cast<const uint4 *>(vnew + 8 * lane);
+            if (nk < 32) qt_att_zero_vrows(s_v + 32 * wave * QT_HD, nk, 32, lane, 64);
             float to[4][2], tM = 0.f, tl = 0.f;
 #pragma unroll
             for (int sl = 0; sl < 4; sl++)
-                qt_att_pv<HPK, 1>(&pp[0][0] + 32 * wave, KVB, &ml[wave][0][0], s_kv[1] + 32 * wave * QT_HD, 32 * sl, lane,
+                qt_att_pv<HPK, 1>(&pp[0][0] + 32 * wave, KVB, &ml[wave][0][0], s_v + 32 * wave * QT_HD, 32 * sl, lane,
                                   to[sl], tM, tl);
-            // every LDS read of this tile has returned before the next tile's copies land
-            __builtin_amdgcn_s_waitcnt(0);
-            if (tix + QT_WAVES < ntile) stage_w(tix + QT_WAVES);
+            qt_wait_lgkm0();                          // every LDS read of the values has returned
+            if (more) stage_w(tix + QT_WAVES, false);
             const float mn = fmaxf(wm, tM);
             const float fr = qt_exp2(wm - mn), fb = qt_exp2(tM - mn);   // first tile: fr = 0, fb = 1
             wl = fmaf(wl, fr, tl * fb);
@@ -237,8 +271,8 @@ __global__ __launch_bounds__(QT_WG) void k_attn(QtAttnArgs a) {
         }
         // ---- merge the four waves' states, waves in order, into the per-lane form of
         // the epilogue (head pg, dims 32 wave + sub and + 16) ----
-        __syncthreads();                              // every wave is done with s_kv
-        float *ws = reinterpret_cast<float *>(s_kvbuf);  // [wave][lane][10]: m, l, o[4][2]
+        __syncthreads();                              // every wave is done with s_k and s_v
+        float *ws = reinterpret_cast<float *>(s_vbuf);  // [wave][lane][10]: m, l, o[4][2]
         {
             float *me = ws + (wave * 64 + lane) * 10;
             me[0] = wm; me[1] = wl;
@@ -273,14 +307,14 @@ __global__ __launch_bounds__(QT_WG) void k_attn(QtAttnArgs a) {
                 __builtin_amdgcn_s_waitcnt(0);
                 const int nrow = pos - j0 - kb;
                 if (PREP && wave == 0 && nrow >= 0 && nrow < nk && lane < 16)
-                    *reinterpret_cast<uint4 *>(&s_kv[0][nrow * QT_HD + qt_kslot(nrow, lane) * 8]) =
+                    *reinterpret_cast<uint4 *>(&s_k[nrow * QT_HD + qt_kslot(nrow, lane) * 8]) =
                         *reinterpret_cast<const uint4 *>(knew + 8 * lane);
                 __syncthreads();
             }
             if (kb + 32 * wave < n) {
                 const int rr[2] = {32 * wave, 32 * wave + 16};
                 float sc[2];
-                qt_att_qk2(&qp[0][0], s_kv[0], rr, lane, sc);
+                qt_att_qk2(&qp[0][0], s_k, rr, lane, sc);
                 sv[b][0] = rr[0] + sub < nk ? sc[0] * scale2 : -INFINITY;
                 sv[b][1] = rr[1] + sub < nk ? sc[1] * scale2 : -INFINITY;
                 wm = fmaxf(wm, group_max<16>(fmaxf(sv[b][0], sv[b][1])));
@@ -306,16 +340,16 @@ __global__ __launch_bounds__(QT_WG) void k_attn(QtAttnArgs a) {
                 __builtin_amdgcn_s_waitcnt(0);
                 const int nrow = pos - j0 - kb;
                 if (PREP && wave == 0 && nrow >= 0 && nrow < nk && lane < 16)
-                    *reinterpret_cast<uint4 *>(&s_kv[1][nrow * QT_HD + qt_vslot(nrow, lane) * 8]) =
+                    *reinterpret_cast<uint4 *>(&s_v[nrow * QT_HD + qt_vslot(nrow, lane) * 8]) =
                         *reinterpret_cast<const uint4 *>(vnew + 8 * lane);
-                qt_att_zero_vrows(s_kv[1], nk, (nk + 31) & ~31, tid, QT_WG);
+                qt_att_zero_vrows(s_v, nk, (nk + 31) & ~31, tid, QT_WG);
                 __syncthreads();
             }
 #pragma unroll
             for (int t = 0; t < 4; t++) {
                 if (4 * b + t >= nt) break;
                 qt_u32x4 pa, vv[2];
-                qt_cm_operands(&pp[0][0], PPC, kb + 32 * t, s_kv[1] + 32 * t * QT_HD, 32 * wave, lane, pa, vv);
+                qt_cm_operands(&pp[0][0], PPC, kb + 32 * t, s_v + 32 * t * QT_HD, 32 * wave, lane, pa, vv);
                 qt_cm_mfma(pa, vv, acc);
             }
         }
@@ -331,15 +365,15 @@ __global__ __launch_bounds__(QT_WG) void k_attn(QtAttnArgs a) {
             stage(kb, true, true);
             __builtin_amdgcn_s_waitcnt(0);
             const int nrow = pos - j0 - kb;   // the appended key's row, if in this block
-            if (PREP && wave == 0 && nrow >= 0 && nrow < nk) qt_att_put_kv(s_kv[0], s_kv[1], nrow, knew, vnew, lane);
-            qt_att_zero_vrows(s_kv[1], nk, (nk + 31) & ~31, tid, QT_WG);
+            if (PREP && wave == 0 && nrow >= 0 && nrow < nk) qt_att_put_kv(s_k, s_v, nrow, knew, vnew, lane);
+            qt_att_zero_vrows(s_v, nk, (nk + 31) & ~31, tid, QT_WG);
             __syncthreads();
         }
         if (32 * wave < nk)
-            qt_att_tiles<HPK>(&qp[0][0], s_kv[0], &pp[0][0], KVB, &ml[0][0][0], wave, nk, scale2, lane);
+            qt_att_tiles<HPK>(&qp[0][0], s_k, &pp[0][0], KVB, &ml[0][0][0], wave, nk, scale2, lane);
         __syncthreads();
         float o[2], M, l;
-        qt_att_pv_n<HPK>((nk + 31) >> 5, &pp[0][0], KVB, &ml[0][0][0], s_kv[1], 32 * wave, lane, o, M, l);
+        qt_att_pv_n<HPK>((nk + 31) >> 5, &pp[0][0], KVB, &ml[0][0][0], s_v, 32 * wave, lane, o, M, l);
         qt_att_run_add(run, o, M, l);
     }
     // lane: head pg, dims 32*wave + sub and + 16
@@ -374,7 +408,7 @@ __global__ __launch_bounds__(QT_WG) void k_attn(QtAttnArgs a) {
     // Merge: all chunk partials into LDS (the K/V buffer, free now) with one parallel
     // load round, then each half-wave merges one (head, dim) output over the chunks
     // (softmax_merge32, lane = chunk).
-    float *mpart = reinterpret_cast<float *>(s_kvbuf);
+    float *mpart = reinterpret_cast<float *>(s_vbuf);
     const float *gp = a.part + (size_t)g * G * HPK * PS;
     {
         // all loads issued before any is consumed (one round trip, not one per element)

@@ -39,98 +39,115 @@ typedef int qt_v4i __attribute__((ext_vector_type(4)));
 #define QT_BG_MAXW 16          // waves per workgroup at most (K <= 8192)
 
 // ---- activation pieces ---------------------------------------------------------------
-// One 1024-thread workgroup per padded stream b < Bp; each thread holds <= 8 elements in
-// registers (one load round), two block reductions (sum of squares, max).  x row b at
-// x + b*xstride; norm_w != NULL: the pieces are of RMSNorm(x)*w
-// (qwen_tts_kernels.c:292-382), else of x.  Padding streams (b >= B) write zero pieces.
-#define QT_BP_T 1024
-#define QT_BP_E 8              // elements per thread: K <= 8192
-__device__ __forceinline__ float bp_block_sum(float v, float *red) {
-    v = group_sum<64>(v);
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    __syncthreads();
-    if (lane == 0) red[wave] = v;
-    __syncthreads();
-    float t = 0.f;
+// The pieces of one stream are made by a group of QT_BP_T threads (four waves): thread t
+// holds the float4 groups g = t + QT_BP_T*j (elements 4g .. 4g+3) in registers, one load
+// round; the RMSNorm sum of squares (norm_w != NULL, qwen_tts_kernels.c:292-382) and the
+// maximum are one in-wave reduction each plus a four-entry LDS combine in a fixed order,
+// so every maker of a stream's pieces (k_bpieces, or the first workgroups of a
+// k_bgemm2_i8 launch) produces the same bytes.  Each thread writes its four elements of
+// each plane as one dword.  A padding stream (xb == NULL) gets zero pieces and S = 0.
+#define QT_BP_T 256            // threads per stream
+#define QT_BP_J 8              // float4 groups per thread: K <= 8192
+struct BpStream {
+    float4 v[QT_BP_J], w[QT_BP_J];
+    // issue the loads (x row and gains); the caller may issue other loads before finish()
+    __device__ __forceinline__ void load(const float *xb, const float *norm_w, int K, int t) {
+        const int ng = K >> 2;
 #pragma unroll
-    for (int i = 0; i < QT_BP_T / 64; i++) t += red[i];
-    return t;
-}
-__device__ __forceinline__ float bp_block_max(float v, float *red) {
-    v = group_max<64>(v);
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    __syncthreads();
-    if (lane == 0) red[wave] = v;
-    __syncthreads();
-    float t = 0.f;
+        for (int j = 0; j < QT_BP_J; j++) {
+            const int g = t + QT_BP_T * j;
+            v[j] = (xb && g < ng) ? *reinterpret_cast<const float4 *>(xb + 4 * g) : make_float4(0.f, 0.f, 0.f, 0.f);
+            w[j] = (norm_w && g < ng) ? *reinterpret_cast<const float4 *>(norm_w + 4 * g) : make_float4(1.f, 1.f, 1.f, 1.f);
+        }
+    }
+    // plane `plane` of x / s = p1 + p2/128 + p3/16384 + e3 (the exact split of the file header)
+    __device__ __forceinline__ static unsigned split(float x, float isc, int plane) {
+        const float y = x * isc;                 // |y| < 128, exact
+        const float f1 = floorf(y);
+        // y - f1 is exact for |y| >= 1 and for y >= 0; for y in (-1/2, 0) it can round,
+        // and for -2^-25 < y < 0 it rounds up to 1.0, which would make plane 2 128 (an
+        // int8 -128): planes 2 and 3 are held to 127, so p1 + 127/128 + 127/16384 =
+        // p1 + 1 - 2^-14 stands for such a y, still within 2^-14 of it
+        const float r1 = (y - f1) * 128.0f;      // [0, 128]
+        const float f2 = fminf(floorf(r1), 127.0f);
+        if (plane == 0) return (unsigned)(int)f1 & 255u;
+        if (plane == 1) return (unsigned)(int)f2 & 255u;
+        const float r2 = (r1 - f2) * 128.0f;
+        return (unsigned)(int)fminf(floorf(r2), 127.0f) & 255u;
+    }
+    // normalise, scale, split and store; red: 8 floats of LDS owned by this group.
+    // Contains one workgroup barrier per reduction (norm must be the same for every group
+    // of a workgroup).  AGENT: stores at device scope (read by workgroups on other XCDs in
+    // the same launch).
+    template <bool AGENT>
+    __device__ __forceinline__ void finish(bool norm, float eps, int K, int b, int Bp, int8_t *P, float *S, float *red,
+                                           int t) {
+        const int lane = t & 63, wv = t >> 6, ng = K >> 2;
+        if (norm) {
+            float ss = 0.f;
 #pragma unroll
-    for (int i = 0; i < QT_BP_T / 64; i++) t = fmaxf(t, red[i]);
-    return t;
-}
+            for (int j = 0; j < QT_BP_J; j++) {
+                ss = fmaf(v[j].x, v[j].x, ss); ss = fmaf(v[j].y, v[j].y, ss);
+                ss = fmaf(v[j].z, v[j].z, ss); ss = fmaf(v[j].w, v[j].w, ss);
+            }
+            ss = group_sum<64>(ss);
+            if (lane == 0) red[wv] = ss;
+            __syncthreads();
+            const float inv = 1.0f / sqrtf((((red[0] + red[1]) + red[2]) + red[3]) / (float)K + eps);
+#pragma unroll
+            for (int j = 0; j < QT_BP_J; j++) {
+                v[j].x = (v[j].x * inv) * w[j].x; v[j].y = (v[j].y * inv) * w[j].y;
+                v[j].z = (v[j].z * inv) * w[j].z; v[j].w = (v[j].w * inv) * w[j].w;
+            }
+        }
+        float m = 0.f;
+#pragma unroll
+        for (int j = 0; j < QT_BP_J; j++)
+            m = fmaxf(fmaxf(m, fmaxf(fabsf(v[j].x), fabsf(v[j].y))), fmaxf(fabsf(v[j].z), fabsf(v[j].w)));
+        m = group_max<64>(m);
+        if (lane == 0) red[4 + wv] = m;
+        __syncthreads();
+        m = fmaxf(fmaxf(red[4], red[5]), fmaxf(red[6], red[7]));
+        // s = 2^(e-6) with 2^e <= m < 2^(e+1); m == 0 (or not finite) -> all pieces zero
+        const bool ok = m > 0.f && m <= 3.0e38f;
+        const int ex = ok ? ilogbf(m) : 0;
+        const float sc = ok ? ldexpf(1.0f, ex - 6) : 0.f, isc = ok ? ldexpf(1.0f, 6 - ex) : 0.f;
+        const size_t cs = (size_t)3 * Bp * 64;
+#pragma unroll
+        for (int j = 0; j < QT_BP_J; j++) {
+            const int g = t + QT_BP_T * j;
+            if (g >= ng) break;
+            unsigned q[3] = {0u, 0u, 0u};
+            if (ok) {
+#pragma unroll
+                for (int p = 0; p < 3; p++)
+                    q[p] = split(v[j].x, isc, p) | split(v[j].y, isc, p) << 8 | split(v[j].z, isc, p) << 16 |
+                           split(v[j].w, isc, p) << 24;
+            }
+            const int k0 = 4 * g;
+            unsigned *d = reinterpret_cast<unsigned *>(P + (size_t)(k0 >> 6) * cs + (size_t)b * 64 + (k0 & 63));
+#pragma unroll
+            for (int p = 0; p < 3; p++) {
+                if (AGENT) __hip_atomic_store(d + p * Bp * 16, q[p], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                else d[p * Bp * 16] = q[p];
+            }
+        }
+        if (t == 0) {
+            if (AGENT) st_agent(S + b, sc);
+            else S[b] = sc;
+        }
+    }
+};
 
+// One QT_BP_T-thread workgroup per padded stream b < Bp; x row b at x + b*xstride;
+// norm_w != NULL: the pieces are of RMSNorm(x)*w, else of x.
 __global__ __launch_bounds__(QT_BP_T) void k_bpieces(const float *x, long long xstride, const float *norm_w, float eps,
                                                      int K, int B, int Bp, int8_t *P, float *S) {
-    __shared__ float red[QT_BP_T / 64];
-    const int b = blockIdx.x, tid = threadIdx.x;
-    const int col1 = b, col2 = Bp + b, col3 = 2 * Bp + b;
-    const size_t cs = (size_t)3 * Bp * 64;      // bytes per k-block of all columns
-    if (b >= B) {
-        for (int k = tid; k < K; k += QT_BP_T) {
-            const size_t o = (size_t)(k >> 6) * cs + (k & 63);
-            P[o + (size_t)col1 * 64] = 0; P[o + (size_t)col2 * 64] = 0; P[o + (size_t)col3 * 64] = 0;
-        }
-        if (tid == 0) S[b] = 0.f;
-        return;
-    }
-    const float *xb = x + (size_t)b * xstride;
-    float v[QT_BP_E], w[QT_BP_E];
-#pragma unroll
-    for (int e = 0; e < QT_BP_E; e++) {
-        const int k = tid + e * QT_BP_T;
-        v[e] = k < K ? xb[k] : 0.f;
-        w[e] = (norm_w && k < K) ? norm_w[k] : 1.f;
-    }
-    if (norm_w) {
-        float ss = 0.f;
-#pragma unroll
-        for (int e = 0; e < QT_BP_E; e++) ss = fmaf(v[e], v[e], ss);
-        ss = bp_block_sum(ss, red);
-        const float inv = 1.0f / sqrtf(ss / (float)K + eps);
-#pragma unroll
-        for (int e = 0; e < QT_BP_E; e++) v[e] = (v[e] * inv) * w[e];
-    }
-    float m = 0.f;
-#pragma unroll
-    for (int e = 0; e < QT_BP_E; e++) m = fmaxf(m, fabsf(v[e]));
-    m = bp_block_max(m, red);
-    // s = 2^(e-6) with 2^e <= m < 2^(e+1); m == 0 (or not finite) -> all pieces zero
-    const bool ok = m > 0.f && m <= 3.0e38f;
-    const int ex = ok ? ilogbf(m) : 0;
-    const float sc = ok ? ldexpf(1.0f, ex - 6) : 0.f, isc = ok ? ldexpf(1.0f, 6 - ex) : 0.f;
-#pragma unroll
-    for (int e = 0; e < QT_BP_E; e++) {
-        const int k = tid + e * QT_BP_T;
-        if (k >= K) break;
-        int q1 = 0, q2 = 0, q3 = 0;
-        if (ok) {
-            const float y = v[e] * isc;          // |y| < 128, exact
-            const float f1 = floorf(y);
-            // y - f1 is exact for |y| >= 1 and for y >= 0; for y in (-1/2, 0) it can round,
-            // and for -2^-25 < y < 0 it rounds up to 1.0, which would make plane 2 128 (an
-            // int8 -128): planes 2 and 3 are held to 127, so p1 + 127/128 + 127/16384 =
-            // p1 + 1 - 2^-14 stands for such a y, still within 2^-14 of it
-            const float r1 = (y - f1) * 128.0f;  // [0, 128]
-            const float f2 = fminf(floorf(r1), 127.0f);
-            const float r2 = (r1 - f2) * 128.0f;
-            const float f3 = fminf(floorf(r2), 127.0f);
-            q1 = (int)f1; q2 = (int)f2; q3 = (int)f3;
-        }
-        const size_t o = (size_t)(k >> 6) * cs + (k & 63);
-        P[o + (size_t)col1 * 64] = (int8_t)q1;
-        P[o + (size_t)col2 * 64] = (int8_t)q2;
-        P[o + (size_t)col3 * 64] = (int8_t)q3;
-    }
-    if (tid == 0) S[b] = sc;
+    __shared__ float red[8];
+    const int b = blockIdx.x;
+    BpStream bs;
+    bs.load(b < B ? x + (size_t)b * xstride : nullptr, norm_w, K, threadIdx.x);
+    bs.finish<false>(norm_w != nullptr, eps, K, b, Bp, P, S, red, threadIdx.x);
 }
 
 // ---- int8 weights x activation pieces --------------------------------------------------
@@ -248,6 +265,12 @@ struct QtBg2Args {
     float *out; long long ostride;
     long long *part;    // S > 1: [gridDim.x][S][units][1 or 2] exact sums
     unsigned *cnt;      // S > 1: [gridDim.x], zero between calls
+    // Pieces made in the same launch (px != NULL): the pieces of px (rows of pxstride,
+    // RMS-normalised with pnorm when it is set) are written to P and S by the launch itself.
+    const float *px; long long pxstride; const float *pnorm; float eps;
+    unsigned *sync;     // px: word 0 the makers' count, word 32*(1+g) workgroup g's go flag (one
+                        // 128-byte line each); all zero between calls
+    unsigned *err;      // px: set to 1 if a wait for the pieces gave up
 };
 
 // registers of a (NT, RT, KB) wave: B fragments, weight fragments, accumulators
@@ -275,12 +298,61 @@ __global__ __launch_bounds__(QT_B2_W * 64) void k_bgemm2_i8(QtBg2Args a) {
     const int kw0 = z * (a.K / S) + wave * KB * 64;
     const size_t cs = (size_t)3 * BP * 64;
 
+    // In-launch pieces: workgroups 0 .. BP/2-1 in dispatch order (blockIdx.x fastest) each
+    // make the pieces of streams 2i and 2i+1 (one per half of the workgroup: every 128-byte
+    // line of P is written by one workgroup), store them at device scope, wait for the
+    // stores to be acknowledged and count themselves in; the last maker to count in re-arms
+    // the count and raises every workgroup's go flag (one line per workgroup: no line is
+    // polled by more than one workgroup).  Every workgroup issues its weight loads first,
+    // then waits for its flag and clears it.  The makers never wait before they publish and
+    // are dispatched before every waiter, so the wait ends.  The B fragments are then read
+    // with ordinary loads: no L2 holds a line of P when the launch starts (the launch
+    // boundary's cache maintenance, which the two-launch form relies on too) and none is
+    // filled before the flags rise, except by its one maker.  The scales S are read at
+    // device scope.
+    const bool fold = a.px != nullptr;
+    const int lin = x + gridDim.x * z;
+    __shared__ float bp_red[2][8];
+    __shared__ unsigned mk_last;
+    BpStream bs;
+    const bool maker = fold && lin < BP / 2;
+    const int bmk = 2 * lin + (tid >> 8);                  // maker: its stream
+    if (maker) bs.load(bmk < a.B ? a.px + (size_t)bmk * a.pxstride : nullptr, a.pnorm, a.K, tid & (QT_BP_T - 1));
     uint4 wa[RT][KB];
 #pragma unroll
     for (int rt = 0; rt < RT; rt++) {
         const uint8_t *wr = a.w + (size_t)min(r0 + 16 * rt + m, a.rows - 1) * a.K + kw0 + grp * 16;
 #pragma unroll
         for (int kb = 0; kb < KB; kb++) wa[rt][kb] = *reinterpret_cast<const uint4 *>(wr + kb * 64);
+    }
+    if (fold) {
+        if (maker) {
+            bs.finish<true>(a.pnorm != nullptr, a.eps, a.K, bmk, BP, const_cast<int8_t *>(a.P), const_cast<float *>(a.S),
+                            bp_red[tid >> 8], tid & (QT_BP_T - 1));
+            __builtin_amdgcn_s_waitcnt(0);
+            __syncthreads();
+            if (tid == 0)
+                mk_last = __hip_atomic_fetch_add(&a.sync[0], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+                          (unsigned)(BP / 2 - 1);
+            __syncthreads();
+            if (mk_last) {   // every maker's stores are acknowledged
+                if (tid == 0) __hip_atomic_store(&a.sync[0], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                for (int i = tid; i < (int)(gridDim.x * gridDim.y); i += NTH)
+                    __hip_atomic_store(&a.sync[32 * (1 + i)], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
+        }
+        if (tid == 0) {
+            unsigned *flag = &a.sync[32 * (1 + lin)], spins = 0;
+            while (__hip_atomic_load(flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == 0u) {
+                if (++spins > (1u << 21)) {   // seconds: a maker is missing; flag it and go on
+                    __hip_atomic_store(a.err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    break;
+                }
+                __builtin_amdgcn_s_sleep(2);
+            }
+            __hip_atomic_store(flag, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        __syncthreads();
     }
     const int8_t *pbase = a.P + (size_t)(kw0 >> 6) * cs + (size_t)m * 64 + grp * 16;
     uint4 bv[KB][NT];
@@ -296,7 +368,7 @@ __global__ __launch_bounds__(QT_B2_W * 64) void k_bgemm2_i8(QtBg2Args a) {
         const bool ok = j < NU && b < a.B && r < a.rows;
 #pragma unroll
         for (int h = 0; h < H; h++) e_sc[u][h] = ok ? a.scale[r + h] : 0.f;
-        e_S[u] = ok ? a.S[b] : 0.f;
+        e_S[u] = ok ? (fold ? ld_agent(a.S + b) : a.S[b]) : 0.f;
         e_res[u] = (ok && EPI == QT_EPI_RESID) ? a.out[(size_t)b * a.ostride + r] : 0.f;
     }
     qt_v4i acc[RT][NT];
@@ -457,9 +529,10 @@ static void qt_b2_epi(int epi, int RT, int KB, const QtBg2Args &a, dim3 grid, hi
 
 // part / cnt: workspace from qt_bgemm2_plan (cnt zeroed once at allocation; the kernel
 // re-arms it).  Returns hipErrorInvalidValue for shapes without a plan.
-extern "C" hipError_t qt_launch_bgemm2_i8(int epi, const uint8_t *w, const float *scale, int rows, int K,
-                                          const int8_t *P, const float *S, int B, int Bp, float *out, long long ostride,
-                                          int *part, unsigned *cnt, hipStream_t st) {
+static hipError_t b2_launch(int epi, const uint8_t *w, const float *scale, int rows, int K, const float *px,
+                            long long pxstride, const float *pnorm, float eps, const int8_t *P, const float *S, int B,
+                            int Bp, float *out, long long ostride, int *part, unsigned *cnt, unsigned *sync,
+                            int sync_wgs, unsigned *derr, hipStream_t st) {
     int KB, SS, RT, ncnt; size_t pints;
     if (rows <= 0 || B <= 0 || B > Bp || !qt_bgemm2_plan(rows, K, Bp, &KB, &SS, &RT, &pints, &ncnt)) return hipErrorInvalidValue;
     if (epi == QT_EPI_SWIGLU && (rows & 1)) return hipErrorInvalidValue;
@@ -467,7 +540,12 @@ extern "C" hipError_t qt_launch_bgemm2_i8(int epi, const uint8_t *w, const float
     QtBg2Args a;
     a.w = w; a.scale = scale; a.rows = rows; a.K = K; a.P = P; a.S = S; a.B = B; a.out = out; a.ostride = ostride;
     a.part = reinterpret_cast<long long *>(part); a.cnt = cnt;
+    a.px = px; a.pxstride = pxstride; a.pnorm = pnorm; a.eps = eps; a.sync = sync; a.err = derr;
     const dim3 grid(((rows + 15) / 16 + RT - 1) / RT, SS);
+    // the in-launch pieces need Bp/2 makers, all in the first row of the grid, and the
+    // pieces routine's register row (K <= 8192)
+    if (px && (!sync || !derr || (int)grid.x < Bp / 2 || (int)(grid.x * grid.y) > sync_wgs ||
+               K > QT_BP_T * 4 * QT_BP_J)) return hipErrorInvalidValue;
     hipError_t err = hipSuccess;
     if (Bp == 16) qt_b2_epi<3>(epi, RT, KB, a, grid, st, err);
     else if (Bp == 32) qt_b2_epi<6>(epi, RT, KB, a, grid, st, err);
@@ -475,6 +553,37 @@ extern "C" hipError_t qt_launch_bgemm2_i8(int epi, const uint8_t *w, const float
     else qt_b2_epi<12>(epi, RT, KB, a, grid, st, err);
     if (err != hipSuccess) return err;
     return hipGetLastError();
+}
+
+extern "C" hipError_t qt_launch_bgemm2_i8(int epi, const uint8_t *w, const float *scale, int rows, int K,
+                                          const int8_t *P, const float *S, int B, int Bp, float *out, long long ostride,
+                                          int *part, unsigned *cnt, hipStream_t st) {
+    return b2_launch(epi, w, scale, rows, K, nullptr, 0, nullptr, 0.f, P, S, B, Bp, out, ostride, part, cnt, nullptr, 0,
+                     nullptr, st);
+}
+
+// The same with the activation pieces made inside the launch (one launch instead of
+// qt_launch_bpieces + qt_launch_bgemm2_i8, same bytes in P and S, same outputs): x rows
+// of xstride, RMS-normalised with norm_w when it is set.  sync: two zeroed words that the
+// kernel re-arms; err: set to 1 if a wait for the pieces gave up (the outputs are then
+// invalid).  Needs a grid of at least Bp/2 row groups and sync of 32*(1 + sync_wgs) words
+// with sync_wgs at least the launch's workgroups (qt_bgemm2_px_wgs).
+extern "C" hipError_t qt_launch_bgemm2_i8_px(int epi, const uint8_t *w, const float *scale, int rows, int K,
+                                             const float *x, long long xstride, const float *norm_w, float eps, int8_t *P,
+                                             float *S, int B, int Bp, float *out, long long ostride, int *part,
+                                             unsigned *cnt, unsigned *sync, int sync_wgs, unsigned *err,
+                                             hipStream_t st) {
+    if (!x) return hipErrorInvalidValue;
+    return b2_launch(epi, w, scale, rows, K, x, xstride, norm_w, eps, P, S, B, Bp, out, ostride, part, cnt, sync,
+                     sync_wgs, err, st);
+}
+
+// Workgroups of the qt_launch_bgemm2_i8_px launch for the shape, 0 if it does not take it.
+extern "C" int qt_bgemm2_px_wgs(int rows, int K, int Bp) {
+    int KB, SS, RT, nc; size_t pi;
+    if (!qt_bgemm2_plan(rows, K, Bp, &KB, &SS, &RT, &pi, &nc)) return 0;
+    const int gx = ((rows + 15) / 16 + RT - 1) / RT;
+    return gx >= Bp / 2 && K <= QT_BP_T * 4 * QT_BP_J ? gx * SS : 0;
 }
 
 // ---- q4_0 weights x activation pieces -------------------------------------------------
@@ -662,7 +771,7 @@ extern "C" hipError_t qt_launch_bgemm_q4(int epi, const uint8_t *w, const uint16
 extern "C" hipError_t qt_launch_bpieces(const float *x, long long xstride, const float *norm_w, float eps, int K, int B,
                                         int Bp, int8_t *P, float *S, hipStream_t st) {
     if (K <= 0 || (K & 63) || B <= 0 || Bp < B || (Bp & 15) || Bp > 64) return hipErrorInvalidValue;
-    if (K > QT_BP_T * QT_BP_E) return hipErrorInvalidValue;
+    if (K > QT_BP_T * 4 * QT_BP_J) return hipErrorInvalidValue;
     hipLaunchKernelGGL(k_bpieces, dim3(Bp), dim3(QT_BP_T), 0, st, x, xstride, norm_w, eps, K, B, Bp, P, S);
     return hipGetLastError();
 }

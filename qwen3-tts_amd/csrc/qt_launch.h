@@ -43,6 +43,11 @@ int qt_bgemm2_plan(int rows, int K, int Bp, int *kb, int *S, int *rt, size_t *pa
 hipError_t qt_launch_bgemm2_i8(int epi, const uint8_t *w, const float *scale, int rows, int K, const int8_t *P,
                                const float *S, int B, int Bp, float *out, long long ostride, int *part, unsigned *cnt,
                                hipStream_t st);
+hipError_t qt_launch_bgemm2_i8_px(int epi, const uint8_t *w, const float *scale, int rows, int K, const float *x,
+                                  long long xstride, const float *norm_w, float eps, int8_t *P, float *S, int B, int Bp,
+                                  float *out, long long ostride, int *part, unsigned *cnt, unsigned *sync,
+                                  int sync_wgs, unsigned *err, hipStream_t st);
+int qt_bgemm2_px_wgs(int rows, int K, int Bp);
 hipError_t qt_launch_bgemm_q4(int epi, const uint8_t *w, const uint16_t *s16, int rows, int K, const int8_t *P,
                               const float *S, int B, int Bp, float *out, long long ostride, hipStream_t st);
 hipError_t qt_launch_advance_pos(int *pos, int n, hipStream_t st);

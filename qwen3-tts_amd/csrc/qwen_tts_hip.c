@@ -1675,6 +1675,9 @@ typedef struct {
     int8_t *pc; float *ps;     /* activation pieces [Kmax/64][3*Bp][64], scales [Bp] */
     uint16_t *pf_p; float *pf_part; /* bf16: activation planes [3][64][Kmax], split-K partials (PF_PART_FLOATS) */
     int *g2_part; unsigned *g2_cnt; /* int8: split-K tiles and counters of qt_launch_bgemm2_i8 */
+    int fold;                  /* int8: pieces made inside each projection launch (qt_launch_bgemm2_i8_px) */
+    unsigned *px_sync;         /* in-launch pieces: count + per-workgroup go flags (128-byte lines), error word */
+    int px_wgs;                /* workgroups px_sync has flags for */
     float *part; unsigned *cnt;
     int *d_pos;                /* [B] */
     float *h_io; int *h_pos;   /* pinned */
@@ -1688,12 +1691,26 @@ static void batch_destroy(batch_t *bt) {
     if (!bt) return;
     if (bt->graph_ready) (void)hipGraphExecDestroy(bt->exec);
     void *bufs[] = {bt->kc, bt->vc, bt->x, bt->qkv, bt->attn, bt->h, bt->hid, bt->pc, bt->ps, bt->part, bt->cnt, bt->d_pos,
-                    bt->kv_stage, bt->pf_p, bt->pf_part, bt->g2_part, bt->g2_cnt};
+                    bt->kv_stage, bt->pf_p, bt->pf_part, bt->g2_part, bt->g2_cnt, bt->px_sync};
     for (size_t i = 0; i < sizeof bufs / sizeof bufs[0]; i++) if (bufs[i]) (void)hipFree(bufs[i]);
     if (bt->h_io) (void)hipHostFree(bt->h_io);
     if (bt->h_pos) (void)hipHostFree(bt->h_pos);
     if (bt->st) (void)hipStreamDestroy(bt->st);
     free(bt);
+}
+
+/* int8: every projection of the layer runs k_bgemm2_i8 and takes in-launch pieces */
+static int batch_px_ok(const batch_t *bt) {
+    const stack_t *s = bt->s;
+    if (s->prec != QWEN_HIP_INT8 || !bt->px_sync) return 0;
+    const int shp[4][2] = {{s->qd + 2 * s->kvd, s->H}, {s->H, s->qd}, {2 * s->F, s->H}, {s->H, s->F}};
+    for (int i = 0; i < 4; i++) {
+        int kb_, S_, rt_, nc; size_t pi;
+        const int n = qt_bgemm2_px_wgs(shp[i][0], shp[i][1], bt->Bp);
+        if (!qt_bgemm2_plan(shp[i][0], shp[i][1], bt->Bp, &kb_, &S_, &rt_, &pi, &nc) || (S_ > 1 && !bt->g2_part) ||
+            n == 0 || n > bt->px_wgs) return 0;
+    }
+    return 1;
 }
 
 static batch_t *batch_create(const stack_t *s, int B, int is_cp) {
@@ -1736,6 +1753,14 @@ static batch_t *batch_create(const stack_t *s, int B, int is_cp) {
             HCK(hipMalloc((void **)&bt->g2_cnt, (size_t)cmax * sizeof(unsigned)));
             HCK(hipMemsetAsync(bt->g2_cnt, 0, (size_t)cmax * sizeof(unsigned), bt->st));
         }
+        for (int i = 0; i < 4; i++) {
+            const int n = qt_bgemm2_px_wgs(shp[i][0], shp[i][1], bt->Bp);
+            if (n > bt->px_wgs) bt->px_wgs = n;
+        }
+        const size_t words = (size_t)32 * (2 + bt->px_wgs);   /* count, flags, error word */
+        HCK(hipMalloc((void **)&bt->px_sync, words * sizeof(unsigned)));
+        HCK(hipMemsetAsync(bt->px_sync, 0, words * sizeof(unsigned), bt->st));
+        bt->fold = batch_px_ok(bt);
     }
     bt->attn_G = s->attn_G;      /* its own: the single state's may change when its cache grows */
     HCK(hipMalloc((void **)&bt->part, (size_t)B * s->nkv * bt->attn_G * (s->nh / s->nkv) * 130 * sizeof(float)));
@@ -1762,6 +1787,10 @@ static hipError_t batch_proj(batch_t *bt, const dmat_t *m, int epi, const float 
         return qt_launch_pf_gemm(epi, (const uint16_t *)m->w, bt->pf_p, bt->B, m->rows, m->cols, dst, (int)dstride,
                                  bt->pf_part, PF_PART_FLOATS, bt->st);
     }
+    if (m->prec == QWEN_HIP_INT8 && bt->fold)
+        return qt_launch_bgemm2_i8_px(epi, m->w, m->scale, m->rows, m->cols, src, sstride, nw, s->eps, bt->pc, bt->ps,
+                                      bt->B, bt->Bp, dst, dstride, bt->g2_part, bt->g2_cnt, bt->px_sync, bt->px_wgs,
+                                      bt->px_sync + 32 * (1 + bt->px_wgs), bt->st);
     if ((e = qt_launch_bpieces(src, sstride, nw, s->eps, m->cols, bt->B, bt->Bp, bt->pc, bt->ps, bt->st))) return e;
     if (m->prec == QWEN_HIP_INT8) {
         int kb_, S_, rt_, nc; size_t pi;
@@ -1823,6 +1852,19 @@ static hipError_t batch_body(void *arg) {
     return qt_launch_rmsnorm_rows_to(bt->x, bt->hid, s->final_norm, bt->B, H, s->eps, bt->d_pos, bt->st);
 }
 
+/* After a synchronisation: fails (and marks the state dead) if an in-launch pieces wait
+ * gave up on the device. */
+static int batch_check_err(batch_t *bt) {
+    unsigned w = 0;
+    if (!bt->px_sync) return 0;
+    HCK(hipMemcpy(&w, bt->px_sync + 32 * (1 + bt->px_wgs), sizeof w, hipMemcpyDeviceToHost));
+    REQ(w == 0, "batched step: a projection gave up waiting for its in-launch activation pieces");
+    return 0;
+fail:
+    bt->dead = 1;
+    return -1;
+}
+
 /* One batched step: x[b] <- in[b] (host), positions <- pos_arr, run, out[b] <- hid or x. */
 static int batch_step_run(batch_t *bt, const float *in, const int *pos_arr, float *out, int use_graph) {
     if (!bt || bt->dead) { SETERR("batch state is dead or NULL"); return -1; }
@@ -1849,6 +1891,7 @@ static int batch_step_run(batch_t *bt, const float *in, const int *pos_arr, floa
     bt->stepped = 1;
     HCK(hipMemcpyAsync(bt->h_io, bt->is_cp ? bt->x : bt->hid, (size_t)B * H * sizeof(float), hipMemcpyDeviceToHost, bt->st));
     HCK(hipStreamSynchronize(bt->st));
+    if (batch_check_err(bt)) return -1;
     if (out) memcpy(out, bt->h_io, (size_t)B * H * sizeof(float));
     return 0;
 fail:
@@ -1956,7 +1999,25 @@ int qwen_hip_talker_batch_sync(void *state) {
     batch_t *bt = (batch_t *)state;
     if (!bt) return -1;
     HCK(hipStreamSynchronize(bt->st));
-    return 0;
+    return batch_check_err(bt);
+fail:
+    bt->dead = 1;
+    return -1;
+}
+/* int8 projections: make the activation pieces inside each projection launch (on = 1,
+ * the default where every projection shape allows it) or in a launch of their own (0).
+ * The two give the same bytes; the switch is for tests and measurement.  Returns the
+ * mode in effect, -1 on error. */
+int qwen_hip_batch_fold_pieces(void *state, int on) {
+    batch_t *bt = (batch_t *)state;
+    if (!bt || bt->dead) { SETERR("batch state is dead or NULL"); return -1; }
+    const int want = on && batch_px_ok(bt);
+    if (want != bt->fold) {
+        HCK(hipStreamSynchronize(bt->st));
+        if (bt->graph_ready) { (void)hipGraphExecDestroy(bt->exec); bt->graph_ready = 0; }
+        bt->fold = want;
+    }
+    return bt->fold;
 fail:
     bt->dead = 1;
     return -1;

@@ -32,6 +32,7 @@ EXPORTS = [
     "qwen_hip_last_error", "qwen_hip_talker_batch_init", "qwen_hip_talker_batch_step", "qwen_hip_talker_batch_step_layers",
     "qwen_hip_talker_batch_upload_slot", "qwen_hip_talker_batch_free", "qwen_hip_talker_batch_download_slot",
     "qwen_hip_talker_batch_step_async", "qwen_hip_talker_batch_sync", "qwen_hip_talker_batch_stream",
+    "qwen_hip_batch_fold_pieces",
     "qwen_hip_cp_batch_init", "qwen_hip_cp_batch_step", "qwen_hip_cp_batch_free", "qwen_hip_op_matmat_int8", "qwen_hip_op_matmat_q4_0",
     "qwen_hip_cp_set_prefill2", "qwen_hip_cp_prefill2",
     "qwen_hip_talker_prefill", "qwen_hip_talker_prefill_async", "qwen_hip_op_prefill_gemm",
@@ -160,6 +161,7 @@ def lib():
         L.qwen_hip_talker_batch_step_async.argtypes = [vp, i]; L.qwen_hip_talker_batch_step_async.restype = i
         L.qwen_hip_talker_batch_sync.argtypes = [vp]; L.qwen_hip_talker_batch_sync.restype = i
         L.qwen_hip_talker_batch_stream.argtypes = [vp]; L.qwen_hip_talker_batch_stream.restype = vp
+        L.qwen_hip_batch_fold_pieces.argtypes = [vp, i]; L.qwen_hip_batch_fold_pieces.restype = i
         L.qwen_hip_cp_batch_init.argtypes = [vp, i]; L.qwen_hip_cp_batch_init.restype = vp
         L.qwen_hip_cp_batch_step.argtypes = [vp, vp, vp]; L.qwen_hip_cp_batch_step.restype = i
         L.qwen_hip_cp_batch_free.argtypes = [vp]
@@ -456,6 +458,13 @@ class TalkerBatch:
         out = np.empty((self.B, self.t.H), np.float32)
         check(lib().qwen_hip_talker_batch_step_layers(self.h, _p(e), _p(p), _p(res), _p(out)), "talker_batch_step_layers")
         return res, out
+
+    def fold_pieces(self, on):
+        """int8: activation pieces inside the projection launches (True) or apart; returns the mode in effect."""
+        r = lib().qwen_hip_batch_fold_pieces(self.h, int(bool(on)))
+        if r < 0:
+            raise RuntimeError("qwen_hip_batch_fold_pieces failed: " + last_error())
+        return bool(r)
 
     def upload_slot(self, b, kv_k, kv_v, n):
         """kv_k/kv_v: [B][n_layers][src_kv_max][kv_dim] bf16 (the batch engine layout)."""

@@ -260,6 +260,38 @@ def test_batch_of_identical_streams_matches_single_step():
     g.free()
 
 
+@need_ref
+@pytest.mark.parametrize("B", [5, 20, 32])
+def test_batch_fold_pieces_matches_separate_launch(B):
+    """int8: the activation pieces made inside each projection launch (the default) and
+    in a launch of their own are the same bytes, so the outputs are the same bit for bit:
+    every layer's residual (ungraphed step) and the graphed step's hidden state.  B = 5 and
+    20 have padding streams (16 and 32 columns)."""
+    print(f"[case] fold pieces B={B}", flush=True)
+    ref, shape = _ref("mini", "int8")
+    layers = hip.layers_from_ref(ref, hip.INT8)
+    cos, sin = ref.rope()
+    g = hip.Talker(shape, layers, ref.final_norm(), cos, sin, hip.INT8, 64)
+    bt = hip.TalkerBatch(g, B)
+    assert bt.fold_pieces(True)
+    emb = ref.codec_emb()
+    rng = np.random.default_rng(7 + B)
+    pos = rng.integers(0, 40, B).astype(np.int32)
+    for it in range(3):
+        E = np.stack([synth.bf16_to_f32(emb[int(rng.integers(0, 2048))]) for _ in range(B)])
+        assert bt.fold_pieces(True)
+        r1, h1 = bt.step_layers(E, pos)
+        g1 = bt.step(E, pos)
+        assert not bt.fold_pieces(False)
+        r2, h2 = bt.step_layers(E, pos)     # same position: rewrites the same KV rows
+        g2 = bt.step(E, pos)
+        assert np.array_equal(r1, r2) and np.array_equal(h1, h2), it
+        assert np.array_equal(g1, g2) and np.array_equal(g1, h1), it
+        pos += 1
+    bt.free()
+    g.free()
+
+
 def test_batch_rejects_bad_arguments():
     shape = synth.SHAPES["tiny"]
     t = synth.generate(shape, 0x5EED0009, 0.0, threads=4, only=lambda n: n.startswith("talker.model."))
