@@ -86,10 +86,18 @@ class HipEvents:
 DEFAULT_WORKLOAD = "talker-1.7B-int8-b1-L2048"
 # fused kernel kinds (qwen_hip_talker_fused_kernel): label, the sources that define it
 FUSED_KERNELS = {
-    2: ("ps::rs::k_rstep role-specialised fused decode step ({prec})",
+    2: ("ps::{ns}::k_rstep role-specialised fused decode step ({prec})",
         ("qt_rstep.hip", "qt_step_common.h", "qt_attn_mf.h", "qt_device.h")),
     1: ("ps::k_pstep<{prec}> fused decode step", ("qt_pstep.hip", "qt_step_common.h", "qt_attn_mf.h", "qt_device.h")),
 }
+
+
+def fused_label(L, g, prec, hidden):
+    """Name of the kernel that runs the state's fused step (qt_rstep.hip is built per geometry:
+    ps::rs for hidden 2048, ps::rs06 for hidden 1024)."""
+    kind = L.qwen_hip_talker_fused_kernel(g.h)
+    return kind, FUSED_KERNELS.get(kind, ("unfused per-kernel path",))[0].format(
+        prec=prec, ns="rs" if hidden == 2048 else "rs06")
 
 
 def kernel_source_sha256(kind):
@@ -354,10 +362,10 @@ def main():
         kern[nm] = ev.elapsed_ms(a, b) * 1e3 / n
     if kern:
         log("[bench] per-kernel avg us: " + ", ".join(f"{k}={v:.2f}" for k, v in kern.items()))
-    kind = L.qwen_hip_talker_fused_kernel(g.h)
+    kind, klabel = fused_label(L, g, prec, s.hidden)
     roofline = {"bound": "hbm", "achieved": round(step_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": round(step_gbs / HBM_PEAK_GBS, 4), "traffic": None,
-                "kernel": FUSED_KERNELS.get(kind, ("unfused per-kernel path",))[0].format(prec=prec),
+                "kernel": klabel,
                 "bytes_per_launch": int(step_bytes * K), "avg_us": round(ms_total * 1e3, 1),
                 "steps_per_launch": K}
     # HBM bytes per launch from the committed rocprofv3 PMC passes for this workload: the
@@ -366,7 +374,7 @@ def main():
     # are the ones profiled (their sha256 is recorded with the counters): otherwise null.
     try:
         t = json.load(open(os.path.join(ROOT, "profiles", "fused_step_traffic.json")))
-        if kind in FUSED_KERNELS and t["workload"] == args.workload and t["kernel"] == FUSED_KERNELS[kind][0].format(prec=prec):
+        if kind in FUSED_KERNELS and t["workload"] == args.workload and t["kernel"] == klabel:
             if t["source_sha256"] == kernel_source_sha256(kind):
                 per_step = t["traffic_bytes_per_step"] + kv_bytes * (L_mid - t["kv_len_mid"])
                 roofline["traffic"] = int(per_step * K)
@@ -514,7 +522,7 @@ def bench_grow(args):
         gbs = (weight_bytes(s, prec) + kv_bytes * (lm + 1) + s.codec_vocab * s.hidden * 2) / (ms * 1e-3) / 1e9
         segs.append({"kv_from": i * seg, "kv_to": (i + 1) * seg, "ms_per_step": round(ms, 4), "gbs": round(gbs, 1)})
         log(f"[bench] grow: KV {i * seg:5d}..{(i + 1) * seg:5d}: {ms * 1e3:.1f} us/step, {gbs:.0f} GB/s")
-    fused = bool(L.qwen_hip_talker_fused(g.h))
+    klabel = fused_label(L, g, prec, s.hidden)[1]
     g.free()
     ms = total_ms / N
     byts = sum(weight_bytes(s, prec) + kv_bytes * (j + 1) + s.codec_vocab * s.hidden * 2 for j in range(N)) / N
@@ -529,7 +537,7 @@ def bench_grow(args):
         "segments": segs,
         "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
-                     "kernel": (f"ps::k_pstep<{prec}> fused decode step" if fused else "unfused per-kernel path"),
+                     "kernel": klabel,
                      "bytes_per_launch": int(byts * seg), "avg_us": round(total_ms / (N // seg) * 1e3, 1),
                      "steps_per_launch": seg},
         "cpu_baseline": None,

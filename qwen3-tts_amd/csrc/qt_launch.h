@@ -85,7 +85,9 @@ hipError_t qt_launch_interleave_rows(const uint16_t *gate, const uint16_t *up, u
 hipError_t qt_launch_kv_relayout(const uint16_t *src, uint16_t *dst, int n, int nkv, int hd, int kv_max, int to_heads,
                                  hipStream_t st);
 
-/* role-specialised persistent decode step (qt_rstep.hip): 1.7B geometry, int8 weights */
+/* role-specialised persistent decode step (qt_rstep.hip), int8 weights: the 1.7B geometry
+ * (qt_rstep_* / qt_launch_rstep) and the 0.6B one (qt_rstep06_* / qt_launch_rstep06, built
+ * from the same source by qt_rstep06.hip); qt_rstep_chunks holds for both */
 int qt_rstep_supported(int prec, int hidden, int inter, int n_heads, int n_kv, int head_dim, int kv_max, int n_layers);
 size_t qt_rstep_region_words(int n_layers);
 size_t qt_rstep_slot_words(void);
@@ -96,6 +98,15 @@ hipError_t qt_launch_rstep(const void *layers_dev, int n_layers, const float *fi
                            unsigned *epoch, int *err, int n_steps, int with_head, const uint16_t *head_w,
                            const uint16_t *emb, int vocab, int *d_frame, int *hist, int hist_len, float *layer_out,
                            hipStream_t st);
+int qt_rstep06_supported(int prec, int hidden, int inter, int n_heads, int n_kv, int head_dim, int kv_max, int n_layers);
+size_t qt_rstep06_region_words(int n_layers);
+size_t qt_rstep06_slot_words(void);
+hipError_t qt_launch_rstep06(const void *layers_dev, int n_layers, const float *final_norm, const float *rope_cos,
+                             const float *rope_sin, uint16_t *kc, uint16_t *vc, int kv_max, float eps, float scale,
+                             unsigned *reg, unsigned long long *slots, float *hid, float *decx, float *xin, int *d_pos,
+                             unsigned *epoch, int *err, int n_steps, int with_head, const uint16_t *head_w,
+                             const uint16_t *emb, int vocab, int *d_frame, int *hist, int hist_len, float *layer_out,
+                             hipStream_t st);
 /* persistent decode step (qt_pstep.hip) */
 int qt_pstep_supported(int prec, int hidden, int inter, int n_heads, int n_kv, int head_dim, int kv_max);
 size_t qt_pstep_ring_words(int hidden, int inter, int n_layers);

@@ -1,6 +1,10 @@
-// qt_rstep.hip — the Talker decode step of the 1.7B geometry with int8 weights (hidden
-// 2048, intermediate 6144, 16 query / 8 kv heads of 128) as ONE persistent cooperative
-// kernel whose workgroups each own ONE phase of the layer.
+// qt_rstep.hip — the Talker decode step with int8 weights (16 query / 8 kv heads of 128)
+// as ONE persistent cooperative kernel whose workgroups each own ONE phase of the layer.
+// Built twice: the 1.7B geometry (hidden 2048, intermediate 6144; namespace ps::rs, entry
+// points qt_rstep_* / qt_launch_rstep) and, with QT_RS_SMALL defined (qt_rstep06.hip),
+// the 0.6B geometry (hidden 1024, intermediate 3072; ps::rs06, qt_rstep06_* /
+// qt_launch_rstep06), which has half the O, GU and DN workgroups and gives the slots left
+// over to the codec head alone.
 //
 // Same math as qwen_talker_step (qwen_tts_talker.c:537-699), same arithmetic per output
 // as the per-kernel path (qt_matvec.hip, qt_attn.hip with 8 key chunks per kv head), so
@@ -30,6 +34,7 @@
 //   slots 12..13  O    xa = x + W_o . attn, 128 rows
 //   slots 14..25  GU   h = SwiGLU(W_gu . RMSNorm(xa)), 128 interleaved rows = 64 h values
 //   slots 26..31  DN   x' = xa + W_dn . h, 48 or 40 rows
+// (0.6B: O slot 12, GU 13..18, DN 19..21 with the same rows per workgroup, 22..31 idle)
 // and after the last layer every workgroup but ATT takes 16 rows of the codec head
 // (final RMSNorm, masked local argmax) and the global argmax over their 192 winners.
 //
@@ -45,24 +50,46 @@
 // stop waiting, and the launch runs to its end.
 #include "qt_step_common.h"
 
+#ifdef QT_RS_SMALL
+#define QT_RS_NS rs06
+#define QT_RS_NAME(a, b) a##06##b
+#else
+#define QT_RS_NS rs
+#define QT_RS_NAME(a, b) a##b
+#endif
+
 namespace ps {
-namespace rs {
-constexpr int H = 2048, F = 6144, NT = 256;
+namespace QT_RS_NS {
+#ifdef QT_RS_SMALL
+constexpr int H = 1024, F = 3072, XO = 1, XG = 6, XD = 3;               // O, GU, DN workgroups per XCD
+#else
+constexpr int H = 2048, F = 6144, XO = 2, XG = 12, XD = 6;
+#endif
+constexpr int NT = 256;
 constexpr unsigned SENT = 0xFFFFFFFFu;
-constexpr int XQ = 4, XATT = 8, XO = 2, XG = 12, XD = 6;                 // workgroups per XCD and role
-constexpr int SQ0 = 0, SA0 = SQ0 + XQ, SO0 = SA0 + XATT, SG0 = SO0 + XO, SD0 = SG0 + XG;
-static_assert(SD0 + XD == NB / 8, "32 workgroups per XCD");
-constexpr int NQ = 8 * XQ, NO = 8 * XO, NG = 8 * XG, ND = 8 * XD;
-constexpr int NHEAD = NQ + NO + NG + ND;         // 192: every role but attention
+constexpr int XQ = 4, XATT = 8, XI = NB / 8 - (XQ + XATT + XO + XG + XD);   // XI: head-only slots
+constexpr int SQ0 = 0, SA0 = SQ0 + XQ, SO0 = SA0 + XATT, SG0 = SO0 + XO, SD0 = SG0 + XG, SI0 = SD0 + XD;
+static_assert(XI >= 0 && SI0 + XI == NB / 8, "32 workgroups per XCD");
+constexpr int NQ = 8 * XQ, NO = 8 * XO, NG = 8 * XG, ND = 8 * XD, NI = 8 * XI;
+constexpr int NHEAD = NQ + NO + NG + ND + NI;    // 192: every workgroup but attention
 constexpr int ACH = XATT;                        // attention chunks per kv head
 constexpr int QROWS = QKVR / NQ, OROWS = H / NO, GROWS = 2 * F / NG;
 static_assert(QROWS == 128 && OROWS == 128 && GROWS == 128, "128 rows per projection workgroup");
+constexpr int EH = H / NT;                       // elements of an H-vector per thread (8 or 4)
+static_assert(EH == 4 || EH == 8, "H-vector split");
+constexpr int UD = F / 768;                      // DN: elements per h unit (three units per lane)
+static_assert(UD == 4 || UD == 8, "h split");
+constexpr int NDB = (H - 40 * ND) / 8;           // DN workgroups of 48 rows; the others take 40
+static_assert(NDB >= 0 && NDB <= ND && 48 * NDB + 40 * (ND - NDB) == H, "DN rows");
+constexpr int PCW = H > QD ? H : QD;             // widest input whose pieces LdsP holds
 constexpr int HEADR = 3072 / NHEAD;              // codec-head rows per workgroup (16)
 constexpr int ABLK = 4;                          // 128-key blocks of a chunk held resident (512 keys)
 constexpr int MAXLR = 32;
-// words of one layer's hand-off block
+// words of one layer's hand-off block (padded so that the head workgroups' clear shares
+// are equal)
 constexpr int R_QKV = 0, R_PO = R_QKV + QKVR, R_PML = R_PO + NKV * HPK * 4 * ACH * 32,
-              R_ATT = R_PML + NKV * HPK * ACH * 2, R_XA = R_ATT + QD, R_H = R_XA + H, R_X = R_H + F, LW = R_X + H;
+              R_ATT = R_PML + NKV * HPK * ACH * 2, R_XA = R_ATT + QD, R_H = R_XA + H, R_X = R_H + F,
+              LW = (R_X + H + 4 * NHEAD - 1) / (4 * NHEAD) * (4 * NHEAD);
 constexpr int CLR16 = LW / (4 * NHEAD);          // 16-byte groups of a layer block each head workgroup clears
 static_assert(CLR16 * 4 * NHEAD == LW && CLR16 <= NT, "clear shares");
 constexpr int SC1 = 16;                          // buffer cache policy: agent scope (sc1)
@@ -227,12 +254,21 @@ __device__ __forceinline__ void put4(float *x, int e0, const uint4 &v) {
 // Pieces live in plane-major LDS rows of COLS + 16 bytes (the pad puts the four planes of
 // one column range on different banks).
 template <int COLS> constexpr int pcs() { return COLS + 16; }
-template <int COLS>
-__device__ __forceinline__ void pcw_put8(uint8_t *pc, int u, const float (&v)[8], float isc) {
-    uint2 pl[4];
-    qt_pc8(v, isc, pl);
+// unit u: elements E*u .. E*u + E-1 (E = 8 or 4), E bytes of each plane
+template <int COLS, int E>
+__device__ __forceinline__ void pcw_put(uint8_t *pc, int u, const float (&v)[E], float isc) {
+    static_assert(E == 8 || E == 4, "unit size");
+    if constexpr (E == 8) {
+        uint2 pl[4];
+        qt_pc8(v, isc, pl);
 #pragma unroll
-    for (int q = 0; q < 4; q++) *reinterpret_cast<uint2 *>(pc + q * pcs<COLS>() + 8 * u) = pl[q];
+        for (int q = 0; q < 4; q++) *reinterpret_cast<uint2 *>(pc + q * pcs<COLS>() + 8 * u) = pl[q];
+    } else {
+        uint32_t pl[4];
+        qt_pc_t4(qt_pc_word(v[0], isc), qt_pc_word(v[1], isc), qt_pc_word(v[2], isc), qt_pc_word(v[3], isc), pl);
+#pragma unroll
+        for (int q = 0; q < 4; q++) *reinterpret_cast<uint32_t *>(pc + q * pcs<COLS>() + 4 * u) = pl[q];
+    }
 }
 // B fragment of columns col0 .. col0 + 63
 template <int COLS>
@@ -314,9 +350,9 @@ struct HeadLds {
     int wbi[4];
     float win[2 * NHEAD];
 };
-struct LdsP {                    // Q, O, GU (2048-column projections)
+struct LdsP {                    // Q, O, GU (and the head-only workgroups)
     float xs[H];                 // the input in element order (RMSNorm: statistics order -> unit order)
-    uint8_t pc[4 * pcs<H>()];
+    uint8_t pc[4 * pcs<PCW>()];
     int red[8 * 16][4][4];       // partial plane sums [row][wave][plane] (K split over the waves)
     float resid[OROWS];
     float wst[8];
@@ -387,13 +423,14 @@ __device__ __forceinline__ int head_phase(const Ctx &c, HeadLds &s, const THead 
     const int par = step & 1;
     const unsigned tag = c.tag0 + (unsigned)step;
     {
-        uint4 v[2];
+        constexpr int KX = H / 4 / NT;
+        uint4 v[KX];
         const unsigned base = (c.blk(par, c.L - 1) + R_X) * 4u;
         RS_MARK(step, c.L, 0);
-        wait16<2, 8>(c.rr, H / 4, [&](int i) { return base + (unsigned)i * 16u; }, v, a.err);
+        wait16<KX, 8>(c.rr, H / 4, [&](int i) { return base + (unsigned)i * 16u; }, v, a.err);
         RS_MARK(step, c.L, 1);
 #pragma unroll
-        for (int k = 0; k < 2; k++) put4<8, H>(s.x, 4 * (tid + NT * k), v[k]);
+        for (int k = 0; k < KX; k++) put4<8, H>(s.x, 4 * (tid + NT * k), v[k]);
     }
     __syncthreads();
     stage_norm<QT_BF16, H>(s.x, s.gain, a.eps, s.xn);
@@ -496,16 +533,16 @@ __device__ __forceinline__ void ksplit_row(const int (*red)[4][4], int r, int (&
 
 // Pieces of RMSNorm(x)*g: x arrives in the statistics' order (thread t: elements t + NT*k),
 // the statistics are summed in that order (thread in k order, wave butterfly, waves in
-// order: pc_stats), x goes through LDS to unit order (thread u: elements 8u .. 8u+7) and
+// order: pc_stats), x goes through LDS to unit order (thread u: elements EH*u .. +EH-1) and
 // the pieces are made there from the same values with the same operations as
 // stage_norm_pc.  gc: gains of the thread's statistics elements, gu: of its unit.  Returns
 // the pieces' scale; ends with a barrier.
-__device__ __forceinline__ float norm_pieces(const float (&xv)[8], const float (&gc)[8], const float (&gu)[8], float *xs,
+__device__ __forceinline__ float norm_pieces(const float (&xv)[EH], const float (&gc)[EH], const float (&gu)[EH], float *xs,
                                              float *wst, uint8_t *pc, float eps) {
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     float ss = 0.f, m = 0.f;
 #pragma unroll
-    for (int k = 0; k < 8; k++) {
+    for (int k = 0; k < EH; k++) {
         ss = fmaf(xv[k], xv[k], ss);
         m = fmaxf(m, fabsf(xv[k] * gc[k]));
     }
@@ -513,26 +550,33 @@ __device__ __forceinline__ float norm_pieces(const float (&xv)[8], const float (
     m = group_max<64>(m);
     if (lane == 0) { wst[2 * wave] = ss; wst[2 * wave + 1] = m; }
 #pragma unroll
-    for (int k = 0; k < 8; k++) xs[tid + NT * k] = xv[k];
+    for (int k = 0; k < EH; k++) xs[tid + NT * k] = xv[k];
     __syncthreads();
     float inv;
     QtPcScale ps;
     pc_norm_scale<4>(wst, H, eps, inv, ps);
-    const float4 p0 = *reinterpret_cast<const float4 *>(xs + 8 * tid), p1 = *reinterpret_cast<const float4 *>(xs + 8 * tid + 4);
-    const float v[8] = {(p0.x * inv) * gu[0], (p0.y * inv) * gu[1], (p0.z * inv) * gu[2], (p0.w * inv) * gu[3],
-                        (p1.x * inv) * gu[4], (p1.y * inv) * gu[5], (p1.z * inv) * gu[6], (p1.w * inv) * gu[7]};
-    pcw_put8<H>(pc, tid, v, ps.isc);
-    wave_lds_order();   // unit tid: wave w makes the pieces of columns 512w .. +511, its own K slice
+    float v[EH];
+#pragma unroll
+    for (int q = 0; q < EH / 4; q++) {
+        const float4 p = *reinterpret_cast<const float4 *>(xs + EH * tid + 4 * q);
+        v[4 * q] = (p.x * inv) * gu[4 * q]; v[4 * q + 1] = (p.y * inv) * gu[4 * q + 1];
+        v[4 * q + 2] = (p.z * inv) * gu[4 * q + 2]; v[4 * q + 3] = (p.w * inv) * gu[4 * q + 3];
+    }
+    pcw_put<H, EH>(pc, tid, v, ps.isc);
+    wave_lds_order();   // unit tid: wave w makes the pieces of columns (H/4)w .. +H/4-1, its own K slice
     return ps.s;
 }
-// the RMSNorm gains a thread needs: statistics elements tid + NT*k, unit elements 8 tid ..
-__device__ __forceinline__ void load_norm_gains(const float *g, float (&gc)[8], float (&gu)[8]) {
+// the RMSNorm gains a thread needs: statistics elements tid + NT*k, unit elements EH tid ..
+__device__ __forceinline__ void load_norm_gains(const float *g, float (&gc)[EH], float (&gu)[EH]) {
     const int tid = threadIdx.x;
     g = uni(g);
 #pragma unroll
-    for (int k = 0; k < 8; k++) gc[k] = ldg(g + tid + NT * k);
-    const float4 a = ldg(reinterpret_cast<const float4 *>(g + 8 * tid)), b = ldg(reinterpret_cast<const float4 *>(g + 8 * tid + 4));
-    gu[0] = a.x; gu[1] = a.y; gu[2] = a.z; gu[3] = a.w; gu[4] = b.x; gu[5] = b.y; gu[6] = b.z; gu[7] = b.w;
+    for (int k = 0; k < EH; k++) gc[k] = ldg(g + tid + NT * k);
+#pragma unroll
+    for (int q = 0; q < EH / 4; q++) {
+        const float4 a = ldg(reinterpret_cast<const float4 *>(g + EH * tid + 4 * q));
+        gu[4 * q] = a.x; gu[4 * q + 1] = a.y; gu[4 * q + 2] = a.z; gu[4 * q + 3] = a.w;
+    }
 }
 __device__ __forceinline__ float4 f4(const uint4 &v) {
     return make_float4(__uint_as_float(v.x), __uint_as_float(v.y), __uint_as_float(v.z), __uint_as_float(v.w));
@@ -546,11 +590,11 @@ __device__ __forceinline__ float amax4(const uint4 &v) {
 __device__ __forceinline__ void role_q(const Ctx &c, LdsP &s, int grp, int qi) {
     const RArgs &a = c.a;
     const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    // 128 rows; wave w takes columns 512w .. +511 of all of them
+    // 128 rows; wave w takes columns (H/4)w .. +H/4-1 of all of them
     const int row0 = qi < 2 ? (2 * grp + qi) * HD : qi == 2 ? QD + grp * HD : QD + KVD + grp * HD;
     RTile16<H, 8, H / 4 / 64> t;
     float rs = 0.f;
-    float gc[8], gu[8];
+    float gc[EH], gu[EH];
     auto load = [&](int l) {
         t.load(c.ly[l].w[0], row0, wave * (H / 4), row0 + QROWS);
         if (tid < QROWS) rs = ldg(uni(c.ly[l].s[0]) + row0 + tid);
@@ -565,18 +609,18 @@ __device__ __forceinline__ void role_q(const Ctx &c, LdsP &s, int grp, int qi) {
         const int par = step & 1;
         const bool last = step + 1 == a.n_steps;
         for (int l = 0; l < c.L; l++) {
-            float xv[8];
+            float xv[EH];
             if (l == 0) {
 #pragma unroll
-                for (int k = 0; k < 8; k++) xv[k] = x0_elem(a, tok, tid + NT * k);
+                for (int k = 0; k < EH; k++) xv[k] = x0_elem(a, tok, tid + NT * k);
             } else {
-                unsigned v[8];
+                unsigned v[EH];
                 const unsigned base = (c.blk(par, l - 1) + R_X) * 4u;
                 RS_MARK(step, l, 0);
-                wait4<8, 32>(c.rr, H, [&](int i) { return base + (unsigned)i * 4u; }, v, a.err);
+                wait4<EH, 32>(c.rr, H, [&](int i) { return base + (unsigned)i * 4u; }, v, a.err);
                 RS_MARK(step, l, 1);
 #pragma unroll
-                for (int k = 0; k < 8; k++) xv[k] = __uint_as_float(v[k]);
+                for (int k = 0; k < EH; k++) xv[k] = __uint_as_float(v[k]);
             }
             const float sA = norm_pieces(xv, gc, gu, s.xs, s.wst, s.pc, a.eps);
             RS_MARK(step, l, 6);
@@ -658,7 +702,7 @@ __device__ __forceinline__ void role_o(const Ctx &c, LdsP &s, int oi) {
             {
                 const float4 p0 = f4(v[0]), p1 = f4(v[1]);
                 const float v8[8] = {p0.x, p0.y, p0.z, p0.w, p1.x, p1.y, p1.z, p1.w};
-                pcw_put8<QD>(s.pc, tid, v8, ps.isc);
+                pcw_put<QD, 8>(s.pc, tid, v8, ps.isc);
             }
             wave_lds_order();   // unit tid: wave w makes the pieces of columns 512w .. +511, its own K slice
             RS_MARK(step, l, 6);
@@ -695,7 +739,7 @@ __device__ __forceinline__ void role_gu(const Ctx &c, LdsP &s, int gi) {
     const int row0 = gi * GROWS;
     RTile16<H, 8, H / 4 / 64> t;
     float rsg = 0.f, rsu = 0.f;
-    float gc[8], gu[8];
+    float gc[EH], gu[EH];
     auto load = [&](int l) {
         t.load(c.ly[l].w[2], row0, wave * (H / 4), row0 + GROWS);
         if (tid < GROWS / 2) {
@@ -713,15 +757,15 @@ __device__ __forceinline__ void role_gu(const Ctx &c, LdsP &s, int gi) {
         const int par = step & 1;
         const bool last = step + 1 == a.n_steps;
         for (int l = 0; l < c.L; l++) {
-            float xv[8];
+            float xv[EH];
             {
-                unsigned v[8];
+                unsigned v[EH];
                 const unsigned base = (c.blk(par, l) + R_XA) * 4u;
                 RS_MARK(step, l, 0);
-                wait4<8, 32>(c.rr, H, [&](int i) { return base + (unsigned)i * 4u; }, v, a.err);
+                wait4<EH, 32>(c.rr, H, [&](int i) { return base + (unsigned)i * 4u; }, v, a.err);
                 RS_MARK(step, l, 1);
 #pragma unroll
-                for (int k = 0; k < 8; k++) xv[k] = __uint_as_float(v[k]);
+                for (int k = 0; k < EH; k++) xv[k] = __uint_as_float(v[k]);
             }
             const float sD = norm_pieces(xv, gc, gu, s.xs, s.wst, s.pc, a.eps);
             RS_MARK(step, l, 6);
@@ -754,16 +798,17 @@ __device__ __forceinline__ void role_gu(const Ctx &c, LdsP &s, int gi) {
 
 // ---- DN: x' = xa + W_dn . h ---------------------------------------------------------------
 // The workgroup's 48 or 40 rows are three 16-row tiles (the third partly empty for 40);
-// wave w takes columns 1536w .. +1535 of all three (tiles 0, 1 in registers, tile 2 in
+// wave w takes columns (F/4)w .. +F/4-1 of all three (tiles 0, 1 in registers, tile 2 in
 // LDS, copied there straight from memory) and the four waves' exact partial sums are
-// added through LDS.  Thread t holds h values 8u .. 8u+7 for u = t + 256k and makes their
-// pieces from registers (the values, scale and order of stage_pc).
+// added through LDS.  Lane l of wave w holds the h units n = 192w + l + 64k (k < 3, UD
+// values each, all in the wave's own K slice) and makes their pieces from registers (the
+// values, scale and order of stage_pc).
 __device__ __forceinline__ void role_dn(const Ctx &c, LdsD &s, int di) {
     const RArgs &a = c.a;
     const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int m16 = lane & 15, kg = lane >> 4;
-    const bool big = di < 16;                  // 16 workgroups of 48 rows, 32 of 40
-    const int row0 = big ? 48 * di : 768 + 40 * (di - 16);
+    const bool big = di < NDB;                 // NDB workgroups of 48 rows, the others 40
+    const int row0 = big ? 48 * di : 48 * NDB + 40 * (di - NDB);
     const int nrows = big ? 48 : 40;
     constexpr int KW = F / 4, S = KW / 64;     // columns and 64-column steps per wave
     const int c0 = wave * KW;
@@ -789,33 +834,39 @@ __device__ __forceinline__ void role_dn(const Ctx &c, LdsD &s, int di) {
         const int par = step & 1;
         const bool last = step + 1 == a.n_steps;
         for (int l = 0; l < c.L; l++) {
-            // thread (wave w, lane) takes h units 192w + lane + 64k (8 values each), all in
-            // the wave's own K slice, and the residual rows of xa
-            uint4 v[7];
+            // thread (wave w, lane) takes h units 192w + lane + 64k (UD values, UD/4 16-byte
+            // groups each), all in the wave's own K slice, and the residual rows of xa
+            constexpr int GPU_ = UD / 4, GD = 3 * GPU_;
+            uint4 v[GD + 1];
             {
                 const unsigned bh = (c.blk(par, l) + R_H) * 4u, bx = (c.blk(par, l) + R_XA + row0) * 4u;
-                const int n16 = 6 * NT + nrows / 4;
+                const int n16 = GD * NT + nrows / 4;
                 RS_MARK(step, l, 0);
-                wait16<7, 16>(c.rr, n16, [&](int i) {
+                wait16<GD + 1, 16>(c.rr, n16, [&](int i) {
                     const int k = i / NT, t = i % NT;
-                    if (k < 6) return bh + (unsigned)(2 * (192 * (t >> 6) + (t & 63) + 64 * (k >> 1)) + (k & 1)) * 16u;
+                    if (k < GD)
+                        return bh + (unsigned)(GPU_ * (192 * (t >> 6) + (t & 63) + 64 * (k / GPU_)) + (k % GPU_)) * 16u;
                     return bx + (unsigned)t * 16u;
                 }, v, a.err);
                 RS_MARK(step, l, 1);
             }
             float m = 0.f;
 #pragma unroll
-            for (int k = 0; k < 6; k++) m = fmaxf(m, amax4(v[k]));
-            if (tid < nrows / 4) *reinterpret_cast<float4 *>(s.resid + 4 * tid) = f4(v[6]);
+            for (int k = 0; k < GD; k++) m = fmaxf(m, amax4(v[k]));
+            if (tid < nrows / 4) *reinterpret_cast<float4 *>(s.resid + 4 * tid) = f4(v[GD]);
             m = group_max<64>(m);
             if (lane == 0) s.wst[wave] = m;
             __syncthreads();
             const QtPcScale ps = qt_pc_scale(fmaxf(fmaxf(s.wst[0], s.wst[1]), fmaxf(s.wst[2], s.wst[3])));
 #pragma unroll
             for (int k = 0; k < 3; k++) {
-                const float4 p0 = f4(v[2 * k]), p1 = f4(v[2 * k + 1]);
-                const float v8[8] = {p0.x, p0.y, p0.z, p0.w, p1.x, p1.y, p1.z, p1.w};
-                pcw_put8<F>(s.pc, 192 * wave + lane + 64 * k, v8, ps.isc);
+                float vu[UD];
+#pragma unroll
+                for (int g2 = 0; g2 < GPU_; g2++) {
+                    const float4 p = f4(v[GPU_ * k + g2]);
+                    vu[4 * g2] = p.x; vu[4 * g2 + 1] = p.y; vu[4 * g2 + 2] = p.z; vu[4 * g2 + 3] = p.w;
+                }
+                pcw_put<F, UD>(s.pc, 192 * wave + lane + 64 * k, vu, ps.isc);
             }
             wave_lds_order();   // the wave's own K slice
             RS_MARK(step, l, 6);
@@ -1154,6 +1205,27 @@ __device__ __forceinline__ void role_att(const Ctx &c, LdsA &s, int g, int ch) {
     }
 }
 
+// ---- head only (the slots the 0.6B geometry leaves over) ------------------------------------
+// Takes part in every step's head phase; clears its shares of the previous step's region at
+// the start of the step (every read of that region came before the previous step's winner
+// exchange, which this workgroup has completed).
+__device__ __forceinline__ void role_idle(const Ctx &c, LdsP &s) {
+    const RArgs &a = c.a;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    THead th;
+    load_gains<4, 8, H>(a.final_norm, s.hd.gain);
+    land();
+    for (int step = 0; step < a.n_steps; step++) {
+        const int par = step & 1;
+        const bool last = step + 1 == a.n_steps;
+        if (step > 0)
+            for (int l = 0; l < c.L; l++) clear_share(c, par ^ 1, l);
+        if (a.with_head) th.load(a.head_w, nullptr, c.hc * HEADR + wave * (HEADR / 4));
+        land();
+        head_phase(c, s.hd, th, step, last);
+    }
+}
+
 __global__ __launch_bounds__(NT, 1) void k_rstep(RArgs a) {
     __shared__ __align__(16) unsigned char lds[LDS_BYTES];
     __shared__ Layer s_layers[MAXLR];
@@ -1166,28 +1238,32 @@ __global__ __launch_bounds__(NT, 1) void k_rstep(RArgs a) {
     if (slot < SA0) hc = (slot - SQ0) * 8 + x;
     else if (slot >= SO0 && slot < SG0) hc = NQ + (slot - SO0) * 8 + x;
     else if (slot >= SG0 && slot < SD0) hc = NQ + NO + (slot - SG0) * 8 + x;
-    else if (slot >= SD0) hc = NQ + NO + NG + (slot - SD0) * 8 + x;
+    else if (slot >= SD0 && slot < SI0) hc = NQ + NO + NG + (slot - SD0) * 8 + x;
+    else if (slot >= SI0) hc = NQ + NO + NG + ND + (slot - SI0) * 8 + x;
     const Ctx c{a, s_layers, brsrc(a.reg), a.n_layers, *a.d_pos, a.with_head ? *a.d_frame : 0, *a.epoch, hc};
     if (slot < SA0) role_q(c, *reinterpret_cast<LdsP *>(lds), x, slot - SQ0);
     else if (slot < SO0) role_att(c, *reinterpret_cast<LdsA *>(lds), x, slot - SA0);
     else if (slot < SG0) role_o(c, *reinterpret_cast<LdsP *>(lds), (slot - SO0) * 8 + x);
     else if (slot < SD0) role_gu(c, *reinterpret_cast<LdsP *>(lds), (slot - SG0) * 8 + x);
-    else role_dn(c, *reinterpret_cast<LdsD *>(lds), (slot - SD0) * 8 + x);
+    else if (XI == 0 || slot < SI0) role_dn(c, *reinterpret_cast<LdsD *>(lds), (slot - SD0) * 8 + x);
+    else role_idle(c, *reinterpret_cast<LdsP *>(lds));
 }
-}  // namespace rs
+}  // namespace QT_RS_NS
 }  // namespace ps
 
 #ifdef QT_RSTEP_TRACE
-extern "C" hipError_t qt_rstep_trace_read(unsigned long long *out) {
-    return hipMemcpyFromSymbol(out, HIP_SYMBOL(ps::rs::rs_trace), sizeof(ps::rs::rs_trace), 0, hipMemcpyDeviceToHost);
+extern "C" hipError_t QT_RS_NAME(qt_rstep, _trace_read)(unsigned long long *out) {
+    return hipMemcpyFromSymbol(out, HIP_SYMBOL(ps::QT_RS_NS::rs_trace), sizeof(ps::QT_RS_NS::rs_trace), 0,
+                               hipMemcpyDeviceToHost);
 }
 #endif
 
-extern "C" int qt_rstep_supported(int prec, int hidden, int inter, int n_heads, int n_kv, int head_dim, int kv_max,
-                                  int n_layers) {
-    if (prec != QT_INT8 || hidden != ps::rs::H || inter != ps::rs::F) return 0;
+extern "C" int QT_RS_NAME(qt_rstep, _supported)(int prec, int hidden, int inter, int n_heads, int n_kv, int head_dim,
+                                                int kv_max, int n_layers) {
+    if (prec != QT_INT8 || hidden != ps::QT_RS_NS::H || inter != ps::QT_RS_NS::F) return 0;
     if (n_heads != ps::NH || n_kv != ps::NKV || head_dim != ps::HD) return 0;
-    if (kv_max > ps::rs::ACH * ps::rs::ABLK * ps::KVB || n_layers < 1 || n_layers > ps::rs::MAXLR) return 0;
+    if (kv_max > ps::QT_RS_NS::ACH * ps::QT_RS_NS::ABLK * ps::KVB || n_layers < 1 || n_layers > ps::QT_RS_NS::MAXLR)
+        return 0;
     int dev = 0, cus = 0, coop = 0;
     if (hipGetDevice(&dev) != hipSuccess) return 0;
     if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
@@ -1195,18 +1271,23 @@ extern "C" int qt_rstep_supported(int prec, int hidden, int inter, int n_heads, 
     return coop && cus >= ps::NB;
 }
 // hand-off words (both parities) and winner words
-extern "C" size_t qt_rstep_region_words(int n_layers) { return (size_t)2 * n_layers * ps::rs::LW; }
-extern "C" size_t qt_rstep_slot_words(void) { return (size_t)2 * ps::rs::NHEAD * 2; }
-// attention key chunks per kv head (the per-kernel attention must use the same split)
+extern "C" size_t QT_RS_NAME(qt_rstep, _region_words)(int n_layers) { return (size_t)2 * n_layers * ps::QT_RS_NS::LW; }
+extern "C" size_t QT_RS_NAME(qt_rstep, _slot_words)(void) { return (size_t)2 * ps::QT_RS_NS::NHEAD * 2; }
+#ifndef QT_RS_SMALL
+// attention key chunks per kv head, both geometries (the per-kernel attention must use the
+// same split)
 extern "C" int qt_rstep_chunks(void) { return ps::rs::ACH; }
+#endif
 
-extern "C" hipError_t qt_launch_rstep(const void *layers_dev, int n_layers, const float *final_norm, const float *rope_cos,
-                                      const float *rope_sin, uint16_t *kc, uint16_t *vc, int kv_max, float eps, float scale,
-                                      unsigned *reg, unsigned long long *slots, float *hid, float *decx, float *xin,
-                                      int *d_pos, unsigned *epoch, int *err, int n_steps, int with_head,
-                                      const uint16_t *head_w, const uint16_t *emb, int vocab, int *d_frame, int *hist,
-                                      int hist_len, float *layer_out, hipStream_t st) {
-    ps::rs::RArgs a;
+extern "C" hipError_t QT_RS_NAME(qt_launch_rstep, )(const void *layers_dev, int n_layers, const float *final_norm,
+                                                    const float *rope_cos, const float *rope_sin, uint16_t *kc,
+                                                    uint16_t *vc, int kv_max, float eps, float scale, unsigned *reg,
+                                                    unsigned long long *slots, float *hid, float *decx, float *xin,
+                                                    int *d_pos, unsigned *epoch, int *err, int n_steps, int with_head,
+                                                    const uint16_t *head_w, const uint16_t *emb, int vocab, int *d_frame,
+                                                    int *hist, int hist_len, float *layer_out, hipStream_t st) {
+    namespace rs = ps::QT_RS_NS;
+    rs::RArgs a;
     a.layers = (const ps::Layer *)layers_dev; a.n_layers = n_layers;
     a.final_norm = final_norm; a.rope_cos = rope_cos; a.rope_sin = rope_sin;
     a.kc = kc; a.vc = vc; a.kv_max = kv_max; a.eps = eps; a.scale = scale;
@@ -1214,11 +1295,11 @@ extern "C" hipError_t qt_launch_rstep(const void *layers_dev, int n_layers, cons
     a.err = err; a.n_steps = n_steps; a.with_head = with_head;
     a.head_w = (const uint8_t *)head_w; a.emb = emb; a.vocab = vocab;
     a.d_frame = d_frame; a.hist = hist; a.hist_len = hist_len; a.layer_out = layer_out;
-    if (n_steps <= 0 || n_layers <= 0 || n_layers > ps::rs::MAXLR || kv_max > ps::rs::ACH * ps::rs::ABLK * ps::KVB)
+    if (n_steps <= 0 || n_layers <= 0 || n_layers > rs::MAXLR || kv_max > rs::ACH * rs::ABLK * ps::KVB)
         return hipErrorInvalidValue;
     if (!with_head && n_steps != 1) return hipErrorInvalidValue;   // without the head the next input is unknown
-    if (with_head && (vocab != ps::rs::NHEAD * ps::rs::HEADR || !head_w || !emb || !d_frame || !hist || hist_len <= 0))
+    if (with_head && (vocab != rs::NHEAD * rs::HEADR || !head_w || !emb || !d_frame || !hist || hist_len <= 0))
         return hipErrorInvalidValue;
     void *args[] = {(void *)&a};
-    return hipLaunchCooperativeKernel((const void *)ps::rs::k_rstep, dim3(ps::NB), dim3(ps::rs::NT), args, 0, st);
+    return hipLaunchCooperativeKernel((const void *)rs::k_rstep, dim3(ps::NB), dim3(rs::NT), args, 0, st);
 }

@@ -313,7 +313,8 @@ typedef struct {
     int ps_on;
     void *ps_layers;        /* device layer table */
     unsigned long long *ps_ring;   /* tagged activation words */
-    int rs_on;              /* the role-specialised kernel (qt_rstep.hip) runs the fused step */
+    int rs_on;              /* the role-specialised kernel (qt_rstep.hip) runs the fused step: 1 its 1.7B
+                             * build, 2 its 0.6B build (qt_rstep06.hip) */
     unsigned *rs_reg;       /* its hand-off words, [2][L][layer block], sentinel when empty */
     unsigned long long *rs_slots;  /* its tagged winner words */
     float *ps_xin;          /* step-0 input of a launch */
@@ -336,6 +337,14 @@ static int rstep_enabled(void) {
     static int on = -1;
     if (on < 0) { const char *e = getenv("QWEN_HIP_RSTEP"); on = !(e && e[0] == '0'); }
     return on;
+}
+
+/* Which build of the role-specialised kernel covers the stack: 1 (1.7B), 2 (0.6B), 0 none. */
+static int rs_kind(const stack_t *s) {
+    if (!rstep_enabled()) return 0;
+    if (qt_rstep_supported(s->prec, s->H, s->F, s->nh, s->nkv, s->hd, s->kv_max, s->L)) return 1;
+    if (qt_rstep06_supported(s->prec, s->H, s->F, s->nh, s->nkv, s->hd, s->kv_max, s->L)) return 2;
+    return 0;
 }
 
 static int persistent_enabled(void) {
@@ -375,17 +384,19 @@ static int ps_setup(talker_t *t) {
     const size_t lb = qt_pstep_layer_bytes();
     const size_t words = qt_pstep_ring_words(s->H, s->F, s->L);
     const unsigned one = 1;   /* ring words start with tag 0: the first step is tag 1 */
-    if (rstep_enabled() && qt_rstep_supported(s->prec, s->H, s->F, s->nh, s->nkv, s->hd, s->kv_max, s->L)) {
+    const int rk = rs_kind(s);
+    if (rk) {
         /* hand-off words start empty (0xFF bytes: the sentinel), winner words with tag 0;
          * the per-kernel step splits attention into the same key chunks */
-        const size_t rw = qt_rstep_region_words(s->L), sw = qt_rstep_slot_words();
+        const size_t rw = rk == 2 ? qt_rstep06_region_words(s->L) : qt_rstep_region_words(s->L);
+        const size_t sw = rk == 2 ? qt_rstep06_slot_words() : qt_rstep_slot_words();
         HCK(hipMalloc((void **)&t->rs_reg, rw * sizeof(unsigned)));
         HCK(hipMalloc((void **)&t->rs_slots, sw * sizeof(unsigned long long)));
         HCK(hipMemsetAsync(t->rs_reg, 0xFF, rw * sizeof(unsigned), t->st));
         HCK(hipMemsetAsync(t->rs_slots, 0, sw * sizeof(unsigned long long), t->st));
         s->step_G = qt_rstep_chunks();
         s->step_onepass = 1;
-        t->rs_on = 1;
+        t->rs_on = rk;
     }
     HCK(hipMalloc((void **)&t->ps_ring, (t->rs_on ? 1 : words) * sizeof(unsigned long long)));
     HCK(hipMalloc((void **)&t->ps_epoch, 64));
@@ -420,7 +431,7 @@ fail:
 static hipError_t ps_launch_ex(talker_t *t, int n_steps, int with_head, float *layer_out) {
     stack_t *s = &t->s;
     if (t->rs_on)
-        return qt_launch_rstep(t->ps_layers, s->L, s->final_norm, s->rope_cos, s->rope_sin, s->kc, s->vc, s->kv_max, s->eps,
+        return (t->rs_on == 2 ? qt_launch_rstep06 : qt_launch_rstep)(t->ps_layers, s->L, s->final_norm, s->rope_cos, s->rope_sin, s->kc, s->vc, s->kv_max, s->eps,
                                1.0f / sqrtf((float)s->hd), t->rs_reg, t->rs_slots, t->io, t->io + s->H, t->ps_xin, t->d_pos,
                                t->ps_epoch, t->ps_err, n_steps, with_head,
                                with_head ? (const uint16_t *)t->head_m.w : NULL, with_head ? t->codec_emb : NULL,
@@ -451,7 +462,7 @@ static int ps_check(talker_t *t) {
  * with the same device position, step tag and next input. */
 static int ps_reselect(talker_t *t) {
     stack_t *s = &t->s;
-    if (rstep_enabled() && qt_rstep_supported(s->prec, s->H, s->F, s->nh, s->nkv, s->hd, s->kv_max, s->L)) {
+    if (rs_kind(s)) {
         s->step_G = qt_rstep_chunks();
         s->step_onepass = 1;
         return 0;
