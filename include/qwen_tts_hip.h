@@ -232,6 +232,11 @@ int   qwen_hip_cp_frame(void *state, const float *talker_hidden, int code0, int 
 int   qwen_hip_cp_frame_async(void *state, int n_frames);
 int   qwen_hip_cp_sync(void *state);
 void *qwen_hip_cp_stream(void *state);
+/* Test/measurement switch (no reference counterpart): frames as one launch of the
+ * role-specialised kernel (on = 1, the default where the CP qualifies: 0.6B geometry, int8
+ * layers and lm heads, no mtp projection, two-position prefill off) or as the per-kernel
+ * launch graph (0); both give the same bits.  Returns the mode in effect, -1 on error. */
+int   qwen_hip_cp_fused(void *state, int on);
 /* replaces qwen_cuda_cp_free                     (qwen_tts_cuda_talker.cu:917) */
 void  qwen_hip_cp_free(void *state);
 /* Diagnostic (no reference counterpart; what the reference keeps in ctx->cp_kv_k/cp_kv_v

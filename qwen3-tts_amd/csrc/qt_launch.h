@@ -98,6 +98,11 @@ hipError_t qt_launch_rstep(const void *layers_dev, int n_layers, const float *fi
                            unsigned *epoch, int *err, int n_steps, int with_head, const uint16_t *head_w,
                            const uint16_t *emb, int vocab, int *d_frame, int *hist, int hist_len, float *layer_out,
                            hipStream_t st);
+hipError_t qt_launch_rstep06_cp(const void *layers_dev, int n_layers, const float *final_norm, const float *rope_cos,
+                                const float *rope_sin, uint16_t *kc, uint16_t *vc, int kv_max, float eps, float scale,
+                                unsigned *reg, unsigned long long *slots, float *hid, float *decx, float *xin,
+                                int *d_pos, unsigned *epoch, int *err, int n_passes, const void *const *cp_tab,
+                                int vocab, int *codes, hipStream_t st);
 int qt_rstep06_supported(int prec, int hidden, int inter, int n_heads, int n_kv, int head_dim, int kv_max, int n_layers);
 size_t qt_rstep06_region_words(int n_layers);
 size_t qt_rstep06_slot_words(void);

@@ -137,6 +137,16 @@ struct RArgs {
     int *d_frame, *hist;
     int hist_len;
     float *layer_out;             // optional [L][H]: every layer's output x of the last step
+    // Code Predictor frame (0.6B build only): step s is pass s at position s; the input of
+    // pass 0 is xin, of pass s >= 1 row codes[s-1] of table cp_emb[s-1]; after pass s >= 1
+    // int8 lm head s-1 (rows cp_head[s-1], scales cp_hs[s-1], `vocab` rows) on the
+    // final-normed x gives codes[s] (plain argmax, lowest index on ties).  Device arrays of
+    // 15 pointers each; codes[0] is the frame's input code.
+    int cp;
+    const uint8_t *const *cp_head;
+    const float *const *cp_hs;
+    const uint16_t *const *cp_emb;
+    int *cp_codes;
 };
 
 // ---- hand-off words ---------------------------------------------------------------------
@@ -169,7 +179,7 @@ __device__ __forceinline__ void wave_lds_order() { asm volatile("" ::: "memory")
 template <int K, int PST, typename OffF>
 __device__ __forceinline__ void wait16(__amdgpu_buffer_rsrc_t r, int n16, OffF off, uint4 (&v)[K], int *err) {
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    if (PST > 0) {
+    if constexpr (PST > 0) {
         const int j = lane * 4 + wave, np = (n16 + PST - 1) / PST;
         const bool act = j < np;
         for (unsigned it = 0;; it++) {
@@ -205,7 +215,7 @@ __device__ __forceinline__ void wait16(__amdgpu_buffer_rsrc_t r, int n16, OffF o
 template <int K, int PST, typename OffF>
 __device__ __forceinline__ void wait4(__amdgpu_buffer_rsrc_t r, int n, OffF off, unsigned (&v)[K], int *err) {
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    if (PST > 0) {
+    if constexpr (PST > 0) {
         const int j = lane * 4 + wave, np = (n + PST - 1) / PST;
         const bool act = j < np;
         for (unsigned it = 0;; it++) {
@@ -349,6 +359,13 @@ struct HeadLds {
     float wbv[4];
     int wbi[4];
     float win[2 * NHEAD];
+#ifdef QT_RS_SMALL
+    float cxs[H];                // Code Predictor lm head: the input in unit order
+    float cwst[8];
+    uint8_t cpc[4 * pcs<H>()];   // pieces of RMSNorm(x) * final_norm
+    int cred[16][4][4];          // partial plane sums [row][wave][plane]
+    float clg[HEADR];            // the workgroup's logits
+#endif
 };
 struct LdsP {                    // Q, O, GU (and the head-only workgroups)
     float xs[H];                 // the input in element order (RMSNorm: statistics order -> unit order)
@@ -410,104 +427,13 @@ __device__ __forceinline__ void clear_share(const Ctx &c, int par, int l) {
     }
 }
 
-// Layer-0 input element i of a step: the embedding of the previous step's token, or xin.
-__device__ __forceinline__ float x0_elem(const RArgs &a, int tok, int i) {
+// Layer-0 input element i of a step: the embedding of the previous step's token, or xin
+// (Code Predictor: xin for pass 0, else row tok of that pass's table).
+__device__ __forceinline__ float x0_elem(const RArgs &a, int tok, int i, int step) {
+#ifdef QT_RS_SMALL
+    if (a.cp) return step == 0 ? ldg(a.xin + i) : bf16f(ldg(uni(ldg(a.cp_emb + step - 1)) + (size_t)tok * H + i));
+#endif
     return tok < 0 ? ldg(a.xin + i) : bf16f(ldg(a.emb + (size_t)tok * H + i));
-}
-
-// ---- head (final norm, codec head rows, masked local argmax, global argmax) ------------
-using THead = Tile<QT_BF16, H, HEADR / 4>;
-__device__ __forceinline__ int head_phase(const Ctx &c, HeadLds &s, const THead &th, int step, bool last) {
-    const RArgs &a = c.a;
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int par = step & 1;
-    const unsigned tag = c.tag0 + (unsigned)step;
-    {
-        constexpr int KX = H / 4 / NT;
-        uint4 v[KX];
-        const unsigned base = (c.blk(par, c.L - 1) + R_X) * 4u;
-        RS_MARK(step, c.L, 0);
-        wait16<KX, 8>(c.rr, H / 4, [&](int i) { return base + (unsigned)i * 16u; }, v, a.err);
-        RS_MARK(step, c.L, 1);
-#pragma unroll
-        for (int k = 0; k < KX; k++) put4<8, H>(s.x, 4 * (tid + NT * k), v[k]);
-    }
-    __syncthreads();
-    stage_norm<QT_BF16, H>(s.x, s.gain, a.eps, s.xn);
-    if (last && c.hc == 0)
-        for (int i = tid; i < H; i += NT) { a.hid[i] = s.xn[xpos<8, H>(i)]; a.decx[i] = s.x[xpos<8, H>(i)]; }
-    float bv = -INFINITY;
-    int bi = 0x7FFFFFFF;
-    if (a.with_head) {
-        float acc[HEADR / 4];
-        tile_dot<QT_BF16, H, HEADR / 4>(th, s.xn, acc);
-        const int frame = c.frame0 + step;
-        if (lane == 0) {
-#pragma unroll
-            for (int r = 0; r < HEADR / 4; r++) {
-                const int i = c.hc * HEADR + wave * (HEADR / 4) + r;
-                float v = fminf(fmaxf(acc[r], -100.0f), 100.0f);
-                if (i >= 2048 && i != 2150) v = -1e30f;
-                if (i == 2150 && frame < 2) v = -1e30f;
-                if (v > bv || (v == bv && i < bi)) { bv = v; bi = i; }
-            }
-            s.wbv[wave] = bv; s.wbi[wave] = bi;
-        }
-        __syncthreads();
-        bv = s.wbv[0]; bi = s.wbi[0];
-        for (int w = 1; w < 4; w++)
-            if (s.wbv[w] > bv || (s.wbv[w] == bv && s.wbi[w] < bi)) { bv = s.wbv[w]; bi = s.wbi[w]; }
-    }
-    // every store of this workgroup (the clears of the previous step's region among them)
-    // is performed before the winner is visible: they are agent-scope (write-through)
-    // stores, so their acknowledgements are the release (a release fence would also write
-    // back the XCD's whole L2, several microseconds)
-    land();
-    __syncthreads();
-    unsigned long long *slots = a.slots + (size_t)par * NHEAD * 2;
-    if (tid == 0) {
-        st_tag(slots + 2 * c.hc, bv, tag);
-        st_tag(slots + 2 * c.hc + 1, __int_as_float(bi), tag);
-    }
-    RS_MARK(step, c.L, 2);
-    gather<2, NT>(2 * NHEAD, [&](int i) { return slots + i; }, s.win, tag, a.err);
-    RS_MARK(step, c.L, 4);
-    float gv = -INFINITY;
-    int gi = 0x7FFFFFFF;
-    for (int i = tid; i < NHEAD; i += NT) {
-        const float v = s.win[2 * i];
-        const int ix = __float_as_int(s.win[2 * i + 1]);
-        if (v > gv || (v == gv && ix < gi)) { gv = v; gi = ix; }
-    }
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) {
-        const float ov = __shfl_xor(gv, o, 64);
-        const int oi = __shfl_xor(gi, o, 64);
-        if (ov > gv || (ov == gv && oi < gi)) { gv = ov; gi = oi; }
-    }
-    __syncthreads();
-    if (lane == 0) { s.wbv[wave] = gv; s.wbi[wave] = gi; }
-    __syncthreads();
-    gv = s.wbv[0]; gi = s.wbi[0];
-    for (int w = 1; w < 4; w++)
-        if (s.wbv[w] > gv || (s.wbv[w] == gv && s.wbi[w] < gi)) { gv = s.wbv[w]; gi = s.wbi[w]; }
-    if (gi < 0 || gi >= a.vocab) gi = 0;
-    if (a.with_head && c.hc == 0 && tid == 0) a.hist[(c.frame0 + step) % a.hist_len] = gi;
-    __syncthreads();
-    if (last)   // every read of this step's region is done (all of them precede the winners)
-        for (int l = 0; l < c.L; l++) clear_share(c, par, l);
-    return a.with_head ? gi : -1;
-}
-
-// 16-byte / 8-byte agent-scope stores of hand-off words
-__device__ __forceinline__ void put4w(const Ctx &c, unsigned word, float a0, float a1, float a2, float a3) {
-    const u32x4_t v = {__float_as_uint(a0), __float_as_uint(a1), __float_as_uint(a2), __float_as_uint(a3)};
-    __builtin_amdgcn_raw_buffer_store_b128(v, c.rr, word * 4u, 0, SC1);
-}
-__device__ __forceinline__ void put2w(const Ctx &c, unsigned word, float a0, float a1) {
-    typedef unsigned u32x2_t __attribute__((ext_vector_type(2)));
-    const u32x2_t v = {__float_as_uint(a0), __float_as_uint(a1)};
-    __builtin_amdgcn_raw_buffer_store_b64(v, c.rr, word * 4u, 0, SC1);
 }
 
 // K split over the waves: each wave's partial plane sums of its tiles' rows into
@@ -586,6 +512,155 @@ __device__ __forceinline__ float amax4(const uint4 &v) {
                  fmaxf(fabsf(__uint_as_float(v.z)), fabsf(__uint_as_float(v.w))));
 }
 
+// ---- head (final norm, codec head rows, masked local argmax, global argmax) ------------
+using THead = Tile<QT_BF16, H, HEADR / 4>;
+// The head rows of a workgroup for the step about to end: the Talker's bf16 codec head, or
+// (Code Predictor) 16 rows of the pass's int8 lm head, one 16-row MFMA tile with the
+// columns split over the waves as in the projections.
+struct HeadTile {
+    THead th;
+#ifdef QT_RS_SMALL
+    RTile16<H, 1, H / 4 / 64> tc;
+    float tcs = 0.f;             // row scale of row hc*HEADR + tid (tid < HEADR)
+#endif
+    __device__ __forceinline__ void load(const RArgs &a, int hc, int wave, int step) {
+        if (a.with_head) th.load(a.head_w, nullptr, hc * HEADR + wave * (HEADR / 4));
+#ifdef QT_RS_SMALL
+        else if (a.cp && step > 0) {
+            const int tid = threadIdx.x, r0 = hc * HEADR;
+            tc.load(uni(ldg(a.cp_head + step - 1)), r0, wave * (H / 4), a.vocab);
+            tcs = (tid < HEADR && r0 + tid < a.vocab) ? ldg(uni(ldg(a.cp_hs + step - 1)) + r0 + tid) : 0.f;
+        }
+#endif
+    }
+};
+__device__ __forceinline__ int head_phase(const Ctx &c, HeadLds &s, const HeadTile &ht, int step, bool last) {
+    const RArgs &a = c.a;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int par = step & 1;
+    const unsigned tag = c.tag0 + (unsigned)step;
+    {
+        constexpr int KX = H / 4 / NT;
+        uint4 v[KX];
+        const unsigned base = (c.blk(par, c.L - 1) + R_X) * 4u;
+        RS_MARK(step, c.L, 0);
+        wait16<KX, 8>(c.rr, H / 4, [&](int i) { return base + (unsigned)i * 16u; }, v, a.err);
+        RS_MARK(step, c.L, 1);
+#pragma unroll
+        for (int k = 0; k < KX; k++) put4<8, H>(s.x, 4 * (tid + NT * k), v[k]);
+    }
+    __syncthreads();
+    stage_norm<QT_BF16, H>(s.x, s.gain, a.eps, s.xn);
+    if (last && c.hc == 0)
+        for (int i = tid; i < H; i += NT) { a.hid[i] = s.xn[xpos<8, H>(i)]; a.decx[i] = s.x[xpos<8, H>(i)]; }
+    float bv = -INFINITY;
+    int bi = 0x7FFFFFFF;
+    if (a.with_head) {
+        float acc[HEADR / 4];
+        tile_dot<QT_BF16, H, HEADR / 4>(ht.th, s.xn, acc);
+        const int frame = c.frame0 + step;
+        if (lane == 0) {
+#pragma unroll
+            for (int r = 0; r < HEADR / 4; r++) {
+                const int i = c.hc * HEADR + wave * (HEADR / 4) + r;
+                float v = fminf(fmaxf(acc[r], -100.0f), 100.0f);
+                if (i >= 2048 && i != 2150) v = -1e30f;
+                if (i == 2150 && frame < 2) v = -1e30f;
+                if (v > bv || (v == bv && i < bi)) { bv = v; bi = i; }
+            }
+            s.wbv[wave] = bv; s.wbi[wave] = bi;
+        }
+        __syncthreads();
+        bv = s.wbv[0]; bi = s.wbi[0];
+        for (int w = 1; w < 4; w++)
+            if (s.wbv[w] > bv || (s.wbv[w] == bv && s.wbi[w] < bi)) { bv = s.wbv[w]; bi = s.wbi[w]; }
+    }
+#ifdef QT_RS_SMALL
+    else if (a.cp && step > 0) {
+        // the lm head on the pieces of RMSNorm(x) * final_norm, made in k_mv's int8 order
+        // (the per-kernel frame's lm-head matvec), so the logits are the same bits; plain
+        // argmax from the start value -1e30, lowest index on ties (k_select mode 0)
+        float xv[EH], gc[EH], gu[EH];
+        load_norm_gains(a.final_norm, gc, gu);
+#pragma unroll
+        for (int k = 0; k < EH; k++) xv[k] = s.x[xpos<8, H>(tid + NT * k)];
+        const float sA = norm_pieces(xv, gc, gu, s.cxs, s.cwst, s.cpc, a.eps);
+        i32x4 acc[1];
+        rdot16<H, 1, H / 4 / 64, 1>(ht.tc, s.cpc, wave * (H / 4), acc);
+        ksplit_store<1>(acc, s.cred);
+        if (tid < HEADR) {
+            int d[4];
+            ksplit_row(s.cred, tid, d);
+            s.clg[tid] = __fmul_rn(qt_pc_dot(d[0], d[1], d[2], d[3], sA), ht.tcs);
+        }
+        __syncthreads();
+        bv = -1e30f;
+        for (int r = 0; r < HEADR; r++) {
+            const int i = c.hc * HEADR + r;
+            const float v = s.clg[r];
+            if (i < a.vocab && (v > bv || (v == bv && i < bi))) { bv = v; bi = i; }
+        }
+    }
+#endif
+    // every store of this workgroup (the clears of the previous step's region among them)
+    // is performed before the winner is visible: they are agent-scope (write-through)
+    // stores, so their acknowledgements are the release (a release fence would also write
+    // back the XCD's whole L2, several microseconds)
+    land();
+    __syncthreads();
+    unsigned long long *slots = a.slots + (size_t)par * NHEAD * 2;
+    if (tid == 0) {
+        st_tag(slots + 2 * c.hc, bv, tag);
+        st_tag(slots + 2 * c.hc + 1, __int_as_float(bi), tag);
+    }
+    RS_MARK(step, c.L, 2);
+    gather<2, NT>(2 * NHEAD, [&](int i) { return slots + i; }, s.win, tag, a.err);
+    RS_MARK(step, c.L, 4);
+    float gv = -INFINITY;
+    int gi = 0x7FFFFFFF;
+    for (int i = tid; i < NHEAD; i += NT) {
+        const float v = s.win[2 * i];
+        const int ix = __float_as_int(s.win[2 * i + 1]);
+        if (v > gv || (v == gv && ix < gi)) { gv = v; gi = ix; }
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        const float ov = __shfl_xor(gv, o, 64);
+        const int oi = __shfl_xor(gi, o, 64);
+        if (ov > gv || (ov == gv && oi < gi)) { gv = ov; gi = oi; }
+    }
+    __syncthreads();
+    if (lane == 0) { s.wbv[wave] = gv; s.wbi[wave] = gi; }
+    __syncthreads();
+    gv = s.wbv[0]; gi = s.wbi[0];
+    for (int w = 1; w < 4; w++)
+        if (s.wbv[w] > gv || (s.wbv[w] == gv && s.wbi[w] < gi)) { gv = s.wbv[w]; gi = s.wbi[w]; }
+    if (gi < 0 || gi >= a.vocab) gi = 0;
+    if (a.with_head && c.hc == 0 && tid == 0) a.hist[(c.frame0 + step) % a.hist_len] = gi;
+#ifdef QT_RS_SMALL
+    if (a.cp) {
+        if (step == 0) gi = ldg(a.cp_codes);   // pass 1 reads the frame's input code
+        else if (c.hc == 0 && tid == 0) a.cp_codes[step] = gi;
+    }
+#endif
+    __syncthreads();
+    if (last)   // every read of this step's region is done (all of them precede the winners)
+        for (int l = 0; l < c.L; l++) clear_share(c, par, l);
+    return (a.with_head || a.cp) ? gi : -1;
+}
+
+// 16-byte / 8-byte agent-scope stores of hand-off words
+__device__ __forceinline__ void put4w(const Ctx &c, unsigned word, float a0, float a1, float a2, float a3) {
+    const u32x4_t v = {__float_as_uint(a0), __float_as_uint(a1), __float_as_uint(a2), __float_as_uint(a3)};
+    __builtin_amdgcn_raw_buffer_store_b128(v, c.rr, word * 4u, 0, SC1);
+}
+__device__ __forceinline__ void put2w(const Ctx &c, unsigned word, float a0, float a1) {
+    typedef unsigned u32x2_t __attribute__((ext_vector_type(2)));
+    const u32x2_t v = {__float_as_uint(a0), __float_as_uint(a1)};
+    __builtin_amdgcn_raw_buffer_store_b64(v, c.rr, word * 4u, 0, SC1);
+}
+
+
 // ---- Q: q|k|v rows ------------------------------------------------------------------------
 __device__ __forceinline__ void role_q(const Ctx &c, LdsP &s, int grp, int qi) {
     const RArgs &a = c.a;
@@ -600,7 +675,7 @@ __device__ __forceinline__ void role_q(const Ctx &c, LdsP &s, int grp, int qi) {
         if (tid < QROWS) rs = ldg(uni(c.ly[l].s[0]) + row0 + tid);
         load_norm_gains(c.ly[l].in_norm, gc, gu);
     };
-    THead th;
+    HeadTile ht;
     load_gains<4, 8, H>(a.final_norm, s.hd.gain);
     load(0);
     land();
@@ -612,7 +687,7 @@ __device__ __forceinline__ void role_q(const Ctx &c, LdsP &s, int grp, int qi) {
             float xv[EH];
             if (l == 0) {
 #pragma unroll
-                for (int k = 0; k < EH; k++) xv[k] = x0_elem(a, tok, tid + NT * k);
+                for (int k = 0; k < EH; k++) xv[k] = x0_elem(a, tok, tid + NT * k, step);
             } else {
                 unsigned v[EH];
                 const unsigned base = (c.blk(par, l - 1) + R_X) * 4u;
@@ -643,9 +718,9 @@ __device__ __forceinline__ void role_q(const Ctx &c, LdsP &s, int grp, int qi) {
         }
         // the codec-head tile is loaded here, not inside the layer loop, so that its
         // registers are live only for the head
-        if (a.with_head) th.load(a.head_w, nullptr, c.hc * HEADR + wave * (HEADR / 4));
+        ht.load(a, c.hc, wave, step);
         land();
-        tok = head_phase(c, s.hd, th, step, last);
+        tok = head_phase(c, s.hd, ht, step, last);
     }
     if (c.hc == 0) {   // workgroup 0: position / frame / tag advance, next launch's input
         if (a.with_head)
@@ -671,7 +746,7 @@ __device__ __forceinline__ void role_o(const Ctx &c, LdsP &s, int oi) {
         t.load(c.ly[l].w[1], row0, wave * (QD / 4), row0 + OROWS);
         if (tid < OROWS) rs = ldg(uni(c.ly[l].s[1]) + row0 + tid);
     };
-    THead th;
+    HeadTile ht;
     load_gains<4, 8, H>(a.final_norm, s.hd.gain);
     load(0);
     land();
@@ -694,7 +769,7 @@ __device__ __forceinline__ void role_o(const Ctx &c, LdsP &s, int oi) {
             }
             float m = fmaxf(amax4(v[0]), amax4(v[1]));
             if (l > 0 && tid < OROWS / 4) *reinterpret_cast<float4 *>(s.resid + 4 * tid) = f4(v[2]);
-            if (l == 0 && tid < OROWS) s.resid[tid] = x0_elem(a, tok, row0 + tid);
+            if (l == 0 && tid < OROWS) s.resid[tid] = x0_elem(a, tok, row0 + tid, step);
             m = group_max<64>(m);
             if (lane == 0) s.wst[wave] = m;
             __syncthreads();
@@ -722,9 +797,9 @@ __device__ __forceinline__ void role_o(const Ctx &c, LdsP &s, int oi) {
             if (l + 1 < c.L) { load(l + 1); land(); }
             RS_MARK(step, l, 3);
         }
-        if (a.with_head) th.load(a.head_w, nullptr, c.hc * HEADR + wave * (HEADR / 4));
+        ht.load(a, c.hc, wave, step);
         land();
-        tok = head_phase(c, s.hd, th, step, last);
+        tok = head_phase(c, s.hd, ht, step, last);
         if (last) break;   // (so the compiler sees the tile below as the next step's only value)
         load(0);
         land();
@@ -749,7 +824,7 @@ __device__ __forceinline__ void role_gu(const Ctx &c, LdsP &s, int gi) {
         }
         load_norm_gains(c.ly[l].post_norm, gc, gu);
     };
-    THead th;
+    HeadTile ht;
     load_gains<4, 8, H>(a.final_norm, s.hd.gain);
     load(0);
     land();
@@ -787,9 +862,9 @@ __device__ __forceinline__ void role_gu(const Ctx &c, LdsP &s, int gi) {
             if (l + 1 < c.L) { load(l + 1); land(); }
             RS_MARK(step, l, 3);
         }
-        if (a.with_head) th.load(a.head_w, nullptr, c.hc * HEADR + wave * (HEADR / 4));
+        ht.load(a, c.hc, wave, step);
         land();
-        head_phase(c, s.hd, th, step, last);
+        head_phase(c, s.hd, ht, step, last);
         if (last) break;   // (so the compiler sees the tile below as the next step's only value)
         load(0);
         land();
@@ -826,7 +901,7 @@ __device__ __forceinline__ void role_dn(const Ctx &c, LdsD &s, int di) {
         }
         if (tid < nrows) rs = ldg(uni(c.ly[l].s[3]) + row0 + tid);
     };
-    THead th;
+    HeadTile ht;
     load_gains<4, 8, H>(a.final_norm, s.hd.gain);
     load(0);
     land();
@@ -916,9 +991,9 @@ __device__ __forceinline__ void role_dn(const Ctx &c, LdsD &s, int di) {
             if (l + 1 < c.L) { load(l + 1); land(); }
             RS_MARK(step, l, 3);
         }
-        if (a.with_head) th.load(a.head_w, nullptr, c.hc * HEADR + wave * (HEADR / 4));
+        ht.load(a, c.hc, wave, step);
         land();
-        head_phase(c, s.hd, th, step, last);
+        head_phase(c, s.hd, ht, step, last);
         if (last) break;   // (so the compiler sees the tile below as the next step's only value)
         load(0);
         land();
@@ -1212,7 +1287,7 @@ __device__ __forceinline__ void role_att(const Ctx &c, LdsA &s, int g, int ch) {
 __device__ __forceinline__ void role_idle(const Ctx &c, LdsP &s) {
     const RArgs &a = c.a;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    THead th;
+    HeadTile ht;
     load_gains<4, 8, H>(a.final_norm, s.hd.gain);
     land();
     for (int step = 0; step < a.n_steps; step++) {
@@ -1220,9 +1295,9 @@ __device__ __forceinline__ void role_idle(const Ctx &c, LdsP &s) {
         const bool last = step + 1 == a.n_steps;
         if (step > 0)
             for (int l = 0; l < c.L; l++) clear_share(c, par ^ 1, l);
-        if (a.with_head) th.load(a.head_w, nullptr, c.hc * HEADR + wave * (HEADR / 4));
+        ht.load(a, c.hc, wave, step);
         land();
-        head_phase(c, s.hd, th, step, last);
+        head_phase(c, s.hd, ht, step, last);
     }
 }
 
@@ -1240,7 +1315,12 @@ __global__ __launch_bounds__(NT, 1) void k_rstep(RArgs a) {
     else if (slot >= SG0 && slot < SD0) hc = NQ + NO + (slot - SG0) * 8 + x;
     else if (slot >= SD0 && slot < SI0) hc = NQ + NO + NG + (slot - SD0) * 8 + x;
     else if (slot >= SI0) hc = NQ + NO + NG + ND + (slot - SI0) * 8 + x;
-    const Ctx c{a, s_layers, brsrc(a.reg), a.n_layers, *a.d_pos, a.with_head ? *a.d_frame : 0, *a.epoch, hc};
+#ifdef QT_RS_SMALL
+    const int pos0 = a.cp ? 0 : *a.d_pos;   // a Code Predictor frame starts at position 0
+#else
+    const int pos0 = *a.d_pos;
+#endif
+    const Ctx c{a, s_layers, brsrc(a.reg), a.n_layers, pos0, a.with_head ? *a.d_frame : 0, *a.epoch, hc};
     if (slot < SA0) role_q(c, *reinterpret_cast<LdsP *>(lds), x, slot - SQ0);
     else if (slot < SO0) role_att(c, *reinterpret_cast<LdsA *>(lds), x, slot - SA0);
     else if (slot < SG0) role_o(c, *reinterpret_cast<LdsP *>(lds), (slot - SO0) * 8 + x);
@@ -1287,7 +1367,7 @@ extern "C" hipError_t QT_RS_NAME(qt_launch_rstep, )(const void *layers_dev, int 
                                                     const uint16_t *head_w, const uint16_t *emb, int vocab, int *d_frame,
                                                     int *hist, int hist_len, float *layer_out, hipStream_t st) {
     namespace rs = ps::QT_RS_NS;
-    rs::RArgs a;
+    rs::RArgs a = {};
     a.layers = (const ps::Layer *)layers_dev; a.n_layers = n_layers;
     a.final_norm = final_norm; a.rope_cos = rope_cos; a.rope_sin = rope_sin;
     a.kc = kc; a.vc = vc; a.kv_max = kv_max; a.eps = eps; a.scale = scale;
@@ -1303,3 +1383,37 @@ extern "C" hipError_t QT_RS_NAME(qt_launch_rstep, )(const void *layers_dev, int 
     void *args[] = {(void *)&a};
     return hipLaunchCooperativeKernel((const void *)rs::k_rstep, dim3(ps::NB), dim3(rs::NT), args, 0, st);
 }
+
+#ifdef QT_RS_SMALL
+// Code Predictor frame (qwen_tts_code_predictor.c:926-1045) in one launch: n_passes passes
+// of the n_layers CP layers at positions 0 .. n_passes-1, pass 0 on xin, the int8 lm head
+// after every pass s >= 1 writing codes[s], pass s+1 on row codes[s] of its table.  cp_tab:
+// device array of 45 pointers (15 lm heads [vocab][1024] int8, their 15 row-scale arrays,
+// the 15 input tables: the Talker's codec embedding, then CP embeddings 0 .. 13).  codes[0]
+// is the frame's input code.
+extern "C" hipError_t qt_launch_rstep06_cp(const void *layers_dev, int n_layers, const float *final_norm,
+                                           const float *rope_cos, const float *rope_sin, uint16_t *kc, uint16_t *vc,
+                                           int kv_max, float eps, float scale, unsigned *reg, unsigned long long *slots,
+                                           float *hid, float *decx, float *xin, int *d_pos, unsigned *epoch, int *err,
+                                           int n_passes, const void *const *cp_tab, int vocab, int *codes,
+                                           hipStream_t st) {
+    namespace rs = ps::rs06;
+    rs::RArgs a = {};
+    a.layers = (const ps::Layer *)layers_dev; a.n_layers = n_layers;
+    a.final_norm = final_norm; a.rope_cos = rope_cos; a.rope_sin = rope_sin;
+    a.kc = kc; a.vc = vc; a.kv_max = kv_max; a.eps = eps; a.scale = scale;
+    a.reg = reg; a.slots = slots; a.hid = hid; a.decx = decx; a.xin = xin; a.d_pos = d_pos; a.epoch = epoch;
+    a.err = err; a.n_steps = n_passes; a.with_head = 0; a.vocab = vocab;
+    a.cp = 1;
+    a.cp_head = reinterpret_cast<const uint8_t *const *>(cp_tab);
+    a.cp_hs = reinterpret_cast<const float *const *>(cp_tab + 15);
+    a.cp_emb = reinterpret_cast<const uint16_t *const *>(cp_tab + 30);
+    a.cp_codes = codes;
+    if (n_passes < 1 || n_passes > 16 || n_passes > kv_max || n_layers <= 0 || n_layers > rs::MAXLR ||
+        kv_max > rs::ACH * rs::ABLK * ps::KVB)
+        return hipErrorInvalidValue;
+    if (!cp_tab || !codes || !xin || vocab < 1 || vocab > rs::NHEAD * rs::HEADR) return hipErrorInvalidValue;
+    void *args[] = {(void *)&a};
+    return hipLaunchCooperativeKernel((const void *)rs::k_rstep, dim3(ps::NB), dim3(rs::NT), args, 0, st);
+}
+#endif

@@ -1240,6 +1240,14 @@ typedef struct {
     int prefill2;                         /* 1: the frame starts with cp_prefill2_body */
     float *x2, *qkv2, *attn2, *h2;        /* device [2][H], [2][QKV], [2][qd], [2][F] */
     int8_t *pc2; float *ps2;              /* activation pieces of the two columns */
+    /* the whole frame as one launch of the role-specialised kernel's 0.6B build
+     * (qt_launch_rstep06_cp): int8 layers and lm heads, no mtp projection */
+    int rs_ok, rs_on;                     /* available / in use */
+    void *rs_layers;                      /* device layer table */
+    unsigned *rs_reg; unsigned long long *rs_slots;
+    void **rs_tab;                        /* device [45]: lm heads, their scales, input tables */
+    unsigned *rs_epoch; int *rs_err, *rs_pos;
+    float *rs_io;                         /* [2H]: final-normed and raw x of the last pass */
     int dead;
 } cp_t;
 
@@ -1251,12 +1259,76 @@ static void cp_destroy(cp_t *c) {
     for (int g = 0; g < 15; g++) { dmat_free(&c->lm[g]); if (c->cp_emb[g]) (void)hipFree(c->cp_emb[g]); }
     dmat_free(&c->mtp);
     void *bufs[] = {c->talker_emb, c->mtp_bias, c->x, c->ebuf, c->logits, c->th, c->d_posv, c->d_codes, c->d_steppos,
-                    c->x2, c->qkv2, c->attn2, c->h2, c->pc2, c->ps2};
+                    c->x2, c->qkv2, c->attn2, c->h2, c->pc2, c->ps2, c->rs_layers, c->rs_reg, c->rs_slots, c->rs_tab,
+                    c->rs_epoch, c->rs_err, c->rs_pos, c->rs_io};
     for (size_t i = 0; i < sizeof bufs / sizeof bufs[0]; i++) if (bufs[i]) (void)hipFree(bufs[i]);
     if (c->h_x) (void)hipHostFree(c->h_x);
     if (c->h_codes) (void)hipHostFree(c->h_codes);
     if (c->st) (void)hipStreamDestroy(c->st);
     free(c);
+}
+
+/* The role-specialised frame's resources, when the CP qualifies: the 0.6B geometry, int8
+ * weights in every layer and lm head, no mtp projection.  The per-kernel path then splits
+ * its attention into the same key chunks with the same one-pass arithmetic, so the two
+ * frames give the same bits. */
+static int cp_rs_setup(cp_t *c) {
+    stack_t *s = &c->s;
+    void *host_tab = NULL;
+    void *ptab[45];
+    const unsigned one = 1;
+    if (!rstep_enabled() || c->has_mtp || c->lm_prec != QWEN_HIP_INT8) return 0;
+    if (!qt_rstep06_supported(s->prec, s->H, s->F, s->nh, s->nkv, s->hd, s->kv_max, s->L)) return 0;
+    for (int l = 0; l < s->L; l++)
+        if (s->qkv[l].prec != QWEN_HIP_INT8 || s->o[l].prec != QWEN_HIP_INT8 || s->gu[l].prec != QWEN_HIP_INT8 ||
+            s->dn[l].prec != QWEN_HIP_INT8) return 0;
+    const size_t lb = qt_pstep_layer_bytes();
+    const size_t rw = qt_rstep06_region_words(s->L), sw = qt_rstep06_slot_words();
+    HCK(hipMalloc((void **)&c->rs_reg, rw * sizeof(unsigned)));
+    HCK(hipMalloc((void **)&c->rs_slots, sw * sizeof(unsigned long long)));
+    HCK(hipMemsetAsync(c->rs_reg, 0xFF, rw * sizeof(unsigned), c->st));
+    HCK(hipMemsetAsync(c->rs_slots, 0, sw * sizeof(unsigned long long), c->st));
+    HCK(hipMalloc((void **)&c->rs_epoch, 64));
+    HCK(hipMalloc((void **)&c->rs_err, 64));
+    HCK(hipMalloc((void **)&c->rs_pos, 64));
+    HCK(hipMalloc((void **)&c->rs_io, (size_t)2 * s->H * sizeof(float)));
+    HCK(hipMemsetAsync(c->rs_err, 0, 64, c->st));
+    HCK(hipMemsetAsync(c->rs_pos, 0, 64, c->st));
+    HCK(hipMemcpyAsync(c->rs_epoch, &one, sizeof one, hipMemcpyHostToDevice, c->st));
+    for (int g = 0; g < 15; g++) {
+        ptab[g] = (void *)c->lm[g].w;
+        ptab[15 + g] = (void *)c->lm[g].scale;
+        ptab[30 + g] = g == 0 ? (void *)c->talker_emb : (void *)c->cp_emb[g - 1];
+    }
+    HCK(hipMalloc((void **)&c->rs_tab, sizeof ptab));
+    HCK(hipMemcpy(c->rs_tab, ptab, sizeof ptab, hipMemcpyHostToDevice));
+    host_tab = calloc((size_t)s->L, lb);
+    REQ(host_tab, "host alloc");
+    for (int l = 0; l < s->L; l++) {
+        const uint8_t *w[4] = {s->qkv[l].w, s->o[l].w, s->gu[l].w, s->dn[l].w};
+        const float *sc[4] = {s->qkv[l].scale, s->o[l].scale, s->gu[l].scale, s->dn[l].scale};
+        const uint16_t *s16[4] = {s->qkv[l].s16, s->o[l].s16, s->gu[l].s16, s->dn[l].s16};
+        qt_pstep_fill_layer((char *)host_tab + (size_t)l * lb, w, sc, s16, s->in_norm[l], s->post_norm[l], s->qn[l], s->kn[l]);
+    }
+    HCK(hipMalloc(&c->rs_layers, (size_t)s->L * lb));
+    HCK(hipMemcpy(c->rs_layers, host_tab, (size_t)s->L * lb, hipMemcpyHostToDevice));
+    HCK(hipStreamSynchronize(c->st));
+    free(host_tab);
+    s->step_G = qt_rstep_chunks();
+    s->step_onepass = 1;
+    c->rs_ok = c->rs_on = 1;
+    return 0;
+fail:
+    free(host_tab);
+    return -1;
+}
+
+static hipError_t cp_rs_launch(cp_t *c) {
+    stack_t *s = &c->s;
+    return qt_launch_rstep06_cp(c->rs_layers, s->L, s->final_norm, s->rope_cos, s->rope_sin, s->kc, s->vc, s->kv_max,
+                                s->eps, 1.0f / sqrtf((float)s->hd), c->rs_reg, c->rs_slots, c->rs_io, c->rs_io + s->H,
+                                c->th, c->rs_pos, c->rs_epoch, c->rs_err, 16, (const void *const *)c->rs_tab,
+                                c->codebook, c->d_codes, c->st);
 }
 
 void *qwen_hip_cp_init(const qwen_hip_cp_desc_t *d) {
@@ -1306,6 +1378,8 @@ void *qwen_hip_cp_init(const qwen_hip_cp_desc_t *d) {
     for (int i = 0; i < 64; i++) c->h_codes[i] = i;
     HCK(hipMemcpy(c->d_posv, c->h_codes, 64 * sizeof(int), hipMemcpyHostToDevice));
     (void)hipFree(tmp);
+    tmp = NULL;
+    if (cp_rs_setup(c) != 0) goto fail;
     return c;
 fail:
     if (tmp) (void)hipFree(tmp);
@@ -1489,6 +1563,18 @@ int qwen_hip_cp_frame(void *state, const float *talker_hidden, int code0, int *o
     c->h_codes[0] = code0;
     HCK(hipMemcpyAsync(c->th, c->h_x, (size_t)c->talker_hidden * sizeof(float), hipMemcpyHostToDevice, c->st));
     HCK(hipMemcpyAsync(c->d_codes, c->h_codes, sizeof(int), hipMemcpyHostToDevice, c->st));
+    if (c->rs_on && !c->prefill2) {
+        HCK(cp_rs_launch(c));
+        c->frame_ready = 1;
+        HCK(hipMemcpyAsync(c->h_codes + 16, c->d_codes, 16 * sizeof(int), hipMemcpyDeviceToHost, c->st));
+        HCK(hipMemcpyAsync(c->h_codes + 32, c->rs_err, sizeof(int), hipMemcpyDeviceToHost, c->st));
+        HCK(hipStreamSynchronize(c->st));
+        REQ(c->h_codes[32] == 0, "CP frame: a wait for another workgroup's data timed out (device error flag set)");
+        for (int g = 0; g < 15; g++) out_codes[g] = c->h_codes[16 + 1 + g];
+        for (int i = 0; i < 16; i++) c->h_codes[16 + i] = 0;
+        c->h_codes[0] = 0;
+        return 0;
+    }
     if (graphs_enabled() && !c->fready) {
         if (capture(c->st, &c->fexec, cp_frame_body, c) != 0) goto fail;
         c->fready = 1;
@@ -1509,6 +1595,11 @@ fail:
 int qwen_hip_cp_frame_async(void *state, int n_frames) {
     cp_t *c = (cp_t *)state;
     if (!c || c->dead || !c->frame_ready) { SETERR("CP frame not initialised"); return -1; }
+    if (c->rs_on && !c->prefill2) {
+        for (int i = 0; i < n_frames; i++) HCK(cp_rs_launch(c));
+        return 0;
+    }
+    REQ(c->fready || !graphs_enabled(), "CP frame graph not captured");
     for (int i = 0; i < n_frames; i++) HCK(graphs_enabled() ? hipGraphLaunch(c->fexec, c->st) : cp_frame_body(c));
     return 0;
 fail:
@@ -1520,7 +1611,26 @@ int qwen_hip_cp_sync(void *state) {
     cp_t *c = (cp_t *)state;
     if (!c) return -1;
     HCK(hipStreamSynchronize(c->st));
+    if (c->rs_ok) {
+        int e = 0;
+        HCK(hipMemcpy(&e, c->rs_err, sizeof e, hipMemcpyDeviceToHost));
+        REQ(e == 0, "CP frame: a wait for another workgroup's data timed out (device error flag set)");
+    }
     return 0;
+fail:
+    c->dead = 1;
+    return -1;
+}
+
+/* Frames on the role-specialised kernel (on = 1, the default where the CP qualifies) or
+ * on the per-kernel graph (0); both give the same bits.  Returns the mode in effect. */
+int qwen_hip_cp_fused(void *state, int on) {
+    cp_t *c = (cp_t *)state;
+    if (!c || c->dead) { SETERR("CP state is dead or NULL"); return -1; }
+    HCK(hipStreamSynchronize(c->st));
+    c->rs_on = on && c->rs_ok;
+    c->frame_ready = 0;       /* the next frame call sets the inputs of the new mode */
+    return c->rs_on;
 fail:
     c->dead = 1;
     return -1;

@@ -22,7 +22,7 @@ EXPORTS = [
     "qwen_hip_talker_upload_kv", "qwen_hip_talker_free", "qwen_hip_talker_download_kv",
     "qwen_hip_talker_greedy", "qwen_hip_talker_greedy_async", "qwen_hip_talker_sync",
     "qwen_hip_talker_stream", "qwen_hip_talker_fused", "qwen_hip_talker_fused_kernel", "qwen_hip_talker_grow_kv", "qwen_hip_talker_kv_max", "qwen_hip_talker_step_nograph", "qwen_hip_talker_launch_kernel", "qwen_hip_cp_init", "qwen_hip_cp_step", "qwen_hip_cp_download_kv",
-    "qwen_hip_cp_frame", "qwen_hip_cp_frame_async", "qwen_hip_cp_sync", "qwen_hip_cp_stream",
+    "qwen_hip_cp_frame", "qwen_hip_cp_frame_async", "qwen_hip_cp_sync", "qwen_hip_cp_stream", "qwen_hip_cp_fused",
     "qwen_hip_cp_free", "qwen_hip_available", "qwen_hip_init", "qwen_hip_free", "qwen_hip_matvec_bf16",
     "qwen_hip_matmat_bf16", "qwen_hip_op_matvec_int8", "qwen_hip_op_matvec_q4_0",
     "qwen_hip_op_matvec_bf16", "qwen_hip_op_causal_attention_bf16kv", "qwen_hip_op_rms_norm",
@@ -124,6 +124,7 @@ def lib():
         L.qwen_hip_cp_frame.argtypes = [vp, vp, i, vp]; L.qwen_hip_cp_frame.restype = i
         L.qwen_hip_cp_frame_async.argtypes = [vp, i]; L.qwen_hip_cp_frame_async.restype = i
         L.qwen_hip_cp_sync.argtypes = [vp]; L.qwen_hip_cp_sync.restype = i
+        L.qwen_hip_cp_fused.argtypes = [vp, i]; L.qwen_hip_cp_fused.restype = i
         L.qwen_hip_cp_stream.argtypes = [vp]; L.qwen_hip_cp_stream.restype = vp
         L.qwen_hip_cp_free.argtypes = [vp]
         L.qwen_hip_available.restype = i
@@ -514,6 +515,13 @@ class CodePredictor:
         v = np.zeros_like(k)
         check(lib().qwen_hip_cp_download_kv(self.h, _p(k), _p(v), n, n), "cp_download_kv")
         return k, v
+
+    def fused(self, on):
+        """Frames on the role-specialised kernel (True) or the per-kernel graph; returns the mode in effect."""
+        r = lib().qwen_hip_cp_fused(self.h, int(bool(on)))
+        if r < 0:
+            raise RuntimeError("qwen_hip_cp_fused failed: " + last_error())
+        return bool(r)
 
     def set_prefill2(self, on):
         """Frames start with the two-position pass (int8 CP weights only)."""

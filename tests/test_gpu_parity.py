@@ -474,6 +474,32 @@ def test_cp_frame_codes_match_reference(name, prec):
 
 
 @need_ref
+def test_cp_frame_fused_matches_launch_graph():
+    """int8 CP without the mtp projection (0.6B geometry): the frame as one launch of the
+    role-specialised kernel and as the per-kernel launch graph give the same codes and the
+    same K/V of all 16 positions, bit for bit, over frames back to back (the fused frame is
+    the default; its codes also match the reference in test_cp_frame_codes_match_reference)."""
+    ref, shape, _ = _ref("mini", "int8")
+    cp = _gpu_cp(ref, shape, hip.INT8)
+    assert cp.fused(True), "the 0.6B int8 CP should take the fused frame"
+    rng = np.random.default_rng(11)
+    for f in range(5):
+        th = rng.standard_normal(shape.hidden).astype(np.float32)
+        th /= np.sqrt((th ** 2).mean())
+        code0 = int(rng.integers(0, 2048))
+        assert cp.fused(True)
+        a = list(cp.frame(th, code0))
+        ka, va = cp.download_kv(16)
+        assert not cp.fused(False)
+        b = list(cp.frame(th, code0))
+        kb, vb = cp.download_kv(16)
+        assert a == b, (f, a, b)
+        assert np.array_equal(ka, kb) and np.array_equal(va, vb), f
+        assert a == list(ref.cp_predict(th, code0)), f
+    cp.fused(True)
+
+
+@need_ref
 @pytest.mark.parametrize("name,prec", [("mini", "bf16"), ("mini", "int8"), ("mini17", "int4"), ("mini17", "int8")])
 def test_load_file_matches_reference_loader(name, prec):
     """qwen_hip_talker_load_file (model.safetensors -> device, gate|up interleaved and
