@@ -192,6 +192,7 @@ SAMPLED_WORKLOADS = {
 # input, Talker step) at the reference's defaults: (shape, precision, prefill L, frames)
 FRAME_WORKLOADS = {
     "frame-0.6B-bf16-sampled": ("0.6B", "bf16", 256, 64),
+    "frame-0.6B-int8-sampled": ("0.6B", "int8", 256, 64),
     "frame-1.7B-int8-sampled": ("1.7B", "int8", 2048, 64),
 }
 # the speech decoder (codes -> 24 kHz audio, one-shot): (frames per decode, default timed decodes)

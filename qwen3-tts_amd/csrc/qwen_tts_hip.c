@@ -1323,13 +1323,14 @@ fail:
     return -1;
 }
 
-static hipError_t cp_rs_launch(cp_t *c) {
+static hipError_t cp_rs_launch_on(cp_t *c, hipStream_t st) {
     stack_t *s = &c->s;
     return qt_launch_rstep06_cp(c->rs_layers, s->L, s->final_norm, s->rope_cos, s->rope_sin, s->kc, s->vc, s->kv_max,
                                 s->eps, 1.0f / sqrtf((float)s->hd), c->rs_reg, c->rs_slots, c->rs_io, c->rs_io + s->H,
                                 c->th, c->rs_pos, c->rs_epoch, c->rs_err, 16, (const void *const *)c->rs_tab,
-                                c->codebook, c->d_codes, c->st);
+                                c->codebook, c->d_codes, st);
 }
+static hipError_t cp_rs_launch(cp_t *c) { return cp_rs_launch_on(c, c->st); }
 
 void *qwen_hip_cp_init(const qwen_hip_cp_desc_t *d) {
     cp_t *c = calloc(1, sizeof *c);
@@ -1701,7 +1702,8 @@ int qwen_hip_generate(void *talker_state, void *cp_state, const uint16_t *codec_
         SETERR("generate: positions exceed kv_max"); return -1;
     }
     if (head_setup(t, codec_head, codec_emb, codec_vocab) != 0) goto fail;
-    if (graphs_enabled() && !c->fready) {
+    const int cp_fused = c->rs_on && !c->prefill2;   /* the CP frame as one launch */
+    if (!cp_fused && graphs_enabled() && !c->fready) {
         if (capture(c->st, &c->fexec, cp_frame_body, c) != 0) goto fail;
         c->fready = 1;
     }
@@ -1738,7 +1740,8 @@ int qwen_hip_generate(void *talker_state, void *cp_state, const uint16_t *codec_
             /* the CP frame for (hidden, code0) */
             HCK(qt_launch_copy_f32(t->io, c->th, H, t->st));
             HCK(hipMemcpyAsync(c->d_codes, tok, sizeof(int), hipMemcpyDeviceToDevice, t->st));
-            HCK(graphs_enabled() ? hipGraphLaunch(c->fexec, t->st) : cp_frame_body_on(c, t->st));
+            HCK(cp_fused ? cp_rs_launch_on(c, t->st)
+                         : graphs_enabled() ? hipGraphLaunch(c->fexec, t->st) : cp_frame_body_on(c, t->st));
             HCK(hipMemcpyAsync(t->gen_codes + (size_t)16 * i, c->d_codes, 16 * sizeof(int), hipMemcpyDeviceToDevice, t->st));
             /* next input, then the Talker step */
             float *xin = t->ps_on ? t->ps_xin : t->io + H;
@@ -1752,8 +1755,10 @@ int qwen_hip_generate(void *talker_state, void *cp_state, const uint16_t *codec_
     HCK(hipMemcpyAsync(t->h_pos + 2, t->smp_seed, sizeof(uint32_t), hipMemcpyDeviceToHost, t->st));
     HCK(hipMemcpyAsync(t->h_out, t->io, (size_t)2 * H * sizeof(float), hipMemcpyDeviceToHost, t->st));
     if (t->ps_on) HCK(hipMemcpyAsync(t->h_err, t->ps_err, sizeof(int), hipMemcpyDeviceToHost, t->st));
+    if (cp_fused) HCK(hipMemcpyAsync(t->h_err + 1, c->rs_err, sizeof(int), hipMemcpyDeviceToHost, t->st));
     HCK(hipStreamSynchronize(t->st));
     if (t->ps_on && ps_check(t) != 0) goto fail;
+    REQ(!cp_fused || t->h_err[1] == 0, "generate: the CP frame's wait for another workgroup's data timed out");
     *seed = (uint32_t)t->h_pos[2];
     if (hidden_out) memcpy(hidden_out, t->h_out, (size_t)H * sizeof(float));
     t->dev_pos = pos + n_frames;
