@@ -102,7 +102,8 @@ hipError_t qt_launch_rstep06_cp(const void *layers_dev, int n_layers, const floa
                                 const float *rope_sin, uint16_t *kc, uint16_t *vc, int kv_max, float eps, float scale,
                                 unsigned *reg, unsigned long long *slots, float *hid, float *decx, float *xin,
                                 int *d_pos, unsigned *epoch, int *err, int n_passes, const void *const *cp_tab,
-                                int vocab, int *codes, hipStream_t st);
+                                int vocab, int *codes, const uint8_t *mtp_w, const float *mtp_s, const float *mtp_b,
+                                hipStream_t st);
 int qt_rstep06_supported(int prec, int hidden, int inter, int n_heads, int n_kv, int head_dim, int kv_max, int n_layers);
 size_t qt_rstep06_region_words(int n_layers);
 size_t qt_rstep06_slot_words(void);

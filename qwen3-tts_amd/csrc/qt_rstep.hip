@@ -89,7 +89,15 @@ constexpr int MAXLR = 32;
 // are equal)
 constexpr int R_QKV = 0, R_PO = R_QKV + QKVR, R_PML = R_PO + NKV * HPK * 4 * ACH * 32,
               R_ATT = R_PML + NKV * HPK * ACH * 2, R_XA = R_ATT + QD, R_H = R_XA + H, R_X = R_H + F,
+#ifdef QT_RS_SMALL
+              R_XIN = R_X + H,           // Code Predictor with the mtp projection: pass input (layer 0's block)
+              LW = (R_XIN + H + 4 * NHEAD - 1) / (4 * NHEAD) * (4 * NHEAD);
+constexpr int EMB = 2048;                        // mtp projection input (the 1.7B Talker's hidden size)
+constexpr int NMTP = H / 16;                     // mtp workgroups (16 rows each, in the head-only slots)
+static_assert(NMTP <= NI && NMTP % 8 == 0, "mtp workgroups");
+#else
               LW = (R_X + H + 4 * NHEAD - 1) / (4 * NHEAD) * (4 * NHEAD);
+#endif
 constexpr int CLR16 = LW / (4 * NHEAD);          // 16-byte groups of a layer block each head workgroup clears
 static_assert(CLR16 * 4 * NHEAD == LW && CLR16 <= NT, "clear shares");
 constexpr int SC1 = 16;                          // buffer cache policy: agent scope (sc1)
@@ -147,6 +155,10 @@ struct RArgs {
     const float *const *cp_hs;
     const uint16_t *const *cp_emb;
     int *cp_codes;
+    // with the mtp projection (mtp_w != NULL): every pass input is W.e + b (int8 rows of
+    // EMB columns, row scales, bias), e the table row (EMB wide) or, for pass 0, xin
+    const uint8_t *mtp_w;
+    const float *mtp_s, *mtp_b;
 };
 
 // ---- hand-off words ---------------------------------------------------------------------
@@ -685,12 +697,21 @@ __device__ __forceinline__ void role_q(const Ctx &c, LdsP &s, int grp, int qi) {
         const bool last = step + 1 == a.n_steps;
         for (int l = 0; l < c.L; l++) {
             float xv[EH];
-            if (l == 0) {
+#ifdef QT_RS_SMALL
+            const bool x0_direct = l == 0 && !a.mtp_w;   // else the pass input comes through R_XIN
+#else
+            const bool x0_direct = l == 0;
+#endif
+            if (x0_direct) {
 #pragma unroll
                 for (int k = 0; k < EH; k++) xv[k] = x0_elem(a, tok, tid + NT * k, step);
             } else {
                 unsigned v[EH];
+#ifdef QT_RS_SMALL
+                const unsigned base = (l == 0 ? c.blk(par, 0) + R_XIN : c.blk(par, l - 1) + R_X) * 4u;
+#else
                 const unsigned base = (c.blk(par, l - 1) + R_X) * 4u;
+#endif
                 RS_MARK(step, l, 0);
                 wait4<EH, 32>(c.rr, H, [&](int i) { return base + (unsigned)i * 4u; }, v, a.err);
                 RS_MARK(step, l, 1);
@@ -757,10 +778,16 @@ __device__ __forceinline__ void role_o(const Ctx &c, LdsP &s, int oi) {
         for (int l = 0; l < c.L; l++) {
             // attn (2048) and, after layer 0, the residual rows of x (128)
             uint4 v[3];
+#ifdef QT_RS_SMALL
+            const bool xres = l > 0 || a.mtp_w;   // residual rows from the hand-off words
+            const unsigned bx = l > 0 ? (c.blk(par, l - 1) + R_X + row0) * 4u : (c.blk(par, 0) + R_XIN + row0) * 4u;
+#else
+            const bool xres = l > 0;
+            const unsigned bx = l > 0 ? (c.blk(par, l - 1) + R_X + row0) * 4u : 0u;
+#endif
             {
                 const unsigned ba = (c.blk(par, l) + R_ATT) * 4u;
-                const unsigned bx = l > 0 ? (c.blk(par, l - 1) + R_X + row0) * 4u : 0u;
-                const int n16 = QD / 4 + (l > 0 ? OROWS / 4 : 0);
+                const int n16 = QD / 4 + (xres ? OROWS / 4 : 0);
                 RS_MARK(step, l, 0);
                 wait16<3, 8>(c.rr, n16, [&](int i) {
                     return i < QD / 4 ? ba + (unsigned)(2 * (i % NT) + i / NT) * 16u : bx + (unsigned)(i - QD / 4) * 16u;
@@ -768,8 +795,8 @@ __device__ __forceinline__ void role_o(const Ctx &c, LdsP &s, int oi) {
                 RS_MARK(step, l, 1);
             }
             float m = fmaxf(amax4(v[0]), amax4(v[1]));
-            if (l > 0 && tid < OROWS / 4) *reinterpret_cast<float4 *>(s.resid + 4 * tid) = f4(v[2]);
-            if (l == 0 && tid < OROWS) s.resid[tid] = x0_elem(a, tok, row0 + tid, step);
+            if (xres && tid < OROWS / 4) *reinterpret_cast<float4 *>(s.resid + 4 * tid) = f4(v[2]);
+            if (!xres && tid < OROWS) s.resid[tid] = x0_elem(a, tok, row0 + tid, step);
             m = group_max<64>(m);
             if (lane == 0) s.wst[wave] = m;
             __syncthreads();
@@ -1284,10 +1311,24 @@ __device__ __forceinline__ void role_att(const Ctx &c, LdsA &s, int g, int ch) {
 // Takes part in every step's head phase; clears its shares of the previous step's region at
 // the start of the step (every read of that region came before the previous step's winner
 // exchange, which this workgroup has completed).
-__device__ __forceinline__ void role_idle(const Ctx &c, LdsP &s) {
+// mi >= 0 (Code Predictor with the mtp projection): rows 16 mi .. +15 of the projection,
+// made for every pass before its layers can start: e's pieces (k_mv's int8 order without a
+// norm: the scale from max|e|), one MFMA row tile with the K split over the waves, row
+// scale, + bias (the per-kernel projection's arithmetic), published to R_XIN.
+__device__ __forceinline__ void role_idle(const Ctx &c, LdsP &s, int mi) {
     const RArgs &a = c.a;
-    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     HeadTile ht;
+#ifdef QT_RS_SMALL
+    const bool mtp = a.mtp_w && mi >= 0;
+    RTile16<EMB, 1, EMB / 4 / 64> tm;
+    float ms = 0.f, mb = 0.f;
+    if (mtp) {
+        tm.load(a.mtp_w, 16 * mi, wave * (EMB / 4), H);
+        if (tid < 16) { ms = ldg(a.mtp_s + 16 * mi + tid); mb = ldg(a.mtp_b + 16 * mi + tid); }
+    }
+    int tok = -1;
+#endif
     load_gains<4, 8, H>(a.final_norm, s.hd.gain);
     land();
     for (int step = 0; step < a.n_steps; step++) {
@@ -1295,9 +1336,48 @@ __device__ __forceinline__ void role_idle(const Ctx &c, LdsP &s) {
         const bool last = step + 1 == a.n_steps;
         if (step > 0)
             for (int l = 0; l < c.L; l++) clear_share(c, par ^ 1, l);
+#ifdef QT_RS_SMALL
+        if (mtp) {
+            static_assert(EMB / 8 == NT, "one 8-element unit of e per thread");
+            float v[8];
+            if (step == 0) {
+                const float4 p = ldg(reinterpret_cast<const float4 *>(a.xin + 8 * tid));
+                const float4 q = ldg(reinterpret_cast<const float4 *>(a.xin + 8 * tid + 4));
+                v[0] = p.x; v[1] = p.y; v[2] = p.z; v[3] = p.w; v[4] = q.x; v[5] = q.y; v[6] = q.z; v[7] = q.w;
+            } else {
+                const uint4 r = ldg(reinterpret_cast<const uint4 *>(uni(ldg(a.cp_emb + step - 1)) + (size_t)tok * EMB + 8 * tid));
+                const unsigned w4[4] = {r.x, r.y, r.z, r.w};
+#pragma unroll
+                for (int k = 0; k < 4; k++) { v[2 * k] = __uint_as_float(w4[k] << 16); v[2 * k + 1] = __uint_as_float(w4[k] & 0xFFFF0000u); }
+            }
+            float m = 0.f;
+#pragma unroll
+            for (int k = 0; k < 8; k++) m = fmaxf(m, fabsf(v[k]));
+            m = group_max<64>(m);
+            if (lane == 0) s.wst[wave] = m;
+            __syncthreads();
+            const QtPcScale ps = qt_pc_scale(fmaxf(fmaxf(s.wst[0], s.wst[1]), fmaxf(s.wst[2], s.wst[3])));
+            pcw_put<EMB, 8>(s.pc, tid, v, ps.isc);
+            wave_lds_order();   // unit tid: wave w makes the pieces of columns 512w .. +511, its own K slice
+            i32x4 acc[1];
+            rdot16<EMB, 1, EMB / 4 / 64, 1>(tm, s.pc, wave * (EMB / 4), acc);
+            ksplit_store<1>(acc, s.red);
+            if (tid < 16) {
+                int d[4];
+                ksplit_row(s.red, tid, d);
+                put(c.wp(par, 0, R_XIN + 16 * mi + tid),
+                    __fadd_rn(__fmul_rn(qt_pc_dot(d[0], d[1], d[2], d[3], ps.s), ms), mb));
+            }
+            __syncthreads();   // s.wst, s.red free for the next pass
+        }
+#endif
         ht.load(a, c.hc, wave, step);
         land();
+#ifdef QT_RS_SMALL
+        tok = head_phase(c, s.hd, ht, step, last);
+#else
         head_phase(c, s.hd, ht, step, last);
+#endif
     }
 }
 
@@ -1326,7 +1406,14 @@ __global__ __launch_bounds__(NT, 1) void k_rstep(RArgs a) {
     else if (slot < SG0) role_o(c, *reinterpret_cast<LdsP *>(lds), (slot - SO0) * 8 + x);
     else if (slot < SD0) role_gu(c, *reinterpret_cast<LdsP *>(lds), (slot - SG0) * 8 + x);
     else if (XI == 0 || slot < SI0) role_dn(c, *reinterpret_cast<LdsD *>(lds), (slot - SD0) * 8 + x);
-    else role_idle(c, *reinterpret_cast<LdsP *>(lds));
+    else {
+#ifdef QT_RS_SMALL
+        const int mi = slot - SI0 < NMTP / 8 ? (slot - SI0) * 8 + x : -1;   // mtp rows of the first NMTP/8 idle slots
+#else
+        const int mi = -1;
+#endif
+        role_idle(c, *reinterpret_cast<LdsP *>(lds), mi);
+    }
 }
 }  // namespace QT_RS_NS
 }  // namespace ps
@@ -1396,6 +1483,7 @@ extern "C" hipError_t qt_launch_rstep06_cp(const void *layers_dev, int n_layers,
                                            int kv_max, float eps, float scale, unsigned *reg, unsigned long long *slots,
                                            float *hid, float *decx, float *xin, int *d_pos, unsigned *epoch, int *err,
                                            int n_passes, const void *const *cp_tab, int vocab, int *codes,
+                                           const uint8_t *mtp_w, const float *mtp_s, const float *mtp_b,
                                            hipStream_t st) {
     namespace rs = ps::rs06;
     rs::RArgs a = {};
@@ -1409,6 +1497,8 @@ extern "C" hipError_t qt_launch_rstep06_cp(const void *layers_dev, int n_layers,
     a.cp_hs = reinterpret_cast<const float *const *>(cp_tab + 15);
     a.cp_emb = reinterpret_cast<const uint16_t *const *>(cp_tab + 30);
     a.cp_codes = codes;
+    a.mtp_w = mtp_w; a.mtp_s = mtp_s; a.mtp_b = mtp_b;
+    if (mtp_w && (!mtp_s || !mtp_b)) return hipErrorInvalidValue;
     if (n_passes < 1 || n_passes > 16 || n_passes > kv_max || n_layers <= 0 || n_layers > rs::MAXLR ||
         kv_max > rs::ACH * rs::ABLK * ps::KVB)
         return hipErrorInvalidValue;

@@ -1277,7 +1277,8 @@ static int cp_rs_setup(cp_t *c) {
     void *host_tab = NULL;
     void *ptab[45];
     const unsigned one = 1;
-    if (!rstep_enabled() || c->has_mtp || c->lm_prec != QWEN_HIP_INT8) return 0;
+    if (!rstep_enabled() || c->lm_prec != QWEN_HIP_INT8) return 0;
+    if (c->has_mtp && (c->mtp.prec != QWEN_HIP_INT8 || c->emb_dim != 2048 || c->talker_hidden != 2048)) return 0;
     if (!qt_rstep06_supported(s->prec, s->H, s->F, s->nh, s->nkv, s->hd, s->kv_max, s->L)) return 0;
     for (int l = 0; l < s->L; l++)
         if (s->qkv[l].prec != QWEN_HIP_INT8 || s->o[l].prec != QWEN_HIP_INT8 || s->gu[l].prec != QWEN_HIP_INT8 ||
@@ -1328,7 +1329,8 @@ static hipError_t cp_rs_launch_on(cp_t *c, hipStream_t st) {
     return qt_launch_rstep06_cp(c->rs_layers, s->L, s->final_norm, s->rope_cos, s->rope_sin, s->kc, s->vc, s->kv_max,
                                 s->eps, 1.0f / sqrtf((float)s->hd), c->rs_reg, c->rs_slots, c->rs_io, c->rs_io + s->H,
                                 c->th, c->rs_pos, c->rs_epoch, c->rs_err, 16, (const void *const *)c->rs_tab,
-                                c->codebook, c->d_codes, st);
+                                c->codebook, c->d_codes, c->has_mtp ? c->mtp.w : NULL,
+                                c->has_mtp ? c->mtp.scale : NULL, c->has_mtp ? c->mtp_bias : NULL, st);
 }
 static hipError_t cp_rs_launch(cp_t *c) { return cp_rs_launch_on(c, c->st); }
 
@@ -1359,7 +1361,11 @@ void *qwen_hip_cp_init(const qwen_hip_cp_desc_t *d) {
     c->has_mtp = d->mtp.w != NULL;
     if (c->has_mtp) {
         int mp = d->mtp_prec;
-        REQ(dmat_alloc(&c->mtp, mp, H, c->emb_dim) == 0, "alloc mtp");
+        /* a quantized CP has its mtp projection in int8 too, as the reference quantizes it
+         * for both --int8 and --int4 (qwen_tts_code_predictor.c:474-476) */
+        const int qt = d->cp.quantize_to;
+        const int mdst = (mp == QWEN_HIP_BF16 && (qt == QWEN_HIP_INT8 || qt == QWEN_HIP_Q4_0)) ? QWEN_HIP_INT8 : mp;
+        REQ(dmat_alloc(&c->mtp, mdst, H, c->emb_dim) == 0, "alloc mtp");
         REQ(dmat_put(&c->mtp, 0, &d->mtp, mp, H, c->st, tmp) == 0, "upload mtp");
         REQ(d->mtp_bias, "mtp projection without bias");
         REQ((c->mtp_bias = up_f32(d->mtp_bias, H, c->st)) != NULL, "mtp bias");

@@ -474,12 +474,15 @@ def test_cp_frame_codes_match_reference(name, prec):
 
 
 @need_ref
-def test_cp_frame_fused_matches_launch_graph():
-    """int8 CP without the mtp projection (0.6B geometry): the frame as one launch of the
+@pytest.mark.parametrize("name", ["mini", "mini17"])
+def test_cp_frame_fused_matches_launch_graph(name):
+    """int8 CP (CP layers of the 0.6B geometry; mini17: with the 1.7B Talker's mtp
+    projection 2048 -> 1024 in front of every pass): the frame as one launch of the
     role-specialised kernel and as the per-kernel launch graph give the same codes and the
-    same K/V of all 16 positions, bit for bit, over frames back to back (the fused frame is
-    the default; its codes also match the reference in test_cp_frame_codes_match_reference)."""
-    ref, shape, _ = _ref("mini", "int8")
+    same K/V of all 16 positions, bit for bit, over frames back to back, and the codes are
+    the reference's qwen_cp_predict (the fused frame is the default)."""
+    print(f"[case] fused CP frame {name}", flush=True)
+    ref, shape, _ = _ref(name, "int8")
     cp = _gpu_cp(ref, shape, hip.INT8)
     assert cp.fused(True), "the 0.6B int8 CP should take the fused frame"
     rng = np.random.default_rng(11)
