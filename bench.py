@@ -118,7 +118,8 @@ def refuse_if_device_error(L, g, workload):
 
 
 # BASELINE configs 1-5 as short runs of their workloads (each in a child process, before the
-# headline's own measurement): (key, workload, extra arguments)
+# headline's own measurement): (key, workload, extra arguments); config 4 also in int8 (the
+# one-launch CP frame)
 CONFIG_RUNS = [
     ("1_0.6B_bf16_L256", "talker-0.6B-bf16-b1-L256", ["--steps", "256", "--warmup", "16"]),
     ("2_0.6B_int8_grow0-2048", "talker-0.6B-int8-grow2048", []),
@@ -126,6 +127,7 @@ CONFIG_RUNS = [
     ("3_1.7B_q4_0_L2048", "talker-1.7B-int4-b1-L2048", ["--steps", "32", "--warmup", "8"]),
     ("3_1.7B_q4_0_L4096", "talker-1.7B-int4-b1-L4096", ["--steps", "32", "--warmup", "8"]),
     ("4_cp_0.6B_bf16_frame", "cp-0.6B-bf16-frame", ["--steps", "100", "--warmup", "10"]),
+    ("4_cp_0.6B_int8_frame", "cp-0.6B-int8-frame", ["--steps", "100", "--warmup", "10"]),
     ("5_1.7B_int8_b32_ragged", "talker-1.7B-int8-b32-ragged", ["--steps", "16", "--warmup", "4"]),
 ]
 
