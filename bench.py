@@ -93,11 +93,12 @@ FUSED_KERNELS = {
 
 
 def fused_label(L, g, prec, hidden):
-    """Name of the kernel that runs the state's fused step (qt_rstep.hip is built per geometry:
-    ps::rs for hidden 2048, ps::rs06 for hidden 1024)."""
+    """Name of the kernel that runs the state's fused step (qt_rstep.hip is built per geometry
+    and weight type: ps::rs for hidden 2048, ps::rs06 for hidden 1024 int8, ps::rs06b for hidden
+    1024 bf16)."""
     kind = L.qwen_hip_talker_fused_kernel(g.h)
-    return kind, FUSED_KERNELS.get(kind, ("unfused per-kernel path",))[0].format(
-        prec=prec, ns="rs" if hidden == 2048 else "rs06")
+    ns = "rs" if hidden == 2048 else ("rs06b" if prec == "bf16" else "rs06")
+    return kind, FUSED_KERNELS.get(kind, ("unfused per-kernel path",))[0].format(prec=prec, ns=ns)
 
 
 def kernel_source_sha256(kind):
@@ -807,6 +808,7 @@ def bench_cp(args):
     rng = np.random.default_rng(0x5EED0002)
     th = rng.standard_normal(s.hidden).astype(np.float32)
     th /= np.sqrt((th ** 2).mean())
+    fused = bool(cp.fused(True)) and not pf2             # the default where the CP qualifies
     codes = cp.frame(th, int(rng.integers(0, 2048)))     # captures the frame graph
     L = hip.lib()
     ev = HipEvents()
@@ -850,7 +852,8 @@ def bench_cp(args):
         "frames_per_s": round(1000.0 / ms, 1), "frame_bytes": int(frame_bytes), "frame_gbs": round(gbs, 1),
         "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
-                     "kernel": "CP frame (per-kernel launches replayed from one hipGraph)",
+                     "kernel": (f"ps::{'rs06b' if prec == 'bf16' else 'rs06'}::k_rstep CP frame, one launch"
+                                if fused else "CP frame (per-kernel launches replayed from one hipGraph)"),
                      "bytes_per_launch": int(frame_bytes), "avg_us": round(ms * 1e3, 1), "steps_per_launch": 1},
         "cpu_baseline": cpu,
     }

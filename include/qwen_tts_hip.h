@@ -233,9 +233,11 @@ int   qwen_hip_cp_frame_async(void *state, int n_frames);
 int   qwen_hip_cp_sync(void *state);
 void *qwen_hip_cp_stream(void *state);
 /* Test/measurement switch (no reference counterpart): frames as one launch of the
- * role-specialised kernel (on = 1, the default where the CP qualifies: 0.6B geometry, int8
- * layers and lm heads, no mtp projection, two-position prefill off) or as the per-kernel
- * launch graph (0); both give the same bits.  Returns the mode in effect, -1 on error. */
+ * role-specialised kernel (on = 1, the default where the CP qualifies: 0.6B geometry, one
+ * weight type, int8 or bf16, in every layer, lm head and the 2048 -> 1024 mtp projection,
+ * two-position prefill off) or as the per-kernel launch graph (0); int8 weights give the
+ * same bits both ways, bf16 weights the same codes with K/V within f32 rounding.  Returns
+ * the mode in effect, -1 on error. */
 int   qwen_hip_cp_fused(void *state, int on);
 /* replaces qwen_cuda_cp_free                     (qwen_tts_cuda_talker.cu:917) */
 void  qwen_hip_cp_free(void *state);

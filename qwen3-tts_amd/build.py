@@ -21,7 +21,7 @@ LIB = os.path.join(PKG, "libqwen_tts_hip.so")
 ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
 ARCH = os.environ.get("QWEN_HIP_ARCH", "gfx950")
 
-HIP_SOURCES = ["qt_matvec.hip", "qt_attn.hip", "qt_misc.hip", "qt_pstep.hip", "qt_rstep.hip", "qt_rstep06.hip", "qt_batch.hip", "qt_prefill.hip", "qt_sample.hip", "qt_sd.hip",
+HIP_SOURCES = ["qt_matvec.hip", "qt_attn.hip", "qt_misc.hip", "qt_pstep.hip", "qt_rstep.hip", "qt_rstep06.hip", "qt_rstep06b.hip", "qt_batch.hip", "qt_prefill.hip", "qt_sample.hip", "qt_sd.hip",
                "qt_noalloc.hip"]
 C_SOURCES = ["qwen_tts_hip.c", "qt_load.c", "qt_sd_host.c"]
 

@@ -113,6 +113,24 @@ hipError_t qt_launch_rstep06(const void *layers_dev, int n_layers, const float *
                              unsigned *epoch, int *err, int n_steps, int with_head, const uint16_t *head_w,
                              const uint16_t *emb, int vocab, int *d_frame, int *hist, int hist_len, float *layer_out,
                              hipStream_t st);
+/* the same kernel's 0.6B build with bf16 weights (qt_rstep06b.hip): bf16 MFMA on three exact
+ * bf16 pieces of every activation; lm heads of the Code Predictor frame bf16 (cp_tab's scale
+ * entries unused), mtp projection bf16 (mtp_s unused) */
+int qt_rstep06b_supported(int prec, int hidden, int inter, int n_heads, int n_kv, int head_dim, int kv_max, int n_layers);
+size_t qt_rstep06b_region_words(int n_layers);
+size_t qt_rstep06b_slot_words(void);
+hipError_t qt_launch_rstep06b(const void *layers_dev, int n_layers, const float *final_norm, const float *rope_cos,
+                              const float *rope_sin, uint16_t *kc, uint16_t *vc, int kv_max, float eps, float scale,
+                              unsigned *reg, unsigned long long *slots, float *hid, float *decx, float *xin, int *d_pos,
+                              unsigned *epoch, int *err, int n_steps, int with_head, const uint16_t *head_w,
+                              const uint16_t *emb, int vocab, int *d_frame, int *hist, int hist_len, float *layer_out,
+                              hipStream_t st);
+hipError_t qt_launch_rstep06b_cp(const void *layers_dev, int n_layers, const float *final_norm, const float *rope_cos,
+                                 const float *rope_sin, uint16_t *kc, uint16_t *vc, int kv_max, float eps, float scale,
+                                 unsigned *reg, unsigned long long *slots, float *hid, float *decx, float *xin,
+                                 int *d_pos, unsigned *epoch, int *err, int n_passes, const void *const *cp_tab,
+                                 int vocab, int *codes, const uint8_t *mtp_w, const float *mtp_s, const float *mtp_b,
+                                 hipStream_t st);
 /* persistent decode step (qt_pstep.hip) */
 int qt_pstep_supported(int prec, int hidden, int inter, int n_heads, int n_kv, int head_dim, int kv_max);
 size_t qt_pstep_ring_words(int hidden, int inter, int n_layers);

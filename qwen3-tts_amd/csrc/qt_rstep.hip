@@ -50,7 +50,10 @@
 // stop waiting, and the launch runs to its end.
 #include "qt_step_common.h"
 
-#ifdef QT_RS_SMALL
+#if defined(QT_RS_SMALL) && defined(QT_RS_BF16)
+#define QT_RS_NS rs06b
+#define QT_RS_NAME(a, b) a##06b##b
+#elif defined(QT_RS_SMALL)
 #define QT_RS_NS rs06
 #define QT_RS_NAME(a, b) a##06##b
 #else
@@ -60,13 +63,27 @@
 
 namespace ps {
 namespace QT_RS_NS {
-#ifdef QT_RS_SMALL
+#if defined(QT_RS_SMALL) && defined(QT_RS_BF16)
+constexpr int H = 1024, F = 3072, XO = 2, XG = 6, XD = 3;               // bf16 O rows take twice the bytes
+#elif defined(QT_RS_SMALL)
 constexpr int H = 1024, F = 3072, XO = 1, XG = 6, XD = 3;               // O, GU, DN workgroups per XCD
 #else
 constexpr int H = 2048, F = 6144, XO = 2, XG = 12, XD = 6;
 #endif
 constexpr int NT = 256;
 constexpr unsigned SENT = 0xFFFFFFFFu;
+// Weight type of the build: int8 rows on v_mfma_i32_16x16x64_i8 against four exact int8
+// activation planes, or (QT_RS_BF16) bf16 rows on v_mfma_f32_16x16x32_bf16 against three
+// exact bf16 planes.  Either way an MFMA step covers 64 bytes of a weight row.
+#ifdef QT_RS_BF16
+constexpr bool WBF = true;
+#else
+constexpr bool WBF = false;
+#endif
+constexpr int WB = WBF ? 2 : 1;                  // bytes per weight
+constexpr int NPL = WBF ? 3 : 4;                 // activation planes
+constexpr int KSTEP = 64 / WB;                   // columns per MFMA step
+template <int C> constexpr int steps() { return C * WB / 64; }   // MFMA steps over C columns
 constexpr int XQ = 4, XATT = 8, XI = NB / 8 - (XQ + XATT + XO + XG + XD);   // XI: head-only slots
 constexpr int SQ0 = 0, SA0 = SQ0 + XQ, SO0 = SA0 + XATT, SG0 = SO0 + XO, SD0 = SG0 + XG, SI0 = SD0 + XD;
 static_assert(XI >= 0 && SI0 + XI == NB / 8, "32 workgroups per XCD");
@@ -74,7 +91,7 @@ constexpr int NQ = 8 * XQ, NO = 8 * XO, NG = 8 * XG, ND = 8 * XD, NI = 8 * XI;
 constexpr int NHEAD = NQ + NO + NG + ND + NI;    // 192: every workgroup but attention
 constexpr int ACH = XATT;                        // attention chunks per kv head
 constexpr int QROWS = QKVR / NQ, OROWS = H / NO, GROWS = 2 * F / NG;
-static_assert(QROWS == 128 && OROWS == 128 && GROWS == 128, "128 rows per projection workgroup");
+static_assert(QROWS == 128 && OROWS == 128 / WB && GROWS == 128, "rows per projection workgroup");
 constexpr int EH = H / NT;                       // elements of an H-vector per thread (8 or 4)
 static_assert(EH == 4 || EH == 8, "H-vector split");
 constexpr int UD = F / 768;                      // DN: elements per h unit (three units per lane)
@@ -273,14 +290,26 @@ __device__ __forceinline__ void put4(float *x, int e0, const uint4 &v) {
 // the four lanes of one quad (DPP quad broadcasts, no LDS round trip).  Exact int32 sums,
 // so the values equal every other way of forming the dot products.
 //
-// Pieces live in plane-major LDS rows of COLS + 16 bytes (the pad puts the four planes of
+// Pieces live in plane-major LDS rows of WB*COLS + 16 bytes (the pad puts the planes of
 // one column range on different banks).
-template <int COLS> constexpr int pcs() { return COLS + 16; }
-// unit u: elements E*u .. E*u + E-1 (E = 8 or 4), E bytes of each plane
+template <int COLS> constexpr int pcs() { return WB * COLS + 16; }
+// unit u: elements E*u .. E*u + E-1 (E = 8 or 4), E elements of each plane (int8: the four
+// exact planes of scale isc; bf16: the three exact bf16 planes of qt_put_pieces)
 template <int COLS, int E>
 __device__ __forceinline__ void pcw_put(uint8_t *pc, int u, const float (&v)[E], float isc) {
     static_assert(E == 8 || E == 4, "unit size");
-    if constexpr (E == 8) {
+    if constexpr (WBF) {
+        uint16_t p3[3][E];
+#pragma unroll
+        for (int e = 0; e < E; e++) qt_put_pieces(&p3[0][e], E, v[e]);
+#pragma unroll
+        for (int q = 0; q < 3; q++) {
+            if constexpr (E == 8)
+                *reinterpret_cast<uint4 *>(pc + q * pcs<COLS>() + 16 * u) = *reinterpret_cast<const uint4 *>(p3[q]);
+            else
+                *reinterpret_cast<uint2 *>(pc + q * pcs<COLS>() + 8 * u) = *reinterpret_cast<const uint2 *>(p3[q]);
+        }
+    } else if constexpr (E == 8) {
         uint2 pl[4];
         qt_pc8(v, isc, pl);
 #pragma unroll
@@ -292,52 +321,66 @@ __device__ __forceinline__ void pcw_put(uint8_t *pc, int u, const float (&v)[E],
         for (int q = 0; q < 4; q++) *reinterpret_cast<uint32_t *>(pc + q * pcs<COLS>() + 4 * u) = pl[q];
     }
 }
-// B fragment of columns col0 .. col0 + 63
+// B fragment of columns col0 .. col0 + KSTEP-1 (planes as columns 0 .. NPL-1)
 template <int COLS>
 __device__ __forceinline__ uint4 pcw_b(const uint8_t *pc, int col0) {
     const int lane = threadIdx.x & 63, n = lane & 15, kg = lane >> 4;
-    const uint4 b = *reinterpret_cast<const uint4 *>(pc + (n & 3) * pcs<COLS>() + col0 + 16 * kg);
-    return n < 4 ? b : make_uint4(0, 0, 0, 0);
+    const uint4 b = *reinterpret_cast<const uint4 *>(pc + (n & 3) * pcs<COLS>() + WB * col0 + 16 * kg);
+    return n < NPL ? b : make_uint4(0, 0, 0, 0);
 }
 // NT16 tiles of 16 rows (row0 + 16t ..) over S 64-column steps from column c0.  Buffer
 // loads: one 32-bit lane offset shared by every load, the row and step parts in scalar
 // registers (64-bit per-lane addresses would hold two VGPRs per load in flight).  Rows at
 // or past row_end are not loaded (their A stays zero).
+// NT16 tiles of 16 rows of COLS-wide weight rows (WB bytes each); S MFMA steps of 64 bytes
+// from column c0 (elements).
 template <int COLS, int NT16, int S>
 struct RTile16 {
     uint4 w[NT16][S];
     __device__ __forceinline__ void load(const uint8_t *W, int row0, int c0, int row_end) {
         const int lane = threadIdx.x & 63, m = lane & 15, kg = lane >> 4;
         const __amdgpu_buffer_rsrc_t r = brsrc(uni(W));
-        const unsigned voff = (unsigned)(m * COLS + 16 * kg);
+        const unsigned voff = (unsigned)(m * WB * COLS + 16 * kg);
 #pragma unroll
         for (int t = 0; t < NT16; t++) {
             const bool ok = row0 + 16 * t + m < row_end;
 #pragma unroll
             for (int s = 0; s < S; s++) {
                 const u32x4_t v = ok ? __builtin_amdgcn_raw_buffer_load_b128(
-                                           r, voff, __builtin_amdgcn_readfirstlane((row0 + 16 * t) * COLS + c0 + 64 * s), 0)
+                                           r, voff, __builtin_amdgcn_readfirstlane(WB * ((row0 + 16 * t) * COLS + c0) + 64 * s), 0)
                                      : u32x4_t{0, 0, 0, 0};
                 w[t][s] = make_uint4(v.x, v.y, v.z, v.w);
             }
         }
     }
 };
-// acc[t] = tile t against the pieces of columns c0 .. c0 + 64*S; CH accumulator chains per
-// tile so that no MFMA waits for the previous one of its chain
+// the build's MFMA: exact int32 plane sums (int8) or f32 sums of exact products (bf16)
+using AccT = std::conditional_t<WBF, qt_f32x4, i32x4>;
+using RedT = std::conditional_t<WBF, float, int>;
+#ifdef QT_RS_BF16
+__device__ __forceinline__ AccT mma(uint4 w, uint4 p, AccT acc) {
+    return qt_mfma_bf16(qt_u32x4{w.x, w.y, w.z, w.w}, qt_u32x4{p.x, p.y, p.z, p.w}, acc);
+}
+__device__ __forceinline__ AccT acc_zero() { return qt_f32x4{0.f, 0.f, 0.f, 0.f}; }
+#else
+__device__ __forceinline__ AccT mma(uint4 w, uint4 p, AccT acc) { return mfma_i8(w, p, acc); }
+__device__ __forceinline__ AccT acc_zero() { return i32x4{0, 0, 0, 0}; }
+#endif
+// acc[t] = tile t against the pieces of columns c0 .. c0 + KSTEP*S; CH accumulator chains
+// per tile so that no MFMA waits for the previous one of its chain
 template <int COLS, int NT16, int S, int CH>
-__device__ __forceinline__ void rdot16(const RTile16<COLS, NT16, S> &t, const uint8_t *pc, int c0, i32x4 (&acc)[NT16]) {
-    i32x4 a[NT16][CH];
+__device__ __forceinline__ void rdot16(const RTile16<COLS, NT16, S> &t, const uint8_t *pc, int c0, AccT (&acc)[NT16]) {
+    AccT a[NT16][CH];
 #pragma unroll
     for (int q = 0; q < NT16; q++)
 #pragma unroll
-        for (int c = 0; c < CH; c++) a[q][c] = i32x4{0, 0, 0, 0};
+        for (int c = 0; c < CH; c++) a[q][c] = acc_zero();
     uint4 b = pcw_b<COLS>(pc, c0);
 #pragma unroll
     for (int s = 0; s < S; s++) {
-        const uint4 bn = pcw_b<COLS>(pc, c0 + 64 * (s + 1 < S ? s + 1 : s));
+        const uint4 bn = pcw_b<COLS>(pc, c0 + KSTEP * (s + 1 < S ? s + 1 : s));
 #pragma unroll
-        for (int q = 0; q < NT16; q++) a[q][s % CH] = mfma_i8(t.w[q][s], b, a[q][s % CH]);
+        for (int q = 0; q < NT16; q++) a[q][s % CH] = mma(t.w[q][s], b, a[q][s % CH]);
         b = bn;
     }
 #pragma unroll
@@ -345,22 +388,6 @@ __device__ __forceinline__ void rdot16(const RTile16<COLS, NT16, S> &t, const ui
         acc[q] = a[q][0];
 #pragma unroll
         for (int c = 1; c < CH; c++) acc[q] += a[q][c];
-    }
-}
-// plane q of each quad's lane 0 value, broadcast from lane q of the quad
-template <int Q>
-__device__ __forceinline__ int quad_bcast(int v) {
-    return __builtin_amdgcn_update_dpp(0, v, Q | (Q << 2) | (Q << 4) | (Q << 6), 0xf, 0xf, false);
-}
-// The four exact plane sums of row 4*(lane/16) + i of a tile, valid in lanes with lane % 16
-// == 0.
-__device__ __forceinline__ void tile_rows(const i32x4 &acc, int (&d)[4][4]) {
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-        d[i][0] = acc[i];
-        d[i][1] = quad_bcast<1>(acc[i]);
-        d[i][2] = quad_bcast<2>(acc[i]);
-        d[i][3] = quad_bcast<3>(acc[i]);
     }
 }
 // ---- LDS --------------------------------------------------------------------------------
@@ -371,26 +398,26 @@ struct HeadLds {
     float wbv[4];
     int wbi[4];
     float win[2 * NHEAD];
-#ifdef QT_RS_SMALL
-    float cxs[H];                // Code Predictor lm head: the input in unit order
+#if defined(QT_RS_SMALL) && !defined(QT_RS_BF16)
+    float cxs[H];                // Code Predictor int8 lm head: the input in unit order
     float cwst[8];
     uint8_t cpc[4 * pcs<H>()];   // pieces of RMSNorm(x) * final_norm
-    int cred[16][4][4];          // partial plane sums [row][wave][plane]
+    int cred[16][4][4];          // partial plane sums [row][wave][plane] (int8 lm head)
     float clg[HEADR];            // the workgroup's logits
 #endif
 };
 struct LdsP {                    // Q, O, GU (and the head-only workgroups)
     float xs[H];                 // the input in element order (RMSNorm: statistics order -> unit order)
-    uint8_t pc[4 * pcs<PCW>()];
-    int red[8 * 16][4][4];       // partial plane sums [row][wave][plane] (K split over the waves)
+    uint8_t pc[NPL * pcs<PCW>()];
+    RedT red[8 * 16][4][4];      // partial plane sums [row][wave][plane] (K split over the waves)
     float resid[OROWS];
     float wst[8];
     HeadLds hd;
 };
 struct LdsD {                    // DN
-    uint8_t pc[4 * pcs<F>()];
-    uint4 tw[4][F / 4 / 64][64]; // tile 2 (rows 32..47): [wave][step][lane]
-    int red[4][3][16][4];        // partial plane sums [wave][tile][row][plane]
+    uint8_t pc[NPL * pcs<F>()];
+    uint4 tw[4][steps<F / 4>()][64]; // tile 2 (rows 32..47): [wave][step][lane]
+    RedT red[4][3][16][4];       // partial plane sums [wave][tile][row][plane]
     float resid[48];
     float wst[8];
     HeadLds hd;
@@ -449,10 +476,10 @@ __device__ __forceinline__ float x0_elem(const RArgs &a, int tok, int i, int ste
 }
 
 // K split over the waves: each wave's partial plane sums of its tiles' rows into
-// red[row][wave][plane] (the lanes of plane columns 0..3), then a barrier; ksplit_row adds
-// the four waves' integers for one row.
-template <int NT16>
-__device__ __forceinline__ void ksplit_store(const i32x4 (&acc)[NT16], int (*red)[4][4]) {
+// red[row][wave][plane] (the lanes of plane columns 0..3; bf16's column 3 holds exact
+// zeros), then a barrier; ksplit_row adds the four waves' sums for one row, waves in order.
+template <int NT16, typename A, typename T>
+__device__ __forceinline__ void ksplit_store(const A (&acc)[NT16], T (*red)[4][4]) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, n = lane & 15, kg = lane >> 4;
     if (n < 4) {
 #pragma unroll
@@ -462,11 +489,16 @@ __device__ __forceinline__ void ksplit_store(const i32x4 (&acc)[NT16], int (*red
     }
     __syncthreads();
 }
-__device__ __forceinline__ void ksplit_row(const int (*red)[4][4], int r, int (&d)[4]) {
-    const int4 a = *reinterpret_cast<const int4 *>(red[r][0]), b = *reinterpret_cast<const int4 *>(red[r][1]);
-    const int4 e = *reinterpret_cast<const int4 *>(red[r][2]), f = *reinterpret_cast<const int4 *>(red[r][3]);
-    d[0] = a.x + b.x + e.x + f.x; d[1] = a.y + b.y + e.y + f.y;
-    d[2] = a.z + b.z + e.z + f.z; d[3] = a.w + b.w + e.w + f.w;
+template <typename T>
+__device__ __forceinline__ void ksplit_row(const T (*red)[4][4], int r, T (&d)[4]) {
+#pragma unroll
+    for (int p = 0; p < 4; p++) d[p] = ((red[r][0][p] + red[r][1][p]) + red[r][2][p]) + red[r][3][p];
+}
+// a row's dot product from its plane sums: int8 s*(D0 + 2^8 D1 + 2^16 D2 + 2^24 D3) times
+// the row scale rs; bf16 the three planes' f32 sums added hi to lo (no row scale)
+__device__ __forceinline__ float row_dot(const RedT (&d)[4], float s, float rs) {
+    if constexpr (WBF) return (d[0] + d[1]) + d[2];
+    else return __fmul_rn(qt_pc_dot(d[0], d[1], d[2], d[3], s), rs);
 }
 
 // Pieces of RMSNorm(x)*g: x arrives in the statistics' order (thread t: elements t + NT*k),
@@ -531,13 +563,16 @@ using THead = Tile<QT_BF16, H, HEADR / 4>;
 // columns split over the waves as in the projections.
 struct HeadTile {
     THead th;
-#ifdef QT_RS_SMALL
-    RTile16<H, 1, H / 4 / 64> tc;
+#if defined(QT_RS_SMALL) && !defined(QT_RS_BF16)
+    RTile16<H, 1, steps<H / 4>()> tc;
     float tcs = 0.f;             // row scale of row hc*HEADR + tid (tid < HEADR)
 #endif
     __device__ __forceinline__ void load(const RArgs &a, int hc, int wave, int step) {
         if (a.with_head) th.load(a.head_w, nullptr, hc * HEADR + wave * (HEADR / 4));
-#ifdef QT_RS_SMALL
+#if defined(QT_RS_SMALL) && defined(QT_RS_BF16)
+        else if (a.cp && step > 0 && hc * HEADR < a.vocab)   // bf16 lm head rows (the codebook is whole tiles)
+            th.load(uni(ldg(a.cp_head + step - 1)), nullptr, hc * HEADR + wave * (HEADR / 4));
+#elif defined(QT_RS_SMALL)
         else if (a.cp && step > 0) {
             const int tid = threadIdx.x, r0 = hc * HEADR;
             tc.load(uni(ldg(a.cp_head + step - 1)), r0, wave * (H / 4), a.vocab);
@@ -587,7 +622,28 @@ __device__ __forceinline__ int head_phase(const Ctx &c, HeadLds &s, const HeadTi
         for (int w = 1; w < 4; w++)
             if (s.wbv[w] > bv || (s.wbv[w] == bv && s.wbi[w] < bi)) { bv = s.wbv[w]; bi = s.wbi[w]; }
     }
-#ifdef QT_RS_SMALL
+#if defined(QT_RS_SMALL) && defined(QT_RS_BF16)
+    else if (a.cp && step > 0) {
+        // bf16 lm head rows on the final-normed x (the Talker head's arithmetic, k_mv's bf16
+        // order); plain argmax from the start value -1e30, lowest index on ties
+        float acc[HEADR / 4];
+        tile_dot<QT_BF16, H, HEADR / 4>(ht.th, s.xn, acc);
+        if (lane == 0) {
+            float b = -1e30f;
+            int ix = 0x7FFFFFFF;
+#pragma unroll
+            for (int r = 0; r < HEADR / 4; r++) {
+                const int i = c.hc * HEADR + wave * (HEADR / 4) + r;
+                if (i < a.vocab && (acc[r] > b || (acc[r] == b && i < ix))) { b = acc[r]; ix = i; }
+            }
+            s.wbv[wave] = b; s.wbi[wave] = ix;
+        }
+        __syncthreads();
+        bv = s.wbv[0]; bi = s.wbi[0];
+        for (int w = 1; w < 4; w++)
+            if (s.wbv[w] > bv || (s.wbv[w] == bv && s.wbi[w] < bi)) { bv = s.wbv[w]; bi = s.wbi[w]; }
+    }
+#elif defined(QT_RS_SMALL)
     else if (a.cp && step > 0) {
         // the lm head on the pieces of RMSNorm(x) * final_norm, made in k_mv's int8 order
         // (the per-kernel frame's lm-head matvec), so the logits are the same bits; plain
@@ -603,7 +659,7 @@ __device__ __forceinline__ int head_phase(const Ctx &c, HeadLds &s, const HeadTi
         if (tid < HEADR) {
             int d[4];
             ksplit_row(s.cred, tid, d);
-            s.clg[tid] = __fmul_rn(qt_pc_dot(d[0], d[1], d[2], d[3], sA), ht.tcs);
+            s.clg[tid] = __fmul_rn(qt_pc_dot(d[0], d[1], d[2], d[3], sA), ht.tcs);   // int8 lm head
         }
         __syncthreads();
         bv = -1e30f;
@@ -679,12 +735,12 @@ __device__ __forceinline__ void role_q(const Ctx &c, LdsP &s, int grp, int qi) {
     const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     // 128 rows; wave w takes columns (H/4)w .. +H/4-1 of all of them
     const int row0 = qi < 2 ? (2 * grp + qi) * HD : qi == 2 ? QD + grp * HD : QD + KVD + grp * HD;
-    RTile16<H, 8, H / 4 / 64> t;
-    float rs = 0.f;
+    RTile16<H, 8, steps<H / 4>()> t;
+    float rs = WBF ? 1.f : 0.f;   // bf16 rows carry no scale
     float gc[EH], gu[EH];
     auto load = [&](int l) {
         t.load(c.ly[l].w[0], row0, wave * (H / 4), row0 + QROWS);
-        if (tid < QROWS) rs = ldg(uni(c.ly[l].s[0]) + row0 + tid);
+        if (!WBF && tid < QROWS) rs = ldg(uni(c.ly[l].s[0]) + row0 + tid);
         load_norm_gains(c.ly[l].in_norm, gc, gu);
     };
     HeadTile ht;
@@ -720,14 +776,14 @@ __device__ __forceinline__ void role_q(const Ctx &c, LdsP &s, int grp, int qi) {
             }
             const float sA = norm_pieces(xv, gc, gu, s.xs, s.wst, s.pc, a.eps);
             RS_MARK(step, l, 6);
-            i32x4 acc[8];
-            rdot16<H, 8, H / 4 / 64, 1>(t, s.pc, wave * (H / 4), acc);
+            AccT acc[8];
+            rdot16<H, 8, steps<H / 4>(), 1>(t, s.pc, wave * (H / 4), acc);
             RS_MARK(step, l, 7);
             ksplit_store<8>(acc, s.red);
             if (tid < QROWS) {
-                int d[4];
+                RedT d[4];
                 ksplit_row(s.red, tid, d);
-                put(c.wp(par, l, R_QKV + row0 + tid), __fmul_rn(qt_pc_dot(d[0], d[1], d[2], d[3], sA), rs));
+                put(c.wp(par, l, R_QKV + row0 + tid), row_dot(d, sA, rs));
             }
             RS_MARK(step, l, 2);
             if (step > 0) clear_share(c, par ^ 1, l);
@@ -761,11 +817,12 @@ __device__ __forceinline__ void role_o(const Ctx &c, LdsP &s, int oi) {
     const RArgs &a = c.a;
     const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int row0 = oi * OROWS;
-    RTile16<QD, 8, QD / 4 / 64> t;
-    float rs = 0.f;
+    constexpr int OT = OROWS / 16;   // row tiles (8 int8, 4 bf16)
+    RTile16<QD, OT, steps<QD / 4>()> t;
+    float rs = WBF ? 1.f : 0.f;   // bf16 rows carry no scale
     auto load = [&](int l) {
         t.load(c.ly[l].w[1], row0, wave * (QD / 4), row0 + OROWS);
-        if (tid < OROWS) rs = ldg(uni(c.ly[l].s[1]) + row0 + tid);
+        if (!WBF && tid < OROWS) rs = ldg(uni(c.ly[l].s[1]) + row0 + tid);
     };
     HeadTile ht;
     load_gains<4, 8, H>(a.final_norm, s.hd.gain);
@@ -808,15 +865,14 @@ __device__ __forceinline__ void role_o(const Ctx &c, LdsP &s, int oi) {
             }
             wave_lds_order();   // unit tid: wave w makes the pieces of columns 512w .. +511, its own K slice
             RS_MARK(step, l, 6);
-            i32x4 acc[8];
-            rdot16<QD, 8, QD / 4 / 64, 1>(t, s.pc, wave * (QD / 4), acc);
+            AccT acc[OT];
+            rdot16<QD, OT, steps<QD / 4>(), 1>(t, s.pc, wave * (QD / 4), acc);
             RS_MARK(step, l, 7);
-            ksplit_store<8>(acc, s.red);
+            ksplit_store<OT>(acc, s.red);
             if (tid < OROWS) {
-                int d[4];
+                RedT d[4];
                 ksplit_row(s.red, tid, d);
-                put(c.wp(par, l, R_XA + row0 + tid),
-                    __fadd_rn(s.resid[tid], __fmul_rn(qt_pc_dot(d[0], d[1], d[2], d[3], ps.s), rs)));
+                put(c.wp(par, l, R_XA + row0 + tid), __fadd_rn(s.resid[tid], row_dot(d, ps.s, rs)));
             }
             RS_MARK(step, l, 2);
             if (step > 0) clear_share(c, par ^ 1, l);
@@ -839,12 +895,12 @@ __device__ __forceinline__ void role_gu(const Ctx &c, LdsP &s, int gi) {
     const RArgs &a = c.a;
     const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int row0 = gi * GROWS;
-    RTile16<H, 8, H / 4 / 64> t;
-    float rsg = 0.f, rsu = 0.f;
+    RTile16<H, 8, steps<H / 4>()> t;
+    float rsg = WBF ? 1.f : 0.f, rsu = rsg;
     float gc[EH], gu[EH];
     auto load = [&](int l) {
         t.load(c.ly[l].w[2], row0, wave * (H / 4), row0 + GROWS);
-        if (tid < GROWS / 2) {
+        if (!WBF && tid < GROWS / 2) {
             const float *S = uni(c.ly[l].s[2]);
             rsg = ldg(S + row0 + 2 * tid);
             rsu = ldg(S + row0 + 2 * tid + 1);
@@ -871,16 +927,16 @@ __device__ __forceinline__ void role_gu(const Ctx &c, LdsP &s, int gi) {
             }
             const float sD = norm_pieces(xv, gc, gu, s.xs, s.wst, s.pc, a.eps);
             RS_MARK(step, l, 6);
-            i32x4 acc[8];
-            rdot16<H, 8, H / 4 / 64, 1>(t, s.pc, wave * (H / 4), acc);
+            AccT acc[8];
+            rdot16<H, 8, steps<H / 4>(), 1>(t, s.pc, wave * (H / 4), acc);
             RS_MARK(step, l, 7);
             ksplit_store<8>(acc, s.red);
             if (tid < GROWS / 2) {
-                int dg[4], du[4];
+                RedT dg[4], du[4];
                 ksplit_row(s.red, 2 * tid, dg);
                 ksplit_row(s.red, 2 * tid + 1, du);
-                const float gt = __fmul_rn(qt_pc_dot(dg[0], dg[1], dg[2], dg[3], sD), rsg);
-                const float up = __fmul_rn(qt_pc_dot(du[0], du[1], du[2], du[3], sD), rsu);
+                const float gt = row_dot(dg, sD, rsg);
+                const float up = row_dot(du, sD, rsu);
                 put(c.wp(par, l, R_H + row0 / 2 + tid), gt / (1.0f + expf(-gt)) * up);
             }
             RS_MARK(step, l, 2);
@@ -912,21 +968,21 @@ __device__ __forceinline__ void role_dn(const Ctx &c, LdsD &s, int di) {
     const bool big = di < NDB;                 // NDB workgroups of 48 rows, the others 40
     const int row0 = big ? 48 * di : 48 * NDB + 40 * (di - NDB);
     const int nrows = big ? 48 : 40;
-    constexpr int KW = F / 4, S = KW / 64;     // columns and 64-column steps per wave
+    constexpr int KW = F / 4, S = steps<KW>();  // columns and 64-byte MFMA steps per wave
     const int c0 = wave * KW;
     RTile16<F, 2, S> t;
-    float rs = 0.f;
+    float rs = WBF ? 1.f : 0.f;   // bf16 rows carry no scale
     auto load = [&](int l) {
         t.load(c.ly[l].w[3], row0, c0, row0 + nrows);
         if (row0 + 32 + m16 < row0 + nrows) {
             const __amdgpu_buffer_rsrc_t r = brsrc(uni(c.ly[l].w[3]));
-            const unsigned voff = (unsigned)(m16 * F + 16 * kg);
+            const unsigned voff = (unsigned)(m16 * WB * F + 16 * kg);
 #pragma unroll
             for (int st = 0; st < S; st++)
                 __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void *)&s.tw[wave][st][0], 16,
-                                                         voff, __builtin_amdgcn_readfirstlane((row0 + 32) * F + c0 + 64 * st), 0, 0);
+                                                         voff, __builtin_amdgcn_readfirstlane(WB * ((row0 + 32) * F + c0) + 64 * st), 0, 0);
         }
-        if (tid < nrows) rs = ldg(uni(c.ly[l].s[3]) + row0 + tid);
+        if (!WBF && tid < nrows) rs = ldg(uni(c.ly[l].s[3]) + row0 + tid);
     };
     HeadTile ht;
     load_gains<4, 8, H>(a.final_norm, s.hd.gain);
@@ -972,21 +1028,21 @@ __device__ __forceinline__ void role_dn(const Ctx &c, LdsD &s, int di) {
             }
             wave_lds_order();   // the wave's own K slice
             RS_MARK(step, l, 6);
-            i32x4 acc[3];
+            AccT acc[3];
             {
-                i32x4 ac[3][2];
+                AccT ac[3][2];
 #pragma unroll
-                for (int q = 0; q < 3; q++) ac[q][0] = ac[q][1] = i32x4{0, 0, 0, 0};
+                for (int q = 0; q < 3; q++) ac[q][0] = ac[q][1] = acc_zero();
                 uint4 b = pcw_b<F>(s.pc, c0);
                 uint4 w2 = s.tw[wave][0][lane];
 #pragma unroll
                 for (int st = 0; st < S; st++) {
                     const int sn = st + 1 < S ? st + 1 : st;
-                    const uint4 bn = pcw_b<F>(s.pc, c0 + 64 * sn);
+                    const uint4 bn = pcw_b<F>(s.pc, c0 + KSTEP * sn);
                     const uint4 w2n = s.tw[wave][sn][lane];
-                    ac[0][st & 1] = mfma_i8(t.w[0][st], b, ac[0][st & 1]);
-                    ac[1][st & 1] = mfma_i8(t.w[1][st], b, ac[1][st & 1]);
-                    ac[2][st & 1] = mfma_i8(w2, b, ac[2][st & 1]);
+                    ac[0][st & 1] = mma(t.w[0][st], b, ac[0][st & 1]);
+                    ac[1][st & 1] = mma(t.w[1][st], b, ac[1][st & 1]);
+                    ac[2][st & 1] = mma(w2, b, ac[2][st & 1]);
                     b = bn;
                     w2 = w2n;
                 }
@@ -1004,10 +1060,10 @@ __device__ __forceinline__ void role_dn(const Ctx &c, LdsD &s, int di) {
             __syncthreads();
             if (tid < nrows) {
                 const int q = tid >> 4, rr = tid & 15;
-                int d[4];
+                RedT d[4];
 #pragma unroll
-                for (int n = 0; n < 4; n++) d[n] = s.red[0][q][rr][n] + s.red[1][q][rr][n] + s.red[2][q][rr][n] + s.red[3][q][rr][n];
-                const float vv = __fmul_rn(qt_pc_dot(d[0], d[1], d[2], d[3], ps.s), rs);
+                for (int n = 0; n < 4; n++) d[n] = ((s.red[0][q][rr][n] + s.red[1][q][rr][n]) + s.red[2][q][rr][n]) + s.red[3][q][rr][n];
+                const float vv = row_dot(d, ps.s, rs);
                 const float xo = __fadd_rn(s.resid[tid], vv);
                 put(c.wp(par, l, R_X + row0 + tid), xo);
                 if (a.layer_out && last) a.layer_out[(size_t)l * H + row0 + tid] = xo;
@@ -1321,11 +1377,11 @@ __device__ __forceinline__ void role_idle(const Ctx &c, LdsP &s, int mi) {
     HeadTile ht;
 #ifdef QT_RS_SMALL
     const bool mtp = a.mtp_w && mi >= 0;
-    RTile16<EMB, 1, EMB / 4 / 64> tm;
+    RTile16<EMB, 1, steps<EMB / 4>()> tm;
     float ms = 0.f, mb = 0.f;
     if (mtp) {
         tm.load(a.mtp_w, 16 * mi, wave * (EMB / 4), H);
-        if (tid < 16) { ms = ldg(a.mtp_s + 16 * mi + tid); mb = ldg(a.mtp_b + 16 * mi + tid); }
+        if (tid < 16) { ms = WBF ? 1.f : ldg(a.mtp_s + 16 * mi + tid); mb = ldg(a.mtp_b + 16 * mi + tid); }
     }
     int tok = -1;
 #endif
@@ -1359,14 +1415,13 @@ __device__ __forceinline__ void role_idle(const Ctx &c, LdsP &s, int mi) {
             const QtPcScale ps = qt_pc_scale(fmaxf(fmaxf(s.wst[0], s.wst[1]), fmaxf(s.wst[2], s.wst[3])));
             pcw_put<EMB, 8>(s.pc, tid, v, ps.isc);
             wave_lds_order();   // unit tid: wave w makes the pieces of columns 512w .. +511, its own K slice
-            i32x4 acc[1];
-            rdot16<EMB, 1, EMB / 4 / 64, 1>(tm, s.pc, wave * (EMB / 4), acc);
+            AccT acc[1];
+            rdot16<EMB, 1, steps<EMB / 4>(), 1>(tm, s.pc, wave * (EMB / 4), acc);
             ksplit_store<1>(acc, s.red);
             if (tid < 16) {
-                int d[4];
+                RedT d[4];
                 ksplit_row(s.red, tid, d);
-                put(c.wp(par, 0, R_XIN + 16 * mi + tid),
-                    __fadd_rn(__fmul_rn(qt_pc_dot(d[0], d[1], d[2], d[3], ps.s), ms), mb));
+                put(c.wp(par, 0, R_XIN + 16 * mi + tid), __fadd_rn(row_dot(d, ps.s, ms), mb));
             }
             __syncthreads();   // s.wst, s.red free for the next pass
         }
@@ -1427,7 +1482,8 @@ extern "C" hipError_t QT_RS_NAME(qt_rstep, _trace_read)(unsigned long long *out)
 
 extern "C" int QT_RS_NAME(qt_rstep, _supported)(int prec, int hidden, int inter, int n_heads, int n_kv, int head_dim,
                                                 int kv_max, int n_layers) {
-    if (prec != QT_INT8 || hidden != ps::QT_RS_NS::H || inter != ps::QT_RS_NS::F) return 0;
+    if (prec != (ps::QT_RS_NS::WBF ? QT_BF16 : QT_INT8) || hidden != ps::QT_RS_NS::H || inter != ps::QT_RS_NS::F)
+        return 0;
     if (n_heads != ps::NH || n_kv != ps::NKV || head_dim != ps::HD) return 0;
     if (kv_max > ps::QT_RS_NS::ACH * ps::QT_RS_NS::ABLK * ps::KVB || n_layers < 1 || n_layers > ps::QT_RS_NS::MAXLR)
         return 0;
@@ -1478,14 +1534,14 @@ extern "C" hipError_t QT_RS_NAME(qt_launch_rstep, )(const void *layers_dev, int 
 // device array of 45 pointers (15 lm heads [vocab][1024] int8, their 15 row-scale arrays,
 // the 15 input tables: the Talker's codec embedding, then CP embeddings 0 .. 13).  codes[0]
 // is the frame's input code.
-extern "C" hipError_t qt_launch_rstep06_cp(const void *layers_dev, int n_layers, const float *final_norm,
+extern "C" hipError_t QT_RS_NAME(qt_launch_rstep, _cp)(const void *layers_dev, int n_layers, const float *final_norm,
                                            const float *rope_cos, const float *rope_sin, uint16_t *kc, uint16_t *vc,
                                            int kv_max, float eps, float scale, unsigned *reg, unsigned long long *slots,
                                            float *hid, float *decx, float *xin, int *d_pos, unsigned *epoch, int *err,
                                            int n_passes, const void *const *cp_tab, int vocab, int *codes,
                                            const uint8_t *mtp_w, const float *mtp_s, const float *mtp_b,
                                            hipStream_t st) {
-    namespace rs = ps::rs06;
+    namespace rs = ps::QT_RS_NS;
     rs::RArgs a = {};
     a.layers = (const ps::Layer *)layers_dev; a.n_layers = n_layers;
     a.final_norm = final_norm; a.rope_cos = rope_cos; a.rope_sin = rope_sin;
@@ -1498,11 +1554,12 @@ extern "C" hipError_t qt_launch_rstep06_cp(const void *layers_dev, int n_layers,
     a.cp_emb = reinterpret_cast<const uint16_t *const *>(cp_tab + 30);
     a.cp_codes = codes;
     a.mtp_w = mtp_w; a.mtp_s = mtp_s; a.mtp_b = mtp_b;
-    if (mtp_w && (!mtp_s || !mtp_b)) return hipErrorInvalidValue;
+    if (mtp_w && ((!rs::WBF && !mtp_s) || !mtp_b)) return hipErrorInvalidValue;
     if (n_passes < 1 || n_passes > 16 || n_passes > kv_max || n_layers <= 0 || n_layers > rs::MAXLR ||
         kv_max > rs::ACH * rs::ABLK * ps::KVB)
         return hipErrorInvalidValue;
     if (!cp_tab || !codes || !xin || vocab < 1 || vocab > rs::NHEAD * rs::HEADR) return hipErrorInvalidValue;
+    if (rs::WBF && vocab % rs::HEADR) return hipErrorInvalidValue;   // bf16 head tiles read whole 16-row tiles
     void *args[] = {(void *)&a};
     return hipLaunchCooperativeKernel((const void *)rs::k_rstep, dim3(ps::NB), dim3(rs::NT), args, 0, st);
 }

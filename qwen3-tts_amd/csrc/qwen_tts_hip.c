@@ -314,7 +314,8 @@ typedef struct {
     void *ps_layers;        /* device layer table */
     unsigned long long *ps_ring;   /* tagged activation words */
     int rs_on;              /* the role-specialised kernel (qt_rstep.hip) runs the fused step: 1 its 1.7B
-                             * build, 2 its 0.6B build (qt_rstep06.hip) */
+                             * build, 2 its 0.6B build (qt_rstep06.hip), 3 its 0.6B bf16 build
+                             * (qt_rstep06b.hip) */
     unsigned *rs_reg;       /* its hand-off words, [2][L][layer block], sentinel when empty */
     unsigned long long *rs_slots;  /* its tagged winner words */
     float *ps_xin;          /* step-0 input of a launch */
@@ -339,12 +340,20 @@ static int rstep_enabled(void) {
     return on;
 }
 
-/* Which build of the role-specialised kernel covers the stack: 1 (1.7B), 2 (0.6B), 0 none. */
+/* Which build of the role-specialised kernel covers the stack: 1 (1.7B int8), 2 (0.6B int8),
+ * 3 (0.6B bf16), 0 none. */
 static int rs_kind(const stack_t *s) {
     if (!rstep_enabled()) return 0;
     if (qt_rstep_supported(s->prec, s->H, s->F, s->nh, s->nkv, s->hd, s->kv_max, s->L)) return 1;
     if (qt_rstep06_supported(s->prec, s->H, s->F, s->nh, s->nkv, s->hd, s->kv_max, s->L)) return 2;
+    if (qt_rstep06b_supported(s->prec, s->H, s->F, s->nh, s->nkv, s->hd, s->kv_max, s->L)) return 3;
     return 0;
+}
+static size_t rs_region_words(int rk, int L) {
+    return rk == 3 ? qt_rstep06b_region_words(L) : rk == 2 ? qt_rstep06_region_words(L) : qt_rstep_region_words(L);
+}
+static size_t rs_slot_words(int rk) {
+    return rk == 3 ? qt_rstep06b_slot_words() : rk == 2 ? qt_rstep06_slot_words() : qt_rstep_slot_words();
 }
 
 static int persistent_enabled(void) {
@@ -388,8 +397,7 @@ static int ps_setup(talker_t *t) {
     if (rk) {
         /* hand-off words start empty (0xFF bytes: the sentinel), winner words with tag 0;
          * the per-kernel step splits attention into the same key chunks */
-        const size_t rw = rk == 2 ? qt_rstep06_region_words(s->L) : qt_rstep_region_words(s->L);
-        const size_t sw = rk == 2 ? qt_rstep06_slot_words() : qt_rstep_slot_words();
+        const size_t rw = rs_region_words(rk, s->L), sw = rs_slot_words(rk);
         HCK(hipMalloc((void **)&t->rs_reg, rw * sizeof(unsigned)));
         HCK(hipMalloc((void **)&t->rs_slots, sw * sizeof(unsigned long long)));
         HCK(hipMemsetAsync(t->rs_reg, 0xFF, rw * sizeof(unsigned), t->st));
@@ -431,7 +439,7 @@ fail:
 static hipError_t ps_launch_ex(talker_t *t, int n_steps, int with_head, float *layer_out) {
     stack_t *s = &t->s;
     if (t->rs_on)
-        return (t->rs_on == 2 ? qt_launch_rstep06 : qt_launch_rstep)(t->ps_layers, s->L, s->final_norm, s->rope_cos, s->rope_sin, s->kc, s->vc, s->kv_max, s->eps,
+        return (t->rs_on == 3 ? qt_launch_rstep06b : t->rs_on == 2 ? qt_launch_rstep06 : qt_launch_rstep)(t->ps_layers, s->L, s->final_norm, s->rope_cos, s->rope_sin, s->kc, s->vc, s->kv_max, s->eps,
                                1.0f / sqrtf((float)s->hd), t->rs_reg, t->rs_slots, t->io, t->io + s->H, t->ps_xin, t->d_pos,
                                t->ps_epoch, t->ps_err, n_steps, with_head,
                                with_head ? (const uint16_t *)t->head_m.w : NULL, with_head ? t->codec_emb : NULL,
@@ -1240,9 +1248,11 @@ typedef struct {
     int prefill2;                         /* 1: the frame starts with cp_prefill2_body */
     float *x2, *qkv2, *attn2, *h2;        /* device [2][H], [2][QKV], [2][qd], [2][F] */
     int8_t *pc2; float *ps2;              /* activation pieces of the two columns */
-    /* the whole frame as one launch of the role-specialised kernel's 0.6B build
-     * (qt_launch_rstep06_cp): int8 layers and lm heads, no mtp projection */
+    /* the whole frame as one launch of the role-specialised kernel's 0.6B build: int8 layers,
+     * lm heads and mtp projection (qt_launch_rstep06_cp) or all of them bf16
+     * (qt_launch_rstep06b_cp) */
     int rs_ok, rs_on;                     /* available / in use */
+    int rs_bf16;                          /* the bf16 build */
     void *rs_layers;                      /* device layer table */
     unsigned *rs_reg; unsigned long long *rs_slots;
     void **rs_tab;                        /* device [45]: lm heads, their scales, input tables */
@@ -1268,23 +1278,27 @@ static void cp_destroy(cp_t *c) {
     free(c);
 }
 
-/* The role-specialised frame's resources, when the CP qualifies: the 0.6B geometry, int8
- * weights in every layer and lm head, no mtp projection.  The per-kernel path then splits
- * its attention into the same key chunks with the same one-pass arithmetic, so the two
- * frames give the same bits. */
+/* The role-specialised frame's resources, when the CP qualifies: the 0.6B geometry, one
+ * precision (int8 or bf16) in every layer, lm head and the mtp projection (which must map the
+ * 2048-wide Talker hidden state).  The per-kernel path then splits its attention into the
+ * same key chunks with the same one-pass arithmetic; with int8 weights the two frames give
+ * the same bits, with bf16 weights the projections sum the same exact products in the MFMA's
+ * order instead of k_mv's. */
 static int cp_rs_setup(cp_t *c) {
     stack_t *s = &c->s;
     void *host_tab = NULL;
     void *ptab[45];
     const unsigned one = 1;
-    if (!rstep_enabled() || c->lm_prec != QWEN_HIP_INT8) return 0;
-    if (c->has_mtp && (c->mtp.prec != QWEN_HIP_INT8 || c->emb_dim != 2048 || c->talker_hidden != 2048)) return 0;
-    if (!qt_rstep06_supported(s->prec, s->H, s->F, s->nh, s->nkv, s->hd, s->kv_max, s->L)) return 0;
+    const int wp = c->lm_prec;
+    if (!rstep_enabled() || (wp != QWEN_HIP_INT8 && wp != QWEN_HIP_BF16)) return 0;
+    if (c->has_mtp && (c->mtp.prec != wp || c->emb_dim != 2048 || c->talker_hidden != 2048)) return 0;
+    const int rk = wp == QWEN_HIP_BF16 ? 3 : 2;
+    if (!(rk == 3 ? qt_rstep06b_supported : qt_rstep06_supported)(s->prec, s->H, s->F, s->nh, s->nkv, s->hd,
+                                                                   s->kv_max, s->L)) return 0;
     for (int l = 0; l < s->L; l++)
-        if (s->qkv[l].prec != QWEN_HIP_INT8 || s->o[l].prec != QWEN_HIP_INT8 || s->gu[l].prec != QWEN_HIP_INT8 ||
-            s->dn[l].prec != QWEN_HIP_INT8) return 0;
+        if (s->qkv[l].prec != wp || s->o[l].prec != wp || s->gu[l].prec != wp || s->dn[l].prec != wp) return 0;
     const size_t lb = qt_pstep_layer_bytes();
-    const size_t rw = qt_rstep06_region_words(s->L), sw = qt_rstep06_slot_words();
+    const size_t rw = rs_region_words(rk, s->L), sw = rs_slot_words(rk);
     HCK(hipMalloc((void **)&c->rs_reg, rw * sizeof(unsigned)));
     HCK(hipMalloc((void **)&c->rs_slots, sw * sizeof(unsigned long long)));
     HCK(hipMemsetAsync(c->rs_reg, 0xFF, rw * sizeof(unsigned), c->st));
@@ -1318,6 +1332,7 @@ static int cp_rs_setup(cp_t *c) {
     s->step_G = qt_rstep_chunks();
     s->step_onepass = 1;
     c->rs_ok = c->rs_on = 1;
+    c->rs_bf16 = rk == 3;
     return 0;
 fail:
     free(host_tab);
@@ -1326,7 +1341,7 @@ fail:
 
 static hipError_t cp_rs_launch_on(cp_t *c, hipStream_t st) {
     stack_t *s = &c->s;
-    return qt_launch_rstep06_cp(c->rs_layers, s->L, s->final_norm, s->rope_cos, s->rope_sin, s->kc, s->vc, s->kv_max,
+    return (c->rs_bf16 ? qt_launch_rstep06b_cp : qt_launch_rstep06_cp)(c->rs_layers, s->L, s->final_norm, s->rope_cos, s->rope_sin, s->kc, s->vc, s->kv_max,
                                 s->eps, 1.0f / sqrtf((float)s->hd), c->rs_reg, c->rs_slots, c->rs_io, c->rs_io + s->H,
                                 c->th, c->rs_pos, c->rs_epoch, c->rs_err, 16, (const void *const *)c->rs_tab,
                                 c->codebook, c->d_codes, c->has_mtp ? c->mtp.w : NULL,
@@ -1630,7 +1645,8 @@ fail:
 }
 
 /* Frames on the role-specialised kernel (on = 1, the default where the CP qualifies) or
- * on the per-kernel graph (0); both give the same bits.  Returns the mode in effect. */
+ * on the per-kernel graph (0); int8 weights give the same bits both ways, bf16 weights the
+ * same codes with K/V within f32 rounding.  Returns the mode in effect. */
 int qwen_hip_cp_fused(void *state, int on) {
     cp_t *c = (cp_t *)state;
     if (!c || c->dead) { SETERR("CP state is dead or NULL"); return -1; }

@@ -239,12 +239,21 @@ def test_upload_kv_roundtrip_and_resume():
 def test_fused_step_matches_kernel_sequence(name, prec):
     """The default step (one persistent kernel, or the captured graph where that is
     unavailable) against the plain launch sequence: same per-row arithmetic (int8: the
-    same exact integer piece sums, MFMA in the fused step at hidden 2048, v_dot4 in the
-    matvec kernel), so the residual stream is bit-identical; the final RMSNorm reduces in
-    a different order."""
+    same exact integer piece sums, MFMA in the fused step, v_dot4 in the matvec kernel),
+    so the residual stream is bit-identical; the final RMSNorm reduces in a different
+    order.  mini bf16 runs the role-specialised kernel's bf16 build: its projections sum
+    the same exact products (bf16 weight x three exact bf16 pieces of the activation) in
+    the MFMA's f32 order instead of the matvec kernel's, so the projections agree to f32
+    rounding; a K/V element whose two f32 values straddle a bf16 truncation boundary
+    (about 1 in 16000) then differs by one bf16 ulp, and that flip moves the residual
+    stream by ~1e-4.  The two paths are held to the bounds the per-kernel path meets
+    against the reference (rel-L2 1e-3 on the residual stream, K/V rows within rel-L2
+    1e-2) and to few K/V flips."""
     print(f"[case] fused vs kernels {name} {prec}", flush=True)
     ref, shape, _ = _ref(name, prec)
     pc = hip.PREC[prec]
+    exact = not (name == "mini" and prec == "bf16")
+    worst = 0.0
     ga = _gpu_talker(ref, shape, pc)
     gb = _gpu_talker(ref, shape, pc)
     emb = ref.codec_emb()
@@ -252,11 +261,31 @@ def test_fused_step_matches_kernel_sequence(name, prec):
         e = synth.bf16_to_f32(emb[pos])
         a = ga.step(e, pos, graph=True)
         b = gb.step(e, pos, graph=False)
-        assert np.array_equal(ga.dec_x(), gb.dec_x()), pos
-        assert rel_l2(a, b) < 1e-6, pos
+        if exact:
+            assert np.array_equal(ga.dec_x(), gb.dec_x()), pos
+            assert rel_l2(a, b) < 1e-6, pos
+        else:
+            assert rel_l2(ga.dec_x(), gb.dec_x()) < 1e-3, (pos, rel_l2(ga.dec_x(), gb.dec_x()))
+            assert rel_l2(a, b) < 1e-3, pos
+        worst = max(worst, rel_l2(ga.dec_x(), gb.dec_x()))
+    print(f"[result] fused vs kernels {name} {prec}: worst residual rel-L2 {worst:.2e}")
     ka, va = ga.download_kv(10)
     kb, vb = gb.download_kv(10)
-    assert np.array_equal(ka, kb) and np.array_equal(va, vb)
+    if exact:
+        assert np.array_equal(ka, kb) and np.array_equal(va, vb)
+    else:
+        _kv_close(ka[:, :10], kb[:, :10])
+        _kv_close(va[:, :10], vb[:, :10])
+
+
+def _kv_close(x, y):
+    """bf16 caches of two paths whose projections differ only in f32 summation order:
+    rows within rel-L2 1e-2, and at most 5 % of the elements differing."""
+    fx, fy = synth.bf16_to_f32(x).astype(np.float64), synth.bf16_to_f32(y).astype(np.float64)
+    num = np.linalg.norm(fx - fy, axis=-1)
+    den = np.linalg.norm(fy, axis=-1)
+    assert (num <= 1e-2 * den + 1e-6).all(), float((num / np.maximum(den, 1e-30)).max())
+    assert (x != y).mean() < 0.05, float((x != y).mean())
 
 
 @need_ref
@@ -474,17 +503,19 @@ def test_cp_frame_codes_match_reference(name, prec):
 
 
 @need_ref
-@pytest.mark.parametrize("name", ["mini", "mini17"])
-def test_cp_frame_fused_matches_launch_graph(name):
-    """int8 CP (CP layers of the 0.6B geometry; mini17: with the 1.7B Talker's mtp
-    projection 2048 -> 1024 in front of every pass): the frame as one launch of the
-    role-specialised kernel and as the per-kernel launch graph give the same codes and the
-    same K/V of all 16 positions, bit for bit, over frames back to back, and the codes are
-    the reference's qwen_cp_predict (the fused frame is the default)."""
-    print(f"[case] fused CP frame {name}", flush=True)
-    ref, shape, _ = _ref(name, "int8")
-    cp = _gpu_cp(ref, shape, hip.INT8)
-    assert cp.fused(True), "the 0.6B int8 CP should take the fused frame"
+@pytest.mark.parametrize("name,prec", [("mini", "int8"), ("mini17", "int8"), ("mini", "bf16"), ("mini17", "bf16")])
+def test_cp_frame_fused_matches_launch_graph(name, prec):
+    """CP layers of the 0.6B geometry (mini17: with the 1.7B Talker's mtp projection
+    2048 -> 1024 in front of every pass): the frame as one launch of the role-specialised
+    kernel and as the per-kernel launch graph give the same codes over frames back to back,
+    the codes are the reference's qwen_cp_predict (the fused frame is the default), and the
+    K/V of all 16 positions are the same bits with int8 weights.  With bf16 weights the
+    fused frame's projections sum the same exact products in the MFMA's f32 order, so its
+    K/V are held to rel-L2 1e-2 per row with few elements differing."""
+    print(f"[case] fused CP frame {name} {prec}", flush=True)
+    ref, shape, _ = _ref(name, prec)
+    cp = _gpu_cp(ref, shape, hip.PREC[prec])
+    assert cp.fused(True), f"the 0.6B {prec} CP should take the fused frame"
     rng = np.random.default_rng(11)
     for f in range(5):
         th = rng.standard_normal(shape.hidden).astype(np.float32)
@@ -497,7 +528,11 @@ def test_cp_frame_fused_matches_launch_graph(name):
         b = list(cp.frame(th, code0))
         kb, vb = cp.download_kv(16)
         assert a == b, (f, a, b)
-        assert np.array_equal(ka, kb) and np.array_equal(va, vb), f
+        if prec == "int8":
+            assert np.array_equal(ka, kb) and np.array_equal(va, vb), f
+        else:
+            _kv_close(ka, kb)
+            _kv_close(va, vb)
         assert a == list(ref.cp_predict(th, code0)), f
     cp.fused(True)
 
