@@ -94,10 +94,10 @@ FUSED_KERNELS = {
 
 def fused_label(L, g, prec, hidden):
     """Name of the kernel that runs the state's fused step (qt_rstep.hip is built per geometry
-    and weight type: ps::rs for hidden 2048, ps::rs06 for hidden 1024 int8, ps::rs06b for hidden
-    1024 bf16)."""
+    and weight type: ps::rs for hidden 2048 int8, ps::rs4 for hidden 2048 q4_0, ps::rs06 for
+    hidden 1024 int8, ps::rs06b for hidden 1024 bf16)."""
     kind = L.qwen_hip_talker_fused_kernel(g.h)
-    ns = "rs" if hidden == 2048 else ("rs06b" if prec == "bf16" else "rs06")
+    ns = ("rs4" if prec == "int4" else "rs") if hidden == 2048 else ("rs06b" if prec == "bf16" else "rs06")
     return kind, FUSED_KERNELS.get(kind, ("unfused per-kernel path",))[0].format(prec=prec, ns=ns)
 
 

@@ -131,6 +131,18 @@ hipError_t qt_launch_rstep06b_cp(const void *layers_dev, int n_layers, const flo
                                  int *d_pos, unsigned *epoch, int *err, int n_passes, const void *const *cp_tab,
                                  int vocab, int *codes, const uint8_t *mtp_w, const float *mtp_s, const float *mtp_b,
                                  hipStream_t st);
+/* the same kernel's 1.7B build with q4_0 weights (qt_rstep4.hip): integer MFMA on the exact
+ * int8 activation planes, each block's f16 scale applied to its exact sums; layer tables
+ * point at the qs rows (w) and the [rows][cols/32] f16 scales (s16) */
+int qt_rstep4_supported(int prec, int hidden, int inter, int n_heads, int n_kv, int head_dim, int kv_max, int n_layers);
+size_t qt_rstep4_region_words(int n_layers);
+size_t qt_rstep4_slot_words(void);
+hipError_t qt_launch_rstep4(const void *layers_dev, int n_layers, const float *final_norm, const float *rope_cos,
+                            const float *rope_sin, uint16_t *kc, uint16_t *vc, int kv_max, float eps, float scale,
+                            unsigned *reg, unsigned long long *slots, float *hid, float *decx, float *xin, int *d_pos,
+                            unsigned *epoch, int *err, int n_steps, int with_head, const uint16_t *head_w,
+                            const uint16_t *emb, int vocab, int *d_frame, int *hist, int hist_len, float *layer_out,
+                            hipStream_t st);
 /* persistent decode step (qt_pstep.hip) */
 int qt_pstep_supported(int prec, int hidden, int inter, int n_heads, int n_kv, int head_dim, int kv_max);
 size_t qt_pstep_ring_words(int hidden, int inter, int n_layers);

@@ -53,6 +53,9 @@
 #if defined(QT_RS_SMALL) && defined(QT_RS_BF16)
 #define QT_RS_NS rs06b
 #define QT_RS_NAME(a, b) a##06b##b
+#elif defined(QT_RS_Q4)
+#define QT_RS_NS rs4
+#define QT_RS_NAME(a, b) a##4##b
 #elif defined(QT_RS_SMALL)
 #define QT_RS_NS rs06
 #define QT_RS_NAME(a, b) a##06##b
@@ -80,7 +83,14 @@ constexpr bool WBF = true;
 #else
 constexpr bool WBF = false;
 #endif
-constexpr int WB = WBF ? 2 : 1;                  // bytes per weight
+#ifdef QT_RS_Q4
+constexpr bool WQ4 = true;                       // q4_0 rows (1.7B geometry only): see QTile16
+#else
+constexpr bool WQ4 = false;
+#endif
+constexpr bool RSC = !WBF && !WQ4;               // int8 rows carry a row scale
+constexpr int PREC = WBF ? QT_BF16 : WQ4 ? QT_Q4 : QT_INT8;
+constexpr int WB = WBF ? 2 : 1;                  // bytes per weight (q4_0: 64 columns per MFMA step too)
 constexpr int NPL = WBF ? 3 : 4;                 // activation planes
 constexpr int KSTEP = 64 / WB;                   // columns per MFMA step
 template <int C> constexpr int steps() { return C * WB / 64; }   // MFMA steps over C columns
@@ -309,6 +319,19 @@ __device__ __forceinline__ void pcw_put(uint8_t *pc, int u, const float (&v)[E],
             else
                 *reinterpret_cast<uint2 *>(pc + q * pcs<COLS>() + 8 * u) = *reinterpret_cast<const uint2 *>(p3[q]);
         }
+    } else if constexpr (WQ4) {
+        // q4_0: each 16-column group is stored even columns first, then odd ones (the
+        // order of a q4_0 byte's low and high nibbles as QTile16's B operand holds them)
+        static_assert(E == 8, "q4_0 pieces: 8-element units");
+        uint2 pl[4];
+        qt_pc8(v, isc, pl);
+        const int g = u >> 1, sub = u & 1;
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            uint8_t *d = pc + q * pcs<COLS>() + 16 * g + 4 * sub;
+            *reinterpret_cast<uint32_t *>(d) = __builtin_amdgcn_perm(pl[q].y, pl[q].x, 0x06040200u);
+            *reinterpret_cast<uint32_t *>(d + 8) = __builtin_amdgcn_perm(pl[q].y, pl[q].x, 0x07050301u);
+        }
     } else if constexpr (E == 8) {
         uint2 pl[4];
         qt_pc8(v, isc, pl);
@@ -353,15 +376,21 @@ struct RTile16 {
             }
         }
     }
+    __device__ __forceinline__ void load(const uint8_t *W, const uint16_t *, int row0, int c0, int row_end) {
+        load(W, row0, c0, row_end);
+    }
 };
 // the build's MFMA: exact int32 plane sums (int8) or f32 sums of exact products (bf16)
-using AccT = std::conditional_t<WBF, qt_f32x4, i32x4>;
-using RedT = std::conditional_t<WBF, float, int>;
+using AccT = std::conditional_t<WQ4, float, std::conditional_t<WBF, qt_f32x4, i32x4>>;
+using RedT = std::conditional_t<WBF || WQ4, float, int>;
 #ifdef QT_RS_BF16
 __device__ __forceinline__ AccT mma(uint4 w, uint4 p, AccT acc) {
     return qt_mfma_bf16(qt_u32x4{w.x, w.y, w.z, w.w}, qt_u32x4{p.x, p.y, p.z, p.w}, acc);
 }
 __device__ __forceinline__ AccT acc_zero() { return qt_f32x4{0.f, 0.f, 0.f, 0.f}; }
+#elif defined(QT_RS_Q4)
+__device__ __forceinline__ i32x4 mma(uint4 w, uint4 p, i32x4 acc) { return mfma_i8(w, p, acc); }
+__device__ __forceinline__ i32x4 acc_zero() { return i32x4{0, 0, 0, 0}; }
 #else
 __device__ __forceinline__ AccT mma(uint4 w, uint4 p, AccT acc) { return mfma_i8(w, p, acc); }
 __device__ __forceinline__ AccT acc_zero() { return i32x4{0, 0, 0, 0}; }
@@ -369,7 +398,8 @@ __device__ __forceinline__ AccT acc_zero() { return i32x4{0, 0, 0, 0}; }
 // acc[t] = tile t against the pieces of columns c0 .. c0 + KSTEP*S; CH accumulator chains
 // per tile so that no MFMA waits for the previous one of its chain
 template <int COLS, int NT16, int S, int CH>
-__device__ __forceinline__ void rdot16(const RTile16<COLS, NT16, S> &t, const uint8_t *pc, int c0, AccT (&acc)[NT16]) {
+__device__ __forceinline__ void rdot16(const RTile16<COLS, NT16, S> &t, const uint8_t *pc, int c0, AccT (&acc)[NT16],
+                                       const int * = nullptr) {
     AccT a[NT16][CH];
 #pragma unroll
     for (int q = 0; q < NT16; q++)
@@ -390,6 +420,169 @@ __device__ __forceinline__ void rdot16(const RTile16<COLS, NT16, S> &t, const ui
         for (int c = 1; c < CH; c++) acc[q] += a[q][c];
     }
 }
+#ifdef QT_RS_Q4
+// ---- q4_0 row tiles ------------------------------------------------------------------------
+// The reference's q4_0 blocks (32 weights w = (n - 8) d, byte i holding n of weights 2i
+// (low nibble) and 2i+1, one f16 scale d; qwen_tts_kernels.c:2815-2816) on the same
+// v_mfma_i32_16x16x64_i8 with the operands swapped: A = the activation pieces, row 4h+p =
+// plane p over block h of the 64-column step (the other block's columns zero, rows 8..15
+// zero), B = 16 weight rows of unsigned nibbles n (lane l: row l%16, the 16 weights
+// 16*(l/16) .. +15 of the step, even ones then odd ones, the pieces' storage order).  Lane
+// l < 32 ends with the four exact plane sums of n*p for row l%16 over block l/16 of the
+// step; subtracting 8 * (the block's piece sums, made once per input by q4_psum) gives the
+// exact sums of (n - 8)*p, the four planes join in two exact 23-bit halves, and the block
+// scale times their f32 value is added to the lane's f32 sum over its blocks.
+// binary16 bits -> f32 as ref_f16_to_f32 (the reference's portable conversion, its
+// subnormal mapping included), with selects instead of branches
+__device__ __forceinline__ float f16_ref_sel(uint32_t h) {
+    const uint32_t sign = (h & 0x8000u) << 16, em = h & 0x7FFFu;
+    const uint32_t sh = ((uint32_t)__clz((int)(em | 1u)) - 21u) & 31u, ms = em << sh;   // (subnormals: 1..10)
+    const uint32_t bi = sign | 0x7F800000u | ((em & 0x3FFu) << 13);
+    const uint32_t bn = sign | ((em + (112u << 10)) << 13);
+    const uint32_t bs = sign | ((112u - sh) << 23) | ((ms & 0x3FFu) << 13);
+    return __uint_as_float(em >= 0x7C00u ? bi : em >= 0x0400u ? bn : em == 0 ? sign : bs);
+}
+template <int COLS, int NT16, int S>
+struct QTile16 {
+    uint2 w[NT16][S];     // the lane's 8 nibble bytes of each tile and step
+    // the block scales go to the wave's LDS area sd[(s*64 + lane)*NT16 + t] (f32; scale of
+    // row l%16 of tile t, block 2s + (l/16)%2 of the slice), which keeps the registers for
+    // the MFMA results
+    static constexpr int SD = S * 64 * NT16;   // floats per wave
+    __device__ __forceinline__ void load(const uint8_t *W, const uint16_t *S16, int row0, int c0, int row_end, float *sd) {
+        typedef unsigned u32x2_t __attribute__((ext_vector_type(2)));
+        const int lane = threadIdx.x & 63, m = lane & 15, kg = lane >> 4, h = kg & 1;
+        const __amdgpu_buffer_rsrc_t r = brsrc(uni(W)), rq = brsrc(uni(S16));
+        const unsigned voff = (unsigned)(m * (COLS / 2) + 8 * kg);
+        const unsigned soff = (unsigned)(m * (COLS / 32) * 2);
+        static_assert(S % 4 == 0, "scale groups");
+        // every load of every tile is issued before the first scale is converted (a
+        // conversion waits for its load, and with it for every load issued before it)
+        unsigned raw[NT16][S];   // dword s: the f16 scales of blocks 2s, 2s+1 of the slice
+#pragma unroll
+        for (int t = 0; t < NT16; t++) {
+            const bool ok = row0 + 16 * t + m < row_end;
+#pragma unroll
+            for (int s = 0; s < S; s++) {
+                const u32x2_t v = ok ? __builtin_amdgcn_raw_buffer_load_b64(
+                                           r, voff, __builtin_amdgcn_readfirstlane(((row0 + 16 * t) * COLS + c0) / 2 + 32 * s), 0)
+                                     : u32x2_t{0, 0};
+                w[t][s] = make_uint2(v.x, v.y);
+            }
+#pragma unroll
+            for (int j = 0; j < S / 4; j++) {
+                const u32x4_t v = ok ? __builtin_amdgcn_raw_buffer_load_b128(
+                                           rq, soff, __builtin_amdgcn_readfirstlane(((row0 + 16 * t) * (COLS / 32) + c0 / 32) * 2 + 16 * j), 0)
+                                     : u32x4_t{0, 0, 0, 0};
+                raw[t][4 * j] = v.x; raw[t][4 * j + 1] = v.y; raw[t][4 * j + 2] = v.z; raw[t][4 * j + 3] = v.w;
+            }
+        }
+#pragma unroll
+        for (int s = 0; s < S; s++) {
+            float v[NT16];
+#pragma unroll
+            for (int t = 0; t < NT16; t++) v[t] = f16_ref_sel(h ? raw[t][s] >> 16 : raw[t][s] & 0xFFFFu);
+            float *dst = sd + (s * 64 + lane) * NT16;
+            if constexpr (NT16 % 4 == 0) {
+#pragma unroll
+                for (int t = 0; t < NT16; t += 4)
+                    *reinterpret_cast<float4 *>(dst + t) = make_float4(v[t], v[t + 1], v[t + 2], v[t + 3]);
+            } else {
+#pragma unroll
+                for (int t = 0; t < NT16; t++) dst[t] = v[t];
+            }
+        }
+    }
+};
+// 8 x the piece sums of each 32-column block of the wave's slice (KW columns from c0), two
+// per block: pq[2b] = 8 (P0 + 2^8 P1), pq[2b+1] = 8 (P2 + 2^8 P3), P_p the sum of plane p
+template <int COLS, int KW>
+__device__ __forceinline__ void q4_psum(const uint8_t *pc, int c0, int *pq) {
+    constexpr int NBK = KW / 32;
+    static_assert(NBK % 16 == 0, "blocks per lane");
+    const int lane = threadIdx.x & 63, p = lane & 3;
+#pragma unroll
+    for (int k = 0; k < NBK / 16; k++) {
+        const int b = (lane >> 2) + 16 * k;
+        const uint4 *src = reinterpret_cast<const uint4 *>(pc + p * pcs<COLS>() + c0 + 32 * b);
+        const uint4 x0 = src[0], x1 = src[1];
+        int sum = 0;
+        sum = __builtin_amdgcn_sdot4((int)x0.x, 0x01010101, sum, false);
+        sum = __builtin_amdgcn_sdot4((int)x0.y, 0x01010101, sum, false);
+        sum = __builtin_amdgcn_sdot4((int)x0.z, 0x01010101, sum, false);
+        sum = __builtin_amdgcn_sdot4((int)x0.w, 0x01010101, sum, false);
+        sum = __builtin_amdgcn_sdot4((int)x1.x, 0x01010101, sum, false);
+        sum = __builtin_amdgcn_sdot4((int)x1.y, 0x01010101, sum, false);
+        sum = __builtin_amdgcn_sdot4((int)x1.z, 0x01010101, sum, false);
+        sum = __builtin_amdgcn_sdot4((int)x1.w, 0x01010101, sum, false);
+        const int hi = __shfl_xor(sum, 1, 64);   // the next plane's sum
+        if ((p & 1) == 0) pq[2 * b + (p >> 1)] = 8 * (sum + 256 * hi);
+    }
+    wave_lds_order();
+}
+template <int COLS, int NT16, int S, int CH>
+__device__ __forceinline__ void rdot16(const QTile16<COLS, NT16, S> &t, const uint8_t *pc, int c0, float (&acc)[NT16],
+                                       const int *pq, const float *sd) {
+    const int lane = threadIdx.x & 63, m = lane & 15, kg = lane >> 4, h = kg & 1;
+    const bool arow = m < 8 && (m >> 2) == (kg >> 1);
+    const uint8_t *pa = pc + (m & 3) * pcs<COLS>() + c0 + 16 * kg;
+    // (loads unconditional, masked with an AND: every address is inside the pieces, and a
+    // select between two uint4 values compiles to a private-memory round trip)
+    const unsigned am = arow ? 0xFFFFFFFFu : 0u;
+    auto ld_a = [&](int off) {
+        const uint4 v = *reinterpret_cast<const uint4 *>(pa + off);
+        return make_uint4(v.x & am, v.y & am, v.z & am, v.w & am);
+    };
+#pragma unroll
+    for (int q = 0; q < NT16; q++) acc[q] = 0.f;
+    uint4 a = ld_a(0);
+#pragma unroll
+    for (int s = 0; s < S; s++) {
+        const int sn = s + 1 < S ? s + 1 : s;
+        const uint4 an = ld_a(64 * sn);
+        const int2 qc = *reinterpret_cast<const int2 *>(pq + 4 * s + 2 * h);
+        float d[NT16];
+        const float *ds = sd + (s * 64 + lane) * NT16;
+        if constexpr (NT16 % 4 == 0) {
+#pragma unroll
+            for (int q = 0; q < NT16; q += 4) {
+                const float4 v = *reinterpret_cast<const float4 *>(ds + q);
+                d[q] = v.x; d[q + 1] = v.y; d[q + 2] = v.z; d[q + 3] = v.w;
+            }
+        } else {
+#pragma unroll
+            for (int q = 0; q < NT16; q++) d[q] = ds[q];
+        }
+        i32x4 D[NT16];   // every MFMA of the step first, then the epilogues (results in flight)
+#pragma unroll
+        for (int q = 0; q < NT16; q++) {
+            const uint2 w = t.w[q][s];
+            const uint4 b = make_uint4(w.x & 0x0F0F0F0Fu, w.y & 0x0F0F0F0Fu, (w.x >> 4) & 0x0F0F0F0Fu,
+                                       (w.y >> 4) & 0x0F0F0F0Fu);
+            D[q] = mfma_i8(a, b, i32x4{0, 0, 0, 0});
+        }
+#pragma unroll
+        for (int q = 0; q < NT16; q++) {
+            const int lo = D[q][0] + (D[q][1] << 8) - qc.x, hi = D[q][2] + (D[q][3] << 8) - qc.y;
+            acc[q] = fmaf(d[q], fmaf((float)hi, 65536.f, (float)lo), acc[q]);
+        }
+        a = an;
+        // keep each step's epilogue here: the sums feed only the lanes < 32 store after the
+        // loop, and the compiler would otherwise sink every step's epilogue down to that
+        // store, holding all the MFMA results at once (spills)
+#pragma unroll
+        for (int q = 0; q < NT16; q++) asm volatile("" : "+v"(acc[q]));
+    }
+}
+template <int COLS, int NT16, int S> using WTile = QTile16<COLS, NT16, S>;
+#define RS_PQ(s, w) (&(s).pq[w][0])
+#define RS_SD(s, w) , (&(s).sd[w][0])
+#else
+template <int COLS, int KW> __device__ __forceinline__ void q4_psum(const uint8_t *, int, int *) {}
+template <int COLS, int NT16, int S> using WTile = RTile16<COLS, NT16, S>;
+#define RS_PQ(s, w) nullptr
+#define RS_SD(s, w)
+#endif
 // ---- LDS --------------------------------------------------------------------------------
 struct HeadLds {
     float x[H];                  // x of the last layer, chunk-transposed (EPC 8)
@@ -409,6 +602,10 @@ struct HeadLds {
 struct LdsP {                    // Q, O, GU (and the head-only workgroups)
     float xs[H];                 // the input in element order (RMSNorm: statistics order -> unit order)
     uint8_t pc[NPL * pcs<PCW>()];
+#ifdef QT_RS_Q4
+    int pq[4][2 * (PCW / 4 / 32)];   // per wave: 8 x its blocks' piece sums (q4_psum)
+    float sd[4][(PCW / 4 / 64) * 64 * 8];   // per wave: its tiles' block scales (QTile16)
+#endif
     RedT red[8 * 16][4][4];      // partial plane sums [row][wave][plane] (K split over the waves)
     float resid[OROWS];
     float wst[8];
@@ -416,7 +613,12 @@ struct LdsP {                    // Q, O, GU (and the head-only workgroups)
 };
 struct LdsD {                    // DN
     uint8_t pc[NPL * pcs<F>()];
+#ifdef QT_RS_Q4
+    int pq[4][2 * (F / 4 / 32)];     // per wave: 8 x its blocks' piece sums (q4_psum)
+    float sd[4][(F / 4 / 64) * 64 * 3];   // per wave: its tiles' block scales (QTile16)
+#else
     uint4 tw[4][steps<F / 4>()][64]; // tile 2 (rows 32..47): [wave][step][lane]
+#endif
     RedT red[4][3][16][4];       // partial plane sums [wave][tile][row][plane]
     float resid[48];
     float wst[8];
@@ -489,6 +691,18 @@ __device__ __forceinline__ void ksplit_store(const A (&acc)[NT16], T (*red)[4][4
     }
     __syncthreads();
 }
+#ifdef QT_RS_Q4
+// q4_0: lane l < 32 holds row l%16's f32 sum over block half l/16: red[row][wave][half]
+template <int NT16>
+__device__ __forceinline__ void ksplit_store(const float (&acc)[NT16], float (*red)[4][4]) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    if (lane < 32) {
+#pragma unroll
+        for (int t = 0; t < NT16; t++) red[16 * t + (lane & 15)][wave][lane >> 4] = acc[t];
+    }
+    __syncthreads();
+}
+#endif
 template <typename T>
 __device__ __forceinline__ void ksplit_row(const T (*red)[4][4], int r, T (&d)[4]) {
 #pragma unroll
@@ -496,9 +710,14 @@ __device__ __forceinline__ void ksplit_row(const T (*red)[4][4], int r, T (&d)[4
 }
 // a row's dot product from its plane sums: int8 s*(D0 + 2^8 D1 + 2^16 D2 + 2^24 D3) times
 // the row scale rs; bf16 the three planes' f32 sums added hi to lo (no row scale)
+// (q4_0: the two block halves' f32 sums times the pieces' scale; the block scales are in)
 __device__ __forceinline__ float row_dot(const RedT (&d)[4], float s, float rs) {
+#if defined(QT_RS_Q4)
+    return (d[0] + d[1]) * s;
+#else
     if constexpr (WBF) return (d[0] + d[1]) + d[2];
     else return __fmul_rn(qt_pc_dot(d[0], d[1], d[2], d[3], s), rs);
+#endif
 }
 
 // Pieces of RMSNorm(x)*g: x arrives in the statistics' order (thread t: elements t + NT*k),
@@ -735,12 +954,12 @@ __device__ __forceinline__ void role_q(const Ctx &c, LdsP &s, int grp, int qi) {
     const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     // 128 rows; wave w takes columns (H/4)w .. +H/4-1 of all of them
     const int row0 = qi < 2 ? (2 * grp + qi) * HD : qi == 2 ? QD + grp * HD : QD + KVD + grp * HD;
-    RTile16<H, 8, steps<H / 4>()> t;
+    WTile<H, 8, steps<H / 4>()> t;
     float rs = WBF ? 1.f : 0.f;   // bf16 rows carry no scale
     float gc[EH], gu[EH];
     auto load = [&](int l) {
-        t.load(c.ly[l].w[0], row0, wave * (H / 4), row0 + QROWS);
-        if (!WBF && tid < QROWS) rs = ldg(uni(c.ly[l].s[0]) + row0 + tid);
+        t.load(c.ly[l].w[0], c.ly[l].s16[0], row0, wave * (H / 4), row0 + QROWS RS_SD(s, wave));
+        if (RSC && tid < QROWS) rs = ldg(uni(c.ly[l].s[0]) + row0 + tid);
         load_norm_gains(c.ly[l].in_norm, gc, gu);
     };
     HeadTile ht;
@@ -775,9 +994,10 @@ __device__ __forceinline__ void role_q(const Ctx &c, LdsP &s, int grp, int qi) {
                 for (int k = 0; k < EH; k++) xv[k] = __uint_as_float(v[k]);
             }
             const float sA = norm_pieces(xv, gc, gu, s.xs, s.wst, s.pc, a.eps);
+            q4_psum<H, H / 4>(s.pc, wave * (H / 4), RS_PQ(s, wave));
             RS_MARK(step, l, 6);
             AccT acc[8];
-            rdot16<H, 8, steps<H / 4>(), 1>(t, s.pc, wave * (H / 4), acc);
+            rdot16<H, 8, steps<H / 4>(), 1>(t, s.pc, wave * (H / 4), acc, RS_PQ(s, wave) RS_SD(s, wave));
             RS_MARK(step, l, 7);
             ksplit_store<8>(acc, s.red);
             if (tid < QROWS) {
@@ -818,11 +1038,11 @@ __device__ __forceinline__ void role_o(const Ctx &c, LdsP &s, int oi) {
     const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int row0 = oi * OROWS;
     constexpr int OT = OROWS / 16;   // row tiles (8 int8, 4 bf16)
-    RTile16<QD, OT, steps<QD / 4>()> t;
+    WTile<QD, OT, steps<QD / 4>()> t;
     float rs = WBF ? 1.f : 0.f;   // bf16 rows carry no scale
     auto load = [&](int l) {
-        t.load(c.ly[l].w[1], row0, wave * (QD / 4), row0 + OROWS);
-        if (!WBF && tid < OROWS) rs = ldg(uni(c.ly[l].s[1]) + row0 + tid);
+        t.load(c.ly[l].w[1], c.ly[l].s16[1], row0, wave * (QD / 4), row0 + OROWS RS_SD(s, wave));
+        if (RSC && tid < OROWS) rs = ldg(uni(c.ly[l].s[1]) + row0 + tid);
     };
     HeadTile ht;
     load_gains<4, 8, H>(a.final_norm, s.hd.gain);
@@ -864,9 +1084,10 @@ __device__ __forceinline__ void role_o(const Ctx &c, LdsP &s, int oi) {
                 pcw_put<QD, 8>(s.pc, tid, v8, ps.isc);
             }
             wave_lds_order();   // unit tid: wave w makes the pieces of columns 512w .. +511, its own K slice
+            q4_psum<QD, QD / 4>(s.pc, wave * (QD / 4), RS_PQ(s, wave));
             RS_MARK(step, l, 6);
             AccT acc[OT];
-            rdot16<QD, OT, steps<QD / 4>(), 1>(t, s.pc, wave * (QD / 4), acc);
+            rdot16<QD, OT, steps<QD / 4>(), 1>(t, s.pc, wave * (QD / 4), acc, RS_PQ(s, wave) RS_SD(s, wave));
             RS_MARK(step, l, 7);
             ksplit_store<OT>(acc, s.red);
             if (tid < OROWS) {
@@ -895,12 +1116,12 @@ __device__ __forceinline__ void role_gu(const Ctx &c, LdsP &s, int gi) {
     const RArgs &a = c.a;
     const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int row0 = gi * GROWS;
-    RTile16<H, 8, steps<H / 4>()> t;
+    WTile<H, 8, steps<H / 4>()> t;
     float rsg = WBF ? 1.f : 0.f, rsu = rsg;
     float gc[EH], gu[EH];
     auto load = [&](int l) {
-        t.load(c.ly[l].w[2], row0, wave * (H / 4), row0 + GROWS);
-        if (!WBF && tid < GROWS / 2) {
+        t.load(c.ly[l].w[2], c.ly[l].s16[2], row0, wave * (H / 4), row0 + GROWS RS_SD(s, wave));
+        if (RSC && tid < GROWS / 2) {
             const float *S = uni(c.ly[l].s[2]);
             rsg = ldg(S + row0 + 2 * tid);
             rsu = ldg(S + row0 + 2 * tid + 1);
@@ -926,9 +1147,10 @@ __device__ __forceinline__ void role_gu(const Ctx &c, LdsP &s, int gi) {
                 for (int k = 0; k < EH; k++) xv[k] = __uint_as_float(v[k]);
             }
             const float sD = norm_pieces(xv, gc, gu, s.xs, s.wst, s.pc, a.eps);
+            q4_psum<H, H / 4>(s.pc, wave * (H / 4), RS_PQ(s, wave));
             RS_MARK(step, l, 6);
             AccT acc[8];
-            rdot16<H, 8, steps<H / 4>(), 1>(t, s.pc, wave * (H / 4), acc);
+            rdot16<H, 8, steps<H / 4>(), 1>(t, s.pc, wave * (H / 4), acc, RS_PQ(s, wave) RS_SD(s, wave));
             RS_MARK(step, l, 7);
             ksplit_store<8>(acc, s.red);
             if (tid < GROWS / 2) {
@@ -964,12 +1186,17 @@ __device__ __forceinline__ void role_gu(const Ctx &c, LdsP &s, int gi) {
 __device__ __forceinline__ void role_dn(const Ctx &c, LdsD &s, int di) {
     const RArgs &a = c.a;
     const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int m16 = lane & 15, kg = lane >> 4;
+    [[maybe_unused]] const int m16 = lane & 15, kg = lane >> 4;
     const bool big = di < NDB;                 // NDB workgroups of 48 rows, the others 40
     const int row0 = big ? 48 * di : 48 * NDB + 40 * (di - NDB);
     const int nrows = big ? 48 : 40;
     constexpr int KW = F / 4, S = steps<KW>();  // columns and 64-byte MFMA steps per wave
     const int c0 = wave * KW;
+#ifdef QT_RS_Q4
+    QTile16<F, 3, S> t;           // all three tiles in registers (half the bytes of int8)
+    float rs = 0.f;
+    auto load = [&](int l) { t.load(c.ly[l].w[3], c.ly[l].s16[3], row0, c0, row0 + nrows, &s.sd[wave][0]); };
+#else
     RTile16<F, 2, S> t;
     float rs = WBF ? 1.f : 0.f;   // bf16 rows carry no scale
     auto load = [&](int l) {
@@ -982,8 +1209,9 @@ __device__ __forceinline__ void role_dn(const Ctx &c, LdsD &s, int di) {
                 __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void *)&s.tw[wave][st][0], 16,
                                                          voff, __builtin_amdgcn_readfirstlane(WB * ((row0 + 32) * F + c0) + 64 * st), 0, 0);
         }
-        if (!WBF && tid < nrows) rs = ldg(uni(c.ly[l].s[3]) + row0 + tid);
+        if (RSC && tid < nrows) rs = ldg(uni(c.ly[l].s[3]) + row0 + tid);
     };
+#endif
     HeadTile ht;
     load_gains<4, 8, H>(a.final_norm, s.hd.gain);
     load(0);
@@ -1027,6 +1255,20 @@ __device__ __forceinline__ void role_dn(const Ctx &c, LdsD &s, int di) {
                 pcw_put<F, UD>(s.pc, 192 * wave + lane + 64 * k, vu, ps.isc);
             }
             wave_lds_order();   // the wave's own K slice
+#ifdef QT_RS_Q4
+            q4_psum<F, KW>(s.pc, c0, RS_PQ(s, wave));
+            RS_MARK(step, l, 6);
+            {
+                float acc[3];
+                rdot16<F, 3, S, 1>(t, s.pc, c0, acc, RS_PQ(s, wave), &s.sd[wave][0]);
+                RS_MARK(step, l, 7);
+                if (lane < 32) {
+#pragma unroll
+                    for (int q = 0; q < 3; q++) s.red[wave][q][lane & 15][lane >> 4] = acc[q];
+                }
+            }
+            __syncthreads();
+#else
             RS_MARK(step, l, 6);
             AccT acc[3];
             {
@@ -1058,6 +1300,7 @@ __device__ __forceinline__ void role_dn(const Ctx &c, LdsD &s, int di) {
                     for (int i = 0; i < 4; i++) s.red[wave][q][4 * kg + i][m16] = acc[q][i];
             }
             __syncthreads();
+#endif
             if (tid < nrows) {
                 const int q = tid >> 4, rr = tid & 15;
                 RedT d[4];
@@ -1482,7 +1725,7 @@ extern "C" hipError_t QT_RS_NAME(qt_rstep, _trace_read)(unsigned long long *out)
 
 extern "C" int QT_RS_NAME(qt_rstep, _supported)(int prec, int hidden, int inter, int n_heads, int n_kv, int head_dim,
                                                 int kv_max, int n_layers) {
-    if (prec != (ps::QT_RS_NS::WBF ? QT_BF16 : QT_INT8) || hidden != ps::QT_RS_NS::H || inter != ps::QT_RS_NS::F)
+    if (prec != ps::QT_RS_NS::PREC || hidden != ps::QT_RS_NS::H || inter != ps::QT_RS_NS::F)
         return 0;
     if (n_heads != ps::NH || n_kv != ps::NKV || head_dim != ps::HD) return 0;
     if (kv_max > ps::QT_RS_NS::ACH * ps::QT_RS_NS::ABLK * ps::KVB || n_layers < 1 || n_layers > ps::QT_RS_NS::MAXLR)
@@ -1496,8 +1739,8 @@ extern "C" int QT_RS_NAME(qt_rstep, _supported)(int prec, int hidden, int inter,
 // hand-off words (both parities) and winner words
 extern "C" size_t QT_RS_NAME(qt_rstep, _region_words)(int n_layers) { return (size_t)2 * n_layers * ps::QT_RS_NS::LW; }
 extern "C" size_t QT_RS_NAME(qt_rstep, _slot_words)(void) { return (size_t)2 * ps::QT_RS_NS::NHEAD * 2; }
-#ifndef QT_RS_SMALL
-// attention key chunks per kv head, both geometries (the per-kernel attention must use the
+#if !defined(QT_RS_SMALL) && !defined(QT_RS_Q4)
+// attention key chunks per kv head, every build (the per-kernel attention must use the
 // same split)
 extern "C" int qt_rstep_chunks(void) { return ps::rs::ACH; }
 #endif

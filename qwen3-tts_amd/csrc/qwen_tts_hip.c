@@ -315,7 +315,7 @@ typedef struct {
     unsigned long long *ps_ring;   /* tagged activation words */
     int rs_on;              /* the role-specialised kernel (qt_rstep.hip) runs the fused step: 1 its 1.7B
                              * build, 2 its 0.6B build (qt_rstep06.hip), 3 its 0.6B bf16 build
-                             * (qt_rstep06b.hip) */
+                             * (qt_rstep06b.hip), 4 its 1.7B q4_0 build (qt_rstep4.hip) */
     unsigned *rs_reg;       /* its hand-off words, [2][L][layer block], sentinel when empty */
     unsigned long long *rs_slots;  /* its tagged winner words */
     float *ps_xin;          /* step-0 input of a launch */
@@ -341,19 +341,22 @@ static int rstep_enabled(void) {
 }
 
 /* Which build of the role-specialised kernel covers the stack: 1 (1.7B int8), 2 (0.6B int8),
- * 3 (0.6B bf16), 0 none. */
+ * 3 (0.6B bf16), 4 (1.7B q4_0), 0 none. */
 static int rs_kind(const stack_t *s) {
     if (!rstep_enabled()) return 0;
     if (qt_rstep_supported(s->prec, s->H, s->F, s->nh, s->nkv, s->hd, s->kv_max, s->L)) return 1;
     if (qt_rstep06_supported(s->prec, s->H, s->F, s->nh, s->nkv, s->hd, s->kv_max, s->L)) return 2;
     if (qt_rstep06b_supported(s->prec, s->H, s->F, s->nh, s->nkv, s->hd, s->kv_max, s->L)) return 3;
+    if (qt_rstep4_supported(s->prec, s->H, s->F, s->nh, s->nkv, s->hd, s->kv_max, s->L)) return 4;
     return 0;
 }
 static size_t rs_region_words(int rk, int L) {
-    return rk == 3 ? qt_rstep06b_region_words(L) : rk == 2 ? qt_rstep06_region_words(L) : qt_rstep_region_words(L);
+    return rk == 4 ? qt_rstep4_region_words(L) : rk == 3 ? qt_rstep06b_region_words(L)
+         : rk == 2 ? qt_rstep06_region_words(L) : qt_rstep_region_words(L);
 }
 static size_t rs_slot_words(int rk) {
-    return rk == 3 ? qt_rstep06b_slot_words() : rk == 2 ? qt_rstep06_slot_words() : qt_rstep_slot_words();
+    return rk == 4 ? qt_rstep4_slot_words() : rk == 3 ? qt_rstep06b_slot_words()
+         : rk == 2 ? qt_rstep06_slot_words() : qt_rstep_slot_words();
 }
 
 static int persistent_enabled(void) {
@@ -439,7 +442,8 @@ fail:
 static hipError_t ps_launch_ex(talker_t *t, int n_steps, int with_head, float *layer_out) {
     stack_t *s = &t->s;
     if (t->rs_on)
-        return (t->rs_on == 3 ? qt_launch_rstep06b : t->rs_on == 2 ? qt_launch_rstep06 : qt_launch_rstep)(t->ps_layers, s->L, s->final_norm, s->rope_cos, s->rope_sin, s->kc, s->vc, s->kv_max, s->eps,
+        return (t->rs_on == 4 ? qt_launch_rstep4 : t->rs_on == 3 ? qt_launch_rstep06b
+                : t->rs_on == 2 ? qt_launch_rstep06 : qt_launch_rstep)(t->ps_layers, s->L, s->final_norm, s->rope_cos, s->rope_sin, s->kc, s->vc, s->kv_max, s->eps,
                                1.0f / sqrtf((float)s->hd), t->rs_reg, t->rs_slots, t->io, t->io + s->H, t->ps_xin, t->d_pos,
                                t->ps_epoch, t->ps_err, n_steps, with_head,
                                with_head ? (const uint16_t *)t->head_m.w : NULL, with_head ? t->codec_emb : NULL,
