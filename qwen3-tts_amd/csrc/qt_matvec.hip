@@ -381,6 +381,135 @@ __global__ __launch_bounds__(QT_WG) void k_mv_generic(QtMvArgs a) {
 }
 
 // ---------------------------------------------------------------------------------
+// q4_0 matvec in the arithmetic of the role-specialised step's q4_0 build (qt_rstep.hip,
+// QTile16), so that the per-kernel q4_0 step and the fused one give the same bits: the
+// input's exact int8 pieces (the int8 path's scale rule: max|x| or, under RMSNorm, the
+// fused step's statistics order and bound), per 32-weight block the exact integer plane
+// sums of (n - 8) * piece joined into f = hi * 2^16 + lo (two exact 23-bit halves), and
+// per row the blocks' d * f accumulated by fmaf in that kernel's order: the K range in
+// four slices, in each slice two chains (blocks 2s + h of the slice, s ascending, h = 0,
+// 1), the four slices' chain sums added in slice order per h, the two h sums added, times
+// the pieces' scale.  Eight lanes take a row (lane 2w + h runs chain (w, h)), 32 rows per
+// workgroup; the pieces of the whole input are made once per workgroup into LDS, each
+// 16-column group stored even columns first (the low nibbles' order).
+template <int COLS, int EPI, bool NORM>
+__global__ __launch_bounds__(QT_WG) void k_mv_q4r(QtMvArgs a) {
+    static_assert(COLS % 256 == 0, "four slices of whole block pairs");
+    constexpr int NBS = COLS / 128;            // blocks per slice
+    constexpr int NS = NBS / 2;                // blocks per chain
+    constexpr int EPT = COLS / QT_WG;          // input elements per thread
+    __shared__ __align__(16) uint32_t pcw[COLS];   // 4 planes x COLS bytes
+    __shared__ float red[2 * QT_WAVES];
+    uint8_t *pc = reinterpret_cast<uint8_t *>(pcw);
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int k = lane & 7, w = k >> 1, h = k & 1;
+    const int row = (blockIdx.x * QT_WAVES + wave) * 8 + (lane >> 3);
+    const bool rok = row < a.M.rows;
+    // ---- every load up front: the chain's blocks and scales, the input, the gains ----
+    uint4 wq[NS];
+    float d[NS];
+#pragma unroll
+    for (int s = 0; s < NS; s++) {
+        const int b = w * NBS + 2 * s + h;
+        wq[s] = rok ? ld_chunk(a.M.w + (size_t)row * (COLS / 2) + (size_t)b * 16) : make_uint4(0, 0, 0, 0);
+        d[s] = rok ? ref_f16_to_f32(a.M.s16[(size_t)row * (COLS / 32) + b]) : 0.f;
+    }
+    float x[EPT], g[EPT];
+#pragma unroll
+    for (int j = 0; j < EPT; j++) {
+        x[j] = a.vin[tid + QT_WG * j];
+        g[j] = NORM ? a.nw[tid + QT_WG * j] : 1.0f;
+    }
+    float rres = 0.f;
+    if ((EPI == QT_EPI_RESID || EPI == QT_EPI_BIAS) && rok && k == 0)
+        rres = EPI == QT_EPI_RESID ? a.resid[row] : a.bias[row];
+    // ---- statistics (thread t: elements t + 256 j; waves in order) and the pieces ----
+    float ss = 0.f, m = 0.f;
+#pragma unroll
+    for (int j = 0; j < EPT; j++) {
+        if (NORM) ss = fmaf(x[j], x[j], ss);
+        m = fmaxf(m, fabsf(NORM ? x[j] * g[j] : x[j]));
+    }
+    if (NORM) ss = group_sum<64>(ss);
+    m = group_max<64>(m);
+    if (lane == 0) { red[2 * wave] = ss; red[2 * wave + 1] = m; }
+    __syncthreads();
+    float inv = 1.f;
+    QtPcScale ps;
+    {
+        float S = red[0], M = red[1];
+#pragma unroll
+        for (int v = 1; v < QT_WAVES; v++) { S += red[2 * v]; M = fmaxf(M, red[2 * v + 1]); }
+        if (NORM) {
+            inv = 1.0f / sqrtf(S / (float)COLS + a.eps);
+            ps = qt_pc_scale((inv * M) * (1.0f + 0x1p-20f));
+        } else {
+            ps = qt_pc_scale(M);
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < EPT; j++) {
+        const int e = tid + QT_WG * j;
+        const float v = NORM ? (x[j] * inv) * g[j] : x[j];
+        if (NORM && a.nout && blockIdx.x == 0) a.nout[e] = v;
+        const uint32_t t = qt_pc_word(v, ps.isc);      // biased digits
+        const int pos = 16 * (e >> 4) + ((e & 1) ? 8 : 0) + ((e & 15) >> 1);
+#pragma unroll
+        for (int q = 0; q < 4; q++) pc[q * COLS + pos] = (uint8_t)(((t >> (8 * q)) & 0xFFu) ^ 0x80u);
+    }
+    __syncthreads();
+    // ---- the chain ----
+    float acc = 0.f;
+#pragma unroll
+    for (int s = 0; s < NS; s++) {
+        const int b = w * NBS + 2 * s + h;
+        const uint32_t w4[4] = {wq[s].x, wq[s].y, wq[s].z, wq[s].w};
+        int D[4], P[4];
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            const uint4 p0 = *reinterpret_cast<const uint4 *>(pc + q * COLS + 32 * b);
+            const uint4 p1 = *reinterpret_cast<const uint4 *>(pc + q * COLS + 32 * b + 16);
+            const uint32_t W[8] = {p0.x, p0.y, p0.z, p0.w, p1.x, p1.y, p1.z, p1.w};
+            int dq = 0, pq = 0;
+#pragma unroll
+            for (int mm = 0; mm < 4; mm++) {
+                // word mm: elements 8mm .. 8mm+7, even ones in the low nibbles
+                const uint32_t ev = W[4 * (mm >> 1) + (mm & 1)], od = W[4 * (mm >> 1) + 2 + (mm & 1)];
+                dq = __builtin_amdgcn_sdot4((int)(w4[mm] & 0x0F0F0F0Fu), (int)ev, dq, false);
+                dq = __builtin_amdgcn_sdot4((int)((w4[mm] >> 4) & 0x0F0F0F0Fu), (int)od, dq, false);
+                pq = __builtin_amdgcn_sdot4((int)ev, 0x01010101, pq, false);
+                pq = __builtin_amdgcn_sdot4((int)od, 0x01010101, pq, false);
+            }
+            D[q] = dq; P[q] = pq;
+        }
+        const int lo = D[0] + (D[1] << 8) - 8 * (P[0] + 256 * P[1]);
+        const int hi = D[2] + (D[3] << 8) - 8 * (P[2] + 256 * P[3]);
+        acc = fmaf(d[s], fmaf((float)hi, 65536.f, (float)lo), acc);
+    }
+    // ---- slices in order per h, then the two h sums, times the pieces' scale ----
+    const int base = lane & ~7;
+    const float c0 = __shfl(acc, base + h, 64), c1 = __shfl(acc, base + 2 + h, 64);
+    const float c2 = __shfl(acc, base + 4 + h, 64), c3 = __shfl(acc, base + 6 + h, 64);
+    const float dh = ((c0 + c1) + c2) + c3;
+    const float v = (__shfl(dh, base, 64) + __shfl(dh, base + 1, 64)) * ps.s;
+    if (EPI == QT_EPI_SWIGLU) {
+        const float u = __shfl(v, (lane + 8) & 63, 64);   // the odd row of the pair
+        if (k == 0 && ((lane >> 3) & 1) == 0 && row + 1 < a.M.rows) a.out[row >> 1] = qt_silu_mul(v, u);
+    } else if (k == 0 && rok) {
+        if (EPI == QT_EPI_STORE) a.out[row] = v;
+        else if (EPI == QT_EPI_RESID) a.resid[row] = __fadd_rn(rres, v);
+        else a.out[row] = __fadd_rn(v, rres);
+    }
+}
+
+template <int COLS, int EPI, bool NORM>
+static hipError_t launch_q4r(const QtMvArgs &a, hipStream_t st) {
+    const int grid = (a.M.rows + 8 * QT_WAVES - 1) / (8 * QT_WAVES);
+    hipLaunchKernelGGL((k_mv_q4r<COLS, EPI, NORM>), dim3(grid), dim3(QT_WG), 0, st, a);
+    return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------------
 // host-side dispatch (C ABI, used by qwen_tts_hip.c)
 
 template <int PREC, int LPR, int CPL, int NR, int EPI, bool NORM>
@@ -439,11 +568,12 @@ static hipError_t dispatch(int prec, const QtMvArgs &a, hipStream_t st) {
             case 6144: return launch_nr<QT_INT8, 64, 6, 2, EPI, NORM>(a, st);
             }
         } else {
+            // q4_0: the fused step's arithmetic and order (k_mv_q4r)
             switch (c) {
-            case 1024: return launch_nr<QT_Q4, 32, 1, 4, EPI, NORM>(a, st);
-            case 2048: return launch_nr<QT_Q4, 64, 1, 4, EPI, NORM>(a, st);
-            case 3072: return launch_nr<QT_Q4, 32, 3, 4, EPI, NORM>(a, st);
-            case 6144: return launch_nr<QT_Q4, 64, 3, 4, EPI, NORM>(a, st);
+            case 1024: return launch_q4r<1024, EPI, NORM>(a, st);
+            case 2048: return launch_q4r<2048, EPI, NORM>(a, st);
+            case 3072: return launch_q4r<3072, EPI, NORM>(a, st);
+            case 6144: return launch_q4r<6144, EPI, NORM>(a, st);
             }
         }
     }
