@@ -1440,6 +1440,11 @@ __device__ __forceinline__ void role_att(const Ctx &c, LdsA &s, int g, int ch) {
     };
     qt_att_zero_rows<HPK>(&s.qp[0][0], HD, tid, NT);
     qt_att_zero_rows<HPK>(&s.pp[0][0], ABLK * KVB, tid, NT);
+    // a launch whose every step has all its keys in chunk 0 (at most 16, e.g. a Code
+    // Predictor frame): chunk 0 writes the attention output itself and no workgroup merges
+    // (the merge of a single partial is o * (1 / l) after +0 terms, done here the same way);
+    // the other chunks then have no work at all
+    const bool one = Geo(c.pos0 + a.n_steps - 1).nch == 1;
     prefetch(0, Geo(c.pos0));
     land();
     const float scale2 = a.scale * QT_LOG2E;
@@ -1525,7 +1530,14 @@ __device__ __forceinline__ void role_att(const Ctx &c, LdsA &s, int g, int ch) {
                 RS_MARK(step, l, 7);
                 // partial of this chunk: o (head lane/16, dims 32 wave + lane%16 and +16), m, l
                 const int hq = lane >> 4;
-                if (hq < HPK) {
+                if (one) {
+                    if (hq < HPK) {
+                        const float il = 1.0f / run.l;
+                        const int ob = R_ATT + (2 * g + hq) * HD + 32 * wave + key;
+                        put(c.wp(par, l, ob), (run.o[0] + 0.0f) * il);
+                        put(c.wp(par, l, ob + 16), (run.o[1] + 0.0f) * il);
+                    }
+                } else if (hq < HPK) {
                     const int ob = R_PO + (((g * HPK + hq) * 4 + wave) * ACH + ch) * 32 + key;
                     put(c.wp(par, l, ob), run.o[0]);
                     put(c.wp(par, l, ob + 16), run.o[1]);
@@ -1546,7 +1558,7 @@ __device__ __forceinline__ void role_att(const Ctx &c, LdsA &s, int g, int ch) {
                 }
             }
             // ---------------- merge: head 2g + ch/4, dims 32 (ch % 4) .. +31 -----------------
-            {
+            if (!one) {
                 const int hh = ch >> 2, dblk = ch & 3;
                 const int nch = ge.nch;
                 {
