@@ -1703,8 +1703,16 @@ __global__ __launch_bounds__(NT, 1) void k_rstep(RArgs a) {
     if (slot < SA0) hc = (slot - SQ0) * 8 + x;
     else if (slot >= SO0 && slot < SG0) hc = NQ + (slot - SO0) * 8 + x;
     else if (slot >= SG0 && slot < SD0) hc = NQ + NO + (slot - SG0) * 8 + x;
+#ifdef QT_RS_SMALL
+    // head rows in the order Q, O, GU, head-only, DN: a Code Predictor's 2048-row lm head then
+    // leaves DN (the last role of a layer to finish, whose head tile would land after the
+    // others are already waiting for it) without rows
+    else if (slot >= SD0 && slot < SI0) hc = NQ + NO + NG + NI + (slot - SD0) * 8 + x;
+    else if (slot >= SI0) hc = NQ + NO + NG + (slot - SI0) * 8 + x;
+#else
     else if (slot >= SD0 && slot < SI0) hc = NQ + NO + NG + (slot - SD0) * 8 + x;
     else if (slot >= SI0) hc = NQ + NO + NG + ND + (slot - SI0) * 8 + x;
+#endif
 #ifdef QT_RS_SMALL
     const int pos0 = a.cp ? 0 : *a.d_pos;   // a Code Predictor frame starts at position 0
 #else
