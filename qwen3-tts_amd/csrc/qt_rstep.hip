@@ -816,7 +816,11 @@ __device__ __forceinline__ int head_phase(const Ctx &c, HeadLds &s, const HeadTi
         for (int k = 0; k < KX; k++) put4<8, H>(s.x, 4 * (tid + NT * k), v[k]);
     }
     __syncthreads();
-    stage_norm<QT_BF16, H>(s.x, s.gain, a.eps, s.xn);
+#if defined(QT_RS_SMALL) && !defined(QT_RS_BF16)
+    // (a Code Predictor's int8 lm head makes its own pieces of the normed x: xn only for hid)
+    if (!a.cp || (last && c.hc == 0))
+#endif
+        stage_norm<QT_BF16, H>(s.x, s.gain, a.eps, s.xn);
     if (last && c.hc == 0)
         for (int i = tid; i < H; i += NT) { a.hid[i] = s.xn[xpos<8, H>(i)]; a.decx[i] = s.x[xpos<8, H>(i)]; }
     float bv = -INFINITY;
@@ -868,9 +872,12 @@ __device__ __forceinline__ int head_phase(const Ctx &c, HeadLds &s, const HeadTi
         // (the per-kernel frame's lm-head matvec), so the logits are the same bits; plain
         // argmax from the start value -1e30, lowest index on ties (k_select mode 0)
         float xv[EH], gc[EH], gu[EH];
-        load_norm_gains(a.final_norm, gc, gu);
 #pragma unroll
-        for (int k = 0; k < EH; k++) xv[k] = s.x[xpos<8, H>(tid + NT * k)];
+        for (int k = 0; k < EH; k++) {   // the final norm's gains from their LDS copy
+            xv[k] = s.x[xpos<8, H>(tid + NT * k)];
+            gc[k] = s.gain[xpos<8, H>(tid + NT * k)];
+            gu[k] = s.gain[xpos<8, H>(EH * tid + k)];
+        }
         const float sA = norm_pieces(xv, gc, gu, s.cxs, s.cwst, s.cpc, a.eps);
         i32x4 acc[1];
         rdot16<H, 1, H / 4 / 64, 1>(ht.tc, s.cpc, wave * (H / 4), acc);
