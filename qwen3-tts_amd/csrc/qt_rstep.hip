@@ -1,14 +1,17 @@
-// qt_rstep.hip — the Talker decode step with int8 weights (16 query / 8 kv heads of 128)
-// as ONE persistent cooperative kernel whose workgroups each own ONE phase of the layer.
-// Built twice: the 1.7B geometry (hidden 2048, intermediate 6144; namespace ps::rs, entry
-// points qt_rstep_* / qt_launch_rstep) and, with QT_RS_SMALL defined (qt_rstep06.hip),
-// the 0.6B geometry (hidden 1024, intermediate 3072; ps::rs06, qt_rstep06_* /
-// qt_launch_rstep06), which has half the O, GU and DN workgroups and gives the slots left
-// over to the codec head alone.
+// qt_rstep.hip — the Talker decode step (16 query / 8 kv heads of 128) as ONE persistent
+// cooperative kernel whose workgroups each own ONE phase of the layer.  Built four times:
+// the 1.7B geometry with int8 weights (hidden 2048, intermediate 6144; namespace ps::rs,
+// entry points qt_rstep_* / qt_launch_rstep); with QT_RS_SMALL (qt_rstep06.hip) the 0.6B
+// geometry (hidden 1024, intermediate 3072; ps::rs06, qt_rstep06_*), which has half the O,
+// GU and DN workgroups and gives the slots left over to the codec head alone (and runs a
+// whole Code Predictor frame as one launch: qt_launch_rstep06_cp); with QT_RS_SMALL and
+// QT_RS_BF16 (qt_rstep06b.hip) the 0.6B geometry with bf16 weights (ps::rs06b); with
+// QT_RS_Q4 (qt_rstep4.hip) the 1.7B geometry with q4_0 weights (ps::rs4).
 //
-// Same math as qwen_talker_step (qwen_tts_talker.c:537-699), same arithmetic per output
-// as the per-kernel path (qt_matvec.hip, qt_attn.hip with 8 key chunks per kv head), so
-// the two agree to the bit.
+// Same math as qwen_talker_step (qwen_tts_talker.c:537-699).  With int8 and q4_0 weights
+// every output has the per-kernel path's arithmetic (qt_matvec.hip, qt_attn.hip with 8 key
+// chunks per kv head), so the two agree to the bit; with bf16 weights the projections sum
+// the same exact products in the MFMA's order, so the two agree to f32 rounding.
 //
 // Why roles.  A decode layer is a chain of six dependent hand-offs (x -> q|k|v ->
 // attention partials -> attention output -> xa -> h -> x'), and each hand-off between
