@@ -374,6 +374,36 @@ def test_greedy_tokens_match_reference(name, prec):
 
 
 @need_ref
+@pytest.mark.parametrize("name,prec", [("mini", "int8"), ("mini17", "int8"), ("mini", "bf16"), ("mini17", "int4")])
+def test_fused_greedy_one_launch_matches_step_launches(name, prec):
+    """A greedy launch of 24 steps from position 0, which crosses 16 keys (so every one of
+    its steps keeps the attention merge of the chunk partials), against the same steps as
+    one launch each (up to 16 keys a launch has every key in chunk 0 and writes the
+    attention output from that chunk, o * (1/l), without the merge): the same tokens, and
+    the same hidden state and K/V to the bit."""
+    print(f"[case] greedy one launch vs step launches {name} {prec}", flush=True)
+    ref, shape, _ = _ref(name, prec)
+    pc = hip.PREC[prec]
+    ga, gb = _gpu_talker(ref, shape, pc), _gpu_talker(ref, shape, pc)
+    emb = np.ascontiguousarray(ref.codec_emb())
+    head = np.ascontiguousarray(ref.codec_head())
+    e0 = synth.bf16_to_f32(emb[321])
+    n = 24
+    ta, ha = ga.greedy(head, emb, e0, 0, 10, n)
+    tb, e = [], e0
+    for i in range(n):
+        t1, hb = gb.greedy(head, emb, e, i, 10 + i, 1)
+        tb.append(int(t1[0]))
+        e = synth.bf16_to_f32(emb[int(t1[0])])
+    assert list(ta) == tb
+    assert np.array_equal(ha.view(np.uint32), hb.view(np.uint32))
+    ka, va = ga.download_kv(n)
+    kb, vb = gb.download_kv(n)
+    assert np.array_equal(ka[:, :n], kb[:, :n]) and np.array_equal(va[:, :n], vb[:, :n])
+    ga.free(); gb.free()
+
+
+@need_ref
 @pytest.mark.parametrize("name,prec,top_p,text_len,warmup", [("mini", "int8", 1.0, 0, 0), ("mini17", "int4", 1.0, 0, 0),
                                                              ("mini", "int8", 0.8, 1, 3), ("mini17", "int8", 0.95, 2, 0)])
 def test_sampled_loop_matches_reference(oracle, name, prec, top_p, text_len, warmup):
