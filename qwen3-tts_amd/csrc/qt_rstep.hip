@@ -175,18 +175,19 @@ struct RArgs {
     int *d_frame, *hist;
     int hist_len;
     float *layer_out;             // optional [L][H]: every layer's output x of the last step
-    // Code Predictor frame (0.6B build only): step s is pass s at position s; the input of
+    // Code Predictor frame (0.6B builds only): step s is pass s at position s; the input of
     // pass 0 is xin, of pass s >= 1 row codes[s-1] of table cp_emb[s-1]; after pass s >= 1
-    // int8 lm head s-1 (rows cp_head[s-1], scales cp_hs[s-1], `vocab` rows) on the
-    // final-normed x gives codes[s] (plain argmax, lowest index on ties).  Device arrays of
-    // 15 pointers each; codes[0] is the frame's input code.
+    // lm head s-1 (`vocab` rows cp_head[s-1]: int8 with row scales cp_hs[s-1], or bf16) on
+    // the final-normed x gives codes[s] (plain argmax, lowest index on ties).  Device arrays
+    // of 15 pointers each; codes[0] is the frame's input code.
     int cp;
     const uint8_t *const *cp_head;
     const float *const *cp_hs;
     const uint16_t *const *cp_emb;
     int *cp_codes;
-    // with the mtp projection (mtp_w != NULL): every pass input is W.e + b (int8 rows of
-    // EMB columns, row scales, bias), e the table row (EMB wide) or, for pass 0, xin
+    // with the mtp projection (mtp_w != NULL): every pass input is W.e + b (rows of EMB
+    // columns in the build's weight type, int8 with row scales mtp_s; bias), e the table
+    // row (EMB wide) or, for pass 0, xin
     const uint8_t *mtp_w;
     const float *mtp_s, *mtp_b;
 };
@@ -781,8 +782,8 @@ __device__ __forceinline__ float amax4(const uint4 &v) {
 // ---- head (final norm, codec head rows, masked local argmax, global argmax) ------------
 using THead = Tile<QT_BF16, H, HEADR / 4>;
 // The head rows of a workgroup for the step about to end: the Talker's bf16 codec head, or
-// (Code Predictor) 16 rows of the pass's int8 lm head, one 16-row MFMA tile with the
-// columns split over the waves as in the projections.
+// (Code Predictor) 16 rows of the pass's lm head: int8, one 16-row MFMA tile with the
+// columns split over the waves as in the projections, or bf16 as the codec head.
 struct HeadTile {
     THead th;
 #if defined(QT_RS_SMALL) && !defined(QT_RS_BF16)
@@ -1802,11 +1803,11 @@ extern "C" hipError_t QT_RS_NAME(qt_launch_rstep, )(const void *layers_dev, int 
 
 #ifdef QT_RS_SMALL
 // Code Predictor frame (qwen_tts_code_predictor.c:926-1045) in one launch: n_passes passes
-// of the n_layers CP layers at positions 0 .. n_passes-1, pass 0 on xin, the int8 lm head
-// after every pass s >= 1 writing codes[s], pass s+1 on row codes[s] of its table.  cp_tab:
-// device array of 45 pointers (15 lm heads [vocab][1024] int8, their 15 row-scale arrays,
-// the 15 input tables: the Talker's codec embedding, then CP embeddings 0 .. 13).  codes[0]
-// is the frame's input code.
+// of the n_layers CP layers at positions 0 .. n_passes-1, pass 0 on xin, the lm head after
+// every pass s >= 1 writing codes[s], pass s+1 on row codes[s] of its table.  cp_tab: device
+// array of 45 pointers (15 lm heads [vocab][1024] in the build's weight type, their 15 row-
+// scale arrays (int8; unused with bf16), the 15 input tables: the Talker's codec embedding,
+// then CP embeddings 0 .. 13).  codes[0] is the frame's input code.
 extern "C" hipError_t QT_RS_NAME(qt_launch_rstep, _cp)(const void *layers_dev, int n_layers, const float *final_norm,
                                            const float *rope_cos, const float *rope_sin, uint16_t *kc, uint16_t *vc,
                                            int kv_max, float eps, float scale, unsigned *reg, unsigned long long *slots,
