@@ -23,6 +23,7 @@
 
 #include <hip/hip_runtime_api.h>
 #include <math.h>
+#include <pthread.h>
 #include <stdarg.h>
 #include <stdio.h>
 #include <stdlib.h>
@@ -135,13 +136,93 @@ static float *up_f32(const float *src, size_t n, hipStream_t st) {
  * [n_kv][kv_max][hd]): one contiguous copy through a device staging buffer plus a
  * relayout kernel, instead of one strided copy per head with 256-byte rows (which
  * pageable memory serves at tens of MB/s).  stage holds n*n_kv*hd bf16. */
+/* Host -> device copies from pageable memory (the reference's KV after its CPU prefill)
+ * through two pinned buffers: the CPU copies the next piece of the source into one buffer
+ * with UP_THREADS threads while the DMA engine moves the previous piece out of the other.
+ * On the MI355X box, 235 MB moved at 40-43 GB/s this way.  hipMemcpy from the same pageable
+ * source moved at 25-29 GB/s: it stages through the runtime's own pinned buffers with one
+ * copying thread.  As with a pageable hipMemcpyAsync, the source may be reused once the call
+ * returns: the DMA still in flight reads the pinned buffer only. */
+#define UP_PIECE ((size_t)4 << 20)
+#define UP_THREADS 4
+typedef struct { void *pin[2]; hipEvent_t ev[2]; int nb; } hpipe_t;
+
+typedef struct { char *d; const char *s; size_t n; } hcopy_t;
+static void *hcopy_run(void *p) {
+    const hcopy_t *j = (const hcopy_t *)p;
+    memcpy(j->d, j->s, j->n);
+    return NULL;
+}
+/* memcpy over up to UP_THREADS page-aligned slices: the calling thread copies the first,
+ * and a slice whose thread could not be created is copied by the caller too */
+static void par_memcpy(void *dst, const void *src, size_t n) {
+    pthread_t th[UP_THREADS];
+    hcopy_t jb[UP_THREADS];
+    int run[UP_THREADS] = {0};
+    const int nt = n >= ((size_t)UP_THREADS << 20) ? UP_THREADS : 1;
+    const size_t per = ((n + nt - 1) / nt + 4095) & ~(size_t)4095;
+    for (int t = 0; t < nt; t++) {
+        const size_t o = (size_t)t * per;
+        jb[t].d = (char *)dst + o;
+        jb[t].s = (const char *)src + o;
+        jb[t].n = o >= n ? 0 : (o + per > n ? n - o : per);
+        if (t > 0 && jb[t].n) run[t] = pthread_create(&th[t], NULL, hcopy_run, &jb[t]) == 0;
+    }
+    hcopy_run(&jb[0]);
+    for (int t = 1; t < nt; t++) {
+        if (run[t]) pthread_join(th[t], NULL);
+        else if (jb[t].n) hcopy_run(&jb[t]);
+    }
+}
+static void hpipe_free(hpipe_t *p) {
+    for (int b = 0; b < 2; b++) {
+        if (p->pin[b]) (void)hipHostFree(p->pin[b]);
+        if (p->ev[b]) (void)hipEventDestroy(p->ev[b]);
+    }
+    memset(p, 0, sizeof *p);
+}
+/* the pinned buffers and events of a pipe that runs on stream st (pinning takes
+ * milliseconds: the Talker makes its pipe at init, other owners on first use) */
+static hipError_t hpipe_init(hpipe_t *p, hipStream_t st) {
+    hipError_t e;
+    if (p->pin[0] && p->pin[1]) return hipSuccess;
+    hpipe_free(p);
+    for (int b = 0; b < 2; b++) {
+        if ((e = hipHostMalloc(&p->pin[b], UP_PIECE, hipHostMallocDefault)) ||
+            (e = hipEventCreateWithFlags(&p->ev[b], hipEventDisableTiming)) || (e = hipEventRecord(p->ev[b], st))) {
+            hpipe_free(p);
+            return e;
+        }
+    }
+    return hipSuccess;
+}
+/* `bytes` from pageable host memory to device memory, in order on stream st (one stream
+ * per pipe) */
+static hipError_t hpipe_upload(hpipe_t *p, void *dev, const void *host, size_t bytes, hipStream_t st) {
+    hipError_t e;
+    if ((e = hpipe_init(p, st))) return e;
+    for (size_t o = 0; o < bytes; o += UP_PIECE) {
+        const size_t n = bytes - o < UP_PIECE ? bytes - o : UP_PIECE;
+        const int b = p->nb;
+        p->nb ^= 1;
+        if ((e = hipEventSynchronize(p->ev[b]))) return e;   /* the copy that last read this buffer is done */
+        par_memcpy(p->pin[b], (const char *)host + o, n);
+        if ((e = hipMemcpyAsync((char *)dev + o, p->pin[b], n, hipMemcpyHostToDevice, st))) return e;
+        if ((e = hipEventRecord(p->ev[b], st))) return e;
+    }
+    return hipSuccess;
+}
+
+/* n positions of one layer's K or V between the host rows [n][nkv*hd] and the device's
+ * head-major cache, through the device staging buffer and the relayout kernel; uploads
+ * go through the pinned pipe */
 static hipError_t kv_xfer(uint16_t *dev_heads, int kv_max, uint16_t *host_rows, int n, int nkv, int hd, int upload,
-                          uint16_t *stage, hipStream_t st) {
+                          uint16_t *stage, hpipe_t *pipe, hipStream_t st) {
     hipError_t e;
     const size_t bytes = (size_t)n * nkv * hd * sizeof(uint16_t);
     if (n <= 0) return hipSuccess;
     if (upload) {
-        if ((e = hipMemcpyAsync(stage, host_rows, bytes, hipMemcpyDefault, st))) return e;
+        if ((e = hpipe_upload(pipe, stage, host_rows, bytes, st))) return e;
         return qt_launch_kv_relayout(stage, dev_heads, n, nkv, hd, kv_max, 1, st);
     }
     if ((e = qt_launch_kv_relayout(dev_heads, stage, n, nkv, hd, kv_max, 0, st))) return e;
@@ -162,6 +243,7 @@ typedef struct {
     float *qkvbuf, *attn, *hbuf;
     float *part; unsigned *cnt;
     uint16_t *kv_stage;        /* [kv_max][n_kv*hd]: KV upload/download staging, made on first use */
+    hpipe_t up;                /* pinned buffers of the KV upload */
 } stack_t;
 
 static void stack_free(stack_t *s) {
@@ -180,6 +262,7 @@ static void stack_free(stack_t *s) {
     void *bufs[] = {s->final_norm, s->rope_cos, s->rope_sin, s->kc, s->vc, s->qkvbuf, s->attn, s->hbuf, s->part, s->cnt,
                     s->kv_stage};
     for (size_t i = 0; i < sizeof bufs / sizeof bufs[0]; i++) if (bufs[i]) (void)hipFree(bufs[i]);
+    hpipe_free(&s->up);
     memset(s, 0, sizeof *s);
 }
 
@@ -546,6 +629,14 @@ void *qwen_hip_talker_init(const qwen_hip_talker_desc_t *desc) {
     if (!t) { SETERR("out of host memory"); return NULL; }
     HCK(hipStreamCreateWithFlags(&t->st, hipStreamNonBlocking));
     if (stack_init(&t->s, desc, t->st) != 0) goto fail;   /* g_err already set */
+    /* the KV hand-off's pinned pipe and device staging, so that upload_kv only copies */
+    HCK(hpipe_init(&t->s.up, t->st));
+    HCK(hipMalloc((void **)&t->s.kv_stage, (size_t)t->s.kv_max * t->s.kvd * sizeof(uint16_t)));
+    /* one small copy and relayout now: the runtime's first-use costs of both (2.7 ms on the
+     * MI355X box) belong to init, not to the first hand-off */
+    HCK(hipMemcpyAsync(t->s.kv_stage, t->s.up.pin[0], 4096, hipMemcpyHostToDevice, t->st));
+    HCK(qt_launch_kv_relayout(t->s.kc, t->s.kv_stage, 1, t->s.nkv, t->s.hd, t->s.kv_max, 0, t->st));
+    HCK(hipStreamSynchronize(t->st));
     const int H = t->s.H;
     t->hist_len = 4096;
     HCK(hipMalloc((void **)&t->io, (size_t)2 * H * sizeof(float)));
@@ -771,8 +862,8 @@ int qwen_hip_talker_upload_kv(void *state, const uint16_t *kv_k, const uint16_t 
     if (!s->kv_stage) HCK(hipMalloc((void **)&s->kv_stage, (size_t)s->kv_max * s->kvd * sizeof(uint16_t)));
     for (int l = 0; l < s->L; l++) {
         const size_t lay = (size_t)l * s->nkv * s->kv_max * s->hd, src = (size_t)l * host_kv_max * s->kvd;
-        HCK(kv_xfer(s->kc + lay, s->kv_max, (uint16_t *)kv_k + src, prefill_len, s->nkv, s->hd, 1, s->kv_stage, t->st));
-        HCK(kv_xfer(s->vc + lay, s->kv_max, (uint16_t *)kv_v + src, prefill_len, s->nkv, s->hd, 1, s->kv_stage, t->st));
+        HCK(kv_xfer(s->kc + lay, s->kv_max, (uint16_t *)kv_k + src, prefill_len, s->nkv, s->hd, 1, s->kv_stage, &s->up, t->st));
+        HCK(kv_xfer(s->vc + lay, s->kv_max, (uint16_t *)kv_v + src, prefill_len, s->nkv, s->hd, 1, s->kv_stage, &s->up, t->st));
     }
     HCK(hipStreamSynchronize(t->st));
     return 0;
@@ -788,8 +879,8 @@ static int stack_download_kv(stack_t *s, hipStream_t st, uint16_t *kv_k, uint16_
     if (!s->kv_stage) HCK(hipMalloc((void **)&s->kv_stage, (size_t)s->kv_max * s->kvd * sizeof(uint16_t)));
     for (int l = 0; l < s->L; l++) {
         const size_t lay = (size_t)l * s->nkv * s->kv_max * s->hd, dst = (size_t)l * host_kv_max * s->kvd;
-        HCK(kv_xfer(s->kc + lay, s->kv_max, kv_k + dst, n, s->nkv, s->hd, 0, s->kv_stage, st));
-        HCK(kv_xfer(s->vc + lay, s->kv_max, kv_v + dst, n, s->nkv, s->hd, 0, s->kv_stage, st));
+        HCK(kv_xfer(s->kc + lay, s->kv_max, kv_k + dst, n, s->nkv, s->hd, 0, s->kv_stage, NULL, st));
+        HCK(kv_xfer(s->vc + lay, s->kv_max, kv_v + dst, n, s->nkv, s->hd, 0, s->kv_stage, NULL, st));
     }
     HCK(hipStreamSynchronize(st));
     return 0;
@@ -1836,6 +1927,7 @@ typedef struct {
     hipGraphExec_t exec; int graph_ready, stepped;   /* stepped: a batch_step has run (inputs set) */
     int last_async;            /* steps replayed since the last batch_step */
     uint16_t *kv_stage;        /* [kv_max][n_kv*hd]: slot upload/download staging, made on first use */
+    hpipe_t up;                /* pinned buffers of the slot upload */
     int dead;
 } batch_t;
 
@@ -1845,6 +1937,7 @@ static void batch_destroy(batch_t *bt) {
     void *bufs[] = {bt->kc, bt->vc, bt->x, bt->qkv, bt->attn, bt->h, bt->hid, bt->pc, bt->ps, bt->part, bt->cnt, bt->d_pos,
                     bt->kv_stage, bt->pf_p, bt->pf_part, bt->g2_part, bt->g2_cnt, bt->px_sync};
     for (size_t i = 0; i < sizeof bufs / sizeof bufs[0]; i++) if (bufs[i]) (void)hipFree(bufs[i]);
+    hpipe_free(&bt->up);
     if (bt->h_io) (void)hipHostFree(bt->h_io);
     if (bt->h_pos) (void)hipHostFree(bt->h_pos);
     if (bt->st) (void)hipStreamDestroy(bt->st);
@@ -2101,8 +2194,8 @@ int qwen_hip_talker_batch_upload_slot(void *state, int b, const uint16_t *kv_k, 
     for (int l = 0; l < s->L; l++) {
         const size_t dst = (size_t)b * per + (size_t)l * s->nkv * bt->kv_max * s->hd;
         const size_t src = (((size_t)b * s->L + l) * src_kv_max) * s->kvd;
-        HCK(kv_xfer(bt->kc + dst, bt->kv_max, (uint16_t *)kv_k + src, prefill_len, s->nkv, s->hd, 1, bt->kv_stage, bt->st));
-        HCK(kv_xfer(bt->vc + dst, bt->kv_max, (uint16_t *)kv_v + src, prefill_len, s->nkv, s->hd, 1, bt->kv_stage, bt->st));
+        HCK(kv_xfer(bt->kc + dst, bt->kv_max, (uint16_t *)kv_k + src, prefill_len, s->nkv, s->hd, 1, bt->kv_stage, &bt->up, bt->st));
+        HCK(kv_xfer(bt->vc + dst, bt->kv_max, (uint16_t *)kv_v + src, prefill_len, s->nkv, s->hd, 1, bt->kv_stage, &bt->up, bt->st));
     }
     HCK(hipStreamSynchronize(bt->st));
     return 0;
@@ -2122,8 +2215,8 @@ int qwen_hip_talker_batch_download_slot(void *state, int b, uint16_t *kv_k, uint
     for (int l = 0; l < s->L; l++) {
         const size_t src = (size_t)b * per + (size_t)l * s->nkv * bt->kv_max * s->hd;
         const size_t dst = (((size_t)b * s->L + l) * dst_kv_max) * s->kvd;
-        HCK(kv_xfer(bt->kc + src, bt->kv_max, kv_k + dst, n, s->nkv, s->hd, 0, bt->kv_stage, bt->st));
-        HCK(kv_xfer(bt->vc + src, bt->kv_max, kv_v + dst, n, s->nkv, s->hd, 0, bt->kv_stage, bt->st));
+        HCK(kv_xfer(bt->kc + src, bt->kv_max, kv_k + dst, n, s->nkv, s->hd, 0, bt->kv_stage, NULL, bt->st));
+        HCK(kv_xfer(bt->vc + src, bt->kv_max, kv_v + dst, n, s->nkv, s->hd, 0, bt->kv_stage, NULL, bt->st));
     }
     HCK(hipStreamSynchronize(bt->st));
     return 0;
