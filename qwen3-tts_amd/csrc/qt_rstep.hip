@@ -428,14 +428,15 @@ __device__ __forceinline__ void rdot16(const RTile16<COLS, NT16, S> &t, const ui
 // ---- q4_0 row tiles ------------------------------------------------------------------------
 // The reference's q4_0 blocks (32 weights w = (n - 8) d, byte i holding n of weights 2i
 // (low nibble) and 2i+1, one f16 scale d; qwen_tts_kernels.c:2815-2816) on the same
-// v_mfma_i32_16x16x64_i8 with the operands swapped: A = the activation pieces, row 4h+p =
-// plane p over block h of the 64-column step (the other block's columns zero, rows 8..15
-// zero), B = 16 weight rows of unsigned nibbles n (lane l: row l%16, the 16 weights
-// 16*(l/16) .. +15 of the step, even ones then odd ones, the pieces' storage order).  Lane
-// l < 32 ends with the four exact plane sums of n*p for row l%16 over block l/16 of the
-// step; subtracting 8 * (the block's piece sums, made once per input by q4_psum) gives the
-// exact sums of (n - 8)*p, the four planes join in two exact 23-bit halves, and the block
-// scale times their f32 value is added to the lane's f32 sum over its blocks.
+// v_mfma_i32_16x16x64_i8 with the operands swapped: A = the activation pieces, row 4h+i =
+// plane (0, 2, 1, 3)[i] over block h of the 64-column step (the other block's columns zero,
+// rows 8..15 zero: those rows read a zero plane), B = 16 weight rows of unsigned nibbles n (lane l:
+// row l%16, the 16 weights 16*(l/16) .. +15 of the step, even ones then odd ones, the
+// pieces' storage order).  The accumulator input holds -8 x the block's piece sums (made
+// once per input by q4_psum) in planes 0 and 2, so lane l < 32 ends with the exact sums of
+// (n - 8)*p for row l%16 over block l/16 of the step; the four planes join in two exact
+// 23-bit halves, and the block scale times their f32 value is added to the lane's f32 sum
+// over its blocks.
 // binary16 bits -> f32 as ref_f16_to_f32 (the reference's portable conversion, its
 // subnormal mapping included), with selects instead of branches
 __device__ __forceinline__ float f16_ref_sel(uint32_t h) {
@@ -498,8 +499,8 @@ struct QTile16 {
         }
     }
 };
-// 8 x the piece sums of each 32-column block of the wave's slice (KW columns from c0), two
-// per block: pq[2b] = 8 (P0 + 2^8 P1), pq[2b+1] = 8 (P2 + 2^8 P3), P_p the sum of plane p
+// -8 x the piece sums of each 32-column block of the wave's slice (KW columns from c0), two
+// per block: pq[2b] = -8 (P0 + 2^8 P1), pq[2b+1] = -8 (P2 + 2^8 P3), P_p the sum of plane p
 template <int COLS, int KW>
 __device__ __forceinline__ void q4_psum(const uint8_t *pc, int c0, int *pq) {
     constexpr int NBK = KW / 32;
@@ -520,23 +521,29 @@ __device__ __forceinline__ void q4_psum(const uint8_t *pc, int c0, int *pq) {
         sum = __builtin_amdgcn_sdot4((int)x1.z, 0x01010101, sum, false);
         sum = __builtin_amdgcn_sdot4((int)x1.w, 0x01010101, sum, false);
         const int hi = __shfl_xor(sum, 1, 64);   // the next plane's sum
-        if ((p & 1) == 0) pq[2 * b + (p >> 1)] = 8 * (sum + 256 * hi);
+        if ((p & 1) == 0) pq[2 * b + (p >> 1)] = -8 * (sum + 256 * hi);
     }
     wave_lds_order();
+}
+// Zero the plane after the NPL piece planes of a COLS-column input, once per launch (the
+// piece writers never touch it), with a barrier before any wave reads it
+template <int COLS>
+__device__ __forceinline__ void q4_zero_plane(uint8_t *pc) {
+    for (int i = threadIdx.x; i < pcs<COLS>() / 16; i += NT)
+        reinterpret_cast<uint4 *>(pc + NPL * pcs<COLS>())[i] = make_uint4(0u, 0u, 0u, 0u);
+    __syncthreads();
 }
 template <int COLS, int NT16, int S, int CH>
 __device__ __forceinline__ void rdot16(const QTile16<COLS, NT16, S> &t, const uint8_t *pc, int c0, float (&acc)[NT16],
                                        const int *pq, const float *sd) {
     const int lane = threadIdx.x & 63, m = lane & 15, kg = lane >> 4, h = kg & 1;
     const bool arow = m < 8 && (m >> 2) == (kg >> 1);
-    const uint8_t *pa = pc + (m & 3) * pcs<COLS>() + c0 + 16 * kg;
-    // (loads unconditional, masked with an AND: every address is inside the pieces, and a
-    // select between two uint4 values compiles to a private-memory round trip)
-    const unsigned am = arow ? 0xFFFFFFFFu : 0u;
-    auto ld_a = [&](int off) {
-        const uint4 v = *reinterpret_cast<const uint4 *>(pa + off);
-        return make_uint4(v.x & am, v.y & am, v.z & am, v.w & am);
-    };
+    // rows that carry no piece read the zero plane after the pieces (q4_zero_plane), so the
+    // loads need no mask; row 4h+i holds plane 0, 2, 1, 3 for i = 0..3, so that the two
+    // corrections (planes 0 and 2) are the first two entries of the accumulator input
+    const int pl = ((m & 1) << 1) | ((m >> 1) & 1);
+    const uint8_t *pa = pc + (arow ? pl : NPL) * pcs<COLS>() + c0 + 16 * kg;
+    auto ld_a = [&](int off) { return *reinterpret_cast<const uint4 *>(pa + off); };
 #pragma unroll
     for (int q = 0; q < NT16; q++) acc[q] = 0.f;
     uint4 a = ld_a(0);
@@ -557,17 +564,20 @@ __device__ __forceinline__ void rdot16(const QTile16<COLS, NT16, S> &t, const ui
 #pragma unroll
             for (int q = 0; q < NT16; q++) d[q] = ds[q];
         }
+        // the step's correction enters every MFMA as its accumulator input (planes 0 and 2,
+        // entries 0 and 1 of the lane's quad), so the epilogue only joins the planes
+        const i32x4 cq = {qc.x, qc.y, 0, 0};
         i32x4 D[NT16];   // every MFMA of the step first, then the epilogues (results in flight)
 #pragma unroll
         for (int q = 0; q < NT16; q++) {
             const uint2 w = t.w[q][s];
             const uint4 b = make_uint4(w.x & 0x0F0F0F0Fu, w.y & 0x0F0F0F0Fu, (w.x >> 4) & 0x0F0F0F0Fu,
                                        (w.y >> 4) & 0x0F0F0F0Fu);
-            D[q] = mfma_i8(a, b, i32x4{0, 0, 0, 0});
+            D[q] = mfma_i8(a, b, cq);
         }
 #pragma unroll
         for (int q = 0; q < NT16; q++) {
-            const int lo = D[q][0] + (D[q][1] << 8) - qc.x, hi = D[q][2] + (D[q][3] << 8) - qc.y;
+            const int lo = D[q][0] + (D[q][2] << 8), hi = D[q][1] + (D[q][3] << 8);
             acc[q] = fmaf(d[q], fmaf((float)hi, 65536.f, (float)lo), acc[q]);
         }
         a = an;
@@ -583,6 +593,7 @@ template <int COLS, int NT16, int S> using WTile = QTile16<COLS, NT16, S>;
 #define RS_SD(s, w) , (&(s).sd[w][0])
 #else
 template <int COLS, int KW> __device__ __forceinline__ void q4_psum(const uint8_t *, int, int *) {}
+template <int COLS> __device__ __forceinline__ void q4_zero_plane(uint8_t *) {}
 template <int COLS, int NT16, int S> using WTile = RTile16<COLS, NT16, S>;
 #define RS_PQ(s, w) nullptr
 #define RS_SD(s, w)
@@ -605,9 +616,9 @@ struct HeadLds {
 };
 struct LdsP {                    // Q, O, GU (and the head-only workgroups)
     float xs[H];                 // the input in element order (RMSNorm: statistics order -> unit order)
-    uint8_t pc[NPL * pcs<PCW>()];
+    uint8_t pc[(NPL + (WQ4 ? 1 : 0)) * pcs<PCW>()];   // q4_0: plus a zero plane (q4_zero_plane)
 #ifdef QT_RS_Q4
-    int pq[4][2 * (PCW / 4 / 32)];   // per wave: 8 x its blocks' piece sums (q4_psum)
+    int pq[4][2 * (PCW / 4 / 32)];   // per wave: -8 x its blocks' piece sums (q4_psum)
     float sd[4][(PCW / 4 / 64) * 64 * 8];   // per wave: its tiles' block scales (QTile16)
 #endif
     RedT red[8 * 16][4][4];      // partial plane sums [row][wave][plane] (K split over the waves)
@@ -616,9 +627,9 @@ struct LdsP {                    // Q, O, GU (and the head-only workgroups)
     HeadLds hd;
 };
 struct LdsD {                    // DN
-    uint8_t pc[NPL * pcs<F>()];
+    uint8_t pc[(NPL + (WQ4 ? 1 : 0)) * pcs<F>()];   // q4_0: plus a zero plane (q4_zero_plane)
 #ifdef QT_RS_Q4
-    int pq[4][2 * (F / 4 / 32)];     // per wave: 8 x its blocks' piece sums (q4_psum)
+    int pq[4][2 * (F / 4 / 32)];     // per wave: -8 x its blocks' piece sums (q4_psum)
     float sd[4][(F / 4 / 64) * 64 * 3];   // per wave: its tiles' block scales (QTile16)
 #else
     uint4 tw[4][steps<F / 4>()][64]; // tile 2 (rows 32..47): [wave][step][lane]
@@ -975,6 +986,7 @@ __device__ __forceinline__ void role_q(const Ctx &c, LdsP &s, int grp, int qi) {
     };
     HeadTile ht;
     load_gains<4, 8, H>(a.final_norm, s.hd.gain);
+    q4_zero_plane<H>(s.pc);
     load(0);
     land();
     int tok = -1;
@@ -1057,6 +1069,7 @@ __device__ __forceinline__ void role_o(const Ctx &c, LdsP &s, int oi) {
     };
     HeadTile ht;
     load_gains<4, 8, H>(a.final_norm, s.hd.gain);
+    q4_zero_plane<QD>(s.pc);
     load(0);
     land();
     int tok = -1;
@@ -1141,6 +1154,7 @@ __device__ __forceinline__ void role_gu(const Ctx &c, LdsP &s, int gi) {
     };
     HeadTile ht;
     load_gains<4, 8, H>(a.final_norm, s.hd.gain);
+    q4_zero_plane<H>(s.pc);
     load(0);
     land();
     for (int step = 0; step < a.n_steps; step++) {
@@ -1225,6 +1239,7 @@ __device__ __forceinline__ void role_dn(const Ctx &c, LdsD &s, int di) {
 #endif
     HeadTile ht;
     load_gains<4, 8, H>(a.final_norm, s.hd.gain);
+    q4_zero_plane<F>(s.pc);
     load(0);
     land();
     for (int step = 0; step < a.n_steps; step++) {
