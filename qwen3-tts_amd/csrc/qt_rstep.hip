@@ -536,23 +536,20 @@ __device__ __forceinline__ void q4_zero_plane(uint8_t *pc) {
 template <int COLS, int NT16, int S, int CH>
 __device__ __forceinline__ void rdot16(const QTile16<COLS, NT16, S> &t, const uint8_t *pc, int c0, float (&acc)[NT16],
                                        const int *pq, const float *sd) {
-    const int lane = threadIdx.x & 63, m = lane & 15, kg = lane >> 4, h = kg & 1;
-    const bool arow = m < 8 && (m >> 2) == (kg >> 1);
-    // rows that carry no piece read the zero plane after the pieces (q4_zero_plane), so the
-    // loads need no mask; row 4h+i holds plane 0, 2, 1, 3 for i = 0..3, so that the two
-    // corrections (planes 0 and 2) are the first two entries of the accumulator input
+    static_assert(S % 2 == 0, "steps are taken in pairs");
+    const int lane = threadIdx.x & 63, m = lane & 15, kg = lane >> 4;
+    // Steps s, s+1 (s even) share one accumulator: the first MFMA fills rows 0..7 (blocks
+    // 2s, 2s+1 of the slice), the second rows 8..15 (blocks 2s+2, 2s+3), so lane group kg
+    // ends with block 2s + kg.  Rows that carry no piece in an MFMA read the zero plane
+    // after the pieces (q4_zero_plane); row 4h+i holds plane 0, 2, 1, 3 for i = 0..3, so
+    // that the two corrections (planes 0 and 2) are the first two entries of the
+    // accumulator input.
     const int pl = ((m & 1) << 1) | ((m >> 1) & 1);
-    const uint8_t *pa = pc + (arow ? pl : NPL) * pcs<COLS>() + c0 + 16 * kg;
-    auto ld_a = [&](int off) { return *reinterpret_cast<const uint4 *>(pa + off); };
-#pragma unroll
-    for (int q = 0; q < NT16; q++) acc[q] = 0.f;
-    uint4 a = ld_a(0);
-#pragma unroll
-    for (int s = 0; s < S; s++) {
-        const int sn = s + 1 < S ? s + 1 : s;
-        const uint4 an = ld_a(64 * sn);
-        const int2 qc = *reinterpret_cast<const int2 *>(pq + 4 * s + 2 * h);
-        float d[NT16];
+    const bool row1 = m < 8 && (m >> 2) == (kg >> 1), row2 = m >= 8 && (m >> 2) - 2 == (kg >> 1);
+    const uint8_t *pa1 = pc + (row1 ? pl : NPL) * pcs<COLS>() + c0 + 16 * kg;
+    const uint8_t *pa2 = pc + (row2 ? pl : NPL) * pcs<COLS>() + c0 + 64 + 16 * kg;
+    auto ld = [](const uint8_t *p, int off) { return *reinterpret_cast<const uint4 *>(p + off); };
+    auto ld_d = [&](int s, float (&d)[NT16]) {   // block scales of step s, lanes < 32
         const float *ds = sd + (s * 64 + lane) * NT16;
         if constexpr (NT16 % 4 == 0) {
 #pragma unroll
@@ -564,26 +561,44 @@ __device__ __forceinline__ void rdot16(const QTile16<COLS, NT16, S> &t, const ui
 #pragma unroll
             for (int q = 0; q < NT16; q++) d[q] = ds[q];
         }
-        // the step's correction enters every MFMA as its accumulator input (planes 0 and 2,
-        // entries 0 and 1 of the lane's quad), so the epilogue only joins the planes
-        const i32x4 cq = {qc.x, qc.y, 0, 0};
-        i32x4 D[NT16];   // every MFMA of the step first, then the epilogues (results in flight)
+    };
+    auto nib = [](uint2 w) {
+        return make_uint4(w.x & 0x0F0F0F0Fu, w.y & 0x0F0F0F0Fu, (w.x >> 4) & 0x0F0F0F0Fu, (w.y >> 4) & 0x0F0F0F0Fu);
+    };
 #pragma unroll
-        for (int q = 0; q < NT16; q++) {
-            const uint2 w = t.w[q][s];
-            const uint4 b = make_uint4(w.x & 0x0F0F0F0Fu, w.y & 0x0F0F0F0Fu, (w.x >> 4) & 0x0F0F0F0Fu,
-                                       (w.y >> 4) & 0x0F0F0F0Fu);
-            D[q] = mfma_i8(a, b, cq);
-        }
+    for (int q = 0; q < NT16; q++) acc[q] = 0.f;
+    uint4 a1 = ld(pa1, 0), a2 = ld(pa2, 0);
+#pragma unroll
+    for (int s = 0; s < S; s += 2) {
+        const int sn = s + 2 < S ? s + 2 : s;
+        const uint4 a1n = ld(pa1, 64 * sn), a2n = ld(pa2, 64 * sn);
+        const int2 qc = *reinterpret_cast<const int2 *>(pq + 4 * s + 2 * kg);
+        float de[NT16], dd[NT16];
+        ld_d(s, de);
+        ld_d(s + 1, dd);
+        // the correction enters the first MFMA of the pair as its accumulator input
+        const i32x4 cq = {qc.x, qc.y, 0, 0};
+        i32x4 D[NT16];   // every MFMA of the pair first, then the epilogues (results in flight)
+#pragma unroll
+        for (int q = 0; q < NT16; q++) D[q] = mfma_i8(a1, nib(t.w[q][s]), cq);
+#pragma unroll
+        for (int q = 0; q < NT16; q++) D[q] = mfma_i8(a2, nib(t.w[q][s + 1]), D[q]);
 #pragma unroll
         for (int q = 0; q < NT16; q++) {
             const int lo = D[q][0] + (D[q][2] << 8), hi = D[q][1] + (D[q][3] << 8);
-            acc[q] = fmaf(d[q], fmaf((float)hi, 65536.f, (float)lo), acc[q]);
+            const float f = fmaf((float)hi, 65536.f, (float)lo);
+            // lanes < 32 take the odd step's value of their row and block from lane + 32
+            // (the swap's second result), so each lane's sum still runs over its blocks in
+            // step order; the first result keeps f in lanes < 32, and the second operand
+            // (lo, dead here) only gives the swap a register to write
+            const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(f), (unsigned)lo, false, false);
+            acc[q] = fmaf(dd[q], __uint_as_float(sw[1]), fmaf(de[q], __uint_as_float(sw[0]), acc[q]));
         }
-        a = an;
-        // keep each step's epilogue here: the sums feed only the lanes < 32 store after the
-        // loop, and the compiler would otherwise sink every step's epilogue down to that
-        // store, holding all the MFMA results at once (spills)
+        a1 = a1n;
+        a2 = a2n;
+        // keep each pair's epilogue here: the sums feed only the lanes < 32 store after the
+        // loop, and the compiler would otherwise sink every epilogue down to that store,
+        // holding all the MFMA results at once (spills)
 #pragma unroll
         for (int q = 0; q < NT16; q++) asm volatile("" : "+v"(acc[q]));
     }
