@@ -82,7 +82,10 @@ int   qwen_hip_talker_step(void *state, const float *embed, float *hidden_out, i
 /* replaces qwen_cuda_talker_get_dec_x            (qwen_tts_cuda_talker.cu:419) */
 void  qwen_hip_talker_get_dec_x(void *state, float *out);
 /* replaces qwen_cuda_talker_upload_kv(state, ctx, prefill_len) (qwen_tts_cuda_talker.cu:424):
- * kv_k/kv_v are the host bf16 caches [n_layers][host_kv_max][kv_dim] (qwen_tts.h:513-518). */
+ * kv_k/kv_v are the host bf16 caches [n_layers][host_kv_max][kv_dim] (qwen_tts.h:513-518),
+ * ordinary pageable memory.  The call copies them through two pinned buffers that the
+ * state made at init: four short-lived host threads fill one buffer while the DMA engine
+ * drains the other.  The caches may be reused as soon as the call returns. */
 int   qwen_hip_talker_upload_kv(void *state, const uint16_t *kv_k, const uint16_t *kv_v,
                                 int host_kv_max, int prefill_len);
 /* replaces qwen_cuda_talker_free                 (qwen_tts_cuda_talker.cu:933) */
