@@ -503,25 +503,37 @@ struct QTile16 {
 // per block: pq[2b] = -8 (P0 + 2^8 P1), pq[2b+1] = -8 (P2 + 2^8 P3), P_p the sum of plane p
 template <int COLS, int KW>
 __device__ __forceinline__ void q4_psum(const uint8_t *pc, int c0, int *pq) {
-    constexpr int NBK = KW / 32;
+    constexpr int NBK = KW / 32, NI = NBK / 16;
     static_assert(NBK % 16 == 0, "blocks per lane");
     const int lane = threadIdx.x & 63, p = lane & 3;
+    // every read first, then the sums (two chains each), then the neighbour plane's sum
+    // from the quad (DPP, no LDS round trip), then the stores
+    uint4 x[NI][2];
 #pragma unroll
-    for (int k = 0; k < NBK / 16; k++) {
+    for (int k = 0; k < NI; k++) {
         const int b = (lane >> 2) + 16 * k;
         const uint4 *src = reinterpret_cast<const uint4 *>(pc + p * pcs<COLS>() + c0 + 32 * b);
-        const uint4 x0 = src[0], x1 = src[1];
-        int sum = 0;
-        sum = __builtin_amdgcn_sdot4((int)x0.x, 0x01010101, sum, false);
-        sum = __builtin_amdgcn_sdot4((int)x0.y, 0x01010101, sum, false);
-        sum = __builtin_amdgcn_sdot4((int)x0.z, 0x01010101, sum, false);
-        sum = __builtin_amdgcn_sdot4((int)x0.w, 0x01010101, sum, false);
-        sum = __builtin_amdgcn_sdot4((int)x1.x, 0x01010101, sum, false);
-        sum = __builtin_amdgcn_sdot4((int)x1.y, 0x01010101, sum, false);
-        sum = __builtin_amdgcn_sdot4((int)x1.z, 0x01010101, sum, false);
-        sum = __builtin_amdgcn_sdot4((int)x1.w, 0x01010101, sum, false);
-        const int hi = __shfl_xor(sum, 1, 64);   // the next plane's sum
-        if ((p & 1) == 0) pq[2 * b + (p >> 1)] = -8 * (sum + 256 * hi);
+        x[k][0] = src[0];
+        x[k][1] = src[1];
+    }
+    int sum[NI];
+#pragma unroll
+    for (int k = 0; k < NI; k++) {
+        int s0 = 0, s1 = 0;
+        s0 = __builtin_amdgcn_sdot4((int)x[k][0].x, 0x01010101, s0, false);
+        s1 = __builtin_amdgcn_sdot4((int)x[k][1].x, 0x01010101, s1, false);
+        s0 = __builtin_amdgcn_sdot4((int)x[k][0].y, 0x01010101, s0, false);
+        s1 = __builtin_amdgcn_sdot4((int)x[k][1].y, 0x01010101, s1, false);
+        s0 = __builtin_amdgcn_sdot4((int)x[k][0].z, 0x01010101, s0, false);
+        s1 = __builtin_amdgcn_sdot4((int)x[k][1].z, 0x01010101, s1, false);
+        s0 = __builtin_amdgcn_sdot4((int)x[k][0].w, 0x01010101, s0, false);
+        s1 = __builtin_amdgcn_sdot4((int)x[k][1].w, 0x01010101, s1, false);
+        sum[k] = s0 + s1;
+    }
+#pragma unroll
+    for (int k = 0; k < NI; k++) {
+        const int hi = __builtin_amdgcn_mov_dpp(sum[k], 0xB1, 0xF, 0xF, false);   // quad_perm(1,0,3,2): plane p ^ 1
+        if ((p & 1) == 0) pq[2 * ((lane >> 2) + 16 * k) + (p >> 1)] = -8 * (sum[k] + 256 * hi);
     }
     wave_lds_order();
 }
